@@ -1,0 +1,115 @@
+/*
+ * ti.h — C ABI of libtabinfer: the MI355X (gfx950) implementation of TabInfer's
+ * quantized decode hot path. This is the drop-in boundary: the reference's JS
+ * engine calls its kernels through closure launchers over WebGPU buffers
+ * (models/qwen3.js, models/lfm25.js) and the native Rust engine calls
+ * n2-kernels; each entry point below replaces one of those and cites it.
+ *
+ * Conventions
+ *  - Every function returns 0 (TI_OK) or a negative TI_ERR_* code; the message
+ *    of the last failure on the calling thread is in ti_last_error().
+ *  - Buffer handles are device pointers returned by ti_buf_alloc (or any other
+ *    device allocation on the context's device). "f16"/"bf16" arrays are
+ *    uint16_t bit patterns. int8 vectors are packed 4 per uint32 little-endian.
+ *  - Compute entry points are stream-ordered on the context's stream and do not
+ *    block; ti_sync waits. A context is used by one thread at a time.
+ *  - Shape preconditions are validated here (K % 32 == 0 for int4/int8 paths,
+ *    K % 64 == 0 for ternary, hd % 32 == 0 and hd <= 128 for attention) and
+ *    fail with TI_ERR_INVALID before anything is launched.
+ *
+ * Data layouts are the reference's own (no re-layout is required by a caller):
+ *  int4 weights  pack u32[N*K/8] (k = 8w+i at bits 4i of word w, nibble = q+8),
+ *                scales f16[N*K/32]                     (models/qwen3.js:3405-3426)
+ *  int8 act      xq u32[K/4], xs f32[K/32], xsum i32[K/16] (models/qwen3.js:332-358)
+ *  int8 KV       per layer kq u32[cap*nKv*hd/4], ks f32[cap*nKv*hd/32], same for v
+ *                (position-major, then head, then dim) (models/qwen3.js:3877-3892)
+ *  ternary       codes u8[N*K/4] (Q2_0_g64 interleaved planes), scales f32[N*K/64]
+ *                                                        (native/docs/FORMAT.md)
+ *  int3 experts  p3 u32[rows*K/32*3] bitplanes, s3 f16[rows*K/32] (models/lfm25.js:833-856)
+ */
+#ifndef TI_H
+#define TI_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TI_OK              0
+#define TI_ERR_INVALID    -1   /* bad argument or shape precondition */
+#define TI_ERR_NO_DEVICE  -2   /* no HIP device (or index out of range) */
+#define TI_ERR_HIP        -3   /* HIP runtime error */
+#define TI_ERR_OOM        -4   /* device allocation failed */
+#define TI_ERR_STATE      -5   /* call out of order (e.g. graph end without begin) */
+
+typedef struct ti_ctx ti_ctx;
+typedef struct ti_graph ti_graph;
+
+/* ---- context, errors ------------------------------------------------------
+ * Replace E.init / E.device (engine/webgpu-engine.js:72-145). */
+const char* ti_last_error(void);
+int ti_version(void);                                 /* 100*major + minor */
+int ti_device_count(int* n);
+int ti_init(int device, ti_ctx** out);
+int ti_shutdown(ti_ctx* ctx);
+
+/* ---- buffers (engine/webgpu-engine.js:156-179, 388-393) ------------------- */
+int ti_buf_alloc(ti_ctx* ctx, size_t bytes, void** dptr);
+int ti_buf_free(ti_ctx* ctx, void* dptr);
+int ti_buf_write(ti_ctx* ctx, void* dst, size_t off, const void* src, size_t bytes);       /* blocking H2D */
+int ti_buf_read(ti_ctx* ctx, const void* src, size_t off, void* dst, size_t bytes);        /* waits, D2H   */
+int ti_buf_copy(ti_ctx* ctx, void* dst, size_t doff, const void* src, size_t soff, size_t bytes);
+int ti_buf_fill_u32(ti_ctx* ctx, void* dst, uint32_t value, size_t count);                 /* kernel fill  */
+int ti_sync(ti_ctx* ctx);
+
+/* ---- batching and timing ---------------------------------------------------
+ * ti_graph_begin/end capture every call in between into one HIP graph — the
+ * analogue of E.beginBatch(Infinity)/E.endBatch() (engine/webgpu-engine.js:357-386).
+ * Events replace the timestamp profiler (engine/webgpu-engine.js:283-306). */
+int ti_graph_begin(ti_ctx* ctx);
+int ti_graph_end(ti_ctx* ctx, ti_graph** out);
+int ti_graph_launch(ti_ctx* ctx, ti_graph* g);
+int ti_graph_destroy(ti_graph* g);
+int ti_event_record(ti_ctx* ctx, int slot);                          /* slot in [0, 64) */
+int ti_event_elapsed_ms(ti_ctx* ctx, int start_slot, int end_slot, float* ms);
+
+/* ---- int4 weights ---------------------------------------------------------- */
+/* A1 quantizeInt4Bf16 (models/qwen3.js:3405-3426), run on the GPU, bit-exact. */
+int ti_quant_int4_bf16(ti_ctx* ctx, const uint16_t* w_bf16, uint32_t* pack, uint16_t* scales,
+                       int N, int K);
+
+/* ---- activations ----------------------------------------------------------- */
+/* A2 quantQ8 (models/qwen3.js:414-420): per-32 int8 + per-16 sums. */
+int ti_quant_act_q8(ti_ctx* ctx, const float* x, uint32_t* xq, float* xs, int32_t* xsum, int K);
+/* QUANTQ8T (models/qwen3.js:1210-1231): T rows, per (token, group). */
+int ti_quant_act_q8_t(ti_ctx* ctx, const float* x, uint32_t* xq, float* xs, int T, int K);
+/* A6 rmsnormQ (models/qwen3.js:569-621): fused RMSNorm + int8 quant. */
+int ti_rmsnorm_q8(ti_ctx* ctx, const float* x, const uint16_t* w, uint32_t* xq, float* xs,
+                  int32_t* xsum, int H, float eps);
+/* rmsnorm (models/qwen3.js:60-88), y[T,H]. */
+int ti_rmsnorm(ti_ctx* ctx, const float* x, const uint16_t* w, float* y, int T, int H, float eps);
+
+/* ---- GEMV (batch 1) --------------------------------------------------------- */
+/* A3 gemvDP4_only (models/qwen3.js:422-427): y (+)= W·x over the int8 activation. */
+int ti_gemv_q4_q8(ti_ctx* ctx, const uint32_t* xq, const float* xs, const uint32_t* pack,
+                  const uint16_t* scales, float* y, int N, int K, int acc);
+/* A4 gemvQ (models/qwen3.js:314-321): f32 activation, used for N >= 16384 (lm_head). */
+int ti_gemv_q4_f32(ti_ctx* ctx, const float* x, const uint32_t* pack, const uint16_t* scales,
+                   float* y, int N, int K, int acc);
+/* A5 gateUpSiluDP4_only (models/qwen3.js:861-877): swi = silu(gate·x)*(up·x). */
+int ti_gateup_silu_q4(ti_ctx* ctx, const uint32_t* xq, const float* xs,
+                      const uint32_t* gpack, const uint16_t* gsc,
+                      const uint32_t* upack, const uint16_t* usc, float* swi, int I, int H);
+/* linearQ router (models/qwen3.js:1588-1608): T==1 and N<16384 -> quant + A3;
+ * T==1 and N>=16384 -> A4; T>1 -> per-token quant + A11 GEMM. */
+int ti_linear_q4(ti_ctx* ctx, const float* x, const uint32_t* pack, const uint16_t* scales,
+                 float* y, int T, int N, int K, int acc);
+/* Integer per-(row, group) dots of A3 (debug/parity: exact int32). */
+int ti_group_dots_q4_q8(ti_ctx* ctx, const uint32_t* xq, const uint32_t* pack, int32_t* dots,
+                        int N, int K);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

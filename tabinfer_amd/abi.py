@@ -1,0 +1,224 @@
+"""ctypes binding of libtabinfer.so (include/ti.h).
+
+This is plumbing for Python callers (the test-suite and bench.py); the JS host
+uses the N-API addon over the same C ABI. Loading fails loudly when the
+library has not been built: there is no fallback implementation.
+"""
+import ctypes as C
+import os
+import re
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libtabinfer.so")
+HEADER = os.path.join(os.path.dirname(HERE), "include", "ti.h")
+
+TI_OK, TI_ERR_INVALID, TI_ERR_NO_DEVICE, TI_ERR_HIP, TI_ERR_OOM, TI_ERR_STATE = 0, -1, -2, -3, -4, -5
+
+
+class TIError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__("ti error %d: %s" % (code, msg))
+        self.code = code
+
+
+_p, _i, _f, _sz, _u32 = C.c_void_p, C.c_int, C.c_float, C.c_size_t, C.c_uint32
+
+# name -> argtypes (all return int unless listed in _RES)
+SIGS = {
+    "ti_version": [],
+    "ti_device_count": [C.POINTER(_i)],
+    "ti_init": [_i, C.POINTER(_p)],
+    "ti_shutdown": [_p],
+    "ti_buf_alloc": [_p, _sz, C.POINTER(_p)],
+    "ti_buf_free": [_p, _p],
+    "ti_buf_write": [_p, _p, _sz, _p, _sz],
+    "ti_buf_read": [_p, _p, _sz, _p, _sz],
+    "ti_buf_copy": [_p, _p, _sz, _p, _sz, _sz],
+    "ti_buf_fill_u32": [_p, _p, _u32, _sz],
+    "ti_sync": [_p],
+    "ti_graph_begin": [_p],
+    "ti_graph_end": [_p, C.POINTER(_p)],
+    "ti_graph_launch": [_p, _p],
+    "ti_graph_destroy": [_p],
+    "ti_event_record": [_p, _i],
+    "ti_event_elapsed_ms": [_p, _i, _i, C.POINTER(_f)],
+    "ti_quant_int4_bf16": [_p, _p, _p, _p, _i, _i],
+    "ti_quant_act_q8": [_p, _p, _p, _p, _p, _i],
+    "ti_quant_act_q8_t": [_p, _p, _p, _p, _i, _i],
+    "ti_rmsnorm_q8": [_p, _p, _p, _p, _p, _p, _i, _f],
+    "ti_rmsnorm": [_p, _p, _p, _p, _i, _i, _f],
+    "ti_gemv_q4_q8": [_p, _p, _p, _p, _p, _p, _i, _i, _i],
+    "ti_gemv_q4_f32": [_p, _p, _p, _p, _p, _i, _i, _i],
+    "ti_gateup_silu_q4": [_p, _p, _p, _p, _p, _p, _p, _p, _i, _i],
+    "ti_linear_q4": [_p, _p, _p, _p, _p, _i, _i, _i, _i],
+    "ti_group_dots_q4_q8": [_p, _p, _p, _p, _i, _i],
+}
+_RES = {"ti_last_error": C.c_char_p}
+
+
+def header_functions(path=HEADER):
+    """Names of every function include/ti.h declares."""
+    txt = open(path).read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    return sorted(set(re.findall(r"\b(ti_[a-z0-9_]+)\s*\(", txt)))
+
+
+def load(path=LIB_PATH):
+    if not os.path.exists(path):
+        raise ImportError("libtabinfer.so is not built (%s); run `python -m tabinfer_amd.build`" % path)
+    lib = C.CDLL(path)
+    lib.ti_last_error.restype = C.c_char_p
+    lib.ti_last_error.argtypes = []
+    for name, args in SIGS.items():
+        fn = getattr(lib, name)
+        fn.restype = C.c_int
+        fn.argtypes = args
+    return lib
+
+
+_LIB = None
+
+
+def lib():
+    global _LIB
+    if _LIB is None:
+        _LIB = load()
+    return _LIB
+
+
+def check(rc):
+    if rc != 0:
+        raise TIError(rc, lib().ti_last_error().decode(errors="replace"))
+    return rc
+
+
+def register(name, argtypes):
+    """Declare an additional entry point (used by modules that extend SIGS)."""
+    SIGS[name] = argtypes
+    if _LIB is not None:
+        fn = getattr(_LIB, name)
+        fn.restype = C.c_int
+        fn.argtypes = argtypes
+
+
+class DevBuf:
+    """A device allocation owned by a Ctx (ptr is the device address)."""
+
+    def __init__(self, ctx, ptr, nbytes):
+        self.ctx, self.ptr, self.nbytes = ctx, ptr, nbytes
+
+    def __int__(self):
+        return self.ptr
+
+    def free(self):
+        if self.ptr:
+            check(lib().ti_buf_free(self.ctx.h, self.ptr))
+            self.ptr = 0
+
+    def at(self, byte_off):
+        """Device address byte_off into this buffer (no ownership)."""
+        return self.ptr + byte_off
+
+
+class Ctx:
+    def __init__(self, device=0):
+        h = C.c_void_p()
+        check(lib().ti_init(device, C.byref(h)))
+        self.h = h.value
+        self._bufs = []
+
+    # ---- memory ---------------------------------------------------------------
+    def alloc(self, nbytes):
+        p = C.c_void_p()
+        check(lib().ti_buf_alloc(self.h, nbytes, C.byref(p)))
+        b = DevBuf(self, p.value, nbytes)
+        self._bufs.append(b)
+        return b
+
+    def upload(self, arr):
+        arr = np.ascontiguousarray(arr)
+        b = self.alloc(max(arr.nbytes, 4))
+        if arr.nbytes:
+            check(lib().ti_buf_write(self.h, b.ptr, 0, arr.ctypes.data, arr.nbytes))
+        return b
+
+    def write(self, buf, arr, off=0):
+        arr = np.ascontiguousarray(arr)
+        check(lib().ti_buf_write(self.h, int(buf), off, arr.ctypes.data, arr.nbytes))
+
+    def download(self, buf, dtype, count, off=0):
+        out = np.empty(count, dtype=dtype)
+        if out.nbytes:
+            check(lib().ti_buf_read(self.h, int(buf), off, out.ctypes.data, out.nbytes))
+        return out
+
+    def zeros(self, nbytes):
+        b = self.alloc(nbytes)
+        check(lib().ti_buf_fill_u32(self.h, b.ptr, 0, (nbytes + 3) // 4))
+        return b
+
+    def fill_u32(self, buf, value, count):
+        check(lib().ti_buf_fill_u32(self.h, int(buf), value, count))
+
+    def sync(self):
+        check(lib().ti_sync(self.h))
+
+    # ---- generic call ---------------------------------------------------------------
+    def call(self, name, *args):
+        fn = getattr(lib(), name)
+        conv = []
+        for a in args:
+            if isinstance(a, DevBuf):
+                conv.append(a.ptr)
+            elif isinstance(a, np.generic):
+                conv.append(a.item())
+            else:
+                conv.append(a)
+        return check(fn(self.h, *conv))
+
+    # ---- timing ---------------------------------------------------------------------
+    def record(self, slot):
+        check(lib().ti_event_record(self.h, slot))
+
+    def elapsed_ms(self, a, b):
+        ms = C.c_float()
+        check(lib().ti_event_elapsed_ms(self.h, a, b, C.byref(ms)))
+        return ms.value
+
+    # ---- graphs -----------------------------------------------------------------------
+    def graph_begin(self):
+        check(lib().ti_graph_begin(self.h))
+
+    def graph_end(self):
+        g = C.c_void_p()
+        check(lib().ti_graph_end(self.h, C.byref(g)))
+        return g.value
+
+    def graph_launch(self, g):
+        check(lib().ti_graph_launch(self.h, g))
+
+    def graph_destroy(self, g):
+        check(lib().ti_graph_destroy(g))
+
+    def close(self):
+        if self.h:
+            for b in self._bufs:
+                if b.ptr:
+                    lib().ti_buf_free(self.h, b.ptr)
+                    b.ptr = 0
+            check(lib().ti_shutdown(self.h))
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+
+def device_count():
+    n = C.c_int()
+    check(lib().ti_device_count(C.byref(n)))
+    return n.value

@@ -1,0 +1,486 @@
+// k_gemv.hip — batch-1 int4 GEMVs (HBM-bound; no MFMA):
+//  A3 int4 x int8      gemvDP4_only        models/qwen3.js:359-427
+//  A4 int4 x f32       gemvQ               models/qwen3.js:276-321
+//  A5 gate+up+SiLU     gateUpSiluDP4_only  models/qwen3.js:679-728, 861-877
+//
+// Mapping (per 64-lane wavefront): a row of K weights is gpr = K/32 groups of
+// 16 bytes (32 nibbles + one f16 scale). LPR lanes share a row and each lane
+// owns GPL groups (gpr = LPR*GPL), so one wave covers 64/LPR rows per pass and
+// every load is one global_load_dwordx4 of a whole quant group. A lane's group
+// indices never change across rows, so its slice of the activation is loaded,
+// permuted and summed once and then lives in registers. R passes are loaded
+// back to back before any arithmetic, to keep several KB in flight per wave.
+//
+// int8 dot: the nibbles of a word are split into even (p & 0x0F0F0F0F) and odd
+// ((p >> 4) & 0x0F0F0F0F) byte lanes and dotted (v_dot4_i32_i8) with the
+// activation bytes permuted the same way; the unsigned-nibble offset is removed
+// once per group: sum (n-8)*x = sum n*x - 8*sum x. The per-group int32 is exact.
+#include "ti_internal.h"
+
+namespace {
+
+constexpr uint32_t M4 = 0x0F0F0F0Fu;
+
+__device__ __forceinline__ uint32_t even_bytes(uint32_t a0, uint32_t a1) {   // [x0,x2,x4,x6]
+    return (a0 & 0xffu) | ((a0 >> 8) & 0xff00u) | ((a1 & 0xffu) << 16) | ((a1 << 8) & 0xff000000u);
+}
+__device__ __forceinline__ uint32_t odd_bytes(uint32_t a0, uint32_t a1) {    // [x1,x3,x5,x7]
+    return ((a0 >> 8) & 0xffu) | ((a0 >> 16) & 0xff00u) | ((a1 << 8) & 0xff0000u) | (a1 & 0xff000000u);
+}
+
+// Activation slice of one group for the int8 path.
+struct ActQ8 {
+    int xe[4], xo[4];
+    int corr;      // 8 * sum of the 32 codes
+    float s;       // activation group scale
+};
+
+__device__ __forceinline__ void load_act_q8(const uint32_t* __restrict__ xq, const float* __restrict__ xs, int g, ActQ8& a) {
+    const uint4* p = reinterpret_cast<const uint4*>(xq + (size_t)g * 8);
+    uint4 u0 = p[0], u1 = p[1];
+    uint32_t w[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+    int sum = 0;
+#pragma unroll
+    for (int m = 0; m < 4; m++) {
+        a.xe[m] = (int)even_bytes(w[2 * m], w[2 * m + 1]);
+        a.xo[m] = (int)odd_bytes(w[2 * m], w[2 * m + 1]);
+        sum = __builtin_amdgcn_sdot4((int)w[2 * m], 0x01010101, sum, false);
+        sum = __builtin_amdgcn_sdot4((int)w[2 * m + 1], 0x01010101, sum, false);
+    }
+    a.corr = 8 * sum;
+    a.s = xs ? xs[g] : 0.0f;
+}
+
+// Exact int32 dot of one weight group (16 bytes) with the lane's activation group.
+__device__ __forceinline__ int group_dot_q8(const uint4 w, const ActQ8& a) {
+    int d = 0;
+    d = __builtin_amdgcn_sdot4((int)(w.x & M4), a.xe[0], d, false);
+    d = __builtin_amdgcn_sdot4((int)((w.x >> 4) & M4), a.xo[0], d, false);
+    d = __builtin_amdgcn_sdot4((int)(w.y & M4), a.xe[1], d, false);
+    d = __builtin_amdgcn_sdot4((int)((w.y >> 4) & M4), a.xo[1], d, false);
+    d = __builtin_amdgcn_sdot4((int)(w.z & M4), a.xe[2], d, false);
+    d = __builtin_amdgcn_sdot4((int)((w.z >> 4) & M4), a.xo[2], d, false);
+    d = __builtin_amdgcn_sdot4((int)(w.w & M4), a.xe[3], d, false);
+    d = __builtin_amdgcn_sdot4((int)((w.w >> 4) & M4), a.xo[3], d, false);
+    return d - a.corr;
+}
+
+__device__ __forceinline__ void store_out(float* __restrict__ y, long row, float v, int acc) {
+    y[row] = acc ? y[row] + v : v;
+}
+
+// ---------------------------------------------------------------------------
+// A3: y (+)= W x, int8 activation
+// ---------------------------------------------------------------------------
+template <int LPR, int GPL, int R>
+__global__ __launch_bounds__(256) void k_gemv_q4_q8(const uint32_t* __restrict__ xq, const float* __restrict__ xs,
+                                                    const uint4* __restrict__ pack, const uint16_t* __restrict__ scales,
+                                                    float* __restrict__ y, int N, int acc) {
+    constexpr int RPP = 64 / LPR;
+    constexpr int GPR = LPR * GPL;
+    const int lane = threadIdx.x & 63;
+    const long wave = (long)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const int sub = lane / LPR, li = lane % LPR;
+    ActQ8 a[GPL];
+#pragma unroll
+    for (int j = 0; j < GPL; j++) load_act_q8(xq, xs, li + LPR * j, a[j]);
+
+    const long row0 = wave * (RPP * R) + sub;
+    uint4 wv[R][GPL];
+    uint16_t sw[R][GPL];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        long row = row0 + (long)r * RPP;
+        bool ok = row < N;
+#pragma unroll
+        for (int j = 0; j < GPL; j++) {
+            long gi = row * GPR + li + LPR * j;
+            wv[r][j] = ok ? pack[gi] : make_uint4(0, 0, 0, 0);
+            sw[r][j] = ok ? scales[gi] : (uint16_t)0;
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        float accv = 0.0f;
+#pragma unroll
+        for (int j = 0; j < GPL; j++) {
+            int d = group_dot_q8(wv[r][j], a[j]);
+            accv = fmaf((float)d, ti_h2f(sw[r][j]) * a[j].s, accv);
+        }
+        accv = ti_seg_sum<LPR>(accv);
+        long row = row0 + (long)r * RPP;
+        if (li == 0 && row < N) store_out(y, row, accv, acc);
+    }
+}
+
+// Any K % 32 == 0: one wave per row, lanes stride the groups.
+__global__ __launch_bounds__(256) void k_gemv_q4_q8_generic(const uint32_t* __restrict__ xq, const float* __restrict__ xs,
+                                                            const uint4* __restrict__ pack, const uint16_t* __restrict__ scales,
+                                                            float* __restrict__ y, int N, int gpr, int acc) {
+    const int lane = threadIdx.x & 63;
+    const long row = (long)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (row >= N) return;
+    float accv = 0.0f;
+    for (int g = lane; g < gpr; g += 64) {
+        ActQ8 a;
+        load_act_q8(xq, xs, g, a);
+        long gi = row * gpr + g;
+        int d = group_dot_q8(pack[gi], a);
+        accv = fmaf((float)d, ti_h2f(scales[gi]) * a.s, accv);
+    }
+    accv = ti_seg_sum<64>(accv);
+    if (lane == 0) store_out(y, row, accv, acc);
+}
+
+// ---------------------------------------------------------------------------
+// A5: swi = silu(gate x) * (up x)
+// ---------------------------------------------------------------------------
+template <int LPR, int GPL, int R>
+__global__ __launch_bounds__(256) void k_gateup_q4_q8(const uint32_t* __restrict__ xq, const float* __restrict__ xs,
+                                                      const uint4* __restrict__ gpack, const uint16_t* __restrict__ gsc,
+                                                      const uint4* __restrict__ upack, const uint16_t* __restrict__ usc,
+                                                      float* __restrict__ swi, int I) {
+    constexpr int RPP = 64 / LPR;
+    constexpr int GPR = LPR * GPL;
+    const int lane = threadIdx.x & 63;
+    const long wave = (long)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const int sub = lane / LPR, li = lane % LPR;
+    ActQ8 a[GPL];
+#pragma unroll
+    for (int j = 0; j < GPL; j++) load_act_q8(xq, xs, li + LPR * j, a[j]);
+    const long row0 = wave * (RPP * R) + sub;
+    uint4 gw[R][GPL], uw[R][GPL];
+    uint16_t gs[R][GPL], us[R][GPL];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        long row = row0 + (long)r * RPP;
+        bool ok = row < I;
+#pragma unroll
+        for (int j = 0; j < GPL; j++) {
+            long gi = row * GPR + li + LPR * j;
+            gw[r][j] = ok ? gpack[gi] : make_uint4(0, 0, 0, 0);
+            uw[r][j] = ok ? upack[gi] : make_uint4(0, 0, 0, 0);
+            gs[r][j] = ok ? gsc[gi] : (uint16_t)0;
+            us[r][j] = ok ? usc[gi] : (uint16_t)0;
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        float ga = 0.0f, ua = 0.0f;
+#pragma unroll
+        for (int j = 0; j < GPL; j++) {
+            ga = fmaf((float)group_dot_q8(gw[r][j], a[j]), ti_h2f(gs[r][j]) * a[j].s, ga);
+            ua = fmaf((float)group_dot_q8(uw[r][j], a[j]), ti_h2f(us[r][j]) * a[j].s, ua);
+        }
+        ga = ti_seg_sum<LPR>(ga);
+        ua = ti_seg_sum<LPR>(ua);
+        long row = row0 + (long)r * RPP;
+        if (li == 0 && row < I) {
+            float silu = ga / (1.0f + expf(-ga));
+            swi[row] = silu * ua;
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void k_gateup_q4_q8_generic(const uint32_t* __restrict__ xq, const float* __restrict__ xs,
+                                                              const uint4* __restrict__ gpack, const uint16_t* __restrict__ gsc,
+                                                              const uint4* __restrict__ upack, const uint16_t* __restrict__ usc,
+                                                              float* __restrict__ swi, int I, int gpr) {
+    const int lane = threadIdx.x & 63;
+    const long row = (long)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (row >= I) return;
+    float ga = 0.0f, ua = 0.0f;
+    for (int g = lane; g < gpr; g += 64) {
+        ActQ8 a;
+        load_act_q8(xq, xs, g, a);
+        long gi = row * gpr + g;
+        ga = fmaf((float)group_dot_q8(gpack[gi], a), ti_h2f(gsc[gi]) * a.s, ga);
+        ua = fmaf((float)group_dot_q8(upack[gi], a), ti_h2f(usc[gi]) * a.s, ua);
+    }
+    ga = ti_seg_sum<64>(ga);
+    ua = ti_seg_sum<64>(ua);
+    if (lane == 0) swi[row] = ga / (1.0f + expf(-ga)) * ua;
+}
+
+// ---------------------------------------------------------------------------
+// A4: y (+)= W x, f32 activation (lm_head path). Per element: one byte->f32
+// convert and one FMA on the unsigned nibble; the -8 offset is removed once per
+// group (sum n*x - 8*sum x).
+// ---------------------------------------------------------------------------
+struct ActF32 {
+    float x[32];   // element order of the group: x[0..31]
+    float corr;    // 8 * sum x
+};
+
+__device__ __forceinline__ void load_act_f32(const float* __restrict__ x, int g, ActF32& a) {
+    const float4* p = reinterpret_cast<const float4*>(x + (size_t)g * 32);
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        float4 t = p[i];
+        a.x[4 * i] = t.x; a.x[4 * i + 1] = t.y; a.x[4 * i + 2] = t.z; a.x[4 * i + 3] = t.w;
+    }
+#pragma unroll
+    for (int i = 0; i < 32; i++) s += a.x[i];
+    a.corr = 8.0f * s;
+}
+
+__device__ __forceinline__ float word_dot_f32(uint32_t p, const float* x8, float acc) {
+    uint32_t lo = p & M4, hi = (p >> 4) & M4;
+    acc = fmaf((float)(lo & 0xffu), x8[0], acc);
+    acc = fmaf((float)(hi & 0xffu), x8[1], acc);
+    acc = fmaf((float)((lo >> 8) & 0xffu), x8[2], acc);
+    acc = fmaf((float)((hi >> 8) & 0xffu), x8[3], acc);
+    acc = fmaf((float)((lo >> 16) & 0xffu), x8[4], acc);
+    acc = fmaf((float)((hi >> 16) & 0xffu), x8[5], acc);
+    acc = fmaf((float)(lo >> 24), x8[6], acc);
+    acc = fmaf((float)(hi >> 24), x8[7], acc);
+    return acc;
+}
+
+__device__ __forceinline__ float group_dot_f32(const uint4 w, const ActF32& a) {
+    float d0 = word_dot_f32(w.x, a.x + 0, 0.0f);
+    float d1 = word_dot_f32(w.y, a.x + 8, 0.0f);
+    float d2 = word_dot_f32(w.z, a.x + 16, 0.0f);
+    float d3 = word_dot_f32(w.w, a.x + 24, 0.0f);
+    return ((d0 + d1) + (d2 + d3)) - a.corr;
+}
+
+template <int LPR, int GPL, int R>
+__global__ __launch_bounds__(256) void k_gemv_q4_f32(const float* __restrict__ x, const uint4* __restrict__ pack,
+                                                     const uint16_t* __restrict__ scales, float* __restrict__ y,
+                                                     int N, int acc) {
+    constexpr int RPP = 64 / LPR;
+    constexpr int GPR = LPR * GPL;
+    const int lane = threadIdx.x & 63;
+    const long wave = (long)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const int sub = lane / LPR, li = lane % LPR;
+    ActF32 a[GPL];
+#pragma unroll
+    for (int j = 0; j < GPL; j++) load_act_f32(x, li + LPR * j, a[j]);
+    const long row0 = wave * (RPP * R) + sub;
+    uint4 wv[R][GPL];
+    uint16_t sw[R][GPL];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        long row = row0 + (long)r * RPP;
+        bool ok = row < N;
+#pragma unroll
+        for (int j = 0; j < GPL; j++) {
+            long gi = row * GPR + li + LPR * j;
+            wv[r][j] = ok ? pack[gi] : make_uint4(0, 0, 0, 0);
+            sw[r][j] = ok ? scales[gi] : (uint16_t)0;
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        float accv = 0.0f;
+#pragma unroll
+        for (int j = 0; j < GPL; j++) accv = fmaf(group_dot_f32(wv[r][j], a[j]), ti_h2f(sw[r][j]), accv);
+        accv = ti_seg_sum<LPR>(accv);
+        long row = row0 + (long)r * RPP;
+        if (li == 0 && row < N) store_out(y, row, accv, acc);
+    }
+}
+
+__global__ __launch_bounds__(256) void k_gemv_q4_f32_generic(const float* __restrict__ x, const uint4* __restrict__ pack,
+                                                             const uint16_t* __restrict__ scales, float* __restrict__ y,
+                                                             int N, int gpr, int acc) {
+    const int lane = threadIdx.x & 63;
+    const long row = (long)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (row >= N) return;
+    float accv = 0.0f;
+    for (int g = lane; g < gpr; g += 64) {
+        ActF32 a;
+        load_act_f32(x, g, a);
+        long gi = row * gpr + g;
+        accv = fmaf(group_dot_f32(pack[gi], a), ti_h2f(scales[gi]), accv);
+    }
+    accv = ti_seg_sum<64>(accv);
+    if (lane == 0) store_out(y, row, accv, acc);
+}
+
+// Debug: exact int32 per (row, group).
+__global__ void k_group_dots(const uint32_t* __restrict__ xq, const uint4* __restrict__ pack, int32_t* __restrict__ dots,
+                             long total, int gpr) {
+    long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= total) return;
+    int g = (int)(i % gpr);
+    ActQ8 a;
+    load_act_q8(xq, nullptr, g, a);
+    dots[i] = group_dot_q8(pack[i], a);
+}
+
+// ---- launch helpers ----------------------------------------------------------
+struct Shape {
+    int lpr, gpl;
+};
+
+// lanes per row = the power-of-two part of gpr (capped at 64); groups per lane = gpr / lanes
+Shape pick_shape(int gpr) {
+    int lpr = 1;
+    while (lpr < 64 && (gpr % (lpr * 2)) == 0) lpr *= 2;
+    return {lpr, gpr / lpr};
+}
+
+int pick_R(long waves_r1) {
+    if (waves_r1 >= 16384) return 4;
+    if (waves_r1 >= 4096) return 2;
+    return 1;
+}
+
+void grid_for(long waves, unsigned& blocks, unsigned& threads) {
+    threads = waves >= 1024 ? 256 : 64;
+    long wpb = threads / 64;
+    blocks = (unsigned)((waves + wpb - 1) / wpb);
+}
+
+#define GEMV_CASES(X)  \
+    X(1, 1) X(1, 3) X(2, 1) X(2, 3) X(4, 1) X(4, 3) X(8, 1) X(8, 3) X(16, 1) X(16, 3) \
+    X(32, 1) X(32, 3) X(64, 1) X(64, 2) X(64, 3) X(64, 4) X(64, 6) X(64, 8)
+
+}  // namespace
+
+int ti_gemv_q4_q8_launch(ti_ctx* c, const uint32_t* xq, const float* xs, const uint32_t* pack, const uint16_t* scales,
+                         float* y, int N, int K, int acc) {
+    int gpr = K / 32;
+    Shape s = pick_shape(gpr);
+    long rpp = 64 / s.lpr;
+    long waves1 = (N + rpp - 1) / rpp;
+    int R = pick_R(waves1);
+    long waves = (N + rpp * R - 1) / (rpp * R);
+    unsigned blocks, threads;
+    grid_for(waves, blocks, threads);
+    const uint4* p4 = reinterpret_cast<const uint4*>(pack);
+#define X(L, G)                                                                                                   \
+    if (s.lpr == L && s.gpl == G) {                                                                               \
+        if (R == 4) k_gemv_q4_q8<L, G, 4><<<blocks, threads, 0, c->stream>>>(xq, xs, p4, scales, y, N, acc);      \
+        else if (R == 2) k_gemv_q4_q8<L, G, 2><<<blocks, threads, 0, c->stream>>>(xq, xs, p4, scales, y, N, acc); \
+        else k_gemv_q4_q8<L, G, 1><<<blocks, threads, 0, c->stream>>>(xq, xs, p4, scales, y, N, acc);             \
+        TI_LAUNCHED("k_gemv_q4_q8");                                                                              \
+        return TI_OK;                                                                                             \
+    }
+    GEMV_CASES(X)
+#undef X
+    unsigned gb, gt;
+    grid_for(N, gb, gt);
+    k_gemv_q4_q8_generic<<<gb, gt, 0, c->stream>>>(xq, xs, p4, scales, y, N, gpr, acc);
+    TI_LAUNCHED("k_gemv_q4_q8_generic");
+    return TI_OK;
+}
+
+static inline bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+extern "C" int ti_gemv_q4_q8(ti_ctx* c, const uint32_t* xq, const float* xs, const uint32_t* pack, const uint16_t* scales,
+                             float* y, int N, int K, int acc) {
+    TI_CHECK_CTX(c);
+    TI_REQUIRE(xq && xs && pack && scales && y, "ti_gemv_q4_q8: null buffer");
+    TI_REQUIRE(N > 0 && K > 0 && K % 32 == 0, "ti_gemv_q4_q8: need N>0 and K a positive multiple of 32 (N=%d K=%d)", N, K);
+    TI_REQUIRE(al16(xq) && al16(pack), "ti_gemv_q4_q8: xq and pack must be 16-byte aligned");
+    return ti_gemv_q4_q8_launch(c, xq, xs, pack, scales, y, N, K, acc);
+}
+
+int ti_gemv_q4_f32_launch(ti_ctx* c, const float* x, const uint32_t* pack, const uint16_t* scales, float* y, int N, int K,
+                          int acc) {
+    int gpr = K / 32;
+    Shape s = pick_shape(gpr);
+    long rpp = 64 / s.lpr;
+    long waves1 = (N + rpp - 1) / rpp;
+    int R = pick_R(waves1);
+    long waves = (N + rpp * R - 1) / (rpp * R);
+    unsigned blocks, threads;
+    grid_for(waves, blocks, threads);
+    const uint4* p4 = reinterpret_cast<const uint4*>(pack);
+#define X(L, G)                                                                                               \
+    if (s.lpr == L && s.gpl == G && G <= 3) {                                                                 \
+        if (R == 4) k_gemv_q4_f32<L, G, 4><<<blocks, threads, 0, c->stream>>>(x, p4, scales, y, N, acc);      \
+        else if (R == 2) k_gemv_q4_f32<L, G, 2><<<blocks, threads, 0, c->stream>>>(x, p4, scales, y, N, acc); \
+        else k_gemv_q4_f32<L, G, 1><<<blocks, threads, 0, c->stream>>>(x, p4, scales, y, N, acc);             \
+        TI_LAUNCHED("k_gemv_q4_f32");                                                                         \
+        return TI_OK;                                                                                         \
+    }
+    X(1, 1) X(2, 1) X(4, 1) X(8, 1) X(16, 1) X(32, 1) X(64, 1) X(64, 2) X(32, 3) X(64, 3)
+#undef X
+    unsigned gb, gt;
+    grid_for(N, gb, gt);
+    k_gemv_q4_f32_generic<<<gb, gt, 0, c->stream>>>(x, p4, scales, y, N, gpr, acc);
+    TI_LAUNCHED("k_gemv_q4_f32_generic");
+    return TI_OK;
+}
+
+extern "C" int ti_gemv_q4_f32(ti_ctx* c, const float* x, const uint32_t* pack, const uint16_t* scales, float* y, int N,
+                              int K, int acc) {
+    TI_CHECK_CTX(c);
+    TI_REQUIRE(x && pack && scales && y, "ti_gemv_q4_f32: null buffer");
+    TI_REQUIRE(N > 0 && K > 0 && K % 32 == 0, "ti_gemv_q4_f32: need N>0 and K a positive multiple of 32 (N=%d K=%d)", N, K);
+    TI_REQUIRE(al16(x) && al16(pack), "ti_gemv_q4_f32: x and pack must be 16-byte aligned");
+    return ti_gemv_q4_f32_launch(c, x, pack, scales, y, N, K, acc);
+}
+
+int ti_gateup_launch(ti_ctx* c, const uint32_t* xq, const float* xs, const uint32_t* gpack, const uint16_t* gsc,
+                     const uint32_t* upack, const uint16_t* usc, float* swi, int I, int H) {
+    int gpr = H / 32;
+    Shape s = pick_shape(gpr);
+    long rpp = 64 / s.lpr;
+    long waves1 = (I + rpp - 1) / rpp;
+    int R = waves1 >= 8192 ? 2 : 1;
+    long waves = (I + rpp * R - 1) / (rpp * R);
+    unsigned blocks, threads;
+    grid_for(waves, blocks, threads);
+    const uint4* g4 = reinterpret_cast<const uint4*>(gpack);
+    const uint4* u4 = reinterpret_cast<const uint4*>(upack);
+#define X(L, G)                                                                                                        \
+    if (s.lpr == L && s.gpl == G) {                                                                                    \
+        if (R == 2) k_gateup_q4_q8<L, G, 2><<<blocks, threads, 0, c->stream>>>(xq, xs, g4, gsc, u4, usc, swi, I);      \
+        else k_gateup_q4_q8<L, G, 1><<<blocks, threads, 0, c->stream>>>(xq, xs, g4, gsc, u4, usc, swi, I);             \
+        TI_LAUNCHED("k_gateup_q4_q8");                                                                                 \
+        return TI_OK;                                                                                                  \
+    }
+    GEMV_CASES(X)
+#undef X
+    unsigned gb, gt;
+    grid_for(I, gb, gt);
+    k_gateup_q4_q8_generic<<<gb, gt, 0, c->stream>>>(xq, xs, g4, gsc, u4, usc, swi, I, gpr);
+    TI_LAUNCHED("k_gateup_q4_q8_generic");
+    return TI_OK;
+}
+
+extern "C" int ti_gateup_silu_q4(ti_ctx* c, const uint32_t* xq, const float* xs, const uint32_t* gpack, const uint16_t* gsc,
+                                 const uint32_t* upack, const uint16_t* usc, float* swi, int I, int H) {
+    TI_CHECK_CTX(c);
+    TI_REQUIRE(xq && xs && gpack && gsc && upack && usc && swi, "ti_gateup_silu_q4: null buffer");
+    TI_REQUIRE(I > 0 && H > 0 && H % 32 == 0, "ti_gateup_silu_q4: need I>0 and H a positive multiple of 32 (I=%d H=%d)", I, H);
+    TI_REQUIRE(al16(xq) && al16(gpack) && al16(upack), "ti_gateup_silu_q4: xq and packs must be 16-byte aligned");
+    return ti_gateup_launch(c, xq, xs, gpack, gsc, upack, usc, swi, I, H);
+}
+
+extern "C" int ti_group_dots_q4_q8(ti_ctx* c, const uint32_t* xq, const uint32_t* pack, int32_t* dots, int N, int K) {
+    TI_CHECK_CTX(c);
+    TI_REQUIRE(xq && pack && dots, "ti_group_dots_q4_q8: null buffer");
+    TI_REQUIRE(N > 0 && K > 0 && K % 32 == 0, "ti_group_dots_q4_q8: bad shape (N=%d K=%d)", N, K);
+    long total = (long)N * (K / 32);
+    k_group_dots<<<(unsigned)((total + 255) / 256), 256, 0, c->stream>>>(xq, reinterpret_cast<const uint4*>(pack), dots,
+                                                                        total, K / 32);
+    TI_LAUNCHED("k_group_dots");
+    return TI_OK;
+}
+
+// linearQ router: the activation scratch lives in the context (allocated once at
+// init), like the reference's _dp4/_dp4g buffers.
+int ti_quant_act_q8_async(ti_ctx* c, const float* x, uint32_t* xq, float* xs, int32_t* xsum, int groups);
+int ti_gemm_q4_q8_launch(ti_ctx* c, const uint32_t* xq, const float* xs, const uint32_t* pack, const uint16_t* scales,
+                         float* y, int T, int N, int K, int acc);
+
+extern "C" int ti_linear_q4(ti_ctx* c, const float* x, const uint32_t* pack, const uint16_t* scales, float* y, int T, int N,
+                            int K, int acc) {
+    TI_CHECK_CTX(c);
+    TI_REQUIRE(x && pack && scales && y, "ti_linear_q4: null buffer");
+    TI_REQUIRE(T > 0 && N > 0 && K > 0 && K % 32 == 0, "ti_linear_q4: bad shape (T=%d N=%d K=%d)", T, N, K);
+    TI_REQUIRE(K <= TI_ACT_CAP && T <= TI_ACT_TMAX, "ti_linear_q4: K<=%d and T<=%d required", TI_ACT_CAP, TI_ACT_TMAX);
+    TI_REQUIRE(al16(x) && al16(pack), "ti_linear_q4: x and pack must be 16-byte aligned");
+    if (T == 1 && N >= 16384) return ti_gemv_q4_f32_launch(c, x, pack, scales, y, N, K, acc);
+    int rc = ti_quant_act_q8_async(c, x, c->act_q, c->act_s, nullptr, T * (K / 32));
+    if (rc) return rc;
+    if (T == 1) return ti_gemv_q4_q8_launch(c, c->act_q, c->act_s, pack, scales, y, N, K, acc);
+    return ti_gemm_q4_q8_launch(c, c->act_q, c->act_s, pack, scales, y, T, N, K, acc);
+}

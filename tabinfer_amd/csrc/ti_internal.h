@@ -1,0 +1,67 @@
+// ti_internal.h — shared host/device helpers for libtabinfer (gfx950 only).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+#include "../../include/ti.h"
+
+// ---- host-side error plumbing ------------------------------------------------
+int ti_fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int ti_hip_fail(hipError_t e, const char* what);
+
+#define TI_CHECK_CTX(ctx) do { if (!(ctx)) return ti_fail(TI_ERR_INVALID, "%s: null context", __func__); } while (0)
+#define TI_REQUIRE(cond, ...) do { if (!(cond)) return ti_fail(TI_ERR_INVALID, __VA_ARGS__); } while (0)
+#define TI_HIP(call) do { hipError_t _e = (call); if (_e != hipSuccess) return ti_hip_fail(_e, #call); } while (0)
+#define TI_LAUNCHED(name) do { hipError_t _e = hipGetLastError(); if (_e != hipSuccess) return ti_hip_fail(_e, name); } while (0)
+
+struct ti_ctx {
+    int device;
+    hipStream_t stream;
+    hipEvent_t ev[64];
+    int capturing;
+    // persistent scratch (allocated at init, never reallocated, so calls may be
+    // captured into graphs): int8 activation for the linearQ router, split-KV
+    // partials, argmax partials.
+    uint32_t* act_q;      // [TI_ACT_CAP/4 * TI_ACT_TMAX]
+    float* act_s;         // [TI_ACT_CAP/32 * TI_ACT_TMAX]
+    int32_t* act_sum;     // [TI_ACT_CAP/16]
+    float* attn_po;       // split-KV partial outputs
+    float* attn_ml;       // split-KV (m, l)
+    float* amax_v;        // argmax partial values
+    uint32_t* amax_i;     // argmax partial indices
+    uint32_t* moe_cnt;    // MoE counting sort: counts / offsets / fill / sorted index
+    uint32_t* moe_off;
+    uint32_t* moe_fill;
+    uint32_t* moe_sidx;
+};
+
+struct ti_graph {
+    hipGraph_t graph;
+    hipGraphExec_t exec;
+    int device;
+};
+
+// Scratch capacities (elements). Activation rows up to 65536 wide, up to 256
+// tokens for the batched path; split-KV partials for up to 64 heads x 512 splits.
+#define TI_ACT_CAP 65536
+#define TI_ACT_TMAX 256
+#define TI_ATTN_HEADS_MAX 64
+#define TI_ATTN_SPLITS_MAX 512
+#define TI_ATTN_HD_MAX 128
+#define TI_AMAX_PARTS 1024
+#define TI_MOE_P_MAX 8192
+#define TI_MOE_E_MAX 256
+
+// ---- device helpers -----------------------------------------------------------
+// f16 bits -> f32 (exact).
+__device__ __forceinline__ float ti_h2f(uint16_t h) {
+    return (float)__builtin_bit_cast(_Float16, h);
+}
+
+// Wavefront-64 butterfly sum over lanes that share the same (lane / width).
+template <int WIDTH>
+__device__ __forceinline__ float ti_seg_sum(float v) {
+#pragma unroll
+    for (int o = WIDTH / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
