@@ -69,6 +69,44 @@ __device__ __forceinline__ void store_out(float* __restrict__ y, long row, float
     y[row] = acc ? y[row] + v : v;
 }
 
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+
+// Weights are streamed exactly once per call: non-temporal loads keep them from
+// displacing the (re-read) activation and scale lines in the caches.
+__device__ __forceinline__ uint4 ld_nt(const uint4* p) {
+    v4u v = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint16_t ld_nt(const uint16_t* p) { return __builtin_nontemporal_load(p); }
+
+// Sum R per-lane accumulators across the LPR lanes that share them, leaving the
+// total of accumulator (li / (LPR/R)) in every lane: each of the first log2(R)
+// butterfly steps hands half of the remaining accumulators to the partner lane,
+// so the whole reduction costs R-1 + log2(LPR/R) shuffles instead of R*log2(LPR).
+template <int LPR, int R>
+__device__ __forceinline__ float transpose_reduce(float (&v)[R], int li) {
+    static_assert(R <= LPR || LPR == 1, "R must not exceed the lanes per row");
+    int k = R;
+#pragma unroll
+    for (int o = LPR / 2; o > 0; o >>= 1) {
+        if (k > 1) {
+            const bool up = (li & o) != 0;
+#pragma unroll
+            for (int i = 0; i < R / 2; i++) {
+                if (i < k / 2) {
+                    float send = up ? v[i] : v[i + k / 2];
+                    float keep = up ? v[i + k / 2] : v[i];
+                    v[i] = keep + __shfl_xor(send, o, 64);
+                }
+            }
+            k >>= 1;
+        } else {
+            v[0] += __shfl_xor(v[0], o, 64);
+        }
+    }
+    return v[0];
+}
+
 // ---------------------------------------------------------------------------
 // A3: y (+)= W x, int8 activation
 // ---------------------------------------------------------------------------
@@ -79,37 +117,62 @@ __global__ __launch_bounds__(256) void k_gemv_q4_q8(const uint32_t* __restrict__
     constexpr int RPP = 64 / LPR;
     constexpr int GPR = LPR * GPL;
     const int lane = threadIdx.x & 63;
-    const long wave = (long)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     const int sub = lane / LPR, li = lane % LPR;
+    const long nwaves = (long)gridDim.x * (blockDim.x >> 6);
+    const long nblocks = (N + RPP * R - 1) / (RPP * R);
+    long b = (long)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (b >= nblocks) return;
+    // every weight/scale load of a block is issued before any arithmetic; rows past
+    // N re-read row N-1 (a valid address, result discarded), so no load sits
+    // behind a branch
+    uint4 wv[2][R][GPL];
+    uint16_t sw[2][R][GPL];
+    auto load = [&](int buf, long blk) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            long row = blk * (RPP * R) + sub + (long)r * RPP;
+            row = row < N ? row : N - 1;
+#pragma unroll
+            for (int j = 0; j < GPL; j++) {
+                long gi = row * GPR + li + LPR * j;
+                wv[buf][r][j] = ld_nt(pack + gi);
+                sw[buf][r][j] = ld_nt(scales + gi);
+            }
+        }
+    };
+    load(0, b);
     ActQ8 a[GPL];
 #pragma unroll
     for (int j = 0; j < GPL; j++) load_act_q8(xq, xs, li + LPR * j, a[j]);
-
-    const long row0 = wave * (RPP * R) + sub;
-    uint4 wv[R][GPL];
-    uint16_t sw[R][GPL];
+    auto finish = [&](int buf, long blk) {
+        float accv[R];
 #pragma unroll
-    for (int r = 0; r < R; r++) {
-        long row = row0 + (long)r * RPP;
-        bool ok = row < N;
+        for (int r = 0; r < R; r++) {
+            float t = 0.0f;
 #pragma unroll
-        for (int j = 0; j < GPL; j++) {
-            long gi = row * GPR + li + LPR * j;
-            wv[r][j] = ok ? pack[gi] : make_uint4(0, 0, 0, 0);
-            sw[r][j] = ok ? scales[gi] : (uint16_t)0;
+            for (int j = 0; j < GPL; j++) {
+                int d = group_dot_q8(wv[buf][r][j], a[j]);
+                t = fmaf((float)d, ti_h2f(sw[buf][r][j]) * a[j].s, t);
+            }
+            accv[r] = t;
         }
-    }
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-        float accv = 0.0f;
-#pragma unroll
-        for (int j = 0; j < GPL; j++) {
-            int d = group_dot_q8(wv[r][j], a[j]);
-            accv = fmaf((float)d, ti_h2f(sw[r][j]) * a[j].s, accv);
-        }
-        accv = ti_seg_sum<LPR>(accv);
-        long row = row0 + (long)r * RPP;
-        if (li == 0 && row < N) store_out(y, row, accv, acc);
+        float tot = transpose_reduce<LPR, R>(accv, li);
+        constexpr int SPAN = LPR / R;        // lanes holding the same row total
+        const long row = blk * (RPP * R) + sub + (long)(li / SPAN) * RPP;
+        if ((li % SPAN) == 0 && row < N) store_out(y, row, tot, acc);
+    };
+    // persistent waves: prefetch block b+nwaves while finishing block b
+    for (;;) {
+        long nb = b + nwaves;
+        if (nb < nblocks) load(1, nb);
+        finish(0, b);
+        if (nb >= nblocks) break;
+        b = nb;
+        nb = b + nwaves;
+        if (nb < nblocks) load(0, nb);
+        finish(1, b);
+        if (nb >= nblocks) break;
+        b = nb;
     }
 }
 
@@ -145,40 +208,44 @@ __global__ __launch_bounds__(256) void k_gateup_q4_q8(const uint32_t* __restrict
     const int lane = threadIdx.x & 63;
     const long wave = (long)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     const int sub = lane / LPR, li = lane % LPR;
-    ActQ8 a[GPL];
-#pragma unroll
-    for (int j = 0; j < GPL; j++) load_act_q8(xq, xs, li + LPR * j, a[j]);
     const long row0 = wave * (RPP * R) + sub;
     uint4 gw[R][GPL], uw[R][GPL];
     uint16_t gs[R][GPL], us[R][GPL];
 #pragma unroll
     for (int r = 0; r < R; r++) {
         long row = row0 + (long)r * RPP;
-        bool ok = row < I;
+        row = row < I ? row : I - 1;
 #pragma unroll
         for (int j = 0; j < GPL; j++) {
             long gi = row * GPR + li + LPR * j;
-            gw[r][j] = ok ? gpack[gi] : make_uint4(0, 0, 0, 0);
-            uw[r][j] = ok ? upack[gi] : make_uint4(0, 0, 0, 0);
-            gs[r][j] = ok ? gsc[gi] : (uint16_t)0;
-            us[r][j] = ok ? usc[gi] : (uint16_t)0;
+            gw[r][j] = ld_nt(gpack + gi);
+            uw[r][j] = ld_nt(upack + gi);
+            gs[r][j] = ld_nt(gsc + gi);
+            us[r][j] = ld_nt(usc + gi);
         }
     }
+    ActQ8 a[GPL];
+#pragma unroll
+    for (int j = 0; j < GPL; j++) load_act_q8(xq, xs, li + LPR * j, a[j]);
+    float ga[R], ua[R];
 #pragma unroll
     for (int r = 0; r < R; r++) {
-        float ga = 0.0f, ua = 0.0f;
+        float tg = 0.0f, tu = 0.0f;
 #pragma unroll
         for (int j = 0; j < GPL; j++) {
-            ga = fmaf((float)group_dot_q8(gw[r][j], a[j]), ti_h2f(gs[r][j]) * a[j].s, ga);
-            ua = fmaf((float)group_dot_q8(uw[r][j], a[j]), ti_h2f(us[r][j]) * a[j].s, ua);
+            tg = fmaf((float)group_dot_q8(gw[r][j], a[j]), ti_h2f(gs[r][j]) * a[j].s, tg);
+            tu = fmaf((float)group_dot_q8(uw[r][j], a[j]), ti_h2f(us[r][j]) * a[j].s, tu);
         }
-        ga = ti_seg_sum<LPR>(ga);
-        ua = ti_seg_sum<LPR>(ua);
-        long row = row0 + (long)r * RPP;
-        if (li == 0 && row < I) {
-            float silu = ga / (1.0f + expf(-ga));
-            swi[row] = silu * ua;
-        }
+        ga[r] = tg;
+        ua[r] = tu;
+    }
+    float g = transpose_reduce<LPR, R>(ga, li);
+    float u = transpose_reduce<LPR, R>(ua, li);
+    constexpr int SPAN = LPR / R;
+    const long row = row0 + (long)(li / SPAN) * RPP;
+    if ((li % SPAN) == 0 && row < I) {
+        float silu = g / (1.0f + expf(-g));
+        swi[row] = silu * u;
     }
 }
 
@@ -246,6 +313,74 @@ __device__ __forceinline__ float group_dot_f32(const uint4 w, const ActF32& a) {
     return ((d0 + d1) + (d2 + d3)) - a.corr;
 }
 
+// f32 activation as exact fixed point: per 32-group, x_j = X_j * 2^(ex-22) with
+// |X_j| <= 2^22 (ex = exponent of the group absmax), X split into three signed
+// int8 limbs X = l2*65536 + l1*256 + l0. Each limb dots with the nibbles through
+// v_dot4_i32_i8 exactly; the only approximation is rounding x to 22 bits below its
+// group maximum (relative 2^-23), i.e. at the level of f32 rounding itself.
+struct ActLimb {
+    int e[3][4], o[3][4];   // limb l, weight word m: even / odd element bytes
+    int corr[3];            // 8 * sum of limb l
+    float S;                // 2^(ex-22)
+};
+
+__device__ __forceinline__ void load_act_limbs(const float* __restrict__ x, int g, ActLimb& a) {
+    const float4* p = reinterpret_cast<const float4*>(x + (size_t)g * 32);
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        float4 t = p[i];
+        v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
+    }
+    float mx = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 32; j++) mx = fmaxf(mx, fabsf(v[j]));
+    int ex = 0;
+    if (mx > 0.0f) (void)frexpf(mx, &ex);          // mx < 2^ex
+    a.S = ldexpf(1.0f, ex - 22);
+    int lb[3][32];
+#pragma unroll
+    for (int j = 0; j < 32; j++) {
+        int X = mx > 0.0f ? (int)rintf(ldexpf(v[j], 22 - ex)) : 0;
+        int l0 = ((X & 0xff) ^ 0x80) - 0x80;
+        int X1 = (X - l0) >> 8;
+        int l1 = ((X1 & 0xff) ^ 0x80) - 0x80;
+        int l2 = (X1 - l1) >> 8;
+        lb[0][j] = l0; lb[1][j] = l1; lb[2][j] = l2;
+    }
+#pragma unroll
+    for (int l = 0; l < 3; l++) {
+        int sum = 0;
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            const int* q = lb[l] + 8 * m;
+            a.e[l][m] = (int)((uint32_t)(q[0] & 0xff) | ((uint32_t)(q[2] & 0xff) << 8) |
+                              ((uint32_t)(q[4] & 0xff) << 16) | ((uint32_t)(q[6] & 0xff) << 24));
+            a.o[l][m] = (int)((uint32_t)(q[1] & 0xff) | ((uint32_t)(q[3] & 0xff) << 8) |
+                              ((uint32_t)(q[5] & 0xff) << 16) | ((uint32_t)(q[7] & 0xff) << 24));
+            sum += q[0] + q[1] + q[2] + q[3] + q[4] + q[5] + q[6] + q[7];
+        }
+        a.corr[l] = 8 * sum;
+    }
+}
+
+// sum_j (n_j - 8) * x_j for one 16-byte weight group, through the three limbs
+__device__ __forceinline__ float group_dot_limbs(const uint4 w, const ActLimb& a) {
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+    int d[3] = {0, 0, 0};
+#pragma unroll
+    for (int m = 0; m < 4; m++) {
+        int lo = (int)(ws[m] & M4), hi = (int)((ws[m] >> 4) & M4);
+#pragma unroll
+        for (int l = 0; l < 3; l++) {
+            d[l] = __builtin_amdgcn_sdot4(lo, a.e[l][m], d[l], false);
+            d[l] = __builtin_amdgcn_sdot4(hi, a.o[l][m], d[l], false);
+        }
+    }
+    int t = (d[2] - a.corr[2]) * 256 + (d[1] - a.corr[1]);     // |t| < 2^23: exact in f32
+    return fmaf((float)t, 256.0f, (float)(d[0] - a.corr[0])) * a.S;
+}
+
 template <int LPR, int GPL, int R>
 __global__ __launch_bounds__(256) void k_gemv_q4_f32(const float* __restrict__ x, const uint4* __restrict__ pack,
                                                      const uint16_t* __restrict__ scales, float* __restrict__ y,
@@ -253,33 +388,56 @@ __global__ __launch_bounds__(256) void k_gemv_q4_f32(const float* __restrict__ x
     constexpr int RPP = 64 / LPR;
     constexpr int GPR = LPR * GPL;
     const int lane = threadIdx.x & 63;
-    const long wave = (long)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     const int sub = lane / LPR, li = lane % LPR;
-    ActF32 a[GPL];
+    const long nwaves = (long)gridDim.x * (blockDim.x >> 6);
+    const long nblocks = (N + RPP * R - 1) / (RPP * R);
+    long b = (long)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (b >= nblocks) return;
+    ActLimb a[GPL];
 #pragma unroll
-    for (int j = 0; j < GPL; j++) load_act_f32(x, li + LPR * j, a[j]);
-    const long row0 = wave * (RPP * R) + sub;
-    uint4 wv[R][GPL];
-    uint16_t sw[R][GPL];
+    for (int j = 0; j < GPL; j++) load_act_limbs(x, li + LPR * j, a[j]);
+    uint4 wv[2][R][GPL];
+    uint16_t sw[2][R][GPL];
+    auto load = [&](int buf, long blk) {
 #pragma unroll
-    for (int r = 0; r < R; r++) {
-        long row = row0 + (long)r * RPP;
-        bool ok = row < N;
+        for (int r = 0; r < R; r++) {
+            long row = blk * (RPP * R) + sub + (long)r * RPP;
+            row = row < N ? row : N - 1;
 #pragma unroll
-        for (int j = 0; j < GPL; j++) {
-            long gi = row * GPR + li + LPR * j;
-            wv[r][j] = ok ? pack[gi] : make_uint4(0, 0, 0, 0);
-            sw[r][j] = ok ? scales[gi] : (uint16_t)0;
+            for (int j = 0; j < GPL; j++) {
+                long gi = row * GPR + li + LPR * j;
+                wv[buf][r][j] = ld_nt(pack + gi);
+                sw[buf][r][j] = ld_nt(scales + gi);
+            }
         }
-    }
+    };
+    auto finish = [&](int buf, long blk) {
+        float accv[R];
 #pragma unroll
-    for (int r = 0; r < R; r++) {
-        float accv = 0.0f;
+        for (int r = 0; r < R; r++) {
+            float t = 0.0f;
 #pragma unroll
-        for (int j = 0; j < GPL; j++) accv = fmaf(group_dot_f32(wv[r][j], a[j]), ti_h2f(sw[r][j]), accv);
-        accv = ti_seg_sum<LPR>(accv);
-        long row = row0 + (long)r * RPP;
-        if (li == 0 && row < N) store_out(y, row, accv, acc);
+            for (int j = 0; j < GPL; j++) t = fmaf(group_dot_limbs(wv[buf][r][j], a[j]), ti_h2f(sw[buf][r][j]), t);
+            accv[r] = t;
+        }
+        float tot = transpose_reduce<LPR, R>(accv, li);
+        constexpr int SPAN = LPR / R;
+        const long row = blk * (RPP * R) + sub + (long)(li / SPAN) * RPP;
+        if ((li % SPAN) == 0 && row < N) store_out(y, row, tot, acc);
+    };
+    // persistent waves: prefetch block b+nwaves while finishing block b
+    load(0, b);
+    for (;;) {
+        long nb = b + nwaves;
+        if (nb < nblocks) load(1, nb);
+        finish(0, b);
+        if (nb >= nblocks) break;
+        b = nb;
+        nb = b + nwaves;
+        if (nb < nblocks) load(0, nb);
+        finish(1, b);
+        if (nb >= nblocks) break;
+        b = nb;
     }
 }
 
@@ -323,16 +481,25 @@ Shape pick_shape(int gpr) {
     return {lpr, gpr / lpr};
 }
 
-int pick_R(long waves_r1) {
-    if (waves_r1 >= 16384) return 4;
-    if (waves_r1 >= 4096) return 2;
-    return 1;
+int pick_R(long waves_r1, int lpr) {
+    int R = waves_r1 >= 8192 ? 4 : waves_r1 >= 4096 ? 2 : 1;
+    while (R > lpr) R >>= 1;
+    return R;
 }
 
 void grid_for(long waves, unsigned& blocks, unsigned& threads) {
     threads = waves >= 1024 ? 256 : 64;
     long wpb = threads / 64;
     blocks = (unsigned)((waves + wpb - 1) / wpb);
+}
+
+// Persistent launches stop at TI_RESIDENT_WAVES waves (256 CUs x 4 SIMDs x 4, what
+// fits at the ~88-110 VGPRs of the double-buffered kernels):
+// beyond that each wave loops over row blocks with a one-block prefetch.
+constexpr long TI_RESIDENT_WAVES = 256 * 4 * 4;
+void grid_persistent(long blocks_total, unsigned& blocks, unsigned& threads) {
+    long waves = blocks_total < TI_RESIDENT_WAVES ? blocks_total : TI_RESIDENT_WAVES;
+    grid_for(waves, blocks, threads);
 }
 
 #define GEMV_CASES(X)  \
@@ -347,15 +514,15 @@ int ti_gemv_q4_q8_launch(ti_ctx* c, const uint32_t* xq, const float* xs, const u
     Shape s = pick_shape(gpr);
     long rpp = 64 / s.lpr;
     long waves1 = (N + rpp - 1) / rpp;
-    int R = pick_R(waves1);
+    int R = pick_R(waves1, s.lpr);
     long waves = (N + rpp * R - 1) / (rpp * R);
     unsigned blocks, threads;
-    grid_for(waves, blocks, threads);
+    grid_persistent(waves, blocks, threads);
     const uint4* p4 = reinterpret_cast<const uint4*>(pack);
 #define X(L, G)                                                                                                   \
     if (s.lpr == L && s.gpl == G) {                                                                               \
-        if (R == 4) k_gemv_q4_q8<L, G, 4><<<blocks, threads, 0, c->stream>>>(xq, xs, p4, scales, y, N, acc);      \
-        else if (R == 2) k_gemv_q4_q8<L, G, 2><<<blocks, threads, 0, c->stream>>>(xq, xs, p4, scales, y, N, acc); \
+        if (R == 4) k_gemv_q4_q8<L, G, (L >= 4 ? 4 : 1)><<<blocks, threads, 0, c->stream>>>(xq, xs, p4, scales, y, N, acc); \
+        else if (R == 2) k_gemv_q4_q8<L, G, (L >= 2 ? 2 : 1)><<<blocks, threads, 0, c->stream>>>(xq, xs, p4, scales, y, N, acc); \
         else k_gemv_q4_q8<L, G, 1><<<blocks, threads, 0, c->stream>>>(xq, xs, p4, scales, y, N, acc);             \
         TI_LAUNCHED("k_gemv_q4_q8");                                                                              \
         return TI_OK;                                                                                             \
@@ -386,15 +553,15 @@ int ti_gemv_q4_f32_launch(ti_ctx* c, const float* x, const uint32_t* pack, const
     Shape s = pick_shape(gpr);
     long rpp = 64 / s.lpr;
     long waves1 = (N + rpp - 1) / rpp;
-    int R = pick_R(waves1);
+    int R = pick_R(waves1, s.lpr);
     long waves = (N + rpp * R - 1) / (rpp * R);
     unsigned blocks, threads;
-    grid_for(waves, blocks, threads);
+    grid_persistent(waves, blocks, threads);
     const uint4* p4 = reinterpret_cast<const uint4*>(pack);
 #define X(L, G)                                                                                               \
     if (s.lpr == L && s.gpl == G && G <= 3) {                                                                 \
-        if (R == 4) k_gemv_q4_f32<L, G, 4><<<blocks, threads, 0, c->stream>>>(x, p4, scales, y, N, acc);      \
-        else if (R == 2) k_gemv_q4_f32<L, G, 2><<<blocks, threads, 0, c->stream>>>(x, p4, scales, y, N, acc); \
+        if (R == 4) k_gemv_q4_f32<L, G, (L >= 4 ? 4 : 1)><<<blocks, threads, 0, c->stream>>>(x, p4, scales, y, N, acc); \
+        else if (R == 2) k_gemv_q4_f32<L, G, (L >= 2 ? 2 : 1)><<<blocks, threads, 0, c->stream>>>(x, p4, scales, y, N, acc); \
         else k_gemv_q4_f32<L, G, 1><<<blocks, threads, 0, c->stream>>>(x, p4, scales, y, N, acc);             \
         TI_LAUNCHED("k_gemv_q4_f32");                                                                         \
         return TI_OK;                                                                                         \
@@ -424,6 +591,7 @@ int ti_gateup_launch(ti_ctx* c, const uint32_t* xq, const float* xs, const uint3
     long rpp = 64 / s.lpr;
     long waves1 = (I + rpp - 1) / rpp;
     int R = waves1 >= 8192 ? 2 : 1;
+    while (R > s.lpr) R >>= 1;
     long waves = (I + rpp * R - 1) / (rpp * R);
     unsigned blocks, threads;
     grid_for(waves, blocks, threads);
@@ -431,7 +599,7 @@ int ti_gateup_launch(ti_ctx* c, const uint32_t* xq, const float* xs, const uint3
     const uint4* u4 = reinterpret_cast<const uint4*>(upack);
 #define X(L, G)                                                                                                        \
     if (s.lpr == L && s.gpl == G) {                                                                                    \
-        if (R == 2) k_gateup_q4_q8<L, G, 2><<<blocks, threads, 0, c->stream>>>(xq, xs, g4, gsc, u4, usc, swi, I);      \
+        if (R == 2) k_gateup_q4_q8<L, G, (L >= 2 ? 2 : 1)><<<blocks, threads, 0, c->stream>>>(xq, xs, g4, gsc, u4, usc, swi, I); \
         else k_gateup_q4_q8<L, G, 1><<<blocks, threads, 0, c->stream>>>(xq, xs, g4, gsc, u4, usc, swi, I);             \
         TI_LAUNCHED("k_gateup_q4_q8");                                                                                 \
         return TI_OK;                                                                                                  \
