@@ -109,6 +109,30 @@ int ti_linear_q4(ti_ctx* ctx, const float* x, const uint32_t* pack, const uint16
 int ti_group_dots_q4_q8(ti_ctx* ctx, const uint32_t* xq, const uint32_t* pack, int32_t* dots,
                         int N, int K);
 
+/* ---- attention over the int8 KV cache ------------------------------------------ */
+/* A7 attnPrepQ8 (models/qwen3.js:2297-2308): per-head RMSNorm(q,k) + split-half RoPE at
+ * `pos`, q -> qr, k and v snorm-quantized into the cache row `pos` (kq/ks/vq/vs are the
+ * layer's cache base pointers). Bit-exact KV codes. */
+int ti_attn_prep_q8(ti_ctx* ctx, const float* q, const float* k, const float* v,
+                    const uint16_t* qn_w, const uint16_t* kn_w, float* qr,
+                    uint32_t* kq, float* ks, uint32_t* vq, float* vs,
+                    int nHq, int nKv, int hd, int pos, float theta, float eps);
+/* A8+A9 attnDecodeStreamQ8 (models/qwen3.js:2165-2173): split-KV decode attention over
+ * S cached positions plus the log-sum-exp combine; out[nHq*hd]. nsplit = 0 picks the
+ * split count; otherwise it is the reference's nsplitOverride (splits of ceil(S/nsplit),
+ * trailing ones may be empty). */
+int ti_attn_decode_q8(ti_ctx* ctx, const float* qr, const uint32_t* kq, const float* ks,
+                      const uint32_t* vq, const float* vs, float* out,
+                      int S, int nHq, int nKv, int hd, int nsplit);
+/* ropeQK (models/qwen3.js:1700-1760): out[t,h,:] = RoPE(RMSNorm(x[t,h,:]) * w) at
+ * pos0+t for T tokens; w == NULL skips the norm. x and out must not alias. */
+int ti_rope_qk(ti_ctx* ctx, const float* x, const uint16_t* w, float* out,
+               int T, int nH, int hd, int pos0, float theta, float eps);
+/* kvQuantWrite (models/qwen3.js:2211-2216): snorm int8 write of T rows of k (roped) and
+ * v at positions pos..pos+T-1. */
+int ti_kv_write_q8(ti_ctx* ctx, const float* kr, const float* v, uint32_t* kq, float* ks,
+                   uint32_t* vq, float* vs, int T, int nKv, int hd, int pos);
+
 #ifdef __cplusplus
 }
 #endif

@@ -54,6 +54,10 @@ SIGS = {
     "ti_gateup_silu_q4": [_p, _p, _p, _p, _p, _p, _p, _p, _i, _i],
     "ti_linear_q4": [_p, _p, _p, _p, _p, _i, _i, _i, _i],
     "ti_group_dots_q4_q8": [_p, _p, _p, _p, _i, _i],
+    "ti_attn_prep_q8": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _f, _f],
+    "ti_attn_decode_q8": [_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i],
+    "ti_rope_qk": [_p, _p, _p, _p, _i, _i, _i, _i, _f, _f],
+    "ti_kv_write_q8": [_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i],
 }
 _RES = {"ti_last_error": C.c_char_p}
 

@@ -58,6 +58,13 @@ __device__ __forceinline__ float ti_h2f(uint16_t h) {
     return (float)__builtin_bit_cast(_Float16, h);
 }
 
+// Non-temporal 16-byte load (streamed data: weights, KV) — global_load_dwordx4 ... nt.
+typedef unsigned int ti_v4u __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ti_ld_nt(const uint4* p) {
+    ti_v4u v = __builtin_nontemporal_load(reinterpret_cast<const ti_v4u*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // Wavefront-64 butterfly sum over lanes that share the same (lane / width).
 template <int WIDTH>
 __device__ __forceinline__ float ti_seg_sum(float v) {
