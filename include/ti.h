@@ -133,6 +133,24 @@ int ti_rope_qk(ti_ctx* ctx, const float* x, const uint16_t* w, float* out,
 int ti_kv_write_q8(ti_ctx* ctx, const float* kr, const float* v, uint32_t* kq, float* ks,
                    uint32_t* vq, float* vs, int T, int nKv, int hd, int pos);
 
+/* ---- ternary Q2_0_g64 ------------------------------------------------------------ */
+/* A12 gemv_tern (native/crates/n2-kernels/src/tern.rs:56-71; cpu/kernel/src/lib.rs:438-441):
+ * out[n] = sum_b s[n,b]*dot_b - sum_b s[n,b]*xsum[b], in units of 1/scale (the caller
+ * multiplies by 1/scale, as the reference's callers do). K % 64 == 0. */
+int ti_tern_gemv(ti_ctx* ctx, float* out, const uint8_t* codes, const float* scales,
+                 const int8_t* act, const int32_t* xsum, int N, int K);
+/* gemm_tern_b4 (cpu/kernel/src/lib.rs:331-367): B activation rows act[B*K], xsum[B*K/64];
+ * row b of the output starts at out + b*out_stride. */
+int ti_tern_gemm(ti_ctx* ctx, float* out, long out_stride, const uint8_t* codes, const float* scales,
+                 const int8_t* act, const int32_t* xsum, int N, int K, int B);
+/* A13 quantize_act_into (tern.rs:206-222, mode 0) or WASM quantize (lib.rs:570-606,
+ * mode 1): per-tensor int8 activation + per-64 sums; the scale (127/amax for mode 0,
+ * amax/127 for mode 1) is written to the device float scale_out. */
+int ti_quant_act_tern(ti_ctx* ctx, const float* x, int8_t* act, int32_t* xsum, float* scale_out,
+                      int K, int mode);
+/* Exact int32 per-(row, block) code dots of A12 (debug/parity). */
+int ti_tern_block_dots(ti_ctx* ctx, const uint8_t* codes, const int8_t* act, int32_t* dots, int N, int K);
+
 #ifdef __cplusplus
 }
 #endif

@@ -58,6 +58,10 @@ SIGS = {
     "ti_attn_decode_q8": [_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i],
     "ti_rope_qk": [_p, _p, _p, _p, _i, _i, _i, _i, _f, _f],
     "ti_kv_write_q8": [_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i],
+    "ti_tern_gemv": [_p, _p, _p, _p, _p, _p, _i, _i],
+    "ti_tern_gemm": [_p, _p, C.c_long, _p, _p, _p, _p, _i, _i, _i],
+    "ti_quant_act_tern": [_p, _p, _p, _p, _p, _i, _i],
+    "ti_tern_block_dots": [_p, _p, _p, _p, _i, _i],
 }
 _RES = {"ti_last_error": C.c_char_p}
 

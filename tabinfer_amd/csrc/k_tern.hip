@@ -1,0 +1,298 @@
+// k_tern.hip — ternary (Q2_0_g64) GEMV and its activation quantizer:
+//  A12 gemv_tern       native/crates/n2-kernels/src/tern.rs:56-119, 246-338;
+//                      cpu/kernel/src/lib.rs:438-544 (B=1) and :331-432 (B=4 batched)
+//  A13 quantize_act    tern.rs:196-222 (n2: 127/amax, round half away from zero)
+//      quantize        cpu/kernel/src/lib.rs:570-606 (WASM: amax/127, nearest-even)
+//
+// out[n] = sum_b s[n,b]*dot_b - sum_b s[n,b]*xsum[b], dot_b = sum code*act over the
+// 64-code block (codes {0,1,2}); the two sums are kept apart and subtracted once
+// per row, as the reference requires. Block layout: 16 bytes, code c at byte c&15,
+// bits 2*(c>>4), so plane j ((byte >> 2j) & 3) holds codes 16j..16j+15 and pairs
+// with the contiguous activations act[64b+16j .. +16] — one v_dot4_i32_i8 per
+// 4 codes, no shuffles.
+#include "ti_internal.h"
+
+namespace {
+
+constexpr uint32_t M2 = 0x03030303u;
+
+// the 64 int8 activations of one block (16 dwords) plus its xsum
+struct ActT {
+    int a[16];
+    float xs;
+};
+
+__device__ __forceinline__ void load_act_tern(const int8_t* __restrict__ act, const int32_t* __restrict__ xsum, int blk,
+                                              ActT& t) {
+    const uint4* p = reinterpret_cast<const uint4*>(act + (size_t)blk * 64);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        uint4 u = p[i];
+        t.a[4 * i] = (int)u.x; t.a[4 * i + 1] = (int)u.y; t.a[4 * i + 2] = (int)u.z; t.a[4 * i + 3] = (int)u.w;
+    }
+    t.xs = xsum ? (float)xsum[blk] : 0.0f;
+}
+
+// exact int32 dot of one 64-code block with the activation block
+__device__ __forceinline__ int tern_block_dot(const uint4 w, const ActT& t) {
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+    int d = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+#pragma unroll
+        for (int m = 0; m < 4; m++) d = __builtin_amdgcn_sdot4((int)((ws[m] >> (2 * j)) & M2), t.a[4 * j + m], d, false);
+    return d;
+}
+
+// Two phases per tile of TR rows (one wavefront per workgroup):
+//  1. lanes compute the exact int32 block dots of the tile (LPR lanes per row, each
+//     owning fixed blocks, so its activation blocks live in registers; 16-byte
+//     coalesced code loads) and park them in LDS as dots[b][row][block];
+//  2. lane (b, r) replays row r's accumulation in the reference's block order —
+//     acc += s*dot, sxs += s*xsum, one subtraction — so the f32 result is
+//     bit-identical to the reference's scalar kernel (tern.rs:79-119).
+template <int LPR, int BPL, int B, int TR>
+__global__ __launch_bounds__(64) void k_tern_gemv(const uint4* __restrict__ codes, const float* __restrict__ scales,
+                                                  const int8_t* __restrict__ act, const int32_t* __restrict__ xsum,
+                                                  float* __restrict__ out, int N, int K, long out_stride) {
+    constexpr int RPP = 64 / LPR;
+    constexpr int NB = LPR * BPL;                // blocks per row
+    constexpr int PASSES = TR / RPP;
+    constexpr int CH = PASSES < 8 ? PASSES : 8;  // passes whose loads are in flight together
+    static_assert(TR % RPP == 0 && TR * B <= 64, "tile shape");
+    __shared__ int dots[B][TR][NB + 1];
+    const int lane = threadIdx.x;
+    const int sub = lane / LPR, li = lane % LPR;
+    ActT at[B][BPL];
+#pragma unroll
+    for (int bb = 0; bb < B; bb++)
+#pragma unroll
+        for (int j = 0; j < BPL; j++) load_act_tern(act + (size_t)bb * K, nullptr, li + LPR * j, at[bb][j]);
+    const long ntiles = (N + TR - 1) / TR;
+    for (long tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+        const long row0 = tile * TR;
+#pragma unroll
+        for (int pc = 0; pc < PASSES; pc += CH) {
+            uint4 cw[CH][BPL];
+#pragma unroll
+            for (int p = 0; p < CH; p++) {
+                long row = row0 + (long)(pc + p) * RPP + sub;
+                row = row < N ? row : N - 1;
+#pragma unroll
+                for (int j = 0; j < BPL; j++) cw[p][j] = ti_ld_nt(codes + row * NB + li + LPR * j);
+            }
+#pragma unroll
+            for (int p = 0; p < CH; p++)
+#pragma unroll
+                for (int j = 0; j < BPL; j++)
+#pragma unroll
+                    for (int bb = 0; bb < B; bb++)
+                        dots[bb][(pc + p) * RPP + sub][li + LPR * j] = tern_block_dot(cw[p][j], at[bb][j]);
+        }
+        __syncthreads();
+        if (lane < TR * B) {
+            const int bb = lane / TR, r = lane % TR;
+            const long row = row0 + r;
+            if (row < N) {
+                const float* srow = scales + row * NB;
+                const int32_t* xs = xsum + (size_t)bb * NB;
+                float acc = 0.0f, sxs = 0.0f;
+                for (int blk = 0; blk < NB; blk++) {
+                    const float sc = srow[blk];
+                    const float p = sc * (float)dots[bb][r][blk];
+                    acc = acc + p;
+                    const float q = sc * (float)xs[blk];
+                    sxs = sxs + q;
+                }
+                out[(size_t)bb * out_stride + row] = acc - sxs;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// any K % 64 == 0: one lane per row, blocks in order (same arithmetic as above)
+__global__ __launch_bounds__(64) void k_tern_gemv_generic(const uint4* __restrict__ codes, const float* __restrict__ scales,
+                                                          const int8_t* __restrict__ act, const int32_t* __restrict__ xsum,
+                                                          float* __restrict__ out, int N, int K, long out_stride) {
+    const long row = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (row >= N) return;
+    const int nb = K / 64;
+    float acc = 0.0f, sxs = 0.0f;
+    for (int blk = 0; blk < nb; blk++) {
+        ActT t;
+        load_act_tern(act, xsum, blk, t);
+        const float sc = scales[row * nb + blk];
+        const float p = sc * (float)tern_block_dot(codes[row * nb + blk], t);
+        acc = acc + p;
+        const float q = sc * t.xs;
+        sxs = sxs + q;
+    }
+    out[row] = acc - sxs;
+}
+
+__global__ void k_tern_block_dots(const uint4* __restrict__ codes, const int8_t* __restrict__ act, int32_t* __restrict__ dots,
+                                  long total, int nb) {
+    long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= total) return;
+    ActT t;
+    load_act_tern(act, nullptr, (int)(i % nb), t);
+    dots[i] = tern_block_dot(codes[i], t);
+}
+
+// ---------------------------------------------------------------------------
+// A13: per-tensor int8 activation quant + per-64 sums, one 1024-thread workgroup.
+// mode 0 (n2): scale = 127/amax (1 if amax == 0), a = clamp(round-half-away(x*scale))
+// mode 1 (WASM): asc = amax/127 (1e-9 if 0), a = clamp(nearest-even(x*(1/asc)))
+// The max is order-independent, so the codes are bit-exact.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(1024) void k_quant_act_tern(const float* __restrict__ x, int8_t* __restrict__ act,
+                                                         int32_t* __restrict__ xsum, float* __restrict__ scale_out,
+                                                         int K, int mode) {
+    __shared__ float red[16];
+    __shared__ float sh_scale;
+    const int t = threadIdx.x;
+    float m = 0.0f;
+    for (int i = t; i < K; i += 1024) m = fmaxf(m, fabsf(x[i]));
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    if ((t & 63) == 0) red[t >> 6] = m;
+    __syncthreads();
+    if (t == 0) {
+        float amax = red[0];
+        for (int w = 1; w < 16; w++) amax = fmaxf(amax, red[w]);
+        float s;
+        if (mode == 0) s = amax > 0.0f ? 127.0f / amax : 1.0f;
+        else s = amax > 0.0f ? amax / 127.0f : 1e-9f;
+        sh_scale = s;
+        *scale_out = s;
+    }
+    __syncthreads();
+    const float s = sh_scale;
+    const float mul = mode == 0 ? s : 1.0f / s;
+    // one wave per 64-block: lane quantizes one element, the wave sums the block
+    const int lane = t & 63;
+    for (int blk = t >> 6; blk < K / 64; blk += 16) {
+        float v = x[blk * 64 + lane] * mul;
+        float r = mode == 0 ? roundf(v) : rintf(v);
+        r = fminf(fmaxf(r, -127.0f), 127.0f);
+        int q = (int)r;
+        act[blk * 64 + lane] = (int8_t)q;
+        int sum = q;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+        if (lane == 0) xsum[blk] = sum;
+    }
+}
+
+struct Shape {
+    int lpr, bpl;
+};
+Shape pick(int nb) {
+    int lpr = 1;
+    while (lpr < 64 && (nb % (lpr * 2)) == 0) lpr *= 2;
+    return {lpr, nb / lpr};
+}
+
+
+}  // namespace
+
+static inline bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// launches the tile kernel when the tile is a whole number of row passes;
+// returns false otherwise (the caller then splits the batch)
+template <int L, int P, int BB, int T>
+static bool launch_tile(ti_ctx* c, unsigned grid, const uint4* c4, const float* scales, const int8_t* act,
+                        const int32_t* xsum, float* out, int N, int K, long out_stride) {
+    if constexpr (T % (64 / L) == 0 && T * BB <= 64) {
+        k_tern_gemv<L, P, BB, T><<<grid, 64, 0, c->stream>>>(c4, scales, act, xsum, out, N, K, out_stride);
+        return true;
+    } else {
+        return false;
+    }
+}
+
+static int tern_launch(ti_ctx* c, float* out, const uint8_t* codes, const float* scales, const int8_t* act,
+                       const int32_t* xsum, int N, int K, int B, long out_stride) {
+    const uint4* c4 = reinterpret_cast<const uint4*>(codes);
+    int nb = K / 64;
+    Shape s = pick(nb);
+    const int TR = B == 1 ? 64 : (B == 2 ? 32 : 16);
+    long ntiles = (N + TR - 1) / TR;
+    long maxg = 256L * 8;                       // persistent: up to 8 tiles in flight per CU
+    unsigned grid = (unsigned)(ntiles < maxg ? ntiles : maxg);
+#define TB(L, P, BB, T) launch_tile<L, P, BB, T>(c, grid, c4, scales, act, xsum, out, N, K, out_stride)
+#define TCASE(L, P)                                                        \
+    if (s.lpr == L && s.bpl == P) {                                        \
+        bool ok = B == 1 ? TB(L, P, 1, 64)                                 \
+                : (B == 2 && P <= 2) ? TB(L, P, 2, 32)                     \
+                : (B == 4 && P == 1) ? TB(L, P, 4, 16) : false;            \
+        if (!ok) goto split;                                               \
+        TI_LAUNCHED("k_tern_gemv");                                        \
+        return TI_OK;                                                      \
+    }
+    TCASE(1, 1) TCASE(2, 1) TCASE(4, 1) TCASE(8, 1) TCASE(16, 1) TCASE(32, 1) TCASE(64, 1)
+    TCASE(32, 3) TCASE(64, 2) TCASE(64, 3)
+#undef TCASE
+#undef TB
+    if (B == 1) {
+        k_tern_gemv_generic<<<(unsigned)((N + 63) / 64), 64, 0, c->stream>>>(c4, scales, act, xsum, out, N, K, out_stride);
+        TI_LAUNCHED("k_tern_gemv_generic");
+        return TI_OK;
+    }
+split:
+    for (int bb = 0; bb < B; bb++) {
+        int rc = tern_launch(c, out + (size_t)bb * out_stride, codes, scales, act + (size_t)bb * K,
+                             xsum + (size_t)bb * nb, N, K, 1, out_stride);
+        if (rc) return rc;
+    }
+    return TI_OK;
+}
+
+extern "C" int ti_tern_gemv(ti_ctx* c, float* out, const uint8_t* codes, const float* scales, const int8_t* act,
+                            const int32_t* xsum, int N, int K) {
+    TI_CHECK_CTX(c);
+    TI_REQUIRE(out && codes && scales && act && xsum, "ti_tern_gemv: null buffer");
+    TI_REQUIRE(N > 0 && K > 0 && K % 64 == 0, "ti_tern_gemv: K must be a positive multiple of 64 (N=%d K=%d)", N, K);
+    TI_REQUIRE(al16(codes) && al16(act), "ti_tern_gemv: codes and act must be 16-byte aligned");
+    return tern_launch(c, out, codes, scales, act, xsum, N, K, 1, N);
+}
+
+extern "C" int ti_tern_gemm(ti_ctx* c, float* out, long out_stride, const uint8_t* codes, const float* scales,
+                            const int8_t* act, const int32_t* xsum, int N, int K, int B) {
+    TI_CHECK_CTX(c);
+    TI_REQUIRE(out && codes && scales && act && xsum, "ti_tern_gemm: null buffer");
+    TI_REQUIRE(N > 0 && K > 0 && K % 64 == 0 && B > 0 && out_stride >= N, "ti_tern_gemm: bad shape (N=%d K=%d B=%d)", N, K, B);
+    TI_REQUIRE(al16(codes) && al16(act), "ti_tern_gemm: codes and act must be 16-byte aligned");
+    // batches of 4 share each code unpack (lib.rs gemm_tern_b4); a tail runs as B=2/1
+    int done = 0;
+    while (done < B) {
+        int bb = B - done >= 4 ? 4 : (B - done >= 2 ? 2 : 1);
+        int rc = tern_launch(c, out + (size_t)done * out_stride, codes, scales, act + (size_t)done * K,
+                             xsum + (size_t)done * (K / 64), N, K, bb, out_stride);
+        if (rc) return rc;
+        done += bb;
+    }
+    return TI_OK;
+}
+
+extern "C" int ti_tern_block_dots(ti_ctx* c, const uint8_t* codes, const int8_t* act, int32_t* dots, int N, int K) {
+    TI_CHECK_CTX(c);
+    TI_REQUIRE(codes && act && dots, "ti_tern_block_dots: null buffer");
+    TI_REQUIRE(N > 0 && K > 0 && K % 64 == 0, "ti_tern_block_dots: bad shape");
+    long total = (long)N * (K / 64);
+    k_tern_block_dots<<<(unsigned)((total + 255) / 256), 256, 0, c->stream>>>(reinterpret_cast<const uint4*>(codes), act,
+                                                                             dots, total, K / 64);
+    TI_LAUNCHED("k_tern_block_dots");
+    return TI_OK;
+}
+
+extern "C" int ti_quant_act_tern(ti_ctx* c, const float* x, int8_t* act, int32_t* xsum, float* scale_out, int K, int mode) {
+    TI_CHECK_CTX(c);
+    TI_REQUIRE(x && act && xsum && scale_out, "ti_quant_act_tern: null buffer");
+    TI_REQUIRE(K > 0 && K % 64 == 0, "ti_quant_act_tern: K must be a positive multiple of 64 (K=%d)", K);
+    TI_REQUIRE(mode == 0 || mode == 1, "ti_quant_act_tern: mode must be 0 (n2) or 1 (wasm)");
+    k_quant_act_tern<<<1, 1024, 0, c->stream>>>(x, act, xsum, scale_out, K, mode);
+    TI_LAUNCHED("k_quant_act_tern");
+    return TI_OK;
+}
