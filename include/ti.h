@@ -151,6 +151,42 @@ int ti_quant_act_tern(ti_ctx* ctx, const float* x, int8_t* act, int32_t* xsum, f
 /* Exact int32 per-(row, block) code dots of A12 (debug/parity). */
 int ti_tern_block_dots(ti_ctx* ctx, const uint8_t* codes, const int8_t* act, int32_t* dots, int N, int K);
 
+/* ---- Qwen3 decoder ---------------------------------------------------------------
+ * The model-level forward of models/qwen3.js (forward :3938-4069, loadModel layout
+ * :3470-3531) as a native object: int4 projections and lm_head, f16 norms and
+ * embeddings, the int8 KV cache, the token history and a device-side position. */
+typedef struct ti_qwen3 ti_qwen3;
+typedef struct {
+    int layers, hidden, intermediate, n_heads, n_kv_heads, head_dim, vocab;
+    float rope_theta, rms_eps;
+    int max_ctx;      /* KV capacity in positions */
+    int max_tokens;   /* largest T accepted by ti_qwen3_forward */
+} ti_qwen3_config;
+int ti_qwen3_create(ti_ctx* ctx, const ti_qwen3_config* cfg, ti_qwen3** out);
+int ti_qwen3_destroy(ti_ctx* ctx, ti_qwen3* m);
+/* Device buffers of a checkpoint tensor by its Hugging Face name (e.g.
+ * "model.layers.3.self_attn.q_proj.weight"): int4 tensors return pack + scales
+ * (fill them with ti_quant_int4_bf16), f16 tensors return data only. */
+int ti_qwen3_tensor(ti_qwen3* m, const char* name, void** data, size_t* data_bytes,
+                    void** scales, size_t* scale_bytes);
+int ti_qwen3_kv(ti_qwen3* m, int layer, uint32_t** kq, float** ks, uint32_t** vq, float** vs);
+int ti_qwen3_logits(ti_qwen3* m, float** logits);
+/* forward(ids, pos) at T >= 1 (models/qwen3.js:3938): history[pos..pos+T) = ids, KV
+ * written, argmax of the last logits to history[pos+T], device position = pos+T. */
+int ti_qwen3_forward(ti_ctx* ctx, ti_qwen3* m, const int32_t* ids, int T, int pos);
+/* forward(null, pos, {chain: true}) (models/qwen3.js:3951-3959, 4055): one step at the
+ * device position P: embeds history[P], writes KV row P, argmax -> history[P+1], P += 1.
+ * Reads nothing from the host, so it can be captured once and replayed per token. */
+int ti_qwen3_decode(ti_ctx* ctx, ti_qwen3* m);
+int ti_qwen3_set_pos(ti_ctx* ctx, ti_qwen3* m, int pos);
+int ti_qwen3_write_tokens(ti_ctx* ctx, ti_qwen3* m, int from, int count, const int32_t* ids);
+int ti_qwen3_read_tokens(ti_ctx* ctx, ti_qwen3* m, int from, int count, int32_t* ids);
+/* T-query causal attention over the int8 KV cache (models/qwen3.js:2534-2577): query t
+ * (positions pos0+t) attends keys [0, pos0+t]; qr/out are [T][nHq][hd]. */
+int ti_attn_causal_q8(ti_ctx* ctx, const float* qr, const uint32_t* kq, const float* ks,
+                      const uint32_t* vq, const float* vs, float* out,
+                      int T, int pos0, int nHq, int nKv, int hd);
+
 #ifdef __cplusplus
 }
 #endif

@@ -62,7 +62,24 @@ SIGS = {
     "ti_tern_gemm": [_p, _p, C.c_long, _p, _p, _p, _p, _i, _i, _i],
     "ti_quant_act_tern": [_p, _p, _p, _p, _p, _i, _i],
     "ti_tern_block_dots": [_p, _p, _p, _p, _i, _i],
+    "ti_qwen3_create": [_p, _p, C.POINTER(_p)],
+    "ti_qwen3_destroy": [_p, _p],
+    "ti_qwen3_tensor": [_p, C.c_char_p, C.POINTER(_p), C.POINTER(_sz), C.POINTER(_p), C.POINTER(_sz)],
+    "ti_qwen3_kv": [_p, _i, C.POINTER(_p), C.POINTER(_p), C.POINTER(_p), C.POINTER(_p)],
+    "ti_qwen3_logits": [_p, C.POINTER(_p)],
+    "ti_qwen3_forward": [_p, _p, _p, _i, _i],
+    "ti_qwen3_decode": [_p, _p],
+    "ti_qwen3_set_pos": [_p, _p, _i],
+    "ti_qwen3_write_tokens": [_p, _p, _i, _i, _p],
+    "ti_qwen3_read_tokens": [_p, _p, _i, _i, _p],
+    "ti_attn_causal_q8": [_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i],
 }
+
+
+class Qwen3Config(C.Structure):
+    _fields_ = [("layers", _i), ("hidden", _i), ("intermediate", _i), ("n_heads", _i), ("n_kv_heads", _i),
+                ("head_dim", _i), ("vocab", _i), ("rope_theta", _f), ("rms_eps", _f), ("max_ctx", _i),
+                ("max_tokens", _i)]
 _RES = {"ti_last_error": C.c_char_p}
 
 
@@ -224,6 +241,57 @@ class Ctx:
 
     def __exit__(self, *exc):
         self.close()
+
+
+class Qwen3:
+    """The native Qwen3 decoder (ti_qwen3_*) on a Ctx."""
+
+    def __init__(self, ctx, **cfg):
+        self.ctx = ctx
+        self.cfg = Qwen3Config(**cfg)
+        h = C.c_void_p()
+        check(lib().ti_qwen3_create(ctx.h, C.byref(self.cfg), C.byref(h)))
+        self.h = h.value
+
+    def tensor(self, name):
+        d, s = C.c_void_p(), C.c_void_p()
+        nd, ns = C.c_size_t(), C.c_size_t()
+        check(lib().ti_qwen3_tensor(self.h, name.encode(), C.byref(d), C.byref(nd), C.byref(s), C.byref(ns)))
+        return d.value, nd.value, s.value, ns.value
+
+    def kv(self, layer):
+        ptrs = [C.c_void_p() for _ in range(4)]
+        check(lib().ti_qwen3_kv(self.h, layer, *[C.byref(p) for p in ptrs]))
+        return [p.value for p in ptrs]
+
+    def logits_ptr(self):
+        p = C.c_void_p()
+        check(lib().ti_qwen3_logits(self.h, C.byref(p)))
+        return p.value
+
+    def forward(self, ids, pos):
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        check(lib().ti_qwen3_forward(self.ctx.h, self.h, ids.ctypes.data, ids.size, pos))
+
+    def decode(self):
+        check(lib().ti_qwen3_decode(self.ctx.h, self.h))
+
+    def set_pos(self, pos):
+        check(lib().ti_qwen3_set_pos(self.ctx.h, self.h, pos))
+
+    def write_tokens(self, start, ids):
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        check(lib().ti_qwen3_write_tokens(self.ctx.h, self.h, start, ids.size, ids.ctypes.data))
+
+    def read_tokens(self, start, count):
+        out = np.zeros(count, np.int32)
+        check(lib().ti_qwen3_read_tokens(self.ctx.h, self.h, start, count, out.ctypes.data))
+        return out
+
+    def close(self):
+        if self.h:
+            check(lib().ti_qwen3_destroy(self.ctx.h, self.h))
+            self.h = None
 
 
 def device_count():

@@ -75,10 +75,12 @@ __global__ __launch_bounds__(128) void k_attn_prep_q8(const float* __restrict__ 
                                                       const uint16_t* __restrict__ kw, float* __restrict__ qr,
                                                       uint32_t* __restrict__ kq, float* __restrict__ ks,
                                                       uint32_t* __restrict__ vq, float* __restrict__ vs,
-                                                      int nHq, int nKv, int hd, int pos, float theta, float eps) {
+                                                      int nHq, int nKv, int hd, int pos, float theta, float eps,
+                                                      const int* __restrict__ dpos) {
     __shared__ float red[128];
     __shared__ float rk[128];
     __shared__ float row[128];
+    if (dpos) pos = *dpos;
     const int j = threadIdx.x;
     const int role = blockIdx.x;
     const bool isQ = role < nHq;
@@ -154,7 +156,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split_q8(const float* __re
                                                                const float* __restrict__ ks, const uint4* __restrict__ vq,
                                                                const float* __restrict__ vs, float* __restrict__ po,
                                                                float* __restrict__ pml, int S, int nKv, int nsplit,
-                                                               int per) {
+                                                               int per, int ns_stride, const int* __restrict__ dpos) {
     constexpr int LPT = HD / 16;              // lanes per token row
     constexpr int TPP = ATT_THREADS / LPT;    // tokens per pass
     constexpr int PASSES = ATT_TILE / TPP;
@@ -167,6 +169,18 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split_q8(const float* __re
     const int lane = tid & 63, wv = tid >> 6;
     const int hk = blockIdx.x % nKv;
     const int split = blockIdx.x / nKv;
+    // query t of a T-token call attends keys [0, S+t); with a device position
+    // the context is *dpos + 1 and splits past it have nothing to do
+    const int qt = blockIdx.y;
+    if (dpos) {
+        S = *dpos + 1;
+        nsplit = (S + per - 1) / per;
+        if (split >= nsplit) return;
+    }
+    S += qt;
+    qr += (size_t)qt * (nKv * G) * HD;
+    po += (size_t)qt * (nKv * G) * ns_stride * HD;
+    pml += (size_t)qt * (nKv * G) * ns_stride * 2;
     const int tp = tid / LPT, sl = tid % LPT;       // token slot in a pass, 16-dim slice
     const int c0 = split * per;
     const int c1 = min(S, c0 + per);
@@ -295,27 +309,30 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split_q8(const float* __re
         float s = 0.0f;
         for (int r = 0; r < TPP; r++) s += pvred[r][o];
         const int h = o / HD, d = o % HD;
-        po[((size_t)(hk * G + h) * nsplit + split) * HD + d] = s;
+        po[((size_t)(hk * G + h) * ns_stride + split) * HD + d] = s;
     }
     if (tid < G) {
-        pml[((size_t)(hk * G + tid) * nsplit + split) * 2] = m_run[tid];
-        pml[((size_t)(hk * G + tid) * nsplit + split) * 2 + 1] = l_run[tid];
+        pml[((size_t)(hk * G + tid) * ns_stride + split) * 2] = m_run[tid];
+        pml[((size_t)(hk * G + tid) * ns_stride + split) * 2 + 1] = l_run[tid];
     }
 }
 
 // A9: O = sum_i o_i e^(m_i-M) / sum_i l_i e^(m_i-M); an empty split carries
 // (m = -3e38, l = 0, o = 0) and contributes nothing.
 __global__ void k_attn_combine(const float* __restrict__ po, const float* __restrict__ pml, float* __restrict__ out,
-                               int nsplit, int hd) {
-    const int hq = blockIdx.x, d = threadIdx.x;
-    const float* ml = pml + (size_t)hq * nsplit * 2;
+                               int nsplit, int hd, int ns_stride, int per, const int* __restrict__ dpos) {
+    const int d = threadIdx.x;
+    const int qt = blockIdx.y;
+    const int hq = blockIdx.x + qt * gridDim.x;        // row of [T][nHq]
+    if (dpos) nsplit = (*dpos + 1 + per - 1) / per;
+    const float* ml = pml + (size_t)hq * ns_stride * 2;
     float M = -3.0e38f;
     for (int i = 0; i < nsplit; i++) M = fmaxf(M, ml[2 * i]);
     float L = 0.0f, o = 0.0f;
     for (int i = 0; i < nsplit; i++) {
         float e = expf(ml[2 * i] - M);
         L += ml[2 * i + 1] * e;
-        if (d < hd) o += po[((size_t)hq * nsplit + i) * hd + d] * e;
+        if (d < hd) o += po[((size_t)hq * ns_stride + i) * hd + d] * e;
     }
     if (d < hd) out[(size_t)hq * hd + d] = o / L;
 }
@@ -334,22 +351,36 @@ static int auto_nsplit(int S, int nKv) {
     return ns;
 }
 
+// T queries (T >= 1) at contexts S, S+1, ..., S+T-1 (causal); with dpos != NULL the
+// context is read on the device (S = *dpos + 1, T must be 1) and the grid covers
+// `cap` positions in splits of `per` keys.
 int ti_attn_decode_launch(ti_ctx* c, const float* qr, const uint32_t* kq, const float* ks, const uint32_t* vq,
-                          const float* vs, float* out, int S, int nHq, int nKv, int hd, int nsplit) {
-    if (nsplit <= 0) nsplit = auto_nsplit(S, nKv);
-    if (nsplit > TI_ATTN_SPLITS_MAX) return ti_fail(TI_ERR_INVALID, "ti_attn_decode_q8: nsplit %d > %d", nsplit, TI_ATTN_SPLITS_MAX);
-    int per = (S + nsplit - 1) / nsplit;
+                          const float* vs, float* out, int S, int T, int nHq, int nKv, int hd, int nsplit,
+                          const int* dpos, int cap) {
+    int per, ns_stride;
+    if (dpos) {
+        per = 128;
+        nsplit = (cap + per - 1) / per;
+        ns_stride = nsplit;
+    } else {
+        int Smax = S + T - 1;
+        if (nsplit <= 0) nsplit = auto_nsplit(Smax, nKv);
+        per = (Smax + nsplit - 1) / nsplit;
+        ns_stride = nsplit;
+    }
+    if (nsplit > TI_ATTN_SPLITS_MAX) return ti_fail(TI_ERR_INVALID, "ti_attn_decode_q8: %d splits > %d", nsplit, TI_ATTN_SPLITS_MAX);
+    if ((long)T * nHq > TI_ATTN_ROWS_MAX) return ti_fail(TI_ERR_INVALID, "ti_attn_decode_q8: T*nHq = %d > %d", T * nHq, TI_ATTN_ROWS_MAX);
     int G = nHq / nKv;
-    dim3 grid(nKv * nsplit);
+    dim3 grid(nKv * nsplit, T);
     const uint4* k4 = reinterpret_cast<const uint4*>(kq);
     const uint4* v4 = reinterpret_cast<const uint4*>(vq);
 #define ATT(HD_, G_) \
-    if (hd == HD_ && G == G_) { k_attn_split_q8<HD_, G_><<<grid, ATT_THREADS, 0, c->stream>>>(qr, k4, ks, v4, vs, c->attn_po, c->attn_ml, S, nKv, nsplit, per); }
+    if (hd == HD_ && G == G_) { k_attn_split_q8<HD_, G_><<<grid, ATT_THREADS, 0, c->stream>>>(qr, k4, ks, v4, vs, c->attn_po, c->attn_ml, S, nKv, nsplit, per, ns_stride, dpos); }
     ATT(128, 1) else ATT(128, 2) else ATT(128, 4) else ATT(64, 1) else ATT(64, 2) else ATT(32, 2)
     else return ti_fail(TI_ERR_INVALID, "ti_attn_decode_q8: unsupported hd=%d / group=%d", hd, G);
 #undef ATT
     TI_LAUNCHED("k_attn_split_q8");
-    k_attn_combine<<<nHq, hd < 64 ? 64 : hd, 0, c->stream>>>(c->attn_po, c->attn_ml, out, nsplit, hd);
+    k_attn_combine<<<dim3(nHq, T), hd < 64 ? 64 : hd, 0, c->stream>>>(c->attn_po, c->attn_ml, out, nsplit, hd, ns_stride, per, dpos);
     TI_LAUNCHED("k_attn_combine");
     return TI_OK;
 }
@@ -361,7 +392,26 @@ extern "C" int ti_attn_decode_q8(ti_ctx* c, const float* qr, const uint32_t* kq,
     TI_REQUIRE(S > 0 && nKv > 0 && nHq % nKv == 0 && nHq <= TI_ATTN_HEADS_MAX, "ti_attn_decode_q8: bad heads/context (S=%d nHq=%d nKv=%d)", S, nHq, nKv);
     TI_REQUIRE(hd % 32 == 0 && hd <= TI_ATTN_HD_MAX, "ti_attn_decode_q8: hd must be a multiple of 32 and <= %d", TI_ATTN_HD_MAX);
     TI_REQUIRE(al16(kq) && al16(vq), "ti_attn_decode_q8: kq/vq must be 16-byte aligned");
-    return ti_attn_decode_launch(c, qr, kq, ks, vq, vs, out, S, nHq, nKv, hd, nsplit);
+    return ti_attn_decode_launch(c, qr, kq, ks, vq, vs, out, S, 1, nHq, nKv, hd, nsplit, nullptr, 0);
+}
+
+extern "C" int ti_attn_causal_q8(ti_ctx* c, const float* qr, const uint32_t* kq, const float* ks, const uint32_t* vq,
+                                 const float* vs, float* out, int T, int pos0, int nHq, int nKv, int hd) {
+    TI_CHECK_CTX(c);
+    TI_REQUIRE(qr && kq && ks && vq && vs && out, "ti_attn_causal_q8: null buffer");
+    TI_REQUIRE(T > 0 && pos0 >= 0 && nKv > 0 && nHq % nKv == 0, "ti_attn_causal_q8: bad shape (T=%d pos0=%d)", T, pos0);
+    TI_REQUIRE(hd % 32 == 0 && hd <= TI_ATTN_HD_MAX, "ti_attn_causal_q8: bad hd=%d", hd);
+    TI_REQUIRE(al16(kq) && al16(vq), "ti_attn_causal_q8: kq/vq must be 16-byte aligned");
+    return ti_attn_decode_launch(c, qr, kq, ks, vq, vs, out, pos0 + 1, T, nHq, nKv, hd, 0, nullptr, 0);
+}
+
+int ti_attn_prep_launch(ti_ctx* c, const float* q, const float* k, const float* v, const uint16_t* qw,
+                        const uint16_t* kw, float* qr, uint32_t* kq, float* ks, uint32_t* vq, float* vs,
+                        int nHq, int nKv, int hd, int pos, float theta, float eps, const int* dpos) {
+    k_attn_prep_q8<<<nHq + 2 * nKv, 128, 0, c->stream>>>(q, k, v, qw, kw, qr, kq, ks, vq, vs, nHq, nKv, hd, pos, theta,
+                                                         eps, dpos);
+    TI_LAUNCHED("k_attn_prep_q8");
+    return TI_OK;
 }
 
 extern "C" int ti_attn_prep_q8(ti_ctx* c, const float* q, const float* k, const float* v, const uint16_t* qw,
@@ -371,9 +421,7 @@ extern "C" int ti_attn_prep_q8(ti_ctx* c, const float* q, const float* k, const 
     TI_REQUIRE(q && k && v && qw && kw && qr && kq && ks && vq && vs, "ti_attn_prep_q8: null buffer");
     TI_REQUIRE(nHq > 0 && nKv > 0 && pos >= 0, "ti_attn_prep_q8: bad heads/pos");
     TI_REQUIRE(hd % 32 == 0 && hd <= 128, "ti_attn_prep_q8: hd must be a multiple of 32 and <= 128 (hd=%d)", hd);
-    k_attn_prep_q8<<<nHq + 2 * nKv, 128, 0, c->stream>>>(q, k, v, qw, kw, qr, kq, ks, vq, vs, nHq, nKv, hd, pos, theta, eps);
-    TI_LAUNCHED("k_attn_prep_q8");
-    return TI_OK;
+    return ti_attn_prep_launch(c, q, k, v, qw, kw, qr, kq, ks, vq, vs, nHq, nKv, hd, pos, theta, eps, nullptr);
 }
 
 extern "C" int ti_rope_qk(ti_ctx* c, const float* x, const uint16_t* w, float* out, int T, int nH, int hd, int pos0,

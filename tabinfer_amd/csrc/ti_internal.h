@@ -46,6 +46,7 @@ struct ti_graph {
 #define TI_ACT_CAP 65536
 #define TI_ACT_TMAX 256
 #define TI_ATTN_HEADS_MAX 64
+#define TI_ATTN_ROWS_MAX 512      // T * nHq of one attention call
 #define TI_ATTN_SPLITS_MAX 512
 #define TI_ATTN_HD_MAX 128
 #define TI_AMAX_PARTS 1024

@@ -1,0 +1,397 @@
+// ti_qwen3.hip — native Qwen3 decoder over the decode-path kernels.
+//
+// Replaces the reference's forward() (models/qwen3.js:3938-4069) and its
+// GPU-resident token chaining (_tokHist, models/qwen3.js:3890, 4055): the model
+// owns its weights (int4 projections + lm_head, f16 norms and embeddings), the
+// int8 KV cache, a token history and a device-side position counter. A decode
+// step reads its position on the device, so one captured HIP graph decodes
+// token after token with no host round trip: embed(tok[pos]) -> 28 layers ->
+// final norm -> lm_head -> argmax writes tok[pos+1] and advances pos.
+#include "ti_internal.h"
+#include <string.h>
+#include <stdio.h>
+#include <string>
+#include <vector>
+
+int ti_gemv_q4_q8_launch(ti_ctx*, const uint32_t*, const float*, const uint32_t*, const uint16_t*, float*, int, int, int);
+int ti_gemv_q4_f32_launch(ti_ctx*, const float*, const uint32_t*, const uint16_t*, float*, int, int, int);
+int ti_gateup_launch(ti_ctx*, const uint32_t*, const float*, const uint32_t*, const uint16_t*, const uint32_t*,
+                     const uint16_t*, float*, int, int);
+int ti_quant_act_q8_async(ti_ctx*, const float*, uint32_t*, float*, int32_t*, int);
+int ti_attn_prep_launch(ti_ctx*, const float*, const float*, const float*, const uint16_t*, const uint16_t*, float*,
+                        uint32_t*, float*, uint32_t*, float*, int, int, int, int, float, float, const int*);
+int ti_attn_decode_launch(ti_ctx*, const float*, const uint32_t*, const float*, const uint32_t*, const float*, float*,
+                          int, int, int, int, int, int, const int*, int);
+
+// ---------------------------------------------------------------------------
+// glue kernels
+// ---------------------------------------------------------------------------
+// embed gather (models/qwen3.js:1621-1633): y[t,h] = f32(emb[ids[off+t]*H + h]);
+// ids out of range are clamped to the vocabulary (a garbage id never reads out of bounds)
+__global__ void k_embed(const uint32_t* __restrict__ ids, const uint16_t* __restrict__ emb, float* __restrict__ y, int T,
+                        int H, int off, const int* __restrict__ dpos, int vocab) {
+    long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long)T * H) return;
+    if (dpos) off = *dpos;
+    int t = (int)(i / H), h = (int)(i % H);
+    uint32_t id = ids[off + t];
+    id = id < (uint32_t)vocab ? id : (uint32_t)(vocab - 1);
+    y[i] = ti_h2f(emb[(size_t)id * H + h]);
+}
+
+// two-stage argmax (models/qwen3.js:2624-2690); ties resolve to the lowest index
+constexpr int AMX_THREADS = 256;
+constexpr int AMX_PARTS = 256;
+
+__device__ __forceinline__ void amx_merge(float& v, int& i, float v2, int i2) {
+    if (v2 > v || (v2 == v && i2 < i)) { v = v2; i = i2; }
+}
+
+__global__ __launch_bounds__(AMX_THREADS) void k_argmax_p1(const float* __restrict__ logits, int N, float* __restrict__ pv,
+                                                           uint32_t* __restrict__ pi) {
+    __shared__ float sv[AMX_THREADS];
+    __shared__ int si[AMX_THREADS];
+    float bv = -3.0e38f;
+    int bi = 0x7fffffff;
+    for (int i = blockIdx.x * AMX_THREADS + threadIdx.x; i < N; i += AMX_PARTS * AMX_THREADS) amx_merge(bv, bi, logits[i], i);
+    sv[threadIdx.x] = bv;
+    si[threadIdx.x] = bi;
+    __syncthreads();
+    for (int s = AMX_THREADS / 2; s > 0; s >>= 1) {
+        if (threadIdx.x < s) {
+            float v = sv[threadIdx.x];
+            int i = si[threadIdx.x];
+            amx_merge(v, i, sv[threadIdx.x + s], si[threadIdx.x + s]);
+            sv[threadIdx.x] = v;
+            si[threadIdx.x] = i;
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) { pv[blockIdx.x] = sv[0]; pi[blockIdx.x] = (uint32_t)si[0]; }
+}
+
+// writes the token to hist[out_pos] (device position: hist[*dpos + 1], then *dpos += 1)
+__global__ __launch_bounds__(AMX_PARTS) void k_argmax_p2(const float* __restrict__ pv, const uint32_t* __restrict__ pi,
+                                                         uint32_t* __restrict__ hist, int out_pos, int* __restrict__ dpos,
+                                                         int advance) {
+    __shared__ float sv[AMX_PARTS];
+    __shared__ int si[AMX_PARTS];
+    sv[threadIdx.x] = pv[threadIdx.x];
+    si[threadIdx.x] = (int)pi[threadIdx.x];
+    __syncthreads();
+    for (int s = AMX_PARTS / 2; s > 0; s >>= 1) {
+        if (threadIdx.x < s) {
+            float v = sv[threadIdx.x];
+            int i = si[threadIdx.x];
+            amx_merge(v, i, sv[threadIdx.x + s], si[threadIdx.x + s]);
+            sv[threadIdx.x] = v;
+            si[threadIdx.x] = i;
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        int p = dpos ? *dpos + 1 : out_pos;
+        hist[p] = (uint32_t)si[0];
+        if (dpos && advance) *dpos = p;
+    }
+}
+
+__global__ void k_set_int(int* __restrict__ p, int v) { *p = v; }
+
+// swi = silu(g) * u (models/qwen3.js swiglu; silu(g) = g / (1 + e^-g))
+__global__ void k_swiglu(const float* __restrict__ g, const float* __restrict__ u, float* __restrict__ y, long n) {
+    long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) { float a = g[i]; y[i] = a / (1.0f + expf(-a)) * u[i]; }
+}
+
+__global__ void k_copy_f32(const float* __restrict__ s, float* __restrict__ d, int n) {
+    int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) d[i] = s[i];
+}
+
+// ---------------------------------------------------------------------------
+// model
+// ---------------------------------------------------------------------------
+namespace {
+struct Lin {
+    uint32_t* pack = nullptr;
+    uint16_t* sc = nullptr;
+    int N = 0, K = 0;
+};
+struct Layer {
+    Lin q, k, v, o, gate, up, down;
+    uint16_t *in_norm = nullptr, *post_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
+    uint32_t *kq = nullptr, *vq = nullptr;
+    float *ks = nullptr, *vs = nullptr;
+};
+}  // namespace
+
+struct ti_qwen3 {
+    ti_qwen3_config cfg;
+    std::vector<Layer> L;
+    uint16_t* embed = nullptr;
+    uint16_t* final_norm = nullptr;
+    Lin lm;
+    float *x, *normed, *q, *k, *v, *qr, *kr, *attn, *gate, *up, *swi, *last, *logits;
+    uint32_t* xq;
+    float* xs;
+    int32_t* xsum;
+    uint32_t* hist;
+    int* dpos;
+    float* amx_v;
+    uint32_t* amx_i;
+    std::vector<void*> allocs;
+};
+
+static int mk(ti_qwen3* m, void** p, size_t bytes) {
+    hipError_t e = hipMalloc(p, bytes ? bytes : 4);
+    if (e != hipSuccess) return ti_hip_fail(e, "ti_qwen3_create hipMalloc");
+    m->allocs.push_back(*p);
+    return TI_OK;
+}
+
+static void release(ti_qwen3* m) {
+    for (void* p : m->allocs) (void)hipFree(p);
+    delete m;
+}
+
+extern "C" int ti_qwen3_create(ti_ctx* c, const ti_qwen3_config* cfg, ti_qwen3** out) {
+    TI_CHECK_CTX(c);
+    TI_REQUIRE(cfg && out, "ti_qwen3_create: null argument");
+    *out = nullptr;
+    const ti_qwen3_config& C = *cfg;
+    TI_REQUIRE(C.layers > 0 && C.hidden > 0 && C.intermediate > 0 && C.n_heads > 0 && C.n_kv_heads > 0 &&
+               C.n_heads % C.n_kv_heads == 0 && C.vocab > 0 && C.max_ctx > 0 && C.max_tokens > 0,
+               "ti_qwen3_create: bad config");
+    TI_REQUIRE(C.hidden % 32 == 0 && C.intermediate % 32 == 0 && C.head_dim % 32 == 0 && C.head_dim <= 128,
+               "ti_qwen3_create: hidden/intermediate/head_dim must be multiples of 32 (head_dim <= 128)");
+    TI_REQUIRE(C.max_tokens <= TI_ACT_TMAX && C.max_tokens * C.n_heads <= TI_ATTN_ROWS_MAX,
+               "ti_qwen3_create: max_tokens too large");
+    TI_REQUIRE((C.max_ctx + 127) / 128 <= TI_ATTN_SPLITS_MAX, "ti_qwen3_create: max_ctx > %d", TI_ATTN_SPLITS_MAX * 128);
+    TI_REQUIRE(!c->capturing, "ti_qwen3_create: not during graph capture");
+    TI_HIP(hipSetDevice(c->device));
+    ti_qwen3* m = new ti_qwen3();
+    m->cfg = C;
+    const int H = C.hidden, I = C.intermediate, hd = C.head_dim;
+    const int nq = C.n_heads * hd, nkv = C.n_kv_heads * hd, T = C.max_tokens;
+    auto lin = [&](Lin& l, int N, int K) -> int {
+        l.N = N;
+        l.K = K;
+        int rc = mk(m, (void**)&l.pack, (size_t)N * K / 2);
+        if (!rc) rc = mk(m, (void**)&l.sc, (size_t)N * K / 16);
+        return rc;
+    };
+    int rc = 0;
+    m->L.resize(C.layers);
+    const size_t kvw = (size_t)C.max_ctx * nkv;   // int8 elements per layer per K or V
+    for (int l = 0; l < C.layers && !rc; l++) {
+        Layer& y = m->L[l];
+        rc = lin(y.q, nq, H); if (!rc) rc = lin(y.k, nkv, H); if (!rc) rc = lin(y.v, nkv, H);
+        if (!rc) rc = lin(y.o, H, nq); if (!rc) rc = lin(y.gate, I, H); if (!rc) rc = lin(y.up, I, H);
+        if (!rc) rc = lin(y.down, H, I);
+        if (!rc) rc = mk(m, (void**)&y.in_norm, H * 2);
+        if (!rc) rc = mk(m, (void**)&y.post_norm, H * 2);
+        if (!rc) rc = mk(m, (void**)&y.q_norm, hd * 2);
+        if (!rc) rc = mk(m, (void**)&y.k_norm, hd * 2);
+        if (!rc) rc = mk(m, (void**)&y.kq, kvw);
+        if (!rc) rc = mk(m, (void**)&y.vq, kvw);
+        if (!rc) rc = mk(m, (void**)&y.ks, kvw / 32 * 4);
+        if (!rc) rc = mk(m, (void**)&y.vs, kvw / 32 * 4);
+    }
+    if (!rc) rc = mk(m, (void**)&m->embed, (size_t)C.vocab * H * 2);
+    if (!rc) rc = mk(m, (void**)&m->final_norm, H * 2);
+    if (!rc) rc = lin(m->lm, C.vocab, H);
+    struct { float** p; size_t n; } fb[] = {{&m->x, (size_t)T * H}, {&m->normed, (size_t)T * H}, {&m->q, (size_t)T * nq},
+                                            {&m->k, (size_t)T * nkv}, {&m->v, (size_t)T * nkv}, {&m->qr, (size_t)T * nq},
+                                            {&m->kr, (size_t)T * nkv}, {&m->attn, (size_t)T * nq}, {&m->gate, (size_t)T * I},
+                                            {&m->up, (size_t)T * I}, {&m->swi, (size_t)T * I}, {&m->last, (size_t)H},
+                                            {&m->logits, (size_t)C.vocab}, {&m->amx_v, (size_t)AMX_PARTS}};
+    for (auto& f : fb) if (!rc) rc = mk(m, (void**)f.p, f.n * 4);
+    const size_t kmax = (size_t)(H > I ? (H > nq ? H : nq) : (I > nq ? I : nq));   // widest GEMV input
+    if (!rc) rc = mk(m, (void**)&m->xq, kmax);
+    if (!rc) rc = mk(m, (void**)&m->xs, kmax / 32 * 4);
+    if (!rc) rc = mk(m, (void**)&m->xsum, kmax / 16 * 4);
+    if (!rc) rc = mk(m, (void**)&m->hist, (size_t)(C.max_ctx + 1) * 4);
+    if (!rc) rc = mk(m, (void**)&m->dpos, 4);
+    if (!rc) rc = mk(m, (void**)&m->amx_i, (size_t)AMX_PARTS * 4);
+    if (!rc) {
+        hipError_t e = hipMemset(m->hist, 0, (size_t)(C.max_ctx + 1) * 4);
+        if (e == hipSuccess) e = hipMemset(m->dpos, 0, 4);
+        if (e == hipSuccess) e = hipDeviceSynchronize();
+        if (e != hipSuccess) rc = ti_hip_fail(e, "ti_qwen3_create clear");
+    }
+    if (rc) { release(m); return rc; }
+    *out = m;
+    return TI_OK;
+}
+
+extern "C" int ti_qwen3_destroy(ti_ctx* c, ti_qwen3* m) {
+    TI_CHECK_CTX(c);
+    if (!m) return TI_OK;
+    TI_REQUIRE(!c->capturing, "ti_qwen3_destroy: not during graph capture");
+    TI_HIP(hipStreamSynchronize(c->stream));
+    release(m);
+    return TI_OK;
+}
+
+// Tensor names follow the Hugging Face checkpoint (models/qwen3.js:3470, 3945-4049).
+extern "C" int ti_qwen3_tensor(ti_qwen3* m, const char* name, void** data, size_t* data_bytes, void** scales,
+                               size_t* scale_bytes) {
+    TI_REQUIRE(m && name && data && data_bytes, "ti_qwen3_tensor: null argument");
+    const ti_qwen3_config& C = m->cfg;
+    *data = nullptr;
+    *data_bytes = 0;
+    if (scales) *scales = nullptr;
+    if (scale_bytes) *scale_bytes = 0;
+    auto f16 = [&](uint16_t* p, size_t n) { *data = p; *data_bytes = n * 2; return TI_OK; };
+    auto lin = [&](Lin& l) {
+        *data = l.pack;
+        *data_bytes = (size_t)l.N * l.K / 2;
+        if (scales) *scales = l.sc;
+        if (scale_bytes) *scale_bytes = (size_t)l.N * l.K / 16;
+        return TI_OK;
+    };
+    std::string s(name);
+    if (s == "model.embed_tokens.weight") return f16(m->embed, (size_t)C.vocab * C.hidden);
+    if (s == "model.norm.weight") return f16(m->final_norm, C.hidden);
+    if (s == "lm_head.weight") return lin(m->lm);
+    int l = -1;
+    char rest[128] = {0};
+    if (sscanf(name, "model.layers.%d.%127s", &l, rest) == 2 && l >= 0 && l < C.layers) {
+        Layer& y = m->L[l];
+        std::string r(rest);
+        if (r == "input_layernorm.weight") return f16(y.in_norm, C.hidden);
+        if (r == "post_attention_layernorm.weight") return f16(y.post_norm, C.hidden);
+        if (r == "self_attn.q_norm.weight") return f16(y.q_norm, C.head_dim);
+        if (r == "self_attn.k_norm.weight") return f16(y.k_norm, C.head_dim);
+        if (r == "self_attn.q_proj.weight") return lin(y.q);
+        if (r == "self_attn.k_proj.weight") return lin(y.k);
+        if (r == "self_attn.v_proj.weight") return lin(y.v);
+        if (r == "self_attn.o_proj.weight") return lin(y.o);
+        if (r == "mlp.gate_proj.weight") return lin(y.gate);
+        if (r == "mlp.up_proj.weight") return lin(y.up);
+        if (r == "mlp.down_proj.weight") return lin(y.down);
+    }
+    return ti_fail(TI_ERR_INVALID, "ti_qwen3_tensor: unknown tensor '%s'", name);
+}
+
+extern "C" int ti_qwen3_kv(ti_qwen3* m, int layer, uint32_t** kq, float** ks, uint32_t** vq, float** vs) {
+    TI_REQUIRE(m && layer >= 0 && layer < m->cfg.layers && kq && ks && vq && vs, "ti_qwen3_kv: bad argument");
+    *kq = m->L[layer].kq;
+    *ks = m->L[layer].ks;
+    *vq = m->L[layer].vq;
+    *vs = m->L[layer].vs;
+    return TI_OK;
+}
+
+extern "C" int ti_qwen3_logits(ti_qwen3* m, float** logits) {
+    TI_REQUIRE(m && logits, "ti_qwen3_logits: null argument");
+    *logits = m->logits;
+    return TI_OK;
+}
+
+extern "C" int ti_qwen3_set_pos(ti_ctx* c, ti_qwen3* m, int pos) {
+    TI_CHECK_CTX(c);
+    TI_REQUIRE(m && pos >= 0 && pos < m->cfg.max_ctx, "ti_qwen3_set_pos: pos %d out of [0, %d)", pos, m ? m->cfg.max_ctx : 0);
+    k_set_int<<<1, 1, 0, c->stream>>>(m->dpos, pos);
+    TI_LAUNCHED("k_set_int");
+    return TI_OK;
+}
+
+extern "C" int ti_qwen3_write_tokens(ti_ctx* c, ti_qwen3* m, int from, int count, const int32_t* ids) {
+    TI_CHECK_CTX(c);
+    TI_REQUIRE(m && ids && from >= 0 && count >= 0 && from + count <= m->cfg.max_ctx + 1, "ti_qwen3_write_tokens: bad range");
+    return ti_buf_write(c, m->hist, (size_t)from * 4, ids, (size_t)count * 4);
+}
+
+extern "C" int ti_qwen3_read_tokens(ti_ctx* c, ti_qwen3* m, int from, int count, int32_t* ids) {
+    TI_CHECK_CTX(c);
+    TI_REQUIRE(m && ids && from >= 0 && count >= 0 && from + count <= m->cfg.max_ctx + 1, "ti_qwen3_read_tokens: bad range");
+    return ti_buf_read(c, m->hist, (size_t)from * 4, ids, (size_t)count * 4);
+}
+
+static int argmax_launch(ti_ctx* c, ti_qwen3* m, int out_pos, const int* dpos) {
+    k_argmax_p1<<<AMX_PARTS, AMX_THREADS, 0, c->stream>>>(m->logits, m->cfg.vocab, m->amx_v, m->amx_i);
+    TI_LAUNCHED("k_argmax_p1");
+    k_argmax_p2<<<1, AMX_PARTS, 0, c->stream>>>(m->amx_v, m->amx_i, m->hist, out_pos, (int*)dpos, 1);
+    TI_LAUNCHED("k_argmax_p2");
+    return TI_OK;
+}
+
+// One decode step at the device position (forward(null, pos, {chain: true})).
+extern "C" int ti_qwen3_decode(ti_ctx* c, ti_qwen3* m) {
+    TI_CHECK_CTX(c);
+    TI_REQUIRE(m, "ti_qwen3_decode: null model");
+    const ti_qwen3_config& C = m->cfg;
+    const int H = C.hidden, I = C.intermediate, hd = C.head_dim, nHq = C.n_heads, nKv = C.n_kv_heads;
+    const int nq = nHq * hd, nkv = nKv * hd;
+    int rc;
+#define RC(x) do { rc = (x); if (rc) return rc; } while (0)
+    k_embed<<<(H + 255) / 256, 256, 0, c->stream>>>(m->hist, m->embed, m->x, 1, H, 0, m->dpos, C.vocab);
+    TI_LAUNCHED("k_embed");
+    for (int l = 0; l < C.layers; l++) {
+        Layer& y = m->L[l];
+        RC(ti_rmsnorm_q8(c, m->x, y.in_norm, m->xq, m->xs, m->xsum, H, C.rms_eps));
+        RC(ti_gemv_q4_q8_launch(c, m->xq, m->xs, y.q.pack, y.q.sc, m->q, nq, H, 0));
+        RC(ti_gemv_q4_q8_launch(c, m->xq, m->xs, y.k.pack, y.k.sc, m->k, nkv, H, 0));
+        RC(ti_gemv_q4_q8_launch(c, m->xq, m->xs, y.v.pack, y.v.sc, m->v, nkv, H, 0));
+        RC(ti_attn_prep_launch(c, m->q, m->k, m->v, y.q_norm, y.k_norm, m->qr, y.kq, y.ks, y.vq, y.vs, nHq, nKv, hd, 0,
+                               C.rope_theta, C.rms_eps, m->dpos));
+        RC(ti_attn_decode_launch(c, m->qr, y.kq, y.ks, y.vq, y.vs, m->attn, 0, 1, nHq, nKv, hd, 0, m->dpos, C.max_ctx));
+        RC(ti_quant_act_q8_async(c, m->attn, m->xq, m->xs, nullptr, nq / 32));
+        RC(ti_gemv_q4_q8_launch(c, m->xq, m->xs, y.o.pack, y.o.sc, m->x, H, nq, 1));
+        RC(ti_rmsnorm_q8(c, m->x, y.post_norm, m->xq, m->xs, m->xsum, H, C.rms_eps));
+        RC(ti_gateup_launch(c, m->xq, m->xs, y.gate.pack, y.gate.sc, y.up.pack, y.up.sc, m->swi, I, H));
+        RC(ti_quant_act_q8_async(c, m->swi, m->xq, m->xs, nullptr, I / 32));
+        RC(ti_gemv_q4_q8_launch(c, m->xq, m->xs, y.down.pack, y.down.sc, m->x, H, I, 1));
+    }
+    RC(ti_rmsnorm(c, m->x, m->final_norm, m->normed, 1, H, C.rms_eps));
+    RC(ti_gemv_q4_f32_launch(c, m->normed, m->lm.pack, m->lm.sc, m->logits, C.vocab, H, 0));
+    RC(argmax_launch(c, m, 0, m->dpos));
+    return TI_OK;
+}
+
+// forward(ids, pos) for T >= 1 host tokens (prefill, or the T-token batch): writes
+// the ids into the token history at [pos, pos+T), runs the T-token forward, puts
+// the argmax of the last token's logits at hist[pos+T] and sets the device
+// position to pos+T, so the next chained step embeds hist[pos+T].
+extern "C" int ti_qwen3_forward(ti_ctx* c, ti_qwen3* m, const int32_t* ids, int T, int pos) {
+    TI_CHECK_CTX(c);
+    TI_REQUIRE(m && ids, "ti_qwen3_forward: null argument");
+    const ti_qwen3_config& C = m->cfg;
+    TI_REQUIRE(T > 0 && T <= C.max_tokens && pos >= 0 && pos + T <= C.max_ctx,
+               "ti_qwen3_forward: T=%d pos=%d outside max_tokens=%d / max_ctx=%d", T, pos, C.max_tokens, C.max_ctx);
+    const int H = C.hidden, I = C.intermediate, hd = C.head_dim, nHq = C.n_heads, nKv = C.n_kv_heads;
+    const int nq = nHq * hd, nkv = nKv * hd;
+    int rc;
+    RC(ti_buf_write(c, m->hist, (size_t)pos * 4, ids, (size_t)T * 4));
+    k_embed<<<(unsigned)(((long)T * H + 255) / 256), 256, 0, c->stream>>>(m->hist, m->embed, m->x, T, H, pos, nullptr, C.vocab);
+    TI_LAUNCHED("k_embed");
+    for (int l = 0; l < C.layers; l++) {
+        Layer& y = m->L[l];
+        RC(ti_rmsnorm(c, m->x, y.in_norm, m->normed, T, H, C.rms_eps));
+        RC(ti_linear_q4(c, m->normed, y.q.pack, y.q.sc, m->q, T, nq, H, 0));
+        RC(ti_linear_q4(c, m->normed, y.k.pack, y.k.sc, m->k, T, nkv, H, 0));
+        RC(ti_linear_q4(c, m->normed, y.v.pack, y.v.sc, m->v, T, nkv, H, 0));
+        RC(ti_rope_qk(c, m->q, y.q_norm, m->qr, T, nHq, hd, pos, C.rope_theta, C.rms_eps));
+        RC(ti_rope_qk(c, m->k, y.k_norm, m->kr, T, nKv, hd, pos, C.rope_theta, C.rms_eps));
+        RC(ti_kv_write_q8(c, m->kr, m->v, y.kq, y.ks, y.vq, y.vs, T, nKv, hd, pos));
+        RC(ti_attn_decode_launch(c, m->qr, y.kq, y.ks, y.vq, y.vs, m->attn, pos + 1, T, nHq, nKv, hd, 0, nullptr, 0));
+        RC(ti_linear_q4(c, m->attn, y.o.pack, y.o.sc, m->x, T, H, nq, 1));
+        RC(ti_rmsnorm(c, m->x, y.post_norm, m->normed, T, H, C.rms_eps));
+        RC(ti_linear_q4(c, m->normed, y.gate.pack, y.gate.sc, m->gate, T, I, H, 0));
+        RC(ti_linear_q4(c, m->normed, y.up.pack, y.up.sc, m->up, T, I, H, 0));
+        k_swiglu<<<(unsigned)(((long)T * I + 255) / 256), 256, 0, c->stream>>>(m->gate, m->up, m->swi, (long)T * I);
+        TI_LAUNCHED("k_swiglu");
+        RC(ti_linear_q4(c, m->swi, y.down.pack, y.down.sc, m->x, T, H, I, 1));
+    }
+    k_copy_f32<<<(H + 255) / 256, 256, 0, c->stream>>>(m->x + (size_t)(T - 1) * H, m->last, H);
+    TI_LAUNCHED("k_copy_f32");
+    RC(ti_rmsnorm(c, m->last, m->final_norm, m->normed, 1, H, C.rms_eps));
+    RC(ti_gemv_q4_f32_launch(c, m->normed, m->lm.pack, m->lm.sc, m->logits, C.vocab, H, 0));
+    RC(argmax_launch(c, m, pos + T, nullptr));
+    k_set_int<<<1, 1, 0, c->stream>>>(m->dpos, pos + T);
+    TI_LAUNCHED("k_set_int");
+    return TI_OK;
+#undef RC
+}

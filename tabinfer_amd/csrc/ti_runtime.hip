@@ -70,8 +70,8 @@ extern "C" int ti_init(int device, ti_ctx** out) {
         {(void**)&c->act_q, (size_t)TI_ACT_CAP * TI_ACT_TMAX},
         {(void**)&c->act_s, (size_t)TI_ACT_CAP / 32 * TI_ACT_TMAX * 4},
         {(void**)&c->act_sum, (size_t)TI_ACT_CAP / 16 * 4},
-        {(void**)&c->attn_po, (size_t)TI_ATTN_HEADS_MAX * TI_ATTN_SPLITS_MAX * TI_ATTN_HD_MAX * 4},
-        {(void**)&c->attn_ml, (size_t)TI_ATTN_HEADS_MAX * TI_ATTN_SPLITS_MAX * 2 * 4},
+        {(void**)&c->attn_po, (size_t)TI_ATTN_ROWS_MAX * TI_ATTN_SPLITS_MAX * TI_ATTN_HD_MAX * 4},
+        {(void**)&c->attn_ml, (size_t)TI_ATTN_ROWS_MAX * TI_ATTN_SPLITS_MAX * 2 * 4},
         {(void**)&c->amax_v, (size_t)TI_AMAX_PARTS * 4},
         {(void**)&c->amax_i, (size_t)TI_AMAX_PARTS * 4},
         {(void**)&c->moe_cnt, (size_t)TI_MOE_E_MAX * 4},
