@@ -109,6 +109,31 @@ int ti_linear_q4(ti_ctx* ctx, const float* x, const uint32_t* pack, const uint16
 int ti_group_dots_q4_q8(ti_ctx* ctx, const uint32_t* xq, const uint32_t* pack, int32_t* dots,
                         int N, int K);
 
+/* ---- fused decode-step launches ---------------------------------------------------
+ * Each replaces a run of the reference's launchers with one kernel; the int8 codes
+ * they produce internally are the ones the separate launchers produce, bit for bit. */
+/* rmsnormQ (models/qwen3.js:614-621) + the projGemv calls that share its output
+ * (q, k, v: models/qwen3.js:3981-3984): ys[i][0..Ns[i]) = W_i . rmsnormQ(x), for nmat
+ * in 1..3 matrices of K columns. norm_w == NULL quantizes x as is (quantQ8).
+ * xq_out/xs_out (both or neither) receive the int8 activation. K <= 16384. */
+int ti_rmsnorm_gemv_q4(ti_ctx* ctx, const float* x, const uint16_t* norm_w, float eps, int K, int nmat,
+                       const uint32_t* const* packs, const uint16_t* const* scales, float* const* ys,
+                       const int* Ns, uint32_t* xq_out, float* xs_out);
+/* rmsnormQ + gateUpSiluDP4_only (models/qwen3.js:4023-4024): swi = silu(gate.x)*(up.x). */
+int ti_rmsnorm_gateup_silu_q4(ti_ctx* ctx, const float* x, const uint16_t* norm_w, float eps,
+                              const uint32_t* gpack, const uint16_t* gsc, const uint32_t* upack,
+                              const uint16_t* usc, float* swi, int I, int H);
+/* final rmsnorm + lm_head gemvQ + argmaxKernel (models/qwen3.js:4037-4055):
+ * logits (may be NULL) = W . rmsnorm(x), tok_hist[out_pos] = argmax (lowest index on
+ * ties). K <= 8192. */
+int ti_rmsnorm_lm_head_argmax(ti_ctx* ctx, const float* x, const uint16_t* norm_w, float eps,
+                              const uint32_t* pack, const uint16_t* scales, float* logits, int N, int K,
+                              uint32_t* tok_hist, int out_pos);
+/* argmaxKernel (models/qwen3.js:2681-2690): tok_hist[out_pos] = argmax(logits[0..N)). */
+int ti_argmax(ti_ctx* ctx, const float* logits, int N, uint32_t* tok_hist, int out_pos);
+/* embedGather (models/qwen3.js:1663-1676): y[t] = f32(emb[ids[id_off+t]]), t < T. */
+int ti_embed(ti_ctx* ctx, const int32_t* ids, const uint16_t* emb, float* y, int T, int H, int id_off, int vocab);
+
 /* ---- attention over the int8 KV cache ------------------------------------------ */
 /* A7 attnPrepQ8 (models/qwen3.js:2297-2308): per-head RMSNorm(q,k) + split-half RoPE at
  * `pos`, q -> qr, k and v snorm-quantized into the cache row `pos` (kq/ks/vq/vs are the
@@ -124,6 +149,15 @@ int ti_attn_prep_q8(ti_ctx* ctx, const float* q, const float* k, const float* v,
 int ti_attn_decode_q8(ti_ctx* ctx, const float* qr, const uint32_t* kq, const float* ks,
                       const uint32_t* vq, const float* vs, float* out,
                       int S, int nHq, int nKv, int hd, int nsplit);
+/* attnPrepQ8 + attnDecodeStreamQ8 + combine as one launch (models/qwen3.js:4001-4002) for
+ * one token at `pos` (< cap, the cache capacity in positions): q/k/v are the token's
+ * projections [nHq*hd], [nKv*hd], [nKv*hd]; k and v are written into cache row pos;
+ * out[nHq*hd] is the attention over positions 0..pos. Splits of >= 128 keys, at most
+ * max_splits (0 = 64). Covers hd 64/128 with nHq/nKv <= 2. */
+int ti_attn_step_q8(ti_ctx* ctx, const float* q, const float* k, const float* v,
+                    const uint16_t* qn_w, const uint16_t* kn_w, uint32_t* kq, float* ks,
+                    uint32_t* vq, float* vs, float* out, int nHq, int nKv, int hd, int pos, int cap,
+                    float theta, float eps, int max_splits);
 /* ropeQK (models/qwen3.js:1700-1760): out[t,h,:] = RoPE(RMSNorm(x[t,h,:]) * w) at
  * pos0+t for T tokens; w == NULL skips the norm. x and out must not alias. */
 int ti_rope_qk(ti_ctx* ctx, const float* x, const uint16_t* w, float* out,

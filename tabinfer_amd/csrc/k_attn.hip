@@ -447,3 +447,322 @@ extern "C" int ti_kv_write_q8(ti_ctx* c, const float* kr, const float* v, uint32
     TI_LAUNCHED("k_kv_write_q8");
     return TI_OK;
 }
+
+// ---------------------------------------------------------------------------
+// Fused decode attention: one launch per layer at T = 1 does attnPrepQ8
+// (models/qwen3.js:2228-2308), attnDecodeStreamQ8 (:2077-2164) and the combine
+// (:2048-2068). Workgroup (256 threads) = (KV head hk, split):
+//  1. RMSNorm + RoPE of the G = nHq/nKv query heads of hk into LDS (each
+//     workgroup recomputes them: 2 x 128 values);
+//  2. the split that holds position pos normalises/ropes k and quantizes k, v
+//     into the cache row pos (snorm int8, as attnPrepQ8) and uses that row from
+//     LDS, so no workgroup waits for another one's write;
+//  3. online softmax over the split in tiles of ATTF_TILE keys; K and V of a tile
+//     are loaded together and the next tile is prefetched during the current one;
+//  4. partials (unnormalised o, m, l) go to scratch; the last workgroup of hk to
+//     finish (device-scope counter, release/acquire fences) merges them by
+//     log-sum-exp and writes the head outputs, then resets the counter.
+// The split count adapts to the context on the device: at least min_per keys
+// per split, at most max_splits splits.
+// ---------------------------------------------------------------------------
+namespace {
+constexpr int ATTF_TILE = 128;
+constexpr int ATTF_MAXS = 64;
+
+struct AttnFArgs {
+    const float* q;
+    const float* k;
+    const float* v;
+    const uint16_t* qw;
+    const uint16_t* kw;
+    uint32_t* kq;
+    float* ks;
+    uint32_t* vq;
+    float* vs;
+    float* out;
+    float* po;
+    float* pml;
+    uint32_t* counter;     // [nKv]
+    const int* dpos;       // device position, or null: use pos
+    int pos;
+    int nKv, max_splits, min_per, cap;
+    float theta, eps;
+};
+
+template <int HD, int G>
+__global__ __launch_bounds__(256) void k_attn_fused_q8(AttnFArgs a) {
+    static_assert(G >= 1 && G <= 2 && HD <= 128 && HD % 32 == 0, "fused attention: G <= 2, HD <= 128");
+    constexpr int LPT = HD / 16;               // lanes per token row (16 bytes each)
+    constexpr int TPP = 256 / LPT;             // tokens per pass
+    constexpr int PASSES = ATTF_TILE / TPP;
+    constexpr int NG = HD / 32;                // scale groups per head row
+    __shared__ float red[256];
+    __shared__ float rk[256];
+    __shared__ float s_q[G][HD];
+    __shared__ float s_row[2][128];
+    __shared__ __align__(16) uint32_t s_kw[HD / 4];
+    __shared__ __align__(16) uint32_t s_vw[HD / 4];
+    __shared__ float s_ksc[NG], s_vsc[NG];
+    __shared__ float sc[G][ATTF_TILE];
+    __shared__ float redm[G][4];
+    __shared__ float reds[G][4];
+    __shared__ float pvred[TPP][G * HD + 1];
+    __shared__ float s_ml[G][ATTF_MAXS][2];
+    __shared__ int s_last;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wv = tid >> 6;
+    const int hk = blockIdx.x % a.nKv;
+    const int split = blockIdx.x / a.nKv;
+    const int pos = a.dpos ? *a.dpos : a.pos;
+    if (pos < 0 || pos >= a.cap) return;       // outside the cache: nothing is read or written
+    const int S = pos + 1;
+    int ns0 = (S + a.min_per - 1) / a.min_per;
+    ns0 = ns0 < a.max_splits ? ns0 : a.max_splits;
+    const int per = (S + ns0 - 1) / ns0;
+    const int nsplit = (S + per - 1) / per;
+    if (split >= nsplit) return;
+    const int c0 = split * per;
+    const int c1 = min(S, c0 + per);
+    const bool has_pos = c1 == S;
+
+    // 1. query heads
+    const int h = tid >> 7, j = tid & 127;
+    {
+        float x = (h < G && j < HD) ? a.q[(size_t)(hk * G + h) * HD + j] : 0.0f;
+        float r = rope_norm(x, j, HD, a.qw, pos, a.theta, a.eps, true, red + h * 128, rk + h * 128);
+        if (h < G && j < HD) s_q[h][j] = r;
+    }
+    // 2. this token's K/V row
+    if (has_pos) {
+        float x = (h == 0 && j < HD) ? a.k[(size_t)hk * HD + j] : 0.0f;
+        float r = rope_norm(x, j, HD, a.kw, pos, a.theta, a.eps, true, red + h * 128, rk + h * 128);
+        if (j < HD) s_row[h][j] = h == 0 ? r : a.v[(size_t)hk * HD + j];
+        __syncthreads();
+        if (tid < 2 * NG) {
+            const int which = tid / NG, g = tid % NG;
+            float vals[32];
+#pragma unroll
+            for (int i = 0; i < 32; i++) vals[i] = s_row[which][g * 32 + i];
+            uint32_t wds[8];
+            float scl;
+            snorm_group(vals, wds, &scl);
+            uint32_t* dq = (which ? a.vq : a.kq) + ((size_t)pos * a.nKv + hk) * (HD / 4) + g * 8;
+            float* ds = (which ? a.vs : a.ks) + ((size_t)pos * a.nKv + hk) * NG + g;
+            uint32_t* lw = which ? s_vw : s_kw;
+#pragma unroll
+            for (int w = 0; w < 8; w++) { dq[w] = wds[w]; lw[g * 8 + w] = wds[w]; }
+            *ds = scl;
+            (which ? s_vsc : s_ksc)[g] = scl;
+        }
+    }
+    __syncthreads();
+
+    const int tp = tid / LPT, sl = tid % LPT;
+    const int row_words4 = a.nKv * HD / 16;
+    const int row_groups = a.nKv * NG;
+    const float qk_scale = 1.0f / (127.0f * sqrtf((float)HD));
+    const uint4* kq4 = reinterpret_cast<const uint4*>(a.kq);
+    const uint4* vq4 = reinterpret_cast<const uint4*>(a.vq);
+    float qv[G][16];
+#pragma unroll
+    for (int hh = 0; hh < G; hh++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) qv[hh][i] = s_q[hh][sl * 16 + i];
+    float m_run[G], l_run[G], acc[G][16];
+#pragma unroll
+    for (int hh = 0; hh < G; hh++) {
+        m_run[hh] = -3.0e38f;
+        l_run[hh] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) acc[hh][i] = 0.0f;
+    }
+
+    uint4 kw[2][PASSES], vw[2][PASSES];
+    float ksc[2][PASSES], vsc[2][PASSES];
+    auto load = [&](int buf, int t0) {
+#pragma unroll
+        for (int p = 0; p < PASSES; p++) {
+            int t = t0 + p * TPP + tp;
+            t = t < c1 ? t : c1 - 1;
+            kw[buf][p] = ti_ld_nt(kq4 + (size_t)t * row_words4 + hk * LPT + sl);
+            vw[buf][p] = ti_ld_nt(vq4 + (size_t)t * row_words4 + hk * LPT + sl);
+            ksc[buf][p] = a.ks[(size_t)t * row_groups + hk * NG + sl / 2];
+            vsc[buf][p] = a.vs[(size_t)t * row_groups + hk * NG + sl / 2];
+        }
+    };
+    auto process = [&](int buf, int t0) {
+        const int n = min(ATTF_TILE, c1 - t0);
+        if (has_pos) {   // the row at pos (and the clamped reads past it) come from LDS
+#pragma unroll
+            for (int p = 0; p < PASSES; p++) {
+                if (min(t0 + p * TPP + tp, c1 - 1) == pos) {
+                    kw[buf][p] = reinterpret_cast<const uint4*>(s_kw)[sl];
+                    vw[buf][p] = reinterpret_cast<const uint4*>(s_vw)[sl];
+                    ksc[buf][p] = s_ksc[sl / 2];
+                    vsc[buf][p] = s_vsc[sl / 2];
+                }
+            }
+        }
+#pragma unroll
+        for (int p = 0; p < PASSES; p++) {
+            const uint32_t ww[4] = {kw[buf][p].x, kw[buf][p].y, kw[buf][p].z, kw[buf][p].w};
+            float part[G];
+#pragma unroll
+            for (int hh = 0; hh < G; hh++) {
+                float d = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 16; i++) d = fmaf(qv[hh][i], i8f(ww[i >> 2], i & 3), d);
+                part[hh] = d * ksc[buf][p];
+            }
+#pragma unroll
+            for (int o = LPT / 2; o > 0; o >>= 1)
+#pragma unroll
+                for (int hh = 0; hh < G; hh++) part[hh] += __shfl_xor(part[hh], o, 64);
+            const int jj = p * TPP + tp;
+            if (sl == 0)
+#pragma unroll
+                for (int hh = 0; hh < G; hh++) sc[hh][jj] = jj < n ? part[hh] * qk_scale : -3.0e38f;
+        }
+        __syncthreads();
+        float mt[G], corr[G];
+#pragma unroll
+        for (int hh = 0; hh < G; hh++) {
+            float v = -3.0e38f;
+            for (int q = tid; q < ATTF_TILE; q += 256) v = fmaxf(v, sc[hh][q]);
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+            if (lane == 0) redm[hh][wv] = v;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int hh = 0; hh < G; hh++) {
+            float v = fmaxf(fmaxf(redm[hh][0], redm[hh][1]), fmaxf(redm[hh][2], redm[hh][3]));
+            mt[hh] = fmaxf(m_run[hh], v);
+            corr[hh] = expf(m_run[hh] - mt[hh]);
+            float s = 0.0f;
+            for (int q = tid; q < ATTF_TILE; q += 256) {
+                float pe = q < n ? expf(sc[hh][q] - mt[hh]) : 0.0f;
+                sc[hh][q] = pe;
+                s += pe;
+            }
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+            if (lane == 0) reds[hh][wv] = s;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int hh = 0; hh < G; hh++) {
+            float s = (reds[hh][0] + reds[hh][1]) + (reds[hh][2] + reds[hh][3]);
+            l_run[hh] = l_run[hh] * corr[hh] + s;
+            m_run[hh] = mt[hh];
+#pragma unroll
+            for (int i = 0; i < 16; i++) acc[hh][i] *= corr[hh];
+        }
+#pragma unroll
+        for (int p = 0; p < PASSES; p++) {
+            const int jj = p * TPP + tp;
+            const uint32_t ww[4] = {vw[buf][p].x, vw[buf][p].y, vw[buf][p].z, vw[buf][p].w};
+#pragma unroll
+            for (int hh = 0; hh < G; hh++) {
+                float pw = sc[hh][jj] * vsc[buf][p] * (1.0f / 127.0f);
+#pragma unroll
+                for (int i = 0; i < 16; i++) acc[hh][i] = fmaf(pw, i8f(ww[i >> 2], i & 3), acc[hh][i]);
+            }
+        }
+        __syncthreads();   // sc is rewritten by the next tile
+    };
+    int t0 = c0;
+    load(0, t0);
+    for (;;) {
+        int nt = t0 + ATTF_TILE;
+        if (nt < c1) load(1, nt);
+        process(0, t0);
+        if (nt >= c1) break;
+        t0 = nt;
+        nt = t0 + ATTF_TILE;
+        if (nt < c1) load(0, nt);
+        process(1, t0);
+        if (nt >= c1) break;
+        t0 = nt;
+    }
+
+    // 4. partials of this split, then the last workgroup of hk merges them
+#pragma unroll
+    for (int hh = 0; hh < G; hh++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) pvred[tp][hh * HD + sl * 16 + i] = acc[hh][i];
+    __syncthreads();
+    const size_t ms = (size_t)a.max_splits;
+    for (int o = tid; o < G * HD; o += 256) {
+        float s = 0.0f;
+        for (int r = 0; r < TPP; r++) s += pvred[r][o];
+        const int hh = o / HD, d = o % HD;
+        a.po[((size_t)(hk * G + hh) * ms + split) * HD + d] = s;
+    }
+    if (tid < G) {
+        a.pml[((size_t)(hk * G + tid) * ms + split) * 2] = m_run[tid];
+        a.pml[((size_t)(hk * G + tid) * ms + split) * 2 + 1] = l_run[tid];
+    }
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) {
+        unsigned prev = __hip_atomic_fetch_add(a.counter + hk, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = prev == (unsigned)(nsplit - 1);
+    }
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+    for (int e = tid; e < G * nsplit * 2; e += 256) {
+        const int hh = e / (nsplit * 2), r = e % (nsplit * 2);
+        s_ml[hh][r >> 1][r & 1] = a.pml[((size_t)(hk * G + hh) * ms + (r >> 1)) * 2 + (r & 1)];
+    }
+    __syncthreads();
+    if (tid < G * HD) {
+        const int hh = tid / HD, d = tid % HD;
+        float M = -3.0e38f;
+        for (int i = 0; i < nsplit; i++) M = fmaxf(M, s_ml[hh][i][0]);
+        float L = 0.0f, o = 0.0f;
+        const float* pp = a.po + (size_t)(hk * G + hh) * ms * HD + d;
+#pragma unroll 16
+        for (int i = 0; i < nsplit; i++) {
+            float e = expf(s_ml[hh][i][0] - M);
+            L += s_ml[hh][i][1] * e;
+            o += pp[(size_t)i * HD] * e;
+        }
+        a.out[(size_t)(hk * G + hh) * HD + d] = o / L;
+    }
+    if (tid == 0) __hip_atomic_store(a.counter + hk, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+}  // namespace
+
+// Fused decode attention; returns TI_ERR_INVALID for head shapes it does not cover
+// (the caller then issues prep + split + combine).
+int ti_attn_fused_launch(ti_ctx* c, const float* q, const float* k, const float* v, const uint16_t* qw,
+                         const uint16_t* kw, uint32_t* kq, float* ks, uint32_t* vq, float* vs, float* out, int nHq,
+                         int nKv, int hd, const int* dpos, int pos, int cap, float theta, float eps, int max_splits) {
+    const int G = nHq / nKv;
+    if (nKv > TI_SYNC_WORDS - TI_SYNC_ATTN) return ti_fail(TI_ERR_INVALID, "fused attention: too many KV heads");
+    if (max_splits <= 0 || max_splits > ATTF_MAXS) max_splits = ATTF_MAXS;
+    AttnFArgs a = {q, k, v, qw, kw, kq, ks, vq, vs, out, c->attn_po, c->attn_ml, c->sync + TI_SYNC_ATTN, dpos, pos,
+                   nKv, max_splits, 128, cap, theta, eps};
+    dim3 grid(nKv * max_splits);
+#define AF(HD_, G_) \
+    if (hd == HD_ && G == G_) { k_attn_fused_q8<HD_, G_><<<grid, 256, 0, c->stream>>>(a); TI_LAUNCHED("k_attn_fused_q8"); return TI_OK; }
+    AF(128, 2) AF(128, 1) AF(64, 2) AF(64, 1)
+#undef AF
+    return ti_fail(TI_ERR_INVALID, "fused attention: no kernel for hd=%d group=%d", hd, G);
+}
+
+extern "C" int ti_attn_step_q8(ti_ctx* c, const float* q, const float* k, const float* v, const uint16_t* qn_w,
+                               const uint16_t* kn_w, uint32_t* kq, float* ks, uint32_t* vq, float* vs, float* out,
+                               int nHq, int nKv, int hd, int pos, int cap, float theta, float eps, int max_splits) {
+    TI_CHECK_CTX(c);
+    TI_REQUIRE(q && k && v && qn_w && kn_w && kq && ks && vq && vs && out, "ti_attn_step_q8: null buffer");
+    TI_REQUIRE(nKv > 0 && nHq % nKv == 0 && nHq <= TI_ATTN_HEADS_MAX, "ti_attn_step_q8: bad heads (nHq=%d nKv=%d)", nHq, nKv);
+    TI_REQUIRE(pos >= 0 && pos < cap, "ti_attn_step_q8: pos %d outside the cache [0, %d)", pos, cap);
+    TI_REQUIRE(al16(kq) && al16(vq), "ti_attn_step_q8: kq/vq must be 16-byte aligned");
+    TI_REQUIRE(max_splits >= 0 && max_splits <= ATTF_MAXS, "ti_attn_step_q8: max_splits in [0, %d]", ATTF_MAXS);
+    return ti_attn_fused_launch(c, q, k, v, qn_w, kn_w, kq, ks, vq, vs, out, nHq, nKv, hd, nullptr, pos, cap, theta, eps,
+                                max_splits);
+}

@@ -5,7 +5,7 @@
 //     plain RMSNorm             models/qwen3.js:60-80
 // Built with -ffp-contract=off: every f32/f64 expression rounds once per
 // operation in the written order, which is what makes these bit-exact.
-#include "ti_internal.h"
+#include "ti_dev.h"
 
 // ---------------------------------------------------------------------------
 // A1: one thread per (row, 32-group). The reference runs this in JavaScript at
@@ -103,51 +103,6 @@ extern "C" int ti_quant_int4_bf16(ti_ctx* c, const uint16_t* w, uint32_t* pack, 
     return TI_OK;
 }
 
-// ---------------------------------------------------------------------------
-// A2: one thread per 32-group. scale = absmax/127, inv = 1/scale (0 if the
-// group is zero), q = clamp(round-half-even(v*inv), -127, 127); the per-16
-// sums feed the ternary identity.
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ void q8_group(const float* v, uint32_t* xq, float* xs, int32_t* xsum16) {
-    float mx = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 32; j++) mx = fmaxf(mx, fabsf(v[j]));
-    float scale = mx / 127.0f;
-    float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
-    *xs = scale;
-    int q[32];
-#pragma unroll
-    for (int j = 0; j < 32; j++) {
-        float p = v[j] * inv;
-        int qi = (int)rintf(p);
-        qi = qi < -127 ? -127 : (qi > 127 ? 127 : qi);
-        q[j] = qi;
-    }
-    uint32_t wds[8];
-#pragma unroll
-    for (int w = 0; w < 8; w++)
-        wds[w] = (uint32_t)(q[4 * w] & 0xff) | ((uint32_t)(q[4 * w + 1] & 0xff) << 8) |
-                 ((uint32_t)(q[4 * w + 2] & 0xff) << 16) | ((uint32_t)(q[4 * w + 3] & 0xff) << 24);
-    uint4* o = reinterpret_cast<uint4*>(xq);
-    o[0] = make_uint4(wds[0], wds[1], wds[2], wds[3]);
-    o[1] = make_uint4(wds[4], wds[5], wds[6], wds[7]);
-    if (xsum16) {
-        int a = 0, b = 0;
-#pragma unroll
-        for (int j = 0; j < 16; j++) { a += q[j]; b += q[16 + j]; }
-        xsum16[0] = a;
-        xsum16[1] = b;
-    }
-}
-
-__device__ __forceinline__ void load32(const float* __restrict__ src, float* v) {
-    const float4* s4 = reinterpret_cast<const float4*>(src);
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        float4 t = s4[i];
-        v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
-    }
-}
 
 __global__ __launch_bounds__(64) void k_quant_act_q8(const float* __restrict__ x, uint32_t* __restrict__ xq,
                                                      float* __restrict__ xs, int32_t* __restrict__ xsum, int ng) {
@@ -180,27 +135,6 @@ extern "C" int ti_quant_act_q8_t(ti_ctx* c, const float* x, uint32_t* xq, float*
     return ti_quant_act_q8_async(c, x, xq, xs, nullptr, (int)ng);
 }
 
-// ---------------------------------------------------------------------------
-// A6 / RMSNorm: one 256-thread workgroup per row. The sum of squares uses the
-// reference's order — 256 strided per-thread partials then a 128..1 tree —
-// so the normalized values, and hence the int8 codes, are reproducible.
-// inv = 1/sqrt(sum/H + eps) with IEEE division and square root.
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ float rms_inv_256(const float* __restrict__ x, int H, float eps, float* red) {
-    int t = threadIdx.x;
-    float s = 0.0f;
-    for (int i = t; i < H; i += 256) { float sq = x[i] * x[i]; s = s + sq; }
-    red[t] = s;
-    __syncthreads();
-#pragma unroll
-    for (int st = 128; st > 0; st >>= 1) {
-        if (t < st) red[t] = red[t] + red[t + st];
-        __syncthreads();
-    }
-    float m = red[0] / (float)H;
-    m = m + eps;
-    return 1.0f / sqrtf(m);
-}
 
 __global__ __launch_bounds__(256) void k_rmsnorm_q8(const float* __restrict__ x, const uint16_t* __restrict__ w,
                                                     uint32_t* __restrict__ xq, float* __restrict__ xs,

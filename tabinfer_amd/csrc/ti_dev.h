@@ -1,0 +1,278 @@
+// ti_dev.h — device helpers shared by the decode-path kernels (gfx950).
+//  int4 x int8 group dots, f32-activation limb dots, the per-32 int8 activation
+//  quantizer and the 256-thread RMSNorm reduction, each in the exact arithmetic
+//  order the reference uses wherever bits matter.
+#pragma once
+#include "ti_internal.h"
+
+namespace {
+
+constexpr uint32_t M4 = 0x0F0F0F0Fu;
+
+__device__ __forceinline__ uint32_t even_bytes(uint32_t a0, uint32_t a1) {   // [x0,x2,x4,x6]
+    return (a0 & 0xffu) | ((a0 >> 8) & 0xff00u) | ((a1 & 0xffu) << 16) | ((a1 << 8) & 0xff000000u);
+}
+__device__ __forceinline__ uint32_t odd_bytes(uint32_t a0, uint32_t a1) {    // [x1,x3,x5,x7]
+    return ((a0 >> 8) & 0xffu) | ((a0 >> 16) & 0xff00u) | ((a1 << 8) & 0xff0000u) | (a1 & 0xff000000u);
+}
+
+// Activation slice of one group for the int8 path.
+struct ActQ8 {
+    int xe[4], xo[4];
+    int corr;      // 8 * sum of the 32 codes
+    float s;       // activation group scale
+};
+
+__device__ __forceinline__ void load_act_q8(const uint32_t* __restrict__ xq, const float* __restrict__ xs, int g, ActQ8& a) {
+    const uint4* p = reinterpret_cast<const uint4*>(xq + (size_t)g * 8);
+    uint4 u0 = p[0], u1 = p[1];
+    uint32_t w[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+    int sum = 0;
+#pragma unroll
+    for (int m = 0; m < 4; m++) {
+        a.xe[m] = (int)even_bytes(w[2 * m], w[2 * m + 1]);
+        a.xo[m] = (int)odd_bytes(w[2 * m], w[2 * m + 1]);
+        sum = __builtin_amdgcn_sdot4((int)w[2 * m], 0x01010101, sum, false);
+        sum = __builtin_amdgcn_sdot4((int)w[2 * m + 1], 0x01010101, sum, false);
+    }
+    a.corr = 8 * sum;
+    a.s = xs ? xs[g] : 0.0f;
+}
+
+// Exact int32 dot of one weight group (16 bytes) with the lane's activation group.
+__device__ __forceinline__ int group_dot_q8(const uint4 w, const ActQ8& a) {
+    int d = 0;
+    d = __builtin_amdgcn_sdot4((int)(w.x & M4), a.xe[0], d, false);
+    d = __builtin_amdgcn_sdot4((int)((w.x >> 4) & M4), a.xo[0], d, false);
+    d = __builtin_amdgcn_sdot4((int)(w.y & M4), a.xe[1], d, false);
+    d = __builtin_amdgcn_sdot4((int)((w.y >> 4) & M4), a.xo[1], d, false);
+    d = __builtin_amdgcn_sdot4((int)(w.z & M4), a.xe[2], d, false);
+    d = __builtin_amdgcn_sdot4((int)((w.z >> 4) & M4), a.xo[2], d, false);
+    d = __builtin_amdgcn_sdot4((int)(w.w & M4), a.xe[3], d, false);
+    d = __builtin_amdgcn_sdot4((int)((w.w >> 4) & M4), a.xo[3], d, false);
+    return d - a.corr;
+}
+
+__device__ __forceinline__ void store_out(float* __restrict__ y, long row, float v, int acc) {
+    y[row] = acc ? y[row] + v : v;
+}
+
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+
+// Weights are streamed exactly once per call: non-temporal loads keep them from
+// displacing the (re-read) activation and scale lines in the caches.
+__device__ __forceinline__ uint4 ld_nt(const uint4* p) {
+    v4u v = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint16_t ld_nt(const uint16_t* p) { return __builtin_nontemporal_load(p); }
+
+// Sum R per-lane accumulators across the LPR lanes that share them, leaving the
+// total of accumulator (li / (LPR/R)) in every lane: each of the first log2(R)
+// butterfly steps hands half of the remaining accumulators to the partner lane,
+// so the whole reduction costs R-1 + log2(LPR/R) shuffles instead of R*log2(LPR).
+template <int LPR, int R>
+__device__ __forceinline__ float transpose_reduce(float (&v)[R], int li) {
+    static_assert(R <= LPR || LPR == 1, "R must not exceed the lanes per row");
+    int k = R;
+#pragma unroll
+    for (int o = LPR / 2; o > 0; o >>= 1) {
+        if (k > 1) {
+            const bool up = (li & o) != 0;
+#pragma unroll
+            for (int i = 0; i < R / 2; i++) {
+                if (i < k / 2) {
+                    float send = up ? v[i] : v[i + k / 2];
+                    float keep = up ? v[i + k / 2] : v[i];
+                    v[i] = keep + __shfl_xor(send, o, 64);
+                }
+            }
+            k >>= 1;
+        } else {
+            v[0] += __shfl_xor(v[0], o, 64);
+        }
+    }
+    return v[0];
+}
+
+// ---------------------------------------------------------------------------
+// A4: y (+)= W x, f32 activation (lm_head path). Per element: one byte->f32
+// convert and one FMA on the unsigned nibble; the -8 offset is removed once per
+// group (sum n*x - 8*sum x).
+// ---------------------------------------------------------------------------
+struct ActF32 {
+    float x[32];   // element order of the group: x[0..31]
+    float corr;    // 8 * sum x
+};
+
+__device__ __forceinline__ void load_act_f32(const float* __restrict__ x, int g, ActF32& a) {
+    const float4* p = reinterpret_cast<const float4*>(x + (size_t)g * 32);
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        float4 t = p[i];
+        a.x[4 * i] = t.x; a.x[4 * i + 1] = t.y; a.x[4 * i + 2] = t.z; a.x[4 * i + 3] = t.w;
+    }
+#pragma unroll
+    for (int i = 0; i < 32; i++) s += a.x[i];
+    a.corr = 8.0f * s;
+}
+
+__device__ __forceinline__ float word_dot_f32(uint32_t p, const float* x8, float acc) {
+    uint32_t lo = p & M4, hi = (p >> 4) & M4;
+    acc = fmaf((float)(lo & 0xffu), x8[0], acc);
+    acc = fmaf((float)(hi & 0xffu), x8[1], acc);
+    acc = fmaf((float)((lo >> 8) & 0xffu), x8[2], acc);
+    acc = fmaf((float)((hi >> 8) & 0xffu), x8[3], acc);
+    acc = fmaf((float)((lo >> 16) & 0xffu), x8[4], acc);
+    acc = fmaf((float)((hi >> 16) & 0xffu), x8[5], acc);
+    acc = fmaf((float)(lo >> 24), x8[6], acc);
+    acc = fmaf((float)(hi >> 24), x8[7], acc);
+    return acc;
+}
+
+__device__ __forceinline__ float group_dot_f32(const uint4 w, const ActF32& a) {
+    float d0 = word_dot_f32(w.x, a.x + 0, 0.0f);
+    float d1 = word_dot_f32(w.y, a.x + 8, 0.0f);
+    float d2 = word_dot_f32(w.z, a.x + 16, 0.0f);
+    float d3 = word_dot_f32(w.w, a.x + 24, 0.0f);
+    return ((d0 + d1) + (d2 + d3)) - a.corr;
+}
+
+// f32 activation as exact fixed point: per 32-group, x_j = X_j * 2^(ex-22) with
+// |X_j| <= 2^22 (ex = exponent of the group absmax), X split into three signed
+// int8 limbs X = l2*65536 + l1*256 + l0. Each limb dots with the nibbles through
+// v_dot4_i32_i8 exactly; the only approximation is rounding x to 22 bits below its
+// group maximum (relative 2^-23), i.e. at the level of f32 rounding itself.
+struct ActLimb {
+    int e[3][4], o[3][4];   // limb l, weight word m: even / odd element bytes
+    int corr[3];            // 8 * sum of limb l
+    float S;                // 2^(ex-22)
+};
+
+__device__ __forceinline__ void load_act_limbs(const float* __restrict__ x, int g, ActLimb& a) {
+    const float4* p = reinterpret_cast<const float4*>(x + (size_t)g * 32);
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        float4 t = p[i];
+        v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
+    }
+    float mx = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 32; j++) mx = fmaxf(mx, fabsf(v[j]));
+    int ex = 0;
+    if (mx > 0.0f) (void)frexpf(mx, &ex);          // mx < 2^ex
+    a.S = ldexpf(1.0f, ex - 22);
+    int lb[3][32];
+#pragma unroll
+    for (int j = 0; j < 32; j++) {
+        int X = mx > 0.0f ? (int)rintf(ldexpf(v[j], 22 - ex)) : 0;
+        int l0 = ((X & 0xff) ^ 0x80) - 0x80;
+        int X1 = (X - l0) >> 8;
+        int l1 = ((X1 & 0xff) ^ 0x80) - 0x80;
+        int l2 = (X1 - l1) >> 8;
+        lb[0][j] = l0; lb[1][j] = l1; lb[2][j] = l2;
+    }
+#pragma unroll
+    for (int l = 0; l < 3; l++) {
+        int sum = 0;
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            const int* q = lb[l] + 8 * m;
+            a.e[l][m] = (int)((uint32_t)(q[0] & 0xff) | ((uint32_t)(q[2] & 0xff) << 8) |
+                              ((uint32_t)(q[4] & 0xff) << 16) | ((uint32_t)(q[6] & 0xff) << 24));
+            a.o[l][m] = (int)((uint32_t)(q[1] & 0xff) | ((uint32_t)(q[3] & 0xff) << 8) |
+                              ((uint32_t)(q[5] & 0xff) << 16) | ((uint32_t)(q[7] & 0xff) << 24));
+            sum += q[0] + q[1] + q[2] + q[3] + q[4] + q[5] + q[6] + q[7];
+        }
+        a.corr[l] = 8 * sum;
+    }
+}
+
+// sum_j (n_j - 8) * x_j for one 16-byte weight group, through the three limbs
+__device__ __forceinline__ float group_dot_limbs(const uint4 w, const ActLimb& a) {
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+    int d[3] = {0, 0, 0};
+#pragma unroll
+    for (int m = 0; m < 4; m++) {
+        int lo = (int)(ws[m] & M4), hi = (int)((ws[m] >> 4) & M4);
+#pragma unroll
+        for (int l = 0; l < 3; l++) {
+            d[l] = __builtin_amdgcn_sdot4(lo, a.e[l][m], d[l], false);
+            d[l] = __builtin_amdgcn_sdot4(hi, a.o[l][m], d[l], false);
+        }
+    }
+    int t = (d[2] - a.corr[2]) * 256 + (d[1] - a.corr[1]);     // |t| < 2^23: exact in f32
+    return fmaf((float)t, 256.0f, (float)(d[0] - a.corr[0])) * a.S;
+}
+
+// ---------------------------------------------------------------------------
+// A2: one thread per 32-group. scale = absmax/127, inv = 1/scale (0 if the
+// group is zero), q = clamp(round-half-even(v*inv), -127, 127); the per-16
+// sums feed the ternary identity.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void q8_group(const float* v, uint32_t* xq, float* xs, int32_t* xsum16) {
+    float mx = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 32; j++) mx = fmaxf(mx, fabsf(v[j]));
+    float scale = mx / 127.0f;
+    float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
+    *xs = scale;
+    int q[32];
+#pragma unroll
+    for (int j = 0; j < 32; j++) {
+        float p = v[j] * inv;
+        int qi = (int)rintf(p);
+        qi = qi < -127 ? -127 : (qi > 127 ? 127 : qi);
+        q[j] = qi;
+    }
+    uint32_t wds[8];
+#pragma unroll
+    for (int w = 0; w < 8; w++)
+        wds[w] = (uint32_t)(q[4 * w] & 0xff) | ((uint32_t)(q[4 * w + 1] & 0xff) << 8) |
+                 ((uint32_t)(q[4 * w + 2] & 0xff) << 16) | ((uint32_t)(q[4 * w + 3] & 0xff) << 24);
+    uint4* o = reinterpret_cast<uint4*>(xq);
+    o[0] = make_uint4(wds[0], wds[1], wds[2], wds[3]);
+    o[1] = make_uint4(wds[4], wds[5], wds[6], wds[7]);
+    if (xsum16) {
+        int a = 0, b = 0;
+#pragma unroll
+        for (int j = 0; j < 16; j++) { a += q[j]; b += q[16 + j]; }
+        xsum16[0] = a;
+        xsum16[1] = b;
+    }
+}
+
+__device__ __forceinline__ void load32(const float* __restrict__ src, float* v) {
+    const float4* s4 = reinterpret_cast<const float4*>(src);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        float4 t = s4[i];
+        v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// A6 / RMSNorm: one 256-thread workgroup per row. The sum of squares uses the
+// reference's order — 256 strided per-thread partials then a 128..1 tree —
+// so the normalized values, and hence the int8 codes, are reproducible.
+// inv = 1/sqrt(sum/H + eps) with IEEE division and square root.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float rms_inv_256(const float* __restrict__ x, int H, float eps, float* red) {
+    int t = threadIdx.x;
+    float s = 0.0f;
+    for (int i = t; i < H; i += 256) { float sq = x[i] * x[i]; s = s + sq; }
+    red[t] = s;
+    __syncthreads();
+#pragma unroll
+    for (int st = 128; st > 0; st >>= 1) {
+        if (t < st) red[t] = red[t] + red[t + st];
+        __syncthreads();
+    }
+    float m = red[0] / (float)H;
+    m = m + eps;
+    return 1.0f / sqrtf(m);
+}
+
+}  // namespace

@@ -33,6 +33,9 @@ struct ti_ctx {
     uint32_t* moe_off;
     uint32_t* moe_fill;
     uint32_t* moe_sidx;
+    // device-scope counters of "last workgroup finishes the reduction" kernels;
+    // zero between launches (each kernel's last workgroup resets its own)
+    uint32_t* sync;
 };
 
 struct ti_graph {
@@ -52,6 +55,9 @@ struct ti_graph {
 #define TI_AMAX_PARTS 1024
 #define TI_MOE_P_MAX 8192
 #define TI_MOE_E_MAX 256
+#define TI_SYNC_WORDS 256
+#define TI_SYNC_LMHEAD 0          // lm_head argmax
+#define TI_SYNC_ATTN 64           // fused attention: one counter per KV head (up to 64)
 
 // ---- device helpers -----------------------------------------------------------
 // f16 bits -> f32 (exact).

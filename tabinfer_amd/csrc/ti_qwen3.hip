@@ -22,6 +22,16 @@ int ti_attn_prep_launch(ti_ctx*, const float*, const float*, const float*, const
                         uint32_t*, float*, uint32_t*, float*, int, int, int, int, float, float, const int*);
 int ti_attn_decode_launch(ti_ctx*, const float*, const uint32_t*, const float*, const uint32_t*, const float*, float*,
                           int, int, int, int, int, int, const int*, int);
+int ti_attn_fused_launch(ti_ctx*, const float*, const float*, const float*, const uint16_t*, const uint16_t*, uint32_t*,
+                         float*, uint32_t*, float*, float*, int, int, int, const int*, int, int, float, float, int);
+int ti_fused_qkv_launch(ti_ctx*, const float*, const uint16_t*, float, int, int, const uint32_t* const*,
+                        const uint16_t* const*, float* const*, const int*, uint32_t*, float*);
+int ti_fused_linear_launch(ti_ctx*, const float*, const uint32_t*, const uint16_t*, float*, int, int, int);
+int ti_fused_gateup_launch(ti_ctx*, const float*, const uint16_t*, float, const uint32_t*, const uint16_t*,
+                           const uint32_t*, const uint16_t*, float*, int, int);
+int ti_fused_lmhead_launch(ti_ctx*, const float*, const uint16_t*, float, const uint32_t*, const uint16_t*, float*, int,
+                           int, uint32_t*, int*, int, int);
+int ti_fused_kmax(int lm);
 
 // ---------------------------------------------------------------------------
 // glue kernels
@@ -168,6 +178,14 @@ extern "C" int ti_qwen3_create(ti_ctx* c, const ti_qwen3_config* cfg, ti_qwen3**
     TI_REQUIRE(C.max_tokens <= TI_ACT_TMAX && C.max_tokens * C.n_heads <= TI_ATTN_ROWS_MAX,
                "ti_qwen3_create: max_tokens too large");
     TI_REQUIRE((C.max_ctx + 127) / 128 <= TI_ATTN_SPLITS_MAX, "ti_qwen3_create: max_ctx > %d", TI_ATTN_SPLITS_MAX * 128);
+    TI_REQUIRE(C.n_heads / C.n_kv_heads <= 2 && (C.head_dim == 64 || C.head_dim == 128),
+               "ti_qwen3_create: the decode step covers head_dim 64/128 with at most 2 query heads per KV head");
+    {
+        int kmax = C.hidden > C.intermediate ? C.hidden : C.intermediate;
+        kmax = kmax > C.n_heads * C.head_dim ? kmax : C.n_heads * C.head_dim;
+        TI_REQUIRE(kmax <= ti_fused_kmax(0) && C.hidden <= ti_fused_kmax(1),
+                   "ti_qwen3_create: hidden <= %d and projection inputs <= %d required", ti_fused_kmax(1), ti_fused_kmax(0));
+    }
     TI_REQUIRE(!c->capturing, "ti_qwen3_create: not during graph capture");
     TI_HIP(hipSetDevice(c->device));
     ti_qwen3* m = new ti_qwen3();
@@ -310,15 +328,40 @@ extern "C" int ti_qwen3_read_tokens(ti_ctx* c, ti_qwen3* m, int from, int count,
     return ti_buf_read(c, m->hist, (size_t)from * 4, ids, (size_t)count * 4);
 }
 
-static int argmax_launch(ti_ctx* c, ti_qwen3* m, int out_pos, const int* dpos) {
-    k_argmax_p1<<<AMX_PARTS, AMX_THREADS, 0, c->stream>>>(m->logits, m->cfg.vocab, m->amx_v, m->amx_i);
+// argmaxKernel (models/qwen3.js:2681-2690): tok_hist[out_pos] = argmax(logits[0..N)),
+// lowest index on ties, two stages.
+extern "C" int ti_argmax(ti_ctx* c, const float* logits, int N, uint32_t* tok_hist, int out_pos) {
+    TI_CHECK_CTX(c);
+    TI_REQUIRE(logits && tok_hist, "ti_argmax: null buffer");
+    TI_REQUIRE(N > 0 && out_pos >= 0, "ti_argmax: need N > 0 and out_pos >= 0 (N=%d out_pos=%d)", N, out_pos);
+    TI_REQUIRE(AMX_PARTS <= TI_AMAX_PARTS, "ti_argmax: partial buffer too small");
+    k_argmax_p1<<<AMX_PARTS, AMX_THREADS, 0, c->stream>>>(logits, N, c->amax_v, c->amax_i);
     TI_LAUNCHED("k_argmax_p1");
-    k_argmax_p2<<<1, AMX_PARTS, 0, c->stream>>>(m->amx_v, m->amx_i, m->hist, out_pos, (int*)dpos, 1);
+    k_argmax_p2<<<1, AMX_PARTS, 0, c->stream>>>(c->amax_v, c->amax_i, tok_hist, out_pos, nullptr, 0);
     TI_LAUNCHED("k_argmax_p2");
     return TI_OK;
 }
 
-// One decode step at the device position (forward(null, pos, {chain: true})).
+// embedGather (models/qwen3.js:1663-1676): y[t, :] = f32(emb[ids[id_off + t], :]) for
+// t < T; ids at or past `vocab` read the last row (no out-of-bounds read).
+extern "C" int ti_embed(ti_ctx* c, const int32_t* ids, const uint16_t* emb, float* y, int T, int H, int id_off,
+                        int vocab) {
+    TI_CHECK_CTX(c);
+    TI_REQUIRE(ids && emb && y, "ti_embed: null buffer");
+    TI_REQUIRE(T > 0 && H > 0 && id_off >= 0 && vocab > 0, "ti_embed: bad shape (T=%d H=%d off=%d vocab=%d)", T, H, id_off, vocab);
+    k_embed<<<(unsigned)(((long)T * H + 255) / 256), 256, 0, c->stream>>>(reinterpret_cast<const uint32_t*>(ids), emb, y,
+                                                                           T, H, id_off, nullptr, vocab);
+    TI_LAUNCHED("k_embed");
+    return TI_OK;
+}
+
+// One decode step at the device position (forward(null, pos, {chain: true}),
+// models/qwen3.js:3951-4055) in 2 + 5 x layers launches:
+//   embed(tok[pos])
+//   per layer: [rmsnormQ + q/k/v GEMVs] [attnPrep + split-KV attention + combine]
+//              [quantQ8 + o_proj + residual] [rmsnormQ + gate/up + SiLU]
+//              [quantQ8 + down_proj + residual]
+//   [final rmsnorm + lm_head + argmax -> tok[pos+1], pos += 1]
 extern "C" int ti_qwen3_decode(ti_ctx* c, ti_qwen3* m) {
     TI_CHECK_CTX(c);
     TI_REQUIRE(m, "ti_qwen3_decode: null model");
@@ -331,23 +374,20 @@ extern "C" int ti_qwen3_decode(ti_ctx* c, ti_qwen3* m) {
     TI_LAUNCHED("k_embed");
     for (int l = 0; l < C.layers; l++) {
         Layer& y = m->L[l];
-        RC(ti_rmsnorm_q8(c, m->x, y.in_norm, m->xq, m->xs, m->xsum, H, C.rms_eps));
-        RC(ti_gemv_q4_q8_launch(c, m->xq, m->xs, y.q.pack, y.q.sc, m->q, nq, H, 0));
-        RC(ti_gemv_q4_q8_launch(c, m->xq, m->xs, y.k.pack, y.k.sc, m->k, nkv, H, 0));
-        RC(ti_gemv_q4_q8_launch(c, m->xq, m->xs, y.v.pack, y.v.sc, m->v, nkv, H, 0));
-        RC(ti_attn_prep_launch(c, m->q, m->k, m->v, y.q_norm, y.k_norm, m->qr, y.kq, y.ks, y.vq, y.vs, nHq, nKv, hd, 0,
-                               C.rope_theta, C.rms_eps, m->dpos));
-        RC(ti_attn_decode_launch(c, m->qr, y.kq, y.ks, y.vq, y.vs, m->attn, 0, 1, nHq, nKv, hd, 0, m->dpos, C.max_ctx));
-        RC(ti_quant_act_q8_async(c, m->attn, m->xq, m->xs, nullptr, nq / 32));
-        RC(ti_gemv_q4_q8_launch(c, m->xq, m->xs, y.o.pack, y.o.sc, m->x, H, nq, 1));
-        RC(ti_rmsnorm_q8(c, m->x, y.post_norm, m->xq, m->xs, m->xsum, H, C.rms_eps));
-        RC(ti_gateup_launch(c, m->xq, m->xs, y.gate.pack, y.gate.sc, y.up.pack, y.up.sc, m->swi, I, H));
-        RC(ti_quant_act_q8_async(c, m->swi, m->xq, m->xs, nullptr, I / 32));
-        RC(ti_gemv_q4_q8_launch(c, m->xq, m->xs, y.down.pack, y.down.sc, m->x, H, I, 1));
+        const uint32_t* packs[3] = {y.q.pack, y.k.pack, y.v.pack};
+        const uint16_t* scs[3] = {y.q.sc, y.k.sc, y.v.sc};
+        float* ys[3] = {m->q, m->k, m->v};
+        const int Ns[3] = {nq, nkv, nkv};
+        RC(ti_fused_qkv_launch(c, m->x, y.in_norm, C.rms_eps, H, 3, packs, scs, ys, Ns, nullptr, nullptr));
+        RC(ti_attn_fused_launch(c, m->q, m->k, m->v, y.q_norm, y.k_norm, y.kq, y.ks, y.vq, y.vs, m->attn, nHq, nKv, hd,
+                                m->dpos, 0, C.max_ctx, C.rope_theta, C.rms_eps, 0));
+        RC(ti_fused_linear_launch(c, m->attn, y.o.pack, y.o.sc, m->x, H, nq, 1));
+        RC(ti_fused_gateup_launch(c, m->x, y.post_norm, C.rms_eps, y.gate.pack, y.gate.sc, y.up.pack, y.up.sc, m->swi,
+                                  I, H));
+        RC(ti_fused_linear_launch(c, m->swi, y.down.pack, y.down.sc, m->x, H, I, 1));
     }
-    RC(ti_rmsnorm(c, m->x, m->final_norm, m->normed, 1, H, C.rms_eps));
-    RC(ti_gemv_q4_f32_launch(c, m->normed, m->lm.pack, m->lm.sc, m->logits, C.vocab, H, 0));
-    RC(argmax_launch(c, m, 0, m->dpos));
+    RC(ti_fused_lmhead_launch(c, m->x, m->final_norm, C.rms_eps, m->lm.pack, m->lm.sc, m->logits, C.vocab, H, m->hist,
+                              m->dpos, 0, C.max_ctx));
     return TI_OK;
 }
 
@@ -387,9 +427,8 @@ extern "C" int ti_qwen3_forward(ti_ctx* c, ti_qwen3* m, const int32_t* ids, int 
     }
     k_copy_f32<<<(H + 255) / 256, 256, 0, c->stream>>>(m->x + (size_t)(T - 1) * H, m->last, H);
     TI_LAUNCHED("k_copy_f32");
-    RC(ti_rmsnorm(c, m->last, m->final_norm, m->normed, 1, H, C.rms_eps));
-    RC(ti_gemv_q4_f32_launch(c, m->normed, m->lm.pack, m->lm.sc, m->logits, C.vocab, H, 0));
-    RC(argmax_launch(c, m, pos + T, nullptr));
+    RC(ti_fused_lmhead_launch(c, m->last, m->final_norm, C.rms_eps, m->lm.pack, m->lm.sc, m->logits, C.vocab, H, m->hist,
+                              nullptr, pos + T, C.max_ctx));
     k_set_int<<<1, 1, 0, c->stream>>>(m->dpos, pos + T);
     TI_LAUNCHED("k_set_int");
     return TI_OK;
