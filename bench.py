@@ -1,22 +1,28 @@
 #!/usr/bin/env python3
 """Benchmark of the quantized decode hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only gemv]
 
-Workload (one "step"): the int4 GEMV set of one Qwen3-0.6B decode step at batch
-1, launched exactly as the reference's decode issues it (models/qwen3.js:
-3981-4049): per layer q/k/v GEMVs on the RMSNorm'd int8 activation (projGemv),
-o_proj through linearQ (int8 quantize + GEMV, fused residual), fused
-gate+up+SiLU, down_proj through linearQ; then the lm_head through linearQ's
-f32-activation GEMV (N = 151936 >= 16384). 28 layers, hidden 1024,
-intermediate 3072, 16/8 heads of dim 128. Weights are seeded bf16 N(0, 0.02)
-quantized on the GPU by the int4 quantizer (the reference's quantizeInt4Bf16);
-activations are seeded N(0,1) rounded to f16. Two independent weight sets
-(2 x 335 MB) alternate between steps so every step streams its weights from HBM,
-not from the 256 MB Infinity Cache. Each step is one captured HIP graph.
+Headline workload (`value`): the int4 GEMV set of one Qwen3-0.6B batch-1 decode
+step (hidden 1024, intermediate 3072, 16/8 heads of dim 128, 28 layers, vocab
+151936), launched the way the decode step launches it (models/qwen3.js:
+3981-4049, fused here): per layer [rmsnormQ + q/k/v GEMVs] [o_proj GEMV on the
+int8 attention output + residual] [rmsnormQ + gate/up + SiLU + quantQ8 of swi]
+[down_proj GEMV + residual], then [final rmsnorm + lm_head 151936x1024 + argmax]. Weights are seeded bf16
+N(0, 0.02) quantized on the GPU by the int4 quantizer; activations are seeded
+N(0,1) rounded to f16. Two independent weight sets (2 x 337 MB) alternate
+between steps, so every step streams its weights from HBM, not from the 256 MB
+Infinity Cache. Each step is one captured HIP graph; `value` = algorithmic
+bytes of the step / wall time of the timed steps (launch gaps included).
 
-Prints one JSON line: value = algorithmic GB/s of the whole step (weights +
-activations + outputs, counted once per launch) over the timed steps.
+Beside it, each bounded to a few seconds (not `value`):
+  decode_1p7b   full Qwen3-1.7B int4/int8-KV decode step (the native decoder, one
+                graph per token, device-side token chaining) at 8k and 32k
+                prefix contexts: tokens/s and whole-step GB/s
+  attention     fused split-KV attention per layer at 4k and 32k (GB/s)
+  ternary       Bonsai-1.7B ternary GEMV set of one layer (GB/s)
+  cpu_baseline  the oracle's int4 GEMV (C, 1 thread) on a bounded sample of the
+                same GEMV set; cpu_tern_avx2: the n2 AVX2 ternary GEMV restated in C
 """
 import argparse
 import json
@@ -30,167 +36,364 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+METRIC = "int4 GEMV HBM GB/s (% of peak) + Qwen3-1.7B bs1 decode tok/s at 32k ctx"
 
 QWEN3_06B = dict(layers=28, hidden=1024, inter=3072, n_heads=16, n_kv=8, head_dim=128, vocab=151936)
+QWEN3_17B = dict(layers=28, hidden=2048, inter=6144, n_heads=16, n_kv=8, head_dim=128, vocab=151936)
 
 
+def log(msg):
+    print("[bench] " + msg, file=sys.stderr, flush=True)
+
+
+# ---- algorithmic bytes (each operand counted once per launch) ------------------------
 def int4_bytes(N, K):
     return N * K // 2 + (N * K // 32) * 2
 
 
-def gemv_q8_bytes(N, K):       # weights + int8 act (codes + scales) + f32 out
-    return int4_bytes(N, K) + K + (K // 32) * 4 + N * 4
+def qkv_bytes(Ns, K):          # f32 x + f16 norm weight in, weights, f32 outputs
+    return K * 4 + K * 2 + sum(int4_bytes(N, K) + N * 4 for N in Ns)
 
 
-def linear_q8_bytes(N, K):     # f32 act in, quantized inside linearQ
-    return int4_bytes(N, K) + K * 4 + N * 4
+def q8_linear_bytes(N, K):     # int8 activation (codes + scales) in, weights, residual read + write
+    return K + (K // 32) * 4 + int4_bytes(N, K) + 2 * N * 4
 
 
-def gemv_f32_bytes(N, K):
-    return int4_bytes(N, K) + K * 4 + N * 4
+def gateup_bytes(I, H):        # f32 x + norm weight in, gate/up weights, swi out as int8 codes + scales
+    return H * 4 + H * 2 + 2 * int4_bytes(I, H) + I + (I // 32) * 4
 
 
-def gateup_bytes(I, H):
-    return 2 * int4_bytes(I, H) + H + (H // 32) * 4 + I * 4
+def lmhead_bytes(N, K):        # f32 x + norm weight in, weights, logits out
+    return K * 4 + K * 2 + int4_bytes(N, K) + N * 4
 
 
+def kv_bytes(S, nKv, hd):      # int8 K and V + their f32 scales, positions [0, S)
+    return S * 2 * (nKv * hd + (nKv * hd // 32) * 4)
+
+
+class Pool:
+    """A device pool of seeded bf16 N(0, 0.02) values from which weights are quantized."""
+
+    def __init__(self, ctx, n, seed):
+        rng = np.random.default_rng(seed)
+        w = (rng.standard_normal(n, dtype=np.float32) * np.float32(0.02))
+        self.buf = ctx.upload((w.view(np.uint32) >> 16).astype(np.uint16))
+        self.n = n
+        self.ctx = ctx
+
+    def quantize_into(self, pack, sc, N, K, rng):
+        rows_per = max(1, min(N, self.n // K))
+        r = 0
+        while r < N:
+            nr = min(rows_per, N - r)
+            off = int(rng.integers(0, (self.n - nr * K) // 32 + 1)) * 32
+            self.ctx.call("ti_quant_int4_bf16", self.buf.at(off * 2), int(pack) + r * K // 2,
+                          int(sc) + r * K // 32 * 2, nr, K)
+            r += nr
+
+    def quantized(self, N, K, rng):
+        pack = self.ctx.alloc(N * K // 2)
+        sc = self.ctx.alloc(N * K // 32 * 2)
+        self.quantize_into(pack, sc, N, K, rng)
+        return pack, sc
+
+
+# ---- the headline GEMV set ------------------------------------------------------------
 class GemvSet:
-    """Device-resident weights and activations of one 0.6B decode step."""
+    """Device-resident int4 weights of one decode step's GEMVs."""
 
     def __init__(self, ctx, cfg, seed, pool):
-        from tabinfer_amd import abi
-        self.ctx, self.cfg = ctx, cfg
         H, I = cfg["hidden"], cfg["inter"]
         nq = cfg["n_heads"] * cfg["head_dim"]
         nkv = cfg["n_kv"] * cfg["head_dim"]
         rng = np.random.default_rng(seed)
         self.shapes = {"q": (nq, H), "k": (nkv, H), "v": (nkv, H), "o": (H, nq),
                        "gate": (I, H), "up": (I, H), "down": (H, I)}
-        self.layers = []
-        for _ in range(cfg["layers"]):
-            L = {}
-            for name, (N, K) in self.shapes.items():
-                L[name] = self._quantized(N, K, rng, pool)
-            self.layers.append(L)
-        self.lm = self._quantized(cfg["vocab"], H, rng, pool)
-
-    def _quantized(self, N, K, rng, pool):
-        """int4-quantize N x K bf16 weights drawn from the device pool, on the GPU."""
-        ctx = self.ctx
-        pack = ctx.alloc(N * K // 2)
-        sc = ctx.alloc(N * K // 32 * 2)
-        pool_buf, pool_n = pool
-        rows_per = max(1, min(N, pool_n // K))
-        r = 0
-        while r < N:
-            nr = min(rows_per, N - r)
-            span = nr * K
-            off = int(rng.integers(0, (pool_n - span) // 32 + 1)) * 32
-            ctx.call("ti_quant_int4_bf16", pool_buf.at(off * 2), pack.at(r * K // 2), sc.at(r * K // 32 * 2), nr, K)
-            r += nr
-        return pack, sc
+        self.layers = [{n: pool.quantized(N, K, rng) for n, (N, K) in self.shapes.items()} for _ in range(cfg["layers"])]
+        self.lm = pool.quantized(cfg["vocab"], H, rng)
 
 
-def make_pool(ctx, n, seed):
-    rng = np.random.default_rng(seed)
-    w = (rng.standard_normal(n, dtype=np.float32) * np.float32(0.02))
-    bf = (w.view(np.uint32) >> 16).astype(np.uint16)
-    return ctx.upload(bf), n
+def c_ptrs(vals):
+    import ctypes as C
+    arr = (C.c_void_p * len(vals))()
+    for i, v in enumerate(vals):
+        arr[i] = int(v)
+    return arr
+
+
+def c_ints(vals):
+    import ctypes as C
+    arr = (C.c_int * len(vals))()
+    for i, v in enumerate(vals):
+        arr[i] = v
+    return arr
 
 
 class Step:
-    """The launch sequence of one decode step's GEMV set (and its byte count)."""
+    """The launch sequence of one decode step's GEMV set, and its byte count."""
 
-    def __init__(self, ctx, cfg, act):
-        self.ctx, self.cfg, self.act = ctx, cfg, act
+    FAMILIES = ("qkv", "o_proj", "gateup", "down", "lm_head")
+
+    def __init__(self, ctx, cfg):
+        self.ctx, self.cfg = ctx, cfg
         H, I = cfg["hidden"], cfg["inter"]
-        nq = cfg["n_heads"] * cfg["head_dim"]
-        nkv = cfg["n_kv"] * cfg["head_dim"]
-        per_layer = (gemv_q8_bytes(nq, H) + 2 * gemv_q8_bytes(nkv, H) + linear_q8_bytes(H, nq)
-                     + gateup_bytes(I, H) + linear_q8_bytes(H, I))
-        self.bytes = cfg["layers"] * per_layer + gemv_f32_bytes(cfg["vocab"], H)
-        self.launches = cfg["layers"] * 8 + 1   # 3 gemv + 2x(quant+gemv) + gateup, + lm_head
+        self.nq = cfg["n_heads"] * cfg["head_dim"]
+        self.nkv = cfg["n_kv"] * cfg["head_dim"]
+        rng = np.random.default_rng(7)
+        f16 = lambda n: rng.standard_normal(n).astype(np.float16).astype(np.float32)
+        self.x = ctx.upload(f16(H))                       # residual stream
+        # the attention output as the fused attention leaves it: quantized per 32 (quantQ8)
+        self.attn_q, self.attn_s = ctx.zeros(self.nq), ctx.zeros(self.nq // 8)
+        ctx.call("ti_quant_act_q8", ctx.upload(f16(self.nq)), self.attn_q, self.attn_s, None, self.nq)
+        self.swq, self.sws = ctx.zeros(I), ctx.zeros(I // 8)    # swi, quantized by the gate/up kernel
+        self.norm = ctx.upload(np.full(H, 0x3C00, np.uint16))   # RMSNorm weights 1.0
+        self.q, self.k, self.v = ctx.zeros(self.nq * 4), ctx.zeros(self.nkv * 4), ctx.zeros(self.nkv * 4)
+        self.logits = ctx.zeros(cfg["vocab"] * 4)
+        self.hist = ctx.zeros(64)
+        self.fam_bytes = {
+            "qkv": qkv_bytes((self.nq, self.nkv, self.nkv), H),
+            "o_proj": q8_linear_bytes(H, self.nq),
+            "gateup": gateup_bytes(I, H),
+            "down": q8_linear_bytes(H, I),
+            "lm_head": lmhead_bytes(cfg["vocab"], H),
+        }
+        L = cfg["layers"]
+        self.fam_launches = {"qkv": L, "o_proj": L, "gateup": L, "down": L, "lm_head": 1}
+        self.bytes = sum(self.fam_bytes[f] * self.fam_launches[f] for f in self.FAMILIES)
+        self.launches = sum(self.fam_launches.values())
 
-    def issue(self, ws):
-        c, a, cfg = self.ctx, self.act, self.cfg
+    def issue(self, ws, families=FAMILIES):
+        c, cfg = self.ctx, self.cfg
         H, I = cfg["hidden"], cfg["inter"]
-        nq = cfg["n_heads"] * cfg["head_dim"]
-        nkv = cfg["n_kv"] * cfg["head_dim"]
-        for L in ws.layers:
-            c.call("ti_gemv_q4_q8", a["xq"], a["xs"], *L["q"], a["q"], nq, H, 0)
-            c.call("ti_gemv_q4_q8", a["xq"], a["xs"], *L["k"], a["k"], nkv, H, 0)
-            c.call("ti_gemv_q4_q8", a["xq"], a["xs"], *L["v"], a["v"], nkv, H, 0)
-            c.call("ti_linear_q4", a["attn"], *L["o"], a["x"], 1, H, nq, 1)
-            c.call("ti_gateup_silu_q4", a["xq"], a["xs"], *L["gate"], *L["up"], a["swi"], I, H)
-            c.call("ti_linear_q4", a["swi"], *L["down"], a["x"], 1, H, I, 1)
-        c.call("ti_linear_q4", a["last"], *ws.lm, a["logits"], 1, cfg["vocab"], H, 0)
+        eps = np.float32(1e-6)
+        for Lw in ws.layers:
+            if "qkv" in families:
+                c.call("ti_rmsnorm_gemv_q4", self.x, self.norm, eps, H, 3,
+                       c_ptrs([Lw["q"][0], Lw["k"][0], Lw["v"][0]]), c_ptrs([Lw["q"][1], Lw["k"][1], Lw["v"][1]]),
+                       c_ptrs([self.q, self.k, self.v]), c_ints([self.nq, self.nkv, self.nkv]), None, None)
+            if "o_proj" in families:
+                c.call("ti_gemv_q4_q8", self.attn_q, self.attn_s, *Lw["o"], self.x, H, self.nq, 1)
+            if "gateup" in families:
+                c.call("ti_rmsnorm_gateup_silu_q4", self.x, self.norm, eps, *Lw["gate"], *Lw["up"], None, I, H,
+                       self.swq, self.sws)
+            if "down" in families:
+                c.call("ti_gemv_q4_q8", self.swq, self.sws, *Lw["down"], self.x, H, I, 1)
+        if "lm_head" in families:
+            c.call("ti_rmsnorm_lm_head_argmax", self.x, self.norm, eps, *ws.lm, self.logits, cfg["vocab"], H,
+                   self.hist, 1)
 
 
-def make_acts(ctx, cfg, seed):
-    rng = np.random.default_rng(seed)
-    H, I = cfg["hidden"], cfg["inter"]
-    nq = cfg["n_heads"] * cfg["head_dim"]
-    f16 = lambda n: rng.standard_normal(n).astype(np.float16).astype(np.float32)
-    x_norm = f16(H)
-    a = {}
-    # q/k/v and gate/up read the RMSNorm'd int8 activation (quantized on the GPU)
-    dx = ctx.upload(x_norm)
-    a["xq"], a["xs"], a["xsum"] = ctx.zeros(H), ctx.zeros(H // 8), ctx.zeros(H // 4)
-    ctx.call("ti_quant_act_q8", dx, a["xq"], a["xs"], a["xsum"], H)
-    a["attn"] = ctx.upload(f16(nq))
-    a["last"] = ctx.upload(f16(H))
-    a["x"] = ctx.upload(f16(H))
-    for name, n in (("q", nq), ("k", cfg["n_kv"] * cfg["head_dim"]), ("v", cfg["n_kv"] * cfg["head_dim"]),
-                    ("swi", I), ("logits", cfg["vocab"])):
-        a[name] = ctx.zeros(n * 4)
-    return a
+def graph_of(ctx, issue):
+    ctx.graph_begin()
+    issue()
+    return ctx.graph_end()
 
 
-def kernel_profile(ctx, step, ws, lm_copies):
-    """Average duration of each kernel family over its launches in one step: the
-    family's launches (real shapes, all 28 layers' weights) are captured into one
-    graph and timed with HIP events on the context stream, so the average includes
-    the back-to-back dispatch gaps (a lower bound on the kernel's bandwidth)."""
-    cfg, a = step.cfg, step.act
-    H, I = cfg["hidden"], cfg["inter"]
-    nq = cfg["n_heads"] * cfg["head_dim"]
-    nkv = cfg["n_kv"] * cfg["head_dim"]
-    fams = {}
+def time_graphs(ctx, graphs, reps):
+    """Average ms of one graph launch over `reps` launches cycling through `graphs`."""
+    ctx.sync()
+    ctx.record(20)
+    for i in range(reps):
+        ctx.graph_launch(graphs[i % len(graphs)])
+    ctx.record(21)
+    ctx.sync()
+    return ctx.elapsed_ms(20, 21) / reps
 
-    def timed(name, issue, n, nbytes):
-        ctx.graph_begin()
-        issue()
-        g = ctx.graph_end()
+
+class Flush:
+    """Evicts the 256 MB Infinity Cache (and L2) between timed graph launches: a
+    512 MB device-to-device copy, outside the timed interval."""
+
+    def __init__(self, ctx, nbytes=512 << 20):
+        self.ctx = ctx
+        self.buf = ctx.alloc(2 * nbytes)
+        self.n = nbytes
+
+    def __call__(self):
+        self.ctx.call("ti_buf_copy", self.buf, self.n, self.buf, 0, self.n)
+
+
+def cold_ms(ctx, graphs, reps, flush):
+    """Average ms of one graph launch, each launch timed alone (HIP events on the
+    context stream) after a cache flush, cycling through `graphs`."""
+    total = 0.0
+    for i in range(reps):
+        flush()
+        ctx.record(30)
+        ctx.graph_launch(graphs[i % len(graphs)])
+        ctx.record(31)
         ctx.sync()
-        ctx.record(0)
-        ctx.graph_launch(g)
-        ctx.record(1)
-        ms = ctx.elapsed_ms(0, 1)
+        total += ctx.elapsed_ms(30, 31)
+    return total / reps
+
+
+def family_profile(ctx, step, sets, flush, reps=12):
+    """Per kernel family: its launches of one step (real shapes, all layers' weights)
+    captured into one graph and timed with HIP events after a cache flush; the
+    average per launch includes the back-to-back dispatch gaps inside the graph."""
+    out = {}
+    for fam in Step.FAMILIES:
+        gs = [graph_of(ctx, lambda ws=ws: step.issue(ws, (fam,))) for ws in sets]
+        time_graphs(ctx, gs, 2)
+        ms = cold_ms(ctx, gs, reps, flush)
+        n = step.fam_launches[fam]
+        us = ms * 1e3 / n
+        out[fam] = {"launches_per_step": n, "avg_us": round(us, 3), "bytes_per_launch": step.fam_bytes[fam],
+                    "GB_s": round(step.fam_bytes[fam] / (us * 1e-6) / 1e9, 1)}
+        for g in gs:
+            ctx.graph_destroy(g)
+    return out
+
+
+# ---- full Qwen3-1.7B decode ----------------------------------------------------------------
+def decode_1p7b(ctx, pool, contexts=(8192, 32768), steps=64):
+    from tabinfer_amd import abi
+    cfg = QWEN3_17B
+    H, I, hd = cfg["hidden"], cfg["inter"], cfg["head_dim"]
+    nq, nkv = cfg["n_heads"] * hd, cfg["n_kv"] * hd
+    cap = max(contexts) + steps + 8
+    m = abi.Qwen3(ctx, layers=cfg["layers"], hidden=H, intermediate=I, n_heads=cfg["n_heads"], n_kv_heads=cfg["n_kv"],
+                  head_dim=hd, vocab=cfg["vocab"], rope_theta=1e6, rms_eps=1e-6, max_ctx=cap, max_tokens=8)
+    rng = np.random.default_rng(17)
+    shapes = {"self_attn.q_proj.weight": (nq, H), "self_attn.k_proj.weight": (nkv, H),
+              "self_attn.v_proj.weight": (nkv, H), "self_attn.o_proj.weight": (H, nq),
+              "mlp.gate_proj.weight": (I, H), "mlp.up_proj.weight": (I, H), "mlp.down_proj.weight": (H, I)}
+    wbytes = 0
+    for l in range(cfg["layers"]):
+        for name, (N, K) in shapes.items():
+            d, nd, s, ns = m.tensor("model.layers.%d.%s" % (l, name))
+            pool.quantize_into(d, s, N, K, rng)
+            wbytes += nd + ns
+        for name in ("input_layernorm.weight", "post_attention_layernorm.weight", "self_attn.q_norm.weight",
+                     "self_attn.k_norm.weight"):
+            d, nd, _, _ = m.tensor("model.layers.%d.%s" % (l, name))
+            ctx.fill_u32(d, 0x3C003C00, nd // 4)      # norm weights 1.0
+    d, nd, s, ns = m.tensor("lm_head.weight")
+    pool.quantize_into(d, s, cfg["vocab"], H, rng)
+    wbytes += nd + ns
+    d, nd, _, _ = m.tensor("model.norm.weight")
+    ctx.fill_u32(d, 0x3C003C00, nd // 4)
+    d, nd, _, _ = m.tensor("model.embed_tokens.weight")   # f16 embeddings: N(0,0.02) bf16 pool bits as f16
+    done = 0
+    while done < nd:
+        n = min(nd - done, pool.n * 2)
+        ctx.call("ti_buf_copy", d, done, pool.buf, 0, n)
+        done += n
+    # seeded random prefix KV, written through the KV quantizer (kvQuantWrite)
+    chunk = 2048
+    kx = ctx.upload(rng.standard_normal(chunk * nkv).astype(np.float16).astype(np.float32))
+    vx = ctx.upload(rng.standard_normal(chunk * nkv).astype(np.float16).astype(np.float32))
+    for l in range(cfg["layers"]):
+        kq, ks, vq, vs = m.kv(l)
+        for p0 in range(0, max(contexts), chunk):
+            ctx.call("ti_kv_write_q8", kx, vx, kq, ks, vq, vs, chunk, cfg["n_kv"], hd, p0)
+    m.write_tokens(0, rng.integers(0, cfg["vocab"], cap + 1).astype(np.int32))
+    ctx.sync()
+    res = {}
+    for S in contexts:
+        m.set_pos(S)
+        ctx.graph_begin()
+        m.decode()
+        g = ctx.graph_end()
+        for _ in range(3):
+            ctx.graph_launch(g)
+        m.set_pos(S)
+        ctx.sync()
+        ctx.record(22)
+        for _ in range(steps):
+            ctx.graph_launch(g)
+        ctx.record(23)
+        ctx.sync()
+        ms = ctx.elapsed_ms(22, 23) / steps
         ctx.graph_destroy(g)
-        fams[name] = {"launches": n, "avg_us": ms * 1e3 / n, "bytes_per_launch": nbytes / n}
-
-    def qkv():
-        for l in ws.layers:
-            for nm, N in (("q", nq), ("k", nkv), ("v", nkv)):
-                ctx.call("ti_gemv_q4_q8", a["xq"], a["xs"], *l[nm], a[nm], N, H, 0)
-    timed("gemv_q4_q8", qkv, 3 * len(ws.layers),
-          len(ws.layers) * (gemv_q8_bytes(nq, H) + 2 * gemv_q8_bytes(nkv, H)))
-
-    def gu():
-        for l in ws.layers:
-            ctx.call("ti_gateup_silu_q4", a["xq"], a["xs"], *l["gate"], *l["up"], a["swi"], I, H)
-    timed("gateup_q4_q8", gu, len(ws.layers), gateup_bytes(I, H) * len(ws.layers))
-
-    def lm():
-        for w in lm_copies:
-            ctx.call("ti_gemv_q4_f32", a["last"], *w, a["logits"], cfg["vocab"], H, 0)
-    timed("gemv_q4_f32", lm, len(lm_copies), gemv_f32_bytes(cfg["vocab"], H) * len(lm_copies))
-    return fams
+        step_bytes = wbytes + cfg["layers"] * kv_bytes(S + steps // 2, cfg["n_kv"], hd)
+        res["ctx_%d" % S] = {"tok_s": round(1e3 / ms, 1), "ms_per_token": round(ms, 4),
+                             "step_GB_s": round(step_bytes / (ms * 1e-3) / 1e9, 1),
+                             "pct_of_hbm_peak": round(100 * step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
+                             "bytes_per_step": step_bytes, "launches_per_step": 2 + 5 * cfg["layers"]}
+        log("decode 1.7B at %d: %.1f tok/s" % (S, 1e3 / ms))
+    tok = m.read_tokens(0, 4)
+    m.close()
+    res["weights_bytes"] = wbytes
+    return res
 
 
+# ---- attention (one layer, fused step) --------------------------------------------------------
+def attention(ctx, flush, contexts=(4096, 32768), reps=6):
+    nHq, nKv, hd = 16, 8, 128
+    rng = np.random.default_rng(23)
+    cap = max(contexts) + 1
+    row_w, row_g = nKv * hd // 4, nKv * hd // 32
+    layers = 8       # distinct layer caches, cycled (8 x 75 MB at 32k: past the Infinity Cache)
+    caches = []
+    kx = ctx.upload(rng.standard_normal(2048 * nKv * hd).astype(np.float16).astype(np.float32))
+    for _ in range(layers):
+        c4 = [ctx.alloc(cap * row_w * 4), ctx.alloc(cap * row_g * 4), ctx.alloc(cap * row_w * 4), ctx.alloc(cap * row_g * 4)]
+        for p0 in range(0, cap - 2048, 2048):
+            ctx.call("ti_kv_write_q8", kx, kx, *c4, 2048, nKv, hd, p0)
+        caches.append(c4)
+    q = ctx.upload(rng.standard_normal(nHq * hd).astype(np.float32))
+    k = ctx.upload(rng.standard_normal(nKv * hd).astype(np.float32))
+    v = ctx.upload(rng.standard_normal(nKv * hd).astype(np.float32))
+    w = ctx.upload(np.full(hd, 0x3C00, np.uint16))
+    out = ctx.zeros(nHq * hd * 4)
+    oq, os_ = ctx.zeros(nHq * hd), ctx.zeros(nHq * hd // 8)
+    res = {}
+    for S in contexts:
+        def issue():
+            for c4 in caches:
+                ctx.call("ti_attn_step_q8", q, k, v, w, w, *c4, out, nHq, nKv, hd, S - 1, cap, np.float32(1e6),
+                         np.float32(1e-6), 0, oq, os_)
+        g = graph_of(ctx, issue)
+        time_graphs(ctx, [g], 2)
+        ms = cold_ms(ctx, [g], reps, flush)
+        ctx.graph_destroy(g)
+        us = ms * 1e3 / layers
+        nb = kv_bytes(S, nKv, hd) + 2 * nHq * hd * 4
+        res["S_%d" % S] = {"avg_us": round(us, 3), "bytes_per_launch": nb, "GB_s": round(nb / (us * 1e-6) / 1e9, 1)}
+    for c4 in caches:
+        for b in c4:
+            b.free()
+    return res
+
+
+# ---- ternary (Bonsai-1.7B layer shapes) ---------------------------------------------------------
+def tern_codes(rng, nbytes):
+    """Packed Q2_0_g64 code bytes with every 2-bit code drawn from {0, 1, 2}."""
+    c = rng.integers(0, 3, (nbytes, 4), dtype=np.uint8)
+    return (c[:, 0] | (c[:, 1] << 2) | (c[:, 2] << 4) | (c[:, 3] << 6)).astype(np.uint8)
+
+
+def ternary(ctx, flush, reps=8):
+    shapes = [(2048, 2048), (1024, 2048), (1024, 2048), (2048, 2048), (6144, 2048), (6144, 2048), (2048, 6144)]
+    rng = np.random.default_rng(3)
+    sets = []
+    for _ in range(8):        # 8 x 15.7 MB layers cycled
+        sets.append([(ctx.upload(tern_codes(rng, N * K // 4)),
+                      ctx.upload(rng.uniform(0.01, 0.05, N * K // 64).astype(np.float16).astype(np.float32)), N, K)
+                     for N, K in shapes])
+    acts = {K: (ctx.upload(rng.integers(-127, 128, K, dtype=np.int8)), ctx.upload(np.zeros(K // 64, np.int32)))
+            for K in (2048, 6144)}
+    outs = {N: ctx.zeros(N * 4) for N in (1024, 2048, 6144)}
+    per_layer = sum(N * K // 4 + (N * K // 64) * 4 + K + (K // 64) * 4 + N * 4 for N, K in shapes)
+
+    def issue():
+        for layer in sets:
+            for codes, sc, N, K in layer:
+                ctx.call("ti_tern_gemv", outs[N], codes, sc, acts[K][0], acts[K][1], N, K)
+    g = graph_of(ctx, issue)
+    time_graphs(ctx, [g], 2)
+    ms = cold_ms(ctx, [g], reps, flush)
+    ctx.graph_destroy(g)
+    us_layer = ms * 1e3 / len(sets)
+    return {"layer_us": round(us_layer, 2), "bytes_per_layer": per_layer,
+            "GB_s": round(per_layer / (us_layer * 1e-6) / 1e9, 1), "launches_per_layer": len(shapes)}
+
+
+# ---- CPU baselines ------------------------------------------------------------------------------
 def cpu_baseline(cfg, budget_s=12.0):
     """The oracle's int4 GEMV (a C port of the reference arithmetic, 1 thread) on a
-    bounded sample of the same GEMV set: layer-shaped GEMVs then the lm_head."""
+    bounded sample of the same GEMV set: layer-shaped GEMVs then lm_head rows."""
     from oracle import oracle as orc
     rng = np.random.default_rng(5)
     H, I = cfg["hidden"], cfg["inter"]
@@ -205,16 +408,15 @@ def cpu_baseline(cfg, budget_s=12.0):
         for pack, sc, N, K in mats:
             xq, xs, _ = orc.quant_act_q8(x[:K])
             orc.gemv_q4_q8(xq, xs, pack, sc, N, K)
-            nbytes += gemv_q8_bytes(N, K)
+            nbytes += int4_bytes(N, K) + K * 4 + N * 4
         layers += 1
-    # lm_head rows, f32 activation path
     N = 16384
     pack = rng.integers(0, 2 ** 32, N * H // 8, dtype=np.uint64).astype(np.uint32)
     sc = rng.uniform(1e-3, 1e-2, N * H // 32).astype(np.float16).view(np.uint16)
     lm_rows = 0
     while time.perf_counter() - t0 < budget_s:
         orc.gemv_q4_f32(x[:H], pack, sc, N, H)
-        nbytes += gemv_f32_bytes(N, H)
+        nbytes += int4_bytes(N, H) + H * 4 + N * 4
         lm_rows += N
     dt = time.perf_counter() - t0
     return {"value": round(nbytes / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
@@ -224,8 +426,8 @@ def cpu_baseline(cfg, budget_s=12.0):
 
 def tern_avx2_baseline(budget_s=6.0):
     """The reference's native CPU path, n2 avx2::gemv_tern (restated in C), on the
-    Bonsai-1.7B ternary GEMV shapes of one layer (q, k, v, o, gate, up, down),
-    min over repetitions; 1 thread (the reference's configuration) and N threads."""
+    Bonsai-1.7B ternary GEMV shapes of one layer, min over repetitions; 1 thread
+    (the reference's configuration) and N threads (static row split)."""
     from oracle import oracle as orc
     if not orc.has_avx2():
         return None
@@ -260,69 +462,73 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
+    ap.add_argument("--only", choices=("gemv", "all"), default="all", help="gemv: the headline workload only")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py runs on one GPU only: this build measures one MI355X's share of the work "
-              "(see DESIGN.md for how the path would shard); --gpus %d is not supported" % args.gpus, file=sys.stderr)
+        print("bench.py measures one MI355X: this build runs on a single GPU (the multi-GPU sharding is a "
+              "design only); --gpus %d is not supported" % args.gpus, file=sys.stderr)
         sys.exit(2)
 
     from tabinfer_amd import abi
     ctx = abi.Ctx(0)
     cfg = QWEN3_06B
-    print("[bench] building weights (2 sets x %.0f MB)" % ((Step(ctx, cfg, None).bytes) / 1e6), file=sys.stderr, flush=True)
-    pool = make_pool(ctx, 48 << 20, 1234)
+    step = Step(ctx, cfg)
+    log("building weights (2 sets x %.0f MB)" % (step.bytes / 1e6))
+    pool = Pool(ctx, 48 << 20, 1234)
     sets = [GemvSet(ctx, cfg, 100 + i, pool) for i in range(2)]
-    act = make_acts(ctx, cfg, 7)
-    step = Step(ctx, cfg, act)
     ctx.sync()
-    graphs = []
-    for ws in sets:
-        ctx.graph_begin()
-        step.issue(ws)
-        graphs.append(ctx.graph_end())
+    graphs = [graph_of(ctx, lambda ws=ws: step.issue(ws)) for ws in sets]
     for i in range(args.warmup):
         ctx.graph_launch(graphs[i % 2])
     ctx.sync()
-    print("[bench] timing %d steps" % args.steps, file=sys.stderr, flush=True)
+    log("timing %d steps" % args.steps)
     ctx.record(10)
     for i in range(args.steps):
         ctx.graph_launch(graphs[i % 2])
     ctx.record(11)
     ctx.sync()
-    ms = ctx.elapsed_ms(10, 11)
-    ms_per_step = ms / args.steps
+    ms_per_step = ctx.elapsed_ms(10, 11) / args.steps
     value = step.bytes / (ms_per_step * 1e-3) / 1e9
+    for g in graphs:
+        ctx.graph_destroy(g)
 
-    lm_extra = [sets[0]._quantized(cfg["vocab"], cfg["hidden"], np.random.default_rng(77 + i), pool) for i in range(2)]
-    last = (args.steps - 1) % 2
-    fams = kernel_profile(ctx, step, sets[1 - last], [sets[0].lm, sets[1].lm] + lm_extra)
-    dom_name = max(fams, key=lambda k: fams[k]["avg_us"] * fams[k]["launches"])
+    log("kernel families")
+    flush = Flush(ctx)
+    fams = family_profile(ctx, step, sets, flush)
+    dom_name = max(fams, key=lambda k: fams[k]["avg_us"] * fams[k]["launches_per_step"])
     dom = fams[dom_name]
     achieved = dom["bytes_per_launch"] / (dom["avg_us"] * 1e-6) / 1e9
     traffic = None
-    tp = os.path.join(ROOT, "profiles", "traffic_%s.json" % dom_name)
+    tp = os.path.join(ROOT, "profiles", "traffic.json")
     if os.path.exists(tp):
-        traffic = json.load(open(tp)).get("hbm_bytes_per_launch")
+        traffic = json.load(open(tp)).get(dom_name)
     out = {
-        "metric": "int4 GEMV HBM GB/s (% of peak) + Qwen3-1.7B bs1 decode tok/s at 32k ctx",
-        "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "int4xint8", "data": "synthetic (seeded bf16 N(0,0.02) weights, GPU-quantized; N(0,1) f16 activations)",
-        "config": {"workload": "Qwen3-0.6B int4 GEMV set of one batch-1 decode step (28 layers q/k/v/o/gate+up/down + lm_head 151936x1024), graph-launched",
+        "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int4xint8",
+        "data": "synthetic (seeded bf16 N(0,0.02) weights, GPU-quantized; N(0,1) f16 activations)",
+        "config": {"workload": "Qwen3-0.6B int4 GEMV set of one batch-1 decode step: 28 x [rmsnorm+q/k/v 1024->2048/1024/1024] "
+                               "[o 2048->1024 +res] [rmsnorm+gate/up 1024->3072 +SiLU+quant] [down 3072->1024 +res] + "
+                               "rmsnorm+lm_head 1024->151936+argmax; fused launches, one HIP graph per step",
                    "bytes_per_step": step.bytes, "launches_per_step": step.launches, "weight_sets": 2,
                    "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2)},
         "roofline": {"bound": "hbm", "kernel": dom_name, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic},
-        "kernels": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in fams.items()},
+        "kernels": fams,
     }
+    if args.only == "all":
+        log("ternary")
+        out["ternary_bonsai_layer"] = ternary(ctx, flush)
+        log("attention")
+        out["attention_layer"] = attention(ctx, flush)
+        log("decode 1.7B")
+        out["decode_1p7b"] = decode_1p7b(ctx, pool)
     if not args.no_cpu:
-        print("[bench] cpu baseline", file=sys.stderr, flush=True)
+        log("cpu baseline")
         out["cpu_baseline"] = cpu_baseline(cfg)
         tb = tern_avx2_baseline()
         if tb:
             out["cpu_tern_avx2"] = tb
-    for g in graphs:
-        ctx.graph_destroy(g)
     ctx.close()
     print(json.dumps(out))
 

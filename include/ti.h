@@ -119,10 +119,13 @@ int ti_group_dots_q4_q8(ti_ctx* ctx, const uint32_t* xq, const uint32_t* pack, i
 int ti_rmsnorm_gemv_q4(ti_ctx* ctx, const float* x, const uint16_t* norm_w, float eps, int K, int nmat,
                        const uint32_t* const* packs, const uint16_t* const* scales, float* const* ys,
                        const int* Ns, uint32_t* xq_out, float* xs_out);
-/* rmsnormQ + gateUpSiluDP4_only (models/qwen3.js:4023-4024): swi = silu(gate.x)*(up.x). */
+/* rmsnormQ + gateUpSiluDP4_only (models/qwen3.js:4023-4024): swi = silu(gate.x)*(up.x).
+ * swi (may be NULL when swi_q is given) receives the f32 values; swi_q/swi_s (both or
+ * neither; I % 32 == 0) receive them quantized per 32 as linearQ's quantQ8 would
+ * (models/qwen3.js:4033), ready for the down projection's gemvDP4. */
 int ti_rmsnorm_gateup_silu_q4(ti_ctx* ctx, const float* x, const uint16_t* norm_w, float eps,
                               const uint32_t* gpack, const uint16_t* gsc, const uint32_t* upack,
-                              const uint16_t* usc, float* swi, int I, int H);
+                              const uint16_t* usc, float* swi, int I, int H, uint32_t* swi_q, float* swi_s);
 /* final rmsnorm + lm_head gemvQ + argmaxKernel (models/qwen3.js:4037-4055):
  * logits (may be NULL) = W . rmsnorm(x), tok_hist[out_pos] = argmax (lowest index on
  * ties). K <= 8192. */
@@ -152,12 +155,13 @@ int ti_attn_decode_q8(ti_ctx* ctx, const float* qr, const uint32_t* kq, const fl
 /* attnPrepQ8 + attnDecodeStreamQ8 + combine as one launch (models/qwen3.js:4001-4002) for
  * one token at `pos` (< cap, the cache capacity in positions): q/k/v are the token's
  * projections [nHq*hd], [nKv*hd], [nKv*hd]; k and v are written into cache row pos;
- * out[nHq*hd] is the attention over positions 0..pos. Splits of >= 128 keys, at most
- * max_splits (0 = 64). Covers hd 64/128 with nHq/nKv <= 2. */
+ * out[nHq*hd] is the attention over positions 0..pos; out_q/out_s (both or neither)
+ * receive it quantized per 32 (quantQ8, for o_proj's linearQ). max_splits workgroups
+ * per KV head (0 = the default, 32; at most 64). Covers hd 64/128 with nHq/nKv <= 2. */
 int ti_attn_step_q8(ti_ctx* ctx, const float* q, const float* k, const float* v,
                     const uint16_t* qn_w, const uint16_t* kn_w, uint32_t* kq, float* ks,
                     uint32_t* vq, float* vs, float* out, int nHq, int nKv, int hd, int pos, int cap,
-                    float theta, float eps, int max_splits);
+                    float theta, float eps, int max_splits, uint32_t* out_q, float* out_s);
 /* ropeQK (models/qwen3.js:1700-1760): out[t,h,:] = RoPE(RMSNorm(x[t,h,:]) * w) at
  * pos0+t for T tokens; w == NULL skips the norm. x and out must not alias. */
 int ti_rope_qk(ti_ctx* ctx, const float* x, const uint16_t* w, float* out,

@@ -55,11 +55,11 @@ SIGS = {
     "ti_linear_q4": [_p, _p, _p, _p, _p, _i, _i, _i, _i],
     "ti_group_dots_q4_q8": [_p, _p, _p, _p, _i, _i],
     "ti_rmsnorm_gemv_q4": [_p, _p, _p, _f, _i, _i, _p, _p, _p, _p, _p, _p],
-    "ti_rmsnorm_gateup_silu_q4": [_p, _p, _p, _f, _p, _p, _p, _p, _p, _i, _i],
+    "ti_rmsnorm_gateup_silu_q4": [_p, _p, _p, _f, _p, _p, _p, _p, _p, _i, _i, _p, _p],
     "ti_rmsnorm_lm_head_argmax": [_p, _p, _p, _f, _p, _p, _p, _i, _i, _p, _i],
     "ti_argmax": [_p, _p, _i, _p, _i],
     "ti_embed": [_p, _p, _p, _p, _i, _i, _i, _i],
-    "ti_attn_step_q8": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _f, _f, _i],
+    "ti_attn_step_q8": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _f, _f, _i, _p, _p],
     "ti_attn_prep_q8": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _f, _f],
     "ti_attn_decode_q8": [_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i],
     "ti_rope_qk": [_p, _p, _p, _p, _i, _i, _i, _i, _f, _f],

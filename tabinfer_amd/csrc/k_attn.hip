@@ -9,6 +9,7 @@
 // int8 codes packed 4 per u32 (snorm: code/127 * group max), one f32 scale per
 // 32 dims.
 #include "ti_internal.h"
+#include <math.h>
 
 // ---------------------------------------------------------------------------
 // snorm int8 (pack4x8snorm): code = floor(0.5 + 127*clamp(x/mx, -1, 1)),
@@ -62,6 +63,37 @@ __device__ float rope_norm(float x, int j, int hd, const uint16_t* __restrict__ 
         float partner = j < half ? rk[j + half] : rk[j - half];
         float rot = j < half ? -partner : partner;
         float a = rk[j] * c, b = rot * s;
+        out = a + b;
+    }
+    __syncthreads();
+    return out;
+}
+
+// rope_norm with the rotation's cos/sin given: cs[i] = cos(pos*theta^(-2i/hd)),
+// cs[hd/2 + i] = sin(...), i < hd/2, evaluated in f64 and rounded to f32 on the host
+// (the same values rope_norm computes on the device), so the hot kernels call no
+// f64 library routine.
+__device__ float rope_norm_tab(float x, int j, int hd, const uint16_t* __restrict__ w, const float* cs, float eps,
+                               float* red, float* rk) {
+    red[j] = j < hd ? x * x : 0.0f;
+    __syncthreads();
+    for (int st = 64; st > 0; st >>= 1) {
+        if (j < st) red[j] = red[j] + red[j + st];
+        __syncthreads();
+    }
+    float m = red[0] / (float)hd;
+    m = m + eps;
+    float inv = 1.0f / sqrtf(m);
+    if (j < hd) { float a = x * inv; rk[j] = a * ti_h2f(w[j]); }
+    __syncthreads();
+    float out = 0.0f;
+    if (j < hd) {
+        const int half = hd / 2;
+        const int fi = j < half ? j : j - half;
+        const float c = cs[fi], sn = cs[half + fi];
+        float partner = j < half ? rk[j + half] : rk[j - half];
+        float rot = j < half ? -partner : partner;
+        float a = rk[j] * c, b = rot * sn;
         out = a + b;
     }
     __syncthreads();
@@ -451,23 +483,25 @@ extern "C" int ti_kv_write_q8(ti_ctx* c, const float* kr, const float* v, uint32
 // ---------------------------------------------------------------------------
 // Fused decode attention: one launch per layer at T = 1 does attnPrepQ8
 // (models/qwen3.js:2228-2308), attnDecodeStreamQ8 (:2077-2164) and the combine
-// (:2048-2068). Workgroup (256 threads) = (KV head hk, split):
-//  1. RMSNorm + RoPE of the G = nHq/nKv query heads of hk into LDS (each
-//     workgroup recomputes them: 2 x 128 values);
-//  2. the split that holds position pos normalises/ropes k and quantizes k, v
-//     into the cache row pos (snorm int8, as attnPrepQ8) and uses that row from
-//     LDS, so no workgroup waits for another one's write;
-//  3. online softmax over the split in tiles of ATTF_TILE keys; K and V of a tile
-//     are loaded together and the next tile is prefetched during the current one;
-//  4. partials (unnormalised o, m, l) go to scratch; the last workgroup of hk to
-//     finish (device-scope counter, release/acquire fences) merges them by
-//     log-sum-exp and writes the head outputs, then resets the counter.
-// The split count adapts to the context on the device: at least min_per keys
-// per split, at most max_splits splits.
+// (:2048-2068). Workgroup (256 threads) = (KV head hk, split w of NS):
+//  - the keys are cut into tiles of ATTF_TILE positions and workgroup w takes
+//    tiles w, w+NS, w+2NS, ... : the first tile's address does not depend on the
+//    context length, so its K/V loads are issued together with the loads of the
+//    device position, the rope row and the q/k/v projections — the kernel pays one
+//    memory round trip before it computes, not three;
+//  - RMSNorm + RoPE of the G = nHq/nKv query heads of hk into LDS (every
+//    workgroup; 2 x 128 values);
+//  - the workgroup holding the last tile normalises/ropes k and quantizes k, v
+//    into cache row pos (snorm int8, as attnPrepQ8) and takes that row from LDS;
+//  - online softmax over its tiles, K and V of a tile loaded together, the next
+//    tile prefetched during the current one;
+//  - partials (unnormalised o, m, l) are published with device-scope stores; the
+//    last workgroup of hk to arrive merges the NS partials by log-sum-exp, writes
+//    the head outputs and resets the counter.
 // ---------------------------------------------------------------------------
 namespace {
-constexpr int ATTF_TILE = 128;
 constexpr int ATTF_MAXS = 64;
+constexpr int ATTF_DEFAULT_SPLITS = 32;   // measured best over 1k..32k contexts on MI355X
 
 struct AttnFArgs {
     const float* q;
@@ -483,61 +517,137 @@ struct AttnFArgs {
     float* po;
     float* pml;
     uint32_t* counter;     // [nKv]
-    const int* dpos;       // device position, or null: use pos
+    // the position and its rotary row come from device memory (dev = 1: the decode
+    // step's device position) or from these arguments; both pointers are always
+    // valid so the kernel loads them unconditionally (no branch, no flat access)
+    const int* dpos;
+    const float* rope_cur;
+    int dev;
     int pos;
-    int nKv, max_splits, min_per, cap;
-    float theta, eps;
+    int nKv, ns, cap;
+    float eps;
+    uint32_t* oq;          // optional: the output quantized per 32 (quantQ8, for o_proj's linearQ)
+    float* os;
+    float rope_row[TI_ATTN_HD_MAX];
 };
 
+// RMSNorm over one head row held by 128 threads (j = element, 0 past hd) in the
+// reference's reduction order — slot j and j+64, then a 32..1 tree — with the last
+// levels as a wave butterfly (a pair's float sum is the same in either order), then
+// split-half RoPE with the given cos/sin row. red/rk: this head's 128-float slices.
+__device__ __forceinline__ float head_norm_rope(float x, int j, int hd, const uint16_t* __restrict__ w, const float* cs,
+                                               float eps, float* red, float* rk, float* tot) {
+    const float sq = j < hd ? x * x : 0.0f;
+    red[j] = sq;
+    __syncthreads();
+    float v = 0.0f;
+    if (j < 64) {
+        v = red[j] + red[j + 64];
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) v = v + __shfl_xor(v, o, 64);
+        if (j == 0) *tot = v;
+    }
+    __syncthreads();
+    float m = *tot / (float)hd;
+    m = m + eps;
+    const float inv = 1.0f / sqrtf(m);
+    if (j < hd) { float t = x * inv; rk[j] = t * ti_h2f(w[j]); }
+    __syncthreads();
+    float out = 0.0f;
+    if (j < hd) {
+        const int half = hd / 2;
+        const int fi = j < half ? j : j - half;
+        const float c = cs[fi], sn = cs[half + fi];
+        const float partner = j < half ? rk[j + half] : rk[j - half];
+        const float rot = j < half ? -partner : partner;
+        const float p0 = rk[j] * c, p1 = rot * sn;
+        out = p0 + p1;
+    }
+    return out;
+}
+
+// signed int8 code k of a packed word as (code + 128): one v_cvt_f32_ubyte
+__device__ __forceinline__ float ub(uint32_t wflip, int k) { return (float)((wflip >> (8 * k)) & 0xffu); }
+
 template <int HD, int G>
-__global__ __launch_bounds__(256) void k_attn_fused_q8(AttnFArgs a) {
-    static_assert(G >= 1 && G <= 2 && HD <= 128 && HD % 32 == 0, "fused attention: G <= 2, HD <= 128");
+__global__ __launch_bounds__(256, 2) void k_attn_fused_q8(AttnFArgs a) {
+    static_assert(G >= 1 && G <= 2 && (HD == 64 || HD == 128), "fused attention: G <= 2, HD 64 or 128");
     constexpr int LPT = HD / 16;               // lanes per token row (16 bytes each)
-    constexpr int TPP = 256 / LPT;             // tokens per pass
-    constexpr int PASSES = ATTF_TILE / TPP;
+    constexpr int TPW = 64 / LPT;              // tokens per wave pass
+    constexpr int PASSES = 4;
+    constexpr int WT = PASSES * TPW;           // tokens per wave tile
     constexpr int NG = HD / 32;                // scale groups per head row
     __shared__ float red[256];
     __shared__ float rk[256];
+    __shared__ float tot[2];
     __shared__ float s_q[G][HD];
-    __shared__ float s_row[2][128];
+    __shared__ float s_row[2][HD];
     __shared__ __align__(16) uint32_t s_kw[HD / 4];
     __shared__ __align__(16) uint32_t s_vw[HD / 4];
     __shared__ float s_ksc[NG], s_vsc[NG];
-    __shared__ float sc[G][ATTF_TILE];
-    __shared__ float redm[G][4];
-    __shared__ float reds[G][4];
-    __shared__ float pvred[TPP][G * HD + 1];
+    __shared__ float s_acc[4][G * HD];
+    __shared__ float s_wml[4][G][2];
     __shared__ float s_ml[G][ATTF_MAXS][2];
+    __shared__ float rope_cs[HD];
     __shared__ int s_last;
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wv = tid >> 6;
+    const int lane = tid & 63, wave = tid >> 6;
     const int hk = blockIdx.x % a.nKv;
-    const int split = blockIdx.x / a.nKv;
-    const int pos = a.dpos ? *a.dpos : a.pos;
-    if (pos < 0 || pos >= a.cap) return;       // outside the cache: nothing is read or written
-    const int S = pos + 1;
-    int ns0 = (S + a.min_per - 1) / a.min_per;
-    ns0 = ns0 < a.max_splits ? ns0 : a.max_splits;
-    const int per = (S + ns0 - 1) / ns0;
-    const int nsplit = (S + per - 1) / per;
-    if (split >= nsplit) return;
-    const int c0 = split * per;
-    const int c1 = min(S, c0 + per);
-    const bool has_pos = c1 == S;
-
-    // 1. query heads
+    const int w = blockIdx.x / a.nKv;
+    const int NS = a.ns;
+    const int NW = NS * 4;                     // waves per KV head
+    const int gw = w * 4 + wave;               // this wave's index among them
     const int h = tid >> 7, j = tid & 127;
-    {
-        float x = (h < G && j < HD) ? a.q[(size_t)(hk * G + h) * HD + j] : 0.0f;
-        float r = rope_norm(x, j, HD, a.qw, pos, a.theta, a.eps, true, red + h * 128, rk + h * 128);
+    const int tp = lane / LPT, sl = lane % LPT;
+    const int row_words4 = a.nKv * HD / 16;
+    const int row_groups = a.nKv * NG;
+    const float qk_scale = 1.0f / (127.0f * sqrtf((float)HD));
+    const uint4* kq4 = reinterpret_cast<const uint4*>(a.kq);
+    const uint4* vq4 = reinterpret_cast<const uint4*>(a.vq);
+
+    // ---- every load that does not depend on the position, in one batch
+    const int pos_dev = *a.dpos;
+    const float cs_dev = a.rope_cur[j < HD ? j : 0];
+    const float cs_arg = a.rope_row[j < HD ? j : 0];
+    const float qx = a.q[(size_t)(hk * G + (h < G ? h : 0)) * HD + (j < HD ? j : 0)];
+    const float kx = a.k[(size_t)hk * HD + (j < HD ? j : 0)];
+    const float vx = a.v[(size_t)hk * HD + (j < HD ? j : 0)];
+    uint4 kw[2][PASSES], vw[2][PASSES];
+    float ksc[2][PASSES], vsc[2][PASSES];
+    int lim = a.cap;                           // clamp bound until the context is known
+    auto load = [&](int buf, int t0) {
+#pragma unroll
+        for (int p = 0; p < PASSES; p++) {
+            int t = t0 + p * TPW + tp;
+            t = t < lim ? t : lim - 1;
+            kw[buf][p] = ti_ld_nt(kq4 + (size_t)t * row_words4 + hk * LPT + sl);
+            vw[buf][p] = ti_ld_nt(vq4 + (size_t)t * row_words4 + hk * LPT + sl);
+            ksc[buf][p] = a.ks[(size_t)t * row_groups + hk * NG + sl / 2];
+            vsc[buf][p] = a.vs[(size_t)t * row_groups + hk * NG + sl / 2];
+        }
+    };
+    load(0, gw * WT);
+
+    const int pos = a.dev ? pos_dev : a.pos;
+    const float csj = a.dev ? cs_dev : cs_arg;
+    const bool valid = pos >= 0 && pos < a.cap;          // outside the cache: nothing is written
+    const int S = valid ? pos + 1 : 0;
+    const int ntiles = (S + WT - 1) / WT;                 // wave tiles of the context
+    const int last_gw = ntiles > 0 ? (ntiles - 1) % NW : -1;
+    const bool has_pos = valid && (last_gw >> 2) == w;    // this workgroup writes/uses cache row pos
+    lim = S > 0 ? S : 1;
+
+    if (tid < HD) rope_cs[tid] = csj;
+    {   // query heads (the first barrier inside publishes rope_cs)
+        const float x = (h < G && j < HD) ? qx : 0.0f;
+        const float r = head_norm_rope(x, j, HD, a.qw, rope_cs, a.eps, red + h * 128, rk + h * 128, tot + h);
         if (h < G && j < HD) s_q[h][j] = r;
     }
-    // 2. this token's K/V row
-    if (has_pos) {
-        float x = (h == 0 && j < HD) ? a.k[(size_t)hk * HD + j] : 0.0f;
-        float r = rope_norm(x, j, HD, a.kw, pos, a.theta, a.eps, true, red + h * 128, rk + h * 128);
-        if (j < HD) s_row[h][j] = h == 0 ? r : a.v[(size_t)hk * HD + j];
+    if (has_pos) {   // this token's K (normed, roped) and V rows, snorm int8, into the cache and LDS
+        const float x = (h == 0 && j < HD) ? kx : 0.0f;
+        const float r = head_norm_rope(x, j, HD, a.kw, rope_cs, a.eps, red + h * 128, rk + h * 128, tot + h);
+        if (j < HD) s_row[h][j] = h == 0 ? r : vx;
         __syncthreads();
         if (tid < 2 * NG) {
             const int which = tid / NG, g = tid % NG;
@@ -551,52 +661,39 @@ __global__ __launch_bounds__(256) void k_attn_fused_q8(AttnFArgs a) {
             float* ds = (which ? a.vs : a.ks) + ((size_t)pos * a.nKv + hk) * NG + g;
             uint32_t* lw = which ? s_vw : s_kw;
 #pragma unroll
-            for (int w = 0; w < 8; w++) { dq[w] = wds[w]; lw[g * 8 + w] = wds[w]; }
+            for (int q = 0; q < 8; q++) { dq[q] = wds[q]; lw[g * 8 + q] = wds[q]; }
             *ds = scl;
             (which ? s_vsc : s_ksc)[g] = scl;
         }
     }
     __syncthreads();
 
-    const int tp = tid / LPT, sl = tid % LPT;
-    const int row_words4 = a.nKv * HD / 16;
-    const int row_groups = a.nKv * NG;
-    const float qk_scale = 1.0f / (127.0f * sqrtf((float)HD));
-    const uint4* kq4 = reinterpret_cast<const uint4*>(a.kq);
-    const uint4* vq4 = reinterpret_cast<const uint4*>(a.vq);
-    float qv[G][16];
+    float qv[G][16], qsum[G];
 #pragma unroll
-    for (int hh = 0; hh < G; hh++)
+    for (int hh = 0; hh < G; hh++) {
+        float s = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 16; i++) qv[hh][i] = s_q[hh][sl * 16 + i];
-    float m_run[G], l_run[G], acc[G][16];
+        for (int i = 0; i < 16; i++) { qv[hh][i] = s_q[hh][sl * 16 + i]; s += qv[hh][i]; }
+        qsum[hh] = 128.0f * s;
+    }
+    float m_run[G], l_run[G], acc[G][16], pws[G];
 #pragma unroll
     for (int hh = 0; hh < G; hh++) {
         m_run[hh] = -3.0e38f;
         l_run[hh] = 0.0f;
+        pws[hh] = 0.0f;
 #pragma unroll
         for (int i = 0; i < 16; i++) acc[hh][i] = 0.0f;
     }
 
-    uint4 kw[2][PASSES], vw[2][PASSES];
-    float ksc[2][PASSES], vsc[2][PASSES];
-    auto load = [&](int buf, int t0) {
-#pragma unroll
-        for (int p = 0; p < PASSES; p++) {
-            int t = t0 + p * TPP + tp;
-            t = t < c1 ? t : c1 - 1;
-            kw[buf][p] = ti_ld_nt(kq4 + (size_t)t * row_words4 + hk * LPT + sl);
-            vw[buf][p] = ti_ld_nt(vq4 + (size_t)t * row_words4 + hk * LPT + sl);
-            ksc[buf][p] = a.ks[(size_t)t * row_groups + hk * NG + sl / 2];
-            vsc[buf][p] = a.vs[(size_t)t * row_groups + hk * NG + sl / 2];
-        }
-    };
+    // one wave tile, no barriers: scores -> wave max -> exp -> P*V. Codes enter as
+    // (code + 128) (v_cvt_f32_ubyte); the offset is removed once per dot (q) and once
+    // at the end (p), where it is exact bookkeeping, not an approximation.
     auto process = [&](int buf, int t0) {
-        const int n = min(ATTF_TILE, c1 - t0);
-        if (has_pos) {   // the row at pos (and the clamped reads past it) come from LDS
+        if (has_pos && t0 + WT >= S) {   // the tile holding pos: that row (and clamped reads past it) from LDS
 #pragma unroll
             for (int p = 0; p < PASSES; p++) {
-                if (min(t0 + p * TPP + tp, c1 - 1) == pos) {
+                if (t0 + p * TPW + tp >= pos) {
                     kw[buf][p] = reinterpret_cast<const uint4*>(s_kw)[sl];
                     vw[buf][p] = reinterpret_cast<const uint4*>(s_vw)[sl];
                     ksc[buf][p] = s_ksc[sl / 2];
@@ -604,133 +701,180 @@ __global__ __launch_bounds__(256) void k_attn_fused_q8(AttnFArgs a) {
                 }
             }
         }
+        float sc[PASSES][G];
 #pragma unroll
         for (int p = 0; p < PASSES; p++) {
-            const uint32_t ww[4] = {kw[buf][p].x, kw[buf][p].y, kw[buf][p].z, kw[buf][p].w};
-            float part[G];
+            const uint32_t ww[4] = {kw[buf][p].x ^ 0x80808080u, kw[buf][p].y ^ 0x80808080u,
+                                    kw[buf][p].z ^ 0x80808080u, kw[buf][p].w ^ 0x80808080u};
 #pragma unroll
             for (int hh = 0; hh < G; hh++) {
                 float d = 0.0f;
 #pragma unroll
-                for (int i = 0; i < 16; i++) d = fmaf(qv[hh][i], i8f(ww[i >> 2], i & 3), d);
-                part[hh] = d * ksc[buf][p];
+                for (int i = 0; i < 16; i++) d = fmaf(qv[hh][i], ub(ww[i >> 2], i & 3), d);
+                sc[p][hh] = (d - qsum[hh]) * ksc[buf][p];
             }
 #pragma unroll
             for (int o = LPT / 2; o > 0; o >>= 1)
 #pragma unroll
-                for (int hh = 0; hh < G; hh++) part[hh] += __shfl_xor(part[hh], o, 64);
-            const int jj = p * TPP + tp;
-            if (sl == 0)
+                for (int hh = 0; hh < G; hh++) sc[p][hh] += __shfl_xor(sc[p][hh], o, 64);
+            const bool live = t0 + p * TPW + tp < S;
 #pragma unroll
-                for (int hh = 0; hh < G; hh++) sc[hh][jj] = jj < n ? part[hh] * qk_scale : -3.0e38f;
+            for (int hh = 0; hh < G; hh++) sc[p][hh] = live ? sc[p][hh] * qk_scale : -3.0e38f;
         }
-        __syncthreads();
-        float mt[G], corr[G];
+        float corr[G];
 #pragma unroll
         for (int hh = 0; hh < G; hh++) {
-            float v = -3.0e38f;
-            for (int q = tid; q < ATTF_TILE; q += 256) v = fmaxf(v, sc[hh][q]);
+            float mx = sc[0][hh];
 #pragma unroll
-            for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-            if (lane == 0) redm[hh][wv] = v;
+            for (int p = 1; p < PASSES; p++) mx = fmaxf(mx, sc[p][hh]);
+#pragma unroll
+            for (int o = LPT; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+            const float mn = fmaxf(m_run[hh], mx);
+            corr[hh] = expf(m_run[hh] - mn);
+            m_run[hh] = mn;
         }
-        __syncthreads();
+        float ps[G];
 #pragma unroll
         for (int hh = 0; hh < G; hh++) {
-            float v = fmaxf(fmaxf(redm[hh][0], redm[hh][1]), fmaxf(redm[hh][2], redm[hh][3]));
-            mt[hh] = fmaxf(m_run[hh], v);
-            corr[hh] = expf(m_run[hh] - mt[hh]);
-            float s = 0.0f;
-            for (int q = tid; q < ATTF_TILE; q += 256) {
-                float pe = q < n ? expf(sc[hh][q] - mt[hh]) : 0.0f;
-                sc[hh][q] = pe;
-                s += pe;
-            }
-#pragma unroll
-            for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
-            if (lane == 0) reds[hh][wv] = s;
-        }
-        __syncthreads();
-#pragma unroll
-        for (int hh = 0; hh < G; hh++) {
-            float s = (reds[hh][0] + reds[hh][1]) + (reds[hh][2] + reds[hh][3]);
-            l_run[hh] = l_run[hh] * corr[hh] + s;
-            m_run[hh] = mt[hh];
+            ps[hh] = 0.0f;
+            pws[hh] *= corr[hh];
 #pragma unroll
             for (int i = 0; i < 16; i++) acc[hh][i] *= corr[hh];
         }
 #pragma unroll
         for (int p = 0; p < PASSES; p++) {
-            const int jj = p * TPP + tp;
-            const uint32_t ww[4] = {vw[buf][p].x, vw[buf][p].y, vw[buf][p].z, vw[buf][p].w};
+            const bool live = t0 + p * TPW + tp < S;
+            const uint32_t ww[4] = {vw[buf][p].x ^ 0x80808080u, vw[buf][p].y ^ 0x80808080u,
+                                    vw[buf][p].z ^ 0x80808080u, vw[buf][p].w ^ 0x80808080u};
 #pragma unroll
             for (int hh = 0; hh < G; hh++) {
-                float pw = sc[hh][jj] * vsc[buf][p] * (1.0f / 127.0f);
+                const float e = live ? expf(sc[p][hh] - m_run[hh]) : 0.0f;
+                ps[hh] += e;
+                // rows past the context may hold anything (even a NaN scale): weight exactly 0
+                const float pw = live ? e * vsc[buf][p] * (1.0f / 127.0f) : 0.0f;
+                pws[hh] += pw;
 #pragma unroll
-                for (int i = 0; i < 16; i++) acc[hh][i] = fmaf(pw, i8f(ww[i >> 2], i & 3), acc[hh][i]);
+                for (int i = 0; i < 16; i++) acc[hh][i] = fmaf(pw, ub(ww[i >> 2], i & 3), acc[hh][i]);
             }
         }
-        __syncthreads();   // sc is rewritten by the next tile
+#pragma unroll
+        for (int hh = 0; hh < G; hh++) {
+#pragma unroll
+            for (int o = LPT; o < 64; o <<= 1) ps[hh] += __shfl_xor(ps[hh], o, 64);
+            l_run[hh] = l_run[hh] * corr[hh] + ps[hh];
+        }
     };
-    int t0 = c0;
-    load(0, t0);
-    for (;;) {
-        int nt = t0 + ATTF_TILE;
-        if (nt < c1) load(1, nt);
+    const int step = NW * WT;
+    int t0 = gw * WT;
+    while (t0 < S) {
+        int nt = t0 + step;
+        if (nt < S) load(1, nt);
         process(0, t0);
-        if (nt >= c1) break;
+        if (nt >= S) break;
         t0 = nt;
-        nt = t0 + ATTF_TILE;
-        if (nt < c1) load(0, nt);
+        nt = t0 + step;
+        if (nt < S) load(0, nt);
         process(1, t0);
-        if (nt >= c1) break;
         t0 = nt;
     }
 
-    // 4. partials of this split, then the last workgroup of hk merges them
+    // wave state -> LDS: acc summed over the wave's token slots, the +128 offset removed
 #pragma unroll
-    for (int hh = 0; hh < G; hh++)
+    for (int hh = 0; hh < G; hh++) {
 #pragma unroll
-        for (int i = 0; i < 16; i++) pvred[tp][hh * HD + sl * 16 + i] = acc[hh][i];
+        for (int o = LPT; o < 64; o <<= 1) {
+            pws[hh] += __shfl_xor(pws[hh], o, 64);
+#pragma unroll
+            for (int i = 0; i < 16; i++) acc[hh][i] += __shfl_xor(acc[hh][i], o, 64);
+        }
+        if (tp == 0) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) s_acc[wave][hh * HD + sl * 16 + i] = acc[hh][i] - 128.0f * pws[hh];
+        }
+        if (lane == 0) {
+            s_wml[wave][hh][0] = m_run[hh];
+            s_wml[wave][hh][1] = l_run[hh];
+        }
+    }
     __syncthreads();
-    const size_t ms = (size_t)a.max_splits;
+    // merge the 4 waves into this split's partial and publish it
+    const size_t ms = (size_t)NS;
     for (int o = tid; o < G * HD; o += 256) {
-        float s = 0.0f;
-        for (int r = 0; r < TPP; r++) s += pvred[r][o];
         const int hh = o / HD, d = o % HD;
-        a.po[((size_t)(hk * G + hh) * ms + split) * HD + d] = s;
+        float M = s_wml[0][hh][0];
+#pragma unroll
+        for (int q = 1; q < 4; q++) M = fmaxf(M, s_wml[q][hh][0]);
+        float O = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 4; q++) O += s_acc[q][o] * expf(s_wml[q][hh][0] - M);
+        ti_pub_store(a.po + ((size_t)(hk * G + hh) * ms + w) * HD + d, O);
     }
     if (tid < G) {
-        a.pml[((size_t)(hk * G + tid) * ms + split) * 2] = m_run[tid];
-        a.pml[((size_t)(hk * G + tid) * ms + split) * 2 + 1] = l_run[tid];
+        float M = s_wml[0][tid][0];
+#pragma unroll
+        for (int q = 1; q < 4; q++) M = fmaxf(M, s_wml[q][tid][0]);
+        float L = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 4; q++) L += s_wml[q][tid][1] * expf(s_wml[q][tid][0] - M);
+        ti_pub_store(a.pml + ((size_t)(hk * G + tid) * ms + w) * 2, M);
+        ti_pub_store(a.pml + ((size_t)(hk * G + tid) * ms + w) * 2 + 1, L);
     }
-    __threadfence();
+    ti_stores_done();
     __syncthreads();
-    if (tid == 0) {
-        unsigned prev = __hip_atomic_fetch_add(a.counter + hk, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = prev == (unsigned)(nsplit - 1);
-    }
+    if (tid == 0) s_last = ti_arrive(a.counter + hk) == (unsigned)(NS - 1);
     __syncthreads();
     if (!s_last) return;
-    __threadfence();
-    for (int e = tid; e < G * nsplit * 2; e += 256) {
-        const int hh = e / (nsplit * 2), r = e % (nsplit * 2);
-        s_ml[hh][r >> 1][r & 1] = a.pml[((size_t)(hk * G + hh) * ms + (r >> 1)) * 2 + (r & 1)];
+    // the last split of hk: log-sum-exp over the splits that saw a tile; the o loads
+    // are issued before the (m, l) pairs are reduced, one round trip for both
+    const int nused = ntiles < NW ? (ntiles + 3) / 4 : NS;
+    constexpr int OC = 16;                         // o values in flight per thread
+    float ov[OC];
+    const int oh = tid / HD, od = tid % HD;
+    const float* pp = a.po + (size_t)(hk * G + (oh < G ? oh : 0)) * ms * HD + od;
+#pragma unroll
+    for (int i = 0; i < OC; i++) ov[i] = i < nused ? ti_pub_load(pp + (size_t)i * HD) : 0.0f;
+    for (int e = tid; e < G * nused * 2; e += 256) {
+        const int hh = e / (nused * 2), r = e % (nused * 2);
+        s_ml[hh][r >> 1][r & 1] = ti_pub_load(a.pml + ((size_t)(hk * G + hh) * ms + (r >> 1)) * 2 + (r & 1));
     }
     __syncthreads();
-    if (tid < G * HD) {
-        const int hh = tid / HD, d = tid % HD;
+    if (valid && tid < G * HD) {
         float M = -3.0e38f;
-        for (int i = 0; i < nsplit; i++) M = fmaxf(M, s_ml[hh][i][0]);
+        for (int i = 0; i < nused; i++) M = fmaxf(M, s_ml[oh][i][0]);
         float L = 0.0f, o = 0.0f;
-        const float* pp = a.po + (size_t)(hk * G + hh) * ms * HD + d;
-#pragma unroll 16
-        for (int i = 0; i < nsplit; i++) {
-            float e = expf(s_ml[hh][i][0] - M);
-            L += s_ml[hh][i][1] * e;
-            o += pp[(size_t)i * HD] * e;
+        for (int i0 = 0; i0 < nused; i0 += OC) {
+            if (i0 > 0) {
+#pragma unroll
+                for (int i = 0; i < OC; i++) ov[i] = i0 + i < nused ? ti_pub_load(pp + (size_t)(i0 + i) * HD) : 0.0f;
+            }
+#pragma unroll
+            for (int i = 0; i < OC; i++) {
+                if (i0 + i < nused) {
+                    const float e = expf(s_ml[oh][i0 + i][0] - M);
+                    L += s_ml[oh][i0 + i][1] * e;
+                    o += ov[i] * e;
+                }
+            }
         }
-        a.out[(size_t)(hk * G + hh) * HD + d] = o / L;
+        const float res = o / L;
+        const size_t e = (size_t)(hk * G + oh) * HD + od;
+        a.out[e] = res;
+        if (a.oq) {   // quantQ8 of 32 consecutive outputs = 32 consecutive lanes (q8_group's arithmetic)
+            float mx = fabsf(res);
+#pragma unroll
+            for (int o2 = 16; o2 > 0; o2 >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o2, 64));
+            const float scale = mx / 127.0f;
+            const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
+            const float pq = res * inv;
+            int qi = (int)rintf(pq);
+            qi = qi < -127 ? -127 : (qi > 127 ? 127 : qi);
+            const uint32_t b = (uint32_t)(qi & 0xff);
+            const int src = (lane & ~3);
+            const uint32_t b0 = __shfl(b, src, 64), b1 = __shfl(b, src + 1, 64);
+            const uint32_t b2 = __shfl(b, src + 2, 64), b3 = __shfl(b, src + 3, 64);
+            if ((lane & 3) == 0) a.oq[e / 4] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+            if ((lane & 31) == 0) a.os[e / 32] = scale;
+        }
     }
     if (tid == 0) __hip_atomic_store(a.counter + hk, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -738,14 +882,34 @@ __global__ __launch_bounds__(256) void k_attn_fused_q8(AttnFArgs a) {
 
 // Fused decode attention; returns TI_ERR_INVALID for head shapes it does not cover
 // (the caller then issues prep + split + combine).
+// rope rows: cs[i] = cos(pos * theta^(-2i/hd)), cs[hd/2 + i] = sin(...), in f64 then f32
+void ti_rope_row(float* cs, int pos, int hd, float theta) {
+    for (int i = 0; i < hd / 2; i++) {
+        double ang = (double)pos * pow((double)theta, -2.0 * (double)i / (double)hd);
+        cs[i] = (float)cos(ang);
+        cs[hd / 2 + i] = (float)sin(ang);
+    }
+}
+
 int ti_attn_fused_launch(ti_ctx* c, const float* q, const float* k, const float* v, const uint16_t* qw,
                          const uint16_t* kw, uint32_t* kq, float* ks, uint32_t* vq, float* vs, float* out, int nHq,
-                         int nKv, int hd, const int* dpos, int pos, int cap, float theta, float eps, int max_splits) {
+                         int nKv, int hd, const int* dpos, int pos, int cap, float theta, float eps, int max_splits,
+                         const float* rope_cur, uint32_t* oq, float* os) {
     const int G = nHq / nKv;
-    if (nKv > TI_SYNC_WORDS - TI_SYNC_ATTN) return ti_fail(TI_ERR_INVALID, "fused attention: too many KV heads");
-    if (max_splits <= 0 || max_splits > ATTF_MAXS) max_splits = ATTF_MAXS;
-    AttnFArgs a = {q, k, v, qw, kw, kq, ks, vq, vs, out, c->attn_po, c->attn_ml, c->sync + TI_SYNC_ATTN, dpos, pos,
-                   nKv, max_splits, 128, cap, theta, eps};
+    if (nKv > TI_SYNC_DUMMY - TI_SYNC_ATTN) return ti_fail(TI_ERR_INVALID, "fused attention: too many KV heads");
+    if (hd > TI_ATTN_HD_MAX) return ti_fail(TI_ERR_INVALID, "fused attention: hd=%d > %d", hd, TI_ATTN_HD_MAX);
+    if (dpos && !rope_cur) return ti_fail(TI_ERR_INVALID, "fused attention: a device position needs its rope row");
+    if (max_splits <= 0 || max_splits > ATTF_MAXS) max_splits = ATTF_DEFAULT_SPLITS;
+    // no more splits than the cache has wave tiles for their 4 waves
+    const int wt = 4 * (64 / (hd / 16));
+    const int cap_splits = (cap + 4 * wt - 1) / (4 * wt);
+    if (max_splits > cap_splits) max_splits = cap_splits;
+    // without a device position, dpos/rope_cur point at a valid dummy (the spare sync words)
+    const int* dp = dpos ? dpos : reinterpret_cast<const int*>(c->sync + TI_SYNC_DUMMY);
+    const float* rc = rope_cur ? rope_cur : reinterpret_cast<const float*>(c->sync + TI_SYNC_DUMMY);
+    AttnFArgs a = {q, k, v, qw, kw, kq, ks, vq, vs, out, c->attn_po, c->attn_ml, c->sync + TI_SYNC_ATTN, dp, rc,
+                   dpos ? 1 : 0, pos, nKv, max_splits, cap, eps, oq, os, {}};
+    if (!dpos) ti_rope_row(a.rope_row, pos, hd, theta);
     dim3 grid(nKv * max_splits);
 #define AF(HD_, G_) \
     if (hd == HD_ && G == G_) { k_attn_fused_q8<HD_, G_><<<grid, 256, 0, c->stream>>>(a); TI_LAUNCHED("k_attn_fused_q8"); return TI_OK; }
@@ -756,13 +920,15 @@ int ti_attn_fused_launch(ti_ctx* c, const float* q, const float* k, const float*
 
 extern "C" int ti_attn_step_q8(ti_ctx* c, const float* q, const float* k, const float* v, const uint16_t* qn_w,
                                const uint16_t* kn_w, uint32_t* kq, float* ks, uint32_t* vq, float* vs, float* out,
-                               int nHq, int nKv, int hd, int pos, int cap, float theta, float eps, int max_splits) {
+                               int nHq, int nKv, int hd, int pos, int cap, float theta, float eps, int max_splits,
+                               uint32_t* out_q, float* out_s) {
     TI_CHECK_CTX(c);
     TI_REQUIRE(q && k && v && qn_w && kn_w && kq && ks && vq && vs && out, "ti_attn_step_q8: null buffer");
     TI_REQUIRE(nKv > 0 && nHq % nKv == 0 && nHq <= TI_ATTN_HEADS_MAX, "ti_attn_step_q8: bad heads (nHq=%d nKv=%d)", nHq, nKv);
     TI_REQUIRE(pos >= 0 && pos < cap, "ti_attn_step_q8: pos %d outside the cache [0, %d)", pos, cap);
     TI_REQUIRE(al16(kq) && al16(vq), "ti_attn_step_q8: kq/vq must be 16-byte aligned");
     TI_REQUIRE(max_splits >= 0 && max_splits <= ATTF_MAXS, "ti_attn_step_q8: max_splits in [0, %d]", ATTF_MAXS);
+    TI_REQUIRE((out_q == nullptr) == (out_s == nullptr), "ti_attn_step_q8: out_q and out_s go together");
     return ti_attn_fused_launch(c, q, k, v, qn_w, kn_w, kq, ks, vq, vs, out, nHq, nKv, hd, nullptr, pos, cap, theta, eps,
-                                max_splits);
+                                max_splits, nullptr, out_q, out_s);
 }

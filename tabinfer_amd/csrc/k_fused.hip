@@ -54,6 +54,8 @@ struct FArgs {
     float* xs_out;
     const uint4* upack;    // gate/up: the up matrix (seg[0] is gate, its y is swi)
     const uint16_t* usc;
+    uint32_t* yq;          // gate/up: swi quantized per 32 (quantQ8) for the down projection
+    float* ys;
 };
 
 // int8 activation of the whole row into LDS (s_xq: K/4 words, s_xs: K/32 scales)
@@ -88,7 +90,91 @@ __device__ __forceinline__ void act_prologue(const FArgs& a, uint32_t* s_xq, flo
     }
 }
 
-// segment of a global row (rows past N are clamped by the caller)
+// Register-resident variant of the prologue for the specialised kernels: thread t
+// holds elements t, t+256, ... (EPT of them), loaded before the weights so that one
+// memory round trip serves the whole prologue. The sum of squares keeps the
+// reference's order (per-thread strided partials, then the 128..1 tree); a 32-group
+// is 32 consecutive lanes, whose absmax is a 32-lane butterfly (max is exact in any
+// order), so every code and scale equals q8_group's.
+template <int EPT>
+struct ActRegs {
+    float x[EPT];
+    uint16_t w[EPT];
+};
+
+template <int MODE, int EPT>
+__device__ __forceinline__ void act_regs_load(const FArgs& a, ActRegs<EPT>& r) {
+    const int t = threadIdx.x;
+    // unconditional loads (clamped index, value masked after): straight-line code
+    // lets the compiler wait for exactly these loads, not the weights behind them
+#pragma unroll
+    for (int i = 0; i < EPT; i++) {
+        const int e = t + 256 * i;
+        const int ec = e < a.K ? e : a.K - 1;
+        r.x[i] = a.x[ec];
+        if (MODE == MODE_NORM) r.w[i] = a.nw[ec];
+    }
+#pragma unroll
+    for (int i = 0; i < EPT; i++) {
+        if (t + 256 * i >= a.K) {
+            r.x[i] = 0.0f;
+            r.w[i] = 0;
+        }
+    }
+}
+
+template <int MODE, int EPT>
+__device__ __forceinline__ void act_regs_quant(const FArgs& a, ActRegs<EPT>& r, uint32_t* s_xq, float* s_xs,
+                                               float* red) {
+    const int t = threadIdx.x;
+    if (MODE == MODE_NORM) {
+        float s = 0.0f;
+#pragma unroll
+        for (int i = 0; i < EPT; i++) {
+            float sq = r.x[i] * r.x[i];
+            s = s + sq;
+        }
+        red[t] = s;
+        __syncthreads();
+#pragma unroll
+        for (int st = 128; st > 0; st >>= 1) {
+            if (t < st) red[t] = red[t] + red[t + st];
+            __syncthreads();
+        }
+        float m = red[0] / (float)a.K;
+        m = m + a.eps;
+        const float inv = 1.0f / sqrtf(m);
+#pragma unroll
+        for (int i = 0; i < EPT; i++) {
+            float p = r.x[i] * inv;
+            r.x[i] = p * ti_h2f(r.w[i]);
+        }
+    }
+    uint8_t* qb = reinterpret_cast<uint8_t*>(s_xq);
+#pragma unroll
+    for (int i = 0; i < EPT; i++) {
+        const int e = t + 256 * i;
+        float mx = fabsf(r.x[i]);
+#pragma unroll
+        for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+        if (e < a.K) {
+            const float scale = mx / 127.0f;
+            const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
+            const float p = r.x[i] * inv;
+            int qi = (int)rintf(p);
+            qi = qi < -127 ? -127 : (qi > 127 ? 127 : qi);
+            qb[e] = (uint8_t)(qi & 0xff);
+            if ((t & 31) == 0) s_xs[e >> 5] = scale;
+        }
+    }
+    __syncthreads();
+    if (a.xq_out && blockIdx.x == 0) {
+        for (int i = t; i < a.K / 4; i += 256) a.xq_out[i] = s_xq[i];
+        for (int g = t; g < a.K / 32; g += 256) a.xs_out[g] = s_xs[g];
+    }
+}
+
+// segment of a global row (the generic kernel: one row per wave)
 __device__ __forceinline__ int seg_of(const FArgs& a, long row, long& local) {
     if (row < a.seg[0].n || a.nseg == 1) { local = row; return 0; }
     row -= a.seg[0].n;
@@ -107,6 +193,31 @@ __device__ __forceinline__ float* seg_y(const FArgs& a, int s) {
     return s == 0 ? a.seg[0].y : (s == 1 ? a.seg[1].y : a.seg[2].y);
 }
 
+// Segment of a row block. Segment sizes are multiples of the block height (the
+// host checks), so a block never straddles two segments and the lookup is
+// wave-uniform: the pointers stay in scalar registers, read from the kernel
+// arguments with constant offsets (a per-lane lookup would turn into dependent
+// vector loads of the argument block before every weight load).
+struct BlkSeg {
+    const uint4* pack;
+    const uint16_t* sc;
+    float* y;
+    int base;
+};
+__device__ __forceinline__ BlkSeg blk_seg(const FArgs& a, int row0) {
+    // selects, no branches: control flow between the activation loads and the
+    // weight loads would make the compiler wait for the weights in the prologue
+    const int n0 = a.seg[0].n, n01 = n0 + a.seg[1].n;
+    const bool in1 = a.nseg > 1 && row0 >= n0;
+    const bool in2 = a.nseg > 2 && row0 >= n01;
+    BlkSeg r;
+    r.pack = in2 ? a.seg[2].pack : (in1 ? a.seg[1].pack : a.seg[0].pack);
+    r.sc = in2 ? a.seg[2].sc : (in1 ? a.seg[1].sc : a.seg[0].sc);
+    r.y = in2 ? a.seg[2].y : (in1 ? a.seg[1].y : a.seg[0].y);
+    r.base = in2 ? n01 : (in1 ? n0 : 0);
+    return r;
+}
+
 __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
 
 template <int LPR, int GPL, int R, int MODE, bool GU>
@@ -119,9 +230,10 @@ __global__ __launch_bounds__(256) void k_fgemv(FArgs a) {
     constexpr int SPAN = LPR / R;          // lanes holding the same row total after the reduce
     const int lane = threadIdx.x & 63;
     const int sub = lane / LPR, li = lane % LPR;
-    const long nwaves = (long)gridDim.x * 4;
-    const long nblocks = ((long)a.N + RPP * R - 1) / (RPP * R);
-    long b = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    constexpr int RB = RPP * R;            // rows per wave block
+    const int nwaves = gridDim.x * 4;
+    const int nblocks = (a.N + RB - 1) / RB;
+    int b = __builtin_amdgcn_readfirstlane((int)(blockIdx.x * 4 + (threadIdx.x >> 6)));
     const bool active = b < nblocks;
 
     uint4 wv[2][R][GPL];
@@ -129,43 +241,42 @@ __global__ __launch_bounds__(256) void k_fgemv(FArgs a) {
     uint4 uv[2][GU ? R : 1][GU ? GPL : 1];
     uint16_t su[2][GU ? R : 1][GU ? GPL : 1];
     float yold[2];
-    auto load = [&](int buf, long blk) {
+    auto load = [&](int buf, int blk) {
+        const BlkSeg sg = blk_seg(a, blk * RB);
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            long row = blk * (RPP * R) + sub + (long)r * RPP;
+            int row = blk * RB + sub + r * RPP;
             row = row < a.N ? row : a.N - 1;
-            long local;
-            const int s = GU ? 0 : seg_of(a, row, local);
-            if (GU) local = row;
-            const uint4* P = GU ? a.seg[0].pack : seg_pack(a, s);
-            const uint16_t* S = GU ? a.seg[0].sc : seg_sc(a, s);
+            const long local = row - sg.base;
 #pragma unroll
             for (int j = 0; j < GPL; j++) {
                 long gi = local * GPR + li + LPR * j;
-                wv[buf][r][j] = ti_ld_nt(P + gi);
-                sw[buf][r][j] = __builtin_nontemporal_load(S + gi);
+                wv[buf][r][j] = ti_ld_nt(sg.pack + gi);
+                sw[buf][r][j] = __builtin_nontemporal_load(sg.sc + gi);
                 if constexpr (GU) {
                     uv[buf][r][j] = ti_ld_nt(a.upack + gi);
                     su[buf][r][j] = __builtin_nontemporal_load(a.usc + gi);
                 }
             }
         }
-        if (!GU && a.acc) {   // residual: the row this lane will store, fetched with the weights
-            long row = blk * (RPP * R) + sub + (long)(li / SPAN) * RPP;
+        if (!GU) {   // residual: the row this lane will store, fetched with the weights (unused if !acc)
+            int row = blk * RB + sub + (li / SPAN) * RPP;
             row = row < a.N ? row : a.N - 1;
-            long local;
-            const int s = seg_of(a, row, local);
-            yold[buf] = seg_y(a, s)[local];
+            yold[buf] = sg.y[row - sg.base];
         }
     };
-    if (active) load(0, b);
-    act_prologue<MODE>(a, s_xq, s_xs, red);
+    constexpr int EPT = (GPR * 32 + 255) / 256;
+    ActRegs<EPT> ar;
+    if (MODE != MODE_Q8) act_regs_load<MODE, EPT>(a, ar);
+    load(0, active ? b : 0);   // unconditional (block 0 for idle waves): no branch between the activation and weight loads
+    if (MODE == MODE_Q8) act_prologue<MODE>(a, s_xq, s_xs, red);
+    else act_regs_quant<MODE, EPT>(a, ar, s_xq, s_xs, red);
     if (!active) return;
     ActQ8 act[GPL];
 #pragma unroll
     for (int j = 0; j < GPL; j++) load_act_q8(s_xq, s_xs, li + LPR * j, act[j]);
 
-    auto finish = [&](int buf, long blk) {
+    auto finish = [&](int buf, int blk) {
         float ga[R], ua[R];
 #pragma unroll
         for (int r = 0; r < R; r++) {
@@ -181,19 +292,18 @@ __global__ __launch_bounds__(256) void k_fgemv(FArgs a) {
         float g = transpose_reduce<LPR, R>(ga, li);
         float u = 0.0f;
         if constexpr (GU) u = transpose_reduce<LPR, R>(ua, li);
-        const long row = blk * (RPP * R) + sub + (long)(li / SPAN) * RPP;
+        const int row = blk * RB + sub + (li / SPAN) * RPP;
         if ((li % SPAN) == 0 && row < a.N) {
             if (GU) {
                 a.seg[0].y[row] = silu_mul(g, u);
             } else {
-                long local;
-                const int s = seg_of(a, row, local);
-                seg_y(a, s)[local] = a.acc ? yold[buf] + g : g;
+                const BlkSeg sg = blk_seg(a, blk * RB);
+                sg.y[row - sg.base] = a.acc ? yold[buf] + g : g;
             }
         }
     };
     for (;;) {
-        long nb = b + nwaves;
+        int nb = b + nwaves;
         if (nb < nblocks) load(1, nb);
         finish(0, b);
         if (nb >= nblocks) break;
@@ -203,6 +313,98 @@ __global__ __launch_bounds__(256) void k_fgemv(FArgs a) {
         finish(1, b);
         if (nb >= nblocks) break;
         b = nb;
+    }
+}
+
+// gate/up + SiLU with the down projection's int8 activation as a by-product: each
+// workgroup computes chunks of 32 consecutive rows (wave w: rows 8w..8w+7), so it
+// holds whole quantQ8 groups of swi and quantizes them itself (linearQ's quantQ8
+// of swi, models/qwen3.js:4033), leaving the down projection a plain int8 GEMV.
+template <int LPR, int GPL>
+__global__ __launch_bounds__(256) void k_gateup_q8out(FArgs a) {
+    __shared__ __align__(16) uint32_t s_xq[FK_MAX / 4];
+    __shared__ float s_xs[FK_MAX / 32];
+    __shared__ float red[256];
+    __shared__ float s_swi[32];
+    constexpr int RPP = 64 / LPR;
+    constexpr int R = 8 / RPP;                 // 8 rows per wave
+    static_assert(R >= 1 && R <= LPR, "gate/up chunk: 8 rows per wave");
+    constexpr int GPR = LPR * GPL;
+    constexpr int SPAN = LPR / R;
+    constexpr int EPT = (GPR * 32 + 255) / 256;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int sub = lane / LPR, li = lane % LPR;
+    const int nchunks = (a.N + 31) / 32;
+    int ch = blockIdx.x;
+    uint4 gw[R][GPL], uw[R][GPL];
+    uint16_t gs[R][GPL], us[R][GPL];
+    auto load = [&](int chunk) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            int row = chunk * 32 + wave * 8 + sub + r * RPP;
+            row = row < a.N ? row : a.N - 1;
+#pragma unroll
+            for (int j = 0; j < GPL; j++) {
+                const long gi = (long)row * GPR + li + LPR * j;
+                gw[r][j] = ti_ld_nt(a.seg[0].pack + gi);
+                uw[r][j] = ti_ld_nt(a.upack + gi);
+                gs[r][j] = __builtin_nontemporal_load(a.seg[0].sc + gi);
+                us[r][j] = __builtin_nontemporal_load(a.usc + gi);
+            }
+        }
+    };
+    ActRegs<EPT> ar;
+    act_regs_load<MODE_NORM, EPT>(a, ar);
+    load(ch < nchunks ? ch : 0);
+    act_regs_quant<MODE_NORM, EPT>(a, ar, s_xq, s_xs, red);
+    ActQ8 act[GPL];
+#pragma unroll
+    for (int j = 0; j < GPL; j++) load_act_q8(s_xq, s_xs, li + LPR * j, act[j]);
+    for (; ch < nchunks; ch += gridDim.x) {
+        float ga[R], ua[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            float tg = 0.0f, tu = 0.0f;
+#pragma unroll
+            for (int j = 0; j < GPL; j++) {
+                tg = fmaf((float)group_dot_q8(gw[r][j], act[j]), ti_h2f(gs[r][j]) * act[j].s, tg);
+                tu = fmaf((float)group_dot_q8(uw[r][j], act[j]), ti_h2f(us[r][j]) * act[j].s, tu);
+            }
+            ga[r] = tg;
+            ua[r] = tu;
+        }
+        const float g = transpose_reduce<LPR, R>(ga, li);
+        const float u = transpose_reduce<LPR, R>(ua, li);
+        const int rl = wave * 8 + sub + (li / SPAN) * RPP;     // row within the chunk
+        const int row = ch * 32 + rl;
+        if ((li % SPAN) == 0) {
+            const float v = row < a.N ? silu_mul(g, u) : 0.0f;
+            if (row < a.N && a.seg[0].y) a.seg[0].y[row] = v;
+            s_swi[rl] = v;
+        }
+        __syncthreads();
+        if (tid < 32) {   // quantQ8 of the chunk's 32 values (q8_group's arithmetic)
+            const float v = s_swi[tid];
+            float mx = fabsf(v);
+#pragma unroll
+            for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+            const float scale = mx / 127.0f;
+            const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
+            const float pq = v * inv;
+            int qi = (int)rintf(pq);
+            qi = qi < -127 ? -127 : (qi > 127 ? 127 : qi);
+            const uint32_t b = (uint32_t)(qi & 0xff);
+            const int src = (tid & 7) * 4;
+            const uint32_t b0 = __shfl(b, src, 64), b1 = __shfl(b, src + 1, 64);
+            const uint32_t b2 = __shfl(b, src + 2, 64), b3 = __shfl(b, src + 3, 64);
+            if (tid < 8) a.yq[(size_t)ch * 8 + tid] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+            if (tid == 0) a.ys[ch] = scale;
+        }
+        if (ch + (int)gridDim.x < nchunks) {
+            __syncthreads();   // s_swi is rewritten by the next chunk
+            load(ch + gridDim.x);
+        }
     }
 }
 
@@ -264,6 +466,9 @@ struct LmArgs {
     int* dpos;             // device position (read, then advanced); may be null
     int out_pos;           // used when dpos is null
     int cap;               // the history holds positions [0, cap]; a step at pos >= cap writes nothing
+    const float* rope_tab; // [cap][rope_hd] cos/sin rows; with rope_cur, the row of the new position
+    float* rope_cur;       // is copied to rope_cur (the fused attention reads it at a fixed address)
+    int rope_hd;
 };
 
 __device__ __forceinline__ void amx_take(float& v, int& i, float v2, int i2) {
@@ -302,12 +507,48 @@ __global__ __launch_bounds__(256) void k_lmhead(LmArgs a) {
             }
         }
     };
-    if (active) load(0, b);
-    // rmsnorm (models/qwen3.js:60-80): y = (x * inv) * w
-    const float inv = rms_inv_256(a.x, a.K, a.eps, red);
-    for (int i = tid; i < a.K; i += 256) {
-        float p = a.x[i] * inv;
-        s_x[i] = p * ti_h2f(a.nw[i]);
+    // rmsnorm (models/qwen3.js:60-80): y = (x * inv) * w, x and w loaded once
+    constexpr int EPT = (GPR * 32 + 255) / 256;
+    float xr[EPT];
+    uint16_t wr[EPT];
+#pragma unroll
+    for (int i = 0; i < EPT; i++) {
+        const int e = tid + 256 * i;
+        const int ec = e < a.K ? e : a.K - 1;
+        xr[i] = a.x[ec];
+        wr[i] = a.nw[ec];
+    }
+    load(0, active ? b : 0);   // unconditional (block 0 for idle waves): no branch between the activation and weight loads
+#pragma unroll
+    for (int i = 0; i < EPT; i++) {
+        if (tid + 256 * i >= a.K) {
+            xr[i] = 0.0f;
+            wr[i] = 0;
+        }
+    }
+    {
+        float s = 0.0f;
+#pragma unroll
+        for (int i = 0; i < EPT; i++) {
+            float sq = xr[i] * xr[i];
+            s = s + sq;
+        }
+        red[tid] = s;
+        __syncthreads();
+#pragma unroll
+        for (int st = 128; st > 0; st >>= 1) {
+            if (tid < st) red[tid] = red[tid] + red[tid + st];
+            __syncthreads();
+        }
+        float m = red[0] / (float)a.K;
+        m = m + a.eps;
+        const float inv = 1.0f / sqrtf(m);
+#pragma unroll
+        for (int i = 0; i < EPT; i++) {
+            const int e = tid + 256 * i;
+            float p = xr[i] * inv;
+            if (e < a.K) s_x[e] = p * ti_h2f(wr[i]);
+        }
     }
     __syncthreads();
     float best_v = -3.0e38f;
@@ -360,23 +601,16 @@ __global__ __launch_bounds__(256) void k_lmhead(LmArgs a) {
         __syncthreads();
     }
     if (tid == 0) {
-        a.part_v[blockIdx.x] = bv_s[0];
-        a.part_i[blockIdx.x] = (uint32_t)bi_s[0];
-        __threadfence();
-        unsigned prev = __hip_atomic_fetch_add(a.counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        last_s = (prev == gridDim.x - 1);
+        ti_pub_store(a.part_v + blockIdx.x, bv_s[0]);
+        ti_pub_store(a.part_i + blockIdx.x, (uint32_t)bi_s[0]);
+        ti_stores_done();
+        last_s = ti_arrive(a.counter) == gridDim.x - 1;
     }
     __syncthreads();
     if (!last_s) return;
-    __threadfence();
     float v = -3.0e38f;
     int i = 0x7fffffff;
-    for (int p = tid; p < (int)gridDim.x; p += 256) {
-        float pv = __uint_as_float(__hip_atomic_load(reinterpret_cast<uint32_t*>(a.part_v) + p, __ATOMIC_RELAXED,
-                                                     __HIP_MEMORY_SCOPE_AGENT));
-        int pi = (int)__hip_atomic_load(a.part_i + p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        amx_take(v, i, pv, pi);
-    }
+    for (int p = tid; p < (int)gridDim.x; p += 256) amx_take(v, i, ti_pub_load(a.part_v + p), (int)ti_pub_load(a.part_i + p));
     bv_s[tid] = v;
     bi_s[tid] = i;
     __syncthreads();
@@ -392,12 +626,17 @@ __global__ __launch_bounds__(256) void k_lmhead(LmArgs a) {
     }
     if (tid == 0) {
         const int pos = a.dpos ? *a.dpos : a.out_pos - 1;
+        last_s = -1;
         if (pos >= 0 && pos < a.cap) {
             a.hist[pos + 1] = (uint32_t)bi_s[0];
             if (a.dpos) *a.dpos = pos + 1;
+            last_s = pos + 1;
         }
         __hip_atomic_store(a.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    __syncthreads();
+    if (a.rope_cur && last_s >= 0 && last_s < a.cap && tid < a.rope_hd)
+        a.rope_cur[tid] = a.rope_tab[(size_t)last_s * a.rope_hd + tid];
 }
 
 // ---- launch shapes -------------------------------------------------------------
@@ -429,7 +668,7 @@ unsigned fgrid(long nblocks) {
 
 // shapes with a specialisation: (lpr, gpl) for K = 32*lpr*gpl
 #define FGEMV_SHAPES(X) X(32, 1) X(64, 1) X(32, 3) X(64, 3) X(64, 2) X(64, 4) X(16, 1) X(8, 1) X(4, 1) X(2, 1) X(1, 1) \
-    X(16, 3) X(8, 3) X(4, 3) X(2, 3) X(1, 3) X(64, 6) X(64, 8)
+    X(16, 3) X(8, 3) X(4, 3) X(2, 3) X(1, 3)
 
 template <int MODE, bool GU>
 static int fgemv_launch(ti_ctx* c, const FArgs& a) {
@@ -437,10 +676,13 @@ static int fgemv_launch(ti_ctx* c, const FArgs& a) {
         return ti_fail(TI_ERR_INVALID, "fused GEMV: K=%d must be a positive multiple of 32 and <= %d", a.K, FK_MAX);
     Shape s = fshape(a.K / 32);
     int R = fpick_R(a.N, s.lpr);
-    long nblocks = ((long)a.N + (64 / s.lpr) * R - 1) / ((64 / s.lpr) * R);
+    const int rb = (64 / s.lpr) * R;
+    bool aligned = true;
+    for (int i = 0; i + 1 < a.nseg; i++) aligned = aligned && a.seg[i].n % rb == 0;
+    long nblocks = ((long)a.N + rb - 1) / rb;
     unsigned grid = fgrid(nblocks);
 #define X(L, G)                                                                                        \
-    if (s.lpr == L && s.gpl == G) {                                                                    \
+    if (aligned && s.lpr == L && s.gpl == G) {                                                         \
         if (R == 4) k_fgemv<L, G, (L >= 4 ? 4 : 1), MODE, GU><<<grid, 256, 0, c->stream>>>(a);         \
         else if (R == 2) k_fgemv<L, G, (L >= 2 ? 2 : 1), MODE, GU><<<grid, 256, 0, c->stream>>>(a);    \
         else k_fgemv<L, G, 1, MODE, GU><<<grid, 256, 0, c->stream>>>(a);                               \
@@ -497,7 +739,8 @@ int ti_fused_linear_launch(ti_ctx* c, const float* x, const uint32_t* pack, cons
 }
 
 int ti_fused_gateup_launch(ti_ctx* c, const float* x, const uint16_t* nw, float eps, const uint32_t* gpack,
-                           const uint16_t* gsc, const uint32_t* upack, const uint16_t* usc, float* swi, int I, int H) {
+                           const uint16_t* gsc, const uint32_t* upack, const uint16_t* usc, float* swi, int I, int H,
+                           uint32_t* swq, float* sws) {
     FArgs a = {};
     a.nseg = 1;
     a.seg[0] = {reinterpret_cast<const uint4*>(gpack), gsc, swi, I};
@@ -508,12 +751,28 @@ int ti_fused_gateup_launch(ti_ctx* c, const float* x, const uint16_t* nw, float 
     a.eps = eps;
     a.upack = reinterpret_cast<const uint4*>(upack);
     a.usc = usc;
-    return fgemv_launch<MODE_NORM, true>(c, a);
+    a.yq = swq;
+    a.ys = sws;
+    if (!swq) return fgemv_launch<MODE_NORM, true>(c, a);
+    if (I % 32 != 0) return ti_fail(TI_ERR_INVALID, "gate/up: I=%d must be a multiple of 32 to quantize swi", I);
+    if (H % 32 != 0 || H > FK_MAX) return ti_fail(TI_ERR_INVALID, "gate/up: H=%d", H);
+    Shape s = fshape(H / 32);
+    const int nchunks = I / 32;
+    const unsigned grid = (unsigned)(nchunks < 1024 ? nchunks : 1024);
+#define X(L, G)                                                                          \
+    if (s.lpr == L && s.gpl == G) {                                                      \
+        k_gateup_q8out<L, G><<<grid, 256, 0, c->stream>>>(a);                            \
+        TI_LAUNCHED("k_gateup_q8out");                                                   \
+        return TI_OK;                                                                    \
+    }
+    X(64, 1) X(32, 1) X(16, 1) X(8, 1) X(64, 3) X(32, 3) X(16, 3) X(8, 3) X(64, 2)
+#undef X
+    return ti_fail(TI_ERR_INVALID, "gate/up: no chunked kernel for H=%d", H);
 }
 
 int ti_fused_lmhead_launch(ti_ctx* c, const float* x, const uint16_t* nw, float eps, const uint32_t* pack,
                            const uint16_t* sc, float* logits, int N, int K, uint32_t* hist, int* dpos, int out_pos,
-                           int cap) {
+                           int cap, const float* rope_tab, float* rope_cur, int rope_hd) {
     if (K % 32 != 0 || K > LM_KMAX || K <= 0)
         return ti_fail(TI_ERR_INVALID, "lm_head: K=%d must be a positive multiple of 32 and <= %d", K, LM_KMAX);
     LmArgs a = {};
@@ -532,6 +791,11 @@ int ti_fused_lmhead_launch(ti_ctx* c, const float* x, const uint16_t* nw, float 
     a.dpos = dpos;
     a.out_pos = out_pos;
     a.cap = cap;
+    a.rope_tab = rope_tab;
+    a.rope_cur = rope_cur;
+    a.rope_hd = rope_hd;
+    if (rope_cur && (!rope_tab || rope_hd <= 0 || rope_hd > 256))
+        return ti_fail(TI_ERR_INVALID, "lm_head: bad rope row arguments");
     Shape s = fshape(K / 32);
     int R = fpick_R(N, s.lpr);
     long nblocks = ((long)N + (64 / s.lpr) * R - 1) / ((64 / s.lpr) * R);
@@ -572,12 +836,17 @@ extern "C" int ti_rmsnorm_gemv_q4(ti_ctx* c, const float* x, const uint16_t* nor
 
 extern "C" int ti_rmsnorm_gateup_silu_q4(ti_ctx* c, const float* x, const uint16_t* norm_w, float eps,
                                          const uint32_t* gpack, const uint16_t* gsc, const uint32_t* upack,
-                                         const uint16_t* usc, float* swi, int I, int H) {
+                                         const uint16_t* usc, float* swi, int I, int H, uint32_t* swi_q,
+                                         float* swi_s) {
     TI_CHECK_CTX(c);
-    TI_REQUIRE(x && norm_w && gpack && gsc && upack && usc && swi, "ti_rmsnorm_gateup_silu_q4: null buffer");
+    TI_REQUIRE(x && norm_w && gpack && gsc && upack && usc, "ti_rmsnorm_gateup_silu_q4: null buffer");
+    TI_REQUIRE(swi || swi_q, "ti_rmsnorm_gateup_silu_q4: no output (swi and swi_q both null)");
+    TI_REQUIRE((swi_q == nullptr) == (swi_s == nullptr), "ti_rmsnorm_gateup_silu_q4: swi_q and swi_s go together");
+    TI_REQUIRE(swi_q || swi, "ti_rmsnorm_gateup_silu_q4: null swi");
     TI_REQUIRE(I > 0 && H > 0 && H % 32 == 0 && H <= FK_MAX, "ti_rmsnorm_gateup_silu_q4: bad shape (I=%d H=%d)", I, H);
+    TI_REQUIRE(!swi_q || I % 32 == 0, "ti_rmsnorm_gateup_silu_q4: I=%d must be a multiple of 32 for swi_q", I);
     TI_REQUIRE(al16(x) && al16(gpack) && al16(upack), "ti_rmsnorm_gateup_silu_q4: x and packs must be 16-byte aligned");
-    return ti_fused_gateup_launch(c, x, norm_w, eps, gpack, gsc, upack, usc, swi, I, H);
+    return ti_fused_gateup_launch(c, x, norm_w, eps, gpack, gsc, upack, usc, swi, I, H, swi_q, swi_s);
 }
 
 extern "C" int ti_rmsnorm_lm_head_argmax(ti_ctx* c, const float* x, const uint16_t* norm_w, float eps,
@@ -588,5 +857,6 @@ extern "C" int ti_rmsnorm_lm_head_argmax(ti_ctx* c, const float* x, const uint16
     TI_REQUIRE(N > 0 && K > 0 && K % 32 == 0 && K <= LM_KMAX, "ti_rmsnorm_lm_head_argmax: bad shape (N=%d K=%d)", N, K);
     TI_REQUIRE(out_pos >= 1, "ti_rmsnorm_lm_head_argmax: out_pos must be >= 1");
     TI_REQUIRE(al16(x) && al16(pack), "ti_rmsnorm_lm_head_argmax: x and pack must be 16-byte aligned");
-    return ti_fused_lmhead_launch(c, x, norm_w, eps, pack, scales, logits, N, K, tok_hist, nullptr, out_pos, out_pos);
+    return ti_fused_lmhead_launch(c, x, norm_w, eps, pack, scales, logits, N, K, tok_hist, nullptr, out_pos, out_pos,
+                                  nullptr, nullptr, 0);
 }

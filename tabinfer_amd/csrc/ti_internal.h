@@ -55,9 +55,10 @@ struct ti_graph {
 #define TI_AMAX_PARTS 1024
 #define TI_MOE_P_MAX 8192
 #define TI_MOE_E_MAX 256
-#define TI_SYNC_WORDS 256
+#define TI_SYNC_WORDS 512
 #define TI_SYNC_LMHEAD 0          // lm_head argmax
 #define TI_SYNC_ATTN 64           // fused attention: one counter per KV head (up to 64)
+#define TI_SYNC_DUMMY 256         // 256 words never written: a valid read target for unused inputs
 
 // ---- device helpers -----------------------------------------------------------
 // f16 bits -> f32 (exact).
@@ -78,4 +79,31 @@ __device__ __forceinline__ float ti_seg_sum(float v) {
 #pragma unroll
     for (int o = WIDTH / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
     return v;
+}
+
+// ---- cross-workgroup hand-off without cache maintenance ----------------------------
+// The "last workgroup finishes the reduction" kernels publish a few words per
+// workgroup. A device-scope fence on gfx950 writes back and invalidates the whole
+// XCD L2 (buffer_wbl2/buffer_inv), which costs microseconds when every workgroup
+// does it; instead the published words are written and read with device-scope
+// atomic stores/loads (sc1: they bypass the non-coherent XCD L2), and the writer
+// waits for its stores to be acknowledged (vmcnt(0)) before bumping the counter.
+__device__ __forceinline__ void ti_pub_store(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void ti_pub_store(uint32_t* p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ti_pub_load(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t ti_pub_load(const uint32_t* p) {
+    return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// all of this thread's prior memory operations acknowledged (gfx9 encoding of
+// s_waitcnt vmcnt(0) expcnt(7) lgkmcnt(15))
+__device__ __forceinline__ void ti_stores_done() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+// bump a completion counter; returns the previous count
+__device__ __forceinline__ uint32_t ti_arrive(uint32_t* counter) {
+    return __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

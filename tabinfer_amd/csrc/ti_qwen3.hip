@@ -23,14 +23,16 @@ int ti_attn_prep_launch(ti_ctx*, const float*, const float*, const float*, const
 int ti_attn_decode_launch(ti_ctx*, const float*, const uint32_t*, const float*, const uint32_t*, const float*, float*,
                           int, int, int, int, int, int, const int*, int);
 int ti_attn_fused_launch(ti_ctx*, const float*, const float*, const float*, const uint16_t*, const uint16_t*, uint32_t*,
-                         float*, uint32_t*, float*, float*, int, int, int, const int*, int, int, float, float, int);
+                         float*, uint32_t*, float*, float*, int, int, int, const int*, int, int, float, float, int,
+                         const float*, uint32_t*, float*);
+void ti_rope_row(float* cs, int pos, int hd, float theta);
 int ti_fused_qkv_launch(ti_ctx*, const float*, const uint16_t*, float, int, int, const uint32_t* const*,
                         const uint16_t* const*, float* const*, const int*, uint32_t*, float*);
 int ti_fused_linear_launch(ti_ctx*, const float*, const uint32_t*, const uint16_t*, float*, int, int, int);
 int ti_fused_gateup_launch(ti_ctx*, const float*, const uint16_t*, float, const uint32_t*, const uint16_t*,
-                           const uint32_t*, const uint16_t*, float*, int, int);
+                           const uint32_t*, const uint16_t*, float*, int, int, uint32_t*, float*);
 int ti_fused_lmhead_launch(ti_ctx*, const float*, const uint16_t*, float, const uint32_t*, const uint16_t*, float*, int,
-                           int, uint32_t*, int*, int, int);
+                           int, uint32_t*, int*, int, int, const float*, float*, int);
 int ti_fused_kmax(int lm);
 
 // ---------------------------------------------------------------------------
@@ -106,7 +108,12 @@ __global__ __launch_bounds__(AMX_PARTS) void k_argmax_p2(const float* __restrict
     }
 }
 
-__global__ void k_set_int(int* __restrict__ p, int v) { *p = v; }
+// device position := pos, and its rotary row into rope_cur (hd threads)
+__global__ void k_set_pos(int* __restrict__ dpos, int pos, const float* __restrict__ rope, float* __restrict__ rope_cur,
+                          int hd, int cap) {
+    if (threadIdx.x == 0) *dpos = pos;
+    if (pos < cap && (int)threadIdx.x < hd) rope_cur[threadIdx.x] = rope[(size_t)pos * hd + threadIdx.x];
+}
 
 // swi = silu(g) * u (models/qwen3.js swiglu; silu(g) = g / (1 + e^-g))
 __global__ void k_swiglu(const float* __restrict__ g, const float* __restrict__ u, float* __restrict__ y, long n) {
@@ -148,6 +155,8 @@ struct ti_qwen3 {
     int32_t* xsum;
     uint32_t* hist;
     int* dpos;
+    float* rope;          // [max_ctx][head_dim] cos/sin rows of the rotary embedding
+    float* rope_cur;      // the row of the device position (kept in step with dpos)
     float* amx_v;
     uint32_t* amx_i;
     std::vector<void*> allocs;
@@ -231,6 +240,15 @@ extern "C" int ti_qwen3_create(ti_ctx* c, const ti_qwen3_config* cfg, ti_qwen3**
     if (!rc) rc = mk(m, (void**)&m->xsum, kmax / 16 * 4);
     if (!rc) rc = mk(m, (void**)&m->hist, (size_t)(C.max_ctx + 1) * 4);
     if (!rc) rc = mk(m, (void**)&m->dpos, 4);
+    if (!rc) rc = mk(m, (void**)&m->rope, (size_t)C.max_ctx * hd * 4);
+    if (!rc) rc = mk(m, (void**)&m->rope_cur, (size_t)hd * 4);
+    if (!rc) {
+        std::vector<float> tab((size_t)C.max_ctx * hd);
+        for (int p = 0; p < C.max_ctx; p++) ti_rope_row(tab.data() + (size_t)p * hd, p, hd, C.rope_theta);
+        hipError_t e = hipMemcpy(m->rope, tab.data(), tab.size() * 4, hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = hipMemcpy(m->rope_cur, tab.data(), (size_t)hd * 4, hipMemcpyHostToDevice);
+        if (e != hipSuccess) rc = ti_hip_fail(e, "ti_qwen3_create rope table");
+    }
     if (!rc) rc = mk(m, (void**)&m->amx_i, (size_t)AMX_PARTS * 4);
     if (!rc) {
         hipError_t e = hipMemset(m->hist, 0, (size_t)(C.max_ctx + 1) * 4);
@@ -311,8 +329,8 @@ extern "C" int ti_qwen3_logits(ti_qwen3* m, float** logits) {
 extern "C" int ti_qwen3_set_pos(ti_ctx* c, ti_qwen3* m, int pos) {
     TI_CHECK_CTX(c);
     TI_REQUIRE(m && pos >= 0 && pos < m->cfg.max_ctx, "ti_qwen3_set_pos: pos %d out of [0, %d)", pos, m ? m->cfg.max_ctx : 0);
-    k_set_int<<<1, 1, 0, c->stream>>>(m->dpos, pos);
-    TI_LAUNCHED("k_set_int");
+    k_set_pos<<<1, 256, 0, c->stream>>>(m->dpos, pos, m->rope, m->rope_cur, m->cfg.head_dim, m->cfg.max_ctx);
+    TI_LAUNCHED("k_set_pos");
     return TI_OK;
 }
 
@@ -358,9 +376,11 @@ extern "C" int ti_embed(ti_ctx* c, const int32_t* ids, const uint16_t* emb, floa
 // One decode step at the device position (forward(null, pos, {chain: true}),
 // models/qwen3.js:3951-4055) in 2 + 5 x layers launches:
 //   embed(tok[pos])
-//   per layer: [rmsnormQ + q/k/v GEMVs] [attnPrep + split-KV attention + combine]
-//              [quantQ8 + o_proj + residual] [rmsnormQ + gate/up + SiLU]
-//              [quantQ8 + down_proj + residual]
+//   per layer: [rmsnormQ + q/k/v GEMVs]
+//              [attnPrep + split-KV attention + combine + quantQ8 of the output]
+//              [o_proj GEMV + residual]
+//              [rmsnormQ + gate/up + SiLU + quantQ8 of swi]
+//              [down_proj GEMV + residual]
 //   [final rmsnorm + lm_head + argmax -> tok[pos+1], pos += 1]
 extern "C" int ti_qwen3_decode(ti_ctx* c, ti_qwen3* m) {
     TI_CHECK_CTX(c);
@@ -380,14 +400,14 @@ extern "C" int ti_qwen3_decode(ti_ctx* c, ti_qwen3* m) {
         const int Ns[3] = {nq, nkv, nkv};
         RC(ti_fused_qkv_launch(c, m->x, y.in_norm, C.rms_eps, H, 3, packs, scs, ys, Ns, nullptr, nullptr));
         RC(ti_attn_fused_launch(c, m->q, m->k, m->v, y.q_norm, y.k_norm, y.kq, y.ks, y.vq, y.vs, m->attn, nHq, nKv, hd,
-                                m->dpos, 0, C.max_ctx, C.rope_theta, C.rms_eps, 0));
-        RC(ti_fused_linear_launch(c, m->attn, y.o.pack, y.o.sc, m->x, H, nq, 1));
-        RC(ti_fused_gateup_launch(c, m->x, y.post_norm, C.rms_eps, y.gate.pack, y.gate.sc, y.up.pack, y.up.sc, m->swi,
-                                  I, H));
-        RC(ti_fused_linear_launch(c, m->swi, y.down.pack, y.down.sc, m->x, H, I, 1));
+                                m->dpos, 0, C.max_ctx, C.rope_theta, C.rms_eps, 0, m->rope_cur, m->xq, m->xs));
+        RC(ti_gemv_q4_q8_launch(c, m->xq, m->xs, y.o.pack, y.o.sc, m->x, H, nq, 1));
+        RC(ti_fused_gateup_launch(c, m->x, y.post_norm, C.rms_eps, y.gate.pack, y.gate.sc, y.up.pack, y.up.sc, nullptr,
+                                  I, H, m->xq, m->xs));
+        RC(ti_gemv_q4_q8_launch(c, m->xq, m->xs, y.down.pack, y.down.sc, m->x, H, I, 1));
     }
     RC(ti_fused_lmhead_launch(c, m->x, m->final_norm, C.rms_eps, m->lm.pack, m->lm.sc, m->logits, C.vocab, H, m->hist,
-                              m->dpos, 0, C.max_ctx));
+                              m->dpos, 0, C.max_ctx, m->rope, m->rope_cur, hd));
     return TI_OK;
 }
 
@@ -428,9 +448,9 @@ extern "C" int ti_qwen3_forward(ti_ctx* c, ti_qwen3* m, const int32_t* ids, int 
     k_copy_f32<<<(H + 255) / 256, 256, 0, c->stream>>>(m->x + (size_t)(T - 1) * H, m->last, H);
     TI_LAUNCHED("k_copy_f32");
     RC(ti_fused_lmhead_launch(c, m->last, m->final_norm, C.rms_eps, m->lm.pack, m->lm.sc, m->logits, C.vocab, H, m->hist,
-                              nullptr, pos + T, C.max_ctx));
-    k_set_int<<<1, 1, 0, c->stream>>>(m->dpos, pos + T);
-    TI_LAUNCHED("k_set_int");
+                              nullptr, pos + T, C.max_ctx, nullptr, nullptr, 0));
+    k_set_pos<<<1, 256, 0, c->stream>>>(m->dpos, pos + T, m->rope, m->rope_cur, hd, C.max_ctx);
+    TI_LAUNCHED("k_set_pos");
     return TI_OK;
 #undef RC
 }

@@ -99,7 +99,7 @@ def test_linear_t1_residual(ctx, orc, N, K):
     assert rel_err(ctx.download(dy, np.float32, N), ref) < TOL
 
 
-@pytest.mark.parametrize("I,H", [(3072, 1024), (6144, 2048), (130, 256)])
+@pytest.mark.parametrize("I,H", [(3072, 1024), (6144, 2048), (130, 256), (1792, 2048), (96, 3072)])
 def test_rmsnorm_gateup(ctx, orc, I, H):
     rng = np.random.default_rng(I + H)
     x = (rng.standard_normal(H) * 2).astype(np.float32)
@@ -108,10 +108,24 @@ def test_rmsnorm_gateup(ctx, orc, I, H):
     gp, gs, dgp, dgs = quantized(ctx, orc, rng, I, H)
     up, us, dup, dus = quantized(ctx, orc, rng, I, H)
     dswi = ctx.zeros(I * 4)
-    ctx.call("ti_rmsnorm_gateup_silu_q4", ctx.upload(x), ctx.upload(nw), eps, dgp, dgs, dup, dus, dswi, I, H)
+    ctx.call("ti_rmsnorm_gateup_silu_q4", ctx.upload(x), ctx.upload(nw), eps, dgp, dgs, dup, dus, dswi, I, H, None, None)
     xq, xs, _ = orc.rmsnorm_q8(x, nw, eps)
     ref = orc.gateup_silu_q4(xq, xs, gp, gs, up, us, I, H)
-    assert rel_err(ctx.download(dswi, np.float32, I), ref) < TOL
+    got = ctx.download(dswi, np.float32, I)
+    assert rel_err(got, ref) < TOL
+    if I % 32 == 0:
+        # the chunked kernel: the same swi, plus swi quantized as linearQ's quantQ8 would
+        sw2, sq, ss = ctx.zeros(I * 4), ctx.zeros(I), ctx.zeros(I // 8)
+        ctx.call("ti_rmsnorm_gateup_silu_q4", ctx.upload(x), ctx.upload(nw), eps, dgp, dgs, dup, dus, sw2, I, H, sq, ss)
+        got2 = ctx.download(sw2, np.float32, I)
+        assert rel_err(got2, ref) < TOL
+        oq, os_, _ = orc.quant_act_q8(got2)
+        assert np.array_equal(ctx.download(sq, np.uint32, I // 4), oq)
+        assert np.array_equal(ctx.download(ss, np.float32, I // 32), os_)
+        # swi itself may be omitted
+        sq2, ss2 = ctx.zeros(I), ctx.zeros(I // 8)
+        ctx.call("ti_rmsnorm_gateup_silu_q4", ctx.upload(x), ctx.upload(nw), eps, dgp, dgs, dup, dus, None, I, H, sq2, ss2)
+        assert np.array_equal(ctx.download(sq2, np.uint32, I // 4), oq)
 
 
 @pytest.mark.parametrize("N,K", [(151936, 1024), (151936, 2048), (1000, 256)])
@@ -190,10 +204,16 @@ def test_attn_step_matches_prep_plus_decode(ctx, orc, nHq, nKv, hd, S, max_split
     ctx.write(cache[0], np.full(row_w, 0xA5A5A5A5, np.uint32), pos * row_w * 4)   # row pos holds garbage
     ctx.write(cache[1], np.full(row_g, 0x7FC00000, np.uint32), pos * row_g * 4)   # (a NaN scale)
     out = ctx.zeros(nHq * hd * 4)
+    oq, os_ = ctx.zeros(nHq * hd), ctx.zeros(nHq * hd // 8)
     for rep in range(2):                                   # the combine counter must be reset between launches
-        ctx.call("ti_attn_step_q8", *d, *cache, out, nHq, nKv, hd, pos, cap, theta, eps, max_splits)
+        ctx.call("ti_attn_step_q8", *d, *cache, out, nHq, nKv, hd, pos, cap, theta, eps, max_splits,
+                 oq if rep else None, os_ if rep else None)
         got = ctx.download(out, np.float32, nHq * hd)
         assert rel_err(got, ref) < TOL, rep
+    # the output quantized as o_proj's linearQ would (quantQ8), bit-exact on the f32 output
+    rq, rs, _ = orc.quant_act_q8(got)
+    assert np.array_equal(ctx.download(oq, np.uint32, nHq * hd // 4), rq)
+    assert np.array_equal(ctx.download(os_, np.float32, nHq * hd // 32), rs)
     gk = ctx.download(cache[0], np.uint32, cap * row_w).reshape(cap, row_w)
     gks = ctx.download(cache[1], np.float32, cap * row_g).reshape(cap, row_g)
     gv = ctx.download(cache[2], np.uint32, cap * row_w).reshape(cap, row_w)
@@ -206,4 +226,4 @@ def test_attn_step_rejects_out_of_capacity(ctx):
     b = ctx.zeros(1 << 16)
     with pytest.raises(abi.TIError):
         ctx.call("ti_attn_step_q8", b, b, b, b, b, b, b, b, b, b, 16, 8, 128, 10, 10, np.float32(1e6),
-                 np.float32(1e-6), 0)
+                 np.float32(1e-6), 0, None, None)
