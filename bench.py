@@ -312,6 +312,24 @@ def decode_1p7b(ctx, pool, contexts=(8192, 32768), steps=64):
                              "pct_of_hbm_peak": round(100 * step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
                              "bytes_per_step": step_bytes, "launches_per_step": 2 + 5 * cfg["layers"]}
         log("decode 1.7B at %d: %.1f tok/s" % (S, 1e3 / ms))
+        # batch 8 (a T = 8 forward of one sequence at positions S..S+7: the MFMA GEMM path)
+        ctx.graph_begin()
+        m.forward(None, S, T=8)
+        g8 = ctx.graph_end()
+        for _ in range(2):
+            ctx.graph_launch(g8)
+        ctx.sync()
+        ctx.record(22)
+        reps = 10
+        for _ in range(reps):
+            ctx.graph_launch(g8)
+        ctx.record(23)
+        ctx.sync()
+        ms8 = ctx.elapsed_ms(22, 23) / reps
+        ctx.graph_destroy(g8)
+        res["ctx_%d" % S]["batch8_tok_s"] = round(8e3 / ms8, 1)
+        res["ctx_%d" % S]["batch8_ms_per_forward"] = round(ms8, 4)
+        log("T=8 forward 1.7B at %d: %.1f tok/s" % (S, 8e3 / ms8))
     tok = m.read_tokens(0, 4)
     m.close()
     res["weights_bytes"] = wbytes

@@ -210,7 +210,9 @@ int ti_qwen3_tensor(ti_qwen3* m, const char* name, void** data, size_t* data_byt
 int ti_qwen3_kv(ti_qwen3* m, int layer, uint32_t** kq, float** ks, uint32_t** vq, float** vs);
 int ti_qwen3_logits(ti_qwen3* m, float** logits);
 /* forward(ids, pos) at T >= 1 (models/qwen3.js:3938): history[pos..pos+T) = ids, KV
- * written, argmax of the last logits to history[pos+T], device position = pos+T. */
+ * written, argmax of the last logits to history[pos+T], device position = pos+T.
+ * ids == NULL takes the tokens already in the history (ti_qwen3_write_tokens), which
+ * makes the call capturable into a graph. */
 int ti_qwen3_forward(ti_ctx* ctx, ti_qwen3* m, const int32_t* ids, int T, int pos);
 /* forward(null, pos, {chain: true}) (models/qwen3.js:3951-3959, 4055): one step at the
  * device position P: embeds history[P], writes KV row P, argmax -> history[P+1], P += 1.

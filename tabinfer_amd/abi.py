@@ -275,7 +275,11 @@ class Qwen3:
         check(lib().ti_qwen3_logits(self.h, C.byref(p)))
         return p.value
 
-    def forward(self, ids, pos):
+    def forward(self, ids, pos, T=None):
+        """forward(ids, pos); ids None runs the T tokens already in the history."""
+        if ids is None:
+            check(lib().ti_qwen3_forward(self.ctx.h, self.h, None, T, pos))
+            return
         ids = np.ascontiguousarray(ids, dtype=np.int32)
         check(lib().ti_qwen3_forward(self.ctx.h, self.h, ids.ctypes.data, ids.size, pos))
 

@@ -1,17 +1,120 @@
-// k_gemm.hip — T>1 int4 x int8 GEMM (gemmDP4A, models/qwen3.js:1326-1407).
-#include "ti_internal.h"
+// k_gemm.hip — T > 1 int4 x int8 GEMM on the matrix cores (gemmDP4A,
+// models/qwen3.js:1326-1407; per-token activation quant QUANTQ8T :1210-1231).
+//
+// y[t][n] (+)= sum_g s_w[n,g] * s_x[t,g] * dot_g(t, n), dot_g the exact int32 dot of
+// the 32-element group g. One v_mfma_i32_16x16x32_i8 computes dot_g for a 16-token x
+// 16-row tile: K = 32 is exactly one scale group, so every MFMA result is one group's
+// int32 partial and is scaled into an f32 accumulator right away, as the reference
+// does per group.
+//
+// Operands (gfx950 16x16x32 i8 layout: lane l feeds row/column l%16 and K slice
+// 8*(l/16)..+8; the result row 4*(l/16)+i, column l%16 lands in lane l, element i):
+//   A = activations, rows = tokens: 8 int8 codes of token l%16, permuted
+//       [x0 x2 x4 x6 | x1 x3 x5 x7] to match B;
+//   B = weights, columns = weight rows: one packed word (8 nibbles) of row n0+l%16,
+//       split into even/odd nibbles and sign-shifted to int8 (nibble - 8).
+// Workgroup = 16 weight rows; its 4 waves take interleaved quarters of the groups and
+// their partials meet in LDS. Tokens beyond 16 are further 16-row M tiles of the same
+// launch (the weight tile is then re-read from L2).
+#include "ti_dev.h"
 
-int ti_gemv_q4_q8_launch(ti_ctx* c, const uint32_t* xq, const float* xs, const uint32_t* pack, const uint16_t* scales,
-                         float* y, int N, int K, int acc);
+namespace {
 
-// One GEMV per token over the per-token int8 rows (exact same arithmetic as
-// the T=1 path).
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// 8 nibbles of a packed word -> two words of signed bytes (nibble - 8): even
+// nibbles (k = 0,2,4,6) and odd nibbles (k = 1,3,5,7)
+__device__ __forceinline__ void nib_to_s8(uint32_t w, uint32_t& lo, uint32_t& hi) {
+    const uint32_t e = (w & 0x0F0F0F0Fu) ^ 0x08080808u;           // nibble ^ 8: sign bit at bit 3
+    const uint32_t o = ((w >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u;
+    lo = e | (((e & 0x08080808u) >> 3) * 0xF0u);                   // sign-extend 4 -> 8 bits per byte
+    hi = o | (((o & 0x08080808u) >> 3) * 0xF0u);
+}
+
+constexpr int GMAX = 512;       // K <= 16384
+constexpr int UNROLL = 4;
+
+__global__ __launch_bounds__(256) void k_gemm_q4_q8_mfma(const uint32_t* __restrict__ xq, const float* __restrict__ xs,
+                                                          const uint32_t* __restrict__ pack,
+                                                          const uint16_t* __restrict__ scales, float* __restrict__ y,
+                                                          int T, int N, int K, int acc) {
+    __shared__ float s_sx[16][GMAX];
+    __shared__ float s_part[4][16][17];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int G = K / 32;
+    const int m = lane & 15, j = lane >> 4;
+    const int n0 = blockIdx.x * 16;
+    const int row = min(n0 + m, N - 1);
+    const uint32_t* prow = pack + (size_t)row * (K / 8);
+    const uint16_t* srow = scales + (size_t)row * G;
+
+    for (int t0 = 0; t0 < T; t0 += 16) {
+        const int tm = min(16, T - t0);
+        __syncthreads();                       // s_sx / s_part of the previous M tile are consumed
+        for (int e = tid; e < 16 * G; e += 256) {
+            const int t = e / G, g = e % G;
+            s_sx[t][g] = t < tm ? xs[(size_t)(t0 + t) * G + g] : 0.0f;
+        }
+        __syncthreads();
+        // token row of this lane's A operand (rows past T read token t0 and are zeroed by s_sx)
+        const int ta = t0 + (m < tm ? m : 0);
+        const uint32_t* arow = xq + (size_t)ta * (K / 4);
+        float accv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        // this wave's groups: wave, wave + 4, ...
+        for (int g0 = wave; g0 < G; g0 += 4 * UNROLL) {
+            uint32_t wq[UNROLL];
+            uint2 aq[UNROLL];
+            uint16_t sw[UNROLL];
+#pragma unroll
+            for (int u = 0; u < UNROLL; u++) {
+                const int g = g0 + 4 * u;
+                const int gc = g < G ? g : G - 1;
+                wq[u] = __builtin_nontemporal_load(prow + 4 * gc + j);
+                aq[u] = *reinterpret_cast<const uint2*>(arow + 8 * gc + 2 * j);
+                sw[u] = srow[gc];
+            }
+#pragma unroll
+            for (int u = 0; u < UNROLL; u++) {
+                const int g = g0 + 4 * u;
+                if (g < G) {
+                    uint32_t blo, bhi;
+                    nib_to_s8(wq[u], blo, bhi);
+                    const uint32_t alo = even_bytes(aq[u].x, aq[u].y), ahi = odd_bytes(aq[u].x, aq[u].y);
+                    const long A = (long)(((uint64_t)ahi << 32) | alo);
+                    const long B = (long)(((uint64_t)bhi << 32) | blo);
+                    const v4i z = {0, 0, 0, 0};
+                    const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, z, 0, 0, 0);
+                    const float s = ti_h2f(sw[u]);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) accv[i] = fmaf((float)d[i], s * s_sx[4 * j + i][g], accv[i]);
+                }
+            }
+        }
+        // the 4 waves' partials: lane holds tokens 4j..4j+3 of column m
+#pragma unroll
+        for (int i = 0; i < 4; i++) s_part[wave][4 * j + i][m] = accv[i];
+        __syncthreads();
+        {
+            const int t = tid / 16, c = tid % 16;    // 256 threads = 16 tokens x 16 rows
+            const int n = n0 + c;
+            if (t < tm && n < N) {
+                const float v = (s_part[0][t][c] + s_part[1][t][c]) + (s_part[2][t][c] + s_part[3][t][c]);
+                float* yp = y + (size_t)(t0 + t) * N + n;
+                *yp = acc ? *yp + v : v;
+            }
+        }
+    }
+}
+
+}  // namespace
+
 int ti_gemm_q4_q8_launch(ti_ctx* c, const uint32_t* xq, const float* xs, const uint32_t* pack, const uint16_t* scales,
                          float* y, int T, int N, int K, int acc) {
-    for (int t = 0; t < T; t++) {
-        int rc = ti_gemv_q4_q8_launch(c, xq + (size_t)t * (K / 4), xs + (size_t)t * (K / 32), pack, scales,
-                                      y + (size_t)t * N, N, K, acc);
-        if (rc) return rc;
-    }
+    if (K % 32 != 0 || K / 32 > GMAX) return ti_fail(TI_ERR_INVALID, "int4 GEMM: K=%d must be a multiple of 32, <= %d", K, GMAX * 32);
+    if (T <= 0 || N <= 0) return ti_fail(TI_ERR_INVALID, "int4 GEMM: T=%d N=%d", T, N);
+    const unsigned grid = (unsigned)((N + 15) / 16);
+    k_gemm_q4_q8_mfma<<<grid, 256, 0, c->stream>>>(xq, xs, pack, scales, y, T, N, K, acc);
+    TI_LAUNCHED("k_gemm_q4_q8_mfma");
     return TI_OK;
 }

@@ -417,14 +417,14 @@ extern "C" int ti_qwen3_decode(ti_ctx* c, ti_qwen3* m) {
 // position to pos+T, so the next chained step embeds hist[pos+T].
 extern "C" int ti_qwen3_forward(ti_ctx* c, ti_qwen3* m, const int32_t* ids, int T, int pos) {
     TI_CHECK_CTX(c);
-    TI_REQUIRE(m && ids, "ti_qwen3_forward: null argument");
+    TI_REQUIRE(m, "ti_qwen3_forward: null model");
     const ti_qwen3_config& C = m->cfg;
     TI_REQUIRE(T > 0 && T <= C.max_tokens && pos >= 0 && pos + T <= C.max_ctx,
                "ti_qwen3_forward: T=%d pos=%d outside max_tokens=%d / max_ctx=%d", T, pos, C.max_tokens, C.max_ctx);
     const int H = C.hidden, I = C.intermediate, hd = C.head_dim, nHq = C.n_heads, nKv = C.n_kv_heads;
     const int nq = nHq * hd, nkv = nKv * hd;
     int rc;
-    RC(ti_buf_write(c, m->hist, (size_t)pos * 4, ids, (size_t)T * 4));
+    if (ids) RC(ti_buf_write(c, m->hist, (size_t)pos * 4, ids, (size_t)T * 4));   // else already in the history
     k_embed<<<(unsigned)(((long)T * H + 255) / 256), 256, 0, c->stream>>>(m->hist, m->embed, m->x, T, H, pos, nullptr, C.vocab);
     TI_LAUNCHED("k_embed");
     for (int l = 0; l < C.layers; l++) {

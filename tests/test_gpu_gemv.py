@@ -162,6 +162,30 @@ def test_linear_router(ctx, orc, T, N, K):
     assert rel_err(ctx.download(dy, np.float32, T * N), ref) < TOL
 
 
+@pytest.mark.parametrize("T,N,K", [(2, 2048, 2048), (8, 6144, 2048), (8, 2048, 6144), (16, 1024, 1024),
+                                   (17, 4096, 2048), (40, 96, 320), (8, 1000, 3072), (256, 256, 1024)])
+def test_gemm_mfma_batched_linear(ctx, orc, T, N, K):
+    """linearQ at T > 1 (models/qwen3.js:1604-1607): per-token quantQ8T + the MFMA int4 x int8
+    GEMM; max relative error 1e-3 against the f64 oracle of the quantized operands, with and
+    without the fused residual."""
+    rng = np.random.default_rng(T * 131 + N + K)
+    pack, sc, dp, ds = _weights(ctx, orc, rng, N, K)
+    X = rng.standard_normal(T * K).astype(np.float32)
+    X[:32] = 0                                            # a zero group in token 0
+    xq, xs = orc.quant_act_q8_t(X, T, K)
+    ref = orc.gemm_q4_q8(xq, xs, pack, sc, T, N, K)
+    dx, dy = ctx.upload(X), ctx.zeros(T * N * 4)
+    ctx.call("ti_linear_q4", dx, dp, ds, dy, T, N, K, 0)
+    got = ctx.download(dy, np.float32, T * N)
+    assert rel_err(got, ref) < TOL
+    for t in range(T):                                    # per token as well: no row leaks into another
+        assert rel_err(got[t * N:(t + 1) * N], ref[t * N:(t + 1) * N]) < TOL
+    y0 = rng.standard_normal(T * N).astype(np.float32)
+    ctx.write(dy, y0)
+    ctx.call("ti_linear_q4", dx, dp, ds, dy, T, N, K, 1)
+    assert rel_err(ctx.download(dy, np.float32, T * N), ref + y0) < TOL
+
+
 def test_shape_errors(ctx):
     d = ctx.zeros(4096)
     with pytest.raises(abi.TIError) as e:
