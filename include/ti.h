@@ -75,37 +75,37 @@ int ti_event_record(ti_ctx* ctx, int slot);                          /* slot in 
 int ti_event_elapsed_ms(ti_ctx* ctx, int start_slot, int end_slot, float* ms);
 
 /* ---- int4 weights ---------------------------------------------------------- */
-/* A1 quantizeInt4Bf16 (models/qwen3.js:3405-3426), run on the GPU, bit-exact. */
+/* quantizeInt4Bf16 (models/qwen3.js:3405-3426), run on the GPU, bit-exact. */
 int ti_quant_int4_bf16(ti_ctx* ctx, const uint16_t* w_bf16, uint32_t* pack, uint16_t* scales,
                        int N, int K);
 
 /* ---- activations ----------------------------------------------------------- */
-/* A2 quantQ8 (models/qwen3.js:414-420): per-32 int8 + per-16 sums. */
+/* quantQ8 (models/qwen3.js:414-420): per-32 int8 + per-16 sums. */
 int ti_quant_act_q8(ti_ctx* ctx, const float* x, uint32_t* xq, float* xs, int32_t* xsum, int K);
 /* QUANTQ8T (models/qwen3.js:1210-1231): T rows, per (token, group). */
 int ti_quant_act_q8_t(ti_ctx* ctx, const float* x, uint32_t* xq, float* xs, int T, int K);
-/* A6 rmsnormQ (models/qwen3.js:569-621): fused RMSNorm + int8 quant. */
+/* rmsnormQ (models/qwen3.js:569-621): fused RMSNorm + int8 quant. */
 int ti_rmsnorm_q8(ti_ctx* ctx, const float* x, const uint16_t* w, uint32_t* xq, float* xs,
                   int32_t* xsum, int H, float eps);
 /* rmsnorm (models/qwen3.js:60-88), y[T,H]. */
 int ti_rmsnorm(ti_ctx* ctx, const float* x, const uint16_t* w, float* y, int T, int H, float eps);
 
 /* ---- GEMV (batch 1) --------------------------------------------------------- */
-/* A3 gemvDP4_only (models/qwen3.js:422-427): y (+)= W·x over the int8 activation. */
+/* gemvDP4_only (models/qwen3.js:422-427): y (+)= W·x over the int8 activation. */
 int ti_gemv_q4_q8(ti_ctx* ctx, const uint32_t* xq, const float* xs, const uint32_t* pack,
                   const uint16_t* scales, float* y, int N, int K, int acc);
-/* A4 gemvQ (models/qwen3.js:314-321): f32 activation, used for N >= 16384 (lm_head). */
+/* gemvQ (models/qwen3.js:314-321): f32 activation, used for N >= 16384 (lm_head). */
 int ti_gemv_q4_f32(ti_ctx* ctx, const float* x, const uint32_t* pack, const uint16_t* scales,
                    float* y, int N, int K, int acc);
-/* A5 gateUpSiluDP4_only (models/qwen3.js:861-877): swi = silu(gate·x)*(up·x). */
+/* gateUpSiluDP4_only (models/qwen3.js:861-877): swi = silu(gate·x)*(up·x). */
 int ti_gateup_silu_q4(ti_ctx* ctx, const uint32_t* xq, const float* xs,
                       const uint32_t* gpack, const uint16_t* gsc,
                       const uint32_t* upack, const uint16_t* usc, float* swi, int I, int H);
-/* linearQ router (models/qwen3.js:1588-1608): T==1 and N<16384 -> quant + A3;
- * T==1 and N>=16384 -> A4; T>1 -> per-token quant + A11 GEMM. */
+/* linearQ router (models/qwen3.js:1588-1608): T==1 and N<16384 -> int8 quant +
+ * gemvDP4; T==1 and N>=16384 -> gemvQ; T>1 -> per-token quant + int8 MFMA GEMM. */
 int ti_linear_q4(ti_ctx* ctx, const float* x, const uint32_t* pack, const uint16_t* scales,
                  float* y, int T, int N, int K, int acc);
-/* Integer per-(row, group) dots of A3 (debug/parity: exact int32). */
+/* Integer per-(row, group) dots of gemvDP4 (debug/parity: exact int32). */
 int ti_group_dots_q4_q8(ti_ctx* ctx, const uint32_t* xq, const uint32_t* pack, int32_t* dots,
                         int N, int K);
 
@@ -138,14 +138,14 @@ int ti_argmax(ti_ctx* ctx, const float* logits, int N, uint32_t* tok_hist, int o
 int ti_embed(ti_ctx* ctx, const int32_t* ids, const uint16_t* emb, float* y, int T, int H, int id_off, int vocab);
 
 /* ---- attention over the int8 KV cache ------------------------------------------ */
-/* A7 attnPrepQ8 (models/qwen3.js:2297-2308): per-head RMSNorm(q,k) + split-half RoPE at
+/* attnPrepQ8 (models/qwen3.js:2297-2308): per-head RMSNorm(q,k) + split-half RoPE at
  * `pos`, q -> qr, k and v snorm-quantized into the cache row `pos` (kq/ks/vq/vs are the
  * layer's cache base pointers). Bit-exact KV codes. */
 int ti_attn_prep_q8(ti_ctx* ctx, const float* q, const float* k, const float* v,
                     const uint16_t* qn_w, const uint16_t* kn_w, float* qr,
                     uint32_t* kq, float* ks, uint32_t* vq, float* vs,
                     int nHq, int nKv, int hd, int pos, float theta, float eps);
-/* A8+A9 attnDecodeStreamQ8 (models/qwen3.js:2165-2173): split-KV decode attention over
+/* attnDecodeStreamQ8 (models/qwen3.js:2165-2173): split-KV decode attention over
  * S cached positions plus the log-sum-exp combine; out[nHq*hd]. nsplit = 0 picks the
  * split count; otherwise it is the reference's nsplitOverride (splits of ceil(S/nsplit),
  * trailing ones may be empty). */
@@ -172,7 +172,7 @@ int ti_kv_write_q8(ti_ctx* ctx, const float* kr, const float* v, uint32_t* kq, f
                    uint32_t* vq, float* vs, int T, int nKv, int hd, int pos);
 
 /* ---- ternary Q2_0_g64 ------------------------------------------------------------ */
-/* A12 gemv_tern (native/crates/n2-kernels/src/tern.rs:56-71; cpu/kernel/src/lib.rs:438-441):
+/* gemv_tern (native/crates/n2-kernels/src/tern.rs:56-71; cpu/kernel/src/lib.rs:438-441):
  * out[n] = sum_b s[n,b]*dot_b - sum_b s[n,b]*xsum[b], in units of 1/scale (the caller
  * multiplies by 1/scale, as the reference's callers do). K % 64 == 0. */
 int ti_tern_gemv(ti_ctx* ctx, float* out, const uint8_t* codes, const float* scales,
@@ -181,13 +181,46 @@ int ti_tern_gemv(ti_ctx* ctx, float* out, const uint8_t* codes, const float* sca
  * row b of the output starts at out + b*out_stride. */
 int ti_tern_gemm(ti_ctx* ctx, float* out, long out_stride, const uint8_t* codes, const float* scales,
                  const int8_t* act, const int32_t* xsum, int N, int K, int B);
-/* A13 quantize_act_into (tern.rs:206-222, mode 0) or WASM quantize (lib.rs:570-606,
+/* quantize_act_into (tern.rs:206-222, mode 0) or WASM quantize (lib.rs:570-606,
  * mode 1): per-tensor int8 activation + per-64 sums; the scale (127/amax for mode 0,
  * amax/127 for mode 1) is written to the device float scale_out. */
 int ti_quant_act_tern(ti_ctx* ctx, const float* x, int8_t* act, int32_t* xsum, float* scale_out,
                       int K, int mode);
-/* Exact int32 per-(row, block) code dots of A12 (debug/parity). */
+/* Exact int32 per-(row, block) code dots of gemv_tern (debug/parity). */
 int ti_tern_block_dots(ti_ctx* ctx, const uint8_t* codes, const int8_t* act, int32_t* dots, int N, int K);
+
+/* ---- int3 MoE experts (LFM2.5) ----------------------------------------------------
+ * int3 group of 32 weights: three u32 bitplanes (bit i of plane b = bit b of q3+4 for
+ * element i) and one f16 scale; the rows of all experts are stacked expert-major
+ * (row = e*N + n), p3 u32[nE*N*K/32*3], s3 f16[nE*N*K/32]. */
+/* _requant43 (models/lfm25.js:833-856): int4 codes -> int3 bitplanes, s3 =
+ * f32ToF16(s4*m/4) by the engine converter (engine/webgpu-engine.js:217-236); bit-exact
+ * with the JavaScript f64 arithmetic. rows*K/32 groups; pack4 16-byte aligned. */
+int ti_requant43(ti_ctx* ctx, const uint32_t* pack4, const uint16_t* sc4, int rows, int K,
+                 uint32_t* p3, uint16_t* s3);
+/* router / ROUTER_WGSL (models/lfm25.js:111-146): s = sigmoid(logit), top-k of s + bias
+ * (strict '>', lowest index wins a tie), wt = s/(sum + 1e-6). bias may be NULL (zero).
+ * logits f32[T*nE] -> idx i32[T*topk], wt f32[T*topk]; nE <= 256, topk <= 64. */
+int ti_router(ti_ctx* ctx, const float* logits, const float* bias, int T, int nE, int topk,
+              int32_t* idx, float* wt);
+/* idxGemv3 (models/lfm25.js:1924-1980): y[k*N+n] = sum_g s3 * sum_32 q3*x over expert
+ * idx[k]'s rows, x row k/xdiv of stride in_stride (f32); a pair whose id is outside
+ * [0, nE) writes nothing. K % 32 == 0, K <= 4096. */
+int ti_moe_gemv_q3(ti_ctx* ctx, const float* x, const uint32_t* p3, const uint16_t* s3,
+                   const int32_t* idx, float* y, int pairs, int N, int K, int in_stride,
+                   int xdiv, int nE);
+/* moeGemm3 (models/lfm25.js:1503-1647): src f32[src_rows*K] is quantized per 32-group to
+ * int8 (quantAct8, :1487-1494) into the context's scratch, then pair p (expert ridx[p],
+ * activation row p/src_div) gives y[p*N+n] = sum_g int32 dot * s_x * s_w. Pairs are
+ * grouped by expert inside the kernel; y stays in pair order. src_rows*K <= 2^24. */
+int ti_moe_gemm_q3(ti_ctx* ctx, const float* src, int src_rows, const uint32_t* p3,
+                   const uint16_t* s3, const int32_t* ridx, float* y, int P, int N, int K,
+                   int src_div, int nE);
+/* swiglu (models/lfm25.js:1831-1847): y[i] = g[i] / (1 + e^-g[i]) * u[i]. */
+int ti_swiglu(ti_ctx* ctx, const float* g, const float* u, float* y, long n);
+/* moeCombine / MOECOMBINE_WGSL (models/lfm25.js:1982-2000): x[t*H+h] += sum_k
+ * wt[t*K+k] * o[(t*K+k)*H+h]. */
+int ti_moe_combine(ti_ctx* ctx, float* x, const float* o, const float* wt, int H, int K, int T);
 
 /* ---- Qwen3 decoder ---------------------------------------------------------------
  * The model-level forward of models/qwen3.js (forward :3938-4069, loadModel layout

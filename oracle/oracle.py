@@ -107,7 +107,7 @@ def f16_array_to_f64(h):
     return np.asarray(h, dtype=np.uint16).view(np.float16).astype(np.float64)
 
 
-# ---- A1 ----------------------------------------------------------------------
+# ---- int4 group quantizer -----------------------------------------------------
 def quant_int4_bf16(w_bf16, N, K):
     w = _c(w_bf16, np.uint16)
     pack = np.zeros(N * K // 8, np.uint32)
@@ -116,7 +116,7 @@ def quant_int4_bf16(w_bf16, N, K):
     return pack, sc
 
 
-# ---- A2 / A6 -------------------------------------------------------------------
+# ---- int8 activation quant, fused RMSNorm + quant -----------------------------
 def quant_act_q8(x):
     x = _c(x, np.float32)
     K = x.size
@@ -154,7 +154,7 @@ def rmsnorm(x, w_f16, T, H, eps):
     return y
 
 
-# ---- A3/A4/A5/A11 ----------------------------------------------------------------
+# ---- int4 GEMV / GEMM oracles --------------------------------------------------
 def group_dots_q4_q8(xq, pack, N, K):
     d = np.zeros(N * (K // 32), np.int32)
     _L.or_group_dots_q4_q8(_ptr(_c(xq, np.uint32)), _ptr(_c(pack, np.uint32)), N, K, _ptr(d))

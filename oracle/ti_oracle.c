@@ -94,7 +94,7 @@ static int32_t js_toint32(double x) {
 }
 
 /* ------------------------------------------------------------------------- */
-/* A1: int4 group quantizer, models/qwen3.js:3405-3426 (= lfm25.js:454-477)  */
+/* int4 group quantizer, models/qwen3.js:3405-3426 (= lfm25.js:454-477)  */
 /* ------------------------------------------------------------------------- */
 void or_quant_int4_bf16(const uint16_t* w, int N, int K, uint32_t* pack, uint16_t* scales) {
     const int G = 32, wpr = K / 8, gpr = K / G;
@@ -124,7 +124,7 @@ void or_quant_int4_bf16(const uint16_t* w, int N, int K, uint32_t* pack, uint16_
 }
 
 /* ------------------------------------------------------------------------- */
-/* A2: per-32 int8 activation quant, models/qwen3.js:332-358                  */
+/* per-32 int8 activation quant, models/qwen3.js:332-358                  */
 /* scale = absmax/127 (f32), inv = 1/scale (0 if scale == 0),                */
 /* q = clamp(round_even(v*inv), -127, 127); xsum per 16.                      */
 /* ------------------------------------------------------------------------- */
@@ -166,7 +166,7 @@ void or_quant_act_q8_t(const float* x, int T, int K, uint32_t* xq, float* xs) {
 }
 
 /* ------------------------------------------------------------------------- */
-/* A6: fused RMSNorm + int8 quant, models/qwen3.js:569-612                    */
+/* fused RMSNorm + int8 quant, models/qwen3.js:569-612                    */
 /* sum of squares: 256 strided per-thread partials (s = s + v*v, two          */
 /* roundings), then the 128..1 tree; inv = 1/sqrt(sum/H + eps) with IEEE     */
 /* sqrt and division (the browser's inverseSqrt is only specified to 2 ULP;  */
@@ -210,7 +210,7 @@ void or_rmsnorm(const float* x, const uint16_t* w, int T, int H, float eps, floa
 }
 
 /* ------------------------------------------------------------------------- */
-/* A3/A4/A5: GEMV oracles in f64 from the quantized operands                  */
+/* GEMV oracles in f64 from the quantized operands                  */
 /* ------------------------------------------------------------------------- */
 static inline int nib_at(const uint32_t* rowp, int k) { return (int)((rowp[k >> 3] >> (4 * (k & 7))) & 0xFu) - 8; }
 static inline int i8_at(const uint32_t* xq, int k) { return (int)(int8_t)((xq[k >> 2] >> (8 * (k & 3))) & 0xFFu); }
@@ -313,7 +313,7 @@ double or_snorm_dequant(uint32_t word, int byte, float scale) {
 }
 
 /* ------------------------------------------------------------------------- */
-/* A7: QK RMSNorm + split-half RoPE + KV write, models/qwen3.js:2228-2296     */
+/* QK RMSNorm + split-half RoPE + KV write, models/qwen3.js:2228-2296     */
 /* RMSNorm over hd: thread j holds x_j^2, tree from 64 down (128 threads).    */
 /* RoPE angle: the reference evaluates pos*pow(theta,-2i/hd) and sin/cos in   */
 /* f32 WGSL builtins (accurate only on [-pi,pi]); this build evaluates the    */
@@ -361,7 +361,7 @@ void or_attn_prep_q8(const float* q, const float* k, const float* v,
 }
 
 /* ------------------------------------------------------------------------- */
-/* A8+A9: decode attention, models/qwen3.js:2077-2164 + 2048-2068.           */
+/* decode attention, models/qwen3.js:2077-2164 + 2048-2068.           */
 /* The split-KV online softmax with an exact LSE merge equals one softmax    */
 /* over all S keys; the oracle evaluates that directly in f64.               */
 /* ------------------------------------------------------------------------- */
@@ -427,7 +427,7 @@ int or_argmax(const float* logits, int N) {
 }
 
 /* ------------------------------------------------------------------------- */
-/* A12/A13 ternary, native/crates/n2-kernels/src/tern.rs                      */
+/* ternary, native/crates/n2-kernels/src/tern.rs                      */
 /* ------------------------------------------------------------------------- */
 #define TG 64
 #define TBPB 16
@@ -560,7 +560,7 @@ void or_n2_fixture(int N, int K, uint64_t seed, uint8_t* codes, float* scales,
 }
 
 /* ------------------------------------------------------------------------- */
-/* A14-A16 int3 MoE, models/lfm25.js                                          */
+/* int3 MoE, models/lfm25.js                                          */
 /* ------------------------------------------------------------------------- */
 
 /* lfm25.js:833-856: int4 -> int3 cascade requant into three bitplanes. */

@@ -45,22 +45,22 @@ uint16_t or_f32_to_f16_eng(float v);  /* engine/webgpu-engine.js:217-236 (+0x100
 double   or_f16_to_f32(uint16_t h);   /* models/qwen3.js:3397-3400 (exact)               */
 float    or_bf16_to_f32(uint16_t b);  /* models/qwen3.js:3409 (u16 << 16)                */
 
-/* ---- A1: int4 group quantizer (models/qwen3.js:3405-3426) ---------------- */
+/* ---- int4 group quantizer (models/qwen3.js:3405-3426) ---------------- */
 void or_quant_int4_bf16(const uint16_t* w_bf16, int N, int K,
                         uint32_t* pack, uint16_t* scales);
 
-/* ---- A2: per-32 int8 activation quant (models/qwen3.js:332-358) ---------- */
+/* ---- per-32 int8 activation quant (models/qwen3.js:332-358) ---------- */
 void or_quant_act_q8(const float* x, int K, uint32_t* xq, float* xs, int32_t* xsum);
 /* batched variant, per (token, group) (models/qwen3.js:1210-1231) */
 void or_quant_act_q8_t(const float* x, int T, int K, uint32_t* xq, float* xs);
 
-/* ---- A6: fused RMSNorm + int8 quant (models/qwen3.js:569-612) ------------ */
+/* ---- fused RMSNorm + int8 quant (models/qwen3.js:569-612) ------------ */
 void or_rmsnorm_q8(const float* x, const uint16_t* w_f16, int H, float eps,
                    uint32_t* xq, float* xs, int32_t* xsum);
 /* plain RMSNorm (models/qwen3.js:60-80), y[T,H] */
 void or_rmsnorm(const float* x, const uint16_t* w_f16, int T, int H, float eps, float* y);
 
-/* ---- A3/A4/A5 GEMV oracles (f64 of quantized operands) -------------------- */
+/* ---- GEMV oracles (f64 of quantized operands) -------------------- */
 /* integer per-(row, group) dots: dots[n*(K/32)+g] = sum (nib-8)*q_x  (exact) */
 void or_group_dots_q4_q8(const uint32_t* xq, const uint32_t* pack, int N, int K, int32_t* dots);
 void or_gemv_q4_q8(const uint32_t* xq, const float* xs, const uint32_t* pack,
@@ -71,7 +71,7 @@ void or_gateup_silu_q4(const uint32_t* xq, const float* xs,
                        const uint32_t* gpack, const uint16_t* gsc,
                        const uint32_t* upack, const uint16_t* usc,
                        int I, int H, double* swi);                             /* models/qwen3.js:679-728 */
-/* A11 batched: Y[T,N] from per-token int8 acts (models/qwen3.js:1326-1388) */
+/* batched: Y[T,N] from per-token int8 acts (models/qwen3.js:1326-1388) */
 void or_gemm_q4_q8(const uint32_t* xq, const float* xs, const uint32_t* pack,
                    const uint16_t* scales, int T, int N, int K, double* y);
 
@@ -80,7 +80,7 @@ void or_gemm_q4_q8(const uint32_t* xq, const float* xs, const uint32_t* pack,
 void or_kv_quant(const float* x, int n, uint32_t* q, float* s);
 double or_snorm_dequant(uint32_t word, int byte, float scale);
 
-/* ---- A7: fused QK-norm + RoPE + KV write (models/qwen3.js:2228-2296) ------ */
+/* ---- fused QK-norm + RoPE + KV write (models/qwen3.js:2228-2296) ------ */
 /* qr[nHq*hd]; kq/vq: the position's nKv*hd/4 words; ks/vs: nKv*hd/32 scales */
 void or_attn_prep_q8(const float* q, const float* k, const float* v,
                      const uint16_t* qw, const uint16_t* kw,
@@ -90,12 +90,12 @@ void or_attn_prep_q8(const float* q, const float* k, const float* v,
 void or_rope_norm_row(const float* x, const uint16_t* w, int hd, int pos,
                       float theta, float eps, int apply_norm, float* out);
 
-/* ---- A8+A9: decode attention over the int8 KV, f64 softmax ---------------- */
+/* ---- decode attention over the int8 KV, f64 softmax ---------------- */
 /* KV layout per position: [nKv][hd] int8 (hd/4 words per head), scales [nKv][hd/32] */
 void or_attn_decode_q8(const float* qr, const uint32_t* kq, const float* ks,
                        const uint32_t* vq, const float* vs,
                        int S, int nHq, int nKv, int hd, double* out);
-/* causal T-token variant (A11 attention): query t attends keys [0, pos0+t] */
+/* causal T-token variant (batched forward attention): query t attends keys [0, pos0+t] */
 void or_attn_causal_q8(const float* qr, const uint32_t* kq, const float* ks,
                        const uint32_t* vq, const float* vs,
                        int T, int pos0, int nHq, int nKv, int hd, double* out);
@@ -104,7 +104,7 @@ void or_attn_causal_q8(const float* qr, const uint32_t* kq, const float* ks,
 void or_embed(const int32_t* ids, const uint16_t* emb_f16, int T, int H, float* y);
 int  or_argmax(const float* logits, int N);   /* lowest index wins ties */
 
-/* ---- A12/A13 ternary (native/crates/n2-kernels/src/tern.rs) --------------- */
+/* ---- ternary (native/crates/n2-kernels/src/tern.rs) --------------- */
 void or_tern_pack(const float* w, int N, int K, uint8_t* codes, float* scales); /* tern.rs:131-160 */
 float or_tern_quant_act_n2(const float* x, int K, int8_t* act, int32_t* xsum);  /* tern.rs:206-222 */
 float or_tern_quant_act_wasm(const float* x, int K, int8_t* act, int32_t* xsum);/* lib.rs:570-606 */
@@ -126,7 +126,7 @@ void or_tern_gemv_avx2(const uint8_t* codes, const float* scales, const int8_t* 
 void or_tern_gemv_avx2_mt(const uint8_t* codes, const float* scales, const int8_t* act,
                           const int32_t* xsum, int N, int K, float* out, int nthreads);
 
-/* ---- A14-A16 int3 MoE (models/lfm25.js) ----------------------------------- */
+/* ---- int3 MoE (models/lfm25.js) ----------------------------------- */
 void or_requant43(const uint32_t* pack4, const uint16_t* sc4, int rows, int K,
                   uint32_t* p3, uint16_t* s3);                                  /* lfm25.js:833-856 */
 void or_router(const float* logits, const float* bias, int T, int nE, int topk,

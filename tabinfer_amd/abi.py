@@ -68,6 +68,12 @@ SIGS = {
     "ti_tern_gemm": [_p, _p, C.c_long, _p, _p, _p, _p, _i, _i, _i],
     "ti_quant_act_tern": [_p, _p, _p, _p, _p, _i, _i],
     "ti_tern_block_dots": [_p, _p, _p, _p, _i, _i],
+    "ti_requant43": [_p, _p, _p, _i, _i, _p, _p],
+    "ti_router": [_p, _p, _p, _i, _i, _i, _p, _p],
+    "ti_moe_gemv_q3": [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i],
+    "ti_moe_gemm_q3": [_p, _p, _i, _p, _p, _p, _p, _i, _i, _i, _i, _i],
+    "ti_swiglu": [_p, _p, _p, _p, C.c_long],
+    "ti_moe_combine": [_p, _p, _p, _p, _i, _i, _i],
     "ti_qwen3_create": [_p, _p, C.POINTER(_p)],
     "ti_qwen3_destroy": [_p, _p],
     "ti_qwen3_tensor": [_p, C.c_char_p, C.POINTER(_p), C.POINTER(_sz), C.POINTER(_p), C.POINTER(_sz)],

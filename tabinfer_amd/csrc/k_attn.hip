@@ -1,9 +1,9 @@
 // k_attn.hip — int8-KV attention of the decode path:
-//  A7 fused QK-RMSNorm + RoPE + int8 KV write   attnPrepQ8     models/qwen3.js:2228-2308
+//  fused QK-RMSNorm + RoPE + int8 KV write   attnPrepQ8     models/qwen3.js:2228-2308
 //     RMSNorm + RoPE for T tokens               ropeQK         models/qwen3.js:1700-1760
 //     int8 KV write for T tokens                kvQuantWrite   models/qwen3.js:2180-2216
-//  A8 split-KV decode attention (partials)      attnDecStreamQ8 models/qwen3.js:2077-2173
-//  A9 log-sum-exp combine                        ATTN_DEC_COMBINE models/qwen3.js:2048-2068
+//  split-KV decode attention (partials)      attnDecStreamQ8 models/qwen3.js:2077-2173
+//  log-sum-exp combine                        ATTN_DEC_COMBINE models/qwen3.js:2048-2068
 //
 // KV layout is the reference's: per layer, position-major, then head, then dim;
 // int8 codes packed 4 per u32 (snorm: code/127 * group max), one f32 scale per
@@ -100,7 +100,7 @@ __device__ float rope_norm_tab(float x, int j, int hd, const uint16_t* __restric
     return out;
 }
 
-// A7: workgroup roles [0,nHq) q-head rope+norm -> qr ; [nHq, nHq+nKv) k-head
+// workgroup roles [0,nHq) q-head rope+norm -> qr ; [nHq, nHq+nKv) k-head
 // rope+norm+quantize into the cache ; [nHq+nKv, nHq+2nKv) v-head quantize.
 __global__ __launch_bounds__(128) void k_attn_prep_q8(const float* __restrict__ q, const float* __restrict__ k,
                                                       const float* __restrict__ v, const uint16_t* __restrict__ qw,
@@ -170,7 +170,7 @@ __global__ void k_kv_write_q8(const float* __restrict__ kr, const float* __restr
 }
 
 // ---------------------------------------------------------------------------
-// A8: split-KV decode attention. Workgroup (256 threads) = (kv head hk, split).
+// split-KV decode attention. Workgroup (256 threads) = (kv head hk, split).
 // All G = nHq/nKv query heads of the group are served from one read of K/V.
 // Token rows are read 16 bytes per lane, LPT = hd/16 lanes per row, so one pass
 // covers 256/LPT tokens; a split is walked in tiles of TILE tokens: scores for
@@ -349,7 +349,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split_q8(const float* __re
     }
 }
 
-// A9: O = sum_i o_i e^(m_i-M) / sum_i l_i e^(m_i-M); an empty split carries
+// O = sum_i o_i e^(m_i-M) / sum_i l_i e^(m_i-M); an empty split carries
 // (m = -3e38, l = 0, o = 0) and contributes nothing.
 __global__ void k_attn_combine(const float* __restrict__ po, const float* __restrict__ pml, float* __restrict__ out,
                                int nsplit, int hd, int ns_stride, int per, const int* __restrict__ dpos) {

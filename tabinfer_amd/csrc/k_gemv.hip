@@ -1,7 +1,7 @@
 // k_gemv.hip — batch-1 int4 GEMVs (HBM-bound; no MFMA):
-//  A3 int4 x int8      gemvDP4_only        models/qwen3.js:359-427
-//  A4 int4 x f32       gemvQ               models/qwen3.js:276-321
-//  A5 gate+up+SiLU     gateUpSiluDP4_only  models/qwen3.js:679-728, 861-877
+//  int4 x int8      gemvDP4_only        models/qwen3.js:359-427
+//  int4 x f32       gemvQ               models/qwen3.js:276-321
+//  gate+up+SiLU     gateUpSiluDP4_only  models/qwen3.js:679-728, 861-877
 //
 // Mapping (per 64-lane wavefront): a row of K weights is gpr = K/32 groups of
 // 16 bytes (32 nibbles + one f16 scale). LPR lanes share a row and each lane
@@ -21,7 +21,7 @@ namespace {
 
 
 // ---------------------------------------------------------------------------
-// A3: y (+)= W x, int8 activation
+// y (+)= W x, int8 activation
 // ---------------------------------------------------------------------------
 template <int LPR, int GPL, int R>
 __global__ __launch_bounds__(256) void k_gemv_q4_q8(const uint32_t* __restrict__ xq, const float* __restrict__ xs,
@@ -109,7 +109,7 @@ __global__ __launch_bounds__(256) void k_gemv_q4_q8_generic(const uint32_t* __re
 }
 
 // ---------------------------------------------------------------------------
-// A5: swi = silu(gate x) * (up x)
+// swi = silu(gate x) * (up x)
 // ---------------------------------------------------------------------------
 template <int LPR, int GPL, int R>
 __global__ __launch_bounds__(256) void k_gateup_q4_q8(const uint32_t* __restrict__ xq, const float* __restrict__ xs,

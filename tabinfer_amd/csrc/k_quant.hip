@@ -1,14 +1,14 @@
 // k_quant.hip — quantizers of the decode path (all integer outputs bit-exact):
-//  A1 int4 weight quantizer     models/qwen3.js:3405-3426 (JS f64 semantics)
-//  A2 per-32 int8 activation    models/qwen3.js:332-358, 1210-1231
-//  A6 fused RMSNorm + int8      models/qwen3.js:569-612
+//  int4 weight quantizer     models/qwen3.js:3405-3426 (JS f64 semantics)
+//  per-32 int8 activation    models/qwen3.js:332-358, 1210-1231
+//  fused RMSNorm + int8      models/qwen3.js:569-612
 //     plain RMSNorm             models/qwen3.js:60-80
 // Built with -ffp-contract=off: every f32/f64 expression rounds once per
 // operation in the written order, which is what makes these bit-exact.
 #include "ti_dev.h"
 
 // ---------------------------------------------------------------------------
-// A1: one thread per (row, 32-group). The reference runs this in JavaScript at
+// one thread per (row, 32-group). The reference runs this in JavaScript at
 // load time, so the arithmetic is f64 (JS numbers), with its own f32->f16
 // rounding (ties away from zero) and Math.round (ties toward +inf).
 // ---------------------------------------------------------------------------

@@ -1,7 +1,7 @@
 // k_tern.hip — ternary (Q2_0_g64) GEMV and its activation quantizer:
-//  A12 gemv_tern       native/crates/n2-kernels/src/tern.rs:56-119, 246-338;
+//  gemv_tern       native/crates/n2-kernels/src/tern.rs:56-119, 246-338;
 //                      cpu/kernel/src/lib.rs:438-544 (B=1) and :331-432 (B=4 batched)
-//  A13 quantize_act    tern.rs:196-222 (n2: 127/amax, round half away from zero)
+//  quantize_act    tern.rs:196-222 (n2: 127/amax, round half away from zero)
 //      quantize        cpu/kernel/src/lib.rs:570-606 (WASM: amax/127, nearest-even)
 //
 // out[n] = sum_b s[n,b]*dot_b - sum_b s[n,b]*xsum[b], dot_b = sum code*act over the
@@ -141,7 +141,7 @@ __global__ void k_tern_block_dots(const uint4* __restrict__ codes, const int8_t*
 }
 
 // ---------------------------------------------------------------------------
-// A13: per-tensor int8 activation quant + per-64 sums, one 1024-thread workgroup.
+// per-tensor int8 activation quant + per-64 sums, one 1024-thread workgroup.
 // mode 0 (n2): scale = 127/amax (1 if amax == 0), a = clamp(round-half-away(x*scale))
 // mode 1 (WASM): asc = amax/127 (1e-9 if 0), a = clamp(nearest-even(x*(1/asc)))
 // The max is order-independent, so the codes are bit-exact.

@@ -96,7 +96,7 @@ __device__ __forceinline__ float transpose_reduce(float (&v)[R], int li) {
 }
 
 // ---------------------------------------------------------------------------
-// A4: y (+)= W x, f32 activation (lm_head path). Per element: one byte->f32
+// y (+)= W x, f32 activation (lm_head path). Per element: one byte->f32
 // convert and one FMA on the unsigned nibble; the -8 offset is removed once per
 // group (sum n*x - 8*sum x).
 // ---------------------------------------------------------------------------
@@ -208,7 +208,7 @@ __device__ __forceinline__ float group_dot_limbs(const uint4 w, const ActLimb& a
 }
 
 // ---------------------------------------------------------------------------
-// A2: one thread per 32-group. scale = absmax/127, inv = 1/scale (0 if the
+// one thread per 32-group. scale = absmax/127, inv = 1/scale (0 if the
 // group is zero), q = clamp(round-half-even(v*inv), -127, 127); the per-16
 // sums feed the ternary identity.
 // ---------------------------------------------------------------------------
@@ -254,7 +254,7 @@ __device__ __forceinline__ void load32(const float* __restrict__ src, float* v) 
 }
 
 // ---------------------------------------------------------------------------
-// A6 / RMSNorm: one 256-thread workgroup per row. The sum of squares uses the
+// RMSNorm: one 256-thread workgroup per row. The sum of squares uses the
 // reference's order — 256 strided per-thread partials then a 128..1 tree —
 // so the normalized values, and hence the int8 codes, are reproducible.
 // inv = 1/sqrt(sum/H + eps) with IEEE division and square root.

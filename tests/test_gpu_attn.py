@@ -1,7 +1,7 @@
 """GPU parity for the int8-KV attention rows.
 
-A7 attnPrep / ropeQK / kvQuantWrite: KV codes, KV scales and RoPE'd rows are
-bit-exact against the oracle. A8+A9 split-KV decode attention: max relative
+attnPrep / ropeQK / kvQuantWrite: KV codes, KV scales and RoPE'd rows are
+bit-exact against the oracle. Split-KV decode attention: max relative
 error <= 1e-3 (normwise) against the oracle's f64 softmax over the dequantized
 cache, on the reference's own fixtures (models/qwen3.js:2901-2937: uneven and
 empty splits) and at Qwen3 geometry for 4k and 32k contexts.

@@ -1,5 +1,5 @@
-"""GPU parity: int4 quantizer (A1), int8 activation quant (A2), fused
-RMSNorm+quant (A6) bit-exact against the oracle; int4 GEMVs (A3/A4/A5) with
+"""GPU parity: int4 quantizer, int8 activation quant, fused
+RMSNorm+quant bit-exact against the oracle; int4 GEMVs with
 exact per-group integer dots and float outputs within max relative error 1e-3
 (normwise, f64 oracle of the quantized operands — models/qwen3.js:3104)."""
 import numpy as np

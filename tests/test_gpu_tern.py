@@ -1,4 +1,4 @@
-"""GPU parity for the ternary Q2_0_g64 rows (A12/A13).
+"""GPU parity for the ternary Q2_0_g64 rows.
 
 Block dots and the activation quantizer are bit-exact, and so is the float
 output: the kernel replays each row's f32 accumulation in the reference's block

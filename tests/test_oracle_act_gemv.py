@@ -1,5 +1,5 @@
-"""Pins for the oracle's int8 activation quant (A2), fused RMSNorm+quant (A6) and
-the int4 GEMV oracles (A3/A4/A5/A11).
+"""Pins for the oracle's int8 activation quant, fused RMSNorm+quant and
+the int4 GEMV oracles.
 
 Independent checks: invariants of the per-32 absmax quantizer
 (models/qwen3.js:343-357), the ties-to-even known answer that distinguishes

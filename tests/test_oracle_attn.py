@@ -1,5 +1,5 @@
-"""Pins for the oracle's int8 KV quantizer, RoPE/QK-norm prep (A7) and decode
-attention (A8/A9).
+"""Pins for the oracle's int8 KV quantizer, RoPE/QK-norm prep and decode
+attention.
 
 Independent checks: the n2 RoPE known-answer tests
 (native/crates/n2-core/src/ops.rs:169-214), pair-norm preservation of a

@@ -1,4 +1,4 @@
-"""Pins for the oracle's f16 converters and the int4 quantizer (A1).
+"""Pins for the oracle's f16 converters and the int4 quantizer.
 
 Independent checks: the reference's own f16 known-answer tests
 (native/crates/n2-core/src/binfmt.rs:406-422), numpy's float16 cast (an

@@ -1,4 +1,4 @@
-"""Pins for the ternary oracle (A12/A13) and the int3 MoE oracle (A14-A16).
+"""Pins for the ternary oracle and the int3 MoE oracle.
 
 Ternary: the reference's own unit tests, reproduced with their generators,
 shapes and seeds (native/crates/n2-kernels/src/tern.rs:351-470) and the
