@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the quantized decode hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only gemv]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only gemv|moe|all]
 
 Headline workload (`value`): the int4 GEMV set of one Qwen3-0.6B batch-1 decode
 step (hidden 1024, intermediate 3072, 16/8 heads of dim 128, 28 layers, vocab
@@ -21,6 +21,9 @@ Beside it, each bounded to a few seconds (not `value`):
                 prefix contexts: tokens/s and whole-step GB/s
   attention     fused split-KV attention per layer at 4k and 32k (GB/s)
   ternary       Bonsai-1.7B ternary GEMV set of one layer (GB/s)
+  moe           LFM2.5-8B-A1B int3 MoE block (router, 32 experts top-4, hidden 2048,
+                expert intermediate 1792) at batch 1 and 16: us per block, GB/s of
+                the distinct experts' weights
   cpu_baseline  the oracle's int4 GEMV (C, 1 thread) on a bounded sample of the
                 same GEMV set; cpu_tern_avx2: the n2 AVX2 ternary GEMV restated in C
 """
@@ -408,6 +411,77 @@ def ternary(ctx, flush, reps=8):
             "GB_s": round(per_layer / (us_layer * 1e-6) / 1e9, 1), "launches_per_layer": len(shapes)}
 
 
+# ---- LFM2.5-8B-A1B int3 MoE experts ------------------------------------------------------------
+def int3_bytes(N, K):
+    return N * K // 32 * 14          # three u32 bitplanes + one f16 scale per 32 weights
+
+
+def moe(ctx, flush, reps=8, layers=2):
+    """One MoE block (router -> w1/w3 -> swiglu -> w2 -> combine, models/lfm25.js:2145-2166)
+    at batch 1 (pair-indexed int3 GEMV) and batch 16 (expert-grouped GEMM), cycling
+    through `layers` independent expert sets so that each launch reads cold weights."""
+    H, I, nE, K = 2048, 1792, 32, 4
+    rng = np.random.default_rng(5)
+    wsets = []
+    for _ in range(layers):
+        lw = []
+        for N, Kc in ((I, H), (I, H), (H, I)):
+            rows = nE * N
+            ng = rows * Kc // 32
+            p3 = ctx.upload(rng.integers(0, 2 ** 32, ng * 3, dtype=np.uint64).astype(np.uint32))
+            s3 = ctx.upload(rng.uniform(0.005, 0.02, ng).astype(np.float16).view(np.uint16))
+            lw.append((p3, s3))
+        wsets.append(lw)
+    out = {}
+    for T in (1, 16):
+        P = T * K
+        logits = rng.standard_normal(T * nE).astype(np.float32)
+        idx = np.zeros(P, np.int32)
+        # distinct experts this routing touches (the bytes a launch must read)
+        s = 1.0 / (1.0 + np.exp(-logits.reshape(T, nE)))
+        for t in range(T):
+            idx[t * K:(t + 1) * K] = np.argsort(-s[t], kind="stable")[:K]
+        ne = len(set(idx.tolist()))
+        b = dict(normed=ctx.upload(rng.standard_normal(T * H).astype(np.float32)), logits=ctx.upload(logits),
+                 bias=ctx.upload(np.zeros(nE, np.float32)), x=ctx.upload(rng.standard_normal(T * H).astype(np.float32)),
+                 idx=ctx.zeros(P * 4), wt=ctx.zeros(P * 4), gate=ctx.zeros(P * I * 4), up=ctx.zeros(P * I * 4),
+                 act=ctx.zeros(P * I * 4), out=ctx.zeros(P * H * 4))
+
+        def issue(lw, T=T, P=P, b=b):
+            (p1, s1), (p3_, s3_), (p2, s2) = lw
+            ctx.call("ti_router", b["logits"], b["bias"], T, nE, K, b["idx"], b["wt"])
+            if T == 1:
+                ctx.call("ti_moe_gemv_q3", b["normed"], p1, s1, b["idx"], b["gate"], P, I, H, H, K, nE)
+                ctx.call("ti_moe_gemv_q3", b["normed"], p3_, s3_, b["idx"], b["up"], P, I, H, H, K, nE)
+                ctx.call("ti_swiglu", b["gate"], b["up"], b["act"], P * I)
+                ctx.call("ti_moe_gemv_q3", b["act"], p2, s2, b["idx"], b["out"], P, H, I, I, 1, nE)
+            else:
+                ctx.call("ti_moe_gemm_q3", b["normed"], T, p1, s1, b["idx"], b["gate"], P, I, H, K, nE)
+                ctx.call("ti_moe_gemm_q3", b["normed"], T, p3_, s3_, b["idx"], b["up"], P, I, H, K, nE)
+                ctx.call("ti_swiglu", b["gate"], b["up"], b["act"], P * I)
+                ctx.call("ti_moe_gemm_q3", b["act"], P, p2, s2, b["idx"], b["out"], P, H, I, 1, nE)
+            ctx.call("ti_moe_combine", b["x"], b["out"], b["wt"], H, K, T)
+
+        gs = [graph_of(ctx, lambda lw=lw: issue(lw)) for lw in wsets]
+        time_graphs(ctx, gs, 2)
+        ms = cold_ms(ctx, gs, reps, flush)
+        wbytes = ne * (2 * int3_bytes(I, H) + int3_bytes(H, I))
+        us = ms * 1e3
+        out["batch%d" % T] = {"block_us": round(us, 2), "distinct_experts": ne, "weight_bytes": wbytes,
+                              "GB_s": round(wbytes / (us * 1e-6) / 1e9, 1),
+                              "pct_of_hbm_peak": round(100 * wbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 2),
+                              "launches": 6}
+        for g in gs:
+            ctx.graph_destroy(g)
+        for v in b.values():
+            v.free()
+    for lw in wsets:
+        for p3, s3 in lw:
+            p3.free()
+            s3.free()
+    return out
+
+
 # ---- CPU baselines ------------------------------------------------------------------------------
 def cpu_baseline(cfg, budget_s=12.0):
     """The oracle's int4 GEMV (a C port of the reference arithmetic, 1 thread) on a
@@ -480,7 +554,8 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
-    ap.add_argument("--only", choices=("gemv", "all"), default="all", help="gemv: the headline workload only")
+    ap.add_argument("--only", choices=("gemv", "all", "moe"), default="all",
+                    help="gemv: the headline workload only; moe: headline + the int3 MoE leg")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one MI355X: this build runs on a single GPU (the multi-GPU sharding is a "
@@ -534,9 +609,14 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic},
         "kernels": fams,
     }
+    if args.only == "moe":
+        log("int3 MoE")
+        out["moe_lfm25_block"] = moe(ctx, flush)
     if args.only == "all":
         log("ternary")
         out["ternary_bonsai_layer"] = ternary(ctx, flush)
+        log("int3 MoE")
+        out["moe_lfm25_block"] = moe(ctx, flush)
         log("attention")
         out["attention_layer"] = attention(ctx, flush)
         log("decode 1.7B")

@@ -231,7 +231,8 @@ typedef struct {
     int layers, hidden, intermediate, n_heads, n_kv_heads, head_dim, vocab;
     float rope_theta, rms_eps;
     int max_ctx;      /* KV capacity in positions */
-    int max_tokens;   /* largest T accepted by ti_qwen3_forward */
+    int max_tokens;   /* largest T accepted by ti_qwen3_forward; <= 256 and max_tokens *
+                         n_heads <= 512 (the T-query attention's scratch) */
 } ti_qwen3_config;
 int ti_qwen3_create(ti_ctx* ctx, const ti_qwen3_config* cfg, ti_qwen3** out);
 int ti_qwen3_destroy(ti_ctx* ctx, ti_qwen3* m);

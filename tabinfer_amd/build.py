@@ -1,4 +1,5 @@
-"""Build libtabinfer.so (gfx950) from tabinfer_amd/csrc with hipcc, in-tree.
+"""Build libtabinfer.so (gfx950) from tabinfer_amd/csrc with hipcc, in-tree, and the
+Node.js addon tabinfer_amd/host/tabinfer.node over it (when Node's headers are present).
 
     python -m tabinfer_amd.build [--force]
 
@@ -52,6 +53,30 @@ def _compile(src, force):
     return obj
 
 
+NODE_INCLUDE = "/usr/include/node"
+ADDON_SRC = os.path.join(HERE, "host", "ti_node.cc")
+ADDON = os.path.join(HERE, "host", "tabinfer.node")
+
+
+def build_addon(force=False):
+    """g++ the N-API addon (plain C ABI of libtabinfer, no HIP code) next to its JS
+    modules; it finds libtabinfer.so through an $ORIGIN-relative rpath."""
+    if not os.path.exists(os.path.join(NODE_INCLUDE, "node_api.h")):
+        return None
+    deps = [ADDON_SRC, os.path.join(INCLUDE, "ti.h"), LIB]
+    if not force and os.path.exists(ADDON) and os.path.getmtime(ADDON) >= max(os.path.getmtime(d) for d in deps):
+        return ADDON
+    cxx = shutil.which("g++") or "g++"
+    cmd = [cxx, "-O2", "-std=c++17", "-shared", "-fPIC", "-Wall", "-Wextra", "-Wno-unused-parameter",
+           "-DNODE_GYP_MODULE_NAME=tabinfer", "-I", NODE_INCLUDE, "-I", INCLUDE, ADDON_SRC,
+           "-L", HERE, "-ltabinfer", "-Wl,-rpath,$ORIGIN/..", "-o", ADDON + ".tmp"]
+    r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("addon build failed:\n" + r.stdout)
+    os.replace(ADDON + ".tmp", ADDON)
+    return ADDON
+
+
 def build(force=False, jobs=None):
     os.makedirs(BUILD, exist_ok=True)
     srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
@@ -64,6 +89,7 @@ def build(force=False, jobs=None):
     if r.returncode != 0:
         raise RuntimeError("link failed:\n" + r.stdout)
     os.replace(tmp, LIB)
+    build_addon(force=True)
     return LIB
 
 

@@ -1,0 +1,430 @@
+'use strict';
+// qwen3-host.js — the Qwen3 decode API of TabInfer (models/qwen3.js, exported at
+// :5529-5534: forward, generate, runConversation, loadModel, ...) over the MI355X library.
+//
+// The model-level forward runs in the native decoder object (ti_qwen3_*): a T-token
+// forward for prefill chunks and a device-position decode step that reads nothing from
+// the host, captured once into a HIP graph and replayed per token (the reference's
+// GPU-resident token chaining, models/qwen3.js:3951-3959 and decodeLoop :4414-4435).
+//
+// Tokenization is not part of this path: loadModel({tokenizer}) takes an object with
+// encodeChat(messages) -> ids, decode(ids) -> string and isStop(id) -> bool (the
+// reference's TOK); without one, prompts are arrays of token ids and decode() returns them.
+const fs = require('fs');
+const { createEngine, bf16ToF16bits, f32ToF16 } = require('./ti-engine');
+
+// models/qwen3.js CONFIGS (Qwen3-0.6B / 1.7B geometry)
+const CONFIGS = {
+  '0.6B': { layers: 28, hidden: 1024, intermediate: 3072, n_heads: 16, n_kv_heads: 8, head_dim: 128, vocab: 151936 },
+  '1.7B': { layers: 28, hidden: 2048, intermediate: 6144, n_heads: 16, n_kv_heads: 8, head_dim: 128, vocab: 151936 },
+};
+const GEN_BATCH = 32;        // decode steps per readback (models/qwen3.js:4416)
+const PREFILL_CHUNK = 256;   // prefill tokens per forward (models/qwen3.js:5250) ...
+const ATTN_ROWS = 512;       // ... within the library's T * n_heads <= 512 (ti_qwen3_config)
+const STAGE_BYTES = 64 << 20;
+
+// ---- safetensors ----------------------------------------------------------------------------
+function readSafetensorsHeader(file) {
+  const fd = fs.openSync(file, 'r');
+  try {
+    const lenBuf = Buffer.alloc(8);
+    fs.readSync(fd, lenBuf, 0, 8, 0);
+    const n = Number(lenBuf.readBigUInt64LE(0));
+    if (n <= 0 || n > (100 << 20)) throw new Error('safetensors: bad header length ' + n + ' in ' + file);
+    const hb = Buffer.alloc(n);
+    fs.readSync(fd, hb, 0, n, 8);
+    const hdr = JSON.parse(hb.toString('utf8'));
+    const tensors = {};
+    for (const [name, info] of Object.entries(hdr)) {
+      if (name === '__metadata__') continue;
+      tensors[name] = { dtype: info.dtype, shape: info.shape, begin: 8 + n + info.data_offsets[0], end: 8 + n + info.data_offsets[1], file };
+    }
+    return tensors;
+  } finally {
+    fs.closeSync(fd);
+  }
+}
+
+function readRange(t, off, bytes) {
+  const fd = fs.openSync(t.file, 'r');
+  try {
+    const b = Buffer.alloc(bytes);
+    let got = 0;
+    while (got < bytes) {
+      const r = fs.readSync(fd, b, got, bytes - got, t.begin + off + got);
+      if (r <= 0) throw new Error('safetensors: short read in ' + t.file);
+      got += r;
+    }
+    return b;
+  } finally {
+    fs.closeSync(fd);
+  }
+}
+
+function toF16Bits(t, buf) {
+  const n = buf.length / (t.dtype === 'F32' ? 4 : 2);
+  if (t.dtype === 'BF16') return bf16ToF16bits(new Uint16Array(buf.buffer, buf.byteOffset, n));
+  if (t.dtype === 'F16') return new Uint16Array(buf.buffer.slice(buf.byteOffset, buf.byteOffset + buf.length));
+  if (t.dtype === 'F32') {
+    const f = new Float32Array(buf.buffer, buf.byteOffset, n), out = new Uint16Array(n);
+    for (let i = 0; i < n; i++) out[i] = f32ToF16(f[i]);
+    return out;
+  }
+  throw new Error('unsupported dtype ' + t.dtype);
+}
+
+// ---- the model ----------------------------------------------------------------------------------
+function createQwen3Host({ device = 0 } = {}) {
+  const eng = createEngine({ device });
+  const { E } = eng;
+  const TI = E.TI, ctx = E.ctx;
+  let M = null;          // native decoder
+  let C = null;          // its config
+  let TOK = null;
+  let _devPos = -1;      // the device-side position as this host last left it
+  let _decodeGraph = null;
+  let _cachedIds = null; // prefix cache: the ids whose KV rows are resident
+  let _toolRunner = null;
+  let _lastGenStats = null;
+
+  function tensorNames(cfg) {
+    const names = ['model.embed_tokens.weight', 'model.norm.weight', 'lm_head.weight'];
+    for (let l = 0; l < cfg.layers; l++) {
+      const p = 'model.layers.' + l + '.';
+      for (const n of ['self_attn.q_proj.weight', 'self_attn.k_proj.weight', 'self_attn.v_proj.weight', 'self_attn.o_proj.weight',
+        'mlp.gate_proj.weight', 'mlp.up_proj.weight', 'mlp.down_proj.weight', 'input_layernorm.weight',
+        'post_attention_layernorm.weight', 'self_attn.q_norm.weight', 'self_attn.k_norm.weight']) names.push(p + n);
+    }
+    return names;
+  }
+
+  // bf16 [N, K] rows from `readRows(row0, rows) -> Uint8Array` -> int4 pack/scales on the GPU
+  function quantizeInto(dst, N, K, readRows, stage) {
+    const rowsPer = Math.max(1, Math.min(N, Math.floor(STAGE_BYTES / (K * 2))));
+    for (let r = 0; r < N; r += rowsPer) {
+      const nr = Math.min(rowsPer, N - r);
+      E.writeBuffer(stage, 0, readRows(r, nr));
+      TI.quant_int4_bf16(ctx, stage, E.view(dst.data, r * K / 2), E.view(dst.scales, r * K / 32 * 2), nr, K);
+    }
+  }
+
+  function loadWeights(files, onProgress) {
+    const all = {};
+    for (const f of files) Object.assign(all, readSafetensorsHeader(f));
+    const names = tensorNames(C);
+    const stage = E.createBuffer(STAGE_BYTES);
+    try {
+      names.forEach((name, i) => {
+        let t = all[name];
+        if (!t && name === 'lm_head.weight') t = all['model.embed_tokens.weight'];   // tied embeddings
+        if (!t) throw new Error('loadModel: checkpoint has no tensor ' + name);
+        const dst = TI.qwen3_tensor(M, name);
+        if (dst.scales) {
+          if (t.dtype !== 'BF16') throw new Error('quant path expects BF16 for ' + name);   // models/qwen3.js:3502
+          const [N, K] = t.shape;
+          if (N * K / 2 !== dst.dataBytes) throw new Error('loadModel: ' + name + ' has shape ' + t.shape + ', the model expects ' + (dst.dataBytes * 2) + ' weights');
+          quantizeInto(dst, N, K, (r0, nr) => readRange(t, r0 * K * 2, nr * K * 2), stage);
+        } else {
+          const bits = toF16Bits(t, readRange(t, 0, t.end - t.begin));
+          if (bits.byteLength !== dst.dataBytes) throw new Error('loadModel: ' + name + ' size mismatch');
+          E.writeBuffer(dst.data, 0, bits);
+        }
+        if (onProgress) onProgress({ phase: 'parse', pct: Math.round(100 * (i + 1) / names.length) });
+      });
+      E.sync();
+    } finally {
+      E.destroy(stage);
+    }
+  }
+
+  // seeded synthetic weights: bf16 N(0, 0.02) projections quantized on the GPU, norms 1.0,
+  // f16 N(0, 1) embeddings (for benchmarks and smoke runs without a checkpoint)
+  function randomWeights(seed) {
+    let s = (seed >>> 0) || 1;
+    const rnd = () => { s ^= s << 13; s >>>= 0; s ^= s >>> 17; s ^= s << 5; s >>>= 0; return s / 4294967296; };
+    const gauss = () => Math.sqrt(-2 * Math.log(rnd() + 1e-12)) * Math.cos(2 * Math.PI * rnd());
+    const stage = E.createBuffer(STAGE_BYTES);
+    const f = new Float32Array(1), u = new Uint32Array(f.buffer);
+    try {
+      for (const name of tensorNames(C)) {
+        const dst = TI.qwen3_tensor(M, name);
+        if (dst.scales) {
+          const n = dst.dataBytes * 2, K = name.endsWith('down_proj.weight') ? C.intermediate
+            : name.endsWith('o_proj.weight') ? C.n_heads * C.head_dim : C.hidden;
+          quantizeInto(dst, n / K, K, (r0, nr) => {
+            const b = new Uint16Array(nr * K);
+            for (let i = 0; i < b.length; i++) { f[0] = 0.02 * gauss(); b[i] = u[0] >>> 16; }
+            return b;
+          }, stage);
+        } else {
+          const n = dst.dataBytes / 2, b = new Uint16Array(n);
+          const emb = name === 'model.embed_tokens.weight';
+          for (let i = 0; i < n; i++) b[i] = emb ? f32ToF16(gauss()) : 0x3c00;
+          E.writeBuffer(dst.data, 0, b);
+        }
+      }
+      E.sync();
+    } finally {
+      E.destroy(stage);
+    }
+  }
+
+  // loadModel({variant, nCtx, config, safetensors, random, tokenizer, onProgress})
+  // (models/qwen3.js:3719): allocates the decoder for `nCtx` positions and fills it
+  async function loadModel(opts = {}) {
+    if (M && !opts.reload) return;
+    if (M) unload();
+    const base = opts.config || CONFIGS[opts.variant || '0.6B'];
+    if (!base) throw new Error('loadModel: unknown variant ' + opts.variant);
+    const maxCtx = opts.nCtx || base.max_ctx || 4096;
+    const chunk = Math.max(1, Math.min(PREFILL_CHUNK, Math.floor(ATTN_ROWS / base.n_heads), maxCtx));
+    C = Object.assign({ rope_theta: 1e6, rms_eps: 1e-6 }, base, { max_ctx: maxCtx, max_tokens: chunk });
+    M = TI.qwen3_create(ctx, C);
+    TOK = opts.tokenizer || null;
+    if (opts.safetensors) loadWeights([].concat(opts.safetensors), opts.onProgress);
+    else if (opts.random != null) randomWeights(opts.random);
+    _devPos = -1;
+    _cachedIds = null;
+  }
+
+  function unload() {
+    if (_decodeGraph) { E.destroyGraph(_decodeGraph); _decodeGraph = null; }
+    if (M) { TI.qwen3_destroy(M); M = null; }
+  }
+
+  function need() { if (!M) throw new Error('no model loaded: call loadModel() first'); }
+  function setPos(pos) { if (_devPos !== pos) { TI.qwen3_set_pos(ctx, M, pos); _devPos = pos; } }
+  function readTok(pos) { return TI.qwen3_read_tokens(ctx, M, pos, 1)[0]; }
+
+  function logitsNow() { return new Float32Array(E.readBytes(TI.qwen3_logits(M), 0, C.vocab * 4)); }
+
+  // distStats over the last logits: logprob of tok, top-k alternatives, entropy (nats)
+  function distStats(logits, tok, k) {
+    let mx = -Infinity;
+    for (let i = 0; i < logits.length; i++) if (logits[i] > mx) mx = logits[i];
+    let z = 0;
+    for (let i = 0; i < logits.length; i++) z += Math.exp(logits[i] - mx);
+    const lz = Math.log(z) + mx;
+    let ent = 0;
+    for (let i = 0; i < logits.length; i++) { const lp = logits[i] - lz; ent -= Math.exp(lp) * lp; }
+    const idx = Array.from(logits.keys()).sort((a, b) => logits[b] - logits[a]).slice(0, k);
+    return { logprob: logits[tok] - lz, alts: idx.map((i) => ({ id: i, logprob: logits[i] - lz })), entropy: ent };
+  }
+
+  // forward(idsArray, posBase, {chain, submitOnly, logprobs}) -> next token id (:3938)
+  async function forward(idsArray, posBase, opts) {
+    need();
+    const chain = !!(opts && opts.chain), submitOnly = !!(opts && opts.submitOnly);
+    if (opts && opts.temp > 0) throw new Error('forward: sampling (temp > 0) is not part of this path; the decode step is argmax');
+    let T;
+    if (chain) {
+      T = 1;
+      setPos(posBase);
+      TI.qwen3_decode(ctx, M);
+    } else {
+      const ids = Int32Array.from(idsArray);
+      T = ids.length;
+      if (T < 1 || T > C.max_tokens) throw new Error('forward: T=' + T + ' outside [1, ' + C.max_tokens + ']');
+      TI.qwen3_forward(ctx, M, ids, T, posBase);
+    }
+    _devPos = posBase + T;
+    if (submitOnly) return undefined;
+    await E.drain();
+    const tok = readTok(posBase + T);
+    if (opts && opts.logprobs) return Object.assign({ tok }, distStats(logitsNow(), tok, 5));
+    return tok;
+  }
+
+  function decodeGraph() {
+    if (!_decodeGraph) {
+      E.beginBatch();
+      try { TI.qwen3_decode(ctx, M); } finally { _decodeGraph = E.endBatch(); }
+    }
+    return _decodeGraph;
+  }
+
+  // decodeLoop (:4414-4435): GEN_BATCH graph replays of the device-position step, then one
+  // readback of the tokens they chained; stops on emitTok() === false, maxTokens or the cache end
+  async function decodeLoop(pos, maxTokens, emitTok, signal, count) {
+    const g = decodeGraph();
+    for (;;) {
+      if (signal && signal.aborted) return;
+      const K = Math.min(GEN_BATCH, C.max_ctx - 1 - pos, maxTokens - count());
+      if (K <= 0) return;
+      setPos(pos);
+      for (let k = 0; k < K; k++) E.launch(g);
+      _devPos = pos + K;
+      await E.drain();
+      const toks = TI.qwen3_read_tokens(ctx, M, pos + 1, K);
+      pos += K;
+      for (let k = 0; k < K; k++) if (!emitTok(toks[k]) || count() >= maxTokens) return;
+    }
+  }
+
+  function encode(x) {
+    if (Array.isArray(x) || ArrayBuffer.isView(x)) return Array.from(x);
+    if (!TOK) throw new Error('a text prompt needs loadModel({tokenizer})');
+    return TOK.encodeChat(typeof x === 'string' ? [{ role: 'user', content: x }] : x);
+  }
+  const decode = (ids) => (TOK ? TOK.decode(ids) : ids.slice());
+  const isStop = (t) => !!(TOK && TOK.isStop && TOK.isStop(t));
+
+  // prefill ids[from..L) in chunks of up to PREFILL_CHUNK (C.max_tokens); returns the token after the last
+  async function prefill(ids, from, signal) {
+    let tok;
+    for (let off = from; off < ids.length; off += C.max_tokens) {
+      if (signal && signal.aborted) throw abortError();
+      tok = await forward(ids.slice(off, Math.min(off + C.max_tokens, ids.length)), off);
+    }
+    return tok;
+  }
+
+  function abortError() { const e = new Error('aborted'); e.name = 'AbortError'; return e; }
+
+  function checkFits(L) {
+    if (L + 64 > C.max_ctx) throw new Error('prompt too long: ' + L + ' tokens — exceeds the context limit (' + C.max_ctx + ').');
+  }
+
+  // generate(prompt, {maxTokens, onToken, onStats, signal}) (:4538-4569)
+  async function generate(prompt, { maxTokens = 64, onToken, onStats, signal, temperature } = {}) {
+    need();
+    if (temperature > 0) throw new Error('generate: sampling is not part of this path (argmax decode only)');
+    _cachedIds = null;
+    const ids = encode(prompt);
+    const L = ids.length;
+    checkFits(L);
+    const t0 = Date.now();
+    const tok0 = await prefill(ids, 0, signal);
+    const ms = Date.now() - t0;
+    _lastGenStats = { prefillTokens: L, prefillMs: ms, prefillTps: +(L / Math.max(ms, 1e-3) * 1000).toFixed(1) };
+    if (onStats) { try { onStats(_lastGenStats); } catch (_) { /* caller's hook */ } }
+    const out = [];
+    const emit = (t) => {
+      if (isStop(t)) return false;
+      out.push(t);
+      if (onToken) { try { onToken(TOK ? TOK.decode([t]) : t); } catch (_) { /* caller's hook */ } }
+      return true;
+    };
+    if (emit(tok0)) await decodeLoop(L, maxTokens, emit, signal, () => out.length);
+    return decode(out);
+  }
+
+  // <think> / <tool_call> splitting of the streamed text (the reference's makeRoundParser)
+  function makeRoundParser(onReasoning, onContent) {
+    const p = { state: 'content', content: '', reasoning: '', toolCalls: [], buf: '' };
+    const OPEN_T = '<think>', CLOSE_T = '</think>', OPEN_C = '<tool_call>', CLOSE_C = '</tool_call>';
+    p.push = (text) => {
+      p.buf += text;
+      for (;;) {
+        if (p.state === 'think') {
+          const i = p.buf.indexOf(CLOSE_T);
+          if (i < 0) { const keep = Math.max(0, p.buf.length - CLOSE_T.length); if (keep) { onReasoning(p.buf.slice(0, keep)); p.reasoning += p.buf.slice(0, keep); p.buf = p.buf.slice(keep); } return; }
+          if (i) { onReasoning(p.buf.slice(0, i)); p.reasoning += p.buf.slice(0, i); }
+          p.buf = p.buf.slice(i + CLOSE_T.length); p.state = 'content';
+        } else if (p.state === 'tool') {
+          const i = p.buf.indexOf(CLOSE_C);
+          if (i < 0) return;
+          p.toolCalls.push(p.buf.slice(0, i).trim()); p.buf = p.buf.slice(i + CLOSE_C.length); p.state = 'content';
+        } else {
+          const it = p.buf.indexOf(OPEN_T), ic = p.buf.indexOf(OPEN_C);
+          const i = it < 0 ? ic : (ic < 0 ? it : Math.min(it, ic));
+          if (i < 0) { const keep = Math.max(0, p.buf.length - OPEN_C.length); if (keep) { onContent(p.buf.slice(0, keep)); p.content += p.buf.slice(0, keep); p.buf = p.buf.slice(keep); } return; }
+          if (i) { onContent(p.buf.slice(0, i)); p.content += p.buf.slice(0, i); }
+          if (i === it) { p.buf = p.buf.slice(i + OPEN_T.length); p.state = 'think'; } else { p.buf = p.buf.slice(i + OPEN_C.length); p.state = 'tool'; }
+        }
+      }
+    };
+    p.flush = () => {
+      if (p.buf) { if (p.state === 'think') { onReasoning(p.buf); p.reasoning += p.buf; } else if (p.state === 'content') { onContent(p.buf); p.content += p.buf; } }
+      p.buf = '';
+    };
+    return p;
+  }
+
+  // _streamIds (:5199-5292) without grammar masking: prefix-cache reuse, chunked prefill of
+  // the rest, then the batched decode loop
+  async function streamIds(ids, { maxTokens, onToken, signal }) {
+    const L = ids.length;
+    checkFits(L);
+    let lcp = 0;
+    if (_cachedIds) { const n = Math.min(_cachedIds.length, L - 1); while (lcp < n && _cachedIds[lcp] === ids[lcp]) lcp++; }
+    const tok0 = await prefill(ids, lcp, signal);
+    _cachedIds = ids.slice();
+    const out = [];
+    const emitTok = (t) => { if (isStop(t)) return false; out.push(t); _cachedIds.push(t); if (onToken) onToken(TOK ? TOK.decode([t]) : String(t)); return true; };
+    if (emitTok(tok0)) await decodeLoop(L, maxTokens, emitTok, signal, () => out.length);
+    _cachedIds = _cachedIds.slice(0, L + out.length);   // KV rows beyond this were written by discarded steps
+    return out;
+  }
+
+  // runConversation({provider, messages, systemPrompt, tools, convId, signal}, emit) (:5397-5522)
+  async function runConversation({ provider, messages, systemPrompt, tools, convId, signal } = {}, emit) {
+    try {
+      if (!M) throw new Error('no model loaded: call loadModel() first');
+      if (!TOK) throw new Error('runConversation needs loadModel({tokenizer})');
+    } catch (e) {
+      emit({ type: 'error', message: 'Qwen3 dense: ' + e.message });
+      emit({ type: 'agent_done' });
+      return;
+    }
+    const maxTokens = (provider && (provider.maxTokens | 0)) || C.max_ctx;
+    const sys = (systemPrompt && typeof systemPrompt === 'object') ? (systemPrompt.content || '') : (systemPrompt || '');
+    const toolList = (Array.isArray(tools) ? tools : []).filter((t) => t && t.type === 'function');
+    const work = [];
+    if (sys) work.push({ role: 'system', content: sys });
+    for (const m of (messages || [])) if (m && m.role) work.push({ role: m.role === 'tool' ? 'user' : m.role, content: m.role === 'tool' ? '<tool_response>\n' + m.content + '\n</tool_response>' : String(m.content == null ? '' : m.content) });
+    const MAX_ROUNDS = toolList.length && _toolRunner ? 8 : 1;
+    try {
+      for (let round = 0; round < MAX_ROUNDS; round++) {
+        if (signal && signal.aborted) throw abortError();
+        emit({ type: 'round_start' });
+        const parser = makeRoundParser((rz) => emit({ type: 'delta', delta: { reasoning: rz } }),
+          (ct) => emit({ type: 'delta', delta: { content: ct } }));
+        const ids = TOK.encodeChat(work);
+        await streamIds(ids, { maxTokens, signal, onToken: (t) => parser.push(t) });
+        parser.flush();
+        const content = parser.content.replace(/^\s+/, '');
+        const toolCalls = [];
+        parser.toolCalls.forEach((raw, k) => {
+          try { const o = JSON.parse(raw); if (o && o.name) toolCalls.push({ id: 'call_' + round + '_' + k, type: 'function', function: { name: o.name, arguments: JSON.stringify(o.arguments || {}) } }); } catch (_) { /* not a call */ }
+        });
+        if (toolCalls.length) emit({ type: 'delta', delta: { tool_calls: toolCalls.map((tc, i) => Object.assign({ index: i }, tc)) } });
+        emit({ type: 'round_end', content });
+        emit({ type: 'usage', usage: { prompt_tokens: ids.length, total_tokens: ids.length } });
+        const asst = { role: 'assistant', content };
+        if (toolCalls.length) asst.tool_calls = toolCalls;
+        emit({ type: 'message_added', message: asst });
+        work.push({ role: 'assistant', content });
+        if (!toolCalls.length || !_toolRunner) break;
+        for (const tc of toolCalls) {
+          emit({ type: 'tool_started', tc });
+          let args = {};
+          try { args = JSON.parse(tc.function.arguments || '{}'); } catch (_) { /* empty args */ }
+          let res;
+          try { res = await _toolRunner(tc.function.name, args, convId, signal); } catch (e) { res = { result: 'Error: ' + ((e && e.message) || e) }; }
+          const text = res && res.result != null ? res.result : '';
+          emit({ type: 'tool_result', id: tc.id, result: text });
+          work.push({ role: 'user', content: '<tool_response>\n' + text + '\n</tool_response>' });
+          emit({ type: 'message_added', message: { role: 'tool', tool_call_id: tc.id, content: text } });
+        }
+      }
+    } catch (e) {
+      if (e && e.name === 'AbortError') throw e;
+      emit({ type: 'error', message: 'Qwen3 dense: ' + ((e && e.message) || e) });
+    }
+    emit({ type: 'agent_done' });
+  }
+
+  return {
+    CONFIGS, engine: eng, loadModel, unload, forward, generate, runConversation, decodeLoop,
+    setToolRunner(fn) { _toolRunner = fn; },
+    lastGenStats: () => _lastGenStats,
+    config: () => C,
+    model: () => M,
+    readTokens: (from, n) => TI.qwen3_read_tokens(ctx, M, from, n),
+    logits: () => logitsNow(),
+    shutdown() { unload(); E.shutdown(); },
+  };
+}
+
+module.exports = { createQwen3Host, CONFIGS, readSafetensorsHeader, GEN_BATCH, PREFILL_CHUNK };

@@ -1,0 +1,877 @@
+// ti_node.cc — Node.js N-API addon over libtabinfer's C ABI (include/ti.h).
+//
+// The reference engine's kernels are closure launchers over WebGPU buffers
+// (models/qwen3.js, models/lfm25.js over engine/webgpu-engine.js). This addon gives
+// the JS host the same objects over the HIP library:
+//   init(device) -> ctx                        E.init (engine/webgpu-engine.js:72-145)
+//   buf_alloc(ctx, bytes) -> buffer            E.createBuffer (:156-160); freed by GC or buf_free
+//   buf_write / buf_read / buf_copy / sync     queue.writeBuffer / E.readF32 / E.copyBuffer
+//   graph_begin / graph_end / graph_launch     E.beginBatch / E.endBatch (:357-386)
+//   every kernel entry point of ti.h           under its C name without the "ti_" prefix
+// Buffers and the other handles are napi_external objects. A device-pointer argument
+// takes a buffer (or a view of one) or null. Errors from the library (shape
+// preconditions, HIP failures) become JS exceptions carrying ti_last_error().
+//
+// Only the plain N-API C API is used (Node 12, N-API 8); no node-addon-api.
+#include <node_api.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <limits>
+#include <string>
+#include <tuple>
+#include <type_traits>
+#include <utility>
+#include <vector>
+
+#include "ti.h"
+
+namespace {
+
+// ---- handles -------------------------------------------------------------------------
+enum Tag : uint32_t { TAG_CTX = 0x74696378, TAG_BUF = 0x74696262, TAG_GRAPH = 0x74696767, TAG_MODEL = 0x7469716d };
+
+// A context lives until its JS handle is finalized (or shutdown() is called) AND every
+// buffer, graph and model made on it is gone: they hold counted references, so a
+// finalizer never runs against a context that was already shut down.
+struct CtxH {
+    uint32_t tag = TAG_CTX;
+    ti_ctx* c = nullptr;
+    int refs = 1;          // the JS handle + one per live dependent handle
+    bool closed = false;
+};
+
+void ctx_unref(CtxH* h) {
+    if (--h->refs == 0) {
+        if (!h->closed && h->c) ti_shutdown(h->c);
+        h->tag = 0;
+        delete h;
+    }
+}
+
+struct BufH {
+    uint32_t tag = TAG_BUF;
+    CtxH* ctx = nullptr;
+    char* ptr = nullptr;
+    size_t bytes = 0;      // 0 = size not known (views into a model's storage)
+    bool owned = false;    // freed with ti_buf_free when collected
+    napi_ref parent = nullptr;   // views keep their parent object alive
+};
+
+struct GraphH {
+    uint32_t tag = TAG_GRAPH;
+    CtxH* ctx = nullptr;
+    ti_graph* g = nullptr;
+};
+
+struct ModelH {
+    uint32_t tag = TAG_MODEL;
+    CtxH* ctx = nullptr;
+    ti_qwen3* m = nullptr;
+};
+
+// ---- error helpers ----------------------------------------------------------------------
+napi_value undefined(napi_env env) {
+    napi_value u;
+    napi_get_undefined(env, &u);
+    return u;
+}
+
+napi_value throw_msg(napi_env env, const std::string& msg) {
+    napi_throw_error(env, nullptr, msg.c_str());
+    return nullptr;
+}
+
+napi_value throw_ti(napi_env env, const char* fn, int rc) {
+    const char* m = ti_last_error();
+    char code[32];
+    std::snprintf(code, sizeof code, "%d", rc);
+    std::string s = std::string(fn) + " failed (" + code + "): " + (m && *m ? m : "unknown error");
+    napi_value err, msg, cv;
+    napi_create_string_utf8(env, s.c_str(), NAPI_AUTO_LENGTH, &msg);
+    napi_create_error(env, nullptr, msg, &err);
+    napi_create_int32(env, rc, &cv);
+    napi_set_named_property(env, err, "code", cv);
+    napi_throw(env, err);
+    return nullptr;
+}
+
+bool arg_error(napi_env env, const char* fn, size_t i, const char* want) {
+    char b[256];
+    std::snprintf(b, sizeof b, "%s: argument %zu must be %s", fn, i, want);
+    napi_throw_type_error(env, nullptr, b);
+    return false;
+}
+
+template <typename H>
+H* handle_of(napi_env env, napi_value v, uint32_t tag) {
+    napi_valuetype t;
+    if (napi_typeof(env, v, &t) != napi_ok || t != napi_external) return nullptr;
+    void* p = nullptr;
+    if (napi_get_value_external(env, v, &p) != napi_ok || !p) return nullptr;
+    H* h = static_cast<H*>(p);
+    return h->tag == tag ? h : nullptr;
+}
+
+bool is_nullish(napi_env env, napi_value v) {
+    napi_valuetype t;
+    napi_typeof(env, v, &t);
+    return t == napi_null || t == napi_undefined;
+}
+
+CtxH* get_ctx(napi_env env, napi_value v, const char* fn) {
+    CtxH* h = handle_of<CtxH>(env, v, TAG_CTX);
+    if (!h) { arg_error(env, fn, 0, "a context from init()"); return nullptr; }
+    if (h->closed) { throw_msg(env, std::string(fn) + ": the context was shut down"); return nullptr; }
+    return h;
+}
+
+// ---- finalizers ---------------------------------------------------------------------------
+void fin_ctx(napi_env, void* data, void*) {
+    ctx_unref(static_cast<CtxH*>(data));
+}
+
+void fin_buf(napi_env env, void* data, void*) {
+    BufH* b = static_cast<BufH*>(data);
+    if (b->owned && b->ptr && !b->ctx->closed) ti_buf_free(b->ctx->c, b->ptr);
+    if (b->parent) napi_delete_reference(env, b->parent);
+    ctx_unref(b->ctx);
+    b->tag = 0;
+    delete b;
+}
+
+void fin_graph(napi_env, void* data, void*) {
+    GraphH* g = static_cast<GraphH*>(data);
+    if (g->g && !g->ctx->closed) ti_graph_destroy(g->g);
+    ctx_unref(g->ctx);
+    g->tag = 0;
+    delete g;
+}
+
+void fin_model(napi_env, void* data, void*) {
+    ModelH* m = static_cast<ModelH*>(data);
+    if (m->m && !m->ctx->closed) ti_qwen3_destroy(m->ctx->c, m->m);
+    ctx_unref(m->ctx);
+    m->tag = 0;
+    delete m;
+}
+
+napi_value make_buf(napi_env env, CtxH* ctx, void* ptr, size_t bytes, bool owned, napi_value parent) {
+    BufH* b = new BufH;
+    b->ctx = ctx;
+    ctx->refs++;
+    b->ptr = static_cast<char*>(ptr);
+    b->bytes = bytes;
+    b->owned = owned;
+    if (parent) napi_create_reference(env, parent, 1, &b->parent);
+    napi_value out;
+    napi_create_external(env, b, fin_buf, nullptr, &out);
+    return out;
+}
+
+// ---- argument conversion for the generic kernel wrapper ------------------------------------
+bool get_i64(napi_env env, napi_value v, int64_t* out, const char* fn, size_t i) {
+    double d;
+    if (napi_get_value_double(env, v, &d) != napi_ok) return arg_error(env, fn, i, "a number");
+    if (d != (double)(int64_t)d) return arg_error(env, fn, i, "an integer");
+    *out = (int64_t)d;
+    return true;
+}
+
+bool get_dptr(napi_env env, napi_value v, void** out, const char* fn, size_t i) {
+    if (is_nullish(env, v)) { *out = nullptr; return true; }
+    BufH* b = handle_of<BufH>(env, v, TAG_BUF);
+    if (!b) return arg_error(env, fn, i, "a device buffer or null");
+    if (!b->ptr) return arg_error(env, fn, i, "a live device buffer (this one was freed)");
+    *out = b->ptr;
+    return true;
+}
+
+template <typename T, typename Enable = void>
+struct Conv;
+
+template <typename T>
+struct Conv<T, typename std::enable_if<std::is_integral<T>::value>::type> {
+    T v{};
+    bool get(napi_env env, napi_value x, const char* fn, size_t i) {
+        int64_t t = 0;
+        if (!get_i64(env, x, &t, fn, i)) return false;
+        if (t < (int64_t)std::numeric_limits<T>::min() || (std::is_signed<T>::value ? t > (int64_t)std::numeric_limits<T>::max()
+                                                                                   : (uint64_t)t > (uint64_t)std::numeric_limits<T>::max()))
+            return arg_error(env, fn, i, "an integer in range");
+        v = (T)t;
+        return true;
+    }
+    T value() const { return v; }
+};
+
+template <>
+struct Conv<float> {
+    float v = 0.0f;
+    bool get(napi_env env, napi_value x, const char* fn, size_t i) {
+        double d;
+        if (napi_get_value_double(env, x, &d) != napi_ok) return arg_error(env, fn, i, "a number");
+        v = (float)d;
+        return true;
+    }
+    float value() const { return v; }
+};
+
+// device pointers: arithmetic element types (const or not) and void
+template <typename P>
+struct Conv<P*, typename std::enable_if<std::is_arithmetic<typename std::remove_const<P>::type>::value ||
+                                        std::is_void<typename std::remove_const<P>::type>::value>::type> {
+    P* v = nullptr;
+    bool get(napi_env env, napi_value x, const char* fn, size_t i) {
+        void* p = nullptr;
+        if (!get_dptr(env, x, &p, fn, i)) return false;
+        v = static_cast<P*>(p);
+        return true;
+    }
+    P* value() const { return v; }
+};
+
+template <typename... A, size_t... I>
+napi_value invoke(napi_env env, napi_value* argv, const char* fn, int (*f)(ti_ctx*, A...), std::index_sequence<I...>) {
+    CtxH* c = get_ctx(env, argv[0], fn);
+    if (!c) return nullptr;
+    std::tuple<Conv<A>...> cv;
+    bool ok = true;
+    (void)std::initializer_list<int>{(ok = ok && std::get<I>(cv).get(env, argv[I + 1], fn, I + 1), 0)...};
+    if (!ok) return nullptr;
+    const int rc = f(c->c, std::get<I>(cv).value()...);
+    return rc ? throw_ti(env, fn, rc) : undefined(env);
+}
+
+template <typename... A>
+napi_value call_entry(napi_env env, napi_callback_info info, const char* fn, int (*f)(ti_ctx*, A...)) {
+    constexpr size_t N = sizeof...(A) + 1;
+    size_t argc = N;
+    napi_value argv[N];
+    napi_get_cb_info(env, info, &argc, argv, nullptr, nullptr);
+    if (argc != N) {
+        char b[160];
+        std::snprintf(b, sizeof b, "%s expects %zu arguments (ctx first), got %zu", fn, N, argc);
+        return throw_msg(env, b);
+    }
+    return invoke(env, argv, fn, f, std::index_sequence_for<A...>{});
+}
+
+// ---- hand-written entries (host memory, handles, arrays) -----------------------------------
+struct Args {
+    napi_value v[12];
+    size_t n = 12;
+    Args(napi_env env, napi_callback_info info) { napi_get_cb_info(env, info, &n, v, nullptr, nullptr); }
+};
+
+bool want_args(napi_env env, const Args& a, size_t n, const char* fn) {
+    if (a.n != n) {
+        char b[128];
+        std::snprintf(b, sizeof b, "%s expects %zu arguments, got %zu", fn, n, a.n);
+        throw_msg(env, b);
+        return false;
+    }
+    return true;
+}
+
+napi_value num(napi_env env, double d) {
+    napi_value r;
+    napi_create_double(env, d, &r);
+    return r;
+}
+
+napi_value js_version(napi_env env, napi_callback_info) { return num(env, ti_version()); }
+
+napi_value js_last_error(napi_env env, napi_callback_info) {
+    napi_value r;
+    napi_create_string_utf8(env, ti_last_error(), NAPI_AUTO_LENGTH, &r);
+    return r;
+}
+
+napi_value js_device_count(napi_env env, napi_callback_info) {
+    int n = 0;
+    const int rc = ti_device_count(&n);
+    return rc ? throw_ti(env, "device_count", rc) : num(env, n);
+}
+
+napi_value js_init(napi_env env, napi_callback_info info) {
+    Args a(env, info);
+    int64_t dev = 0;
+    if (a.n >= 1 && !is_nullish(env, a.v[0]) && !get_i64(env, a.v[0], &dev, "init", 0)) return nullptr;
+    ti_ctx* c = nullptr;
+    const int rc = ti_init((int)dev, &c);
+    if (rc) return throw_ti(env, "init", rc);
+    CtxH* h = new CtxH;
+    h->c = c;
+    napi_value out;
+    napi_create_external(env, h, fin_ctx, nullptr, &out);
+    return out;
+}
+
+napi_value js_shutdown(napi_env env, napi_callback_info info) {
+    Args a(env, info);
+    if (!want_args(env, a, 1, "shutdown")) return nullptr;
+    CtxH* h = handle_of<CtxH>(env, a.v[0], TAG_CTX);
+    if (!h) return arg_error(env, "shutdown", 0, "a context"), nullptr;
+    if (!h->closed) {
+        const int rc = ti_shutdown(h->c);
+        h->closed = true;
+        h->c = nullptr;
+        if (rc) return throw_ti(env, "shutdown", rc);
+    }
+    return undefined(env);
+}
+
+napi_value js_buf_alloc(napi_env env, napi_callback_info info) {
+    Args a(env, info);
+    if (!want_args(env, a, 2, "buf_alloc")) return nullptr;
+    CtxH* c = get_ctx(env, a.v[0], "buf_alloc");
+    int64_t bytes;
+    if (!c || !get_i64(env, a.v[1], &bytes, "buf_alloc", 1)) return nullptr;
+    if (bytes <= 0) return arg_error(env, "buf_alloc", 1, "a positive byte count"), nullptr;
+    void* p = nullptr;
+    const int rc = ti_buf_alloc(c->c, (size_t)bytes, &p);
+    if (rc) return throw_ti(env, "buf_alloc", rc);
+    return make_buf(env, c, p, (size_t)bytes, true, nullptr);
+}
+
+napi_value js_buf_free(napi_env env, napi_callback_info info) {
+    Args a(env, info);
+    if (!want_args(env, a, 1, "buf_free")) return nullptr;
+    BufH* b = handle_of<BufH>(env, a.v[0], TAG_BUF);
+    if (!b) return arg_error(env, "buf_free", 0, "a device buffer"), nullptr;
+    if (b->owned && b->ptr && !b->ctx->closed) {
+        const int rc = ti_buf_free(b->ctx->c, b->ptr);
+        if (rc) return throw_ti(env, "buf_free", rc);
+    }
+    b->ptr = nullptr;
+    return undefined(env);
+}
+
+// buf_view(buffer, byteOffset[, bytes]): a non-owning view that keeps `buffer` alive
+napi_value js_buf_view(napi_env env, napi_callback_info info) {
+    Args a(env, info);
+    if (a.n < 2 || a.n > 3) return throw_msg(env, "buf_view expects (buffer, byteOffset[, bytes])");
+    BufH* b = handle_of<BufH>(env, a.v[0], TAG_BUF);
+    if (!b || !b->ptr) return arg_error(env, "buf_view", 0, "a live device buffer"), nullptr;
+    int64_t off, len = -1;
+    if (!get_i64(env, a.v[1], &off, "buf_view", 1)) return nullptr;
+    if (a.n == 3 && !get_i64(env, a.v[2], &len, "buf_view", 2)) return nullptr;
+    if (off < 0 || (b->bytes && (size_t)off > b->bytes)) return throw_msg(env, "buf_view: offset outside the buffer");
+    size_t rest = b->bytes ? b->bytes - (size_t)off : 0;
+    if (len >= 0) {
+        if (b->bytes && (size_t)len > rest) return throw_msg(env, "buf_view: view extends past the buffer");
+        rest = (size_t)len;
+    }
+    return make_buf(env, b->ctx, b->ptr + off, rest, false, a.v[0]);
+}
+
+napi_value js_buf_bytes(napi_env env, napi_callback_info info) {
+    Args a(env, info);
+    BufH* b = a.n == 1 ? handle_of<BufH>(env, a.v[0], TAG_BUF) : nullptr;
+    if (!b) return arg_error(env, "buf_bytes", 0, "a device buffer"), nullptr;
+    return num(env, (double)b->bytes);
+}
+
+// host bytes of a TypedArray / DataView / ArrayBuffer / Buffer
+bool host_bytes(napi_env env, napi_value v, void** data, size_t* len, const char* fn, size_t i) {
+    bool is;
+    napi_is_typedarray(env, v, &is);
+    if (is) {
+        napi_typedarray_type t;
+        size_t n, off;
+        napi_value ab;
+        napi_get_typedarray_info(env, v, &t, &n, data, &ab, &off);
+        size_t es = 1;
+        switch (t) {
+            case napi_int16_array: case napi_uint16_array: es = 2; break;
+            case napi_int32_array: case napi_uint32_array: case napi_float32_array: es = 4; break;
+            case napi_float64_array: case napi_bigint64_array: case napi_biguint64_array: es = 8; break;
+            default: es = 1;
+        }
+        *len = n * es;
+        return true;
+    }
+    napi_is_dataview(env, v, &is);
+    if (is) {
+        napi_value ab;
+        size_t off;
+        napi_get_dataview_info(env, v, len, data, &ab, &off);
+        return true;
+    }
+    napi_is_arraybuffer(env, v, &is);
+    if (is) {
+        napi_get_arraybuffer_info(env, v, data, len);
+        return true;
+    }
+    return arg_error(env, fn, i, "a TypedArray, DataView or ArrayBuffer");
+}
+
+// buf_write(ctx, buffer, byteOffset, typedArray)
+napi_value js_buf_write(napi_env env, napi_callback_info info) {
+    Args a(env, info);
+    if (!want_args(env, a, 4, "buf_write")) return nullptr;
+    CtxH* c = get_ctx(env, a.v[0], "buf_write");
+    void* dst;
+    int64_t off;
+    void* src;
+    size_t len;
+    if (!c || !get_dptr(env, a.v[1], &dst, "buf_write", 1) || !get_i64(env, a.v[2], &off, "buf_write", 2) ||
+        !host_bytes(env, a.v[3], &src, &len, "buf_write", 3))
+        return nullptr;
+    BufH* b = handle_of<BufH>(env, a.v[1], TAG_BUF);
+    if (!dst || off < 0 || (b->bytes && (size_t)off + len > b->bytes)) return throw_msg(env, "buf_write: outside the buffer");
+    const int rc = ti_buf_write(c->c, dst, (size_t)off, src, len);
+    return rc ? throw_ti(env, "buf_write", rc) : undefined(env);
+}
+
+// buf_read(ctx, buffer, byteOffset, bytes) -> ArrayBuffer (waits for the stream)
+napi_value js_buf_read(napi_env env, napi_callback_info info) {
+    Args a(env, info);
+    if (!want_args(env, a, 4, "buf_read")) return nullptr;
+    CtxH* c = get_ctx(env, a.v[0], "buf_read");
+    void* src;
+    int64_t off, len;
+    if (!c || !get_dptr(env, a.v[1], &src, "buf_read", 1) || !get_i64(env, a.v[2], &off, "buf_read", 2) ||
+        !get_i64(env, a.v[3], &len, "buf_read", 3))
+        return nullptr;
+    BufH* b = handle_of<BufH>(env, a.v[1], TAG_BUF);
+    if (!src || off < 0 || len < 0 || (b->bytes && (size_t)(off + len) > b->bytes)) return throw_msg(env, "buf_read: outside the buffer");
+    void* data;
+    napi_value ab;
+    napi_create_arraybuffer(env, (size_t)len, &data, &ab);
+    const int rc = ti_buf_read(c->c, src, (size_t)off, data, (size_t)len);
+    return rc ? throw_ti(env, "buf_read", rc) : ab;
+}
+
+// sync_async(ctx) -> Promise: waits on a worker thread so the event loop keeps running.
+// The caller issues nothing else on the context until the promise settles.
+struct SyncWork {
+    napi_async_work work = nullptr;
+    napi_deferred deferred = nullptr;
+    CtxH* ctx = nullptr;
+    int rc = 0;
+    std::string err;
+};
+
+void sync_execute(napi_env, void* data) {
+    SyncWork* w = static_cast<SyncWork*>(data);
+    w->rc = ti_sync(w->ctx->c);
+    if (w->rc) w->err = ti_last_error();
+}
+
+void sync_complete(napi_env env, napi_status, void* data) {
+    SyncWork* w = static_cast<SyncWork*>(data);
+    if (w->rc) {
+        napi_value msg, err;
+        napi_create_string_utf8(env, ("sync failed: " + w->err).c_str(), NAPI_AUTO_LENGTH, &msg);
+        napi_create_error(env, nullptr, msg, &err);
+        napi_reject_deferred(env, w->deferred, err);
+    } else {
+        napi_resolve_deferred(env, w->deferred, undefined(env));
+    }
+    napi_delete_async_work(env, w->work);
+    ctx_unref(w->ctx);
+    delete w;
+}
+
+napi_value js_sync_async(napi_env env, napi_callback_info info) {
+    Args a(env, info);
+    if (!want_args(env, a, 1, "sync_async")) return nullptr;
+    CtxH* c = get_ctx(env, a.v[0], "sync_async");
+    if (!c) return nullptr;
+    SyncWork* w = new SyncWork;
+    w->ctx = c;
+    c->refs++;
+    napi_value promise, name;
+    napi_create_promise(env, &w->deferred, &promise);
+    napi_create_string_utf8(env, "ti_sync", NAPI_AUTO_LENGTH, &name);
+    napi_create_async_work(env, nullptr, name, sync_execute, sync_complete, w, &w->work);
+    napi_queue_async_work(env, w->work);
+    return promise;
+}
+
+napi_value js_graph_end(napi_env env, napi_callback_info info) {
+    Args a(env, info);
+    if (!want_args(env, a, 1, "graph_end")) return nullptr;
+    CtxH* c = get_ctx(env, a.v[0], "graph_end");
+    if (!c) return nullptr;
+    ti_graph* g = nullptr;
+    const int rc = ti_graph_end(c->c, &g);
+    if (rc) return throw_ti(env, "graph_end", rc);
+    GraphH* h = new GraphH;
+    h->ctx = c;
+    c->refs++;
+    h->g = g;
+    napi_value out;
+    napi_create_external(env, h, fin_graph, nullptr, &out);
+    return out;
+}
+
+napi_value js_graph_launch(napi_env env, napi_callback_info info) {
+    Args a(env, info);
+    if (!want_args(env, a, 2, "graph_launch")) return nullptr;
+    CtxH* c = get_ctx(env, a.v[0], "graph_launch");
+    GraphH* g = handle_of<GraphH>(env, a.v[1], TAG_GRAPH);
+    if (!c) return nullptr;
+    if (!g || !g->g) return arg_error(env, "graph_launch", 1, "a live graph"), nullptr;
+    const int rc = ti_graph_launch(c->c, g->g);
+    return rc ? throw_ti(env, "graph_launch", rc) : undefined(env);
+}
+
+napi_value js_graph_destroy(napi_env env, napi_callback_info info) {
+    Args a(env, info);
+    GraphH* g = a.n == 1 ? handle_of<GraphH>(env, a.v[0], TAG_GRAPH) : nullptr;
+    if (!g) return arg_error(env, "graph_destroy", 0, "a graph"), nullptr;
+    if (g->g && !g->ctx->closed) ti_graph_destroy(g->g);
+    g->g = nullptr;
+    return undefined(env);
+}
+
+napi_value js_event_elapsed_ms(napi_env env, napi_callback_info info) {
+    Args a(env, info);
+    if (!want_args(env, a, 3, "event_elapsed_ms")) return nullptr;
+    CtxH* c = get_ctx(env, a.v[0], "event_elapsed_ms");
+    int64_t s0, s1;
+    if (!c || !get_i64(env, a.v[1], &s0, "event_elapsed_ms", 1) || !get_i64(env, a.v[2], &s1, "event_elapsed_ms", 2)) return nullptr;
+    float ms = 0.0f;
+    const int rc = ti_event_elapsed_ms(c->c, (int)s0, (int)s1, &ms);
+    return rc ? throw_ti(env, "event_elapsed_ms", rc) : num(env, ms);
+}
+
+// rmsnorm_gemv_q4(ctx, x, norm_w, eps, K, [packs], [scales], [ys], [Ns], xq_out, xs_out)
+napi_value js_rmsnorm_gemv_q4(napi_env env, napi_callback_info info) {
+    const char* fn = "rmsnorm_gemv_q4";
+    Args a(env, info);
+    if (!want_args(env, a, 11, fn)) return nullptr;
+    CtxH* c = get_ctx(env, a.v[0], fn);
+    void *x, *nw, *xq, *xs;
+    double eps;
+    int64_t K;
+    if (!c || !get_dptr(env, a.v[1], &x, fn, 1) || !get_dptr(env, a.v[2], &nw, fn, 2)) return nullptr;
+    if (napi_get_value_double(env, a.v[3], &eps) != napi_ok) return arg_error(env, fn, 3, "a number"), nullptr;
+    if (!get_i64(env, a.v[4], &K, fn, 4) || !get_dptr(env, a.v[9], &xq, fn, 9) || !get_dptr(env, a.v[10], &xs, fn, 10)) return nullptr;
+    uint32_t n[4] = {0, 0, 0, 0};
+    void* arr[3][3] = {};
+    int Ns[3] = {0, 0, 0};
+    for (int k = 0; k < 4; k++) {
+        bool is;
+        napi_is_array(env, a.v[5 + k], &is);
+        if (!is) return arg_error(env, fn, 5 + k, "an array"), nullptr;
+        napi_get_array_length(env, a.v[5 + k], &n[k]);
+        if (n[k] < 1 || n[k] > 3 || n[k] != n[0]) return throw_msg(env, "rmsnorm_gemv_q4: packs/scales/ys/Ns need 1..3 entries each, all alike");
+        for (uint32_t i = 0; i < n[k]; i++) {
+            napi_value e;
+            napi_get_element(env, a.v[5 + k], i, &e);
+            if (k < 3) {
+                if (!get_dptr(env, e, &arr[k][i], fn, 5 + k)) return nullptr;
+            } else {
+                int64_t t;
+                if (!get_i64(env, e, &t, fn, 8)) return nullptr;
+                Ns[i] = (int)t;
+            }
+        }
+    }
+    const int rc = ti_rmsnorm_gemv_q4(c->c, (const float*)x, (const uint16_t*)nw, (float)eps, (int)K, (int)n[0],
+                                      (const uint32_t* const*)arr[0], (const uint16_t* const*)arr[1], (float* const*)arr[2],
+                                      Ns, (uint32_t*)xq, (float*)xs);
+    return rc ? throw_ti(env, fn, rc) : undefined(env);
+}
+
+// ---- Qwen3 decoder object ---------------------------------------------------------------
+bool cfg_int(napi_env env, napi_value o, const char* key, int* out, bool required, int dflt) {
+    bool has;
+    napi_has_named_property(env, o, key, &has);
+    if (!has) {
+        if (required) { throw_msg(env, std::string("qwen3_create: config.") + key + " is required"); return false; }
+        *out = dflt;
+        return true;
+    }
+    napi_value v;
+    napi_get_named_property(env, o, key, &v);
+    int64_t t;
+    if (!get_i64(env, v, &t, key, 1)) return false;
+    *out = (int)t;
+    return true;
+}
+
+bool cfg_float(napi_env env, napi_value o, const char* key, float* out, float dflt) {
+    bool has;
+    napi_has_named_property(env, o, key, &has);
+    if (!has) { *out = dflt; return true; }
+    napi_value v;
+    napi_get_named_property(env, o, key, &v);
+    double d;
+    if (napi_get_value_double(env, v, &d) != napi_ok) { arg_error(env, key, 1, "a number"); return false; }
+    *out = (float)d;
+    return true;
+}
+
+// qwen3_create(ctx, {layers, hidden, intermediate, n_heads, n_kv_heads, head_dim, vocab,
+//                    rope_theta, rms_eps, max_ctx, max_tokens})
+napi_value js_qwen3_create(napi_env env, napi_callback_info info) {
+    Args a(env, info);
+    if (!want_args(env, a, 2, "qwen3_create")) return nullptr;
+    CtxH* c = get_ctx(env, a.v[0], "qwen3_create");
+    if (!c) return nullptr;
+    ti_qwen3_config cfg;
+    std::memset(&cfg, 0, sizeof cfg);
+    napi_value o = a.v[1];
+    if (!cfg_int(env, o, "layers", &cfg.layers, true, 0) || !cfg_int(env, o, "hidden", &cfg.hidden, true, 0) ||
+        !cfg_int(env, o, "intermediate", &cfg.intermediate, true, 0) || !cfg_int(env, o, "n_heads", &cfg.n_heads, true, 0) ||
+        !cfg_int(env, o, "n_kv_heads", &cfg.n_kv_heads, true, 0) || !cfg_int(env, o, "head_dim", &cfg.head_dim, true, 0) ||
+        !cfg_int(env, o, "vocab", &cfg.vocab, true, 0) || !cfg_float(env, o, "rope_theta", &cfg.rope_theta, 1000000.0f) ||
+        !cfg_float(env, o, "rms_eps", &cfg.rms_eps, 1e-6f) || !cfg_int(env, o, "max_ctx", &cfg.max_ctx, false, 4096) ||
+        !cfg_int(env, o, "max_tokens", &cfg.max_tokens, false, 256))
+        return nullptr;
+    ti_qwen3* m = nullptr;
+    const int rc = ti_qwen3_create(c->c, &cfg, &m);
+    if (rc) return throw_ti(env, "qwen3_create", rc);
+    ModelH* h = new ModelH;
+    h->ctx = c;
+    c->refs++;
+    h->m = m;
+    napi_value out;
+    napi_create_external(env, h, fin_model, nullptr, &out);
+    return out;
+}
+
+ModelH* get_model(napi_env env, napi_value v, const char* fn, size_t i) {
+    ModelH* m = handle_of<ModelH>(env, v, TAG_MODEL);
+    if (!m || !m->m) { arg_error(env, fn, i, "a live model from qwen3_create()"); return nullptr; }
+    if (m->ctx->closed) { throw_msg(env, std::string(fn) + ": the model's context was shut down"); return nullptr; }
+    return m;
+}
+
+napi_value js_qwen3_destroy(napi_env env, napi_callback_info info) {
+    Args a(env, info);
+    ModelH* m = a.n == 1 ? get_model(env, a.v[0], "qwen3_destroy", 0) : nullptr;
+    if (!m) return a.n == 1 ? nullptr : throw_msg(env, "qwen3_destroy expects (model)");
+    const int rc = ti_qwen3_destroy(m->ctx->c, m->m);
+    m->m = nullptr;
+    return rc ? throw_ti(env, "qwen3_destroy", rc) : undefined(env);
+}
+
+// qwen3_tensor(model, name) -> {data, dataBytes, scales|null, scaleBytes}
+napi_value js_qwen3_tensor(napi_env env, napi_callback_info info) {
+    Args a(env, info);
+    if (!want_args(env, a, 2, "qwen3_tensor")) return nullptr;
+    ModelH* m = get_model(env, a.v[0], "qwen3_tensor", 0);
+    if (!m) return nullptr;
+    char name[256];
+    size_t nl;
+    if (napi_get_value_string_utf8(env, a.v[1], name, sizeof name, &nl) != napi_ok) return arg_error(env, "qwen3_tensor", 1, "a string"), nullptr;
+    void *d = nullptr, *s = nullptr;
+    size_t db = 0, sb = 0;
+    const int rc = ti_qwen3_tensor(m->m, name, &d, &db, &s, &sb);
+    if (rc) return throw_ti(env, "qwen3_tensor", rc);
+    napi_value o, nul;
+    napi_create_object(env, &o);
+    napi_get_null(env, &nul);
+    napi_set_named_property(env, o, "data", make_buf(env, m->ctx, d, db, false, a.v[0]));
+    napi_set_named_property(env, o, "dataBytes", num(env, (double)db));
+    napi_set_named_property(env, o, "scales", s ? make_buf(env, m->ctx, s, sb, false, a.v[0]) : nul);
+    napi_set_named_property(env, o, "scaleBytes", num(env, (double)sb));
+    return o;
+}
+
+// qwen3_kv(model, layer) -> {kq, ks, vq, vs}
+napi_value js_qwen3_kv(napi_env env, napi_callback_info info) {
+    Args a(env, info);
+    if (!want_args(env, a, 2, "qwen3_kv")) return nullptr;
+    ModelH* m = get_model(env, a.v[0], "qwen3_kv", 0);
+    int64_t layer;
+    if (!m || !get_i64(env, a.v[1], &layer, "qwen3_kv", 1)) return nullptr;
+    uint32_t *kq, *vq;
+    float *ks, *vs;
+    const int rc = ti_qwen3_kv(m->m, (int)layer, &kq, &ks, &vq, &vs);
+    if (rc) return throw_ti(env, "qwen3_kv", rc);
+    napi_value o;
+    napi_create_object(env, &o);
+    napi_set_named_property(env, o, "kq", make_buf(env, m->ctx, kq, 0, false, a.v[0]));
+    napi_set_named_property(env, o, "ks", make_buf(env, m->ctx, ks, 0, false, a.v[0]));
+    napi_set_named_property(env, o, "vq", make_buf(env, m->ctx, vq, 0, false, a.v[0]));
+    napi_set_named_property(env, o, "vs", make_buf(env, m->ctx, vs, 0, false, a.v[0]));
+    return o;
+}
+
+napi_value js_qwen3_logits(napi_env env, napi_callback_info info) {
+    Args a(env, info);
+    ModelH* m = a.n == 1 ? get_model(env, a.v[0], "qwen3_logits", 0) : nullptr;
+    if (!m) return a.n == 1 ? nullptr : throw_msg(env, "qwen3_logits expects (model)");
+    float* l = nullptr;
+    const int rc = ti_qwen3_logits(m->m, &l);
+    return rc ? throw_ti(env, "qwen3_logits", rc) : make_buf(env, m->ctx, l, 0, false, a.v[0]);
+}
+
+bool host_i32(napi_env env, napi_value v, const int32_t** data, size_t* n, const char* fn, size_t i) {
+    bool is;
+    napi_is_typedarray(env, v, &is);
+    if (!is) return arg_error(env, fn, i, "an Int32Array");
+    napi_typedarray_type t;
+    void* d;
+    napi_value ab;
+    size_t off;
+    napi_get_typedarray_info(env, v, &t, n, &d, &ab, &off);
+    if (t != napi_int32_array) return arg_error(env, fn, i, "an Int32Array");
+    *data = static_cast<const int32_t*>(d);
+    return true;
+}
+
+// qwen3_forward(ctx, model, ids: Int32Array | null, T, pos)
+napi_value js_qwen3_forward(napi_env env, napi_callback_info info) {
+    const char* fn = "qwen3_forward";
+    Args a(env, info);
+    if (!want_args(env, a, 5, fn)) return nullptr;
+    CtxH* c = get_ctx(env, a.v[0], fn);
+    ModelH* m = c ? get_model(env, a.v[1], fn, 1) : nullptr;
+    int64_t T, pos;
+    if (!m || !get_i64(env, a.v[3], &T, fn, 3) || !get_i64(env, a.v[4], &pos, fn, 4)) return nullptr;
+    const int32_t* ids = nullptr;
+    if (!is_nullish(env, a.v[2])) {
+        size_t n;
+        if (!host_i32(env, a.v[2], &ids, &n, fn, 2)) return nullptr;
+        if ((int64_t)n < T) return throw_msg(env, "qwen3_forward: ids holds fewer than T tokens");
+    }
+    const int rc = ti_qwen3_forward(c->c, m->m, ids, (int)T, (int)pos);
+    return rc ? throw_ti(env, fn, rc) : undefined(env);
+}
+
+napi_value js_qwen3_decode(napi_env env, napi_callback_info info) {
+    Args a(env, info);
+    if (!want_args(env, a, 2, "qwen3_decode")) return nullptr;
+    CtxH* c = get_ctx(env, a.v[0], "qwen3_decode");
+    ModelH* m = c ? get_model(env, a.v[1], "qwen3_decode", 1) : nullptr;
+    if (!m) return nullptr;
+    const int rc = ti_qwen3_decode(c->c, m->m);
+    return rc ? throw_ti(env, "qwen3_decode", rc) : undefined(env);
+}
+
+napi_value js_qwen3_set_pos(napi_env env, napi_callback_info info) {
+    Args a(env, info);
+    if (!want_args(env, a, 3, "qwen3_set_pos")) return nullptr;
+    CtxH* c = get_ctx(env, a.v[0], "qwen3_set_pos");
+    ModelH* m = c ? get_model(env, a.v[1], "qwen3_set_pos", 1) : nullptr;
+    int64_t pos;
+    if (!m || !get_i64(env, a.v[2], &pos, "qwen3_set_pos", 2)) return nullptr;
+    const int rc = ti_qwen3_set_pos(c->c, m->m, (int)pos);
+    return rc ? throw_ti(env, "qwen3_set_pos", rc) : undefined(env);
+}
+
+// qwen3_write_tokens(ctx, model, from, ids: Int32Array)
+napi_value js_qwen3_write_tokens(napi_env env, napi_callback_info info) {
+    const char* fn = "qwen3_write_tokens";
+    Args a(env, info);
+    if (!want_args(env, a, 4, fn)) return nullptr;
+    CtxH* c = get_ctx(env, a.v[0], fn);
+    ModelH* m = c ? get_model(env, a.v[1], fn, 1) : nullptr;
+    int64_t from;
+    const int32_t* ids;
+    size_t n;
+    if (!m || !get_i64(env, a.v[2], &from, fn, 2) || !host_i32(env, a.v[3], &ids, &n, fn, 3)) return nullptr;
+    const int rc = ti_qwen3_write_tokens(c->c, m->m, (int)from, (int)n, ids);
+    return rc ? throw_ti(env, fn, rc) : undefined(env);
+}
+
+// qwen3_read_tokens(ctx, model, from, count) -> Int32Array
+napi_value js_qwen3_read_tokens(napi_env env, napi_callback_info info) {
+    const char* fn = "qwen3_read_tokens";
+    Args a(env, info);
+    if (!want_args(env, a, 4, fn)) return nullptr;
+    CtxH* c = get_ctx(env, a.v[0], fn);
+    ModelH* m = c ? get_model(env, a.v[1], fn, 1) : nullptr;
+    int64_t from, count;
+    if (!m || !get_i64(env, a.v[2], &from, fn, 2) || !get_i64(env, a.v[3], &count, fn, 3)) return nullptr;
+    if (count < 0 || count > (1 << 26)) return throw_msg(env, "qwen3_read_tokens: bad count");
+    void* data;
+    napi_value ab, arr;
+    napi_create_arraybuffer(env, (size_t)count * 4, &data, &ab);
+    const int rc = ti_qwen3_read_tokens(c->c, m->m, (int)from, (int)count, static_cast<int32_t*>(data));
+    if (rc) return throw_ti(env, fn, rc);
+    napi_create_typedarray(env, napi_int32_array, (size_t)count, ab, 0, &arr);
+    return arr;
+}
+
+#define FN(js, f) {js, nullptr, f, nullptr, nullptr, nullptr, napi_enumerable, nullptr}
+#define ENTRY(js, fn)                                                                                 \
+    {js, nullptr, [](napi_env e, napi_callback_info i) -> napi_value { return call_entry(e, i, #fn, fn); }, \
+     nullptr, nullptr, nullptr, napi_enumerable, nullptr}
+
+napi_value module_init(napi_env env, napi_value exports) {
+    const napi_property_descriptor props[] = {
+        FN("version", js_version),
+        FN("last_error", js_last_error),
+        FN("device_count", js_device_count),
+        FN("init", js_init),
+        FN("shutdown", js_shutdown),
+        FN("buf_alloc", js_buf_alloc),
+        FN("buf_free", js_buf_free),
+        FN("buf_view", js_buf_view),
+        FN("buf_bytes", js_buf_bytes),
+        FN("buf_write", js_buf_write),
+        FN("buf_read", js_buf_read),
+        ENTRY("buf_copy", ti_buf_copy),
+        ENTRY("buf_fill_u32", ti_buf_fill_u32),
+        ENTRY("sync", ti_sync),
+        FN("sync_async", js_sync_async),
+        ENTRY("graph_begin", ti_graph_begin),
+        FN("graph_end", js_graph_end),
+        FN("graph_launch", js_graph_launch),
+        FN("graph_destroy", js_graph_destroy),
+        ENTRY("event_record", ti_event_record),
+        FN("event_elapsed_ms", js_event_elapsed_ms),
+        // int4 weights, activations, GEMV / GEMM
+        ENTRY("quant_int4_bf16", ti_quant_int4_bf16),
+        ENTRY("quant_act_q8", ti_quant_act_q8),
+        ENTRY("quant_act_q8_t", ti_quant_act_q8_t),
+        ENTRY("rmsnorm_q8", ti_rmsnorm_q8),
+        ENTRY("rmsnorm", ti_rmsnorm),
+        ENTRY("gemv_q4_q8", ti_gemv_q4_q8),
+        ENTRY("gemv_q4_f32", ti_gemv_q4_f32),
+        ENTRY("gateup_silu_q4", ti_gateup_silu_q4),
+        ENTRY("linear_q4", ti_linear_q4),
+        ENTRY("group_dots_q4_q8", ti_group_dots_q4_q8),
+        FN("rmsnorm_gemv_q4", js_rmsnorm_gemv_q4),
+        ENTRY("rmsnorm_gateup_silu_q4", ti_rmsnorm_gateup_silu_q4),
+        ENTRY("rmsnorm_lm_head_argmax", ti_rmsnorm_lm_head_argmax),
+        ENTRY("argmax", ti_argmax),
+        ENTRY("embed", ti_embed),
+        // attention over the int8 KV cache
+        ENTRY("attn_prep_q8", ti_attn_prep_q8),
+        ENTRY("attn_decode_q8", ti_attn_decode_q8),
+        ENTRY("attn_step_q8", ti_attn_step_q8),
+        ENTRY("rope_qk", ti_rope_qk),
+        ENTRY("kv_write_q8", ti_kv_write_q8),
+        ENTRY("attn_causal_q8", ti_attn_causal_q8),
+        // ternary
+        ENTRY("tern_gemv", ti_tern_gemv),
+        ENTRY("tern_gemm", ti_tern_gemm),
+        ENTRY("quant_act_tern", ti_quant_act_tern),
+        ENTRY("tern_block_dots", ti_tern_block_dots),
+        // int3 MoE
+        ENTRY("requant43", ti_requant43),
+        ENTRY("router", ti_router),
+        ENTRY("moe_gemv_q3", ti_moe_gemv_q3),
+        ENTRY("moe_gemm_q3", ti_moe_gemm_q3),
+        ENTRY("swiglu", ti_swiglu),
+        ENTRY("moe_combine", ti_moe_combine),
+        // Qwen3 decoder
+        FN("qwen3_create", js_qwen3_create),
+        FN("qwen3_destroy", js_qwen3_destroy),
+        FN("qwen3_tensor", js_qwen3_tensor),
+        FN("qwen3_kv", js_qwen3_kv),
+        FN("qwen3_logits", js_qwen3_logits),
+        FN("qwen3_forward", js_qwen3_forward),
+        FN("qwen3_decode", js_qwen3_decode),
+        FN("qwen3_set_pos", js_qwen3_set_pos),
+        FN("qwen3_write_tokens", js_qwen3_write_tokens),
+        FN("qwen3_read_tokens", js_qwen3_read_tokens),
+    };
+    napi_define_properties(env, exports, sizeof props / sizeof props[0], props);
+    return exports;
+}
+
+}  // namespace
+
+NAPI_MODULE(NODE_GYP_MODULE_NAME, module_init)

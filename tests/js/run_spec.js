@@ -1,0 +1,91 @@
+'use strict';
+// Drives the JS host from a spec written by the Python tests:
+//   node tests/js/run_spec.js <dir>
+// <dir>/spec.json:
+//   buffers: {name: {file: "x.bin"} | {bytes: n}}            device buffers (files are raw bytes)
+//   calls:   [{fn: "L.gemvDP4_only", args: [...]}, {read: name, bytes, out}, {read_dp4: "xq", bytes, out}]
+//            an argument is a number/boolean/null, {buf: name}, {rec: {pack, scales, N, K}},
+//            {kv: {kq, ks, vq, vs}}, {emb: {buf, vocab}} or {rec3: {pack, scales, nE}}
+//   model:   {config, nCtx, safetensors, prompt, maxTokens, dump: [tensor names]}   (optional)
+// Writes <dir>/result.json (and the files named by `read`).
+const fs = require('fs');
+const path = require('path');
+const { createQwen3Host } = require(path.join(__dirname, '..', '..', 'tabinfer_amd', 'host', 'qwen3-host.js'));
+
+async function main() {
+  const dir = process.argv[2];
+  const spec = JSON.parse(fs.readFileSync(path.join(dir, 'spec.json'), 'utf8'));
+  const host = createQwen3Host({ device: 0 });
+  const { E, L, Tern, Moe, _dp4 } = host.engine;
+  const groups = { L, Tern, Moe };
+  const bufs = {};
+  const result = { calls: 0 };
+  for (const [name, b] of Object.entries(spec.buffers || {})) {
+    if (b.file) {
+      const data = fs.readFileSync(path.join(dir, b.file));
+      bufs[name] = E.createBuffer(data.length);
+      E.writeBuffer(bufs[name], 0, new Uint8Array(data.buffer, data.byteOffset, data.length));
+    } else {
+      bufs[name] = E.createBuffer(b.bytes);
+      E.fillU32(bufs[name], 0, Math.ceil(b.bytes / 4));
+    }
+  }
+  const B = (n) => { if (!(n in bufs)) throw new Error('spec: no buffer ' + n); return bufs[n]; };
+  const arg = (a) => {
+    if (a === null || typeof a !== 'object') return a;
+    if ('buf' in a) return B(a.buf);
+    if ('rec' in a) return { pack: B(a.rec.pack), scales: B(a.rec.scales), N: a.rec.N, K: a.rec.K };
+    if ('kv' in a) return { kq: B(a.kv.kq), ks: B(a.kv.ks), vq: B(a.kv.vq), vs: B(a.kv.vs) };
+    if ('emb' in a) return { buf: B(a.emb.buf), vocab: a.emb.vocab };
+    if ('rec3' in a) return { pack: B(a.rec3.pack), scales: B(a.rec3.scales), nE: a.rec3.nE };
+    throw new Error('spec: bad argument ' + JSON.stringify(a));
+  };
+  for (const c of spec.calls || []) {
+    if (c.fn) {
+      const [g, f] = c.fn.split('.');
+      if (!groups[g] || typeof groups[g][f] !== 'function') throw new Error('spec: no launcher ' + c.fn);
+      groups[g][f](...c.args.map(arg));
+      result.calls++;
+    } else if (c.read) {
+      fs.writeFileSync(path.join(dir, c.out), Buffer.from(E.readBytes(B(c.read), c.offset || 0, c.bytes)));
+    } else if (c.read_dp4) {
+      fs.writeFileSync(path.join(dir, c.out), Buffer.from(E.readBytes(_dp4[c.read_dp4], 0, c.bytes)));
+    }
+  }
+  if (spec.model) {
+    const m = spec.model;
+    await host.loadModel({ config: m.config, nCtx: m.nCtx, safetensors: m.safetensors });
+    result.forward = await host.forward(m.prompt, 0);
+    const gen = await host.generate(m.prompt, { maxTokens: m.maxTokens });
+    result.generate = Array.from(gen);
+    result.dumps = {};
+    for (const name of m.dump || []) {
+      const t = E.TI.qwen3_tensor(host.model(), name);
+      const d = Buffer.from(E.readBytes(t.data, 0, t.dataBytes));
+      const s = t.scales ? Buffer.from(E.readBytes(t.scales, 0, t.scaleBytes)) : null;
+      fs.writeFileSync(path.join(dir, name + '.data'), d);
+      if (s) fs.writeFileSync(path.join(dir, name + '.scales'), s);
+      result.dumps[name] = !!s;
+    }
+    const events = [];
+    m.chat && (await runChat(host, m, events));
+    result.events = events;
+  }
+  E.sync();
+  fs.writeFileSync(path.join(dir, 'result.json'), JSON.stringify(result));
+  host.shutdown();
+}
+
+// a toy tokenizer over raw ids: encodeChat joins the messages' id lists
+async function runChat(host, m, events) {
+  const tok = {
+    encodeChat: (msgs) => [].concat(...msgs.map((x) => x.content.split(' ').map(Number))),
+    decode: (ids) => ids.map((i) => '<' + i + '>').join(''),
+    isStop: (id) => id === m.chat.stop,
+  };
+  await host.loadModel({ config: m.config, nCtx: m.nCtx, safetensors: m.safetensors, tokenizer: tok, reload: true });
+  await host.runConversation({ provider: { maxTokens: m.maxTokens }, messages: [{ role: 'user', content: m.prompt.join(' ') }] },
+    (ev) => events.push(ev));
+}
+
+main().catch((e) => { console.error(e && e.stack ? e.stack : e); process.exit(1); });

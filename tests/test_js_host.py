@@ -1,0 +1,106 @@
+"""CPU checks of the JavaScript host (tabinfer_amd/host): the N-API addon loads without a
+GPU and exports every entry point of include/ti.h; its two f32 -> f16 converters equal the
+oracle's restatements of models/qwen3.js:3357-3374 and engine/webgpu-engine.js:217-236
+bit for bit; the safetensors reader parses a file written here; bad handles and a missing
+device are JS exceptions."""
+import json
+import os
+import shutil
+import struct
+import subprocess
+
+import numpy as np
+import pytest
+
+from tabinfer_amd import abi
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ADDON = os.path.join(ROOT, "tabinfer_amd", "host", "tabinfer.node")
+NODE = shutil.which("node")
+
+pytestmark = pytest.mark.skipif(NODE is None, reason="node is not installed")
+
+
+def write_safetensors(path, tensors):
+    """tensors: name -> (dtype string, shape, raw bytes)."""
+    hdr, off, blobs = {}, 0, []
+    for name, (dt, shape, raw) in tensors.items():
+        hdr[name] = {"dtype": dt, "shape": list(shape), "data_offsets": [off, off + len(raw)]}
+        off += len(raw)
+        blobs.append(raw)
+    h = json.dumps(hdr).encode()
+    h += b" " * (-len(h) % 8)
+    with open(path, "wb") as f:
+        f.write(struct.pack("<Q", len(h)))
+        f.write(h)
+        for b in blobs:
+            f.write(b)
+
+
+def f32_sweep(rng):
+    edge = np.array([0.0, -0.0, 1.0, -1.0, 65504.0, 65520.0, 65519.996, 1e-8, -1e-8, 6.1e-5, 5.96e-8, 2.98e-8,
+                     2.9802322e-08, 8.940697e-08, np.inf, -np.inf, np.nan, 1e30, -3.0e38, 0.33325195, 0.3334961],
+                    np.float32)
+    # f16 rounding boundaries: the midpoints between neighbouring f16 values, and one ulp either side
+    h = rng.integers(0, 0x7bff, 4000).astype(np.uint16)
+    lo = h.view(np.float16).astype(np.float32)
+    hi = (h + 1).view(np.float16).astype(np.float32)
+    mid = ((lo.astype(np.float64) + hi.astype(np.float64)) / 2).astype(np.float32)
+    near = np.concatenate([mid, np.nextafter(mid, np.float32(np.inf)), np.nextafter(mid, np.float32(-np.inf))])
+    rnd = rng.integers(0, 2 ** 32, 20000, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    return np.concatenate([edge, near, -near, rnd]).astype(np.float32)
+
+
+@pytest.fixture(scope="module")
+def checks(tmp_path_factory):
+    if not os.path.exists(ADDON):
+        pytest.fail("tabinfer.node is not built: run python -m tabinfer_amd.build")
+    d = tmp_path_factory.mktemp("jscpu")
+    vals = f32_sweep(np.random.default_rng(3))
+    vals.tofile(str(d / "f32.bin"))
+    write_safetensors(str(d / "tiny.safetensors"), {
+        "a.weight": ("BF16", (2, 3), np.arange(6, dtype=np.uint16).tobytes()),
+        "b": ("F32", (4,), np.ones(4, np.float32).tobytes()),
+    })
+    r = subprocess.run([NODE, os.path.join(ROOT, "tests", "js", "cpu_checks.js"), str(d)],
+                       stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout
+    out = json.load(open(str(d / "out.json")))
+    return vals, out
+
+
+def test_addon_exports_every_entry_point(checks):
+    _, out = checks
+    want = {n[len("ti_"):] for n in abi.header_functions()}
+    missing = sorted(want - set(out["exports"]))
+    assert not missing, missing
+    assert out["version"] == abi.lib().ti_version()
+
+
+def test_js_f16_converters_match_the_oracle(checks, orc):
+    vals, out = checks
+    q3 = np.array([orc.f32_to_f16_q3(v) for v in vals])
+    en = np.array([orc.f32_to_f16_eng(v) for v in vals])
+    assert np.array_equal(np.array(out["f16_q3"]), q3)
+    assert np.array_equal(np.array(out["f16_eng"]), en)
+    # the two converters do differ (ties), so the comparison above can tell them apart
+    assert np.any(q3 != en)
+    bf = (vals.view(np.uint32) >> 16).astype(np.uint32)
+    want = np.array([orc.f32_to_f16_q3(np.uint32(b << 16).view(np.float32)) for b in bf])
+    assert np.array_equal(np.array(out["bf16_to_f16"]), want)
+
+
+def test_safetensors_header(checks):
+    _, out = checks
+    h = out["header"]
+    assert h["a.weight"]["dtype"] == "BF16" and h["a.weight"]["shape"] == [2, 3]
+    assert h["b"]["end"] - h["b"]["begin"] == 16
+    assert h["b"]["begin"] == h["a.weight"]["end"]
+
+
+def test_errors_are_exceptions(checks):
+    _, out = checks
+    assert out["ctxError"].startswith("TypeError") and "context" in out["ctxError"]
+    if abi.device_count() == 0:
+        assert out["initError"]["code"] == abi.TI_ERR_NO_DEVICE
+        assert "no HIP device" in out["initError"]["message"]
