@@ -157,7 +157,8 @@ int ti_attn_decode_q8(ti_ctx* ctx, const float* qr, const uint32_t* kq, const fl
  * projections [nHq*hd], [nKv*hd], [nKv*hd]; k and v are written into cache row pos;
  * out[nHq*hd] is the attention over positions 0..pos; out_q/out_s (both or neither)
  * receive it quantized per 32 (quantQ8, for o_proj's linearQ). max_splits workgroups
- * per KV head (0 = the default, 32; at most 64). Covers hd 64/128 with nHq/nKv <= 2. */
+ * per KV head (0 = the default: 32, or 64 for caches over 16384 positions; at most 64).
+ * Covers hd 64/128 with nHq/nKv <= 2. */
 int ti_attn_step_q8(ti_ctx* ctx, const float* q, const float* k, const float* v,
                     const uint16_t* qn_w, const uint16_t* kn_w, uint32_t* kq, float* ks,
                     uint32_t* vq, float* vs, float* out, int nHq, int nKv, int hd, int pos, int cap,

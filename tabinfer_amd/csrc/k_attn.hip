@@ -501,7 +501,10 @@ extern "C" int ti_kv_write_q8(ti_ctx* c, const float* kr, const float* v, uint32
 // ---------------------------------------------------------------------------
 namespace {
 constexpr int ATTF_MAXS = 64;
-constexpr int ATTF_DEFAULT_SPLITS = 32;   // measured best over 1k..32k contexts on MI355X
+// default workgroups per KV head, by cache capacity (the split count is fixed when a
+// decode step is captured, the context length is not): measured on MI355X, 32 is best
+// for contexts up to ~16k, 64 beyond (more waves streaming the keys)
+constexpr int ATTF_SPLITS_SHORT = 32, ATTF_SPLITS_LONG = 64, ATTF_LONG_CAP = 16384;
 
 struct AttnFArgs {
     const float* q;
@@ -535,8 +538,8 @@ struct AttnFArgs {
 // reference's reduction order — slot j and j+64, then a 32..1 tree — with the last
 // levels as a wave butterfly (a pair's float sum is the same in either order), then
 // split-half RoPE with the given cos/sin row. red/rk: this head's 128-float slices.
-__device__ __forceinline__ float head_norm_rope(float x, int j, int hd, const uint16_t* __restrict__ w, const float* cs,
-                                               float eps, float* red, float* rk, float* tot) {
+__device__ __forceinline__ float head_norm_rope(float x, int j, int hd, float wj, const float* cs, float eps, float* red,
+                                               float* rk, float* tot) {
     const float sq = j < hd ? x * x : 0.0f;
     red[j] = sq;
     __syncthreads();
@@ -551,7 +554,7 @@ __device__ __forceinline__ float head_norm_rope(float x, int j, int hd, const ui
     float m = *tot / (float)hd;
     m = m + eps;
     const float inv = 1.0f / sqrtf(m);
-    if (j < hd) { float t = x * inv; rk[j] = t * ti_h2f(w[j]); }
+    if (j < hd) { float t = x * inv; rk[j] = t * wj; }
     __syncthreads();
     float out = 0.0f;
     if (j < hd) {
@@ -581,20 +584,24 @@ __global__ __launch_bounds__(256, 2) void k_attn_fused_q8(AttnFArgs a) {
     __shared__ float rk[256];
     __shared__ float tot[2];
     __shared__ float s_q[G][HD];
-    __shared__ float s_row[2][HD];
     __shared__ __align__(16) uint32_t s_kw[HD / 4];
     __shared__ __align__(16) uint32_t s_vw[HD / 4];
     __shared__ float s_ksc[NG], s_vsc[NG];
-    __shared__ float s_acc[4][G * HD];
+    __shared__ __align__(16) float s_red[4][TPW][G * HD];
     __shared__ float s_wml[4][G][2];
     __shared__ float s_ml[G][ATTF_MAXS][2];
+    __shared__ float s_e[G][ATTF_MAXS];
+    __shared__ float s_L[G];
     __shared__ float rope_cs[HD];
     __shared__ int s_last;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
-    const int hk = blockIdx.x % a.nKv;
-    const int w = blockIdx.x / a.nKv;
+    // split-major across the XCDs (workgroup i runs on XCD i % 8): the NS/8 splits of an
+    // XCD are the same for every KV head, so one position's scale line (all heads' groups,
+    // 128 B) is fetched into one XCD's L2 and shared by the 8 head workgroups, not into 8
+    const int w = blockIdx.x % a.ns;
+    const int hk = blockIdx.x / a.ns;
     const int NS = a.ns;
     const int NW = NS * 4;                     // waves per KV head
     const int gw = w * 4 + wave;               // this wave's index among them
@@ -613,6 +620,9 @@ __global__ __launch_bounds__(256, 2) void k_attn_fused_q8(AttnFArgs a) {
     const float qx = a.q[(size_t)(hk * G + (h < G ? h : 0)) * HD + (j < HD ? j : 0)];
     const float kx = a.k[(size_t)hk * HD + (j < HD ? j : 0)];
     const float vx = a.v[(size_t)hk * HD + (j < HD ? j : 0)];
+    // the norm weights too: a load issued after the tiles' would wait for them (vmcnt is in order)
+    const float qwj = ti_h2f(a.qw[j < HD ? j : 0]);
+    const float kwj = ti_h2f(a.kw[j < HD ? j : 0]);
     uint4 kw[2][PASSES], vw[2][PASSES];
     float ksc[2][PASSES], vsc[2][PASSES];
     int lim = a.cap;                           // clamp bound until the context is known
@@ -641,29 +651,33 @@ __global__ __launch_bounds__(256, 2) void k_attn_fused_q8(AttnFArgs a) {
     if (tid < HD) rope_cs[tid] = csj;
     {   // query heads (the first barrier inside publishes rope_cs)
         const float x = (h < G && j < HD) ? qx : 0.0f;
-        const float r = head_norm_rope(x, j, HD, a.qw, rope_cs, a.eps, red + h * 128, rk + h * 128, tot + h);
+        const float r = head_norm_rope(x, j, HD, qwj, rope_cs, a.eps, red + h * 128, rk + h * 128, tot + h);
         if (h < G && j < HD) s_q[h][j] = r;
     }
     if (has_pos) {   // this token's K (normed, roped) and V rows, snorm int8, into the cache and LDS
         const float x = (h == 0 && j < HD) ? kx : 0.0f;
-        const float r = head_norm_rope(x, j, HD, a.kw, rope_cs, a.eps, red + h * 128, rk + h * 128, tot + h);
-        if (j < HD) s_row[h][j] = h == 0 ? r : vx;
-        __syncthreads();
-        if (tid < 2 * NG) {
-            const int which = tid / NG, g = tid % NG;
-            float vals[32];
+        const float r = head_norm_rope(x, j, HD, kwj, rope_cs, a.eps, red + h * 128, rk + h * 128, tot + h);
+        // one element per lane, a 32-group = 32 lanes of one wave: group max by shuffles,
+        // the code of each element (snorm_code), 4 codes packed by the group's lanes
+        const float val = h == 0 ? r : vx;
+        float mx = j < HD ? fabsf(val) : 0.0f;
 #pragma unroll
-            for (int i = 0; i < 32; i++) vals[i] = s_row[which][g * 32 + i];
-            uint32_t wds[8];
-            float scl;
-            snorm_group(vals, wds, &scl);
-            uint32_t* dq = (which ? a.vq : a.kq) + ((size_t)pos * a.nKv + hk) * (HD / 4) + g * 8;
-            float* ds = (which ? a.vs : a.ks) + ((size_t)pos * a.nKv + hk) * NG + g;
-            uint32_t* lw = which ? s_vw : s_kw;
-#pragma unroll
-            for (int q = 0; q < 8; q++) { dq[q] = wds[q]; lw[g * 8 + q] = wds[q]; }
-            *ds = scl;
-            (which ? s_vsc : s_ksc)[g] = scl;
+        for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+        mx = fmaxf(mx, 1e-12f);
+        const uint32_t code = snorm_code(val, mx);
+        const int src = lane & ~3;
+        const uint32_t word = __shfl(code, src, 64) | (__shfl(code, src + 1, 64) << 8) |
+                              (__shfl(code, src + 2, 64) << 16) | (__shfl(code, src + 3, 64) << 24);
+        if (j < HD) {
+            const size_t rowq = ((size_t)pos * a.nKv + hk) * (HD / 4), rows = ((size_t)pos * a.nKv + hk) * NG;
+            if ((j & 3) == 0) {
+                (h ? a.vq : a.kq)[rowq + j / 4] = word;
+                (h ? s_vw : s_kw)[j / 4] = word;
+            }
+            if ((j & 31) == 0) {
+                (h ? a.vs : a.ks)[rows + j / 32] = mx;
+                (h ? s_vsc : s_ksc)[j / 32] = mx;
+            }
         }
     }
     __syncthreads();
@@ -778,35 +792,37 @@ __global__ __launch_bounds__(256, 2) void k_attn_fused_q8(AttnFArgs a) {
         t0 = nt;
     }
 
-    // wave state -> LDS: acc summed over the wave's token slots, the +128 offset removed
+    // wave state -> LDS, one row per token slot with the +128 offset removed (a shuffle
+    // tree over the slots costs more than the 32 LDS reads of the merge below)
 #pragma unroll
     for (int hh = 0; hh < G; hh++) {
+        float4* dst = reinterpret_cast<float4*>(&s_red[wave][tp][hh * HD + sl * 16]);
+        const float off = 128.0f * pws[hh];
 #pragma unroll
-        for (int o = LPT; o < 64; o <<= 1) {
-            pws[hh] += __shfl_xor(pws[hh], o, 64);
-#pragma unroll
-            for (int i = 0; i < 16; i++) acc[hh][i] += __shfl_xor(acc[hh][i], o, 64);
-        }
-        if (tp == 0) {
-#pragma unroll
-            for (int i = 0; i < 16; i++) s_acc[wave][hh * HD + sl * 16 + i] = acc[hh][i] - 128.0f * pws[hh];
-        }
+        for (int i = 0; i < 4; i++)
+            dst[i] = make_float4(acc[hh][4 * i] - off, acc[hh][4 * i + 1] - off, acc[hh][4 * i + 2] - off,
+                                 acc[hh][4 * i + 3] - off);
         if (lane == 0) {
             s_wml[wave][hh][0] = m_run[hh];
             s_wml[wave][hh][1] = l_run[hh];
         }
     }
     __syncthreads();
-    // merge the 4 waves into this split's partial and publish it
+    // merge the 4 waves x TPW slots into this split's partial and publish it
     const size_t ms = (size_t)NS;
-    for (int o = tid; o < G * HD; o += 256) {
-        const int hh = o / HD, d = o % HD;
+    if (tid < G * HD) {
+        const int hh = tid / HD, d = tid % HD;
         float M = s_wml[0][hh][0];
 #pragma unroll
         for (int q = 1; q < 4; q++) M = fmaxf(M, s_wml[q][hh][0]);
         float O = 0.0f;
 #pragma unroll
-        for (int q = 0; q < 4; q++) O += s_acc[q][o] * expf(s_wml[q][hh][0] - M);
+        for (int q = 0; q < 4; q++) {
+            float sq = 0.0f;
+#pragma unroll
+            for (int t = 0; t < TPW; t++) sq += s_red[q][t][tid];
+            O += sq * expf(s_wml[q][hh][0] - M);
+        }
         ti_pub_store(a.po + ((size_t)(hk * G + hh) * ms + w) * HD + d, O);
     }
     if (tid < G) {
@@ -827,35 +843,38 @@ __global__ __launch_bounds__(256, 2) void k_attn_fused_q8(AttnFArgs a) {
     // the last split of hk: log-sum-exp over the splits that saw a tile; the o loads
     // are issued before the (m, l) pairs are reduced, one round trip for both
     const int nused = ntiles < NW ? (ntiles + 3) / 4 : NS;
-    constexpr int OC = 16;                         // o values in flight per thread
-    float ov[OC];
+    // every split's o in one round trip (indices past nused repeat the last one and get
+    // weight 0), then the splits' weights once per head: one wave per head, lane = split
+    float ov[ATTF_MAXS];
     const int oh = tid / HD, od = tid % HD;
     const float* pp = a.po + (size_t)(hk * G + (oh < G ? oh : 0)) * ms * HD + od;
 #pragma unroll
-    for (int i = 0; i < OC; i++) ov[i] = i < nused ? ti_pub_load(pp + (size_t)i * HD) : 0.0f;
+    for (int i = 0; i < ATTF_MAXS; i++) ov[i] = ti_pub_load(pp + (size_t)(i < nused ? i : nused - 1) * HD);
     for (int e = tid; e < G * nused * 2; e += 256) {
         const int hh = e / (nused * 2), r = e % (nused * 2);
         s_ml[hh][r >> 1][r & 1] = ti_pub_load(a.pml + ((size_t)(hk * G + hh) * ms + (r >> 1)) * 2 + (r & 1));
     }
     __syncthreads();
+    if (wave < G) {
+        const bool in = lane < nused;
+        const float m = in ? s_ml[wave][lane][0] : -3.0e38f;
+        float M = m;
+#pragma unroll
+        for (int o2 = 32; o2 > 0; o2 >>= 1) M = fmaxf(M, __shfl_xor(M, o2, 64));
+        const float e = in ? expf(m - M) : 0.0f;
+        float L = in ? s_ml[wave][lane][1] * e : 0.0f;
+#pragma unroll
+        for (int o2 = 32; o2 > 0; o2 >>= 1) L += __shfl_xor(L, o2, 64);
+        s_e[wave][lane] = e;
+        if (lane == 0) s_L[wave] = L;
+    }
+    __syncthreads();
     if (valid && tid < G * HD) {
-        float M = -3.0e38f;
-        for (int i = 0; i < nused; i++) M = fmaxf(M, s_ml[oh][i][0]);
-        float L = 0.0f, o = 0.0f;
-        for (int i0 = 0; i0 < nused; i0 += OC) {
-            if (i0 > 0) {
+        float o4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                for (int i = 0; i < OC; i++) ov[i] = i0 + i < nused ? ti_pub_load(pp + (size_t)(i0 + i) * HD) : 0.0f;
-            }
-#pragma unroll
-            for (int i = 0; i < OC; i++) {
-                if (i0 + i < nused) {
-                    const float e = expf(s_ml[oh][i0 + i][0] - M);
-                    L += s_ml[oh][i0 + i][1] * e;
-                    o += ov[i] * e;
-                }
-            }
-        }
+        for (int i = 0; i < ATTF_MAXS; i++) o4[i & 3] = fmaf(ov[i], s_e[oh][i], o4[i & 3]);
+        const float o = (o4[0] + o4[1]) + (o4[2] + o4[3]);
+        const float L = s_L[oh];
         const float res = o / L;
         const size_t e = (size_t)(hk * G + oh) * HD + od;
         a.out[e] = res;
@@ -899,7 +918,7 @@ int ti_attn_fused_launch(ti_ctx* c, const float* q, const float* k, const float*
     if (nKv > TI_SYNC_DUMMY - TI_SYNC_ATTN) return ti_fail(TI_ERR_INVALID, "fused attention: too many KV heads");
     if (hd > TI_ATTN_HD_MAX) return ti_fail(TI_ERR_INVALID, "fused attention: hd=%d > %d", hd, TI_ATTN_HD_MAX);
     if (dpos && !rope_cur) return ti_fail(TI_ERR_INVALID, "fused attention: a device position needs its rope row");
-    if (max_splits <= 0 || max_splits > ATTF_MAXS) max_splits = ATTF_DEFAULT_SPLITS;
+    if (max_splits <= 0 || max_splits > ATTF_MAXS) max_splits = cap > ATTF_LONG_CAP ? ATTF_SPLITS_LONG : ATTF_SPLITS_SHORT;
     // no more splits than the cache has wave tiles for their 4 waves
     const int wt = 4 * (64 / (hd / 16));
     const int cap_splits = (cap + 4 * wt - 1) / (4 * wt);
