@@ -396,19 +396,32 @@ def ternary(ctx, flush, reps=8):
     acts = {K: (ctx.upload(rng.integers(-127, 128, K, dtype=np.int8)), ctx.upload(np.zeros(K // 64, np.int32)))
             for K in (2048, 6144)}
     outs = {N: ctx.zeros(N * 4) for N in (1024, 2048, 6144)}
+    outs2 = {6144: ctx.zeros(6144 * 4)}
     per_layer = sum(N * K // 4 + (N * K // 64) * 4 + K + (K // 64) * 4 + N * 4 for N, K in shapes)
 
+    import ctypes as C
+    arr = lambda vals, t=C.c_void_p: (t * len(vals))(*vals)
+    outs3 = [ctx.zeros(N * 4) for N in (2048, 1024, 1024)]
+
     def issue():
+        # as a decode step launches them: q/k/v and gate/up share their activation
         for layer in sets:
-            for codes, sc, N, K in layer:
-                ctx.call("ti_tern_gemv", outs[N], codes, sc, acts[K][0], acts[K][1], N, K)
+            (qc, qs, _, _), (kc, ks, _, _), (vc, vs, _, _), (oc, os_, _, _), (gc, gs, _, _), (uc, us, _, _), (dc, ds, _, _) = layer
+            a, x = acts[2048]
+            ctx.call("ti_tern_gemv_multi", a, x, 2048, 3, arr([qc.ptr, kc.ptr, vc.ptr]), arr([qs.ptr, ks.ptr, vs.ptr]),
+                     arr([o.ptr for o in outs3]), arr([2048, 1024, 1024], C.c_int))
+            ctx.call("ti_tern_gemv", outs[2048], oc, os_, a, x, 2048, 2048)
+            ctx.call("ti_tern_gemv_multi", a, x, 2048, 2, arr([gc.ptr, uc.ptr]), arr([gs.ptr, us.ptr]),
+                     arr([outs[6144].ptr, outs2[6144].ptr]), arr([6144, 6144], C.c_int))
+            ctx.call("ti_tern_gemv", outs[2048], dc, ds, acts[6144][0], acts[6144][1], 2048, 6144)
     g = graph_of(ctx, issue)
     time_graphs(ctx, [g], 2)
     ms = cold_ms(ctx, [g], reps, flush)
     ctx.graph_destroy(g)
     us_layer = ms * 1e3 / len(sets)
     return {"layer_us": round(us_layer, 2), "bytes_per_layer": per_layer,
-            "GB_s": round(per_layer / (us_layer * 1e-6) / 1e9, 1), "launches_per_layer": len(shapes)}
+            "GB_s": round(per_layer / (us_layer * 1e-6) / 1e9, 1), "launches_per_layer": 4,
+            "launches": "q/k/v in one, o, gate/up in one, down"}
 
 
 # ---- LFM2.5-8B-A1B int3 MoE experts ------------------------------------------------------------

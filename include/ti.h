@@ -178,6 +178,11 @@ int ti_kv_write_q8(ti_ctx* ctx, const float* kr, const float* v, uint32_t* kq, f
  * multiplies by 1/scale, as the reference's callers do). K % 64 == 0. */
 int ti_tern_gemv(ti_ctx* ctx, float* out, const uint8_t* codes, const float* scales,
                  const int8_t* act, const int32_t* xsum, int N, int K);
+/* gemv_tern over 1..3 matrices that share the activation (q/k/v, gate/up) in one launch:
+ * outs[i][0..Ns[i]) as ti_tern_gemv for each, bit for bit. K % 1024 == 0, K <= 8192. */
+int ti_tern_gemv_multi(ti_ctx* ctx, const int8_t* act, const int32_t* xsum, int K, int nmat,
+                       const uint8_t* const* codes, const float* const* scales, float* const* outs,
+                       const int* Ns);
 /* gemm_tern_b4 (cpu/kernel/src/lib.rs:331-367): B activation rows act[B*K], xsum[B*K/64];
  * row b of the output starts at out + b*out_stride. */
 int ti_tern_gemm(ti_ctx* ctx, float* out, long out_stride, const uint8_t* codes, const float* scales,

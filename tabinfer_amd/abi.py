@@ -66,6 +66,7 @@ SIGS = {
     "ti_kv_write_q8": [_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i],
     "ti_tern_gemv": [_p, _p, _p, _p, _p, _p, _i, _i],
     "ti_tern_gemm": [_p, _p, C.c_long, _p, _p, _p, _p, _i, _i, _i],
+    "ti_tern_gemv_multi": [_p, _p, _p, _i, _i, _p, _p, _p, _p],
     "ti_quant_act_tern": [_p, _p, _p, _p, _p, _i, _i],
     "ti_tern_block_dots": [_p, _p, _p, _p, _i, _i],
     "ti_requant43": [_p, _p, _p, _i, _i, _p, _p],

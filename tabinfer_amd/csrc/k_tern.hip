@@ -111,6 +111,79 @@ __global__ __launch_bounds__(64) void k_tern_gemv(const uint4* __restrict__ code
     }
 }
 
+// B = 1 with K a multiple of 1024 (16 lanes x BPL blocks per row): 4 rows per wave,
+// 16 rows per workgroup, so a 2048-row matrix spreads over 512 waves (the tile kernel
+// above gives one wave 64 rows: too few waves for the small per-layer matrices).
+// Lanes compute the exact block dots and fetch the block scales; after one barrier,
+// lane 0 of each row's 16 replays the row's accumulation in the reference's block
+// order from LDS.
+struct TernMats {
+    const uint4* codes[3];
+    const float* scales[3];
+    float* out[3];
+    int N[3];
+    int blk0[3];      // first workgroup of each matrix (16 rows per workgroup)
+    int nmat;
+};
+
+template <int BPL>
+__global__ __launch_bounds__(256) void k_tern_gemv_r4(TernMats m, const int8_t* __restrict__ act,
+                                                      const int32_t* __restrict__ xsum) {
+    constexpr int LPR = 16, RW = 4, NB = LPR * BPL;
+    __shared__ int s_dot[4][RW][NB + 1];
+    __shared__ float s_sc[4][RW][NB + 1];
+    __shared__ float s_xs[NB];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r = lane / LPR, li = lane % LPR;
+    // the matrix of this workgroup (uniform: selects, no divergent indexing of the kernargs)
+    const int b = blockIdx.x;
+    const int mi = (m.nmat > 1 && b >= m.blk0[1]) + (m.nmat > 2 && b >= m.blk0[2]);
+    const uint4* codes = mi == 0 ? m.codes[0] : (mi == 1 ? m.codes[1] : m.codes[2]);
+    const float* scales = mi == 0 ? m.scales[0] : (mi == 1 ? m.scales[1] : m.scales[2]);
+    float* out = mi == 0 ? m.out[0] : (mi == 1 ? m.out[1] : m.out[2]);
+    const int N = mi == 0 ? m.N[0] : (mi == 1 ? m.N[1] : m.N[2]);
+    const int b0 = mi == 0 ? 0 : (mi == 1 ? m.blk0[1] : m.blk0[2]);
+    const long row = ((long)(b - b0) * 4 + wave) * RW + r;
+    const long rowc = row < N ? row : N - 1;
+    uint4 cw[BPL];
+    float sc[BPL];
+#pragma unroll
+    for (int j = 0; j < BPL; j++) {
+        cw[j] = ti_ld_nt(codes + rowc * NB + li + LPR * j);
+        sc[j] = scales[rowc * NB + li + LPR * j];
+    }
+    for (int i = tid; i < NB; i += 256) s_xs[i] = (float)xsum[i];
+#pragma unroll
+    for (int j = 0; j < BPL; j++) {
+        ActT t;
+        load_act_tern(act, nullptr, li + LPR * j, t);
+        s_dot[wave][r][li + LPR * j] = tern_block_dot(cw[j], t);
+        s_sc[wave][r][li + LPR * j] = sc[j];
+    }
+    __syncthreads();
+    if (li == 0 && row < N) {
+        float acc = 0.0f, sxs = 0.0f;
+#pragma unroll 8
+        for (int blk = 0; blk < NB; blk++) {
+            const float s = s_sc[wave][r][blk];
+            const float p = s * (float)s_dot[wave][r][blk];
+            acc = acc + p;
+            const float q = s * s_xs[blk];
+            sxs = sxs + q;
+        }
+        out[row] = acc - sxs;
+    }
+}
+
+static bool r4_launch(ti_ctx* c, const TernMats& m, int nb, const int8_t* act, const int32_t* xsum, int grid) {
+    if (nb % 16 != 0 || nb / 16 > 8) return false;
+#define R4(P) \
+    if (nb / 16 == P) { k_tern_gemv_r4<P><<<grid, 256, 0, c->stream>>>(m, act, xsum); return true; }
+    R4(1) R4(2) R4(3) R4(4) R4(5) R4(6) R4(7) R4(8)
+#undef R4
+    return false;
+}
+
 // any K % 64 == 0: one lane per row, blocks in order (same arithmetic as above)
 __global__ __launch_bounds__(64) void k_tern_gemv_generic(const uint4* __restrict__ codes, const float* __restrict__ scales,
                                                           const int8_t* __restrict__ act, const int32_t* __restrict__ xsum,
@@ -216,6 +289,18 @@ static int tern_launch(ti_ctx* c, float* out, const uint8_t* codes, const float*
                        const int32_t* xsum, int N, int K, int B, long out_stride) {
     const uint4* c4 = reinterpret_cast<const uint4*>(codes);
     int nb = K / 64;
+    if (B == 1 && N <= (1 << 30) - 16) {
+        TernMats m = {};
+        m.codes[0] = m.codes[1] = m.codes[2] = c4;
+        m.scales[0] = m.scales[1] = m.scales[2] = scales;
+        m.out[0] = m.out[1] = m.out[2] = out;
+        m.N[0] = m.N[1] = m.N[2] = N;
+        m.nmat = 1;
+        if (r4_launch(c, m, nb, act, xsum, (N + 15) / 16)) {
+            TI_LAUNCHED("k_tern_gemv_r4");
+            return TI_OK;
+        }
+    }
     Shape s = pick(nb);
     const int TR = B == 1 ? 64 : (B == 2 ? 32 : 16);
     long ntiles = (N + TR - 1) / TR;
@@ -256,6 +341,36 @@ extern "C" int ti_tern_gemv(ti_ctx* c, float* out, const uint8_t* codes, const f
     TI_REQUIRE(N > 0 && K > 0 && K % 64 == 0, "ti_tern_gemv: K must be a positive multiple of 64 (N=%d K=%d)", N, K);
     TI_REQUIRE(al16(codes) && al16(act), "ti_tern_gemv: codes and act must be 16-byte aligned");
     return tern_launch(c, out, codes, scales, act, xsum, N, K, 1, N);
+}
+
+extern "C" int ti_tern_gemv_multi(ti_ctx* c, const int8_t* act, const int32_t* xsum, int K, int nmat,
+                                  const uint8_t* const* codes, const float* const* scales, float* const* outs,
+                                  const int* Ns) {
+    TI_CHECK_CTX(c);
+    TI_REQUIRE(act && xsum && codes && scales && outs && Ns, "ti_tern_gemv_multi: null argument");
+    TI_REQUIRE(nmat >= 1 && nmat <= 3, "ti_tern_gemv_multi: nmat must be 1..3 (nmat=%d)", nmat);
+    TI_REQUIRE(K > 0 && K % 1024 == 0 && K <= 8192, "ti_tern_gemv_multi: K must be a multiple of 1024, <= 8192 (K=%d)", K);
+    TI_REQUIRE(al16(act), "ti_tern_gemv_multi: act must be 16-byte aligned");
+    TernMats m = {};
+    long blocks = 0;
+    for (int i = 0; i < 3; i++) {
+        const int s = i < nmat ? i : nmat - 1;
+        if (i < nmat) {
+            TI_REQUIRE(codes[i] && scales[i] && outs[i] && Ns[i] > 0, "ti_tern_gemv_multi: matrix %d: null buffer or N <= 0", i);
+            TI_REQUIRE(al16(codes[i]), "ti_tern_gemv_multi: codes[%d] must be 16-byte aligned", i);
+        }
+        m.codes[i] = reinterpret_cast<const uint4*>(codes[s]);
+        m.scales[i] = scales[s];
+        m.out[i] = outs[s];
+        m.N[i] = Ns[s];
+        m.blk0[i] = (int)blocks;
+        if (i < nmat) blocks += (Ns[i] + 15) / 16;
+    }
+    TI_REQUIRE(blocks < (1L << 31), "ti_tern_gemv_multi: too many rows");
+    m.nmat = nmat;
+    if (!r4_launch(c, m, K / 64, act, xsum, (int)blocks)) return ti_fail(TI_ERR_INVALID, "ti_tern_gemv_multi: no kernel for K=%d", K);
+    TI_LAUNCHED("k_tern_gemv_r4");
+    return TI_OK;
 }
 
 extern "C" int ti_tern_gemm(ti_ctx* c, float* out, long out_stride, const uint8_t* codes, const float* scales,

@@ -154,6 +154,10 @@ function createEngine({ device = 0 } = {}) {
   const Tern = {
     // gemv_tern(out, codes, scales, act, xsum, n, k): out in units of 1/scale
     gemv_tern(outBuf, codesBuf, scalesBuf, actBuf, xsumBuf, n, k) { TI.tern_gemv(ctx, outBuf, codesBuf, scalesBuf, actBuf, xsumBuf, n, k); },
+    // several matrices over one activation (q/k/v, gate/up) in one launch: [{codes, scales, out, n}]
+    gemv_tern_multi(mats, actBuf, xsumBuf, k) {
+      TI.tern_gemv_multi(ctx, actBuf, xsumBuf, k, mats.map((m) => m.codes), mats.map((m) => m.scales), mats.map((m) => m.out), mats.map((m) => m.n));
+    },
     gemm_tern(outBuf, outStride, codesBuf, scalesBuf, actBuf, xsumBuf, n, k, b) {
       TI.tern_gemm(ctx, outBuf, outStride, codesBuf, scalesBuf, actBuf, xsumBuf, n, k, b);
     },

@@ -579,6 +579,58 @@ napi_value js_rmsnorm_gemv_q4(napi_env env, napi_callback_info info) {
     return rc ? throw_ti(env, fn, rc) : undefined(env);
 }
 
+// an array argument of 1..3 device buffers (or of integers)
+bool get_dptr_list(napi_env env, napi_value v, void** out, uint32_t* n, const char* fn, size_t i) {
+    bool is;
+    napi_is_array(env, v, &is);
+    if (!is) return arg_error(env, fn, i, "an array of 1..3 device buffers");
+    napi_get_array_length(env, v, n);
+    if (*n < 1 || *n > 3) return arg_error(env, fn, i, "an array of 1..3 device buffers");
+    for (uint32_t k = 0; k < *n; k++) {
+        napi_value e;
+        napi_get_element(env, v, k, &e);
+        if (!get_dptr(env, e, &out[k], fn, i)) return false;
+    }
+    return true;
+}
+
+bool get_int_list(napi_env env, napi_value v, int* out, uint32_t n, const char* fn, size_t i) {
+    bool is;
+    napi_is_array(env, v, &is);
+    uint32_t len = 0;
+    if (is) napi_get_array_length(env, v, &len);
+    if (!is || len != n) return arg_error(env, fn, i, "an array of integers, one per matrix");
+    for (uint32_t k = 0; k < n; k++) {
+        napi_value e;
+        int64_t t;
+        napi_get_element(env, v, k, &e);
+        if (!get_i64(env, e, &t, fn, i)) return false;
+        out[k] = (int)t;
+    }
+    return true;
+}
+
+// tern_gemv_multi(ctx, act, xsum, K, [codes], [scales], [outs], [Ns])
+napi_value js_tern_gemv_multi(napi_env env, napi_callback_info info) {
+    const char* fn = "tern_gemv_multi";
+    Args a(env, info);
+    if (!want_args(env, a, 8, fn)) return nullptr;
+    CtxH* c = get_ctx(env, a.v[0], fn);
+    void *act, *xsum, *cd[3], *sc[3], *o[3];
+    int64_t K;
+    uint32_t n0, n1, n2;
+    int Ns[3];
+    if (!c || !get_dptr(env, a.v[1], &act, fn, 1) || !get_dptr(env, a.v[2], &xsum, fn, 2) || !get_i64(env, a.v[3], &K, fn, 3) ||
+        !get_dptr_list(env, a.v[4], cd, &n0, fn, 4) || !get_dptr_list(env, a.v[5], sc, &n1, fn, 5) ||
+        !get_dptr_list(env, a.v[6], o, &n2, fn, 6))
+        return nullptr;
+    if (n1 != n0 || n2 != n0) return throw_msg(env, "tern_gemv_multi: codes/scales/outs need the same length");
+    if (!get_int_list(env, a.v[7], Ns, n0, fn, 7)) return nullptr;
+    const int rc = ti_tern_gemv_multi(c->c, (const int8_t*)act, (const int32_t*)xsum, (int)K, (int)n0, (const uint8_t* const*)cd,
+                                      (const float* const*)sc, (float* const*)o, Ns);
+    return rc ? throw_ti(env, fn, rc) : undefined(env);
+}
+
 // ---- Qwen3 decoder object ---------------------------------------------------------------
 bool cfg_int(napi_env env, napi_value o, const char* key, int* out, bool required, int dflt) {
     bool has;
@@ -847,6 +899,7 @@ napi_value module_init(napi_env env, napi_value exports) {
         // ternary
         ENTRY("tern_gemv", ti_tern_gemv),
         ENTRY("tern_gemm", ti_tern_gemm),
+        FN("tern_gemv_multi", js_tern_gemv_multi),
         ENTRY("quant_act_tern", ti_quant_act_tern),
         ENTRY("tern_block_dots", ti_tern_block_dots),
         // int3 MoE

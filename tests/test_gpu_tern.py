@@ -115,3 +115,33 @@ def test_tern_gemm_batched_rows_match_gemv(ctx, orc, B):
     for b in range(B):
         ref = orc.tern_gemv_scalar(codes, sc, acts[b][0], acts[b][1], n, k)
         assert np.array_equal(out[b, :n], ref)
+
+
+@pytest.mark.parametrize("k,ns", [(2048, (2048, 1024, 1024)), (2048, (6144, 6144)), (6144, (2048,)), (1024, (37, 1000, 5))])
+def test_tern_gemv_multi_is_bit_exact(ctx, orc, k, ns):
+    """q/k/v (or gate/up) in one launch: every matrix bit-identical to the scalar kernel."""
+    import ctypes as C
+    rng = np.random.default_rng(k + len(ns))
+    act, xsum, _ = orc.tern_quant_act_n2(rng.standard_normal(k).astype(np.float32))
+    mats = [_bonsai(rng, n, k) for n in ns]
+    dc = [ctx.upload(c) for c, _ in mats]
+    ds = [ctx.upload(s) for _, s in mats]
+    do = [ctx.upload(np.full(n, np.nan, np.float32)) for n in ns]
+    da, dx = ctx.upload(act), ctx.upload(xsum)
+    arr = lambda bufs: (C.c_void_p * len(bufs))(*[b.ptr for b in bufs])
+    ctx.call("ti_tern_gemv_multi", da, dx, k, len(ns), arr(dc), arr(ds), arr(do), (C.c_int * len(ns))(*ns))
+    for (codes, sc), n, o in zip(mats, ns, do):
+        assert np.array_equal(ctx.download(o, np.float32, n), orc.tern_gemv_scalar(codes, sc, act, xsum, n, k))
+    for b in dc + ds + do + [da, dx]:
+        b.free()
+
+
+def test_tern_gemv_multi_rejects_bad_shapes(ctx):
+    import ctypes as C
+    d = ctx.zeros(4096)
+    one = (C.c_void_p * 1)(d.ptr)
+    with pytest.raises(abi.TIError):
+        ctx.call("ti_tern_gemv_multi", d, d, 192, 1, one, one, one, (C.c_int * 1)(4))     # K % 1024
+    with pytest.raises(abi.TIError):
+        ctx.call("ti_tern_gemv_multi", d, d, 1024, 4, one, one, one, (C.c_int * 1)(4))    # nmat > 3
+    d.free()
