@@ -222,6 +222,15 @@ int ti_moe_gemv_q3(ti_ctx* ctx, const float* x, const uint32_t* p3, const uint16
 int ti_moe_gemm_q3(ti_ctx* ctx, const float* src, int src_rows, const uint32_t* p3,
                    const uint16_t* s3, const int32_t* ridx, float* y, int P, int N, int K,
                    int src_div, int nE);
+/* The MoE block of one decode token (models/lfm25.js:2145-2166 at T = 1, after the router
+ * logits) in two launches: [router + w1/w3 + swiglu] and [w2 + combine]:
+ * x[H] += sum_k wt[k] * w2_{idx[k]} (silu(w1 normed) * (w3 normed)). idx/wt[topk] receive
+ * the routing, act[topk*I] the expert activations. nE <= 256, topk in {1, 2, 4, 8},
+ * H and I multiples of 32, <= 4096. */
+int ti_moe_decode_q3(ti_ctx* ctx, float* x, const float* normed, const float* logits, const float* bias,
+                     const uint32_t* w1p, const uint16_t* w1s, const uint32_t* w3p, const uint16_t* w3s,
+                     const uint32_t* w2p, const uint16_t* w2s, int32_t* idx, float* wt, float* act,
+                     int H, int I, int nE, int topk);
 /* swiglu (models/lfm25.js:1831-1847): y[i] = g[i] / (1 + e^-g[i]) * u[i]. */
 int ti_swiglu(ti_ctx* ctx, const float* g, const float* u, float* y, long n);
 /* moeCombine / MOECOMBINE_WGSL (models/lfm25.js:1982-2000): x[t*H+h] += sum_k

@@ -74,6 +74,7 @@ SIGS = {
     "ti_moe_gemv_q3": [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i],
     "ti_moe_gemm_q3": [_p, _p, _i, _p, _p, _p, _p, _i, _i, _i, _i, _i],
     "ti_swiglu": [_p, _p, _p, _p, C.c_long],
+    "ti_moe_decode_q3": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i],
     "ti_moe_combine": [_p, _p, _p, _p, _i, _i, _i],
     "ti_qwen3_create": [_p, _p, C.POINTER(_p)],
     "ti_qwen3_destroy": [_p, _p],

@@ -328,6 +328,308 @@ __global__ __launch_bounds__(256) void k_moe_gemm_q3(const uint32_t* __restrict_
     }
 }
 
+// ---- one decode token, fused: [router + w1/w3 + swiglu] and [w2 + combine] ----------------
+// The router's top-k for one token, computed by one wave (every wave that needs it gets
+// the same answer, so no barrier): experts e = lane + 64 i, sigmoid and selection as
+// k_router (strict '>', lowest index on ties, weights s / (sum + 1e-6)).
+constexpr int RT_EPL = 4;     // experts per lane (nE <= 256)
+constexpr int RT_KMAX = 8;    // top-k held in registers
+__device__ __forceinline__ void wave_route(const float* __restrict__ logits, const float* __restrict__ bias, int nE,
+                                           int topk, int lane, int* ek, float* wk) {
+    float sc[RT_EPL], sel[RT_EPL];
+#pragma unroll
+    for (int i = 0; i < RT_EPL; i++) {
+        const int e = lane + 64 * i;
+        const int ec = e < nE ? e : 0;
+        const float l = logits[ec];
+        const float sg = 1.0f / (1.0f + expf(-l));
+        sc[i] = sg;
+        sel[i] = e < nE ? sg + (bias ? bias[ec] : 0.0f) : -3.0e38f;
+    }
+    float sum = 0.0f;
+    float chosen_s[RT_KMAX];
+#pragma unroll
+    for (int k = 0; k < RT_KMAX; k++) {
+        if (k < topk) {
+            float bv = -1.0e30f;
+            int bi = 0x7fffffff;
+#pragma unroll
+            for (int i = 0; i < RT_EPL; i++)
+                if (sel[i] > bv) { bv = sel[i]; bi = lane + 64 * i; }
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) {
+                const float ov = __shfl_xor(bv, o, 64);
+                const int oi = __shfl_xor(bi, o, 64);
+                if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+            }
+            if (bi == 0x7fffffff) bi = 0;
+            const int owner = bi & 63, slot = bi >> 6;
+            float mine = sc[0];
+#pragma unroll
+            for (int i = 1; i < RT_EPL; i++) mine = slot == i ? sc[i] : mine;
+            const float s_b = __shfl(mine, owner, 64);
+#pragma unroll
+            for (int i = 0; i < RT_EPL; i++)
+                if (lane == owner && slot == i) sel[i] = -2.0e30f;
+            ek[k] = bi;
+            chosen_s[k] = s_b;
+            sum = sum + s_b;
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < RT_KMAX; k++)
+        if (k < topk) wk[k] = chosen_s[k] / (sum + 1e-6f);
+}
+
+// grid (row blocks of 4R, topk): workgroup (., k) runs the router, takes expert e of
+// slot k, and computes act[k*I + n] = silu(w1_e x)_n * (w3_e x)_n for its 4R rows
+// (R per wave) with the exact fixed-point dot of k_moe_gemv_q3. Workgroup (0, k) stores
+// slot k's expert id and weight.
+template <int GL, int R>
+__global__ __launch_bounds__(256) void k_moe_gateup_dec(const float* __restrict__ x, const float* __restrict__ logits,
+                                                        const float* __restrict__ bias, int nE, int topk,
+                                                        const uint32_t* __restrict__ p1, const uint16_t* __restrict__ s1,
+                                                        const uint32_t* __restrict__ p3, const uint16_t* __restrict__ s3,
+                                                        float* __restrict__ act, int32_t* __restrict__ idx,
+                                                        float* __restrict__ wt, int I, int H) {
+    const int k = blockIdx.y;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int gpr = H / 32;
+    // x once per workgroup, coalesced, into LDS (group g padded to 36 floats: conflict-free
+    // 16-byte reads of a lane's group); the loads do not wait for the router
+    __shared__ __align__(16) float s_x[GL * 64 * 36];
+    for (int i = threadIdx.x; i < H / 4; i += 256) {
+        const float4 t = reinterpret_cast<const float4*>(x)[i];
+        *reinterpret_cast<float4*>(&s_x[(i / 8) * 36 + (i % 8) * 4]) = t;
+    }
+    int ek[RT_KMAX];
+    float wk[RT_KMAX];
+    wave_route(logits, bias, nE, topk, lane, ek, wk);
+    int e = ek[0];
+    float w = wk[0];
+#pragma unroll
+    for (int i = 1; i < RT_KMAX; i++) {
+        e = k == i ? ek[i] : e;
+        w = k == i ? wk[i] : w;
+    }
+    if (blockIdx.x == 0 && wave == 0 && lane == 0) {
+        idx[k] = e;
+        wt[k] = w;
+    }
+    const int row0 = (blockIdx.x * 4 + wave) * R;
+    uint32_t pg[GL][R][3], pu[GL][R][3];
+    uint16_t sg[GL][R], su[GL][R];
+#pragma unroll
+    for (int h = 0; h < GL; h++) {
+        const int g = lane + 64 * h;
+        const int gc = g < gpr ? g : gpr - 1;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const int n = min(row0 + r, I - 1);
+            const size_t gi = ((size_t)e * I + n) * gpr + gc;
+#pragma unroll
+            for (int b = 0; b < 3; b++) {
+                pg[h][r][b] = __builtin_nontemporal_load(p1 + gi * 3 + b);
+                pu[h][r][b] = __builtin_nontemporal_load(p3 + gi * 3 + b);
+            }
+            sg[h][r] = s1[gi];
+            su[h][r] = s3[gi];
+        }
+    }
+    __syncthreads();
+    float accv[2 * R] = {};
+#pragma unroll
+    for (int h = 0; h < GL; h++) {
+        const int g = lane + 64 * h;
+        const int gc = g < gpr ? g : gpr - 1;
+        float v[32];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float4 t = *reinterpret_cast<const float4*>(&s_x[gc * 36 + 4 * i]);
+            v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
+        }
+        Limbs L;
+        make_limbs(v, L);
+        const bool live = lane + 64 * h < gpr;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const float dg = group_dot_q3_limbs(pg[h][r][0], pg[h][r][1], pg[h][r][2], L);
+            const float du = group_dot_q3_limbs(pu[h][r][0], pu[h][r][1], pu[h][r][2], L);
+            accv[r] = live ? fmaf(dg, ti_h2f(sg[h][r]), accv[r]) : accv[r];
+            accv[R + r] = live ? fmaf(du, ti_h2f(su[h][r]), accv[R + r]) : accv[R + r];
+        }
+    }
+    // slot s (gate rows 0..R-1, up rows R..2R-1) ends in lanes s*SPAN .. s*SPAN+SPAN-1
+    constexpr int SPAN = 64 / (2 * R);
+    const float tot = transpose_reduce<64, 2 * R>(accv, lane);
+    const float up = __shfl(tot, lane + SPAN * R, 64);
+    const int r = lane / SPAN;
+    const int n = row0 + r;
+    if (lane % SPAN == 0 && r < R && n < I) act[(size_t)k * I + n] = tot / (1.0f + expf(-tot)) * up;
+}
+
+// grid (row blocks of 16): rows n of w2 for every slot k (expert idx[k], activation row
+// act[k*I ..]), then x[n] += sum_k wt[k] * out_k[n] in slot order (moeCombine's order).
+template <int GL, int P>
+__global__ __launch_bounds__(256) void k_moe_down_dec(const float* __restrict__ act, const uint32_t* __restrict__ p2,
+                                                      const uint16_t* __restrict__ s2, const int32_t* __restrict__ idx,
+                                                      const float* __restrict__ wt, float* __restrict__ x, int H, int I,
+                                                      int nE) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int gpr = I / 32;
+    const int row0 = (blockIdx.x * 4 + wave) * MOE_R;
+    int ek[P];
+#pragma unroll
+    for (int k = 0; k < P; k++) {
+        const int e = idx[k];
+        ek[k] = e < 0 ? 0 : (e >= nE ? nE - 1 : e);   // ids come from the router: always in range
+    }
+    float accv[MOE_R * P] = {};
+#pragma unroll
+    for (int h = 0; h < GL; h++) {
+        const int g = lane + 64 * h;
+        const int gc = g < gpr ? g : gpr - 1;
+        const bool live = g < gpr;
+        uint32_t pl[P][MOE_R][3];
+        uint16_t sv[P][MOE_R];
+#pragma unroll
+        for (int k = 0; k < P; k++)
+#pragma unroll
+            for (int r = 0; r < MOE_R; r++) {
+                const int n = min(row0 + r, H - 1);
+                const size_t gi = ((size_t)ek[k] * H + n) * gpr + gc;
+#pragma unroll
+                for (int b = 0; b < 3; b++) pl[k][r][b] = __builtin_nontemporal_load(p2 + gi * 3 + b);
+                sv[k][r] = s2[gi];
+            }
+#pragma unroll
+        for (int k = 0; k < P; k++) {
+            float vv[32];
+            const float4* src = reinterpret_cast<const float4*>(act + (size_t)k * I + (size_t)gc * 32);
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float4 t = src[i];
+                vv[4 * i] = t.x; vv[4 * i + 1] = t.y; vv[4 * i + 2] = t.z; vv[4 * i + 3] = t.w;
+            }
+            Limbs L;
+            make_limbs(vv, L);
+#pragma unroll
+            for (int r = 0; r < MOE_R; r++) {
+                const float d = group_dot_q3_limbs(pl[k][r][0], pl[k][r][1], pl[k][r][2], L);
+                accv[r * P + k] = live ? fmaf(d, ti_h2f(sv[k][r]), accv[r * P + k]) : accv[r * P + k];
+            }
+        }
+    }
+    constexpr int SLOTS = MOE_R * P, SPAN = 64 / SLOTS;
+    const float tot = transpose_reduce<64, SLOTS>(accv, lane);
+    // row r's P slots are in lanes (r*P + k) * SPAN
+    const int r = lane / (P * SPAN);
+    float o[P];
+#pragma unroll
+    for (int k = 0; k < P; k++) o[k] = __shfl(tot, (r * P + k) * SPAN, 64);
+    const int n = row0 + r;
+    if (lane % (P * SPAN) == 0 && n < H) {
+        float sacc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < P; k++) {
+            const float pr = wt[k] * o[k];
+            sacc = sacc + pr;
+        }
+        x[n] = x[n] + sacc;
+    }
+}
+
+// the same with the slots' activation limbs computed once per workgroup (wave k: slot k,
+// P <= 4) and shared through LDS; R rows per wave (I <= 2048)
+struct LimbsPacked {
+    int4 w[7];          // l[3][8] as 6 int4, then sum[3] and the scale's bits
+};
+template <int P, int R>
+__global__ __launch_bounds__(256) void k_moe_down_dec_pl(const float* __restrict__ act, const uint32_t* __restrict__ p2,
+                                                         const uint16_t* __restrict__ s2, const int32_t* __restrict__ idx,
+                                                         const float* __restrict__ wt, float* __restrict__ x, int H, int I,
+                                                         int nE) {
+    static_assert(P >= 1 && P <= 4, "one wave per slot");
+    __shared__ LimbsPacked s_l[P][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int gpr = I / 32;
+    const int g = lane, gc = g < gpr ? g : gpr - 1;
+    const bool live = g < gpr;
+    const int row0 = (blockIdx.x * 4 + wave) * R;
+    int ek[P];
+#pragma unroll
+    for (int k = 0; k < P; k++) {
+        const int e = idx[k];
+        ek[k] = e < 0 ? 0 : (e >= nE ? nE - 1 : e);   // ids come from the router: always in range
+    }
+    uint32_t pl[P][R][3];
+    uint16_t sv[P][R];
+#pragma unroll
+    for (int k = 0; k < P; k++)
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const int n = min(row0 + r, H - 1);
+            const size_t gi = ((size_t)ek[k] * H + n) * gpr + gc;
+#pragma unroll
+            for (int b = 0; b < 3; b++) pl[k][r][b] = __builtin_nontemporal_load(p2 + gi * 3 + b);
+            sv[k][r] = s2[gi];
+        }
+    if (wave < P) {
+        float vv[32];
+        const float4* src = reinterpret_cast<const float4*>(act + (size_t)wave * I + (size_t)gc * 32);
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float4 t = src[i];
+            vv[4 * i] = t.x; vv[4 * i + 1] = t.y; vv[4 * i + 2] = t.z; vv[4 * i + 3] = t.w;
+        }
+        Limbs L;
+        make_limbs(vv, L);
+        LimbsPacked& d = s_l[wave][lane];
+#pragma unroll
+        for (int q = 0; q < 3; q++) {
+            d.w[2 * q] = make_int4(L.l[q][0], L.l[q][1], L.l[q][2], L.l[q][3]);
+            d.w[2 * q + 1] = make_int4(L.l[q][4], L.l[q][5], L.l[q][6], L.l[q][7]);
+        }
+        d.w[6] = make_int4(L.sum[0], L.sum[1], L.sum[2], __float_as_int(L.S));
+    }
+    __syncthreads();
+    float accv[R * P];
+#pragma unroll
+    for (int k = 0; k < P; k++) {
+        const LimbsPacked& d = s_l[k][lane];
+        Limbs L;
+#pragma unroll
+        for (int q = 0; q < 3; q++) {
+            const int4 a = d.w[2 * q], b = d.w[2 * q + 1];
+            L.l[q][0] = a.x; L.l[q][1] = a.y; L.l[q][2] = a.z; L.l[q][3] = a.w;
+            L.l[q][4] = b.x; L.l[q][5] = b.y; L.l[q][6] = b.z; L.l[q][7] = b.w;
+        }
+        const int4 t = d.w[6];
+        L.sum[0] = t.x; L.sum[1] = t.y; L.sum[2] = t.z; L.S = __int_as_float(t.w);
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const float dd = group_dot_q3_limbs(pl[k][r][0], pl[k][r][1], pl[k][r][2], L);
+            accv[r * P + k] = live ? dd * ti_h2f(sv[k][r]) : 0.0f;
+        }
+    }
+    constexpr int SLOTS = R * P, SPAN = 64 / SLOTS;
+    const float tot = transpose_reduce<64, SLOTS>(accv, lane);
+    const int r = lane / (P * SPAN);
+    float o[P];
+#pragma unroll
+    for (int k = 0; k < P; k++) o[k] = __shfl(tot, (r * P + k) * SPAN, 64);
+    const int n = row0 + r;
+    if (lane % (P * SPAN) == 0 && r < R && n < H) {
+        float sacc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < P; k++) {
+            const float pr = wt[k] * o[k];
+            sacc = sacc + pr;
+        }
+        x[n] = x[n] + sacc;
+    }
+}
+
 // swiglu (lfm25.js:1831-1847): y = g / (1 + e^-g) * u
 __global__ void k_swiglu_f32(const float* __restrict__ g, const float* __restrict__ u, float* __restrict__ y, long n) {
     const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -414,6 +716,40 @@ extern "C" int ti_moe_gemm_q3(ti_ctx* c, const float* src, int src_rows, const u
     else k_moe_gemm_q3<2><<<grid, 256, 0, c->stream>>>(c->act_q, c->act_s, p3, s3, ridx, y, P, N, K, src_div);
     TI_LAUNCHED("k_moe_gemm_q3");
     return TI_OK;
+}
+
+extern "C" int ti_moe_decode_q3(ti_ctx* c, float* x, const float* normed, const float* logits, const float* bias,
+                                const uint32_t* w1p, const uint16_t* w1s, const uint32_t* w3p, const uint16_t* w3s,
+                                const uint32_t* w2p, const uint16_t* w2s, int32_t* idx, float* wt, float* act, int H, int I,
+                                int nE, int topk) {
+    TI_CHECK_CTX(c);
+    TI_REQUIRE(x && normed && logits && w1p && w1s && w3p && w3s && w2p && w2s && idx && wt && act,
+               "ti_moe_decode_q3: null buffer");
+    TI_REQUIRE(nE > 0 && nE <= RT_EPL * 64 && (topk == 1 || topk == 2 || topk == 4 || topk == 8) && topk <= nE,
+               "ti_moe_decode_q3: need nE <= 256 and topk in {1, 2, 4, 8} (nE=%d topk=%d)", nE, topk);
+    TI_REQUIRE(H > 0 && I > 0 && H % 32 == 0 && I % 32 == 0 && H <= 4096 && I <= 4096,
+               "ti_moe_decode_q3: H, I multiples of 32, <= 4096 (H=%d I=%d)", H, I);
+    TI_REQUIRE(al16(normed) && al16(act), "ti_moe_decode_q3: normed and act must be 16-byte aligned");
+    // measured on MI355X (LFM2.5 shapes): 4 rows per wave for w1/w3, 2 for w2
+    constexpr int K1R = 4, R2 = 2;
+    dim3 g1((unsigned)((I + 4 * K1R - 1) / (4 * K1R)), (unsigned)topk);
+    if (H <= 2048) k_moe_gateup_dec<1, K1R><<<g1, 256, 0, c->stream>>>(normed, logits, bias, nE, topk, w1p, w1s, w3p, w3s, act, idx, wt, I, H);
+    else k_moe_gateup_dec<2, K1R><<<g1, 256, 0, c->stream>>>(normed, logits, bias, nE, topk, w1p, w1s, w3p, w3s, act, idx, wt, I, H);
+    TI_LAUNCHED("k_moe_gateup_dec");
+    if (I <= 2048 && topk <= 4) {
+        const unsigned g4 = (unsigned)((H + 4 * R2 - 1) / (4 * R2));
+        if (topk == 1) k_moe_down_dec_pl<1, R2><<<g4, 256, 0, c->stream>>>(act, w2p, w2s, idx, wt, x, H, I, nE);
+        else if (topk == 2) k_moe_down_dec_pl<2, R2><<<g4, 256, 0, c->stream>>>(act, w2p, w2s, idx, wt, x, H, I, nE);
+        else k_moe_down_dec_pl<4, R2><<<g4, 256, 0, c->stream>>>(act, w2p, w2s, idx, wt, x, H, I, nE);
+        TI_LAUNCHED("k_moe_down_dec");
+        return TI_OK;
+    }
+    const unsigned g2 = (unsigned)((H + 15) / 16);
+#define DD(GL_, P_) \
+    if ((I <= 2048) == (GL_ == 1) && topk == P_) { k_moe_down_dec<GL_, P_><<<g2, 256, 0, c->stream>>>(act, w2p, w2s, idx, wt, x, H, I, nE); TI_LAUNCHED("k_moe_down_dec"); return TI_OK; }
+    DD(1, 1) DD(1, 2) DD(1, 4) DD(1, 8) DD(2, 1) DD(2, 2) DD(2, 4) DD(2, 8)
+#undef DD
+    return ti_fail(TI_ERR_INVALID, "ti_moe_decode_q3: no kernel for I=%d topk=%d", I, topk);
 }
 
 extern "C" int ti_swiglu(ti_ctx* c, const float* g, const float* u, float* y, long n) {

@@ -325,3 +325,51 @@ def test_moe_shape_errors(ctx):
     with pytest.raises(abi.TIError):
         ctx.call("ti_router", d, None, 1, 300, 4, d, d)                       # nE > 256
     d.free()
+
+
+# ---- the fused decode block ---------------------------------------------------------------
+@pytest.mark.parametrize("H,I,nE,topk", [(H, I, NE, TOPK), (4096, 1024, 8, 2), (1024, 4096, 100, 8), (512, 256, 256, 1)])
+def test_moe_decode_fused_matches_chain(ctx, orc, H, I, nE, topk):
+    """ti_moe_decode_q3 (2 launches) against the oracle chain, and its routing against
+    ti_router bit for bit."""
+    rng = np.random.default_rng(H + I + nE + topk)
+    w1, w3 = rand_planes(rng, nE * I, H), rand_planes(rng, nE * I, H)
+    w2 = rand_planes(rng, nE * H, I)
+    normed = rng.standard_normal(H).astype(np.float32)
+    logits = rng.standard_normal(nE).astype(np.float32)
+    bias = (rng.standard_normal(nE) * 0.05).astype(np.float32)
+    x = rng.standard_normal(H).astype(np.float32)
+    d = {k: ctx.upload(v) for k, v in dict(normed=normed, logits=logits, bias=bias, x=x, p1=w1[0], s1=w1[1],
+                                             p3=w3[0], s3=w3[1], p2=w2[0], s2=w2[1]).items()}
+    d["idx"], d["wt"], d["act"] = ctx.zeros(topk * 4), ctx.zeros(topk * 4), ctx.zeros(topk * I * 4)
+    d["ridx"], d["rwt"] = ctx.zeros(topk * 4), ctx.zeros(topk * 4)
+    ctx.call("ti_moe_decode_q3", d["x"], d["normed"], d["logits"], d["bias"], d["p1"], d["s1"], d["p3"], d["s3"],
+             d["p2"], d["s2"], d["idx"], d["wt"], d["act"], H, I, nE, topk)
+    ctx.call("ti_router", d["logits"], d["bias"], 1, nE, topk, d["ridx"], d["rwt"])
+    idx = ctx.download(d["idx"], np.int32, topk)
+    assert np.array_equal(idx, ctx.download(d["ridx"], np.int32, topk))
+    assert np.array_equal(ctx.download(d["wt"], np.float32, topk), ctx.download(d["rwt"], np.float32, topk))
+    oi, ow = orc.router(logits, bias, 1, nE, topk)
+    assert np.array_equal(idx, oi)
+    g = orc.moe_gemv_q3(normed, *w1, oi, topk, I, H, H, topk)
+    u = orc.moe_gemv_q3(normed, *w3, oi, topk, I, H, H, topk)
+    a = g / (1.0 + np.exp(-g)) * u
+    assert norm_err(ctx.download(d["act"], np.float32, topk * I), a) <= 1e-4
+    o = orc.moe_gemv_q3(a.astype(np.float32), *w2, oi, topk, H, I, I, 1)
+    want = (ow.astype(np.float64)[:, None] * o.reshape(topk, H)).sum(0)
+    got = ctx.download(d["x"], np.float32, H).astype(np.float64) - x
+    assert norm_err(got, want) <= 1e-4
+    for b in d.values():
+        b.free()
+
+
+def test_moe_decode_rejects_bad_shapes(ctx):
+    dd = ctx.zeros(4096)
+    args = [dd] * 13
+    with pytest.raises(abi.TIError):
+        ctx.call("ti_moe_decode_q3", *args, 2048, 1792, 32, 3)      # topk 3
+    with pytest.raises(abi.TIError):
+        ctx.call("ti_moe_decode_q3", *args, 2048, 1792, 300, 4)     # nE > 256
+    with pytest.raises(abi.TIError):
+        ctx.call("ti_moe_decode_q3", *args, 8192, 1792, 32, 4)      # H > 4096
+    dd.free()
