@@ -349,24 +349,263 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split_q8(const float* __re
     }
 }
 
+// ---------------------------------------------------------------------------
+// T > 1 queries (a prefill chunk or a T-token batch, models/qwen3.js:2534-2577): one
+// pass over a split's keys serves every query row of the KV head, instead of one pass
+// per query. Workgroup (256 threads) = (split, KV head, group of 16 query rows; row
+// ri = (t, h) with t = query, h = head of the group). Key tiles of 64:
+//  - S = Q K^T on the matrix cores: v_mfma_f32_16x16x32_f16, one MFMA per 32-dim scale
+//    group and per 16 keys (wave w: keys 16w..16w+15). K codes are exact in f16; q is
+//    split into f16 hi + lo (q = hi + lo to ~2^-22), two MFMAs per group, so the
+//    scores keep f32 accuracy. Each group's partial is scaled by its key's K scale.
+//  - causal mask (key < S0 + t), online softmax per row (tile maxima and sums through
+//    LDS, the running (m, l) in LDS);
+//  - P V with f32 FMAs from the V tile staged in LDS: wave w owns the 32 dims of scale
+//    group w, each lane one dim and 8 rows.
+// Partials (o, m, l) go to the split-KV scratch in k_attn_split_q8's layout; the same
+// k_attn_combine merges them.
+// ---------------------------------------------------------------------------
+typedef _Float16 am_half8 __attribute__((ext_vector_type(8)));
+typedef float am_f4 __attribute__((ext_vector_type(4)));
+constexpr int AM_ROWS = 16, AM_KT = 64;
+
+struct AttnMArgs {
+    const float* qr;
+    const uint8_t* kq;
+    const float* ks;
+    const uint4* vq;
+    const float* vs;
+    float* po;
+    float* pml;
+    int S0, T, nHq, nKv, G, nsplit, per, ns_stride;
+};
+
+__global__ __launch_bounds__(256) void k_attn_multi_q8(AttnMArgs a) {
+    constexpr int HD = 128, NG = HD / 32;
+    __shared__ __align__(16) int8_t s_v[AM_KT][HD];
+    __shared__ float s_vs[AM_KT][NG];
+    __shared__ __align__(16) float s_p[AM_KT][AM_ROWS];
+    __shared__ float s_mx[2][4][AM_ROWS], s_sm[2][4][AM_ROWS];
+    __shared__ float s_m[AM_ROWS], s_l[AM_ROWS];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int split = blockIdx.x % a.nsplit, hk = blockIdx.x / a.nsplit;
+    const int rg = blockIdx.y;
+    const int nrows = a.G * a.T;
+    const int Smax = a.S0 + a.T - 1;
+    const int c0 = split * a.per;
+    const int c1 = min(Smax, c0 + a.per);
+    const int row_bytes = a.nKv * HD, row_words4 = a.nKv * HD / 16, row_groups = a.nKv * NG;
+    const float qk_scale = 1.0f / (127.0f * sqrtf((float)HD));
+    if (tid < AM_ROWS) {
+        s_m[tid] = -3.0e38f;
+        s_l[tid] = 0.0f;
+    }
+    // A operands: query row (lane % 16), dims 32g + 8 (lane / 16) .. +8, as f16 hi + lo
+    const int ak = lane >> 4;
+    am_half8 qh[NG], ql[NG];
+    {
+        const int gr = rg * AM_ROWS + (lane & 15);
+        const bool ok = gr < nrows;
+        const int t = ok ? gr / a.G : 0, h = ok ? gr % a.G : 0;
+        const float* q = a.qr + ((size_t)t * a.nHq + hk * a.G + h) * HD;
+#pragma unroll
+        for (int g = 0; g < NG; g++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float v = ok ? q[32 * g + 8 * ak + e] : 0.0f;
+                const _Float16 hi = (_Float16)v;
+                qh[g][e] = hi;
+                ql[g][e] = (_Float16)(v - (float)hi);
+            }
+    }
+    // this lane's score rows (4 (lane / 16) + i) and their causal limits
+    int lim[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int gr = rg * AM_ROWS + 4 * ak + i;
+        lim[i] = gr < nrows ? min(c1, a.S0 + gr / a.G) : 0;     // keys [c0, lim) are visible
+    }
+    // this lane's P V rows (8 (lane / 32) + i) and dim
+    const int pr0 = 8 * (lane >> 5), d = 32 * wave + (lane & 31);
+    float acc[8] = {};
+    int it = 0;
+    for (int t0 = c0; t0 < c1; t0 += AM_KT, it ^= 1) {
+        // V tile and its scales into LDS (coalesced)
+        for (int i = tid; i < AM_KT * HD / 16; i += 256) {
+            const int j = i / (HD / 16), c = i % (HD / 16);
+            int key = t0 + j;
+            key = key < c1 ? key : c1 - 1;
+            *reinterpret_cast<uint4*>(&s_v[j][c * 16]) = ti_ld_nt(a.vq + (size_t)key * row_words4 + hk * (HD / 16) + c);
+        }
+        {
+            const int j = tid / NG, g = tid % NG;
+            int key = t0 + j;
+            key = key < c1 ? key : c1 - 1;
+            s_vs[j][g] = a.vs[(size_t)key * row_groups + hk * NG + g];
+        }
+        // K operands of this wave's 16 keys: key (lane % 16), dims 32g + 8 (lane / 16) .. +8
+        const int kk = t0 + 16 * wave + (lane & 15);
+        const int kc = kk < c1 ? kk : c1 - 1;
+        am_half8 kb[NG];
+        float ksc[NG];
+#pragma unroll
+        for (int g = 0; g < NG; g++) {
+            const uint2 w = *reinterpret_cast<const uint2*>(a.kq + (size_t)kc * row_bytes + hk * HD + 32 * g + 8 * ak);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                kb[g][e] = (_Float16)(int)(int8_t)((w.x >> (8 * e)) & 0xffu);
+                kb[g][4 + e] = (_Float16)(int)(int8_t)((w.y >> (8 * e)) & 0xffu);
+            }
+            ksc[g] = a.ks[(size_t)kc * row_groups + hk * NG + g];
+        }
+        am_f4 sc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int g = 0; g < NG; g++) {
+            const am_f4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+            am_f4 dg = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[g], kb[g], z, 0, 0, 0);
+            dg = __builtin_amdgcn_mfma_f32_16x16x32_f16(ql[g], kb[g], dg, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; i++) sc[i] = fmaf(dg[i], ksc[g], sc[i]);
+        }
+        // mask, scale, tile maxima of this wave's 16 keys per row
+        float s[4], mx[4];
+        bool ok[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            ok[i] = kk < lim[i];
+            s[i] = ok[i] ? sc[i] * qk_scale : -3.0e38f;
+            mx[i] = s[i];
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) mx[i] = fmaxf(mx[i], __shfl_xor(mx[i], o, 64));
+        }
+        if ((lane & 15) == 0)
+#pragma unroll
+            for (int i = 0; i < 4; i++) s_mx[it][wave][4 * ak + i] = mx[i];
+        __syncthreads();                                   // (1) tile maxima, V tile
+        float ps[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int r = 4 * ak + i;
+            float mt = s_mx[it][0][r];
+#pragma unroll
+            for (int w = 1; w < 4; w++) mt = fmaxf(mt, s_mx[it][w][r]);
+            const float mnew = fmaxf(s_m[r], mt);
+            const float p = ok[i] ? expf(s[i] - mnew) : 0.0f;
+            s_p[16 * wave + (lane & 15)][r] = p;
+            ps[i] = p;
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) ps[i] += __shfl_xor(ps[i], o, 64);
+        }
+        if ((lane & 15) == 0)
+#pragma unroll
+            for (int i = 0; i < 4; i++) s_sm[it][wave][4 * ak + i] = ps[i];
+        __syncthreads();                                   // (2) p
+        // P V for this lane's 8 rows and dim d (scale group = wave)
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int r = pr0 + i;
+            float mt = s_mx[it][0][r];
+#pragma unroll
+            for (int w = 1; w < 4; w++) mt = fmaxf(mt, s_mx[it][w][r]);
+            const float mo = s_m[r], mnew = fmaxf(mo, mt);
+            acc[i] *= mo == mnew ? 1.0f : expf(mo - mnew);
+        }
+        // every key of the tile (p is 0 past the split's end; the clamped V rows are finite)
+#pragma unroll 16
+        for (int j = 0; j < AM_KT; j++) {
+            const float cv = (float)s_v[j][d] * s_vs[j][wave];
+            const float4 pa = *reinterpret_cast<const float4*>(&s_p[j][pr0]);
+            const float4 pb = *reinterpret_cast<const float4*>(&s_p[j][pr0 + 4]);
+            acc[0] = fmaf(pa.x, cv, acc[0]); acc[1] = fmaf(pa.y, cv, acc[1]);
+            acc[2] = fmaf(pa.z, cv, acc[2]); acc[3] = fmaf(pa.w, cv, acc[3]);
+            acc[4] = fmaf(pb.x, cv, acc[4]); acc[5] = fmaf(pb.y, cv, acc[5]);
+            acc[6] = fmaf(pb.z, cv, acc[6]); acc[7] = fmaf(pb.w, cv, acc[7]);
+        }
+        __syncthreads();                                   // (3) s_v, s_p, s_m read
+        if (tid < AM_ROWS) {
+            const int r = tid;
+            float mt = s_mx[it][0][r], sum = 0.0f;
+#pragma unroll
+            for (int w = 1; w < 4; w++) mt = fmaxf(mt, s_mx[it][w][r]);
+#pragma unroll
+            for (int w = 0; w < 4; w++) sum += s_sm[it][w][r];
+            const float mo = s_m[r], mnew = fmaxf(mo, mt);
+            s_l[r] = s_l[r] * (mo == mnew ? 1.0f : expf(mo - mnew)) + sum;
+            s_m[r] = mnew;
+        }
+    }
+    __syncthreads();
+    // partials, in k_attn_split_q8's layout: row (t, hq) -> [t][hq][split]
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int gr = rg * AM_ROWS + pr0 + i;
+        if (gr < nrows) {
+            const int t = gr / a.G, hq = hk * a.G + gr % a.G;
+            a.po[(((size_t)t * a.nHq + hq) * a.ns_stride + split) * HD + d] = acc[i] * (1.0f / 127.0f);
+        }
+    }
+    if (tid < AM_ROWS) {
+        const int gr = rg * AM_ROWS + tid;
+        if (gr < nrows) {
+            const int t = gr / a.G, hq = hk * a.G + gr % a.G;
+            float* ml = a.pml + (((size_t)t * a.nHq + hq) * a.ns_stride + split) * 2;
+            ml[0] = s_m[tid];
+            ml[1] = s_l[tid];
+        }
+    }
+}
+
 // O = sum_i o_i e^(m_i-M) / sum_i l_i e^(m_i-M); an empty split carries
 // (m = -3e38, l = 0, o = 0) and contributes nothing.
-__global__ void k_attn_combine(const float* __restrict__ po, const float* __restrict__ pml, float* __restrict__ out,
-                               int nsplit, int hd, int ns_stride, int per, const int* __restrict__ dpos) {
-    const int d = threadIdx.x;
+__global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ po, const float* __restrict__ pml,
+                                                      float* __restrict__ out, int nsplit, int hd, int ns_stride, int per,
+                                                      const int* __restrict__ dpos) {
+    // one workgroup per output row: the splits' (m, l) into LDS and their weights
+    // e_i = exp(m_i - M) computed once; then 2 threads per dim sum o_i e_i over
+    // alternate chunks of 16 splits (16 loads in flight), and the halves meet in LDS
+    __shared__ float s_e[TI_ATTN_SPLITS_MAX];
+    __shared__ float s_red[2][TI_ATTN_HD_MAX];
+    __shared__ float s_w[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int qt = blockIdx.y;
     const int hq = blockIdx.x + qt * gridDim.x;        // row of [T][nHq]
     if (dpos) nsplit = (*dpos + 1 + per - 1) / per;
     const float* ml = pml + (size_t)hq * ns_stride * 2;
     float M = -3.0e38f;
-    for (int i = 0; i < nsplit; i++) M = fmaxf(M, ml[2 * i]);
-    float L = 0.0f, o = 0.0f;
-    for (int i = 0; i < nsplit; i++) {
-        float e = expf(ml[2 * i] - M);
+    for (int i = tid; i < nsplit; i += 256) M = fmaxf(M, ml[2 * i]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+    if (lane == 0) s_w[wave] = M;
+    __syncthreads();
+    M = fmaxf(fmaxf(s_w[0], s_w[1]), fmaxf(s_w[2], s_w[3]));
+    float L = 0.0f;
+    for (int i = tid; i < nsplit; i += 256) {
+        const float e = expf(ml[2 * i] - M);
+        s_e[i] = e;
         L += ml[2 * i + 1] * e;
-        if (d < hd) o += po[((size_t)hq * ns_stride + i) * hd + d] * e;
     }
-    if (d < hd) out[(size_t)hq * hd + d] = o / L;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) L += __shfl_xor(L, o, 64);
+    __syncthreads();                       // s_w (maxima) read by everyone before reuse
+    if (lane == 0) s_w[wave] = L;
+    __syncthreads();
+    L = (s_w[0] + s_w[1]) + (s_w[2] + s_w[3]);
+    const int d = tid % TI_ATTN_HD_MAX, q4 = tid / TI_ATTN_HD_MAX;    // 2 x 128 threads
+    float o = 0.0f;
+    if (d < hd) {
+        const float* pp = po + (size_t)hq * ns_stride * hd + d;
+        for (int i0 = q4 * 16; i0 < nsplit; i0 += 32) {
+            float v[16];
+#pragma unroll
+            for (int k = 0; k < 16; k++) v[k] = i0 + k < nsplit ? pp[(size_t)(i0 + k) * hd] : 0.0f;
+#pragma unroll
+            for (int k = 0; k < 16; k++)
+                if (i0 + k < nsplit) o += v[k] * s_e[i0 + k];
+        }
+    }
+    s_red[q4][d] = o;
+    __syncthreads();
+    if (q4 == 0 && d < hd) out[(size_t)hq * hd + d] = (s_red[0][d] + s_red[1][d]) / L;
 }
 }  // namespace
 
@@ -403,6 +642,23 @@ int ti_attn_decode_launch(ti_ctx* c, const float* qr, const uint32_t* kq, const 
     if (nsplit > TI_ATTN_SPLITS_MAX) return ti_fail(TI_ERR_INVALID, "ti_attn_decode_q8: %d splits > %d", nsplit, TI_ATTN_SPLITS_MAX);
     if ((long)T * nHq > TI_ATTN_ROWS_MAX) return ti_fail(TI_ERR_INVALID, "ti_attn_decode_q8: T*nHq = %d > %d", T * nHq, TI_ATTN_ROWS_MAX);
     int G = nHq / nKv;
+    if (!dpos && T > 1 && hd == 128) {   // one pass over the keys for all T queries
+        const int Smax = S + T - 1;
+        const int want = (1024 + nKv - 1) / nKv;
+        int per2 = (Smax + want - 1) / want;
+        per2 = ((per2 + AM_KT - 1) / AM_KT) * AM_KT;
+        if (per2 < AM_KT) per2 = AM_KT;
+        int ns2 = (Smax + per2 - 1) / per2;
+        while (ns2 > TI_ATTN_SPLITS_MAX) { per2 += AM_KT; ns2 = (Smax + per2 - 1) / per2; }
+        AttnMArgs m = {qr, reinterpret_cast<const uint8_t*>(kq), ks, reinterpret_cast<const uint4*>(vq), vs,
+                       c->attn_po, c->attn_ml, S, T, nHq, nKv, G, ns2, per2, ns2};
+        dim3 g2(nKv * ns2, (G * T + AM_ROWS - 1) / AM_ROWS);
+        k_attn_multi_q8<<<g2, 256, 0, c->stream>>>(m);
+        TI_LAUNCHED("k_attn_multi_q8");
+        k_attn_combine<<<dim3(nHq, T), 256, 0, c->stream>>>(c->attn_po, c->attn_ml, out, ns2, hd, ns2, per2, nullptr);
+        TI_LAUNCHED("k_attn_combine");
+        return TI_OK;
+    }
     dim3 grid(nKv * nsplit, T);
     const uint4* k4 = reinterpret_cast<const uint4*>(kq);
     const uint4* v4 = reinterpret_cast<const uint4*>(vq);
@@ -412,7 +668,7 @@ int ti_attn_decode_launch(ti_ctx* c, const float* qr, const uint32_t* kq, const 
     else return ti_fail(TI_ERR_INVALID, "ti_attn_decode_q8: unsupported hd=%d / group=%d", hd, G);
 #undef ATT
     TI_LAUNCHED("k_attn_split_q8");
-    k_attn_combine<<<dim3(nHq, T), hd < 64 ? 64 : hd, 0, c->stream>>>(c->attn_po, c->attn_ml, out, nsplit, hd, ns_stride, per, dpos);
+    k_attn_combine<<<dim3(nHq, T), 256, 0, c->stream>>>(c->attn_po, c->attn_ml, out, nsplit, hd, ns_stride, per, dpos);
     TI_LAUNCHED("k_attn_combine");
     return TI_OK;
 }

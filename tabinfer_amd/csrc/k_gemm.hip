@@ -13,8 +13,8 @@
 //       [x0 x2 x4 x6 | x1 x3 x5 x7] to match B;
 //   B = weights, columns = weight rows: one packed word (8 nibbles) of row n0+l%16,
 //       split into even/odd nibbles and sign-shifted to int8 (nibble - 8).
-// Workgroup = 16 weight rows; its 4 waves take interleaved quarters of the groups and
-// their partials meet in LDS. Tokens beyond 16 are further 16-row M tiles of the same
+// Workgroup = 16 weight rows; its 8 waves take every 8th group and their partials meet
+// in LDS. Tokens beyond 16 are further 16-row M tiles of the same
 // launch (the weight tile is then re-read from L2).
 #include "ti_dev.h"
 
@@ -32,14 +32,18 @@ __device__ __forceinline__ void nib_to_s8(uint32_t w, uint32_t& lo, uint32_t& hi
 }
 
 constexpr int GMAX = 512;       // K <= 16384
-constexpr int UNROLL = 4;
 
-__global__ __launch_bounds__(256) void k_gemm_q4_q8_mfma(const uint32_t* __restrict__ xq, const float* __restrict__ xs,
-                                                          const uint32_t* __restrict__ pack,
-                                                          const uint16_t* __restrict__ scales, float* __restrict__ y,
-                                                          int T, int N, int K, int acc) {
+// WAVES waves per 16-row tile, each on every WAVES-th group; UNROLL groups per wave have
+// their loads in flight together (WAVES * UNROLL groups cover K = 32 * WAVES * UNROLL in
+// one batch: 2048 for (8, 8)).
+template <int WAVES, int UNROLL>
+__global__ __launch_bounds__(64 * WAVES) void k_gemm_q4_q8_mfma(const uint32_t* __restrict__ xq, const float* __restrict__ xs,
+                                                               const uint32_t* __restrict__ pack,
+                                                               const uint16_t* __restrict__ scales, float* __restrict__ y,
+                                                               int T, int N, int K, int acc) {
+    constexpr int SX_PER = (16 * GMAX + 64 * WAVES - 1) / (64 * WAVES);
     __shared__ float s_sx[16][GMAX];
-    __shared__ float s_part[4][16][17];
+    __shared__ float s_part[WAVES][16][17];
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int G = K / 32;
@@ -51,55 +55,80 @@ __global__ __launch_bounds__(256) void k_gemm_q4_q8_mfma(const uint32_t* __restr
 
     for (int t0 = 0; t0 < T; t0 += 16) {
         const int tm = min(16, T - t0);
-        __syncthreads();                       // s_sx / s_part of the previous M tile are consumed
-        for (int e = tid; e < 16 * G; e += 256) {
-            const int t = e / G, g = e % G;
-            s_sx[t][g] = t < tm ? xs[(size_t)(t0 + t) * G + g] : 0.0f;
-        }
-        __syncthreads();
         // token row of this lane's A operand (rows past T read token t0 and are zeroed by s_sx)
         const int ta = t0 + (m < tm ? m : 0);
         const uint32_t* arow = xq + (size_t)ta * (K / 4);
-        float accv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        // this wave's groups: wave, wave + 4, ...
-        for (int g0 = wave; g0 < G; g0 += 4 * UNROLL) {
-            uint32_t wq[UNROLL];
-            uint2 aq[UNROLL];
-            uint16_t sw[UNROLL];
+        uint32_t wq[UNROLL];
+        uint2 aq[UNROLL];
+        uint16_t sw[UNROLL];
+        auto load = [&](int g0) {
 #pragma unroll
             for (int u = 0; u < UNROLL; u++) {
-                const int g = g0 + 4 * u;
+                const int g = g0 + WAVES * u;
                 const int gc = g < G ? g : G - 1;
-                wq[u] = __builtin_nontemporal_load(prow + 4 * gc + j);
+                wq[u] = prow[4 * gc + j];
                 aq[u] = *reinterpret_cast<const uint2*>(arow + 8 * gc + 2 * j);
                 sw[u] = srow[gc];
             }
+        };
+        load(wave);                            // the first batch is in flight while the scales are staged
+        __syncthreads();                       // s_sx / s_part of the previous M tile are consumed
+        {   // the tile's activation scales: every load issued before the first store
+            float v[SX_PER];
 #pragma unroll
-            for (int u = 0; u < UNROLL; u++) {
-                const int g = g0 + 4 * u;
-                if (g < G) {
-                    uint32_t blo, bhi;
-                    nib_to_s8(wq[u], blo, bhi);
-                    const uint32_t alo = even_bytes(aq[u].x, aq[u].y), ahi = odd_bytes(aq[u].x, aq[u].y);
-                    const long A = (long)(((uint64_t)ahi << 32) | alo);
-                    const long B = (long)(((uint64_t)bhi << 32) | blo);
-                    const v4i z = {0, 0, 0, 0};
-                    const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, z, 0, 0, 0);
-                    const float s = ti_h2f(sw[u]);
+            for (int k = 0; k < SX_PER; k++) {
+                const int e = tid + k * 64 * WAVES;
+                const int t = e / G, g = e % G;
+                const int tc = t < tm ? t : 0;
+                v[k] = e < 16 * G ? xs[(size_t)(t0 + tc) * G + g] : 0.0f;
+            }
 #pragma unroll
-                    for (int i = 0; i < 4; i++) accv[i] = fmaf((float)d[i], s * s_sx[4 * j + i][g], accv[i]);
-                }
+            for (int k = 0; k < SX_PER; k++) {
+                const int e = tid + k * 64 * WAVES;
+                const int t = e / G, g = e % G;
+                if (e < 16 * G) s_sx[t][g] = t < tm ? v[k] : 0.0f;
             }
         }
-        // the 4 waves' partials: lane holds tokens 4j..4j+3 of column m
+        __syncthreads();
+        float accv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int g0 = wave; g0 < G; g0 += WAVES * UNROLL) {
+            if (g0 != wave) load(g0);
+            float sxv[UNROLL][4];
+#pragma unroll
+            for (int u = 0; u < UNROLL; u++) {
+                const int g = g0 + WAVES * u;
+                const int gc = g < G ? g : G - 1;
+#pragma unroll
+                for (int i = 0; i < 4; i++) sxv[u][i] = s_sx[4 * j + i][gc];
+            }
+            // no branch on g < G here: a guarded use lets the compiler sink the loads into
+            // the branch, one memory round trip per group; past G the weight is zeroed
+#pragma unroll
+            for (int u = 0; u < UNROLL; u++) {
+                const int g = g0 + WAVES * u;
+                uint32_t blo, bhi;
+                nib_to_s8(wq[u], blo, bhi);
+                const uint32_t alo = even_bytes(aq[u].x, aq[u].y), ahi = odd_bytes(aq[u].x, aq[u].y);
+                const long A = (long)(((uint64_t)ahi << 32) | alo);
+                const long B = (long)(((uint64_t)bhi << 32) | blo);
+                const v4i z = {0, 0, 0, 0};
+                const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, z, 0, 0, 0);
+                const float sg = g < G ? ti_h2f(sw[u]) : 0.0f;
+#pragma unroll
+                for (int i = 0; i < 4; i++) accv[i] = fmaf((float)d[i], sg * sxv[u][i], accv[i]);
+            }
+        }
+        // the waves' partials: lane holds tokens 4j..4j+3 of column m
 #pragma unroll
         for (int i = 0; i < 4; i++) s_part[wave][4 * j + i][m] = accv[i];
         __syncthreads();
-        {
+        if (tid < 256) {
             const int t = tid / 16, c = tid % 16;    // 256 threads = 16 tokens x 16 rows
             const int n = n0 + c;
             if (t < tm && n < N) {
-                const float v = (s_part[0][t][c] + s_part[1][t][c]) + (s_part[2][t][c] + s_part[3][t][c]);
+                float v = 0.0f;
+#pragma unroll
+                for (int w = 0; w < WAVES; w++) v += s_part[w][t][c];
                 float* yp = y + (size_t)(t0 + t) * N + n;
                 *yp = acc ? *yp + v : v;
             }
@@ -114,7 +143,7 @@ int ti_gemm_q4_q8_launch(ti_ctx* c, const uint32_t* xq, const float* xs, const u
     if (K % 32 != 0 || K / 32 > GMAX) return ti_fail(TI_ERR_INVALID, "int4 GEMM: K=%d must be a multiple of 32, <= %d", K, GMAX * 32);
     if (T <= 0 || N <= 0) return ti_fail(TI_ERR_INVALID, "int4 GEMM: T=%d N=%d", T, N);
     const unsigned grid = (unsigned)((N + 15) / 16);
-    k_gemm_q4_q8_mfma<<<grid, 256, 0, c->stream>>>(xq, xs, pack, scales, y, T, N, K, acc);
+    k_gemm_q4_q8_mfma<8, 8><<<grid, 512, 0, c->stream>>>(xq, xs, pack, scales, y, T, N, K, acc);
     TI_LAUNCHED("k_gemm_q4_q8_mfma");
     return TI_OK;
 }

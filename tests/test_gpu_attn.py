@@ -141,3 +141,31 @@ def test_attn_errors(ctx):
         ctx.call("ti_attn_decode_q8", d, d, d, d, d, d, 10, 15, 8, 128, 0)      # nHq % nKv != 0
     with pytest.raises(abi.TIError):
         ctx.call("ti_rope_qk", d, d, d, 1, 1, 128, 0, np.float32(1e6), np.float32(1e-6))   # in-place
+
+
+@pytest.mark.parametrize("T,pos0,nHq,nKv,hd", [(2, 0, 16, 8, 128), (8, 100, 16, 8, 128), (8, 4095, 16, 8, 128),
+                                               (32, 1000, 16, 8, 128), (5, 63, 4, 2, 128), (8, 300, 8, 8, 128),
+                                               (3, 40, 8, 2, 128), (4, 50, 4, 2, 64)])
+def test_attn_causal_matches_oracle(ctx, orc, T, pos0, nHq, nKv, hd):
+    """T queries at positions pos0..pos0+T-1 over one cache (query t sees keys
+    [0, pos0+t]): the one-pass multi-query kernel (hd 128) and the per-query path (hd 64)
+    against the oracle's f64 softmax."""
+    rng = np.random.default_rng(T * 7 + pos0 + hd)
+    S = pos0 + T
+    K = rng.standard_normal(S * nKv * hd).astype(np.float32)
+    V = rng.standard_normal(S * nKv * hd).astype(np.float32)
+    kq, ks = orc.kv_quant(K)
+    vq, vs = orc.kv_quant(V)
+    Q = (rng.standard_normal(T * nHq * hd) * 2).astype(np.float32)
+    bufs = [ctx.upload(a) for a in (Q, kq, ks, vq, vs)]
+    out = ctx.upload(np.full(T * nHq * hd, np.nan, np.float32))
+    ctx.call("ti_attn_causal_q8", *bufs, out, T, pos0, nHq, nKv, hd)
+    got = ctx.download(out, np.float32, T * nHq * hd)
+    ref = orc.attn_causal_q8(Q, kq, ks, vq, vs, T, pos0, nHq, nKv, hd)
+    assert rel_err(got, ref) < TOL
+    # each query row alone is the decode attention over its prefix
+    for t in (0, T - 1):
+        one = orc.attn_decode_q8(Q[t * nHq * hd:(t + 1) * nHq * hd], kq, ks, vq, vs, pos0 + t + 1, nHq, nKv, hd)
+        assert rel_err(got.reshape(T, -1)[t], one) < TOL
+    for b in bufs + [out]:
+        b.free()
