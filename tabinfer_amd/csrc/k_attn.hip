@@ -261,7 +261,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split_q8(const float* __re
 #pragma unroll
             for (int o = LPT / 2; o > 0; o >>= 1)
 #pragma unroll
-                for (int h = 0; h < G; h++) part[h] += __shfl_xor(part[h], o, 64);
+                for (int h = 0; h < G; h++) part[h] += ti_xor(part[h], o);
             const int j = p * TPP + tp;
             if (sl == 0 && j < ATT_TILE)
 #pragma unroll
@@ -275,7 +275,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split_q8(const float* __re
             float v = -3.0e38f;
             for (int j = tid; j < ATT_TILE; j += ATT_THREADS) v = fmaxf(v, sc[h][j]);
 #pragma unroll
-            for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+            for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, ti_xor(v, o));
             if (lane == 0) redm[h][wv] = v;
         }
         __syncthreads();
@@ -294,7 +294,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split_q8(const float* __re
                 s += pe;
             }
 #pragma unroll
-            for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+            for (int o = 32; o > 0; o >>= 1) s += ti_xor(s, o);
             if (lane == 0) reds[h][wv] = s;
         }
         __syncthreads();
@@ -476,7 +476,7 @@ __global__ __launch_bounds__(256) void k_attn_multi_q8(AttnMArgs a) {
             s[i] = ok[i] ? sc[i] * qk_scale : -3.0e38f;
             mx[i] = s[i];
 #pragma unroll
-            for (int o = 1; o < 16; o <<= 1) mx[i] = fmaxf(mx[i], __shfl_xor(mx[i], o, 64));
+            for (int o = 1; o < 16; o <<= 1) mx[i] = fmaxf(mx[i], ti_xor(mx[i], o));
         }
         if ((lane & 15) == 0)
 #pragma unroll
@@ -494,7 +494,7 @@ __global__ __launch_bounds__(256) void k_attn_multi_q8(AttnMArgs a) {
             s_p[16 * wave + (lane & 15)][r] = p;
             ps[i] = p;
 #pragma unroll
-            for (int o = 1; o < 16; o <<= 1) ps[i] += __shfl_xor(ps[i], o, 64);
+            for (int o = 1; o < 16; o <<= 1) ps[i] += ti_xor(ps[i], o);
         }
         if ((lane & 15) == 0)
 #pragma unroll
@@ -574,7 +574,7 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ 
     float M = -3.0e38f;
     for (int i = tid; i < nsplit; i += 256) M = fmaxf(M, ml[2 * i]);
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, ti_xor(M, o));
     if (lane == 0) s_w[wave] = M;
     __syncthreads();
     M = fmaxf(fmaxf(s_w[0], s_w[1]), fmaxf(s_w[2], s_w[3]));
@@ -585,7 +585,7 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ 
         L += ml[2 * i + 1] * e;
     }
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) L += __shfl_xor(L, o, 64);
+    for (int o = 32; o > 0; o >>= 1) L += ti_xor(L, o);
     __syncthreads();                       // s_w (maxima) read by everyone before reuse
     if (lane == 0) s_w[wave] = L;
     __syncthreads();
@@ -803,7 +803,7 @@ __device__ __forceinline__ float head_norm_rope(float x, int j, int hd, float wj
     if (j < 64) {
         v = red[j] + red[j + 64];
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) v = v + __shfl_xor(v, o, 64);
+        for (int o = 32; o > 0; o >>= 1) v = v + ti_xor(v, o);
         if (j == 0) *tot = v;
     }
     __syncthreads();
@@ -918,12 +918,10 @@ __global__ __launch_bounds__(256, 2) void k_attn_fused_q8(AttnFArgs a) {
         const float val = h == 0 ? r : vx;
         float mx = j < HD ? fabsf(val) : 0.0f;
 #pragma unroll
-        for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+        for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, ti_xor(mx, o));
         mx = fmaxf(mx, 1e-12f);
         const uint32_t code = snorm_code(val, mx);
-        const int src = lane & ~3;
-        const uint32_t word = __shfl(code, src, 64) | (__shfl(code, src + 1, 64) << 8) |
-                              (__shfl(code, src + 2, 64) << 16) | (__shfl(code, src + 3, 64) << 24);
+        const uint32_t word = ti_quad_or(code << (8 * (lane & 3)));
         if (j < HD) {
             const size_t rowq = ((size_t)pos * a.nKv + hk) * (HD / 4), rows = ((size_t)pos * a.nKv + hk) * NG;
             if ((j & 3) == 0) {
@@ -986,7 +984,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_fused_q8(AttnFArgs a) {
 #pragma unroll
             for (int o = LPT / 2; o > 0; o >>= 1)
 #pragma unroll
-                for (int hh = 0; hh < G; hh++) sc[p][hh] += __shfl_xor(sc[p][hh], o, 64);
+                for (int hh = 0; hh < G; hh++) sc[p][hh] += ti_xor(sc[p][hh], o);
             const bool live = t0 + p * TPW + tp < S;
 #pragma unroll
             for (int hh = 0; hh < G; hh++) sc[p][hh] = live ? sc[p][hh] * qk_scale : -3.0e38f;
@@ -998,7 +996,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_fused_q8(AttnFArgs a) {
 #pragma unroll
             for (int p = 1; p < PASSES; p++) mx = fmaxf(mx, sc[p][hh]);
 #pragma unroll
-            for (int o = LPT; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+            for (int o = LPT; o < 64; o <<= 1) mx = fmaxf(mx, ti_xor(mx, o));
             const float mn = fmaxf(m_run[hh], mx);
             corr[hh] = expf(m_run[hh] - mn);
             m_run[hh] = mn;
@@ -1030,7 +1028,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_fused_q8(AttnFArgs a) {
 #pragma unroll
         for (int hh = 0; hh < G; hh++) {
 #pragma unroll
-            for (int o = LPT; o < 64; o <<= 1) ps[hh] += __shfl_xor(ps[hh], o, 64);
+            for (int o = LPT; o < 64; o <<= 1) ps[hh] += ti_xor(ps[hh], o);
             l_run[hh] = l_run[hh] * corr[hh] + ps[hh];
         }
     };
@@ -1116,11 +1114,11 @@ __global__ __launch_bounds__(256, 2) void k_attn_fused_q8(AttnFArgs a) {
         const float m = in ? s_ml[wave][lane][0] : -3.0e38f;
         float M = m;
 #pragma unroll
-        for (int o2 = 32; o2 > 0; o2 >>= 1) M = fmaxf(M, __shfl_xor(M, o2, 64));
+        for (int o2 = 32; o2 > 0; o2 >>= 1) M = fmaxf(M, ti_xor(M, o2));
         const float e = in ? expf(m - M) : 0.0f;
         float L = in ? s_ml[wave][lane][1] * e : 0.0f;
 #pragma unroll
-        for (int o2 = 32; o2 > 0; o2 >>= 1) L += __shfl_xor(L, o2, 64);
+        for (int o2 = 32; o2 > 0; o2 >>= 1) L += ti_xor(L, o2);
         s_e[wave][lane] = e;
         if (lane == 0) s_L[wave] = L;
     }
@@ -1137,17 +1135,15 @@ __global__ __launch_bounds__(256, 2) void k_attn_fused_q8(AttnFArgs a) {
         if (a.oq) {   // quantQ8 of 32 consecutive outputs = 32 consecutive lanes (q8_group's arithmetic)
             float mx = fabsf(res);
 #pragma unroll
-            for (int o2 = 16; o2 > 0; o2 >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o2, 64));
+            for (int o2 = 16; o2 > 0; o2 >>= 1) mx = fmaxf(mx, ti_xor(mx, o2));
             const float scale = mx / 127.0f;
             const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
             const float pq = res * inv;
             int qi = (int)rintf(pq);
             qi = qi < -127 ? -127 : (qi > 127 ? 127 : qi);
             const uint32_t b = (uint32_t)(qi & 0xff);
-            const int src = (lane & ~3);
-            const uint32_t b0 = __shfl(b, src, 64), b1 = __shfl(b, src + 1, 64);
-            const uint32_t b2 = __shfl(b, src + 2, 64), b3 = __shfl(b, src + 3, 64);
-            if ((lane & 3) == 0) a.oq[e / 4] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+            const uint32_t word = ti_quad_or(b << (8 * (lane & 3)));
+            if ((lane & 3) == 0) a.oq[e / 4] = word;
             if ((lane & 31) == 0) a.os[e / 32] = scale;
         }
     }

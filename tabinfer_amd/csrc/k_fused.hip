@@ -134,14 +134,7 @@ __device__ __forceinline__ void act_regs_quant(const FArgs& a, ActRegs<EPT>& r, 
             float sq = r.x[i] * r.x[i];
             s = s + sq;
         }
-        red[t] = s;
-        __syncthreads();
-#pragma unroll
-        for (int st = 128; st > 0; st >>= 1) {
-            if (t < st) red[t] = red[t] + red[t + st];
-            __syncthreads();
-        }
-        float m = red[0] / (float)a.K;
+        float m = ti_tree_sum_256(s, red) / (float)a.K;
         m = m + a.eps;
         const float inv = 1.0f / sqrtf(m);
 #pragma unroll
@@ -151,12 +144,13 @@ __device__ __forceinline__ void act_regs_quant(const FArgs& a, ActRegs<EPT>& r, 
         }
     }
     uint8_t* qb = reinterpret_cast<uint8_t*>(s_xq);
+    float gmx[EPT];
+#pragma unroll
+    for (int i = 0; i < EPT; i++) gmx[i] = ti_max32_nonneg(fabsf(r.x[i]));   // independent chains, all VALU
 #pragma unroll
     for (int i = 0; i < EPT; i++) {
         const int e = t + 256 * i;
-        float mx = fabsf(r.x[i]);
-#pragma unroll
-        for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+        const float mx = gmx[i];
         if (e < a.K) {
             const float scale = mx / 127.0f;
             const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
@@ -384,22 +378,17 @@ __global__ __launch_bounds__(256) void k_gateup_q8out(FArgs a) {
             s_swi[rl] = v;
         }
         __syncthreads();
-        if (tid < 32) {   // quantQ8 of the chunk's 32 values (q8_group's arithmetic)
-            const float v = s_swi[tid];
-            float mx = fabsf(v);
-#pragma unroll
-            for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+        if (wave == 0) {   // quantQ8 of the chunk's 32 values (q8_group's arithmetic); lanes 32..63 mirror 0..31
+            const float v = s_swi[lane & 31];
+            const float mx = ti_max32_nonneg(fabsf(v));
             const float scale = mx / 127.0f;
             const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
             const float pq = v * inv;
             int qi = (int)rintf(pq);
             qi = qi < -127 ? -127 : (qi > 127 ? 127 : qi);
-            const uint32_t b = (uint32_t)(qi & 0xff);
-            const int src = (tid & 7) * 4;
-            const uint32_t b0 = __shfl(b, src, 64), b1 = __shfl(b, src + 1, 64);
-            const uint32_t b2 = __shfl(b, src + 2, 64), b3 = __shfl(b, src + 3, 64);
-            if (tid < 8) a.yq[(size_t)ch * 8 + tid] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
-            if (tid == 0) a.ys[ch] = scale;
+            const uint32_t word = ti_quad_or((uint32_t)(qi & 0xff) << (8 * (lane & 3)));
+            if (lane < 32 && (lane & 3) == 0) a.yq[(size_t)ch * 8 + (lane >> 2)] = word;
+            if (lane == 0) a.ys[ch] = scale;
         }
         if (ch + (int)gridDim.x < nchunks) {
             __syncthreads();   // s_swi is rewritten by the next chunk
@@ -475,6 +464,16 @@ __device__ __forceinline__ void amx_take(float& v, int& i, float v2, int i2) {
     if (v2 > v || (v2 == v && i2 < i)) { v = v2; i = i2; }
 }
 
+// argmax over the wave (value, then lowest index), left in every lane
+__device__ __forceinline__ void wave_argmax(float& v, int& i) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float v2 = ti_xor(v, o);
+        const int i2 = ti_xor_i(i, o);
+        amx_take(v, i, v2, i2);
+    }
+}
+
 template <int LPR, int GPL, int R>
 __global__ __launch_bounds__(256) void k_lmhead(LmArgs a) {
     __shared__ __align__(16) float s_x[LM_KMAX];
@@ -533,14 +532,7 @@ __global__ __launch_bounds__(256) void k_lmhead(LmArgs a) {
             float sq = xr[i] * xr[i];
             s = s + sq;
         }
-        red[tid] = s;
-        __syncthreads();
-#pragma unroll
-        for (int st = 128; st > 0; st >>= 1) {
-            if (tid < st) red[tid] = red[tid] + red[tid + st];
-            __syncthreads();
-        }
-        float m = red[0] / (float)a.K;
+        float m = ti_tree_sum_256(s, red) / (float)a.K;
         m = m + a.eps;
         const float inv = 1.0f / sqrtf(m);
 #pragma unroll
@@ -586,23 +578,20 @@ __global__ __launch_bounds__(256) void k_lmhead(LmArgs a) {
             b = nb;
         }
     }
-    // workgroup argmax (lowest index wins ties)
-    bv_s[tid] = best_v;
-    bi_s[tid] = best_i;
-    __syncthreads();
-    for (int s = 128; s > 0; s >>= 1) {
-        if (tid < s) {
-            float v = bv_s[tid];
-            int i = bi_s[tid];
-            amx_take(v, i, bv_s[tid + s], bi_s[tid + s]);
-            bv_s[tid] = v;
-            bi_s[tid] = i;
-        }
-        __syncthreads();
+    // workgroup argmax (lowest index wins ties): wave butterflies, then the 4 wave winners
+    wave_argmax(best_v, best_i);
+    if (lane == 0) {
+        bv_s[tid >> 6] = best_v;
+        bi_s[tid >> 6] = best_i;
     }
+    __syncthreads();
     if (tid == 0) {
-        ti_pub_store(a.part_v + blockIdx.x, bv_s[0]);
-        ti_pub_store(a.part_i + blockIdx.x, (uint32_t)bi_s[0]);
+        float v = bv_s[0];
+        int i = bi_s[0];
+#pragma unroll
+        for (int w = 1; w < 4; w++) amx_take(v, i, bv_s[w], bi_s[w]);
+        ti_pub_store(a.part_v + blockIdx.x, v);
+        ti_pub_store(a.part_i + blockIdx.x, (uint32_t)i);
         ti_stores_done();
         last_s = ti_arrive(a.counter) == gridDim.x - 1;
     }
@@ -611,24 +600,22 @@ __global__ __launch_bounds__(256) void k_lmhead(LmArgs a) {
     float v = -3.0e38f;
     int i = 0x7fffffff;
     for (int p = tid; p < (int)gridDim.x; p += 256) amx_take(v, i, ti_pub_load(a.part_v + p), (int)ti_pub_load(a.part_i + p));
-    bv_s[tid] = v;
-    bi_s[tid] = i;
-    __syncthreads();
-    for (int s = 128; s > 0; s >>= 1) {
-        if (tid < s) {
-            float vv = bv_s[tid];
-            int ii = bi_s[tid];
-            amx_take(vv, ii, bv_s[tid + s], bi_s[tid + s]);
-            bv_s[tid] = vv;
-            bi_s[tid] = ii;
-        }
-        __syncthreads();
+    wave_argmax(v, i);
+    __syncthreads();   // every thread has read last_s / the first-stage winners
+    if (lane == 0) {
+        bv_s[tid >> 6] = v;
+        bi_s[tid >> 6] = i;
     }
+    __syncthreads();
     if (tid == 0) {
+        float vv = bv_s[0];
+        int ii = bi_s[0];
+#pragma unroll
+        for (int w = 1; w < 4; w++) amx_take(vv, ii, bv_s[w], bi_s[w]);
         const int pos = a.dpos ? *a.dpos : a.out_pos - 1;
         last_s = -1;
         if (pos >= 0 && pos < a.cap) {
-            a.hist[pos + 1] = (uint32_t)bi_s[0];
+            a.hist[pos + 1] = (uint32_t)ii;
             if (a.dpos) *a.dpos = pos + 1;
             last_s = pos + 1;
         }

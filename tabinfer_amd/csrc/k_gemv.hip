@@ -40,6 +40,19 @@ __global__ __launch_bounds__(256) void k_gemv_q4_q8(const uint32_t* __restrict__
     // behind a branch
     uint4 wv[2][R][GPL];
     uint16_t sw[2][R][GPL];
+    float yold[2];
+    constexpr int SPAN = LPR / R;        // lanes holding the same row total
+    // raw activation loads first, unpacked after the weight loads are issued: the
+    // activation's wait (vmcnt counts in order) then does not include the weights
+    uint4 araw[GPL][2];
+    float asc[GPL];
+#pragma unroll
+    for (int j = 0; j < GPL; j++) {
+        const uint4* p = reinterpret_cast<const uint4*>(xq + (size_t)(li + LPR * j) * 8);
+        araw[j][0] = p[0];
+        araw[j][1] = p[1];
+        asc[j] = xs[li + LPR * j];
+    }
     auto load = [&](int buf, long blk) {
 #pragma unroll
         for (int r = 0; r < R; r++) {
@@ -52,11 +65,15 @@ __global__ __launch_bounds__(256) void k_gemv_q4_q8(const uint32_t* __restrict__
                 sw[buf][r][j] = ld_nt(scales + gi);
             }
         }
+        // the residual of the row this lane stores, fetched with the weights (not after the dots)
+        long orow = blk * (RPP * R) + sub + (long)(li / SPAN) * RPP;
+        orow = orow < N ? orow : N - 1;
+        yold[buf] = y[orow];
     };
     load(0, b);
     ActQ8 a[GPL];
 #pragma unroll
-    for (int j = 0; j < GPL; j++) load_act_q8(xq, xs, li + LPR * j, a[j]);
+    for (int j = 0; j < GPL; j++) act_q8_from_words(araw[j], asc[j], a[j]);
     auto finish = [&](int buf, long blk) {
         float accv[R];
 #pragma unroll
@@ -70,9 +87,8 @@ __global__ __launch_bounds__(256) void k_gemv_q4_q8(const uint32_t* __restrict__
             accv[r] = t;
         }
         float tot = transpose_reduce<LPR, R>(accv, li);
-        constexpr int SPAN = LPR / R;        // lanes holding the same row total
         const long row = blk * (RPP * R) + sub + (long)(li / SPAN) * RPP;
-        if ((li % SPAN) == 0 && row < N) store_out(y, row, tot, acc);
+        if ((li % SPAN) == 0 && row < N) y[row] = acc ? yold[buf] + tot : tot;
     };
     // persistent waves: prefetch block b+nwaves while finishing block b
     for (;;) {

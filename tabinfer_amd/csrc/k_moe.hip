@@ -108,8 +108,8 @@ __global__ __launch_bounds__(64) void k_router(const float* __restrict__ logits,
         }
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) {
-            const float ov = __shfl_xor(bv, o, 64);
-            const int oi = __shfl_xor(bi, o, 64);
+            const float ov = ti_xor(bv, o);
+            const int oi = ti_xor_i(bi, o);
             if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
         }
         if (bi == 0x7fffffff) bi = 0;                   // nothing above -1e30: index 0, as a scan would
@@ -358,8 +358,8 @@ __device__ __forceinline__ void wave_route(const float* __restrict__ logits, con
                 if (sel[i] > bv) { bv = sel[i]; bi = lane + 64 * i; }
 #pragma unroll
             for (int o = 32; o > 0; o >>= 1) {
-                const float ov = __shfl_xor(bv, o, 64);
-                const int oi = __shfl_xor(bi, o, 64);
+                const float ov = ti_xor(bv, o);
+                const int oi = ti_xor_i(bi, o);
                 if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
             }
             if (bi == 0x7fffffff) bi = 0;

@@ -228,7 +228,7 @@ __global__ __launch_bounds__(1024) void k_quant_act_tern(const float* __restrict
     float m = 0.0f;
     for (int i = t; i < K; i += 1024) m = fmaxf(m, fabsf(x[i]));
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, ti_xor(m, o));
     if ((t & 63) == 0) red[t >> 6] = m;
     __syncthreads();
     if (t == 0) {
@@ -253,7 +253,7 @@ __global__ __launch_bounds__(1024) void k_quant_act_tern(const float* __restrict
         act[blk * 64 + lane] = (int8_t)q;
         int sum = q;
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+        for (int o = 32; o > 0; o >>= 1) sum += ti_xor(sum, o);
         if (lane == 0) xsum[blk] = sum;
     }
 }

@@ -23,6 +23,21 @@ struct ActQ8 {
     float s;       // activation group scale
 };
 
+// the group's 32 codes (two 16-byte words) and scale, unpacked for group_dot_q8
+__device__ __forceinline__ void act_q8_from_words(const uint4 (&u)[2], float s, ActQ8& a) {
+    uint32_t w[8] = {u[0].x, u[0].y, u[0].z, u[0].w, u[1].x, u[1].y, u[1].z, u[1].w};
+    int sum = 0;
+#pragma unroll
+    for (int m = 0; m < 4; m++) {
+        a.xe[m] = (int)even_bytes(w[2 * m], w[2 * m + 1]);
+        a.xo[m] = (int)odd_bytes(w[2 * m], w[2 * m + 1]);
+        sum = __builtin_amdgcn_sdot4((int)w[2 * m], 0x01010101, sum, false);
+        sum = __builtin_amdgcn_sdot4((int)w[2 * m + 1], 0x01010101, sum, false);
+    }
+    a.corr = 8 * sum;
+    a.s = s;
+}
+
 __device__ __forceinline__ void load_act_q8(const uint32_t* __restrict__ xq, const float* __restrict__ xs, int g, ActQ8& a) {
     const uint4* p = reinterpret_cast<const uint4*>(xq + (size_t)g * 8);
     uint4 u0 = p[0], u1 = p[1];
@@ -84,12 +99,12 @@ __device__ __forceinline__ float transpose_reduce(float (&v)[R], int li) {
                 if (i < k / 2) {
                     float send = up ? v[i] : v[i + k / 2];
                     float keep = up ? v[i + k / 2] : v[i];
-                    v[i] = keep + __shfl_xor(send, o, 64);
+                    v[i] = keep + ti_xor(send, o);
                 }
             }
             k >>= 1;
         } else {
-            v[0] += __shfl_xor(v[0], o, 64);
+            v[0] += ti_xor(v[0], o);
         }
     }
     return v[0];
@@ -263,14 +278,8 @@ __device__ __forceinline__ float rms_inv_256(const float* __restrict__ x, int H,
     int t = threadIdx.x;
     float s = 0.0f;
     for (int i = t; i < H; i += 256) { float sq = x[i] * x[i]; s = s + sq; }
-    red[t] = s;
-    __syncthreads();
-#pragma unroll
-    for (int st = 128; st > 0; st >>= 1) {
-        if (t < st) red[t] = red[t] + red[t + st];
-        __syncthreads();
-    }
-    float m = red[0] / (float)H;
+    float m = ti_tree_sum_256(s, red) / (float)H;
+    __syncthreads();   // red is free again for the caller
     m = m + eps;
     return 1.0f / sqrtf(m);
 }

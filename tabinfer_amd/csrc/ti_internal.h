@@ -73,11 +73,88 @@ __device__ __forceinline__ uint4 ti_ld_nt(const uint4* p) {
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-// Wavefront-64 butterfly sum over lanes that share the same (lane / width).
+// ---- lane exchange as VALU operations ------------------------------------------------
+// ti_xor(v, o): the value held by lane (lane ^ o), o in {1, 2, 4, 8, 16, 32}, without
+// an LDS round trip (__shfl_xor lowers to ds_bpermute, ~100+ cycles each, and a chain
+// of them serialises a reduction). DPP within a 16-lane row: quad_perm for 1 and 2,
+// row_shl/row_shr:4 picked by lane bit 2, row_ror:8; across rows the gfx950 permlane
+// swaps: permlane16_swap(v, v) yields {rows 0,0,2,2 ; rows 1,1,3,3} and
+// permlane32_swap(v, v) yields {halves 0,0 ; halves 1,1} (lane layouts checked on
+// the device). `o` must be a compile-time constant after unrolling.
+__device__ __forceinline__ int ti_xor_i(int v, int o) {
+    const int lane = threadIdx.x & 63;
+    switch (o) {
+        case 1: return __builtin_amdgcn_update_dpp(v, v, 0xB1, 0xF, 0xF, false);
+        case 2: return __builtin_amdgcn_update_dpp(v, v, 0x4E, 0xF, 0xF, false);
+        case 4: {
+            const int up = __builtin_amdgcn_update_dpp(v, v, 0x104, 0xF, 0xF, false);   // lane + 4
+            const int dn = __builtin_amdgcn_update_dpp(v, v, 0x114, 0xF, 0xF, false);   // lane - 4
+            return (lane & 4) ? dn : up;
+        }
+        case 8: return __builtin_amdgcn_update_dpp(v, v, 0x128, 0xF, 0xF, false);
+        case 16: {
+            const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+            return (lane & 16) ? (int)r[0] : (int)r[1];
+        }
+        default: {
+            const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+            return (lane & 32) ? (int)r[0] : (int)r[1];
+        }
+    }
+}
+__device__ __forceinline__ float ti_xor(float v, int o) {
+    return __builtin_bit_cast(float, ti_xor_i(__builtin_bit_cast(int, v), o));
+}
+__device__ __forceinline__ uint32_t ti_xor(uint32_t v, int o) { return (uint32_t)ti_xor_i((int)v, o); }
+__device__ __forceinline__ int ti_xor(int v, int o) { return ti_xor_i(v, o); }
+
+// Wavefront-64 butterfly sum over lanes that share the same (lane / width): pairs at
+// distance width/2 first, down to 1 (every lane of a segment ends with the same sum).
 template <int WIDTH>
 __device__ __forceinline__ float ti_seg_sum(float v) {
 #pragma unroll
-    for (int o = WIDTH / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    for (int o = WIDTH / 2; o > 0; o >>= 1) v += ti_xor(v, o);
+    return v;
+}
+
+// Maximum of a non-negative float over each aligned group of 32 lanes, returned in
+// every lane. Max is exact in any order, so the pairing may differ from xor: after
+// quads agree, row_half_mirror and row_mirror pair each lane with the other half of
+// its 8- and 16-lane block. Compared as unsigned bit patterns (valid for x >= 0).
+__device__ __forceinline__ float ti_max32_nonneg(float x) {
+    uint32_t m = __builtin_bit_cast(uint32_t, x);
+    m = max(m, (uint32_t)__builtin_amdgcn_update_dpp((int)m, (int)m, 0xB1, 0xF, 0xF, false));
+    m = max(m, (uint32_t)__builtin_amdgcn_update_dpp((int)m, (int)m, 0x4E, 0xF, 0xF, false));
+    m = max(m, (uint32_t)__builtin_amdgcn_update_dpp((int)m, (int)m, 0x141, 0xF, 0xF, false));
+    m = max(m, (uint32_t)__builtin_amdgcn_update_dpp((int)m, (int)m, 0x140, 0xF, 0xF, false));
+    const auto r = __builtin_amdgcn_permlane16_swap((int)m, (int)m, false, false);
+    m = max((uint32_t)r[0], (uint32_t)r[1]);
+    return __builtin_bit_cast(float, m);
+}
+
+// OR of a word over each aligned quad of lanes, in every lane of the quad (packs four
+// lanes' bytes into one word).
+__device__ __forceinline__ uint32_t ti_quad_or(uint32_t v) {
+    v |= (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0xB1, 0xF, 0xF, false);
+    v |= (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x4E, 0xF, 0xF, false);
+    return v;
+}
+
+// Total of one float per thread over a 256-thread workgroup, in the association of
+// the tree `for st = 128..1: red[t] += red[t + st]` (rmsnormQ's order), returned in
+// every thread with one barrier: levels 128 and 64 combine the four waves' partials
+// read back from LDS, levels 32..1 are an exact xor butterfly (lane t < st adds lane
+// t + st, as the tree does; the partner lane computes the same sum). `red` holds 256
+// floats and must not be reused before the caller's next barrier.
+__device__ __forceinline__ float ti_tree_sum_256(float s, float* red) {
+    const int t = threadIdx.x, l = t & 63;
+    red[t] = s;
+    __syncthreads();
+    const float a = red[l] + red[l + 128];
+    const float b = red[l + 64] + red[l + 192];
+    float v = a + b;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = v + ti_xor(v, o);
     return v;
 }
 
