@@ -894,6 +894,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_fused_q8(AttnFArgs a) {
         }
     };
     load(0, gw * WT);
+    TI_ISSUE_FENCE();
 
     const int pos = a.dev ? pos_dev : a.pos;
     const float csj = a.dev ? cs_dev : cs_arg;

@@ -96,14 +96,22 @@ __device__ __forceinline__ void act_prologue(const FArgs& a, uint32_t* s_xq, flo
 // reference's order (per-thread strided partials, then the 128..1 tree); a 32-group
 // is 32 consecutive lanes, whose absmax is a 32-lane butterfly (max is exact in any
 // order), so every code and scale equals q8_group's.
-template <int EPT>
+template <int EPT, bool FULL>
 struct ActRegs {
+    // CONTIG: K = 256*EPT (FULL) and EPT divides 32 or is a multiple of it. The quantizer
+    // then works on a second, contiguous copy (thread t: elements EPT*t .. EPT*t+EPT-1),
+    // so a 32-group spans 32/EPT neighbouring lanes and each thread computes its
+    // group's scale once; the strided copy only feeds the sum of squares.
+    static constexpr bool CONTIG = FULL && (EPT <= 32 ? (32 % EPT == 0) : (EPT % 32 == 0));
+    static constexpr int NC = CONTIG ? EPT : 1;
     float x[EPT];
     uint16_t w[EPT];
+    float xc[NC];
+    uint16_t wc[NC];
 };
 
-template <int MODE, int EPT>
-__device__ __forceinline__ void act_regs_load(const FArgs& a, ActRegs<EPT>& r) {
+template <int MODE, int EPT, bool FULL>
+__device__ __forceinline__ void act_regs_load(const FArgs& a, ActRegs<EPT, FULL>& r) {
     const int t = threadIdx.x;
     // unconditional loads (clamped index, value masked after): straight-line code
     // lets the compiler wait for exactly these loads, not the weights behind them
@@ -114,6 +122,23 @@ __device__ __forceinline__ void act_regs_load(const FArgs& a, ActRegs<EPT>& r) {
         r.x[i] = a.x[ec];
         if (MODE == MODE_NORM) r.w[i] = a.nw[ec];
     }
+    if constexpr (ActRegs<EPT, FULL>::CONTIG) {   // FULL: K = 256*EPT exactly
+        if constexpr (EPT % 4 == 0) {
+            const float4* xs4 = reinterpret_cast<const float4*>(a.x + (size_t)EPT * t);
+#pragma unroll
+            for (int i = 0; i < EPT / 4; i++) {
+                const float4 v = xs4[i];
+                r.xc[4 * i] = v.x; r.xc[4 * i + 1] = v.y; r.xc[4 * i + 2] = v.z; r.xc[4 * i + 3] = v.w;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < EPT; i++) r.xc[i] = a.x[(size_t)EPT * t + i];
+        }
+        if (MODE == MODE_NORM) {
+#pragma unroll
+            for (int i = 0; i < EPT; i++) r.wc[i] = a.nw[(size_t)EPT * t + i];
+        }
+    }
 #pragma unroll
     for (int i = 0; i < EPT; i++) {
         if (t + 256 * i >= a.K) {
@@ -123,10 +148,33 @@ __device__ __forceinline__ void act_regs_load(const FArgs& a, ActRegs<EPT>& r) {
     }
 }
 
-template <int MODE, int EPT>
-__device__ __forceinline__ void act_regs_quant(const FArgs& a, ActRegs<EPT>& r, uint32_t* s_xq, float* s_xs,
+// group absmax over the 32/EPT lanes of a contiguous 32-group (after the in-thread max)
+template <int EPT>
+__device__ __forceinline__ float group_max_contig(float m) {
+    uint32_t u = __builtin_bit_cast(uint32_t, m);
+    if constexpr (EPT <= 16) u = max(u, (uint32_t)__builtin_amdgcn_update_dpp((int)u, (int)u, 0xB1, 0xF, 0xF, false));
+    if constexpr (EPT <= 8) u = max(u, (uint32_t)__builtin_amdgcn_update_dpp((int)u, (int)u, 0x4E, 0xF, 0xF, false));
+    if constexpr (EPT <= 4) u = max(u, (uint32_t)__builtin_amdgcn_update_dpp((int)u, (int)u, 0x141, 0xF, 0xF, false));
+    if constexpr (EPT <= 2) u = max(u, (uint32_t)__builtin_amdgcn_update_dpp((int)u, (int)u, 0x140, 0xF, 0xF, false));
+    if constexpr (EPT <= 1) {
+        const auto r = __builtin_amdgcn_permlane16_swap((int)u, (int)u, false, false);
+        u = max((uint32_t)r[0], (uint32_t)r[1]);
+    }
+    return __builtin_bit_cast(float, u);
+}
+
+// q8_group's arithmetic for one element, given its group scale
+__device__ __forceinline__ int q8_code(float v, float inv) {
+    const float p = v * inv;
+    int qi = (int)rintf(p);
+    return qi < -127 ? -127 : (qi > 127 ? 127 : qi);
+}
+
+template <int MODE, int EPT, bool FULL>
+__device__ __forceinline__ void act_regs_quant(const FArgs& a, ActRegs<EPT, FULL>& r, uint32_t* s_xq, float* s_xs,
                                                float* red) {
     const int t = threadIdx.x;
+    float inv_rms = 0.0f;
     if (MODE == MODE_NORM) {
         float s = 0.0f;
 #pragma unroll
@@ -136,29 +184,83 @@ __device__ __forceinline__ void act_regs_quant(const FArgs& a, ActRegs<EPT>& r, 
         }
         float m = ti_tree_sum_256(s, red) / (float)a.K;
         m = m + a.eps;
-        const float inv = 1.0f / sqrtf(m);
+        inv_rms = 1.0f / sqrtf(m);
+    }
+    if constexpr (ActRegs<EPT, FULL>::CONTIG) {
+        float v[EPT];
+        float mx = 0.0f;
 #pragma unroll
         for (int i = 0; i < EPT; i++) {
-            float p = r.x[i] * inv;
-            r.x[i] = p * ti_h2f(r.w[i]);
+            v[i] = r.xc[i];
+            if (MODE == MODE_NORM) {
+                const float p = v[i] * inv_rms;
+                v[i] = p * ti_h2f(r.wc[i]);
+            }
         }
-    }
-    uint8_t* qb = reinterpret_cast<uint8_t*>(s_xq);
-    float gmx[EPT];
+        uint8_t* qb = reinterpret_cast<uint8_t*>(s_xq);
+        if constexpr (EPT <= 32) {
 #pragma unroll
-    for (int i = 0; i < EPT; i++) gmx[i] = ti_max32_nonneg(fabsf(r.x[i]));   // independent chains, all VALU
-#pragma unroll
-    for (int i = 0; i < EPT; i++) {
-        const int e = t + 256 * i;
-        const float mx = gmx[i];
-        if (e < a.K) {
+            for (int i = 0; i < EPT; i++) mx = fmaxf(mx, fabsf(v[i]));
+            mx = group_max_contig<EPT>(mx);
             const float scale = mx / 127.0f;
             const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
-            const float p = r.x[i] * inv;
-            int qi = (int)rintf(p);
-            qi = qi < -127 ? -127 : (qi > 127 ? 127 : qi);
-            qb[e] = (uint8_t)(qi & 0xff);
-            if ((t & 31) == 0) s_xs[e >> 5] = scale;
+            uint32_t wd[(EPT + 3) / 4] = {};
+#pragma unroll
+            for (int i = 0; i < EPT; i++) wd[i / 4] |= (uint32_t)(q8_code(v[i], inv) & 0xff) << (8 * (i % 4));
+            if constexpr (EPT >= 4) {
+#pragma unroll
+                for (int k = 0; k < EPT / 4; k++) s_xq[EPT / 4 * t + k] = wd[k];
+            } else {
+#pragma unroll
+                for (int i = 0; i < EPT; i++) qb[EPT * t + i] = (uint8_t)((wd[0] >> (8 * i)) & 0xff);
+            }
+            if (t % (32 / EPT) == 0) s_xs[EPT * t / 32] = scale;
+        } else {   // several whole groups per thread
+#pragma unroll
+            for (int g = 0; g < EPT / 32; g++) {
+                float gm = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 32; i++) gm = fmaxf(gm, fabsf(v[32 * g + i]));
+                const float scale = gm / 127.0f;
+                const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    uint32_t wd = 0;
+#pragma unroll
+                    for (int i = 0; i < 4; i++) wd |= (uint32_t)(q8_code(v[32 * g + 4 * k + i], inv) & 0xff) << (8 * i);
+                    s_xq[EPT / 4 * t + 8 * g + k] = wd;
+                }
+                s_xs[EPT / 32 * t + g] = scale;
+            }
+        }
+    } else {
+        if (MODE == MODE_NORM) {
+#pragma unroll
+            for (int i = 0; i < EPT; i++) {
+                float p = r.x[i] * inv_rms;
+                r.x[i] = p * ti_h2f(r.w[i]);
+            }
+        }
+        uint8_t* qb = reinterpret_cast<uint8_t*>(s_xq);
+        // EPT independent chains (group max, two IEEE divisions, rounding) computed
+        // without branches so they interleave; only the LDS stores are predicated
+        float gsc[EPT];
+        int gq[EPT];
+#pragma unroll
+        for (int i = 0; i < EPT; i++) {
+            const float mx = ti_max32_nonneg(fabsf(r.x[i]));
+            const float scale = mx / 127.0f;
+            const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
+            gsc[i] = scale;
+            gq[i] = q8_code(r.x[i], inv);
+        }
+#pragma unroll
+        for (int i = 0; i < EPT; i++) {
+            const int e = t + 256 * i;
+            if (e < a.K) {
+                qb[e] = (uint8_t)(gq[i] & 0xff);
+                if ((t & 31) == 0) s_xs[e >> 5] = gsc[i];
+            }
         }
     }
     __syncthreads();
@@ -260,11 +362,12 @@ __global__ __launch_bounds__(256) void k_fgemv(FArgs a) {
         }
     };
     constexpr int EPT = (GPR * 32 + 255) / 256;
-    ActRegs<EPT> ar;
-    if (MODE != MODE_Q8) act_regs_load<MODE, EPT>(a, ar);
+    ActRegs<EPT, GPR % 8 == 0> ar;
+    if (MODE != MODE_Q8) act_regs_load<MODE>(a, ar);
     load(0, active ? b : 0);   // unconditional (block 0 for idle waves): no branch between the activation and weight loads
+    TI_ISSUE_FENCE();
     if (MODE == MODE_Q8) act_prologue<MODE>(a, s_xq, s_xs, red);
-    else act_regs_quant<MODE, EPT>(a, ar, s_xq, s_xs, red);
+    else act_regs_quant<MODE>(a, ar, s_xq, s_xs, red);
     if (!active) return;
     ActQ8 act[GPL];
 #pragma unroll
@@ -348,10 +451,11 @@ __global__ __launch_bounds__(256) void k_gateup_q8out(FArgs a) {
             }
         }
     };
-    ActRegs<EPT> ar;
-    act_regs_load<MODE_NORM, EPT>(a, ar);
+    ActRegs<EPT, GPR % 8 == 0> ar;
+    act_regs_load<MODE_NORM>(a, ar);
     load(ch < nchunks ? ch : 0);
-    act_regs_quant<MODE_NORM, EPT>(a, ar, s_xq, s_xs, red);
+    TI_ISSUE_FENCE();
+    act_regs_quant<MODE_NORM>(a, ar, s_xq, s_xs, red);
     ActQ8 act[GPL];
 #pragma unroll
     for (int j = 0; j < GPL; j++) load_act_q8(s_xq, s_xs, li + LPR * j, act[j]);
@@ -518,6 +622,7 @@ __global__ __launch_bounds__(256) void k_lmhead(LmArgs a) {
         wr[i] = a.nw[ec];
     }
     load(0, active ? b : 0);   // unconditional (block 0 for idle waves): no branch between the activation and weight loads
+    TI_ISSUE_FENCE();
 #pragma unroll
     for (int i = 0; i < EPT; i++) {
         if (tid + 256 * i >= a.K) {

@@ -71,6 +71,7 @@ __global__ __launch_bounds__(256) void k_gemv_q4_q8(const uint32_t* __restrict__
         yold[buf] = y[orow];
     };
     load(0, b);
+    TI_ISSUE_FENCE();
     ActQ8 a[GPL];
 #pragma unroll
     for (int j = 0; j < GPL; j++) act_q8_from_words(araw[j], asc[j], a[j]);

@@ -84,24 +84,53 @@ __device__ __forceinline__ uint16_t ld_nt(const uint16_t* p) { return __builtin_
 
 // Sum R per-lane accumulators across the LPR lanes that share them, leaving the
 // total of accumulator (li / (LPR/R)) in every lane: each of the first log2(R)
-// butterfly steps hands half of the remaining accumulators to the partner lane,
-// so the whole reduction costs R-1 + log2(LPR/R) shuffles instead of R*log2(LPR).
+// butterfly steps hands half of the remaining accumulators to the partner lane
+// (lane li ^ o): the lane whose bit o is set keeps the upper half and receives the
+// partner's upper half, the other keeps and receives the lower half. Costs R-1 +
+// log2(LPR/R) exchanges instead of R*log2(LPR). The exchanges need no per-lane
+// selects, which the compiler would otherwise turn into dynamic register-array
+// indexing: across 32/16 lanes the permlane swaps deliver exactly (kept, received)
+// as their two results; within a row, bank-masked DPP writes the upper lanes' values
+// over the lower lanes'. Every sum is kept + received, as a plain xor butterfly forms it.
+__device__ __forceinline__ float tr_pair(float lo, float hi, int o) {
+    const int l = __builtin_bit_cast(int, lo), h = __builtin_bit_cast(int, hi);
+    if (o == 32) {
+        const auto r = __builtin_amdgcn_permlane32_swap(l, h, false, false);
+        return __builtin_bit_cast(float, (int)r[0]) + __builtin_bit_cast(float, (int)r[1]);
+    }
+    if (o == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(l, h, false, false);
+        return __builtin_bit_cast(float, (int)r[0]) + __builtin_bit_cast(float, (int)r[1]);
+    }
+    if (o == 8) {   // banks 2,3 (lanes 8-15 of a row) hold the upper half; row_ror:8 is xor 8
+        const int keep = __builtin_amdgcn_update_dpp(l, h, 0xE4, 0xF, 0xC, false);
+        int recv = __builtin_amdgcn_update_dpp(l, l, 0x128, 0xF, 0x3, false);
+        recv = __builtin_amdgcn_update_dpp(recv, h, 0x128, 0xF, 0xC, false);
+        return __builtin_bit_cast(float, keep) + __builtin_bit_cast(float, recv);
+    }
+    if (o == 4) {   // banks 1,3 hold the upper half; partner lane +4 (row_shl) below, -4 (row_shr) above
+        const int keep = __builtin_amdgcn_update_dpp(l, h, 0xE4, 0xF, 0xA, false);
+        int recv = __builtin_amdgcn_update_dpp(l, l, 0x104, 0xF, 0x5, false);
+        recv = __builtin_amdgcn_update_dpp(recv, h, 0x114, 0xF, 0xA, false);
+        return __builtin_bit_cast(float, keep) + __builtin_bit_cast(float, recv);
+    }
+    // o = 2, 1: both halves exchanged, the sums selected (no array element is selected)
+    const bool up = (threadIdx.x & o) != 0;
+    const float slo = lo + ti_xor(lo, o), shi = hi + ti_xor(hi, o);
+    return up ? shi : slo;
+}
+
 template <int LPR, int R>
 __device__ __forceinline__ float transpose_reduce(float (&v)[R], int li) {
     static_assert(R <= LPR || LPR == 1, "R must not exceed the lanes per row");
+    (void)li;
     int k = R;
 #pragma unroll
     for (int o = LPR / 2; o > 0; o >>= 1) {
         if (k > 1) {
-            const bool up = (li & o) != 0;
 #pragma unroll
-            for (int i = 0; i < R / 2; i++) {
-                if (i < k / 2) {
-                    float send = up ? v[i] : v[i + k / 2];
-                    float keep = up ? v[i + k / 2] : v[i];
-                    v[i] = keep + ti_xor(send, o);
-                }
-            }
+            for (int i = 0; i < R / 2; i++)
+                if (i < k / 2) v[i] = tr_pair(v[i], v[i + k / 2], o);
             k >>= 1;
         } else {
             v[0] += ti_xor(v[0], o);

@@ -73,6 +73,11 @@ __device__ __forceinline__ uint4 ti_ld_nt(const uint4* p) {
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// Keep every memory operation issued so far above this point: the scheduler may
+// otherwise sink a kernel's weight loads below the wait for its activation loads,
+// which serialises two memory round trips that were meant to overlap.
+#define TI_ISSUE_FENCE() __builtin_amdgcn_sched_barrier(0)
+
 // ---- lane exchange as VALU operations ------------------------------------------------
 // ti_xor(v, o): the value held by lane (lane ^ o), o in {1, 2, 4, 8, 16, 32}, without
 // an LDS round trip (__shfl_xor lowers to ds_bpermute, ~100+ cycles each, and a chain
