@@ -828,6 +828,108 @@ __device__ __forceinline__ float head_norm_rope(float x, int j, int hd, float wj
 // signed int8 code k of a packed word as (code + 128): one v_cvt_f32_ubyte
 __device__ __forceinline__ float ub(uint32_t wflip, int k) { return (float)((wflip >> (8 * k)) & 0xffu); }
 
+// The end of a fused attention workgroup, shared by the decode kernels: merge the 4
+// waves' slots (s_red: unnormalised outputs with the +128 code offset already removed,
+// s_wml: per-wave (m, l)) into this split's partial and publish it; the last split of
+// KV head hk to arrive merges the NS partials by log-sum-exp, writes the head outputs
+// (and their quantQ8 codes) and resets the counter.
+template <int HD, int G, int TPW>
+__device__ __forceinline__ void attn_merge_tail(const AttnFArgs& a, int hk, int w, int NS, int ntiles, bool valid,
+                                                float (&s_red)[4][TPW][G * HD], float (&s_wml)[4][G][2],
+                                                float (&s_ml)[G][ATTF_MAXS][2], float (&s_e)[G][ATTF_MAXS], float* s_L,
+                                                int* s_last_p) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int NW = NS * 4;
+    int& s_last = *s_last_p;
+    __syncthreads();
+    // merge the 4 waves x TPW slots into this split's partial and publish it
+    const size_t ms = (size_t)NS;
+    if (tid < G * HD) {
+        const int hh = tid / HD, d = tid % HD;
+        float M = s_wml[0][hh][0];
+#pragma unroll
+        for (int q = 1; q < 4; q++) M = fmaxf(M, s_wml[q][hh][0]);
+        float O = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            float sq = 0.0f;
+#pragma unroll
+            for (int t = 0; t < TPW; t++) sq += s_red[q][t][tid];
+            O += sq * expf(s_wml[q][hh][0] - M);
+        }
+        ti_pub_store(a.po + ((size_t)(hk * G + hh) * ms + w) * HD + d, O);
+    }
+    if (tid < G) {
+        float M = s_wml[0][tid][0];
+#pragma unroll
+        for (int q = 1; q < 4; q++) M = fmaxf(M, s_wml[q][tid][0]);
+        float L = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 4; q++) L += s_wml[q][tid][1] * expf(s_wml[q][tid][0] - M);
+        ti_pub_store(a.pml + ((size_t)(hk * G + tid) * ms + w) * 2, M);
+        ti_pub_store(a.pml + ((size_t)(hk * G + tid) * ms + w) * 2 + 1, L);
+    }
+    ti_stores_done();
+    __syncthreads();
+    if (tid == 0) s_last = ti_arrive(a.counter + hk) == (unsigned)(NS - 1);
+    __syncthreads();
+    if (!s_last) return;
+    // the last split of hk: log-sum-exp over the splits that saw a tile; the o loads
+    // are issued before the (m, l) pairs are reduced, one round trip for both
+    const int nused = ntiles < NW ? (ntiles + 3) / 4 : NS;
+    // every split's o in one round trip (indices past nused repeat the last one and get
+    // weight 0), then the splits' weights once per head: one wave per head, lane = split
+    float ov[ATTF_MAXS];
+    const int oh = tid / HD, od = tid % HD;
+    const float* pp = a.po + (size_t)(hk * G + (oh < G ? oh : 0)) * ms * HD + od;
+#pragma unroll
+    for (int i = 0; i < ATTF_MAXS; i++) ov[i] = ti_pub_load(pp + (size_t)(i < nused ? i : nused - 1) * HD);
+    for (int e = tid; e < G * nused * 2; e += 256) {
+        const int hh = e / (nused * 2), r = e % (nused * 2);
+        s_ml[hh][r >> 1][r & 1] = ti_pub_load(a.pml + ((size_t)(hk * G + hh) * ms + (r >> 1)) * 2 + (r & 1));
+    }
+    __syncthreads();
+    if (wave < G) {
+        const bool in = lane < nused;
+        const float m = in ? s_ml[wave][lane][0] : -3.0e38f;
+        float M = m;
+#pragma unroll
+        for (int o2 = 32; o2 > 0; o2 >>= 1) M = fmaxf(M, ti_xor(M, o2));
+        const float e = in ? expf(m - M) : 0.0f;
+        float L = in ? s_ml[wave][lane][1] * e : 0.0f;
+#pragma unroll
+        for (int o2 = 32; o2 > 0; o2 >>= 1) L += ti_xor(L, o2);
+        s_e[wave][lane] = e;
+        if (lane == 0) s_L[wave] = L;
+    }
+    __syncthreads();
+    if (valid && tid < G * HD) {
+        float o4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int i = 0; i < ATTF_MAXS; i++) o4[i & 3] = fmaf(ov[i], s_e[oh][i], o4[i & 3]);
+        const float o = (o4[0] + o4[1]) + (o4[2] + o4[3]);
+        const float L = s_L[oh];
+        const float res = o / L;
+        const size_t e = (size_t)(hk * G + oh) * HD + od;
+        a.out[e] = res;
+        if (a.oq) {   // quantQ8 of 32 consecutive outputs = 32 consecutive lanes (q8_group's arithmetic)
+            float mx = fabsf(res);
+#pragma unroll
+            for (int o2 = 16; o2 > 0; o2 >>= 1) mx = fmaxf(mx, ti_xor(mx, o2));
+            const float scale = mx / 127.0f;
+            const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
+            const float pq = res * inv;
+            int qi = (int)rintf(pq);
+            qi = qi < -127 ? -127 : (qi > 127 ? 127 : qi);
+            const uint32_t b = (uint32_t)(qi & 0xff);
+            const uint32_t word = ti_quad_or(b << (8 * (lane & 3)));
+            if ((lane & 3) == 0) a.oq[e / 4] = word;
+            if ((lane & 31) == 0) a.os[e / 32] = scale;
+        }
+    }
+    if (tid == 0) __hip_atomic_store(a.counter + hk, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 template <int HD, int G>
 __global__ __launch_bounds__(256, 2) void k_attn_fused_q8(AttnFArgs a) {
     static_assert(G >= 1 && G <= 2 && (HD == 64 || HD == 128), "fused attention: G <= 2, HD 64 or 128");
@@ -1062,93 +1164,375 @@ __global__ __launch_bounds__(256, 2) void k_attn_fused_q8(AttnFArgs a) {
             s_wml[wave][hh][1] = l_run[hh];
         }
     }
-    __syncthreads();
-    // merge the 4 waves x TPW slots into this split's partial and publish it
-    const size_t ms = (size_t)NS;
-    if (tid < G * HD) {
-        const int hh = tid / HD, d = tid % HD;
-        float M = s_wml[0][hh][0];
+    attn_merge_tail<HD, G, TPW>(a, hk, w, NS, ntiles, valid, s_red, s_wml, s_ml, s_e, s_L, &s_last);
+}
+
+// head_dim 128 variant of k_attn_fused_q8 with Q K^T on the matrix cores.
+// q (normed and roped, f32) is split per head into three int8 limbs,
+// q = S0*c0 + S1*c1 + S2*c2 with S0 = max|q|/127, S1 = S0/254, S2 = S1/254 (each limb's
+// residual is within half its step, so |c| <= 127 and the representation error is
+// below max|q| * 6.2e-8, the size of f32 rounding). One v_mfma_i32_16x16x32_i8 per
+// 32-dim scale group and 16 tokens gives the exact int32 dots of all limbs:
+//   A (16 x 32): row r = 4*(head) + limb, rows with limb 3 zero, rows 8..15 repeat 0..7;
+//   B (32 x 16): column = token, K = the group's 32 dims; lane l supplies 8 codes of
+//                token l%16 at dims 32g + 8(l/16)..+7. K tiles reach LDS by direct
+//                global->LDS loads in the coalesced row-slice order (8 lanes per 128-byte
+//                token row; the 16-byte slices XOR-permuted by token, passes 1088 bytes
+//                apart, so the 8-byte operand reads hit distinct banks) and are read
+//                back per lane in the MFMA order;
+//   C: lane l holds rows 4(l/16)..+3 of column l%16 = the three limb dots of token l%16
+//      for head (l/16)%2, which it scales by its token's group scale itself.
+// So every lane ends with the score of one (head, token) pair; no code of K is
+// converted on the VALU. P*V stays on the VALU as in k_attn_fused_q8 (4 passes of 8
+// tokens, 16 dims per lane), the probabilities reaching the V lanes by ds_bpermute.
+template <int G>
+__global__ __launch_bounds__(256, 2) void k_attn_fused_mq8(AttnFArgs a) {
+    static_assert(G == 1 || G == 2, "MFMA decode attention: G <= 2");
+    constexpr int HD = 128;
+    constexpr int LPT = HD / 16;               // lanes per token row in the P*V layout
+    constexpr int TPW = 64 / LPT;              // tokens per P*V pass
+    constexpr int PASSES = 4;
+    constexpr int WT = PASSES * TPW;           // tokens per wave tile (32 = 2 MFMA blocks of 16)
+    constexpr int NG = HD / 32;
+    typedef int v4i __attribute__((ext_vector_type(4)));
+    __shared__ float s_qmax[2];
+    __shared__ __align__(8) int8_t s_ql[G][3][HD];
+    __shared__ __align__(16) uint32_t s_kw[HD / 4];
+    __shared__ __align__(16) uint32_t s_vw[HD / 4];
+    __shared__ __align__(16) float s_ksc[NG];
+    __shared__ float s_vsc[NG];
+    // per wave: two K tiles (4 passes of 1 KB, 1088 bytes apart so that passes 2b and
+    // 2b+1 sit 64 bytes apart in the banks) during the tile loop, then the wave's P*V
+    // slots for the merge (s_red), which fit in the same bytes
+    constexpr int KT_PASS = 1024 + 64;
+    constexpr int KT_BYTES = 4 * KT_PASS;
+    static_assert(TPW * G * HD * 4 <= 2 * KT_BYTES, "s_red must fit the K tile region");
+    __shared__ __align__(16) uint8_t s_kt[4][2 * KT_BYTES];
+    float (&s_red)[4][TPW][G * HD] = *reinterpret_cast<float (*)[4][TPW][G * HD]>(&s_kt[0][0]);
+    __shared__ float s_wml[4][G][2];
+    __shared__ float s_ml[G][ATTF_MAXS][2];
+    __shared__ float s_e[G][ATTF_MAXS];
+    __shared__ float s_L[G];
+    __shared__ int s_last;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int w = blockIdx.x % a.ns;           // split-major across the XCDs (see k_attn_fused_q8)
+    const int hk = blockIdx.x / a.ns;
+    const int NS = a.ns;
+    const int NW = NS * 4;
+    const int gw = w * 4 + wave;
+    const int tp = lane / LPT, sl = lane % LPT;   // P*V layout
+    const int tk = lane & 15, kq4 = lane >> 4;     // MFMA layout: token of the block, K quarter
+    const float qk_scale = 1.0f / (127.0f * sqrtf((float)HD));
+    const uint8_t* kqb = reinterpret_cast<const uint8_t*>(a.kq);
+    const float4* ks4 = reinterpret_cast<const float4*>(a.ks);
+    uint8_t* ktw = &s_kt[wave][0];
+    const uint4* vq4 = reinterpret_cast<const uint4*>(a.vq);
+
+    // ---- every load that does not depend on the position, in one batch. Wave 0 (and 1
+    // when G = 2) holds query head `wave`, wave 2 the new K row, wave 3 the new V row;
+    // lane L holds elements L and L + 64, so RMSNorm, RoPE and the limb split of q run in
+    // registers (an LDS access before the first tile's direct loads land would wait for them)
+    const int pos_dev = *a.dpos;
+    const float* xrow = wave < 2 ? a.q + (size_t)(hk * G + (wave < G ? wave : 0)) * HD
+                                 : (wave == 2 ? a.k : a.v) + (size_t)hk * HD;
+    const uint16_t* nwrow = wave < 2 ? a.qw : a.kw;
+    const float x0 = xrow[lane], x1 = xrow[lane + 64];
+    const float w0 = ti_h2f(nwrow[lane]), w1 = ti_h2f(nwrow[lane + 64]);
+    const float c_dev = a.rope_cur[lane], s_dev = a.rope_cur[lane + 64];
+    const float c_arg = a.rope_row[lane], s_arg = a.rope_row[lane + 64];
+    float4 ksb[2][2];            // [buffer][block]: the 4 group scales of this lane's MFMA token
+    uint4 vw[2][PASSES];
+    float vsc[2][PASSES];
+    int lim = a.cap;
+    auto load = [&](int buf, int t0) {
 #pragma unroll
-        for (int q = 1; q < 4; q++) M = fmaxf(M, s_wml[q][hh][0]);
-        float O = 0.0f;
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            float sq = 0.0f;
-#pragma unroll
-            for (int t = 0; t < TPW; t++) sq += s_red[q][t][tid];
-            O += sq * expf(s_wml[q][hh][0] - M);
+        for (int p = 0; p < PASSES; p++) {   // K: lane (tp, sl) fetches slice sl ^ tp of token p*8 + tp
+            int t = t0 + p * TPW + tp;
+            t = t < lim ? t : lim - 1;
+            const uint8_t* src = kqb + ((size_t)t * a.nKv + hk) * HD + 16 * (sl ^ tp);
+            __builtin_amdgcn_global_load_lds(src, ktw + buf * KT_BYTES + p * KT_PASS, 16, 0, 0);
         }
-        ti_pub_store(a.po + ((size_t)(hk * G + hh) * ms + w) * HD + d, O);
-    }
-    if (tid < G) {
-        float M = s_wml[0][tid][0];
 #pragma unroll
-        for (int q = 1; q < 4; q++) M = fmaxf(M, s_wml[q][tid][0]);
-        float L = 0.0f;
+        for (int b = 0; b < 2; b++) {
+            int t = t0 + 16 * b + tk;
+            t = t < lim ? t : lim - 1;
+            ksb[buf][b] = ks4[(size_t)t * a.nKv + hk];
+        }
 #pragma unroll
-        for (int q = 0; q < 4; q++) L += s_wml[q][tid][1] * expf(s_wml[q][tid][0] - M);
-        ti_pub_store(a.pml + ((size_t)(hk * G + tid) * ms + w) * 2, M);
-        ti_pub_store(a.pml + ((size_t)(hk * G + tid) * ms + w) * 2 + 1, L);
-    }
-    ti_stores_done();
-    __syncthreads();
-    if (tid == 0) s_last = ti_arrive(a.counter + hk) == (unsigned)(NS - 1);
-    __syncthreads();
-    if (!s_last) return;
-    // the last split of hk: log-sum-exp over the splits that saw a tile; the o loads
-    // are issued before the (m, l) pairs are reduced, one round trip for both
-    const int nused = ntiles < NW ? (ntiles + 3) / 4 : NS;
-    // every split's o in one round trip (indices past nused repeat the last one and get
-    // weight 0), then the splits' weights once per head: one wave per head, lane = split
-    float ov[ATTF_MAXS];
-    const int oh = tid / HD, od = tid % HD;
-    const float* pp = a.po + (size_t)(hk * G + (oh < G ? oh : 0)) * ms * HD + od;
+        for (int p = 0; p < PASSES; p++) {
+            int t = t0 + p * TPW + tp;
+            t = t < lim ? t : lim - 1;
+            vw[buf][p] = ti_ld_nt(vq4 + ((size_t)t * a.nKv + hk) * LPT + sl);
+            vsc[buf][p] = a.vs[((size_t)t * a.nKv + hk) * NG + sl / 2];
+        }
+    };
+    // the first tile's K goes through registers (16-byte row slices, as the direct loads
+    // would place them) and is written to LDS after the prologue: a direct load in flight
+    // makes every wait a full one (their completions are not ordered with other loads),
+    // which would hold the q prologue until the whole first tile had landed
+    uint4 kfirst[PASSES];
+    {
+        const int t0 = gw * WT;
 #pragma unroll
-    for (int i = 0; i < ATTF_MAXS; i++) ov[i] = ti_pub_load(pp + (size_t)(i < nused ? i : nused - 1) * HD);
-    for (int e = tid; e < G * nused * 2; e += 256) {
-        const int hh = e / (nused * 2), r = e % (nused * 2);
-        s_ml[hh][r >> 1][r & 1] = ti_pub_load(a.pml + ((size_t)(hk * G + hh) * ms + (r >> 1)) * 2 + (r & 1));
-    }
-    __syncthreads();
-    if (wave < G) {
-        const bool in = lane < nused;
-        const float m = in ? s_ml[wave][lane][0] : -3.0e38f;
-        float M = m;
+        for (int p = 0; p < PASSES; p++) {
+            int t = t0 + p * TPW + tp;
+            t = t < lim ? t : lim - 1;
+            kfirst[p] = ti_ld_nt(reinterpret_cast<const uint4*>(kqb + ((size_t)t * a.nKv + hk) * HD) + sl);
+        }
 #pragma unroll
-        for (int o2 = 32; o2 > 0; o2 >>= 1) M = fmaxf(M, ti_xor(M, o2));
-        const float e = in ? expf(m - M) : 0.0f;
-        float L = in ? s_ml[wave][lane][1] * e : 0.0f;
+        for (int b = 0; b < 2; b++) {
+            int t = t0 + 16 * b + tk;
+            t = t < lim ? t : lim - 1;
+            ksb[0][b] = ks4[(size_t)t * a.nKv + hk];
+        }
 #pragma unroll
-        for (int o2 = 32; o2 > 0; o2 >>= 1) L += ti_xor(L, o2);
-        s_e[wave][lane] = e;
-        if (lane == 0) s_L[wave] = L;
-    }
-    __syncthreads();
-    if (valid && tid < G * HD) {
-        float o4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int i = 0; i < ATTF_MAXS; i++) o4[i & 3] = fmaf(ov[i], s_e[oh][i], o4[i & 3]);
-        const float o = (o4[0] + o4[1]) + (o4[2] + o4[3]);
-        const float L = s_L[oh];
-        const float res = o / L;
-        const size_t e = (size_t)(hk * G + oh) * HD + od;
-        a.out[e] = res;
-        if (a.oq) {   // quantQ8 of 32 consecutive outputs = 32 consecutive lanes (q8_group's arithmetic)
-            float mx = fabsf(res);
-#pragma unroll
-            for (int o2 = 16; o2 > 0; o2 >>= 1) mx = fmaxf(mx, ti_xor(mx, o2));
-            const float scale = mx / 127.0f;
-            const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
-            const float pq = res * inv;
-            int qi = (int)rintf(pq);
-            qi = qi < -127 ? -127 : (qi > 127 ? 127 : qi);
-            const uint32_t b = (uint32_t)(qi & 0xff);
-            const uint32_t word = ti_quad_or(b << (8 * (lane & 3)));
-            if ((lane & 3) == 0) a.oq[e / 4] = word;
-            if ((lane & 31) == 0) a.os[e / 32] = scale;
+        for (int p = 0; p < PASSES; p++) {
+            int t = t0 + p * TPW + tp;
+            t = t < lim ? t : lim - 1;
+            vw[0][p] = ti_ld_nt(vq4 + ((size_t)t * a.nKv + hk) * LPT + sl);
+            vsc[0][p] = a.vs[((size_t)t * a.nKv + hk) * NG + sl / 2];
         }
     }
-    if (tid == 0) __hip_atomic_store(a.counter + hk, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    TI_ISSUE_FENCE();
+
+    const int pos = a.dev ? pos_dev : a.pos;
+    const bool valid = pos >= 0 && pos < a.cap;
+    const int S = valid ? pos + 1 : 0;
+    const int ntiles = (S + WT - 1) / WT;
+    const int last_gw = ntiles > 0 ? (ntiles - 1) % NW : -1;
+    const bool has_pos = valid && (last_gw >> 2) == w;
+    lim = S > 0 ? S : 1;
+    // the MFMA B operands of a tile from LDS (after its loads have landed); the token at
+    // pos comes from its LDS row instead (it is being written by this launch)
+    auto kops = [&](int buf, int t0, long (&kb)[2][NG]) {
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+            const int tl = 16 * b + tk, p = tl >> 3, tq = tl & 7;
+            const bool own = has_pos && t0 + tl >= pos;
+#pragma unroll
+            for (int g = 0; g < NG; g++) {
+                const int sl2 = 2 * g + (kq4 >> 1);
+                const uint8_t* src = own ? reinterpret_cast<const uint8_t*>(s_kw) + 16 * sl2 + 8 * (kq4 & 1)
+                                         : ktw + buf * KT_BYTES + p * KT_PASS + 16 * (tq * 8 + (sl2 ^ tq)) + 8 * (kq4 & 1);
+                kb[b][g] = *reinterpret_cast<const long*>(src);
+            }
+            if (own) ksb[buf][b] = *reinterpret_cast<const float4*>(s_ksc);
+        }
+    };
+
+    const float cr = a.dev ? c_dev : c_arg, sr = a.dev ? s_dev : s_arg;
+    // RMSNorm in attnPrepQ8's order (slot j + slot j+64, then an exact 32..1 xor tree)
+    // and split-half RoPE, for the q heads and the new K row
+    float o0 = x0, o1 = x1;
+    if (wave < 3) {
+        float v = x0 * x0 + x1 * x1;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) v = v + ti_xor(v, o);
+        float m = v / (float)HD;
+        m = m + a.eps;
+        const float inv = 1.0f / sqrtf(m);
+        const float t0n = x0 * inv, t1n = x1 * inv;
+        const float r0 = t0n * w0, r1 = t1n * w1;
+        const float p00 = r0 * cr, p01 = (-r1) * sr;
+        const float p10 = r1 * cr, p11 = r0 * sr;
+        o0 = p00 + p01;
+        o1 = p10 + p11;
+    }
+    if (has_pos && wave >= 2) {   // this token's K (normed, roped) and V rows, snorm int8, into the cache and LDS
+        const bool isv = wave == 3;
+        const float mx0 = fmaxf(ti_max32_nonneg(fabsf(o0)), 1e-12f);
+        const float mx1 = fmaxf(ti_max32_nonneg(fabsf(o1)), 1e-12f);
+        const uint32_t wd0 = ti_quad_or(snorm_code(o0, mx0) << (8 * (lane & 3)));
+        const uint32_t wd1 = ti_quad_or(snorm_code(o1, mx1) << (8 * (lane & 3)));
+        const size_t rowq = ((size_t)pos * a.nKv + hk) * (HD / 4), rows = ((size_t)pos * a.nKv + hk) * NG;
+        uint32_t* gq = isv ? a.vq : a.kq;
+        float* gs = isv ? a.vs : a.ks;
+        uint32_t* lq = isv ? s_vw : s_kw;
+        float* lsc = isv ? s_vsc : s_ksc;
+        if ((lane & 3) == 0) {
+            gq[rowq + lane / 4] = wd0;
+            gq[rowq + 16 + lane / 4] = wd1;
+            lq[lane / 4] = wd0;
+            lq[16 + lane / 4] = wd1;
+        }
+        if ((lane & 31) == 0) {
+            gs[rows + lane / 32] = mx0;
+            gs[rows + 2 + lane / 32] = mx1;
+            lsc[lane / 32] = mx0;
+            lsc[2 + lane / 32] = mx1;
+        }
+    }
+    if (wave < G) {   // q limbs: q = S0*c0 + S1*c1 + S2*c2, codes into LDS
+        float qm = fmaxf(fabsf(o0), fabsf(o1));
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) qm = fmaxf(qm, ti_xor(qm, o));
+        const float S0 = qm / 127.0f, S1 = S0 / 254.0f, S2 = S1 / 254.0f;
+        const float i0 = S0 > 0.0f ? 1.0f / S0 : 0.0f, i1 = S1 > 0.0f ? 1.0f / S1 : 0.0f, i2 = S2 > 0.0f ? 1.0f / S2 : 0.0f;
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+            const float v = e ? o1 : o0;
+            const float c0 = fminf(fmaxf(rintf(v * i0), -127.0f), 127.0f);
+            const float r1 = fmaf(-S0, c0, v);
+            const float c1 = fminf(fmaxf(rintf(r1 * i1), -127.0f), 127.0f);
+            const float r2 = fmaf(-S1, c1, r1);
+            const float c2 = fminf(fmaxf(rintf(r2 * i2), -127.0f), 127.0f);
+            s_ql[wave][0][lane + 64 * e] = (int8_t)c0;
+            s_ql[wave][1][lane + 64 * e] = (int8_t)c1;
+            s_ql[wave][2][lane + 64 * e] = (int8_t)c2;
+        }
+        if (lane == 0) s_qmax[wave] = qm;
+    }
+#pragma unroll
+    for (int p = 0; p < PASSES; p++)   // the first tile's K into LDS buffer 0, slot (tp, sl ^ tp)
+        *reinterpret_cast<uint4*>(ktw + p * KT_PASS + 16 * (tp * 8 + (sl ^ tp))) = kfirst[p];
+    __syncthreads();
+
+    // ---- the MFMA A operands (row = lane%16: head ah, limb alimb) and this lane's limb scales
+    const int arow = lane & 15;
+    const int ah = G == 2 ? (arow >> 2) & 1 : 0, alimb = arow & 3;
+    const int sh = G == 2 ? (lane >> 4) & 1 : 0;          // head of this lane's scores
+    float Sq[2][3];
+#pragma unroll
+    for (int hh = 0; hh < 2; hh++) {
+        const float qm = hh < G ? s_qmax[hh] : 0.0f;
+        Sq[hh][0] = qm / 127.0f;
+        Sq[hh][1] = Sq[hh][0] / 254.0f;
+        Sq[hh][2] = Sq[hh][1] / 254.0f;
+    }
+    long qa[NG];
+#pragma unroll
+    for (int g = 0; g < NG; g++) {
+        const long v = *reinterpret_cast<const long*>(&s_ql[ah][alimb < 3 ? alimb : 0][g * 32 + 8 * kq4]);
+        qa[g] = alimb < 3 ? v : 0;
+    }
+    const float L0 = Sq[sh][0], L1 = Sq[sh][1], L2 = Sq[sh][2];
+
+    float m_run = -3.0e38f, l_lane = 0.0f;   // score lanes: running max of head sh, partial sum of p
+    float acc[G][16], pws[G];                 // P*V lanes
+#pragma unroll
+    for (int hh = 0; hh < G; hh++) {
+        pws[hh] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) acc[hh][i] = 0.0f;
+    }
+
+    auto process = [&](int buf, int t0, const long (&kb)[2][NG]) {
+        if (has_pos && t0 + WT >= S) {   // the tile holding pos: that V row (and clamped reads past it) from LDS
+#pragma unroll
+            for (int p = 0; p < PASSES; p++) {
+                if (t0 + p * TPW + tp >= pos) {
+                    vw[buf][p] = reinterpret_cast<const uint4*>(s_vw)[sl];
+                    vsc[buf][p] = s_vsc[sl / 2];
+                }
+            }
+        }
+        // scores of this lane's (head sh, token tk) in blocks 0 and 1
+        float sc[2];
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+            const float kg[NG] = {ksb[buf][b].x, ksb[buf][b].y, ksb[buf][b].z, ksb[buf][b].w};
+            float d = 0.0f;
+#pragma unroll
+            for (int g = 0; g < NG; g++) {
+                const v4i z = {0, 0, 0, 0};
+                const v4i c = __builtin_amdgcn_mfma_i32_16x16x32_i8(qa[g], kb[b][g], z, 0, 0, 0);
+                const float lq = fmaf(L2, (float)c[2], fmaf(L1, (float)c[1], L0 * (float)c[0]));
+                d = fmaf(kg[g], lq, d);
+            }
+            sc[b] = t0 + 16 * b + tk < S ? d * qk_scale : -3.0e38f;
+        }
+        // online softmax per head over the 16 lanes of a row (rows 2,3 repeat rows 0,1)
+        float mt = fmaxf(sc[0], sc[1]);
+        mt = fmaxf(mt, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, mt), __builtin_bit_cast(int, mt), 0xB1, 0xF, 0xF, false)));
+        mt = fmaxf(mt, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, mt), __builtin_bit_cast(int, mt), 0x4E, 0xF, 0xF, false)));
+        mt = fmaxf(mt, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, mt), __builtin_bit_cast(int, mt), 0x141, 0xF, 0xF, false)));
+        mt = fmaxf(mt, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, mt), __builtin_bit_cast(int, mt), 0x140, 0xF, 0xF, false)));
+        const float mn = fmaxf(m_run, mt);
+        const float corr = expf(m_run - mn);
+        m_run = mn;
+        float pe[2];
+#pragma unroll
+        for (int b = 0; b < 2; b++) pe[b] = t0 + 16 * b + tk < S ? expf(sc[b] - mn) : 0.0f;
+        l_lane = fmaf(l_lane, corr, pe[0] + pe[1]);
+        // P*V: rescale only when a head's maximum moved (wave-uniform test)
+        const float c0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, corr), 0));
+        const float c1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, corr), 16));
+        const float cs[2] = {c0, c1};
+#pragma unroll
+        for (int hh = 0; hh < G; hh++) {
+            if (cs[hh] != 1.0f) {
+                pws[hh] *= cs[hh];
+#pragma unroll
+                for (int i = 0; i < 16; i++) acc[hh][i] *= cs[hh];
+            }
+        }
+#pragma unroll
+        for (int p = 0; p < PASSES; p++) {
+            const bool live = t0 + p * TPW + tp < S;
+            const int src = (p & 1) * TPW + tp;          // lane of this token's score in head 0; head 1 is +16
+            const uint32_t ww[4] = {vw[buf][p].x ^ 0x80808080u, vw[buf][p].y ^ 0x80808080u,
+                                    vw[buf][p].z ^ 0x80808080u, vw[buf][p].w ^ 0x80808080u};
+#pragma unroll
+            for (int hh = 0; hh < G; hh++) {
+                const float pv = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(4 * (src + 16 * hh), __builtin_bit_cast(int, pe[p >> 1])));
+                const float pw = live ? pv * vsc[buf][p] * (1.0f / 127.0f) : 0.0f;
+                pws[hh] += pw;
+#pragma unroll
+                for (int i = 0; i < 16; i++) acc[hh][i] = fmaf(pw, ub(ww[i >> 2], i & 3), acc[hh][i]);
+            }
+        }
+    };
+    // every memory operation in flight at the top of an iteration belongs to the tile
+    // about to be processed: wait for all of them, read its K operands out of LDS, then
+    // start the next tile's loads (into the other LDS buffer) and compute
+    const int step = NW * WT;
+    int t0 = gw * WT;
+    long kb[2][NG];
+    while (t0 < S) {
+        __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+        TI_ISSUE_FENCE();
+        kops(0, t0, kb);
+        int nt = t0 + step;
+        if (nt < S) load(1, nt);
+        process(0, t0, kb);
+        if (nt >= S) break;
+        t0 = nt;
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+        TI_ISSUE_FENCE();
+        kops(1, t0, kb);
+        nt = t0 + step;
+        if (nt < S) load(0, nt);
+        process(1, t0, kb);
+        t0 = nt;
+    }
+    __syncthreads();   // the K tile region becomes s_red: no wave of this workgroup still reads its tiles
+
+    // wave state -> LDS: P*V slots with the +128 offset removed; (m, l) of each head
+    {
+        float l16 = l_lane;
+        l16 += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, l16), __builtin_bit_cast(int, l16), 0xB1, 0xF, 0xF, false));
+        l16 += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, l16), __builtin_bit_cast(int, l16), 0x4E, 0xF, 0xF, false));
+        l16 += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, l16), __builtin_bit_cast(int, l16), 0x141, 0xF, 0xF, false));
+        l16 += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, l16), __builtin_bit_cast(int, l16), 0x140, 0xF, 0xF, false));
+#pragma unroll
+        for (int hh = 0; hh < G; hh++) {
+            const float mh = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, m_run), 16 * hh));
+            const float lh = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, l16), 16 * hh));
+            float4* dst = reinterpret_cast<float4*>(&s_red[wave][tp][hh * HD + sl * 16]);
+            const float off = 128.0f * pws[hh];
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                dst[i] = make_float4(acc[hh][4 * i] - off, acc[hh][4 * i + 1] - off, acc[hh][4 * i + 2] - off,
+                                     acc[hh][4 * i + 3] - off);
+            if (lane == 0) {
+                s_wml[wave][hh][0] = mh;
+                s_wml[wave][hh][1] = lh;
+            }
+        }
+    }
+    attn_merge_tail<HD, G, TPW>(a, hk, w, NS, ntiles, valid, s_red, s_wml, s_ml, s_e, s_L, &s_last);
 }
 }  // namespace
 
@@ -1185,7 +1569,10 @@ int ti_attn_fused_launch(ti_ctx* c, const float* q, const float* k, const float*
     dim3 grid(nKv * max_splits);
 #define AF(HD_, G_) \
     if (hd == HD_ && G == G_) { k_attn_fused_q8<HD_, G_><<<grid, 256, 0, c->stream>>>(a); TI_LAUNCHED("k_attn_fused_q8"); return TI_OK; }
-    AF(128, 2) AF(128, 1) AF(64, 2) AF(64, 1)
+    // head_dim 128 (the Qwen3 heads): Q K^T on the matrix cores
+    if (hd == 128 && G == 2) { k_attn_fused_mq8<2><<<grid, 256, 0, c->stream>>>(a); TI_LAUNCHED("k_attn_fused_mq8"); return TI_OK; }
+    if (hd == 128 && G == 1) { k_attn_fused_mq8<1><<<grid, 256, 0, c->stream>>>(a); TI_LAUNCHED("k_attn_fused_mq8"); return TI_OK; }
+    AF(64, 2) AF(64, 1)
 #undef AF
     return ti_fail(TI_ERR_INVALID, "fused attention: no kernel for hd=%d group=%d", hd, G);
 }
