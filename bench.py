@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the quantized decode hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only gemv|moe|all]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only gemv|moe|decode|all]
 
 Headline workload (`value`): the int4 GEMV set of one Qwen3-0.6B batch-1 decode
 step (hidden 1024, intermediate 3072, 16/8 heads of dim 128, 28 layers, vocab
@@ -249,7 +249,7 @@ def family_profile(ctx, step, sets, flush, reps=12):
 
 
 # ---- full Qwen3-1.7B decode ----------------------------------------------------------------
-def decode_1p7b(ctx, pool, contexts=(8192, 32768), steps=64):
+def decode_1p7b(ctx, pool, contexts=(8192, 32768), steps=64, batch8=True):
     from tabinfer_amd import abi
     cfg = QWEN3_17B
     H, I, hd = cfg["hidden"], cfg["inter"], cfg["head_dim"]
@@ -315,6 +315,8 @@ def decode_1p7b(ctx, pool, contexts=(8192, 32768), steps=64):
                              "pct_of_hbm_peak": round(100 * step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
                              "bytes_per_step": step_bytes, "launches_per_step": 2 + 5 * cfg["layers"]}
         log("decode 1.7B at %d: %.1f tok/s" % (S, 1e3 / ms))
+        if not batch8:
+            continue
         # batch 8 (a T = 8 forward of one sequence at positions S..S+7: the MFMA GEMM path)
         ctx.graph_begin()
         m.forward(None, S, T=8)
@@ -573,8 +575,11 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
-    ap.add_argument("--only", choices=("gemv", "all", "moe"), default="all",
-                    help="gemv: the headline workload only; moe: headline + the int3 MoE leg")
+    ap.add_argument("--only", choices=("gemv", "all", "moe", "decode"), default="all",
+                    help="gemv: the headline workload only; moe: headline + the int3 MoE leg; "
+                         "decode: the Qwen3-1.7B batch-1 decode leg alone, --steps tokens (no headline line)")
+    ap.add_argument("--ctx", type=int, nargs="*", default=None,
+                    help="context lengths of the decode leg (default 8192 32768)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one MI355X: this build runs on a single GPU (the multi-GPU sharding is a "
@@ -583,6 +588,14 @@ def main():
 
     from tabinfer_amd import abi
     ctx = abi.Ctx(0)
+    contexts = tuple(args.ctx) if args.ctx else (8192, 32768)
+    if args.only == "decode":   # the Qwen3-1.7B decode leg alone (profiling runs)
+        pool = Pool(ctx, 48 << 20, 1234)
+        log("decode 1.7B")
+        res = decode_1p7b(ctx, pool, contexts=contexts, steps=args.steps, batch8=False)
+        ctx.close()
+        print(json.dumps({"decode_1p7b": res}))
+        return
     cfg = QWEN3_06B
     step = Step(ctx, cfg)
     log("building weights (2 sets x %.0f MB)" % (step.bytes / 1e6))
@@ -639,7 +652,7 @@ def main():
         log("attention")
         out["attention_layer"] = attention(ctx, flush)
         log("decode 1.7B")
-        out["decode_1p7b"] = decode_1p7b(ctx, pool)
+        out["decode_1p7b"] = decode_1p7b(ctx, pool, contexts=contexts)
     if not args.no_cpu:
         log("cpu baseline")
         out["cpu_baseline"] = cpu_baseline(cfg)
