@@ -580,13 +580,17 @@ __device__ __forceinline__ void wave_argmax(float& v, int& i) {
 
 template <int LPR, int GPL, int R>
 __global__ __launch_bounds__(256) void k_lmhead(LmArgs a) {
-    __shared__ __align__(16) float s_x[LM_KMAX];
-    __shared__ float red[256];
-    __shared__ float bv_s[256];
-    __shared__ int bi_s[256];
-    __shared__ int last_s;
     constexpr int RPP = 64 / LPR;
     constexpr int GPR = LPR * GPL;
+    // LDS sized by this instantiation's K = 32*GPR (not the largest K): every workgroup of
+    // the persistent grid stays resident (a workgroup that had to wait for a slot would
+    // start its full share of rows late and set the kernel's end)
+    __shared__ __align__(16) float s_x[GPR * 32];
+    __shared__ ActLimb s_al[GPR];
+    __shared__ float red[256];
+    __shared__ float bv_s[4];
+    __shared__ int bi_s[4];
+    __shared__ int last_s;
     constexpr int SPAN = LPR / R;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -648,12 +652,16 @@ __global__ __launch_bounds__(256) void k_lmhead(LmArgs a) {
         }
     }
     __syncthreads();
+    // the exact three-limb form of each 32-group, computed once per workgroup (one thread
+    // per group) and read by every lane that dots with that group
+    for (int g = tid; g < GPR; g += 256) load_act_limbs(s_x, g, s_al[g]);
+    __syncthreads();
     float best_v = -3.0e38f;
     int best_i = 0x7fffffff;
     if (active) {
         ActLimb act[GPL];
 #pragma unroll
-        for (int j = 0; j < GPL; j++) load_act_limbs(s_x, li + LPR * j, act[j]);
+        for (int j = 0; j < GPL; j++) act[j] = s_al[li + LPR * j];
         auto finish = [&](int buf, long blk) {
             float accv[R];
 #pragma unroll
