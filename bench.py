@@ -249,7 +249,7 @@ def family_profile(ctx, step, sets, flush, reps=12):
 
 
 # ---- full Qwen3-1.7B decode ----------------------------------------------------------------
-def decode_1p7b(ctx, pool, contexts=(8192, 32768), steps=64, batch8=True):
+def decode_1p7b(ctx, pool, contexts=(8192, 32768), steps=64, batch8=True, batch1=True):
     from tabinfer_amd import abi
     cfg = QWEN3_17B
     H, I, hd = cfg["hidden"], cfg["inter"], cfg["head_dim"]
@@ -294,27 +294,29 @@ def decode_1p7b(ctx, pool, contexts=(8192, 32768), steps=64, batch8=True):
     ctx.sync()
     res = {}
     for S in contexts:
-        m.set_pos(S)
-        ctx.graph_begin()
-        m.decode()
-        g = ctx.graph_end()
-        for _ in range(3):
-            ctx.graph_launch(g)
-        m.set_pos(S)
-        ctx.sync()
-        ctx.record(22)
-        for _ in range(steps):
-            ctx.graph_launch(g)
-        ctx.record(23)
-        ctx.sync()
-        ms = ctx.elapsed_ms(22, 23) / steps
-        ctx.graph_destroy(g)
-        step_bytes = wbytes + cfg["layers"] * kv_bytes(S + steps // 2, cfg["n_kv"], hd)
-        res["ctx_%d" % S] = {"tok_s": round(1e3 / ms, 1), "ms_per_token": round(ms, 4),
-                             "step_GB_s": round(step_bytes / (ms * 1e-3) / 1e9, 1),
-                             "pct_of_hbm_peak": round(100 * step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
-                             "bytes_per_step": step_bytes, "launches_per_step": 2 + 5 * cfg["layers"]}
-        log("decode 1.7B at %d: %.1f tok/s" % (S, 1e3 / ms))
+        res["ctx_%d" % S] = {}
+        if batch1:
+            m.set_pos(S)
+            ctx.graph_begin()
+            m.decode()
+            g = ctx.graph_end()
+            for _ in range(3):
+                ctx.graph_launch(g)
+            m.set_pos(S)
+            ctx.sync()
+            ctx.record(22)
+            for _ in range(steps):
+                ctx.graph_launch(g)
+            ctx.record(23)
+            ctx.sync()
+            ms = ctx.elapsed_ms(22, 23) / steps
+            ctx.graph_destroy(g)
+            step_bytes = wbytes + cfg["layers"] * kv_bytes(S + steps // 2, cfg["n_kv"], hd)
+            res["ctx_%d" % S].update({"tok_s": round(1e3 / ms, 1), "ms_per_token": round(ms, 4),
+                                      "step_GB_s": round(step_bytes / (ms * 1e-3) / 1e9, 1),
+                                      "pct_of_hbm_peak": round(100 * step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
+                                      "bytes_per_step": step_bytes, "launches_per_step": 2 + 5 * cfg["layers"]})
+            log("decode 1.7B at %d: %.1f tok/s" % (S, 1e3 / ms))
         if not batch8:
             continue
         # batch 8 (a T = 8 forward of one sequence at positions S..S+7: the MFMA GEMM path)
@@ -575,9 +577,10 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
-    ap.add_argument("--only", choices=("gemv", "all", "moe", "decode"), default="all",
+    ap.add_argument("--only", choices=("gemv", "all", "moe", "decode", "decode8"), default="all",
                     help="gemv: the headline workload only; moe: headline + the int3 MoE leg; "
-                         "decode: the Qwen3-1.7B batch-1 decode leg alone, --steps tokens (no headline line)")
+                         "decode: the Qwen3-1.7B batch-1 decode leg alone, --steps tokens (no headline line); "
+                         "decode8: its batch-8 (T = 8 forward) leg alone")
     ap.add_argument("--ctx", type=int, nargs="*", default=None,
                     help="context lengths of the decode leg (default 8192 32768)")
     args = ap.parse_args()
@@ -589,10 +592,11 @@ def main():
     from tabinfer_amd import abi
     ctx = abi.Ctx(0)
     contexts = tuple(args.ctx) if args.ctx else (8192, 32768)
-    if args.only == "decode":   # the Qwen3-1.7B decode leg alone (profiling runs)
+    if args.only in ("decode", "decode8"):   # one Qwen3-1.7B decode leg alone (profiling runs)
         pool = Pool(ctx, 48 << 20, 1234)
         log("decode 1.7B")
-        res = decode_1p7b(ctx, pool, contexts=contexts, steps=args.steps, batch8=False)
+        res = decode_1p7b(ctx, pool, contexts=contexts, steps=args.steps, batch8=args.only == "decode8",
+                          batch1=args.only == "decode")
         ctx.close()
         print(json.dumps({"decode_1p7b": res}))
         return

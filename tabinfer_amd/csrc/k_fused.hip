@@ -148,28 +148,6 @@ __device__ __forceinline__ void act_regs_load(const FArgs& a, ActRegs<EPT, FULL>
     }
 }
 
-// group absmax over the 32/EPT lanes of a contiguous 32-group (after the in-thread max)
-template <int EPT>
-__device__ __forceinline__ float group_max_contig(float m) {
-    uint32_t u = __builtin_bit_cast(uint32_t, m);
-    if constexpr (EPT <= 16) u = max(u, (uint32_t)__builtin_amdgcn_update_dpp((int)u, (int)u, 0xB1, 0xF, 0xF, false));
-    if constexpr (EPT <= 8) u = max(u, (uint32_t)__builtin_amdgcn_update_dpp((int)u, (int)u, 0x4E, 0xF, 0xF, false));
-    if constexpr (EPT <= 4) u = max(u, (uint32_t)__builtin_amdgcn_update_dpp((int)u, (int)u, 0x141, 0xF, 0xF, false));
-    if constexpr (EPT <= 2) u = max(u, (uint32_t)__builtin_amdgcn_update_dpp((int)u, (int)u, 0x140, 0xF, 0xF, false));
-    if constexpr (EPT <= 1) {
-        const auto r = __builtin_amdgcn_permlane16_swap((int)u, (int)u, false, false);
-        u = max((uint32_t)r[0], (uint32_t)r[1]);
-    }
-    return __builtin_bit_cast(float, u);
-}
-
-// q8_group's arithmetic for one element, given its group scale
-__device__ __forceinline__ int q8_code(float v, float inv) {
-    const float p = v * inv;
-    int qi = (int)rintf(p);
-    return qi < -127 ? -127 : (qi > 127 ? 127 : qi);
-}
-
 template <int MODE, int EPT, bool FULL>
 __device__ __forceinline__ void act_regs_quant(const FArgs& a, ActRegs<EPT, FULL>& r, uint32_t* s_xq, float* s_xs,
                                                float* red) {
@@ -313,8 +291,6 @@ __device__ __forceinline__ BlkSeg blk_seg(const FArgs& a, int row0) {
     r.base = in2 ? n01 : (in1 ? n0 : 0);
     return r;
 }
-
-__device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
 
 template <int LPR, int GPL, int R, int MODE, bool GU>
 __global__ __launch_bounds__(256) void k_fgemv(FArgs a) {

@@ -22,15 +22,6 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-// 8 nibbles of a packed word -> two words of signed bytes (nibble - 8): even
-// nibbles (k = 0,2,4,6) and odd nibbles (k = 1,3,5,7)
-__device__ __forceinline__ void nib_to_s8(uint32_t w, uint32_t& lo, uint32_t& hi) {
-    const uint32_t e = (w & 0x0F0F0F0Fu) ^ 0x08080808u;           // nibble ^ 8: sign bit at bit 3
-    const uint32_t o = ((w >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u;
-    lo = e | (((e & 0x08080808u) >> 3) * 0xF0u);                   // sign-extend 4 -> 8 bits per byte
-    hi = o | (((o & 0x08080808u) >> 3) * 0xF0u);
-}
-
 constexpr int GMAX = 512;       // K <= 16384
 
 // WAVES waves per 16-row tile, each on every WAVES-th group; UNROLL groups per wave have

@@ -313,4 +313,39 @@ __device__ __forceinline__ float rms_inv_256(const float* __restrict__ x, int H,
     return 1.0f / sqrtf(m);
 }
 
+// ---- shared by the fused T-token and batch-1 projections ----------------------------
+// 8 nibbles of a packed word -> two words of signed bytes (nibble - 8): even
+// nibbles (k = 0,2,4,6) and odd nibbles (k = 1,3,5,7)
+__device__ __forceinline__ void nib_to_s8(uint32_t w, uint32_t& lo, uint32_t& hi) {
+    const uint32_t e = (w & 0x0F0F0F0Fu) ^ 0x08080808u;           // nibble ^ 8: sign bit at bit 3
+    const uint32_t o = ((w >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u;
+    lo = e | (((e & 0x08080808u) >> 3) * 0xF0u);                   // sign-extend 4 -> 8 bits per byte
+    hi = o | (((o & 0x08080808u) >> 3) * 0xF0u);
+}
+
+// group absmax over the 32/EPT lanes of a contiguous 32-group (after the in-thread max)
+template <int EPT>
+__device__ __forceinline__ float group_max_contig(float m) {
+    uint32_t u = __builtin_bit_cast(uint32_t, m);
+    if constexpr (EPT <= 16) u = max(u, (uint32_t)__builtin_amdgcn_update_dpp((int)u, (int)u, 0xB1, 0xF, 0xF, false));
+    if constexpr (EPT <= 8) u = max(u, (uint32_t)__builtin_amdgcn_update_dpp((int)u, (int)u, 0x4E, 0xF, 0xF, false));
+    if constexpr (EPT <= 4) u = max(u, (uint32_t)__builtin_amdgcn_update_dpp((int)u, (int)u, 0x141, 0xF, 0xF, false));
+    if constexpr (EPT <= 2) u = max(u, (uint32_t)__builtin_amdgcn_update_dpp((int)u, (int)u, 0x140, 0xF, 0xF, false));
+    if constexpr (EPT <= 1) {
+        const auto r = __builtin_amdgcn_permlane16_swap((int)u, (int)u, false, false);
+        u = max((uint32_t)r[0], (uint32_t)r[1]);
+    }
+    return __builtin_bit_cast(float, u);
+}
+
+// q8_group's arithmetic for one element, given its group scale
+__device__ __forceinline__ int q8_code(float v, float inv) {
+    const float p = v * inv;
+    int qi = (int)rintf(p);
+    return qi < -127 ? -127 : (qi > 127 ? 127 : qi);
+}
+
+// SwiGLU of one row: silu(g) * u, silu(g) = g / (1 + e^-g)
+__device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
+
 }  // namespace

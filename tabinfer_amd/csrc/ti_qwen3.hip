@@ -34,6 +34,13 @@ int ti_fused_gateup_launch(ti_ctx*, const float*, const uint16_t*, float, const 
 int ti_fused_lmhead_launch(ti_ctx*, const float*, const uint16_t*, float, const uint32_t*, const uint16_t*, float*, int,
                            int, uint32_t*, int*, int, int, const float*, float*, int);
 int ti_fused_kmax(int lm);
+bool ti_tgemm_ok(int T, int K, int norm, int gateup);
+int ti_tgemm_launch(ti_ctx* c, int norm, const float* x, const uint16_t* nw, float eps, const uint32_t* xq,
+                    const float* xs, int nseg, const uint32_t* const* packs, const uint16_t* const* scs,
+                    float* const* ys, const int* Ns, int T, int K, int acc);
+int ti_tgemm_gateup_launch(ti_ctx* c, const float* x, const uint16_t* nw, float eps, const uint32_t* gpack,
+                           const uint16_t* gsc, const uint32_t* upack, const uint16_t* usc, int I, int H, int T,
+                           uint32_t* swq, float* sws);
 
 // ---------------------------------------------------------------------------
 // glue kernels
@@ -235,8 +242,8 @@ extern "C" int ti_qwen3_create(ti_ctx* c, const ti_qwen3_config* cfg, ti_qwen3**
                                             {&m->logits, (size_t)C.vocab}, {&m->amx_v, (size_t)AMX_PARTS}};
     for (auto& f : fb) if (!rc) rc = mk(m, (void**)f.p, f.n * 4);
     const size_t kmax = (size_t)(H > I ? (H > nq ? H : nq) : (I > nq ? I : nq));   // widest GEMV input
-    if (!rc) rc = mk(m, (void**)&m->xq, kmax);
-    if (!rc) rc = mk(m, (void**)&m->xs, kmax / 32 * 4);
+    if (!rc) rc = mk(m, (void**)&m->xq, (size_t)T * kmax);                          // [T][kmax] int8 codes
+    if (!rc) rc = mk(m, (void**)&m->xs, (size_t)T * kmax / 32 * 4);
     if (!rc) rc = mk(m, (void**)&m->xsum, kmax / 16 * 4);
     if (!rc) rc = mk(m, (void**)&m->hist, (size_t)(C.max_ctx + 1) * 4);
     if (!rc) rc = mk(m, (void**)&m->dpos, 4);
@@ -427,16 +434,37 @@ extern "C" int ti_qwen3_forward(ti_ctx* c, ti_qwen3* m, const int32_t* ids, int 
     if (ids) RC(ti_buf_write(c, m->hist, (size_t)pos * 4, ids, (size_t)T * 4));   // else already in the history
     k_embed<<<(unsigned)(((long)T * H + 255) / 256), 256, 0, c->stream>>>(m->hist, m->embed, m->x, T, H, pos, nullptr, C.vocab);
     TI_LAUNCHED("k_embed");
+    // 2..16 tokens: five launches per layer around the attention, the projections on
+    // the matrix cores with their norm / quantizer / SwiGLU fused (k_tgemm.hip)
+    const bool fused = ti_tgemm_ok(T, H, 1, 1) && ti_tgemm_ok(T, nq, 0, 0) && ti_tgemm_ok(T, I, 0, 0) &&
+                       nq % 16 == 0 && nkv % 16 == 0 && I % 32 == 0;
     for (int l = 0; l < C.layers; l++) {
         Layer& y = m->L[l];
-        RC(ti_rmsnorm(c, m->x, y.in_norm, m->normed, T, H, C.rms_eps));
-        RC(ti_linear_q4(c, m->normed, y.q.pack, y.q.sc, m->q, T, nq, H, 0));
-        RC(ti_linear_q4(c, m->normed, y.k.pack, y.k.sc, m->k, T, nkv, H, 0));
-        RC(ti_linear_q4(c, m->normed, y.v.pack, y.v.sc, m->v, T, nkv, H, 0));
+        if (fused) {
+            const uint32_t* packs[3] = {y.q.pack, y.k.pack, y.v.pack};
+            const uint16_t* scs[3] = {y.q.sc, y.k.sc, y.v.sc};
+            float* ys[3] = {m->q, m->k, m->v};
+            const int Ns[3] = {nq, nkv, nkv};
+            RC(ti_tgemm_launch(c, 1, m->x, y.in_norm, C.rms_eps, nullptr, nullptr, 3, packs, scs, ys, Ns, T, H, 0));
+        } else {
+            RC(ti_rmsnorm(c, m->x, y.in_norm, m->normed, T, H, C.rms_eps));
+            RC(ti_linear_q4(c, m->normed, y.q.pack, y.q.sc, m->q, T, nq, H, 0));
+            RC(ti_linear_q4(c, m->normed, y.k.pack, y.k.sc, m->k, T, nkv, H, 0));
+            RC(ti_linear_q4(c, m->normed, y.v.pack, y.v.sc, m->v, T, nkv, H, 0));
+        }
         RC(ti_rope_qk(c, m->q, y.q_norm, m->qr, T, nHq, hd, pos, C.rope_theta, C.rms_eps));
         RC(ti_rope_qk(c, m->k, y.k_norm, m->kr, T, nKv, hd, pos, C.rope_theta, C.rms_eps));
         RC(ti_kv_write_q8(c, m->kr, m->v, y.kq, y.ks, y.vq, y.vs, T, nKv, hd, pos));
         RC(ti_attn_decode_launch(c, m->qr, y.kq, y.ks, y.vq, y.vs, m->attn, pos + 1, T, nHq, nKv, hd, 0, nullptr, 0));
+        if (fused) {
+            RC(ti_quant_act_q8_async(c, m->attn, m->xq, m->xs, nullptr, T * (nq / 32)));
+            RC(ti_tgemm_launch(c, 0, nullptr, nullptr, 0.0f, m->xq, m->xs, 1, &y.o.pack, &y.o.sc, &m->x, &H, T, nq, 1));
+            RC(ti_tgemm_gateup_launch(c, m->x, y.post_norm, C.rms_eps, y.gate.pack, y.gate.sc, y.up.pack, y.up.sc, I, H,
+                                      T, m->xq, m->xs));
+            RC(ti_tgemm_launch(c, 0, nullptr, nullptr, 0.0f, m->xq, m->xs, 1, &y.down.pack, &y.down.sc, &m->x, &H, T, I,
+                               1));
+            continue;
+        }
         RC(ti_linear_q4(c, m->attn, y.o.pack, y.o.sc, m->x, T, H, nq, 1));
         RC(ti_rmsnorm(c, m->x, y.post_norm, m->normed, T, H, C.rms_eps));
         RC(ti_linear_q4(c, m->normed, y.gate.pack, y.gate.sc, m->gate, T, I, H, 0));

@@ -123,30 +123,39 @@ def test_graph_replay_decodes_like_eager(ctx):
         m.close()
 
 
+def _seed_prefix(ctx, orc, m, ref, cfg, P, seed):
+    """A seeded random prefix KV of P tokens in every layer, written through the KV
+    quantizer into both the model and the reference decoder."""
+    rng = np.random.default_rng(seed)
+    nkv = cfg["n_kv_heads"] * cfg["head_dim"]
+    for l in range(cfg["layers"]):
+        K = rng.standard_normal(P * nkv).astype(np.float16).astype(np.float32)
+        V = rng.standard_normal(P * nkv).astype(np.float16).astype(np.float32)
+        kq, ks = orc.kv_quant(K)
+        vq, vs = orc.kv_quant(V)
+        dk = m.kv(l)
+        for dst, src in zip(dk, (kq, ks, vq, vs)):
+            ctx.write(dst, src)
+        ref.kv[l][0][:P], ref.kv[l][1][:P] = kq.reshape(P, -1), ks.reshape(P, -1)
+        ref.kv[l][2][:P], ref.kv[l][3][:P] = vq.reshape(P, -1), vs.reshape(P, -1)
+
+
+CFG_17B = dict(layers=2, hidden=2048, intermediate=6144, n_heads=16, n_kv_heads=8, head_dim=128, vocab=151936,
+               rope_theta=1e6, rms_eps=1e-6, max_ctx=4200, max_tokens=1)
+
+
 def test_qwen3_17b_geometry_over_4k_prefix(ctx, orc):
     """Qwen3-1.7B layer geometry (hidden 2048, intermediate 6144, 16/8 heads of 128,
     vocab 151936), 2 layers, one decode step at position 4096 over a seeded prefix KV
     written through the attention-prep quantizer."""
-    cfg = dict(layers=2, hidden=2048, intermediate=6144, n_heads=16, n_kv_heads=8, head_dim=128, vocab=151936,
-               rope_theta=1e6, rms_eps=1e-6, max_ctx=4200, max_tokens=1)
+    cfg = CFG_17B
     W = Q.make_weights(cfg, 4)
     m = abi.Qwen3(ctx, **cfg)
     try:
         Q.load_into(m, W)
         ref = Q.RefDecoder(cfg, W, cfg["max_ctx"])
-        rng = np.random.default_rng(9)
         P = 4096
-        nkv = 8 * 128
-        for l in range(cfg["layers"]):
-            K = rng.standard_normal(P * nkv).astype(np.float16).astype(np.float32)
-            V = rng.standard_normal(P * nkv).astype(np.float16).astype(np.float32)
-            kq, ks = orc.kv_quant(K)
-            vq, vs = orc.kv_quant(V)
-            dk = m.kv(l)
-            for dst, src in zip(dk, (kq, ks, vq, vs)):
-                ctx.write(dst, src)
-            ref.kv[l][0][:P], ref.kv[l][1][:P] = kq.reshape(P, -1), ks.reshape(P, -1)
-            ref.kv[l][2][:P], ref.kv[l][3][:P] = vq.reshape(P, -1), vs.reshape(P, -1)
+        _seed_prefix(ctx, orc, m, ref, cfg, P, 9)
         tok = 4242
         m.write_tokens(P, np.array([tok], np.int32))
         m.set_pos(P)
@@ -158,3 +167,62 @@ def test_qwen3_17b_geometry_over_4k_prefix(ctx, orc):
             assert int(m.read_tokens(P + 1, 1)[0]) == rt
     finally:
         m.close()
+
+
+def test_qwen3_17b_geometry_batch8_over_4k_prefix(ctx, orc):
+    """The batch-8 configuration at the Qwen3-1.7B geometry: one T=8 forward at
+    positions 4096..4103 over a seeded 4k prefix (the fused matrix-core projections:
+    RMSNorm + quantQ8T prologues, three-matrix q/k/v, gate/up with the SwiGLU +
+    quantQ8 epilogue, residual o/down) against 8 reference steps: last-token logits
+    within 1e-3, the 8 new KV rows within one int8 step."""
+    cfg = dict(CFG_17B, max_tokens=8)
+    W = Q.make_weights(cfg, 5)
+    m = abi.Qwen3(ctx, **cfg)
+    try:
+        Q.load_into(m, W)
+        ref = Q.RefDecoder(cfg, W, cfg["max_ctx"])
+        P = 4096
+        _seed_prefix(ctx, orc, m, ref, cfg, P, 10)
+        ids = np.array([4242, 17, 151935, 0, 99, 1000, 77777, 5], np.int32)
+        m.forward(ids, P)
+        for i, t in enumerate(ids):
+            rl, rt = ref.step(int(t), P + i)
+        assert rel_err(_logits(ctx, m, cfg["vocab"]), rl) < TOL
+        if margin_ok(rl):
+            assert int(m.read_tokens(P + 8, 1)[0]) == rt
+        nkv = cfg["n_kv_heads"] * cfg["head_dim"]
+        for l in range(cfg["layers"]):
+            kq, _, vq, _ = m.kv(l)
+            for dev, r in ((kq, ref.kv[l][0]), (vq, ref.kv[l][2])):
+                g = ctx.download(dev, np.uint32, (P + 8) * nkv // 4).view(np.int8).astype(int).reshape(P + 8, -1)[P:]
+                rr = r[P:P + 8].view(np.int8).astype(int).reshape(8, -1)
+                # layer 0 sees bit-exact activation codes (only the f32 sums differ); layer 1
+                # inherits layer 0's float rounding, which moves codes at rounding boundaries
+                assert np.max(np.abs(g - rr)) <= 1
+                assert np.mean(g != rr) < (0.002 if l == 0 else 0.05), (l, np.mean(g != rr))
+    finally:
+        m.close()
+
+
+@pytest.mark.parametrize("T", [2, 16])
+def test_batched_forward_t_sizes(ctx, T):
+    """T-token forwards at the ends of the fused range (2 and 16 tokens) give the same
+    last logits as T single-token forwards."""
+    cfg = dict(SMALL, max_tokens=16)
+    W = Q.make_weights(cfg, 6)
+    a, b = abi.Qwen3(ctx, **cfg), abi.Qwen3(ctx, **cfg)
+    try:
+        Q.load_into(a, W)
+        Q.load_into(b, W)
+        ids = (np.arange(T, dtype=np.int32) * 131 + 7) % cfg["vocab"]
+        pre = np.array([1, 2, 3], np.int32)
+        a.forward(pre, 0)
+        a.forward(ids, 3)
+        b.forward(pre, 0)
+        for p in range(T):
+            b.forward(ids[p:p + 1], 3 + p)
+        la, lb = _logits(ctx, a, cfg["vocab"]), _logits(ctx, b, cfg["vocab"])
+        assert rel_err(la, lb) < TOL
+    finally:
+        a.close()
+        b.close()
