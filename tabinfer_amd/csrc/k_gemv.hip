@@ -476,7 +476,7 @@ extern "C" int ti_linear_q4(ti_ctx* c, const float* x, const uint32_t* pack, con
     int rc = ti_quant_act_q8_async(c, x, c->act_q, c->act_s, nullptr, T * (K / 32));
     if (rc) return rc;
     if (T == 1) return ti_gemv_q4_q8_launch(c, c->act_q, c->act_s, pack, scales, y, N, K, acc);
-    if (ti_tgemm_ok(T, K, 0, 0) && reinterpret_cast<uintptr_t>(scales) % 8 == 0)
+    if (ti_tgemm_ok(T, K, 0, 0) && reinterpret_cast<uintptr_t>(scales) % 16 == 0)
         return ti_tgemm_launch(c, 0, nullptr, nullptr, 0.0f, c->act_q, c->act_s, 1, &pack, &scales, &y, &N, T, K, acc);
     return ti_gemm_q4_q8_launch(c, c->act_q, c->act_s, pack, scales, y, T, N, K, acc);
 }

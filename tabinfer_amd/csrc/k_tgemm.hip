@@ -20,25 +20,29 @@
 // activations (row = token), B = weights (column = weight row). Each int32 group dot is
 // scaled by s_w[n,g] * s_x[t,g] into an f32 accumulator, as the reference does per group.
 //
-// Weights are streamed like the batch-1 GEMVs: 16-byte loads, every load of a wave in
-// flight before its first use. Lane (m, j) (m = l%16, j = l/16) loads the whole 16-byte
-// group g0+j of row m (the four lanes of a row read 64 contiguous bytes); the MFMA wants
-// word j of ONE group in the four lanes of a row, so a 4x4 transpose across the lane
-// rows (two permlane32 swaps, two permlane16 swaps: no LDS) turns the four loaded groups
-// into the B operands of four MFMAs. The 8 scales of a row's 4 groups come as one 8-byte
-// load. A wave owns a 16-row block and a 1/KS share of K; the KS partials of a block
-// meet in LDS. Tokens past T are computed as padding and never stored.
+// The VALU work per group is what bounds these kernels (a wave64 VALU op takes 4
+// cycles; the MFMA is cheap), so everything that can be done once per workgroup is
+// taken out of the group loop:
+//   - the weight nibbles go into B unsigned (nibble = w + 8, two ANDs and a shift), and
+//     the MFMA's accumulator input carries -8 * sum(a) of the group, so the int32 result
+//     is the signed dot exactly;
+//   - the activation codes are stored in LDS already in B's byte order (per 8-byte K
+//     slice: even elements, then odd elements), with the -8*sum(a) terms and the scales
+//     token-minor ([g][16]: one 16-byte read gives a lane its 4 tokens).
 //
-// Activation codes: TG_NORM keeps them in LDS ([T][K/4 + 2] words: the 2-word pad puts
-// the 16 token rows of an A-operand read on distinct banks), TG_Q8 loads the A operands
-// straight from the producer's [T][K/4] buffer with the weights. Activation scales are
-// staged token-minor in LDS ([g][16]): one 16-byte read gives a lane its 4 tokens.
+// Weights are streamed like the batch-1 GEMVs: 16-byte loads, all of a wave's loads in
+// flight before the first use, issued after the activation loads so that the prologue
+// waits for its own data only. Lane (m, j) (m = l%16, j = l/16) loads the whole 16-byte
+// group g0+j of row m (a row's four lanes read 64 contiguous bytes); the MFMA wants word
+// j of ONE group in a row's four lanes, so a 4x4 transpose across the lane rows (two
+// permlane32 swaps, two permlane16 swaps: no LDS) turns four loaded groups into the B
+// operands of four MFMAs. A wave owns a 16-row block and a 1/KS share of K; the KS
+// partials of a block meet in LDS. Tokens past T are computed as padding, never stored.
 #include "ti_dev.h"
 
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
-typedef uint32_t v2u __attribute__((ext_vector_type(2)));
 
 enum { TG_Q8 = 0, TG_NORM = 1 };
 
@@ -46,7 +50,7 @@ constexpr int TG_TMAX = 16;
 
 struct TgSeg {
     const uint4* pack;
-    const v2u* sc;       // f16 scales, 4 per 8-byte word
+    const uint4* sc;     // f16 scales, 8 per 16-byte word
     float* y;            // [T][n]
     int n;
 };
@@ -58,22 +62,42 @@ struct TgArgs {
     int K;
     int T;
     int acc;             // y += W x (residual)
-    int S;               // LDS row stride of the activation codes, words
+    int S;               // LDS row stride of the activation codes, words (K/4 + 2)
     const float* x;      // TG_NORM: [T][K] f32
     const uint16_t* nw;  // TG_NORM: f16 norm weight [K]
     float eps;
     const uint32_t* xq;  // TG_Q8: [T][K/4] codes
     const float* xs;     // TG_Q8: [T][K/32] scales
     const uint4* upack;  // gate/up: the up matrix (seg[0] is gate)
-    const v2u* usc;
+    const uint4* usc;
     uint32_t* yq;        // gate/up: swi codes [T][N/4]
     float* ys;           // gate/up: swi scales [T][N/32]
 };
 
-// LDS carve-up (dynamic): codes [T][S] (TG_NORM), scales [G][16], partials [4][16][17],
-// norm partial sums [TP][256] (TG_NORM)
-__host__ __device__ constexpr int tg_part_floats() { return 4 * 16 * 17; }
-__host__ __device__ constexpr int tg_codes_words(int T, int S) { return (T * S + 3) & ~3; }   // keeps s_as 16-byte aligned
+// LDS (dynamic), in words: codes [T][S] (rounded to 4), scales [G][16] f32, -8*sum(a)
+// [G][16] i32, partials [W][16][17] f32, norm partial sums [TP][256] f32 (TG_NORM)
+__host__ __device__ constexpr int tg_codes_words(int T, int S) { return (T * S + 3) & ~3; }
+__host__ __device__ constexpr int tg_lds_words(int T, int K, int W, int TP) {
+    return tg_codes_words(T, K / 4 + 2) + 2 * (K / 32) * 16 + W * 16 * 17 + TP * 256;
+}
+
+struct TgLds {
+    uint32_t* aq;
+    float* as;
+    int* corr;
+    float* part;
+    float* red;
+};
+__device__ __forceinline__ TgLds tg_carve(uint32_t* base, int T, int K, int W) {
+    const int G = K / 32;
+    TgLds L;
+    L.aq = base;
+    L.as = reinterpret_cast<float*>(base + tg_codes_words(T, K / 4 + 2));
+    L.corr = reinterpret_cast<int*>(L.as + G * 16);
+    L.part = reinterpret_cast<float*>(L.corr + G * 16);
+    L.red = L.part + W * 16 * 17;
+    return L;
+}
 
 // 4x4 transpose of words across the four 16-lane rows: in, lane row j holds words 0..3
 // of group j; out, b[u] in lane row j is word j of group u. permlane32_swap(a, b) gives
@@ -90,6 +114,10 @@ __device__ __forceinline__ void tr4_rows(const uint4 w, uint32_t (&b)[4]) {
     b[3] = r1[1];
 }
 
+__device__ __forceinline__ int byte_sum(uint32_t w, int acc) {
+    return __builtin_amdgcn_sdot4((int)w, 0x01010101, acc, false);
+}
+
 // sum of a token's 256 per-thread partials in the reference's tree order (red holds them)
 __device__ __forceinline__ float tg_tree(const float* red) {
     const int l = threadIdx.x & 63;
@@ -101,100 +129,193 @@ __device__ __forceinline__ float tg_tree(const float* red) {
     return v;
 }
 
-// Per-token RMSNorm + quantQ8T of the T x K activation into LDS, K = 256*KU, TP tokens
-// per pass. Thread t holds elements t, t+256, ... of each token for the sum of squares
-// (the reference's 256 strided partials, then its 128..1 tree), and a contiguous copy,
+// ---- TG_NORM prologue ---------------------------------------------------------------
+// Per-token RMSNorm + quantQ8T of the T x K activation, K = 256*KU, TP tokens per pass.
+// Thread t holds elements t, t+256, ... of each token for the sum of squares (the
+// reference's 256 strided partials, then its 128..1 tree), and a contiguous copy,
 // elements KU*t .. KU*t+KU-1, for the quantizer: a 32-group spans 32/KU neighbouring
 // lanes, each thread computes its group's scale once. Codes and scales equal
 // rmsnorm + q8_group's, bit for bit.
 template <int KU, int TP>
-__device__ __forceinline__ void tg_norm_prologue(const TgArgs& a, uint32_t* s_aq, float* s_as, float* red) {
-    constexpr int K = 256 * KU;
-    const int t = threadIdx.x, T = a.T, S = a.S;
+struct NormRegs {
+    float xsd[TP][KU];
+    float xc[TP][KU];
     uint16_t wc[KU];
+};
+
+template <int KU, int TP>
+__device__ __forceinline__ void tg_norm_load(const TgArgs& a, int p0, NormRegs<KU, TP>& r) {
+    constexpr int K = 256 * KU;
+    const int t = threadIdx.x, T = a.T;
 #pragma unroll
-    for (int i = 0; i < KU; i++) wc[i] = a.nw[KU * t + i];
-    for (int p0 = 0; p0 < T; p0 += TP) {
-        float xsd[TP][KU], xc[TP][KU];
+    for (int tp = 0; tp < TP; tp++) {
+        const int tok = min(p0 + tp, T - 1);
+        const float* xr = a.x + (size_t)tok * K;
 #pragma unroll
-        for (int tp = 0; tp < TP; tp++) {
-            const int tok = min(p0 + tp, T - 1);
-            const float* xr = a.x + (size_t)tok * K;
+        for (int i = 0; i < KU; i++) r.xsd[tp][i] = xr[t + 256 * i];
+        if constexpr (KU % 4 == 0) {
+            const float4* x4 = reinterpret_cast<const float4*>(xr + KU * t);
 #pragma unroll
-            for (int i = 0; i < KU; i++) xsd[tp][i] = xr[t + 256 * i];
-            if constexpr (KU % 4 == 0) {
-                const float4* x4 = reinterpret_cast<const float4*>(xr + KU * t);
-#pragma unroll
-                for (int i = 0; i < KU / 4; i++) {
-                    const float4 v = x4[i];
-                    xc[tp][4 * i] = v.x; xc[tp][4 * i + 1] = v.y; xc[tp][4 * i + 2] = v.z; xc[tp][4 * i + 3] = v.w;
-                }
-            } else {
-#pragma unroll
-                for (int i = 0; i < KU; i++) xc[tp][i] = xr[KU * t + i];
+            for (int i = 0; i < KU / 4; i++) {
+                const float4 v = x4[i];
+                r.xc[tp][4 * i] = v.x; r.xc[tp][4 * i + 1] = v.y; r.xc[tp][4 * i + 2] = v.z; r.xc[tp][4 * i + 3] = v.w;
             }
+        } else {
+#pragma unroll
+            for (int i = 0; i < KU; i++) r.xc[tp][i] = xr[KU * t + i];
         }
-#pragma unroll
-        for (int tp = 0; tp < TP; tp++) {
-            float s = 0.0f;
-#pragma unroll
-            for (int i = 0; i < KU; i++) {
-                const float sq = xsd[tp][i] * xsd[tp][i];
-                s = s + sq;
-            }
-            red[tp * 256 + t] = s;
-        }
-        __syncthreads();
-#pragma unroll
-        for (int tp = 0; tp < TP; tp++) {
-            const int tok = p0 + tp;
-            float m = tg_tree(red + tp * 256) / (float)K;
-            m = m + a.eps;
-            const float inv_rms = 1.0f / sqrtf(m);
-            float v[KU];
-            float mx = 0.0f;
-#pragma unroll
-            for (int i = 0; i < KU; i++) {
-                const float p = xc[tp][i] * inv_rms;
-                v[i] = p * ti_h2f(wc[i]);
-                mx = fmaxf(mx, fabsf(v[i]));
-            }
-            mx = group_max_contig<KU>(mx);
-            const float scale = mx / 127.0f;
-            const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
-            uint32_t wd[(KU + 3) / 4] = {};
-#pragma unroll
-            for (int i = 0; i < KU; i++) wd[i / 4] |= (uint32_t)(q8_code(v[i], inv) & 0xff) << (8 * (i % 4));
-            if (tok < T) {
-                if constexpr (KU >= 4) {
-#pragma unroll
-                    for (int k = 0; k < KU / 4; k++) s_aq[tok * S + KU / 4 * t + k] = wd[k];
-                } else {
-                    uint8_t* qb = reinterpret_cast<uint8_t*>(s_aq + tok * S);
-#pragma unroll
-                    for (int i = 0; i < KU; i++) qb[KU * t + i] = (uint8_t)((wd[0] >> (8 * i)) & 0xff);
-                }
-                if (t % (32 / KU) == 0) s_as[(KU * t / 32) * 16 + tok] = scale;
-            }
-        }
-        __syncthreads();   // codes visible; red free for the next pass
     }
 }
 
-// activation scales [T][G] -> LDS [G][16] (TG_Q8): every load issued before the stores
-__device__ __forceinline__ void tg_stage_scales(const TgArgs& a, float* s_as) {
-    const int G = a.K / 32, n = a.T * G, t = threadIdx.x;
-    constexpr int SPT = TG_TMAX * 256 / 256;   // T * G <= 16 * 256
-    float v[SPT];
+// one pass: codes of tokens p0 .. p0+TP-1 into LDS. KU >= 8: a thread's elements are
+// whole K slices, written in B's byte order with the group's -8*sum(a) (the slices of
+// a group are neighbouring lanes); KU < 8: natural order, tg_norm_finish reorders.
+template <int KU, int TP>
+__device__ __forceinline__ void tg_norm_pass(const TgArgs& a, int p0, const NormRegs<KU, TP>& r, const TgLds& L) {
+    constexpr int K = 256 * KU;
+    const int t = threadIdx.x, T = a.T, S = a.S;
 #pragma unroll
-    for (int k = 0; k < SPT; k++) {
-        const int e = t + 256 * k;
-        v[k] = a.xs[e < n ? e : n - 1];
+    for (int tp = 0; tp < TP; tp++) {
+        float s = 0.0f;
+#pragma unroll
+        for (int i = 0; i < KU; i++) {
+            const float sq = r.xsd[tp][i] * r.xsd[tp][i];
+            s = s + sq;
+        }
+        L.red[tp * 256 + t] = s;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int tp = 0; tp < TP; tp++) {
+        const int tok = p0 + tp;
+        float m = tg_tree(L.red + tp * 256) / (float)K;
+        m = m + a.eps;
+        const float inv_rms = 1.0f / sqrtf(m);
+        float v[KU];
+        float mx = 0.0f;
+#pragma unroll
+        for (int i = 0; i < KU; i++) {
+            const float p = r.xc[tp][i] * inv_rms;
+            v[i] = p * ti_h2f(r.wc[i]);
+            mx = fmaxf(mx, fabsf(v[i]));
+        }
+        mx = group_max_contig<KU>(mx);
+        const float scale = mx / 127.0f;
+        const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
+        int q[KU];
+#pragma unroll
+        for (int i = 0; i < KU; i++) q[i] = q8_code(v[i], inv);
+        if constexpr (KU >= 8) {
+            // slices 8c..8c+7 (c = KU/8*t + k): even elements then odd elements
+            int sum = 0;
+            uint32_t wd[KU / 4];
+#pragma unroll
+            for (int k = 0; k < KU / 8; k++) {
+                uint32_t e = 0, o = 0;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    e |= (uint32_t)(q[8 * k + 2 * i] & 0xff) << (8 * i);
+                    o |= (uint32_t)(q[8 * k + 2 * i + 1] & 0xff) << (8 * i);
+                }
+                wd[2 * k] = e;
+                wd[2 * k + 1] = o;
+                sum = byte_sum(o, byte_sum(e, sum));
+            }
+            sum += ti_xor(sum, 1);
+            if constexpr (KU == 8) sum += ti_xor(sum, 2);   // a group is 32/KU lanes
+            if (tok < T) {
+#pragma unroll
+                for (int k = 0; k < KU / 4; k++) L.aq[tok * S + KU / 4 * t + k] = wd[k];
+                if (t % (32 / KU) == 0) {
+                    const int g = KU * t / 32;
+                    L.as[g * 16 + tok] = scale;
+                    L.corr[g * 16 + tok] = -8 * sum;
+                }
+            }
+        } else {
+            uint32_t wd = 0;
+#pragma unroll
+            for (int i = 0; i < KU; i++) wd |= (uint32_t)(q[i] & 0xff) << (8 * i);
+            if (tok < T) {
+                if constexpr (KU == 4) {
+                    L.aq[tok * S + t] = wd;
+                } else {
+                    uint8_t* qb = reinterpret_cast<uint8_t*>(L.aq + tok * S);
+#pragma unroll
+                    for (int i = 0; i < KU; i++) qb[KU * t + i] = (uint8_t)((wd >> (8 * i)) & 0xff);
+                }
+                if (t % (32 / KU) == 0) L.as[(KU * t / 32) * 16 + tok] = scale;
+            }
+        }
+    }
+    __syncthreads();   // codes visible; red free for the next pass
+}
+
+// KU < 8: natural-order codes -> B's byte order and the -8*sum(a) terms, a group per thread
+__device__ __forceinline__ void tg_norm_finish(const TgArgs& a, const TgLds& L, int nthreads) {
+    const int G = a.K / 32, S = a.S;
+    for (int idx = threadIdx.x; idx < a.T * G; idx += nthreads) {
+        const int t = idx / G, g = idx % G;
+        uint2* p = reinterpret_cast<uint2*>(L.aq + t * S + 8 * g);
+        int sum = 0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint2 w = p[k];
+            sum = byte_sum(w.y, byte_sum(w.x, sum));
+            p[k] = make_uint2(even_bytes(w.x, w.y), odd_bytes(w.x, w.y));
+        }
+        L.corr[g * 16 + t] = -8 * sum;
+    }
+    __syncthreads();
+}
+
+// ---- TG_Q8 prologue -----------------------------------------------------------------
+// The producer's [T][K/4] codes and [T][K/32] scales, staged into LDS in B's byte
+// order: 16-byte units (two K slices, half a group) per thread, the two halves of a
+// group in neighbouring lanes (they add their sums by DPP). UQ, SQ: loads per thread.
+template <int UQ, int SQ>
+struct Q8Regs {
+    uint4 c[UQ];
+    float s[SQ];
+};
+
+template <int UQ, int SQ>
+__device__ __forceinline__ void tg_q8_load(const TgArgs& a, Q8Regs<UQ, SQ>& r, int nthreads) {
+    const int units = a.T * (a.K / 16), ns = a.T * (a.K / 32);
+    const uint4* src = reinterpret_cast<const uint4*>(a.xq);
+#pragma unroll
+    for (int k = 0; k < UQ; k++) {
+        const int u = threadIdx.x + nthreads * k;
+        r.c[k] = src[u < units ? u : units - 1];
     }
 #pragma unroll
-    for (int k = 0; k < SPT; k++) {
-        const int e = t + 256 * k;
-        if (e < n) s_as[(e % G) * 16 + e / G] = v[k];
+    for (int k = 0; k < SQ; k++) {
+        const int e = threadIdx.x + nthreads * k;
+        r.s[k] = a.xs[e < ns ? e : ns - 1];
+    }
+}
+
+template <int UQ, int SQ>
+__device__ __forceinline__ void tg_q8_stage(const TgArgs& a, const Q8Regs<UQ, SQ>& r, const TgLds& L, int nthreads) {
+    const int G = a.K / 32, upr = a.K / 16, units = a.T * upr, ns = a.T * G, S = a.S;
+#pragma unroll
+    for (int k = 0; k < UQ; k++) {
+        const int u = threadIdx.x + nthreads * k;
+        const int t = u / upr, c = u % upr, g = c >> 1, h = c & 1;
+        const uint4 w = r.c[k];
+        int sum = byte_sum(w.w, byte_sum(w.z, byte_sum(w.y, byte_sum(w.x, 0))));
+        sum += ti_xor(sum, 1);                       // the other half of the group (u ^ 1)
+        if (u < units) {
+            uint2* p = reinterpret_cast<uint2*>(L.aq + t * S + 8 * g + 4 * h);
+            p[0] = make_uint2(even_bytes(w.x, w.y), odd_bytes(w.x, w.y));
+            p[1] = make_uint2(even_bytes(w.z, w.w), odd_bytes(w.z, w.w));
+            if (h == 0) L.corr[g * 16 + t] = -8 * sum;
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < SQ; k++) {
+        const int e = threadIdx.x + nthreads * k;
+        if (e < ns) L.as[(e % G) * 16 + e / G] = r.s[k];
     }
     __syncthreads();
 }
@@ -202,7 +323,7 @@ __device__ __forceinline__ void tg_stage_scales(const TgArgs& a, float* s_as) {
 // Segment of a 16-row block: selects on wave-uniform values (pointers stay scalar).
 struct TgBlk {
     const uint4* pack;
-    const v2u* sc;
+    const uint4* sc;
     float* y;
     int base, n;
 };
@@ -219,29 +340,32 @@ __device__ __forceinline__ TgBlk tg_blk(const TgArgs& a, int row0) {
     return r;
 }
 
-// MODE: TG_NORM / TG_Q8 input. GU: gate/up epilogue (KS = 1, one 32-row chunk per
-// workgroup: waves 0,1 gate rows +0/+16, waves 2,3 up rows +0/+16). KS waves share a
-// 16-row block, each on NL steps of 4 groups. KU, TP: TG_NORM's prologue shape.
-template <int MODE, bool GU, int KS, int NL, int KU, int TP>
-__global__ __launch_bounds__(256) void k_tgemm(TgArgs a) {
-    static_assert(!GU || KS == 1, "gate/up: one wave per 16-row block");
+constexpr int tg_uq(int W, int KS, int NL) { return 2 * NL * KS / W > 0 ? 2 * NL * KS / W : 1; }
+constexpr int tg_sq(int W, int KS, int NL) { return (NL * KS + W - 1) / W; }
+
+// MODE: TG_NORM (W = 4) / TG_Q8 input. GU: gate/up epilogue (W = 4, KS = 1: waves 0,1
+// gate rows +0/+16 of the workgroup's 32-row chunk, waves 2,3 up rows). W waves per
+// workgroup, KS waves per 16-row block, each on NL steps of 4 groups (K = 128*KS*NL).
+// KU, TP: TG_NORM's prologue shape.
+template <int MODE, bool GU, int W, int KS, int NL, int KU, int TP>
+__global__ __launch_bounds__(64 * W) void k_tgemm(TgArgs a) {
+    static_assert(MODE == TG_Q8 || W == 4, "the norm prologue runs on 256 threads");
+    static_assert(!GU || (W == 4 && KS == 1), "gate/up: four 16-row blocks per workgroup");
+    static_assert(NL % 2 == 0, "scales are loaded 8 groups at a time");
     extern __shared__ __align__(16) uint32_t s_dyn[];
     const int T = a.T, G = a.K / 32, S = a.S;
-    uint32_t* s_aq = s_dyn;
-    float* s_as = reinterpret_cast<float*>(s_dyn + (MODE == TG_NORM ? tg_codes_words(T, S) : 0));
-    float* s_part = s_as + G * 16;
-    float* red = s_part + tg_part_floats();
+    const TgLds L = tg_carve(s_dyn, T, a.K, W);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int m = lane & 15, j = lane >> 4;
-    constexpr int BPW = 4 / KS;
+    constexpr int BPW = W / KS;
 
     // this wave's block: rows [row0, row0+16) of one matrix, groups [gbase, gbase + 4*NL)
     const int gbase = (wave % KS) * 4 * NL;
     int row0;
     bool valid = true;
     const uint4* P;
-    const v2u* SC;
+    const uint4* SC;
     TgBlk bs;
     if constexpr (GU) {
         row0 = blockIdx.x * 32 + 16 * (wave & 1);
@@ -262,27 +386,29 @@ __global__ __launch_bounds__(256) void k_tgemm(TgArgs a) {
     const int lrow = min(row0 - bs.base + m, bs.n - 1);
     const int tA = min(m, T - 1);                    // this lane's A-operand token
 
-    uint4 wv[NL];
-    v2u sv[NL];
-    uint2 aq[MODE == TG_Q8 ? NL : 1][4];
+    // 1. activation loads first: the prologue then waits for these only
+    NormRegs<MODE == TG_NORM ? KU : 1, MODE == TG_NORM ? TP : 1> nr;
+    Q8Regs<tg_uq(W, KS, NL), tg_sq(W, KS, NL)> qr;
+    if constexpr (MODE == TG_NORM) {
+#pragma unroll
+        for (int i = 0; i < KU; i++) nr.wc[i] = a.nw[KU * tid + i];
+        tg_norm_load<KU, TP>(a, 0, nr);
+    } else {
+        tg_q8_load(a, qr, 64 * W);
+    }
+    // 2. the weights and scales of every step
+    uint4 wv[NL], sv[NL / 2];
     {
         const uint4* pr = P + (size_t)lrow * G + gbase + j;
-        const v2u* sr = SC + ((size_t)lrow * G + gbase) / 4;
+        const uint4* sr = SC + ((size_t)lrow * G + gbase) / 8;
 #pragma unroll
         for (int s = 0; s < NL; s++) {
             wv[s] = ti_ld_nt(pr + 4 * s);
-            sv[s] = __builtin_nontemporal_load(sr + s);
-        }
-        if constexpr (MODE == TG_Q8) {
-            const uint2* ar = reinterpret_cast<const uint2*>(a.xq + (size_t)tA * (a.K / 4)) + 4 * gbase + j;
-#pragma unroll
-            for (int s = 0; s < NL; s++)
-#pragma unroll
-                for (int u = 0; u < 4; u++) aq[s][u] = ar[4 * (4 * s + u)];
+            if (s % 2 == 0) sv[s / 2] = ti_ld_nt(sr + s / 2);
         }
     }
     // residual rows this thread stores (KS waves of a block: 16*T outputs over 64*KS lanes)
-    constexpr int NE = GU ? 1 : (16 * TG_TMAX) / (64 * KS);
+    constexpr int NE = GU ? 1 : (16 * TG_TMAX + 64 * KS - 1) / (64 * KS);
     float yold[NE];
     if constexpr (!GU) {
 #pragma unroll
@@ -295,30 +421,37 @@ __global__ __launch_bounds__(256) void k_tgemm(TgArgs a) {
     }
     TI_ISSUE_FENCE();
 
-    if constexpr (MODE == TG_NORM) tg_norm_prologue<KU, TP>(a, s_aq, s_as, red);
-    else tg_stage_scales(a, s_as);
+    // 3. prologue: codes in B's byte order, scales, -8*sum(a) into LDS
+    if constexpr (MODE == TG_NORM) {
+        for (int p0 = 0; p0 < T; p0 += TP) {
+            if (p0 > 0) tg_norm_load<KU, TP>(a, p0, nr);
+            tg_norm_pass<KU, TP>(a, p0, nr, L);
+        }
+        if constexpr (KU < 8) tg_norm_finish(a, L, 256);
+    } else {
+        tg_q8_stage(a, qr, L, 64 * W);
+    }
 
+    // 4. the group loop
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int s = 0; s < NL; s++) {
         uint32_t bw[4];
         tr4_rows(wv[s], bw);
+        const uint4 sc4 = sv[s / 2];
 #pragma unroll
         for (int u = 0; u < 4; u++) {
             const int g = gbase + 4 * s + u;
-            uint2 av;
-            if constexpr (MODE == TG_Q8) av = aq[s][u];
-            else av = *reinterpret_cast<const uint2*>(s_aq + tA * S + 8 * g + 2 * j);
-            const uint32_t alo = even_bytes(av.x, av.y), ahi = odd_bytes(av.x, av.y);
-            uint32_t blo, bhi;
-            nib_to_s8(bw[u], blo, bhi);
-            const long A = (long)(((uint64_t)ahi << 32) | alo);
-            const long B = (long)(((uint64_t)bhi << 32) | blo);
-            const v4i z = {0, 0, 0, 0};
-            const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, z, 0, 0, 0);
-            const float4 sx = *reinterpret_cast<const float4*>(s_as + g * 16 + 4 * j);
-            const uint32_t sp = (u & 2) ? sv[s].y : sv[s].x;
-            const float sw = ti_h2f((uint16_t)((u & 1) ? (sp >> 16) : (sp & 0xffff)));
+            const uint2 av = *reinterpret_cast<const uint2*>(L.aq + tA * S + 8 * g + 2 * j);
+            const v4i cv = *reinterpret_cast<const v4i*>(L.corr + g * 16 + 4 * j);
+            const float4 sx = *reinterpret_cast<const float4*>(L.as + g * 16 + 4 * j);
+            const long A = (long)(((uint64_t)av.y << 32) | av.x);
+            const uint32_t lo = bw[u] & 0x0F0F0F0Fu, hi = (bw[u] >> 4) & 0x0F0F0F0Fu;
+            const long B = (long)(((uint64_t)hi << 32) | lo);
+            const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, cv, 0, 0, 0);
+            const int h = 4 * (s & 1) + u;             // this group's half in sc4
+            const uint32_t sp = h < 2 ? sc4.x : (h < 4 ? sc4.y : (h < 6 ? sc4.z : sc4.w));
+            const float sw = ti_h2f((uint16_t)((h & 1) ? (sp >> 16) : (sp & 0xffff)));
             acc[0] = fmaf((float)d[0], sw * sx.x, acc[0]);
             acc[1] = fmaf((float)d[1], sw * sx.y, acc[1]);
             acc[2] = fmaf((float)d[2], sw * sx.z, acc[2]);
@@ -327,7 +460,7 @@ __global__ __launch_bounds__(256) void k_tgemm(TgArgs a) {
     }
     // partials: lane (m, j) holds tokens 4j..4j+3 of row m of the wave's block
 #pragma unroll
-    for (int i = 0; i < 4; i++) s_part[(wave * 16 + 4 * j + i) * 17 + m] = acc[i];
+    for (int i = 0; i < 4; i++) L.part[(wave * 16 + 4 * j + i) * 17 + m] = acc[i];
     __syncthreads();
 
     if constexpr (GU) {
@@ -336,8 +469,8 @@ __global__ __launch_bounds__(256) void k_tgemm(TgArgs a) {
         const int r = tid & 31;
         const int ch = blockIdx.x;
         for (int tok = tid >> 5; tok < T; tok += 8) {
-            const float gv = s_part[((r >> 4) * 16 + tok) * 17 + (r & 15)];
-            const float uv = s_part[((2 + (r >> 4)) * 16 + tok) * 17 + (r & 15)];
+            const float gv = L.part[((r >> 4) * 16 + tok) * 17 + (r & 15)];
+            const float uv = L.part[((2 + (r >> 4)) * 16 + tok) * 17 + (r & 15)];
             const float v = silu_mul(gv, uv);
             const float mx = ti_max32_nonneg(fabsf(v));
             const float scale = mx / 127.0f;
@@ -358,7 +491,7 @@ __global__ __launch_bounds__(256) void k_tgemm(TgArgs a) {
             if (tok < T && lr < bs.n) {
                 float v = 0.0f;
 #pragma unroll
-                for (int k = 0; k < KS; k++) v += s_part[((w0 + k) * 16 + tok) * 17 + mm];
+                for (int k = 0; k < KS; k++) v += L.part[((w0 + k) * 16 + tok) * 17 + mm];
                 bs.y[(size_t)tok * bs.n + lr] = a.acc ? yold[r] + v : v;
             }
         }
@@ -366,17 +499,18 @@ __global__ __launch_bounds__(256) void k_tgemm(TgArgs a) {
 }
 
 // ---- host dispatch ------------------------------------------------------------------
-// (KS, NL) per K: NL = K/32 / (4*KS) steps of 4 groups per wave
-bool tg_split(int G, int& KS, int& NL) {
+// (W, KS, NL) per K = 128*KS*NL: TG_Q8 runs 8-wave workgroups where K allows (all SIMDs
+// of the chip busy at N = 2048); TG_NORM runs 4 waves (its prologue is 256 threads).
+bool tg_split_q8(int G, int& W, int& KS, int& NL) {
     switch (G) {
-        case 8: KS = 1; NL = 2; return true;
-        case 16: KS = 1; NL = 4; return true;
-        case 32: KS = 2; NL = 4; return true;
-        case 64: KS = 2; NL = 8; return true;
-        case 96: KS = 4; NL = 6; return true;
-        case 128: KS = 4; NL = 8; return true;
-        case 192: KS = 4; NL = 12; return true;
-        case 256: KS = 4; NL = 16; return true;
+        case 8: W = 4; KS = 1; NL = 2; return true;
+        case 16: W = 4; KS = 2; NL = 2; return true;
+        case 32: W = 8; KS = 4; NL = 2; return true;
+        case 64: W = 8; KS = 8; NL = 2; return true;
+        case 96: W = 8; KS = 4; NL = 6; return true;
+        case 128: W = 8; KS = 8; NL = 4; return true;
+        case 192: W = 8; KS = 8; NL = 6; return true;
+        case 256: W = 8; KS = 8; NL = 8; return true;
         default: return false;
     }
 }
@@ -389,23 +523,18 @@ int tg_ku(int K) {   // TG_NORM prologue: K = 256*KU, KU in {1, 2, 4, 8, 16}
 
 constexpr int tg_tp(int ku) { return ku >= 16 ? 4 : 8; }
 
-size_t tg_lds(int mode, int T, int K, int ku) {
-    const int G = K / 32;
-    size_t w = (size_t)G * 16 + tg_part_floats();
-    if (mode == TG_NORM) w += (size_t)tg_codes_words(T, K / 4 + 2) + (size_t)tg_tp(ku) * 256;
-    return w * 4;
-}
-
-template <int MODE, bool GU, int KS, int NL, int KU>
-int tg_go(ti_ctx* c, const TgArgs& a, unsigned grid, size_t lds, const char* name) {
+template <int MODE, bool GU, int W, int KS, int NL, int KU>
+int tg_go(ti_ctx* c, const TgArgs& a, unsigned grid, const char* name) {
+    constexpr int TP = MODE == TG_NORM ? tg_tp(KU) : 0;
+    const size_t lds = (size_t)tg_lds_words(a.T, a.K, W, TP) * 4;
     static bool attr = false;
     if (!attr && lds > 65536) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_tgemm<MODE, GU, KS, NL, KU, tg_tp(KU)>),
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_tgemm<MODE, GU, W, KS, NL, KU, TP>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         if (e != hipSuccess) return ti_hip_fail(e, "k_tgemm LDS attribute");
         attr = true;
     }
-    k_tgemm<MODE, GU, KS, NL, KU, tg_tp(KU)><<<grid, 256, lds, c->stream>>>(a);
+    k_tgemm<MODE, GU, W, KS, NL, KU, TP><<<grid, 64 * W, lds, c->stream>>>(a);
     TI_LAUNCHED(name);
     return TI_OK;
 }
@@ -413,16 +542,18 @@ int tg_go(ti_ctx* c, const TgArgs& a, unsigned grid, size_t lds, const char* nam
 }  // namespace
 
 // Which T-token projections take the fused path: 2..16 tokens, K/32 in the split
-// table, and (TG_NORM) K = 256 * {1,2,4,8,16}.
+// table, and (TG_NORM) K = 256 * {1,2,4,8,16}; gate/up needs K <= 2048.
 bool ti_tgemm_ok(int T, int K, int norm, int gateup) {
-    int KS, NL;
-    if (T < 2 || T > TG_TMAX || K % 32 || !tg_split(K / 32, KS, NL)) return false;
+    int W, KS, NL;
+    if (T < 2 || T > TG_TMAX || K % 32 || !tg_split_q8(K / 32, W, KS, NL)) return false;
     if (norm && !tg_ku(K)) return false;
-    return !gateup || K / 128 <= 16;                // gate/up runs KS = 1: NL = K/128 <= 16
+    return !gateup || K <= 2048;
 }
 
 // q/k/v-style: y_s[t][:] = W_s rmsnorm(x[t]) for up to three segments sharing the
 // activation (TG_NORM), or y[t][:] (+)= W xq[t] on int8 input (TG_Q8, one segment).
+// Scales must be 16-byte aligned (K/32 groups of f16 per row, K % 256 == 0 keeps every
+// row aligned).
 int ti_tgemm_launch(ti_ctx* c, int norm, const float* x, const uint16_t* nw, float eps, const uint32_t* xq,
                     const float* xs, int nseg, const uint32_t* const* packs, const uint16_t* const* scs,
                     float* const* ys, const int* Ns, int T, int K, int acc) {
@@ -430,9 +561,9 @@ int ti_tgemm_launch(ti_ctx* c, int norm, const float* x, const uint16_t* nw, flo
     a.nseg = nseg;
     a.N = 0;
     for (int s = 0; s < nseg; s++) {
-        a.seg[s] = {reinterpret_cast<const uint4*>(packs[s]), reinterpret_cast<const v2u*>(scs[s]), ys[s], Ns[s]};
+        a.seg[s] = {reinterpret_cast<const uint4*>(packs[s]), reinterpret_cast<const uint4*>(scs[s]), ys[s], Ns[s]};
         if (s + 1 < nseg && Ns[s] % 16) return ti_fail(TI_ERR_INVALID, "T-token GEMM: segment rows must be multiples of 16");
-        if (reinterpret_cast<uintptr_t>(scs[s]) % 8) return ti_fail(TI_ERR_INVALID, "T-token GEMM: scales must be 8-byte aligned");
+        if (reinterpret_cast<uintptr_t>(scs[s]) % 16) return ti_fail(TI_ERR_INVALID, "T-token GEMM: scales must be 16-byte aligned");
         a.N += Ns[s];
     }
     a.K = K;
@@ -444,25 +575,26 @@ int ti_tgemm_launch(ti_ctx* c, int norm, const float* x, const uint16_t* nw, flo
     a.eps = eps;
     a.xq = xq;
     a.xs = xs;
-    int KS, NL;
     if (!ti_tgemm_ok(T, K, norm, 0)) return ti_fail(TI_ERR_INVALID, "T-token GEMM: unsupported T=%d K=%d", T, K);
-    tg_split(K / 32, KS, NL);
-    const int ku = norm ? tg_ku(K) : 0;
-    const unsigned grid = (unsigned)(((a.N + 15) / 16 + 4 / KS - 1) / (4 / KS));
-    const size_t lds = tg_lds(norm ? TG_NORM : TG_Q8, T, K, ku);
+    const int nb = (a.N + 15) / 16;
     if (norm) {
-        switch (ku) {
-            case 1: return tg_go<TG_NORM, false, 1, 2, 1>(c, a, grid, lds, "k_tgemm_norm");
-            case 2: return tg_go<TG_NORM, false, 1, 4, 2>(c, a, grid, lds, "k_tgemm_norm");
-            case 4: return tg_go<TG_NORM, false, 2, 4, 4>(c, a, grid, lds, "k_tgemm_norm");
-            case 8: return tg_go<TG_NORM, false, 2, 8, 8>(c, a, grid, lds, "k_tgemm_norm");
-            case 16: return tg_go<TG_NORM, false, 4, 8, 16>(c, a, grid, lds, "k_tgemm_norm");
+        // 4 waves: KS = K/512 waves per block (K/32 = 4*KS*NL with NL = 2 .. 8)
+        const unsigned g1 = (unsigned)((nb + 3) / 4), g2 = (unsigned)((nb + 1) / 2), g4 = (unsigned)nb;
+        switch (tg_ku(K)) {
+            case 1: return tg_go<TG_NORM, false, 4, 1, 2, 1>(c, a, g1, "k_tgemm_norm");
+            case 2: return tg_go<TG_NORM, false, 4, 2, 2, 2>(c, a, g2, "k_tgemm_norm");
+            case 4: return tg_go<TG_NORM, false, 4, 4, 2, 4>(c, a, g4, "k_tgemm_norm");
+            case 8: return tg_go<TG_NORM, false, 4, 4, 4, 8>(c, a, g4, "k_tgemm_norm");
+            case 16: return tg_go<TG_NORM, false, 4, 4, 8, 16>(c, a, g4, "k_tgemm_norm");
         }
     } else {
         switch (K / 32) {
-#define TGQ(G_, KS_, NL_) case G_: return tg_go<TG_Q8, false, KS_, NL_, 0>(c, a, grid, lds, "k_tgemm_q8");
-            TGQ(8, 1, 2) TGQ(16, 1, 4) TGQ(32, 2, 4) TGQ(64, 2, 8) TGQ(96, 4, 6) TGQ(128, 4, 8) TGQ(192, 4, 12)
-            TGQ(256, 4, 16)
+#define TGQ(G_, W_, KS_, NL_)                                                                        \
+    case G_:                                                                                         \
+        return tg_go<TG_Q8, false, W_, KS_, NL_, 0>(c, a, (unsigned)((nb + W_ / KS_ - 1) / (W_ / KS_)), \
+                                                    "k_tgemm_q8");
+            TGQ(8, 4, 1, 2) TGQ(16, 4, 2, 2) TGQ(32, 8, 4, 2) TGQ(64, 8, 8, 2) TGQ(96, 8, 4, 6) TGQ(128, 8, 8, 4)
+            TGQ(192, 8, 8, 6) TGQ(256, 8, 8, 8)
 #undef TGQ
         }
     }
@@ -474,10 +606,10 @@ int ti_tgemm_gateup_launch(ti_ctx* c, const float* x, const uint16_t* nw, float 
                            const uint16_t* gsc, const uint32_t* upack, const uint16_t* usc, int I, int H, int T,
                            uint32_t* swq, float* sws) {
     if (!ti_tgemm_ok(T, H, 1, 1) || I % 32) return ti_fail(TI_ERR_INVALID, "T-token gate/up: unsupported T=%d H=%d I=%d", T, H, I);
-    if (reinterpret_cast<uintptr_t>(gsc) % 8 || reinterpret_cast<uintptr_t>(usc) % 8)
-        return ti_fail(TI_ERR_INVALID, "T-token gate/up: scales must be 8-byte aligned");
+    if (reinterpret_cast<uintptr_t>(gsc) % 16 || reinterpret_cast<uintptr_t>(usc) % 16)
+        return ti_fail(TI_ERR_INVALID, "T-token gate/up: scales must be 16-byte aligned");
     TgArgs a = {};
-    a.seg[0] = {reinterpret_cast<const uint4*>(gpack), reinterpret_cast<const v2u*>(gsc), nullptr, I};
+    a.seg[0] = {reinterpret_cast<const uint4*>(gpack), reinterpret_cast<const uint4*>(gsc), nullptr, I};
     a.nseg = 1;
     a.N = I;
     a.K = H;
@@ -487,17 +619,15 @@ int ti_tgemm_gateup_launch(ti_ctx* c, const float* x, const uint16_t* nw, float 
     a.nw = nw;
     a.eps = eps;
     a.upack = reinterpret_cast<const uint4*>(upack);
-    a.usc = reinterpret_cast<const v2u*>(usc);
+    a.usc = reinterpret_cast<const uint4*>(usc);
     a.yq = swq;
     a.ys = sws;
-    const int ku = tg_ku(H);
-    const size_t lds = tg_lds(TG_NORM, T, H, ku);
     const unsigned grid = (unsigned)(I / 32);
-    switch (ku) {
-        case 1: return tg_go<TG_NORM, true, 1, 2, 1>(c, a, grid, lds, "k_tgemm_gateup");
-        case 2: return tg_go<TG_NORM, true, 1, 4, 2>(c, a, grid, lds, "k_tgemm_gateup");
-        case 4: return tg_go<TG_NORM, true, 1, 8, 4>(c, a, grid, lds, "k_tgemm_gateup");
-        case 8: return tg_go<TG_NORM, true, 1, 16, 8>(c, a, grid, lds, "k_tgemm_gateup");
+    switch (tg_ku(H)) {
+        case 1: return tg_go<TG_NORM, true, 4, 1, 2, 1>(c, a, grid, "k_tgemm_gateup");
+        case 2: return tg_go<TG_NORM, true, 4, 1, 4, 2>(c, a, grid, "k_tgemm_gateup");
+        case 4: return tg_go<TG_NORM, true, 4, 1, 8, 4>(c, a, grid, "k_tgemm_gateup");
+        case 8: return tg_go<TG_NORM, true, 4, 1, 16, 8>(c, a, grid, "k_tgemm_gateup");
     }
     return ti_fail(TI_ERR_INVALID, "T-token gate/up: no kernel for H=%d", H);
 }
