@@ -11,16 +11,6 @@
 #include "ti_internal.h"
 #include <math.h>
 
-// ---------------------------------------------------------------------------
-// snorm int8 (pack4x8snorm): code = floor(0.5 + 127*clamp(x/mx, -1, 1)),
-// evaluated exactly (double) on the f32 quotient; mx = max(1e-12, max|x|).
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ uint32_t snorm_code(float x, float mx) {
-    float e = x / mx;
-    e = e > 1.0f ? 1.0f : (e < -1.0f ? -1.0f : e);
-    return (uint32_t)((int)floor(0.5 + 127.0 * (double)e) & 0xff);
-}
-
 // Quantize 32 values held by one thread into 8 words + a scale.
 __device__ __forceinline__ void snorm_group(const float* v, uint32_t* q, float* s) {
     float mx = 1e-12f;

@@ -163,6 +163,14 @@ __device__ __forceinline__ float ti_tree_sum_256(float s, float* red) {
     return v;
 }
 
+// snorm int8 of the KV cache (pack4x8snorm): code = floor(0.5 + 127*clamp(x/mx, -1, 1)),
+// evaluated exactly (double) on the f32 quotient; mx = max(1e-12, max|x|) of the 32-group.
+__device__ __forceinline__ uint32_t snorm_code(float x, float mx) {
+    float e = x / mx;
+    e = e > 1.0f ? 1.0f : (e < -1.0f ? -1.0f : e);
+    return (uint32_t)((int)floor(0.5 + 127.0 * (double)e) & 0xff);
+}
+
 // ---- cross-workgroup hand-off without cache maintenance ----------------------------
 // The "last workgroup finishes the reduction" kernels publish a few words per
 // workgroup. A device-scope fence on gfx950 writes back and invalidates the whole

@@ -41,6 +41,10 @@ int ti_tgemm_launch(ti_ctx* c, int norm, const float* x, const uint16_t* nw, flo
 int ti_tgemm_gateup_launch(ti_ctx* c, const float* x, const uint16_t* nw, float eps, const uint32_t* gpack,
                            const uint16_t* gsc, const uint32_t* upack, const uint16_t* usc, int I, int H, int T,
                            uint32_t* swq, float* sws);
+bool ti_tattn_ok(int T, int nHq, int nKv, int hd);
+int ti_tattn_launch(ti_ctx* c, const float* q, const float* k, const float* v, const uint16_t* qw, const uint16_t* kw,
+                    const float* rope, uint32_t* kq, float* ks, uint32_t* vq, float* vs, int S0, int T, int nHq, int nKv,
+                    int hd, float eps, uint32_t* oq, float* os);
 
 // ---------------------------------------------------------------------------
 // glue kernels
@@ -438,6 +442,7 @@ extern "C" int ti_qwen3_forward(ti_ctx* c, ti_qwen3* m, const int32_t* ids, int 
     // the matrix cores with their norm / quantizer / SwiGLU fused (k_tgemm.hip)
     const bool fused = ti_tgemm_ok(T, H, 1, 1) && ti_tgemm_ok(T, nq, 0, 0) && ti_tgemm_ok(T, I, 0, 0) &&
                        nq % 16 == 0 && nkv % 16 == 0 && I % 32 == 0;
+    const bool fused_attn = ti_tattn_ok(T, nHq, nKv, hd);
     for (int l = 0; l < C.layers; l++) {
         Layer& y = m->L[l];
         if (fused) {
@@ -452,12 +457,17 @@ extern "C" int ti_qwen3_forward(ti_ctx* c, ti_qwen3* m, const int32_t* ids, int 
             RC(ti_linear_q4(c, m->normed, y.k.pack, y.k.sc, m->k, T, nkv, H, 0));
             RC(ti_linear_q4(c, m->normed, y.v.pack, y.v.sc, m->v, T, nkv, H, 0));
         }
-        RC(ti_rope_qk(c, m->q, y.q_norm, m->qr, T, nHq, hd, pos, C.rope_theta, C.rms_eps));
-        RC(ti_rope_qk(c, m->k, y.k_norm, m->kr, T, nKv, hd, pos, C.rope_theta, C.rms_eps));
-        RC(ti_kv_write_q8(c, m->kr, m->v, y.kq, y.ks, y.vq, y.vs, T, nKv, hd, pos));
-        RC(ti_attn_decode_launch(c, m->qr, y.kq, y.ks, y.vq, y.vs, m->attn, pos + 1, T, nHq, nKv, hd, 0, nullptr, 0));
+        if (fused && fused_attn) {
+            RC(ti_tattn_launch(c, m->q, m->k, m->v, y.q_norm, y.k_norm, m->rope, y.kq, y.ks, y.vq, y.vs, pos, T, nHq, nKv,
+                               hd, C.rms_eps, m->xq, m->xs));
+        } else {
+            RC(ti_rope_qk(c, m->q, y.q_norm, m->qr, T, nHq, hd, pos, C.rope_theta, C.rms_eps));
+            RC(ti_rope_qk(c, m->k, y.k_norm, m->kr, T, nKv, hd, pos, C.rope_theta, C.rms_eps));
+            RC(ti_kv_write_q8(c, m->kr, m->v, y.kq, y.ks, y.vq, y.vs, T, nKv, hd, pos));
+            RC(ti_attn_decode_launch(c, m->qr, y.kq, y.ks, y.vq, y.vs, m->attn, pos + 1, T, nHq, nKv, hd, 0, nullptr, 0));
+        }
         if (fused) {
-            RC(ti_quant_act_q8_async(c, m->attn, m->xq, m->xs, nullptr, T * (nq / 32)));
+            if (!fused_attn) RC(ti_quant_act_q8_async(c, m->attn, m->xq, m->xs, nullptr, T * (nq / 32)));
             RC(ti_tgemm_launch(c, 0, nullptr, nullptr, 0.0f, m->xq, m->xs, 1, &y.o.pack, &y.o.sc, &m->x, &H, T, nq, 1));
             RC(ti_tgemm_gateup_launch(c, m->x, y.post_norm, C.rms_eps, y.gate.pack, y.gate.sc, y.up.pack, y.up.sc, I, H,
                                       T, m->xq, m->xs));
