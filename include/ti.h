@@ -87,6 +87,9 @@ int ti_quant_act_q8_t(ti_ctx* ctx, const float* x, uint32_t* xq, float* xs, int 
 /* rmsnormQ (models/qwen3.js:569-621): fused RMSNorm + int8 quant. */
 int ti_rmsnorm_q8(ti_ctx* ctx, const float* x, const uint16_t* w, uint32_t* xq, float* xs,
                   int32_t* xsum, int H, float eps);
+/* rmsnorm (models/qwen3.js:60-88) + QUANTQ8T (:1210-1231) of T rows, the int8 input of the
+ * T-token projections: xq[T][H/4], xs[T][H/32]. H = 256 * {1, 2, 4, 8, 16}. */
+int ti_rmsnorm_q8_t(ti_ctx* ctx, const float* x, const uint16_t* w, uint32_t* xq, float* xs, int T, int H, float eps);
 /* rmsnorm (models/qwen3.js:60-88), y[T,H]. */
 int ti_rmsnorm(ti_ctx* ctx, const float* x, const uint16_t* w, float* y, int T, int H, float eps);
 

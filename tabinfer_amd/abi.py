@@ -49,6 +49,7 @@ SIGS = {
     "ti_quant_act_q8_t": [_p, _p, _p, _p, _i, _i],
     "ti_rmsnorm_q8": [_p, _p, _p, _p, _p, _p, _i, _f],
     "ti_rmsnorm": [_p, _p, _p, _p, _i, _i, _f],
+    "ti_rmsnorm_q8_t": [_p, _p, _p, _p, _p, _i, _i, _f],
     "ti_gemv_q4_q8": [_p, _p, _p, _p, _p, _p, _i, _i, _i],
     "ti_gemv_q4_f32": [_p, _p, _p, _p, _p, _i, _i, _i],
     "ti_gateup_silu_q4": [_p, _p, _p, _p, _p, _p, _p, _p, _i, _i],

@@ -1,18 +1,23 @@
 // k_tgemm.hip — the projections of a T-token forward (2 <= T <= 16: the batch-8
-// decode step, short prefills) as single launches on the matrix cores.
+// decode step, short prefills) on the matrix cores.
 //
 // The reference runs a T-token linear as quantQ8T + gemmDP4A (models/qwen3.js:1210-1231,
-// 1326-1407), preceded by an rmsnorm dispatch (:569-612) for q/k/v and gate/up, and
-// followed by a SwiGLU dispatch before the down projection. Here each projection is
-// one launch:
+// 1326-1407), after an rmsnorm dispatch (:569-612) for q/k/v and gate/up and a SwiGLU
+// dispatch before the down projection. Here:
 //
-//   TG_NORM   per-token RMSNorm + quantQ8T of x in every workgroup's prologue, then
-//             the GEMM over up to three matrices sharing the activation (q, k, v)
-//   TG_Q8     the GEMM on int8 activations another kernel produced (o_proj after the
-//             attention, down_proj after gate/up), + the residual
-//   gate/up   TG_NORM prologue, gate and up rows of one 32-row chunk in one workgroup,
-//             silu(g)*u and its per-token quantQ8 (32 rows = one scale group) in the
-//             epilogue: the down projection's int8 input, with no f32 round trip
+//   k_tnorm_q8  per-token RMSNorm + quantQ8T, one workgroup per token (shared by the
+//               q/k/v and gate/up projections of a layer)
+//   k_tgemm     the GEMM on int8 activations (the norm codes, the attention output's,
+//               SwiGLU's) over up to three matrices sharing them (q, k, v), with the
+//               residual (o_proj, down_proj), or
+//   gate/up     gate and up rows of one 32-row chunk in one workgroup, silu(g)*u and
+//               its per-token quantQ8 (32 rows = one scale group) in the epilogue: the
+//               down projection's int8 input, with no f32 round trip
+//
+// (An earlier variant computed the RMSNorm in every GEMM workgroup's prologue: at T = 8
+// each workgroup then read the whole T x K f32 activation twice, 24-32 MB of L2 reads per
+// projection, and the q/k/v and gate/up kernels took 11 and 16 us against 4.8 + 4.5 and
+// 9.8 + 4.5 us for norm kernel + int8 GEMM.)
 //
 // GEMM core. One v_mfma_i32_16x16x32_i8 computes the exact int32 dot of one 32-element
 // scale group for 16 tokens x 16 weight rows (lane l feeds row/column l%16, K slice
@@ -20,13 +25,13 @@
 // activations (row = token), B = weights (column = weight row). Each int32 group dot is
 // scaled by s_w[n,g] * s_x[t,g] into an f32 accumulator, as the reference does per group.
 //
-// The VALU work per group is what bounds these kernels (a wave64 VALU op takes 4
+// The VALU work per group is what bounds the group loop (a wave64 VALU op takes 4
 // cycles; the MFMA is cheap), so everything that can be done once per workgroup is
-// taken out of the group loop:
+// taken out of it:
 //   - the weight nibbles go into B unsigned (nibble = w + 8, two ANDs and a shift), and
 //     the MFMA's accumulator input carries -8 * sum(a) of the group, so the int32 result
 //     is the signed dot exactly;
-//   - the activation codes are stored in LDS already in B's byte order (per 8-byte K
+//   - the activation codes are staged in LDS already in B's byte order (per 8-byte K
 //     slice: even elements, then odd elements), with the -8*sum(a) terms and the scales
 //     token-minor ([g][16]: one 16-byte read gives a lane its 4 tokens).
 //
@@ -43,8 +48,6 @@
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
-
-enum { TG_Q8 = 0, TG_NORM = 1 };
 
 constexpr int TG_TMAX = 16;
 
@@ -63,11 +66,8 @@ struct TgArgs {
     int T;
     int acc;             // y += W x (residual)
     int S;               // LDS row stride of the activation codes, words (K/4 + 2)
-    const float* x;      // TG_NORM: [T][K] f32
-    const uint16_t* nw;  // TG_NORM: f16 norm weight [K]
-    float eps;
-    const uint32_t* xq;  // TG_Q8: [T][K/4] codes
-    const float* xs;     // TG_Q8: [T][K/32] scales
+    const uint32_t* xq;  // [T][K/4] codes
+    const float* xs;     // [T][K/32] scales
     const uint4* upack;  // gate/up: the up matrix (seg[0] is gate)
     const uint4* usc;
     uint32_t* yq;        // gate/up: swi codes [T][N/4]
@@ -75,10 +75,10 @@ struct TgArgs {
 };
 
 // LDS (dynamic), in words: codes [T][S] (rounded to 4), scales [G][16] f32, -8*sum(a)
-// [G][16] i32, partials [W][16][17] f32, norm partial sums [TP][256] f32 (TG_NORM)
+// [G][16] i32, partials [W][16][17] f32
 __host__ __device__ constexpr int tg_codes_words(int T, int S) { return (T * S + 3) & ~3; }
-__host__ __device__ constexpr int tg_lds_words(int T, int K, int W, int TP) {
-    return tg_codes_words(T, K / 4 + 2) + 2 * (K / 32) * 16 + W * 16 * 17 + TP * 256;
+__host__ __device__ constexpr int tg_lds_words(int T, int K, int W) {
+    return tg_codes_words(T, K / 4 + 2) + 2 * (K / 32) * 16 + W * 16 * 17;
 }
 
 struct TgLds {
@@ -86,16 +86,14 @@ struct TgLds {
     float* as;
     int* corr;
     float* part;
-    float* red;
 };
-__device__ __forceinline__ TgLds tg_carve(uint32_t* base, int T, int K, int W) {
+__device__ __forceinline__ TgLds tg_carve(uint32_t* base, int T, int K) {
     const int G = K / 32;
     TgLds L;
     L.aq = base;
     L.as = reinterpret_cast<float*>(base + tg_codes_words(T, K / 4 + 2));
     L.corr = reinterpret_cast<int*>(L.as + G * 16);
     L.part = reinterpret_cast<float*>(L.corr + G * 16);
-    L.red = L.part + W * 16 * 17;
     return L;
 }
 
@@ -118,158 +116,7 @@ __device__ __forceinline__ int byte_sum(uint32_t w, int acc) {
     return __builtin_amdgcn_sdot4((int)w, 0x01010101, acc, false);
 }
 
-// sum of a token's 256 per-thread partials in the reference's tree order (red holds them)
-__device__ __forceinline__ float tg_tree(const float* red) {
-    const int l = threadIdx.x & 63;
-    const float a = red[l] + red[l + 128];
-    const float b = red[l + 64] + red[l + 192];
-    float v = a + b;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = v + ti_xor(v, o);
-    return v;
-}
-
-// ---- TG_NORM prologue ---------------------------------------------------------------
-// Per-token RMSNorm + quantQ8T of the T x K activation, K = 256*KU, TP tokens per pass.
-// Thread t holds elements t, t+256, ... of each token for the sum of squares (the
-// reference's 256 strided partials, then its 128..1 tree), and a contiguous copy,
-// elements KU*t .. KU*t+KU-1, for the quantizer: a 32-group spans 32/KU neighbouring
-// lanes, each thread computes its group's scale once. Codes and scales equal
-// rmsnorm + q8_group's, bit for bit.
-template <int KU, int TP>
-struct NormRegs {
-    float xsd[TP][KU];
-    float xc[TP][KU];
-    uint16_t wc[KU];
-};
-
-template <int KU, int TP>
-__device__ __forceinline__ void tg_norm_load(const TgArgs& a, int p0, NormRegs<KU, TP>& r) {
-    constexpr int K = 256 * KU;
-    const int t = threadIdx.x, T = a.T;
-#pragma unroll
-    for (int tp = 0; tp < TP; tp++) {
-        const int tok = min(p0 + tp, T - 1);
-        const float* xr = a.x + (size_t)tok * K;
-#pragma unroll
-        for (int i = 0; i < KU; i++) r.xsd[tp][i] = xr[t + 256 * i];
-        if constexpr (KU % 4 == 0) {
-            const float4* x4 = reinterpret_cast<const float4*>(xr + KU * t);
-#pragma unroll
-            for (int i = 0; i < KU / 4; i++) {
-                const float4 v = x4[i];
-                r.xc[tp][4 * i] = v.x; r.xc[tp][4 * i + 1] = v.y; r.xc[tp][4 * i + 2] = v.z; r.xc[tp][4 * i + 3] = v.w;
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < KU; i++) r.xc[tp][i] = xr[KU * t + i];
-        }
-    }
-}
-
-// one pass: codes of tokens p0 .. p0+TP-1 into LDS. KU >= 8: a thread's elements are
-// whole K slices, written in B's byte order with the group's -8*sum(a) (the slices of
-// a group are neighbouring lanes); KU < 8: natural order, tg_norm_finish reorders.
-template <int KU, int TP>
-__device__ __forceinline__ void tg_norm_pass(const TgArgs& a, int p0, const NormRegs<KU, TP>& r, const TgLds& L) {
-    constexpr int K = 256 * KU;
-    const int t = threadIdx.x, T = a.T, S = a.S;
-#pragma unroll
-    for (int tp = 0; tp < TP; tp++) {
-        float s = 0.0f;
-#pragma unroll
-        for (int i = 0; i < KU; i++) {
-            const float sq = r.xsd[tp][i] * r.xsd[tp][i];
-            s = s + sq;
-        }
-        L.red[tp * 256 + t] = s;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int tp = 0; tp < TP; tp++) {
-        const int tok = p0 + tp;
-        float m = tg_tree(L.red + tp * 256) / (float)K;
-        m = m + a.eps;
-        const float inv_rms = 1.0f / sqrtf(m);
-        float v[KU];
-        float mx = 0.0f;
-#pragma unroll
-        for (int i = 0; i < KU; i++) {
-            const float p = r.xc[tp][i] * inv_rms;
-            v[i] = p * ti_h2f(r.wc[i]);
-            mx = fmaxf(mx, fabsf(v[i]));
-        }
-        mx = group_max_contig<KU>(mx);
-        const float scale = mx / 127.0f;
-        const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
-        int q[KU];
-#pragma unroll
-        for (int i = 0; i < KU; i++) q[i] = q8_code(v[i], inv);
-        if constexpr (KU >= 8) {
-            // slices 8c..8c+7 (c = KU/8*t + k): even elements then odd elements
-            int sum = 0;
-            uint32_t wd[KU / 4];
-#pragma unroll
-            for (int k = 0; k < KU / 8; k++) {
-                uint32_t e = 0, o = 0;
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    e |= (uint32_t)(q[8 * k + 2 * i] & 0xff) << (8 * i);
-                    o |= (uint32_t)(q[8 * k + 2 * i + 1] & 0xff) << (8 * i);
-                }
-                wd[2 * k] = e;
-                wd[2 * k + 1] = o;
-                sum = byte_sum(o, byte_sum(e, sum));
-            }
-            sum += ti_xor(sum, 1);
-            if constexpr (KU == 8) sum += ti_xor(sum, 2);   // a group is 32/KU lanes
-            if (tok < T) {
-#pragma unroll
-                for (int k = 0; k < KU / 4; k++) L.aq[tok * S + KU / 4 * t + k] = wd[k];
-                if (t % (32 / KU) == 0) {
-                    const int g = KU * t / 32;
-                    L.as[g * 16 + tok] = scale;
-                    L.corr[g * 16 + tok] = -8 * sum;
-                }
-            }
-        } else {
-            uint32_t wd = 0;
-#pragma unroll
-            for (int i = 0; i < KU; i++) wd |= (uint32_t)(q[i] & 0xff) << (8 * i);
-            if (tok < T) {
-                if constexpr (KU == 4) {
-                    L.aq[tok * S + t] = wd;
-                } else {
-                    uint8_t* qb = reinterpret_cast<uint8_t*>(L.aq + tok * S);
-#pragma unroll
-                    for (int i = 0; i < KU; i++) qb[KU * t + i] = (uint8_t)((wd >> (8 * i)) & 0xff);
-                }
-                if (t % (32 / KU) == 0) L.as[(KU * t / 32) * 16 + tok] = scale;
-            }
-        }
-    }
-    __syncthreads();   // codes visible; red free for the next pass
-}
-
-// KU < 8: natural-order codes -> B's byte order and the -8*sum(a) terms, a group per thread
-__device__ __forceinline__ void tg_norm_finish(const TgArgs& a, const TgLds& L, int nthreads) {
-    const int G = a.K / 32, S = a.S;
-    for (int idx = threadIdx.x; idx < a.T * G; idx += nthreads) {
-        const int t = idx / G, g = idx % G;
-        uint2* p = reinterpret_cast<uint2*>(L.aq + t * S + 8 * g);
-        int sum = 0;
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const uint2 w = p[k];
-            sum = byte_sum(w.y, byte_sum(w.x, sum));
-            p[k] = make_uint2(even_bytes(w.x, w.y), odd_bytes(w.x, w.y));
-        }
-        L.corr[g * 16 + t] = -8 * sum;
-    }
-    __syncthreads();
-}
-
-// ---- TG_Q8 prologue -----------------------------------------------------------------
+// ---- prologue ------------------------------------------------------------------------
 // The producer's [T][K/4] codes and [T][K/32] scales, staged into LDS in B's byte
 // order: 16-byte units (two K slices, half a group) per thread, the two halves of a
 // group in neighbouring lanes (they add their sums by DPP). UQ, SQ: loads per thread.
@@ -343,18 +190,16 @@ __device__ __forceinline__ TgBlk tg_blk(const TgArgs& a, int row0) {
 constexpr int tg_uq(int W, int KS, int NL) { return 2 * NL * KS / W > 0 ? 2 * NL * KS / W : 1; }
 constexpr int tg_sq(int W, int KS, int NL) { return (NL * KS + W - 1) / W; }
 
-// MODE: TG_NORM (W = 4) / TG_Q8 input. GU: gate/up epilogue (W = 4, KS = 1: waves 0,1
-// gate rows +0/+16 of the workgroup's 32-row chunk, waves 2,3 up rows). W waves per
-// workgroup, KS waves per 16-row block, each on NL steps of 4 groups (K = 128*KS*NL).
-// KU, TP: TG_NORM's prologue shape.
-template <int MODE, bool GU, int W, int KS, int NL, int KU, int TP>
+// W waves per workgroup, KS waves per 16-row block, each on NL steps of 4 groups
+// (K = 128*KS*NL). GU: gate/up epilogue (four blocks per workgroup: gate rows +0/+16 of
+// the workgroup's 32-row chunk, then up rows +0/+16).
+template <bool GU, int W, int KS, int NL>
 __global__ __launch_bounds__(64 * W) void k_tgemm(TgArgs a) {
-    static_assert(MODE == TG_Q8 || W == 4, "the norm prologue runs on 256 threads");
-    static_assert(!GU || (W == 4 && KS == 1), "gate/up: four 16-row blocks per workgroup");
+    static_assert(!GU || W / KS == 4, "gate/up: four 16-row blocks per workgroup");
     static_assert(NL % 2 == 0, "scales are loaded 8 groups at a time");
     extern __shared__ __align__(16) uint32_t s_dyn[];
     const int T = a.T, G = a.K / 32, S = a.S;
-    const TgLds L = tg_carve(s_dyn, T, a.K, W);
+    const TgLds L = tg_carve(s_dyn, T, a.K);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int m = lane & 15, j = lane >> 4;
@@ -367,10 +212,11 @@ __global__ __launch_bounds__(64 * W) void k_tgemm(TgArgs a) {
     const uint4* P;
     const uint4* SC;
     TgBlk bs;
-    if constexpr (GU) {
-        row0 = blockIdx.x * 32 + 16 * (wave & 1);
-        P = wave < 2 ? a.seg[0].pack : a.upack;
-        SC = wave < 2 ? a.seg[0].sc : a.usc;
+    if constexpr (GU) {   // blocks 0, 1: gate rows +0/+16 of the chunk; 2, 3: up rows
+        const int b = wave / KS;
+        row0 = blockIdx.x * 32 + 16 * (b & 1);
+        P = b < 2 ? a.seg[0].pack : a.upack;
+        SC = b < 2 ? a.seg[0].sc : a.usc;
         bs.base = 0;
         bs.n = a.N;
     } else {
@@ -387,15 +233,8 @@ __global__ __launch_bounds__(64 * W) void k_tgemm(TgArgs a) {
     const int tA = min(m, T - 1);                    // this lane's A-operand token
 
     // 1. activation loads first: the prologue then waits for these only
-    NormRegs<MODE == TG_NORM ? KU : 1, MODE == TG_NORM ? TP : 1> nr;
     Q8Regs<tg_uq(W, KS, NL), tg_sq(W, KS, NL)> qr;
-    if constexpr (MODE == TG_NORM) {
-#pragma unroll
-        for (int i = 0; i < KU; i++) nr.wc[i] = a.nw[KU * tid + i];
-        tg_norm_load<KU, TP>(a, 0, nr);
-    } else {
-        tg_q8_load(a, qr, 64 * W);
-    }
+    tg_q8_load(a, qr, 64 * W);
     // 2. the weights and scales of every step
     uint4 wv[NL], sv[NL / 2];
     {
@@ -422,15 +261,7 @@ __global__ __launch_bounds__(64 * W) void k_tgemm(TgArgs a) {
     TI_ISSUE_FENCE();
 
     // 3. prologue: codes in B's byte order, scales, -8*sum(a) into LDS
-    if constexpr (MODE == TG_NORM) {
-        for (int p0 = 0; p0 < T; p0 += TP) {
-            if (p0 > 0) tg_norm_load<KU, TP>(a, p0, nr);
-            tg_norm_pass<KU, TP>(a, p0, nr, L);
-        }
-        if constexpr (KU < 8) tg_norm_finish(a, L, 256);
-    } else {
-        tg_q8_stage(a, qr, L, 64 * W);
-    }
+    tg_q8_stage(a, qr, L, 64 * W);
 
     // 4. the group loop
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -468,9 +299,13 @@ __global__ __launch_bounds__(64 * W) void k_tgemm(TgArgs a) {
         // (q8_group's arithmetic: scale = absmax/127, round-half-even, clamp 127)
         const int r = tid & 31;
         const int ch = blockIdx.x;
-        for (int tok = tid >> 5; tok < T; tok += 8) {
-            const float gv = L.part[((r >> 4) * 16 + tok) * 17 + (r & 15)];
-            const float uv = L.part[((2 + (r >> 4)) * 16 + tok) * 17 + (r & 15)];
+        for (int tok = tid >> 5; tok < T; tok += 2 * W) {
+            float gv = 0.0f, uv = 0.0f;
+#pragma unroll
+            for (int k = 0; k < KS; k++) {
+                gv += L.part[(((r >> 4) * KS + k) * 16 + tok) * 17 + (r & 15)];
+                uv += L.part[(((2 + (r >> 4)) * KS + k) * 16 + tok) * 17 + (r & 15)];
+            }
             const float v = silu_mul(gv, uv);
             const float mx = ti_max32_nonneg(fabsf(v));
             const float scale = mx / 127.0f;
@@ -498,10 +333,74 @@ __global__ __launch_bounds__(64 * W) void k_tgemm(TgArgs a) {
     }
 }
 
+// Per-token RMSNorm + quantQ8T of a [T][K] activation, one workgroup per token (the
+// rmsnorm + quantQ8T dispatches the projections of a T-token forward share): the sum of
+// squares in the reference's order (256 strided partials, 128..1 tree), then the
+// quantizer on contiguous KU-element runs (a 32-group = 32/KU lanes); codes [T][K/4] and
+// scales [T][K/32], bit-exact with rmsnorm + q8_group.
+template <int KU>
+__global__ __launch_bounds__(256) void k_tnorm_q8(const float* __restrict__ x, const uint16_t* __restrict__ nw, float eps,
+                                                  uint32_t* __restrict__ xq, float* __restrict__ xs) {
+    constexpr int K = 256 * KU;
+    __shared__ float red[256];
+    const int t = threadIdx.x;
+    const float* xr = x + (size_t)blockIdx.x * K;
+    float xsd[KU], xc[KU];
+    uint16_t wc[KU];
+#pragma unroll
+    for (int i = 0; i < KU; i++) {
+        xsd[i] = xr[t + 256 * i];
+        wc[i] = nw[KU * t + i];
+    }
+    if constexpr (KU % 4 == 0) {
+        const float4* x4 = reinterpret_cast<const float4*>(xr + KU * t);
+#pragma unroll
+        for (int i = 0; i < KU / 4; i++) {
+            const float4 v = x4[i];
+            xc[4 * i] = v.x; xc[4 * i + 1] = v.y; xc[4 * i + 2] = v.z; xc[4 * i + 3] = v.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < KU; i++) xc[i] = xr[KU * t + i];
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < KU; i++) {
+        const float sq = xsd[i] * xsd[i];
+        s = s + sq;
+    }
+    float m = ti_tree_sum_256(s, red) / (float)K;
+    m = m + eps;
+    const float inv_rms = 1.0f / sqrtf(m);
+    float v[KU], mx = 0.0f;
+#pragma unroll
+    for (int i = 0; i < KU; i++) {
+        const float p = xc[i] * inv_rms;
+        v[i] = p * ti_h2f(wc[i]);
+        mx = fmaxf(mx, fabsf(v[i]));
+    }
+    mx = group_max_contig<KU>(mx);
+    const float scale = mx / 127.0f;
+    const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
+    uint32_t wd[(KU + 3) / 4] = {};
+#pragma unroll
+    for (int i = 0; i < KU; i++) wd[i / 4] |= (uint32_t)(q8_code(v[i], inv) & 0xff) << (8 * (i % 4));
+    uint32_t* q = xq + (size_t)blockIdx.x * (K / 4);
+    if constexpr (KU >= 4) {
+#pragma unroll
+        for (int k = 0; k < KU / 4; k++) q[KU / 4 * t + k] = wd[k];
+    } else {
+        uint8_t* qb = reinterpret_cast<uint8_t*>(q);
+#pragma unroll
+        for (int i = 0; i < KU; i++) qb[KU * t + i] = (uint8_t)((wd[0] >> (8 * i)) & 0xff);
+    }
+    if (t % (32 / KU) == 0) xs[(size_t)blockIdx.x * (K / 32) + KU * t / 32] = scale;
+}
+
 // ---- host dispatch ------------------------------------------------------------------
-// (W, KS, NL) per K = 128*KS*NL: TG_Q8 runs 8-wave workgroups where K allows (all SIMDs
-// of the chip busy at N = 2048); TG_NORM runs 4 waves (its prologue is 256 threads).
-bool tg_split_q8(int G, int& W, int& KS, int& NL) {
+// (W, KS, NL) per K = 128*KS*NL: 8-wave workgroups where K allows (all SIMDs of the
+// chip busy at N = 2048)
+bool tg_split(int G, int& W, int& KS, int& NL) {
     switch (G) {
         case 8: W = 4; KS = 1; NL = 2; return true;
         case 16: W = 4; KS = 2; NL = 2; return true;
@@ -515,48 +414,55 @@ bool tg_split_q8(int G, int& W, int& KS, int& NL) {
     }
 }
 
-int tg_ku(int K) {   // TG_NORM prologue: K = 256*KU, KU in {1, 2, 4, 8, 16}
+int tg_ku(int K) {   // k_tnorm_q8: K = 256*KU, KU in {1, 2, 4, 8, 16}
     if (K % 256) return 0;
     const int ku = K / 256;
     return (ku == 1 || ku == 2 || ku == 4 || ku == 8 || ku == 16) ? ku : 0;
 }
 
-constexpr int tg_tp(int ku) { return ku >= 16 ? 4 : 8; }
-
-template <int MODE, bool GU, int W, int KS, int NL, int KU>
+template <bool GU, int W, int KS, int NL>
 int tg_go(ti_ctx* c, const TgArgs& a, unsigned grid, const char* name) {
-    constexpr int TP = MODE == TG_NORM ? tg_tp(KU) : 0;
-    const size_t lds = (size_t)tg_lds_words(a.T, a.K, W, TP) * 4;
+    const size_t lds = (size_t)tg_lds_words(a.T, a.K, W) * 4;
     static bool attr = false;
     if (!attr && lds > 65536) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_tgemm<MODE, GU, W, KS, NL, KU, TP>),
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_tgemm<GU, W, KS, NL>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         if (e != hipSuccess) return ti_hip_fail(e, "k_tgemm LDS attribute");
         attr = true;
     }
-    k_tgemm<MODE, GU, W, KS, NL, KU, TP><<<grid, 64 * W, lds, c->stream>>>(a);
+    k_tgemm<GU, W, KS, NL><<<grid, 64 * W, lds, c->stream>>>(a);
     TI_LAUNCHED(name);
     return TI_OK;
 }
 
 }  // namespace
 
-// Which T-token projections take the fused path: 2..16 tokens, K/32 in the split
-// table, and (TG_NORM) K = 256 * {1,2,4,8,16}; gate/up needs K <= 2048.
-bool ti_tgemm_ok(int T, int K, int norm, int gateup) {
+// Which T-token projections take these kernels: 2..16 tokens, K/32 in the split table.
+bool ti_tgemm_ok(int T, int K) {
     int W, KS, NL;
-    if (T < 2 || T > TG_TMAX || K % 32 || !tg_split_q8(K / 32, W, KS, NL)) return false;
-    if (norm && !tg_ku(K)) return false;
-    return !gateup || K <= 2048;
+    return T >= 2 && T <= TG_TMAX && K % 32 == 0 && tg_split(K / 32, W, KS, NL);
+}
+bool ti_tnorm_ok(int K) { return tg_ku(K) != 0; }
+bool ti_tgemm_gateup_ok(int T, int H) {
+    const int G = H / 32;
+    return ti_tgemm_ok(T, H) && (G == 8 || G == 16 || G == 32 || G == 64 || G == 128);
 }
 
-// q/k/v-style: y_s[t][:] = W_s rmsnorm(x[t]) for up to three segments sharing the
-// activation (TG_NORM), or y[t][:] (+)= W xq[t] on int8 input (TG_Q8, one segment).
-// Scales must be 16-byte aligned (K/32 groups of f16 per row, K % 256 == 0 keeps every
-// row aligned).
-int ti_tgemm_launch(ti_ctx* c, int norm, const float* x, const uint16_t* nw, float eps, const uint32_t* xq,
-                    const float* xs, int nseg, const uint32_t* const* packs, const uint16_t* const* scs,
-                    float* const* ys, const int* Ns, int T, int K, int acc) {
+// rmsnorm + quantQ8T of T tokens: xq [T][K/4], xs [T][K/32]; K = 256 * {1,2,4,8,16}
+int ti_tnorm_q8_launch(ti_ctx* c, const float* x, const uint16_t* nw, float eps, uint32_t* xq, float* xs, int T, int K) {
+    switch (tg_ku(K)) {
+#define TN(KU_) case KU_: k_tnorm_q8<KU_><<<T, 256, 0, c->stream>>>(x, nw, eps, xq, xs); TI_LAUNCHED("k_tnorm_q8"); return TI_OK;
+        TN(1) TN(2) TN(4) TN(8) TN(16)
+#undef TN
+    }
+    return ti_fail(TI_ERR_INVALID, "T-token norm: no kernel for K=%d", K);
+}
+
+// y_s[t][:] (+)= W_s a_t for up to three segments sharing the int8 activation
+// (xq [T][K/4], xs [T][K/32]). Scales must be 16-byte aligned (K % 256 == 0 keeps every
+// row aligned); segments before the last must have a multiple of 16 rows.
+int ti_tgemm_launch(ti_ctx* c, const uint32_t* xq, const float* xs, int nseg, const uint32_t* const* packs,
+                    const uint16_t* const* scs, float* const* ys, const int* Ns, int T, int K, int acc) {
     TgArgs a = {};
     a.nseg = nseg;
     a.N = 0;
@@ -570,42 +476,24 @@ int ti_tgemm_launch(ti_ctx* c, int norm, const float* x, const uint16_t* nw, flo
     a.T = T;
     a.acc = acc;
     a.S = K / 4 + 2;
-    a.x = x;
-    a.nw = nw;
-    a.eps = eps;
     a.xq = xq;
     a.xs = xs;
-    if (!ti_tgemm_ok(T, K, norm, 0)) return ti_fail(TI_ERR_INVALID, "T-token GEMM: unsupported T=%d K=%d", T, K);
+    if (!ti_tgemm_ok(T, K)) return ti_fail(TI_ERR_INVALID, "T-token GEMM: unsupported T=%d K=%d", T, K);
     const int nb = (a.N + 15) / 16;
-    if (norm) {
-        // 4 waves: KS = K/512 waves per block (K/32 = 4*KS*NL with NL = 2 .. 8)
-        const unsigned g1 = (unsigned)((nb + 3) / 4), g2 = (unsigned)((nb + 1) / 2), g4 = (unsigned)nb;
-        switch (tg_ku(K)) {
-            case 1: return tg_go<TG_NORM, false, 4, 1, 2, 1>(c, a, g1, "k_tgemm_norm");
-            case 2: return tg_go<TG_NORM, false, 4, 2, 2, 2>(c, a, g2, "k_tgemm_norm");
-            case 4: return tg_go<TG_NORM, false, 4, 4, 2, 4>(c, a, g4, "k_tgemm_norm");
-            case 8: return tg_go<TG_NORM, false, 4, 4, 4, 8>(c, a, g4, "k_tgemm_norm");
-            case 16: return tg_go<TG_NORM, false, 4, 4, 8, 16>(c, a, g4, "k_tgemm_norm");
-        }
-    } else {
-        switch (K / 32) {
-#define TGQ(G_, W_, KS_, NL_)                                                                        \
-    case G_:                                                                                         \
-        return tg_go<TG_Q8, false, W_, KS_, NL_, 0>(c, a, (unsigned)((nb + W_ / KS_ - 1) / (W_ / KS_)), \
-                                                    "k_tgemm_q8");
-            TGQ(8, 4, 1, 2) TGQ(16, 4, 2, 2) TGQ(32, 8, 4, 2) TGQ(64, 8, 8, 2) TGQ(96, 8, 4, 6) TGQ(128, 8, 8, 4)
-            TGQ(192, 8, 8, 6) TGQ(256, 8, 8, 8)
+    switch (K / 32) {
+#define TGQ(G_, W_, KS_, NL_) \
+    case G_: return tg_go<false, W_, KS_, NL_>(c, a, (unsigned)((nb + W_ / KS_ - 1) / (W_ / KS_)), "k_tgemm");
+        TGQ(8, 4, 1, 2) TGQ(16, 4, 2, 2) TGQ(32, 8, 4, 2) TGQ(64, 8, 8, 2) TGQ(96, 8, 4, 6) TGQ(128, 8, 8, 4)
+        TGQ(192, 8, 8, 6) TGQ(256, 8, 8, 8)
 #undef TGQ
-        }
     }
     return ti_fail(TI_ERR_INVALID, "T-token GEMM: no kernel for K=%d", K);
 }
 
-// gate/up: swq[t] = quantQ8(silu(Wg rmsnorm(x[t])) * (Wu rmsnorm(x[t]))), scales sws[t]
-int ti_tgemm_gateup_launch(ti_ctx* c, const float* x, const uint16_t* nw, float eps, const uint32_t* gpack,
-                           const uint16_t* gsc, const uint32_t* upack, const uint16_t* usc, int I, int H, int T,
-                           uint32_t* swq, float* sws) {
-    if (!ti_tgemm_ok(T, H, 1, 1) || I % 32) return ti_fail(TI_ERR_INVALID, "T-token gate/up: unsupported T=%d H=%d I=%d", T, H, I);
+// gate/up on int8 input (the codes of ti_tnorm_q8): swq[t] = quantQ8(silu(Wg a_t) * (Wu a_t))
+int ti_tgemm_gateup_launch(ti_ctx* c, const uint32_t* xq, const float* xs, const uint32_t* gpack, const uint16_t* gsc,
+                           const uint32_t* upack, const uint16_t* usc, int I, int H, int T, uint32_t* swq, float* sws) {
+    if (!ti_tgemm_gateup_ok(T, H) || I % 32) return ti_fail(TI_ERR_INVALID, "T-token gate/up: unsupported T=%d H=%d I=%d", T, H, I);
     if (reinterpret_cast<uintptr_t>(gsc) % 16 || reinterpret_cast<uintptr_t>(usc) % 16)
         return ti_fail(TI_ERR_INVALID, "T-token gate/up: scales must be 16-byte aligned");
     TgArgs a = {};
@@ -615,19 +503,28 @@ int ti_tgemm_gateup_launch(ti_ctx* c, const float* x, const uint16_t* nw, float 
     a.K = H;
     a.T = T;
     a.S = H / 4 + 2;
-    a.x = x;
-    a.nw = nw;
-    a.eps = eps;
+    a.xq = xq;
+    a.xs = xs;
     a.upack = reinterpret_cast<const uint4*>(upack);
     a.usc = reinterpret_cast<const uint4*>(usc);
     a.yq = swq;
     a.ys = sws;
     const unsigned grid = (unsigned)(I / 32);
-    switch (tg_ku(H)) {
-        case 1: return tg_go<TG_NORM, true, 4, 1, 2, 1>(c, a, grid, "k_tgemm_gateup");
-        case 2: return tg_go<TG_NORM, true, 4, 1, 4, 2>(c, a, grid, "k_tgemm_gateup");
-        case 4: return tg_go<TG_NORM, true, 4, 1, 8, 4>(c, a, grid, "k_tgemm_gateup");
-        case 8: return tg_go<TG_NORM, true, 4, 1, 16, 8>(c, a, grid, "k_tgemm_gateup");
+    switch (H / 32) {   // 8 waves: 4 blocks x KS = 2 (K/32 = 8 * NL); K = 256: 4 waves
+        case 8: return tg_go<true, 4, 1, 2>(c, a, grid, "k_tgemm_gateup");
+        case 16: return tg_go<true, 8, 2, 2>(c, a, grid, "k_tgemm_gateup");
+        case 32: return tg_go<true, 8, 2, 4>(c, a, grid, "k_tgemm_gateup");
+        case 64: return tg_go<true, 8, 2, 8>(c, a, grid, "k_tgemm_gateup");
+        case 128: return tg_go<true, 8, 2, 16>(c, a, grid, "k_tgemm_gateup");
     }
     return ti_fail(TI_ERR_INVALID, "T-token gate/up: no kernel for H=%d", H);
+}
+
+extern "C" int ti_rmsnorm_q8_t(ti_ctx* c, const float* x, const uint16_t* w, uint32_t* xq, float* xs, int T, int H,
+                               float eps) {
+    TI_CHECK_CTX(c);
+    TI_REQUIRE(x && w && xq && xs, "ti_rmsnorm_q8_t: null buffer");
+    TI_REQUIRE(T > 0 && T < (1 << 20) && tg_ku(H), "ti_rmsnorm_q8_t: need T > 0 and H = 256 * {1,2,4,8,16} (T=%d H=%d)", T, H);
+    TI_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0, "ti_rmsnorm_q8_t: x must be 16-byte aligned");
+    return ti_tnorm_q8_launch(c, x, w, eps, xq, xs, T, H);
 }

@@ -34,14 +34,16 @@ int ti_fused_gateup_launch(ti_ctx*, const float*, const uint16_t*, float, const 
 int ti_fused_lmhead_launch(ti_ctx*, const float*, const uint16_t*, float, const uint32_t*, const uint16_t*, float*, int,
                            int, uint32_t*, int*, int, int, const float*, float*, int);
 int ti_fused_kmax(int lm);
-bool ti_tgemm_ok(int T, int K, int norm, int gateup);
-int ti_tgemm_launch(ti_ctx* c, int norm, const float* x, const uint16_t* nw, float eps, const uint32_t* xq,
-                    const float* xs, int nseg, const uint32_t* const* packs, const uint16_t* const* scs,
-                    float* const* ys, const int* Ns, int T, int K, int acc);
-int ti_tgemm_gateup_launch(ti_ctx* c, const float* x, const uint16_t* nw, float eps, const uint32_t* gpack,
-                           const uint16_t* gsc, const uint32_t* upack, const uint16_t* usc, int I, int H, int T,
-                           uint32_t* swq, float* sws);
+bool ti_tgemm_ok(int T, int K);
+bool ti_tnorm_ok(int K);
+bool ti_tgemm_gateup_ok(int T, int H);
+int ti_tnorm_q8_launch(ti_ctx* c, const float* x, const uint16_t* nw, float eps, uint32_t* xq, float* xs, int T, int K);
+int ti_tgemm_launch(ti_ctx* c, const uint32_t* xq, const float* xs, int nseg, const uint32_t* const* packs,
+                    const uint16_t* const* scs, float* const* ys, const int* Ns, int T, int K, int acc);
+int ti_tgemm_gateup_launch(ti_ctx* c, const uint32_t* xq, const float* xs, const uint32_t* gpack, const uint16_t* gsc,
+                           const uint32_t* upack, const uint16_t* usc, int I, int H, int T, uint32_t* swq, float* sws);
 bool ti_tattn_ok(int T, int nHq, int nKv, int hd);
+
 int ti_tattn_launch(ti_ctx* c, const float* q, const float* k, const float* v, const uint16_t* qw, const uint16_t* kw,
                     const float* rope, uint32_t* kq, float* ks, uint32_t* vq, float* vs, int S0, int T, int nHq, int nKv,
                     int hd, float eps, uint32_t* oq, float* os);
@@ -438,9 +440,12 @@ extern "C" int ti_qwen3_forward(ti_ctx* c, ti_qwen3* m, const int32_t* ids, int 
     if (ids) RC(ti_buf_write(c, m->hist, (size_t)pos * 4, ids, (size_t)T * 4));   // else already in the history
     k_embed<<<(unsigned)(((long)T * H + 255) / 256), 256, 0, c->stream>>>(m->hist, m->embed, m->x, T, H, pos, nullptr, C.vocab);
     TI_LAUNCHED("k_embed");
-    // 2..16 tokens: five launches per layer around the attention, the projections on
-    // the matrix cores with their norm / quantizer / SwiGLU fused (k_tgemm.hip)
-    const bool fused = ti_tgemm_ok(T, H, 1, 1) && ti_tgemm_ok(T, nq, 0, 0) && ti_tgemm_ok(T, I, 0, 0) &&
+    // 2..16 tokens: per layer [rmsnorm + quantQ8T] [q/k/v] [attention] [split merge +
+    // quantQ8T] [o_proj + residual] [rmsnorm + quantQ8T] [gate/up + SiLU + quantQ8T]
+    // [down + residual], the projections on the matrix cores (k_tgemm.hip, k_tattn.hip);
+    // the per-token norm codes live in the context's activation scratch, the attention
+    // and SwiGLU codes in the model's
+    const bool fused = ti_tnorm_ok(H) && ti_tgemm_gateup_ok(T, H) && ti_tgemm_ok(T, nq) && ti_tgemm_ok(T, I) &&
                        nq % 16 == 0 && nkv % 16 == 0 && I % 32 == 0;
     const bool fused_attn = ti_tattn_ok(T, nHq, nKv, hd);
     for (int l = 0; l < C.layers; l++) {
@@ -450,7 +455,8 @@ extern "C" int ti_qwen3_forward(ti_ctx* c, ti_qwen3* m, const int32_t* ids, int 
             const uint16_t* scs[3] = {y.q.sc, y.k.sc, y.v.sc};
             float* ys[3] = {m->q, m->k, m->v};
             const int Ns[3] = {nq, nkv, nkv};
-            RC(ti_tgemm_launch(c, 1, m->x, y.in_norm, C.rms_eps, nullptr, nullptr, 3, packs, scs, ys, Ns, T, H, 0));
+            RC(ti_tnorm_q8_launch(c, m->x, y.in_norm, C.rms_eps, c->act_q, c->act_s, T, H));
+            RC(ti_tgemm_launch(c, c->act_q, c->act_s, 3, packs, scs, ys, Ns, T, H, 0));
         } else {
             RC(ti_rmsnorm(c, m->x, y.in_norm, m->normed, T, H, C.rms_eps));
             RC(ti_linear_q4(c, m->normed, y.q.pack, y.q.sc, m->q, T, nq, H, 0));
@@ -468,11 +474,11 @@ extern "C" int ti_qwen3_forward(ti_ctx* c, ti_qwen3* m, const int32_t* ids, int 
         }
         if (fused) {
             if (!fused_attn) RC(ti_quant_act_q8_async(c, m->attn, m->xq, m->xs, nullptr, T * (nq / 32)));
-            RC(ti_tgemm_launch(c, 0, nullptr, nullptr, 0.0f, m->xq, m->xs, 1, &y.o.pack, &y.o.sc, &m->x, &H, T, nq, 1));
-            RC(ti_tgemm_gateup_launch(c, m->x, y.post_norm, C.rms_eps, y.gate.pack, y.gate.sc, y.up.pack, y.up.sc, I, H,
-                                      T, m->xq, m->xs));
-            RC(ti_tgemm_launch(c, 0, nullptr, nullptr, 0.0f, m->xq, m->xs, 1, &y.down.pack, &y.down.sc, &m->x, &H, T, I,
-                               1));
+            RC(ti_tgemm_launch(c, m->xq, m->xs, 1, &y.o.pack, &y.o.sc, &m->x, &H, T, nq, 1));
+            RC(ti_tnorm_q8_launch(c, m->x, y.post_norm, C.rms_eps, c->act_q, c->act_s, T, H));
+            RC(ti_tgemm_gateup_launch(c, c->act_q, c->act_s, y.gate.pack, y.gate.sc, y.up.pack, y.up.sc, I, H, T, m->xq,
+                                      m->xs));
+            RC(ti_tgemm_launch(c, m->xq, m->xs, 1, &y.down.pack, &y.down.sc, &m->x, &H, T, I, 1));
             continue;
         }
         RC(ti_linear_q4(c, m->attn, y.o.pack, y.o.sc, m->x, T, H, nq, 1));

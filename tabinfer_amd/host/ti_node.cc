@@ -878,6 +878,7 @@ napi_value module_init(napi_env env, napi_value exports) {
         ENTRY("quant_act_q8", ti_quant_act_q8),
         ENTRY("quant_act_q8_t", ti_quant_act_q8_t),
         ENTRY("rmsnorm_q8", ti_rmsnorm_q8),
+        ENTRY("rmsnorm_q8_t", ti_rmsnorm_q8_t),
         ENTRY("rmsnorm", ti_rmsnorm),
         ENTRY("gemv_q4_q8", ti_gemv_q4_q8),
         ENTRY("gemv_q4_f32", ti_gemv_q4_f32),

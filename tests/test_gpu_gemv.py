@@ -92,6 +92,26 @@ def test_rmsnorm_q8_bit_exact(ctx, orc, H):
     assert np.array_equal(ctx.download(dy, np.float32, y.size), y)
 
 
+@pytest.mark.parametrize("T,H", [(1, 256), (5, 512), (8, 1024), (8, 2048), (16, 2048), (3, 4096)])
+def test_rmsnorm_q8_t_bit_exact(ctx, orc, T, H):
+    """rmsnorm + QUANTQ8T of T rows (the T-token forward's norm kernel): every code and
+    scale equals the oracle's rmsnorm_q8 of that row."""
+    rng = np.random.default_rng(T * 7 + H)
+    X = (rng.standard_normal(T * H) * 3).astype(np.float32)
+    X[:H // 2] *= 1e-3                                  # a row with small values in part
+    w = (1.0 + 0.1 * rng.standard_normal(H)).astype(np.float16).view(np.uint16)
+    dX, dw = ctx.upload(X), ctx.upload(w)
+    dq, ds = ctx.zeros(T * H), ctx.zeros(T * H // 8)
+    ctx.call("ti_rmsnorm_q8_t", dX, dw, dq, ds, T, H, np.float32(1e-6))
+    gq = ctx.download(dq, np.uint32, T * H // 4).reshape(T, -1)
+    gs = ctx.download(ds, np.float32, T * H // 32).reshape(T, -1)
+    for t in range(T):
+        xq, xs, _ = orc.rmsnorm_q8(X[t * H:(t + 1) * H], w, 1e-6)
+        assert np.array_equal(gq[t], xq) and np.array_equal(gs[t], xs), t
+    with pytest.raises(abi.TIError):
+        ctx.call("ti_rmsnorm_q8_t", dX, dw, dq, ds, T, 320, np.float32(1e-6))
+
+
 def _weights(ctx, orc, rng, N, K):
     w = bf16_normal(rng, N * K)
     pack, sc = orc.quant_int4_bf16(w, N, K)
