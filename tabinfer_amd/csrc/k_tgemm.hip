@@ -130,15 +130,17 @@ template <int UQ, int SQ>
 __device__ __forceinline__ void tg_q8_load(const TgArgs& a, Q8Regs<UQ, SQ>& r, int nthreads) {
     const int units = a.T * (a.K / 16), ns = a.T * (a.K / 32);
     const uint4* src = reinterpret_cast<const uint4*>(a.xq);
+    // UQ / SQ cover 16 tokens; rounds wholly past T are skipped (a workgroup-uniform
+    // test, so no load is issued for them), the partial one reads clamped indices
 #pragma unroll
     for (int k = 0; k < UQ; k++) {
         const int u = threadIdx.x + nthreads * k;
-        r.c[k] = src[u < units ? u : units - 1];
+        if (nthreads * k < units) r.c[k] = src[u < units ? u : units - 1];
     }
 #pragma unroll
     for (int k = 0; k < SQ; k++) {
         const int e = threadIdx.x + nthreads * k;
-        r.s[k] = a.xs[e < ns ? e : ns - 1];
+        if (nthreads * k < ns) r.s[k] = a.xs[e < ns ? e : ns - 1];
     }
 }
 
@@ -147,6 +149,7 @@ __device__ __forceinline__ void tg_q8_stage(const TgArgs& a, const Q8Regs<UQ, SQ
     const int G = a.K / 32, upr = a.K / 16, units = a.T * upr, ns = a.T * G, S = a.S;
 #pragma unroll
     for (int k = 0; k < UQ; k++) {
+        if (nthreads * k >= units) break;                 // workgroup-uniform
         const int u = threadIdx.x + nthreads * k;
         const int t = u / upr, c = u % upr, g = c >> 1, h = c & 1;
         const uint4 w = r.c[k];
@@ -162,7 +165,7 @@ __device__ __forceinline__ void tg_q8_stage(const TgArgs& a, const Q8Regs<UQ, SQ
 #pragma unroll
     for (int k = 0; k < SQ; k++) {
         const int e = threadIdx.x + nthreads * k;
-        if (e < ns) L.as[(e % G) * 16 + e / G] = r.s[k];
+        if (nthreads * k < ns && e < ns) L.as[(e % G) * 16 + e / G] = r.s[k];
     }
     __syncthreads();
 }
