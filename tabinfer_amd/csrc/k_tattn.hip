@@ -67,8 +67,9 @@ struct TAttnArgs {
 // byte is the f16 1024 + code + 128, and one packed f16 subtraction removes the 1152
 __device__ __forceinline__ void i8x4_to_h2x2(uint32_t w, h2& a, h2& b) {
     const uint32_t u = w ^ 0x80808080u;
-    const uint32_t p0 = (u & 0xffu) | ((u & 0xff00u) << 8) | 0x64006400u;
-    const uint32_t p1 = ((u >> 16) & 0xffu) | ((u >> 8) & 0xff0000u) | 0x64006400u;
+    // v_perm_b32: selector bytes 0-3 pick the second operand's bytes, 4-7 the first's
+    const uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);   // [u0, 64, u1, 64]
+    const uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);   // [u2, 64, u3, 64]
     const h2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
     a = __builtin_bit_cast(h2, p0) - bias;
     b = __builtin_bit_cast(h2, p1) - bias;
@@ -138,13 +139,13 @@ __global__ __launch_bounds__(64 * TA_W) void k_attn_tq8(TAttnArgs a) {
 #pragma unroll
         for (int p = 0; p < 4; p++) {
             int key = k0 + (lane >> 3) + 8 * p;
-            key = key < S0 ? key : S0 - 1;
+            key = key < S0 ? key : (S0 > 0 ? S0 - 1 : 0);
             const size_t off = ((size_t)key * a.nKv + hk) * HD + 16 * (lane & 7);
             kr[p] = ti_ld_nt(reinterpret_cast<const uint4*>(a.kq + off));
             vr[p] = ti_ld_nt(reinterpret_cast<const uint4*>(a.vq + off));
         }
         int key = k0 + (lane >> 1);
-        key = key < S0 ? key : S0 - 1;
+        key = key < S0 ? key : (S0 > 0 ? S0 - 1 : 0);
         const size_t so = ((size_t)key * a.nKv + hk) * NG + 2 * (lane & 1);
         ksr = *reinterpret_cast<const float2*>(a.ks + so);
         vsr = *reinterpret_cast<const float2*>(a.vs + so);
@@ -170,7 +171,8 @@ __global__ __launch_bounds__(64 * TA_W) void k_attn_tq8(TAttnArgs a) {
         qc[i][0] = cs[lane];
         qc[i][1] = cs[lane + 64];
     }
-    if (tail_wg) {
+    {   // unconditional (clamped) loads: straight-line code lets the prologue wait for
+        // exactly its own loads, not the key block's issued after them
 #pragma unroll
         for (int i = 0; i < KPW; i++) {
             const int jb = wave + TA_W * i;               // job: K rows 0..T-1, then V rows
@@ -187,7 +189,7 @@ __global__ __launch_bounds__(64 * TA_W) void k_attn_tq8(TAttnArgs a) {
     }
     // the wave's first block is in flight during the prologue (its loads are issued after
     // the prologue's, so waiting for those does not wait for these)
-    if (gw < nb) load_blk(gw * TA_BLK);
+    load_blk((gw < nb ? gw : 0) * TA_BLK);              // a dummy block (unused) past nb
     TI_ISSUE_FENCE();
     // ---- q rows: RMSNorm + RoPE, f16 hi + lo into LDS (rows past R are zero)
 #pragma unroll

@@ -232,3 +232,55 @@ def test_batched_forward_t_sizes(ctx, T):
     finally:
         a.close()
         b.close()
+
+def test_qwen3_06b_geometry_batch8_over_1k_prefix(ctx, orc):
+    """The batch-8 forward at the Qwen3-0.6B geometry (hidden 1024, intermediate 3072,
+    16/8 heads of 128: the K = 1024 / 2048 / 3072 projection kernels and the KU = 4 norm
+    kernel) over a seeded 1k prefix (a partial last key block), against 8 reference steps.
+    One layer: with two, one int8 activation code of layer 1 that flips at a rounding
+    boundary (f32 sums in a different order than the oracle's f64) moves the logits by a
+    few 1e-3 on either path, batch-8 or single-token, depending on the seed."""
+    cfg = dict(layers=1, hidden=1024, intermediate=3072, n_heads=16, n_kv_heads=8, head_dim=128, vocab=151936,
+               rope_theta=1e6, rms_eps=1e-6, max_ctx=1100, max_tokens=8)
+    W = Q.make_weights(cfg, 7)
+    m = abi.Qwen3(ctx, **cfg)
+    try:
+        Q.load_into(m, W)
+        ref = Q.RefDecoder(cfg, W, cfg["max_ctx"])
+        P = 1000
+        _seed_prefix(ctx, orc, m, ref, cfg, P, 11)
+        ids = np.array([1, 151000, 42, 4242, 7, 99999, 3, 12345], np.int32)
+        m.forward(ids, P)
+        for i, t in enumerate(ids):
+            rl, rt = ref.step(int(t), P + i)
+        assert rel_err(_logits(ctx, m, cfg["vocab"]), rl) < TOL
+        if margin_ok(rl):
+            assert int(m.read_tokens(P + 8, 1)[0]) == rt
+    finally:
+        m.close()
+
+def test_batched_forward_g1_16_tokens(ctx):
+    """T = 16 tokens with one query head per KV head (G = 1: 16 query rows per KV head, the
+    attention kernel's full row tile, causal over the 16 new keys) against 16 single-token
+    forwards."""
+    cfg = dict(layers=2, hidden=256, intermediate=512, n_heads=2, n_kv_heads=2, head_dim=128, vocab=1000,
+               rope_theta=1e6, rms_eps=1e-6, max_ctx=128, max_tokens=16)
+    W = Q.make_weights(cfg, 8)
+    a, b = abi.Qwen3(ctx, **cfg), abi.Qwen3(ctx, **cfg)
+    try:
+        Q.load_into(a, W)
+        Q.load_into(b, W)
+        pre = (np.arange(40, dtype=np.int32) * 37 + 5) % cfg["vocab"]
+        ids = (np.arange(16, dtype=np.int32) * 53 + 11) % cfg["vocab"]
+        a.forward(pre[:16], 0)
+        a.forward(pre[16:32], 16)
+        a.forward(pre[32:], 32)
+        a.forward(ids, 40)
+        for p in range(40):
+            b.forward(pre[p:p + 1], p)
+        for p in range(16):
+            b.forward(ids[p:p + 1], 40 + p)
+        assert rel_err(_logits(ctx, a, cfg["vocab"]), _logits(ctx, b, cfg["vocab"])) < TOL
+    finally:
+        a.close()
+        b.close()
