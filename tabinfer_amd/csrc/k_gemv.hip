@@ -459,9 +459,6 @@ int ti_gemm_q4_q8_launch(ti_ctx* c, const uint32_t* xq, const float* xs, const u
                          float* y, int T, int N, int K, int acc);
 int ti_fused_linear_launch(ti_ctx*, const float*, const uint32_t*, const uint16_t*, float*, int, int, int);
 int ti_fused_kmax(int lm);
-bool ti_tgemm_ok(int T, int K);
-int ti_tgemm_launch(ti_ctx* c, const uint32_t* xq, const float* xs, int nseg, const uint32_t* const* packs,
-                    const uint16_t* const* scs, float* const* ys, const int* Ns, int T, int K, int acc);
 
 extern "C" int ti_linear_q4(ti_ctx* c, const float* x, const uint32_t* pack, const uint16_t* scales, float* y, int T, int N,
                             int K, int acc) {
@@ -476,6 +473,7 @@ extern "C" int ti_linear_q4(ti_ctx* c, const float* x, const uint32_t* pack, con
     if (rc) return rc;
     if (T == 1) return ti_gemv_q4_q8_launch(c, c->act_q, c->act_s, pack, scales, y, N, K, acc);
     if (ti_tgemm_ok(T, K) && reinterpret_cast<uintptr_t>(scales) % 16 == 0)
-        return ti_tgemm_launch(c, c->act_q, c->act_s, 1, &pack, &scales, &y, &N, T, K, acc);
+        return ti_tgemm_launch(c, TgIn{c->act_q, c->act_s, nullptr, nullptr, 0.0f, nullptr}, 1, &pack, &scales, &y, &N, T, K,
+                               acc, nullptr);
     return ti_gemm_q4_q8_launch(c, c->act_q, c->act_s, pack, scales, y, T, N, K, acc);
 }

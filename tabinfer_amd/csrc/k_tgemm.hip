@@ -50,6 +50,7 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int TG_TMAX = 16;
+enum { TG_Q8 = 0, TG_NORM = 1 };
 
 struct TgSeg {
     const uint4* pack;
@@ -72,13 +73,24 @@ struct TgArgs {
     const uint4* usc;
     uint32_t* yq;        // gate/up: swi codes [T][N/4]
     float* ys;           // gate/up: swi scales [T][N/32]
+    // TG_NORM input: the f32 activation, its norm weight and its RMSNorm partial sums
+    // ([T][256]: partial t = sum over i of x[t + 256 i]^2, the reference's order)
+    const float* x;
+    const uint16_t* nw;
+    float eps;
+    const float* pin;
+    // PART epilogue: the output's partial sums ([T][256]) for the next projection's norm;
+    // block b owns output rows t + 256 i for 16/pku consecutive t and every i < pku
+    float* pout;
+    int pku;
 };
 
 // LDS (dynamic), in words: codes [T][S] (rounded to 4), scales [G][16] f32, -8*sum(a)
-// [G][16] i32, partials [W][16][17] f32
+// [G][16] i32, partials [W][16][17] f32, per-token 1/rms [16], the residual outputs of the
+// workgroup's xnblk = W/KS blocks [xnblk][16][16] (PART; else xnblk = 0)
 __host__ __device__ constexpr int tg_codes_words(int T, int S) { return (T * S + 3) & ~3; }
-__host__ __device__ constexpr int tg_lds_words(int T, int K, int W) {
-    return tg_codes_words(T, K / 4 + 2) + 2 * (K / 32) * 16 + W * 16 * 17;
+__host__ __device__ constexpr int tg_lds_words(int T, int K, int W, int xnblk) {
+    return tg_codes_words(T, K / 4 + 2) + 2 * (K / 32) * 16 + W * 16 * 17 + 16 + xnblk * 256;
 }
 
 struct TgLds {
@@ -86,14 +98,18 @@ struct TgLds {
     float* as;
     int* corr;
     float* part;
+    float* inv;
+    float* xn;
 };
-__device__ __forceinline__ TgLds tg_carve(uint32_t* base, int T, int K) {
+__device__ __forceinline__ TgLds tg_carve(uint32_t* base, int T, int K, int W) {
     const int G = K / 32;
     TgLds L;
     L.aq = base;
     L.as = reinterpret_cast<float*>(base + tg_codes_words(T, K / 4 + 2));
     L.corr = reinterpret_cast<int*>(L.as + G * 16);
     L.part = reinterpret_cast<float*>(L.corr + G * 16);
+    L.inv = L.part + W * 16 * 17;
+    L.xn = L.inv + 16;
     return L;
 }
 
@@ -170,6 +186,112 @@ __device__ __forceinline__ void tg_q8_stage(const TgArgs& a, const Q8Regs<UQ, SQ
     __syncthreads();
 }
 
+// ---- RMSNorm prologue (TG_NORM) ---------------------------------------------------
+// The f32 activation x [T][K] (K = 256*KU) with its partial sums from the producing
+// projection's epilogue. Each wave: the 1/rms of tokens wave, wave + W, ... from the 256
+// partials (the reference's 128..1 tree, as ti_tree_sum_256 adds them), then the quantQ8T
+// codes of its own K/W slice of every token (8 consecutive elements per lane, a 32-group
+// = 4 lanes), in B's byte order with scales and -8*sum(a): the same codes as rmsnorm +
+// q8_group. RX = rounds of 64/(K/(8W)) tokens a lane covers.
+template <int RX>
+struct NormRegs {
+    float4 x[RX][2];
+    uint4 w;
+    float pt[(TG_TMAX + 3) / 4][4];
+};
+
+// Issue order: partial sums (needed first), norm weight, activation; rounds past T are not
+// issued (workgroup-uniform tests: a later unconditional load still lets the compiler
+// wait for these by count).
+template <int RX>
+__device__ __forceinline__ void tg_norm_load(const TgArgs& a, NormRegs<RX>& r, int W) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, K = a.K, T = a.T;
+    const int lpt = K / (8 * W), tpr = 64 / lpt;
+    const int e0 = wave * (K / W) + 8 * (lane % lpt);
+#pragma unroll
+    for (int k = 0; k < (TG_TMAX + 3) / 4; k++) {
+        const int tok = min(wave + W * k, T - 1);
+        if (W * k < T) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) r.pt[k][i] = a.pin[(size_t)tok * 256 + lane + 64 * i];
+        }
+    }
+    r.w = *reinterpret_cast<const uint4*>(a.nw + e0);
+#pragma unroll
+    for (int q = 0; q < RX; q++) {
+        if (q * tpr < T) {
+            const int tok = min(q * tpr + lane / lpt, T - 1);
+            const float4* xp = reinterpret_cast<const float4*>(a.x + (size_t)tok * K + e0);
+            r.x[q][0] = xp[0];
+            r.x[q][1] = xp[1];
+        }
+    }
+}
+
+template <int RX>
+__device__ __forceinline__ void tg_norm_stage(const TgArgs& a, const NormRegs<RX>& r, const TgLds& L, int W) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, K = a.K, T = a.T, S = a.S;
+#pragma unroll
+    for (int k = 0; k < (TG_TMAX + 3) / 4; k++) {
+        const int tok = wave + W * k;
+        if (W * k < T) {
+            const float x0 = r.pt[k][0] + r.pt[k][2];    // partials l + l+128
+            const float x1 = r.pt[k][1] + r.pt[k][3];    // partials l+64 + l+192
+            float v = x0 + x1;
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) v = v + ti_xor(v, o);
+            float mm = v / (float)K;
+            mm = mm + a.eps;
+            if (lane == 0 && tok < T) L.inv[tok] = 1.0f / sqrtf(mm);
+        }
+    }
+    __syncthreads();
+    const int lpt = K / (8 * W), tpr = 64 / lpt;
+    const int e0 = wave * (K / W) + 8 * (lane % lpt);
+    const uint32_t ww[4] = {r.w.x, r.w.y, r.w.z, r.w.w};
+#pragma unroll
+    for (int q = 0; q < RX; q++) {
+        const int tok = q * tpr + lane / lpt;
+        if (q * tpr >= T) break;                         // wave-uniform
+        const float inv_rms = L.inv[tok < T ? tok : 0];
+        const float xv[8] = {r.x[q][0].x, r.x[q][0].y, r.x[q][0].z, r.x[q][0].w,
+                             r.x[q][1].x, r.x[q][1].y, r.x[q][1].z, r.x[q][1].w};
+        float v[8], mx = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float pp = xv[i] * inv_rms;
+            v[i] = pp * ti_h2f((uint16_t)((ww[i / 2] >> (16 * (i & 1))) & 0xffff));
+            mx = fmaxf(mx, fabsf(v[i]));
+        }
+        mx = group_max_contig<8>(mx);
+        const float scale = mx / 127.0f;
+        const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
+        int qc[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) qc[i] = q8_code(v[i], inv);
+        uint32_t e = 0, o = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            e |= (uint32_t)(qc[2 * i] & 0xff) << (8 * i);
+            o |= (uint32_t)(qc[2 * i + 1] & 0xff) << (8 * i);
+        }
+        int sum = byte_sum(o, byte_sum(e, 0));
+        sum += ti_xor(sum, 1);
+        sum += ti_xor(sum, 2);
+        if (tok < T) {
+            *reinterpret_cast<uint2*>(L.aq + tok * S + e0 / 4) = make_uint2(e, o);
+            if ((lane & 3) == 0) {
+                L.as[(e0 / 32) * 16 + tok] = scale;
+                L.corr[(e0 / 32) * 16 + tok] = -8 * sum;
+            }
+        }
+    }
+    __syncthreads();
+}
+
+// rounds of the norm prologue: a lane covers 64 / (K / (8W)) tokens per round, K = 128 KS NL
+constexpr int tg_rx(int W, int KS, int NL) { return (TG_TMAX * 16 * KS * NL / W + 63) / 64 > 0 ? (TG_TMAX * 16 * KS * NL / W + 63) / 64 : 1; }
+
 // Segment of a 16-row block: selects on wave-uniform values (pointers stay scalar).
 struct TgBlk {
     const uint4* pack;
@@ -195,14 +317,17 @@ constexpr int tg_sq(int W, int KS, int NL) { return (NL * KS + W - 1) / W; }
 
 // W waves per workgroup, KS waves per 16-row block, each on NL steps of 4 groups
 // (K = 128*KS*NL). GU: gate/up epilogue (four blocks per workgroup: gate rows +0/+16 of
-// the workgroup's 32-row chunk, then up rows +0/+16).
-template <bool GU, int W, int KS, int NL>
+// the workgroup's 32-row chunk, then up rows +0/+16). IN: TG_Q8 codes or TG_NORM
+// (RMSNorm + quantQ8T in the prologue). PART: residual epilogue that also writes the
+// output's RMSNorm partial sums (block b owns rows t + 256 i).
+template <bool GU, int W, int KS, int NL, int IN, bool PART>
 __global__ __launch_bounds__(64 * W) void k_tgemm(TgArgs a) {
     static_assert(!GU || W / KS == 4, "gate/up: four 16-row blocks per workgroup");
+    static_assert(!(GU && PART), "the partial sums come from residual projections");
     static_assert(NL % 2 == 0, "scales are loaded 8 groups at a time");
     extern __shared__ __align__(16) uint32_t s_dyn[];
     const int T = a.T, G = a.K / 32, S = a.S;
-    const TgLds L = tg_carve(s_dyn, T, a.K);
+    const TgLds L = tg_carve(s_dyn, T, a.K, W);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int m = lane & 15, j = lane >> 4;
@@ -232,12 +357,19 @@ __global__ __launch_bounds__(64 * W) void k_tgemm(TgArgs a) {
         P = bs.pack;
         SC = bs.sc;
     }
-    const int lrow = min(row0 - bs.base + m, bs.n - 1);
+    // PART: block b's row for lane m is t + 256 i, t = b*(16/pku) + m % (16/pku), i = m / (16/pku)
+    const int tpb = PART ? 16 / a.pku : 16;
+    auto out_row = [&](int mm) {
+        return PART ? (row0 / 16) * tpb + mm % tpb + 256 * (mm / tpb) : min(row0 - bs.base + mm, bs.n - 1);
+    };
+    const int lrow = out_row(m);
     const int tA = min(m, T - 1);                    // this lane's A-operand token
 
     // 1. activation loads first: the prologue then waits for these only
-    Q8Regs<tg_uq(W, KS, NL), tg_sq(W, KS, NL)> qr;
-    tg_q8_load(a, qr, 64 * W);
+    Q8Regs<IN == TG_Q8 ? tg_uq(W, KS, NL) : 1, IN == TG_Q8 ? tg_sq(W, KS, NL) : 1> qr;
+    NormRegs<IN == TG_NORM ? tg_rx(W, KS, NL) : 1> nr;
+    if constexpr (IN == TG_Q8) tg_q8_load(a, qr, 64 * W);
+    else tg_norm_load(a, nr, W);
     // 2. the weights and scales of every step
     uint4 wv[NL], sv[NL / 2];
     {
@@ -257,14 +389,15 @@ __global__ __launch_bounds__(64 * W) void k_tgemm(TgArgs a) {
         for (int r = 0; r < NE; r++) {
             const int e = (wave % KS) * 64 + lane + r * 64 * KS;
             const int tok = min(e >> 4, T - 1);
-            const int lr = min(row0 - bs.base + (e & 15), bs.n - 1);
+            const int lr = out_row(e & 15);
             yold[r] = a.acc ? bs.y[(size_t)tok * bs.n + lr] : 0.0f;
         }
     }
     TI_ISSUE_FENCE();
 
     // 3. prologue: codes in B's byte order, scales, -8*sum(a) into LDS
-    tg_q8_stage(a, qr, L, 64 * W);
+    if constexpr (IN == TG_Q8) tg_q8_stage(a, qr, L, 64 * W);
+    else tg_norm_stage(a, nr, L, W);
 
     // 4. the group loop
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -319,18 +452,33 @@ __global__ __launch_bounds__(64 * W) void k_tgemm(TgArgs a) {
             if (r == 0) a.ys[(size_t)tok * (a.N / 32) + ch] = scale;
         }
     } else {
-        if (!valid) return;
         const int w0 = (wave / KS) * KS;
+        float* xn = L.xn + (wave / KS) * 256;            // this block's outputs [tok][16] (PART)
 #pragma unroll
         for (int r = 0; r < NE; r++) {
             const int e = (wave % KS) * 64 + lane + r * 64 * KS;
             const int tok = e >> 4, mm = e & 15;
-            const int lr = row0 - bs.base + mm;
-            if (tok < T && lr < bs.n) {
+            const int lr = PART ? out_row(mm) : row0 - bs.base + mm;
+            if (valid && tok < T && lr < bs.n) {
                 float v = 0.0f;
 #pragma unroll
                 for (int k = 0; k < KS; k++) v += L.part[((w0 + k) * 16 + tok) * 17 + mm];
-                bs.y[(size_t)tok * bs.n + lr] = a.acc ? yold[r] + v : v;
+                const float yn = a.acc ? yold[r] + v : v;
+                bs.y[(size_t)tok * bs.n + lr] = yn;
+                if (PART) xn[tok * 16 + mm] = yn;
+            }
+        }
+        if constexpr (PART) {   // partial t = sum over i of x[t + 256 i]^2, in i order
+            __syncthreads();
+            for (int idx = (wave % KS) * 64 + lane; valid && idx < T * tpb; idx += 64 * KS) {
+                const int tok = idx / tpb, tl = idx % tpb;
+                float sp = 0.0f;
+                for (int i = 0; i < a.pku; i++) {
+                    const float xv = xn[tok * 16 + tl + tpb * i];
+                    const float sq = xv * xv;
+                    sp = sp + sq;
+                }
+                a.pout[(size_t)tok * 256 + (row0 / 16) * tpb + tl] = sp;
             }
         }
     }
@@ -400,18 +548,31 @@ __global__ __launch_bounds__(256) void k_tnorm_q8(const float* __restrict__ x, c
     if (t % (32 / KU) == 0) xs[(size_t)blockIdx.x * (K / 32) + KU * t / 32] = scale;
 }
 
+// The RMSNorm partial sums of a [T][K] activation (K = 256 KU) that no projection
+// produced (the embeddings): p[t][u] = sum over i of x[t][u + 256 i]^2, in i order.
+__global__ __launch_bounds__(256) void k_tsumsq(const float* __restrict__ x, float* __restrict__ p, int K) {
+    const float* xr = x + (size_t)blockIdx.x * K;
+    float s = 0.0f;
+    for (int i = threadIdx.x; i < K; i += 256) {
+        const float sq = xr[i] * xr[i];
+        s = s + sq;
+    }
+    p[(size_t)blockIdx.x * 256 + threadIdx.x] = s;
+}
+
 // ---- host dispatch ------------------------------------------------------------------
-// (W, KS, NL) per K = 128*KS*NL: 8-wave workgroups where K allows (all SIMDs of the
-// chip busy at N = 2048)
+// (W, KS, NL) per K = 128*KS*NL: 8 or 12 waves per workgroup (more loads in flight
+// per CU: the N = 2048 projections fill only 128 CUs with 16-row blocks; K = 6144 at
+// 12 waves measured 8.8 against 9.5 us at 8)
 bool tg_split(int G, int& W, int& KS, int& NL) {
     switch (G) {
         case 8: W = 4; KS = 1; NL = 2; return true;
         case 16: W = 4; KS = 2; NL = 2; return true;
         case 32: W = 8; KS = 4; NL = 2; return true;
         case 64: W = 8; KS = 8; NL = 2; return true;
-        case 96: W = 8; KS = 4; NL = 6; return true;
+        case 96: W = 12; KS = 12; NL = 2; return true;
         case 128: W = 8; KS = 8; NL = 4; return true;
-        case 192: W = 8; KS = 8; NL = 6; return true;
+        case 192: W = 12; KS = 12; NL = 4; return true;
         case 256: W = 8; KS = 8; NL = 8; return true;
         default: return false;
     }
@@ -423,19 +584,37 @@ int tg_ku(int K) {   // k_tnorm_q8: K = 256*KU, KU in {1, 2, 4, 8, 16}
     return (ku == 1 || ku == 2 || ku == 4 || ku == 8 || ku == 16) ? ku : 0;
 }
 
-template <bool GU, int W, int KS, int NL>
+template <bool GU, int W, int KS, int NL, int IN, bool PART>
 int tg_go(ti_ctx* c, const TgArgs& a, unsigned grid, const char* name) {
-    const size_t lds = (size_t)tg_lds_words(a.T, a.K, W) * 4;
+    const size_t lds = (size_t)tg_lds_words(a.T, a.K, W, PART ? W / KS : 0) * 4;
     static bool attr = false;
     if (!attr && lds > 65536) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_tgemm<GU, W, KS, NL>),
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_tgemm<GU, W, KS, NL, IN, PART>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         if (e != hipSuccess) return ti_hip_fail(e, "k_tgemm LDS attribute");
         attr = true;
     }
-    k_tgemm<GU, W, KS, NL><<<grid, 64 * W, lds, c->stream>>>(a);
+    k_tgemm<GU, W, KS, NL, IN, PART><<<grid, 64 * W, lds, c->stream>>>(a);
     TI_LAUNCHED(name);
     return TI_OK;
+}
+
+// dispatch over K for the non-gate/up kernels: (W, KS, NL) from the split table (the
+// norm prologue exists for K <= 2048 only)
+template <int IN, bool PART>
+int tg_dispatch(ti_ctx* c, const TgArgs& a, int nb, const char* name) {
+#define TGQ(G_, W_, KS_, NL_) \
+    case G_: return tg_go<false, W_, KS_, NL_, IN, PART>(c, a, (unsigned)((nb + W_ / KS_ - 1) / (W_ / KS_)), name);
+    if constexpr (IN == TG_NORM) {
+        switch (a.K / 32) { TGQ(8, 4, 1, 2) TGQ(16, 4, 2, 2) TGQ(32, 8, 4, 2) TGQ(64, 8, 8, 2) }
+    } else {
+        switch (a.K / 32) {
+            TGQ(8, 4, 1, 2) TGQ(16, 4, 2, 2) TGQ(32, 8, 4, 2) TGQ(64, 8, 8, 2) TGQ(96, 12, 12, 2) TGQ(128, 8, 8, 4)
+            TGQ(192, 12, 12, 4) TGQ(256, 8, 8, 8)
+        }
+    }
+#undef TGQ
+    return ti_fail(TI_ERR_INVALID, "T-token GEMM: no kernel for K=%d", a.K);
 }
 
 }  // namespace
@@ -446,6 +625,14 @@ bool ti_tgemm_ok(int T, int K) {
     return T >= 2 && T <= TG_TMAX && K % 32 == 0 && tg_split(K / 32, W, KS, NL);
 }
 bool ti_tnorm_ok(int K) { return tg_ku(K) != 0; }
+// the norm prologue: K = 256 * {1,2,4,8}, 8 elements per lane, a 32-group within 4 lanes
+bool ti_tgemm_norm_ok(int T, int K) {
+    int W, KS, NL;
+    if (!ti_tgemm_ok(T, K) || !tg_ku(K) || K > 2048) return false;
+    tg_split(K / 32, W, KS, NL);
+    const int gw = K / 32 == 8 ? 4 : 8;               // the gate/up kernels' W at this K
+    return K % (32 * W) == 0 && K % (32 * gw) == 0;
+}
 bool ti_tgemm_gateup_ok(int T, int H) {
     const int G = H / 32;
     return ti_tgemm_ok(T, H) && (G == 8 || G == 16 || G == 32 || G == 64 || G == 128);
@@ -461,11 +648,14 @@ int ti_tnorm_q8_launch(ti_ctx* c, const float* x, const uint16_t* nw, float eps,
     return ti_fail(TI_ERR_INVALID, "T-token norm: no kernel for K=%d", K);
 }
 
-// y_s[t][:] (+)= W_s a_t for up to three segments sharing the int8 activation
-// (xq [T][K/4], xs [T][K/32]). Scales must be 16-byte aligned (K % 256 == 0 keeps every
-// row aligned); segments before the last must have a multiple of 16 rows.
-int ti_tgemm_launch(ti_ctx* c, const uint32_t* xq, const float* xs, int nseg, const uint32_t* const* packs,
-                    const uint16_t* const* scs, float* const* ys, const int* Ns, int T, int K, int acc) {
+// y_s[t][:] (+)= W_s a_t for up to three segments sharing the activation: int8 codes
+// (in.xq [T][K/4], in.xs [T][K/32]) or, with in.x set, RMSNorm + quantQ8T of in.x in the
+// prologue from the partial sums in.pin. pout: also write the output's partial sums
+// (one segment, N = 256 * {1,2,4,8,16}, acc = 1: the residual stream). Scales must be
+// 16-byte aligned (K % 256 == 0 keeps every row aligned); segments before the last must
+// have a multiple of 16 rows.
+int ti_tgemm_launch(ti_ctx* c, const TgIn& in, int nseg, const uint32_t* const* packs, const uint16_t* const* scs,
+                    float* const* ys, const int* Ns, int T, int K, int acc, float* pout) {
     TgArgs a = {};
     a.nseg = nseg;
     a.N = 0;
@@ -479,24 +669,29 @@ int ti_tgemm_launch(ti_ctx* c, const uint32_t* xq, const float* xs, int nseg, co
     a.T = T;
     a.acc = acc;
     a.S = K / 4 + 2;
-    a.xq = xq;
-    a.xs = xs;
+    a.xq = in.xq;
+    a.xs = in.xs;
+    a.x = in.x;
+    a.nw = in.nw;
+    a.eps = in.eps;
+    a.pin = in.pin;
+    a.pout = pout;
     if (!ti_tgemm_ok(T, K)) return ti_fail(TI_ERR_INVALID, "T-token GEMM: unsupported T=%d K=%d", T, K);
-    const int nb = (a.N + 15) / 16;
-    switch (K / 32) {
-#define TGQ(G_, W_, KS_, NL_) \
-    case G_: return tg_go<false, W_, KS_, NL_>(c, a, (unsigned)((nb + W_ / KS_ - 1) / (W_ / KS_)), "k_tgemm");
-        TGQ(8, 4, 1, 2) TGQ(16, 4, 2, 2) TGQ(32, 8, 4, 2) TGQ(64, 8, 8, 2) TGQ(96, 8, 4, 6) TGQ(128, 8, 8, 4)
-        TGQ(192, 8, 8, 6) TGQ(256, 8, 8, 8)
-#undef TGQ
+    if (in.x && !ti_tgemm_norm_ok(T, K)) return ti_fail(TI_ERR_INVALID, "T-token GEMM: no norm prologue for T=%d K=%d", T, K);
+    if (pout) {
+        a.pku = tg_ku(a.N);
+        if (nseg != 1 || !acc || !a.pku) return ti_fail(TI_ERR_INVALID, "T-token GEMM: partial sums need one residual segment, N = 256*{1,2,4,8,16}");
     }
-    return ti_fail(TI_ERR_INVALID, "T-token GEMM: no kernel for K=%d", K);
+    const int nb = (a.N + 15) / 16;
+    if (in.x) return tg_dispatch<TG_NORM, false>(c, a, nb, "k_tgemm");
+    return pout ? tg_dispatch<TG_Q8, true>(c, a, nb, "k_tgemm") : tg_dispatch<TG_Q8, false>(c, a, nb, "k_tgemm");
 }
 
-// gate/up on int8 input (the codes of ti_tnorm_q8): swq[t] = quantQ8(silu(Wg a_t) * (Wu a_t))
-int ti_tgemm_gateup_launch(ti_ctx* c, const uint32_t* xq, const float* xs, const uint32_t* gpack, const uint16_t* gsc,
-                           const uint32_t* upack, const uint16_t* usc, int I, int H, int T, uint32_t* swq, float* sws) {
+// gate/up: swq[t] = quantQ8(silu(Wg a_t) * (Wu a_t)), a_t as for ti_tgemm_launch
+int ti_tgemm_gateup_launch(ti_ctx* c, const TgIn& in, const uint32_t* gpack, const uint16_t* gsc, const uint32_t* upack,
+                           const uint16_t* usc, int I, int H, int T, uint32_t* swq, float* sws) {
     if (!ti_tgemm_gateup_ok(T, H) || I % 32) return ti_fail(TI_ERR_INVALID, "T-token gate/up: unsupported T=%d H=%d I=%d", T, H, I);
+    if (in.x && !ti_tgemm_norm_ok(T, H)) return ti_fail(TI_ERR_INVALID, "T-token gate/up: no norm prologue for H=%d", H);
     if (reinterpret_cast<uintptr_t>(gsc) % 16 || reinterpret_cast<uintptr_t>(usc) % 16)
         return ti_fail(TI_ERR_INVALID, "T-token gate/up: scales must be 16-byte aligned");
     TgArgs a = {};
@@ -506,21 +701,43 @@ int ti_tgemm_gateup_launch(ti_ctx* c, const uint32_t* xq, const float* xs, const
     a.K = H;
     a.T = T;
     a.S = H / 4 + 2;
-    a.xq = xq;
-    a.xs = xs;
+    a.xq = in.xq;
+    a.xs = in.xs;
+    a.x = in.x;
+    a.nw = in.nw;
+    a.eps = in.eps;
+    a.pin = in.pin;
     a.upack = reinterpret_cast<const uint4*>(upack);
     a.usc = reinterpret_cast<const uint4*>(usc);
     a.yq = swq;
     a.ys = sws;
     const unsigned grid = (unsigned)(I / 32);
-    switch (H / 32) {   // 8 waves: 4 blocks x KS = 2 (K/32 = 8 * NL); K = 256: 4 waves
-        case 8: return tg_go<true, 4, 1, 2>(c, a, grid, "k_tgemm_gateup");
-        case 16: return tg_go<true, 8, 2, 2>(c, a, grid, "k_tgemm_gateup");
-        case 32: return tg_go<true, 8, 2, 4>(c, a, grid, "k_tgemm_gateup");
-        case 64: return tg_go<true, 8, 2, 8>(c, a, grid, "k_tgemm_gateup");
-        case 128: return tg_go<true, 8, 2, 16>(c, a, grid, "k_tgemm_gateup");
+    const char* nm = "k_tgemm_gateup";
+    if (in.x) {
+        switch (H / 32) {   // 8 waves: 4 blocks x KS = 2 (K/32 = 8 * NL); K = 256: 4 waves
+            case 8: return tg_go<true, 4, 1, 2, TG_NORM, false>(c, a, grid, nm);
+            case 16: return tg_go<true, 8, 2, 2, TG_NORM, false>(c, a, grid, nm);
+            case 32: return tg_go<true, 8, 2, 4, TG_NORM, false>(c, a, grid, nm);
+            case 64: return tg_go<true, 8, 2, 8, TG_NORM, false>(c, a, grid, nm);
+        }
+    } else {
+        switch (H / 32) {
+            case 8: return tg_go<true, 4, 1, 2, TG_Q8, false>(c, a, grid, nm);
+            case 16: return tg_go<true, 8, 2, 2, TG_Q8, false>(c, a, grid, nm);
+            case 32: return tg_go<true, 8, 2, 4, TG_Q8, false>(c, a, grid, nm);
+            case 64: return tg_go<true, 8, 2, 8, TG_Q8, false>(c, a, grid, nm);
+            case 128: return tg_go<true, 8, 2, 16, TG_Q8, false>(c, a, grid, nm);
+        }
     }
     return ti_fail(TI_ERR_INVALID, "T-token gate/up: no kernel for H=%d", H);
+}
+
+// RMSNorm partial sums of T rows of K = 256 * {1,2,4,8,16} (the embeddings of a forward)
+int ti_tsumsq_launch(ti_ctx* c, const float* x, float* p, int T, int K) {
+    if (!tg_ku(K)) return ti_fail(TI_ERR_INVALID, "T-token partial sums: K=%d", K);
+    k_tsumsq<<<T, 256, 0, c->stream>>>(x, p, K);
+    TI_LAUNCHED("k_tsumsq");
+    return TI_OK;
 }
 
 extern "C" int ti_rmsnorm_q8_t(ti_ctx* c, const float* x, const uint16_t* w, uint32_t* xq, float* xs, int T, int H,

@@ -60,6 +60,34 @@ struct ti_graph {
 #define TI_SYNC_ATTN 64           // fused attention: one counter per KV head (up to 64)
 #define TI_SYNC_DUMMY 256         // 256 words never written: a valid read target for unused inputs
 
+// ---- the T-token forward (2 <= T <= 16) ---------------------------------------------
+// Input of a T-token projection: int8 codes (xq [T][K/4], xs [T][K/32]) or, with x set,
+// the f32 activation x [T][K] that the kernel RMS-normalises (weight nw, eps) and
+// quantises itself, from its partial sums pin [T][256] (p[t][u] = sum over i of
+// x[t][u + 256 i]^2: what a residual projection's epilogue or ti_tsumsq_launch writes).
+struct TgIn {
+    const uint32_t* xq;
+    const float* xs;
+    const float* x;
+    const uint16_t* nw;
+    float eps;
+    const float* pin;
+};
+bool ti_tgemm_ok(int T, int K);
+bool ti_tgemm_norm_ok(int T, int K);
+bool ti_tnorm_ok(int K);
+bool ti_tgemm_gateup_ok(int T, int H);
+int ti_tnorm_q8_launch(ti_ctx* c, const float* x, const uint16_t* nw, float eps, uint32_t* xq, float* xs, int T, int K);
+int ti_tsumsq_launch(ti_ctx* c, const float* x, float* p, int T, int K);
+int ti_tgemm_launch(ti_ctx* c, const TgIn& in, int nseg, const uint32_t* const* packs, const uint16_t* const* scs,
+                    float* const* ys, const int* Ns, int T, int K, int acc, float* pout);
+int ti_tgemm_gateup_launch(ti_ctx* c, const TgIn& in, const uint32_t* gpack, const uint16_t* gsc, const uint32_t* upack,
+                           const uint16_t* usc, int I, int H, int T, uint32_t* swq, float* sws);
+bool ti_tattn_ok(int T, int nHq, int nKv, int hd);
+int ti_tattn_launch(ti_ctx* c, const float* q, const float* k, const float* v, const uint16_t* qw, const uint16_t* kw,
+                    const float* rope, uint32_t* kq, float* ks, uint32_t* vq, float* vs, int S0, int T, int nHq, int nKv,
+                    int hd, float eps, uint32_t* oq, float* os);
+
 // ---- device helpers -----------------------------------------------------------
 // f16 bits -> f32 (exact).
 __device__ __forceinline__ float ti_h2f(uint16_t h) {

@@ -34,19 +34,6 @@ int ti_fused_gateup_launch(ti_ctx*, const float*, const uint16_t*, float, const 
 int ti_fused_lmhead_launch(ti_ctx*, const float*, const uint16_t*, float, const uint32_t*, const uint16_t*, float*, int,
                            int, uint32_t*, int*, int, int, const float*, float*, int);
 int ti_fused_kmax(int lm);
-bool ti_tgemm_ok(int T, int K);
-bool ti_tnorm_ok(int K);
-bool ti_tgemm_gateup_ok(int T, int H);
-int ti_tnorm_q8_launch(ti_ctx* c, const float* x, const uint16_t* nw, float eps, uint32_t* xq, float* xs, int T, int K);
-int ti_tgemm_launch(ti_ctx* c, const uint32_t* xq, const float* xs, int nseg, const uint32_t* const* packs,
-                    const uint16_t* const* scs, float* const* ys, const int* Ns, int T, int K, int acc);
-int ti_tgemm_gateup_launch(ti_ctx* c, const uint32_t* xq, const float* xs, const uint32_t* gpack, const uint16_t* gsc,
-                           const uint32_t* upack, const uint16_t* usc, int I, int H, int T, uint32_t* swq, float* sws);
-bool ti_tattn_ok(int T, int nHq, int nKv, int hd);
-
-int ti_tattn_launch(ti_ctx* c, const float* q, const float* k, const float* v, const uint16_t* qw, const uint16_t* kw,
-                    const float* rope, uint32_t* kq, float* ks, uint32_t* vq, float* vs, int S0, int T, int nHq, int nKv,
-                    int hd, float eps, uint32_t* oq, float* os);
 
 // ---------------------------------------------------------------------------
 // glue kernels
@@ -166,6 +153,7 @@ struct ti_qwen3 {
     uint32_t* xq;
     float* xs;
     int32_t* xsum;
+    float* psum;          // [16][256] RMSNorm partial sums of x (the T-token forward)
     uint32_t* hist;
     int* dpos;
     float* rope;          // [max_ctx][head_dim] cos/sin rows of the rotary embedding
@@ -251,6 +239,7 @@ extern "C" int ti_qwen3_create(ti_ctx* c, const ti_qwen3_config* cfg, ti_qwen3**
     if (!rc) rc = mk(m, (void**)&m->xq, (size_t)T * kmax);                          // [T][kmax] int8 codes
     if (!rc) rc = mk(m, (void**)&m->xs, (size_t)T * kmax / 32 * 4);
     if (!rc) rc = mk(m, (void**)&m->xsum, kmax / 16 * 4);
+    if (!rc) rc = mk(m, (void**)&m->psum, 16 * 256 * 4);
     if (!rc) rc = mk(m, (void**)&m->hist, (size_t)(C.max_ctx + 1) * 4);
     if (!rc) rc = mk(m, (void**)&m->dpos, 4);
     if (!rc) rc = mk(m, (void**)&m->rope, (size_t)C.max_ctx * hd * 4);
@@ -440,14 +429,25 @@ extern "C" int ti_qwen3_forward(ti_ctx* c, ti_qwen3* m, const int32_t* ids, int 
     if (ids) RC(ti_buf_write(c, m->hist, (size_t)pos * 4, ids, (size_t)T * 4));   // else already in the history
     k_embed<<<(unsigned)(((long)T * H + 255) / 256), 256, 0, c->stream>>>(m->hist, m->embed, m->x, T, H, pos, nullptr, C.vocab);
     TI_LAUNCHED("k_embed");
-    // 2..16 tokens: per layer [rmsnorm + quantQ8T] [q/k/v] [attention] [split merge +
-    // quantQ8T] [o_proj + residual] [rmsnorm + quantQ8T] [gate/up + SiLU + quantQ8T]
-    // [down + residual], the projections on the matrix cores (k_tgemm.hip, k_tattn.hip);
-    // the per-token norm codes live in the context's activation scratch, the attention
-    // and SwiGLU codes in the model's
+    // 2..16 tokens: per layer [rmsnorm + quantQ8T + q/k/v] [attention] [split merge +
+    // quantQ8T] [o_proj + residual] [rmsnorm + quantQ8T + gate/up + SiLU + quantQ8T]
+    // [down + residual], the projections on the matrix cores (k_tgemm.hip, k_tattn.hip).
+    // Up to 4 tokens the residual projections also write the RMSNorm partial sums of the
+    // new x (m->psum), from which the next projection normalises and quantises x in its
+    // prologue (two launches fewer per layer); past 4 tokens that prologue (every
+    // workgroup quantises all T x H elements) costs more than the launch it saves, and a
+    // per-token norm kernel writes the codes into the context's activation scratch
+    // first (1.7B geometry at 8k: T = 2 1.22 against 1.29 ms, T = 4 1.26 against 1.32,
+    // T = 8 1.39 against 1.36, T = 16 3.13 against 2.94; both paths give the same bits).
+    // The attention and SwiGLU codes live in the model's scratch.
     const bool fused = ti_tnorm_ok(H) && ti_tgemm_gateup_ok(T, H) && ti_tgemm_ok(T, nq) && ti_tgemm_ok(T, I) &&
                        nq % 16 == 0 && nkv % 16 == 0 && I % 32 == 0;
     const bool fused_attn = ti_tattn_ok(T, nHq, nKv, hd);
+    const bool norm_in = fused && T <= 4 && ti_tgemm_norm_ok(T, H);
+    if (norm_in) RC(ti_tsumsq_launch(c, m->x, m->psum, T, H));
+    float* const pout = norm_in ? m->psum : nullptr;
+    const TgIn codes_in = {c->act_q, c->act_s, nullptr, nullptr, 0.0f, nullptr};
+    const TgIn attn_in = {m->xq, m->xs, nullptr, nullptr, 0.0f, nullptr};
     for (int l = 0; l < C.layers; l++) {
         Layer& y = m->L[l];
         if (fused) {
@@ -455,8 +455,9 @@ extern "C" int ti_qwen3_forward(ti_ctx* c, ti_qwen3* m, const int32_t* ids, int 
             const uint16_t* scs[3] = {y.q.sc, y.k.sc, y.v.sc};
             float* ys[3] = {m->q, m->k, m->v};
             const int Ns[3] = {nq, nkv, nkv};
-            RC(ti_tnorm_q8_launch(c, m->x, y.in_norm, C.rms_eps, c->act_q, c->act_s, T, H));
-            RC(ti_tgemm_launch(c, c->act_q, c->act_s, 3, packs, scs, ys, Ns, T, H, 0));
+            const TgIn in_norm = {nullptr, nullptr, m->x, y.in_norm, C.rms_eps, m->psum};
+            if (!norm_in) RC(ti_tnorm_q8_launch(c, m->x, y.in_norm, C.rms_eps, c->act_q, c->act_s, T, H));
+            RC(ti_tgemm_launch(c, norm_in ? in_norm : codes_in, 3, packs, scs, ys, Ns, T, H, 0, nullptr));
         } else {
             RC(ti_rmsnorm(c, m->x, y.in_norm, m->normed, T, H, C.rms_eps));
             RC(ti_linear_q4(c, m->normed, y.q.pack, y.q.sc, m->q, T, nq, H, 0));
@@ -474,11 +475,12 @@ extern "C" int ti_qwen3_forward(ti_ctx* c, ti_qwen3* m, const int32_t* ids, int 
         }
         if (fused) {
             if (!fused_attn) RC(ti_quant_act_q8_async(c, m->attn, m->xq, m->xs, nullptr, T * (nq / 32)));
-            RC(ti_tgemm_launch(c, m->xq, m->xs, 1, &y.o.pack, &y.o.sc, &m->x, &H, T, nq, 1));
-            RC(ti_tnorm_q8_launch(c, m->x, y.post_norm, C.rms_eps, c->act_q, c->act_s, T, H));
-            RC(ti_tgemm_gateup_launch(c, c->act_q, c->act_s, y.gate.pack, y.gate.sc, y.up.pack, y.up.sc, I, H, T, m->xq,
-                                      m->xs));
-            RC(ti_tgemm_launch(c, m->xq, m->xs, 1, &y.down.pack, &y.down.sc, &m->x, &H, T, I, 1));
+            RC(ti_tgemm_launch(c, attn_in, 1, &y.o.pack, &y.o.sc, &m->x, &H, T, nq, 1, pout));
+            const TgIn post_norm = {nullptr, nullptr, m->x, y.post_norm, C.rms_eps, m->psum};
+            if (!norm_in) RC(ti_tnorm_q8_launch(c, m->x, y.post_norm, C.rms_eps, c->act_q, c->act_s, T, H));
+            RC(ti_tgemm_gateup_launch(c, norm_in ? post_norm : codes_in, y.gate.pack, y.gate.sc, y.up.pack, y.up.sc, I, H,
+                                      T, m->xq, m->xs));
+            RC(ti_tgemm_launch(c, attn_in, 1, &y.down.pack, &y.down.sc, &m->x, &H, T, I, 1, pout));
             continue;
         }
         RC(ti_linear_q4(c, m->attn, y.o.pack, y.o.sc, m->x, T, H, nq, 1));

@@ -169,38 +169,48 @@ def test_qwen3_17b_geometry_over_4k_prefix(ctx, orc):
         m.close()
 
 
-def test_qwen3_17b_geometry_batch8_over_4k_prefix(ctx, orc):
-    """The batch-8 configuration at the Qwen3-1.7B geometry: one T=8 forward at
-    positions 4096..4103 over a seeded 4k prefix (the fused matrix-core projections:
-    RMSNorm + quantQ8T prologues, three-matrix q/k/v, gate/up with the SwiGLU +
-    quantQ8 epilogue, residual o/down) against 8 reference steps: last-token logits
-    within 1e-3, the 8 new KV rows within one int8 step."""
+@pytest.mark.parametrize("T", [4, 8])
+def test_qwen3_17b_geometry_batch8_over_4k_prefix(ctx, orc, T):
+    """The batch configuration at the Qwen3-1.7B geometry: one T-token forward at
+    positions 4096.. over a seeded 4k prefix (the fused matrix-core projections:
+    three-matrix q/k/v, gate/up with the SwiGLU + quantQ8 epilogue, residual o/down;
+    T = 4 normalises and quantises x in the q/k/v and gate/up prologues from the partial
+    sums the residual projections write, T = 8 runs the per-token norm kernel) against T
+    reference steps and T single-token decode steps.
+
+    Layer 0 sees bit-exact activation codes (only the f32 sums differ): its T new KV
+    rows are within one int8 step of the reference's. Layer 1 inherits layer 0's float
+    rounding: one activation code that flips at a rounding boundary shifts that token's
+    whole K/V row by up to two steps and the logits by a few 1e-3, on the single-token
+    path as much as here (T = 4 with these ids: 2.3e-3 on both). So the logits must match
+    the single-token path's within 1e-5 and be no further from the reference than it is
+    (or within 1e-3)."""
     cfg = dict(CFG_17B, max_tokens=8)
     W = Q.make_weights(cfg, 5)
-    m = abi.Qwen3(ctx, **cfg)
+    m, one = abi.Qwen3(ctx, **cfg), abi.Qwen3(ctx, **cfg)
     try:
         Q.load_into(m, W)
+        Q.load_into(one, W)
         ref = Q.RefDecoder(cfg, W, cfg["max_ctx"])
         P = 4096
         _seed_prefix(ctx, orc, m, ref, cfg, P, 10)
-        ids = np.array([4242, 17, 151935, 0, 99, 1000, 77777, 5], np.int32)
+        _seed_prefix(ctx, orc, one, Q.RefDecoder(cfg, W, cfg["max_ctx"]), cfg, P, 10)
+        ids = np.array([4242, 17, 151935, 0, 99, 1000, 77777, 5], np.int32)[:T]
         m.forward(ids, P)
         for i, t in enumerate(ids):
+            one.forward(ids[i:i + 1], P + i)
             rl, rt = ref.step(int(t), P + i)
-        assert rel_err(_logits(ctx, m, cfg["vocab"]), rl) < TOL
+        lt, l1 = _logits(ctx, m, cfg["vocab"]), _logits(ctx, one, cfg["vocab"])
+        assert rel_err(lt, l1) < 1e-5
+        assert rel_err(lt, rl) < max(TOL, 1.5 * rel_err(l1, rl))
         if margin_ok(rl):
-            assert int(m.read_tokens(P + 8, 1)[0]) == rt
+            assert int(m.read_tokens(P + T, 1)[0]) == rt
         nkv = cfg["n_kv_heads"] * cfg["head_dim"]
         for l in range(cfg["layers"]):
             kq, _, vq, _ = m.kv(l)
             for dev, r in ((kq, ref.kv[l][0]), (vq, ref.kv[l][2])):
-                g = ctx.download(dev, np.uint32, (P + 8) * nkv // 4).view(np.int8).astype(int).reshape(P + 8, -1)[P:]
-                rr = r[P:P + 8].view(np.int8).astype(int).reshape(8, -1)
-                # layer 0 sees bit-exact activation codes (only the f32 sums differ). Layer 1
-                # inherits layer 0's float rounding: one activation code of a token that
-                # flips at a rounding boundary shifts that token's whole K/V row by up to two
-                # steps (seen on one of the 8 tokens, on the single-token path as well); the
-                # end-to-end bound is the logits check above
+                g = ctx.download(dev, np.uint32, (P + T) * nkv // 4).view(np.int8).astype(int).reshape(P + T, -1)[P:]
+                rr = r[P:P + T].view(np.int8).astype(int).reshape(T, -1)
                 d = np.abs(g - rr)
                 if l == 0:
                     assert d.max() <= 1 and np.mean(d > 0) < 0.002, (l, d.max(), np.mean(d > 0))
@@ -208,6 +218,7 @@ def test_qwen3_17b_geometry_batch8_over_4k_prefix(ctx, orc):
                     assert d.max() <= 2 and np.mean(d > 0) < 0.1, (l, d.max(), np.mean(d > 0))
     finally:
         m.close()
+        one.close()
 
 
 @pytest.mark.parametrize("T", [2, 16])
