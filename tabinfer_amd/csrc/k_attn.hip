@@ -866,7 +866,7 @@ __device__ __forceinline__ void attn_merge_tail(const AttnFArgs& a, int hk, int 
     if (!s_last) return;
     // the last split of hk: log-sum-exp over the splits that saw a tile; the o loads
     // are issued before the (m, l) pairs are reduced, one round trip for both
-    const int nused = ntiles < NW ? (ntiles + 3) / 4 : NS;
+    const int nused = ntiles < NW ? (ntiles > 0 ? (ntiles + 3) / 4 : 1) : NS;   // >= 1: no index -1
     // every split's o in one round trip (indices past nused repeat the last one and get
     // weight 0), then the splits' weights once per head: one wave per head, lane = split
     float ov[ATTF_MAXS];

@@ -1,17 +1,20 @@
 // k_tattn.hip — the attention of a T-token forward (the batch-8 decode step, short
-// prefills; head_dim 128, T * G <= 16 query rows per KV head) as one launch per layer.
+// prefills; head_dim 128, T <= 16, T * G <= 32 query rows per KV head) as one launch per layer.
 //
 // The reference runs it as ropeQK for q and k (models/qwen3.js:1700-1760), kvQuantWrite
 // (:2180-2216), the T-query attention (:2534-2577) and the log-sum-exp combine
 // (:2048-2068), then quantQ8T of the output for o_proj (:1210-1231). Here:
 //
-//  - workgroup (8 waves) = (KV head hk, split); the keys of hk are cut into blocks of 32
-//    and the waves of the NS splits take blocks round robin (gw: blocks gw, gw + 8NS, ..);
-//    the T new keys (positions S0 .. S0+T-1) are one more block, computed in the
-//    prologue of the workgroup whose wave takes it, which also writes them into the
-//    cache (snorm int8, as kvQuantWrite) — no other workgroup reads those positions;
-//  - every workgroup RMSNorms + RoPEs the 16 query rows (t, h) of hk (q_norm, the rope
-//    row of position S0 + t) and keeps them as f16 hi + lo (q = hi + lo to ~2^-22);
+//  - workgroup (8 waves) = (KV head hk, row tile rt, split); the keys of hk are cut into
+//    blocks of 32 and the waves of the NS splits take blocks round robin (gw: blocks gw,
+//    gw + 8NS, ..); the T new keys (positions S0 .. S0+T-1) are one more block, computed
+//    in the prologue of the workgroup whose wave takes it, which also writes them into
+//    the cache (snorm int8, as kvQuantWrite; row tile 0 only) — no other workgroup reads
+//    those positions;
+//  - a row tile is 16 query rows (t, h) of hk (rows 16 rt ..; more than 16 rows, up to
+//    32, take a second tile that streams the keys again): every workgroup RMSNorms +
+//    RoPEs its rows (q_norm, the rope row of position S0 + t) and keeps them as f16 hi +
+//    lo (q = hi + lo to ~2^-22);
 //  - per block, S^T = K Q^T on the matrix cores (v_mfma_f32_16x16x32_f16: K codes are
 //    exact in f16, two MFMAs per 32-dim scale group for q's two halves, each group's dot
 //    scaled by its key's K scale), causal mask, online softmax per row;
@@ -61,6 +64,7 @@ struct TAttnArgs {
     float* pml;
     int S0, T, nKv, G, NS;
     float eps;
+    int RT;                // row tiles: workgroups (hk, rt, split) serve rows 16 rt .. 16 rt + 15
 };
 
 // 4 int8 codes -> f16 pairs, exactly: the biased byte (code + 128) below an 0x64 high
@@ -118,7 +122,9 @@ __global__ __launch_bounds__(64 * TA_W) void k_attn_tq8(TAttnArgs a) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int NS = a.NS;
-    const int split = blockIdx.x % NS, hk = blockIdx.x / NS;
+    const int split = blockIdx.x % NS, hr = blockIdx.x / NS;
+    const int rt = hr % a.RT, hk = hr / a.RT;
+    const int rbase = TA_ROWS * rt;                      // this workgroup's first query row
     const int T = a.T, G = a.G, R = T * G, S0 = a.S0;
     const int nq = a.nKv * G * HD, nkv = a.nKv * HD;
     const int nb = (S0 + TA_BLK - 1) / TA_BLK;          // blocks of cached keys
@@ -161,8 +167,8 @@ __global__ __launch_bounds__(64 * TA_W) void k_attn_tq8(TAttnArgs a) {
     kwv[1] = ti_h2f(a.kw[lane + 64]);
 #pragma unroll
     for (int i = 0; i < QPW; i++) {
-        const int r = wave + TA_W * i;
-        const int rc = r < R ? r : 0;
+        const int rg = rbase + wave + TA_W * i;
+        const int rc = rg < R ? rg : 0;
         const int t = rc / G, h = rc % G;
         const float* src = a.q + (size_t)t * nq + (size_t)(hk * G + h) * HD;
         qx[i][0] = src[lane];
@@ -197,7 +203,7 @@ __global__ __launch_bounds__(64 * TA_W) void k_attn_tq8(TAttnArgs a) {
         const int r = wave + TA_W * i;
         float o0, o1;
         norm_rope(qx[i][0], qx[i][1], qwv[0], qwv[1], qc[i][0], qc[i][1], a.eps, o0, o1);
-        if (r >= R) o0 = o1 = 0.0f;
+        if (rbase + r >= R) o0 = o1 = 0.0f;
         const _Float16 h0 = (_Float16)o0, h1 = (_Float16)o1;
         s_qh[r][lane] = h0;
         s_qh[r][lane + 64] = h1;
@@ -228,14 +234,18 @@ __global__ __launch_bounds__(64 * TA_W) void k_attn_tq8(TAttnArgs a) {
                 float* lsc = isv ? &s_vs[TA_W][t][0] : &s_ks[TA_W][t][0];
                 const float lm = isv ? 1.0f : qk2;
                 if ((lane & 3) == 0) {
-                    gq[lane / 4] = wd0;
-                    gq[16 + lane / 4] = wd1;
+                    if (rt == 0) {                        // one row tile writes the cache
+                        gq[lane / 4] = wd0;
+                        gq[16 + lane / 4] = wd1;
+                    }
                     *reinterpret_cast<uint32_t*>(lt + lane) = wd0;
                     *reinterpret_cast<uint32_t*>(lt + 64 + lane) = wd1;
                 }
                 if ((lane & 31) == 0) {
-                    gs[lane / 32] = mx0;
-                    gs[2 + lane / 32] = mx1;
+                    if (rt == 0) {
+                        gs[lane / 32] = mx0;
+                        gs[2 + lane / 32] = mx1;
+                    }
                     lsc[lane / 32] = mx0 * lm;
                     lsc[2 + lane / 32] = mx1 * lm;
                 }
@@ -261,7 +271,7 @@ __global__ __launch_bounds__(64 * TA_W) void k_attn_tq8(TAttnArgs a) {
         qh[g] = *reinterpret_cast<const h8*>(&s_qh[r16][32 * g + 8 * jq]);
         ql[g] = *reinterpret_cast<const h8*>(&s_ql[r16][32 * g + 8 * jq]);
     }
-    const int trow = r16 / G;                            // this lane's score row's token
+    const int trow = (rbase + r16) / G;                  // this lane's score row's token
     // per-lane state: score lanes (row r16) the reference maximum and a partial sum of p;
     // O lanes (rows 4jq..4jq+3, dim 16D + r16) the unnormalised outputs
     float m_run = -3.0e38f, l_run = 0.0f;
@@ -429,7 +439,7 @@ __global__ __launch_bounds__(64 * TA_W) void k_attn_tq8(TAttnArgs a) {
 #pragma unroll
         for (int w = 0; w < TA_W; w++) o[k] = fmaf(s_om[w][row][d0 + k], e[w], o[k]);
     }
-    const size_t pr = ((size_t)hk * NS + split) * TA_ROWS + row;
+    const size_t pr = (((size_t)hk * a.RT + rt) * NS + split) * TA_ROWS + row;
     *reinterpret_cast<float4*>(a.po + pr * HD + d0) = make_float4(o[0], o[1], o[2], o[3]);
     if (d0 == 0) *reinterpret_cast<float2*>(a.pml + pr * 2) = make_float2(M, L);
 }
@@ -442,7 +452,7 @@ struct TCombArgs {
     const float* pml;
     uint32_t* oq;          // [T][nHq*HD/4]
     float* os;             // [T][nHq*HD/32]
-    int NS, nKv, G, R;
+    int NS, nKv, G, R, RT;
 };
 
 __global__ __launch_bounds__(HD) void k_attn_tcombine(TCombArgs c) {
@@ -450,13 +460,14 @@ __global__ __launch_bounds__(HD) void k_attn_tcombine(TCombArgs c) {
     __shared__ float s_L;
     const int hk = blockIdx.x / c.R, row = blockIdx.x % c.R, d = threadIdx.x;
     const int NS = c.NS;
+    const size_t pbase = ((size_t)hk * c.RT + row / TA_ROWS) * NS;   // this row's tile's splits
     float ov[TA_MAXS];
 #pragma unroll
     for (int s = 0; s < TA_MAXS; s++)   // every load at once; splits past NS repeat the last one
-        ov[s] = c.po[(((size_t)hk * NS + (s < NS ? s : NS - 1)) * TA_ROWS + row) * HD + d];
+        ov[s] = c.po[((pbase + (s < NS ? s : NS - 1)) * TA_ROWS + row % TA_ROWS) * HD + d];
     if (d < 64) {   // wave 0: lane s holds split s's (m, l); the split weights 2^(m_s - M)
         const bool in = d < NS;
-        const float2 ml = *reinterpret_cast<const float2*>(c.pml + (((size_t)hk * NS + (in ? d : 0)) * TA_ROWS + row) * 2);
+        const float2 ml = *reinterpret_cast<const float2*>(c.pml + ((pbase + (in ? d : 0)) * TA_ROWS + row % TA_ROWS) * 2);
         const float m = in ? ml.x : -3.0e38f;
         float M = m;
 #pragma unroll
@@ -485,9 +496,10 @@ __global__ __launch_bounds__(HD) void k_attn_tcombine(TCombArgs c) {
 
 }  // namespace
 
-// Whether the T-token attention takes this kernel: head_dim 128, T*G <= 16 rows.
+// Whether the T-token attention takes this kernel: head_dim 128, T*G <= 32 query rows
+// per KV head (two row tiles of 16), T <= 16 new keys.
 bool ti_tattn_ok(int T, int nHq, int nKv, int hd) {
-    return hd == HD && nKv > 0 && nHq % nKv == 0 && T >= 1 && T * (nHq / nKv) <= TA_ROWS;
+    return hd == HD && nKv > 0 && nHq % nKv == 0 && T >= 1 && T <= 16 && T * (nHq / nKv) <= 2 * TA_ROWS;
 }
 
 // T new tokens at positions S0 .. S0+T-1 of one layer: q, k, v are the projections
@@ -498,19 +510,20 @@ int ti_tattn_launch(ti_ctx* c, const float* q, const float* k, const float* v, c
                     int hd, float eps, uint32_t* oq, float* os) {
     if (!ti_tattn_ok(T, nHq, nKv, hd)) return ti_fail(TI_ERR_INVALID, "T-token attention: unsupported T=%d heads %d/%d hd=%d", T, nHq, nKv, hd);
     const int nb = (S0 + TA_BLK - 1) / TA_BLK;
-    // about 2048 waves (8 per CU) over the KV heads, at most TA_MAXS splits, none
-    // without a block
-    int NS = (2048 / TA_W + nKv - 1) / nKv;
+    // about 2048 waves (8 per CU) over the KV heads and row tiles, at most TA_MAXS
+    // splits, none without a block (a second row tile streams the keys again: 32 rows
+    // would need twice the O registers of a wave)
+    const int R = T * (nHq / nKv), RT = (R + TA_ROWS - 1) / TA_ROWS;
+    int NS = (2048 / TA_W + nKv * RT - 1) / (nKv * RT);
     const int need = (nb + 1 + TA_W - 1) / TA_W;
     if (NS > need) NS = need;
     if (NS > TA_MAXS) NS = TA_MAXS;
     if (NS < 1) NS = 1;
     TAttnArgs a = {q, k, v, qw, kw, rope, reinterpret_cast<uint8_t*>(kq), ks, reinterpret_cast<uint8_t*>(vq), vs,
-                   c->attn_po, c->attn_ml, S0, T, nKv, nHq / nKv, NS, eps};
-    k_attn_tq8<<<nKv * NS, 64 * TA_W, 0, c->stream>>>(a);
+                   c->attn_po, c->attn_ml, S0, T, nKv, nHq / nKv, NS, eps, RT};
+    k_attn_tq8<<<nKv * RT * NS, 64 * TA_W, 0, c->stream>>>(a);
     TI_LAUNCHED("k_attn_tq8");
-    const int R = T * (nHq / nKv);
-    TCombArgs cb = {c->attn_po, c->attn_ml, oq, os, NS, nKv, nHq / nKv, R};
+    TCombArgs cb = {c->attn_po, c->attn_ml, oq, os, NS, nKv, nHq / nKv, R, RT};
     k_attn_tcombine<<<nKv * R, HD, 0, c->stream>>>(cb);
     TI_LAUNCHED("k_attn_tcombine");
     return TI_OK;

@@ -244,6 +244,33 @@ def test_batched_forward_t_sizes(ctx, T):
         a.close()
         b.close()
 
+@pytest.mark.parametrize("T", [12, 16])
+def test_batched_forward_two_row_tiles(ctx, T):
+    """T tokens x 2 query heads per KV head = 24 / 32 query rows: the T-token attention
+    serves them as two row tiles of 16 (the second partly empty at T = 12), over a
+    40-token prefix (cached key blocks and the new-key block); last logits as T
+    single-token forwards."""
+    cfg = dict(layers=2, hidden=256, intermediate=512, n_heads=4, n_kv_heads=2, head_dim=128, vocab=1000,
+               rope_theta=1e6, rms_eps=1e-6, max_ctx=128, max_tokens=64)
+    W = Q.make_weights(cfg, 9)
+    a, b = abi.Qwen3(ctx, **cfg), abi.Qwen3(ctx, **cfg)
+    try:
+        Q.load_into(a, W)
+        Q.load_into(b, W)
+        pre = (np.arange(40, dtype=np.int32) * 37 + 11) % cfg["vocab"]
+        ids = (np.arange(T, dtype=np.int32) * 131 + 7) % cfg["vocab"]
+        a.forward(pre, 0)
+        a.forward(ids, 40)
+        b.forward(pre, 0)
+        for p in range(T):
+            b.forward(ids[p:p + 1], 40 + p)
+        la, lb = _logits(ctx, a, cfg["vocab"]), _logits(ctx, b, cfg["vocab"])
+        assert rel_err(la, lb) < TOL
+    finally:
+        a.close()
+        b.close()
+
+
 def test_qwen3_06b_geometry_batch8_over_1k_prefix(ctx, orc):
     """The batch-8 forward at the Qwen3-0.6B geometry (hidden 1024, intermediate 3072,
     16/8 heads of 128: the K = 1024 / 2048 / 3072 projection kernels and the KU = 4 norm
