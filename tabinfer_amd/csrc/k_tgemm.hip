@@ -83,6 +83,12 @@ struct TgArgs {
     // block b owns output rows t + 256 i for 16/pku consecutive t and every i < pku
     float* pout;
     int pku;
+    // split-K (SPLIT): K above is one half; kld = the rows' full K (activation and weight
+    // row strides). Workgroup 2b + h computes half h of block b, publishes it to sp, and
+    // the second of the pair to arrive (counter scnt[b]) adds the halves in order 0, 1
+    int kld;
+    float* sp;
+    uint32_t* scnt;
 };
 
 // LDS (dynamic), in words: codes [T][S] (rounded to 4), scales [G][16] f32, -8*sum(a)
@@ -142,21 +148,27 @@ struct Q8Regs {
     float s[SQ];
 };
 
-template <int UQ, int SQ>
-__device__ __forceinline__ void tg_q8_load(const TgArgs& a, Q8Regs<UQ, SQ>& r, int nthreads) {
-    const int units = a.T * (a.K / 16), ns = a.T * (a.K / 32);
+template <int UQ, int SQ, bool SLICE>
+__device__ __forceinline__ void tg_q8_load(const TgArgs& a, Q8Regs<UQ, SQ>& r, int nthreads, int part) {
+    const int upr = a.K / 16, G = a.K / 32;
+    const int units = a.T * upr, ns = a.T * G;
     const uint4* src = reinterpret_cast<const uint4*>(a.xq);
     // UQ / SQ cover 16 tokens; rounds wholly past T are skipped (a workgroup-uniform
-    // test, so no load is issued for them), the partial one reads clamped indices
+    // test, so no load is issued for them), the partial one reads clamped indices.
+    // SLICE: the K slice `part` of rows kld wide
 #pragma unroll
     for (int k = 0; k < UQ; k++) {
-        const int u = threadIdx.x + nthreads * k;
-        if (nthreads * k < units) r.c[k] = src[u < units ? u : units - 1];
+        int u = threadIdx.x + nthreads * k;
+        u = u < units ? u : units - 1;
+        if (SLICE) u = (u / upr) * (a.kld / 16) + part * upr + u % upr;
+        if (nthreads * k < units) r.c[k] = src[u];
     }
 #pragma unroll
     for (int k = 0; k < SQ; k++) {
-        const int e = threadIdx.x + nthreads * k;
-        if (nthreads * k < ns) r.s[k] = a.xs[e < ns ? e : ns - 1];
+        int e = threadIdx.x + nthreads * k;
+        e = e < ns ? e : ns - 1;
+        if (SLICE) e = (e / G) * (a.kld / 32) + part * G + e % G;
+        if (nthreads * k < ns) r.s[k] = a.xs[e];
     }
 }
 
@@ -320,10 +332,11 @@ constexpr int tg_sq(int W, int KS, int NL) { return (NL * KS + W - 1) / W; }
 // the workgroup's 32-row chunk, then up rows +0/+16). IN: TG_Q8 codes or TG_NORM
 // (RMSNorm + quantQ8T in the prologue). PART: residual epilogue that also writes the
 // output's RMSNorm partial sums (block b owns rows t + 256 i).
-template <bool GU, int W, int KS, int NL, int IN, bool PART>
+template <bool GU, int W, int KS, int NL, int IN, bool PART, bool SPLIT = false>
 __global__ __launch_bounds__(64 * W) void k_tgemm(TgArgs a) {
     static_assert(!GU || W / KS == 4, "gate/up: four 16-row blocks per workgroup");
     static_assert(!(GU && PART), "the partial sums come from residual projections");
+    static_assert(!SPLIT || (!GU && !PART && IN == TG_Q8 && W == KS), "split-K: one residual block per workgroup");
     static_assert(NL % 2 == 0, "scales are loaded 8 groups at a time");
     extern __shared__ __align__(16) uint32_t s_dyn[];
     const int T = a.T, G = a.K / 32, S = a.S;
@@ -332,6 +345,9 @@ __global__ __launch_bounds__(64 * W) void k_tgemm(TgArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int m = lane & 15, j = lane >> 4;
     constexpr int BPW = W / KS;
+    const int part = SPLIT ? blockIdx.x & 1 : 0;         // split-K half
+    const int bidx = SPLIT ? blockIdx.x >> 1 : blockIdx.x;
+    const int Gld = SPLIT ? a.kld / 32 : G, goff = part * G;   // weight row stride, this half's groups
 
     // this wave's block: rows [row0, row0+16) of one matrix, groups [gbase, gbase + 4*NL)
     const int gbase = (wave % KS) * 4 * NL;
@@ -349,7 +365,7 @@ __global__ __launch_bounds__(64 * W) void k_tgemm(TgArgs a) {
         bs.n = a.N;
     } else {
         const int nb = (a.N + 15) / 16;
-        int blk = blockIdx.x * BPW + wave / KS;
+        int blk = bidx * BPW + wave / KS;
         valid = blk < nb;
         blk = valid ? blk : nb - 1;
         row0 = blk * 16;
@@ -368,13 +384,13 @@ __global__ __launch_bounds__(64 * W) void k_tgemm(TgArgs a) {
     // 1. activation loads first: the prologue then waits for these only
     Q8Regs<IN == TG_Q8 ? tg_uq(W, KS, NL) : 1, IN == TG_Q8 ? tg_sq(W, KS, NL) : 1> qr;
     NormRegs<IN == TG_NORM ? tg_rx(W, KS, NL) : 1> nr;
-    if constexpr (IN == TG_Q8) tg_q8_load(a, qr, 64 * W);
+    if constexpr (IN == TG_Q8) tg_q8_load<tg_uq(W, KS, NL), tg_sq(W, KS, NL), SPLIT>(a, qr, 64 * W, part);
     else tg_norm_load(a, nr, W);
     // 2. the weights and scales of every step
     uint4 wv[NL], sv[NL / 2];
     {
-        const uint4* pr = P + (size_t)lrow * G + gbase + j;
-        const uint4* sr = SC + ((size_t)lrow * G + gbase) / 8;
+        const uint4* pr = P + (size_t)lrow * Gld + goff + gbase + j;
+        const uint4* sr = SC + ((size_t)lrow * Gld + goff + gbase) / 8;
 #pragma unroll
         for (int s = 0; s < NL; s++) {
             wv[s] = ti_ld_nt(pr + 4 * s);
@@ -454,16 +470,47 @@ __global__ __launch_bounds__(64 * W) void k_tgemm(TgArgs a) {
     } else {
         const int w0 = (wave / KS) * KS;
         float* xn = L.xn + (wave / KS) * 256;            // this block's outputs [tok][16] (PART)
+        float vr[NE];
+#pragma unroll
+        for (int r = 0; r < NE; r++) {
+            const int e = (wave % KS) * 64 + lane + r * 64 * KS;
+            const int tok = e >> 4, mm = e & 15;
+            vr[r] = 0.0f;
+#pragma unroll
+            for (int k = 0; k < KS; k++) vr[r] += L.part[((w0 + k) * 16 + (tok < TG_TMAX ? tok : 0)) * 17 + mm];
+        }
+        if constexpr (SPLIT) {
+            // publish this half (device-scope stores), count the pair; the second to arrive
+            // adds the halves in order 0, 1 and stores, then resets the counter
+            int& s_second = *reinterpret_cast<int*>(L.inv);   // (the norm slots are unused here)
+            const size_t base = (size_t)bidx * 2 * 256;
+#pragma unroll
+            for (int r = 0; r < NE; r++) {
+                const int e = (wave % KS) * 64 + lane + r * 64 * KS;
+                if (e < 16 * T) ti_pub_store(a.sp + base + (size_t)part * 256 + e, vr[r]);
+            }
+            ti_stores_done();
+            __syncthreads();
+            if (tid == 0) s_second = ti_arrive(a.scnt + bidx) == 1u;
+            __syncthreads();
+            if (!s_second) return;
+#pragma unroll
+            for (int r = 0; r < NE; r++) {
+                const int e = (wave % KS) * 64 + lane + r * 64 * KS;
+                if (e < 16 * T) {
+                    const float o = ti_pub_load(a.sp + base + (size_t)(part ^ 1) * 256 + e);
+                    vr[r] = part == 0 ? vr[r] + o : o + vr[r];
+                }
+            }
+            if (tid == 0) __hip_atomic_store(a.scnt + bidx, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
 #pragma unroll
         for (int r = 0; r < NE; r++) {
             const int e = (wave % KS) * 64 + lane + r * 64 * KS;
             const int tok = e >> 4, mm = e & 15;
             const int lr = PART ? out_row(mm) : row0 - bs.base + mm;
             if (valid && tok < T && lr < bs.n) {
-                float v = 0.0f;
-#pragma unroll
-                for (int k = 0; k < KS; k++) v += L.part[((w0 + k) * 16 + tok) * 17 + mm];
-                const float yn = a.acc ? yold[r] + v : v;
+                const float yn = a.acc ? yold[r] + vr[r] : vr[r];
                 bs.y[(size_t)tok * bs.n + lr] = yn;
                 if (PART) xn[tok * 16 + mm] = yn;
             }
@@ -584,17 +631,17 @@ int tg_ku(int K) {   // k_tnorm_q8: K = 256*KU, KU in {1, 2, 4, 8, 16}
     return (ku == 1 || ku == 2 || ku == 4 || ku == 8 || ku == 16) ? ku : 0;
 }
 
-template <bool GU, int W, int KS, int NL, int IN, bool PART>
+template <bool GU, int W, int KS, int NL, int IN, bool PART, bool SPLIT = false>
 int tg_go(ti_ctx* c, const TgArgs& a, unsigned grid, const char* name) {
     const size_t lds = (size_t)tg_lds_words(a.T, a.K, W, PART ? W / KS : 0) * 4;
     static bool attr = false;
     if (!attr && lds > 65536) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_tgemm<GU, W, KS, NL, IN, PART>),
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_tgemm<GU, W, KS, NL, IN, PART, SPLIT>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         if (e != hipSuccess) return ti_hip_fail(e, "k_tgemm LDS attribute");
         attr = true;
     }
-    k_tgemm<GU, W, KS, NL, IN, PART><<<grid, 64 * W, lds, c->stream>>>(a);
+    k_tgemm<GU, W, KS, NL, IN, PART, SPLIT><<<grid, 64 * W, lds, c->stream>>>(a);
     TI_LAUNCHED(name);
     return TI_OK;
 }
@@ -683,6 +730,18 @@ int ti_tgemm_launch(ti_ctx* c, const TgIn& in, int nseg, const uint32_t* const* 
         if (nseg != 1 || !acc || !a.pku) return ti_fail(TI_ERR_INVALID, "T-token GEMM: partial sums need one residual segment, N = 256*{1,2,4,8,16}");
     }
     const int nb = (a.N + 15) / 16;
+    // K = 6144 residual projections (down at the 1.7B geometry) with at most 128 blocks
+    // fill only half the CUs with 16-row blocks: two workgroups per block, each on one
+    // half of K (12 waves, 96 groups), the second to finish adding the halves
+    if (!in.x && !pout && nseg == 1 && acc && K == 6144 && nb <= TI_TG_SPLIT_BLOCKS) {
+        a.K = K / 2;
+        a.S = a.K / 4 + 2;
+        a.kld = K;
+        a.sp = c->tg_part;
+        a.scnt = c->sync + TI_SYNC_TGEMM;
+        return tg_go<false, 12, 12, 2, TG_Q8, false, true>(c, a, (unsigned)(2 * nb), "k_tgemm");
+    }
+    a.kld = K;
     if (in.x) return tg_dispatch<TG_NORM, false>(c, a, nb, "k_tgemm");
     return pout ? tg_dispatch<TG_Q8, true>(c, a, nb, "k_tgemm") : tg_dispatch<TG_Q8, false>(c, a, nb, "k_tgemm");
 }

@@ -33,6 +33,7 @@ struct ti_ctx {
     uint32_t* moe_off;
     uint32_t* moe_fill;
     uint32_t* moe_sidx;
+    float* tg_part;       // split-K halves of the T-token projections ([TI_TG_SPLIT_BLOCKS][2][256])
     // device-scope counters of "last workgroup finishes the reduction" kernels;
     // zero between launches (each kernel's last workgroup resets its own)
     uint32_t* sync;
@@ -58,6 +59,8 @@ struct ti_graph {
 #define TI_SYNC_WORDS 512
 #define TI_SYNC_LMHEAD 0          // lm_head argmax
 #define TI_SYNC_ATTN 64           // fused attention: one counter per KV head (up to 64)
+#define TI_SYNC_TGEMM 128         // split-K T-token projections: one counter per 16-row block
+#define TI_TG_SPLIT_BLOCKS 128    // (blocks of one split-K launch, at most)
 #define TI_SYNC_DUMMY 256         // 256 words never written: a valid read target for unused inputs
 
 // ---- the T-token forward (2 <= T <= 16) ---------------------------------------------

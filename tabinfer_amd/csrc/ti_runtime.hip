@@ -40,7 +40,7 @@ extern "C" int ti_device_count(int* n) {
 
 static void free_scratch(ti_ctx* c) {
     void* ps[] = {c->act_q, c->act_s, c->act_sum, c->attn_po, c->attn_ml, c->amax_v, c->amax_i,
-                  c->moe_cnt, c->moe_off, c->moe_fill, c->moe_sidx, c->sync};
+                  c->moe_cnt, c->moe_off, c->moe_fill, c->moe_sidx, c->tg_part, c->sync};
     for (void* p : ps) if (p) (void)hipFree(p);
 }
 
@@ -78,6 +78,7 @@ extern "C" int ti_init(int device, ti_ctx** out) {
         {(void**)&c->moe_off, (size_t)(TI_MOE_E_MAX + 1) * 4},
         {(void**)&c->moe_fill, (size_t)TI_MOE_E_MAX * 4},
         {(void**)&c->moe_sidx, (size_t)TI_MOE_P_MAX * 4},
+        {(void**)&c->tg_part, (size_t)TI_TG_SPLIT_BLOCKS * 2 * 256 * 4},
         {(void**)&c->sync, (size_t)TI_SYNC_WORDS * 4},
     };
     for (auto& a : allocs) {

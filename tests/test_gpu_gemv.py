@@ -183,7 +183,8 @@ def test_linear_router(ctx, orc, T, N, K):
 
 
 @pytest.mark.parametrize("T,N,K", [(2, 2048, 2048), (8, 6144, 2048), (8, 2048, 6144), (16, 1024, 1024),
-                                   (17, 4096, 2048), (40, 96, 320), (8, 1000, 3072), (256, 256, 1024)])
+                                   (17, 4096, 2048), (40, 96, 320), (8, 1000, 3072), (256, 256, 1024),
+                                   (16, 2048, 6144), (3, 1000, 6144)])
 def test_gemm_mfma_batched_linear(ctx, orc, T, N, K):
     """linearQ at T > 1 (models/qwen3.js:1604-1607): per-token quantQ8T + the MFMA int4 x int8
     GEMM; max relative error 1e-3 against the f64 oracle of the quantized operands, with and
@@ -204,6 +205,10 @@ def test_gemm_mfma_batched_linear(ctx, orc, T, N, K):
     ctx.write(dy, y0)
     ctx.call("ti_linear_q4", dx, dp, ds, dy, T, N, K, 1)
     assert rel_err(ctx.download(dy, np.float32, T * N), ref + y0) < TOL
+    # again: the residual K = 6144 projections run as two K halves whose per-block
+    # counters the second half resets for the next launch
+    ctx.call("ti_linear_q4", dx, dp, ds, dy, T, N, K, 1)
+    assert rel_err(ctx.download(dy, np.float32, T * N), 2 * ref + y0) < TOL
 
 
 def test_shape_errors(ctx):
