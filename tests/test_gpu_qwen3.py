@@ -271,6 +271,43 @@ def test_batched_forward_two_row_tiles(ctx, T):
         b.close()
 
 
+@pytest.mark.parametrize("T", [4, 8])
+def test_batched_forward_graph_replays(ctx, T):
+    """The T-token forward captured in a HIP graph and replayed (the device-side counters of
+    the split-K down projection and of the attention merge reset themselves; for T = 4 the
+    norm partial sums flow between the projections): every replay, with eager work and a
+    synchronisation in between, gives the eager forward's logits and KV rows bit for bit."""
+    cfg = dict(layers=1, hidden=2048, intermediate=6144, n_heads=16, n_kv_heads=8, head_dim=128, vocab=1000,
+               rope_theta=1e6, rms_eps=1e-6, max_ctx=256, max_tokens=16)
+    W = Q.make_weights(cfg, 12)
+    m = abi.Qwen3(ctx, **cfg)
+    try:
+        Q.load_into(m, W)
+        pre = (np.arange(16, dtype=np.int32) * 29 + 5) % cfg["vocab"]
+        m.forward(pre, 0)
+        P = 16
+        ids = (np.arange(T, dtype=np.int32) * 131 + 7) % cfg["vocab"]
+        m.forward(ids, P)
+        l0 = _logits(ctx, m, cfg["vocab"]).copy()
+        nkv = cfg["n_kv_heads"] * cfg["head_dim"]
+        kq = m.kv(0)[0]
+        k0 = ctx.download(kq, np.uint32, (P + T) * nkv // 4).copy()
+        ctx.graph_begin()
+        m.forward(None, P, T=T)
+        g = ctx.graph_end()
+        try:
+            for rep in range(3):
+                ctx.graph_launch(g)
+                ctx.sync()
+                assert np.array_equal(_logits(ctx, m, cfg["vocab"]), l0), rep
+                assert np.array_equal(ctx.download(kq, np.uint32, (P + T) * nkv // 4), k0), rep
+                ctx.download(m.logits_ptr(), np.float32, 16)      # eager work between replays
+        finally:
+            ctx.graph_destroy(g)
+    finally:
+        m.close()
+
+
 def test_qwen3_06b_geometry_batch8_over_1k_prefix(ctx, orc):
     """The batch-8 forward at the Qwen3-0.6B geometry (hidden 1024, intermediate 3072,
     16/8 heads of 128: the K = 1024 / 2048 / 3072 projection kernels and the KU = 4 norm
