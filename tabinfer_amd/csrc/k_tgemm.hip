@@ -6,16 +6,20 @@
 // dispatch before the down projection. Here:
 //
 //   k_tnorm_q8  per-token RMSNorm + quantQ8T, one workgroup per token (shared by the
-//               q/k/v and gate/up projections of a layer)
+//               q/k/v and gate/up projections of a layer; T > 4)
 //   k_tgemm     the GEMM on int8 activations (the norm codes, the attention output's,
 //               SwiGLU's) over up to three matrices sharing them (q, k, v), with the
-//               residual (o_proj, down_proj), or
+//               residual (o_proj, down_proj; K = 6144 as two K halves per block), or
 //   gate/up     gate and up rows of one 32-row chunk in one workgroup, silu(g)*u and
 //               its per-token quantQ8 (32 rows = one scale group) in the epilogue: the
-//               down projection's int8 input, with no f32 round trip
+//               down projection's int8 input, with no f32 round trip.
+//   For T <= 4 the residual projections also write the RMSNorm's per-token partial sums
+//   (TG_NORM / PART below) and q/k/v and gate/up normalise and quantise x in their
+//   prologue from them: every workgroup then quantises all T x K elements, which costs
+//   less than the norm launch up to T = 4 and more beyond.
 //
-// (An earlier variant computed the RMSNorm in every GEMM workgroup's prologue: at T = 8
-// each workgroup then read the whole T x K f32 activation twice, 24-32 MB of L2 reads per
+// (A first variant computed the sum of squares in every GEMM prologue as well: at T = 8
+// each workgroup read the whole T x K f32 activation twice, 24-32 MB of L2 reads per
 // projection, and the q/k/v and gate/up kernels took 11 and 16 us against 4.8 + 4.5 and
 // 9.8 + 4.5 us for norm kernel + int8 GEMM.)
 //
@@ -301,8 +305,11 @@ __device__ __forceinline__ void tg_norm_stage(const TgArgs& a, const NormRegs<RX
     __syncthreads();
 }
 
-// rounds of the norm prologue: a lane covers 64 / (K / (8W)) tokens per round, K = 128 KS NL
-constexpr int tg_rx(int W, int KS, int NL) { return (TG_TMAX * 16 * KS * NL / W + 63) / 64 > 0 ? (TG_TMAX * 16 * KS * NL / W + 63) / 64 : 1; }
+// rounds of the norm prologue for 16 tokens: a round covers 64 / (K / (8W)) tokens, so
+// 16 tokens take K / (32 W) rounds (K = 128 KS NL), at least one
+constexpr int tg_rx(int W, int KS, int NL) {
+    return (4 * KS * NL + W - 1) / W > 0 ? (4 * KS * NL + W - 1) / W : 1;
+}
 
 // Segment of a 16-row block: selects on wave-uniform values (pointers stay scalar).
 struct TgBlk {
