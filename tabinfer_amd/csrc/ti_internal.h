@@ -56,10 +56,10 @@ struct ti_graph {
 #define TI_AMAX_PARTS 1024
 #define TI_MOE_P_MAX 8192
 #define TI_MOE_E_MAX 256
-#define TI_SYNC_WORDS 512
+#define TI_SYNC_WORDS 1024
 #define TI_SYNC_LMHEAD 0          // lm_head argmax
 #define TI_SYNC_ATTN 64           // fused attention: one counter per KV head (up to 64)
-#define TI_SYNC_TGEMM 128         // split-K T-token projections: one counter per 16-row block
+#define TI_SYNC_TGEMM 512         // split-K T-token projections: one counter per 16-row block
 #define TI_TG_SPLIT_BLOCKS 128    // (blocks of one split-K launch, at most)
 #define TI_SYNC_DUMMY 256         // 256 words never written: a valid read target for unused inputs
 
