@@ -1242,7 +1242,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_fused_mq8(AttnFArgs a) {
             int t = t0 + p * TPW + tp;
             t = t < lim ? t : lim - 1;
             const uint8_t* src = kqb + ((size_t)t * a.nKv + hk) * HD + 16 * (sl ^ tp);
-            __builtin_amdgcn_global_load_lds(src, ktw + buf * KT_BYTES + p * KT_PASS, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(src, ktw + buf * KT_BYTES + p * KT_PASS, 16, 0, 2);   // aux 2: nt, streamed like the weights
         }
 #pragma unroll
         for (int b = 0; b < 2; b++) {
