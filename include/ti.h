@@ -130,12 +130,15 @@ int ti_rmsnorm_gateup_silu_q4(ti_ctx* ctx, const float* x, const uint16_t* norm_
                               const uint32_t* gpack, const uint16_t* gsc, const uint32_t* upack,
                               const uint16_t* usc, float* swi, int I, int H, uint32_t* swi_q, float* swi_s);
 /* final rmsnorm + lm_head gemvQ + argmaxKernel (models/qwen3.js:4037-4055):
- * logits (may be NULL) = W . rmsnorm(x), tok_hist[out_pos] = argmax (lowest index on
- * ties). K <= 8192. */
+ * logits (may be NULL) = W . rmsnorm(x), tok_hist[out_pos] = argmax with argmaxKernel's
+ * tie order (below). K <= 8192. */
 int ti_rmsnorm_lm_head_argmax(ti_ctx* ctx, const float* x, const uint16_t* norm_w, float eps,
                               const uint32_t* pack, const uint16_t* scales, float* logits, int N, int K,
                               uint32_t* tok_hist, int out_pos);
-/* argmaxKernel (models/qwen3.js:2681-2690): tok_hist[out_pos] = argmax(logits[0..N)). */
+/* argmaxKernel (models/qwen3.js:2681-2690): tok_hist[out_pos] = argmax(logits[0..N)).
+ * Equal maxima resolve as the reference's trees resolve them: N < 16384 by its one
+ * 256-thread workgroup, larger N by its 64 x 256 two-stage pair (index 16394 beats 300).
+ * Only logits above -3e38 are candidates; with none the token is 0. */
 int ti_argmax(ti_ctx* ctx, const float* logits, int N, uint32_t* tok_hist, int out_pos);
 /* embedGather (models/qwen3.js:1663-1676): y[t] = f32(emb[ids[id_off+t]]), t < T. */
 int ti_embed(ti_ctx* ctx, const int32_t* ids, const uint16_t* emb, float* y, int T, int H, int id_off, int vocab);

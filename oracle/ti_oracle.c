@@ -414,16 +414,55 @@ void or_attn_causal_q8(const float* qr, const uint32_t* kq, const float* ks,
 
 /* ------------------------------------------------------------------------- */
 /* decode-step glue: embed gather (models/qwen3.js:1621-1633), argmax         */
-/* (models/qwen3.js:2624-2690; this oracle resolves ties to the lowest index) */
+/* (models/qwen3.js:2624-2690)                                                */
 /* ------------------------------------------------------------------------- */
 void or_embed(const int32_t* ids, const uint16_t* emb, int T, int H, float* y) {
     for (int t = 0; t < T; t++)
         for (int h = 0; h < H; h++) y[(size_t)t * H + h] = (float)or_f16_to_f32(emb[(size_t)ids[t] * H + h]);
 }
+
+/* The shared-memory tree of the argmax kernels over nthr per-thread (max, index) slots:
+ * for s = nthr/2 .. 1, slot l < s takes slot l+s only if strictly greater
+ * (models/qwen3.js:2642, 2664, 2677). Each thread's slot holds the first strict maximum
+ * of its strided scan, from (-3e38, 0) (:2640, 2662). */
+static void amx_tree(int nthr, float* sv, uint32_t* si) {
+    for (int s = nthr / 2; s > 0; s /= 2)
+        for (int l = 0; l < s; l++)
+            if (sv[l + s] > sv[l]) { sv[l] = sv[l + s]; si[l] = si[l + s]; }
+}
+
+/* argmaxKernel (models/qwen3.js:2681-2690): N < 16384 runs the one-workgroup kernel
+ * (256 threads striding by 256, :2626-2645); larger N the two-stage pair (64
+ * workgroups of 256 threads over interleaved slices striding by 64*256, then one
+ * 64-thread workgroup over the partials, :2651-2679). Evaluated literally, so ties
+ * resolve as the reference's trees resolve them (not to the lowest index). */
 int or_argmax(const float* logits, int N) {
-    int bi = 0; float bv = -3.0e38f;
-    for (int i = 0; i < N; i++) if (logits[i] > bv) { bv = logits[i]; bi = i; }
-    return bi;
+    enum { WG = 256, WGS = 64 };
+    float sv[WG];
+    uint32_t si[WG];
+    if (N < 16384) {
+        for (int t = 0; t < WG; t++) {
+            float bv = -3.0e38f; uint32_t bi = 0;
+            for (int i = t; i < N; i += WG) if (logits[i] > bv) { bv = logits[i]; bi = (uint32_t)i; }
+            sv[t] = bv; si[t] = bi;
+        }
+        amx_tree(WG, sv, si);
+        return (int)si[0];
+    }
+    float pv[WGS];
+    uint32_t pi[WGS];
+    for (int w = 0; w < WGS; w++) {
+        for (int t = 0; t < WG; t++) {
+            float bv = -3.0e38f; uint32_t bi = 0;
+            for (long i = (long)w * WG + t; i < N; i += (long)WGS * WG)
+                if (logits[i] > bv) { bv = logits[i]; bi = (uint32_t)i; }
+            sv[t] = bv; si[t] = bi;
+        }
+        amx_tree(WG, sv, si);
+        pv[w] = sv[0]; pi[w] = si[0];
+    }
+    amx_tree(WGS, pv, pi);
+    return (int)pi[0];
 }
 
 /* ------------------------------------------------------------------------- */

@@ -102,7 +102,7 @@ void or_attn_causal_q8(const float* qr, const uint32_t* kq, const float* ks,
 
 /* ---- decode-step glue ---------------------------------------------------- */
 void or_embed(const int32_t* ids, const uint16_t* emb_f16, int T, int H, float* y);
-int  or_argmax(const float* logits, int N);   /* lowest index wins ties */
+int  or_argmax(const float* logits, int N);   /* the reference's one/two-stage trees, their tie order */
 
 /* ---- ternary (native/crates/n2-kernels/src/tern.rs) --------------- */
 void or_tern_pack(const float* w, int N, int K, uint8_t* codes, float* scales); /* tern.rs:131-160 */

@@ -540,17 +540,13 @@ struct LmArgs {
     int rope_hd;
 };
 
-__device__ __forceinline__ void amx_take(float& v, int& i, float v2, int i2) {
-    if (v2 > v || (v2 == v && i2 < i)) { v = v2; i = i2; }
-}
-
-// argmax over the wave (value, then lowest index), left in every lane
-__device__ __forceinline__ void wave_argmax(float& v, int& i) {
+// argmax over the wave (value, then the reference's tie rank), left in every lane
+__device__ __forceinline__ void wave_argmax(float& v, int& i, int N) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
         const float v2 = ti_xor(v, o);
         const int i2 = ti_xor_i(i, o);
-        amx_take(v, i, v2, i2);
+        ti_amx_take(v, i, v2, i2, N);
     }
 }
 
@@ -651,7 +647,7 @@ __global__ __launch_bounds__(256) void k_lmhead(LmArgs a) {
             const long row = blk * (RPP * R) + sub + (long)(li / SPAN) * RPP;
             if ((li % SPAN) == 0 && row < a.N) {
                 if (a.logits) a.logits[row] = tot;
-                amx_take(best_v, best_i, tot, (int)row);
+                ti_amx_take(best_v, best_i, tot, (int)row, a.N);
             }
         };
         for (;;) {
@@ -667,8 +663,8 @@ __global__ __launch_bounds__(256) void k_lmhead(LmArgs a) {
             b = nb;
         }
     }
-    // workgroup argmax (lowest index wins ties): wave butterflies, then the 4 wave winners
-    wave_argmax(best_v, best_i);
+    // workgroup argmax (ties by the reference's rank): wave butterflies, then the 4 wave winners
+    wave_argmax(best_v, best_i, a.N);
     if (lane == 0) {
         bv_s[tid >> 6] = best_v;
         bi_s[tid >> 6] = best_i;
@@ -678,7 +674,7 @@ __global__ __launch_bounds__(256) void k_lmhead(LmArgs a) {
         float v = bv_s[0];
         int i = bi_s[0];
 #pragma unroll
-        for (int w = 1; w < 4; w++) amx_take(v, i, bv_s[w], bi_s[w]);
+        for (int w = 1; w < 4; w++) ti_amx_take(v, i, bv_s[w], bi_s[w], a.N);
         ti_pub_store(a.part_v + blockIdx.x, v);
         ti_pub_store(a.part_i + blockIdx.x, (uint32_t)i);
         ti_stores_done();
@@ -688,8 +684,8 @@ __global__ __launch_bounds__(256) void k_lmhead(LmArgs a) {
     if (!last_s) return;
     float v = -3.0e38f;
     int i = 0x7fffffff;
-    for (int p = tid; p < (int)gridDim.x; p += 256) amx_take(v, i, ti_pub_load(a.part_v + p), (int)ti_pub_load(a.part_i + p));
-    wave_argmax(v, i);
+    for (int p = tid; p < (int)gridDim.x; p += 256) ti_amx_take(v, i, ti_pub_load(a.part_v + p), (int)ti_pub_load(a.part_i + p), a.N);
+    wave_argmax(v, i, a.N);
     __syncthreads();   // every thread has read last_s / the first-stage winners
     if (lane == 0) {
         bv_s[tid >> 6] = v;
@@ -700,11 +696,11 @@ __global__ __launch_bounds__(256) void k_lmhead(LmArgs a) {
         float vv = bv_s[0];
         int ii = bi_s[0];
 #pragma unroll
-        for (int w = 1; w < 4; w++) amx_take(vv, ii, bv_s[w], bi_s[w]);
+        for (int w = 1; w < 4; w++) ti_amx_take(vv, ii, bv_s[w], bi_s[w], a.N);
         const int pos = a.dpos ? *a.dpos : a.out_pos - 1;
         last_s = -1;
         if (pos >= 0 && pos < a.cap) {
-            a.hist[pos + 1] = (uint32_t)ii;
+            a.hist[pos + 1] = (uint32_t)ti_amx_result(vv, ii);
             if (a.dpos) *a.dpos = pos + 1;
             last_s = pos + 1;
         }

@@ -202,6 +202,34 @@ __device__ __forceinline__ uint32_t snorm_code(float x, float mx) {
     return (uint32_t)((int)floor(0.5 + 127.0 * (double)e) & 0xff);
 }
 
+// ---- argmax tie order of the reference (models/qwen3.js:2624-2690) ----------------------
+// The reference's argmax keeps, per thread, the first strict maximum of a strided scan and
+// then folds the threads' slots in a shared-memory tree where slot l takes slot l+s only if
+// strictly greater (s = n/2 .. 1). Among equal maxima that tree favours the slot whose
+// number, read with its bits reversed, is smallest (slot 0 beats 1 at the last level, 0
+// beats 2 one level up, ...). Index i of an N-logit argmax therefore ranks as
+//   N >= 16384 (64 workgroups x 256 threads, then 64 partials):
+//       (bitrev6(workgroup (i >> 8) & 63), bitrev8(thread i & 255), i >> 14)
+//   N <  16384 (one workgroup of 256 threads): (bitrev8(thread i & 255), i >> 8)
+// and the smaller rank wins a tie. Only logits above -3e38 are candidates (NaN never is);
+// with none the answer is index 0. Merging (value, index) pairs with ti_amx_take is
+// associative and commutative, so any reduction order gives the reference's index.
+__device__ __forceinline__ uint32_t ti_amx_rank(uint32_t i, int N) {
+    if (N >= 16384)
+        return ((__builtin_bitreverse32((i >> 8) & 63u) >> 26) << 26) | ((__builtin_bitreverse32(i & 255u) >> 24) << 18) |
+               (i >> 14);
+    return ((__builtin_bitreverse32(i & 255u) >> 24) << 6) | (i >> 8);
+}
+// keep (v, i) or take (v2, i2); start from (-3e38, any index)
+__device__ __forceinline__ void ti_amx_take(float& v, int& i, float v2, int i2, int N) {
+    if (v2 > v || (v2 == v && v > -3.0e38f && ti_amx_rank((uint32_t)i2, N) < ti_amx_rank((uint32_t)i, N))) {
+        v = v2;
+        i = i2;
+    }
+}
+// the answer of a finished reduction
+__device__ __forceinline__ int ti_amx_result(float v, int i) { return v > -3.0e38f ? i : 0; }
+
 // ---- cross-workgroup hand-off without cache maintenance ----------------------------
 // The "last workgroup finishes the reduction" kernels publish a few words per
 // workgroup. A device-scope fence on gfx950 writes back and invalidates the whole

@@ -51,12 +51,22 @@ __global__ void k_embed(const uint32_t* __restrict__ ids, const uint16_t* __rest
     y[i] = ti_h2f(emb[(size_t)id * H + h]);
 }
 
-// two-stage argmax (models/qwen3.js:2624-2690); ties resolve to the lowest index
+// two-stage argmax (models/qwen3.js:2624-2690): 256 workgroups fold interleaved slices,
+// one workgroup folds their partials; ties resolve by the reference's rank (ti_amx_take)
 constexpr int AMX_THREADS = 256;
 constexpr int AMX_PARTS = 256;
 
-__device__ __forceinline__ void amx_merge(float& v, int& i, float v2, int i2) {
-    if (v2 > v || (v2 == v && i2 < i)) { v = v2; i = i2; }
+__device__ __forceinline__ void amx_fold_lds(float* sv, int* si, int n, int N) {
+    for (int s = n / 2; s > 0; s >>= 1) {
+        if ((int)threadIdx.x < s) {
+            float v = sv[threadIdx.x];
+            int i = si[threadIdx.x];
+            ti_amx_take(v, i, sv[threadIdx.x + s], si[threadIdx.x + s], N);
+            sv[threadIdx.x] = v;
+            si[threadIdx.x] = i;
+        }
+        __syncthreads();
+    }
 }
 
 __global__ __launch_bounds__(AMX_THREADS) void k_argmax_p1(const float* __restrict__ logits, int N, float* __restrict__ pv,
@@ -64,26 +74,17 @@ __global__ __launch_bounds__(AMX_THREADS) void k_argmax_p1(const float* __restri
     __shared__ float sv[AMX_THREADS];
     __shared__ int si[AMX_THREADS];
     float bv = -3.0e38f;
-    int bi = 0x7fffffff;
-    for (int i = blockIdx.x * AMX_THREADS + threadIdx.x; i < N; i += AMX_PARTS * AMX_THREADS) amx_merge(bv, bi, logits[i], i);
+    int bi = 0;
+    for (int i = blockIdx.x * AMX_THREADS + threadIdx.x; i < N; i += AMX_PARTS * AMX_THREADS) ti_amx_take(bv, bi, logits[i], i, N);
     sv[threadIdx.x] = bv;
     si[threadIdx.x] = bi;
     __syncthreads();
-    for (int s = AMX_THREADS / 2; s > 0; s >>= 1) {
-        if (threadIdx.x < s) {
-            float v = sv[threadIdx.x];
-            int i = si[threadIdx.x];
-            amx_merge(v, i, sv[threadIdx.x + s], si[threadIdx.x + s]);
-            sv[threadIdx.x] = v;
-            si[threadIdx.x] = i;
-        }
-        __syncthreads();
-    }
+    amx_fold_lds(sv, si, AMX_THREADS, N);
     if (threadIdx.x == 0) { pv[blockIdx.x] = sv[0]; pi[blockIdx.x] = (uint32_t)si[0]; }
 }
 
 // writes the token to hist[out_pos] (device position: hist[*dpos + 1], then *dpos += 1)
-__global__ __launch_bounds__(AMX_PARTS) void k_argmax_p2(const float* __restrict__ pv, const uint32_t* __restrict__ pi,
+__global__ __launch_bounds__(AMX_PARTS) void k_argmax_p2(const float* __restrict__ pv, const uint32_t* __restrict__ pi, int N,
                                                          uint32_t* __restrict__ hist, int out_pos, int* __restrict__ dpos,
                                                          int advance) {
     __shared__ float sv[AMX_PARTS];
@@ -91,19 +92,10 @@ __global__ __launch_bounds__(AMX_PARTS) void k_argmax_p2(const float* __restrict
     sv[threadIdx.x] = pv[threadIdx.x];
     si[threadIdx.x] = (int)pi[threadIdx.x];
     __syncthreads();
-    for (int s = AMX_PARTS / 2; s > 0; s >>= 1) {
-        if (threadIdx.x < s) {
-            float v = sv[threadIdx.x];
-            int i = si[threadIdx.x];
-            amx_merge(v, i, sv[threadIdx.x + s], si[threadIdx.x + s]);
-            sv[threadIdx.x] = v;
-            si[threadIdx.x] = i;
-        }
-        __syncthreads();
-    }
+    amx_fold_lds(sv, si, AMX_PARTS, N);
     if (threadIdx.x == 0) {
         int p = dpos ? *dpos + 1 : out_pos;
-        hist[p] = (uint32_t)si[0];
+        hist[p] = (uint32_t)ti_amx_result(sv[0], si[0]);
         if (dpos && advance) *dpos = p;
     }
 }
@@ -349,7 +341,7 @@ extern "C" int ti_qwen3_read_tokens(ti_ctx* c, ti_qwen3* m, int from, int count,
 }
 
 // argmaxKernel (models/qwen3.js:2681-2690): tok_hist[out_pos] = argmax(logits[0..N)),
-// lowest index on ties, two stages.
+// ties resolved as the reference's one-stage (N < 16384) or two-stage trees resolve them.
 extern "C" int ti_argmax(ti_ctx* c, const float* logits, int N, uint32_t* tok_hist, int out_pos) {
     TI_CHECK_CTX(c);
     TI_REQUIRE(logits && tok_hist, "ti_argmax: null buffer");
@@ -357,7 +349,7 @@ extern "C" int ti_argmax(ti_ctx* c, const float* logits, int N, uint32_t* tok_hi
     TI_REQUIRE(AMX_PARTS <= TI_AMAX_PARTS, "ti_argmax: partial buffer too small");
     k_argmax_p1<<<AMX_PARTS, AMX_THREADS, 0, c->stream>>>(logits, N, c->amax_v, c->amax_i);
     TI_LAUNCHED("k_argmax_p1");
-    k_argmax_p2<<<1, AMX_PARTS, 0, c->stream>>>(c->amax_v, c->amax_i, tok_hist, out_pos, nullptr, 0);
+    k_argmax_p2<<<1, AMX_PARTS, 0, c->stream>>>(c->amax_v, c->amax_i, N, tok_hist, out_pos, nullptr, 0);
     TI_LAUNCHED("k_argmax_p2");
     return TI_OK;
 }

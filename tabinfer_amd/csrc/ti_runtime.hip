@@ -38,10 +38,15 @@ extern "C" int ti_device_count(int* n) {
     return TI_OK;
 }
 
-static void free_scratch(ti_ctx* c) {
+// Releases everything a (possibly partly built) context holds: scratch, the 64 events,
+// the stream, the host struct. Used by ti_shutdown and by every ti_init error path.
+static void destroy_ctx(ti_ctx* c) {
     void* ps[] = {c->act_q, c->act_s, c->act_sum, c->attn_po, c->attn_ml, c->amax_v, c->amax_i,
                   c->moe_cnt, c->moe_off, c->moe_fill, c->moe_sidx, c->tg_part, c->sync};
     for (void* p : ps) if (p) (void)hipFree(p);
+    for (int i = 0; i < 64; i++) if (c->ev[i]) (void)hipEventDestroy(c->ev[i]);
+    if (c->stream) (void)hipStreamDestroy(c->stream);
+    free(c);
 }
 
 extern "C" int ti_init(int device, ti_ctx** out) {
@@ -61,10 +66,10 @@ extern "C" int ti_init(int device, ti_ctx** out) {
     if (!c) return ti_fail(TI_ERR_OOM, "ti_init: host allocation failed");
     c->device = device;
     hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
-    if (e != hipSuccess) { free(c); return ti_hip_fail(e, "hipStreamCreateWithFlags"); }
+    if (e != hipSuccess) { c->stream = nullptr; destroy_ctx(c); return ti_hip_fail(e, "hipStreamCreateWithFlags"); }
     for (int i = 0; i < 64; i++) {
         e = hipEventCreate(&c->ev[i]);
-        if (e != hipSuccess) { for (int j = 0; j < i; j++) (void)hipEventDestroy(c->ev[j]); (void)hipStreamDestroy(c->stream); free(c); return ti_hip_fail(e, "hipEventCreate"); }
+        if (e != hipSuccess) { c->ev[i] = nullptr; destroy_ctx(c); return ti_hip_fail(e, "hipEventCreate"); }
     }
     struct { void** p; size_t bytes; } allocs[] = {
         {(void**)&c->act_q, (size_t)TI_ACT_CAP * TI_ACT_TMAX},
@@ -83,18 +88,12 @@ extern "C" int ti_init(int device, ti_ctx** out) {
     };
     for (auto& a : allocs) {
         e = hipMalloc(a.p, a.bytes);
-        if (e != hipSuccess) {
-            free_scratch(c);
-            for (int j = 0; j < 64; j++) (void)hipEventDestroy(c->ev[j]);
-            (void)hipStreamDestroy(c->stream);
-            free(c);
-            return ti_hip_fail(e, "ti_init scratch hipMalloc");
-        }
+        if (e != hipSuccess) { destroy_ctx(c); return ti_hip_fail(e, "ti_init scratch hipMalloc"); }
     }
     e = hipMemset(c->moe_cnt, 0, TI_MOE_E_MAX * 4);
     if (e == hipSuccess) e = hipMemset(c->sync, 0, TI_SYNC_WORDS * 4);
     if (e == hipSuccess) e = hipDeviceSynchronize();
-    if (e != hipSuccess) { free_scratch(c); free(c); return ti_hip_fail(e, "ti_init scratch clear"); }
+    if (e != hipSuccess) { destroy_ctx(c); return ti_hip_fail(e, "ti_init scratch clear"); }
     *out = c;
     return TI_OK;
 }
@@ -103,10 +102,7 @@ extern "C" int ti_shutdown(ti_ctx* c) {
     TI_CHECK_CTX(c);
     TI_HIP(hipSetDevice(c->device));
     (void)hipStreamSynchronize(c->stream);
-    free_scratch(c);
-    for (int i = 0; i < 64; i++) (void)hipEventDestroy(c->ev[i]);
-    (void)hipStreamDestroy(c->stream);
-    free(c);
+    destroy_ctx(c);
     return TI_OK;
 }
 

@@ -348,12 +348,15 @@ function createQwen3Host({ device = 0 } = {}) {
     checkFits(L);
     let lcp = 0;
     if (_cachedIds) { const n = Math.min(_cachedIds.length, L - 1); while (lcp < n && _cachedIds[lcp] === ids[lcp]) lcp++; }
+    _cachedIds = null;   // from here on rows lcp.. are being overwritten
     const tok0 = await prefill(ids, lcp, signal);
-    _cachedIds = ids.slice();
     const out = [];
-    const emitTok = (t) => { if (isStop(t)) return false; out.push(t); _cachedIds.push(t); if (onToken) onToken(TOK ? TOK.decode([t]) : String(t)); return true; };
+    const emitTok = (t) => { if (isStop(t)) return false; out.push(t); if (onToken) onToken(TOK ? TOK.decode([t]) : String(t)); return true; };
     if (emitTok(tok0)) await decodeLoop(L, maxTokens, emitTok, signal, () => out.length);
-    _cachedIds = _cachedIds.slice(0, L + out.length);   // KV rows beyond this were written by discarded steps
+    // Rows [0, L) hold the prompt. The step at position L + j wrote the row of out[j] and
+    // produced out[j + 1], so rows exist for out[0 .. n-2]; the last emitted token's row
+    // is written only if a later step ran, which a stop at maxTokens or the cache end skips.
+    _cachedIds = ids.concat(out.slice(0, Math.max(0, out.length - 1)));
     return out;
   }
 

@@ -50,25 +50,38 @@ void ctx_unref(CtxH* h) {
     }
 }
 
+struct ModelH {
+    uint32_t tag = TAG_MODEL;
+    CtxH* ctx = nullptr;
+    ti_qwen3* m = nullptr;     // null once destroyed
+    ti_qwen3_config cfg;       // sizes of the views it hands out
+};
+
+// A device buffer, or a view into another buffer or into a model's storage. A view holds
+// a reference to its parent's JS object (so the parent's handle outlives it) and checks
+// the parent is still live on every use: buf_free of the parent or qwen3_destroy of the
+// model turns its views dead instead of leaving them pointing into freed memory.
 struct BufH {
     uint32_t tag = TAG_BUF;
     CtxH* ctx = nullptr;
-    char* ptr = nullptr;
-    size_t bytes = 0;      // 0 = size not known (views into a model's storage)
-    bool owned = false;    // freed with ti_buf_free when collected
-    napi_ref parent = nullptr;   // views keep their parent object alive
+    char* ptr = nullptr;       // null once freed
+    size_t bytes = 0;
+    bool owned = false;        // freed with ti_buf_free when collected
+    napi_ref parent = nullptr; // the parent object (buffer or model), kept alive
+    BufH* pbuf = nullptr;      // the parent's handle when it is a buffer
+    ModelH* pmodel = nullptr;  // ... when it is a model
 };
+
+bool buf_live(const BufH* b) {
+    for (; b; b = b->pbuf)
+        if (!b->ptr || (b->pmodel && !b->pmodel->m)) return false;
+    return true;
+}
 
 struct GraphH {
     uint32_t tag = TAG_GRAPH;
     CtxH* ctx = nullptr;
     ti_graph* g = nullptr;
-};
-
-struct ModelH {
-    uint32_t tag = TAG_MODEL;
-    CtxH* ctx = nullptr;
-    ti_qwen3* m = nullptr;
 };
 
 // ---- error helpers ----------------------------------------------------------------------
@@ -164,7 +177,11 @@ napi_value make_buf(napi_env env, CtxH* ctx, void* ptr, size_t bytes, bool owned
     b->ptr = static_cast<char*>(ptr);
     b->bytes = bytes;
     b->owned = owned;
-    if (parent) napi_create_reference(env, parent, 1, &b->parent);
+    if (parent) {
+        napi_create_reference(env, parent, 1, &b->parent);
+        b->pbuf = handle_of<BufH>(env, parent, TAG_BUF);
+        b->pmodel = handle_of<ModelH>(env, parent, TAG_MODEL);
+    }
     napi_value out;
     napi_create_external(env, b, fin_buf, nullptr, &out);
     return out;
@@ -183,7 +200,7 @@ bool get_dptr(napi_env env, napi_value v, void** out, const char* fn, size_t i) 
     if (is_nullish(env, v)) { *out = nullptr; return true; }
     BufH* b = handle_of<BufH>(env, v, TAG_BUF);
     if (!b) return arg_error(env, fn, i, "a device buffer or null");
-    if (!b->ptr) return arg_error(env, fn, i, "a live device buffer (this one was freed)");
+    if (!buf_live(b)) return arg_error(env, fn, i, "a live device buffer (this one, or the buffer or model it views, was freed)");
     *out = b->ptr;
     return true;
 }
@@ -354,14 +371,14 @@ napi_value js_buf_view(napi_env env, napi_callback_info info) {
     Args a(env, info);
     if (a.n < 2 || a.n > 3) return throw_msg(env, "buf_view expects (buffer, byteOffset[, bytes])");
     BufH* b = handle_of<BufH>(env, a.v[0], TAG_BUF);
-    if (!b || !b->ptr) return arg_error(env, "buf_view", 0, "a live device buffer"), nullptr;
+    if (!b || !buf_live(b)) return arg_error(env, "buf_view", 0, "a live device buffer"), nullptr;
     int64_t off, len = -1;
     if (!get_i64(env, a.v[1], &off, "buf_view", 1)) return nullptr;
     if (a.n == 3 && !get_i64(env, a.v[2], &len, "buf_view", 2)) return nullptr;
-    if (off < 0 || (b->bytes && (size_t)off > b->bytes)) return throw_msg(env, "buf_view: offset outside the buffer");
-    size_t rest = b->bytes ? b->bytes - (size_t)off : 0;
+    if (off < 0 || (size_t)off > b->bytes) return throw_msg(env, "buf_view: offset outside the buffer");
+    size_t rest = b->bytes - (size_t)off;
     if (len >= 0) {
-        if (b->bytes && (size_t)len > rest) return throw_msg(env, "buf_view: view extends past the buffer");
+        if ((size_t)len > rest) return throw_msg(env, "buf_view: view extends past the buffer");
         rest = (size_t)len;
     }
     return make_buf(env, b->ctx, b->ptr + off, rest, false, a.v[0]);
@@ -421,7 +438,7 @@ napi_value js_buf_write(napi_env env, napi_callback_info info) {
         !host_bytes(env, a.v[3], &src, &len, "buf_write", 3))
         return nullptr;
     BufH* b = handle_of<BufH>(env, a.v[1], TAG_BUF);
-    if (!dst || off < 0 || (b->bytes && (size_t)off + len > b->bytes)) return throw_msg(env, "buf_write: outside the buffer");
+    if (!dst || off < 0 || (size_t)off > b->bytes || len > b->bytes - (size_t)off) return throw_msg(env, "buf_write: outside the buffer");
     const int rc = ti_buf_write(c->c, dst, (size_t)off, src, len);
     return rc ? throw_ti(env, "buf_write", rc) : undefined(env);
 }
@@ -437,7 +454,8 @@ napi_value js_buf_read(napi_env env, napi_callback_info info) {
         !get_i64(env, a.v[3], &len, "buf_read", 3))
         return nullptr;
     BufH* b = handle_of<BufH>(env, a.v[1], TAG_BUF);
-    if (!src || off < 0 || len < 0 || (b->bytes && (size_t)(off + len) > b->bytes)) return throw_msg(env, "buf_read: outside the buffer");
+    if (!src || off < 0 || len < 0 || (size_t)off > b->bytes || (size_t)len > b->bytes - (size_t)off)
+        return throw_msg(env, "buf_read: outside the buffer");
     void* data;
     napi_value ab;
     napi_create_arraybuffer(env, (size_t)len, &data, &ab);
@@ -684,6 +702,7 @@ napi_value js_qwen3_create(napi_env env, napi_callback_info info) {
     h->ctx = c;
     c->refs++;
     h->m = m;
+    h->cfg = cfg;
     napi_value out;
     napi_create_external(env, h, fin_model, nullptr, &out);
     return out;
@@ -741,10 +760,11 @@ napi_value js_qwen3_kv(napi_env env, napi_callback_info info) {
     if (rc) return throw_ti(env, "qwen3_kv", rc);
     napi_value o;
     napi_create_object(env, &o);
-    napi_set_named_property(env, o, "kq", make_buf(env, m->ctx, kq, 0, false, a.v[0]));
-    napi_set_named_property(env, o, "ks", make_buf(env, m->ctx, ks, 0, false, a.v[0]));
-    napi_set_named_property(env, o, "vq", make_buf(env, m->ctx, vq, 0, false, a.v[0]));
-    napi_set_named_property(env, o, "vs", make_buf(env, m->ctx, vs, 0, false, a.v[0]));
+    const size_t codes = (size_t)m->cfg.max_ctx * m->cfg.n_kv_heads * m->cfg.head_dim;   // int8 per K or V
+    napi_set_named_property(env, o, "kq", make_buf(env, m->ctx, kq, codes, false, a.v[0]));
+    napi_set_named_property(env, o, "ks", make_buf(env, m->ctx, ks, codes / 32 * 4, false, a.v[0]));
+    napi_set_named_property(env, o, "vq", make_buf(env, m->ctx, vq, codes, false, a.v[0]));
+    napi_set_named_property(env, o, "vs", make_buf(env, m->ctx, vs, codes / 32 * 4, false, a.v[0]));
     return o;
 }
 
@@ -754,7 +774,7 @@ napi_value js_qwen3_logits(napi_env env, napi_callback_info info) {
     if (!m) return a.n == 1 ? nullptr : throw_msg(env, "qwen3_logits expects (model)");
     float* l = nullptr;
     const int rc = ti_qwen3_logits(m->m, &l);
-    return rc ? throw_ti(env, "qwen3_logits", rc) : make_buf(env, m->ctx, l, 0, false, a.v[0]);
+    return rc ? throw_ti(env, "qwen3_logits", rc) : make_buf(env, m->ctx, l, (size_t)m->cfg.vocab * 4, false, a.v[0]);
 }
 
 bool host_i32(napi_env env, napi_value v, const int32_t** data, size_t* n, const char* fn, size_t i) {

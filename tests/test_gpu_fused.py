@@ -128,6 +128,36 @@ def test_rmsnorm_gateup(ctx, orc, I, H):
         assert np.array_equal(ctx.download(sq2, np.uint32, I // 4), oq)
 
 
+@pytest.mark.parametrize("N,K,tied", [(151936, 1024, (300, 16394)), (151936, 2048, (98765, 98766)),
+                                      (1000, 256, (64, 128)), (1000, 256, (5, 261))])
+def test_lm_head_argmax_ties(ctx, orc, N, K, tied):
+    """The fused lm_head's argmax resolves equal logits as argmaxKernel does. The tied rows
+    share one packed row with a single non-zero 32-group of large codes (every other group
+    has code 8, i.e. 0): their logits are the same exact sum of one group's dot, so they
+    are equal bit for bit whatever the reduction order."""
+    rng = np.random.default_rng(K + tied[0])
+    x = (rng.standard_normal(K) * 2).astype(np.float32)
+    nw = (1 + 0.1 * rng.standard_normal(K)).astype(np.float16).view(np.uint16)
+    eps = np.float32(1e-6)
+    pack, sc, _, _ = quantized(ctx, orc, rng, N, K)
+    pack, sc = pack.reshape(N, K // 8).copy(), sc.reshape(N, K // 32).copy()
+    row = np.full(K // 8, 0x88888888, np.uint32)
+    normed = orc.rmsnorm(x, nw, 1, K, eps)
+    g = int(np.argmax(np.abs(normed[:K - K % 32].reshape(-1, 32)).sum(axis=1)))
+    signs = np.where(normed[32 * g:32 * g + 32] >= 0, 15, 1)            # q = +7 / -7 along the sign of x
+    for w in range(4):
+        row[4 * g + w] = sum(int(signs[8 * w + e]) << (4 * e) for e in range(8))
+    for r in tied:
+        pack[r], sc[r] = row, np.float16(0.5).view(np.uint16)
+    pack, sc = pack.ravel(), sc.ravel()
+    dp, ds = ctx.upload(pack), ctx.upload(sc)
+    dl, hist = ctx.zeros(N * 4), ctx.zeros(16 * 4)
+    ctx.call("ti_rmsnorm_lm_head_argmax", ctx.upload(x), ctx.upload(nw), eps, dp, ds, dl, N, K, hist, 5)
+    got = ctx.download(dl, np.float32, N)
+    assert got[tied[0]] == got[tied[1]] and got[tied[0]] == got.max()
+    assert int(ctx.download(hist, np.uint32, 16)[5]) == orc.argmax(got)
+
+
 @pytest.mark.parametrize("N,K", [(151936, 1024), (151936, 2048), (1000, 256)])
 def test_lm_head_argmax(ctx, orc, N, K):
     rng = np.random.default_rng(N + K)
@@ -152,15 +182,35 @@ def test_lm_head_argmax(ctx, orc, N, K):
     assert int(ctx.download(hist, np.uint32, 16)[6]) == tok
 
 
-def test_argmax_and_embed(ctx, orc):
+def _tie_cases(rng):
+    """(N, logits, expected index) for argmax: the reference's tie order across workgroups,
+    threads and one thread's scan, heavy ties, and the values never selected."""
+    cases = []
+    for N, idx, want in [(151936, (300, 16394), 16394), (151936, (98765, 98766), 98766), (151936, (256, 512), 512),
+                         (151936, (16384, 0), 0), (1000, (64, 128), 128), (1000, (5, 261), 5), (16384, (16383, 256), 256)]:
+        x = rng.standard_normal(N).astype(np.float32)
+        x[list(idx)] = 50.0                               # models/qwen3.js:3171-3180 known answer, tied
+        cases.append((N, x, want))
+    for N in (151936, 1000):
+        x = rng.integers(-3, 4, N).astype(np.float32)
+        cases.append((N, x, None))
+    cases.append((151936, np.full(151936, -np.inf, np.float32), 0))
+    x = np.full(1000, np.nan, np.float32)
+    x[7] = -3.0e38
+    x[9] = 1.0
+    cases.append((1000, x, 9))
+    return cases
+
+
+def test_argmax_tie_order_and_embed(ctx, orc):
     rng = np.random.default_rng(9)
-    N = 151936
-    logits = rng.standard_normal(N).astype(np.float32)
-    logits[98765] = 50.0                                  # models/qwen3.js:3171-3180 known answer
-    logits[98766] = 50.0                                  # a tie: the lowest index wins
     hist = ctx.zeros(8 * 4)
-    ctx.call("ti_argmax", ctx.upload(logits), N, hist, 3)
-    assert int(ctx.download(hist, np.uint32, 8)[3]) == 98765
+    for N, logits, want in _tie_cases(rng):
+        ref = orc.argmax(logits)
+        if want is not None:
+            assert ref == want, (N, want)
+        ctx.call("ti_argmax", ctx.upload(logits), N, hist, 3)
+        assert int(ctx.download(hist, np.uint32, 8)[3]) == ref, (N, ref)
     V, H = 100, 64
     emb = rng.standard_normal(V * H).astype(np.float16)
     ids = np.array([5, 0, 99, 1234], np.int32)               # the last id is past the vocabulary
