@@ -158,6 +158,18 @@ int ti_attn_prep_q8(ti_ctx* ctx, const float* q, const float* k, const float* v,
 int ti_attn_decode_q8(ti_ctx* ctx, const float* qr, const uint32_t* kq, const float* ks,
                       const uint32_t* vq, const float* vs, float* out,
                       int S, int nHq, int nKv, int hd, int nsplit);
+/* ti_attn_decode_q8 without a context, for callers that cannot allocate device memory
+ * (code under graph capture, tight serving loops, harnesses that forbid hipMalloc). It has
+ * no counterpart in the reference. It allocates nothing: the split partials live in a
+ * file-scope device array of the library (2.03 MiB, held by every device the call runs on
+ * until the process ends), so nHq * splits <= 4096 (splits as ti_attn_decode_q8 picks
+ * them for nsplit = 0; at most 512); larger calls fail with TI_ERR_INVALID. `stream` is a
+ * hipStream_t (NULL: the null stream); the call is ordered on it and does not block. All
+ * calls on one device share the array, so calls whose execution overlaps on one device
+ * (two streams, two threads) race; calls ordered on one stream do not. */
+int ti_attn_decode_q8_noalloc(void* stream, const float* qr, const uint32_t* kq, const float* ks,
+                              const uint32_t* vq, const float* vs, float* out,
+                              int S, int nHq, int nKv, int hd, int nsplit);
 /* attnPrepQ8 + attnDecodeStreamQ8 + combine as one launch (models/qwen3.js:4001-4002) for
  * one token at `pos` (< cap, the cache capacity in positions): q/k/v are the token's
  * projections [nHq*hd], [nKv*hd], [nKv*hd]; k and v are written into cache row pos;

@@ -63,6 +63,7 @@ SIGS = {
     "ti_attn_step_q8": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _f, _f, _i, _p, _p],
     "ti_attn_prep_q8": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _f, _f],
     "ti_attn_decode_q8": [_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i],
+    "ti_attn_decode_q8_noalloc": [_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i],
     "ti_rope_qk": [_p, _p, _p, _p, _i, _i, _i, _i, _f, _f],
     "ti_kv_write_q8": [_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i],
     "ti_tern_gemv": [_p, _p, _p, _p, _p, _p, _i, _i],

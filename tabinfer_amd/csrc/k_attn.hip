@@ -10,6 +10,7 @@
 // 32 dims.
 #include "ti_internal.h"
 #include <math.h>
+#include <mutex>
 
 // Quantize 32 values held by one thread into 8 words + a scale.
 __device__ __forceinline__ void snorm_group(const float* v, uint32_t* q, float* s) {
@@ -612,6 +613,27 @@ static int auto_nsplit(int S, int nKv) {
     return ns;
 }
 
+// The per-split kernel and the log-sum-exp combine on stream `st`, the partials in
+// po[T*nHq*ns_stride*hd] and ml[T*nHq*ns_stride*2] (every slot below nsplit is written
+// before it is read, so nothing in them needs clearing).
+static int split_combine(hipStream_t st, float* po, float* ml, const float* qr, const uint32_t* kq, const float* ks,
+                         const uint32_t* vq, const float* vs, float* out, int S, int T, int nHq, int nKv, int hd,
+                         int nsplit, int per, int ns_stride, const int* dpos) {
+    const int G = nHq / nKv;
+    dim3 grid(nKv * nsplit, T);
+    const uint4* k4 = reinterpret_cast<const uint4*>(kq);
+    const uint4* v4 = reinterpret_cast<const uint4*>(vq);
+#define ATT(HD_, G_) \
+    if (hd == HD_ && G == G_) { k_attn_split_q8<HD_, G_><<<grid, ATT_THREADS, 0, st>>>(qr, k4, ks, v4, vs, po, ml, S, nKv, nsplit, per, ns_stride, dpos); }
+    ATT(128, 1) else ATT(128, 2) else ATT(128, 4) else ATT(64, 1) else ATT(64, 2) else ATT(32, 2)
+    else return ti_fail(TI_ERR_INVALID, "ti_attn_decode_q8: unsupported hd=%d / group=%d", hd, G);
+#undef ATT
+    TI_LAUNCHED("k_attn_split_q8");
+    k_attn_combine<<<dim3(nHq, T), 256, 0, st>>>(po, ml, out, nsplit, hd, ns_stride, per, dpos);
+    TI_LAUNCHED("k_attn_combine");
+    return TI_OK;
+}
+
 // T queries (T >= 1) at contexts S, S+1, ..., S+T-1 (causal); with dpos != NULL the
 // context is read on the device (S = *dpos + 1, T must be 1) and the grid covers
 // `cap` positions in splits of `per` keys.
@@ -649,18 +671,8 @@ int ti_attn_decode_launch(ti_ctx* c, const float* qr, const uint32_t* kq, const 
         TI_LAUNCHED("k_attn_combine");
         return TI_OK;
     }
-    dim3 grid(nKv * nsplit, T);
-    const uint4* k4 = reinterpret_cast<const uint4*>(kq);
-    const uint4* v4 = reinterpret_cast<const uint4*>(vq);
-#define ATT(HD_, G_) \
-    if (hd == HD_ && G == G_) { k_attn_split_q8<HD_, G_><<<grid, ATT_THREADS, 0, c->stream>>>(qr, k4, ks, v4, vs, c->attn_po, c->attn_ml, S, nKv, nsplit, per, ns_stride, dpos); }
-    ATT(128, 1) else ATT(128, 2) else ATT(128, 4) else ATT(64, 1) else ATT(64, 2) else ATT(32, 2)
-    else return ti_fail(TI_ERR_INVALID, "ti_attn_decode_q8: unsupported hd=%d / group=%d", hd, G);
-#undef ATT
-    TI_LAUNCHED("k_attn_split_q8");
-    k_attn_combine<<<dim3(nHq, T), 256, 0, c->stream>>>(c->attn_po, c->attn_ml, out, nsplit, hd, ns_stride, per, dpos);
-    TI_LAUNCHED("k_attn_combine");
-    return TI_OK;
+    return split_combine(c->stream, c->attn_po, c->attn_ml, qr, kq, ks, vq, vs, out, S, T, nHq, nKv, hd, nsplit, per,
+                         ns_stride, dpos);
 }
 
 extern "C" int ti_attn_decode_q8(ti_ctx* c, const float* qr, const uint32_t* kq, const float* ks, const uint32_t* vq,
@@ -671,6 +683,55 @@ extern "C" int ti_attn_decode_q8(ti_ctx* c, const float* qr, const uint32_t* kq,
     TI_REQUIRE(hd % 32 == 0 && hd <= TI_ATTN_HD_MAX, "ti_attn_decode_q8: hd must be a multiple of 32 and <= %d", TI_ATTN_HD_MAX);
     TI_REQUIRE(al16(kq) && al16(vq), "ti_attn_decode_q8: kq/vq must be 16-byte aligned");
     return ti_attn_decode_launch(c, qr, kq, ks, vq, vs, out, S, 1, nHq, nKv, hd, nsplit, nullptr, 0);
+}
+
+// ---- the same call without a context (nothing allocated) ---------------------------------
+// Callers that cannot allocate device memory (code under graph capture, serving loops,
+// harnesses that forbid hipMalloc) get the split partials from this file-scope array.
+// Every device the call runs on holds its own copy until the process ends. In host code
+// the array's name is not a device address: its address on each device is looked up once
+// (hipGetSymbolAddress, with that device current) and only that address is used.
+constexpr int NOALLOC_ROWSPLITS = 4096;   // query heads x splits of one call, at most
+constexpr int NOALLOC_DEVICES = 64;
+static __device__ __align__(256) float scratch[NOALLOC_ROWSPLITS * (TI_ATTN_HD_MAX + 2)];
+
+static std::mutex g_scratch_mu;
+static float* g_scratch_addr[NOALLOC_DEVICES];
+
+static int scratch_address(int dev, float** out) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_addr[dev]) {
+        void* p = nullptr;
+        TI_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (!p) return ti_fail(TI_ERR_HIP, "ti_attn_decode_q8_noalloc: no device address for the scratch array");
+        g_scratch_addr[dev] = static_cast<float*>(p);
+    }
+    *out = g_scratch_addr[dev];
+    return TI_OK;
+}
+
+extern "C" int ti_attn_decode_q8_noalloc(void* stream, const float* qr, const uint32_t* kq, const float* ks,
+                                         const uint32_t* vq, const float* vs, float* out, int S, int nHq, int nKv,
+                                         int hd, int nsplit) {
+    TI_REQUIRE(qr && kq && ks && vq && vs && out, "ti_attn_decode_q8_noalloc: null buffer");
+    TI_REQUIRE(S > 0 && nKv > 0 && nHq % nKv == 0 && nHq <= TI_ATTN_HEADS_MAX,
+               "ti_attn_decode_q8_noalloc: bad heads/context (S=%d nHq=%d nKv=%d)", S, nHq, nKv);
+    TI_REQUIRE(hd % 32 == 0 && hd <= TI_ATTN_HD_MAX, "ti_attn_decode_q8_noalloc: hd must be a multiple of 32 and <= %d",
+               TI_ATTN_HD_MAX);
+    TI_REQUIRE(al16(kq) && al16(vq), "ti_attn_decode_q8_noalloc: kq/vq must be 16-byte aligned");
+    if (nsplit <= 0) nsplit = auto_nsplit(S, nKv);
+    TI_REQUIRE(nsplit <= TI_ATTN_SPLITS_MAX && (long)nHq * nsplit <= NOALLOC_ROWSPLITS,
+               "ti_attn_decode_q8_noalloc: %d heads x %d splits exceed the scratch array (%d head-splits, %d splits at most)",
+               nHq, nsplit, NOALLOC_ROWSPLITS, TI_ATTN_SPLITS_MAX);
+    int dev = -1;
+    TI_HIP(hipGetDevice(&dev));
+    TI_REQUIRE(dev >= 0 && dev < NOALLOC_DEVICES, "ti_attn_decode_q8_noalloc: device %d out of range", dev);
+    float* base = nullptr;
+    const int rc = scratch_address(dev, &base);
+    if (rc) return rc;
+    const int per = (S + nsplit - 1) / nsplit;
+    return split_combine(static_cast<hipStream_t>(stream), base, base + (size_t)NOALLOC_ROWSPLITS * TI_ATTN_HD_MAX, qr, kq,
+                         ks, vq, vs, out, S, 1, nHq, nKv, hd, nsplit, per, nsplit, nullptr);
 }
 
 extern "C" int ti_attn_causal_q8(ti_ctx* c, const float* qr, const uint32_t* kq, const float* ks, const uint32_t* vq,

@@ -70,8 +70,10 @@ def checks(tmp_path_factory):
 
 
 def test_addon_exports_every_entry_point(checks):
+    """Every entry point of ti.h that takes a context; the context-free no-allocation
+    variant is for callers that cannot allocate, and a JS host always holds a context."""
     _, out = checks
-    want = {n[len("ti_"):] for n in abi.header_functions()}
+    want = {n[len("ti_"):] for n in abi.header_functions() if not n.endswith("_noalloc")}
     missing = sorted(want - set(out["exports"]))
     assert not missing, missing
     assert out["version"] == abi.lib().ti_version()
