@@ -286,6 +286,23 @@ int ti_qwen3_forward(ti_ctx* ctx, ti_qwen3* m, const int32_t* ids, int T, int po
  * Reads nothing from the host, so it can be captured once and replayed per token. */
 int ti_qwen3_decode(ti_ctx* ctx, ti_qwen3* m);
 int ti_qwen3_set_pos(ti_ctx* ctx, ti_qwen3* m, int pos);
+/* Parity trace (debug; no reference counterpart: it exposes the intermediate values the
+ * reference's forward keeps in its own buffers, models/qwen3.js:3959-4049). With buf set,
+ * every later ti_qwen3_decode / ti_qwen3_forward also copies into buf, per layer l, 13
+ * fields of cfg.max_tokens rows each, in this order (32-bit words per row; nq = n_heads *
+ * head_dim, nkv = n_kv_heads * head_dim, H = hidden, I = intermediate):
+ *   x_in f32[H]      residual entering the layer
+ *   xn_q u32[H/4]    rmsnormQ codes of x_in (input of q/k/v), xn_s f32[H/32] their scales
+ *   q f32[nq], k f32[nkv], v f32[nkv]   the projections (before the q/k norms and RoPE)
+ *   attn f32[nq]     attention output; a_q u32[nq/4], a_s f32[nq/32] its quantQ8 codes
+ *   x_mid f32[H]     residual after o_proj
+ *   swi f32[I]       silu(gate)*up; s_q u32[I/4], s_s f32[I/32] its quantQ8 codes
+ * then, after the last layer, x_final f32[max_tokens][H]. A call fills rows [0, T). Fields
+ * a path does not materialise are left as they were: xn_* for 2 <= T <= 4 (the
+ * projections normalise in their prologue), attn and swi for fused T >= 2 (codes only).
+ * bytes must cover 4 * (layers * sum of the fields' words * max_tokens + max_tokens * H).
+ * buf == NULL switches tracing off (the default; the traced step launches extra copies). */
+int ti_qwen3_trace(ti_qwen3* m, void* buf, size_t bytes);
 int ti_qwen3_write_tokens(ti_ctx* ctx, ti_qwen3* m, int from, int count, const int32_t* ids);
 int ti_qwen3_read_tokens(ti_ctx* ctx, ti_qwen3* m, int from, int count, int32_t* ids);
 /* T-query causal attention over the int8 KV cache (models/qwen3.js:2534-2577): query t

@@ -66,6 +66,7 @@ _sig("or_attn_prep_q8", None, [_p, _p, _p, _p, _p, _i, _i, _i, _i, _f, _f, _p, _
 _sig("or_rope_norm_row", None, [_p, _p, _i, _i, _f, _f, _i, _p])
 _sig("or_attn_decode_q8", None, [_p, _p, _p, _p, _p, _i, _i, _i, _i, _p])
 _sig("or_attn_causal_q8", None, [_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p])
+_sig("or_attn_causal_q8_kvheads", None, [_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _p])
 _sig("or_embed", None, [_p, _p, _i, _i, _p])
 _sig("or_argmax", _i, [_p, _i])
 _sig("or_tern_pack", None, [_p, _i, _i, _p, _p])
@@ -78,6 +79,10 @@ _sig("or_n2_fixture", None, [_i, _i, C.c_uint64, _p, _p, _p, _p, _p, _p])
 _sig("or_has_avx2", _i, [])
 _sig("or_tern_gemv_avx2", None, [_p, _p, _p, _p, _i, _i, _p])
 _sig("or_tern_gemv_avx2_mt", None, [_p, _p, _p, _p, _i, _i, _p, _i])
+_sig("or_tern_pool_start", _i, [_i])
+_sig("or_tern_pool_stop", None, [])
+_sig("or_tern_pool_run", None, [_p, _i])
+_sig("or_tern_set_serial", None, [_p, _i])
 _sig("or_requant43", None, [_p, _p, _i, _i, _p, _p])
 _sig("or_router", None, [_p, _p, _i, _i, _i, _p, _p])
 _sig("or_moe_gemv_q3", None, [_p, _p, _p, _p, _i, _i, _i, _i, _i, _p])
@@ -238,6 +243,73 @@ def attn_causal_q8(qr, kq, ks, vq, vs, T, pos0, nHq, nKv, hd):
     return out
 
 
+# ---- parallel forms for full-size checks (ctypes releases the GIL during each call) ----
+_POOL = None
+
+
+def _pool():
+    global _POOL
+    if _POOL is None:
+        import concurrent.futures as cf
+        _POOL = cf.ThreadPoolExecutor(max(1, min(16, os.cpu_count() or 1)))
+    return _POOL
+
+
+def _row_chunks(N, parts):
+    step = max(32, -(-N // parts))
+    return [(r, min(N, r + step)) for r in range(0, N, step)]
+
+
+def gemv_q4_q8_par(xq, xs, pack, sc, N, K, parts=16):
+    """gemv_q4_q8 with its rows split over threads (each row's arithmetic unchanged)."""
+    xq, xs, pack, sc = _c(xq, np.uint32), _c(xs, np.float32), _c(pack, np.uint32), _c(sc, np.uint16)
+    y = np.zeros(N, np.float64)
+    def run(r0, r1):
+        _L.or_gemv_q4_q8(_ptr(xq), _ptr(xs), pack.ctypes.data + r0 * K // 2, sc.ctypes.data + r0 * K // 16,
+                         r1 - r0, K, y.ctypes.data + r0 * 8)
+    list(_pool().map(lambda rr: run(*rr), _row_chunks(N, parts)))
+    return y
+
+
+def gemv_q4_f32_par(x, pack, sc, N, K, parts=16):
+    x, pack, sc = _c(x, np.float32), _c(pack, np.uint32), _c(sc, np.uint16)
+    y = np.zeros(N, np.float64)
+    def run(r0, r1):
+        _L.or_gemv_q4_f32(_ptr(x), pack.ctypes.data + r0 * K // 2, sc.ctypes.data + r0 * K // 16, r1 - r0, K,
+                          y.ctypes.data + r0 * 8)
+    list(_pool().map(lambda rr: run(*rr), _row_chunks(N, parts)))
+    return y
+
+
+def gateup_silu_q4_par(xq, xs, gp, gs, up, us, I, H, parts=16):
+    xq, xs = _c(xq, np.uint32), _c(xs, np.float32)
+    gp, gs, up, us = _c(gp, np.uint32), _c(gs, np.uint16), _c(up, np.uint32), _c(us, np.uint16)
+    y = np.zeros(I, np.float64)
+    def run(r0, r1):
+        _L.or_gateup_silu_q4(_ptr(xq), _ptr(xs), gp.ctypes.data + r0 * H // 2, gs.ctypes.data + r0 * H // 16,
+                             up.ctypes.data + r0 * H // 2, us.ctypes.data + r0 * H // 16, r1 - r0, H,
+                             y.ctypes.data + r0 * 8)
+    list(_pool().map(lambda rr: run(*rr), _row_chunks(I, parts)))
+    return y
+
+
+def attn_causal_q8_kvheads(qr, kq, ks, vq, vs, T, pos0, nHq, nKv, hd, hk0, hk1, out=None):
+    out = np.zeros(T * nHq * hd, np.float64) if out is None else out
+    _L.or_attn_causal_q8_kvheads(_ptr(_c(qr, np.float32)), _ptr(_c(kq, np.uint32)), _ptr(_c(ks, np.float32)),
+                                 _ptr(_c(vq, np.uint32)), _ptr(_c(vs, np.float32)), T, pos0, nHq, nKv, hd, hk0, hk1,
+                                 _ptr(out))
+    return out
+
+
+def attn_causal_q8_par(qr, kq, ks, vq, vs, T, pos0, nHq, nKv, hd):
+    """attn_causal_q8 with one thread per KV head (bit-identical results)."""
+    qr, kq, ks, vq, vs = _c(qr, np.float32), _c(kq, np.uint32), _c(ks, np.float32), _c(vq, np.uint32), _c(vs, np.float32)
+    out = np.zeros(T * nHq * hd, np.float64)
+    list(_pool().map(lambda h: attn_causal_q8_kvheads(qr, kq, ks, vq, vs, T, pos0, nHq, nKv, hd, h, h + 1, out),
+                     range(nKv)))
+    return out
+
+
 def embed(ids, emb, T, H):
     y = np.zeros(T * H, np.float32)
     _L.or_embed(_ptr(_c(ids, np.int32)), _ptr(_c(emb, np.uint16)), T, H, _ptr(y))
@@ -317,6 +389,35 @@ def tern_gemv_avx2(codes, sc, act, xsum, N, K, nthreads=1):
     else:
         _L.or_tern_gemv_avx2_mt(*args, nthreads)
     return out
+
+
+class _TernMat(C.Structure):
+    _fields_ = [("codes", C.c_void_p), ("scales", C.c_void_p), ("act", C.c_void_p), ("xsum", C.c_void_p),
+                ("out", C.c_void_p), ("N", C.c_int), ("K", C.c_int)]
+
+
+class TernPool:
+    """The AVX2 ternary GEMV over a whole set of matrices on a persistent thread pool
+    (or_tern_pool_*): `run()` is one pass, each matrix row-split over the threads with a
+    barrier after it. mats: [(codes u8, scales f32, act i8, xsum i32, out f32, N, K)],
+    contiguous arrays kept alive by this object."""
+
+    def __init__(self, mats, nthreads):
+        self.keep = mats
+        self.arr = (_TernMat * len(mats))(*[_TernMat(c.ctypes.data, s_.ctypes.data, a.ctypes.data, x.ctypes.data,
+                                                     o.ctypes.data, N, K) for c, s_, a, x, o, N, K in mats])
+        self.n = len(mats)
+        self.threads = int(_L.or_tern_pool_start(nthreads))
+
+    def run(self):
+        _L.or_tern_pool_run(C.cast(self.arr, C.c_void_p), self.n)
+
+    def run_serial(self):
+        """The same pass on the calling thread alone."""
+        _L.or_tern_set_serial(C.cast(self.arr, C.c_void_p), self.n)
+
+    def close(self):
+        _L.or_tern_pool_stop()
 
 
 def tern_gemv_avx2_into(codes, sc, act, xsum, N, K, out, nthreads=1):

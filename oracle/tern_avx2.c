@@ -81,24 +81,96 @@ void or_tern_gemv_avx2(const uint8_t* codes, const float* scales, const int8_t* 
     rows_avx2(codes, scales, act, xsum, 0, N, K, out);
 }
 
-typedef struct { const uint8_t* c; const float* s; const int8_t* a; const int32_t* x; int r0, r1, K; float* o; } job_t;
-static void* job_run(void* p) { job_t* j = (job_t*)p; rows_avx2(j->c, j->s, j->a, j->x, j->r0, j->r1, j->K, j->o); return NULL; }
+/* ---- a persistent thread pool over a GEMV set --------------------------------------
+ * The reference's multi-worker CPU engine splits each GEMV's rows statically over its
+ * workers and meets at a barrier before the next one (cpu/cpukern-fwd-worker.js:1-4);
+ * this pool does the same with threads created once (or_tern_pool_start), so a timed
+ * pass pays no thread creation. The calling thread is worker 0. */
+static struct {
+    int n;                              /* workers including the caller; 0 = not started */
+    pthread_t th[256];
+    pthread_mutex_t mu;
+    pthread_cond_t cv;
+    pthread_barrier_t bar;
+    unsigned gen;                       /* bumped per pass; workers run one pass per bump */
+    int quit;
+    const or_tern_mat* mats;
+    int nmat;
+} P;
+
+static void pass_rows(int w) {
+    for (int m = 0; m < P.nmat; m++) {
+        const or_tern_mat* t = &P.mats[m];
+        const int r0 = (int)((long)t->N * w / P.n), r1 = (int)((long)t->N * (w + 1) / P.n);
+        if (r0 < r1) rows_avx2(t->codes, t->scales, t->act, t->xsum, r0, r1, t->K, t->out);
+        pthread_barrier_wait(&P.bar);
+    }
+}
+
+static void* worker(void* arg) {
+    const int w = (int)(long)arg;
+    unsigned seen = 0;
+    for (;;) {
+        pthread_mutex_lock(&P.mu);
+        while (P.gen == seen && !P.quit) pthread_cond_wait(&P.cv, &P.mu);
+        seen = P.gen;
+        const int quit = P.quit;
+        pthread_mutex_unlock(&P.mu);
+        if (quit) return NULL;
+        pass_rows(w);
+    }
+}
+
+int or_tern_pool_start(int nthreads) {
+    if (P.n) or_tern_pool_stop();
+    if (nthreads < 1) nthreads = 1;
+    if (nthreads > 256) nthreads = 256;
+    pthread_mutex_init(&P.mu, NULL);
+    pthread_cond_init(&P.cv, NULL);
+    pthread_barrier_init(&P.bar, NULL, (unsigned)nthreads);
+    P.gen = 0;
+    P.quit = 0;
+    P.n = nthreads;
+    for (int w = 1; w < nthreads; w++)
+        if (pthread_create(&P.th[w], NULL, worker, (void*)(long)w) != 0) return -1;
+    return nthreads;
+}
+
+void or_tern_pool_stop(void) {
+    if (!P.n) return;
+    pthread_mutex_lock(&P.mu);
+    P.quit = 1;
+    pthread_cond_broadcast(&P.cv);
+    pthread_mutex_unlock(&P.mu);
+    for (int w = 1; w < P.n; w++) pthread_join(P.th[w], NULL);
+    pthread_barrier_destroy(&P.bar);
+    pthread_cond_destroy(&P.cv);
+    pthread_mutex_destroy(&P.mu);
+    P.n = 0;
+}
+
+void or_tern_pool_run(const or_tern_mat* mats, int nmat) {
+    if (!P.n) or_tern_pool_start(1);
+    P.mats = mats;
+    P.nmat = nmat;
+    pthread_mutex_lock(&P.mu);
+    P.gen++;
+    pthread_cond_broadcast(&P.cv);
+    pthread_mutex_unlock(&P.mu);
+    pass_rows(0);                 /* the last barrier of the pass: every worker is done */
+}
+
+/* the same set on the calling thread alone, matrix after matrix (the reference's
+ * single-threaded configuration, native/crates/n2-cli/src/main.rs:377) */
+void or_tern_set_serial(const or_tern_mat* mats, int nmat) {
+    for (int m = 0; m < nmat; m++)
+        rows_avx2(mats[m].codes, mats[m].scales, mats[m].act, mats[m].xsum, 0, mats[m].N, mats[m].K, mats[m].out);
+}
 
 void or_tern_gemv_avx2_mt(const uint8_t* codes, const float* scales, const int8_t* act,
                           const int32_t* xsum, int N, int K, float* out, int nthreads) {
     if (nthreads <= 1) { rows_avx2(codes, scales, act, xsum, 0, N, K, out); return; }
-    if (nthreads > 256) nthreads = 256;
-    pthread_t th[256]; job_t jobs[256];
-    int per = (N + nthreads - 1) / nthreads;
-    int started = 0;
-    for (int t = 0; t < nthreads; t++) {
-        int r0 = t * per, r1 = r0 + per; if (r1 > N) r1 = N;
-        if (r0 >= r1) break;
-        jobs[t] = (job_t){codes, scales, act, xsum, r0, r1, K, out};
-        if (t == 0) continue;
-        pthread_create(&th[t], NULL, job_run, &jobs[t]);
-        started = t;
-    }
-    job_run(&jobs[0]);
-    for (int t = 1; t <= started; t++) pthread_join(th[t], NULL);
+    if (P.n != nthreads) or_tern_pool_start(nthreads);
+    or_tern_mat m = {codes, scales, act, xsum, out, N, K};
+    or_tern_pool_run(&m, 1);
 }

@@ -401,6 +401,53 @@ void or_attn_decode_q8(const float* qr, const uint32_t* kq, const float* ks,
         attn_one(qr + hq * hd, kq, ks, vq, vs, S, nKv, hd, hq / grp, out + hq * hd);
 }
 
+/* The same arithmetic as attn_one for every query head of KV heads [hk0, hk1) and T
+ * causal queries (query t attends keys [0, pos0+t]), with each KV head's keys and values
+ * dequantized once (the sums run in attn_one's order, so the results are bit-identical
+ * to or_attn_causal_q8's for those heads). Disjoint head ranges may run in parallel. */
+void or_attn_causal_q8_kvheads(const float* qr, const uint32_t* kq, const float* ks,
+                               const uint32_t* vq, const float* vs,
+                               int T, int pos0, int nHq, int nKv, int hd, int hk0, int hk1, double* out) {
+    int grp = nHq / nKv, kv4 = nKv * hd / 4, kvg = nKv * hd / 32, S = pos0 + T;
+    double scale = 1.0 / sqrt((double)hd);
+    double* K = (double*)malloc(sizeof(double) * (size_t)S * hd);
+    double* V = (double*)malloc(sizeof(double) * (size_t)S * hd);
+    double* sc = (double*)malloc(sizeof(double) * (size_t)S);
+    for (int hk = hk0; hk < hk1; hk++) {
+        for (int t = 0; t < S; t++)
+            for (int i = 0; i < hd; i++) {
+                K[(size_t)t * hd + i] = or_snorm_dequant(kq[(size_t)t * kv4 + hk * (hd / 4) + (i >> 2)], i & 3,
+                                                         ks[(size_t)t * kvg + hk * (hd / 32) + (i >> 5)]);
+                V[(size_t)t * hd + i] = or_snorm_dequant(vq[(size_t)t * kv4 + hk * (hd / 4) + (i >> 2)], i & 3,
+                                                         vs[(size_t)t * kvg + hk * (hd / 32) + (i >> 5)]);
+            }
+        for (int q = 0; q < T; q++)
+            for (int hq = hk * grp; hq < (hk + 1) * grp; hq++) {
+                const float* qrow = qr + ((size_t)q * nHq + hq) * hd;
+                double* o = out + ((size_t)q * nHq + hq) * hd;
+                int nkeys = pos0 + q + 1;
+                double m = -INFINITY;
+                for (int t = 0; t < nkeys; t++) {
+                    double d = 0;
+                    for (int i = 0; i < hd; i++) d += (double)qrow[i] * K[(size_t)t * hd + i];
+                    sc[t] = d * scale;
+                    if (sc[t] > m) m = sc[t];
+                }
+                double den = 0;
+                for (int i = 0; i < hd; i++) o[i] = 0;
+                for (int t = 0; t < nkeys; t++) {
+                    double w = exp(sc[t] - m);
+                    den += w;
+                    for (int i = 0; i < hd; i++) o[i] += w * V[(size_t)t * hd + i];
+                }
+                for (int i = 0; i < hd; i++) o[i] /= den;
+            }
+    }
+    free(K);
+    free(V);
+    free(sc);
+}
+
 /* models/qwen3.js:2534-2577 (causal, T queries at positions pos0..pos0+T-1) */
 void or_attn_causal_q8(const float* qr, const uint32_t* kq, const float* ks,
                        const uint32_t* vq, const float* vs,

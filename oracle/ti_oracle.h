@@ -100,6 +100,13 @@ void or_attn_causal_q8(const float* qr, const uint32_t* kq, const float* ks,
                        const uint32_t* vq, const float* vs,
                        int T, int pos0, int nHq, int nKv, int hd, double* out);
 
+/* the causal variant restricted to KV heads [hk0, hk1) (and their query heads), each KV
+ * head dequantized once; bit-identical to or_attn_causal_q8 on those heads. out is the
+ * full [T][nHq][hd] array; only the range's heads are written. */
+void or_attn_causal_q8_kvheads(const float* qr, const uint32_t* kq, const float* ks,
+                               const uint32_t* vq, const float* vs,
+                               int T, int pos0, int nHq, int nKv, int hd, int hk0, int hk1, double* out);
+
 /* ---- decode-step glue ---------------------------------------------------- */
 void or_embed(const int32_t* ids, const uint16_t* emb_f16, int T, int H, float* y);
 int  or_argmax(const float* logits, int N);   /* the reference's one/two-stage trees, their tie order */
@@ -122,9 +129,19 @@ void or_n2_fixture(int N, int K, uint64_t seed, uint8_t* codes, float* scales,
 int  or_has_avx2(void);
 void or_tern_gemv_avx2(const uint8_t* codes, const float* scales, const int8_t* act,
                        const int32_t* xsum, int N, int K, float* out);
-/* static row split over nthreads (cpu/cpukern-fwd-worker.js:1-4 model) */
+/* static row split over nthreads (cpu/cpukern-fwd-worker.js:1-4 model), on the pool below */
 void or_tern_gemv_avx2_mt(const uint8_t* codes, const float* scales, const int8_t* act,
                           const int32_t* xsum, int N, int K, float* out, int nthreads);
+/* A persistent pool (threads created once) that runs a whole GEMV set: each matrix's rows
+ * split statically over the workers, a barrier after each matrix (as a forward pass needs
+ * between dependent GEMVs). The caller is worker 0. */
+typedef struct {
+    const uint8_t* codes; const float* scales; const int8_t* act; const int32_t* xsum; float* out; int N, K;
+} or_tern_mat;
+int  or_tern_pool_start(int nthreads);
+void or_tern_pool_stop(void);
+void or_tern_pool_run(const or_tern_mat* mats, int nmat);
+void or_tern_set_serial(const or_tern_mat* mats, int nmat);   /* one thread, no pool */
 
 /* ---- int3 MoE (models/lfm25.js) ----------------------------------- */
 void or_requant43(const uint32_t* pack4, const uint16_t* sc4, int rows, int K,

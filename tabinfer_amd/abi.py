@@ -86,6 +86,7 @@ SIGS = {
     "ti_qwen3_forward": [_p, _p, _p, _i, _i],
     "ti_qwen3_decode": [_p, _p],
     "ti_qwen3_set_pos": [_p, _p, _i],
+    "ti_qwen3_trace": [_p, _p, _sz],
     "ti_qwen3_write_tokens": [_p, _p, _i, _i, _p],
     "ti_qwen3_read_tokens": [_p, _p, _i, _i, _p],
     "ti_attn_causal_q8": [_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i],
@@ -298,6 +299,10 @@ class Qwen3:
 
     def set_pos(self, pos):
         check(lib().ti_qwen3_set_pos(self.ctx.h, self.h, pos))
+
+    def trace(self, buf):
+        """Route the parity trace (ti_qwen3_trace) into the DevBuf `buf`; None stops it."""
+        check(lib().ti_qwen3_trace(self.h, int(buf) if buf is not None else None, buf.nbytes if buf is not None else 0))
 
     def write_tokens(self, start, ids):
         ids = np.ascontiguousarray(ids, dtype=np.int32)

@@ -152,8 +152,55 @@ struct ti_qwen3 {
     float* rope_cur;      // the row of the device position (kept in step with dpos)
     float* amx_v;
     uint32_t* amx_i;
+    uint32_t* trace = nullptr;   // caller's trace buffer (ti_qwen3_trace), or null
     std::vector<void*> allocs;
 };
+
+// ---- the parity trace (ti_qwen3_trace) -------------------------------------------------
+// Per layer, fields of max_tokens rows each, in this order (32-bit words per row):
+enum TraceField { TR_X_IN, TR_XN_Q, TR_XN_S, TR_Q, TR_K, TR_V, TR_ATTN, TR_A_Q, TR_A_S, TR_X_MID, TR_SWI, TR_S_Q, TR_S_S,
+                  TR_NFIELDS };
+static size_t trace_row_words(const ti_qwen3_config& C, int f) {
+    const size_t H = C.hidden, I = C.intermediate, nq = (size_t)C.n_heads * C.head_dim, nkv = (size_t)C.n_kv_heads * C.head_dim;
+    switch (f) {
+        case TR_X_IN: case TR_X_MID: return H;
+        case TR_XN_Q: return H / 4;
+        case TR_XN_S: return H / 32;
+        case TR_Q: case TR_ATTN: return nq;
+        case TR_K: case TR_V: return nkv;
+        case TR_A_Q: return nq / 4;
+        case TR_A_S: return nq / 32;
+        case TR_SWI: return I;
+        case TR_S_Q: return I / 4;
+        default: return I / 32;   // TR_S_S
+    }
+}
+static size_t trace_layer_words(const ti_qwen3_config& C) {
+    size_t w = 0;
+    for (int f = 0; f < TR_NFIELDS; f++) w += trace_row_words(C, f) * C.max_tokens;
+    return w;
+}
+// the slot of (layer, field); layer == layers is the final residual (TR_X_IN only)
+static uint32_t* trace_slot(ti_qwen3* m, int layer, int f) {
+    size_t off = (size_t)layer * trace_layer_words(m->cfg);
+    for (int g = 0; g < f; g++) off += trace_row_words(m->cfg, g) * m->cfg.max_tokens;
+    return m->trace + off;
+}
+
+__global__ void k_copy_u32(const uint32_t* __restrict__ s, uint32_t* __restrict__ d, long n) {
+    const long stride = (long)gridDim.x * blockDim.x;
+    for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) d[i] = s[i];
+}
+
+// copy `rows` rows of field f from src into the trace (nothing when no trace is set)
+static int trace_put(ti_ctx* c, ti_qwen3* m, int layer, int f, const void* src, int rows) {
+    if (!m->trace) return TI_OK;
+    const long n = (long)trace_row_words(m->cfg, f) * rows;
+    const long blocks = (n + 255) / 256 < 1024 ? (n + 255) / 256 : 1024;
+    k_copy_u32<<<(unsigned)blocks, 256, 0, c->stream>>>(static_cast<const uint32_t*>(src), trace_slot(m, layer, f), n);
+    TI_LAUNCHED("k_copy_u32 (trace)");
+    return TI_OK;
+}
 
 static int mk(ti_qwen3* m, void** p, size_t bytes) {
     hipError_t e = hipMalloc(p, bytes ? bytes : 4);
@@ -320,6 +367,16 @@ extern "C" int ti_qwen3_logits(ti_qwen3* m, float** logits) {
     return TI_OK;
 }
 
+extern "C" int ti_qwen3_trace(ti_qwen3* m, void* buf, size_t bytes) {
+    TI_REQUIRE(m, "ti_qwen3_trace: null model");
+    if (!buf) { m->trace = nullptr; return TI_OK; }
+    const size_t need = (trace_layer_words(m->cfg) * m->cfg.layers + (size_t)m->cfg.hidden * m->cfg.max_tokens) * 4;
+    TI_REQUIRE(bytes >= need, "ti_qwen3_trace: the trace needs %zu bytes (got %zu)", need, bytes);
+    TI_REQUIRE(((uintptr_t)buf & 15) == 0, "ti_qwen3_trace: buffer must be 16-byte aligned");
+    m->trace = static_cast<uint32_t*>(buf);
+    return TI_OK;
+}
+
 extern "C" int ti_qwen3_set_pos(ti_ctx* c, ti_qwen3* m, int pos) {
     TI_CHECK_CTX(c);
     TI_REQUIRE(m && pos >= 0 && pos < m->cfg.max_ctx, "ti_qwen3_set_pos: pos %d out of [0, %d)", pos, m ? m->cfg.max_ctx : 0);
@@ -386,20 +443,34 @@ extern "C" int ti_qwen3_decode(ti_ctx* c, ti_qwen3* m) {
 #define RC(x) do { rc = (x); if (rc) return rc; } while (0)
     k_embed<<<(H + 255) / 256, 256, 0, c->stream>>>(m->hist, m->embed, m->x, 1, H, 0, m->dpos, C.vocab);
     TI_LAUNCHED("k_embed");
+    const bool tr = m->trace != nullptr;
     for (int l = 0; l < C.layers; l++) {
         Layer& y = m->L[l];
         const uint32_t* packs[3] = {y.q.pack, y.k.pack, y.v.pack};
         const uint16_t* scs[3] = {y.q.sc, y.k.sc, y.v.sc};
         float* ys[3] = {m->q, m->k, m->v};
         const int Ns[3] = {nq, nkv, nkv};
-        RC(ti_fused_qkv_launch(c, m->x, y.in_norm, C.rms_eps, H, 3, packs, scs, ys, Ns, nullptr, nullptr));
+        RC(trace_put(c, m, l, TR_X_IN, m->x, 1));
+        RC(ti_fused_qkv_launch(c, m->x, y.in_norm, C.rms_eps, H, 3, packs, scs, ys, Ns,
+                               tr ? trace_slot(m, l, TR_XN_Q) : nullptr,
+                               tr ? reinterpret_cast<float*>(trace_slot(m, l, TR_XN_S)) : nullptr));
+        RC(trace_put(c, m, l, TR_Q, m->q, 1));
+        RC(trace_put(c, m, l, TR_K, m->k, 1));
+        RC(trace_put(c, m, l, TR_V, m->v, 1));
         RC(ti_attn_fused_launch(c, m->q, m->k, m->v, y.q_norm, y.k_norm, y.kq, y.ks, y.vq, y.vs, m->attn, nHq, nKv, hd,
                                 m->dpos, 0, C.max_ctx, C.rope_theta, C.rms_eps, 0, m->rope_cur, m->xq, m->xs));
+        RC(trace_put(c, m, l, TR_ATTN, m->attn, 1));
+        RC(trace_put(c, m, l, TR_A_Q, m->xq, 1));
+        RC(trace_put(c, m, l, TR_A_S, m->xs, 1));
         RC(ti_gemv_q4_q8_launch(c, m->xq, m->xs, y.o.pack, y.o.sc, m->x, H, nq, 1));
-        RC(ti_fused_gateup_launch(c, m->x, y.post_norm, C.rms_eps, y.gate.pack, y.gate.sc, y.up.pack, y.up.sc, nullptr,
-                                  I, H, m->xq, m->xs));
+        RC(trace_put(c, m, l, TR_X_MID, m->x, 1));
+        RC(ti_fused_gateup_launch(c, m->x, y.post_norm, C.rms_eps, y.gate.pack, y.gate.sc, y.up.pack, y.up.sc,
+                                  tr ? reinterpret_cast<float*>(trace_slot(m, l, TR_SWI)) : nullptr, I, H, m->xq, m->xs));
+        RC(trace_put(c, m, l, TR_S_Q, m->xq, 1));
+        RC(trace_put(c, m, l, TR_S_S, m->xs, 1));
         RC(ti_gemv_q4_q8_launch(c, m->xq, m->xs, y.down.pack, y.down.sc, m->x, H, I, 1));
     }
+    RC(trace_put(c, m, C.layers, TR_X_IN, m->x, 1));
     RC(ti_fused_lmhead_launch(c, m->x, m->final_norm, C.rms_eps, m->lm.pack, m->lm.sc, m->logits, C.vocab, H, m->hist,
                               m->dpos, 0, C.max_ctx, m->rope, m->rope_cur, hd));
     return TI_OK;
@@ -442,13 +513,18 @@ extern "C" int ti_qwen3_forward(ti_ctx* c, ti_qwen3* m, const int32_t* ids, int 
     const TgIn attn_in = {m->xq, m->xs, nullptr, nullptr, 0.0f, nullptr};
     for (int l = 0; l < C.layers; l++) {
         Layer& y = m->L[l];
+        RC(trace_put(c, m, l, TR_X_IN, m->x, T));
         if (fused) {
             const uint32_t* packs[3] = {y.q.pack, y.k.pack, y.v.pack};
             const uint16_t* scs[3] = {y.q.sc, y.k.sc, y.v.sc};
             float* ys[3] = {m->q, m->k, m->v};
             const int Ns[3] = {nq, nkv, nkv};
             const TgIn in_norm = {nullptr, nullptr, m->x, y.in_norm, C.rms_eps, m->psum};
-            if (!norm_in) RC(ti_tnorm_q8_launch(c, m->x, y.in_norm, C.rms_eps, c->act_q, c->act_s, T, H));
+            if (!norm_in) {
+                RC(ti_tnorm_q8_launch(c, m->x, y.in_norm, C.rms_eps, c->act_q, c->act_s, T, H));
+                RC(trace_put(c, m, l, TR_XN_Q, c->act_q, T));
+                RC(trace_put(c, m, l, TR_XN_S, c->act_s, T));
+            }
             RC(ti_tgemm_launch(c, norm_in ? in_norm : codes_in, 3, packs, scs, ys, Ns, T, H, 0, nullptr));
         } else {
             RC(ti_rmsnorm(c, m->x, y.in_norm, m->normed, T, H, C.rms_eps));
@@ -465,24 +541,39 @@ extern "C" int ti_qwen3_forward(ti_ctx* c, ti_qwen3* m, const int32_t* ids, int 
             RC(ti_kv_write_q8(c, m->kr, m->v, y.kq, y.ks, y.vq, y.vs, T, nKv, hd, pos));
             RC(ti_attn_decode_launch(c, m->qr, y.kq, y.ks, y.vq, y.vs, m->attn, pos + 1, T, nHq, nKv, hd, 0, nullptr, 0));
         }
+        RC(trace_put(c, m, l, TR_Q, m->q, T));
+        RC(trace_put(c, m, l, TR_K, m->k, T));
+        RC(trace_put(c, m, l, TR_V, m->v, T));
         if (fused) {
-            if (!fused_attn) RC(ti_quant_act_q8_async(c, m->attn, m->xq, m->xs, nullptr, T * (nq / 32)));
+            if (!fused_attn) {
+                RC(trace_put(c, m, l, TR_ATTN, m->attn, T));
+                RC(ti_quant_act_q8_async(c, m->attn, m->xq, m->xs, nullptr, T * (nq / 32)));
+            }
+            RC(trace_put(c, m, l, TR_A_Q, m->xq, T));
+            RC(trace_put(c, m, l, TR_A_S, m->xs, T));
             RC(ti_tgemm_launch(c, attn_in, 1, &y.o.pack, &y.o.sc, &m->x, &H, T, nq, 1, pout));
+            RC(trace_put(c, m, l, TR_X_MID, m->x, T));
             const TgIn post_norm = {nullptr, nullptr, m->x, y.post_norm, C.rms_eps, m->psum};
             if (!norm_in) RC(ti_tnorm_q8_launch(c, m->x, y.post_norm, C.rms_eps, c->act_q, c->act_s, T, H));
             RC(ti_tgemm_gateup_launch(c, norm_in ? post_norm : codes_in, y.gate.pack, y.gate.sc, y.up.pack, y.up.sc, I, H,
                                       T, m->xq, m->xs));
+            RC(trace_put(c, m, l, TR_S_Q, m->xq, T));
+            RC(trace_put(c, m, l, TR_S_S, m->xs, T));
             RC(ti_tgemm_launch(c, attn_in, 1, &y.down.pack, &y.down.sc, &m->x, &H, T, I, 1, pout));
             continue;
         }
+        RC(trace_put(c, m, l, TR_ATTN, m->attn, T));
         RC(ti_linear_q4(c, m->attn, y.o.pack, y.o.sc, m->x, T, H, nq, 1));
+        RC(trace_put(c, m, l, TR_X_MID, m->x, T));
         RC(ti_rmsnorm(c, m->x, y.post_norm, m->normed, T, H, C.rms_eps));
         RC(ti_linear_q4(c, m->normed, y.gate.pack, y.gate.sc, m->gate, T, I, H, 0));
         RC(ti_linear_q4(c, m->normed, y.up.pack, y.up.sc, m->up, T, I, H, 0));
         k_swiglu<<<(unsigned)(((long)T * I + 255) / 256), 256, 0, c->stream>>>(m->gate, m->up, m->swi, (long)T * I);
         TI_LAUNCHED("k_swiglu");
+        RC(trace_put(c, m, l, TR_SWI, m->swi, T));
         RC(ti_linear_q4(c, m->swi, y.down.pack, y.down.sc, m->x, T, H, I, 1));
     }
+    RC(trace_put(c, m, C.layers, TR_X_IN, m->x, T));
     k_copy_f32<<<(H + 255) / 256, 256, 0, c->stream>>>(m->x + (size_t)(T - 1) * H, m->last, H);
     TI_LAUNCHED("k_copy_f32");
     RC(ti_fused_lmhead_launch(c, m->last, m->final_norm, C.rms_eps, m->lm.pack, m->lm.sc, m->logits, C.vocab, H, m->hist,

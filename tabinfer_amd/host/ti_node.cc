@@ -831,6 +831,18 @@ napi_value js_qwen3_set_pos(napi_env env, napi_callback_info info) {
     return rc ? throw_ti(env, "qwen3_set_pos", rc) : undefined(env);
 }
 
+// qwen3_trace(model, buffer | null): parity trace of the decoder's intermediate values
+napi_value js_qwen3_trace(napi_env env, napi_callback_info info) {
+    Args a(env, info);
+    if (!want_args(env, a, 2, "qwen3_trace")) return nullptr;
+    ModelH* m = get_model(env, a.v[0], "qwen3_trace", 0);
+    void* p = nullptr;
+    if (!m || !get_dptr(env, a.v[1], &p, "qwen3_trace", 1)) return nullptr;
+    BufH* b = p ? handle_of<BufH>(env, a.v[1], TAG_BUF) : nullptr;
+    const int rc = ti_qwen3_trace(m->m, p, b ? b->bytes : 0);
+    return rc ? throw_ti(env, "qwen3_trace", rc) : undefined(env);
+}
+
 // qwen3_write_tokens(ctx, model, from, ids: Int32Array)
 napi_value js_qwen3_write_tokens(napi_env env, napi_callback_info info) {
     const char* fn = "qwen3_write_tokens";
@@ -940,6 +952,7 @@ napi_value module_init(napi_env env, napi_value exports) {
         FN("qwen3_forward", js_qwen3_forward),
         FN("qwen3_decode", js_qwen3_decode),
         FN("qwen3_set_pos", js_qwen3_set_pos),
+        FN("qwen3_trace", js_qwen3_trace),
         FN("qwen3_write_tokens", js_qwen3_write_tokens),
         FN("qwen3_read_tokens", js_qwen3_read_tokens),
     };
