@@ -71,7 +71,8 @@ int ti_graph_begin(ti_ctx* ctx);
 int ti_graph_end(ti_ctx* ctx, ti_graph** out);
 int ti_graph_launch(ti_ctx* ctx, ti_graph* g);
 int ti_graph_destroy(ti_graph* g);
-int ti_event_record(ti_ctx* ctx, int slot);                          /* slot in [0, 64) */
+int ti_event_record(ti_ctx* ctx, int slot);                          /* slot in [0, 64); inside a
+                                                                        capture: a graph node */
 int ti_event_elapsed_ms(ti_ctx* ctx, int start_slot, int end_slot, float* ms);
 
 /* ---- int4 weights ---------------------------------------------------------- */
@@ -212,6 +213,45 @@ int ti_quant_act_tern(ti_ctx* ctx, const float* x, int8_t* act, int32_t* xsum, f
                       int K, int mode);
 /* Exact int32 per-(row, block) code dots of gemv_tern (debug/parity). */
 int ti_tern_block_dots(ti_ctx* ctx, const uint8_t* codes, const int8_t* act, int32_t* dots, int N, int K);
+
+/* ---- the .cpu.bin weight container (native/docs/FORMAT.md) ----------------------------
+ * Reader of the native ternary engine's container (native/crates/n2-core/src/binfmt.rs:
+ * 104-257, written by native/tools/pack_bin.py): [u32 le header_len][UTF-8 JSON header]
+ * [blob], header {"G": 64, "tensors": {name: {...}}} with blob-relative offsets. Host
+ * only (no GPU needed). Open and parse fail with TI_ERR_INVALID and the reference's
+ * message for each rule it enforces: a header overrunning the file, a header that is not
+ * UTF-8 or JSON, G != 64, no `tensors` object, a tensor without `kind` or of an unknown
+ * kind, K % G != 0, codesLen != N*K/4, scalesLen != N*(K/G)*4, a byte range overrunning
+ * the blob; and, when a tensor is viewed, f32 ranges that are not whole f32s at 4-byte-
+ * aligned offsets. The blob lives in a 16-byte-aligned host allocation owned by the handle. */
+typedef struct ti_cpubin ti_cpubin;
+#define TI_CPUBIN_TERN      1   /* Q2_0_g64 codes u8[N*K/4] + f32 scales [N*K/64] */
+#define TI_CPUBIN_EMBED_F16 2   /* f16 bit patterns, shape[] */
+#define TI_CPUBIN_F32       3   /* f32, shape[] */
+typedef struct {
+    int kind;
+    long long N, K;             /* tern */
+    int ndim;                   /* embed_f16 / f32 */
+    long long shape[4];
+    const void* data;           /* codes (tern) or the values, in the container's blob */
+    size_t data_bytes;
+    const void* scales;         /* tern only */
+    size_t scale_bytes;
+} ti_cpubin_tensor_info;
+/* Container::open (binfmt.rs:104-134): the header, then the blob streamed into its own
+ * aligned allocation. */
+int ti_cpubin_open(const char* path, ti_cpubin** out);
+/* Container::from_bytes (binfmt.rs:136-157): a whole file held in memory (copied). */
+int ti_cpubin_parse(const void* data, size_t bytes, ti_cpubin** out);
+int ti_cpubin_close(ti_cpubin* c);
+int ti_cpubin_summary(const ti_cpubin* c, int* group_size, int* n_tensors, size_t* blob_bytes);
+/* the i-th tensor name, in name order (the reference's BTreeMap order) */
+int ti_cpubin_name(const ti_cpubin* c, int i, const char** name);
+/* ternary / view_f32 / the embedding table (binfmt.rs:260-320): a tensor's kind, shape and
+ * host views into the blob (valid until ti_cpubin_close). */
+int ti_cpubin_tensor(const ti_cpubin* c, const char* name, ti_cpubin_tensor_info* info);
+/* embed_row (binfmt.rs:321-342): row `row` of an embed_f16 tensor decoded to f32. */
+int ti_cpubin_embed_row(const ti_cpubin* c, const char* name, long long row, float* dst, int dim);
 
 /* ---- int3 MoE experts (LFM2.5) ----------------------------------------------------
  * int3 group of 32 weights: three u32 bitplanes (bit i of plane b = bit b of q3+4 for

@@ -97,6 +97,23 @@ class Qwen3Config(C.Structure):
     _fields_ = [("layers", _i), ("hidden", _i), ("intermediate", _i), ("n_heads", _i), ("n_kv_heads", _i),
                 ("head_dim", _i), ("vocab", _i), ("rope_theta", _f), ("rms_eps", _f), ("max_ctx", _i),
                 ("max_tokens", _i)]
+
+
+class CpuBinTensor(C.Structure):
+    """ti_cpubin_tensor_info"""
+    _fields_ = [("kind", _i), ("N", C.c_longlong), ("K", C.c_longlong), ("ndim", _i), ("shape", C.c_longlong * 4),
+                ("data", _p), ("data_bytes", _sz), ("scales", _p), ("scale_bytes", _sz)]
+
+
+SIGS.update({
+    "ti_cpubin_open": [C.c_char_p, C.POINTER(_p)],
+    "ti_cpubin_parse": [_p, _sz, C.POINTER(_p)],
+    "ti_cpubin_close": [_p],
+    "ti_cpubin_summary": [_p, C.POINTER(_i), C.POINTER(_i), C.POINTER(_sz)],
+    "ti_cpubin_name": [_p, _i, C.POINTER(C.c_char_p)],
+    "ti_cpubin_tensor": [_p, C.c_char_p, C.POINTER(CpuBinTensor)],
+    "ti_cpubin_embed_row": [_p, C.c_char_p, C.c_longlong, _p, _i],
+})
 _RES = {"ti_last_error": C.c_char_p}
 
 
@@ -317,6 +334,59 @@ class Qwen3:
         if self.h:
             check(lib().ti_qwen3_destroy(self.ctx.h, self.h))
             self.h = None
+
+
+class CpuBin:
+    """A `.cpu.bin` container read by the library (ti_cpubin_*, host only)."""
+
+    TERN, EMBED_F16, F32 = 1, 2, 3
+
+    def __init__(self, path=None, data=None):
+        h = C.c_void_p()
+        if path is not None:
+            check(lib().ti_cpubin_open(path.encode(), C.byref(h)))
+        else:
+            buf = bytes(data)
+            check(lib().ti_cpubin_parse(C.c_char_p(buf), len(buf), C.byref(h)))
+        self.h = h.value
+
+    def summary(self):
+        g, n, b = C.c_int(), C.c_int(), C.c_size_t()
+        check(lib().ti_cpubin_summary(self.h, C.byref(g), C.byref(n), C.byref(b)))
+        return g.value, n.value, b.value
+
+    def names(self):
+        out = []
+        for i in range(self.summary()[1]):
+            p = C.c_char_p()
+            check(lib().ti_cpubin_name(self.h, i, C.byref(p)))
+            out.append(p.value.decode())
+        return out
+
+    def tensor(self, name):
+        """(kind, info, data bytes, scale bytes) with numpy copies of the blob ranges."""
+        t = CpuBinTensor()
+        check(lib().ti_cpubin_tensor(self.h, name.encode(), C.byref(t)))
+        data = np.ctypeslib.as_array((C.c_uint8 * t.data_bytes).from_address(t.data)).copy() if t.data_bytes else np.zeros(0, np.uint8)
+        sc = (np.ctypeslib.as_array((C.c_uint8 * t.scale_bytes).from_address(t.scales)).copy()
+              if t.scale_bytes else np.zeros(0, np.uint8))
+        return t, data, sc
+
+    def embed_row(self, name, row, dim):
+        out = np.zeros(dim, np.float32)
+        check(lib().ti_cpubin_embed_row(self.h, name.encode(), row, out.ctypes.data, dim))
+        return out
+
+    def close(self):
+        if self.h:
+            lib().ti_cpubin_close(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
 
 
 def device_count():

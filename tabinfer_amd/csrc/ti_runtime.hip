@@ -213,7 +213,10 @@ extern "C" int ti_sync(ti_ctx* c) {
 extern "C" int ti_event_record(ti_ctx* c, int slot) {
     TI_CHECK_CTX(c);
     TI_REQUIRE(slot >= 0 && slot < 64, "ti_event_record: slot %d out of [0,64)", slot);
-    TI_HIP(hipEventRecord(c->ev[slot], c->stream));
+    // inside a capture the record becomes an event-record node of the graph (an external
+    // event), so every replay timestamps the point where it sits between the kernels
+    if (c->capturing) TI_HIP(hipEventRecordWithFlags(c->ev[slot], c->stream, hipEventRecordExternal));
+    else TI_HIP(hipEventRecord(c->ev[slot], c->stream));
     return TI_OK;
 }
 

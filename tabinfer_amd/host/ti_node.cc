@@ -30,7 +30,8 @@
 namespace {
 
 // ---- handles -------------------------------------------------------------------------
-enum Tag : uint32_t { TAG_CTX = 0x74696378, TAG_BUF = 0x74696262, TAG_GRAPH = 0x74696767, TAG_MODEL = 0x7469716d };
+enum Tag : uint32_t { TAG_CTX = 0x74696378, TAG_BUF = 0x74696262, TAG_GRAPH = 0x74696767, TAG_MODEL = 0x7469716d,
+                     TAG_CPUBIN = 0x74696362 };
 
 // A context lives until its JS handle is finalized (or shutdown() is called) AND every
 // buffer, graph and model made on it is gone: they hold counted references, so a
@@ -140,7 +141,20 @@ CtxH* get_ctx(napi_env env, napi_value v, const char* fn) {
     return h;
 }
 
+// A .cpu.bin container (host memory only; no context).
+struct CpuBinH {
+    uint32_t tag = TAG_CPUBIN;
+    ti_cpubin* c = nullptr;   // null once closed
+};
+
 // ---- finalizers ---------------------------------------------------------------------------
+void fin_cpubin(napi_env, void* data, void*) {
+    CpuBinH* h = static_cast<CpuBinH*>(data);
+    if (h->c) ti_cpubin_close(h->c);
+    h->tag = 0;
+    delete h;
+}
+
 void fin_ctx(napi_env, void* data, void*) {
     ctx_unref(static_cast<CtxH*>(data));
 }
@@ -859,6 +873,145 @@ napi_value js_qwen3_write_tokens(napi_env env, napi_callback_info info) {
 }
 
 // qwen3_read_tokens(ctx, model, from, count) -> Int32Array
+// ---- the .cpu.bin container (binfmt.rs Container) ------------------------------------------
+napi_value wrap_cpubin(napi_env env, ti_cpubin* c) {
+    CpuBinH* h = new CpuBinH;
+    h->c = c;
+    napi_value out;
+    napi_create_external(env, h, fin_cpubin, nullptr, &out);
+    return out;
+}
+
+CpuBinH* get_cpubin(napi_env env, napi_value v, const char* fn) {
+    CpuBinH* h = handle_of<CpuBinH>(env, v, TAG_CPUBIN);
+    if (!h || !h->c) { arg_error(env, fn, 0, "an open container from cpubin_open()"); return nullptr; }
+    return h;
+}
+
+// cpubin_open(path) -> container
+napi_value js_cpubin_open(napi_env env, napi_callback_info info) {
+    Args a(env, info);
+    if (!want_args(env, a, 1, "cpubin_open")) return nullptr;
+    char path[4096];
+    size_t n;
+    if (napi_get_value_string_utf8(env, a.v[0], path, sizeof path, &n) != napi_ok) return arg_error(env, "cpubin_open", 0, "a path"), nullptr;
+    ti_cpubin* c = nullptr;
+    const int rc = ti_cpubin_open(path, &c);
+    return rc ? throw_ti(env, "cpubin_open", rc) : wrap_cpubin(env, c);
+}
+
+// cpubin_parse(bytes: TypedArray | ArrayBuffer) -> container (Container::from_bytes)
+napi_value js_cpubin_parse(napi_env env, napi_callback_info info) {
+    Args a(env, info);
+    if (!want_args(env, a, 1, "cpubin_parse")) return nullptr;
+    void* d;
+    size_t len;
+    if (!host_bytes(env, a.v[0], &d, &len, "cpubin_parse", 0)) return nullptr;
+    ti_cpubin* c = nullptr;
+    const int rc = ti_cpubin_parse(d, len, &c);
+    return rc ? throw_ti(env, "cpubin_parse", rc) : wrap_cpubin(env, c);
+}
+
+napi_value js_cpubin_close(napi_env env, napi_callback_info info) {
+    Args a(env, info);
+    CpuBinH* h = a.n == 1 ? get_cpubin(env, a.v[0], "cpubin_close") : nullptr;
+    if (!h) return a.n == 1 ? nullptr : throw_msg(env, "cpubin_close expects (container)");
+    ti_cpubin_close(h->c);
+    h->c = nullptr;
+    return undefined(env);
+}
+
+// cpubin_summary(container) -> {groupSize, tensors, blobBytes}
+napi_value js_cpubin_summary(napi_env env, napi_callback_info info) {
+    Args a(env, info);
+    CpuBinH* h = a.n == 1 ? get_cpubin(env, a.v[0], "cpubin_summary") : nullptr;
+    if (!h) return a.n == 1 ? nullptr : throw_msg(env, "cpubin_summary expects (container)");
+    int g = 0, n = 0;
+    size_t b = 0;
+    const int rc = ti_cpubin_summary(h->c, &g, &n, &b);
+    if (rc) return throw_ti(env, "cpubin_summary", rc);
+    napi_value o;
+    napi_create_object(env, &o);
+    napi_set_named_property(env, o, "groupSize", num(env, g));
+    napi_set_named_property(env, o, "tensors", num(env, n));
+    napi_set_named_property(env, o, "blobBytes", num(env, (double)b));
+    return o;
+}
+
+// cpubin_name(container, i) -> the i-th tensor name (name order)
+napi_value js_cpubin_name(napi_env env, napi_callback_info info) {
+    Args a(env, info);
+    if (!want_args(env, a, 2, "cpubin_name")) return nullptr;
+    CpuBinH* h = get_cpubin(env, a.v[0], "cpubin_name");
+    int64_t i;
+    if (!h || !get_i64(env, a.v[1], &i, "cpubin_name", 1)) return nullptr;
+    const char* name = nullptr;
+    const int rc = ti_cpubin_name(h->c, (int)i, &name);
+    if (rc) return throw_ti(env, "cpubin_name", rc);
+    napi_value out;
+    napi_create_string_utf8(env, name, NAPI_AUTO_LENGTH, &out);
+    return out;
+}
+
+napi_value copy_bytes(napi_env env, const void* p, size_t n) {
+    void* d;
+    napi_value ab, u8;
+    napi_create_arraybuffer(env, n, &d, &ab);
+    if (n) std::memcpy(d, p, n);
+    napi_create_typedarray(env, napi_uint8_array, n, ab, 0, &u8);
+    return u8;
+}
+
+// cpubin_tensor(container, name) -> {kind: 'tern'|'embed_f16'|'f32', N, K, shape, data: Uint8Array,
+// scales: Uint8Array | null} (copies of the blob ranges)
+napi_value js_cpubin_tensor(napi_env env, napi_callback_info info) {
+    Args a(env, info);
+    if (!want_args(env, a, 2, "cpubin_tensor")) return nullptr;
+    CpuBinH* h = get_cpubin(env, a.v[0], "cpubin_tensor");
+    if (!h) return nullptr;
+    char name[512];
+    size_t nl;
+    if (napi_get_value_string_utf8(env, a.v[1], name, sizeof name, &nl) != napi_ok) return arg_error(env, "cpubin_tensor", 1, "a string"), nullptr;
+    ti_cpubin_tensor_info t;
+    const int rc = ti_cpubin_tensor(h->c, name, &t);
+    if (rc) return throw_ti(env, "cpubin_tensor", rc);
+    napi_value o, kind, shape, nul;
+    napi_create_object(env, &o);
+    napi_get_null(env, &nul);
+    napi_create_string_utf8(env, t.kind == TI_CPUBIN_TERN ? "tern" : t.kind == TI_CPUBIN_EMBED_F16 ? "embed_f16" : "f32",
+                            NAPI_AUTO_LENGTH, &kind);
+    napi_set_named_property(env, o, "kind", kind);
+    napi_set_named_property(env, o, "N", num(env, (double)t.N));
+    napi_set_named_property(env, o, "K", num(env, (double)t.K));
+    napi_create_array_with_length(env, (size_t)t.ndim, &shape);
+    for (int i = 0; i < t.ndim; i++) napi_set_element(env, shape, (uint32_t)i, num(env, (double)t.shape[i]));
+    napi_set_named_property(env, o, "shape", shape);
+    napi_set_named_property(env, o, "data", copy_bytes(env, t.data, t.data_bytes));
+    napi_set_named_property(env, o, "scales", t.scales ? copy_bytes(env, t.scales, t.scale_bytes) : nul);
+    return o;
+}
+
+// cpubin_embed_row(container, name, row, dim) -> Float32Array
+napi_value js_cpubin_embed_row(napi_env env, napi_callback_info info) {
+    Args a(env, info);
+    if (!want_args(env, a, 4, "cpubin_embed_row")) return nullptr;
+    CpuBinH* h = get_cpubin(env, a.v[0], "cpubin_embed_row");
+    if (!h) return nullptr;
+    char name[512];
+    size_t nl;
+    int64_t row, dim;
+    if (napi_get_value_string_utf8(env, a.v[1], name, sizeof name, &nl) != napi_ok) return arg_error(env, "cpubin_embed_row", 1, "a string"), nullptr;
+    if (!get_i64(env, a.v[2], &row, "cpubin_embed_row", 2) || !get_i64(env, a.v[3], &dim, "cpubin_embed_row", 3)) return nullptr;
+    if (dim < 0 || dim > (1 << 24)) return throw_msg(env, "cpubin_embed_row: bad dim");
+    void* d;
+    napi_value ab, f32;
+    napi_create_arraybuffer(env, (size_t)dim * 4, &d, &ab);
+    const int rc = ti_cpubin_embed_row(h->c, name, row, static_cast<float*>(d), (int)dim);
+    if (rc) return throw_ti(env, "cpubin_embed_row", rc);
+    napi_create_typedarray(env, napi_float32_array, (size_t)dim, ab, 0, &f32);
+    return f32;
+}
+
 napi_value js_qwen3_read_tokens(napi_env env, napi_callback_info info) {
     const char* fn = "qwen3_read_tokens";
     Args a(env, info);
@@ -955,6 +1108,13 @@ napi_value module_init(napi_env env, napi_value exports) {
         FN("qwen3_trace", js_qwen3_trace),
         FN("qwen3_write_tokens", js_qwen3_write_tokens),
         FN("qwen3_read_tokens", js_qwen3_read_tokens),
+        FN("cpubin_open", js_cpubin_open),
+        FN("cpubin_parse", js_cpubin_parse),
+        FN("cpubin_close", js_cpubin_close),
+        FN("cpubin_summary", js_cpubin_summary),
+        FN("cpubin_name", js_cpubin_name),
+        FN("cpubin_tensor", js_cpubin_tensor),
+        FN("cpubin_embed_row", js_cpubin_embed_row),
     };
     napi_define_properties(env, exports, sizeof props / sizeof props[0], props);
     return exports;
