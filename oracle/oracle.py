@@ -83,6 +83,13 @@ _sig("or_tern_pool_start", _i, [_i])
 _sig("or_tern_pool_stop", None, [])
 _sig("or_tern_pool_run", None, [_p, _i])
 _sig("or_tern_set_serial", None, [_p, _i])
+_sig("or_n2_rmsnorm", None, [_p, _p, _i, _f, _p])
+_sig("or_n2_rmsnorm_heads", None, [_p, _p, _i, _i, _f])
+_sig("or_n2_rope_table", None, [_i, _i, _f, _p])
+_sig("or_n2_rope_with_table", None, [_p, _i, _i, _p])
+_sig("or_n2_swiglu", None, [_p, _p, _i, _p])
+_sig("or_n2_attention", None, [_p, _p, _p, _i, _i, _i, _i, _p])
+_sig("or_n2_argmax", _i, [_p, _i])
 _sig("or_requant43", None, [_p, _p, _i, _i, _p, _p])
 _sig("or_router", None, [_p, _p, _i, _i, _i, _p, _p])
 _sig("or_moe_gemv_q3", None, [_p, _p, _p, _p, _i, _i, _i, _i, _i, _p])
@@ -459,3 +466,48 @@ def moe_combine(x, o, wt, H, K, T):
     x = np.array(x, dtype=np.float32, copy=True)
     _L.or_moe_combine(_ptr(x), _ptr(_c(o, np.float32)), _ptr(_c(wt, np.float32)), H, K, T)
     return x
+
+
+# ---- the Bonsai forward's f32 glue (ops.rs, model.rs) ----------------------------------------
+def n2_rmsnorm(x, w, eps):
+    x, w = _c(x, np.float32), _c(w, np.float32)
+    out = np.zeros(x.size, np.float32)
+    _L.or_n2_rmsnorm(_ptr(x), _ptr(w), x.size, eps, _ptr(out))
+    return out
+
+
+def n2_rmsnorm_heads(t, w, n_heads, head_dim, eps):
+    t = np.array(t, np.float32)
+    _L.or_n2_rmsnorm_heads(_ptr(t), _ptr(_c(w, np.float32)), n_heads, head_dim, eps)
+    return t
+
+
+def n2_rope_table(head_dim, pos, theta):
+    t = np.zeros(head_dim, np.float32)
+    _L.or_n2_rope_table(head_dim, pos, theta, _ptr(t))
+    return t
+
+
+def n2_rope_with_table(t, n_heads, head_dim, table):
+    t = np.array(t, np.float32)
+    _L.or_n2_rope_with_table(_ptr(t), n_heads, head_dim, _ptr(_c(table, np.float32)))
+    return t
+
+
+def n2_swiglu(gate, up):
+    g, u = _c(gate, np.float32), _c(up, np.float32)
+    out = np.zeros(g.size, np.float32)
+    _L.or_n2_swiglu(_ptr(g), _ptr(u), g.size, _ptr(out))
+    return out
+
+
+def n2_attention(q, kc, vc, S, n_heads, n_kv, head_dim):
+    out = np.zeros(n_heads * head_dim, np.float32)
+    _L.or_n2_attention(_ptr(_c(q, np.float32)), _ptr(_c(kc, np.float32)), _ptr(_c(vc, np.float32)), S, n_heads, n_kv,
+                       head_dim, _ptr(out))
+    return out
+
+
+def n2_argmax(x):
+    x = _c(x, np.float32)
+    return int(_L.or_n2_argmax(_ptr(x), x.size))

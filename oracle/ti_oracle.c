@@ -758,3 +758,105 @@ void or_moe_combine(float* x, const float* o, const float* wt, int H, int K, int
             x[(size_t)t * H + h] = x[(size_t)t * H + h] + s;
         }
 }
+
+/* ------------------------------------------------------------------------- */
+/* The Bonsai-1.7B forward's f32 glue, native/crates/n2-core/src/ops.rs and    */
+/* model.rs:349-501, in the reference's own f32 arithmetic and order (every sum */
+/* sequential from index 0, no fused multiply-adds: the Makefile builds with   */
+/* -ffp-contract=off).                                                          */
+/* ------------------------------------------------------------------------- */
+
+/* ops.rs:14-22: out = x * (1 / sqrt(mean(x^2) + eps)) * w */
+void or_n2_rmsnorm(const float* x, const float* w, int n, float eps, float* out) {
+    float ss = 0.0f;
+    for (int i = 0; i < n; i++) ss += x[i] * x[i];
+    const float mean = ss / (float)n;
+    const float inv = 1.0f / sqrtf(mean + eps);
+    for (int i = 0; i < n; i++) out[i] = x[i] * inv * w[i];
+}
+
+/* ops.rs:29-40: the same over each head of t[n_heads * head_dim], in place */
+void or_n2_rmsnorm_heads(float* t, const float* w, int n_heads, int head_dim, float eps) {
+    for (int h = 0; h < n_heads; h++) {
+        float* x = t + (size_t)h * head_dim;
+        float ss = 0.0f;
+        for (int i = 0; i < head_dim; i++) ss += x[i] * x[i];
+        const float mean = ss / (float)head_dim;
+        const float inv = 1.0f / sqrtf(mean + eps);
+        for (int i = 0; i < head_dim; i++) x[i] = x[i] * inv * w[i];
+    }
+}
+
+/* ops.rs:79-90: table[i] = cos, table[half + i] = sin of pos * theta^(-2i/head_dim) (f32) */
+void or_n2_rope_table(int head_dim, int pos, float theta, float* table) {
+    const int half = head_dim / 2;
+    for (int i = 0; i < half; i++) {
+        const float e = -((float)(2 * i)) / (float)head_dim;
+        const float inv = powf(theta, e);
+        const float ang = (float)pos * inv;
+        table[i] = cosf(ang);
+        table[half + i] = sinf(ang);
+    }
+}
+
+/* ops.rs:93-107: split-half rotation of every head with a table, in place */
+void or_n2_rope_with_table(float* t, int n_heads, int head_dim, const float* table) {
+    const int half = head_dim / 2;
+    for (int h = 0; h < n_heads; h++) {
+        float* x = t + (size_t)h * head_dim;
+        for (int i = 0; i < half; i++) {
+            const float x0 = x[i], x1 = x[half + i];
+            x[i] = x0 * table[i] - x1 * table[half + i];
+            x[half + i] = x1 * table[i] + x0 * table[half + i];
+        }
+    }
+}
+
+/* ops.rs:110-117 */
+void or_n2_swiglu(const float* gate, const float* up, int n, float* out) {
+    for (int i = 0; i < n; i++) {
+        const float g = gate[i];
+        out[i] = (g / (1.0f + expf(-g))) * up[i];
+    }
+}
+
+/* model.rs:421-447 with ops.rs:120-135: GQA attention of q[n_heads * head_dim] (normed,
+ * roped) over the f32 cache k/v[S][n_kv * head_dim]; scores scaled by 1/sqrt(head_dim),
+ * softmax max-subtracted, out = sum_p w_p v_p */
+void or_n2_attention(const float* q, const float* kc, const float* vc, int S, int n_heads, int n_kv, int head_dim,
+                     float* out) {
+    const int kv_dim = n_kv * head_dim, qpk = n_heads / n_kv;
+    const float scale = 1.0f / sqrtf((float)head_dim);
+    float* sc = (float*)malloc(sizeof(float) * (size_t)(S > 0 ? S : 1));
+    for (int h = 0; h < n_heads; h++) {
+        const int kvh = h / qpk;
+        const float* qh = q + (size_t)h * head_dim;
+        for (int p = 0; p < S; p++) {
+            const float* kh = kc + (size_t)p * kv_dim + (size_t)kvh * head_dim;
+            float dot = 0.0f;
+            for (int i = 0; i < head_dim; i++) dot += kh[i] * qh[i];
+            sc[p] = dot * scale;
+        }
+        float mx = -INFINITY;
+        for (int p = 0; p < S; p++) mx = fmaxf(mx, sc[p]);
+        float sum = 0.0f;
+        for (int p = 0; p < S; p++) { sc[p] = expf(sc[p] - mx); sum += sc[p]; }
+        const float inv = 1.0f / sum;
+        for (int p = 0; p < S; p++) sc[p] *= inv;
+        float* o = out + (size_t)h * head_dim;
+        for (int i = 0; i < head_dim; i++) o[i] = 0.0f;
+        for (int p = 0; p < S; p++) {
+            const float* vh = vc + (size_t)p * kv_dim + (size_t)kvh * head_dim;
+            for (int i = 0; i < head_dim; i++) o[i] += sc[p] * vh[i];
+        }
+    }
+    free(sc);
+}
+
+/* ops.rs:138-149: index of the largest element, the lowest index on ties (start -inf, 0) */
+int or_n2_argmax(const float* x, int n) {
+    int best = 0;
+    float bv = -INFINITY;
+    for (int i = 0; i < n; i++) if (x[i] > bv) { bv = x[i]; best = i; }
+    return best;
+}

@@ -143,6 +143,16 @@ void or_tern_pool_stop(void);
 void or_tern_pool_run(const or_tern_mat* mats, int nmat);
 void or_tern_set_serial(const or_tern_mat* mats, int nmat);   /* one thread, no pool */
 
+/* ---- the Bonsai forward's f32 glue (native/crates/n2-core/src/ops.rs, model.rs:349-501) */
+void or_n2_rmsnorm(const float* x, const float* w, int n, float eps, float* out);      /* ops.rs:14-22   */
+void or_n2_rmsnorm_heads(float* t, const float* w, int n_heads, int head_dim, float eps); /* ops.rs:29-40 */
+void or_n2_rope_table(int head_dim, int pos, float theta, float* table);               /* ops.rs:79-90   */
+void or_n2_rope_with_table(float* t, int n_heads, int head_dim, const float* table);   /* ops.rs:93-107  */
+void or_n2_swiglu(const float* gate, const float* up, int n, float* out);             /* ops.rs:110-117 */
+void or_n2_attention(const float* q, const float* kc, const float* vc, int S, int n_heads, int n_kv,
+                     int head_dim, float* out);                                        /* model.rs:421-447 */
+int  or_n2_argmax(const float* x, int n);                                              /* ops.rs:138-149 */
+
 /* ---- int3 MoE (models/lfm25.js) ----------------------------------- */
 void or_requant43(const uint32_t* pack4, const uint16_t* sc4, int rows, int K,
                   uint32_t* p3, uint16_t* s3);                                  /* lfm25.js:833-856 */

@@ -2,9 +2,13 @@
 
     python -m tabinfer_amd.rocprof_summary stats  <dir-with-run_kernel_stats.csv>
     python -m tabinfer_amd.rocprof_summary pmc    <fetch-dir> <write-dir> [--calib KERNEL BYTES]
+    python -m tabinfer_amd.rocprof_summary counters <dir> COUNTER [COUNTER ...]
 
 `stats` prints the per-kernel table of a `rocprofv3 --kernel-trace --stats`
 run (calls, average and total duration).
+
+`counters` prints, per kernel, the average of each named counter per dispatch
+of one `rocprofv3 --pmc` run (e.g. the MFMA counters).
 
 `pmc` prints, per kernel, the average FETCH_SIZE and WRITE_SIZE (KiB per
 dispatch) of two `rocprofv3 --pmc` runs. With --calib, the counters of the
@@ -74,9 +78,21 @@ def pmc(fetch_dir, write_dir, calib=None):
     return "\n".join(lines)
 
 
+def counters(d, names):
+    avgs = [pmc_avg(d, n) for n in names]
+    kernels = sorted(set().union(*[a[0].keys() for a in avgs]))
+    lines = ["| kernel | dispatches | " + " | ".join(names) + " |", "|---|---:|" + "---:|" * len(names)]
+    for k in kernels:
+        n = max(a[1].get(k, 0) for a in avgs)
+        lines.append("| %s | %d | %s |" % (short(k), n, " | ".join("%.0f" % a[0][k] if k in a[0] else "-" for a in avgs)))
+    return "\n".join(lines)
+
+
 def main(argv):
     if len(argv) >= 2 and argv[0] == "stats":
         print(stats(argv[1]))
+    elif len(argv) >= 3 and argv[0] == "counters":
+        print(counters(argv[1], argv[2:]))
     elif len(argv) >= 3 and argv[0] == "pmc":
         calib = None
         if "--calib" in argv:
