@@ -253,6 +253,50 @@ int ti_cpubin_tensor(const ti_cpubin* c, const char* name, ti_cpubin_tensor_info
 /* embed_row (binfmt.rs:321-342): row `row` of an embed_f16 tensor decoded to f32. */
 int ti_cpubin_embed_row(const ti_cpubin* c, const char* name, long long row, float* dst, int dim);
 
+/* ---- the Bonsai-1.7B ternary decoder ----------------------------------------------------
+ * The native engine's Model (native/crates/n2-core/src/model.rs:349-501, ops.rs) on the GPU:
+ * ternary projections and lm_head in the .cpu.bin layout (Q2_0_g64 codes + f32 scales),
+ * f32 norms, f16 embeddings, an f32 KV cache of max_ctx positions, a token history and a
+ * device-side position. Per token: rmsnorm, per-tensor int8 quantize_act, ternary GEMVs
+ * scaled by 1/scale, qk-norm, split-half RoPE, GQA attention, SwiGLU, residuals, final
+ * norm, lm_head, argmax (ops::argmax, the lowest index on ties). head_dim 128 with two
+ * query heads per KV head; hidden, intermediate and n_heads * head_dim multiples of 1024,
+ * at most 8192. */
+typedef struct ti_bonsai ti_bonsai;
+typedef struct {
+    int layers, hidden, intermediate, n_heads, n_kv_heads, head_dim, vocab;
+    float rope_theta, rms_eps;
+    int max_ctx;      /* KV capacity in positions */
+} ti_bonsai_config;
+int ti_bonsai_create(ti_ctx* ctx, const ti_bonsai_config* cfg, ti_bonsai** out);
+int ti_bonsai_destroy(ti_ctx* ctx, ti_bonsai* m);
+/* Model::load + check_shapes (model.rs:256-322): every tensor the forward needs, of the kind
+ * and size the config implies, uploaded from an open container (ti_cpubin_open). */
+int ti_bonsai_load(ti_ctx* ctx, ti_bonsai* m, const ti_cpubin* bin);
+/* device buffers of a tensor by its container name: ternary tensors return codes + scales,
+ * norms f32, the embedding f16 */
+int ti_bonsai_tensor(ti_bonsai* m, const char* name, void** data, size_t* data_bytes, void** scales,
+                     size_t* scale_bytes);
+int ti_bonsai_kv(ti_bonsai* m, int layer, float** kc, float** vc);   /* f32 [max_ctx][n_kv*head_dim] */
+int ti_bonsai_logits(ti_bonsai* m, float** logits);                   /* f32 [vocab], last decode */
+/* Model::forward per prompt token at positions pos.. (logits for the last one only, as n2's
+ * prefill): history[pos..pos+T) = ids, argmax of the last logits -> history[pos+T], device
+ * position = pos+T. ids == NULL takes the tokens already in the history. */
+int ti_bonsai_forward(ti_ctx* ctx, ti_bonsai* m, const int32_t* ids, int T, int pos);
+/* one token at the device position P: embeds history[P], writes KV row P, argmax ->
+ * history[P+1], P += 1. Reads nothing from the host (capturable, replayable). */
+int ti_bonsai_decode(ti_ctx* ctx, ti_bonsai* m);
+int ti_bonsai_set_pos(ti_ctx* ctx, ti_bonsai* m, int pos);
+int ti_bonsai_write_tokens(ti_ctx* ctx, ti_bonsai* m, int from, int count, const int32_t* ids);
+int ti_bonsai_read_tokens(ti_ctx* ctx, ti_bonsai* m, int from, int count, int32_t* ids);
+/* Parity trace (debug; no reference counterpart). With buf set, every later step also copies
+ * per layer, in 32-bit words: x_in[H], xn[H], its int8 codes [H/4] and scale [1], q/k/v as
+ * the GEMVs leave them (units of 1/scale) [nq][nkv][nkv], attn[nq], its codes [nq/4] and
+ * scale [1], x_mid[H], xn2[H], codes [H/4], scale [1], gate[I], up[I] (units of 1/scale),
+ * swi[I], codes [I/4], scale [1], down[H] (units of 1/scale); after the last layer x_final[H],
+ * xn_final[H], codes [H/4], scale [1]. NULL switches it off. */
+int ti_bonsai_trace(ti_bonsai* m, void* buf, size_t bytes);
+
 /* ---- int3 MoE experts (LFM2.5) ----------------------------------------------------
  * int3 group of 32 weights: three u32 bitplanes (bit i of plane b = bit b of q3+4 for
  * element i) and one f16 scale; the rows of all experts are stacked expert-major

@@ -300,6 +300,17 @@ def gateup_silu_q4_par(xq, xs, gp, gs, up, us, I, H, parts=16):
     return y
 
 
+def tern_gemv_scalar_par(codes, sc, act, xsum, N, K, parts=16):
+    """tern_gemv_scalar with its rows split over threads (each row's arithmetic unchanged)."""
+    codes, sc, act, xsum = _c(codes, np.uint8), _c(sc, np.float32), _c(act, np.int8), _c(xsum, np.int32)
+    out = np.zeros(N, np.float32)
+    def run(r0, r1):
+        _L.or_tern_gemv_scalar(codes.ctypes.data + r0 * K // 4, sc.ctypes.data + r0 * (K // 64) * 4, _ptr(act),
+                               _ptr(xsum), r1 - r0, K, out.ctypes.data + r0 * 4)
+    list(_pool().map(lambda rr: run(*rr), _row_chunks(N, parts)))
+    return out
+
+
 def attn_causal_q8_kvheads(qr, kq, ks, vq, vs, T, pos0, nHq, nKv, hd, hk0, hk1, out=None):
     out = np.zeros(T * nHq * hd, np.float64) if out is None else out
     _L.or_attn_causal_q8_kvheads(_ptr(_c(qr, np.float32)), _ptr(_c(kq, np.uint32)), _ptr(_c(ks, np.float32)),

@@ -105,7 +105,24 @@ class CpuBinTensor(C.Structure):
                 ("data", _p), ("data_bytes", _sz), ("scales", _p), ("scale_bytes", _sz)]
 
 
+class BonsaiConfig(C.Structure):
+    _fields_ = [("layers", _i), ("hidden", _i), ("intermediate", _i), ("n_heads", _i), ("n_kv_heads", _i),
+                ("head_dim", _i), ("vocab", _i), ("rope_theta", _f), ("rms_eps", _f), ("max_ctx", _i)]
+
+
 SIGS.update({
+    "ti_bonsai_create": [_p, C.POINTER(BonsaiConfig), C.POINTER(_p)],
+    "ti_bonsai_destroy": [_p, _p],
+    "ti_bonsai_load": [_p, _p, _p],
+    "ti_bonsai_tensor": [_p, C.c_char_p, C.POINTER(_p), C.POINTER(_sz), C.POINTER(_p), C.POINTER(_sz)],
+    "ti_bonsai_kv": [_p, _i, C.POINTER(_p), C.POINTER(_p)],
+    "ti_bonsai_logits": [_p, C.POINTER(_p)],
+    "ti_bonsai_forward": [_p, _p, _p, _i, _i],
+    "ti_bonsai_decode": [_p, _p],
+    "ti_bonsai_set_pos": [_p, _p, _i],
+    "ti_bonsai_write_tokens": [_p, _p, _i, _i, _p],
+    "ti_bonsai_read_tokens": [_p, _p, _i, _i, _p],
+    "ti_bonsai_trace": [_p, _p, _sz],
     "ti_cpubin_open": [C.c_char_p, C.POINTER(_p)],
     "ti_cpubin_parse": [_p, _sz, C.POINTER(_p)],
     "ti_cpubin_close": [_p],
@@ -333,6 +350,66 @@ class Qwen3:
     def close(self):
         if self.h:
             check(lib().ti_qwen3_destroy(self.ctx.h, self.h))
+            self.h = None
+
+
+class Bonsai:
+    """The native Bonsai ternary decoder (ti_bonsai_*) on a Ctx."""
+
+    def __init__(self, ctx, **cfg):
+        self.ctx = ctx
+        self.cfg = BonsaiConfig(**cfg)
+        h = C.c_void_p()
+        check(lib().ti_bonsai_create(ctx.h, C.byref(self.cfg), C.byref(h)))
+        self.h = h.value
+
+    def tensor(self, name):
+        d, s = C.c_void_p(), C.c_void_p()
+        nd, ns = C.c_size_t(), C.c_size_t()
+        check(lib().ti_bonsai_tensor(self.h, name.encode(), C.byref(d), C.byref(nd), C.byref(s), C.byref(ns)))
+        return d.value, nd.value, s.value, ns.value
+
+    def load(self, cpubin):
+        check(lib().ti_bonsai_load(self.ctx.h, self.h, cpubin.h))
+
+    def kv(self, layer):
+        k, v = C.c_void_p(), C.c_void_p()
+        check(lib().ti_bonsai_kv(self.h, layer, C.byref(k), C.byref(v)))
+        return k.value, v.value
+
+    def logits_ptr(self):
+        p = C.c_void_p()
+        check(lib().ti_bonsai_logits(self.h, C.byref(p)))
+        return p.value
+
+    def forward(self, ids, pos, T=None):
+        if ids is None:
+            check(lib().ti_bonsai_forward(self.ctx.h, self.h, None, T, pos))
+            return
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        check(lib().ti_bonsai_forward(self.ctx.h, self.h, ids.ctypes.data, ids.size, pos))
+
+    def decode(self):
+        check(lib().ti_bonsai_decode(self.ctx.h, self.h))
+
+    def set_pos(self, pos):
+        check(lib().ti_bonsai_set_pos(self.ctx.h, self.h, pos))
+
+    def write_tokens(self, start, ids):
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        check(lib().ti_bonsai_write_tokens(self.ctx.h, self.h, start, ids.size, ids.ctypes.data))
+
+    def read_tokens(self, start, count):
+        out = np.zeros(count, np.int32)
+        check(lib().ti_bonsai_read_tokens(self.ctx.h, self.h, start, count, out.ctypes.data))
+        return out
+
+    def trace(self, buf):
+        check(lib().ti_bonsai_trace(self.h, int(buf) if buf is not None else None, buf.nbytes if buf is not None else 0))
+
+    def close(self):
+        if self.h:
+            check(lib().ti_bonsai_destroy(self.ctx.h, self.h))
             self.h = None
 
 

@@ -1,0 +1,845 @@
+// ti_bonsai.hip — the Bonsai-1.7B ternary decoder on the GPU: the native engine's forward
+// (native/crates/n2-core/src/model.rs:349-501 with ops.rs) around the ternary GEMV.
+//
+// Per token, as model.rs computes it: embed (f16 row) -> per layer: rmsnorm, per-tensor
+// int8 quantize (n2 quantize_act), q/k/v ternary GEMVs scaled by 1/scale, per-head
+// qk-norm, split-half RoPE (theta 1e6), the post-RoPE key and the value appended to an
+// f32 KV cache, GQA attention (softmax over 1/sqrt(hd)-scaled scores), quantize, o_proj,
+// residual, rmsnorm, quantize, gate/up, SwiGLU, quantize, down, residual -> final rmsnorm,
+// quantize, ternary lm_head scaled by 1/scale -> logits, argmax (ops::argmax: the lowest
+// index on ties). The ternary GEMVs are the library's bit-exact kernels (k_tern.hip); the
+// int8 codes are exact functions of their f32 inputs; every 1/scale product and residual
+// add uses the reference's f32 operations in its order. The reductions (norm sums, the
+// attention) run as trees, not the reference's sequential sums.
+//
+// The position lives on the device (the decode step is one graph, replayed per token):
+// the step embeds hist[P], writes KV row P, and (with logits) puts the argmax in hist[P+1]
+// and advances P.
+#include "ti_internal.h"
+#include <math.h>
+#include <string.h>
+#include <stdio.h>
+#include <string>
+#include <vector>
+
+namespace {
+
+constexpr int BN_THREADS = 1024;
+constexpr int BN_ATTN_CHUNK = 256;        // keys per attention workgroup
+constexpr int BN_AMAX_PARTS = 256;
+
+// total of one float per thread over a 1024-thread workgroup (a tree; every thread gets it)
+__device__ __forceinline__ float wg_sum_1024(float v, float* red) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += ti_xor(v, o);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float s = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 16; w++) s += red[w];
+    return s;
+}
+
+__device__ __forceinline__ float wg_max_1024(float v, float* red) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, ti_xor(v, o));
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float m = red[0];
+#pragma unroll
+    for (int w = 1; w < 16; w++) m = fmaxf(m, red[w]);
+    return m;
+}
+
+// n2 quantize_act of v[n] held EPT per thread (tern.rs:206-222): scale = 127/amax (1 if
+// amax = 0), a = clamp(round-half-away(v * scale), -127, 127), xsum per 64.
+template <int EPT>
+__device__ __forceinline__ void quant_n2(const float (&v)[EPT], int n, int8_t* __restrict__ act,
+                                         int32_t* __restrict__ xsum, float* __restrict__ scale_out, float* red) {
+    const int t = threadIdx.x;
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < EPT; i++)
+        if (t + BN_THREADS * i < n) m = fmaxf(m, fabsf(v[i]));
+    const float amax = wg_max_1024(m, red);
+    const float scale = amax > 0.0f ? 127.0f / amax : 1.0f;
+    if (t == 0) *scale_out = scale;
+    // element e = t + 1024 i: its 64-block is e / 64, one wave's lanes cover one block
+#pragma unroll
+    for (int i = 0; i < EPT; i++) {
+        const int e = t + BN_THREADS * i;
+        int q = 0;
+        if (e < n) {
+            float r = roundf(v[i] * scale);
+            r = fminf(fmaxf(r, -127.0f), 127.0f);
+            q = (int)r;
+            act[e] = (int8_t)q;
+        }
+        int sum = q;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) sum += ti_xor(sum, o);
+        if ((t & 63) == 0 && e < n) xsum[e / 64] = sum;
+    }
+}
+
+// ---- embed: x = f32(emb[hist[P]]) ---------------------------------------------------------
+__global__ void k_bn_embed(const uint32_t* __restrict__ hist, const int* __restrict__ dpos, const uint16_t* __restrict__ emb,
+                           float* __restrict__ x, int H, int vocab, int cap) {
+    const int P = *dpos;
+    if (P >= cap) return;                              // past the cache: the step writes nothing
+    uint32_t id = hist[P];
+    id = id < (uint32_t)vocab ? id : (uint32_t)(vocab - 1);
+    for (int i = threadIdx.x; i < H; i += blockDim.x) x[i] = ti_h2f(emb[(size_t)id * H + i]);
+}
+
+// ---- residual add + rmsnorm + quantize (one workgroup) --------------------------------------
+// with add: x[i] = x[i] + add[i] * (1 / add_scale) (model.rs linear's scaling, then the
+// residual add); then xn = x * (1 / sqrt(mean(x^2) + eps)) * w (ops.rs:14-22) and the n2
+// quantizer of xn.
+template <int EPT>
+__global__ __launch_bounds__(BN_THREADS) void k_bn_norm_quant(float* __restrict__ x, const float* __restrict__ add,
+                                                             const float* __restrict__ add_scale, const float* __restrict__ w,
+                                                             float eps, int H, float* __restrict__ xn_out,
+                                                             int8_t* __restrict__ act, int32_t* __restrict__ xsum,
+                                                             float* __restrict__ scale_out) {
+    __shared__ float red[16];
+    const int t = threadIdx.x;
+    float v[EPT];
+    const float inv_add = add ? 1.0f / *add_scale : 0.0f;
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < EPT; i++) {
+        const int e = t + BN_THREADS * i;
+        v[i] = 0.0f;
+        if (e < H) {
+            float xe = x[e];
+            if (add) {
+                const float d = add[e] * inv_add;
+                xe = xe + d;
+                x[e] = xe;
+            }
+            v[i] = xe;
+            ss = ss + xe * xe;
+        }
+    }
+    const float mean = wg_sum_1024(ss, red) / (float)H;
+    const float inv = 1.0f / sqrtf(mean + eps);
+#pragma unroll
+    for (int i = 0; i < EPT; i++) {
+        const int e = t + BN_THREADS * i;
+        if (e < H) {
+            v[i] = v[i] * inv * w[e];
+            if (xn_out) xn_out[e] = v[i];
+        }
+    }
+    quant_n2<EPT>(v, H, act, xsum, scale_out, red);
+}
+
+// ---- quantize an f32 vector (the attention output) -----------------------------------------
+template <int EPT>
+__global__ __launch_bounds__(BN_THREADS) void k_bn_quant(const float* __restrict__ x, int n, int8_t* __restrict__ act,
+                                                        int32_t* __restrict__ xsum, float* __restrict__ scale_out) {
+    __shared__ float red[16];
+    float v[EPT];
+#pragma unroll
+    for (int i = 0; i < EPT; i++) {
+        const int e = threadIdx.x + BN_THREADS * i;
+        v[i] = e < n ? x[e] : 0.0f;
+    }
+    quant_n2<EPT>(v, n, act, xsum, scale_out, red);
+}
+
+// ---- SwiGLU of the scaled gate/up + quantize (ops.rs:110-117) ---------------------------------
+template <int EPT>
+__global__ __launch_bounds__(BN_THREADS) void k_bn_swiglu_quant(const float* __restrict__ graw, const float* __restrict__ uraw,
+                                                               const float* __restrict__ gu_scale, int n,
+                                                               float* __restrict__ swi_out, int8_t* __restrict__ act,
+                                                               int32_t* __restrict__ xsum, float* __restrict__ scale_out) {
+    __shared__ float red[16];
+    const float inv = 1.0f / *gu_scale;
+    float v[EPT];
+#pragma unroll
+    for (int i = 0; i < EPT; i++) {
+        const int e = threadIdx.x + BN_THREADS * i;
+        v[i] = 0.0f;
+        if (e < n) {
+            const float g = graw[e] * inv;
+            const float u = uraw[e] * inv;
+            v[i] = (g / (1.0f + expf(-g))) * u;
+            if (swi_out) swi_out[e] = v[i];
+        }
+    }
+    quant_n2<EPT>(v, n, act, xsum, scale_out, red);
+}
+
+// ---- q/k/v: scale, per-head RMSNorm, RoPE, KV append (model.rs:399-418) -----------------------
+// workgroup h < nHq: query head h -> qr; nHq <= h < nHq + nKv: KV head h - nHq -> the K row
+// (normed, roped) and the V row (scaled) of position P in the f32 cache. hd threads.
+__global__ __launch_bounds__(128) void k_bn_prep(const float* __restrict__ qraw, const float* __restrict__ kraw,
+                                                 const float* __restrict__ vraw, const float* __restrict__ scale,
+                                                 const float* __restrict__ qn, const float* __restrict__ kn,
+                                                 const float* __restrict__ rope, const int* __restrict__ dpos,
+                                                 float* __restrict__ qr, float* __restrict__ kc, float* __restrict__ vc,
+                                                 int nHq, int nKv, int hd, float eps, int cap) {
+    __shared__ float red[128];
+    __shared__ float y[128];
+    const int i = threadIdx.x, h = blockIdx.x, half = hd / 2;
+    const int P = *dpos;
+    if (P >= cap) return;
+    const bool isq = h < nHq;
+    const int hh = isq ? h : h - nHq;
+    const float inv = 1.0f / *scale;
+    const float raw = i < hd ? (isq ? qraw : kraw)[(size_t)hh * hd + i] : 0.0f;
+    const float a = raw * inv;
+    red[i] = i < hd ? a * a : 0.0f;
+    __syncthreads();
+    for (int st = 64; st > 0; st >>= 1) {
+        if (i < st) red[i] = red[i] + red[i + st];
+        __syncthreads();
+    }
+    const float mean = red[0] / (float)hd;
+    const float rinv = 1.0f / sqrtf(mean + eps);
+    const float nw = i < hd ? (isq ? qn : kn)[i] : 0.0f;
+    const float yn = a * rinv * nw;
+    y[i] = yn;
+    __syncthreads();
+    if (i < hd) {
+        const float* tab = rope + (size_t)P * hd;
+        const int j = i < half ? i : i - half;
+        const float c = tab[j], s = tab[half + j];
+        const float x0 = y[j], x1 = y[half + j];
+        const float r = i < half ? x0 * c - x1 * s : x1 * c + x0 * s;
+        const size_t kv_dim = (size_t)nKv * hd;
+        if (isq) {
+            qr[(size_t)hh * hd + i] = r;
+        } else {
+            kc[(size_t)P * kv_dim + (size_t)hh * hd + i] = r;
+            vc[(size_t)P * kv_dim + (size_t)hh * hd + i] = vraw[(size_t)hh * hd + i] * inv;
+        }
+    }
+}
+
+// ---- GQA attention over the f32 cache (model.rs:421-447) ------------------------------------
+// workgroup (KV head, split of BN_ATTN_CHUNK keys), G query heads of hd dims (G * hd <= 256):
+// scores by 16 lanes per key (8 dims each), a max/exp/sum over the chunk, then P V with
+// one thread per (head, dim); partials (o, m, l) per (query head, split).
+template <int G, int HD>
+__global__ __launch_bounds__(256) void k_bn_attn(const float* __restrict__ qr, const float* __restrict__ kc,
+                                                 const float* __restrict__ vc, const int* __restrict__ dpos, int nKv,
+                                                 float* __restrict__ po, float* __restrict__ pml, int ns_stride, int cap) {
+    constexpr int LPK = 16, DPL = HD / LPK;            // lanes per key, dims per lane
+    constexpr int KPP = 256 / LPK;                     // keys per pass
+    __shared__ float sc[G][BN_ATTN_CHUNK];
+    __shared__ float red[G][4];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int hk = blockIdx.x % nKv, split = blockIdx.x / nKv;
+    const int S = min(*dpos + 1, cap);
+    const int c0 = split * BN_ATTN_CHUNK;
+    if (c0 >= S) return;                               // the combine reads splits below ceil(S / chunk) only
+    const int n = min(BN_ATTN_CHUNK, S - c0);
+    const size_t kv_dim = (size_t)nKv * HD;
+    const float scale = 1.0f / sqrtf((float)HD);
+    const int kl = t / LPK, sl = t % LPK;
+    float q[G][DPL];
+#pragma unroll
+    for (int g = 0; g < G; g++)
+#pragma unroll
+        for (int d = 0; d < DPL; d++) q[g][d] = qr[(size_t)(hk * G + g) * HD + sl * DPL + d];
+    for (int j0 = 0; j0 < n; j0 += KPP) {
+        const int j = j0 + kl;
+        const int key = c0 + (j < n ? j : n - 1);
+        const float* kr = kc + (size_t)key * kv_dim + (size_t)hk * HD + sl * DPL;
+        float kv[DPL];
+#pragma unroll
+        for (int d = 0; d < DPL; d++) kv[d] = kr[d];
+        float part[G];
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            float s = 0.0f;
+#pragma unroll
+            for (int d = 0; d < DPL; d++) s = s + kv[d] * q[g][d];
+            part[g] = s;
+        }
+#pragma unroll
+        for (int o = LPK / 2; o > 0; o >>= 1)
+#pragma unroll
+            for (int g = 0; g < G; g++) part[g] += ti_xor(part[g], o);
+        if (sl == 0 && j < n)
+#pragma unroll
+            for (int g = 0; g < G; g++) sc[g][j] = part[g] * scale;
+    }
+    __syncthreads();
+    float m[G], l[G];
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        float v = -INFINITY;
+        for (int j = t; j < n; j += 256) v = fmaxf(v, sc[g][j]);
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, ti_xor(v, o));
+        if (lane == 0) red[g][wave] = v;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < G; g++) m[g] = fmaxf(fmaxf(red[g][0], red[g][1]), fmaxf(red[g][2], red[g][3]));
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        float s = 0.0f;
+        for (int j = t; j < n; j += 256) {
+            const float p = expf(sc[g][j] - m[g]);
+            sc[g][j] = p;
+            s += p;
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) s += ti_xor(s, o);
+        if (lane == 0) red[g][wave] = s;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < G; g++) l[g] = (red[g][0] + red[g][1]) + (red[g][2] + red[g][3]);
+    // P V: thread (g, d)
+    if (t < G * HD) {
+        const int g = t / HD, d = t % HD;
+        const float* vcol = vc + (size_t)c0 * kv_dim + (size_t)hk * HD + d;
+        float o = 0.0f;
+        for (int j = 0; j < n; j++) o = fmaf(sc[g][j], vcol[(size_t)j * kv_dim], o);
+        const size_t slot = (size_t)(hk * G + g) * ns_stride + split;
+        po[slot * HD + d] = o;
+        if (d == 0) {
+            pml[slot * 2] = m[g];
+            pml[slot * 2 + 1] = l[g];
+        }
+    }
+}
+
+// out[h] = sum_i o_i e^(m_i - M) / sum_i l_i e^(m_i - M) over the splits that hold keys
+__global__ __launch_bounds__(128) void k_bn_attn_combine(const float* __restrict__ po, const float* __restrict__ pml,
+                                                         const int* __restrict__ dpos, int ns_stride, int hd,
+                                                         float* __restrict__ out, int cap) {
+    const int h = blockIdx.x, d = threadIdx.x;
+    const int ns = (min(*dpos + 1, cap) + BN_ATTN_CHUNK - 1) / BN_ATTN_CHUNK;
+    const float* ml = pml + (size_t)h * ns_stride * 2;
+    float M = -INFINITY;
+    for (int i = 0; i < ns; i++) M = fmaxf(M, ml[2 * i]);
+    float L = 0.0f, o = 0.0f;
+    for (int i = 0; i < ns; i++) {
+        const float e = expf(ml[2 * i] - M);
+        L += ml[2 * i + 1] * e;
+        if (d < hd) o = fmaf(po[((size_t)h * ns_stride + i) * hd + d], e, o);
+    }
+    if (d < hd) out[(size_t)h * hd + d] = o / L;
+}
+
+// ---- logits = raw * (1 / scale), argmax (ops::argmax: larger wins, the lower index on ties,
+// only values above -inf) in two stages; the second writes hist[P + 1] and advances P.
+__device__ __forceinline__ void n2_take(float& v, int& i, float v2, int i2) {
+    if (v2 > v || (v2 == v && v2 > -INFINITY && i2 < i)) {
+        v = v2;
+        i = i2;
+    }
+}
+
+__global__ __launch_bounds__(256) void k_bn_logits(const float* __restrict__ raw, const float* __restrict__ scale, int N,
+                                                   float* __restrict__ logits, float* __restrict__ pv, int* __restrict__ pi) {
+    __shared__ float sv[256];
+    __shared__ int si[256];
+    const float inv = 1.0f / *scale;
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < N; i += gridDim.x * 256) {
+        const float v = raw[i] * inv;
+        logits[i] = v;
+        n2_take(bv, bi, v, i);
+    }
+    sv[threadIdx.x] = bv;
+    si[threadIdx.x] = bi;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+        if ((int)threadIdx.x < s) {
+            float v = sv[threadIdx.x];
+            int i = si[threadIdx.x];
+            n2_take(v, i, sv[threadIdx.x + s], si[threadIdx.x + s]);
+            sv[threadIdx.x] = v;
+            si[threadIdx.x] = i;
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        pv[blockIdx.x] = sv[0];
+        pi[blockIdx.x] = si[0];
+    }
+}
+
+__global__ __launch_bounds__(BN_AMAX_PARTS) void k_bn_argmax(const float* __restrict__ pv, const int* __restrict__ pi, int parts,
+                                                            uint32_t* __restrict__ hist, int* __restrict__ dpos, int cap) {
+    __shared__ float sv[BN_AMAX_PARTS];
+    __shared__ int si[BN_AMAX_PARTS];
+    const int t = threadIdx.x;
+    sv[t] = t < parts ? pv[t] : -INFINITY;
+    si[t] = t < parts ? pi[t] : 0x7fffffff;
+    __syncthreads();
+    for (int s = BN_AMAX_PARTS / 2; s > 0; s >>= 1) {
+        if (t < s) {
+            float v = sv[t];
+            int i = si[t];
+            n2_take(v, i, sv[t + s], si[t + s]);
+            sv[t] = v;
+            si[t] = i;
+        }
+        __syncthreads();
+    }
+    if (t == 0) {
+        const int P = *dpos;
+        if (P + 1 <= cap) hist[P + 1] = (uint32_t)(sv[0] > -INFINITY ? si[0] : 0);
+        *dpos = P + 1;
+    }
+}
+
+__global__ void k_bn_advance(int* __restrict__ dpos) { *dpos = *dpos + 1; }
+__global__ void k_bn_set_pos(int* __restrict__ dpos, int pos) { *dpos = pos; }
+
+__global__ void k_bn_copy_u32(const uint32_t* __restrict__ s, uint32_t* __restrict__ d, long n) {
+    const long stride = (long)gridDim.x * blockDim.x;
+    for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) d[i] = s[i];
+}
+
+struct TLin {
+    uint8_t* codes = nullptr;
+    float* scales = nullptr;
+    int N = 0, K = 0;
+};
+struct BLayer {
+    TLin q, k, v, o, gate, up, down;
+    float *in_norm = nullptr, *post_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
+    float *kc = nullptr, *vc = nullptr;
+};
+
+}  // namespace
+
+struct ti_bonsai {
+    ti_bonsai_config cfg;
+    std::vector<BLayer> L;
+    uint16_t* embed = nullptr;
+    float* final_norm = nullptr;
+    TLin lm;
+    float *x, *xn, *qraw, *kraw, *vraw, *qr, *attn, *oraw, *graw, *uraw, *swi, *draw, *lraw, *logits;
+    int8_t* act;
+    int32_t* xsum;
+    float* scales;        // [4]: a (input norm), b (attention), c (post norm), d (swi)
+    float *po, *pml;      // attention split partials
+    float* amax_v;
+    int* amax_i;
+    uint32_t* hist;
+    int* dpos;
+    float* rope;          // [max_ctx][head_dim]: cos then sin of each position (ops.rs rope_table)
+    uint32_t* trace = nullptr;
+    std::vector<void*> allocs;
+};
+
+// ---- the parity trace (ti_bonsai_trace) -----------------------------------------------------
+namespace {
+enum BField { B_X_IN, B_XN, B_A_ACT, B_A_SCALE, B_Q, B_K, B_V, B_ATTN, B_B_ACT, B_B_SCALE, B_X_MID, B_XN2, B_C_ACT,
+              B_C_SCALE, B_G, B_U, B_SWI, B_D_ACT, B_D_SCALE, B_D, B_NFIELDS };
+size_t bfield_words(const ti_bonsai_config& C, int f) {
+    const size_t H = C.hidden, I = C.intermediate, nq = (size_t)C.n_heads * C.head_dim, nkv = (size_t)C.n_kv_heads * C.head_dim;
+    switch (f) {
+        case B_X_IN: case B_XN: case B_X_MID: case B_XN2: case B_D: return H;
+        case B_A_ACT: case B_C_ACT: return H / 4;
+        case B_Q: case B_ATTN: return nq;
+        case B_B_ACT: return nq / 4;
+        case B_K: case B_V: return nkv;
+        case B_G: case B_U: case B_SWI: return I;
+        case B_D_ACT: return I / 4;
+        default: return 1;    // the scales
+    }
+}
+size_t blayer_words(const ti_bonsai_config& C) {
+    size_t w = 0;
+    for (int f = 0; f < B_NFIELDS; f++) w += bfield_words(C, f);
+    return w;
+}
+}  // namespace
+
+static uint32_t* bslot(ti_bonsai* m, int layer, int f) {
+    size_t off = (size_t)layer * blayer_words(m->cfg);
+    for (int g = 0; g < f; g++) off += bfield_words(m->cfg, g);
+    return m->trace + off;
+}
+
+static int bput(ti_ctx* c, ti_bonsai* m, int layer, int f, const void* src) {
+    if (!m->trace) return TI_OK;
+    const long n = (long)bfield_words(m->cfg, f);
+    k_bn_copy_u32<<<(unsigned)((n + 255) / 256 < 256 ? (n + 255) / 256 : 256), 256, 0, c->stream>>>(
+        static_cast<const uint32_t*>(src), bslot(m, layer, f), n);
+    TI_LAUNCHED("k_bn_copy_u32 (trace)");
+    return TI_OK;
+}
+
+static int bmk(ti_bonsai* m, void** p, size_t bytes) {
+    hipError_t e = hipMalloc(p, bytes ? bytes : 4);
+    if (e != hipSuccess) return ti_hip_fail(e, "ti_bonsai_create hipMalloc");
+    m->allocs.push_back(*p);
+    return TI_OK;
+}
+
+static void brelease(ti_bonsai* m) {
+    for (void* p : m->allocs) (void)hipFree(p);
+    delete m;
+}
+
+extern "C" int ti_bonsai_create(ti_ctx* c, const ti_bonsai_config* cfg, ti_bonsai** out) {
+    TI_CHECK_CTX(c);
+    TI_REQUIRE(cfg && out, "ti_bonsai_create: null argument");
+    *out = nullptr;
+    const ti_bonsai_config& C = *cfg;
+    TI_REQUIRE(C.layers > 0 && C.hidden > 0 && C.intermediate > 0 && C.n_heads > 0 && C.n_kv_heads > 0 && C.vocab > 0 &&
+               C.max_ctx > 0 && C.n_heads % C.n_kv_heads == 0, "ti_bonsai_create: bad config");
+    TI_REQUIRE(C.hidden % 1024 == 0 && C.hidden <= 8192 && C.intermediate % 1024 == 0 && C.intermediate <= 8192,
+               "ti_bonsai_create: hidden and intermediate must be multiples of 1024, at most 8192");
+    TI_REQUIRE(C.head_dim == 128 && C.n_heads / C.n_kv_heads == 2 && (C.n_heads * C.head_dim) % 1024 == 0 &&
+               C.n_heads * C.head_dim <= 8192, "ti_bonsai_create: the decoder covers head_dim 128 with 2 query heads per KV head");
+    TI_REQUIRE(!c->capturing, "ti_bonsai_create: not during graph capture");
+    TI_HIP(hipSetDevice(c->device));
+    ti_bonsai* m = new ti_bonsai();
+    m->cfg = C;
+    const int H = C.hidden, I = C.intermediate, hd = C.head_dim;
+    const int nq = C.n_heads * hd, nkv = C.n_kv_heads * hd;
+    int rc = 0;
+    auto lin = [&](TLin& l, int N, int K) {
+        l.N = N;
+        l.K = K;
+        int r = bmk(m, (void**)&l.codes, (size_t)N * K / 4);
+        if (!r) r = bmk(m, (void**)&l.scales, (size_t)N * (K / 64) * 4);
+        return r;
+    };
+    m->L.resize(C.layers);
+    const size_t kvf = (size_t)C.max_ctx * nkv * 4;
+    for (int l = 0; l < C.layers && !rc; l++) {
+        BLayer& y = m->L[l];
+        rc = lin(y.q, nq, H); if (!rc) rc = lin(y.k, nkv, H); if (!rc) rc = lin(y.v, nkv, H);
+        if (!rc) rc = lin(y.o, H, nq); if (!rc) rc = lin(y.gate, I, H); if (!rc) rc = lin(y.up, I, H);
+        if (!rc) rc = lin(y.down, H, I);
+        if (!rc) rc = bmk(m, (void**)&y.in_norm, H * 4);
+        if (!rc) rc = bmk(m, (void**)&y.post_norm, H * 4);
+        if (!rc) rc = bmk(m, (void**)&y.q_norm, hd * 4);
+        if (!rc) rc = bmk(m, (void**)&y.k_norm, hd * 4);
+        if (!rc) rc = bmk(m, (void**)&y.kc, kvf);
+        if (!rc) rc = bmk(m, (void**)&y.vc, kvf);
+    }
+    if (!rc) rc = bmk(m, (void**)&m->embed, (size_t)C.vocab * H * 2);
+    if (!rc) rc = bmk(m, (void**)&m->final_norm, H * 4);
+    if (!rc) rc = lin(m->lm, C.vocab, H);
+    const int widest = I > H ? (I > nq ? I : nq) : (H > nq ? H : nq);
+    const int nsplit = (C.max_ctx + BN_ATTN_CHUNK - 1) / BN_ATTN_CHUNK;
+    struct { float** p; size_t n; } fb[] = {{&m->x, (size_t)H}, {&m->xn, (size_t)H}, {&m->qraw, (size_t)nq},
+                                            {&m->kraw, (size_t)nkv}, {&m->vraw, (size_t)nkv}, {&m->qr, (size_t)nq},
+                                            {&m->attn, (size_t)nq}, {&m->oraw, (size_t)H}, {&m->graw, (size_t)I},
+                                            {&m->uraw, (size_t)I}, {&m->swi, (size_t)I}, {&m->draw, (size_t)H},
+                                            {&m->lraw, (size_t)C.vocab}, {&m->logits, (size_t)C.vocab}, {&m->scales, 4},
+                                            {&m->po, (size_t)C.n_heads * nsplit * hd}, {&m->pml, (size_t)C.n_heads * nsplit * 2},
+                                            {&m->amax_v, BN_AMAX_PARTS}};
+    for (auto& f : fb) if (!rc) rc = bmk(m, (void**)f.p, f.n * 4);
+    if (!rc) rc = bmk(m, (void**)&m->act, (size_t)widest);
+    if (!rc) rc = bmk(m, (void**)&m->xsum, (size_t)widest / 64 * 4);
+    if (!rc) rc = bmk(m, (void**)&m->amax_i, BN_AMAX_PARTS * 4);
+    if (!rc) rc = bmk(m, (void**)&m->hist, (size_t)(C.max_ctx + 1) * 4);
+    if (!rc) rc = bmk(m, (void**)&m->dpos, 4);
+    if (!rc) rc = bmk(m, (void**)&m->rope, (size_t)C.max_ctx * hd * 4);
+    if (!rc) {
+        // ops.rs:79-90 in f32 with the platform's powf / cosf / sinf, the functions Rust's
+        // f32::powf and sin_cos call on Linux
+        std::vector<float> tab((size_t)C.max_ctx * hd);
+        const int half = hd / 2;
+        for (int p = 0; p < C.max_ctx; p++)
+            for (int i = 0; i < half; i++) {
+                const float e = -((float)(2 * i)) / (float)hd;
+                const float ang = (float)p * powf(C.rope_theta, e);
+                tab[(size_t)p * hd + i] = cosf(ang);
+                tab[(size_t)p * hd + half + i] = sinf(ang);
+            }
+        hipError_t e = hipMemcpy(m->rope, tab.data(), tab.size() * 4, hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = hipMemset(m->hist, 0, (size_t)(C.max_ctx + 1) * 4);
+        if (e == hipSuccess) e = hipMemset(m->dpos, 0, 4);
+        if (e == hipSuccess) e = hipDeviceSynchronize();
+        if (e != hipSuccess) rc = ti_hip_fail(e, "ti_bonsai_create set-up");
+    }
+    if (rc) { brelease(m); return rc; }
+    *out = m;
+    return TI_OK;
+}
+
+extern "C" int ti_bonsai_destroy(ti_ctx* c, ti_bonsai* m) {
+    TI_CHECK_CTX(c);
+    if (!m) return TI_OK;
+    TI_REQUIRE(!c->capturing, "ti_bonsai_destroy: not during graph capture");
+    TI_HIP(hipStreamSynchronize(c->stream));
+    brelease(m);
+    return TI_OK;
+}
+
+// Tensor names and kinds are the container's (native/tools/pack_bin.py; model.rs:275-304):
+// ternary projections and lm_head return codes + scales, norms f32, the embedding f16.
+extern "C" int ti_bonsai_tensor(ti_bonsai* m, const char* name, void** data, size_t* data_bytes, void** scales,
+                                size_t* scale_bytes) {
+    TI_REQUIRE(m && name && data && data_bytes, "ti_bonsai_tensor: null argument");
+    const ti_bonsai_config& C = m->cfg;
+    *data = nullptr;
+    *data_bytes = 0;
+    if (scales) *scales = nullptr;
+    if (scale_bytes) *scale_bytes = 0;
+    auto vec = [&](void* p, size_t bytes) { *data = p; *data_bytes = bytes; return TI_OK; };
+    auto lin = [&](TLin& l) {
+        *data = l.codes;
+        *data_bytes = (size_t)l.N * l.K / 4;
+        if (scales) *scales = l.scales;
+        if (scale_bytes) *scale_bytes = (size_t)l.N * (l.K / 64) * 4;
+        return TI_OK;
+    };
+    std::string s(name);
+    if (s == "model.embed_tokens.weight") return vec(m->embed, (size_t)C.vocab * C.hidden * 2);
+    if (s == "model.norm.weight") return vec(m->final_norm, (size_t)C.hidden * 4);
+    if (s == "lm_head.weight") return lin(m->lm);
+    int l = -1;
+    char rest[128] = {0};
+    if (sscanf(name, "model.layers.%d.%127s", &l, rest) == 2 && l >= 0 && l < C.layers) {
+        BLayer& y = m->L[l];
+        std::string r(rest);
+        if (r == "input_layernorm.weight") return vec(y.in_norm, (size_t)C.hidden * 4);
+        if (r == "post_attention_layernorm.weight") return vec(y.post_norm, (size_t)C.hidden * 4);
+        if (r == "self_attn.q_norm.weight") return vec(y.q_norm, (size_t)C.head_dim * 4);
+        if (r == "self_attn.k_norm.weight") return vec(y.k_norm, (size_t)C.head_dim * 4);
+        if (r == "self_attn.q_proj.weight") return lin(y.q);
+        if (r == "self_attn.k_proj.weight") return lin(y.k);
+        if (r == "self_attn.v_proj.weight") return lin(y.v);
+        if (r == "self_attn.o_proj.weight") return lin(y.o);
+        if (r == "mlp.gate_proj.weight") return lin(y.gate);
+        if (r == "mlp.up_proj.weight") return lin(y.up);
+        if (r == "mlp.down_proj.weight") return lin(y.down);
+    }
+    return ti_fail(TI_ERR_INVALID, "ti_bonsai_tensor: unknown tensor '%s'", name);
+}
+
+// Model::load + check_shapes (model.rs:256-322): every tensor the forward needs, of the
+// kind and shape the config implies, uploaded from the container.
+extern "C" int ti_bonsai_load(ti_ctx* c, ti_bonsai* m, const ti_cpubin* bin) {
+    TI_CHECK_CTX(c);
+    TI_REQUIRE(m && bin, "ti_bonsai_load: null argument");
+    TI_REQUIRE(!c->capturing, "ti_bonsai_load: not during graph capture");
+    const ti_bonsai_config& C = m->cfg;
+    std::vector<std::string> names = {"model.embed_tokens.weight", "model.norm.weight", "lm_head.weight"};
+    const char* per[] = {"input_layernorm.weight", "post_attention_layernorm.weight", "self_attn.q_norm.weight",
+                         "self_attn.k_norm.weight", "self_attn.q_proj.weight", "self_attn.k_proj.weight",
+                         "self_attn.v_proj.weight", "self_attn.o_proj.weight", "mlp.gate_proj.weight", "mlp.up_proj.weight",
+                         "mlp.down_proj.weight"};
+    for (int l = 0; l < C.layers; l++)
+        for (const char* p : per) names.push_back("model.layers." + std::to_string(l) + "." + p);
+    for (auto& n : names) {
+        ti_cpubin_tensor_info t;
+        if (ti_cpubin_tensor(bin, n.c_str(), &t)) return ti_fail(TI_ERR_INVALID, "missing tensor `%s`", n.c_str());
+        void *d = nullptr, *s = nullptr;
+        size_t db = 0, sb = 0;
+        int rc = ti_bonsai_tensor(m, n.c_str(), &d, &db, &s, &sb);
+        if (rc) return rc;
+        const int want = s ? TI_CPUBIN_TERN : (n == "model.embed_tokens.weight" ? TI_CPUBIN_EMBED_F16 : TI_CPUBIN_F32);
+        const char* wk = want == TI_CPUBIN_TERN ? "tern" : want == TI_CPUBIN_F32 ? "f32" : "embed_f16";
+        if (t.kind != want) return ti_fail(TI_ERR_INVALID, "%s: expected `%s`", n.c_str(), wk);
+        if (want == TI_CPUBIN_TERN && ((size_t)t.N * t.K / 4 != db || t.scale_bytes != sb))
+            return ti_fail(TI_ERR_INVALID, "%s: container says [%lld, %lld], config implies %zu codes bytes", n.c_str(), t.N,
+                           t.K, db);
+        if (t.data_bytes != db)
+            return ti_fail(TI_ERR_INVALID, "%s: container holds %zu bytes, the config implies %zu", n.c_str(), t.data_bytes, db);
+        TI_HIP(hipMemcpyAsync(d, t.data, db, hipMemcpyHostToDevice, c->stream));
+        if (s) TI_HIP(hipMemcpyAsync(s, t.scales, sb, hipMemcpyHostToDevice, c->stream));
+    }
+    TI_HIP(hipStreamSynchronize(c->stream));
+    return TI_OK;
+}
+
+extern "C" int ti_bonsai_kv(ti_bonsai* m, int layer, float** kc, float** vc) {
+    TI_REQUIRE(m && kc && vc && layer >= 0 && layer < m->cfg.layers, "ti_bonsai_kv: bad argument");
+    *kc = m->L[layer].kc;
+    *vc = m->L[layer].vc;
+    return TI_OK;
+}
+
+extern "C" int ti_bonsai_logits(ti_bonsai* m, float** logits) {
+    TI_REQUIRE(m && logits, "ti_bonsai_logits: null argument");
+    *logits = m->logits;
+    return TI_OK;
+}
+
+extern "C" int ti_bonsai_set_pos(ti_ctx* c, ti_bonsai* m, int pos) {
+    TI_CHECK_CTX(c);
+    TI_REQUIRE(m && pos >= 0 && pos < m->cfg.max_ctx, "ti_bonsai_set_pos: pos %d out of [0, %d)", pos, m ? m->cfg.max_ctx : 0);
+    k_bn_set_pos<<<1, 1, 0, c->stream>>>(m->dpos, pos);
+    TI_LAUNCHED("k_bn_set_pos");
+    return TI_OK;
+}
+
+extern "C" int ti_bonsai_write_tokens(ti_ctx* c, ti_bonsai* m, int from, int count, const int32_t* ids) {
+    TI_CHECK_CTX(c);
+    TI_REQUIRE(m && ids && from >= 0 && count >= 0 && from + count <= m->cfg.max_ctx + 1, "ti_bonsai_write_tokens: bad range");
+    return ti_buf_write(c, m->hist, (size_t)from * 4, ids, (size_t)count * 4);
+}
+
+extern "C" int ti_bonsai_read_tokens(ti_ctx* c, ti_bonsai* m, int from, int count, int32_t* ids) {
+    TI_CHECK_CTX(c);
+    TI_REQUIRE(m && ids && from >= 0 && count >= 0 && from + count <= m->cfg.max_ctx + 1, "ti_bonsai_read_tokens: bad range");
+    return ti_buf_read(c, m->hist, (size_t)from * 4, ids, (size_t)count * 4);
+}
+
+extern "C" int ti_bonsai_trace(ti_bonsai* m, void* buf, size_t bytes) {
+    TI_REQUIRE(m, "ti_bonsai_trace: null model");
+    if (!buf) { m->trace = nullptr; return TI_OK; }
+    const size_t need = (blayer_words(m->cfg) * m->cfg.layers + 2 * (size_t)m->cfg.hidden + m->cfg.hidden / 4 + 1) * 4;
+    TI_REQUIRE(bytes >= need, "ti_bonsai_trace: the trace needs %zu bytes (got %zu)", need, bytes);
+    TI_REQUIRE(((uintptr_t)buf & 15) == 0, "ti_bonsai_trace: buffer must be 16-byte aligned");
+    m->trace = static_cast<uint32_t*>(buf);
+    return TI_OK;
+}
+
+static int bn_norm_quant(ti_ctx* c, float* x, const float* add, const float* add_scale, const float* w, float eps, int H,
+                         float* xn, int8_t* act, int32_t* xsum, float* scale) {
+    const int ept = (H + BN_THREADS - 1) / BN_THREADS;
+#define NQ(E) if (ept <= E) { k_bn_norm_quant<E><<<1, BN_THREADS, 0, c->stream>>>(x, add, add_scale, w, eps, H, xn, act, xsum, scale); }
+    NQ(2) else NQ(4) else NQ(8) else return ti_fail(TI_ERR_INVALID, "bonsai: hidden %d too wide", H);
+#undef NQ
+    TI_LAUNCHED("k_bn_norm_quant");
+    return TI_OK;
+}
+
+// One token at the device position P (model.rs:349-501): with logits, the argmax goes to
+// hist[P + 1]; P advances either way.
+static int bonsai_step(ti_ctx* c, ti_bonsai* m, bool want_logits) {
+    const ti_bonsai_config& C = m->cfg;
+    const int H = C.hidden, I = C.intermediate, hd = C.head_dim, nHq = C.n_heads, nKv = C.n_kv_heads;
+    const int nq = nHq * hd, nkv = nKv * hd;
+    const int nsplit = (C.max_ctx + BN_ATTN_CHUNK - 1) / BN_ATTN_CHUNK;
+    float* sa = m->scales;
+    float* sb = m->scales + 1;
+    float* scl = m->scales + 2;
+    float* sd = m->scales + 3;
+    int rc;
+#define RC(x) do { rc = (x); if (rc) return rc; } while (0)
+    k_bn_embed<<<1, 256, 0, c->stream>>>(m->hist, m->dpos, m->embed, m->x, H, C.vocab, C.max_ctx);
+    TI_LAUNCHED("k_bn_embed");
+    for (int l = 0; l < C.layers; l++) {
+        BLayer& y = m->L[l];
+        const bool first = l == 0;
+        // the previous layer's down projection is added in this norm's prologue
+        if (m->trace && !first) RC(bput(c, m, l - 1, B_D, m->draw));
+        RC(bn_norm_quant(c, m->x, first ? nullptr : m->draw, sd, y.in_norm, C.rms_eps, H, m->xn, m->act, m->xsum, sa));
+        if (m->trace) {
+            // x_in of this layer: x before the add is the previous x_out; trace the sum
+            RC(bput(c, m, l, B_X_IN, m->x));
+            RC(bput(c, m, l, B_XN, m->xn));
+            RC(bput(c, m, l, B_A_ACT, m->act));
+            RC(bput(c, m, l, B_A_SCALE, sa));
+        }
+        const uint8_t* cq[3] = {y.q.codes, y.k.codes, y.v.codes};
+        const float* sq[3] = {y.q.scales, y.k.scales, y.v.scales};
+        float* oq[3] = {m->qraw, m->kraw, m->vraw};
+        const int nqkv[3] = {nq, nkv, nkv};
+        RC(ti_tern_gemv_multi(c, m->act, m->xsum, H, 3, cq, sq, oq, nqkv));
+        if (m->trace) {
+            RC(bput(c, m, l, B_Q, m->qraw));
+            RC(bput(c, m, l, B_K, m->kraw));
+            RC(bput(c, m, l, B_V, m->vraw));
+        }
+        k_bn_prep<<<nHq + nKv, 128, 0, c->stream>>>(m->qraw, m->kraw, m->vraw, sa, y.q_norm, y.k_norm, m->rope, m->dpos, m->qr,
+                                                    y.kc, y.vc, nHq, nKv, hd, C.rms_eps, C.max_ctx);
+        TI_LAUNCHED("k_bn_prep");
+        k_bn_attn<2, 128><<<nKv * nsplit, 256, 0, c->stream>>>(m->qr, y.kc, y.vc, m->dpos, nKv, m->po, m->pml, nsplit,
+                                                               C.max_ctx);
+        TI_LAUNCHED("k_bn_attn");
+        k_bn_attn_combine<<<nHq, 128, 0, c->stream>>>(m->po, m->pml, m->dpos, nsplit, hd, m->attn, C.max_ctx);
+        TI_LAUNCHED("k_bn_attn_combine");
+        const int eq = (nq + BN_THREADS - 1) / BN_THREADS;
+#define QT(E) if (eq <= E) { k_bn_quant<E><<<1, BN_THREADS, 0, c->stream>>>(m->attn, nq, m->act, m->xsum, sb); }
+        QT(2) else QT(4) else QT(8) else return ti_fail(TI_ERR_INVALID, "bonsai: q width %d", nq);
+#undef QT
+        TI_LAUNCHED("k_bn_quant");
+        if (m->trace) {
+            RC(bput(c, m, l, B_ATTN, m->attn));
+            RC(bput(c, m, l, B_B_ACT, m->act));
+            RC(bput(c, m, l, B_B_SCALE, sb));
+        }
+        RC(ti_tern_gemv(c, m->oraw, y.o.codes, y.o.scales, m->act, m->xsum, H, nq));
+        RC(bn_norm_quant(c, m->x, m->oraw, sb, y.post_norm, C.rms_eps, H, m->xn, m->act, m->xsum, scl));
+        if (m->trace) {
+            RC(bput(c, m, l, B_X_MID, m->x));
+            RC(bput(c, m, l, B_XN2, m->xn));
+            RC(bput(c, m, l, B_C_ACT, m->act));
+            RC(bput(c, m, l, B_C_SCALE, scl));
+        }
+        const uint8_t* cg[2] = {y.gate.codes, y.up.codes};
+        const float* sg[2] = {y.gate.scales, y.up.scales};
+        float* og[2] = {m->graw, m->uraw};
+        const int ngu[2] = {I, I};
+        RC(ti_tern_gemv_multi(c, m->act, m->xsum, H, 2, cg, sg, og, ngu));
+        const int ei = (I + BN_THREADS - 1) / BN_THREADS;
+#define SQ(E) if (ei <= E) { k_bn_swiglu_quant<E><<<1, BN_THREADS, 0, c->stream>>>(m->graw, m->uraw, scl, I, m->swi, m->act, m->xsum, sd); }
+        SQ(2) else SQ(4) else SQ(8) else return ti_fail(TI_ERR_INVALID, "bonsai: intermediate %d", I);
+#undef SQ
+        TI_LAUNCHED("k_bn_swiglu_quant");
+        if (m->trace) {
+            RC(bput(c, m, l, B_G, m->graw));
+            RC(bput(c, m, l, B_U, m->uraw));
+            RC(bput(c, m, l, B_SWI, m->swi));
+            RC(bput(c, m, l, B_D_ACT, m->act));
+            RC(bput(c, m, l, B_D_SCALE, sd));
+        }
+        RC(ti_tern_gemv(c, m->draw, y.down.codes, y.down.scales, m->act, m->xsum, H, I));
+    }
+    if (m->trace) RC(bput(c, m, C.layers - 1, B_D, m->draw));
+    if (!want_logits) {
+        // a prompt token: its KV rows are written; the residual restarts at the next
+        // token's embedding, so nothing past the last layer is computed (model.rs:486-490)
+        k_bn_advance<<<1, 1, 0, c->stream>>>(m->dpos);
+        TI_LAUNCHED("k_bn_advance");
+        return TI_OK;
+    }
+    RC(bn_norm_quant(c, m->x, m->draw, sd, m->final_norm, C.rms_eps, H, m->xn, m->act, m->xsum, sa));
+    if (m->trace) {
+        uint32_t* fin = bslot(m, C.layers, 0);
+        // x_final, xn_final, its codes and scale after the last layer
+        k_bn_copy_u32<<<8, 256, 0, c->stream>>>(reinterpret_cast<const uint32_t*>(m->x), fin, H);
+        k_bn_copy_u32<<<8, 256, 0, c->stream>>>(reinterpret_cast<const uint32_t*>(m->xn), fin + H, H);
+        k_bn_copy_u32<<<8, 256, 0, c->stream>>>(reinterpret_cast<const uint32_t*>(m->act), fin + 2 * H, H / 4);
+        k_bn_copy_u32<<<1, 64, 0, c->stream>>>(reinterpret_cast<const uint32_t*>(sa), fin + 2 * H + H / 4, 1);
+        TI_LAUNCHED("k_bn_copy_u32 (trace)");
+    }
+    RC(ti_tern_gemv(c, m->lraw, m->lm.codes, m->lm.scales, m->act, m->xsum, C.vocab, H));
+    k_bn_logits<<<BN_AMAX_PARTS, 256, 0, c->stream>>>(m->lraw, sa, C.vocab, m->logits, m->amax_v, m->amax_i);
+    TI_LAUNCHED("k_bn_logits");
+    k_bn_argmax<<<1, BN_AMAX_PARTS, 0, c->stream>>>(m->amax_v, m->amax_i, BN_AMAX_PARTS, m->hist, m->dpos, C.max_ctx);
+    TI_LAUNCHED("k_bn_argmax");
+    return TI_OK;
+#undef RC
+}
+
+// Model::forward at the device position (model.rs:349-501), logits and greedy token:
+// graph-capturable (reads nothing from the host).
+extern "C" int ti_bonsai_decode(ti_ctx* c, ti_bonsai* m) {
+    TI_CHECK_CTX(c);
+    TI_REQUIRE(m, "ti_bonsai_decode: null model");
+    return bonsai_step(c, m, true);
+}
+
+// Prompt tokens ids[0..T) at positions pos.. (Model::forward per token, logits only for the
+// last, as n2-cli's prefill calls it): the argmax of the last token's logits goes to
+// hist[pos + T] and the device position becomes pos + T.
+extern "C" int ti_bonsai_forward(ti_ctx* c, ti_bonsai* m, const int32_t* ids, int T, int pos) {
+    TI_CHECK_CTX(c);
+    TI_REQUIRE(m, "ti_bonsai_forward: null model");
+    TI_REQUIRE(T > 0 && pos >= 0 && pos + T <= m->cfg.max_ctx, "ti_bonsai_forward: T=%d pos=%d outside max_ctx=%d", T, pos,
+               m->cfg.max_ctx);
+    int rc;
+    if (ids && (rc = ti_buf_write(c, m->hist, (size_t)pos * 4, ids, (size_t)T * 4))) return rc;
+    if ((rc = ti_bonsai_set_pos(c, m, pos))) return rc;
+    for (int t = 0; t < T; t++)
+        if ((rc = bonsai_step(c, m, t == T - 1))) return rc;
+    return TI_OK;
+}

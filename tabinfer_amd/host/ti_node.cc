@@ -31,7 +31,7 @@ namespace {
 
 // ---- handles -------------------------------------------------------------------------
 enum Tag : uint32_t { TAG_CTX = 0x74696378, TAG_BUF = 0x74696262, TAG_GRAPH = 0x74696767, TAG_MODEL = 0x7469716d,
-                     TAG_CPUBIN = 0x74696362 };
+                     TAG_CPUBIN = 0x74696362, TAG_BONSAI = 0x7469626e };
 
 // A context lives until its JS handle is finalized (or shutdown() is called) AND every
 // buffer, graph and model made on it is gone: they hold counted references, so a
@@ -70,12 +70,15 @@ struct BufH {
     bool owned = false;        // freed with ti_buf_free when collected
     napi_ref parent = nullptr; // the parent object (buffer or model), kept alive
     BufH* pbuf = nullptr;      // the parent's handle when it is a buffer
-    ModelH* pmodel = nullptr;  // ... when it is a model
+    ModelH* pmodel = nullptr;  // ... when it is a Qwen3 model
+    struct BonsaiH* pbonsai = nullptr;   // ... when it is a Bonsai model
 };
+
+bool bonsai_live(const struct BonsaiH* h);
 
 bool buf_live(const BufH* b) {
     for (; b; b = b->pbuf)
-        if (!b->ptr || (b->pmodel && !b->pmodel->m)) return false;
+        if (!b->ptr || (b->pmodel && !b->pmodel->m) || (b->pbonsai && !bonsai_live(b->pbonsai))) return false;
     return true;
 }
 
@@ -141,6 +144,15 @@ CtxH* get_ctx(napi_env env, napi_value v, const char* fn) {
     return h;
 }
 
+// A Bonsai ternary decoder (ti_bonsai_*); its views (tensors, KV, logits) keep it alive
+// and die with it, as the Qwen3 decoder's do.
+struct BonsaiH {
+    uint32_t tag = TAG_BONSAI;
+    CtxH* ctx = nullptr;
+    ti_bonsai* m = nullptr;
+    ti_bonsai_config cfg;
+};
+
 // A .cpu.bin container (host memory only; no context).
 struct CpuBinH {
     uint32_t tag = TAG_CPUBIN;
@@ -148,6 +160,16 @@ struct CpuBinH {
 };
 
 // ---- finalizers ---------------------------------------------------------------------------
+bool bonsai_live(const BonsaiH* h) { return h->m != nullptr; }
+
+void fin_bonsai(napi_env, void* data, void*) {
+    BonsaiH* h = static_cast<BonsaiH*>(data);
+    if (h->m && !h->ctx->closed) ti_bonsai_destroy(h->ctx->c, h->m);
+    ctx_unref(h->ctx);
+    h->tag = 0;
+    delete h;
+}
+
 void fin_cpubin(napi_env, void* data, void*) {
     CpuBinH* h = static_cast<CpuBinH*>(data);
     if (h->c) ti_cpubin_close(h->c);
@@ -195,6 +217,7 @@ napi_value make_buf(napi_env env, CtxH* ctx, void* ptr, size_t bytes, bool owned
         napi_create_reference(env, parent, 1, &b->parent);
         b->pbuf = handle_of<BufH>(env, parent, TAG_BUF);
         b->pmodel = handle_of<ModelH>(env, parent, TAG_MODEL);
+        b->pbonsai = handle_of<BonsaiH>(env, parent, TAG_BONSAI);
     }
     napi_value out;
     napi_create_external(env, b, fin_buf, nullptr, &out);
@@ -1012,6 +1035,199 @@ napi_value js_cpubin_embed_row(napi_env env, napi_callback_info info) {
     return f32;
 }
 
+// ---- the Bonsai decoder (ti_bonsai_*) ------------------------------------------------------------
+BonsaiH* get_bonsai(napi_env env, napi_value v, const char* fn, size_t i) {
+    BonsaiH* h = handle_of<BonsaiH>(env, v, TAG_BONSAI);
+    if (!h || !h->m) { arg_error(env, fn, i, "a live model from bonsai_create()"); return nullptr; }
+    if (h->ctx->closed) { throw_msg(env, std::string(fn) + ": the model's context was shut down"); return nullptr; }
+    return h;
+}
+
+// bonsai_create(ctx, {layers, hidden, intermediate, n_heads, n_kv_heads, head_dim, vocab,
+// rope_theta, rms_eps, max_ctx}) -> model
+napi_value js_bonsai_create(napi_env env, napi_callback_info info) {
+    Args a(env, info);
+    if (!want_args(env, a, 2, "bonsai_create")) return nullptr;
+    CtxH* c = get_ctx(env, a.v[0], "bonsai_create");
+    if (!c) return nullptr;
+    ti_bonsai_config cfg;
+    std::memset(&cfg, 0, sizeof cfg);
+    napi_value o = a.v[1];
+    if (!cfg_int(env, o, "layers", &cfg.layers, true, 0) || !cfg_int(env, o, "hidden", &cfg.hidden, true, 0) ||
+        !cfg_int(env, o, "intermediate", &cfg.intermediate, true, 0) || !cfg_int(env, o, "n_heads", &cfg.n_heads, true, 0) ||
+        !cfg_int(env, o, "n_kv_heads", &cfg.n_kv_heads, true, 0) || !cfg_int(env, o, "head_dim", &cfg.head_dim, true, 0) ||
+        !cfg_int(env, o, "vocab", &cfg.vocab, true, 0) || !cfg_float(env, o, "rope_theta", &cfg.rope_theta, 1000000.0f) ||
+        !cfg_float(env, o, "rms_eps", &cfg.rms_eps, 1e-6f) || !cfg_int(env, o, "max_ctx", &cfg.max_ctx, false, 4096))
+        return nullptr;
+    ti_bonsai* m = nullptr;
+    const int rc = ti_bonsai_create(c->c, &cfg, &m);
+    if (rc) return throw_ti(env, "bonsai_create", rc);
+    BonsaiH* h = new BonsaiH;
+    h->ctx = c;
+    c->refs++;
+    h->m = m;
+    h->cfg = cfg;
+    napi_value out;
+    napi_create_external(env, h, fin_bonsai, nullptr, &out);
+    return out;
+}
+
+napi_value js_bonsai_destroy(napi_env env, napi_callback_info info) {
+    Args a(env, info);
+    BonsaiH* h = a.n == 1 ? get_bonsai(env, a.v[0], "bonsai_destroy", 0) : nullptr;
+    if (!h) return a.n == 1 ? nullptr : throw_msg(env, "bonsai_destroy expects (model)");
+    const int rc = ti_bonsai_destroy(h->ctx->c, h->m);
+    h->m = nullptr;
+    return rc ? throw_ti(env, "bonsai_destroy", rc) : undefined(env);
+}
+
+// bonsai_load(ctx, model, container)
+napi_value js_bonsai_load(napi_env env, napi_callback_info info) {
+    Args a(env, info);
+    if (!want_args(env, a, 3, "bonsai_load")) return nullptr;
+    CtxH* c = get_ctx(env, a.v[0], "bonsai_load");
+    BonsaiH* h = c ? get_bonsai(env, a.v[1], "bonsai_load", 1) : nullptr;
+    CpuBinH* b = handle_of<CpuBinH>(env, a.v[2], TAG_CPUBIN);
+    if (!h) return nullptr;
+    if (!b || !b->c) return arg_error(env, "bonsai_load", 2, "an open container from cpubin_open()"), nullptr;
+    const int rc = ti_bonsai_load(c->c, h->m, b->c);
+    return rc ? throw_ti(env, "bonsai_load", rc) : undefined(env);
+}
+
+// bonsai_tensor(model, name) -> {data, dataBytes, scales|null, scaleBytes}
+napi_value js_bonsai_tensor(napi_env env, napi_callback_info info) {
+    Args a(env, info);
+    if (!want_args(env, a, 2, "bonsai_tensor")) return nullptr;
+    BonsaiH* h = get_bonsai(env, a.v[0], "bonsai_tensor", 0);
+    if (!h) return nullptr;
+    char name[256];
+    size_t nl;
+    if (napi_get_value_string_utf8(env, a.v[1], name, sizeof name, &nl) != napi_ok) return arg_error(env, "bonsai_tensor", 1, "a string"), nullptr;
+    void *d = nullptr, *s = nullptr;
+    size_t db = 0, sb = 0;
+    const int rc = ti_bonsai_tensor(h->m, name, &d, &db, &s, &sb);
+    if (rc) return throw_ti(env, "bonsai_tensor", rc);
+    napi_value o, nul;
+    napi_create_object(env, &o);
+    napi_get_null(env, &nul);
+    napi_set_named_property(env, o, "data", make_buf(env, h->ctx, d, db, false, a.v[0]));
+    napi_set_named_property(env, o, "dataBytes", num(env, (double)db));
+    napi_set_named_property(env, o, "scales", s ? make_buf(env, h->ctx, s, sb, false, a.v[0]) : nul);
+    napi_set_named_property(env, o, "scaleBytes", num(env, (double)sb));
+    return o;
+}
+
+// bonsai_kv(model, layer) -> {kc, vc}
+napi_value js_bonsai_kv(napi_env env, napi_callback_info info) {
+    Args a(env, info);
+    if (!want_args(env, a, 2, "bonsai_kv")) return nullptr;
+    BonsaiH* h = get_bonsai(env, a.v[0], "bonsai_kv", 0);
+    int64_t layer;
+    if (!h || !get_i64(env, a.v[1], &layer, "bonsai_kv", 1)) return nullptr;
+    float *kc, *vc;
+    const int rc = ti_bonsai_kv(h->m, (int)layer, &kc, &vc);
+    if (rc) return throw_ti(env, "bonsai_kv", rc);
+    const size_t bytes = (size_t)h->cfg.max_ctx * h->cfg.n_kv_heads * h->cfg.head_dim * 4;
+    napi_value o;
+    napi_create_object(env, &o);
+    napi_set_named_property(env, o, "kc", make_buf(env, h->ctx, kc, bytes, false, a.v[0]));
+    napi_set_named_property(env, o, "vc", make_buf(env, h->ctx, vc, bytes, false, a.v[0]));
+    return o;
+}
+
+napi_value js_bonsai_logits(napi_env env, napi_callback_info info) {
+    Args a(env, info);
+    BonsaiH* h = a.n == 1 ? get_bonsai(env, a.v[0], "bonsai_logits", 0) : nullptr;
+    if (!h) return a.n == 1 ? nullptr : throw_msg(env, "bonsai_logits expects (model)");
+    float* l = nullptr;
+    const int rc = ti_bonsai_logits(h->m, &l);
+    return rc ? throw_ti(env, "bonsai_logits", rc) : make_buf(env, h->ctx, l, (size_t)h->cfg.vocab * 4, false, a.v[0]);
+}
+
+// bonsai_forward(ctx, model, ids: Int32Array | null, T, pos)
+napi_value js_bonsai_forward(napi_env env, napi_callback_info info) {
+    const char* fn = "bonsai_forward";
+    Args a(env, info);
+    if (!want_args(env, a, 5, fn)) return nullptr;
+    CtxH* c = get_ctx(env, a.v[0], fn);
+    BonsaiH* h = c ? get_bonsai(env, a.v[1], fn, 1) : nullptr;
+    int64_t T, pos;
+    if (!h || !get_i64(env, a.v[3], &T, fn, 3) || !get_i64(env, a.v[4], &pos, fn, 4)) return nullptr;
+    const int32_t* ids = nullptr;
+    if (!is_nullish(env, a.v[2])) {
+        size_t n;
+        if (!host_i32(env, a.v[2], &ids, &n, fn, 2)) return nullptr;
+        if ((int64_t)n < T) return throw_msg(env, "bonsai_forward: ids holds fewer than T tokens");
+    }
+    const int rc = ti_bonsai_forward(c->c, h->m, ids, (int)T, (int)pos);
+    return rc ? throw_ti(env, fn, rc) : undefined(env);
+}
+
+napi_value js_bonsai_decode(napi_env env, napi_callback_info info) {
+    Args a(env, info);
+    if (!want_args(env, a, 2, "bonsai_decode")) return nullptr;
+    CtxH* c = get_ctx(env, a.v[0], "bonsai_decode");
+    BonsaiH* h = c ? get_bonsai(env, a.v[1], "bonsai_decode", 1) : nullptr;
+    if (!h) return nullptr;
+    const int rc = ti_bonsai_decode(c->c, h->m);
+    return rc ? throw_ti(env, "bonsai_decode", rc) : undefined(env);
+}
+
+napi_value js_bonsai_set_pos(napi_env env, napi_callback_info info) {
+    Args a(env, info);
+    if (!want_args(env, a, 3, "bonsai_set_pos")) return nullptr;
+    CtxH* c = get_ctx(env, a.v[0], "bonsai_set_pos");
+    BonsaiH* h = c ? get_bonsai(env, a.v[1], "bonsai_set_pos", 1) : nullptr;
+    int64_t pos;
+    if (!h || !get_i64(env, a.v[2], &pos, "bonsai_set_pos", 2)) return nullptr;
+    const int rc = ti_bonsai_set_pos(c->c, h->m, (int)pos);
+    return rc ? throw_ti(env, "bonsai_set_pos", rc) : undefined(env);
+}
+
+napi_value js_bonsai_write_tokens(napi_env env, napi_callback_info info) {
+    const char* fn = "bonsai_write_tokens";
+    Args a(env, info);
+    if (!want_args(env, a, 4, fn)) return nullptr;
+    CtxH* c = get_ctx(env, a.v[0], fn);
+    BonsaiH* h = c ? get_bonsai(env, a.v[1], fn, 1) : nullptr;
+    int64_t from;
+    const int32_t* ids;
+    size_t n;
+    if (!h || !get_i64(env, a.v[2], &from, fn, 2) || !host_i32(env, a.v[3], &ids, &n, fn, 3)) return nullptr;
+    const int rc = ti_bonsai_write_tokens(c->c, h->m, (int)from, (int)n, ids);
+    return rc ? throw_ti(env, fn, rc) : undefined(env);
+}
+
+napi_value js_bonsai_read_tokens(napi_env env, napi_callback_info info) {
+    const char* fn = "bonsai_read_tokens";
+    Args a(env, info);
+    if (!want_args(env, a, 4, fn)) return nullptr;
+    CtxH* c = get_ctx(env, a.v[0], fn);
+    BonsaiH* h = c ? get_bonsai(env, a.v[1], fn, 1) : nullptr;
+    int64_t from, count;
+    if (!h || !get_i64(env, a.v[2], &from, fn, 2) || !get_i64(env, a.v[3], &count, fn, 3)) return nullptr;
+    if (count < 0 || count > (1 << 26)) return throw_msg(env, "bonsai_read_tokens: bad count");
+    void* data;
+    napi_value ab, arr;
+    napi_create_arraybuffer(env, (size_t)count * 4, &data, &ab);
+    const int rc = ti_bonsai_read_tokens(c->c, h->m, (int)from, (int)count, static_cast<int32_t*>(data));
+    if (rc) return throw_ti(env, fn, rc);
+    napi_create_typedarray(env, napi_int32_array, (size_t)count, ab, 0, &arr);
+    return arr;
+}
+
+// bonsai_trace(model, buffer | null)
+napi_value js_bonsai_trace(napi_env env, napi_callback_info info) {
+    Args a(env, info);
+    if (!want_args(env, a, 2, "bonsai_trace")) return nullptr;
+    BonsaiH* h = get_bonsai(env, a.v[0], "bonsai_trace", 0);
+    void* p = nullptr;
+    if (!h || !get_dptr(env, a.v[1], &p, "bonsai_trace", 1)) return nullptr;
+    BufH* b = p ? handle_of<BufH>(env, a.v[1], TAG_BUF) : nullptr;
+    const int rc = ti_bonsai_trace(h->m, p, b ? b->bytes : 0);
+    return rc ? throw_ti(env, "bonsai_trace", rc) : undefined(env);
+}
+
 napi_value js_qwen3_read_tokens(napi_env env, napi_callback_info info) {
     const char* fn = "qwen3_read_tokens";
     Args a(env, info);
@@ -1108,6 +1324,18 @@ napi_value module_init(napi_env env, napi_value exports) {
         FN("qwen3_trace", js_qwen3_trace),
         FN("qwen3_write_tokens", js_qwen3_write_tokens),
         FN("qwen3_read_tokens", js_qwen3_read_tokens),
+        FN("bonsai_create", js_bonsai_create),
+        FN("bonsai_destroy", js_bonsai_destroy),
+        FN("bonsai_load", js_bonsai_load),
+        FN("bonsai_tensor", js_bonsai_tensor),
+        FN("bonsai_kv", js_bonsai_kv),
+        FN("bonsai_logits", js_bonsai_logits),
+        FN("bonsai_forward", js_bonsai_forward),
+        FN("bonsai_decode", js_bonsai_decode),
+        FN("bonsai_set_pos", js_bonsai_set_pos),
+        FN("bonsai_write_tokens", js_bonsai_write_tokens),
+        FN("bonsai_read_tokens", js_bonsai_read_tokens),
+        FN("bonsai_trace", js_bonsai_trace),
         FN("cpubin_open", js_cpubin_open),
         FN("cpubin_parse", js_cpubin_parse),
         FN("cpubin_close", js_cpubin_close),
