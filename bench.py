@@ -634,6 +634,9 @@ def ab_min(a, b, reps, warmup):
     return ta, tb
 
 
+CPU_REPS = 241
+
+
 def cpu_baseline(threads=16):
     """The reference's native CPU path, n2 avx2::gemv_tern (restated in C,
     oracle/tern_avx2.c), over the whole Bonsai-1.7B ternary GEMV set of one decode step
@@ -642,7 +645,8 @@ def cpu_baseline(threads=16):
     the reference's discipline (timing.rs): a base-vs-base control that must read
     1.00 +- 0.15 (retried up to 3 times, else the figures are withheld), then 1 thread
     (the reference's configuration) against N threads on a persistent pool (a barrier after
-    each GEMV, as a forward pass needs), alternating order, 3 warm-ups, min of 31."""
+    each GEMV, as a forward pass needs), alternating order, 3 warm-ups, min of CPU_REPS (at
+    least the reference's 31; 241 passes of each make a ~10 s sample)."""
     from oracle import oracle as orc
     if not orc.has_avx2():
         return None
@@ -678,7 +682,7 @@ def cpu_baseline(threads=16):
             if abs(control - 1.0) <= 0.15:
                 break
         clean = abs(control - 1.0) <= 0.15
-        t1, tn = ab_min(pool.run_serial, pool.run, 31, 3)
+        t1, tn = ab_min(pool.run_serial, pool.run, CPU_REPS, 3)
     finally:
         pool.close()
     dt = time.perf_counter() - t0
@@ -686,8 +690,8 @@ def cpu_baseline(threads=16):
     res = {"value": round(nb / t1 / 1e9, 2) if clean else None, "unit": "GB/s", "cores": 1, "kind": "port",
            "sample": "n2 avx2::gemv_tern restated in C (oracle/tern_avx2.c), the reference's native CPU path (it "
                      "has no CPU int4 path): the Bonsai-1.7B ternary GEMV set of one decode step, 28 layers + "
-                     "lm_head 151936x2048, %.1f MB; min of 31 alternating 1-thread/%d-thread passes after 3 "
-                     "warm-ups; %.1f s" % (nb / 1e6, pool.threads, dt),
+                     "lm_head 151936x2048, %.1f MB; min of %d alternating 1-thread/%d-thread passes after 3 "
+                     "warm-ups; %.1f s" % (nb / 1e6, CPU_REPS, pool.threads, dt),
            "ms_per_step_1t": round(t1 * 1e3, 2), "GMAC_s_1t": round(macs / t1 / 1e9, 2),
            "threads_n": {"threads": pool.threads, "GB_s": round(nb / tn / 1e9, 2) if clean else None,
                          "GMAC_s": round(macs / tn / 1e9, 2) if clean else None, "ms_per_step": round(tn * 1e3, 2)},
