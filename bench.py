@@ -594,6 +594,78 @@ def ternary_step(ctx, reps=10):
             "what": "28 layers (q/k/v in one launch, o, gate/up in one launch, down) + lm_head 151936x2048, distinct weights"}
 
 
+def bonsai_decode(ctx, contexts=(1024, 8192), steps=64):
+    """The Bonsai-1.7B ternary decoder (ti_bonsai_*, model.rs's forward) at batch 1: one
+    captured decode step (~11 launches per layer) replayed token after token over an f32 KV
+    prefix of S positions; every layer's distinct ternary weights (541 MB with the lm_head)
+    and the f32 KV cache (S x 8 KV heads x 128 x 2 x 4 B per layer) stream from HBM."""
+    from tabinfer_amd import abi
+    rng = np.random.default_rng(5)
+    H, I, nq, nkv = BONSAI_H, 6144, 2048, 1024
+    shapes = {"self_attn.q_proj.weight": (nq, H), "self_attn.k_proj.weight": (nkv, H), "self_attn.v_proj.weight": (nkv, H),
+              "self_attn.o_proj.weight": (H, nq), "mlp.gate_proj.weight": (I, H), "mlp.up_proj.weight": (I, H),
+              "mlp.down_proj.weight": (H, I)}
+    src = {}
+    for name, (N, K) in shapes.items():
+        if (N, K) not in src:
+            src[(N, K)] = (ctx.upload(tern_codes_fast(rng, N * K // 4)),
+                           ctx.upload(rng.uniform(0.01, 0.05, N * K // 64).astype(np.float16).astype(np.float32)))
+    out = {}
+    for S in contexts:
+        m = abi.Bonsai(ctx, layers=BONSAI_LAYERS, hidden=H, intermediate=I, n_heads=16, n_kv_heads=8, head_dim=128,
+                       vocab=BONSAI_VOCAB, rope_theta=1e6, rms_eps=1e-6, max_ctx=S + steps + 8)
+        try:
+            for l in range(BONSAI_LAYERS):
+                pre = "model.layers.%d." % l
+                for name, (N, K) in shapes.items():
+                    dp, nd, sp, ns = m.tensor(pre + name)
+                    c0, s0 = src[(N, K)]
+                    ctx.call("ti_buf_copy", dp, 0, c0, 0, nd)
+                    ctx.call("ti_buf_copy", sp, 0, s0, 0, ns)
+                for name in ("input_layernorm.weight", "post_attention_layernorm.weight", "self_attn.q_norm.weight",
+                             "self_attn.k_norm.weight"):
+                    dp, nd, _, _ = m.tensor(pre + name)
+                    ctx.call("ti_buf_fill_u32", dp, 0x3F800000, nd // 4)            # 1.0f
+                k, v = m.kv(l)
+                n = (S + steps + 8) * nkv
+                ctx.call("ti_buf_fill_u32", k, 0x3C23D70A, n)                        # 0.01f
+                ctx.call("ti_buf_fill_u32", v, 0x3C23D70A, n)
+            dp, nd, _, _ = m.tensor("model.norm.weight")
+            ctx.call("ti_buf_fill_u32", dp, 0x3F800000, nd // 4)
+            dp, nd, sp, ns = m.tensor("lm_head.weight")
+            ctx.write(dp, tern_codes_fast(rng, nd))
+            ctx.write(sp, rng.uniform(0.01, 0.05, ns // 4).astype(np.float16).astype(np.float32))
+            dp, nd, _, _ = m.tensor("model.embed_tokens.weight")
+            ctx.call("ti_buf_fill_u32", dp, 0x2E663266, nd // 4)                  # f16 pairs ~0.1 / ~0.2
+            m.write_tokens(S, np.array([17], np.int32))
+            m.set_pos(S)
+            ctx.sync()
+            g = graph_of(ctx, m.decode)
+            try:
+                for _ in range(4):
+                    ctx.graph_launch(g)
+                ctx.sync()
+                m.set_pos(S)
+                ctx.sync()
+                ctx.record(30)
+                for _ in range(steps):
+                    ctx.graph_launch(g)
+                ctx.record(31)
+                ctx.sync()
+                ms = ctx.elapsed_ms(30, 31) / steps
+            finally:
+                ctx.graph_destroy(g)
+        finally:
+            m.close()
+        wb, _ = bonsai_set_bytes()
+        kvb = BONSAI_LAYERS * S * nkv * 2 * 4
+        out["ctx_%d" % S] = {"tok_s": round(1e3 / ms, 1), "ms_per_token": round(ms, 4),
+                             "step_GB_s": round((wb + kvb) / (ms * 1e-3) / 1e9, 1),
+                             "pct_of_hbm_peak": round(100 * (wb + kvb) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
+                             "bytes_per_step": wb + kvb}
+    return out
+
+
 # ---- the CPU baseline: the reference's native CPU path on config 1 --------------------------------
 def cpu_features():
     """CPU model, logical CPUs, usable CPUs and the SIMD features that set the ternary
@@ -707,10 +779,12 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
-    ap.add_argument("--only", choices=("gemv", "all", "moe", "decode", "decode8"), default="all",
+    ap.add_argument("--only", choices=("gemv", "all", "moe", "decode", "decode8", "tern", "bonsai"),
+                    default="all",
                     help="gemv: the headline workload only; moe: headline + the int3 MoE leg; "
                          "decode: the Qwen3-1.7B batch-1 decode leg alone, --steps tokens (no headline line); "
-                         "decode8: its batch-8 (T = 8 forward) leg alone")
+                         "decode8: its batch-8 (T = 8 forward) leg alone; tern: the ternary GEMV step alone; "
+                         "bonsai: the Bonsai decoder alone at --ctx (default 1024) (no headline line)")
     ap.add_argument("--ctx", type=int, nargs="*", default=None,
                     help="context lengths of the decode leg (default 8192 32768)")
     args = ap.parse_args()
@@ -729,6 +803,16 @@ def main():
                           batch1=args.only == "decode")
         ctx.close()
         print(json.dumps({"decode_1p7b": res}))
+        return
+    if args.only in ("tern", "bonsai"):       # one ternary leg alone, one graph per process (profiling runs)
+        if args.only == "tern":
+            log("ternary step")
+            res = {"ternary_bonsai_step": ternary_step(ctx)}
+        else:
+            log("bonsai decode")
+            res = {"bonsai_decode": bonsai_decode(ctx, contexts=tuple(args.ctx) if args.ctx else (1024,))}
+        ctx.close()
+        print(json.dumps(res))
         return
     cfg = QWEN3_06B
     step = Step(ctx, cfg)
@@ -795,6 +879,8 @@ def main():
         out["attention_layer"] = attention(ctx, flush)
         log("decode 1.7B")
         out["decode_1p7b"] = decode_1p7b(ctx, pool, contexts=contexts)
+        log("bonsai decode")
+        out["bonsai_decode"] = bonsai_decode(ctx)
     if not args.no_cpu:
         log("cpu baseline")
         cb = cpu_baseline()

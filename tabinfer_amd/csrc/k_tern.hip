@@ -111,28 +111,29 @@ __global__ __launch_bounds__(64) void k_tern_gemv(const uint4* __restrict__ code
     }
 }
 
-// B = 1 with K a multiple of 1024 (16 lanes x BPL blocks per row): 4 rows per wave,
-// 16 rows per workgroup, so a 2048-row matrix spreads over 512 waves (the tile kernel
-// above gives one wave 64 rows: too few waves for the small per-layer matrices).
-// Lanes compute the exact block dots and fetch the block scales; after one barrier,
-// lane 0 of each row's 16 replays the row's accumulation in the reference's block
-// order from LDS.
+// B = 1, the latency-bound decode shapes: LPR lanes per row (32 when the row's block count
+// is a multiple of 32, else 16), lane li owning blocks li + LPR j, so a 2048-row matrix
+// spreads over 256 workgroups of 4 waves. Every lane forms its blocks' exact int32 dots and
+// the two products s*dot and s*xsum (the same IEEE products the reference forms) and parks
+// them in LDS; then lane 0 of the row adds the s*dot products and lane 1 the s*xsum
+// products, each in block order (tern.rs:79-119's two chains), four per LDS read, and the
+// row's result is their difference. A row's products come from its own wave, so the
+// hand-off is a wave-level one: LDS operations of a wave complete in program order.
 struct TernMats {
     const uint4* codes[3];
     const float* scales[3];
     float* out[3];
     int N[3];
-    int blk0[3];      // first workgroup of each matrix (16 rows per workgroup)
+    int blk0[3];      // first workgroup of each matrix
     int nmat;
 };
 
-template <int BPL>
-__global__ __launch_bounds__(256) void k_tern_gemv_r4(TernMats m, const int8_t* __restrict__ act,
+template <int LPR, int BPL>
+__global__ __launch_bounds__(256) void k_tern_gemv_rw(TernMats m, const int8_t* __restrict__ act,
                                                       const int32_t* __restrict__ xsum) {
-    constexpr int LPR = 16, RW = 4, NB = LPR * BPL;
-    __shared__ int s_dot[4][RW][NB + 1];
-    __shared__ float s_sc[4][RW][NB + 1];
-    __shared__ float s_xs[NB];
+    constexpr int RW = 64 / LPR, NB = LPR * BPL, RPB = 4 * RW;
+    static_assert(NB % 4 == 0, "four products per LDS read");
+    __shared__ float4 s_pq[4][RW][2][NB / 4];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r = lane / LPR, li = lane % LPR;
     // the matrix of this workgroup (uniform: selects, no divergent indexing of the kernargs)
@@ -143,44 +144,67 @@ __global__ __launch_bounds__(256) void k_tern_gemv_r4(TernMats m, const int8_t* 
     float* out = mi == 0 ? m.out[0] : (mi == 1 ? m.out[1] : m.out[2]);
     const int N = mi == 0 ? m.N[0] : (mi == 1 ? m.N[1] : m.N[2]);
     const int b0 = mi == 0 ? 0 : (mi == 1 ? m.blk0[1] : m.blk0[2]);
-    const long row = ((long)(b - b0) * 4 + wave) * RW + r;
+    const long row = (long)(b - b0) * RPB + wave * RW + r;
     const long rowc = row < N ? row : N - 1;
     uint4 cw[BPL];
-    float sc[BPL];
+    float sc[BPL], xs[BPL];
 #pragma unroll
     for (int j = 0; j < BPL; j++) {
         cw[j] = ti_ld_nt(codes + rowc * NB + li + LPR * j);
         sc[j] = scales[rowc * NB + li + LPR * j];
+        xs[j] = (float)xsum[li + LPR * j];
     }
-    for (int i = tid; i < NB; i += 256) s_xs[i] = (float)xsum[i];
+    float* sp = reinterpret_cast<float*>(&s_pq[wave][r][0][0]);
+    float* sq = reinterpret_cast<float*>(&s_pq[wave][r][1][0]);
 #pragma unroll
     for (int j = 0; j < BPL; j++) {
         ActT t;
-        load_act_tern(act, nullptr, li + LPR * j, t);
-        s_dot[wave][r][li + LPR * j] = tern_block_dot(cw[j], t);
-        s_sc[wave][r][li + LPR * j] = sc[j];
+        const int blk = li + LPR * j;
+        load_act_tern(act, nullptr, blk, t);
+        sp[blk] = sc[j] * (float)tern_block_dot(cw[j], t);
+        sq[blk] = sc[j] * xs[j];
     }
-    __syncthreads();
-    if (li == 0 && row < N) {
-        float acc = 0.0f, sxs = 0.0f;
-#pragma unroll 8
-        for (int blk = 0; blk < NB; blk++) {
-            const float s = s_sc[wave][r][blk];
-            const float p = s * (float)s_dot[wave][r][blk];
-            acc = acc + p;
-            const float q = s * s_xs[blk];
-            sxs = sxs + q;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float v = 0.0f;
+    if (li < 2) {
+        const float4* pq = &s_pq[wave][r][li][0];
+#pragma unroll 6
+        for (int i = 0; i < NB / 4; i++) {
+            const float4 p = pq[i];
+            v = v + p.x;
+            v = v + p.y;
+            v = v + p.z;
+            v = v + p.w;
         }
-        out[row] = acc - sxs;
     }
+    const float sxs = __shfl_down(v, 1);
+    if (li == 0 && row < N) out[row] = v - sxs;
 }
 
-static bool r4_launch(ti_ctx* c, const TernMats& m, int nb, const int8_t* act, const int32_t* xsum, int grid) {
-    if (nb % 16 != 0 || nb / 16 > 8) return false;
-#define R4(P) \
-    if (nb / 16 == P) { k_tern_gemv_r4<P><<<grid, 256, 0, c->stream>>>(m, act, xsum); return true; }
-    R4(1) R4(2) R4(3) R4(4) R4(5) R4(6) R4(7) R4(8)
-#undef R4
+// rows per workgroup of k_tern_gemv_rw for nb blocks per row; 0: no instantiation
+static int rw_rows(int nb) {
+    if (nb % 32 == 0 && nb / 32 <= 4) return 8;
+    if (nb % 16 == 0 && nb / 16 <= 7) return 16;
+    return 0;
+}
+
+// sets m.blk0 for the kernel's rows per workgroup and launches; false: no kernel for nb
+static bool rw_launch(ti_ctx* c, TernMats& m, int nb, const int8_t* act, const int32_t* xsum) {
+    const int rpb = rw_rows(nb);
+    if (!rpb) return false;
+    long blocks = 0;
+    for (int i = 0; i < 3; i++) {
+        m.blk0[i] = (int)blocks;
+        if (i < m.nmat) blocks += (m.N[i] + rpb - 1) / rpb;
+    }
+    if (blocks >= (1L << 31)) return false;
+    const unsigned grid = (unsigned)blocks;
+#define RW(L, P) \
+    if (nb == L * P) { k_tern_gemv_rw<L, P><<<grid, 256, 0, c->stream>>>(m, act, xsum); return true; }
+    RW(32, 1) RW(32, 2) RW(32, 3) RW(32, 4) RW(16, 1) RW(16, 3) RW(16, 5) RW(16, 7)
+#undef RW
     return false;
 }
 
@@ -296,8 +320,8 @@ static int tern_launch(ti_ctx* c, float* out, const uint8_t* codes, const float*
         m.out[0] = m.out[1] = m.out[2] = out;
         m.N[0] = m.N[1] = m.N[2] = N;
         m.nmat = 1;
-        if (r4_launch(c, m, nb, act, xsum, (N + 15) / 16)) {
-            TI_LAUNCHED("k_tern_gemv_r4");
+        if (rw_launch(c, m, nb, act, xsum)) {
+            TI_LAUNCHED("k_tern_gemv_rw");
             return TI_OK;
         }
     }
@@ -352,7 +376,6 @@ extern "C" int ti_tern_gemv_multi(ti_ctx* c, const int8_t* act, const int32_t* x
     TI_REQUIRE(K > 0 && K % 1024 == 0 && K <= 8192, "ti_tern_gemv_multi: K must be a multiple of 1024, <= 8192 (K=%d)", K);
     TI_REQUIRE(al16(act), "ti_tern_gemv_multi: act must be 16-byte aligned");
     TernMats m = {};
-    long blocks = 0;
     for (int i = 0; i < 3; i++) {
         const int s = i < nmat ? i : nmat - 1;
         if (i < nmat) {
@@ -363,13 +386,10 @@ extern "C" int ti_tern_gemv_multi(ti_ctx* c, const int8_t* act, const int32_t* x
         m.scales[i] = scales[s];
         m.out[i] = outs[s];
         m.N[i] = Ns[s];
-        m.blk0[i] = (int)blocks;
-        if (i < nmat) blocks += (Ns[i] + 15) / 16;
     }
-    TI_REQUIRE(blocks < (1L << 31), "ti_tern_gemv_multi: too many rows");
     m.nmat = nmat;
-    if (!r4_launch(c, m, K / 64, act, xsum, (int)blocks)) return ti_fail(TI_ERR_INVALID, "ti_tern_gemv_multi: no kernel for K=%d", K);
-    TI_LAUNCHED("k_tern_gemv_r4");
+    if (!rw_launch(c, m, K / 64, act, xsum)) return ti_fail(TI_ERR_INVALID, "ti_tern_gemv_multi: no kernel for K=%d", K);
+    TI_LAUNCHED("k_tern_gemv_rw");
     return TI_OK;
 }
 
