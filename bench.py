@@ -594,7 +594,7 @@ def ternary_step(ctx, reps=10):
             "what": "28 layers (q/k/v in one launch, o, gate/up in one launch, down) + lm_head 151936x2048, distinct weights"}
 
 
-def bonsai_decode(ctx, contexts=(1024, 8192), steps=64):
+def bonsai_decode(ctx, contexts=(1024, 8192), steps=64, eager=False):
     """The Bonsai-1.7B ternary decoder (ti_bonsai_*, model.rs's forward) at batch 1: one
     captured decode step (~11 launches per layer) replayed token after token over an f32 KV
     prefix of S positions; every layer's distinct ternary weights (541 MB with the lm_head)
@@ -640,21 +640,33 @@ def bonsai_decode(ctx, contexts=(1024, 8192), steps=64):
             m.write_tokens(S, np.array([17], np.int32))
             m.set_pos(S)
             ctx.sync()
-            g = graph_of(ctx, m.decode)
-            try:
+            if eager:                       # launched directly (kernel traces without graphs)
                 for _ in range(4):
-                    ctx.graph_launch(g)
-                ctx.sync()
+                    m.decode()
                 m.set_pos(S)
                 ctx.sync()
                 ctx.record(30)
                 for _ in range(steps):
-                    ctx.graph_launch(g)
+                    m.decode()
                 ctx.record(31)
                 ctx.sync()
                 ms = ctx.elapsed_ms(30, 31) / steps
-            finally:
-                ctx.graph_destroy(g)
+            else:
+                g = graph_of(ctx, m.decode)
+                try:
+                    for _ in range(4):
+                        ctx.graph_launch(g)
+                    ctx.sync()
+                    m.set_pos(S)
+                    ctx.sync()
+                    ctx.record(30)
+                    for _ in range(steps):
+                        ctx.graph_launch(g)
+                    ctx.record(31)
+                    ctx.sync()
+                    ms = ctx.elapsed_ms(30, 31) / steps
+                finally:
+                    ctx.graph_destroy(g)
         finally:
             m.close()
         wb, _ = bonsai_set_bytes()
@@ -785,6 +797,7 @@ def main():
                          "decode: the Qwen3-1.7B batch-1 decode leg alone, --steps tokens (no headline line); "
                          "decode8: its batch-8 (T = 8 forward) leg alone; tern: the ternary GEMV step alone; "
                          "bonsai: the Bonsai decoder alone at --ctx (default 1024) (no headline line)")
+    ap.add_argument("--eager", action="store_true", help="--only bonsai: launch the steps directly, without a graph")
     ap.add_argument("--ctx", type=int, nargs="*", default=None,
                     help="context lengths of the decode leg (default 8192 32768)")
     args = ap.parse_args()
@@ -810,7 +823,8 @@ def main():
             res = {"ternary_bonsai_step": ternary_step(ctx)}
         else:
             log("bonsai decode")
-            res = {"bonsai_decode": bonsai_decode(ctx, contexts=tuple(args.ctx) if args.ctx else (1024,))}
+            res = {"bonsai_decode": bonsai_decode(ctx, contexts=tuple(args.ctx) if args.ctx else (1024,),
+                                                  eager=args.eager)}
         ctx.close()
         print(json.dumps(res))
         return

@@ -266,7 +266,7 @@ typedef struct ti_bonsai ti_bonsai;
 typedef struct {
     int layers, hidden, intermediate, n_heads, n_kv_heads, head_dim, vocab;
     float rope_theta, rms_eps;
-    int max_ctx;      /* KV capacity in positions */
+    int max_ctx;      /* KV capacity in positions, <= 40960 */
 } ti_bonsai_config;
 int ti_bonsai_create(ti_ctx* ctx, const ti_bonsai_config* cfg, ti_bonsai** out);
 int ti_bonsai_destroy(ti_ctx* ctx, ti_bonsai* m);

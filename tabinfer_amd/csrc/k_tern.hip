@@ -251,8 +251,7 @@ __global__ __launch_bounds__(1024) void k_quant_act_tern(const float* __restrict
     const int t = threadIdx.x;
     float m = 0.0f;
     for (int i = t; i < K; i += 1024) m = fmaxf(m, fabsf(x[i]));
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, ti_xor(m, o));
+    m = ti_wave_max(m);
     if ((t & 63) == 0) red[t >> 6] = m;
     __syncthreads();
     if (t == 0) {
@@ -275,9 +274,7 @@ __global__ __launch_bounds__(1024) void k_quant_act_tern(const float* __restrict
         r = fminf(fmaxf(r, -127.0f), 127.0f);
         int q = (int)r;
         act[blk * 64 + lane] = (int8_t)q;
-        int sum = q;
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) sum += ti_xor(sum, o);
+        const int sum = ti_wave_sum_i(q);
         if (lane == 0) xsum[blk] = sum;
     }
 }

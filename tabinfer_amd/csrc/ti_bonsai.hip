@@ -25,13 +25,11 @@
 namespace {
 
 constexpr int BN_THREADS = 1024;
-constexpr int BN_ATTN_CHUNK = 256;        // keys per attention workgroup
 constexpr int BN_AMAX_PARTS = 256;
 
 // total of one float per thread over a 1024-thread workgroup (a tree; every thread gets it)
 __device__ __forceinline__ float wg_sum_1024(float v, float* red) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += ti_xor(v, o);
+    v = ti_wave_sum(v);
     __syncthreads();
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
     __syncthreads();
@@ -42,8 +40,7 @@ __device__ __forceinline__ float wg_sum_1024(float v, float* red) {
 }
 
 __device__ __forceinline__ float wg_max_1024(float v, float* red) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, ti_xor(v, o));
+    v = ti_wave_max(v);
     __syncthreads();
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
     __syncthreads();
@@ -77,9 +74,7 @@ __device__ __forceinline__ void quant_n2(const float (&v)[EPT], int n, int8_t* _
             q = (int)r;
             act[e] = (int8_t)q;
         }
-        int sum = q;
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) sum += ti_xor(sum, o);
+        const int sum = ti_wave_sum_i(q);
         if ((t & 63) == 0 && e < n) xsum[e / 64] = sum;
     }
 }
@@ -106,22 +101,31 @@ __global__ __launch_bounds__(BN_THREADS) void k_bn_norm_quant(float* __restrict_
                                                              float* __restrict__ scale_out) {
     __shared__ float red[16];
     const int t = threadIdx.x;
-    float v[EPT];
+    float v[EPT], a[EPT], wv[EPT];
+    // every load first (clamped indices), so they are in flight together
+#pragma unroll
+    for (int i = 0; i < EPT; i++) {
+        const int e = min(t + BN_THREADS * i, H - 1);
+        v[i] = x[e];
+        a[i] = add ? add[e] : 0.0f;
+        wv[i] = w[e];
+    }
     const float inv_add = add ? 1.0f / *add_scale : 0.0f;
     float ss = 0.0f;
 #pragma unroll
     for (int i = 0; i < EPT; i++) {
         const int e = t + BN_THREADS * i;
-        v[i] = 0.0f;
         if (e < H) {
-            float xe = x[e];
+            float xe = v[i];
             if (add) {
-                const float d = add[e] * inv_add;
+                const float d = a[i] * inv_add;
                 xe = xe + d;
                 x[e] = xe;
             }
             v[i] = xe;
             ss = ss + xe * xe;
+        } else {
+            v[i] = 0.0f;
         }
     }
     const float mean = wg_sum_1024(ss, red) / (float)H;
@@ -130,25 +134,11 @@ __global__ __launch_bounds__(BN_THREADS) void k_bn_norm_quant(float* __restrict_
     for (int i = 0; i < EPT; i++) {
         const int e = t + BN_THREADS * i;
         if (e < H) {
-            v[i] = v[i] * inv * w[e];
+            v[i] = v[i] * inv * wv[i];
             if (xn_out) xn_out[e] = v[i];
         }
     }
     quant_n2<EPT>(v, H, act, xsum, scale_out, red);
-}
-
-// ---- quantize an f32 vector (the attention output) -----------------------------------------
-template <int EPT>
-__global__ __launch_bounds__(BN_THREADS) void k_bn_quant(const float* __restrict__ x, int n, int8_t* __restrict__ act,
-                                                        int32_t* __restrict__ xsum, float* __restrict__ scale_out) {
-    __shared__ float red[16];
-    float v[EPT];
-#pragma unroll
-    for (int i = 0; i < EPT; i++) {
-        const int e = threadIdx.x + BN_THREADS * i;
-        v[i] = e < n ? x[e] : 0.0f;
-    }
-    quant_n2<EPT>(v, n, act, xsum, scale_out, red);
 }
 
 // ---- SwiGLU of the scaled gate/up + quantize (ops.rs:110-117) ---------------------------------
@@ -158,16 +148,22 @@ __global__ __launch_bounds__(BN_THREADS) void k_bn_swiglu_quant(const float* __r
                                                                float* __restrict__ swi_out, int8_t* __restrict__ act,
                                                                int32_t* __restrict__ xsum, float* __restrict__ scale_out) {
     __shared__ float red[16];
+    float g[EPT], u[EPT], v[EPT];
+#pragma unroll
+    for (int i = 0; i < EPT; i++) {
+        const int e = min((int)threadIdx.x + BN_THREADS * i, n - 1);
+        g[i] = graw[e];
+        u[i] = uraw[e];
+    }
     const float inv = 1.0f / *gu_scale;
-    float v[EPT];
 #pragma unroll
     for (int i = 0; i < EPT; i++) {
         const int e = threadIdx.x + BN_THREADS * i;
         v[i] = 0.0f;
         if (e < n) {
-            const float g = graw[e] * inv;
-            const float u = uraw[e] * inv;
-            v[i] = (g / (1.0f + expf(-g))) * u;
+            const float gg = g[i] * inv;
+            const float uu = u[i] * inv;
+            v[i] = (gg / (1.0f + expf(-gg))) * uu;
             if (swi_out) swi_out[e] = v[i];
         }
     }
@@ -222,51 +218,68 @@ __global__ __launch_bounds__(128) void k_bn_prep(const float* __restrict__ qraw,
 }
 
 // ---- GQA attention over the f32 cache (model.rs:421-447) ------------------------------------
-// workgroup (KV head, split of BN_ATTN_CHUNK keys), G query heads of hd dims (G * hd <= 256):
-// scores by 16 lanes per key (8 dims each), a max/exp/sum over the chunk, then P V with
-// one thread per (head, dim); partials (o, m, l) per (query head, split).
-template <int G, int HD>
+// keys per attention workgroup for a cache of cap positions: 64, or more for long caches, so
+// that the split count stays within 160
+constexpr int BN_MAX_CTX = 256 * 160;
+__host__ __device__ inline int bn_chunk(int cap) {
+    return cap <= 64 * 160 ? 64 : (cap <= 128 * 160 ? 128 : 256);
+}
+
+// workgroup (KV head hk, split of CH keys), the G = 2 query heads of hk (hd 128):
+//  scores: 4 lanes per key, 32 dims each (8 float4 loads a lane, in flight together), a quad
+//          sum, 64 keys per pass;
+//  max / exp / sum over the split's keys;
+//  P V: lane (key group kg = t / 32, dims 4 (t % 32) ..) over keys kg, kg + 8, .. (one float4
+//       of V serves both heads), then the 8 key-group partials summed in order;
+//  partials (o, m, l) per (query head, split).
+template <int CH>
 __global__ __launch_bounds__(256) void k_bn_attn(const float* __restrict__ qr, const float* __restrict__ kc,
                                                  const float* __restrict__ vc, const int* __restrict__ dpos, int nKv,
                                                  float* __restrict__ po, float* __restrict__ pml, int ns_stride, int cap) {
-    constexpr int LPK = 16, DPL = HD / LPK;            // lanes per key, dims per lane
-    constexpr int KPP = 256 / LPK;                     // keys per pass
-    __shared__ float sc[G][BN_ATTN_CHUNK];
+    constexpr int G = 2, HD = 128;
+    __shared__ float sc[G][CH];
+    __shared__ float4 so[8][G][HD / 4];
     __shared__ float red[G][4];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int hk = blockIdx.x % nKv, split = blockIdx.x / nKv;
     const int S = min(*dpos + 1, cap);
-    const int c0 = split * BN_ATTN_CHUNK;
-    if (c0 >= S) return;                               // the combine reads splits below ceil(S / chunk) only
-    const int n = min(BN_ATTN_CHUNK, S - c0);
-    const size_t kv_dim = (size_t)nKv * HD;
+    const int c0 = split * CH;
+    if (c0 >= S) return;                               // the merge reads splits below ceil(S / CH) only
+    const int n = min(CH, S - c0);
+    const size_t kvd = (size_t)nKv * HD;
     const float scale = 1.0f / sqrtf((float)HD);
-    const int kl = t / LPK, sl = t % LPK;
-    float q[G][DPL];
+    const int qd = t & 3;
+    float4 q[G][8];
 #pragma unroll
     for (int g = 0; g < G; g++)
 #pragma unroll
-        for (int d = 0; d < DPL; d++) q[g][d] = qr[(size_t)(hk * G + g) * HD + sl * DPL + d];
-    for (int j0 = 0; j0 < n; j0 += KPP) {
-        const int j = j0 + kl;
+        for (int i = 0; i < 8; i++) q[g][i] = reinterpret_cast<const float4*>(qr + (size_t)(hk * G + g) * HD + qd * 32)[i];
+    for (int k0 = 0; k0 < n; k0 += 64) {
+        const int j = k0 + (t >> 2);
         const int key = c0 + (j < n ? j : n - 1);
-        const float* kr = kc + (size_t)key * kv_dim + (size_t)hk * HD + sl * DPL;
-        float kv[DPL];
+        const float4* kr = reinterpret_cast<const float4*>(kc + (size_t)key * kvd + (size_t)hk * HD + qd * 32);
+        float4 kv[8];
 #pragma unroll
-        for (int d = 0; d < DPL; d++) kv[d] = kr[d];
+        for (int i = 0; i < 8; i++) kv[i] = kr[i];
         float part[G];
 #pragma unroll
         for (int g = 0; g < G; g++) {
             float s = 0.0f;
 #pragma unroll
-            for (int d = 0; d < DPL; d++) s = s + kv[d] * q[g][d];
+            for (int i = 0; i < 8; i++) {
+                s = s + kv[i].x * q[g][i].x;
+                s = s + kv[i].y * q[g][i].y;
+                s = s + kv[i].z * q[g][i].z;
+                s = s + kv[i].w * q[g][i].w;
+            }
             part[g] = s;
         }
 #pragma unroll
-        for (int o = LPK / 2; o > 0; o >>= 1)
-#pragma unroll
-            for (int g = 0; g < G; g++) part[g] += ti_xor(part[g], o);
-        if (sl == 0 && j < n)
+        for (int g = 0; g < G; g++) {
+            part[g] += ti_xor(part[g], 1);
+            part[g] += ti_xor(part[g], 2);
+        }
+        if (qd == 0 && j < n)
 #pragma unroll
             for (int g = 0; g < G; g++) sc[g][j] = part[g] * scale;
     }
@@ -276,8 +289,7 @@ __global__ __launch_bounds__(256) void k_bn_attn(const float* __restrict__ qr, c
     for (int g = 0; g < G; g++) {
         float v = -INFINITY;
         for (int j = t; j < n; j += 256) v = fmaxf(v, sc[g][j]);
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, ti_xor(v, o));
+        v = ti_wave_max(v);
         if (lane == 0) red[g][wave] = v;
     }
     __syncthreads();
@@ -292,44 +304,97 @@ __global__ __launch_bounds__(256) void k_bn_attn(const float* __restrict__ qr, c
             sc[g][j] = p;
             s += p;
         }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) s += ti_xor(s, o);
+        s = ti_wave_sum(s);
         if (lane == 0) red[g][wave] = s;
     }
     __syncthreads();
 #pragma unroll
     for (int g = 0; g < G; g++) l[g] = (red[g][0] + red[g][1]) + (red[g][2] + red[g][3]);
-    // P V: thread (g, d)
-    if (t < G * HD) {
-        const int g = t / HD, d = t % HD;
-        const float* vcol = vc + (size_t)c0 * kv_dim + (size_t)hk * HD + d;
-        float o = 0.0f;
-        for (int j = 0; j < n; j++) o = fmaf(sc[g][j], vcol[(size_t)j * kv_dim], o);
+    const int kg = t >> 5, d4 = t & 31;
+    float4 o[G];
+#pragma unroll
+    for (int g = 0; g < G; g++) o[g] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const float4* vb = reinterpret_cast<const float4*>(vc + (size_t)c0 * kvd + (size_t)hk * HD) + d4;
+#pragma unroll 4
+    for (int j = kg; j < n; j += 8) {
+        const float4 vv = vb[(size_t)j * (kvd / 4)];
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            const float p = sc[g][j];
+            o[g].x = fmaf(p, vv.x, o[g].x);
+            o[g].y = fmaf(p, vv.y, o[g].y);
+            o[g].z = fmaf(p, vv.z, o[g].z);
+            o[g].w = fmaf(p, vv.w, o[g].w);
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < G; g++) so[kg][g][d4] = o[g];
+    __syncthreads();
+    {
+        const int g = t >> 7, d = t & 127;
+        const float* sof = reinterpret_cast<const float*>(so);
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; k++) acc += sof[(k * G + g) * HD + d];
         const size_t slot = (size_t)(hk * G + g) * ns_stride + split;
-        po[slot * HD + d] = o;
+        po[slot * HD + d] = acc;
         if (d == 0) {
-            pml[slot * 2] = m[g];
-            pml[slot * 2 + 1] = l[g];
+            pml[slot * 2] = g == 0 ? m[0] : m[1];
+            pml[slot * 2 + 1] = g == 0 ? l[0] : l[1];
         }
     }
 }
 
-// out[h] = sum_i o_i e^(m_i - M) / sum_i l_i e^(m_i - M) over the splits that hold keys
-__global__ __launch_bounds__(128) void k_bn_attn_combine(const float* __restrict__ po, const float* __restrict__ pml,
-                                                         const int* __restrict__ dpos, int ns_stride, int hd,
-                                                         float* __restrict__ out, int cap) {
-    const int h = blockIdx.x, d = threadIdx.x;
-    const int ns = (min(*dpos + 1, cap) + BN_ATTN_CHUNK - 1) / BN_ATTN_CHUNK;
-    const float* ml = pml + (size_t)h * ns_stride * 2;
-    float M = -INFINITY;
-    for (int i = 0; i < ns; i++) M = fmaxf(M, ml[2 * i]);
-    float L = 0.0f, o = 0.0f;
-    for (int i = 0; i < ns; i++) {
-        const float e = expf(ml[2 * i] - M);
-        L += ml[2 * i + 1] * e;
-        if (d < hd) o = fmaf(po[((size_t)h * ns_stride + i) * hd + d], e, o);
+// out[h][d] = sum_i o_i e^(m_i - M) / sum_i l_i e^(m_i - M) over the splits that hold keys,
+// for every query head, then the n2 quantizer of the whole output (one workgroup: the
+// per-tensor scale needs every element). Wave w < n_heads finds head w's M, the split weights
+// e^(m_i - M) (into LDS) and L; then thread (h, d) sums its head's o_i in split order.
+constexpr int BN_MERGE_SPLITS = 160;   // split slots per head: bn_chunk keeps a cache of BN_MAX_CTX within them
+
+template <int EPT>
+__global__ __launch_bounds__(BN_THREADS) void k_bn_merge_quant(const float* __restrict__ po, const float* __restrict__ pml,
+                                                              const int* __restrict__ dpos, int ns_stride, int nq,
+                                                              int chunk, float* __restrict__ out, int8_t* __restrict__ act,
+                                                              int32_t* __restrict__ xsum, float* __restrict__ scale_out,
+                                                              int cap) {
+    constexpr int HD = 128, HMAX = EPT * BN_THREADS / HD;
+    __shared__ float red[16];
+    __shared__ float s_w[HMAX][BN_MERGE_SPLITS];
+    __shared__ float s_l[HMAX];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int ns = (min(*dpos + 1, cap) + chunk - 1) / chunk;
+    const int nh = nq / HD;
+    for (int h = wave; h < nh; h += BN_THREADS / 64) {
+        const float* ml = pml + (size_t)h * ns_stride * 2;
+        float M = -INFINITY;
+        for (int k = lane; k < ns; k += 64) M = fmaxf(M, ml[2 * k]);
+        M = ti_wave_max(M);
+        float L = 0.0f;
+        for (int k = lane; k < ns; k += 64) {
+            const float e2 = expf(ml[2 * k] - M);
+            s_w[h][k] = e2;
+            L += ml[2 * k + 1] * e2;
+        }
+        L = ti_wave_sum(L);
+        if (lane == 0) s_l[h] = L;
     }
-    if (d < hd) out[(size_t)h * hd + d] = o / L;
+    __syncthreads();
+    float v[EPT];
+#pragma unroll
+    for (int i = 0; i < EPT; i++) {
+        const int e = t + BN_THREADS * i;
+        v[i] = 0.0f;
+        if (e < nq) {
+            const int h = e / HD, d = e % HD;
+            const float* ob = po + (size_t)h * ns_stride * HD + d;
+            float o = 0.0f;
+#pragma unroll 8
+            for (int k = 0; k < ns; k++) o = fmaf(ob[(size_t)k * HD], s_w[h][k], o);
+            v[i] = o / s_l[h];
+            out[e] = v[i];
+        }
+    }
+    quant_n2<EPT>(v, nq, act, xsum, scale_out, red);
 }
 
 // ---- logits = raw * (1 / scale), argmax (ops::argmax: larger wins, the lower index on ties,
@@ -500,6 +565,8 @@ extern "C" int ti_bonsai_create(ti_ctx* c, const ti_bonsai_config* cfg, ti_bonsa
                "ti_bonsai_create: hidden and intermediate must be multiples of 1024, at most 8192");
     TI_REQUIRE(C.head_dim == 128 && C.n_heads / C.n_kv_heads == 2 && (C.n_heads * C.head_dim) % 1024 == 0 &&
                C.n_heads * C.head_dim <= 8192, "ti_bonsai_create: the decoder covers head_dim 128 with 2 query heads per KV head");
+    TI_REQUIRE(C.max_ctx <= BN_MAX_CTX, "ti_bonsai_create: max_ctx %d is above the decoder's %d positions", C.max_ctx,
+               BN_MAX_CTX);
     TI_REQUIRE(!c->capturing, "ti_bonsai_create: not during graph capture");
     TI_HIP(hipSetDevice(c->device));
     ti_bonsai* m = new ti_bonsai();
@@ -532,7 +599,7 @@ extern "C" int ti_bonsai_create(ti_ctx* c, const ti_bonsai_config* cfg, ti_bonsa
     if (!rc) rc = bmk(m, (void**)&m->final_norm, H * 4);
     if (!rc) rc = lin(m->lm, C.vocab, H);
     const int widest = I > H ? (I > nq ? I : nq) : (H > nq ? H : nq);
-    const int nsplit = (C.max_ctx + BN_ATTN_CHUNK - 1) / BN_ATTN_CHUNK;
+    const int nsplit = (C.max_ctx + bn_chunk(C.max_ctx) - 1) / bn_chunk(C.max_ctx);
     struct { float** p; size_t n; } fb[] = {{&m->x, (size_t)H}, {&m->xn, (size_t)H}, {&m->qraw, (size_t)nq},
                                             {&m->kraw, (size_t)nkv}, {&m->vraw, (size_t)nkv}, {&m->qr, (size_t)nq},
                                             {&m->attn, (size_t)nq}, {&m->oraw, (size_t)H}, {&m->graw, (size_t)I},
@@ -716,7 +783,7 @@ static int bonsai_step(ti_ctx* c, ti_bonsai* m, bool want_logits) {
     const ti_bonsai_config& C = m->cfg;
     const int H = C.hidden, I = C.intermediate, hd = C.head_dim, nHq = C.n_heads, nKv = C.n_kv_heads;
     const int nq = nHq * hd, nkv = nKv * hd;
-    const int nsplit = (C.max_ctx + BN_ATTN_CHUNK - 1) / BN_ATTN_CHUNK;
+    const int nsplit = (C.max_ctx + bn_chunk(C.max_ctx) - 1) / bn_chunk(C.max_ctx);
     float* sa = m->scales;
     float* sb = m->scales + 1;
     float* scl = m->scales + 2;
@@ -751,16 +818,16 @@ static int bonsai_step(ti_ctx* c, ti_bonsai* m, bool want_logits) {
         k_bn_prep<<<nHq + nKv, 128, 0, c->stream>>>(m->qraw, m->kraw, m->vraw, sa, y.q_norm, y.k_norm, m->rope, m->dpos, m->qr,
                                                     y.kc, y.vc, nHq, nKv, hd, C.rms_eps, C.max_ctx);
         TI_LAUNCHED("k_bn_prep");
-        k_bn_attn<2, 128><<<nKv * nsplit, 256, 0, c->stream>>>(m->qr, y.kc, y.vc, m->dpos, nKv, m->po, m->pml, nsplit,
-                                                               C.max_ctx);
+        const int chunk = bn_chunk(C.max_ctx);
+        if (chunk == 64) k_bn_attn<64><<<nKv * nsplit, 256, 0, c->stream>>>(m->qr, y.kc, y.vc, m->dpos, nKv, m->po, m->pml, nsplit, C.max_ctx);
+        else if (chunk == 128) k_bn_attn<128><<<nKv * nsplit, 256, 0, c->stream>>>(m->qr, y.kc, y.vc, m->dpos, nKv, m->po, m->pml, nsplit, C.max_ctx);
+        else k_bn_attn<256><<<nKv * nsplit, 256, 0, c->stream>>>(m->qr, y.kc, y.vc, m->dpos, nKv, m->po, m->pml, nsplit, C.max_ctx);
         TI_LAUNCHED("k_bn_attn");
-        k_bn_attn_combine<<<nHq, 128, 0, c->stream>>>(m->po, m->pml, m->dpos, nsplit, hd, m->attn, C.max_ctx);
-        TI_LAUNCHED("k_bn_attn_combine");
         const int eq = (nq + BN_THREADS - 1) / BN_THREADS;
-#define QT(E) if (eq <= E) { k_bn_quant<E><<<1, BN_THREADS, 0, c->stream>>>(m->attn, nq, m->act, m->xsum, sb); }
-        QT(2) else QT(4) else QT(8) else return ti_fail(TI_ERR_INVALID, "bonsai: q width %d", nq);
-#undef QT
-        TI_LAUNCHED("k_bn_quant");
+#define MQ(E) if (eq <= E) { k_bn_merge_quant<E><<<1, BN_THREADS, 0, c->stream>>>(m->po, m->pml, m->dpos, nsplit, nq, chunk, m->attn, m->act, m->xsum, sb, C.max_ctx); }
+        MQ(2) else MQ(4) else MQ(8) else return ti_fail(TI_ERR_INVALID, "bonsai: q width %d", nq);
+#undef MQ
+        TI_LAUNCHED("k_bn_merge_quant");
         if (m->trace) {
             RC(bput(c, m, l, B_ATTN, m->attn));
             RC(bput(c, m, l, B_B_ACT, m->act));

@@ -144,6 +144,25 @@ __device__ __forceinline__ float ti_xor(float v, int o) {
 __device__ __forceinline__ uint32_t ti_xor(uint32_t v, int o) { return (uint32_t)ti_xor_i((int)v, o); }
 __device__ __forceinline__ int ti_xor(int v, int o) { return ti_xor_i(v, o); }
 
+// Whole-wave butterflies with the offsets spelled out (32, 16, 8, 4, 2, 1). A loop over the
+// offset is not always unrolled (inside an unrolled outer loop the compiler may keep it),
+// and ti_xor of a run-time offset is a chain of branches: these stay straight-line.
+__device__ __forceinline__ int ti_wave_sum_i(int v) {
+    v += ti_xor_i(v, 32); v += ti_xor_i(v, 16); v += ti_xor_i(v, 8);
+    v += ti_xor_i(v, 4); v += ti_xor_i(v, 2); v += ti_xor_i(v, 1);
+    return v;
+}
+__device__ __forceinline__ float ti_wave_sum(float v) {
+    v += ti_xor(v, 32); v += ti_xor(v, 16); v += ti_xor(v, 8);
+    v += ti_xor(v, 4); v += ti_xor(v, 2); v += ti_xor(v, 1);
+    return v;
+}
+__device__ __forceinline__ float ti_wave_max(float v) {
+    v = fmaxf(v, ti_xor(v, 32)); v = fmaxf(v, ti_xor(v, 16)); v = fmaxf(v, ti_xor(v, 8));
+    v = fmaxf(v, ti_xor(v, 4)); v = fmaxf(v, ti_xor(v, 2)); v = fmaxf(v, ti_xor(v, 1));
+    return v;
+}
+
 // Wavefront-64 butterfly sum over lanes that share the same (lane / width): pairs at
 // distance width/2 first, down to 1 (every lane of a segment ends with the same sum).
 template <int WIDTH>
