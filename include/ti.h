@@ -59,6 +59,13 @@ int ti_buf_alloc(ti_ctx* ctx, size_t bytes, void** dptr);
 int ti_buf_free(ti_ctx* ctx, void* dptr);
 int ti_buf_write(ti_ctx* ctx, void* dst, size_t off, const void* src, size_t bytes);       /* blocking H2D */
 int ti_buf_read(ti_ctx* ctx, const void* src, size_t off, void* dst, size_t bytes);        /* waits, D2H   */
+/* The mapAsync-style readback of the engine's staging buffers (engine/webgpu-engine.js:169-179,
+ * models/qwen3.js:4423): a stream-ordered D2H copy that returns at once; it has landed when
+ * an event recorded after it completes (ti_event_record + ti_event_wait). dst should be
+ * page-locked (ti_host_alloc) for the copy to be asynchronous. Refused during a capture. */
+int ti_buf_read_async(ti_ctx* ctx, const void* src, size_t off, void* dst, size_t bytes);
+int ti_host_alloc(size_t bytes, void** host_ptr);                                           /* pinned */
+int ti_host_free(void* host_ptr);
 int ti_buf_copy(ti_ctx* ctx, void* dst, size_t doff, const void* src, size_t soff, size_t bytes);
 int ti_buf_fill_u32(ti_ctx* ctx, void* dst, uint32_t value, size_t count);                 /* kernel fill  */
 int ti_sync(ti_ctx* ctx);
@@ -74,6 +81,10 @@ int ti_graph_destroy(ti_graph* g);
 int ti_event_record(ti_ctx* ctx, int slot);                          /* slot in [0, 64); inside a
                                                                         capture: a graph node */
 int ti_event_elapsed_ms(ti_ctx* ctx, int start_slot, int end_slot, float* ms);
+/* Waits for the last record of one slot, not the whole stream (the readback of one
+ * in-flight batch while later batches run). Callable from another thread than the
+ * context's owner, provided the slot is not re-recorded until it returns. */
+int ti_event_wait(ti_ctx* ctx, int slot);
 
 /* ---- int4 weights ---------------------------------------------------------- */
 /* quantizeInt4Bf16 (models/qwen3.js:3405-3426), run on the GPU, bit-exact. */
@@ -141,6 +152,11 @@ int ti_rmsnorm_lm_head_argmax(ti_ctx* ctx, const float* x, const uint16_t* norm_
  * 256-thread workgroup, larger N by its 64 x 256 two-stage pair (index 16394 beats 300).
  * Only logits above -3e38 are candidates; with none the token is 0. */
 int ti_argmax(ti_ctx* ctx, const float* logits, int N, uint32_t* tok_hist, int out_pos);
+/* gumbelNoise(logits, N, temp) (models/qwen3.js:2722-2740): logits[i] += temp * g_i with
+ * g_i = -log(-log(u_i)), u_i = ((pcg(i ^ seed * 2654435761) >> 8) + 0.5) / 2^24, in
+ * place; ti_argmax of the result samples softmax(logits / temp). `seed` is the already
+ * advanced seed of this step (the reference advances _rngSeed before each call). */
+int ti_gumbel_noise(ti_ctx* ctx, float* logits, int N, uint32_t seed, float temp);
 /* embedGather (models/qwen3.js:1663-1676): y[t] = f32(emb[ids[id_off+t]]), t < T. */
 int ti_embed(ti_ctx* ctx, const int32_t* ids, const uint16_t* emb, float* y, int T, int H, int id_off, int vocab);
 
@@ -349,7 +365,7 @@ typedef struct {
     float rope_theta, rms_eps;
     int max_ctx;      /* KV capacity in positions */
     int max_tokens;   /* largest T accepted by ti_qwen3_forward; <= 256 and max_tokens *
-                         n_heads <= 512 (the T-query attention's scratch) */
+                         n_heads <= 4096 (the T-query attention's rows) */
 } ti_qwen3_config;
 int ti_qwen3_create(ti_ctx* ctx, const ti_qwen3_config* cfg, ti_qwen3** out);
 int ti_qwen3_destroy(ti_ctx* ctx, ti_qwen3* m);
@@ -370,6 +386,18 @@ int ti_qwen3_forward(ti_ctx* ctx, ti_qwen3* m, const int32_t* ids, int T, int po
  * Reads nothing from the host, so it can be captured once and replayed per token. */
 int ti_qwen3_decode(ti_ctx* ctx, ti_qwen3* m);
 int ti_qwen3_set_pos(ti_ctx* ctx, ti_qwen3* m, int pos);
+/* forward(..., {temp}) (models/qwen3.js:4052, 4538-4567): the temperature of the following
+ * decode steps and forwards, read on the device (so one captured step serves any
+ * temperature); <= 0 is greedy (the default). With temp > 0 each step's lm_head adds
+ * temp * g to every logit (ti_gumbel_noise's g) before its argmax, with the seed
+ * s = 1664525 s + 1013904223 advanced once per sampled step, as the reference's
+ * _rngSeed (:2733-2737); the logits buffer keeps the logits without the noise.
+ * Stream-ordered, capturable. */
+int ti_qwen3_sampling(ti_ctx* ctx, ti_qwen3* m, float temperature);
+/* The seed stream's state: the last seed used (a new decoder holds 0x9E3779B9, the
+ * reference's initial _rngSeed). ti_qwen3_seed is stream-ordered; get waits. */
+int ti_qwen3_seed(ti_ctx* ctx, ti_qwen3* m, uint32_t state);
+int ti_qwen3_get_seed(ti_ctx* ctx, ti_qwen3* m, uint32_t* state);
 /* Parity trace (debug; no reference counterpart: it exposes the intermediate values the
  * reference's forward keeps in its own buffers, models/qwen3.js:3959-4049). With buf set,
  * every later ti_qwen3_decode / ti_qwen3_forward also copies into buf, per layer l, 13
@@ -389,6 +417,9 @@ int ti_qwen3_set_pos(ti_ctx* ctx, ti_qwen3* m, int pos);
 int ti_qwen3_trace(ti_qwen3* m, void* buf, size_t bytes);
 int ti_qwen3_write_tokens(ti_ctx* ctx, ti_qwen3* m, int from, int count, const int32_t* ids);
 int ti_qwen3_read_tokens(ti_ctx* ctx, ti_qwen3* m, int from, int count, int32_t* ids);
+/* The same read queued behind the steps already issued (decodeLoop's readU32Range,
+ * models/qwen3.js:4423), without waiting: see ti_buf_read_async. */
+int ti_qwen3_read_tokens_async(ti_ctx* ctx, ti_qwen3* m, int from, int count, int32_t* ids);
 /* T-query causal attention over the int8 KV cache (models/qwen3.js:2534-2577): query t
  * (positions pos0+t) attends keys [0, pos0+t]; qr/out are [T][nHq][hd]. */
 int ti_attn_causal_q8(ti_ctx* ctx, const float* qr, const uint32_t* kq, const float* ks,

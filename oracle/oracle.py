@@ -69,6 +69,9 @@ _sig("or_attn_causal_q8", None, [_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p])
 _sig("or_attn_causal_q8_kvheads", None, [_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _p])
 _sig("or_embed", None, [_p, _p, _i, _i, _p])
 _sig("or_argmax", _i, [_p, _i])
+_sig("or_pcg", C.c_uint32, [C.c_uint32])
+_sig("or_seed_next", C.c_uint32, [C.c_uint32])
+_sig("or_gumbel_noise", None, [_p, _i, C.c_uint32, _f])
 _sig("or_tern_pack", None, [_p, _i, _i, _p, _p])
 _sig("or_tern_quant_act_n2", _f, [_p, _i, _p, _p])
 _sig("or_tern_quant_act_wasm", _f, [_p, _i, _p, _p])
@@ -337,6 +340,24 @@ def embed(ids, emb, T, H):
 def argmax(logits):
     lg = _c(logits, np.float32)
     return int(_L.or_argmax(_ptr(lg), lg.size))
+
+
+SEED_INIT = 0x9E3779B9    # the reference's initial _rngSeed (models/qwen3.js:2733)
+
+
+def pcg(v):
+    return int(_L.or_pcg(int(v) & 0xFFFFFFFF))
+
+
+def seed_next(s):
+    return int(_L.or_seed_next(int(s) & 0xFFFFFFFF))
+
+
+def gumbel_noise(logits, seed, temp):
+    """logits + temp * Gumbel noise of the step's seed (a new array; f32 as the shader)."""
+    lg = np.array(logits, np.float32, copy=True)
+    _L.or_gumbel_noise(_ptr(lg), lg.size, int(seed) & 0xFFFFFFFF, float(temp))
+    return lg
 
 
 # ---- ternary ------------------------------------------------------------------------

@@ -468,6 +468,30 @@ void or_embed(const int32_t* ids, const uint16_t* emb, int T, int H, float* y) {
         for (int h = 0; h < H; h++) y[(size_t)t * H + h] = (float)or_f16_to_f32(emb[(size_t)ids[t] * H + h]);
 }
 
+/* pcg (models/qwen3.js:2725): the 32-bit PCG hash (one LCG step, then the random
+ * xorshift and multiply of PCG-RXS-M-XS). */
+uint32_t or_pcg(uint32_t v) {
+    uint32_t s = v * 747796405u + 2891336453u;
+    uint32_t w = ((s >> ((s >> 28u) + 4u)) ^ s) * 277803737u;
+    return (w >> 22u) ^ w;
+}
+
+/* the per-step seed update of gumbelNoise (models/qwen3.js:2735) */
+uint32_t or_seed_next(uint32_t s) { return s * 1664525u + 1013904223u; }
+
+/* GUMBEL_WGSL (models/qwen3.js:2722-2732), in f32 as the shader computes it:
+ * h = pcg(i ^ seed * 2654435761), u = (f32(h >> 8) + 0.5) / 2^24 (in (0, 1), exact),
+ * logits[i] = logits[i] + temp * (-log(-log(u))). */
+void or_gumbel_noise(float* logits, int N, uint32_t seed, float temp) {
+    for (int i = 0; i < N; i++) {
+        uint32_t h = or_pcg((uint32_t)i ^ (seed * 2654435761u));
+        float u = ((float)(h >> 8u) + 0.5f) / 16777216.0f;
+        float g = -logf(-logf(u));
+        float d = temp * g;
+        logits[i] = logits[i] + d;
+    }
+}
+
 /* The shared-memory tree of the argmax kernels over nthr per-thread (max, index) slots:
  * for s = nthr/2 .. 1, slot l < s takes slot l+s only if strictly greater
  * (models/qwen3.js:2642, 2664, 2677). Each thread's slot holds the first strict maximum

@@ -29,6 +29,10 @@
  *      known-answer tests (tern.rs:437-470); scalar vs dequant oracle rel<1e-5.
  *  or_attn_* : f64 softmax oracle, nsplit invariance, RoPE known-answer tests
  *      (native/crates/n2-core/src/ops.rs:169-214).
+ *  or_argmax : a numpy emulation of the reference's two-stage tree on random ties.
+ *  or_gumbel_noise, or_pcg : the reference's own self-test (models/qwen3.js:3198-3214:
+ *      P(5)/P(9) = e at T = 1 with its seed stream, T -> 0 greedy) on a larger sample,
+ *      the Gumbel mean and variance (Euler's gamma, pi^2/6), u uniform on (0, 1).
  */
 #ifndef TI_ORACLE_H
 #define TI_ORACLE_H
@@ -110,6 +114,11 @@ void or_attn_causal_q8_kvheads(const float* qr, const uint32_t* kq, const float*
 /* ---- decode-step glue ---------------------------------------------------- */
 void or_embed(const int32_t* ids, const uint16_t* emb_f16, int T, int H, float* y);
 int  or_argmax(const float* logits, int N);   /* the reference's one/two-stage trees, their tie order */
+/* Gumbel-max temperature sampling (models/qwen3.js:2713-2740): the PCG hash, the seed
+ * stream's step, and logits[i] += temp * -log(-log(u_i)) in f32 as the WGSL kernel. */
+uint32_t or_pcg(uint32_t v);
+uint32_t or_seed_next(uint32_t s);
+void or_gumbel_noise(float* logits, int N, uint32_t seed, float temp);
 
 /* ---- ternary (native/crates/n2-kernels/src/tern.rs) --------------- */
 void or_tern_pack(const float* w, int N, int K, uint8_t* codes, float* scales); /* tern.rs:131-160 */

@@ -35,6 +35,9 @@ SIGS = {
     "ti_buf_free": [_p, _p],
     "ti_buf_write": [_p, _p, _sz, _p, _sz],
     "ti_buf_read": [_p, _p, _sz, _p, _sz],
+    "ti_buf_read_async": [_p, _p, _sz, _p, _sz],
+    "ti_host_alloc": [_sz, C.POINTER(_p)],
+    "ti_host_free": [_p],
     "ti_buf_copy": [_p, _p, _sz, _p, _sz, _sz],
     "ti_buf_fill_u32": [_p, _p, _u32, _sz],
     "ti_sync": [_p],
@@ -44,6 +47,7 @@ SIGS = {
     "ti_graph_destroy": [_p],
     "ti_event_record": [_p, _i],
     "ti_event_elapsed_ms": [_p, _i, _i, C.POINTER(_f)],
+    "ti_event_wait": [_p, _i],
     "ti_quant_int4_bf16": [_p, _p, _p, _p, _i, _i],
     "ti_quant_act_q8": [_p, _p, _p, _p, _p, _i],
     "ti_quant_act_q8_t": [_p, _p, _p, _p, _i, _i],
@@ -59,6 +63,7 @@ SIGS = {
     "ti_rmsnorm_gateup_silu_q4": [_p, _p, _p, _f, _p, _p, _p, _p, _p, _i, _i, _p, _p],
     "ti_rmsnorm_lm_head_argmax": [_p, _p, _p, _f, _p, _p, _p, _i, _i, _p, _i],
     "ti_argmax": [_p, _p, _i, _p, _i],
+    "ti_gumbel_noise": [_p, _p, _i, C.c_uint32, _f],
     "ti_embed": [_p, _p, _p, _p, _i, _i, _i, _i],
     "ti_attn_step_q8": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _f, _f, _i, _p, _p],
     "ti_attn_prep_q8": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _f, _f],
@@ -86,9 +91,13 @@ SIGS = {
     "ti_qwen3_forward": [_p, _p, _p, _i, _i],
     "ti_qwen3_decode": [_p, _p],
     "ti_qwen3_set_pos": [_p, _p, _i],
+    "ti_qwen3_sampling": [_p, _p, _f],
+    "ti_qwen3_seed": [_p, _p, C.c_uint32],
+    "ti_qwen3_get_seed": [_p, _p, C.POINTER(C.c_uint32)],
     "ti_qwen3_trace": [_p, _p, _sz],
     "ti_qwen3_write_tokens": [_p, _p, _i, _i, _p],
     "ti_qwen3_read_tokens": [_p, _p, _i, _i, _p],
+    "ti_qwen3_read_tokens_async": [_p, _p, _i, _i, _p],
     "ti_attn_causal_q8": [_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i],
 }
 
@@ -333,6 +342,18 @@ class Qwen3:
 
     def set_pos(self, pos):
         check(lib().ti_qwen3_set_pos(self.ctx.h, self.h, pos))
+
+    def sampling(self, temperature):
+        """Temperature of the following steps (ti_qwen3_sampling); 0 is greedy."""
+        check(lib().ti_qwen3_sampling(self.ctx.h, self.h, float(temperature)))
+
+    def seed(self, state):
+        check(lib().ti_qwen3_seed(self.ctx.h, self.h, int(state) & 0xFFFFFFFF))
+
+    def get_seed(self):
+        v = C.c_uint32()
+        check(lib().ti_qwen3_get_seed(self.ctx.h, self.h, C.byref(v)))
+        return v.value
 
     def trace(self, buf):
         """Route the parity trace (ti_qwen3_trace) into the DevBuf `buf`; None stops it."""

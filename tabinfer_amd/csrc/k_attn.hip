@@ -647,12 +647,18 @@ int ti_attn_decode_launch(ti_ctx* c, const float* qr, const uint32_t* kq, const 
         ns_stride = nsplit;
     } else {
         int Smax = S + T - 1;
-        if (nsplit <= 0) nsplit = auto_nsplit(Smax, nKv);
+        if (nsplit <= 0) {
+            nsplit = auto_nsplit(Smax, nKv);
+            const long fit = TI_ATTN_ROWSPLITS / ((long)T * nHq > 0 ? (long)T * nHq : 1);
+            if (nsplit > fit) nsplit = fit > 0 ? (int)fit : 1;   // many query rows: fewer, longer splits
+        }
         per = (Smax + nsplit - 1) / nsplit;
         ns_stride = nsplit;
     }
     if (nsplit > TI_ATTN_SPLITS_MAX) return ti_fail(TI_ERR_INVALID, "ti_attn_decode_q8: %d splits > %d", nsplit, TI_ATTN_SPLITS_MAX);
     if ((long)T * nHq > TI_ATTN_ROWS_MAX) return ti_fail(TI_ERR_INVALID, "ti_attn_decode_q8: T*nHq = %d > %d", T * nHq, TI_ATTN_ROWS_MAX);
+    if ((long)T * nHq * nsplit > TI_ATTN_ROWSPLITS)
+        return ti_fail(TI_ERR_INVALID, "ti_attn_decode_q8: T*nHq*nsplit = %ld > %d", (long)T * nHq * nsplit, TI_ATTN_ROWSPLITS);
     int G = nHq / nKv;
     if (!dpos && T > 1 && hd == 128) {   // one pass over the keys for all T queries
         const int Smax = S + T - 1;
@@ -661,7 +667,10 @@ int ti_attn_decode_launch(ti_ctx* c, const float* qr, const uint32_t* kq, const 
         per2 = ((per2 + AM_KT - 1) / AM_KT) * AM_KT;
         if (per2 < AM_KT) per2 = AM_KT;
         int ns2 = (Smax + per2 - 1) / per2;
-        while (ns2 > TI_ATTN_SPLITS_MAX) { per2 += AM_KT; ns2 = (Smax + per2 - 1) / per2; }
+        while (ns2 > TI_ATTN_SPLITS_MAX || (long)ns2 * T * nHq > TI_ATTN_ROWSPLITS) {
+            per2 += AM_KT;
+            ns2 = (Smax + per2 - 1) / per2;
+        }
         AttnMArgs m = {qr, reinterpret_cast<const uint8_t*>(kq), ks, reinterpret_cast<const uint4*>(vq), vs,
                        c->attn_po, c->attn_ml, S, T, nHq, nKv, G, ns2, per2, ns2};
         dim3 g2(nKv * ns2, (G * T + AM_ROWS - 1) / AM_ROWS);

@@ -538,6 +538,8 @@ struct LmArgs {
     const float* rope_tab; // [cap][rope_hd] cos/sin rows; with rope_cur, the row of the new position
     float* rope_cur;       // is copied to rope_cur (the fused attention reads it at a fixed address)
     int rope_hd;
+    uint32_t* samp;        // sampling words (TI_SAMP_*) or null: temperature > 0 adds T g to every
+                           // logit before the argmax, and the last workgroup advances the seed
 };
 
 // argmax over the wave (value, then the reference's tie rank), left in every lane
@@ -630,6 +632,12 @@ __global__ __launch_bounds__(256) void k_lmhead(LmArgs a) {
     __syncthreads();
     float best_v = -3.0e38f;
     int best_i = 0x7fffffff;
+    float temp = 0.0f;
+    uint32_t seed = 0;
+    if (a.samp) {
+        temp = __uint_as_float(a.samp[TI_SAMP_TEMP]);
+        seed = ti_seed_next(a.samp[TI_SAMP_STATE]);
+    }
     if (active) {
         ActLimb act[GPL];
 #pragma unroll
@@ -647,6 +655,10 @@ __global__ __launch_bounds__(256) void k_lmhead(LmArgs a) {
             const long row = blk * (RPP * R) + sub + (long)(li / SPAN) * RPP;
             if ((li % SPAN) == 0 && row < a.N) {
                 if (a.logits) a.logits[row] = tot;
+                if (temp > 0.0f) {
+                    const float g = temp * ti_gumbel((uint32_t)row, seed);
+                    tot = tot + g;
+                }
                 ti_amx_take(best_v, best_i, tot, (int)row, a.N);
             }
         };
@@ -702,6 +714,7 @@ __global__ __launch_bounds__(256) void k_lmhead(LmArgs a) {
         if (pos >= 0 && pos < a.cap) {
             a.hist[pos + 1] = (uint32_t)ti_amx_result(vv, ii);
             if (a.dpos) *a.dpos = pos + 1;
+            if (temp > 0.0f) a.samp[TI_SAMP_STATE] = seed;   // every workgroup read the state before it arrived
             last_s = pos + 1;
         }
         __hip_atomic_store(a.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -844,7 +857,7 @@ int ti_fused_gateup_launch(ti_ctx* c, const float* x, const uint16_t* nw, float 
 
 int ti_fused_lmhead_launch(ti_ctx* c, const float* x, const uint16_t* nw, float eps, const uint32_t* pack,
                            const uint16_t* sc, float* logits, int N, int K, uint32_t* hist, int* dpos, int out_pos,
-                           int cap, const float* rope_tab, float* rope_cur, int rope_hd) {
+                           int cap, const float* rope_tab, float* rope_cur, int rope_hd, uint32_t* samp) {
     if (K % 32 != 0 || K > LM_KMAX || K <= 0)
         return ti_fail(TI_ERR_INVALID, "lm_head: K=%d must be a positive multiple of 32 and <= %d", K, LM_KMAX);
     LmArgs a = {};
@@ -866,6 +879,7 @@ int ti_fused_lmhead_launch(ti_ctx* c, const float* x, const uint16_t* nw, float 
     a.rope_tab = rope_tab;
     a.rope_cur = rope_cur;
     a.rope_hd = rope_hd;
+    a.samp = samp;
     if (rope_cur && (!rope_tab || rope_hd <= 0 || rope_hd > 256))
         return ti_fail(TI_ERR_INVALID, "lm_head: bad rope row arguments");
     Shape s = fshape(K / 32);
@@ -930,5 +944,5 @@ extern "C" int ti_rmsnorm_lm_head_argmax(ti_ctx* c, const float* x, const uint16
     TI_REQUIRE(out_pos >= 1, "ti_rmsnorm_lm_head_argmax: out_pos must be >= 1");
     TI_REQUIRE(al16(x) && al16(pack), "ti_rmsnorm_lm_head_argmax: x and pack must be 16-byte aligned");
     return ti_fused_lmhead_launch(c, x, norm_w, eps, pack, scales, logits, N, K, tok_hist, nullptr, out_pos, out_pos,
-                                  nullptr, nullptr, 0);
+                                  nullptr, nullptr, 0, nullptr);
 }

@@ -46,12 +46,13 @@ struct ti_graph {
 };
 
 // Scratch capacities (elements). Activation rows up to 65536 wide, up to 256
-// tokens for the batched path; split-KV partials for up to 64 heads x 512 splits.
+// tokens for the batched path; split-KV partials for (query rows x splits) <= 512 x 512.
 #define TI_ACT_CAP 65536
 #define TI_ACT_TMAX 256
 #define TI_ATTN_HEADS_MAX 64
-#define TI_ATTN_ROWS_MAX 512      // T * nHq of one attention call
+#define TI_ATTN_ROWS_MAX 4096     // T * nHq of one attention call (a 256-token prefill of 16 heads)
 #define TI_ATTN_SPLITS_MAX 512
+#define TI_ATTN_ROWSPLITS (512 * 512)   // (T * nHq) x splits of one call: the partials' capacity
 #define TI_ATTN_HD_MAX 128
 #define TI_AMAX_PARTS 1024
 #define TI_MOE_P_MAX 8192
@@ -248,6 +249,29 @@ __device__ __forceinline__ void ti_amx_take(float& v, int& i, float v2, int i2, 
 }
 // the answer of a finished reduction
 __device__ __forceinline__ int ti_amx_result(float v, int i) { return v > -3.0e38f ? i : 0; }
+
+// ---- Gumbel-max temperature sampling (models/qwen3.js:2713-2740) -------------------
+// argmax(logit + T g), g = -log(-log(u)), is a sample of softmax(logits / T). u comes from
+// the PCG hash (the 32-bit pcg_hash of Jarzynski and Olano, "Hash Functions for GPU
+// Rendering", 2020) of the index mixed with the step's seed: 24 bits plus one half,
+// over 2^24, so u is in (0, 1) and exact in f32. The seed stream advances by the LCG
+// s' = 1664525 s + 1013904223 (mod 2^32) once per sampled step, before use.
+__host__ __device__ __forceinline__ uint32_t ti_pcg(uint32_t v) {
+    const uint32_t s = v * 747796405u + 2891336453u;
+    const uint32_t w = ((s >> ((s >> 28u) + 4u)) ^ s) * 277803737u;
+    return (w >> 22u) ^ w;
+}
+__host__ __device__ __forceinline__ uint32_t ti_seed_next(uint32_t s) { return s * 1664525u + 1013904223u; }
+__device__ __forceinline__ float ti_gumbel(uint32_t i, uint32_t seed) {
+    const uint32_t h = ti_pcg(i ^ (seed * 2654435761u));
+    const float u = ((float)(h >> 8u) + 0.5f) / 16777216.0f;
+    return -logf(-logf(u));
+}
+// the sampling words a decoder keeps on the device: [0] temperature (f32; <= 0: greedy),
+// [1] the seed stream's state (the last seed used)
+#define TI_SAMP_TEMP 0
+#define TI_SAMP_STATE 1
+#define TI_SEED_INIT 0x9E3779B9u
 
 // ---- cross-workgroup hand-off without cache maintenance ----------------------------
 // The "last workgroup finishes the reduction" kernels publish a few words per

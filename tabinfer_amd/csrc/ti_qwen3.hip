@@ -32,7 +32,7 @@ int ti_fused_linear_launch(ti_ctx*, const float*, const uint32_t*, const uint16_
 int ti_fused_gateup_launch(ti_ctx*, const float*, const uint16_t*, float, const uint32_t*, const uint16_t*,
                            const uint32_t*, const uint16_t*, float*, int, int, uint32_t*, float*);
 int ti_fused_lmhead_launch(ti_ctx*, const float*, const uint16_t*, float, const uint32_t*, const uint16_t*, float*, int,
-                           int, uint32_t*, int*, int, int, const float*, float*, int);
+                           int, uint32_t*, int*, int, int, const float*, float*, int, uint32_t*);
 int ti_fused_kmax(int lm);
 
 // ---------------------------------------------------------------------------
@@ -148,6 +148,7 @@ struct ti_qwen3 {
     float* psum;          // [16][256] RMSNorm partial sums of x (the T-token forward)
     uint32_t* hist;
     int* dpos;
+    uint32_t* samp;       // sampling words: temperature, seed state (TI_SAMP_*)
     float* rope;          // [max_ctx][head_dim] cos/sin rows of the rotary embedding
     float* rope_cur;      // the row of the device position (kept in step with dpos)
     float* amx_v;
@@ -281,6 +282,12 @@ extern "C" int ti_qwen3_create(ti_ctx* c, const ti_qwen3_config* cfg, ti_qwen3**
     if (!rc) rc = mk(m, (void**)&m->psum, 16 * 256 * 4);
     if (!rc) rc = mk(m, (void**)&m->hist, (size_t)(C.max_ctx + 1) * 4);
     if (!rc) rc = mk(m, (void**)&m->dpos, 4);
+    if (!rc) rc = mk(m, (void**)&m->samp, 2 * 4);
+    if (!rc) {
+        const uint32_t s0[2] = {0u, TI_SEED_INIT};   // greedy; the reference's first seed state
+        hipError_t e = hipMemcpy(m->samp, s0, sizeof(s0), hipMemcpyHostToDevice);
+        if (e != hipSuccess) rc = ti_hip_fail(e, "ti_qwen3_create sampling words");
+    }
     if (!rc) rc = mk(m, (void**)&m->rope, (size_t)C.max_ctx * hd * 4);
     if (!rc) rc = mk(m, (void**)&m->rope_cur, (size_t)hd * 4);
     if (!rc) {
@@ -385,6 +392,40 @@ extern "C" int ti_qwen3_set_pos(ti_ctx* c, ti_qwen3* m, int pos) {
     return TI_OK;
 }
 
+__global__ void k_set_word(uint32_t* __restrict__ dst, uint32_t v) {
+    if (threadIdx.x == 0) *dst = v;
+}
+
+// forward(..., {temp}) (models/qwen3.js:4052): the temperature of the following steps and
+// forwards (<= 0: greedy), read on the device, so a captured decode step samples at
+// whatever temperature was last set. Stream-ordered; may be captured.
+extern "C" int ti_qwen3_sampling(ti_ctx* c, ti_qwen3* m, float temperature) {
+    TI_CHECK_CTX(c);
+    TI_REQUIRE(m, "ti_qwen3_sampling: null model");
+    TI_REQUIRE(temperature == temperature, "ti_qwen3_sampling: temperature is NaN");
+    const float t = temperature > 0.0f ? temperature : 0.0f;
+    k_set_word<<<1, 64, 0, c->stream>>>(m->samp + TI_SAMP_TEMP, __builtin_bit_cast(uint32_t, t));
+    TI_LAUNCHED("k_set_word");
+    return TI_OK;
+}
+
+// The seed stream's state (_rngSeed, models/qwen3.js:2733): each sampled step first
+// advances it (s = 1664525 s + 1013904223) and samples with the result. A new decoder
+// starts at 0x9E3779B9, as the reference's module does.
+extern "C" int ti_qwen3_seed(ti_ctx* c, ti_qwen3* m, uint32_t state) {
+    TI_CHECK_CTX(c);
+    TI_REQUIRE(m, "ti_qwen3_seed: null model");
+    k_set_word<<<1, 64, 0, c->stream>>>(m->samp + TI_SAMP_STATE, state);
+    TI_LAUNCHED("k_set_word");
+    return TI_OK;
+}
+
+extern "C" int ti_qwen3_get_seed(ti_ctx* c, ti_qwen3* m, uint32_t* state) {
+    TI_CHECK_CTX(c);
+    TI_REQUIRE(m && state, "ti_qwen3_get_seed: null argument");
+    return ti_buf_read(c, m->samp, TI_SAMP_STATE * 4, state, 4);
+}
+
 extern "C" int ti_qwen3_write_tokens(ti_ctx* c, ti_qwen3* m, int from, int count, const int32_t* ids) {
     TI_CHECK_CTX(c);
     TI_REQUIRE(m && ids && from >= 0 && count >= 0 && from + count <= m->cfg.max_ctx + 1, "ti_qwen3_write_tokens: bad range");
@@ -395,6 +436,15 @@ extern "C" int ti_qwen3_read_tokens(ti_ctx* c, ti_qwen3* m, int from, int count,
     TI_CHECK_CTX(c);
     TI_REQUIRE(m && ids && from >= 0 && count >= 0 && from + count <= m->cfg.max_ctx + 1, "ti_qwen3_read_tokens: bad range");
     return ti_buf_read(c, m->hist, (size_t)from * 4, ids, (size_t)count * 4);
+}
+
+// readU32Range(_tokHist, from, count) as submitted in decodeLoop (models/qwen3.js:4423): the
+// copy is queued behind the steps already issued and does not wait
+extern "C" int ti_qwen3_read_tokens_async(ti_ctx* c, ti_qwen3* m, int from, int count, int32_t* ids) {
+    TI_CHECK_CTX(c);
+    TI_REQUIRE(m && ids && from >= 0 && count >= 0 && from + count <= m->cfg.max_ctx + 1,
+               "ti_qwen3_read_tokens_async: bad range");
+    return ti_buf_read_async(c, m->hist, (size_t)from * 4, ids, (size_t)count * 4);
 }
 
 // argmaxKernel (models/qwen3.js:2681-2690): tok_hist[out_pos] = argmax(logits[0..N)),
@@ -408,6 +458,25 @@ extern "C" int ti_argmax(ti_ctx* c, const float* logits, int N, uint32_t* tok_hi
     TI_LAUNCHED("k_argmax_p1");
     k_argmax_p2<<<1, AMX_PARTS, 0, c->stream>>>(c->amax_v, c->amax_i, N, tok_hist, out_pos, nullptr, 0);
     TI_LAUNCHED("k_argmax_p2");
+    return TI_OK;
+}
+
+// gumbelNoise (models/qwen3.js:2722-2740): logits[i] += temp * (-log(-log(u_i))), u_i from
+// the PCG hash of i and `seed` (the caller advances the seed stream, as the reference's
+// host does before each sampled step); an argmax of the result is the sample.
+__global__ void k_gumbel(float* __restrict__ logits, int N, uint32_t seed, float temp) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= N) return;
+    const float g = temp * ti_gumbel((uint32_t)i, seed);
+    logits[i] = logits[i] + g;
+}
+
+extern "C" int ti_gumbel_noise(ti_ctx* c, float* logits, int N, uint32_t seed, float temp) {
+    TI_CHECK_CTX(c);
+    TI_REQUIRE(logits && N > 0, "ti_gumbel_noise: need logits and N > 0 (N=%d)", N);
+    TI_REQUIRE(temp == temp, "ti_gumbel_noise: temperature is NaN");
+    k_gumbel<<<(unsigned)((N + 255) / 256), 256, 0, c->stream>>>(logits, N, seed, temp);
+    TI_LAUNCHED("k_gumbel");
     return TI_OK;
 }
 
@@ -472,7 +541,7 @@ extern "C" int ti_qwen3_decode(ti_ctx* c, ti_qwen3* m) {
     }
     RC(trace_put(c, m, C.layers, TR_X_IN, m->x, 1));
     RC(ti_fused_lmhead_launch(c, m->x, m->final_norm, C.rms_eps, m->lm.pack, m->lm.sc, m->logits, C.vocab, H, m->hist,
-                              m->dpos, 0, C.max_ctx, m->rope, m->rope_cur, hd));
+                              m->dpos, 0, C.max_ctx, m->rope, m->rope_cur, hd, m->samp));
     return TI_OK;
 }
 
@@ -577,7 +646,7 @@ extern "C" int ti_qwen3_forward(ti_ctx* c, ti_qwen3* m, const int32_t* ids, int 
     k_copy_f32<<<(H + 255) / 256, 256, 0, c->stream>>>(m->x + (size_t)(T - 1) * H, m->last, H);
     TI_LAUNCHED("k_copy_f32");
     RC(ti_fused_lmhead_launch(c, m->last, m->final_norm, C.rms_eps, m->lm.pack, m->lm.sc, m->logits, C.vocab, H, m->hist,
-                              nullptr, pos + T, C.max_ctx, nullptr, nullptr, 0));
+                              nullptr, pos + T, C.max_ctx, nullptr, nullptr, 0, m->samp));
     k_set_pos<<<1, 256, 0, c->stream>>>(m->dpos, pos + T, m->rope, m->rope_cur, hd, C.max_ctx);
     TI_LAUNCHED("k_set_pos");
     return TI_OK;

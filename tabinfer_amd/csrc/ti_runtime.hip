@@ -75,8 +75,8 @@ extern "C" int ti_init(int device, ti_ctx** out) {
         {(void**)&c->act_q, (size_t)TI_ACT_CAP * TI_ACT_TMAX},
         {(void**)&c->act_s, (size_t)TI_ACT_CAP / 32 * TI_ACT_TMAX * 4},
         {(void**)&c->act_sum, (size_t)TI_ACT_CAP / 16 * 4},
-        {(void**)&c->attn_po, (size_t)TI_ATTN_ROWS_MAX * TI_ATTN_SPLITS_MAX * TI_ATTN_HD_MAX * 4},
-        {(void**)&c->attn_ml, (size_t)TI_ATTN_ROWS_MAX * TI_ATTN_SPLITS_MAX * 2 * 4},
+        {(void**)&c->attn_po, (size_t)TI_ATTN_ROWSPLITS * TI_ATTN_HD_MAX * 4},
+        {(void**)&c->attn_ml, (size_t)TI_ATTN_ROWSPLITS * 2 * 4},
         {(void**)&c->amax_v, (size_t)TI_AMAX_PARTS * 4},
         {(void**)&c->amax_i, (size_t)TI_AMAX_PARTS * 4},
         {(void**)&c->moe_cnt, (size_t)TI_MOE_E_MAX * 4},
@@ -145,6 +145,31 @@ extern "C" int ti_buf_read(ti_ctx* c, const void* src, size_t off, void* dst, si
     TI_HIP(hipSetDevice(c->device));
     TI_HIP(hipMemcpyAsync(dst, (const char*)src + off, bytes, hipMemcpyDeviceToHost, c->stream));
     TI_HIP(hipStreamSynchronize(c->stream));
+    return TI_OK;
+}
+
+// Stream-ordered device -> host copy that does not wait: complete once the work issued
+// before it is (ti_event_record after it, then ti_event_wait). dst should be pinned
+// (ti_host_alloc) for the copy to run asynchronously.
+extern "C" int ti_buf_read_async(ti_ctx* c, const void* src, size_t off, void* dst, size_t bytes) {
+    TI_CHECK_CTX(c);
+    TI_REQUIRE(src && dst, "ti_buf_read_async: null buffer");
+    TI_REQUIRE(!c->capturing, "ti_buf_read_async: not during graph capture");
+    if (!bytes) return TI_OK;
+    TI_HIP(hipMemcpyAsync(dst, static_cast<const char*>(src) + off, bytes, hipMemcpyDeviceToHost, c->stream));
+    return TI_OK;
+}
+
+// page-locked host memory (hipHostMalloc), the target of asynchronous reads
+extern "C" int ti_host_alloc(size_t bytes, void** out) {
+    TI_REQUIRE(out && bytes > 0, "ti_host_alloc: need bytes > 0 and an output pointer");
+    *out = nullptr;
+    TI_HIP(hipHostMalloc(out, bytes, hipHostMallocDefault));
+    return TI_OK;
+}
+
+extern "C" int ti_host_free(void* p) {
+    if (p) TI_HIP(hipHostFree(p));
     return TI_OK;
 }
 
@@ -217,6 +242,16 @@ extern "C" int ti_event_record(ti_ctx* c, int slot) {
     // event), so every replay timestamps the point where it sits between the kernels
     if (c->capturing) TI_HIP(hipEventRecordWithFlags(c->ev[slot], c->stream, hipEventRecordExternal));
     else TI_HIP(hipEventRecord(c->ev[slot], c->stream));
+    return TI_OK;
+}
+
+// Waits for the last record of one slot (not the whole stream), so a host can consume an
+// early batch while later ones run. May run on another thread than the context's owner,
+// provided nothing re-records the slot until it returns.
+extern "C" int ti_event_wait(ti_ctx* c, int slot) {
+    TI_CHECK_CTX(c);
+    TI_REQUIRE(slot >= 0 && slot < 64, "ti_event_wait: slot %d out of [0,64)", slot);
+    TI_HIP(hipEventSynchronize(c->ev[slot]));
     return TI_OK;
 }
 

@@ -18,9 +18,11 @@ const CONFIGS = {
   '0.6B': { layers: 28, hidden: 1024, intermediate: 3072, n_heads: 16, n_kv_heads: 8, head_dim: 128, vocab: 151936 },
   '1.7B': { layers: 28, hidden: 2048, intermediate: 6144, n_heads: 16, n_kv_heads: 8, head_dim: 128, vocab: 151936 },
 };
-const GEN_BATCH = 32;        // decode steps per readback (models/qwen3.js:4416)
+const GEN_BATCH = 32;        // decode steps per readback (models/qwen3.js:4535)
+const PIPE_DEPTH = 3;        // batches in flight, so the GPU never waits for a readback (:4537)
+const PIPE_SLOT0 = 56;       // event slots PIPE_SLOT0 .. + PIPE_DEPTH - 1 mark the batches' readbacks
 const PREFILL_CHUNK = 256;   // prefill tokens per forward (models/qwen3.js:5250) ...
-const ATTN_ROWS = 512;       // ... within the library's T * n_heads <= 512 (ti_qwen3_config)
+const ATTN_ROWS = 4096;      // ... within the library's T * n_heads <= 4096 (ti_qwen3_config)
 const STAGE_BYTES = 64 << 20;
 
 // ---- safetensors ----------------------------------------------------------------------------
@@ -71,6 +73,33 @@ function toF16Bits(t, buf) {
     return out;
   }
   throw new Error('unsupported dtype ' + t.dtype);
+}
+
+// toolPreamble (:5294-5320): Qwen3's own (Hermes) tool block, appended to the system prompt,
+// the text its chat template renders (the model was trained on exactly this wording)
+function toolPreamble(tools) {
+  const fns = (tools || []).filter((t) => t && t.type === 'function' && t.function);
+  if (!fns.length) return '';
+  const sigs = fns.map((t) => JSON.stringify({ type: 'function', function: t.function })).join('\n');
+  return ['# Tools', '', 'You may call one or more functions to assist with the user query.', '',
+    'You are provided with function signatures within <tools></tools> XML tags:', '<tools>', sigs, '</tools>', '',
+    'For each function call, return a json object with function name and arguments within <tool_call></tool_call> XML tags:',
+    '<tool_call>', '{"name": <function-name>, "arguments": <args-json-object>}', '</tool_call>'].join('\n');
+}
+
+// every message as plain text for the encoder (:5429-5441): assistant tool calls as
+// <tool_call> blocks, tool results as <tool_response> user turns, text parts joined
+function renderMessage(m) {
+  let c = m.content;
+  if (Array.isArray(c)) c = c.filter((p) => p && p.type === 'text').map((p) => p.text || '').join('\n');
+  c = c == null ? '' : String(c);
+  if (m.role === 'tool') return { role: 'user', content: '<tool_response>\n' + c + '\n</tool_response>' };
+  if (m.role === 'assistant' && Array.isArray(m.tool_calls) && m.tool_calls.length) {
+    const tc = m.tool_calls.map((t) => '<tool_call>\n{"name": "' + ((t.function && t.function.name) || '') + '", "arguments": ' +
+      ((t.function && t.function.arguments) || '{}') + '}\n</tool_call>').join('\n');
+    c = c ? c + '\n' + tc : tc;
+  }
+  return { role: m.role, content: c };
 }
 
 // ---- the model ----------------------------------------------------------------------------------
@@ -180,6 +209,7 @@ function createQwen3Host({ device = 0 } = {}) {
     const chunk = Math.max(1, Math.min(PREFILL_CHUNK, Math.floor(ATTN_ROWS / base.n_heads), maxCtx));
     C = Object.assign({ rope_theta: 1e6, rms_eps: 1e-6 }, base, { max_ctx: maxCtx, max_tokens: chunk });
     M = TI.qwen3_create(ctx, C);
+    _temp = 0;                           // a new decoder samples greedily until told otherwise
     TOK = opts.tokenizer || null;
     if (opts.safetensors) loadWeights([].concat(opts.safetensors), opts.onProgress);
     else if (opts.random != null) randomWeights(opts.random);
@@ -189,10 +219,14 @@ function createQwen3Host({ device = 0 } = {}) {
 
   function unload() {
     if (_decodeGraph) { E.destroyGraph(_decodeGraph); _decodeGraph = null; }
+    if (_pipe) { E.sync(); for (const b of _pipe) TI.host_free(b.buffer); _pipe = null; }
     if (M) { TI.qwen3_destroy(M); M = null; }
   }
 
   function need() { if (!M) throw new Error('no model loaded: call loadModel() first'); }
+  // the decoder's sampling temperature (device-side, read by every step; 0 = greedy)
+  let _temp = 0;
+  function setTemp(t) { if (t !== _temp) { TI.qwen3_sampling(ctx, M, t); _temp = t; } }
   function setPos(pos) { if (_devPos !== pos) { TI.qwen3_set_pos(ctx, M, pos); _devPos = pos; } }
   function readTok(pos) { return TI.qwen3_read_tokens(ctx, M, pos, 1)[0]; }
 
@@ -215,7 +249,7 @@ function createQwen3Host({ device = 0 } = {}) {
   async function forward(idsArray, posBase, opts) {
     need();
     const chain = !!(opts && opts.chain), submitOnly = !!(opts && opts.submitOnly);
-    if (opts && opts.temp > 0) throw new Error('forward: sampling (temp > 0) is not part of this path; the decode step is argmax');
+    setTemp(opts && opts.temp > 0 ? +opts.temp : 0);   // :4052, Gumbel-max in the lm_head
     let T;
     if (chain) {
       T = 1;
@@ -243,21 +277,43 @@ function createQwen3Host({ device = 0 } = {}) {
     return _decodeGraph;
   }
 
-  // decodeLoop (:4414-4435): GEN_BATCH graph replays of the device-position step, then one
-  // readback of the tokens they chained; stops on emitTok() === false, maxTokens or the cache end
-  async function decodeLoop(pos, maxTokens, emitTok, signal, count) {
+  // decodeLoop (:4414-4435): batches of GEN_BATCH graph replays of the device-position step,
+  // each followed by a queued readback of the tokens it chained; PIPE_DEPTH batches stay in
+  // flight, and the host consumes the oldest while the GPU runs the newer ones. Stops on
+  // emitTok() === false, maxTokens or the cache end; batches still in flight then run out
+  // (as the reference's discarded batches do) before their buffers are reused.
+  let _pipe = null;
+  async function decodeLoop(pos, maxTokens, emitTok, signal, count, temp) {
     const g = decodeGraph();
-    for (;;) {
-      if (signal && signal.aborted) return;
-      const K = Math.min(GEN_BATCH, C.max_ctx - 1 - pos, maxTokens - count());
-      if (K <= 0) return;
-      setPos(pos);
+    if (!_pipe) _pipe = Array.from({ length: PIPE_DEPTH }, () => new Int32Array(TI.host_alloc(GEN_BATCH * 4)));
+    setTemp(temp > 0 ? +temp : 0);
+    setPos(pos);
+    let submitted = 0, seq = 0;
+    const submitBatch = () => {
+      if (signal && signal.aborted) return null;
+      const K = Math.min(GEN_BATCH, C.max_ctx - 1 - pos, maxTokens + GEN_BATCH - submitted);
+      if (K <= 0) return null;
+      const base = pos, i = seq++ % PIPE_DEPTH;
       for (let k = 0; k < K; k++) E.launch(g);
-      _devPos = pos + K;
-      await E.drain();
-      const toks = TI.qwen3_read_tokens(ctx, M, pos + 1, K);
-      pos += K;
-      for (let k = 0; k < K; k++) if (!emitTok(toks[k]) || count() >= maxTokens) return;
+      pos += K; submitted += K; _devPos = pos;
+      TI.qwen3_read_tokens_async(ctx, M, base + 1, K, _pipe[i]);
+      TI.event_record(ctx, PIPE_SLOT0 + i);
+      return { K, buf: _pipe[i], done: TI.event_wait_async(ctx, PIPE_SLOT0 + i) };
+    };
+    const inflight = [];
+    try {
+      while (inflight.length < PIPE_DEPTH) { const b = submitBatch(); if (!b) break; inflight.push(b); }
+      while (inflight.length) {
+        const cur = inflight.shift();
+        await cur.done;
+        const toks = cur.buf.slice(0, cur.K);              // copied out before the buffer is reused
+        let stop = !!(signal && signal.aborted);
+        if (!stop) for (let k = 0; k < cur.K; k++) { if (!emitTok(toks[k]) || count() >= maxTokens) { stop = true; break; } }
+        if (stop) break;
+        const b = submitBatch(); if (b) inflight.push(b);
+      }
+    } finally {
+      for (const b of inflight) await b.done.catch(() => {});
     }
   }
 
@@ -269,12 +325,14 @@ function createQwen3Host({ device = 0 } = {}) {
   const decode = (ids) => (TOK ? TOK.decode(ids) : ids.slice());
   const isStop = (t) => !!(TOK && TOK.isStop && TOK.isStop(t));
 
-  // prefill ids[from..L) in chunks of up to PREFILL_CHUNK (C.max_tokens); returns the token after the last
-  async function prefill(ids, from, signal) {
+  // prefill ids[from..L) in chunks of up to PREFILL_CHUNK (C.max_tokens); returns the token
+  // after the last; a temperature applies to the last chunk's token only (:4553-4556)
+  async function prefill(ids, from, signal, temp) {
     let tok;
     for (let off = from; off < ids.length; off += C.max_tokens) {
       if (signal && signal.aborted) throw abortError();
-      tok = await forward(ids.slice(off, Math.min(off + C.max_tokens, ids.length)), off);
+      const last = off + C.max_tokens >= ids.length;
+      tok = await forward(ids.slice(off, Math.min(off + C.max_tokens, ids.length)), off, last && temp ? { temp } : undefined);
     }
     return tok;
   }
@@ -288,13 +346,13 @@ function createQwen3Host({ device = 0 } = {}) {
   // generate(prompt, {maxTokens, onToken, onStats, signal}) (:4538-4569)
   async function generate(prompt, { maxTokens = 64, onToken, onStats, signal, temperature } = {}) {
     need();
-    if (temperature > 0) throw new Error('generate: sampling is not part of this path (argmax decode only)');
+    const temp = temperature > 0 ? +temperature : 0;
     _cachedIds = null;
     const ids = encode(prompt);
     const L = ids.length;
     checkFits(L);
     const t0 = Date.now();
-    const tok0 = await prefill(ids, 0, signal);
+    const tok0 = await prefill(ids, 0, signal, temp);
     const ms = Date.now() - t0;
     _lastGenStats = { prefillTokens: L, prefillMs: ms, prefillTps: +(L / Math.max(ms, 1e-3) * 1000).toFixed(1) };
     if (onStats) { try { onStats(_lastGenStats); } catch (_) { /* caller's hook */ } }
@@ -305,7 +363,7 @@ function createQwen3Host({ device = 0 } = {}) {
       if (onToken) { try { onToken(TOK ? TOK.decode([t]) : t); } catch (_) { /* caller's hook */ } }
       return true;
     };
-    if (emit(tok0)) await decodeLoop(L, maxTokens, emit, signal, () => out.length);
+    if (emit(tok0)) await decodeLoop(L, maxTokens, emit, signal, () => out.length, temp);
     return decode(out);
   }
 
@@ -343,16 +401,17 @@ function createQwen3Host({ device = 0 } = {}) {
 
   // _streamIds (:5199-5292) without grammar masking: prefix-cache reuse, chunked prefill of
   // the rest, then the batched decode loop
-  async function streamIds(ids, { maxTokens, onToken, signal }) {
+  async function streamIds(ids, { maxTokens, onToken, signal, temperature }) {
+    const temp = temperature > 0 ? +temperature : 0;
     const L = ids.length;
     checkFits(L);
     let lcp = 0;
     if (_cachedIds) { const n = Math.min(_cachedIds.length, L - 1); while (lcp < n && _cachedIds[lcp] === ids[lcp]) lcp++; }
     _cachedIds = null;   // from here on rows lcp.. are being overwritten
-    const tok0 = await prefill(ids, lcp, signal);
+    const tok0 = await prefill(ids, lcp, signal, temp);
     const out = [];
     const emitTok = (t) => { if (isStop(t)) return false; out.push(t); if (onToken) onToken(TOK ? TOK.decode([t]) : String(t)); return true; };
-    if (emitTok(tok0)) await decodeLoop(L, maxTokens, emitTok, signal, () => out.length);
+    if (emitTok(tok0)) await decodeLoop(L, maxTokens, emitTok, signal, () => out.length, temp);
     // Rows [0, L) hold the prompt. The step at position L + j wrote the row of out[j] and
     // produced out[j + 1], so rows exist for out[0 .. n-2]; the last emitted token's row
     // is written only if a later step ran, which a stop at maxTokens or the cache end skips.
@@ -360,7 +419,8 @@ function createQwen3Host({ device = 0 } = {}) {
     return out;
   }
 
-  // runConversation({provider, messages, systemPrompt, tools, convId, signal}, emit) (:5397-5522)
+  // runConversation({provider, messages, systemPrompt, tools, convId, signal}, emit) (:5397-5522):
+  // rounds of prefill + decode with the event stream; tool calls run through setToolRunner
   async function runConversation({ provider, messages, systemPrompt, tools, convId, signal } = {}, emit) {
     try {
       if (!M) throw new Error('no model loaded: call loadModel() first');
@@ -371,48 +431,69 @@ function createQwen3Host({ device = 0 } = {}) {
       return;
     }
     const maxTokens = (provider && (provider.maxTokens | 0)) || C.max_ctx;
-    const sys = (systemPrompt && typeof systemPrompt === 'object') ? (systemPrompt.content || '') : (systemPrompt || '');
+    let sys = (systemPrompt && typeof systemPrompt === 'object') ? (systemPrompt.content || '') : (systemPrompt || '');
     const toolList = (Array.isArray(tools) ? tools : []).filter((t) => t && t.type === 'function');
+    const pre = toolPreamble(toolList);
+    if (pre) sys = sys ? sys + '\n\n' + pre : pre;
     const work = [];
     if (sys) work.push({ role: 'system', content: sys });
-    for (const m of (messages || [])) if (m && m.role) work.push({ role: m.role === 'tool' ? 'user' : m.role, content: m.role === 'tool' ? '<tool_response>\n' + m.content + '\n</tool_response>' : String(m.content == null ? '' : m.content) });
-    const MAX_ROUNDS = toolList.length && _toolRunner ? 8 : 1;
+    for (const m of (messages || [])) if (m && m.role) work.push(renderMessage(m));
+    const MAX_ROUNDS = toolList.length ? 8 : 1;
     try {
       for (let round = 0; round < MAX_ROUNDS; round++) {
         if (signal && signal.aborted) throw abortError();
         emit({ type: 'round_start' });
-        const parser = makeRoundParser((rz) => emit({ type: 'delta', delta: { reasoning: rz } }),
-          (ct) => emit({ type: 'delta', delta: { content: ct } }));
+        let firstTok = false;
+        const clearInfo = () => { if (!firstTok) { firstTok = true; emit({ type: 'info', message: null }); } };
+        const parser = makeRoundParser((rz) => { clearInfo(); emit({ type: 'delta', delta: { reasoning: rz } }); },
+          (ct) => { clearInfo(); emit({ type: 'delta', delta: { content: ct } }); });
         const ids = TOK.encodeChat(work);
         await streamIds(ids, { maxTokens, signal, onToken: (t) => parser.push(t) });
         parser.flush();
-        const content = parser.content.replace(/^\s+/, '');
+        if (signal && signal.aborted) throw abortError();
+        emit({ type: 'info', message: null });
+        let content = parser.content.replace(/^\s+/, '');
         const toolCalls = [];
         parser.toolCalls.forEach((raw, k) => {
           try { const o = JSON.parse(raw); if (o && o.name) toolCalls.push({ id: 'call_' + round + '_' + k, type: 'function', function: { name: o.name, arguments: JSON.stringify(o.arguments || {}) } }); } catch (_) { /* not a call */ }
         });
-        if (toolCalls.length) emit({ type: 'delta', delta: { tool_calls: toolCalls.map((tc, i) => Object.assign({ index: i }, tc)) } });
+        // never a blank turn (:5474-5486): no answer and no call means the budget ran out
+        if (!content && !toolCalls.length) {
+          const cutMidThink = parser.state === 'think' || parser.reasoning.length > 0;
+          content = cutMidThink
+            ? '⚠️ I ran out of room to answer: this conversation is near the model\'s context limit (' + C.max_ctx + ' tokens), so it used the remaining budget on reasoning and couldn\'t finish a reply. Start a new chat, remove a large earlier message (e.g. a long command output), or raise **Context size** in the provider settings.'
+            : '⚠️ The model produced no output. Try resending, or start a new chat if the history is very long.';
+          emit({ type: 'delta', delta: { content } });
+        }
+        if (toolCalls.length) emit({ type: 'delta', delta: { tool_calls: toolCalls.map((tc, i) => ({ index: i, id: tc.id, type: 'function', function: { name: tc.function.name, arguments: tc.function.arguments } })) } });
         emit({ type: 'round_end', content });
+        // usage as the reference reports it (:5488-5492): the exact prompt token count
         emit({ type: 'usage', usage: { prompt_tokens: ids.length, total_tokens: ids.length } });
         const asst = { role: 'assistant', content };
         if (toolCalls.length) asst.tool_calls = toolCalls;
         emit({ type: 'message_added', message: asst });
-        work.push({ role: 'assistant', content });
-        if (!toolCalls.length || !_toolRunner) break;
+        work.push(renderMessage(asst));
+        if (!toolCalls.length) break;
+        if (!_toolRunner) { emit({ type: 'info', message: null }); break; }
         for (const tc of toolCalls) {
+          if (signal && signal.aborted) throw abortError();
           emit({ type: 'tool_started', tc });
           let args = {};
           try { args = JSON.parse(tc.function.arguments || '{}'); } catch (_) { /* empty args */ }
           let res;
-          try { res = await _toolRunner(tc.function.name, args, convId, signal); } catch (e) { res = { result: 'Error: ' + ((e && e.message) || e) }; }
+          try { res = await _toolRunner(tc.function.name, args, convId, signal); } catch (e) {
+            if (e && e.name === 'AbortError') throw e;
+            res = { result: 'Error: ' + ((e && e.message) || e) };
+          }
           const text = res && res.result != null ? res.result : '';
-          emit({ type: 'tool_result', id: tc.id, result: text });
-          work.push({ role: 'user', content: '<tool_response>\n' + text + '\n</tool_response>' });
+          emit({ type: 'tool_result', id: tc.id, result: text, artifacts: res && res.artifacts });
+          work.push(renderMessage({ role: 'tool', tool_call_id: tc.id, content: text }));
           emit({ type: 'message_added', message: { role: 'tool', tool_call_id: tc.id, content: text } });
         }
       }
     } catch (e) {
       if (e && e.name === 'AbortError') throw e;
+      emit({ type: 'info', message: null });
       emit({ type: 'error', message: 'Qwen3 dense: ' + ((e && e.message) || e) });
     }
     emit({ type: 'agent_done' });
@@ -430,4 +511,5 @@ function createQwen3Host({ device = 0 } = {}) {
   };
 }
 
-module.exports = { createQwen3Host, CONFIGS, readSafetensorsHeader, GEN_BATCH, PREFILL_CHUNK };
+module.exports = { createQwen3Host, CONFIGS, readSafetensorsHeader, toolPreamble, renderMessage, GEN_BATCH, PIPE_DEPTH,
+  PREFILL_CHUNK };

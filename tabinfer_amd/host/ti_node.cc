@@ -19,7 +19,9 @@
 #include <cstdio>
 #include <cstring>
 #include <limits>
+#include <mutex>
 #include <string>
+#include <unordered_set>
 #include <tuple>
 #include <type_traits>
 #include <utility>
@@ -506,13 +508,14 @@ struct SyncWork {
     napi_async_work work = nullptr;
     napi_deferred deferred = nullptr;
     CtxH* ctx = nullptr;
+    int slot = -1;         // >= 0: wait for that event slot only (event_wait_async)
     int rc = 0;
     std::string err;
 };
 
 void sync_execute(napi_env, void* data) {
     SyncWork* w = static_cast<SyncWork*>(data);
-    w->rc = ti_sync(w->ctx->c);
+    w->rc = w->slot >= 0 ? ti_event_wait(w->ctx->c, w->slot) : ti_sync(w->ctx->c);
     if (w->rc) w->err = ti_last_error();
 }
 
@@ -545,6 +548,128 @@ napi_value js_sync_async(napi_env env, napi_callback_info info) {
     napi_create_async_work(env, nullptr, name, sync_execute, sync_complete, w, &w->work);
     napi_queue_async_work(env, w->work);
     return promise;
+}
+
+// event_wait_async(ctx, slot) -> Promise: resolves once the last record of the slot has
+// completed; the context's owner keeps issuing work meanwhile (the slot is not re-recorded
+// until the promise settles)
+napi_value js_event_wait_async(napi_env env, napi_callback_info info) {
+    Args a(env, info);
+    if (!want_args(env, a, 2, "event_wait_async")) return nullptr;
+    CtxH* c = get_ctx(env, a.v[0], "event_wait_async");
+    int64_t slot;
+    if (!c || !get_i64(env, a.v[1], &slot, "event_wait_async", 1)) return nullptr;
+    if (slot < 0 || slot >= 64) return throw_msg(env, "event_wait_async: slot out of [0, 64)");
+    SyncWork* w = new SyncWork;
+    w->ctx = c;
+    w->slot = (int)slot;
+    c->refs++;
+    napi_value promise, name;
+    napi_create_promise(env, &w->deferred, &promise);
+    napi_create_string_utf8(env, "ti_event_wait", NAPI_AUTO_LENGTH, &name);
+    napi_create_async_work(env, nullptr, name, sync_execute, sync_complete, w, &w->work);
+    napi_queue_async_work(env, w->work);
+    return promise;
+}
+
+// host_alloc(bytes) -> ArrayBuffer over page-locked memory, freed by host_free(ab) (which
+// detaches it) or with the ArrayBuffer; the live set keeps the two from freeing twice
+std::mutex g_pin_mu;
+std::unordered_set<void*> g_pinned;
+
+bool pin_release(void* p) {
+    std::lock_guard<std::mutex> lk(g_pin_mu);
+    return g_pinned.erase(p) > 0;
+}
+
+void fin_host(napi_env, void* data, void*) {
+    if (pin_release(data)) ti_host_free(data);
+}
+
+napi_value js_host_alloc(napi_env env, napi_callback_info info) {
+    Args a(env, info);
+    if (!want_args(env, a, 1, "host_alloc")) return nullptr;
+    int64_t bytes;
+    if (!get_i64(env, a.v[0], &bytes, "host_alloc", 0)) return nullptr;
+    if (bytes <= 0 || bytes > (int64_t(1) << 32)) return throw_msg(env, "host_alloc: bytes out of (0, 4 GiB]");
+    void* p = nullptr;
+    const int rc = ti_host_alloc((size_t)bytes, &p);
+    if (rc) return throw_ti(env, "host_alloc", rc);
+    {
+        std::lock_guard<std::mutex> lk(g_pin_mu);
+        g_pinned.insert(p);
+    }
+    napi_value ab;
+    if (napi_create_external_arraybuffer(env, p, (size_t)bytes, fin_host, nullptr, &ab) != napi_ok) {
+        if (pin_release(p)) ti_host_free(p);
+        return throw_msg(env, "host_alloc: cannot wrap the memory");
+    }
+    return ab;
+}
+
+// host_free(ab): frees a host_alloc ArrayBuffer now (it is detached: length 0 afterwards)
+napi_value js_host_free(napi_env env, napi_callback_info info) {
+    Args a(env, info);
+    if (!want_args(env, a, 1, "host_free")) return nullptr;
+    bool is_ab = false;
+    napi_is_arraybuffer(env, a.v[0], &is_ab);
+    if (!is_ab) return arg_error(env, "host_free", 0, "an ArrayBuffer from host_alloc"), nullptr;
+    void* data = nullptr;
+    size_t len = 0;
+    napi_get_arraybuffer_info(env, a.v[0], &data, &len);
+    if (!data || !pin_release(data)) return throw_msg(env, "host_free: not a live host_alloc buffer");
+    napi_detach_arraybuffer(env, a.v[0]);
+    const int rc = ti_host_free(data);
+    return rc ? throw_ti(env, "host_free", rc) : undefined(env);
+}
+
+// bytes of a TypedArray / ArrayBuffer argument (host memory)
+bool host_bytes(napi_env env, napi_value v, void** data, size_t* len) {
+    bool is = false;
+    napi_is_typedarray(env, v, &is);
+    if (is) {
+        napi_typedarray_type tt;
+        size_t n, off;
+        napi_value ab;
+        napi_get_typedarray_info(env, v, &tt, &n, data, &ab, &off);
+        size_t el = 1;
+        switch (tt) {
+            case napi_int16_array: case napi_uint16_array: el = 2; break;
+            case napi_int32_array: case napi_uint32_array: case napi_float32_array: el = 4; break;
+            case napi_float64_array: case napi_bigint64_array: case napi_biguint64_array: el = 8; break;
+            default: el = 1;
+        }
+        *len = n * el;
+        return true;
+    }
+    napi_is_arraybuffer(env, v, &is);
+    if (is) {
+        napi_get_arraybuffer_info(env, v, data, len);
+        return true;
+    }
+    return false;
+}
+
+// buf_read_async(ctx, buf, off, dst, bytes): queued D2H into dst (host_alloc memory), no wait
+napi_value js_buf_read_async(napi_env env, napi_callback_info info) {
+    const char* fn = "buf_read_async";
+    Args a(env, info);
+    if (!want_args(env, a, 5, fn)) return nullptr;
+    CtxH* c = get_ctx(env, a.v[0], fn);
+    void* src;
+    int64_t off, len;
+    if (!c || !get_dptr(env, a.v[1], &src, fn, 1) || !get_i64(env, a.v[2], &off, fn, 2) ||
+        !get_i64(env, a.v[4], &len, fn, 4))
+        return nullptr;
+    BufH* b = handle_of<BufH>(env, a.v[1], TAG_BUF);
+    if (!src || off < 0 || len < 0 || (size_t)off > b->bytes || (size_t)len > b->bytes - (size_t)off)
+        return throw_msg(env, "buf_read_async: outside the buffer");
+    void* dst;
+    size_t cap;
+    if (!host_bytes(env, a.v[3], &dst, &cap)) return arg_error(env, fn, 3, "a TypedArray or ArrayBuffer"), nullptr;
+    if ((size_t)len > cap) return throw_msg(env, "buf_read_async: the destination is too small");
+    const int rc = ti_buf_read_async(c->c, src, (size_t)off, dst, (size_t)len);
+    return rc ? throw_ti(env, fn, rc) : undefined(env);
 }
 
 napi_value js_graph_end(napi_env env, napi_callback_info info) {
@@ -866,6 +991,48 @@ napi_value js_qwen3_set_pos(napi_env env, napi_callback_info info) {
     if (!m || !get_i64(env, a.v[2], &pos, "qwen3_set_pos", 2)) return nullptr;
     const int rc = ti_qwen3_set_pos(c->c, m->m, (int)pos);
     return rc ? throw_ti(env, "qwen3_set_pos", rc) : undefined(env);
+}
+
+// qwen3_sampling(ctx, model, temperature): the temperature of the following steps (0: greedy)
+napi_value js_qwen3_sampling(napi_env env, napi_callback_info info) {
+    const char* fn = "qwen3_sampling";
+    Args a(env, info);
+    if (!want_args(env, a, 3, fn)) return nullptr;
+    CtxH* c = get_ctx(env, a.v[0], fn);
+    ModelH* m = c ? get_model(env, a.v[1], fn, 1) : nullptr;
+    double t;
+    if (!m) return nullptr;
+    if (napi_get_value_double(env, a.v[2], &t) != napi_ok) return arg_error(env, fn, 2, "a number"), nullptr;
+    const int rc = ti_qwen3_sampling(c->c, m->m, (float)t);
+    return rc ? throw_ti(env, fn, rc) : undefined(env);
+}
+
+// qwen3_seed(ctx, model, state) / qwen3_get_seed(ctx, model) -> state: the seed stream
+napi_value js_qwen3_seed(napi_env env, napi_callback_info info) {
+    const char* fn = "qwen3_seed";
+    Args a(env, info);
+    if (!want_args(env, a, 3, fn)) return nullptr;
+    CtxH* c = get_ctx(env, a.v[0], fn);
+    ModelH* m = c ? get_model(env, a.v[1], fn, 1) : nullptr;
+    int64_t st;
+    if (!m || !get_i64(env, a.v[2], &st, fn, 2)) return nullptr;
+    const int rc = ti_qwen3_seed(c->c, m->m, (uint32_t)(st & 0xFFFFFFFF));
+    return rc ? throw_ti(env, fn, rc) : undefined(env);
+}
+
+napi_value js_qwen3_get_seed(napi_env env, napi_callback_info info) {
+    const char* fn = "qwen3_get_seed";
+    Args a(env, info);
+    if (!want_args(env, a, 2, fn)) return nullptr;
+    CtxH* c = get_ctx(env, a.v[0], fn);
+    ModelH* m = c ? get_model(env, a.v[1], fn, 1) : nullptr;
+    if (!m) return nullptr;
+    uint32_t st = 0;
+    const int rc = ti_qwen3_get_seed(c->c, m->m, &st);
+    if (rc) return throw_ti(env, fn, rc);
+    napi_value out;
+    napi_create_uint32(env, st, &out);
+    return out;
 }
 
 // qwen3_trace(model, buffer | null): parity trace of the decoder's intermediate values
@@ -1228,6 +1395,31 @@ napi_value js_bonsai_trace(napi_env env, napi_callback_info info) {
     return rc ? throw_ti(env, "bonsai_trace", rc) : undefined(env);
 }
 
+// qwen3_read_tokens_async(ctx, model, from, count, int32array): queued D2H of the token
+// history into the array (from host_alloc); complete once an event recorded after it is
+napi_value js_qwen3_read_tokens_async(napi_env env, napi_callback_info info) {
+    const char* fn = "qwen3_read_tokens_async";
+    Args a(env, info);
+    if (!want_args(env, a, 5, fn)) return nullptr;
+    CtxH* c = get_ctx(env, a.v[0], fn);
+    ModelH* m = c ? get_model(env, a.v[1], fn, 1) : nullptr;
+    int64_t from, count;
+    if (!m || !get_i64(env, a.v[2], &from, fn, 2) || !get_i64(env, a.v[3], &count, fn, 3)) return nullptr;
+    bool is_ta = false;
+    napi_is_typedarray(env, a.v[4], &is_ta);
+    if (!is_ta) return arg_error(env, fn, 4, "an Int32Array"), nullptr;
+    napi_typedarray_type tt;
+    size_t len;
+    void* data;
+    napi_value ab;
+    size_t boff;
+    napi_get_typedarray_info(env, a.v[4], &tt, &len, &data, &ab, &boff);
+    if (tt != napi_int32_array) return arg_error(env, fn, 4, "an Int32Array"), nullptr;
+    if (count < 0 || (size_t)count > len) return throw_msg(env, "qwen3_read_tokens_async: count exceeds the array");
+    const int rc = ti_qwen3_read_tokens_async(c->c, m->m, (int)from, (int)count, static_cast<int32_t*>(data));
+    return rc ? throw_ti(env, fn, rc) : undefined(env);
+}
+
 napi_value js_qwen3_read_tokens(napi_env env, napi_callback_info info) {
     const char* fn = "qwen3_read_tokens";
     Args a(env, info);
@@ -1268,12 +1460,17 @@ napi_value module_init(napi_env env, napi_value exports) {
         ENTRY("buf_fill_u32", ti_buf_fill_u32),
         ENTRY("sync", ti_sync),
         FN("sync_async", js_sync_async),
+        FN("event_wait_async", js_event_wait_async),
+        FN("host_alloc", js_host_alloc),
+        FN("host_free", js_host_free),
+        FN("buf_read_async", js_buf_read_async),
         ENTRY("graph_begin", ti_graph_begin),
         FN("graph_end", js_graph_end),
         FN("graph_launch", js_graph_launch),
         FN("graph_destroy", js_graph_destroy),
         ENTRY("event_record", ti_event_record),
         FN("event_elapsed_ms", js_event_elapsed_ms),
+        ENTRY("event_wait", ti_event_wait),
         // int4 weights, activations, GEMV / GEMM
         ENTRY("quant_int4_bf16", ti_quant_int4_bf16),
         ENTRY("quant_act_q8", ti_quant_act_q8),
@@ -1290,6 +1487,7 @@ napi_value module_init(napi_env env, napi_value exports) {
         ENTRY("rmsnorm_gateup_silu_q4", ti_rmsnorm_gateup_silu_q4),
         ENTRY("rmsnorm_lm_head_argmax", ti_rmsnorm_lm_head_argmax),
         ENTRY("argmax", ti_argmax),
+        ENTRY("gumbel_noise", ti_gumbel_noise),
         ENTRY("embed", ti_embed),
         // attention over the int8 KV cache
         ENTRY("attn_prep_q8", ti_attn_prep_q8),
@@ -1321,6 +1519,10 @@ napi_value module_init(napi_env env, napi_value exports) {
         FN("qwen3_forward", js_qwen3_forward),
         FN("qwen3_decode", js_qwen3_decode),
         FN("qwen3_set_pos", js_qwen3_set_pos),
+        FN("qwen3_read_tokens_async", js_qwen3_read_tokens_async),
+        FN("qwen3_sampling", js_qwen3_sampling),
+        FN("qwen3_seed", js_qwen3_seed),
+        FN("qwen3_get_seed", js_qwen3_get_seed),
         FN("qwen3_trace", js_qwen3_trace),
         FN("qwen3_write_tokens", js_qwen3_write_tokens),
         FN("qwen3_read_tokens", js_qwen3_read_tokens),

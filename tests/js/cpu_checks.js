@@ -3,12 +3,12 @@
 //   node tests/js/cpu_checks.js <dir>
 // reads <dir>/f32.bin (float32 values) and <dir>/tiny.safetensors, writes <dir>/out.json with
 // the addon's exports, both f32 -> f16 converters over the values, the parsed safetensors
-// header and the error raised by a call without a context.
+// header, the error raised by a call without a context, and the conversation's text renderings.
 const fs = require('fs');
 const path = require('path');
 const HOST = path.join(__dirname, '..', '..', 'tabinfer_amd', 'host');
 const eng = require(path.join(HOST, 'ti-engine.js'));
-const { readSafetensorsHeader } = require(path.join(HOST, 'qwen3-host.js'));
+const { readSafetensorsHeader, toolPreamble, renderMessage } = require(path.join(HOST, 'qwen3-host.js'));
 
 const dir = process.argv[2];
 const raw = fs.readFileSync(path.join(dir, 'f32.bin'));
@@ -28,5 +28,11 @@ const out = {
   f16_q3: q3, f16_eng: en, bf16_to_f16: Array.from(eng.bf16ToF16bits(bf)),
   header: readSafetensorsHeader(path.join(dir, 'tiny.safetensors')),
   ctxError, initError,
+  preamble: toolPreamble([{ type: 'function', function: { name: 'get_time', parameters: { type: 'object', properties: {} } } },
+    { type: 'other' }]),
+  preambleNone: toolPreamble([]),
+  rendered: [renderMessage({ role: 'tool', content: '42' }),
+    renderMessage({ role: 'assistant', content: 'ok', tool_calls: [{ function: { name: 'f', arguments: '{"a":1}' } }] }),
+    renderMessage({ role: 'user', content: [{ type: 'text', text: 'a' }, { type: 'image' }, { type: 'text', text: 'b' }] })],
 };
 fs.writeFileSync(path.join(dir, 'out.json'), JSON.stringify(out));

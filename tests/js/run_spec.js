@@ -7,6 +7,9 @@
 //            an argument is a number/boolean/null, {buf: name}, {rec: {pack, scales, N, K}},
 //            {kv: {kq, ks, vq, vs}}, {emb: {buf, vocab}} or {rec3: {pack, scales, nE}}
 //   model:   {config, nCtx, safetensors, prompt, maxTokens, dump: [tensor names]}   (optional)
+//            gens: [{prompt, maxTokens, temperature}]   generate() runs on a freshly loaded model
+//            prefix: {first, second, maxTokens}   conversation `second` after `first` (prefix
+//                    cache reuse) and again cold on a reloaded model
 // Writes <dir>/result.json (and the files named by `read`).
 const fs = require('fs');
 const path = require('path');
@@ -70,6 +73,15 @@ async function main() {
     const events = [];
     m.chat && (await runChat(host, m, events));
     result.events = events;
+    if (m.gens) {
+      result.gens = [];
+      for (const g of m.gens) {
+        await host.loadModel({ config: m.config, nCtx: m.nCtx, safetensors: m.safetensors, reload: true });
+        const out = await host.generate(g.prompt, { maxTokens: g.maxTokens, temperature: g.temperature });
+        result.gens.push(Array.from(out));
+      }
+    }
+    if (m.prefix) result.prefix = await runPrefix(host, m);
   }
   E.sync();
   fs.writeFileSync(path.join(dir, 'result.json'), JSON.stringify(result));
@@ -86,6 +98,29 @@ async function runChat(host, m, events) {
   await host.loadModel({ config: m.config, nCtx: m.nCtx, safetensors: m.safetensors, tokenizer: tok, reload: true });
   await host.runConversation({ provider: { maxTokens: m.maxTokens }, messages: [{ role: 'user', content: m.prompt.join(' ') }] },
     (ev) => events.push(ev));
+}
+
+// runConversation over id "text": the tokens of `second` after `first` ran (its KV rows reused
+// by the prefix cache) and of `second` on a reloaded model (cold prefill)
+async function runPrefix(host, m) {
+  const tok = {
+    encodeChat: (msgs) => [].concat(...msgs.map((x) => x.content.split(' ').filter((w) => w).map(Number))),
+    decode: (ids) => ids.map((i) => ' ' + i).join(''),
+    isStop: () => false,
+  };
+  const conv = async (msgs) => {
+    const ev = [];
+    await host.runConversation({ provider: { maxTokens: m.prefix.maxTokens }, messages: msgs }, (e) => ev.push(e));
+    return ev.filter((e) => e.type === 'delta' && e.delta.content).map((e) => e.delta.content).join('').trim();
+  };
+  const load = () => host.loadModel({ config: m.config, nCtx: m.nCtx, safetensors: m.safetensors, tokenizer: tok, reload: true });
+  await load();
+  const a1 = await conv(m.prefix.first);
+  const second = m.prefix.first.concat([{ role: 'assistant', content: a1 }], m.prefix.second);
+  const warm = await conv(second);
+  await load();
+  const cold = await conv(second);
+  return { first: a1, warm, cold };
 }
 
 main().catch((e) => { console.error(e && e.stack ? e.stack : e); process.exit(1); });

@@ -2,7 +2,9 @@
 addon): the reference's launchers, called by their models/qwen3.js / models/lfm25.js names
 and argument order, give the oracle's results; loadModel streams a bf16 safetensors
 checkpoint through the GPU quantizer bit-exactly; forward/generate/runConversation produce
-the same tokens as the same decoder driven from Python."""
+the same tokens as the same decoder driven from Python; generate() (greedy and with a
+temperature, through the three-deep readback pipeline) follows the oracle decoder; a
+conversation that reuses the prefix cache after a maxTokens stop decodes as a cold one."""
 import json
 import os
 import shutil
@@ -13,6 +15,7 @@ import numpy as np
 import pytest
 
 from tabinfer_amd import abi
+import qwen3_ref as Q
 
 sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
 from test_js_host import write_safetensors  # noqa: E402
@@ -261,3 +264,87 @@ def test_load_forward_generate_conversation(tmp_path, orc):
     assert text == "".join("<%d>" % t for t in toks)
     usage = [e for e in ev if e["type"] == "usage"][0]["usage"]
     assert usage["prompt_tokens"] == L
+
+
+def _checkpoint(d, rng, c):
+    """A bf16 safetensors checkpoint of geometry c (tied embeddings) and the oracle's view
+    of it: int4 projections by the oracle quantizer, f16 norms / embeddings by the
+    loader's own bf16 -> f16 rounding."""
+    H, I, hd = c["hidden"], c["intermediate"], c["head_dim"]
+    nq, nkv = c["n_heads"] * hd, c["n_kv_heads"] * hd
+    shapes = {"self_attn.q_proj.weight": (nq, H), "self_attn.k_proj.weight": (nkv, H), "self_attn.v_proj.weight": (nkv, H),
+              "self_attn.o_proj.weight": (H, nq), "mlp.gate_proj.weight": (I, H), "mlp.up_proj.weight": (I, H),
+              "mlp.down_proj.weight": (H, I)}
+    T = {}
+    for l in range(c["layers"]):
+        p = "model.layers.%d." % l
+        for nm, (N, K) in shapes.items():
+            T[p + nm] = (N, K, bf16(rng, N * K))
+        for nm, n in (("input_layernorm.weight", H), ("post_attention_layernorm.weight", H),
+                      ("self_attn.q_norm.weight", hd), ("self_attn.k_norm.weight", hd)):
+            T[p + nm] = (n, None, bf16(rng, n, 0.1))
+    T["model.norm.weight"] = (H, None, bf16(rng, H, 0.1))
+    T["model.embed_tokens.weight"] = (c["vocab"], H, bf16(rng, c["vocab"] * H, 0.5))
+    for nm, (n, K, b) in list(T.items()):
+        if K is None:
+            f = (b.astype(np.uint32) << 16).view(np.float32) + np.float32(1.0)
+            T[nm] = (n, None, (f.view(np.uint32) >> 16).astype(np.uint16))
+    ckpt = os.path.join(d, "model.safetensors")
+    write_safetensors(ckpt, {nm: ("BF16", (n,) if K is None else (n, K), b.tobytes()) for nm, (n, K, b) in T.items()})
+    return T, ckpt
+
+
+def _oracle_weights(orc, T):
+    f16 = lambda b: np.array([orc.f32_to_f16_q3(np.uint32(int(v) << 16).view(np.float32)) for v in b], np.uint16)
+    W = {}
+    for nm, (n, K, b) in T.items():
+        if nm == "model.embed_tokens.weight":
+            W[nm] = f16(b)
+            W["lm_head.weight"] = orc.quant_int4_bf16(b, n, K)
+        elif K is None:
+            W[nm] = f16(b)
+        else:
+            W[nm] = orc.quant_int4_bf16(b, n, K)
+    return W
+
+
+def test_generate_follows_the_oracle_decoder(tmp_path, orc):
+    """generate() in JS (prefill, then the pipelined decodeLoop: 3 batches of 32 steps in
+    flight) against the oracle decoder token by token, greedy and at temperature 0.7 with
+    the reference's seed stream. The oracle is fed the GPU's tokens; a token is compared
+    where the oracle's top two (perturbed) logits are apart by more than 4e-3 of their
+    scale (the GPU's logits are within 1e-3), and most of them must be. Then a conversation continued after a maxTokens stop (prefix cache reused) gives
+    the same tokens as the same conversation prefilled cold."""
+    d = str(tmp_path)
+    rng = np.random.default_rng(31)
+    c = SMALL
+    T, ckpt = _checkpoint(d, rng, c)
+    W = _oracle_weights(orc, T)
+    prompt = [11, 502, 7, 999, 123, 4, 88, 5, 600]
+    n_tok, temp = 70, 0.7
+    spec = {"model": {"config": c, "nCtx": 160, "safetensors": ckpt, "prompt": prompt, "maxTokens": 4,
+                      "gens": [{"prompt": prompt, "maxTokens": n_tok}, {"prompt": prompt, "maxTokens": n_tok, "temperature": temp}],
+                      "prefix": {"first": [{"role": "user", "content": "3 14 15 92 65"}],
+                                 "second": [{"role": "user", "content": "35 89 79"}], "maxTokens": 12}}}
+    res = run_spec(d, spec, {})
+    for run, t in ((res["gens"][0], 0.0), (res["gens"][1], temp)):
+        assert len(run) == n_tok
+        ref = Q.RefDecoder(c, W, 160)
+        for p, tk in enumerate(prompt):
+            rl, _ = ref.step(int(tk), p)
+        st, compared = orc.SEED_INIT, 0
+        for j, got in enumerate(run):
+            v = rl.astype(np.float32)
+            if t > 0:
+                st = orc.seed_next(st)
+                v = orc.gumbel_noise(v, st, t)
+            srt = np.sort(v.astype(np.float64))
+            if srt[-1] - srt[-2] > 4e-3 * np.abs(rl).max():    # not a near tie
+                assert got == orc.argmax(v), (t, j)
+                compared += 1
+            rl, _ = ref.step(int(got), len(prompt) + j)         # the oracle continues from the GPU's token
+        print("[js] generate at T=%.1f: %d of %d tokens compared with the oracle" % (t, compared, n_tok), flush=True)
+        assert compared >= 40
+    pr = res["prefix"]
+    assert len(pr["first"].split()) == 12
+    assert pr["warm"] == pr["cold"] and len(pr["warm"].split()) == 12

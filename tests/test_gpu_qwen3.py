@@ -79,6 +79,49 @@ def test_prefill_then_chained_decode(ctx):
         m.close()
 
 
+def test_prefill_in_256_token_chunks(ctx):
+    """The reference's prefill chunk (PREFILL_CHUNK = 256, models/qwen3.js:5245-5256): a
+    300-token prompt as a 256-token forward and a 44-token one, with 16 query heads of 128
+    (4096 query rows in one attention call, the split count cut to fit the partials), then
+    chained decode steps, against the oracle decoder run token by token."""
+    cfg = dict(SMALL, n_heads=16, n_kv_heads=8, head_dim=128, max_ctx=320, max_tokens=256)
+    W = Q.make_weights(cfg, 6)
+    m = abi.Qwen3(ctx, **cfg)
+    try:
+        Q.load_into(m, W)
+        ref = Q.RefDecoder(cfg, W, cfg["max_ctx"])
+        ids = (np.arange(300, dtype=np.int64) * 7919 % cfg["vocab"]).astype(np.int32)
+        m.forward(ids[:256], 0)
+        m.forward(ids[256:], 256)
+        for p, t in enumerate(ids):
+            rl, rt = ref.step(int(t), p)
+        got = _logits(ctx, m, cfg["vocab"])
+        assert rel_err(got, rl) < TOL
+        tok = int(m.read_tokens(300, 1)[0])
+        if margin_ok(rl):
+            assert tok == rt
+        for p in range(300, 304):
+            m.decode()
+            rl, rt = ref.step(tok, p)
+            assert rel_err(_logits(ctx, m, cfg["vocab"]), rl) < TOL
+            tok = int(m.read_tokens(p + 1, 1)[0])
+            if margin_ok(rl):
+                assert tok == rt
+        # every KV row of the chunks within one int8 step of the oracle's: layer 0's K/V come
+        # straight from the embeddings (flips only where the GEMM's f32 order lands on the
+        # other side of a rounding boundary), layer 1's also carry layer 0's flips
+        nkv = cfg["n_kv_heads"] * cfg["head_dim"]
+        for layer, frac in ((0, 0.005), (1, 0.02)):
+            kq, ks, vq, vs = m.kv(layer)
+            gk = ctx.download(kq, np.uint32, 300 * nkv // 4).view(np.int8).astype(int).reshape(300, -1)
+            rk = ref.kv[layer][0][:300].view(np.int8).astype(int).reshape(300, -1)
+            print("[qwen3] 256-token chunks: layer %d K codes differing %.4f" % (layer, np.mean(gk != rk)), flush=True)
+            assert np.max(np.abs(gk - rk)) <= 1
+            assert np.mean(gk != rk) < frac
+    finally:
+        m.close()
+
+
 def test_batched_forward_matches_sequential(ctx):
     """A T=8 forward (the batch-8 configuration) gives the same last logits as 8
     single-token forwards."""

@@ -106,3 +106,24 @@ def test_errors_are_exceptions(checks):
     if abi.device_count() == 0:
         assert out["initError"]["code"] == abi.TI_ERR_NO_DEVICE
         assert "no HIP device" in out["initError"]["message"]
+
+
+def test_tool_preamble_and_message_rendering(checks):
+    """toolPreamble (models/qwen3.js:5294-5320): Qwen3's Hermes tool block, each tool's
+    {"type": "function", "function": ...} signature on its own line inside <tools>, non-function
+    tools dropped, nothing without tools; message rendering (:5429-5441): tool results as
+    <tool_response> user turns, assistant tool calls as <tool_call> blocks, text parts joined."""
+    _, out = checks
+    sig = '{"type":"function","function":{"name":"get_time","parameters":{"type":"object","properties":{}}}}'
+    want = "\n".join(["# Tools", "", "You may call one or more functions to assist with the user query.", "",
+                      "You are provided with function signatures within <tools></tools> XML tags:", "<tools>", sig,
+                      "</tools>", "",
+                      "For each function call, return a json object with function name and arguments within "
+                      "<tool_call></tool_call> XML tags:",
+                      "<tool_call>", '{"name": <function-name>, "arguments": <args-json-object>}', "</tool_call>"])
+    assert out["preamble"] == want
+    assert out["preambleNone"] == ""
+    tool, asst, user = out["rendered"]
+    assert tool == {"role": "user", "content": "<tool_response>\n42\n</tool_response>"}
+    assert asst == {"role": "assistant", "content": 'ok\n<tool_call>\n{"name": "f", "arguments": {"a":1}}\n</tool_call>'}
+    assert user == {"role": "user", "content": "a\nb"}
