@@ -91,6 +91,25 @@ int ti_event_wait(ti_ctx* ctx, int slot);
 int ti_quant_int4_bf16(ti_ctx* ctx, const uint16_t* w_bf16, uint32_t* pack, uint16_t* scales,
                        int N, int K);
 
+/* ---- the on-GPU ternary format (models/qwen3.js:3428-3469) ---------------------
+ * quantizeTernaryBf16, run on the GPU, bit-exact: pack u32[N*K/16] holds c = w + 1 in {0, 1, 2}
+ * for weight k of a row at bits 8(k&3) + 2((k>>2)&3) of word k/16; scales f16[N*K/32] are
+ * each 32-group's largest bf16 magnitude. A nonzero magnitude more than 2 bf16 ULPs below its
+ * group's maximum means the tensor is not ternary: *not_ternary (a device word the caller
+ * zeroes first) becomes nonzero, where the reference returns null and its loader quantizes
+ * to int4 instead. K % 64 == 0. */
+int ti_quant_tern_bf16(ti_ctx* ctx, const uint16_t* w_bf16, uint32_t* pack, uint16_t* scales,
+                       int N, int K, uint32_t* not_ternary);
+/* gemvTern2 / gemvTern_only (models/qwen3.js:449-503, 548-556): y (+)= W x over quantQ8's
+ * int8 activation (xq, xs) and its per-16 sums xsum; each 32-group is an exact int32 sum
+ * (sum c x - sum x) scaled by the weight and activation scales. */
+int ti_gemv_tern2(ti_ctx* ctx, const uint32_t* xq, const float* xs, const int32_t* xsum,
+                  const uint32_t* pack, const uint16_t* scales, float* y, int N, int K, int acc);
+/* gateupTern2 (models/qwen3.js:747-810, 862-870): swi = silu(gate x) * (up x). */
+int ti_gateup_silu_tern2(ti_ctx* ctx, const uint32_t* xq, const float* xs, const int32_t* xsum,
+                         const uint32_t* gpack, const uint16_t* gscales, const uint32_t* upack,
+                         const uint16_t* uscales, float* swi, int I, int H);
+
 /* ---- activations ----------------------------------------------------------- */
 /* quantQ8 (models/qwen3.js:414-420): per-32 int8 + per-16 sums. */
 int ti_quant_act_q8(ti_ctx* ctx, const float* x, uint32_t* xq, float* xs, int32_t* xsum, int K);

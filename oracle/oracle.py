@@ -57,6 +57,9 @@ _sig("or_rmsnorm_q8", None, [_p, _p, _i, _f, _p, _p, _p])
 _sig("or_rmsnorm", None, [_p, _p, _i, _i, _f, _p])
 _sig("or_group_dots_q4_q8", None, [_p, _p, _i, _i, _p])
 _sig("or_gemv_q4_q8", None, [_p, _p, _p, _p, _i, _i, _p])
+_sig("or_quant_tern_bf16", _i, [_p, _i, _i, _p, _p])
+_sig("or_gemv_tern2", None, [_p, _p, _p, _p, _i, _i, _p])
+_sig("or_gateup_silu_tern2", None, [_p, _p, _p, _p, _p, _p, _i, _i, _p])
 _sig("or_gemv_q4_f32", None, [_p, _p, _p, _i, _i, _p])
 _sig("or_gateup_silu_q4", None, [_p, _p, _p, _p, _p, _p, _i, _i, _p])
 _sig("or_gemm_q4_q8", None, [_p, _p, _p, _p, _i, _i, _i, _p])
@@ -180,6 +183,29 @@ def gemv_q4_q8(xq, xs, pack, sc, N, K):
     y = np.zeros(N, np.float64)
     _L.or_gemv_q4_q8(_ptr(_c(xq, np.uint32)), _ptr(_c(xs, np.float32)), _ptr(_c(pack, np.uint32)),
                      _ptr(_c(sc, np.uint16)), N, K, _ptr(y))
+    return y
+
+
+def quant_tern_bf16(w_bf16, N, K):
+    """(pack, scales) of the on-GPU ternary format, or None where the reference returns null."""
+    w = _c(w_bf16, np.uint16)
+    pack = np.zeros(N * K // 16, np.uint32)
+    sc = np.zeros(N * K // 32, np.uint16)
+    ok = _L.or_quant_tern_bf16(_ptr(w), N, K, _ptr(pack), _ptr(sc))
+    return (pack, sc) if ok else None
+
+
+def gemv_tern2(xq, xs, pack, sc, N, K):
+    y = np.zeros(N, np.float64)
+    _L.or_gemv_tern2(_ptr(_c(xq, np.uint32)), _ptr(_c(xs, np.float32)), _ptr(_c(pack, np.uint32)),
+                     _ptr(_c(sc, np.uint16)), N, K, _ptr(y))
+    return y
+
+
+def gateup_silu_tern2(xq, xs, gp, gs, up, us, I, H):
+    y = np.zeros(I, np.float64)
+    _L.or_gateup_silu_tern2(_ptr(_c(xq, np.uint32)), _ptr(_c(xs, np.float32)), _ptr(_c(gp, np.uint32)),
+                            _ptr(_c(gs, np.uint16)), _ptr(_c(up, np.uint32)), _ptr(_c(us, np.uint16)), I, H, _ptr(y))
     return y
 
 

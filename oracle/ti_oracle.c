@@ -243,6 +243,79 @@ void or_gemv_q4_q8(const uint32_t* xq, const float* xs, const uint32_t* pack,
     }
 }
 
+/* quantizeTernaryBf16 (models/qwen3.js:3435-3469), literally: a pre-check of the first
+ * rows (an early exit only: the full pass applies the same test), then per 32-group the
+ * largest magnitude (bf16 bits & 0x7FFF as integers) is the scale (bf16 -> f16 through
+ * the f32 -> f16 rounding of :3357-3374), each weight's code is 1 for a zero magnitude,
+ * else 0 for a set sign bit and 2 otherwise, at bits 8(k&3) + 2((k>>2)&3) of word k/16;
+ * any nonzero magnitude more than TOL = 2 below its group's maximum returns 0. */
+int or_quant_tern_bf16(const uint16_t* u16, int N, int K, uint32_t* pack, uint16_t* scales) {
+    const int G = 32, TOL = 2;
+    if (K % 64 != 0) return 0;
+    const int wpr = K / 16, gpr = K / G;
+    const int pre = N < 4 ? N : 4;
+    for (int n = 0; n < pre; n++)
+        for (int g = 0; g < gpr; g++) {
+            int mx = 0;
+            for (int j = 0; j < G; j++) { int m = u16[(size_t)n * K + g * G + j] & 0x7FFF; if (m > mx) mx = m; }
+            for (int j = 0; j < G; j++) { int m = u16[(size_t)n * K + g * G + j] & 0x7FFF; if (m != 0 && mx - m > TOL) return 0; }
+        }
+    memset(pack, 0, (size_t)N * wpr * 4);
+    for (int n = 0; n < N; n++) {
+        const uint16_t* rU = u16 + (size_t)n * K;
+        uint32_t* rP = pack + (size_t)n * wpr;
+        for (int g = 0; g < gpr; g++) {
+            int mx = 0;
+            for (int j = 0; j < G; j++) { int m = rU[g * G + j] & 0x7FFF; if (m > mx) mx = m; }
+            uint32_t fb = (uint32_t)mx << 16;
+            float f;
+            memcpy(&f, &fb, 4);
+            scales[(size_t)n * gpr + g] = or_f32_to_f16_q3(f);
+            for (int j = 0; j < G; j++) {
+                int k = g * G + j, bits = rU[k], m = bits & 0x7FFF;
+                if (m != 0 && mx - m > TOL) return 0;
+                uint32_t c = m == 0 ? 1u : ((bits & 0x8000) ? 0u : 2u);
+                rP[k >> 4] |= c << (((k & 3) << 3) + ((k >> 2) & 3) * 2);
+            }
+        }
+    }
+    return 1;
+}
+
+/* the code of weight k in a row of the ternary format, minus 1: the weight's sign */
+static int tern2_w(const uint32_t* rp, int k) {
+    return (int)((rp[k >> 4] >> (((k & 3) << 3) + ((k >> 2) & 3) * 2)) & 3u) - 1;
+}
+
+/* gemvTern2 (models/qwen3.js:449-503): y[n] = sum_g f16(s[n,g]) * xs[g] * (sum_j w x) over
+ * 32-groups; the group sum is the reference's sum c x - sum x, exact. */
+void or_gemv_tern2(const uint32_t* xq, const float* xs, const uint32_t* pack, const uint16_t* scales,
+                   int N, int K, double* y) {
+    const int gpr = K / 32, wpr = K / 16;
+    for (int n = 0; n < N; n++) {
+        const uint32_t* rp = pack + (size_t)n * wpr;
+        double acc = 0;
+        for (int g = 0; g < gpr; g++) {
+            long d = 0;
+            for (int j = 0; j < 32; j++) { int k = g * 32 + j; d += tern2_w(rp, k) * i8_at(xq, k); }
+            acc += or_f16_to_f32(scales[(size_t)n * gpr + g]) * (double)xs[g] * (double)d;
+        }
+        y[n] = acc;
+    }
+}
+
+/* gateupTern2 (models/qwen3.js:747-810): swi = silu(g) * u */
+void or_gateup_silu_tern2(const uint32_t* xq, const float* xs, const uint32_t* gpack, const uint16_t* gsc,
+                          const uint32_t* upack, const uint16_t* usc, int I, int H, double* swi) {
+    double* g = (double*)malloc(sizeof(double) * (size_t)I);
+    double* u = (double*)malloc(sizeof(double) * (size_t)I);
+    or_gemv_tern2(xq, xs, gpack, gsc, I, H, g);
+    or_gemv_tern2(xq, xs, upack, usc, I, H, u);
+    for (int i = 0; i < I; i++) swi[i] = g[i] / (1.0 + exp(-g[i])) * u[i];
+    free(g);
+    free(u);
+}
+
 /* models/qwen3.js:276-313: y[n] = sum_k f16(s)*(nib-8)*x[k], x f32 */
 void or_gemv_q4_f32(const float* x, const uint32_t* pack, const uint16_t* scales,
                     int N, int K, double* y) {

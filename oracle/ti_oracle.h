@@ -30,6 +30,9 @@
  *  or_attn_* : f64 softmax oracle, nsplit invariance, RoPE known-answer tests
  *      (native/crates/n2-core/src/ops.rs:169-214).
  *  or_argmax : a numpy emulation of the reference's two-stage tree on random ties.
+ *  or_quant_tern_bf16 : exact dequantization of ternary inputs (a wrong bit layout or sign
+ *      map fails it), the 2-ULP acceptance edge, a hand-placed known answer;
+ *  or_gemv_tern2, or_gateup_silu_tern2 : a dense f64 matmul of the dequantized operands.
  *  or_gumbel_noise, or_pcg : the reference's own self-test (models/qwen3.js:3198-3214:
  *      P(5)/P(9) = e at T = 1 with its seed stream, T -> 0 greedy) on a larger sample,
  *      the Gumbel mean and variance (Euler's gamma, pi^2/6), u uniform on (0, 1).
@@ -75,6 +78,14 @@ void or_gateup_silu_q4(const uint32_t* xq, const float* xs,
                        const uint32_t* gpack, const uint16_t* gsc,
                        const uint32_t* upack, const uint16_t* usc,
                        int I, int H, double* swi);                             /* models/qwen3.js:679-728 */
+/* the on-GPU ternary format (models/qwen3.js:3428-3469): returns 1 and fills pack[N*K/16],
+ * scales[N*K/32] for a ternary tensor, 0 (the reference's null) otherwise */
+int  or_quant_tern_bf16(const uint16_t* w_bf16, int N, int K, uint32_t* pack, uint16_t* scales);
+/* gemvTern2 (models/qwen3.js:449-503) and gateupTern2 (:747-810), f64 of the exact group sums */
+void or_gemv_tern2(const uint32_t* xq, const float* xs, const uint32_t* pack, const uint16_t* scales,
+                   int N, int K, double* y);
+void or_gateup_silu_tern2(const uint32_t* xq, const float* xs, const uint32_t* gpack, const uint16_t* gsc,
+                          const uint32_t* upack, const uint16_t* usc, int I, int H, double* swi);
 /* batched: Y[T,N] from per-token int8 acts (models/qwen3.js:1326-1388) */
 void or_gemm_q4_q8(const uint32_t* xq, const float* xs, const uint32_t* pack,
                    const uint16_t* scales, int T, int N, int K, double* y);

@@ -49,6 +49,9 @@ SIGS = {
     "ti_event_elapsed_ms": [_p, _i, _i, C.POINTER(_f)],
     "ti_event_wait": [_p, _i],
     "ti_quant_int4_bf16": [_p, _p, _p, _p, _i, _i],
+    "ti_quant_tern_bf16": [_p, _p, _p, _p, _i, _i, _p],
+    "ti_gemv_tern2": [_p, _p, _p, _p, _p, _p, _p, _i, _i, _i],
+    "ti_gateup_silu_tern2": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i],
     "ti_quant_act_q8": [_p, _p, _p, _p, _p, _i],
     "ti_quant_act_q8_t": [_p, _p, _p, _p, _i, _i],
     "ti_rmsnorm_q8": [_p, _p, _p, _p, _p, _p, _i, _f],

@@ -1,5 +1,6 @@
 // k_quant.hip — quantizers of the decode path (all integer outputs bit-exact):
 //  int4 weight quantizer     models/qwen3.js:3405-3426 (JS f64 semantics)
+//  ternary weight format     models/qwen3.js:3435-3469
 //  per-32 int8 activation    models/qwen3.js:332-358, 1210-1231
 //  fused RMSNorm + int8      models/qwen3.js:569-612
 //     plain RMSNorm             models/qwen3.js:60-80
@@ -103,6 +104,60 @@ extern "C" int ti_quant_int4_bf16(ti_ctx* c, const uint16_t* w, uint32_t* pack, 
     return TI_OK;
 }
 
+
+// ---------------------------------------------------------------------------
+// quantizeTernaryBf16 (models/qwen3.js:3435-3469), one thread per (row, 32-group): the
+// group's scale is its largest bf16 magnitude (bits & 0x7FFF compared as integers), in
+// f16 by the reference's f32 -> f16 rounding; code = 1 for a zero, 0 for a negative, 2
+// for a positive weight, at bits 8(k&3) + 2((k>>2)&3) of word k/16. A nonzero magnitude
+// more than 2 bf16 ULPs below its group's maximum means the tensor is not ternary (the
+// reference's null, after which its loader quantizes to int4): *not_ternary gets 1.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_quant_tern_bf16(const uint16_t* __restrict__ w, uint32_t* __restrict__ pack,
+                                                         uint16_t* __restrict__ scales, uint32_t* __restrict__ not_ternary,
+                                                         long ngroups) {
+    const long gi = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gi >= ngroups) return;
+    const uint4* src = reinterpret_cast<const uint4*>(w + gi * 32);
+    uint32_t u[16];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        uint4 v = src[i];
+        u[4 * i] = v.x; u[4 * i + 1] = v.y; u[4 * i + 2] = v.z; u[4 * i + 3] = v.w;
+    }
+    uint32_t mx = 0;
+#pragma unroll
+    for (int j = 0; j < 32; j++) {
+        const uint32_t m = (u[j >> 1] >> (16 * (j & 1))) & 0x7FFFu;
+        mx = m > mx ? m : mx;
+    }
+    bool bad = false;
+    uint32_t words[2] = {0u, 0u};
+#pragma unroll
+    for (int j = 0; j < 32; j++) {
+        const uint32_t bits = (u[j >> 1] >> (16 * (j & 1))) & 0xFFFFu, m = bits & 0x7FFFu;
+        if (m != 0u && mx - m > 2u) bad = true;
+        const uint32_t c = m == 0u ? 1u : ((bits & 0x8000u) ? 0u : 2u);
+        words[j >> 4] |= c << (((j & 3) << 3) + ((j >> 2) & 3) * 2);
+    }
+    reinterpret_cast<uint2*>(pack)[gi] = make_uint2(words[0], words[1]);
+    scales[gi] = (uint16_t)f32_to_f16_q3(__uint_as_float(mx << 16));
+    if (bad) __hip_atomic_fetch_or(not_ternary, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+extern "C" int ti_quant_tern_bf16(ti_ctx* c, const uint16_t* w, uint32_t* pack, uint16_t* scales, int N, int K,
+                                  uint32_t* not_ternary) {
+    TI_CHECK_CTX(c);
+    TI_REQUIRE(w && pack && scales && not_ternary, "ti_quant_tern_bf16: null buffer");
+    TI_REQUIRE(N > 0 && K > 0 && K % 64 == 0, "ti_quant_tern_bf16: need N>0, K>0, K%%64==0 (N=%d K=%d)", N, K);
+    TI_REQUIRE(((uintptr_t)w & 15) == 0 && ((uintptr_t)pack & 7) == 0, "ti_quant_tern_bf16: w 16-byte, pack 8-byte aligned");
+    const long ng = (long)N * (K / 32);
+    const long blocks = (ng + 255) / 256;
+    TI_REQUIRE(blocks < (1L << 31), "ti_quant_tern_bf16: too large");
+    k_quant_tern_bf16<<<(unsigned)blocks, 256, 0, c->stream>>>(w, pack, scales, not_ternary, ng);
+    TI_LAUNCHED("k_quant_tern_bf16");
+    return TI_OK;
+}
 
 __global__ __launch_bounds__(64) void k_quant_act_q8(const float* __restrict__ x, uint32_t* __restrict__ xq,
                                                      float* __restrict__ xs, int32_t* __restrict__ xsum, int ng) {

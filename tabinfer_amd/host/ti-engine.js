@@ -112,9 +112,32 @@ function createEngine({ device = 0 } = {}) {
     TI.quant_int4_bf16(ctx, bf16Buf, pack, sc, rows, K);
   }
 
+  // quantizeTernaryBf16 (models/qwen3.js:3435-3469) on the GPU: bf16 rows on the device ->
+  // a ternary record {pack, scales, N, K, tern: true}, or null where the tensor is not
+  // ternary (the caller then quantizes to int4, as the reference's loader does)
+  const _ternFlag = E.createBuffer(4);
+  function quantizeTernaryBf16(bf16Buf, N, K) {
+    const rec = { pack: E.createBuffer(N * K / 4), scales: E.createBuffer(N * K / 32 * 2), N, K, tern: true };
+    E.fillU32(_ternFlag, 0, 1);
+    TI.quant_tern_bf16(ctx, bf16Buf, rec.pack, rec.scales, N, K, _ternFlag);
+    if (new Uint32Array(E.readBytes(_ternFlag, 0, 4))[0] === 0) return rec;
+    E.destroy(rec.pack);
+    E.destroy(rec.scales);
+    return null;
+  }
+  // gemvTern_only (:548-556): the ternary GEMV against the activation quantQ8 left in _dp4
+  function gemvTern_only(wrec, yBuf, N, K, acc) {
+    TI.gemv_tern2(ctx, _dp4.xq, _dp4.xs, _dp4.xsum, wrec.pack, wrec.scales, yBuf, N, K, b01(acc));
+  }
+
   // ---- models/qwen3.js launchers ---------------------------------------------------------------
   const L = {
-    quantizeInt4Bf16, int4Record,
+    quantizeInt4Bf16, int4Record, quantizeTernaryBf16, gemvTern_only,
+    // projGemv (:558-561): the kind router of the decode call sites sharing one activation
+    projGemv(wrec, yBuf, N, K, acc) {
+      if (wrec.tern) return gemvTern_only(wrec, yBuf, N, K, acc);
+      return TI.gemv_q4_q8(ctx, _dp4.xq, _dp4.xs, wrec.pack, wrec.scales, yBuf, N, K, b01(acc));
+    },
     quantQ8(xBuf, K) { TI.quant_act_q8(ctx, xBuf, _dp4.xq, _dp4.xs, _dp4.xsum, K); },                       // :414
     rmsnormQ(xBuf, wBuf, H, eps) { TI.rmsnorm_q8(ctx, xBuf, wBuf, _dp4.xq, _dp4.xs, _dp4.xsum, H, eps); },  // :614
     rmsnorm(xBuf, wBuf, yBuf, T, H, eps) { TI.rmsnorm(ctx, xBuf, wBuf, yBuf, T, H, eps); },                // :81
@@ -125,9 +148,22 @@ function createEngine({ device = 0 } = {}) {
       TI.gemv_q4_f32(ctx, xBuf, packBuf, scBuf, yBuf, N, K, b01(acc));
     },
     gateUpSiluDP4_only(gRec, uRec, swiBuf, I, H /* , NR */) {                                              // :861
+      if (gRec.tern) {                                                                                       // :862-870
+        TI.gateup_silu_tern2(ctx, _dp4.xq, _dp4.xs, _dp4.xsum, gRec.pack, gRec.scales, uRec.pack, uRec.scales, swiBuf, I, H);
+        return;
+      }
       TI.gateup_silu_q4(ctx, _dp4.xq, _dp4.xs, gRec.pack, gRec.scales, uRec.pack, uRec.scales, swiBuf, I, H);
     },
-    linearQ(xBuf, wrec, yBuf, T, N, K, acc) { TI.linear_q4(ctx, xBuf, wrec.pack, wrec.scales, yBuf, T, N, K, b01(acc)); }, // :1588
+    linearQ(xBuf, wrec, yBuf, T, N, K, acc) {                                                              // :1588
+      if (wrec.tern) {        // :1594-1598: quantQ8 + the ternary GEMV, token by token (no ternary GEMM here)
+        for (let t = 0; t < T; t++) {
+          TI.quant_act_q8(ctx, T > 1 ? E.view(xBuf, t * K * 4) : xBuf, _dp4.xq, _dp4.xs, _dp4.xsum, K);
+          gemvTern_only(wrec, T > 1 ? E.view(yBuf, t * N * 4) : yBuf, N, K, acc);
+        }
+        return;
+      }
+      TI.linear_q4(ctx, xBuf, wrec.pack, wrec.scales, yBuf, T, N, K, b01(acc));
+    },
     attnPrepQ8(qBuf, kBuf, vBuf, qwBuf, kwBuf, qrBuf, kv, nHq, nKv, hd, posBase, theta, eps) {             // :2297
       TI.attn_prep_q8(ctx, qBuf, kBuf, vBuf, qwBuf, kwBuf, qrBuf, kv.kq, kv.ks, kv.vq, kv.vs, nHq, nKv, hd, posBase, theta, eps);
     },

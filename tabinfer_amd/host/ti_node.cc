@@ -1473,6 +1473,9 @@ napi_value module_init(napi_env env, napi_value exports) {
         ENTRY("event_wait", ti_event_wait),
         // int4 weights, activations, GEMV / GEMM
         ENTRY("quant_int4_bf16", ti_quant_int4_bf16),
+        ENTRY("quant_tern_bf16", ti_quant_tern_bf16),
+        ENTRY("gemv_tern2", ti_gemv_tern2),
+        ENTRY("gateup_silu_tern2", ti_gateup_silu_tern2),
         ENTRY("quant_act_q8", ti_quant_act_q8),
         ENTRY("quant_act_q8_t", ti_quant_act_q8_t),
         ENTRY("rmsnorm_q8", ti_rmsnorm_q8),

@@ -5,7 +5,8 @@
 //   buffers: {name: {file: "x.bin"} | {bytes: n}}            device buffers (files are raw bytes)
 //   calls:   [{fn: "L.gemvDP4_only", args: [...]}, {read: name, bytes, out}, {read_dp4: "xq", bytes, out}]
 //            an argument is a number/boolean/null, {buf: name}, {rec: {pack, scales, N, K}},
-//            {kv: {kq, ks, vq, vs}}, {emb: {buf, vocab}} or {rec3: {pack, scales, nE}}
+//            {kv: {kq, ks, vq, vs}}, {emb: {buf, vocab}}, {rec3: {pack, scales, nE}} or {trec: name}
+//            (a record made by {tern_quant: name, src: buffer, N, K}: L.quantizeTernaryBf16)
 //   model:   {config, nCtx, safetensors, prompt, maxTokens, dump: [tensor names]}   (optional)
 //            gens: [{prompt, maxTokens, temperature}]   generate() runs on a freshly loaded model
 //            prefix: {first, second, maxTokens}   conversation `second` after `first` (prefix
@@ -34,6 +35,7 @@ async function main() {
     }
   }
   const B = (n) => { if (!(n in bufs)) throw new Error('spec: no buffer ' + n); return bufs[n]; };
+  const trecs = {};
   const arg = (a) => {
     if (a === null || typeof a !== 'object') return a;
     if ('buf' in a) return B(a.buf);
@@ -41,6 +43,7 @@ async function main() {
     if ('kv' in a) return { kq: B(a.kv.kq), ks: B(a.kv.ks), vq: B(a.kv.vq), vs: B(a.kv.vs) };
     if ('emb' in a) return { buf: B(a.emb.buf), vocab: a.emb.vocab };
     if ('rec3' in a) return { pack: B(a.rec3.pack), scales: B(a.rec3.scales), nE: a.rec3.nE };
+    if ('trec' in a) { if (!trecs[a.trec]) throw new Error('spec: no ternary record ' + a.trec); return trecs[a.trec]; }
     throw new Error('spec: bad argument ' + JSON.stringify(a));
   };
   for (const c of spec.calls || []) {
@@ -53,6 +56,14 @@ async function main() {
       fs.writeFileSync(path.join(dir, c.out), Buffer.from(E.readBytes(B(c.read), c.offset || 0, c.bytes)));
     } else if (c.read_dp4) {
       fs.writeFileSync(path.join(dir, c.out), Buffer.from(E.readBytes(_dp4[c.read_dp4], 0, c.bytes)));
+    } else if (c.tern_quant) {            // L.quantizeTernaryBf16 -> a named record (or null)
+      const rec = L.quantizeTernaryBf16(B(c.src), c.N, c.K);
+      result[c.tern_quant] = !!rec;
+      if (rec) {
+        trecs[c.tern_quant] = rec;
+        fs.writeFileSync(path.join(dir, c.tern_quant + '.pack'), Buffer.from(E.readBytes(rec.pack, 0, c.N * c.K / 4)));
+        fs.writeFileSync(path.join(dir, c.tern_quant + '.scales'), Buffer.from(E.readBytes(rec.scales, 0, c.N * c.K / 16)));
+      }
     }
   }
   if (spec.model) {

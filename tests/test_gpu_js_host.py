@@ -180,6 +180,54 @@ def test_attention_ternary_moe_launchers(tmp_path, orc):
     assert rel(load(d, "my.out", np.float32), orc.moe_gemv_q3(mx, p3, s3, oi, topk, mN, mK, mK, topk)) < 1e-4
 
 
+def test_ternary_format_launchers(tmp_path, orc):
+    """quantizeTernaryBf16 (bit-exact, and null for a continuous tensor), then gemvTern_only,
+    projGemv, gateUpSiluDP4_only and linearQ (T = 1 and T = 3) routing the ternary records."""
+    from tern2_data import ternary_bf16
+    d = str(tmp_path)
+    rng = np.random.default_rng(24)
+    N, K, I = 256, 2048, 512
+    w, g, u = ternary_bf16(rng, N, K), ternary_bf16(rng, I, K), ternary_bf16(rng, I, K)
+    cont = bf16(rng, N * K)
+    x = rng.standard_normal(3 * K).astype(np.float32)
+    files = {"w.bin": w, "g.bin": g, "u.bin": u, "cont.bin": cont, "x.bin": x}
+    B = lambda n: {"buf": n}
+    spec = {
+        "buffers": dict({k[:-4]: {"file": k} for k in files}, y={"bytes": N * 4}, yp={"bytes": N * 4},
+                        swi={"bytes": I * 4}, yl={"bytes": 3 * N * 4}),
+        "calls": [
+            {"tern_quant": "tw", "src": "w", "N": N, "K": K},
+            {"tern_quant": "tg", "src": "g", "N": I, "K": K},
+            {"tern_quant": "tu", "src": "u", "N": I, "K": K},
+            {"tern_quant": "tc", "src": "cont", "N": N, "K": K},
+            {"fn": "L.quantQ8", "args": [B("x"), K]},
+            {"fn": "L.gemvTern_only", "args": [{"trec": "tw"}, B("y"), N, K, False]},
+            {"read": "y", "bytes": N * 4, "out": "y.out"},
+            {"fn": "L.projGemv", "args": [{"trec": "tw"}, B("yp"), N, K, False]},
+            {"read": "yp", "bytes": N * 4, "out": "yp.out"},
+            {"fn": "L.gateUpSiluDP4_only", "args": [{"trec": "tg"}, {"trec": "tu"}, B("swi"), I, K]},
+            {"read": "swi", "bytes": I * 4, "out": "swi.out"},
+            {"fn": "L.linearQ", "args": [B("x"), {"trec": "tw"}, B("yl"), 3, N, K, False]},
+            {"read": "yl", "bytes": 3 * N * 4, "out": "yl.out"},
+        ],
+    }
+    res = run_spec(d, spec, files)
+    assert res["tw"] and res["tg"] and res["tu"] and not res["tc"]
+    pw, sw = orc.quant_tern_bf16(w, N, K)
+    assert np.array_equal(load(d, "tw.pack", np.uint32), pw) and np.array_equal(load(d, "tw.scales", np.uint16), sw)
+    pg, sg = orc.quant_tern_bf16(g, I, K)
+    pu, su = orc.quant_tern_bf16(u, I, K)
+    xq, xs, _ = orc.quant_act_q8(x[:K])
+    want = orc.gemv_tern2(xq, xs, pw, sw, N, K)
+    assert rel(load(d, "y.out", np.float32), want) < 1e-3
+    assert np.array_equal(load(d, "yp.out", np.float32), load(d, "y.out", np.float32))
+    assert rel(load(d, "swi.out", np.float32), orc.gateup_silu_tern2(xq, xs, pg, sg, pu, su, I, K)) < 1e-3
+    yl = load(d, "yl.out", np.float32).reshape(3, N)
+    for t in range(3):
+        xq, xs, _ = orc.quant_act_q8(x[t * K:(t + 1) * K])
+        assert rel(yl[t], orc.gemv_tern2(xq, xs, pw, sw, N, K)) < 1e-3
+
+
 SMALL = dict(layers=2, hidden=256, intermediate=512, n_heads=4, n_kv_heads=2, head_dim=64, vocab=1000,
              rope_theta=1e6, rms_eps=1e-6)
 
