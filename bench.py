@@ -594,6 +594,58 @@ def ternary_step(ctx, reps=10):
             "what": "28 layers (q/k/v in one launch, o, gate/up in one launch, down) + lm_head 151936x2048, distinct weights"}
 
 
+def tern2_step(ctx, reps=10):
+    """The Bonsai-1.7B GEMV set of one decode step in the reference's on-GPU ternary format
+    (quantizeTernaryBf16's codes, f16 scales per 32; gemvTern2 / gateupTern2): 28 distinct
+    layers of q, k, v, o (ti_gemv_tern2 each), gate/up + SiLU (ti_gateup_silu_tern2), down,
+    then the 151936 x 2048 lm_head, one graph; int8 activations with their sums."""
+    rng = np.random.default_rng(4)
+    def mat(N, K):
+        return (ctx.upload(tern_codes_fast(rng, N * K // 4)),
+                ctx.upload(rng.uniform(0.01, 0.05, N * K // 32).astype(np.float16).view(np.uint16)))
+    src = {shape: mat(*shape) for shape in set(BONSAI_SHAPES)}
+    layers = []
+    for l in range(BONSAI_LAYERS):
+        mats = []
+        for N, K in BONSAI_SHAPES:
+            c0, s0 = src[(N, K)]
+            c2, s2 = ctx.alloc(N * K // 4), ctx.alloc(N * K // 16)
+            ctx.call("ti_buf_copy", c2, 0, c0, 0, N * K // 4)
+            ctx.call("ti_buf_copy", s2, 0, s0, 0, N * K // 16)
+            mats.append((c2, s2))
+        layers.append(mats)
+    lm = mat(BONSAI_VOCAB, BONSAI_H)
+    acts = {}
+    for K in (2048, 6144):
+        acts[K] = (ctx.upload(rng.integers(0, 2 ** 32, K // 4, dtype=np.uint64).astype(np.uint32)),
+                   ctx.upload(rng.uniform(0.01, 0.02, K // 32).astype(np.float32)),
+                   ctx.upload(rng.integers(-500, 500, K // 16).astype(np.int32)))
+    outs = {N: ctx.zeros(N * 4) for N in (1024, 2048, 6144, BONSAI_VOCAB)}
+
+    def issue():
+        a = acts[2048]
+        for (q, k, v, o, g, u, d) in layers:
+            for (cm, sm), N in ((q, 2048), (k, 1024), (v, 1024), (o, 2048)):
+                ctx.call("ti_gemv_tern2", *a, cm, sm, outs[N], N, 2048, 0)
+            ctx.call("ti_gateup_silu_tern2", *a, g[0], g[1], u[0], u[1], outs[6144], 6144, 2048)
+            ctx.call("ti_gemv_tern2", *acts[6144], d[0], d[1], outs[2048], 2048, 6144, 0)
+        ctx.call("ti_gemv_tern2", *a, lm[0], lm[1], outs[BONSAI_VOCAB], BONSAI_VOCAB, BONSAI_H, 0)
+
+    g = graph_of(ctx, issue)
+    time_graphs(ctx, [g], 2)
+    ms = time_graphs(ctx, [g], reps)
+    ctx.graph_destroy(g)
+    for mats in layers:
+        for c2, s2 in mats:
+            c2.free()
+            s2.free()
+    nb = BONSAI_LAYERS * sum(N * K * 5 // 16 for N, K in BONSAI_SHAPES) + BONSAI_VOCAB * BONSAI_H * 5 // 16
+    return {"step_us": round(ms * 1e3, 1), "bytes_per_step": nb, "GB_s": round(nb / (ms * 1e-3) / 1e9, 1),
+            "pct_of_hbm_peak": round(100 * nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2), "launches_per_step": 6 * BONSAI_LAYERS + 1,
+            "what": "28 layers (q, k, v, o, gate/up + SiLU, down) + lm_head 151936x2048 in the reference's on-GPU "
+                    "ternary format (2-bit codes, f16 scale per 32), distinct weights"}
+
+
 def bonsai_decode(ctx, contexts=(1024, 8192), steps=64, eager=False):
     """The Bonsai-1.7B ternary decoder (ti_bonsai_*, model.rs's forward) at batch 1: one
     captured decode step (~11 launches per layer) replayed token after token over an f32 KV
@@ -791,11 +843,12 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
-    ap.add_argument("--only", choices=("gemv", "all", "moe", "decode", "decode8", "tern", "bonsai"),
+    ap.add_argument("--only", choices=("gemv", "all", "moe", "decode", "decode8", "tern", "tern2", "bonsai"),
                     default="all",
                     help="gemv: the headline workload only; moe: headline + the int3 MoE leg; "
                          "decode: the Qwen3-1.7B batch-1 decode leg alone, --steps tokens (no headline line); "
-                         "decode8: its batch-8 (T = 8 forward) leg alone; tern: the ternary GEMV step alone; "
+                         "decode8: its batch-8 (T = 8 forward) leg alone; tern: the ternary GEMV step alone; tern2: "
+                         "the same step in the on-GPU ternary format; "
                          "bonsai: the Bonsai decoder alone at --ctx (default 1024) (no headline line)")
     ap.add_argument("--eager", action="store_true", help="--only bonsai: launch the steps directly, without a graph")
     ap.add_argument("--ctx", type=int, nargs="*", default=None,
@@ -817,10 +870,13 @@ def main():
         ctx.close()
         print(json.dumps({"decode_1p7b": res}))
         return
-    if args.only in ("tern", "bonsai"):       # one ternary leg alone, one graph per process (profiling runs)
+    if args.only in ("tern", "tern2", "bonsai"):   # one ternary leg alone, one graph per process (profiling runs)
         if args.only == "tern":
             log("ternary step")
             res = {"ternary_bonsai_step": ternary_step(ctx)}
+        elif args.only == "tern2":
+            log("ternary step, on-GPU format")
+            res = {"ternary_gpu_format_step": tern2_step(ctx)}
         else:
             log("bonsai decode")
             res = {"bonsai_decode": bonsai_decode(ctx, contexts=tuple(args.ctx) if args.ctx else (1024,),
@@ -887,6 +943,8 @@ def main():
         out["gemv_set_1p7b"] = gemv_set_1p7b(ctx, pool, flush)
         log("ternary step")
         out["ternary_bonsai_step"] = ternary_step(ctx)
+        log("ternary step, on-GPU format")
+        out["ternary_gpu_format_step"] = tern2_step(ctx)
         log("int3 MoE")
         out["moe_lfm25_block"] = moe(ctx, flush)
         log("attention")
