@@ -1227,73 +1227,134 @@ __global__ __launch_bounds__(256, 2) void k_attn_fused_q8(AttnFArgs a) {
     attn_merge_tail<HD, G, TPW>(a, hk, w, NS, ntiles, valid, s_red, s_wml, s_ml, s_e, s_L, &s_last);
 }
 
-// head_dim 128 variant of k_attn_fused_q8 with Q K^T on the matrix cores.
-// q (normed and roped, f32) is split per head into three int8 limbs,
-// q = S0*c0 + S1*c1 + S2*c2 with S0 = max|q|/127, S1 = S0/254, S2 = S1/254 (each limb's
-// residual is within half its step, so |c| <= 127 and the representation error is
-// below max|q| * 6.2e-8, the size of f32 rounding). One v_mfma_i32_16x16x32_i8 per
-// 32-dim scale group and 16 tokens gives the exact int32 dots of all limbs:
-//   A (16 x 32): row r = 4*(head) + limb, rows with limb 3 zero, rows 8..15 repeat 0..7;
-//   B (32 x 16): column = token, K = the group's 32 dims; lane l supplies 8 codes of
-//                token l%16 at dims 32g + 8(l/16)..+7. K tiles reach LDS by direct
-//                global->LDS loads in the coalesced row-slice order (8 lanes per 128-byte
-//                token row; the 16-byte slices XOR-permuted by token, passes 1088 bytes
-//                apart, so the 8-byte operand reads hit distinct banks) and are read
-//                back per lane in the MFMA order;
-//   C: lane l holds rows 4(l/16)..+3 of column l%16 = the three limb dots of token l%16
-//      for head (l/16)%2, which it scales by its token's group scale itself.
-// So every lane ends with the score of one (head, token) pair; no code of K is
-// converted on the VALU. P*V stays on the VALU as in k_attn_fused_q8 (4 passes of 8
-// tokens, 16 dims per lane), the probabilities reaching the V lanes by ds_bpermute.
+// head_dim 128 decode attention with both products on the matrix cores.
+//
+// A wave tile is 32 keys. Its K and V codes and its scale rows reach LDS by buffer loads
+// written straight to LDS; the tile's buffer resources start at the tile and end at the
+// last valid key, so no lane clamps its index (keys past the end read as zero, and are
+// masked anyway). In LDS a key row's 16-byte slices are XOR-permuted by (key >> 1) & 7,
+// which leaves both operand reads below free of bank conflicts.
+//  - Q K^T: q (normed and roped, f32) split per head into three int8 limbs,
+//    q = S0*c0 + S1*c1 + S2*c2 with S0 = max|q|/127, S1 = S0/254, S2 = S1/254 (each limb's
+//    residual is within half its step, so |c| <= 127 and the representation error is
+//    below max|q| * 6.2e-8, the size of f32 rounding). Per 32-dim scale group two
+//    v_mfma_i32_16x16x32_i8 accumulate into one result: the first holds the limbs in A
+//    rows 0..7 (row 4 h + limb) against keys 0..15, the second in rows 8..15 against
+//    keys 16..31. So lane l ends with the three limb dots of head (l >> 4) & 1 and key
+//    16 (l >> 5) + (l & 15): one score per lane, in base-2 units (log2 e and
+//    1/(127 sqrt(hd)) ride on the limb scales).
+//  - softmax per head over its 32 lanes, p = 2^(s - m) against the running maximum.
+//  - P V: P'_g = p * vs(key, g), the V scale of the key's 32-dim group g, as f16 hi + lo
+//    (~2^-22 relative), parked in LDS per (head, group, key). A (16 x 32) row
+//    m = 8 (g >> 1) + 4 h + 2 (g & 1) + (hi: 0, lo: 1); B = the V codes of 8 keys per
+//    lane group for 16 dims, transposed by ds_read_b64_tr_b8 and converted to f16
+//    exactly; one v_mfma_f32_16x16x32_f16 per 16 dims. Lane group q holds rows
+//    4q .. 4q+3 = head q & 1, groups 2 (q >> 1) + {0, 1}: the head's outputs at dims
+//    64 (q >> 1) .. +63 are the sums of its hi and lo rows there (the other rows of those
+//    columns pair P' of another group with these dims and are never read).
+//  The head of a lane's scores and of its P V rows is the same ((l >> 4) & 1), so the
+//  rescale by the moved maximum needs no exchange.
+constexpr int PV_WT = 32;                  // keys per wave tile
+constexpr int PV_TB = PV_WT * 128;         // bytes of one tile's K (or V) codes
+constexpr int PV_PH = 640;                 // bytes between the two heads' P' rows (conflict-free stores)
+
+typedef int pv_v4i __attribute__((ext_vector_type(4)));
+typedef int pv_v2i __attribute__((ext_vector_type(2)));
+typedef float pv_f4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void* pv_lds_t;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t pv_rsrc(const void* base, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes > 0 ? bytes : 0, 0x00020000);
+}
+
+// max / sum over the 16 lanes of a row (DPP), every lane receiving the result
+__device__ __forceinline__ float pv_row_max(float v) {
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false)));
+    return v;
+}
+__device__ __forceinline__ float pv_row_sum(float v) {
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
+    return v;
+}
+
 template <int G>
-__global__ __launch_bounds__(256, 2) void k_attn_fused_mq8(AttnFArgs a) {
+__global__ __launch_bounds__(256, 2) void k_attn_fused_pv(AttnFArgs a) {
     static_assert(G == 1 || G == 2, "MFMA decode attention: G <= 2");
-    constexpr int HD = 128;
-    constexpr int LPT = HD / 16;               // lanes per token row in the P*V layout
-    constexpr int TPW = 64 / LPT;              // tokens per P*V pass
-    constexpr int PASSES = 4;
-    constexpr int WT = PASSES * TPW;           // tokens per wave tile (32 = 2 MFMA blocks of 16)
-    constexpr int NG = HD / 32;
-    typedef int v4i __attribute__((ext_vector_type(4)));
+    constexpr int HD = 128, NG = HD / 32;
     __shared__ float s_qmax[2];
-    __shared__ __align__(8) int8_t s_ql[G][3][HD];
+    __shared__ __align__(16) int8_t s_ql[G][3][HD];
     __shared__ __align__(16) uint32_t s_kw[HD / 4];
     __shared__ __align__(16) uint32_t s_vw[HD / 4];
     __shared__ __align__(16) float s_ksc[NG];
-    __shared__ float s_vsc[NG];
-    // per wave: two K tiles (4 passes of 1 KB, 1088 bytes apart so that passes 2b and
-    // 2b+1 sit 64 bytes apart in the banks) during the tile loop, then the wave's P*V
-    // slots for the merge (s_red), which fit in the same bytes
-    constexpr int KT_PASS = 1024 + 64;
-    constexpr int KT_BYTES = 4 * KT_PASS;
-    static_assert(TPW * G * HD * 4 <= 2 * KT_BYTES, "s_red must fit the K tile region");
-    __shared__ __align__(16) uint8_t s_kt[4][2 * KT_BYTES];
-    float (&s_red)[4][TPW][G * HD] = *reinterpret_cast<float (*)[4][TPW][G * HD]>(&s_kt[0][0]);
+    __shared__ __align__(16) float s_vsc[NG];
+    __shared__ __align__(16) uint8_t s_k[4][2][PV_TB];            // [wave][buffer] K tiles
+    __shared__ __align__(16) uint8_t s_v[4][2][PV_TB];            // V tiles
+    __shared__ __align__(16) float s_sc[4][2][2][PV_WT][NG];      // [wave][buffer][K, V][key][group] scales
+    __shared__ __align__(16) uint8_t s_pa[4][2 * PV_PH];          // P' words [head][group][key]: hi | lo << 16
     __shared__ float s_wml[4][G][2];
-    __shared__ float s_ml[G][ATTF_MAXS][2];
-    __shared__ float s_e[G][ATTF_MAXS];
     __shared__ float s_L[G];
     __shared__ int s_last;
+    // after the tile loop: the waves' outputs over the K tiles, the split merge's (m, l)
+    // and weights over the V tiles
+    float (&s_red)[4][1][G * HD] = *reinterpret_cast<float (*)[4][1][G * HD]>(&s_k[0][0][0]);
+    float (&s_ml)[G][ATTF_MAXS][2] = *reinterpret_cast<float (*)[G][ATTF_MAXS][2]>(&s_v[0][0][0]);
+    float (&s_e)[G][ATTF_MAXS] = *reinterpret_cast<float (*)[G][ATTF_MAXS]>(&s_v[1][0][0]);
+    static_assert(4 * G * HD * 4 <= (int)sizeof(s_k) && G * ATTF_MAXS * 8 <= 2 * PV_TB, "merge areas fit the tiles");
 
-    const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int w = blockIdx.x % a.ns;           // split-major across the XCDs (see k_attn_fused_q8)
     const int hk = blockIdx.x / a.ns;
     const int NS = a.ns;
     const int NW = NS * 4;
     const int gw = w * 4 + wave;
-    const int tp = lane / LPT, sl = lane % LPT;   // P*V layout
-    const int tk = lane & 15, kq4 = lane >> 4;     // MFMA layout: token of the block, K quarter
-    const float qk_scale = 1.0f / (127.0f * sqrtf((float)HD));
-    const uint8_t* kqb = reinterpret_cast<const uint8_t*>(a.kq);
-    const float4* ks4 = reinterpret_cast<const float4*>(a.ks);
-    uint8_t* ktw = &s_kt[wave][0];
-    const uint4* vq4 = reinterpret_cast<const uint4*>(a.vq);
+    const int r16 = lane & 15, kq = lane >> 4;    // MFMA lanes: row / column, K quarter
+    const int sh = kq & 1;                        // head of this lane's scores and P V rows
+    const int key_t = 16 * (lane >> 5) + r16;     // key (in the tile) of this lane's score
+    const uint32_t rowb = (uint32_t)a.nKv * HD;   // cache bytes per position (codes)
+    const uint32_t rows16 = (uint32_t)a.nKv * 16; // bytes per position (the 4 group scales)
+    const float l2s = 1.4426950408889634f / (127.0f * sqrtf((float)HD));
+
+    // tile lanes: pass p carries key 8p + lane/8; LDS slot lane%8 of it holds slice
+    // (lane%8) ^ ((key >> 1) & 7). Scale rows in LDS as [K, V][key][group]: the first
+    // tile's by lane (lane < 32 the K row of key lane, else the V row of key lane - 32),
+    // the others' as dwords (lane: key 16j + lane/4, group lane%4).
+    uint32_t toff[4];
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+        const int key = 8 * p + (lane >> 3);
+        toff[p] = (uint32_t)key * rowb + 16u * (uint32_t)((lane & 7) ^ ((key >> 1) & 7));
+    }
+    const uint32_t soff = (uint32_t)(lane & 31) * rows16;
+    const uint32_t soff4[2] = {(uint32_t)(lane >> 2) * rows16 + 4u * (uint32_t)(lane & 3),
+                               (uint32_t)(16 + (lane >> 2)) * rows16 + 4u * (uint32_t)(lane & 3)};
+    const uint8_t* kq_b = reinterpret_cast<const uint8_t*>(a.kq);
+    const uint8_t* vq_b = reinterpret_cast<const uint8_t*>(a.vq);
+    const uint8_t* ks_b = reinterpret_cast<const uint8_t*>(a.ks);
+    const uint8_t* vs_b = reinterpret_cast<const uint8_t*>(a.vs);
+    // the resources of the tile at t0 when positions below lim are valid
+    auto tile_rs = [&](int t0, int lim, __amdgpu_buffer_rsrc_t& rk, __amdgpu_buffer_rsrc_t& rv,
+                       __amdgpu_buffer_rsrc_t& rks, __amdgpu_buffer_rsrc_t& rvs) {
+        const int n = lim - t0;
+        const size_t row0 = (size_t)t0 * a.nKv + hk;
+        const int cb = n > 0 ? (int)((uint32_t)(n - 1) * rowb + HD) : 0;
+        const int sb = n > 0 ? (int)((uint32_t)(n - 1) * rows16 + 16) : 0;
+        rk = pv_rsrc(kq_b + row0 * HD, cb);
+        rv = pv_rsrc(vq_b + row0 * HD, cb);
+        rks = pv_rsrc(ks_b + row0 * 16, sb);
+        rvs = pv_rsrc(vs_b + row0 * 16, sb);
+    };
 
     // ---- every load that does not depend on the position, in one batch. Wave 0 (and 1
     // when G = 2) holds query head `wave`, wave 2 the new K row, wave 3 the new V row;
     // lane L holds elements L and L + 64, so RMSNorm, RoPE and the limb split of q run in
-    // registers (an LDS access before the first tile's direct loads land would wait for them)
+    // registers
     const int pos_dev = *a.dpos;
     const float* xrow = wave < 2 ? a.q + (size_t)(hk * G + (wave < G ? wave : 0)) * HD
                                  : (wave == 2 ? a.k : a.v) + (size_t)hk * HD;
@@ -1302,91 +1363,33 @@ __global__ __launch_bounds__(256, 2) void k_attn_fused_mq8(AttnFArgs a) {
     const float w0 = ti_h2f(nwrow[lane]), w1 = ti_h2f(nwrow[lane + 64]);
     const float c_dev = a.rope_cur[lane], s_dev = a.rope_cur[lane + 64];
     const float c_arg = a.rope_row[lane], s_arg = a.rope_row[lane + 64];
-    float4 ksb[2][2];            // [buffer][block]: the 4 group scales of this lane's MFMA token
-    uint4 vw[2][PASSES];
-    float vsc[2][PASSES];
-    int lim = a.cap;
-    auto load = [&](int buf, int t0) {
-#pragma unroll
-        for (int p = 0; p < PASSES; p++) {   // K: lane (tp, sl) fetches slice sl ^ tp of token p*8 + tp
-            int t = t0 + p * TPW + tp;
-            t = t < lim ? t : lim - 1;
-            const uint8_t* src = kqb + ((size_t)t * a.nKv + hk) * HD + 16 * (sl ^ tp);
-            __builtin_amdgcn_global_load_lds(src, ktw + buf * KT_BYTES + p * KT_PASS, 16, 0, 2);   // aux 2: nt, streamed like the weights
-        }
-#pragma unroll
-        for (int b = 0; b < 2; b++) {
-            int t = t0 + 16 * b + tk;
-            t = t < lim ? t : lim - 1;
-            ksb[buf][b] = ks4[(size_t)t * a.nKv + hk];
-        }
-#pragma unroll
-        for (int p = 0; p < PASSES; p++) {
-            int t = t0 + p * TPW + tp;
-            t = t < lim ? t : lim - 1;
-            vw[buf][p] = ti_ld_nt(vq4 + ((size_t)t * a.nKv + hk) * LPT + sl);
-            vsc[buf][p] = a.vs[((size_t)t * a.nKv + hk) * NG + sl / 2];
-        }
-    };
-    // the first tile's K goes through registers (16-byte row slices, as the direct loads
-    // would place them) and is written to LDS after the prologue: a direct load in flight
-    // makes every wait a full one (their completions are not ordered with other loads),
-    // which would hold the q prologue until the whole first tile had landed
-    uint4 kfirst[PASSES];
+    // the first tile through registers, bounded by the capacity until the context is known
+    // (a load straight to LDS in flight would make the prologue's waits full ones)
+    uint4 kf[4], vf[4], sf;
     {
-        const int t0 = gw * WT;
+        __amdgpu_buffer_rsrc_t rk, rv, rks, rvs;
+        tile_rs(gw * PV_WT, a.cap, rk, rv, rks, rvs);
 #pragma unroll
-        for (int p = 0; p < PASSES; p++) {
-            int t = t0 + p * TPW + tp;
-            t = t < lim ? t : lim - 1;
-            kfirst[p] = ti_ld_nt(reinterpret_cast<const uint4*>(kqb + ((size_t)t * a.nKv + hk) * HD) + sl);
+        for (int p = 0; p < 4; p++) {
+            kf[p] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, toff[p], 0, 2));
+            vf[p] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, toff[p], 0, 2));
         }
-#pragma unroll
-        for (int b = 0; b < 2; b++) {
-            int t = t0 + 16 * b + tk;
-            t = t < lim ? t : lim - 1;
-            ksb[0][b] = ks4[(size_t)t * a.nKv + hk];
-        }
-#pragma unroll
-        for (int p = 0; p < PASSES; p++) {
-            int t = t0 + p * TPW + tp;
-            t = t < lim ? t : lim - 1;
-            vw[0][p] = ti_ld_nt(vq4 + ((size_t)t * a.nKv + hk) * LPT + sl);
-            vsc[0][p] = a.vs[((size_t)t * a.nKv + hk) * NG + sl / 2];
-        }
+        const uint4 sk = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rks, soff, 0, 2));
+        const uint4 sv = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rvs, soff, 0, 2));
+        sf = lane < 32 ? sk : sv;
     }
     TI_ISSUE_FENCE();
 
     const int pos = a.dev ? pos_dev : a.pos;
     const bool valid = pos >= 0 && pos < a.cap;
     const int S = valid ? pos + 1 : 0;
-    const int ntiles = (S + WT - 1) / WT;
+    const int ntiles = (S + PV_WT - 1) / PV_WT;
     const int last_gw = ntiles > 0 ? (ntiles - 1) % NW : -1;
     const bool has_pos = valid && (last_gw >> 2) == w;
-    lim = S > 0 ? S : 1;
-    // the MFMA B operands of a tile from LDS (after its loads have landed); the token at
-    // pos comes from its LDS row instead (it is being written by this launch)
-    auto kops = [&](int buf, int t0, long (&kb)[2][NG]) {
-#pragma unroll
-        for (int b = 0; b < 2; b++) {
-            const int tl = 16 * b + tk, p = tl >> 3, tq = tl & 7;
-            const bool own = has_pos && t0 + tl >= pos;
-#pragma unroll
-            for (int g = 0; g < NG; g++) {
-                const int sl2 = 2 * g + (kq4 >> 1);
-                const uint8_t* src = own ? reinterpret_cast<const uint8_t*>(s_kw) + 16 * sl2 + 8 * (kq4 & 1)
-                                         : ktw + buf * KT_BYTES + p * KT_PASS + 16 * (tq * 8 + (sl2 ^ tq)) + 8 * (kq4 & 1);
-                kb[b][g] = *reinterpret_cast<const long*>(src);
-            }
-            if (own) ksb[buf][b] = *reinterpret_cast<const float4*>(s_ksc);
-        }
-    };
 
     const float cr = a.dev ? c_dev : c_arg, sr = a.dev ? s_dev : s_arg;
-    // RMSNorm in attnPrepQ8's order (slot j + slot j+64, then an exact 32..1 xor tree)
-    // and split-half RoPE, for the q heads and the new K row
     float o0 = x0, o1 = x1;
-    if (wave < 3) {
+    if (wave < 3) {   // RMSNorm in attnPrepQ8's order, split-half RoPE
         float v = x0 * x0 + x1 * x1;
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) v = v + ti_xor(v, o);
@@ -1400,26 +1403,20 @@ __global__ __launch_bounds__(256, 2) void k_attn_fused_mq8(AttnFArgs a) {
         o0 = p00 + p01;
         o1 = p10 + p11;
     }
-    if (has_pos && wave >= 2) {   // this token's K (normed, roped) and V rows, snorm int8, into the cache and LDS
+    if (has_pos && wave >= 2) {   // this token's K (normed, roped) and V rows, snorm int8, into LDS
+        // (into the cache after the tile loop)
         const bool isv = wave == 3;
         const float mx0 = fmaxf(ti_max32_nonneg(fabsf(o0)), 1e-12f);
         const float mx1 = fmaxf(ti_max32_nonneg(fabsf(o1)), 1e-12f);
         const uint32_t wd0 = ti_quad_or(snorm_code(o0, mx0) << (8 * (lane & 3)));
         const uint32_t wd1 = ti_quad_or(snorm_code(o1, mx1) << (8 * (lane & 3)));
-        const size_t rowq = ((size_t)pos * a.nKv + hk) * (HD / 4), rows = ((size_t)pos * a.nKv + hk) * NG;
-        uint32_t* gq = isv ? a.vq : a.kq;
-        float* gs = isv ? a.vs : a.ks;
         uint32_t* lq = isv ? s_vw : s_kw;
         float* lsc = isv ? s_vsc : s_ksc;
         if ((lane & 3) == 0) {
-            gq[rowq + lane / 4] = wd0;
-            gq[rowq + 16 + lane / 4] = wd1;
             lq[lane / 4] = wd0;
             lq[16 + lane / 4] = wd1;
         }
         if ((lane & 31) == 0) {
-            gs[rows + lane / 32] = mx0;
-            gs[rows + 2 + lane / 32] = mx1;
             lsc[lane / 32] = mx0;
             lsc[2 + lane / 32] = mx1;
         }
@@ -1445,154 +1442,205 @@ __global__ __launch_bounds__(256, 2) void k_attn_fused_mq8(AttnFArgs a) {
         if (lane == 0) s_qmax[wave] = qm;
     }
 #pragma unroll
-    for (int p = 0; p < PASSES; p++)   // the first tile's K into LDS buffer 0, slot (tp, sl ^ tp)
-        *reinterpret_cast<uint4*>(ktw + p * KT_PASS + 16 * (tp * 8 + (sl ^ tp))) = kfirst[p];
+    for (int p = 0; p < 4; p++) {   // the first tile into buffer 0, in the order the direct loads use
+        *reinterpret_cast<uint4*>(&s_k[wave][0][p * 1024 + 16 * lane]) = kf[p];
+        *reinterpret_cast<uint4*>(&s_v[wave][0][p * 1024 + 16 * lane]) = vf[p];
+    }
+    *reinterpret_cast<uint4*>(reinterpret_cast<uint8_t*>(&s_sc[wave][0][0][0][0]) + 16 * lane) = sf;
     __syncthreads();
 
-    // ---- the MFMA A operands (row = lane%16: head ah, limb alimb) and this lane's limb scales
-    const int arow = lane & 15;
-    const int ah = G == 2 ? (arow >> 2) & 1 : 0, alimb = arow & 3;
-    const int sh = G == 2 ? (lane >> 4) & 1 : 0;          // head of this lane's scores
-    float Sq[2][3];
+    // ---- score operands: A0 rows 0..7 / A1 rows 8..15 = (head, limb), limb 3 zero; this
+    // lane's K quarter of each group is dims 32g + 8kq .. +7
+    long qa0[NG], qa1[NG];
+    {
+        const int m = r16 & 7, ah = G == 2 ? m >> 2 : 0, al = m & 3;
 #pragma unroll
-    for (int hh = 0; hh < 2; hh++) {
-        const float qm = hh < G ? s_qmax[hh] : 0.0f;
-        Sq[hh][0] = qm / 127.0f;
-        Sq[hh][1] = Sq[hh][0] / 254.0f;
-        Sq[hh][2] = Sq[hh][1] / 254.0f;
-    }
-    long qa[NG];
-#pragma unroll
-    for (int g = 0; g < NG; g++) {
-        const long v = *reinterpret_cast<const long*>(&s_ql[ah][alimb < 3 ? alimb : 0][g * 32 + 8 * kq4]);
-        qa[g] = alimb < 3 ? v : 0;
-    }
-    const float L0 = Sq[sh][0], L1 = Sq[sh][1], L2 = Sq[sh][2];
-
-    float m_run = -3.0e38f, l_lane = 0.0f;   // score lanes: running max of head sh, partial sum of p
-    float acc[G][16], pws[G];                 // P*V lanes
-#pragma unroll
-    for (int hh = 0; hh < G; hh++) {
-        pws[hh] = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 16; i++) acc[hh][i] = 0.0f;
-    }
-
-    auto process = [&](int buf, int t0, const long (&kb)[2][NG]) {
-        if (has_pos && t0 + WT >= S) {   // the tile holding pos: that V row (and clamped reads past it) from LDS
-#pragma unroll
-            for (int p = 0; p < PASSES; p++) {
-                if (t0 + p * TPW + tp >= pos) {
-                    vw[buf][p] = reinterpret_cast<const uint4*>(s_vw)[sl];
-                    vsc[buf][p] = s_vsc[sl / 2];
-                }
-            }
+        for (int g = 0; g < NG; g++) {
+            const long v = *reinterpret_cast<const long*>(&s_ql[ah][al < 3 ? al : 0][g * 32 + 8 * kq]);
+            const long vv = al < 3 ? v : 0;
+            qa0[g] = r16 < 8 ? vv : 0;
+            qa1[g] = r16 < 8 ? 0 : vv;
         }
-        // scores of this lane's (head sh, token tk) in blocks 0 and 1
-        float sc[2];
+    }
+    float L0, L1, L2;
+    {
+        const float qm = s_qmax[G == 2 ? sh : 0];
+        const float S0 = qm / 127.0f, S1 = S0 / 254.0f, S2 = S1 / 254.0f;
+        L0 = S0 * l2s;
+        L1 = S1 * l2s;
+        L2 = S2 * l2s;
+    }
+    // operand offsets in a tile: K of block b (keys 16b..16b+15) and group g for this lane's
+    // key r16 and quarter kq; V (transposing read) of 16-dim block D: lanes 2r, 2r+1 of lane
+    // group kq address key 8kq + r, 8-byte half r16 & 1
+    uint32_t koff[2][NG], voff8[8];
 #pragma unroll
-        for (int b = 0; b < 2; b++) {
-            const float kg[NG] = {ksb[buf][b].x, ksb[buf][b].y, ksb[buf][b].z, ksb[buf][b].w};
-            float d = 0.0f;
+    for (int b = 0; b < 2; b++)
 #pragma unroll
-            for (int g = 0; g < NG; g++) {
-                const v4i z = {0, 0, 0, 0};
-                const v4i c = __builtin_amdgcn_mfma_i32_16x16x32_i8(qa[g], kb[b][g], z, 0, 0, 0);
-                const float lq = fmaf(L2, (float)c[2], fmaf(L1, (float)c[1], L0 * (float)c[0]));
-                d = fmaf(kg[g], lq, d);
-            }
-            sc[b] = t0 + 16 * b + tk < S ? d * qk_scale : -3.0e38f;
+        for (int g = 0; g < NG; g++) {
+            const int key = 16 * b + r16;
+            koff[b][g] = (uint32_t)(key * 128 + 16 * ((2 * g + (kq >> 1)) ^ ((key >> 1) & 7)) + 8 * (kq & 1));
         }
-        // online softmax per head over the 16 lanes of a row (rows 2,3 repeat rows 0,1)
-        float mt = fmaxf(sc[0], sc[1]);
-        mt = fmaxf(mt, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, mt), __builtin_bit_cast(int, mt), 0xB1, 0xF, 0xF, false)));
-        mt = fmaxf(mt, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, mt), __builtin_bit_cast(int, mt), 0x4E, 0xF, 0xF, false)));
-        mt = fmaxf(mt, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, mt), __builtin_bit_cast(int, mt), 0x141, 0xF, 0xF, false)));
-        mt = fmaxf(mt, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, mt), __builtin_bit_cast(int, mt), 0x140, 0xF, 0xF, false)));
+    {
+        const int key = 8 * kq + (r16 >> 1);
+#pragma unroll
+        for (int D = 0; D < 8; D++) voff8[D] = (uint32_t)(key * 128 + 16 * (D ^ ((key >> 1) & 7)) + 8 * (r16 & 1));
+    }
+    // P' words: this lane's (head sh, key key_t) at [sh][g][key_t]; the A row of this lane
+    // (m = r16: g = 2 (m >> 3) + ((m >> 1) & 1), head (m >> 2) & 1, hi/lo m & 1) over keys 8kq..8kq+7
+    const uint32_t pa_w = (uint32_t)(sh * PV_PH + 4 * key_t);
+    const uint32_t pa_r = (uint32_t)(((r16 >> 2) & 1) * PV_PH + (2 * (r16 >> 3) + ((r16 >> 1) & 1)) * 128 + 32 * kq);
+    const uint32_t psel = (r16 & 1) ? 0x07060302u : 0x05040100u;   // the lo or hi halves of two words
+    const bool pa_zero = G == 1 && sh == 1;                           // rows of a head that is not there
+
+    float m_run = -3.0e38f, l_lane = 0.0f;
+    pv_f4 O[8];
+#pragma unroll
+    for (int D = 0; D < 8; D++) O[D] = pv_f4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    auto process = [&](int b, int t0) {
+        const uint8_t* kt = &s_k[wave][b][0];
+        const uint8_t* vt = &s_v[wave][b][0];
+        uint8_t* pa = &s_pa[wave][0];
+        const float4 kg = *reinterpret_cast<const float4*>(&s_sc[wave][b][0][key_t][0]);
+        const float4 vg = *reinterpret_cast<const float4*>(&s_sc[wave][b][1][key_t][0]);
+        const float kgs[NG] = {kg.x, kg.y, kg.z, kg.w};
+        const float vgs[NG] = {vg.x, vg.y, vg.z, vg.w};
+        float d = 0.0f;
+#pragma unroll
+        for (int g = 0; g < NG; g++) {
+            const long k0 = *reinterpret_cast<const long*>(kt + koff[0][g]);
+            const long k1 = *reinterpret_cast<const long*>(kt + koff[1][g]);
+            pv_v4i c = {0, 0, 0, 0};
+            c = __builtin_amdgcn_mfma_i32_16x16x32_i8(qa0[g], k0, c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_i32_16x16x32_i8(qa1[g], k1, c, 0, 0, 0);
+            const float lq = fmaf(L2, (float)c[2], fmaf(L1, (float)c[1], L0 * (float)c[0]));
+            d = fmaf(kgs[g], lq, d);
+        }
+        const bool live = t0 + key_t < S;
+        const float s2 = live ? d : -3.0e38f;
+        // the head's 32 lanes: r16 + 16 {sh, sh + 2}
+        float mt = pv_row_max(s2);
+        mt = fmaxf(mt, ti_xor(mt, 32));
         const float mn = fmaxf(m_run, mt);
-        const float corr = expf(m_run - mn);
+        const float corr = __builtin_amdgcn_exp2f(m_run - mn);
         m_run = mn;
-        float pe[2];
+        const float p = live ? __builtin_amdgcn_exp2f(s2 - mn) : 0.0f;
+        l_lane = fmaf(l_lane, corr, p);
+        if (__any(corr != 1.0f)) {   // a head's maximum moved: rescale its rows
 #pragma unroll
-        for (int b = 0; b < 2; b++) pe[b] = t0 + 16 * b + tk < S ? expf(sc[b] - mn) : 0.0f;
-        l_lane = fmaf(l_lane, corr, pe[0] + pe[1]);
-        // P*V: rescale only when a head's maximum moved (wave-uniform test)
-        const float c0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, corr), 0));
-        const float c1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, corr), 16));
-        const float cs[2] = {c0, c1};
-#pragma unroll
-        for (int hh = 0; hh < G; hh++) {
-            if (cs[hh] != 1.0f) {
-                pws[hh] *= cs[hh];
-#pragma unroll
-                for (int i = 0; i < 16; i++) acc[hh][i] *= cs[hh];
-            }
+            for (int D = 0; D < 8; D++) O[D] *= corr;
         }
+        // P'_g as f16 hi | lo << 16 (keys past the context: exactly 0, whatever their scale holds)
 #pragma unroll
-        for (int p = 0; p < PASSES; p++) {
-            const bool live = t0 + p * TPW + tp < S;
-            const int src = (p & 1) * TPW + tp;          // lane of this token's score in head 0; head 1 is +16
-            const uint32_t ww[4] = {vw[buf][p].x ^ 0x80808080u, vw[buf][p].y ^ 0x80808080u,
-                                    vw[buf][p].z ^ 0x80808080u, vw[buf][p].w ^ 0x80808080u};
+        for (int g = 0; g < NG; g++) {
+            const float pv = (live && !pa_zero) ? p * vgs[g] : 0.0f;
+            const _Float16 hi = (_Float16)pv;
+            const _Float16 lo = (_Float16)(pv - (float)hi);
+            *reinterpret_cast<uint32_t*>(pa + pa_w + 128 * g) =
+                (uint32_t)__builtin_bit_cast(uint16_t, hi) | ((uint32_t)__builtin_bit_cast(uint16_t, lo) << 16);
+        }
+        // the other lanes' P' words: one wave's LDS accesses complete in order
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const uint4 wa = *reinterpret_cast<const uint4*>(pa + pa_r);
+        const uint4 wb = *reinterpret_cast<const uint4*>(pa + pa_r + 16);
+        const uint4 ap = make_uint4(__builtin_amdgcn_perm(wa.y, wa.x, psel), __builtin_amdgcn_perm(wa.w, wa.z, psel),
+                                    __builtin_amdgcn_perm(wb.y, wb.x, psel), __builtin_amdgcn_perm(wb.w, wb.z, psel));
+        const ti_h8 A = __builtin_bit_cast(ti_h8, ap);
 #pragma unroll
-            for (int hh = 0; hh < G; hh++) {
-                const float pv = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(4 * (src + 16 * hh), __builtin_bit_cast(int, pe[p >> 1])));
-                const float pw = live ? pv * vsc[buf][p] * (1.0f / 127.0f) : 0.0f;
-                pws[hh] += pw;
-#pragma unroll
-                for (int i = 0; i < 16; i++) acc[hh][i] = fmaf(pw, ub(ww[i >> 2], i & 3), acc[hh][i]);
-            }
+        for (int D = 0; D < 8; D++) {
+            const pv_v2i vb = __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) pv_v2i*)(vt + voff8[D]));
+            O[D] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, ti_i8x8_h8((uint32_t)vb.x, (uint32_t)vb.y), O[D], 0, 0, 0);
         }
     };
-    // every memory operation in flight at the top of an iteration belongs to the tile
-    // about to be processed: wait for all of them, read its K operands out of LDS, then
-    // start the next tile's loads (into the other LDS buffer) and compute
-    const int step = NW * WT;
-    int t0 = gw * WT;
-    long kb[2][NG];
+    // the tile holding pos: that key's rows from the prologue's LDS copy (this launch writes
+    // them to the cache)
+    auto own_row = [&](int b, int t0) {
+        const int i = pos - t0, swz = (i >> 1) & 7;
+        if (lane < 8) {
+            *reinterpret_cast<uint4*>(&s_k[wave][b][i * 128 + 16 * (lane ^ swz)]) = reinterpret_cast<const uint4*>(s_kw)[lane];
+        } else if (lane < 16) {
+            *reinterpret_cast<uint4*>(&s_v[wave][b][i * 128 + 16 * ((lane - 8) ^ swz)]) = reinterpret_cast<const uint4*>(s_vw)[lane - 8];
+        } else if (lane == 16) {
+            *reinterpret_cast<float4*>(&s_sc[wave][b][0][i][0]) = *reinterpret_cast<const float4*>(s_ksc);
+        } else if (lane == 17) {
+            *reinterpret_cast<float4*>(&s_sc[wave][b][1][i][0]) = *reinterpret_cast<const float4*>(s_vsc);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+    auto load_tile = [&](int b, int t0) {
+        __amdgpu_buffer_rsrc_t rk, rv, rks, rvs;
+        tile_rs(t0, S, rk, rv, rks, rvs);
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (pv_lds_t)&s_k[wave][b][p * 1024], 16, toff[p], 0, 0, 2);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (pv_lds_t)&s_v[wave][b][p * 1024], 16, toff[p], 0, 0, 2);
+        }
+        // scale rows as dwords (one resource per instruction: a lane-dependent choice of
+        // resource would become a loop over the distinct values)
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rks, (pv_lds_t)&s_sc[wave][b][0][16 * j][0], 4, soff4[j], 0, 0, 2);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rvs, (pv_lds_t)&s_sc[wave][b][1][16 * j][0], 4, soff4[j], 0, 0, 2);
+        }
+    };
+
+    // every memory operation in flight at the top of an iteration belongs to the tile about
+    // to be processed: wait for all of them, then start the next tile's loads into the
+    // other buffer and compute (measured: a second tile in flight per wave, through
+    // registers, is slower)
+    const int step = NW * PV_WT;
+    int t0 = gw * PV_WT;
     while (t0 < S) {
         __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
         TI_ISSUE_FENCE();
-        kops(0, t0, kb);
+        if (has_pos && pos >= t0 && pos < t0 + PV_WT) own_row(0, t0);
         int nt = t0 + step;
-        if (nt < S) load(1, nt);
-        process(0, t0, kb);
+        if (nt < S) load_tile(1, nt);
+        process(0, t0);
         if (nt >= S) break;
         t0 = nt;
         __builtin_amdgcn_s_waitcnt(0x0F70);
         TI_ISSUE_FENCE();
-        kops(1, t0, kb);
+        if (has_pos && pos >= t0 && pos < t0 + PV_WT) own_row(1, t0);
         nt = t0 + step;
-        if (nt < S) load(0, nt);
-        process(1, t0, kb);
+        if (nt < S) load_tile(0, nt);
+        process(1, t0);
         t0 = nt;
     }
-    __syncthreads();   // the K tile region becomes s_red: no wave of this workgroup still reads its tiles
+    if (has_pos && wave >= 2) {   // the new K / V row into the cache, from LDS
+        const bool isv = wave == 3;
+        const size_t rowq = ((size_t)pos * a.nKv + hk) * (HD / 4), rows = ((size_t)pos * a.nKv + hk) * NG;
+        if (lane < HD / 4) (isv ? a.vq : a.kq)[rowq + lane] = (isv ? s_vw : s_kw)[lane];
+        if (lane < NG) (isv ? a.vs : a.ks)[rows + lane] = (isv ? s_vsc : s_ksc)[lane];
+    }
+    __syncthreads();   // the tiles become s_red: no wave still reads them
 
-    // wave state -> LDS: P*V slots with the +128 offset removed; (m, l) of each head
+    // wave state -> LDS: lane group q holds head q & 1 at dims 16 D + r16, D = 4 (q >> 1) + j,
+    // as its rows 2 (j >> 1) (hi) and 2 (j >> 1) + 1 (lo); then (m, l) of each head in
+    // natural-log units
     {
-        float l16 = l_lane;
-        l16 += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, l16), __builtin_bit_cast(int, l16), 0xB1, 0xF, 0xF, false));
-        l16 += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, l16), __builtin_bit_cast(int, l16), 0x4E, 0xF, 0xF, false));
-        l16 += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, l16), __builtin_bit_cast(int, l16), 0x141, 0xF, 0xF, false));
-        l16 += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, l16), __builtin_bit_cast(int, l16), 0x140, 0xF, 0xF, false));
+        float l32 = pv_row_sum(l_lane);
+        l32 += ti_xor(l32, 32);
+        const bool upper = kq >= 2;
 #pragma unroll
-        for (int hh = 0; hh < G; hh++) {
-            const float mh = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, m_run), 16 * hh));
-            const float lh = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, l16), 16 * hh));
-            float4* dst = reinterpret_cast<float4*>(&s_red[wave][tp][hh * HD + sl * 16]);
-            const float off = 128.0f * pws[hh];
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-                dst[i] = make_float4(acc[hh][4 * i] - off, acc[hh][4 * i + 1] - off, acc[hh][4 * i + 2] - off,
-                                     acc[hh][4 * i + 3] - off);
-            if (lane == 0) {
-                s_wml[wave][hh][0] = mh;
-                s_wml[wave][hh][1] = lh;
-            }
+        for (int j = 0; j < 4; j++) {
+            const int i0 = 2 * (j >> 1);
+            const float hi = upper ? O[4 + j][i0] : O[j][i0];
+            const float lo = upper ? O[4 + j][i0 + 1] : O[j][i0 + 1];
+            const int D = 4 * (kq >> 1) + j;
+            if (sh < G) s_red[wave][0][sh * HD + 16 * D + r16] = (hi + lo) * (1.0f / 127.0f);
+        }
+        if (sh < G && r16 == 0 && kq < 2) {
+            s_wml[wave][sh][0] = m_run * 0.6931471805599453f;
+            s_wml[wave][sh][1] = l32;
         }
     }
-    attn_merge_tail<HD, G, TPW>(a, hk, w, NS, ntiles, valid, s_red, s_wml, s_ml, s_e, s_L, &s_last);
+    attn_merge_tail<HD, G, 1>(a, hk, w, NS, ntiles, valid, s_red, s_wml, s_ml, s_e, s_L, &s_last);
 }
 }  // namespace
 
@@ -1630,8 +1678,8 @@ int ti_attn_fused_launch(ti_ctx* c, const float* q, const float* k, const float*
 #define AF(HD_, G_) \
     if (hd == HD_ && G == G_) { k_attn_fused_q8<HD_, G_><<<grid, 256, 0, c->stream>>>(a); TI_LAUNCHED("k_attn_fused_q8"); return TI_OK; }
     // head_dim 128 (the Qwen3 heads): Q K^T on the matrix cores
-    if (hd == 128 && G == 2) { k_attn_fused_mq8<2><<<grid, 256, 0, c->stream>>>(a); TI_LAUNCHED("k_attn_fused_mq8"); return TI_OK; }
-    if (hd == 128 && G == 1) { k_attn_fused_mq8<1><<<grid, 256, 0, c->stream>>>(a); TI_LAUNCHED("k_attn_fused_mq8"); return TI_OK; }
+    if (hd == 128 && G == 2) { k_attn_fused_pv<2><<<grid, 256, 0, c->stream>>>(a); TI_LAUNCHED("k_attn_fused_pv"); return TI_OK; }
+    if (hd == 128 && G == 1) { k_attn_fused_pv<1><<<grid, 256, 0, c->stream>>>(a); TI_LAUNCHED("k_attn_fused_pv"); return TI_OK; }
     AF(64, 2) AF(64, 1)
 #undef AF
     return ti_fail(TI_ERR_INVALID, "fused attention: no kernel for hd=%d group=%d", hd, G);

@@ -34,8 +34,7 @@
 
 namespace {
 
-typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef ti_h8 h8;
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef int v2i __attribute__((ext_vector_type(2)));
 
@@ -66,28 +65,6 @@ struct TAttnArgs {
     float eps;
     int RT;                // row tiles: workgroups (hk, rt, split) serve rows 16 rt .. 16 rt + 15
 };
-
-// 4 int8 codes -> f16 pairs, exactly: the biased byte (code + 128) below an 0x64 high
-// byte is the f16 1024 + code + 128, and one packed f16 subtraction removes the 1152
-__device__ __forceinline__ void i8x4_to_h2x2(uint32_t w, h2& a, h2& b) {
-    const uint32_t u = w ^ 0x80808080u;
-    // v_perm_b32: selector bytes 0-3 pick the second operand's bytes, 4-7 the first's
-    const uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);   // [u0, 64, u1, 64]
-    const uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);   // [u2, 64, u3, 64]
-    const h2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
-    a = __builtin_bit_cast(h2, p0) - bias;
-    b = __builtin_bit_cast(h2, p1) - bias;
-}
-
-// 8 int8 codes (two words, byte e = element e) -> f16, assembled as four packed words
-__device__ __forceinline__ h8 i8x8_to_h8(uint32_t lo, uint32_t hi) {
-    h2 a, b, c, d;
-    i8x4_to_h2x2(lo, a, b);
-    i8x4_to_h2x2(hi, c, d);
-    const uint4 w = make_uint4(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b),
-                               __builtin_bit_cast(uint32_t, c), __builtin_bit_cast(uint32_t, d));
-    return __builtin_bit_cast(h8, w);
-}
 
 // RMSNorm in the reference's order for a head row held as (element L, element L+64) by
 // the 64 lanes (slot j + slot j+64, then an exact 32..1 xor tree), then split-half RoPE
@@ -309,7 +286,7 @@ __global__ __launch_bounds__(64 * TA_W) void k_attn_tq8(TAttnArgs a) {
 #pragma unroll
             for (int g = 0; g < NG; g++) {
                 const uint2 kw2 = *reinterpret_cast<const uint2*>(kt + (16 * b + r16) * TA_KS + 32 * g + 8 * jq);
-                const h8 ka = i8x8_to_h8(kw2.x, kw2.y);
+                const h8 ka = ti_i8x8_h8(kw2.x, kw2.y);
                 const f4 z = {0.0f, 0.0f, 0.0f, 0.0f};
                 f4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qh[g], z, 0, 0, 0);
                 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql[g], d, 0, 0, 0);
@@ -386,7 +363,7 @@ __global__ __launch_bounds__(64 * TA_W) void k_attn_tq8(TAttnArgs a) {
         for (int D = 0; D < 8; D++) {
             const v2i vb = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
                 (__attribute__((address_space(3))) v2i*)(vrow + 16 * D));
-            const h8 vh = i8x8_to_h8((uint32_t)vb.x, (uint32_t)vb.y);
+            const h8 vh = ti_i8x8_h8((uint32_t)vb.x, (uint32_t)vb.y);
             O[D] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph[D >> 1], vh, O[D], 0, 0, 0);
             O[D] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl[D >> 1], vh, O[D], 0, 0, 0);
         }

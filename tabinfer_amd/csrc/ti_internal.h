@@ -105,6 +105,29 @@ __device__ __forceinline__ uint4 ti_ld_nt(const uint4* p) {
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// 8 int8 codes (two words, byte e = element e) -> 8 f16 values, exactly: the biased byte
+// (code + 128) under an 0x64 high byte is the f16 1024 + code + 128 (one v_perm_b32 per
+// two codes; selector bytes 0-3 pick the second operand's bytes, 4-7 the first's), and a
+// packed f16 subtraction removes the 1152.
+typedef _Float16 ti_h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 ti_h2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void ti_i8x4_h2x2(uint32_t w, ti_h2& a, ti_h2& b) {
+    const uint32_t u = w ^ 0x80808080u;
+    const uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);   // [u0, 64, u1, 64]
+    const uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);   // [u2, 64, u3, 64]
+    const ti_h2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+    a = __builtin_bit_cast(ti_h2, p0) - bias;
+    b = __builtin_bit_cast(ti_h2, p1) - bias;
+}
+__device__ __forceinline__ ti_h8 ti_i8x8_h8(uint32_t lo, uint32_t hi) {
+    ti_h2 a, b, c, d;
+    ti_i8x4_h2x2(lo, a, b);
+    ti_i8x4_h2x2(hi, c, d);
+    const uint4 w = make_uint4(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b),
+                               __builtin_bit_cast(uint32_t, c), __builtin_bit_cast(uint32_t, d));
+    return __builtin_bit_cast(ti_h8, w);
+}
+
 // Keep every memory operation issued so far above this point: the scheduler may
 // otherwise sink a kernel's weight loads below the wait for its activation loads,
 // which serialises two memory round trips that were meant to overlap.
