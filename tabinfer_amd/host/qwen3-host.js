@@ -7,11 +7,16 @@
 // the host, captured once into a HIP graph and replayed per token (the reference's
 // GPU-resident token chaining, models/qwen3.js:3951-3959 and decodeLoop :4414-4435).
 //
-// Tokenization is not part of this path: loadModel({tokenizer}) takes an object with
-// encodeChat(messages) -> ids, decode(ids) -> string and isStop(id) -> bool (the
-// reference's TOK); without one, prompts are arrays of token ids and decode() returns them.
+// Tokenization: loadModel({tokenizer}) takes a path to a local tokenizer.json (or its
+// directory; tokenizer.js, the reference's TOK), or any object with encodeChat(messages)
+// -> ids, decode(ids) -> string and isStop(id) -> bool; with neither, the tokenizer.json
+// beside the safetensors file is used when there is one, else prompts are arrays of token
+// ids and decode() returns them.
 const fs = require('fs');
+const path = require('path');
 const { createEngine, bf16ToF16bits, f32ToF16 } = require('./ti-engine');
+const { loadTokenizer } = require('./tokenizer');
+const QC = require('./quant-cache');
 
 // models/qwen3.js CONFIGS (Qwen3-0.6B / 1.7B geometry)
 const CONFIGS = {
@@ -102,6 +107,19 @@ function renderMessage(m) {
   return { role: m.role, content: c };
 }
 
+// The system-prompt KV anchor's decision (models/qwen3.js:5378-5389): may a conversation whose
+// prompt `ids` begins with the system block `sysIds` take KV rows [0, P) as they stand?
+// Only when the block is long enough (16 tokens), the live prefix cache does not already
+// cover it, and the anchor records exactly this block.
+function claimSystemBlock(ids, sysIds, cachedIds, anchorIds) {
+  if (!sysIds || sysIds.length < 16) return false;
+  const P = sysIds.length;
+  const covers = (a, n) => { if (!a || a.length < n) return false; for (let i = 0; i < n; i++) if (a[i] !== sysIds[i]) return false; return true; };
+  if (!covers(ids, P)) return false;
+  if (covers(cachedIds, P)) return false;
+  return !!anchorIds && anchorIds.length === P && covers(anchorIds, P);
+}
+
 // ---- the model ----------------------------------------------------------------------------------
 function createQwen3Host({ device = 0 } = {}) {
   const eng = createEngine({ device });
@@ -115,6 +133,8 @@ function createQwen3Host({ device = 0 } = {}) {
   let _cachedIds = null; // prefix cache: the ids whose KV rows are resident
   let _toolRunner = null;
   let _lastGenStats = null;
+  let _lastLoadCached = false;
+  let _sysAnchor = null; // {ids}: KV rows [0, ids.length) hold this system block (:5363-5395)
 
   function tensorNames(cfg) {
     const names = ['model.embed_tokens.weight', 'model.norm.weight', 'lm_head.weight'];
@@ -198,21 +218,85 @@ function createQwen3Host({ device = 0 } = {}) {
     }
   }
 
-  // loadModel({variant, nCtx, config, safetensors, random, tokenizer, onProgress})
-  // (models/qwen3.js:3719): allocates the decoder for `nCtx` positions and fills it
+  // the tensors of the decoder as quant-cache segments, in stream order
+  function cacheSegments() {
+    const segs = [];
+    for (const name of tensorNames(C)) {
+      const t = TI.qwen3_tensor(M, name);
+      if (t.scales) {
+        const K = name.endsWith('down_proj.weight') ? C.intermediate : name.endsWith('o_proj.weight') ? C.n_heads * C.head_dim : C.hidden;
+        const N = t.dataBytes * 2 / K;
+        const meta = { kind: 'int4', shape: [N, K], numel: N * K, N, K };
+        segs.push(Object.assign({ name, role: 'pack', len: t.dataBytes, buf: t.data }, meta));
+        segs.push(Object.assign({ name, role: 'scales', len: t.scaleBytes, buf: t.scales }, meta));
+      } else {
+        const numel = t.dataBytes / 2;
+        const shape = name === 'model.embed_tokens.weight' ? [C.vocab, C.hidden] : [numel];
+        segs.push({ name, role: 'buf', len: t.dataBytes, buf: t.data, kind: 'f16', shape, numel });
+      }
+    }
+    return segs;
+  }
+
+  // the fast load (models/qwen3.js:3675-3717): every segment of a valid cache written
+  // straight into the decoder's buffers; false when the directory holds no usable cache
+  function loadQuantCache(dir, variant, onProgress) {
+    const bufs = new Map(cacheSegments().map((s) => [s.name + '.' + s.role, s]));
+    return QC.readQuantCache(dir, variant, C, (seg, off, bytes) => E.writeBuffer(bufs.get(seg.name + '.' + seg.role).buf, off, bytes), {
+      onProgress,
+      check: (seg) => {
+        const mine = bufs.get(seg.name + '.' + seg.role);
+        if (!mine || mine.len !== seg.len) throw new Error('quant cache: segment ' + seg.name + '.' + seg.role + ' does not fit this model');
+      },
+    });
+  }
+
+  // the writer (:3629-3664): the quantized bytes read back from the GPU, one tensor at a time
+  function writeQuantCache(dir, variant) {
+    E.sync();
+    return QC.writeQuantCache(dir, variant, C, cacheSegments(), (seg) => new Uint8Array(E.readBytes(seg.buf, 0, seg.len)));
+  }
+
+  // loadModel({variant, nCtx, config, safetensors, random, tokenizer, quantCache, onProgress})
+  // (models/qwen3.js:3719): allocates the decoder for `nCtx` positions and fills it. With
+  // quantCache (a directory), a valid cache of this variant and geometry is loaded instead
+  // of the checkpoint; after a checkpoint load the cache is (re)written. A cache that
+  // cannot be read falls back to the checkpoint (:3752-3759); a failed write only warns.
   async function loadModel(opts = {}) {
     if (M && !opts.reload) return;
     if (M) unload();
     const base = opts.config || CONFIGS[opts.variant || '0.6B'];
     if (!base) throw new Error('loadModel: unknown variant ' + opts.variant);
+    const variant = opts.variant || (opts.config ? 'custom' : '0.6B');
     const maxCtx = opts.nCtx || base.max_ctx || 4096;
     const chunk = Math.max(1, Math.min(PREFILL_CHUNK, Math.floor(ATTN_ROWS / base.n_heads), maxCtx));
     C = Object.assign({ rope_theta: 1e6, rms_eps: 1e-6 }, base, { max_ctx: maxCtx, max_tokens: chunk });
     M = TI.qwen3_create(ctx, C);
     _temp = 0;                           // a new decoder samples greedily until told otherwise
-    TOK = opts.tokenizer || null;
-    if (opts.safetensors) loadWeights([].concat(opts.safetensors), opts.onProgress);
-    else if (opts.random != null) randomWeights(opts.random);
+    _sysAnchor = null;
+    TOK = typeof opts.tokenizer === 'string' ? loadTokenizer(opts.tokenizer) : (opts.tokenizer || null);
+    if (!TOK && opts.safetensors) {
+      const beside = path.join(path.dirname([].concat(opts.safetensors)[0]), 'tokenizer.json');
+      if (fs.existsSync(beside)) TOK = loadTokenizer(beside);
+    }
+    let cached = false;
+    if (opts.quantCache) {
+      try { cached = loadQuantCache(opts.quantCache, variant, opts.onProgress); } catch (e) {
+        console.warn('[qwen3] quant cache load failed, loading the checkpoint:', (e && e.message) || e);
+      }
+    }
+    if (!cached) {
+      if (opts.safetensors) {
+        loadWeights([].concat(opts.safetensors), opts.onProgress);
+        if (opts.quantCache) {
+          try { writeQuantCache(opts.quantCache, variant); } catch (e) {
+            console.warn('[qwen3] quant cache write failed (the next load quantizes again):', (e && e.message) || e);
+          }
+        }
+      } else if (opts.random != null) randomWeights(opts.random);
+    }
+    E.sync();
+    _lastLoadCached = cached;
     _devPos = -1;
     _cachedIds = null;
   }
@@ -245,8 +329,15 @@ function createQwen3Host({ device = 0 } = {}) {
     return { logprob: logits[tok] - lz, alts: idx.map((i) => ({ id: i, logprob: logits[i] - lz })), entropy: ent };
   }
 
-  // forward(idsArray, posBase, {chain, submitOnly, logprobs}) -> next token id (:3938)
+  // forward(idsArray, posBase, {chain, submitOnly, logprobs}) -> next token id (:3938).
+  // A caller's forward may overwrite any KV rows, so it drops the prefix caches; the
+  // host's own prefill goes through fwd, which keeps them.
   async function forward(idsArray, posBase, opts) {
+    _cachedIds = null;
+    _sysAnchor = null;
+    return fwd(idsArray, posBase, opts);
+  }
+  async function fwd(idsArray, posBase, opts) {
     need();
     const chain = !!(opts && opts.chain), submitOnly = !!(opts && opts.submitOnly);
     setTemp(opts && opts.temp > 0 ? +opts.temp : 0);   // :4052, Gumbel-max in the lm_head
@@ -323,6 +414,9 @@ function createQwen3Host({ device = 0 } = {}) {
     return TOK.encodeChat(typeof x === 'string' ? [{ role: 'user', content: x }] : x);
   }
   const decode = (ids) => (TOK ? TOK.decode(ids) : ids.slice());
+  // the text each emitted token completes (a tokenizer without a stream decoder: its decode of the token)
+  const textStream = () => (TOK && TOK.streamDecoder ? TOK.streamDecoder()
+    : { push: (t) => (TOK ? TOK.decode([t]) : String(t)), flush: () => '' });
   const isStop = (t) => !!(TOK && TOK.isStop && TOK.isStop(t));
 
   // prefill ids[from..L) in chunks of up to PREFILL_CHUNK (C.max_tokens); returns the token
@@ -332,7 +426,7 @@ function createQwen3Host({ device = 0 } = {}) {
     for (let off = from; off < ids.length; off += C.max_tokens) {
       if (signal && signal.aborted) throw abortError();
       const last = off + C.max_tokens >= ids.length;
-      tok = await forward(ids.slice(off, Math.min(off + C.max_tokens, ids.length)), off, last && temp ? { temp } : undefined);
+      tok = await fwd(ids.slice(off, Math.min(off + C.max_tokens, ids.length)), off, last && temp ? { temp } : undefined);
     }
     return tok;
   }
@@ -348,6 +442,7 @@ function createQwen3Host({ device = 0 } = {}) {
     need();
     const temp = temperature > 0 ? +temperature : 0;
     _cachedIds = null;
+    _sysAnchor = null;                   // the one-shot path prefills from position 0 (:4540)
     const ids = encode(prompt);
     const L = ids.length;
     checkFits(L);
@@ -357,13 +452,15 @@ function createQwen3Host({ device = 0 } = {}) {
     _lastGenStats = { prefillTokens: L, prefillMs: ms, prefillTps: +(L / Math.max(ms, 1e-3) * 1000).toFixed(1) };
     if (onStats) { try { onStats(_lastGenStats); } catch (_) { /* caller's hook */ } }
     const out = [];
+    const sd = textStream();
     const emit = (t) => {
       if (isStop(t)) return false;
       out.push(t);
-      if (onToken) { try { onToken(TOK ? TOK.decode([t]) : t); } catch (_) { /* caller's hook */ } }
+      if (onToken) { const x = TOK ? sd.push(t) : t; if (x !== '') { try { onToken(x); } catch (_) { /* caller's hook */ } } }
       return true;
     };
     if (emit(tok0)) await decodeLoop(L, maxTokens, emit, signal, () => out.length, temp);
+    if (onToken && TOK) { const x = sd.flush(); if (x) { try { onToken(x); } catch (_) { /* caller's hook */ } } }
     return decode(out);
   }
 
@@ -408,15 +505,36 @@ function createQwen3Host({ device = 0 } = {}) {
     let lcp = 0;
     if (_cachedIds) { const n = Math.min(_cachedIds.length, L - 1); while (lcp < n && _cachedIds[lcp] === ids[lcp]) lcp++; }
     _cachedIds = null;   // from here on rows lcp.. are being overwritten
-    const tok0 = await prefill(ids, lcp, signal, temp);
+    if (_sysAnchor && lcp < _sysAnchor.ids.length) _sysAnchor = null;
+    let tok0;
+    try { tok0 = await prefill(ids, lcp, signal, temp); } catch (e) {
+      _sysAnchor = null;                 // the KV prefix is now partial (:5257-5259)
+      throw e;
+    }
     const out = [];
-    const emitTok = (t) => { if (isStop(t)) return false; out.push(t); if (onToken) onToken(TOK ? TOK.decode([t]) : String(t)); return true; };
+    const sd = textStream();
+    const emitTok = (t) => { if (isStop(t)) return false; out.push(t); if (onToken) { const x = sd.push(t); if (x) onToken(x); } return true; };
     if (emitTok(tok0)) await decodeLoop(L, maxTokens, emitTok, signal, () => out.length, temp);
+    if (onToken) { const x = sd.flush(); if (x) onToken(x); }
     // Rows [0, L) hold the prompt. The step at position L + j wrote the row of out[j] and
     // produced out[j + 1], so rows exist for out[0 .. n-2]; the last emitted token's row
     // is written only if a later step ran, which a stop at maxTokens or the cache end skips.
     _cachedIds = ids.concat(out.slice(0, Math.max(0, out.length - 1)));
     return out;
+  }
+
+  // The system-prompt KV anchor (:5363-5395): after round 0 of a conversation, KV rows
+  // [0, P) hold the system block (system prompt + tool preamble, P tokens, no generation
+  // prompt); a later conversation with the same system block whose prefix cache no longer
+  // covers it claims those rows instead of prefilling them again. Any prefill that starts
+  // below P drops the anchor first (its rows are being rewritten); a successful round 0
+  // records it again.
+  const startsWith = (ids, pre) => !!pre && ids.length >= pre.length && pre.every((t, i) => ids[i] === t);
+  function sysCacheClaim(ids, sysIds, emit) {
+    if (!claimSystemBlock(ids, sysIds, _cachedIds, _sysAnchor && _sysAnchor.ids)) return false;
+    _cachedIds = sysIds;
+    emit({ type: 'info', message: 'Using cached system prompt…' });
+    return true;
   }
 
   // runConversation({provider, messages, systemPrompt, tools, convId, signal}, emit) (:5397-5522):
@@ -437,6 +555,7 @@ function createQwen3Host({ device = 0 } = {}) {
     if (pre) sys = sys ? sys + '\n\n' + pre : pre;
     const work = [];
     if (sys) work.push({ role: 'system', content: sys });
+    const sysIds = sys ? TOK.encodeChat([{ role: 'system', content: sys }], { addGenerationPrompt: false }) : null;
     for (const m of (messages || [])) if (m && m.role) work.push(renderMessage(m));
     const MAX_ROUNDS = toolList.length ? 8 : 1;
     try {
@@ -448,7 +567,9 @@ function createQwen3Host({ device = 0 } = {}) {
         const parser = makeRoundParser((rz) => { clearInfo(); emit({ type: 'delta', delta: { reasoning: rz } }); },
           (ct) => { clearInfo(); emit({ type: 'delta', delta: { content: ct } }); });
         const ids = TOK.encodeChat(work);
+        if (round === 0) sysCacheClaim(ids, sysIds, emit);
         await streamIds(ids, { maxTokens, signal, onToken: (t) => parser.push(t) });
+        if (round === 0) _sysAnchor = sysIds && sysIds.length >= 16 && startsWith(ids, sysIds) ? { ids: sysIds } : null;
         parser.flush();
         if (signal && signal.aborted) throw abortError();
         emit({ type: 'info', message: null });
@@ -503,6 +624,8 @@ function createQwen3Host({ device = 0 } = {}) {
     CONFIGS, engine: eng, loadModel, unload, forward, generate, runConversation, decodeLoop,
     setToolRunner(fn) { _toolRunner = fn; },
     lastGenStats: () => _lastGenStats,
+    loadedFromCache: () => _lastLoadCached,
+    tokenizer: () => TOK,
     config: () => C,
     model: () => M,
     readTokens: (from, n) => TI.qwen3_read_tokens(ctx, M, from, n),
@@ -511,5 +634,5 @@ function createQwen3Host({ device = 0 } = {}) {
   };
 }
 
-module.exports = { createQwen3Host, CONFIGS, readSafetensorsHeader, toolPreamble, renderMessage, GEN_BATCH, PIPE_DEPTH,
-  PREFILL_CHUNK };
+module.exports = { createQwen3Host, CONFIGS, readSafetensorsHeader, toolPreamble, renderMessage, claimSystemBlock, GEN_BATCH,
+  PIPE_DEPTH, PREFILL_CHUNK };

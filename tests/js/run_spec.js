@@ -11,6 +11,9 @@
 //            gens: [{prompt, maxTokens, temperature}]   generate() runs on a freshly loaded model
 //            prefix: {first, second, maxTokens}   conversation `second` after `first` (prefix
 //                    cache reuse) and again cold on a reloaded model
+//            qcache: {dir, dump, prompt, maxTokens}   load from safetensors writing the quant
+//                    cache, then from the cache alone, then after a manifest of another geometry
+//            tokchat: {tokenizer, text, system, maxTokens}   generate() and runConversation on text
 // Writes <dir>/result.json (and the files named by `read`).
 const fs = require('fs');
 const path = require('path');
@@ -93,6 +96,8 @@ async function main() {
       }
     }
     if (m.prefix) result.prefix = await runPrefix(host, m);
+    if (m.qcache) result.qcache = await runQcache(host, m, dir);
+    if (m.tokchat) result.tokchat = await runTokChat(host, m);
   }
   E.sync();
   fs.writeFileSync(path.join(dir, 'result.json'), JSON.stringify(result));
@@ -132,6 +137,54 @@ async function runPrefix(host, m) {
   await load();
   const cold = await conv(second);
   return { first: a1, warm, cold };
+}
+
+// the quantized-weights cache: a checkpoint load writes it (tensors dumped as a.*), a load
+// from the cache alone reads it (b.*); a manifest edited to another geometry is no cache
+async function runQcache(host, m, dir) {
+  const { E } = host.engine;
+  const q = m.qcache;
+  const base = { config: m.config, nCtx: m.nCtx, quantCache: q.dir, reload: true };
+  const dump = (tag) => {
+    for (const name of q.dump) {
+      const t = E.TI.qwen3_tensor(host.model(), name);
+      fs.writeFileSync(path.join(dir, tag + '.' + name + '.data'), Buffer.from(E.readBytes(t.data, 0, t.dataBytes)));
+      if (t.scales) fs.writeFileSync(path.join(dir, tag + '.' + name + '.scales'), Buffer.from(E.readBytes(t.scales, 0, t.scaleBytes)));
+    }
+  };
+  const out = { fromCache: [], gens: [] };
+  await host.loadModel(Object.assign({ safetensors: m.safetensors }, base));
+  out.fromCache.push(host.loadedFromCache());
+  dump('a');
+  out.gens.push(Array.from(await host.generate(q.prompt, { maxTokens: q.maxTokens })));
+  await host.loadModel(base);                          // no checkpoint: the cache alone
+  out.fromCache.push(host.loadedFromCache());
+  dump('b');
+  out.gens.push(Array.from(await host.generate(q.prompt, { maxTokens: q.maxTokens })));
+  const mf = path.join(q.dir, 'v1', 'custom', 'manifest');
+  const man = JSON.parse(fs.readFileSync(mf, 'utf8'));
+  man.config.vocab += 1;
+  fs.writeFileSync(mf, JSON.stringify(man));
+  await host.loadModel(Object.assign({ safetensors: m.safetensors }, base));   // a miss: the checkpoint, the cache rewritten
+  out.fromCache.push(host.loadedFromCache());
+  await host.loadModel(base);
+  out.fromCache.push(host.loadedFromCache());
+  out.gens.push(Array.from(await host.generate(q.prompt, { maxTokens: q.maxTokens })));
+  out.manifest = JSON.parse(fs.readFileSync(mf, 'utf8'));
+  return out;
+}
+
+// text through the tokenizer: generate()'s streamed pieces and result, the prompt length,
+// and a conversation's usage and content
+async function runTokChat(host, m) {
+  const t = m.tokchat;
+  await host.loadModel({ config: m.config, nCtx: m.nCtx, safetensors: m.safetensors, tokenizer: t.tokenizer, reload: true });
+  const pieces = [];
+  const text = await host.generate(t.text, { maxTokens: t.maxTokens, onToken: (x) => pieces.push(x) });
+  const out = { text, pieces, prefill: host.lastGenStats().prefillTokens, events: [] };
+  await host.runConversation({ provider: { maxTokens: t.maxTokens }, systemPrompt: t.system,
+    messages: [{ role: 'user', content: t.text }] }, (ev) => out.events.push(ev));
+  return out;
 }
 
 main().catch((e) => { console.error(e && e.stack ? e.stack : e); process.exit(1); });

@@ -396,3 +396,56 @@ def test_generate_follows_the_oracle_decoder(tmp_path, orc):
     pr = res["prefix"]
     assert len(pr["first"].split()) == 12
     assert pr["warm"] == pr["cold"] and len(pr["warm"].split()) == 12
+
+
+def test_quant_cache_and_text_prompts(tmp_path, orc):
+    """loadModel({quantCache}) (models/qwen3.js:3626-3759): a checkpoint load writes the cache,
+    a load from the cache alone gives every tensor byte for byte and the same generated
+    tokens, a manifest of another geometry is a miss (the checkpoint is read and the cache
+    rewritten). Then text through the tokenizer.json of tests/test_js_tokenizer.py's kind:
+    generate()'s prompt is the library's ChatML encoding, its streamed pieces join to its
+    result, and a conversation reports the same prompt length in its usage."""
+    tokenizers = pytest.importorskip("tokenizers")
+    from tokenizers import Regex, Tokenizer, decoders, models, pre_tokenizers, trainers
+    from test_js_tokenizer import QWEN, SPECIALS
+    d = str(tmp_path)
+    rng = np.random.default_rng(41)
+    c = dict(SMALL)
+    T, ckpt = _checkpoint(d, rng, c)
+    names = ["model.embed_tokens.weight", "lm_head.weight", "model.norm.weight", "model.layers.1.mlp.down_proj.weight",
+             "model.layers.0.self_attn.q_norm.weight", "model.layers.1.self_attn.v_proj.weight"]
+    prompt = [11, 502, 7, 999, 123]
+    # a small byte-level BPE tokenizer (ids below the model's vocabulary)
+    tok = Tokenizer(models.BPE())
+    tok.pre_tokenizer = pre_tokenizers.Sequence([pre_tokenizers.Split(Regex(QWEN), behavior="isolated", invert=False),
+                                                 pre_tokenizers.ByteLevel(add_prefix_space=False, use_regex=False)])
+    tok.decoder = decoders.ByteLevel()
+    tok.train_from_iterator([open(os.path.join(ROOT, "DESIGN.md"), encoding="utf-8").read(), "你好 🙂 café"] * 4,
+                            trainers.BpeTrainer(vocab_size=900, initial_alphabet=pre_tokenizers.ByteLevel.alphabet(),
+                                                special_tokens=SPECIALS, show_progress=False))
+    assert tok.get_vocab_size() <= c["vocab"]
+    tdir = os.path.join(d, "tok")
+    os.makedirs(tdir)
+    tok.save(os.path.join(tdir, "tokenizer.json"))
+    text, system = "Summarise the decode attention in one line, please 🙂", "You are a careful assistant. " * 6
+    spec = {"model": {"config": c, "nCtx": 256, "safetensors": ckpt, "prompt": prompt, "maxTokens": 2,
+                      "qcache": {"dir": os.path.join(d, "qc"), "dump": names, "prompt": prompt, "maxTokens": 24},
+                      "tokchat": {"tokenizer": tdir, "text": text, "system": system, "maxTokens": 20}}}
+    res = run_spec(d, spec, {})
+    q = res["qcache"]
+    assert q["fromCache"] == [False, True, False, True]
+    for nm in names:
+        for part in ("data", "scales"):
+            fa = os.path.join(d, "a.%s.%s" % (nm, part))
+            if os.path.exists(fa):
+                assert open(fa, "rb").read() == open(os.path.join(d, "b.%s.%s" % (nm, part)), "rb").read(), (nm, part)
+    assert q["gens"][0] == q["gens"][1] == q["gens"][2] and len(q["gens"][0]) == 24
+    assert q["manifest"]["config"]["vocab"] == c["vocab"] and q["manifest"]["chunkSize"] == 64 << 20
+    tc = res["tokchat"]
+    want = tok.encode("<|im_start|>user\n%s<|im_end|>\n<|im_start|>assistant\n" % text).ids
+    assert tc["prefill"] == len(want)
+    assert "".join(tc["pieces"]) == tc["text"]
+    usage = [e for e in tc["events"] if e["type"] == "usage"]
+    chat = "<|im_start|>system\n%s<|im_end|>\n<|im_start|>user\n%s<|im_end|>\n<|im_start|>assistant\n" % (system, text)
+    assert usage and usage[0]["usage"]["prompt_tokens"] == len(tok.encode(chat).ids)
+    assert any(e["type"] == "agent_done" for e in tc["events"]) and not any(e["type"] == "error" for e in tc["events"])
