@@ -16,6 +16,7 @@ const fs = require('fs');
 const path = require('path');
 const { createEngine, bf16ToF16bits, f32ToF16 } = require('./ti-engine');
 const { loadTokenizer } = require('./tokenizer');
+const { selfTestKernels } = require('./self-test');
 const QC = require('./quant-cache');
 
 // models/qwen3.js CONFIGS (Qwen3-0.6B / 1.7B geometry)
@@ -625,6 +626,7 @@ function createQwen3Host({ device = 0 } = {}) {
     setToolRunner(fn) { _toolRunner = fn; },
     lastGenStats: () => _lastGenStats,
     loadedFromCache: () => _lastLoadCached,
+    selfTestKernels: () => selfTestKernels(eng),        // models/qwen3.js:2753, exported at :5529
     tokenizer: () => TOK,
     config: () => C,
     model: () => M,

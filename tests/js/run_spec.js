@@ -7,6 +7,7 @@
 //            an argument is a number/boolean/null, {buf: name}, {rec: {pack, scales, N, K}},
 //            {kv: {kq, ks, vq, vs}}, {emb: {buf, vocab}}, {rec3: {pack, scales, nE}} or {trec: name}
 //            (a record made by {tern_quant: name, src: buffer, N, K}: L.quantizeTernaryBf16)
+//   selftest: true   host.selfTestKernels() -> result.selftest
 //   model:   {config, nCtx, safetensors, prompt, maxTokens, dump: [tensor names]}   (optional)
 //            gens: [{prompt, maxTokens, temperature}]   generate() runs on a freshly loaded model
 //            prefix: {first, second, maxTokens}   conversation `second` after `first` (prefix
@@ -69,6 +70,7 @@ async function main() {
       }
     }
   }
+  if (spec.selftest) result.selftest = host.selfTestKernels();
   if (spec.model) {
     const m = spec.model;
     await host.loadModel({ config: m.config, nCtx: m.nCtx, safetensors: m.safetensors });

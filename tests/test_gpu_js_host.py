@@ -449,3 +449,16 @@ def test_quant_cache_and_text_prompts(tmp_path, orc):
     chat = "<|im_start|>system\n%s<|im_end|>\n<|im_start|>user\n%s<|im_end|>\n<|im_start|>assistant\n" % (system, text)
     assert usage and usage[0]["usage"]["prompt_tokens"] == len(tok.encode(chat).ids)
     assert any(e["type"] == "agent_done" for e in tc["events"]) and not any(e["type"] == "error" for e in tc["events"])
+
+
+def test_self_test_kernels(tmp_path):
+    """selfTestKernels() (models/qwen3.js:2753-3219, exported at :5529): every check of the
+    host's own launcher self-test passes on the GPU (each launcher against an f64
+    restatement in JS, the quantizers as round trips, the argmax tie order, the Gumbel
+    sampler's frequencies)."""
+    res = run_spec(str(tmp_path), {"selftest": True}, {})
+    st = res["selftest"]
+    print("[js] selfTestKernels:", ", ".join("%s %.2e" % (c["name"], c["err"]) for c in st), flush=True)
+    names = [c["name"] for c in st]
+    assert len(names) >= 18 and len(set(names)) == len(names)
+    assert all(c["ok"] for c in st), [c for c in st if not c["ok"]]
