@@ -218,11 +218,12 @@ __global__ __launch_bounds__(128) void k_bn_prep(const float* __restrict__ qraw,
 }
 
 // ---- GQA attention over the f32 cache (model.rs:421-447) ------------------------------------
-// keys per attention workgroup for a cache of cap positions: 64, or more for long caches, so
-// that the split count stays within 160
+// keys per attention workgroup for a cache of cap positions: 64, or more for longer caches, so
+// that the grid (8 KV heads x splits) stays within one round of resident workgroups (three
+// 4-wave workgroups per CU) up to 12288 positions, and the split count within 160
 constexpr int BN_MAX_CTX = 256 * 160;
 __host__ __device__ inline int bn_chunk(int cap) {
-    return cap <= 64 * 160 ? 64 : (cap <= 128 * 160 ? 128 : 256);
+    return cap <= 64 * 96 ? 64 : (cap <= 128 * 96 ? 128 : 256);
 }
 
 // workgroup (KV head hk, split of CH keys), the G = 2 query heads of hk (hd 128):
@@ -254,6 +255,16 @@ __global__ __launch_bounds__(256) void k_bn_attn(const float* __restrict__ qr, c
     for (int g = 0; g < G; g++)
 #pragma unroll
         for (int i = 0; i < 8; i++) q[g][i] = reinterpret_cast<const float4*>(qr + (size_t)(hk * G + g) * HD + qd * 32)[i];
+    // the V rows of the first 64 keys, for the P V pass below, issued before the K loads so
+    // that both tiles are in flight together (one memory round trip instead of two)
+    const int kg = t >> 5, d4 = t & 31;
+    const float4* vb = reinterpret_cast<const float4*>(vc + (size_t)c0 * kvd + (size_t)hk * HD) + d4;
+    float4 vpre[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int j = kg + 8 * i;
+        vpre[i] = vb[(size_t)(j < n ? j : n - 1) * (kvd / 4)];
+    }
     for (int k0 = 0; k0 < n; k0 += 64) {
         const int j = k0 + (t >> 2);
         const int key = c0 + (j < n ? j : n - 1);
@@ -310,13 +321,25 @@ __global__ __launch_bounds__(256) void k_bn_attn(const float* __restrict__ qr, c
     __syncthreads();
 #pragma unroll
     for (int g = 0; g < G; g++) l[g] = (red[g][0] + red[g][1]) + (red[g][2] + red[g][3]);
-    const int kg = t >> 5, d4 = t & 31;
     float4 o[G];
 #pragma unroll
     for (int g = 0; g < G; g++) o[g] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    const float4* vb = reinterpret_cast<const float4*>(vc + (size_t)c0 * kvd + (size_t)hk * HD) + d4;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {                      // keys kg + 8i < 64: the prefetched rows
+        const int j = kg + 8 * i;
+        if (j < n) {
+#pragma unroll
+            for (int g = 0; g < G; g++) {
+                const float p = sc[g][j];
+                o[g].x = fmaf(p, vpre[i].x, o[g].x);
+                o[g].y = fmaf(p, vpre[i].y, o[g].y);
+                o[g].z = fmaf(p, vpre[i].z, o[g].z);
+                o[g].w = fmaf(p, vpre[i].w, o[g].w);
+            }
+        }
+    }
 #pragma unroll 4
-    for (int j = kg; j < n; j += 8) {
+    for (int j = kg + 64; j < n; j += 8) {
         const float4 vv = vb[(size_t)j * (kvd / 4)];
 #pragma unroll
         for (int g = 0; g < G; g++) {
@@ -346,55 +369,91 @@ __global__ __launch_bounds__(256) void k_bn_attn(const float* __restrict__ qr, c
 }
 
 // out[h][d] = sum_i o_i e^(m_i - M) / sum_i l_i e^(m_i - M) over the splits that hold keys,
-// for every query head, then the n2 quantizer of the whole output (one workgroup: the
-// per-tensor scale needs every element). Wave w < n_heads finds head w's M, the split weights
-// e^(m_i - M) (into LDS) and L; then thread (h, d) sums its head's o_i in split order.
+// then the n2 quantizer of the whole output. One workgroup per KV head (its G = 2 query
+// heads), 1024 threads: thread (quarter q, head g, dim d) loads its quarter of the splits'
+// partials (every load in flight at once, before the split weights are known: one memory
+// round trip), waves 0 and 1 find their head's M, the weights e^(m_i - M) and L, and each
+// (g, d) adds its four quarter sums in order. The last of the nKv workgroups to finish
+// quantizes the whole output (the per-tensor scale needs every element); the head outputs
+// reach it through device-scope stores and loads, and it resets the counter.
 constexpr int BN_MERGE_SPLITS = 160;   // split slots per head: bn_chunk keeps a cache of BN_MAX_CTX within them
+constexpr int BN_MQ = BN_MERGE_SPLITS / 4;   // splits per quarter, at most
 
 template <int EPT>
 __global__ __launch_bounds__(BN_THREADS) void k_bn_merge_quant(const float* __restrict__ po, const float* __restrict__ pml,
                                                               const int* __restrict__ dpos, int ns_stride, int nq,
                                                               int chunk, float* __restrict__ out, int8_t* __restrict__ act,
                                                               int32_t* __restrict__ xsum, float* __restrict__ scale_out,
-                                                              int cap) {
-    constexpr int HD = 128, HMAX = EPT * BN_THREADS / HD;
+                                                              uint32_t* __restrict__ counter, int cap) {
+    constexpr int HD = 128, G = 2;
     __shared__ float red[16];
-    __shared__ float s_w[HMAX][BN_MERGE_SPLITS];
-    __shared__ float s_l[HMAX];
+    __shared__ float s_w[G][BN_MERGE_SPLITS];
+    __shared__ float s_l[G];
+    __shared__ float s_part[4][G][HD];
+    __shared__ int s_last;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int q = t >> 8, g = (t >> 7) & 1, d = t & 127;
+    const int hk = blockIdx.x;
     const int ns = (min(*dpos + 1, cap) + chunk - 1) / chunk;
-    const int nh = nq / HD;
-    for (int h = wave; h < nh; h += BN_THREADS / 64) {
-        const float* ml = pml + (size_t)h * ns_stride * 2;
+    // this thread's partials: splits q, q + 4, .. of query head 2 hk + g
+    const float* ob = po + (size_t)(hk * G + g) * ns_stride * HD + d;
+    float ov[BN_MQ];
+#pragma unroll
+    for (int i = 0; i < BN_MQ; i++) {
+        const int k = q + 4 * i;
+        ov[i] = k < ns ? ob[(size_t)k * HD] : 0.0f;
+    }
+    if (wave < G) {
+        const float* ml = pml + (size_t)(hk * G + wave) * ns_stride * 2;
+        float mk[BN_MERGE_SPLITS / 64 + 1], lk[BN_MERGE_SPLITS / 64 + 1];
         float M = -INFINITY;
-        for (int k = lane; k < ns; k += 64) M = fmaxf(M, ml[2 * k]);
+#pragma unroll
+        for (int i = 0; i * 64 < BN_MERGE_SPLITS; i++) {
+            const int k = lane + 64 * i;
+            mk[i] = k < ns ? ml[2 * k] : -INFINITY;
+            lk[i] = k < ns ? ml[2 * k + 1] : 0.0f;
+            M = fmaxf(M, mk[i]);
+        }
         M = ti_wave_max(M);
         float L = 0.0f;
-        for (int k = lane; k < ns; k += 64) {
-            const float e2 = expf(ml[2 * k] - M);
-            s_w[h][k] = e2;
-            L += ml[2 * k + 1] * e2;
+#pragma unroll
+        for (int i = 0; i * 64 < BN_MERGE_SPLITS; i++) {
+            const int k = lane + 64 * i;
+            if (k < ns) {
+                const float e2 = expf(mk[i] - M);
+                s_w[wave][k] = e2;
+                L += lk[i] * e2;
+            }
         }
         L = ti_wave_sum(L);
-        if (lane == 0) s_l[h] = L;
+        if (lane == 0) s_l[wave] = L;
     }
     __syncthreads();
+    float o = 0.0f;
+#pragma unroll
+    for (int i = 0; i < BN_MQ; i++) {
+        const int k = q + 4 * i;
+        if (k < ns) o = fmaf(ov[i], s_w[g][k], o);
+    }
+    s_part[q][g][d] = o;
+    __syncthreads();
+    if (q == 0) {
+        const float v = ((s_part[0][g][d] + s_part[1][g][d]) + (s_part[2][g][d] + s_part[3][g][d])) / s_l[g];
+        ti_pub_store(out + (size_t)(hk * G + g) * HD + d, v);
+    }
+    ti_stores_done();
+    __syncthreads();
+    if (t == 0) s_last = ti_arrive(counter) == gridDim.x - 1;
+    __syncthreads();
+    if (!s_last) return;
     float v[EPT];
 #pragma unroll
     for (int i = 0; i < EPT; i++) {
         const int e = t + BN_THREADS * i;
-        v[i] = 0.0f;
-        if (e < nq) {
-            const int h = e / HD, d = e % HD;
-            const float* ob = po + (size_t)h * ns_stride * HD + d;
-            float o = 0.0f;
-#pragma unroll 8
-            for (int k = 0; k < ns; k++) o = fmaf(ob[(size_t)k * HD], s_w[h][k], o);
-            v[i] = o / s_l[h];
-            out[e] = v[i];
-        }
+        v[i] = e < nq ? ti_pub_load(out + e) : 0.0f;
     }
     quant_n2<EPT>(v, nq, act, xsum, scale_out, red);
+    if (t == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---- logits = raw * (1 / scale), argmax (ops::argmax: larger wins, the lower index on ties,
@@ -824,7 +883,7 @@ static int bonsai_step(ti_ctx* c, ti_bonsai* m, bool want_logits) {
         else k_bn_attn<256><<<nKv * nsplit, 256, 0, c->stream>>>(m->qr, y.kc, y.vc, m->dpos, nKv, m->po, m->pml, nsplit, C.max_ctx);
         TI_LAUNCHED("k_bn_attn");
         const int eq = (nq + BN_THREADS - 1) / BN_THREADS;
-#define MQ(E) if (eq <= E) { k_bn_merge_quant<E><<<1, BN_THREADS, 0, c->stream>>>(m->po, m->pml, m->dpos, nsplit, nq, chunk, m->attn, m->act, m->xsum, sb, C.max_ctx); }
+#define MQ(E) if (eq <= E) { k_bn_merge_quant<E><<<nKv, BN_THREADS, 0, c->stream>>>(m->po, m->pml, m->dpos, nsplit, nq, chunk, m->attn, m->act, m->xsum, sb, c->sync + TI_SYNC_BONSAI, C.max_ctx); }
         MQ(2) else MQ(4) else MQ(8) else return ti_fail(TI_ERR_INVALID, "bonsai: q width %d", nq);
 #undef MQ
         TI_LAUNCHED("k_bn_merge_quant");

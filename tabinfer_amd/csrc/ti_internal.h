@@ -59,6 +59,7 @@ struct ti_graph {
 #define TI_MOE_E_MAX 256
 #define TI_SYNC_WORDS 1024
 #define TI_SYNC_LMHEAD 0          // lm_head argmax
+#define TI_SYNC_BONSAI 1          // Bonsai attention merge: the head workgroups' arrivals
 #define TI_SYNC_ATTN 64           // fused attention: one counter per KV head (up to 64)
 #define TI_SYNC_TGEMM 512         // split-K T-token projections: one counter per 16-row block
 #define TI_TG_SPLIT_BLOCKS 128    // (blocks of one split-K launch, at most)
