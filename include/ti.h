@@ -211,7 +211,8 @@ int ti_attn_decode_q8_noalloc(void* stream, const float* qr, const uint32_t* kq,
  * projections [nHq*hd], [nKv*hd], [nKv*hd]; k and v are written into cache row pos;
  * out[nHq*hd] is the attention over positions 0..pos; out_q/out_s (both or neither)
  * receive it quantized per 32 (quantQ8, for o_proj's linearQ). max_splits workgroups
- * per KV head (0 = the default: 32, or 64 for caches over 16384 positions; at most 64).
+ * per KV head (0 = the default for pos + 1 positions: 16 up to 4096, then about one per
+ * 512 positions, between 24 and 64; at most 64).
  * Covers hd 64/128 with nHq/nKv <= 2. */
 int ti_attn_step_q8(ti_ctx* ctx, const float* q, const float* k, const float* v,
                     const uint16_t* qn_w, const uint16_t* kn_w, uint32_t* kq, float* ks,
@@ -405,6 +406,14 @@ int ti_qwen3_forward(ti_ctx* ctx, ti_qwen3* m, const int32_t* ids, int T, int po
  * Reads nothing from the host, so it can be captured once and replayed per token. */
 int ti_qwen3_decode(ti_ctx* ctx, ti_qwen3* m);
 int ti_qwen3_set_pos(ti_ctx* ctx, ti_qwen3* m, int pos);
+/* The reference picks the decode attention's split count from the context on every
+ * dispatch (_decNsplit, models/qwen3.js:2354). A captured step fixes it when it is
+ * captured, from the position last set on the host (ti_qwen3_set_pos, or the end of a
+ * ti_qwen3_forward): *splits receives the count a step captured at pos uses (16 up to
+ * 4096 positions, then about one per 512 positions, between 24 and 64). A caller that
+ * replays a captured step captures it again when this value changes for its position;
+ * a step replayed past its capture's tier stays correct. */
+int ti_qwen3_decode_splits(const ti_qwen3* m, int pos, int* splits);
 /* forward(..., {temp}) (models/qwen3.js:4052, 4538-4567): the temperature of the following
  * decode steps and forwards, read on the device (so one captured step serves any
  * temperature); <= 0 is greedy (the default). With temp > 0 each step's lm_head adds

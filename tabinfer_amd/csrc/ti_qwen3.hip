@@ -22,6 +22,7 @@ int ti_attn_prep_launch(ti_ctx*, const float*, const float*, const float*, const
                         uint32_t*, float*, uint32_t*, float*, int, int, int, int, float, float, const int*);
 int ti_attn_decode_launch(ti_ctx*, const float*, const uint32_t*, const float*, const uint32_t*, const float*, float*,
                           int, int, int, int, int, int, const int*, int);
+int ti_attn_decode_splits(int S);
 int ti_attn_fused_launch(ti_ctx*, const float*, const float*, const float*, const uint16_t*, const uint16_t*, uint32_t*,
                          float*, uint32_t*, float*, float*, int, int, int, const int*, int, int, float, float, int,
                          const float*, uint32_t*, float*);
@@ -154,6 +155,7 @@ struct ti_qwen3 {
     float* amx_v;
     uint32_t* amx_i;
     uint32_t* trace = nullptr;   // caller's trace buffer (ti_qwen3_trace), or null
+    int pos_hint = 0;            // the position last set from the host (set_pos, or a forward's end)
     std::vector<void*> allocs;
 };
 
@@ -389,6 +391,22 @@ extern "C" int ti_qwen3_set_pos(ti_ctx* c, ti_qwen3* m, int pos) {
     TI_REQUIRE(m && pos >= 0 && pos < m->cfg.max_ctx, "ti_qwen3_set_pos: pos %d out of [0, %d)", pos, m ? m->cfg.max_ctx : 0);
     k_set_pos<<<1, 256, 0, c->stream>>>(m->dpos, pos, m->rope, m->rope_cur, m->cfg.head_dim, m->cfg.max_ctx);
     TI_LAUNCHED("k_set_pos");
+    m->pos_hint = pos;
+    return TI_OK;
+}
+
+// The decode step's attention splits per KV head for a step at pos: the reference picks its
+// split count from the context on every dispatch (_decNsplit, models/qwen3.js:2354); a
+// captured step fixes it when it is captured, from the position last set on the host.
+static int decode_splits(const ti_qwen3* m, int pos) {
+    const int S = pos + 1 < m->cfg.max_ctx ? pos + 1 : m->cfg.max_ctx;
+    return ti_attn_decode_splits(S);
+}
+
+extern "C" int ti_qwen3_decode_splits(const ti_qwen3* m, int pos, int* splits) {
+    TI_REQUIRE(m && splits, "ti_qwen3_decode_splits: null argument");
+    TI_REQUIRE(pos >= 0 && pos < m->cfg.max_ctx, "ti_qwen3_decode_splits: pos %d out of [0, %d)", pos, m->cfg.max_ctx);
+    *splits = decode_splits(m, pos);
     return TI_OK;
 }
 
@@ -527,7 +545,8 @@ extern "C" int ti_qwen3_decode(ti_ctx* c, ti_qwen3* m) {
         RC(trace_put(c, m, l, TR_K, m->k, 1));
         RC(trace_put(c, m, l, TR_V, m->v, 1));
         RC(ti_attn_fused_launch(c, m->q, m->k, m->v, y.q_norm, y.k_norm, y.kq, y.ks, y.vq, y.vs, m->attn, nHq, nKv, hd,
-                                m->dpos, 0, C.max_ctx, C.rope_theta, C.rms_eps, 0, m->rope_cur, m->xq, m->xs));
+                                m->dpos, 0, C.max_ctx, C.rope_theta, C.rms_eps, decode_splits(m, m->pos_hint), m->rope_cur,
+                                m->xq, m->xs));
         RC(trace_put(c, m, l, TR_ATTN, m->attn, 1));
         RC(trace_put(c, m, l, TR_A_Q, m->xq, 1));
         RC(trace_put(c, m, l, TR_A_S, m->xs, 1));
@@ -649,6 +668,7 @@ extern "C" int ti_qwen3_forward(ti_ctx* c, ti_qwen3* m, const int32_t* ids, int 
                               nullptr, pos + T, C.max_ctx, nullptr, nullptr, 0, m->samp));
     k_set_pos<<<1, 256, 0, c->stream>>>(m->dpos, pos + T, m->rope, m->rope_cur, hd, C.max_ctx);
     TI_LAUNCHED("k_set_pos");
+    m->pos_hint = pos + T < C.max_ctx ? pos + T : C.max_ctx - 1;
     return TI_OK;
 #undef RC
 }

@@ -130,7 +130,7 @@ function createQwen3Host({ device = 0 } = {}) {
   let C = null;          // its config
   let TOK = null;
   let _devPos = -1;      // the device-side position as this host last left it
-  let _decodeGraph = null;
+  let _decodeGraph = null, _decodeSplits = -1;
   let _cachedIds = null; // prefix cache: the ids whose KV rows are resident
   let _toolRunner = null;
   let _lastGenStats = null;
@@ -303,7 +303,7 @@ function createQwen3Host({ device = 0 } = {}) {
   }
 
   function unload() {
-    if (_decodeGraph) { E.destroyGraph(_decodeGraph); _decodeGraph = null; }
+    if (_decodeGraph) { E.destroyGraph(_decodeGraph); _decodeGraph = null; _decodeSplits = -1; }
     if (_pipe) { E.sync(); for (const b of _pipe) TI.host_free(b.buffer); _pipe = null; }
     if (M) { TI.qwen3_destroy(M); M = null; }
   }
@@ -361,11 +361,18 @@ function createQwen3Host({ device = 0 } = {}) {
     return tok;
   }
 
-  function decodeGraph() {
-    if (!_decodeGraph) {
-      E.beginBatch();
-      try { TI.qwen3_decode(ctx, M); } finally { _decodeGraph = E.endBatch(); }
-    }
+  // the captured step for a loop starting at pos: its attention split count follows the
+  // context (qwen3_decode_splits), so a loop at a position of another tier captures anew,
+  // after the earlier graph's replays have drained
+  function decodeGraph(pos) {
+    const ns = TI.qwen3_decode_splits(M, pos);
+    if (_decodeGraph && _decodeSplits === ns) return _decodeGraph;
+    if (_decodeGraph) { E.sync(); E.destroyGraph(_decodeGraph); _decodeGraph = null; }
+    TI.qwen3_set_pos(ctx, M, pos);   // the capture reads the position last set on the host
+    _devPos = pos;
+    E.beginBatch();
+    try { TI.qwen3_decode(ctx, M); } finally { _decodeGraph = E.endBatch(); }
+    _decodeSplits = ns;
     return _decodeGraph;
   }
 
@@ -376,7 +383,7 @@ function createQwen3Host({ device = 0 } = {}) {
   // (as the reference's discarded batches do) before their buffers are reused.
   let _pipe = null;
   async function decodeLoop(pos, maxTokens, emitTok, signal, count, temp) {
-    const g = decodeGraph();
+    const g = decodeGraph(pos);
     if (!_pipe) _pipe = Array.from({ length: PIPE_DEPTH }, () => new Int32Array(TI.host_alloc(GEN_BATCH * 4)));
     setTemp(temp > 0 ? +temp : 0);
     setPos(pos);

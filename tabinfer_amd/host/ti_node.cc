@@ -993,6 +993,19 @@ napi_value js_qwen3_set_pos(napi_env env, napi_callback_info info) {
     return rc ? throw_ti(env, "qwen3_set_pos", rc) : undefined(env);
 }
 
+// qwen3_decode_splits(model, pos) -> the attention splits of a decode step captured at pos
+napi_value js_qwen3_decode_splits(napi_env env, napi_callback_info info) {
+    const char* fn = "qwen3_decode_splits";
+    Args a(env, info);
+    if (!want_args(env, a, 2, fn)) return nullptr;
+    ModelH* m = get_model(env, a.v[0], fn, 0);
+    int64_t pos;
+    if (!m || !get_i64(env, a.v[1], &pos, fn, 1)) return nullptr;
+    int n = 0;
+    const int rc = ti_qwen3_decode_splits(m->m, (int)pos, &n);
+    return rc ? throw_ti(env, fn, rc) : num(env, n);
+}
+
 // qwen3_sampling(ctx, model, temperature): the temperature of the following steps (0: greedy)
 napi_value js_qwen3_sampling(napi_env env, napi_callback_info info) {
     const char* fn = "qwen3_sampling";
@@ -1522,6 +1535,7 @@ napi_value module_init(napi_env env, napi_value exports) {
         FN("qwen3_forward", js_qwen3_forward),
         FN("qwen3_decode", js_qwen3_decode),
         FN("qwen3_set_pos", js_qwen3_set_pos),
+        FN("qwen3_decode_splits", js_qwen3_decode_splits),
         FN("qwen3_read_tokens_async", js_qwen3_read_tokens_async),
         FN("qwen3_sampling", js_qwen3_sampling),
         FN("qwen3_seed", js_qwen3_seed),

@@ -167,6 +167,53 @@ def test_graph_replay_decodes_like_eager(ctx):
         m.close()
 
 
+def test_decode_splits_follow_the_context(ctx):
+    """The attention split count of a captured step follows the context it is captured at
+    (ti_qwen3_decode_splits: 16 up to 4096 positions, then ceil(S / 512) between 24 and
+    64); a step captured at a short context and replayed over a long one gives the logits
+    and token of a step captured there (only the split count, hence the summation order of
+    the split merge, differs)."""
+    cfg = dict(SMALL, head_dim=128, max_ctx=33000)
+    m = abi.Qwen3(ctx, **cfg)
+    try:
+        want = {0: 16, 4095: 16, 4096: 24, 8191: 24, 12287: 24, 12288: 25, 16383: 32, 16384: 33, 32767: 64,
+                32999: 64}
+        assert {p: m.decode_splits(p) for p in want} == want
+        with pytest.raises(abi.TIError):
+            m.decode_splits(33000)
+        Q.load_into(m, Q.make_weights(cfg, 5))
+        P, chunk, nkv = 9000, 1000, cfg["n_kv_heads"] * cfg["head_dim"]
+        rng = np.random.default_rng(8)
+        kx = ctx.upload(rng.standard_normal(chunk * nkv).astype(np.float32))
+        vx = ctx.upload(rng.standard_normal(chunk * nkv).astype(np.float32))
+        for l in range(cfg["layers"]):
+            kq, ks, vq, vs = m.kv(l)
+            for p0 in range(0, P, chunk):
+                ctx.call("ti_kv_write_q8", kx, vx, kq, ks, vq, vs, chunk, cfg["n_kv_heads"], cfg["head_dim"], p0)
+        m.write_tokens(0, rng.integers(0, cfg["vocab"], P + 2).astype(np.int32))
+        m.set_pos(P)
+        m.decode()                                  # eager at the long context: 24 splits
+        ctx.sync()
+        want_logits = _logits(ctx, m, cfg["vocab"]).copy()
+        want_tok = int(m.read_tokens(P + 1, 1)[0])
+        m.set_pos(100)                              # captured at a short context: 16 splits
+        ctx.graph_begin()
+        m.decode()
+        g = ctx.graph_end()
+        try:
+            m.set_pos(P)
+            ctx.graph_launch(g)
+            ctx.sync()
+            got = _logits(ctx, m, cfg["vocab"])
+            assert rel_err(got, want_logits) < TOL   # (an int8 code of the output may flip at a rounding edge)
+            if margin_ok(want_logits):
+                assert int(m.read_tokens(P + 1, 1)[0]) == want_tok
+        finally:
+            ctx.graph_destroy(g)
+    finally:
+        m.close()
+
+
 def _seed_prefix(ctx, orc, m, ref, cfg, P, seed):
     """A seeded random prefix KV of P tokens in every layer, written through the KV
     quantizer into both the model and the reference decoder."""
