@@ -339,7 +339,7 @@ constexpr int tg_sq(int W, int KS, int NL) { return (NL * KS + W - 1) / W; }
 // the workgroup's 32-row chunk, then up rows +0/+16). IN: TG_Q8 codes or TG_NORM
 // (RMSNorm + quantQ8T in the prologue). PART: residual epilogue that also writes the
 // output's RMSNorm partial sums (block b owns rows t + 256 i).
-template <bool GU, int W, int KS, int NL, int IN, bool PART, bool SPLIT = false>
+template <bool GU, int W, int KS, int NL, int IN, bool PART, bool SPLIT = false, bool DUAL = false>
 __global__ __launch_bounds__(64 * W) void k_tgemm(TgArgs a) {
     static_assert(!GU || W / KS == 4, "gate/up: four 16-row blocks per workgroup");
     static_assert(!(GU && PART), "the partial sums come from residual projections");
@@ -424,31 +424,72 @@ __global__ __launch_bounds__(64 * W) void k_tgemm(TgArgs a) {
 
     // 4. the group loop
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (DUAL) {
+        // T <= 8: one v_mfma_i32_16x16x64_i8 per pair of groups (2p', 2p'+1). Bytes 0-7 of
+        // every lane's A and B operands carry the even group's K slice j, bytes 8-15 the odd
+        // group's (A and B share their (lane row, byte) -> k pairing, so C sums over both);
+        // A rows 0-7 are the tokens of the even group with the odd half zero, rows 8-15 the
+        // same tokens of the odd group with the even half zero. Lane (m, j) then holds tokens
+        // 4(j&1)..+3 of row m for group 2p' + (j>>1): half the scaling work of one MFMA per
+        // group, with no padding rows.
+        const int hiA = m >> 3, jh = j >> 1, jt = 4 * (j & 1);
+        const uint32_t* arow = L.aq + min(m & 7, T - 1) * S + 8 * hiA + 2 * j;
 #pragma unroll
-    for (int s = 0; s < NL; s++) {
-        uint32_t bw[4];
-        tr4_rows(wv[s], bw);
-        const uint4 sc4 = sv[s / 2];
+        for (int s = 0; s < NL; s++) {
+            uint32_t bw[4];
+            tr4_rows(wv[s], bw);
+            const uint4 sc4 = sv[s / 2];
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int g = gbase + 4 * s + u;
-            const uint2 av = *reinterpret_cast<const uint2*>(L.aq + tA * S + 8 * g + 2 * j);
-            const v4i cv = *reinterpret_cast<const v4i*>(L.corr + g * 16 + 4 * j);
-            const float4 sx = *reinterpret_cast<const float4*>(L.as + g * 16 + 4 * j);
-            const long A = (long)(((uint64_t)av.y << 32) | av.x);
-            const uint32_t lo = bw[u] & 0x0F0F0F0Fu, hi = (bw[u] >> 4) & 0x0F0F0F0Fu;
-            const long B = (long)(((uint64_t)hi << 32) | lo);
-            const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, cv, 0, 0, 0);
-            const int h = 4 * (s & 1) + u;             // this group's half in sc4
-            const uint32_t sp = h < 2 ? sc4.x : (h < 4 ? sc4.y : (h < 6 ? sc4.z : sc4.w));
-            const float sw = ti_h2f((uint16_t)((h & 1) ? (sp >> 16) : (sp & 0xffff)));
-            acc[0] = fmaf((float)d[0], sw * sx.x, acc[0]);
-            acc[1] = fmaf((float)d[1], sw * sx.y, acc[1]);
-            acc[2] = fmaf((float)d[2], sw * sx.z, acc[2]);
-            acc[3] = fmaf((float)d[3], sw * sx.w, acc[3]);
+            for (int pp = 0; pp < 2; pp++) {
+                const int g = gbase + 4 * s + 2 * pp;      // the pair's even group
+                const uint2 av = *reinterpret_cast<const uint2*>(arow + 8 * g);
+                const v4i cv = *reinterpret_cast<const v4i*>(L.corr + (g + jh) * 16 + jt);
+                const float4 sx = *reinterpret_cast<const float4*>(L.as + (g + jh) * 16 + jt);
+                const v4i A = hiA ? v4i{0, 0, (int)av.x, (int)av.y} : v4i{(int)av.x, (int)av.y, 0, 0};
+                const uint32_t w0 = bw[2 * pp], w1 = bw[2 * pp + 1];
+                const v4i B = {(int)(w0 & 0x0F0F0F0Fu), (int)((w0 >> 4) & 0x0F0F0F0Fu), (int)(w1 & 0x0F0F0F0Fu),
+                               (int)((w1 >> 4) & 0x0F0F0F0Fu)};
+                const v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, cv, 0, 0, 0);
+                const int h = 4 * (s & 1) + 2 * pp;        // the pair's scales: halves of word h/2 of sc4
+                const uint32_t sp = h < 2 ? sc4.x : (h < 4 ? sc4.y : (h < 6 ? sc4.z : sc4.w));
+                const float sw = ti_h2f((uint16_t)(sp >> (16 * jh)));
+                acc[0] = fmaf((float)d[0], sw * sx.x, acc[0]);
+                acc[1] = fmaf((float)d[1], sw * sx.y, acc[1]);
+                acc[2] = fmaf((float)d[2], sw * sx.z, acc[2]);
+                acc[3] = fmaf((float)d[3], sw * sx.w, acc[3]);
+            }
+        }
+        // lanes j and j ^ 2 hold the same (row, tokens) over the even and odd groups
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[i] = acc[i] + ti_xor(acc[i], 32);
+    } else {
+#pragma unroll
+        for (int s = 0; s < NL; s++) {
+            uint32_t bw[4];
+            tr4_rows(wv[s], bw);
+            const uint4 sc4 = sv[s / 2];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int g = gbase + 4 * s + u;
+                const uint2 av = *reinterpret_cast<const uint2*>(L.aq + tA * S + 8 * g + 2 * j);
+                const v4i cv = *reinterpret_cast<const v4i*>(L.corr + g * 16 + 4 * j);
+                const float4 sx = *reinterpret_cast<const float4*>(L.as + g * 16 + 4 * j);
+                const long A = (long)(((uint64_t)av.y << 32) | av.x);
+                const uint32_t lo = bw[u] & 0x0F0F0F0Fu, hi = (bw[u] >> 4) & 0x0F0F0F0Fu;
+                const long B = (long)(((uint64_t)hi << 32) | lo);
+                const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, cv, 0, 0, 0);
+                const int h = 4 * (s & 1) + u;             // this group's half in sc4
+                const uint32_t sp = h < 2 ? sc4.x : (h < 4 ? sc4.y : (h < 6 ? sc4.z : sc4.w));
+                const float sw = ti_h2f((uint16_t)((h & 1) ? (sp >> 16) : (sp & 0xffff)));
+                acc[0] = fmaf((float)d[0], sw * sx.x, acc[0]);
+                acc[1] = fmaf((float)d[1], sw * sx.y, acc[1]);
+                acc[2] = fmaf((float)d[2], sw * sx.z, acc[2]);
+                acc[3] = fmaf((float)d[3], sw * sx.w, acc[3]);
+            }
         }
     }
-    // partials: lane (m, j) holds tokens 4j..4j+3 of row m of the wave's block
+    // partials: lane (m, j) holds tokens 4j..4j+3 of row m of the wave's block (DUAL: lanes
+    // j >= 2 repeat tokens 0..7 in the slots of tokens 8..15, which T <= 8 never reads)
 #pragma unroll
     for (int i = 0; i < 4; i++) L.part[(wave * 16 + 4 * j + i) * 17 + m] = acc[i];
     __syncthreads();
@@ -638,19 +679,26 @@ int tg_ku(int K) {   // k_tnorm_q8: K = 256*KU, KU in {1, 2, 4, 8, 16}
     return (ku == 1 || ku == 2 || ku == 4 || ku == 8 || ku == 16) ? ku : 0;
 }
 
-template <bool GU, int W, int KS, int NL, int IN, bool PART, bool SPLIT = false>
-int tg_go(ti_ctx* c, const TgArgs& a, unsigned grid, const char* name) {
+template <bool GU, int W, int KS, int NL, int IN, bool PART, bool SPLIT, bool DUAL>
+int tg_go1(ti_ctx* c, const TgArgs& a, unsigned grid, const char* name) {
     const size_t lds = (size_t)tg_lds_words(a.T, a.K, W, PART ? W / KS : 0) * 4;
     static bool attr = false;
     if (!attr && lds > 65536) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_tgemm<GU, W, KS, NL, IN, PART, SPLIT>),
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_tgemm<GU, W, KS, NL, IN, PART, SPLIT, DUAL>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         if (e != hipSuccess) return ti_hip_fail(e, "k_tgemm LDS attribute");
         attr = true;
     }
-    k_tgemm<GU, W, KS, NL, IN, PART, SPLIT><<<grid, 64 * W, lds, c->stream>>>(a);
+    k_tgemm<GU, W, KS, NL, IN, PART, SPLIT, DUAL><<<grid, 64 * W, lds, c->stream>>>(a);
     TI_LAUNCHED(name);
     return TI_OK;
+}
+
+// T <= 8 takes the pairwise-group MFMA loop (no padding token rows)
+template <bool GU, int W, int KS, int NL, int IN, bool PART, bool SPLIT = false>
+int tg_go(ti_ctx* c, const TgArgs& a, unsigned grid, const char* name) {
+    if (a.T <= 8) return tg_go1<GU, W, KS, NL, IN, PART, SPLIT, true>(c, a, grid, name);
+    return tg_go1<GU, W, KS, NL, IN, PART, SPLIT, false>(c, a, grid, name);
 }
 
 // dispatch over K for the non-gate/up kernels: (W, KS, NL) from the split table (the

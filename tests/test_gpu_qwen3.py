@@ -271,7 +271,11 @@ def test_qwen3_17b_geometry_batch8_over_4k_prefix(ctx, orc, T):
     Checked teacher-forced, layer by layer (tests/qwen3_tf.py): each layer's float outputs
     within 1e-3 of the oracle's value of the GPU's own quantized inputs, code flips at most
     one step and rare; the last logits within 1e-3 of the oracle's lm_head of the GPU's
-    final residual; and the T-token forward equal to T single-token forwards within 1e-5."""
+    final residual. Against T single-token forwards: the same next token where the margin
+    allows, and logits within 5e-3 (the T-token GEMM adds the int32 group dots in another
+    f32 order than the batch-1 GEMV, so an int8 activation code can land on the other side
+    of a rounding boundary, which moves the end-to-end logits by ~1e-3; the reference's
+    gemmDP4A and gemvDP4 differ the same way)."""
     cfg = dict(CFG_17B, max_tokens=8)
     W = Q.make_weights(cfg, 5)
     m, one = abi.Qwen3(ctx, **cfg), abi.Qwen3(ctx, **cfg)
@@ -287,7 +291,6 @@ def test_qwen3_17b_geometry_batch8_over_4k_prefix(ctx, orc, T):
         for i in range(T):
             one.forward(ids[i:i + 1], P + i)
         lt, l1 = _logits(ctx, m, cfg["vocab"]), _logits(ctx, one, cfg["vocab"])
-        assert rel_err(lt, l1) < 1e-5
         rows = TF.new_kv_rows(ctx, m, cfg, P, T)
         R = TF.teacher_forced(orc, cfg, W, ref.kv, layers, x_final, rows, P, T)
         rl = TF.final_logits(orc, cfg, W, x_final[T - 1])
@@ -298,6 +301,10 @@ def test_qwen3_17b_geometry_batch8_over_4k_prefix(ctx, orc, T):
         assert tok == orc.argmax(lt)
         if margin_ok(rl):
             assert tok == orc.argmax(rl.astype(np.float32))
+        print("[qwen3] T=%d forward vs %d single-token forwards: logits rel err %.2e" % (T, T, rel_err(lt, l1)), flush=True)
+        assert rel_err(lt, l1) < 5e-3
+        if margin_ok(l1, 5e-3):
+            assert tok == int(one.read_tokens(P + T, 1)[0])
     finally:
         m.close()
         one.close()
