@@ -276,6 +276,35 @@ def family_profile(ctx, step, sets, flush, reps=12):
     return out
 
 
+# ---- the launch boundary ----------------------------------------------------------------------
+def launch_floor(ctx, n, reps=20):
+    """The cost of a kernel boundary when nothing else is done: chains of n stream-ordered
+    launches captured in one HIP graph and launched like a decode step, (a) 4 KB copies
+    of one workgroup, each reading what the previous one wrote, (b) 256 KB fills of 256
+    workgroups (a full grid, as the step's kernels have). Returns us per launch of each."""
+    buf = ctx.alloc(8192)
+    big = ctx.alloc(2 << 20)
+    ctx.call("ti_buf_fill_u32", buf, 1, 2048)
+
+    def copies():
+        for i in range(n):
+            src, dst = (0, 4096) if i % 2 == 0 else (4096, 0)
+            ctx.call("ti_buf_copy", buf, dst, buf, src, 4096)
+
+    def fills():
+        for i in range(n):
+            ctx.call("ti_buf_fill_u32", big.at((i % 8) << 18), i, 1 << 16)
+    out = []
+    for issue in (copies, fills):
+        g = graph_of(ctx, issue)
+        time_graphs(ctx, [g], 3)
+        out.append(time_graphs(ctx, [g], reps) * 1e3 / n)
+        ctx.graph_destroy(g)
+    buf.free()
+    big.free()
+    return out
+
+
 # ---- the Qwen3-1.7B int4 GEMV set (the north-star shapes), weights only ------------------------
 def gemv_set_1p7b(ctx, pool, flush, steps=20):
     """The int4 GEMV set of one Qwen3-1.7B batch-1 decode step, launched as the decode step
@@ -905,6 +934,8 @@ def main():
     for g in graphs:
         ctx.graph_destroy(g)
 
+    log("launch floor")
+    floor_copy_us, floor_us = launch_floor(ctx, step.launches)
     log("kernel families")
     flush = Flush(ctx)
     kern = family_profile(ctx, step, sets, flush)
@@ -934,6 +965,14 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "timing": timing, "traffic_source": traffic_src},
         "kernels": kern,
+        "launch_floor": {
+            "us_per_launch": round(floor_us, 3), "us_per_launch_1wg_copy": round(floor_copy_us, 3),
+            "launches": step.launches, "floor_ms_per_step": round(floor_us * step.launches * 1e-3, 4),
+            "step_over_floor": round(ms_per_step / (floor_us * step.launches * 1e-3), 3),
+            "what": "chains of %d stream-ordered launches in one HIP graph doing (almost) nothing: 256 KB fills "
+                    "of 256 workgroups (us_per_launch), 4 KB copies of one workgroup each reading the previous "
+                    "one's output (us_per_launch_1wg_copy); the step's kernel boundaries alone cost "
+                    "floor_ms_per_step; step_over_floor = ms_per_step / floor_ms_per_step" % step.launches},
     }
     if args.only == "moe":
         log("int3 MoE")
@@ -953,6 +992,11 @@ def main():
         out["decode_1p7b"] = decode_1p7b(ctx, pool, contexts=contexts)
         log("bonsai decode")
         out["bonsai_decode"] = bonsai_decode(ctx)
+        # the same boundary floor under each batch-1 step of its launch count
+        for leg in (out["gemv_set_1p7b"], out["ternary_bonsai_step"], out["ternary_gpu_format_step"],
+                    *(v for k, v in out["decode_1p7b"].items() if k.startswith("ctx_"))):
+            if isinstance(leg, dict) and "launches_per_step" in leg:
+                leg["launch_floor_ms"] = round(floor_us * leg["launches_per_step"] * 1e-3, 4)
     if not args.no_cpu:
         log("cpu baseline")
         cb = cpu_baseline()
