@@ -20,6 +20,9 @@ Beside it, each bounded to a few seconds (not `value`):
                 one step back to back in one graph, after a cache flush); the dominant
                 family by total time sets `roofline`
   gemv_set_1p7b the same GEMV set at the Qwen3-1.7B shapes (967.75 MB of int4 weights)
+  gemv_sustained_1p7b  the projection GEMV kernel at the 1.7B reduction sizes over 198 MB
+                of stacked rows per launch: its streaming rate with the launch amortised
+  launch_floor  chains of 113 stream-ordered launches that do (almost) nothing
   decode_1p7b   full Qwen3-1.7B int4/int8-KV decode step (the native decoder, one
                 graph per token, device-side token chaining) at 8k and 32k prefix
                 contexts: tokens/s and whole-step GB/s; and one T = 8 forward (8
@@ -302,6 +305,42 @@ def launch_floor(ctx, n, reps=20):
         ctx.graph_destroy(g)
     buf.free()
     big.free()
+    return out
+
+
+# ---- the projection kernel's sustained rate at the Qwen3-1.7B K's ----------------------------
+def gemv_sustained(ctx, pool, reps=12):
+    """The batch-1 projection GEMV (int8 activation codes x int4 weights, ti_gemv_q4_q8) over
+    many rows at the Qwen3-1.7B reduction sizes: the 28 layers' gate matrices stacked
+    (172032 x 2048, 198 MB) and their down matrices stacked (57344 x 6144, 198 MB), four
+    launches back to back in one graph over two weight sets (past the 256 MB Infinity
+    Cache). The kernel's streaming rate once its launch and first round trip are amortised,
+    which the decode step's 1-14 MB GEMVs never reach (see launch_floor)."""
+    rng = np.random.default_rng(77)
+    out = {}
+    for name, N, K in (("gate_x28_2048", 172032, 2048), ("down_x28_6144", 57344, 6144)):
+        sets = [pool.quantized(N, K, rng) for _ in range(2)]
+        x = ctx.upload(rng.standard_normal(K).astype(np.float32))
+        xq, xs, xsum = ctx.zeros(K), ctx.zeros(K // 8), ctx.zeros(K)
+        ctx.call("ti_quant_act_q8", x, xq, xs, xsum, K)
+        y = ctx.zeros(N * 4)
+
+        def issue():
+            for i in range(4):
+                p, sc = sets[i % 2]
+                ctx.call("ti_gemv_q4_q8", xq, xs, p, sc, y, N, K, 0)
+        g = graph_of(ctx, issue)
+        time_graphs(ctx, [g], 2)
+        us = time_graphs(ctx, [g], reps) * 1e3 / 4
+        ctx.graph_destroy(g)
+        nb = int4_bytes(N, K) + K + (K // 32) * 4 + N * 4
+        out[name] = {"N": N, "K": K, "us_per_launch": round(us, 2), "bytes_per_launch": nb,
+                     "GB_s": round(nb / (us * 1e-6) / 1e9, 1), "pct_of_hbm_peak": round(100 * nb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 1)}
+        for b in (x, xq, xs, xsum, y):
+            b.free()
+        for p, sc in sets:
+            p.free()
+            sc.free()
     return out
 
 
@@ -980,6 +1019,8 @@ def main():
     if args.only == "all":
         log("Qwen3-1.7B int4 GEMV set")
         out["gemv_set_1p7b"] = gemv_set_1p7b(ctx, pool, flush)
+        log("projection GEMV, sustained")
+        out["gemv_sustained_1p7b"] = gemv_sustained(ctx, pool)
         log("ternary step")
         out["ternary_bonsai_step"] = ternary_step(ctx)
         log("ternary step, on-GPU format")
