@@ -246,22 +246,43 @@ __global__ __launch_bounds__(256) void k_moe_gemv_q3(const float* __restrict__ x
 
 // ---- T > 1: rows of one expert against all pairs routed to it ----------------------
 // grid (row blocks of 16, experts). The workgroup scans the routing ids 256 at a time and
-// lists its expert's pairs in pair order (ballot compaction in LDS). On the first hit each
-// wave turns its 4 rows' bitplanes into (q + 4) bytes, kept in registers; every listed
-// pair then reads its int8 activation group (L2-resident) and scale:
+// lists its expert's pairs in pair order (ballot compaction in LDS). Each wave turns its 4
+// rows' bitplanes into (q + 4) bytes, kept in registers; the listed pairs then read their
+// int8 activation groups (L2-resident) and scales, four pairs' loads in flight at once:
 //   dot = sum (q + 4) a - 4 sum a   (exact int32),   y[pair, n] = sum_g dot * s_x * s_w.
-// Workgroups of experts nobody chose read only the ids.
+// spec (most experts are routed to, as at 16 tokens x top-4 over 32 experts): the weight
+// loads are issued before the scan, so their round trip overlaps it; otherwise they wait
+// for the first hit and the workgroups of experts nobody chose read only the ids.
+constexpr int MOE_PB = 4;          // pairs whose activation loads are in flight together
 template <int GL>
 __global__ __launch_bounds__(256) void k_moe_gemm_q3(const uint32_t* __restrict__ xq, const float* __restrict__ xs,
                                                      const uint32_t* __restrict__ p3, const uint16_t* __restrict__ s3,
                                                      const int32_t* __restrict__ ridx, float* __restrict__ y, int P, int N,
-                                                     int K, int src_div) {
+                                                     int K, int src_div, int spec) {
     __shared__ int s_list[256];
     __shared__ int s_wcnt[4];
     const int e = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int gpr = K / 32;
     const int row0 = blockIdx.x * 16 + wave * MOE_R;
+    uint32_t pb[MOE_R][GL][3];
+    uint16_t sr[MOE_R][GL];
+    auto wload = [&]() {
+#pragma unroll
+        for (int r = 0; r < MOE_R; r++) {
+            const int n = min(row0 + r, N - 1);
+#pragma unroll
+            for (int h = 0; h < GL; h++) {
+                const int g = lane + 64 * h;
+                const int gc = g < gpr ? g : gpr - 1;
+                const size_t gi = ((size_t)e * N + n) * gpr + gc;
+#pragma unroll
+                for (int b = 0; b < 3; b++) pb[r][h][b] = __builtin_nontemporal_load(p3 + gi * 3 + b);
+                sr[r][h] = s3[gi];
+            }
+        }
+    };
+    if (spec) wload();
     uint32_t qb[MOE_R][GL][8];
     float sw[MOE_R][GL];
     bool have = false;
@@ -281,49 +302,58 @@ __global__ __launch_bounds__(256) void k_moe_gemm_q3(const uint32_t* __restrict_
         if (tot == 0) continue;
         if (!have) {
             have = true;
+            if (!spec) wload();
 #pragma unroll
-            for (int r = 0; r < MOE_R; r++) {
-                const int n = min(row0 + r, N - 1);
+            for (int r = 0; r < MOE_R; r++)
+#pragma unroll
+                for (int h = 0; h < GL; h++) {
+                    const int g = lane + 64 * h;
+                    sw[r][h] = g < gpr ? ti_h2f(sr[r][h]) : 0.0f;
+#pragma unroll
+                    for (int w = 0; w < 8; w++) qb[r][h][w] = q3_bytes(pb[r][h][0], pb[r][h][1], pb[r][h][2], 4 * w);
+                }
+        }
+        for (int i0 = 0; i0 < tot; i0 += MOE_PB) {
+            uint4 u0[MOE_PB][GL], u1[MOE_PB][GL];
+            float as[MOE_PB][GL];
+            int pairs[MOE_PB];
+#pragma unroll
+            for (int q = 0; q < MOE_PB; q++) {   // every pair's loads first (past tot: the last pair again)
+                pairs[q] = s_list[min(i0 + q, tot - 1)];
+                const int src = pairs[q] / src_div;
 #pragma unroll
                 for (int h = 0; h < GL; h++) {
                     const int g = lane + 64 * h;
                     const int gc = g < gpr ? g : gpr - 1;
-                    const size_t gi = ((size_t)e * N + n) * gpr + gc;
-                    const uint32_t b0 = __builtin_nontemporal_load(p3 + gi * 3);
-                    const uint32_t b1 = __builtin_nontemporal_load(p3 + gi * 3 + 1);
-                    const uint32_t b2 = __builtin_nontemporal_load(p3 + gi * 3 + 2);
-                    sw[r][h] = g < gpr ? ti_h2f(s3[gi]) : 0.0f;
-#pragma unroll
-                    for (int w = 0; w < 8; w++) qb[r][h][w] = q3_bytes(b0, b1, b2, 4 * w);
+                    const uint4* a4 = reinterpret_cast<const uint4*>(xq + (size_t)src * (K / 4) + gc * 8);
+                    u0[q][h] = a4[0];
+                    u1[q][h] = a4[1];
+                    as[q][h] = xs[(size_t)src * gpr + gc];
                 }
             }
-        }
-        for (int i = 0; i < tot; i++) {
-            const int pair = s_list[i];
-            const int src = pair / src_div;
-            float accv[MOE_R] = {};
 #pragma unroll
-            for (int h = 0; h < GL; h++) {
-                const int g = lane + 64 * h;
-                const int gc = g < gpr ? g : gpr - 1;
-                const uint4* a4 = reinterpret_cast<const uint4*>(xq + (size_t)src * (K / 4) + gc * 8);
-                const uint4 u0 = a4[0], u1 = a4[1];
-                const float as = xs[(size_t)src * gpr + gc];
-                const int a[8] = {(int)u0.x, (int)u0.y, (int)u0.z, (int)u0.w, (int)u1.x, (int)u1.y, (int)u1.z, (int)u1.w};
-                int asum = 0;
+            for (int q = 0; q < MOE_PB; q++) {
+                if (i0 + q >= tot) break;                   // workgroup-uniform
+                float accv[MOE_R] = {};
 #pragma unroll
-                for (int w = 0; w < 8; w++) asum = __builtin_amdgcn_sdot4(a[w], 0x01010101, asum, false);
+                for (int h = 0; h < GL; h++) {
+                    const int a[8] = {(int)u0[q][h].x, (int)u0[q][h].y, (int)u0[q][h].z, (int)u0[q][h].w,
+                                      (int)u1[q][h].x, (int)u1[q][h].y, (int)u1[q][h].z, (int)u1[q][h].w};
+                    int asum = 0;
 #pragma unroll
-                for (int r = 0; r < MOE_R; r++) {
-                    int d = 0;
+                    for (int w = 0; w < 8; w++) asum = __builtin_amdgcn_sdot4(a[w], 0x01010101, asum, false);
 #pragma unroll
-                    for (int w = 0; w < 8; w++) d = __builtin_amdgcn_sdot4((int)qb[r][h][w], a[w], d, false);
-                    accv[r] = fmaf((float)(d - 4 * asum), as * sw[r][h], accv[r]);
+                    for (int r = 0; r < MOE_R; r++) {
+                        int d = 0;
+#pragma unroll
+                        for (int w = 0; w < 8; w++) d = __builtin_amdgcn_sdot4((int)qb[r][h][w], a[w], d, false);
+                        accv[r] = fmaf((float)(d - 4 * asum), as[q][h] * sw[r][h], accv[r]);
+                    }
                 }
+                const float tot_r = transpose_reduce<64, MOE_R>(accv, lane);
+                const int n = row0 + lane / (64 / MOE_R);
+                if ((lane % (64 / MOE_R)) == 0 && n < N) y[(size_t)pairs[q] * N + n] = tot_r;
             }
-            const float tot_r = transpose_reduce<64, MOE_R>(accv, lane);
-            const int n = row0 + lane / (64 / MOE_R);
-            if ((lane % (64 / MOE_R)) == 0 && n < N) y[(size_t)pair * N + n] = tot_r;
         }
     }
 }
@@ -712,8 +742,9 @@ extern "C" int ti_moe_gemm_q3(ti_ctx* c, const float* src, int src_rows, const u
     int rc = ti_quant_act_q8_async(c, src, c->act_q, c->act_s, nullptr, src_rows * (K / 32));
     if (rc) return rc;
     dim3 grid((unsigned)((N + 15) / 16), (unsigned)nE);
-    if (K <= 2048) k_moe_gemm_q3<1><<<grid, 256, 0, c->stream>>>(c->act_q, c->act_s, p3, s3, ridx, y, P, N, K, src_div);
-    else k_moe_gemm_q3<2><<<grid, 256, 0, c->stream>>>(c->act_q, c->act_s, p3, s3, ridx, y, P, N, K, src_div);
+    const int spec = 2 * P >= nE;   // most experts are routed to: weights loaded before the scan
+    if (K <= 2048) k_moe_gemm_q3<1><<<grid, 256, 0, c->stream>>>(c->act_q, c->act_s, p3, s3, ridx, y, P, N, K, src_div, spec);
+    else k_moe_gemm_q3<2><<<grid, 256, 0, c->stream>>>(c->act_q, c->act_s, p3, s3, ridx, y, P, N, K, src_div, spec);
     TI_LAUNCHED("k_moe_gemm_q3");
     return TI_OK;
 }
