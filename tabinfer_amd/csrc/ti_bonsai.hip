@@ -170,53 +170,6 @@ __global__ __launch_bounds__(BN_THREADS) void k_bn_swiglu_quant(const float* __r
     quant_n2<EPT>(v, n, act, xsum, scale_out, red);
 }
 
-// ---- q/k/v: scale, per-head RMSNorm, RoPE, KV append (model.rs:399-418) -----------------------
-// workgroup h < nHq: query head h -> qr; nHq <= h < nHq + nKv: KV head h - nHq -> the K row
-// (normed, roped) and the V row (scaled) of position P in the f32 cache. hd threads.
-__global__ __launch_bounds__(128) void k_bn_prep(const float* __restrict__ qraw, const float* __restrict__ kraw,
-                                                 const float* __restrict__ vraw, const float* __restrict__ scale,
-                                                 const float* __restrict__ qn, const float* __restrict__ kn,
-                                                 const float* __restrict__ rope, const int* __restrict__ dpos,
-                                                 float* __restrict__ qr, float* __restrict__ kc, float* __restrict__ vc,
-                                                 int nHq, int nKv, int hd, float eps, int cap) {
-    __shared__ float red[128];
-    __shared__ float y[128];
-    const int i = threadIdx.x, h = blockIdx.x, half = hd / 2;
-    const int P = *dpos;
-    if (P >= cap) return;
-    const bool isq = h < nHq;
-    const int hh = isq ? h : h - nHq;
-    const float inv = 1.0f / *scale;
-    const float raw = i < hd ? (isq ? qraw : kraw)[(size_t)hh * hd + i] : 0.0f;
-    const float a = raw * inv;
-    red[i] = i < hd ? a * a : 0.0f;
-    __syncthreads();
-    for (int st = 64; st > 0; st >>= 1) {
-        if (i < st) red[i] = red[i] + red[i + st];
-        __syncthreads();
-    }
-    const float mean = red[0] / (float)hd;
-    const float rinv = 1.0f / sqrtf(mean + eps);
-    const float nw = i < hd ? (isq ? qn : kn)[i] : 0.0f;
-    const float yn = a * rinv * nw;
-    y[i] = yn;
-    __syncthreads();
-    if (i < hd) {
-        const float* tab = rope + (size_t)P * hd;
-        const int j = i < half ? i : i - half;
-        const float c = tab[j], s = tab[half + j];
-        const float x0 = y[j], x1 = y[half + j];
-        const float r = i < half ? x0 * c - x1 * s : x1 * c + x0 * s;
-        const size_t kv_dim = (size_t)nKv * hd;
-        if (isq) {
-            qr[(size_t)hh * hd + i] = r;
-        } else {
-            kc[(size_t)P * kv_dim + (size_t)hh * hd + i] = r;
-            vc[(size_t)P * kv_dim + (size_t)hh * hd + i] = vraw[(size_t)hh * hd + i] * inv;
-        }
-    }
-}
-
 // ---- GQA attention over the f32 cache (model.rs:421-447) ------------------------------------
 // keys per attention workgroup for a cache of cap positions: 64, or more for longer caches, so
 // that the grid (8 KV heads x splits) stays within one round of resident workgroups (three
@@ -227,44 +180,102 @@ __host__ __device__ inline int bn_chunk(int cap) {
 }
 
 // workgroup (KV head hk, split of CH keys), the G = 2 query heads of hk (hd 128):
+//  prologue (model.rs:399-418): q of both heads scaled by 1/scale, per-head RMSNorm (the sum
+//          of squares as a 64..1 tree), the q_norm weight and split-half RoPE at position P,
+//          into LDS (every workgroup); the workgroup whose split holds P also forms K (scaled,
+//          k_norm, RoPE) and V (scaled) of hk at P, stores them into the cache and waits for
+//          the stores before it loads its keys (no other workgroup reads row P);
 //  scores: 4 lanes per key, 32 dims each (8 float4 loads a lane, in flight together), a quad
 //          sum, 64 keys per pass;
 //  max / exp / sum over the split's keys;
 //  P V: lane (key group kg = t / 32, dims 4 (t % 32) ..) over keys kg, kg + 8, .. (one float4
 //       of V serves both heads), then the 8 key-group partials summed in order;
 //  partials (o, m, l) per (query head, split).
+// RMSNorm of one head row held one element per thread (the 128 threads with act, element
+// i, LDS slots from `base`): the sum of squares as a 64..1 tree in red, then split-half RoPE
+// from the table row. Every thread of the workgroup calls it (it holds barriers); only
+// those with act write.
+__device__ __forceinline__ float bn_head_norm_rope(float a, int i, float nw, const float* tab, float eps, float* red,
+                                                   float* y, int base, bool act) {
+    constexpr int HD = 128, half = HD / 2;
+    if (act) red[base + i] = a * a;
+    __syncthreads();
+    for (int st = 64; st > 0; st >>= 1) {
+        if (act && i < st) red[base + i] = red[base + i] + red[base + i + st];
+        __syncthreads();
+    }
+    const float mean = red[base] / (float)HD;
+    const float rinv = 1.0f / sqrtf(mean + eps);
+    if (act) y[base + i] = a * rinv * nw;
+    __syncthreads();
+    const int j = i < half ? i : i - half;
+    const float c = tab[j], s = tab[half + j];
+    const float x0 = y[base + j], x1 = y[base + half + j];
+    return i < half ? x0 * c - x1 * s : x1 * c + x0 * s;
+}
+
 template <int CH>
-__global__ __launch_bounds__(256) void k_bn_attn(const float* __restrict__ qr, const float* __restrict__ kc,
-                                                 const float* __restrict__ vc, const int* __restrict__ dpos, int nKv,
+__global__ __launch_bounds__(256) void k_bn_attn(const float* __restrict__ qraw, const float* __restrict__ kraw,
+                                                 const float* __restrict__ vraw, const float* __restrict__ act_scale,
+                                                 const float* __restrict__ qn, const float* __restrict__ kn,
+                                                 const float* __restrict__ rope, float eps, float* __restrict__ kc,
+                                                 float* __restrict__ vc, const int* __restrict__ dpos, int nKv,
                                                  float* __restrict__ po, float* __restrict__ pml, int ns_stride, int cap) {
     constexpr int G = 2, HD = 128;
     __shared__ float sc[G][CH];
     __shared__ float4 so[8][G][HD / 4];
     __shared__ float red[G][4];
+    __shared__ __align__(16) float s_q[G][HD];
+    __shared__ float s_red[G * HD], s_y[G * HD];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int hk = blockIdx.x % nKv, split = blockIdx.x / nKv;
-    const int S = min(*dpos + 1, cap);
+    const int P = *dpos;
+    const int S = min(P + 1, cap);
     const int c0 = split * CH;
     if (c0 >= S) return;                               // the merge reads splits below ceil(S / CH) only
     const int n = min(CH, S - c0);
+    const bool own = P < cap && P < c0 + CH;           // this split holds row P: it writes K, V there first
     const size_t kvd = (size_t)nKv * HD;
     const float scale = 1.0f / sqrtf((float)HD);
     const int qd = t & 3;
+    // prologue loads: raw q of both heads (thread t: head t / 128, dim t % 128), the scale,
+    // the norm weight and the rope row of P; the own split's K, V raw rows as well
+    const int pg = t >> 7, pi = t & 127;
+    const float inv = 1.0f / *act_scale;
+    const float qa = qraw[(size_t)(hk * G + pg) * HD + pi] * inv;
+    const float qnw = qn[pi];
+    const float* tab = rope + (size_t)(P < cap ? P : 0) * HD;
+    // the V rows of the first 64 keys, for the P V pass below, issued before the K loads so
+    // that both tiles are in flight together (one memory round trip instead of two); the
+    // own split issues them after its stores of row P have landed
+    const int kg = t >> 5, d4 = t & 31;
+    const float4* vb = reinterpret_cast<const float4*>(vc + (size_t)c0 * kvd + (size_t)hk * HD) + d4;
+    float4 vpre[8];
+    auto vload = [&]() {
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int j = kg + 8 * i;
+            vpre[i] = vb[(size_t)(j < n ? j : n - 1) * (kvd / 4)];
+        }
+    };
+    if (!own) vload();
+    s_q[pg][pi] = bn_head_norm_rope(qa, pi, qnw, tab, eps, s_red, s_y, pg * HD, true);
+    if (own) {   // K (threads 0..127) and V (128..255) of hk at P (model.rs:405-418)
+        const size_t row = (size_t)P * kvd + (size_t)hk * HD + pi;
+        __syncthreads();   // every thread has read the q tree's slots
+        const float kr = bn_head_norm_rope(kraw[(size_t)hk * HD + pi] * inv, pi, kn[pi], tab, eps, s_red, s_y, 0, pg == 0);
+        if (pg == 0) kc[row] = kr;
+        else vc[row] = vraw[(size_t)hk * HD + pi] * inv;
+        ti_stores_done();
+        __syncthreads();
+        vload();
+    }
+    __syncthreads();
     float4 q[G][8];
 #pragma unroll
     for (int g = 0; g < G; g++)
 #pragma unroll
-        for (int i = 0; i < 8; i++) q[g][i] = reinterpret_cast<const float4*>(qr + (size_t)(hk * G + g) * HD + qd * 32)[i];
-    // the V rows of the first 64 keys, for the P V pass below, issued before the K loads so
-    // that both tiles are in flight together (one memory round trip instead of two)
-    const int kg = t >> 5, d4 = t & 31;
-    const float4* vb = reinterpret_cast<const float4*>(vc + (size_t)c0 * kvd + (size_t)hk * HD) + d4;
-    float4 vpre[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const int j = kg + 8 * i;
-        vpre[i] = vb[(size_t)(j < n ? j : n - 1) * (kvd / 4)];
-    }
+        for (int i = 0; i < 8; i++) q[g][i] = reinterpret_cast<const float4*>(&s_q[g][qd * 32])[i];
     for (int k0 = 0; k0 < n; k0 += 64) {
         const int j = k0 + (t >> 2);
         const int key = c0 + (j < n ? j : n - 1);
@@ -548,7 +559,7 @@ struct ti_bonsai {
     uint16_t* embed = nullptr;
     float* final_norm = nullptr;
     TLin lm;
-    float *x, *xn, *qraw, *kraw, *vraw, *qr, *attn, *oraw, *graw, *uraw, *swi, *draw, *lraw, *logits;
+    float *x, *xn, *qraw, *kraw, *vraw, *attn, *oraw, *graw, *uraw, *swi, *draw, *lraw, *logits;
     int8_t* act;
     int32_t* xsum;
     float* scales;        // [4]: a (input norm), b (attention), c (post norm), d (swi)
@@ -660,7 +671,7 @@ extern "C" int ti_bonsai_create(ti_ctx* c, const ti_bonsai_config* cfg, ti_bonsa
     const int widest = I > H ? (I > nq ? I : nq) : (H > nq ? H : nq);
     const int nsplit = (C.max_ctx + bn_chunk(C.max_ctx) - 1) / bn_chunk(C.max_ctx);
     struct { float** p; size_t n; } fb[] = {{&m->x, (size_t)H}, {&m->xn, (size_t)H}, {&m->qraw, (size_t)nq},
-                                            {&m->kraw, (size_t)nkv}, {&m->vraw, (size_t)nkv}, {&m->qr, (size_t)nq},
+                                            {&m->kraw, (size_t)nkv}, {&m->vraw, (size_t)nkv},
                                             {&m->attn, (size_t)nq}, {&m->oraw, (size_t)H}, {&m->graw, (size_t)I},
                                             {&m->uraw, (size_t)I}, {&m->swi, (size_t)I}, {&m->draw, (size_t)H},
                                             {&m->lraw, (size_t)C.vocab}, {&m->logits, (size_t)C.vocab}, {&m->scales, 4},
@@ -874,13 +885,13 @@ static int bonsai_step(ti_ctx* c, ti_bonsai* m, bool want_logits) {
             RC(bput(c, m, l, B_K, m->kraw));
             RC(bput(c, m, l, B_V, m->vraw));
         }
-        k_bn_prep<<<nHq + nKv, 128, 0, c->stream>>>(m->qraw, m->kraw, m->vraw, sa, y.q_norm, y.k_norm, m->rope, m->dpos, m->qr,
-                                                    y.kc, y.vc, nHq, nKv, hd, C.rms_eps, C.max_ctx);
-        TI_LAUNCHED("k_bn_prep");
         const int chunk = bn_chunk(C.max_ctx);
-        if (chunk == 64) k_bn_attn<64><<<nKv * nsplit, 256, 0, c->stream>>>(m->qr, y.kc, y.vc, m->dpos, nKv, m->po, m->pml, nsplit, C.max_ctx);
-        else if (chunk == 128) k_bn_attn<128><<<nKv * nsplit, 256, 0, c->stream>>>(m->qr, y.kc, y.vc, m->dpos, nKv, m->po, m->pml, nsplit, C.max_ctx);
-        else k_bn_attn<256><<<nKv * nsplit, 256, 0, c->stream>>>(m->qr, y.kc, y.vc, m->dpos, nKv, m->po, m->pml, nsplit, C.max_ctx);
+#define BA(CH_) k_bn_attn<CH_><<<nKv * nsplit, 256, 0, c->stream>>>(m->qraw, m->kraw, m->vraw, sa, y.q_norm, y.k_norm, m->rope, \
+                                                                    C.rms_eps, y.kc, y.vc, m->dpos, nKv, m->po, m->pml, nsplit, C.max_ctx)
+        if (chunk == 64) BA(64);
+        else if (chunk == 128) BA(128);
+        else BA(256);
+#undef BA
         TI_LAUNCHED("k_bn_attn");
         const int eq = (nq + BN_THREADS - 1) / BN_THREADS;
 #define MQ(E) if (eq <= E) { k_bn_merge_quant<E><<<nKv, BN_THREADS, 0, c->stream>>>(m->po, m->pml, m->dpos, nsplit, nq, chunk, m->attn, m->act, m->xsum, sb, c->sync + TI_SYNC_BONSAI, C.max_ctx); }
