@@ -184,11 +184,13 @@ def test_linear_router(ctx, orc, T, N, K):
 
 @pytest.mark.parametrize("T,N,K", [(2, 2048, 2048), (8, 6144, 2048), (8, 2048, 6144), (16, 1024, 1024),
                                    (17, 4096, 2048), (40, 96, 320), (8, 1000, 3072), (256, 256, 1024),
-                                   (16, 2048, 6144), (3, 1000, 6144)])
+                                   (16, 2048, 6144), (3, 1000, 6144), (5, 2048, 2048), (7, 4096, 1024),
+                                   (9, 2048, 2048)])
 def test_gemm_mfma_batched_linear(ctx, orc, T, N, K):
     """linearQ at T > 1 (models/qwen3.js:1604-1607): per-token quantQ8T + the MFMA int4 x int8
     GEMM; max relative error 1e-3 against the f64 oracle of the quantized operands, with and
-    without the fused residual."""
+    without the fused residual. T <= 8 takes the pairwise-group MFMA (odd T: padding token
+    rows repeat the last token), T = 9 the one-group-per-MFMA loop."""
     rng = np.random.default_rng(T * 131 + N + K)
     pack, sc, dp, ds = _weights(ctx, orc, rng, N, K)
     X = rng.standard_normal(T * K).astype(np.float32)
