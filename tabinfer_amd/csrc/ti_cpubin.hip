@@ -297,11 +297,15 @@ static int cpubin_assemble(const uint8_t* hdr, size_t hdr_len, ti_cpubin* c) {
             if ((rc = usize_field(t, name, "codesLen", &x.codes_len)) || (rc = usize_field(t, name, "scalesLen", &x.scales_len)))
                 return rc;
             // the declared byte counts against the shape: a packer/reader disagreement
-            // fails here, at load, instead of as plausible garbage at inference
-            if (x.codes_len != x.N * x.K / 4)
-                return ti_fail(TI_ERR_INVALID, "%s: codesLen=%lld but N*K/4=%lld", name, x.codes_len, x.N * x.K / 4);
-            if (x.scales_len != x.N * (x.K / G) * 4)
-                return ti_fail(TI_ERR_INVALID, "%s: scalesLen=%lld but N*(K/G)*4=%lld", name, x.scales_len, x.N * (x.K / G) * 4);
+            // fails here, at load, instead of as plausible garbage at inference (the products
+            // in checked arithmetic: N and K may each be up to 2^62)
+            long long nk = 0, ng4 = 0;
+            if (__builtin_mul_overflow(x.N, x.K, &nk) || __builtin_mul_overflow(x.N, (x.K / G) * 4, &ng4))
+                return ti_fail(TI_ERR_INVALID, "%s: N=%lld x K=%lld overflows the byte counts", name, x.N, x.K);
+            if (x.codes_len != nk / 4)
+                return ti_fail(TI_ERR_INVALID, "%s: codesLen=%lld but N*K/4=%lld", name, x.codes_len, nk / 4);
+            if (x.scales_len != ng4)
+                return ti_fail(TI_ERR_INVALID, "%s: scalesLen=%lld but N*(K/G)*4=%lld", name, x.scales_len, ng4);
             if ((rc = usize_field(t, name, "codesOff", &x.codes_off)) || (rc = usize_field(t, name, "scalesOff", &x.scales_off)))
                 return rc;
         } else if (kind->str == "embed_f16" || kind->str == "f32") {
@@ -324,8 +328,10 @@ static int cpubin_assemble(const uint8_t* hdr, size_t hdr_len, ti_cpubin* c) {
     // every declared byte range lies inside the blob (binfmt.rs:229-250)
     const long long blob = (long long)c->blob_len;
     auto inside = [&](const ti_cpubin::Tensor& t, long long off, long long len) -> int {
-        if (off + len > blob)
-            return ti_fail(TI_ERR_INVALID, "%s: range %lld..%lld overruns the %lld-byte blob", t.name.c_str(), off, off + len, blob);
+        // off and len are each in [0, 2^62]: compare without forming a sum that could wrap
+        if (off > blob || len > blob - off)
+            return ti_fail(TI_ERR_INVALID, "%s: range at %lld of %lld bytes overruns the %lld-byte blob", t.name.c_str(), off,
+                           len, blob);
         return TI_OK;
     };
     for (auto& t : c->tensors) {

@@ -74,6 +74,10 @@ def test_rejects_an_overrunning_range():
     (container({"w": tern(2, 64, 0, 112)}, bytes(116)), "overruns"),
     (container({"w": dict(tern(2, 64, 0, 32), N=-2)}, bytes(128)), "non-negative integer"),
     (container({"e": {"kind": "embed_f16", "shape": [2, "x"], "off": 0, "len": 8}}, bytes(16)), "shape"),
+    # ranges and shapes near the 2^62 field limit: no sum or product may wrap past a check
+    (container({"w": {"kind": "f32", "shape": [1], "off": 1 << 62, "len": 1 << 62}}, bytes(16)), "overruns"),
+    (container({"w": {"kind": "f32", "shape": [1], "off": 8, "len": (1 << 62) - 4}}, bytes(16)), "overruns"),
+    (container({"w": tern(1 << 40, 1 << 40, 0, 0, codesLen=0, scalesLen=0)}, bytes(16)), "overflows"),
 ])
 def test_rejects_each_rule(data, needle):
     refused(data, needle)
