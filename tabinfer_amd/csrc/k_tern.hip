@@ -128,12 +128,33 @@ struct TernMats {
     int nmat;
 };
 
-template <int LPR, int BPL>
+//
+// NQE > 0: the input is the residual x (+ add / add_scale) instead of ready codes. Every
+// workgroup runs the Bonsai decoder's residual add, RMSNorm and n2 quantizer over the whole
+// K = 256 NQE vector itself (NQE consecutive elements per thread; the same inputs and the
+// same operations in every workgroup, so every workgroup holds the same codes), keeps the
+// codes and block sums in LDS, and workgroup 0 publishes x + add, xn, the codes, the block
+// sums and the scale for the kernels after this one. The norm's loads are issued before
+// the weights', so its waits do not wait for the weight stream.
+//
+// SWI: the input is the gate/up pair instead: every workgroup forms the SwiGLU of the scaled
+// gate/up over the whole K = 2048 BPL vector (element 8 (tid + 256 k) + i at thread tid, so
+// a 64-code block is 8 threads' chunks) and the n2 quantizer of it, and workgroup 0
+// publishes the SwiGLU output, the codes, the block sums and the scale.
+template <int LPR, int BPL, int NQE, bool SWI = false>
 __global__ __launch_bounds__(256) void k_tern_gemv_rw(TernMats m, const int8_t* __restrict__ act,
-                                                      const int32_t* __restrict__ xsum) {
+                                                      const int32_t* __restrict__ xsum, ti_tern_norm nq,
+                                                      ti_tern_swiglu sw) {
     constexpr int RW = 64 / LPR, NB = LPR * BPL, RPB = 4 * RW;
     static_assert(NB % 4 == 0, "four products per LDS read");
+    static_assert(NQE == 0 || (NB * 64 == 256 * NQE && NQE % 4 == 0 && 64 % NQE == 0), "norm width = K");
+    static_assert(!SWI || (NQE == 0 && LPR == 32), "SwiGLU prologue: K = 2048 BPL");
+    constexpr bool PRO = NQE > 0 || SWI;
+    constexpr int NQA = PRO ? 64 * NB / 4 : 1, NQB = PRO ? NB : 1;
     __shared__ float4 s_pq[4][RW][2][NB / 4];
+    __shared__ __align__(16) uint32_t s_act[NQA];
+    __shared__ int32_t s_xs[NQB];
+    __shared__ float s_red[8];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r = lane / LPR, li = lane % LPR;
     // the matrix of this workgroup (uniform: selects, no divergent indexing of the kernargs)
@@ -148,11 +169,159 @@ __global__ __launch_bounds__(256) void k_tern_gemv_rw(TernMats m, const int8_t* 
     const long rowc = row < N ? row : N - 1;
     uint4 cw[BPL];
     float sc[BPL], xs[BPL];
+    constexpr int NQR = NQE > 0 ? NQE : 1;
+    float nx[NQR], na[NQR], nw[NQR];
+    if constexpr (NQE > 0) {
+#pragma unroll
+        for (int i = 0; i < NQE; i += 4) {
+            const float4 x4 = *reinterpret_cast<const float4*>(nq.x + tid * NQE + i);
+            const float4 w4 = *reinterpret_cast<const float4*>(nq.w + tid * NQE + i);
+            const float4 a4 = nq.add ? *reinterpret_cast<const float4*>(nq.add + tid * NQE + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+            nx[i] = x4.x; nx[i + 1] = x4.y; nx[i + 2] = x4.z; nx[i + 3] = x4.w;
+            nw[i] = w4.x; nw[i + 1] = w4.y; nw[i + 2] = w4.z; nw[i + 3] = w4.w;
+            na[i] = a4.x; na[i + 1] = a4.y; na[i + 2] = a4.z; na[i + 3] = a4.w;
+        }
+        TI_ISSUE_FENCE();
+    }
+    constexpr int SWR = SWI ? 8 * BPL : 1;
+    float sg[SWR], su[SWR];
+    if constexpr (SWI) {
+#pragma unroll
+        for (int k = 0; k < BPL; k++)
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const size_t e = (size_t)8 * (tid + 256 * k) + 4 * h;
+                const float4 g4 = *reinterpret_cast<const float4*>(sw.g + e);
+                const float4 u4 = *reinterpret_cast<const float4*>(sw.u + e);
+                sg[8 * k + 4 * h] = g4.x; sg[8 * k + 4 * h + 1] = g4.y; sg[8 * k + 4 * h + 2] = g4.z; sg[8 * k + 4 * h + 3] = g4.w;
+                su[8 * k + 4 * h] = u4.x; su[8 * k + 4 * h + 1] = u4.y; su[8 * k + 4 * h + 2] = u4.z; su[8 * k + 4 * h + 3] = u4.w;
+            }
+        TI_ISSUE_FENCE();
+    }
 #pragma unroll
     for (int j = 0; j < BPL; j++) {
         cw[j] = ti_ld_nt(codes + rowc * NB + li + LPR * j);
         sc[j] = scales[rowc * NB + li + LPR * j];
-        xs[j] = (float)xsum[li + LPR * j];
+        if constexpr (!PRO) xs[j] = (float)xsum[li + LPR * j];
+    }
+    const int8_t* av = act;
+    if constexpr (SWI) {
+        TI_ISSUE_FENCE();
+        // ops.rs:110-117 on the scaled gate/up, then quantize_act (tern.rs:206-222)
+        const float inv = 1.0f / *sw.gu_scale;
+        float mx = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8 * BPL; e++) {
+            const float gg = sg[e] * inv;
+            const float uu = su[e] * inv;
+            sg[e] = (gg / (1.0f + expf(-gg))) * uu;
+            mx = fmaxf(mx, fabsf(sg[e]));
+        }
+        mx = ti_wave_max(mx);
+        if (lane == 0) s_red[4 + wave] = mx;
+        __syncthreads();
+        const float amax = fmaxf(fmaxf(s_red[4], s_red[5]), fmaxf(s_red[6], s_red[7]));
+        const float qs = amax > 0.0f ? 127.0f / amax : 1.0f;
+#pragma unroll
+        for (int k = 0; k < BPL; k++) {
+            const int ch = tid + 256 * k;                // 8-element chunk; block ch / 8
+            uint32_t wd[2];
+            int bs = 0;
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                uint32_t w = 0;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    float rq = roundf(sg[8 * k + 4 * h + i] * qs);
+                    rq = fminf(fmaxf(rq, -127.0f), 127.0f);
+                    const int q = (int)rq;
+                    bs += q;
+                    w |= (uint32_t)(q & 0xff) << (8 * i);
+                }
+                wd[h] = w;
+            }
+            *reinterpret_cast<uint2*>(&s_act[2 * ch]) = make_uint2(wd[0], wd[1]);
+            bs += __shfl_xor(bs, 4);
+            bs += __shfl_xor(bs, 2);
+            bs += __shfl_xor(bs, 1);
+            if ((tid & 7) == 0) s_xs[ch / 8] = bs;
+            if (blockIdx.x == 0) {
+                *reinterpret_cast<float4*>(sw.swi_out + 8 * ch) = make_float4(sg[8 * k], sg[8 * k + 1], sg[8 * k + 2], sg[8 * k + 3]);
+                *reinterpret_cast<float4*>(sw.swi_out + 8 * ch + 4) =
+                    make_float4(sg[8 * k + 4], sg[8 * k + 5], sg[8 * k + 6], sg[8 * k + 7]);
+                *reinterpret_cast<uint2*>(sw.act_out + 8 * ch) = make_uint2(wd[0], wd[1]);
+                if ((tid & 7) == 0) sw.xsum_out[ch / 8] = bs;
+            }
+        }
+        if (blockIdx.x == 0 && tid == 0) *sw.scale_out = qs;
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < BPL; j++) xs[j] = (float)s_xs[li + LPR * j];
+        av = reinterpret_cast<const int8_t*>(s_act);
+    }
+    if constexpr (NQE > 0) {
+        TI_ISSUE_FENCE();
+        constexpr int TPB = 64 / NQE;                    // threads per 64-code block
+        const float inv_add = nq.add ? 1.0f / *nq.add_scale : 0.0f;
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NQE; i++) {
+            if (nq.add) {
+                const float d = na[i] * inv_add;
+                nx[i] = nx[i] + d;
+            }
+            ss = ss + nx[i] * nx[i];
+        }
+        ss = ti_wave_sum(ss);
+        if (lane == 0) s_red[wave] = ss;
+        __syncthreads();
+        const float mean = (s_red[0] + s_red[1] + s_red[2] + s_red[3]) / (float)(256 * NQE);
+        const float inv = 1.0f / sqrtf(mean + nq.eps);
+        float mx = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NQE; i++) {
+            na[i] = nx[i] * inv * nw[i];                  // xn
+            mx = fmaxf(mx, fabsf(na[i]));
+        }
+        mx = ti_wave_max(mx);
+        if (lane == 0) s_red[4 + wave] = mx;
+        __syncthreads();
+        const float amax = fmaxf(fmaxf(s_red[4], s_red[5]), fmaxf(s_red[6], s_red[7]));
+        const float qs = amax > 0.0f ? 127.0f / amax : 1.0f;
+        uint32_t wd[NQE / 4];
+        int bs = 0;
+#pragma unroll
+        for (int k = 0; k < NQE / 4; k++) {
+            uint32_t w = 0;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                float rq = roundf(na[4 * k + i] * qs);
+                rq = fminf(fmaxf(rq, -127.0f), 127.0f);
+                const int q = (int)rq;
+                bs += q;
+                w |= (uint32_t)(q & 0xff) << (8 * i);
+            }
+            wd[k] = w;
+            s_act[tid * (NQE / 4) + k] = w;
+        }
+#pragma unroll
+        for (int o = TPB / 2; o > 0; o >>= 1) bs += __shfl_xor(bs, o);
+        if (tid % TPB == 0) s_xs[tid / TPB] = bs;
+        if (blockIdx.x == 0) {
+#pragma unroll
+            for (int i = 0; i < NQE; i += 4) {
+                *reinterpret_cast<float4*>(nq.x_out + tid * NQE + i) = make_float4(nx[i], nx[i + 1], nx[i + 2], nx[i + 3]);
+                *reinterpret_cast<float4*>(nq.xn_out + tid * NQE + i) = make_float4(na[i], na[i + 1], na[i + 2], na[i + 3]);
+            }
+#pragma unroll
+            for (int k = 0; k < NQE / 4; k++) reinterpret_cast<uint32_t*>(nq.act_out)[tid * (NQE / 4) + k] = wd[k];
+            if (tid % TPB == 0) nq.xsum_out[tid / TPB] = bs;
+            if (tid == 0) *nq.scale_out = qs;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < BPL; j++) xs[j] = (float)s_xs[li + LPR * j];
+        av = reinterpret_cast<const int8_t*>(s_act);
     }
     float* sp = reinterpret_cast<float*>(&s_pq[wave][r][0][0]);
     float* sq = reinterpret_cast<float*>(&s_pq[wave][r][1][0]);
@@ -160,7 +329,7 @@ __global__ __launch_bounds__(256) void k_tern_gemv_rw(TernMats m, const int8_t* 
     for (int j = 0; j < BPL; j++) {
         ActT t;
         const int blk = li + LPR * j;
-        load_act_tern(act, nullptr, blk, t);
+        load_act_tern(av, nullptr, blk, t);
         sp[blk] = sc[j] * (float)tern_block_dot(cw[j], t);
         sq[blk] = sc[j] * xs[j];
     }
@@ -191,7 +360,9 @@ static int rw_rows(int nb) {
 }
 
 // sets m.blk0 for the kernel's rows per workgroup and launches; false: no kernel for nb
-static bool rw_launch(ti_ctx* c, TernMats& m, int nb, const int8_t* act, const int32_t* xsum) {
+// (with nq: only K = 1024 and 2048, the norm prologue's widths)
+static bool rw_launch(ti_ctx* c, TernMats& m, int nb, const int8_t* act, const int32_t* xsum,
+                      const ti_tern_norm* nq = nullptr, const ti_tern_swiglu* sw = nullptr) {
     const int rpb = rw_rows(nb);
     if (!rpb) return false;
     long blocks = 0;
@@ -201,8 +372,21 @@ static bool rw_launch(ti_ctx* c, TernMats& m, int nb, const int8_t* act, const i
     }
     if (blocks >= (1L << 31)) return false;
     const unsigned grid = (unsigned)blocks;
+    const ti_tern_norm nnone = {};
+    const ti_tern_swiglu snone = {};
+    if (nq) {
+        if (nb == 32) { k_tern_gemv_rw<32, 1, 8><<<grid, 256, 0, c->stream>>>(m, act, xsum, *nq, snone); return true; }
+        if (nb == 16) { k_tern_gemv_rw<16, 1, 4><<<grid, 256, 0, c->stream>>>(m, act, xsum, *nq, snone); return true; }
+        return false;
+    }
+    if (sw) {
+        if (nb == 32) { k_tern_gemv_rw<32, 1, 0, true><<<grid, 256, 0, c->stream>>>(m, act, xsum, nnone, *sw); return true; }
+        if (nb == 64) { k_tern_gemv_rw<32, 2, 0, true><<<grid, 256, 0, c->stream>>>(m, act, xsum, nnone, *sw); return true; }
+        if (nb == 96) { k_tern_gemv_rw<32, 3, 0, true><<<grid, 256, 0, c->stream>>>(m, act, xsum, nnone, *sw); return true; }
+        return false;
+    }
 #define RW(L, P) \
-    if (nb == L * P) { k_tern_gemv_rw<L, P><<<grid, 256, 0, c->stream>>>(m, act, xsum); return true; }
+    if (nb == L * P) { k_tern_gemv_rw<L, P, 0><<<grid, 256, 0, c->stream>>>(m, act, xsum, nnone, snone); return true; }
     RW(32, 1) RW(32, 2) RW(32, 3) RW(32, 4) RW(16, 1) RW(16, 3) RW(16, 5) RW(16, 7)
 #undef RW
     return false;
@@ -387,6 +571,64 @@ extern "C" int ti_tern_gemv_multi(ti_ctx* c, const int8_t* act, const int32_t* x
     m.nmat = nmat;
     if (!rw_launch(c, m, K / 64, act, xsum)) return ti_fail(TI_ERR_INVALID, "ti_tern_gemv_multi: no kernel for K=%d", K);
     TI_LAUNCHED("k_tern_gemv_rw");
+    return TI_OK;
+}
+
+// q/k/v (or gate/up) of the Bonsai decoder with the residual add + RMSNorm + quantizer of
+// their input in every workgroup's prologue (k_tern_gemv_rw with NQE > 0): K = 1024 or 2048.
+bool ti_tern_norm_ok(int K) { return K == 1024 || K == 2048; }
+
+int ti_tern_gemv_multi_norm(ti_ctx* c, const ti_tern_norm* nq, int K, int nmat, const uint8_t* const* codes,
+                            const float* const* scales, float* const* outs, const int* Ns) {
+    TI_CHECK_CTX(c);
+    TI_REQUIRE(nq && nq->x && nq->w && nq->add_scale && nq->x_out && nq->xn_out && nq->act_out && nq->xsum_out &&
+                   nq->scale_out, "ti_tern_gemv_multi_norm: null norm buffer");
+    TI_REQUIRE(ti_tern_norm_ok(K), "ti_tern_gemv_multi_norm: K must be 1024 or 2048 (K=%d)", K);
+    TI_REQUIRE(nq->x_out != nq->x, "ti_tern_gemv_multi_norm: x_out must not alias x");
+    TI_REQUIRE(al16(nq->x) && al16(nq->w) && al16(nq->x_out) && al16(nq->xn_out) && al16(nq->act_out) &&
+                   (!nq->add || al16(nq->add)), "ti_tern_gemv_multi_norm: vectors must be 16-byte aligned");
+    TI_REQUIRE(nmat >= 1 && nmat <= 3 && codes && scales && outs && Ns, "ti_tern_gemv_multi_norm: bad matrices");
+    TernMats m = {};
+    for (int i = 0; i < 3; i++) {
+        const int s = i < nmat ? i : nmat - 1;
+        if (i < nmat) {
+            TI_REQUIRE(codes[i] && scales[i] && outs[i] && Ns[i] > 0, "ti_tern_gemv_multi_norm: matrix %d: null buffer or N <= 0", i);
+            TI_REQUIRE(al16(codes[i]), "ti_tern_gemv_multi_norm: codes[%d] must be 16-byte aligned", i);
+        }
+        m.codes[i] = reinterpret_cast<const uint4*>(codes[s]);
+        m.scales[i] = scales[s];
+        m.out[i] = outs[s];
+        m.N[i] = Ns[s];
+    }
+    m.nmat = nmat;
+    if (!rw_launch(c, m, K / 64, nullptr, nullptr, nq)) return ti_fail(TI_ERR_INVALID, "ti_tern_gemv_multi_norm: no kernel for K=%d", K);
+    TI_LAUNCHED("k_tern_gemv_rw (norm)");
+    return TI_OK;
+}
+
+// the down projection of the Bonsai decoder with the SwiGLU + quantizer of its input in
+// every workgroup's prologue (k_tern_gemv_rw with SWI): K = 2048, 4096 or 6144.
+bool ti_tern_swiglu_ok(int K) { return K == 2048 || K == 4096 || K == 6144; }
+
+int ti_tern_gemv_swiglu(ti_ctx* c, const ti_tern_swiglu* sw, float* out, const uint8_t* codes, const float* scales, int N,
+                        int K) {
+    TI_CHECK_CTX(c);
+    TI_REQUIRE(sw && sw->g && sw->u && sw->gu_scale && sw->swi_out && sw->act_out && sw->xsum_out && sw->scale_out,
+               "ti_tern_gemv_swiglu: null SwiGLU buffer");
+    TI_REQUIRE(ti_tern_swiglu_ok(K), "ti_tern_gemv_swiglu: K must be 2048, 4096 or 6144 (K=%d)", K);
+    TI_REQUIRE(out && codes && scales && N > 0, "ti_tern_gemv_swiglu: null matrix or N <= 0");
+    TI_REQUIRE(al16(codes) && al16(sw->g) && al16(sw->u) && al16(sw->swi_out) && al16(sw->act_out),
+               "ti_tern_gemv_swiglu: buffers must be 16-byte aligned");
+    TernMats m = {};
+    for (int i = 0; i < 3; i++) {
+        m.codes[i] = reinterpret_cast<const uint4*>(codes);
+        m.scales[i] = scales;
+        m.out[i] = out;
+        m.N[i] = N;
+    }
+    m.nmat = 1;
+    if (!rw_launch(c, m, K / 64, nullptr, nullptr, nullptr, sw)) return ti_fail(TI_ERR_INVALID, "ti_tern_gemv_swiglu: no kernel for K=%d", K);
+    TI_LAUNCHED("k_tern_gemv_rw (swiglu)");
     return TI_OK;
 }
 

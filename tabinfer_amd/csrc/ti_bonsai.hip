@@ -559,7 +559,7 @@ struct ti_bonsai {
     uint16_t* embed = nullptr;
     float* final_norm = nullptr;
     TLin lm;
-    float *x, *xn, *qraw, *kraw, *vraw, *attn, *oraw, *graw, *uraw, *swi, *draw, *lraw, *logits;
+    float *x, *x2, *xn, *qraw, *kraw, *vraw, *attn, *oraw, *graw, *uraw, *swi, *draw, *lraw, *logits;
     int8_t* act;
     int32_t* xsum;
     float* scales;        // [4]: a (input norm), b (attention), c (post norm), d (swi)
@@ -670,7 +670,7 @@ extern "C" int ti_bonsai_create(ti_ctx* c, const ti_bonsai_config* cfg, ti_bonsa
     if (!rc) rc = lin(m->lm, C.vocab, H);
     const int widest = I > H ? (I > nq ? I : nq) : (H > nq ? H : nq);
     const int nsplit = (C.max_ctx + bn_chunk(C.max_ctx) - 1) / bn_chunk(C.max_ctx);
-    struct { float** p; size_t n; } fb[] = {{&m->x, (size_t)H}, {&m->xn, (size_t)H}, {&m->qraw, (size_t)nq},
+    struct { float** p; size_t n; } fb[] = {{&m->x, (size_t)H}, {&m->x2, (size_t)H}, {&m->xn, (size_t)H}, {&m->qraw, (size_t)nq},
                                             {&m->kraw, (size_t)nkv}, {&m->vraw, (size_t)nkv},
                                             {&m->attn, (size_t)nq}, {&m->oraw, (size_t)H}, {&m->graw, (size_t)I},
                                             {&m->uraw, (size_t)I}, {&m->swi, (size_t)I}, {&m->draw, (size_t)H},
@@ -858,6 +858,9 @@ static int bonsai_step(ti_ctx* c, ti_bonsai* m, bool want_logits) {
     float* sb = m->scales + 1;
     float* scl = m->scales + 2;
     float* sd = m->scales + 3;
+    // the residual add + norm + quantizer before q/k/v and gate/up run in those projections'
+    // prologues (ti_tern_gemv_multi_norm) where the hidden width allows
+    const bool fuse = ti_tern_norm_ok(H);
     int rc;
 #define RC(x) do { rc = (x); if (rc) return rc; } while (0)
     k_bn_embed<<<1, 256, 0, c->stream>>>(m->hist, m->dpos, m->embed, m->x, H, C.vocab, C.max_ctx);
@@ -867,19 +870,28 @@ static int bonsai_step(ti_ctx* c, ti_bonsai* m, bool want_logits) {
         const bool first = l == 0;
         // the previous layer's down projection is added in this norm's prologue
         if (m->trace && !first) RC(bput(c, m, l - 1, B_D, m->draw));
-        RC(bn_norm_quant(c, m->x, first ? nullptr : m->draw, sd, y.in_norm, C.rms_eps, H, m->xn, m->act, m->xsum, sa));
-        if (m->trace) {
-            // x_in of this layer: x before the add is the previous x_out; trace the sum
-            RC(bput(c, m, l, B_X_IN, m->x));
-            RC(bput(c, m, l, B_XN, m->xn));
-            RC(bput(c, m, l, B_A_ACT, m->act));
-            RC(bput(c, m, l, B_A_SCALE, sa));
-        }
         const uint8_t* cq[3] = {y.q.codes, y.k.codes, y.v.codes};
         const float* sq[3] = {y.q.scales, y.k.scales, y.v.scales};
         float* oq[3] = {m->qraw, m->kraw, m->vraw};
         const int nqkv[3] = {nq, nkv, nkv};
-        RC(ti_tern_gemv_multi(c, m->act, m->xsum, H, 3, cq, sq, oq, nqkv));
+        // with the norm in the projections' prologue the residual moves x -> x2 here and
+        // back x2 -> x in the post-attention norm (a launch's workgroups still read its input)
+        float* xmid = fuse ? m->x2 : m->x;
+        if (fuse) {
+            const ti_tern_norm nin = {m->x, first ? nullptr : m->draw, sd, y.in_norm, C.rms_eps,
+                                      m->x2, m->xn, m->act, m->xsum, sa};
+            RC(ti_tern_gemv_multi_norm(c, &nin, H, 3, cq, sq, oq, nqkv));
+        } else {
+            RC(bn_norm_quant(c, m->x, first ? nullptr : m->draw, sd, y.in_norm, C.rms_eps, H, m->xn, m->act, m->xsum, sa));
+        }
+        if (m->trace) {
+            // x_in of this layer: x before the add is the previous x_out; trace the sum
+            RC(bput(c, m, l, B_X_IN, xmid));
+            RC(bput(c, m, l, B_XN, m->xn));
+            RC(bput(c, m, l, B_A_ACT, m->act));
+            RC(bput(c, m, l, B_A_SCALE, sa));
+        }
+        if (!fuse) RC(ti_tern_gemv_multi(c, m->act, m->xsum, H, 3, cq, sq, oq, nqkv));
         if (m->trace) {
             RC(bput(c, m, l, B_Q, m->qraw));
             RC(bput(c, m, l, B_K, m->kraw));
@@ -904,23 +916,35 @@ static int bonsai_step(ti_ctx* c, ti_bonsai* m, bool want_logits) {
             RC(bput(c, m, l, B_B_SCALE, sb));
         }
         RC(ti_tern_gemv(c, m->oraw, y.o.codes, y.o.scales, m->act, m->xsum, H, nq));
-        RC(bn_norm_quant(c, m->x, m->oraw, sb, y.post_norm, C.rms_eps, H, m->xn, m->act, m->xsum, scl));
+        const uint8_t* cg[2] = {y.gate.codes, y.up.codes};
+        const float* sg[2] = {y.gate.scales, y.up.scales};
+        float* og[2] = {m->graw, m->uraw};
+        const int ngu[2] = {I, I};
+        if (fuse) {
+            const ti_tern_norm npost = {xmid, m->oraw, sb, y.post_norm, C.rms_eps, m->x, m->xn, m->act, m->xsum, scl};
+            RC(ti_tern_gemv_multi_norm(c, &npost, H, 2, cg, sg, og, ngu));
+        } else {
+            RC(bn_norm_quant(c, m->x, m->oraw, sb, y.post_norm, C.rms_eps, H, m->xn, m->act, m->xsum, scl));
+        }
         if (m->trace) {
             RC(bput(c, m, l, B_X_MID, m->x));
             RC(bput(c, m, l, B_XN2, m->xn));
             RC(bput(c, m, l, B_C_ACT, m->act));
             RC(bput(c, m, l, B_C_SCALE, scl));
         }
-        const uint8_t* cg[2] = {y.gate.codes, y.up.codes};
-        const float* sg[2] = {y.gate.scales, y.up.scales};
-        float* og[2] = {m->graw, m->uraw};
-        const int ngu[2] = {I, I};
-        RC(ti_tern_gemv_multi(c, m->act, m->xsum, H, 2, cg, sg, og, ngu));
-        const int ei = (I + BN_THREADS - 1) / BN_THREADS;
+        if (!fuse) RC(ti_tern_gemv_multi(c, m->act, m->xsum, H, 2, cg, sg, og, ngu));
+        const bool fuse_swi = ti_tern_swiglu_ok(I);
+        if (fuse_swi) {
+            // the SwiGLU and its quantizer run in the down projection's prologue
+            const ti_tern_swiglu swd = {m->graw, m->uraw, scl, m->swi, m->act, m->xsum, sd};
+            RC(ti_tern_gemv_swiglu(c, &swd, m->draw, y.down.codes, y.down.scales, H, I));
+        } else {
+            const int ei = (I + BN_THREADS - 1) / BN_THREADS;
 #define SQ(E) if (ei <= E) { k_bn_swiglu_quant<E><<<1, BN_THREADS, 0, c->stream>>>(m->graw, m->uraw, scl, I, m->swi, m->act, m->xsum, sd); }
-        SQ(2) else SQ(4) else SQ(8) else return ti_fail(TI_ERR_INVALID, "bonsai: intermediate %d", I);
+            SQ(2) else SQ(4) else SQ(8) else return ti_fail(TI_ERR_INVALID, "bonsai: intermediate %d", I);
 #undef SQ
-        TI_LAUNCHED("k_bn_swiglu_quant");
+            TI_LAUNCHED("k_bn_swiglu_quant");
+        }
         if (m->trace) {
             RC(bput(c, m, l, B_G, m->graw));
             RC(bput(c, m, l, B_U, m->uraw));
@@ -928,7 +952,7 @@ static int bonsai_step(ti_ctx* c, ti_bonsai* m, bool want_logits) {
             RC(bput(c, m, l, B_D_ACT, m->act));
             RC(bput(c, m, l, B_D_SCALE, sd));
         }
-        RC(ti_tern_gemv(c, m->draw, y.down.codes, y.down.scales, m->act, m->xsum, H, I));
+        if (!fuse_swi) RC(ti_tern_gemv(c, m->draw, y.down.codes, y.down.scales, m->act, m->xsum, H, I));
     }
     if (m->trace) RC(bput(c, m, C.layers - 1, B_D, m->draw));
     if (!want_logits) {

@@ -78,6 +78,40 @@ struct TgIn {
     float eps;
     const float* pin;
 };
+// The residual add + RMSNorm + n2 quantizer run in the prologue of the ternary projections
+// that consume it (k_tern.hip): x_out = x + add * (1 / *add_scale) (x alone without add),
+// xn_out = x_out * (1 / sqrt(mean(x_out^2) + eps)) * w, codes act_out (127 / amax, rounded
+// half away from zero), 64-block sums xsum_out, the quantizer's 127 / amax in *scale_out.
+// x_out must not alias x: other workgroups of the launch still read x.
+struct ti_tern_norm {
+    const float* x;
+    const float* add;
+    const float* add_scale;
+    const float* w;
+    float eps;
+    float* x_out;
+    float* xn_out;
+    int8_t* act_out;
+    int32_t* xsum_out;
+    float* scale_out;
+};
+// The SwiGLU of the scaled gate/up and its n2 quantizer in the down projection's prologue:
+// swi = silu(g / *gu_scale) * (u / *gu_scale), codes, block sums, scale as above.
+struct ti_tern_swiglu {
+    const float* g;
+    const float* u;
+    const float* gu_scale;
+    float* swi_out;
+    int8_t* act_out;
+    int32_t* xsum_out;
+    float* scale_out;
+};
+bool ti_tern_swiglu_ok(int K);
+int ti_tern_gemv_swiglu(ti_ctx* c, const ti_tern_swiglu* sw, float* out, const uint8_t* codes, const float* scales, int N,
+                        int K);
+bool ti_tern_norm_ok(int K);
+int ti_tern_gemv_multi_norm(ti_ctx* c, const ti_tern_norm* nq, int K, int nmat, const uint8_t* const* codes,
+                            const float* const* scales, float* const* outs, const int* Ns);
 bool ti_tgemm_ok(int T, int K);
 bool ti_tgemm_norm_ok(int T, int K);
 bool ti_tnorm_ok(int K);
