@@ -175,7 +175,7 @@ __global__ __launch_bounds__(256) void k_tern_gemv_rw(TernMats m, const int8_t* 
 #pragma unroll
         for (int i = 0; i < NQE; i += 4) {
             const float4 x4 = *reinterpret_cast<const float4*>(nq.x + tid * NQE + i);
-            const float4 w4 = *reinterpret_cast<const float4*>(nq.w + tid * NQE + i);
+            const float4 w4 = nq.w ? *reinterpret_cast<const float4*>(nq.w + tid * NQE + i) : make_float4(1.f, 1.f, 1.f, 1.f);
             const float4 a4 = nq.add ? *reinterpret_cast<const float4*>(nq.add + tid * NQE + i) : make_float4(0.f, 0.f, 0.f, 0.f);
             nx[i] = x4.x; nx[i + 1] = x4.y; nx[i + 2] = x4.z; nx[i + 3] = x4.w;
             nw[i] = w4.x; nw[i + 1] = w4.y; nw[i + 2] = w4.z; nw[i + 3] = w4.w;
@@ -263,25 +263,33 @@ __global__ __launch_bounds__(256) void k_tern_gemv_rw(TernMats m, const int8_t* 
         TI_ISSUE_FENCE();
         constexpr int TPB = 64 / NQE;                    // threads per 64-code block
         const float inv_add = nq.add ? 1.0f / *nq.add_scale : 0.0f;
-        float ss = 0.0f;
-#pragma unroll
-        for (int i = 0; i < NQE; i++) {
-            if (nq.add) {
-                const float d = na[i] * inv_add;
-                nx[i] = nx[i] + d;
-            }
-            ss = ss + nx[i] * nx[i];
-        }
-        ss = ti_wave_sum(ss);
-        if (lane == 0) s_red[wave] = ss;
-        __syncthreads();
-        const float mean = (s_red[0] + s_red[1] + s_red[2] + s_red[3]) / (float)(256 * NQE);
-        const float inv = 1.0f / sqrtf(mean + nq.eps);
         float mx = 0.0f;
+        if (nq.w) {                                      // uniform: residual add + RMSNorm
+            float ss = 0.0f;
 #pragma unroll
-        for (int i = 0; i < NQE; i++) {
-            na[i] = nx[i] * inv * nw[i];                  // xn
-            mx = fmaxf(mx, fabsf(na[i]));
+            for (int i = 0; i < NQE; i++) {
+                if (nq.add) {
+                    const float d = na[i] * inv_add;
+                    nx[i] = nx[i] + d;
+                }
+                ss = ss + nx[i] * nx[i];
+            }
+            ss = ti_wave_sum(ss);
+            if (lane == 0) s_red[wave] = ss;
+            __syncthreads();
+            const float mean = (s_red[0] + s_red[1] + s_red[2] + s_red[3]) / (float)(256 * NQE);
+            const float inv = 1.0f / sqrtf(mean + nq.eps);
+#pragma unroll
+            for (int i = 0; i < NQE; i++) {
+                na[i] = nx[i] * inv * nw[i];              // xn
+                mx = fmaxf(mx, fabsf(na[i]));
+            }
+        } else {                                         // the quantizer alone (x as is)
+#pragma unroll
+            for (int i = 0; i < NQE; i++) {
+                na[i] = nx[i];
+                mx = fmaxf(mx, fabsf(na[i]));
+            }
         }
         mx = ti_wave_max(mx);
         if (lane == 0) s_red[4 + wave] = mx;
@@ -310,8 +318,10 @@ __global__ __launch_bounds__(256) void k_tern_gemv_rw(TernMats m, const int8_t* 
         if (blockIdx.x == 0) {
 #pragma unroll
             for (int i = 0; i < NQE; i += 4) {
-                *reinterpret_cast<float4*>(nq.x_out + tid * NQE + i) = make_float4(nx[i], nx[i + 1], nx[i + 2], nx[i + 3]);
-                *reinterpret_cast<float4*>(nq.xn_out + tid * NQE + i) = make_float4(na[i], na[i + 1], na[i + 2], na[i + 3]);
+                if (nq.x_out)
+                    *reinterpret_cast<float4*>(nq.x_out + tid * NQE + i) = make_float4(nx[i], nx[i + 1], nx[i + 2], nx[i + 3]);
+                if (nq.xn_out)
+                    *reinterpret_cast<float4*>(nq.xn_out + tid * NQE + i) = make_float4(na[i], na[i + 1], na[i + 2], na[i + 3]);
             }
 #pragma unroll
             for (int k = 0; k < NQE / 4; k++) reinterpret_cast<uint32_t*>(nq.act_out)[tid * (NQE / 4) + k] = wd[k];
@@ -581,8 +591,9 @@ bool ti_tern_norm_ok(int K) { return K == 1024 || K == 2048; }
 int ti_tern_gemv_multi_norm(ti_ctx* c, const ti_tern_norm* nq, int K, int nmat, const uint8_t* const* codes,
                             const float* const* scales, float* const* outs, const int* Ns) {
     TI_CHECK_CTX(c);
-    TI_REQUIRE(nq && nq->x && nq->w && nq->add_scale && nq->x_out && nq->xn_out && nq->act_out && nq->xsum_out &&
-                   nq->scale_out, "ti_tern_gemv_multi_norm: null norm buffer");
+    TI_REQUIRE(nq && nq->x && nq->act_out && nq->xsum_out && nq->scale_out && (!nq->add || nq->add_scale),
+               "ti_tern_gemv_multi_norm: null norm buffer");
+    TI_REQUIRE(nq->w || !nq->add, "ti_tern_gemv_multi_norm: a residual add needs the norm");
     TI_REQUIRE(ti_tern_norm_ok(K), "ti_tern_gemv_multi_norm: K must be 1024 or 2048 (K=%d)", K);
     TI_REQUIRE(nq->x_out != nq->x, "ti_tern_gemv_multi_norm: x_out must not alias x");
     TI_REQUIRE(al16(nq->x) && al16(nq->w) && al16(nq->x_out) && al16(nq->xn_out) && al16(nq->act_out) &&

@@ -452,6 +452,7 @@ __global__ __launch_bounds__(BN_THREADS) void k_bn_merge_quant(const float* __re
         const float v = ((s_part[0][g][d] + s_part[1][g][d]) + (s_part[2][g][d] + s_part[3][g][d])) / s_l[g];
         ti_pub_store(out + (size_t)(hk * G + g) * HD + d, v);
     }
+    if (!act) return;                                  // the next launch quantizes out
     ti_stores_done();
     __syncthreads();
     if (t == 0) s_last = ti_arrive(counter) == gridDim.x - 1;
@@ -906,16 +907,27 @@ static int bonsai_step(ti_ctx* c, ti_bonsai* m, bool want_logits) {
 #undef BA
         TI_LAUNCHED("k_bn_attn");
         const int eq = (nq + BN_THREADS - 1) / BN_THREADS;
-#define MQ(E) if (eq <= E) { k_bn_merge_quant<E><<<nKv, BN_THREADS, 0, c->stream>>>(m->po, m->pml, m->dpos, nsplit, nq, chunk, m->attn, m->act, m->xsum, sb, c->sync + TI_SYNC_BONSAI, C.max_ctx); }
+        // with the quantizer in the o projection's prologue the merge only merges
+        const bool fuse_o = ti_tern_norm_ok(nq);
+        int8_t* mact = fuse_o ? nullptr : m->act;
+#define MQ(E) if (eq <= E) { k_bn_merge_quant<E><<<nKv, BN_THREADS, 0, c->stream>>>(m->po, m->pml, m->dpos, nsplit, nq, chunk, m->attn, mact, m->xsum, sb, c->sync + TI_SYNC_BONSAI, C.max_ctx); }
         MQ(2) else MQ(4) else MQ(8) else return ti_fail(TI_ERR_INVALID, "bonsai: q width %d", nq);
 #undef MQ
         TI_LAUNCHED("k_bn_merge_quant");
+        if (fuse_o) {
+            const ti_tern_norm nqo = {m->attn, nullptr, nullptr, nullptr, 0.0f, nullptr, nullptr, m->act, m->xsum, sb};
+            float* oo[1] = {m->oraw};
+            const uint8_t* co[1] = {y.o.codes};
+            const float* so[1] = {y.o.scales};
+            const int no[1] = {H};
+            RC(ti_tern_gemv_multi_norm(c, &nqo, nq, 1, co, so, oo, no));
+        }
         if (m->trace) {
             RC(bput(c, m, l, B_ATTN, m->attn));
             RC(bput(c, m, l, B_B_ACT, m->act));
             RC(bput(c, m, l, B_B_SCALE, sb));
         }
-        RC(ti_tern_gemv(c, m->oraw, y.o.codes, y.o.scales, m->act, m->xsum, H, nq));
+        if (!fuse_o) RC(ti_tern_gemv(c, m->oraw, y.o.codes, y.o.scales, m->act, m->xsum, H, nq));
         const uint8_t* cg[2] = {y.gate.codes, y.up.codes};
         const float* sg[2] = {y.gate.scales, y.up.scales};
         float* og[2] = {m->graw, m->uraw};

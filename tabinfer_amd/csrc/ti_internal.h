@@ -82,7 +82,8 @@ struct TgIn {
 // that consume it (k_tern.hip): x_out = x + add * (1 / *add_scale) (x alone without add),
 // xn_out = x_out * (1 / sqrt(mean(x_out^2) + eps)) * w, codes act_out (127 / amax, rounded
 // half away from zero), 64-block sums xsum_out, the quantizer's 127 / amax in *scale_out.
-// x_out must not alias x: other workgroups of the launch still read x.
+// x_out must not alias x: other workgroups of the launch still read x. Without w the
+// prologue is the quantizer of x alone (no add; x_out, xn_out may be null).
 struct ti_tern_norm {
     const float* x;
     const float* add;
