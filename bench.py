@@ -515,7 +515,7 @@ def int3_bytes(N, K):
 
 def moe(ctx, flush, reps=4, layers=16):
     """One MoE block (router -> w1/w3 -> swiglu -> w2 -> combine, models/lfm25.js:2145-2166)
-    at batch 1 (the fused decode launches) and batch 16 (expert-grouped GEMMs), over
+    at batch 1 (the fused decode launches) and batch 16 (ti_moe_prefill_q3: expert-grouped GEMMs, 6 launches), over
     `layers` independent expert sets (copies of one seeded set at distinct addresses) in
     one graph, so the weights stream from HBM (16 x 19 MB at batch 1, past the 256 MB
     Infinity Cache) the way consecutive decode layers do; us per block = graph time / layers."""
@@ -557,12 +557,9 @@ def moe(ctx, flush, reps=4, layers=16):
                     ctx.call("ti_moe_decode_q3", b["x"], b["normed"], b["logits"], b["bias"], p1, s1, p3_, s3_, p2, s2,
                              b["idx"], b["wt"], b["act"], H, I, nE, K)
                     continue
-                ctx.call("ti_router", b["logits"], b["bias"], T, nE, K, b["idx"], b["wt"])
-                ctx.call("ti_moe_gemm_q3", b["normed"], T, p1, s1, b["idx"], b["gate"], P, I, H, K, nE)
-                ctx.call("ti_moe_gemm_q3", b["normed"], T, p3_, s3_, b["idx"], b["up"], P, I, H, K, nE)
-                ctx.call("ti_swiglu", b["gate"], b["up"], b["act"], P * I)
-                ctx.call("ti_moe_gemm_q3", b["act"], P, p2, s2, b["idx"], b["out"], P, H, I, 1, nE)
-                ctx.call("ti_moe_combine", b["x"], b["out"], b["wt"], H, K, T)
+                # the prefill block: router, [w1 + w3], [swiglu + quant], w2, combine
+                ctx.call("ti_moe_prefill_q3", b["x"], b["normed"], b["logits"], b["bias"], p1, s1, p3_, s3_, p2, s2,
+                         b["idx"], b["wt"], b["gate"], b["up"], b["act"], b["out"], T, H, I, nE, K)
 
         g = graph_of(ctx, issue)
         time_graphs(ctx, [g], 1)
@@ -572,7 +569,7 @@ def moe(ctx, flush, reps=4, layers=16):
         out["batch%d" % T] = {"block_us": round(us, 2), "distinct_experts": ne, "weight_bytes": wbytes,
                               "GB_s": round(wbytes / (us * 1e-6) / 1e9, 1),
                               "pct_of_hbm_peak": round(100 * wbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 2),
-                              "launches": 2 if T == 1 else 9}
+                              "launches": 2 if T == 1 else 6}
         for v in b.values():
             v.free()
     for lw in wsets:

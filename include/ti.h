@@ -369,6 +369,17 @@ int ti_moe_decode_q3(ti_ctx* ctx, float* x, const float* normed, const float* lo
                      const uint32_t* w1p, const uint16_t* w1s, const uint32_t* w3p, const uint16_t* w3s,
                      const uint32_t* w2p, const uint16_t* w2s, int32_t* idx, float* wt, float* act,
                      int H, int I, int nE, int topk);
+/* The MoE block of T > 1 tokens (models/lfm25.js:2145-2158, the prefill branch after the
+ * router logits: router, moeGemm3 w1 and w3, swiglu, moeGemm3 w2, moeCombine) in six
+ * launches instead of nine: normed is quantized once for w1 and w3, both run in one launch,
+ * and the SwiGLU is formed inside the quantizer of w2's input. The same arithmetic as that
+ * chain of ti_router, ti_moe_gemm_q3, ti_swiglu, ti_moe_gemm_q3, ti_moe_combine: idx/wt[T*topk]
+ * the routing, gate/up/act[T*topk*I] and out[T*topk*H] its intermediates, x[T*H] += the
+ * combined experts. nE <= 256, H and I multiples of 32 <= 4096, T*H and T*topk*I <= 2^24. */
+int ti_moe_prefill_q3(ti_ctx* ctx, float* x, const float* normed, const float* logits, const float* bias,
+                      const uint32_t* w1p, const uint16_t* w1s, const uint32_t* w3p, const uint16_t* w3s,
+                      const uint32_t* w2p, const uint16_t* w2s, int32_t* idx, float* wt, float* gate, float* up,
+                      float* act, float* out, int T, int H, int I, int nE, int topk);
 /* swiglu (models/lfm25.js:1831-1847): y[i] = g[i] / (1 + e^-g[i]) * u[i]. */
 int ti_swiglu(ti_ctx* ctx, const float* g, const float* u, float* y, long n);
 /* moeCombine / MOECOMBINE_WGSL (models/lfm25.js:1982-2000): x[t*H+h] += sum_k

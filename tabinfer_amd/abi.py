@@ -86,6 +86,7 @@ SIGS = {
     "ti_swiglu": [_p, _p, _p, _p, C.c_long],
     "ti_moe_decode_q3": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i],
     "ti_moe_combine": [_p, _p, _p, _p, _i, _i, _i],
+    "ti_moe_prefill_q3": [_p] * 17 + [_i] * 5,
     "ti_qwen3_create": [_p, _p, C.POINTER(_p)],
     "ti_qwen3_destroy": [_p, _p],
     "ti_qwen3_tensor": [_p, C.c_char_p, C.POINTER(_p), C.POINTER(_sz), C.POINTER(_p), C.POINTER(_sz)],

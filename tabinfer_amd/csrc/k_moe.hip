@@ -255,10 +255,15 @@ __global__ __launch_bounds__(256) void k_moe_gemv_q3(const float* __restrict__ x
 // for the first hit and the workgroups of experts nobody chose read only the ids.
 constexpr int MOE_PB = 4;          // pairs whose activation loads are in flight together
 template <int GL>
+// grid.z = 2 runs a second matrix (p3b, s3b -> yb) of the same shape on the same activation.
 __global__ __launch_bounds__(256) void k_moe_gemm_q3(const uint32_t* __restrict__ xq, const float* __restrict__ xs,
-                                                     const uint32_t* __restrict__ p3, const uint16_t* __restrict__ s3,
-                                                     const int32_t* __restrict__ ridx, float* __restrict__ y, int P, int N,
-                                                     int K, int src_div, int spec) {
+                                                     const uint32_t* __restrict__ p3a, const uint16_t* __restrict__ s3a,
+                                                     const int32_t* __restrict__ ridx, float* __restrict__ ya, int P, int N,
+                                                     int K, int src_div, int spec, const uint32_t* __restrict__ p3b,
+                                                     const uint16_t* __restrict__ s3b, float* __restrict__ yb) {
+    const uint32_t* __restrict__ p3 = blockIdx.z ? p3b : p3a;
+    const uint16_t* __restrict__ s3 = blockIdx.z ? s3b : s3a;
+    float* __restrict__ y = blockIdx.z ? yb : ya;
     __shared__ int s_list[256];
     __shared__ int s_wcnt[4];
     const int e = blockIdx.y;
@@ -743,9 +748,68 @@ extern "C" int ti_moe_gemm_q3(ti_ctx* c, const float* src, int src_rows, const u
     if (rc) return rc;
     dim3 grid((unsigned)((N + 15) / 16), (unsigned)nE);
     const int spec = 2 * P >= nE;   // most experts are routed to: weights loaded before the scan
-    if (K <= 2048) k_moe_gemm_q3<1><<<grid, 256, 0, c->stream>>>(c->act_q, c->act_s, p3, s3, ridx, y, P, N, K, src_div, spec);
-    else k_moe_gemm_q3<2><<<grid, 256, 0, c->stream>>>(c->act_q, c->act_s, p3, s3, ridx, y, P, N, K, src_div, spec);
+    if (K <= 2048) k_moe_gemm_q3<1><<<grid, 256, 0, c->stream>>>(c->act_q, c->act_s, p3, s3, ridx, y, P, N, K, src_div, spec, p3, s3, y);
+    else k_moe_gemm_q3<2><<<grid, 256, 0, c->stream>>>(c->act_q, c->act_s, p3, s3, ridx, y, P, N, K, src_div, spec, p3, s3, y);
     TI_LAUNCHED("k_moe_gemm_q3");
+    return TI_OK;
+}
+
+// quantAct8 of swiglu(g, u) (lfm25.js:1831-1847 then :1487-1494): group gi's 32 values
+// a / (1 + e^-a) * u with k_swiglu_f32's operations, written to act as well, then q8_group.
+__global__ __launch_bounds__(64) void k_quant_swiglu_q8(const float* __restrict__ g, const float* __restrict__ u,
+                                                        float* __restrict__ act, uint32_t* __restrict__ xq,
+                                                        float* __restrict__ xs, int ng) {
+    const int gi = blockIdx.x * blockDim.x + threadIdx.x;
+    if (gi >= ng) return;
+    float v[32], w[32];
+    load32(g + (size_t)gi * 32, v);
+    load32(u + (size_t)gi * 32, w);
+#pragma unroll
+    for (int j = 0; j < 32; j++) {
+        const float a = v[j];
+        v[j] = a / (1.0f + expf(-a)) * w[j];
+    }
+    float4* ao = reinterpret_cast<float4*>(act + (size_t)gi * 32);
+#pragma unroll
+    for (int j = 0; j < 8; j++) ao[j] = make_float4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
+    q8_group(v, xq + (size_t)gi * 8, xs + gi, nullptr);
+}
+
+extern "C" int ti_moe_prefill_q3(ti_ctx* c, float* x, const float* normed, const float* logits, const float* bias,
+                                 const uint32_t* w1p, const uint16_t* w1s, const uint32_t* w3p, const uint16_t* w3s,
+                                 const uint32_t* w2p, const uint16_t* w2s, int32_t* idx, float* wt, float* gate,
+                                 float* up, float* act, float* out, int T, int H, int I, int nE, int topk) {
+    TI_CHECK_CTX(c);
+    TI_REQUIRE(x && normed && logits && w1p && w1s && w3p && w3s && w2p && w2s && idx && wt && gate && up && act && out,
+               "ti_moe_prefill_q3: null buffer");
+    TI_REQUIRE(T > 0 && nE > 0 && nE <= ROUTER_EMAX && nE < 65536 && topk > 0 && topk <= nE && topk <= 64,
+               "ti_moe_prefill_q3: need T > 0, 0 < topk <= nE <= %d (T=%d nE=%d topk=%d)", ROUTER_EMAX, T, nE, topk);
+    TI_REQUIRE(H > 0 && I > 0 && H % 32 == 0 && I % 32 == 0 && H <= 4096 && I <= 4096,
+               "ti_moe_prefill_q3: H, I multiples of 32, <= 4096 (H=%d I=%d)", H, I);
+    const long P = (long)T * topk;
+    const long cap = (long)TI_ACT_CAP * TI_ACT_TMAX;
+    TI_REQUIRE((long)T * H <= cap && P * I <= cap, "ti_moe_prefill_q3: T*H=%ld or P*I=%ld exceeds %ld", (long)T * H,
+               P * I, cap);
+    TI_REQUIRE(al16(gate) && al16(up) && al16(act), "ti_moe_prefill_q3: gate, up and act must be 16-byte aligned");
+    k_router<<<T, 64, 0, c->stream>>>(logits, bias, nE, topk, idx, wt);
+    TI_LAUNCHED("k_router");
+    int rc = ti_quant_act_q8_async(c, normed, c->act_q, c->act_s, nullptr, T * (H / 32));
+    if (rc) return rc;
+    const int spec = 2 * P >= nE;
+    dim3 g13((unsigned)((I + 15) / 16), (unsigned)nE, 2);
+    if (H <= 2048) k_moe_gemm_q3<1><<<g13, 256, 0, c->stream>>>(c->act_q, c->act_s, w1p, w1s, idx, gate, (int)P, I, H, topk, spec, w3p, w3s, up);
+    else k_moe_gemm_q3<2><<<g13, 256, 0, c->stream>>>(c->act_q, c->act_s, w1p, w1s, idx, gate, (int)P, I, H, topk, spec, w3p, w3s, up);
+    TI_LAUNCHED("k_moe_gemm_q3 (w1, w3)");
+    const long ng = P * (I / 32);
+    k_quant_swiglu_q8<<<(unsigned)((ng + 63) / 64), 64, 0, c->stream>>>(gate, up, act, c->act_q, c->act_s, (int)ng);
+    TI_LAUNCHED("k_quant_swiglu_q8");
+    dim3 g2((unsigned)((H + 15) / 16), (unsigned)nE, 1);
+    if (I <= 2048) k_moe_gemm_q3<1><<<g2, 256, 0, c->stream>>>(c->act_q, c->act_s, w2p, w2s, idx, out, (int)P, H, I, 1, spec, w2p, w2s, out);
+    else k_moe_gemm_q3<2><<<g2, 256, 0, c->stream>>>(c->act_q, c->act_s, w2p, w2s, idx, out, (int)P, H, I, 1, spec, w2p, w2s, out);
+    TI_LAUNCHED("k_moe_gemm_q3 (w2)");
+    const long th = (long)T * H;
+    k_moe_combine<<<(unsigned)((th + 255) / 256), 256, 0, c->stream>>>(x, out, wt, H, topk, th);
+    TI_LAUNCHED("k_moe_combine");
     return TI_OK;
 }
 

@@ -1525,6 +1525,7 @@ napi_value module_init(napi_env env, napi_value exports) {
         ENTRY("moe_gemm_q3", ti_moe_gemm_q3),
         ENTRY("swiglu", ti_swiglu),
         ENTRY("moe_decode_q3", ti_moe_decode_q3),
+        ENTRY("moe_prefill_q3", ti_moe_prefill_q3),
         ENTRY("moe_combine", ti_moe_combine),
         // Qwen3 decoder
         FN("qwen3_create", js_qwen3_create),

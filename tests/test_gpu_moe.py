@@ -379,3 +379,64 @@ def test_moe_decode_rejects_bad_shapes(ctx):
     with pytest.raises(abi.TIError):
         ctx.call("ti_moe_decode_q3", *args, 8192, 1792, 32, 4)      # H > 4096
     dd.free()
+
+
+# ---- the fused T > 1 block ------------------------------------------------------------------
+@pytest.mark.parametrize("T,H,I,nE,topk", [(16, H, I, NE, TOPK), (3, H, I, NE, TOPK), (8, 4096, 1024, 8, 2),
+                                           (5, 1024, 4096, 100, 8)])
+def test_moe_prefill_fused_matches_chain(ctx, orc, T, H, I, nE, topk):
+    """ti_moe_prefill_q3 (6 launches) against the chain of separate calls it replaces
+    (ti_router, ti_moe_gemm_q3 x 2, ti_swiglu, ti_moe_gemm_q3, ti_moe_combine): routing,
+    gate/up, activations, expert outputs and the residual bit for bit; and the routing
+    against the oracle's."""
+    rng = np.random.default_rng(7 * T + H + I + nE + topk)
+    P = T * topk
+    w1, w3 = rand_planes(rng, nE * I, H), rand_planes(rng, nE * I, H)
+    w2 = rand_planes(rng, nE * H, I)
+    normed = rng.standard_normal(T * H).astype(np.float32)
+    logits = rng.standard_normal(T * nE).astype(np.float32)
+    bias = (rng.standard_normal(nE) * 0.05).astype(np.float32)
+    x = rng.standard_normal(T * H).astype(np.float32)
+    d = {k: ctx.upload(v) for k, v in dict(normed=normed, logits=logits, bias=bias, p1=w1[0], s1=w1[1], p3=w3[0],
+                                             s3=w3[1], p2=w2[0], s2=w2[1]).items()}
+    runs = []
+    for fused in (True, False):
+        b = dict(x=ctx.upload(x))
+        for k, n in dict(idx=P, wt=P, gate=P * I, up=P * I, act=P * I, out=P * H).items():
+            b[k] = ctx.zeros(n * 4)
+        if fused:
+            ctx.call("ti_moe_prefill_q3", b["x"], d["normed"], d["logits"], d["bias"], d["p1"], d["s1"], d["p3"],
+                     d["s3"], d["p2"], d["s2"], b["idx"], b["wt"], b["gate"], b["up"], b["act"], b["out"],
+                     T, H, I, nE, topk)
+        else:
+            ctx.call("ti_router", d["logits"], d["bias"], T, nE, topk, b["idx"], b["wt"])
+            ctx.call("ti_moe_gemm_q3", d["normed"], T, d["p1"], d["s1"], b["idx"], b["gate"], P, I, H, topk, nE)
+            ctx.call("ti_moe_gemm_q3", d["normed"], T, d["p3"], d["s3"], b["idx"], b["up"], P, I, H, topk, nE)
+            ctx.call("ti_swiglu", b["gate"], b["up"], b["act"], P * I)
+            ctx.call("ti_moe_gemm_q3", b["act"], P, d["p2"], d["s2"], b["idx"], b["out"], P, H, I, 1, nE)
+            ctx.call("ti_moe_combine", b["x"], b["out"], b["wt"], H, topk, T)
+        runs.append({k: ctx.download(v, np.int32 if k == "idx" else np.float32,
+                                     {"x": T * H, "idx": P, "wt": P, "out": P * H}.get(k, P * I))
+                     for k, v in b.items()})
+        for v in b.values():
+            v.free()
+    for k in runs[0]:
+        assert np.array_equal(runs[0][k].view(np.uint32), runs[1][k].view(np.uint32)), k
+    oi, _ = orc.router(logits, bias, T, nE, topk)
+    assert np.array_equal(runs[0]["idx"], oi)
+    for v in d.values():
+        v.free()
+
+
+def test_moe_prefill_rejects_bad_shapes(ctx):
+    d = ctx.zeros(4096)
+    args = [d] * 16
+    with pytest.raises(abi.TIError):
+        ctx.call("ti_moe_prefill_q3", *args, 2, 48, 64, 8, 2)          # H % 32
+    with pytest.raises(abi.TIError):
+        ctx.call("ti_moe_prefill_q3", *args, 2, 64, 8192, 8, 2)        # I > 4096
+    with pytest.raises(abi.TIError):
+        ctx.call("ti_moe_prefill_q3", *args, 2, 64, 64, 300, 2)        # nE > 256
+    with pytest.raises(abi.TIError):
+        ctx.call("ti_moe_prefill_q3", *args, 0, 64, 64, 8, 2)          # T = 0
+    d.free()
