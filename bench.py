@@ -515,7 +515,7 @@ def int3_bytes(N, K):
 
 def moe(ctx, flush, reps=4, layers=16):
     """One MoE block (router -> w1/w3 -> swiglu -> w2 -> combine, models/lfm25.js:2145-2166)
-    at batch 1 (the fused decode launches) and batch 16 (ti_moe_prefill_q3: expert-grouped GEMMs, 6 launches), over
+    at batch 1 (the fused decode launches) and batch 16 (ti_moe_prefill_q3: expert-grouped GEMMs, 5 launches), over
     `layers` independent expert sets (copies of one seeded set at distinct addresses) in
     one graph, so the weights stream from HBM (16 x 19 MB at batch 1, past the 256 MB
     Infinity Cache) the way consecutive decode layers do; us per block = graph time / layers."""
@@ -557,7 +557,7 @@ def moe(ctx, flush, reps=4, layers=16):
                     ctx.call("ti_moe_decode_q3", b["x"], b["normed"], b["logits"], b["bias"], p1, s1, p3_, s3_, p2, s2,
                              b["idx"], b["wt"], b["act"], H, I, nE, K)
                     continue
-                # the prefill block: router, [w1 + w3], [swiglu + quant], w2, combine
+                # the prefill block: [router + quant], [w1 + w3], [swiglu + quant], w2, combine
                 ctx.call("ti_moe_prefill_q3", b["x"], b["normed"], b["logits"], b["bias"], p1, s1, p3_, s3_, p2, s2,
                          b["idx"], b["wt"], b["gate"], b["up"], b["act"], b["out"], T, H, I, nE, K)
 
@@ -569,7 +569,7 @@ def moe(ctx, flush, reps=4, layers=16):
         out["batch%d" % T] = {"block_us": round(us, 2), "distinct_experts": ne, "weight_bytes": wbytes,
                               "GB_s": round(wbytes / (us * 1e-6) / 1e9, 1),
                               "pct_of_hbm_peak": round(100 * wbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 2),
-                              "launches": 2 if T == 1 else 6}
+                              "launches": 2 if T == 1 else 5}
         for v in b.values():
             v.free()
     for lw in wsets:

@@ -370,8 +370,9 @@ int ti_moe_decode_q3(ti_ctx* ctx, float* x, const float* normed, const float* lo
                      const uint32_t* w2p, const uint16_t* w2s, int32_t* idx, float* wt, float* act,
                      int H, int I, int nE, int topk);
 /* The MoE block of T > 1 tokens (models/lfm25.js:2145-2158, the prefill branch after the
- * router logits: router, moeGemm3 w1 and w3, swiglu, moeGemm3 w2, moeCombine) in six
- * launches instead of nine: normed is quantized once for w1 and w3, both run in one launch,
+ * router logits: router, moeGemm3 w1 and w3, swiglu, moeGemm3 w2, moeCombine) in five
+ * launches instead of nine: the router shares a launch with normed's quantizer, normed is
+ * quantized once for w1 and w3, both run in one launch,
  * and the SwiGLU is formed inside the quantizer of w2's input. The same arithmetic as that
  * chain of ti_router, ti_moe_gemm_q3, ti_swiglu, ti_moe_gemm_q3, ti_moe_combine: idx/wt[T*topk]
  * the routing, gate/up/act[T*topk*I] and out[T*topk*H] its intermediates, x[T*H] += the

@@ -86,11 +86,11 @@ __global__ __launch_bounds__(256) void k_requant43(const uint32_t* __restrict__ 
 // one wave per token: s = sigmoid(logit) in f32, top-k of s + bias by strict '>' (the
 // lowest index wins a tie), weights s / (sum + 1e-6)
 constexpr int ROUTER_EMAX = 256;
-__global__ __launch_bounds__(64) void k_router(const float* __restrict__ logits, const float* __restrict__ bias, int nE,
-                                               int topk, int32_t* __restrict__ idx, float* __restrict__ wt) {
+__device__ __forceinline__ void router_token(int t, const float* __restrict__ logits, const float* __restrict__ bias,
+                                             int nE, int topk, int32_t* __restrict__ idx, float* __restrict__ wt) {
     __shared__ float sc[ROUTER_EMAX], sel[ROUTER_EMAX];
     __shared__ int chosen[ROUTER_EMAX];
-    const int t = blockIdx.x, lane = threadIdx.x;
+    const int lane = threadIdx.x;
     for (int e = lane; e < nE; e += 64) {
         const float l = logits[(size_t)t * nE + e];
         const float s = 1.0f / (1.0f + expf(-l));
@@ -126,6 +126,29 @@ __global__ __launch_bounds__(64) void k_router(const float* __restrict__ logits,
         idx[(size_t)t * topk + lane] = b;
         wt[(size_t)t * topk + lane] = sc[b] / (sum + 1e-6f);
     }
+}
+
+__global__ __launch_bounds__(64) void k_router(const float* __restrict__ logits, const float* __restrict__ bias, int nE,
+                                               int topk, int32_t* __restrict__ idx, float* __restrict__ wt) {
+    router_token(blockIdx.x, logits, bias, nE, topk, idx, wt);
+}
+
+// the router (workgroups 0 .. T-1, one per token) and, in the same launch, quantAct8 of
+// the normed rows (the remaining workgroups, a 32-group per thread): the two do not depend
+// on each other
+__global__ __launch_bounds__(64) void k_router_quant(const float* __restrict__ logits, const float* __restrict__ bias,
+                                                     int nE, int topk, int32_t* __restrict__ idx, float* __restrict__ wt,
+                                                     int T, const float* __restrict__ x, uint32_t* __restrict__ xq,
+                                                     float* __restrict__ xs, int ng) {
+    if ((int)blockIdx.x < T) {
+        router_token(blockIdx.x, logits, bias, nE, topk, idx, wt);
+        return;
+    }
+    const int gi = ((int)blockIdx.x - T) * 64 + threadIdx.x;
+    if (gi >= ng) return;
+    float v[32];
+    load32(x + (size_t)gi * 32, v);
+    q8_group(v, xq + (size_t)gi * 8, xs + gi, nullptr);
 }
 
 // ---- decode: pair-indexed GEMV with the f32 activation ----------------------------
@@ -791,10 +814,10 @@ extern "C" int ti_moe_prefill_q3(ti_ctx* c, float* x, const float* normed, const
     TI_REQUIRE((long)T * H <= cap && P * I <= cap, "ti_moe_prefill_q3: T*H=%ld or P*I=%ld exceeds %ld", (long)T * H,
                P * I, cap);
     TI_REQUIRE(al16(gate) && al16(up) && al16(act), "ti_moe_prefill_q3: gate, up and act must be 16-byte aligned");
-    k_router<<<T, 64, 0, c->stream>>>(logits, bias, nE, topk, idx, wt);
-    TI_LAUNCHED("k_router");
-    int rc = ti_quant_act_q8_async(c, normed, c->act_q, c->act_s, nullptr, T * (H / 32));
-    if (rc) return rc;
+    const int nq = T * (H / 32);
+    k_router_quant<<<(unsigned)(T + (nq + 63) / 64), 64, 0, c->stream>>>(logits, bias, nE, topk, idx, wt, T, normed,
+                                                                          c->act_q, c->act_s, nq);
+    TI_LAUNCHED("k_router_quant");
     const int spec = 2 * P >= nE;
     dim3 g13((unsigned)((I + 15) / 16), (unsigned)nE, 2);
     if (H <= 2048) k_moe_gemm_q3<1><<<g13, 256, 0, c->stream>>>(c->act_q, c->act_s, w1p, w1s, idx, gate, (int)P, I, H, topk, spec, w3p, w3s, up);

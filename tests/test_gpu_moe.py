@@ -385,7 +385,7 @@ def test_moe_decode_rejects_bad_shapes(ctx):
 @pytest.mark.parametrize("T,H,I,nE,topk", [(16, H, I, NE, TOPK), (3, H, I, NE, TOPK), (8, 4096, 1024, 8, 2),
                                            (5, 1024, 4096, 100, 8)])
 def test_moe_prefill_fused_matches_chain(ctx, orc, T, H, I, nE, topk):
-    """ti_moe_prefill_q3 (6 launches) against the chain of separate calls it replaces
+    """ti_moe_prefill_q3 (5 launches) against the chain of separate calls it replaces
     (ti_router, ti_moe_gemm_q3 x 2, ti_swiglu, ti_moe_gemm_q3, ti_moe_combine): routing,
     gate/up, activations, expert outputs and the residual bit for bit; and the routing
     against the oracle's."""
