@@ -376,7 +376,8 @@ int ti_moe_decode_q3(ti_ctx* ctx, float* x, const float* normed, const float* lo
  * and the SwiGLU is formed inside the quantizer of w2's input. The same arithmetic as that
  * chain of ti_router, ti_moe_gemm_q3, ti_swiglu, ti_moe_gemm_q3, ti_moe_combine: idx/wt[T*topk]
  * the routing, gate/up/act[T*topk*I] and out[T*topk*H] its intermediates, x[T*H] += the
- * combined experts. nE <= 256, H and I multiples of 32 <= 4096, T*H and T*topk*I <= 2^24. */
+ * combined experts. nE <= 256, H and I multiples of 32 <= 4096, T*H and T*topk*I <= 2^24;
+ * normed, gate, up and act 16-byte aligned. */
 int ti_moe_prefill_q3(ti_ctx* ctx, float* x, const float* normed, const float* logits, const float* bias,
                       const uint32_t* w1p, const uint16_t* w1s, const uint32_t* w3p, const uint16_t* w3s,
                       const uint32_t* w2p, const uint16_t* w2s, int32_t* idx, float* wt, float* gate, float* up,

@@ -813,7 +813,8 @@ extern "C" int ti_moe_prefill_q3(ti_ctx* c, float* x, const float* normed, const
     const long cap = (long)TI_ACT_CAP * TI_ACT_TMAX;
     TI_REQUIRE((long)T * H <= cap && P * I <= cap, "ti_moe_prefill_q3: T*H=%ld or P*I=%ld exceeds %ld", (long)T * H,
                P * I, cap);
-    TI_REQUIRE(al16(gate) && al16(up) && al16(act), "ti_moe_prefill_q3: gate, up and act must be 16-byte aligned");
+    TI_REQUIRE(al16(normed) && al16(gate) && al16(up) && al16(act),
+               "ti_moe_prefill_q3: normed, gate, up and act must be 16-byte aligned");
     const int nq = T * (H / 32);
     k_router_quant<<<(unsigned)(T + (nq + 63) / 64), 64, 0, c->stream>>>(logits, bias, nE, topk, idx, wt, T, normed,
                                                                           c->act_q, c->act_s, nq);
