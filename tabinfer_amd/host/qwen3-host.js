@@ -18,6 +18,7 @@ const { createEngine, bf16ToF16bits, f32ToF16 } = require('./ti-engine');
 const { loadTokenizer } = require('./tokenizer');
 const { selfTestKernels } = require('./self-test');
 const QC = require('./quant-cache');
+const CONV = require('./conversation');
 
 // models/qwen3.js CONFIGS (Qwen3-0.6B / 1.7B geometry)
 const CONFIGS = {
@@ -83,35 +84,6 @@ function toF16Bits(t, buf) {
 
 // toolPreamble (:5294-5320): Qwen3's own (Hermes) tool block, appended to the system prompt,
 // the text its chat template renders (the model was trained on exactly this wording)
-function toolPreamble(tools) {
-  const fns = (tools || []).filter((t) => t && t.type === 'function' && t.function);
-  if (!fns.length) return '';
-  const sigs = fns.map((t) => JSON.stringify({ type: 'function', function: t.function })).join('\n');
-  return ['# Tools', '', 'You may call one or more functions to assist with the user query.', '',
-    'You are provided with function signatures within <tools></tools> XML tags:', '<tools>', sigs, '</tools>', '',
-    'For each function call, return a json object with function name and arguments within <tool_call></tool_call> XML tags:',
-    '<tool_call>', '{"name": <function-name>, "arguments": <args-json-object>}', '</tool_call>'].join('\n');
-}
-
-// every message as plain text for the encoder (:5429-5441): assistant tool calls as
-// <tool_call> blocks, tool results as <tool_response> user turns, text parts joined
-function renderMessage(m) {
-  let c = m.content;
-  if (Array.isArray(c)) c = c.filter((p) => p && p.type === 'text').map((p) => p.text || '').join('\n');
-  c = c == null ? '' : String(c);
-  if (m.role === 'tool') return { role: 'user', content: '<tool_response>\n' + c + '\n</tool_response>' };
-  if (m.role === 'assistant' && Array.isArray(m.tool_calls) && m.tool_calls.length) {
-    const tc = m.tool_calls.map((t) => '<tool_call>\n{"name": "' + ((t.function && t.function.name) || '') + '", "arguments": ' +
-      ((t.function && t.function.arguments) || '{}') + '}\n</tool_call>').join('\n');
-    c = c ? c + '\n' + tc : tc;
-  }
-  return { role: m.role, content: c };
-}
-
-// The system-prompt KV anchor's decision (models/qwen3.js:5378-5389): may a conversation whose
-// prompt `ids` begins with the system block `sysIds` take KV rows [0, P) as they stand?
-// Only when the block is long enough (16 tokens), the live prefix cache does not already
-// cover it, and the anchor records exactly this block.
 function claimSystemBlock(ids, sysIds, cachedIds, anchorIds) {
   if (!sysIds || sysIds.length < 16) return false;
   const P = sysIds.length;
@@ -472,38 +444,6 @@ function createQwen3Host({ device = 0 } = {}) {
     return decode(out);
   }
 
-  // <think> / <tool_call> splitting of the streamed text (the reference's makeRoundParser)
-  function makeRoundParser(onReasoning, onContent) {
-    const p = { state: 'content', content: '', reasoning: '', toolCalls: [], buf: '' };
-    const OPEN_T = '<think>', CLOSE_T = '</think>', OPEN_C = '<tool_call>', CLOSE_C = '</tool_call>';
-    p.push = (text) => {
-      p.buf += text;
-      for (;;) {
-        if (p.state === 'think') {
-          const i = p.buf.indexOf(CLOSE_T);
-          if (i < 0) { const keep = Math.max(0, p.buf.length - CLOSE_T.length); if (keep) { onReasoning(p.buf.slice(0, keep)); p.reasoning += p.buf.slice(0, keep); p.buf = p.buf.slice(keep); } return; }
-          if (i) { onReasoning(p.buf.slice(0, i)); p.reasoning += p.buf.slice(0, i); }
-          p.buf = p.buf.slice(i + CLOSE_T.length); p.state = 'content';
-        } else if (p.state === 'tool') {
-          const i = p.buf.indexOf(CLOSE_C);
-          if (i < 0) return;
-          p.toolCalls.push(p.buf.slice(0, i).trim()); p.buf = p.buf.slice(i + CLOSE_C.length); p.state = 'content';
-        } else {
-          const it = p.buf.indexOf(OPEN_T), ic = p.buf.indexOf(OPEN_C);
-          const i = it < 0 ? ic : (ic < 0 ? it : Math.min(it, ic));
-          if (i < 0) { const keep = Math.max(0, p.buf.length - OPEN_C.length); if (keep) { onContent(p.buf.slice(0, keep)); p.content += p.buf.slice(0, keep); p.buf = p.buf.slice(keep); } return; }
-          if (i) { onContent(p.buf.slice(0, i)); p.content += p.buf.slice(0, i); }
-          if (i === it) { p.buf = p.buf.slice(i + OPEN_T.length); p.state = 'think'; } else { p.buf = p.buf.slice(i + OPEN_C.length); p.state = 'tool'; }
-        }
-      }
-    };
-    p.flush = () => {
-      if (p.buf) { if (p.state === 'think') { onReasoning(p.buf); p.reasoning += p.buf; } else if (p.state === 'content') { onContent(p.buf); p.content += p.buf; } }
-      p.buf = '';
-    };
-    return p;
-  }
-
   // _streamIds (:5199-5292) without grammar masking: prefix-cache reuse, chunked prefill of
   // the rest, then the batched decode loop
   async function streamIds(ids, { maxTokens, onToken, signal, temperature }) {
@@ -545,87 +485,34 @@ function createQwen3Host({ device = 0 } = {}) {
     return true;
   }
 
-  // runConversation({provider, messages, systemPrompt, tools, convId, signal}, emit) (:5397-5522):
-  // rounds of prefill + decode with the event stream; tool calls run through setToolRunner
+  // runConversation({provider, messages, systemPrompt, tools, convId, signal}, emit)
+  // (models/qwen3.js:5397-5522): the system block (system prompt + tool preamble) and the
+  // rendered messages form the transcript; conversation.js runs the rounds over streamIds,
+  // with the system-prompt KV anchor claimed before round 0 and recorded after it.
   async function runConversation({ provider, messages, systemPrompt, tools, convId, signal } = {}, emit) {
-    try {
-      if (!M) throw new Error('no model loaded: call loadModel() first');
-      if (!TOK) throw new Error('runConversation needs loadModel({tokenizer})');
-    } catch (e) {
-      emit({ type: 'error', message: 'Qwen3 dense: ' + e.message });
+    const unusable = !M ? 'no model loaded: call loadModel() first' : (!TOK ? 'runConversation needs loadModel({tokenizer})' : null);
+    if (unusable) {
+      emit({ type: 'error', message: CONV.ERROR_PREFIX + unusable });
       emit({ type: 'agent_done' });
       return;
     }
+    const offered = (Array.isArray(tools) ? tools : []).filter((t) => t && t.type === 'function');
+    const sysText = [(systemPrompt && typeof systemPrompt === 'object') ? (systemPrompt.content || '') : (systemPrompt || ''),
+      CONV.toolPreamble(offered)].filter(Boolean).join('\n\n');
+    const transcript = sysText ? [{ role: 'system', content: sysText }] : [];
+    for (const m of (messages || [])) if (m && m.role) transcript.push(CONV.renderMessage(m));
+    const sysIds = sysText ? TOK.encodeChat([{ role: 'system', content: sysText }], { addGenerationPrompt: false }) : null;
     const maxTokens = (provider && (provider.maxTokens | 0)) || C.max_ctx;
-    let sys = (systemPrompt && typeof systemPrompt === 'object') ? (systemPrompt.content || '') : (systemPrompt || '');
-    const toolList = (Array.isArray(tools) ? tools : []).filter((t) => t && t.type === 'function');
-    const pre = toolPreamble(toolList);
-    if (pre) sys = sys ? sys + '\n\n' + pre : pre;
-    const work = [];
-    if (sys) work.push({ role: 'system', content: sys });
-    const sysIds = sys ? TOK.encodeChat([{ role: 'system', content: sys }], { addGenerationPrompt: false }) : null;
-    for (const m of (messages || [])) if (m && m.role) work.push(renderMessage(m));
-    const MAX_ROUNDS = toolList.length ? 8 : 1;
-    try {
-      for (let round = 0; round < MAX_ROUNDS; round++) {
-        if (signal && signal.aborted) throw abortError();
-        emit({ type: 'round_start' });
-        let firstTok = false;
-        const clearInfo = () => { if (!firstTok) { firstTok = true; emit({ type: 'info', message: null }); } };
-        const parser = makeRoundParser((rz) => { clearInfo(); emit({ type: 'delta', delta: { reasoning: rz } }); },
-          (ct) => { clearInfo(); emit({ type: 'delta', delta: { content: ct } }); });
-        const ids = TOK.encodeChat(work);
-        if (round === 0) sysCacheClaim(ids, sysIds, emit);
-        await streamIds(ids, { maxTokens, signal, onToken: (t) => parser.push(t) });
-        if (round === 0) _sysAnchor = sysIds && sysIds.length >= 16 && startsWith(ids, sysIds) ? { ids: sysIds } : null;
-        parser.flush();
-        if (signal && signal.aborted) throw abortError();
-        emit({ type: 'info', message: null });
-        let content = parser.content.replace(/^\s+/, '');
-        const toolCalls = [];
-        parser.toolCalls.forEach((raw, k) => {
-          try { const o = JSON.parse(raw); if (o && o.name) toolCalls.push({ id: 'call_' + round + '_' + k, type: 'function', function: { name: o.name, arguments: JSON.stringify(o.arguments || {}) } }); } catch (_) { /* not a call */ }
-        });
-        // never a blank turn (:5474-5486): no answer and no call means the budget ran out
-        if (!content && !toolCalls.length) {
-          const cutMidThink = parser.state === 'think' || parser.reasoning.length > 0;
-          content = cutMidThink
-            ? '⚠️ I ran out of room to answer: this conversation is near the model\'s context limit (' + C.max_ctx + ' tokens), so it used the remaining budget on reasoning and couldn\'t finish a reply. Start a new chat, remove a large earlier message (e.g. a long command output), or raise **Context size** in the provider settings.'
-            : '⚠️ The model produced no output. Try resending, or start a new chat if the history is very long.';
-          emit({ type: 'delta', delta: { content } });
-        }
-        if (toolCalls.length) emit({ type: 'delta', delta: { tool_calls: toolCalls.map((tc, i) => ({ index: i, id: tc.id, type: 'function', function: { name: tc.function.name, arguments: tc.function.arguments } })) } });
-        emit({ type: 'round_end', content });
-        // usage as the reference reports it (:5488-5492): the exact prompt token count
-        emit({ type: 'usage', usage: { prompt_tokens: ids.length, total_tokens: ids.length } });
-        const asst = { role: 'assistant', content };
-        if (toolCalls.length) asst.tool_calls = toolCalls;
-        emit({ type: 'message_added', message: asst });
-        work.push(renderMessage(asst));
-        if (!toolCalls.length) break;
-        if (!_toolRunner) { emit({ type: 'info', message: null }); break; }
-        for (const tc of toolCalls) {
-          if (signal && signal.aborted) throw abortError();
-          emit({ type: 'tool_started', tc });
-          let args = {};
-          try { args = JSON.parse(tc.function.arguments || '{}'); } catch (_) { /* empty args */ }
-          let res;
-          try { res = await _toolRunner(tc.function.name, args, convId, signal); } catch (e) {
-            if (e && e.name === 'AbortError') throw e;
-            res = { result: 'Error: ' + ((e && e.message) || e) };
-          }
-          const text = res && res.result != null ? res.result : '';
-          emit({ type: 'tool_result', id: tc.id, result: text, artifacts: res && res.artifacts });
-          work.push(renderMessage({ role: 'tool', tool_call_id: tc.id, content: text }));
-          emit({ type: 'message_added', message: { role: 'tool', tool_call_id: tc.id, content: text } });
-        }
-      }
-    } catch (e) {
-      if (e && e.name === 'AbortError') throw e;
-      emit({ type: 'info', message: null });
-      emit({ type: 'error', message: 'Qwen3 dense: ' + ((e && e.message) || e) });
-    }
-    emit({ type: 'agent_done' });
+    const deps = {
+      encode: (msgs) => TOK.encodeChat(msgs),
+      stream: (ids, onText) => streamIds(ids, { maxTokens, signal, onToken: onText }),
+      runTool: _toolRunner,
+      hooks: {
+        beforeFirst: (ids) => sysCacheClaim(ids, sysIds, emit),
+        afterFirst: (ids) => { _sysAnchor = sysIds && sysIds.length >= 16 && startsWith(ids, sysIds) ? { ids: sysIds } : null; },
+      },
+    };
+    await CONV.converse({ transcript, toolsOffered: offered.length > 0, ctxLimit: C.max_ctx, convId, signal }, deps, emit);
   }
 
   return {
@@ -643,5 +530,5 @@ function createQwen3Host({ device = 0 } = {}) {
   };
 }
 
-module.exports = { createQwen3Host, CONFIGS, readSafetensorsHeader, toolPreamble, renderMessage, claimSystemBlock, GEN_BATCH,
+module.exports = { createQwen3Host, CONFIGS, readSafetensorsHeader, toolPreamble: CONV.toolPreamble, renderMessage: CONV.renderMessage, claimSystemBlock, GEN_BATCH,
   PIPE_DEPTH, PREFILL_CHUNK };

@@ -127,3 +127,95 @@ def test_tool_preamble_and_message_rendering(checks):
     assert tool == {"role": "user", "content": "<tool_response>\n42\n</tool_response>"}
     assert asst == {"role": "assistant", "content": 'ok\n<tool_call>\n{"name": "f", "arguments": {"a":1}}\n</tool_call>'}
     assert user == {"role": "user", "content": "a\nb"}
+
+
+@pytest.fixture(scope="module")
+def conv(tmp_path_factory):
+    out = tmp_path_factory.mktemp("conv") / "conv.json"
+    subprocess.run([NODE, os.path.join(ROOT, "tests", "js", "conv_spec.js"), str(out)], check=True, timeout=60)
+    with open(out) as f:
+        d = json.load(f)
+    return {c["name"]: c for c in d["cases"]}, d["parsed"]
+
+
+def kinds(case):
+    return [e["type"] for e in case["events"] if not e["type"].startswith("_")]
+
+
+def deltas(case, field):
+    return "".join(e["delta"][field] for e in case["events"] if e["type"] == "delta" and field in e["delta"])
+
+
+def test_conversation_plain_turn(conv):
+    """One round without tools: reasoning and content stream apart (tags split across
+    pieces), the status line clears at the first piece, usage counts the prompt exactly."""
+    c = conv[0]["plain"]
+    k = kinds(c)
+    assert k[0] == "round_start" and k[1] == "info" and k[-1] == "agent_done"
+    assert k[-5:] == ["info", "round_end", "usage", "message_added", "agent_done"]
+    assert deltas(c, "reasoning") == "why so"
+    assert deltas(c, "content") == "\n\nHello world"
+    end = [e for e in c["events"] if e["type"] == "round_end"][0]
+    assert end["content"] == "Hello world"                       # leading whitespace dropped
+    usage = [e for e in c["events"] if e["type"] == "usage"][0]["usage"]
+    assert usage == {"prompt_tokens": len("<user>hi"), "total_tokens": len("<user>hi")}
+    assert [e["type"] for e in c["events"]].count("_before") == 1
+
+
+def test_conversation_tool_round(conv):
+    """A call is parsed, announced as one tool_calls delta, run, and its result re-enters
+    the transcript as a <tool_response> user turn; a body that is not JSON is no call but
+    still takes its index in the ids."""
+    c = conv[0]["tool"]
+    assert c["toolCalls"] == [{"n": "get_time", "a": {"tz": "UTC"}}]
+    tcd = [e["delta"]["tool_calls"] for e in c["events"] if e["type"] == "delta" and "tool_calls" in e["delta"]]
+    assert tcd == [[{"index": 0, "id": "call_0_0", "type": "function",
+                     "function": {"name": "get_time", "arguments": '{"tz":"UTC"}'}}]]
+    started = [e for e in c["events"] if e["type"] == "tool_started"]
+    assert started[0]["tc"]["id"] == "call_0_0"
+    res = [e for e in c["events"] if e["type"] == "tool_result"]
+    assert res == [{"type": "tool_result", "id": "call_0_0", "result": "R1"}]
+    added = [e["message"] for e in c["events"] if e["type"] == "message_added"]
+    assert added[0]["role"] == "assistant" and added[0]["tool_calls"][0]["id"] == "call_0_0"
+    assert added[1] == {"role": "tool", "tool_call_id": "call_0_0", "content": "R1"}
+    assert added[2] == {"role": "assistant", "content": "It is noon."}
+    second = c["prompts"][1]
+    assert second[1] == {"role": "assistant",
+                         "content": '<tool_call>\n{"name": "get_time", "arguments": {"tz":"UTC"}}\n</tool_call>'}
+    assert second[2] == {"role": "user", "content": "<tool_response>\nR1\n</tool_response>"}
+    assert kinds(c).count("round_start") == 2
+
+
+def test_conversation_tool_errors_and_limits(conv):
+    cases = conv[0]
+    err = [e for e in cases["tool_error"]["events"] if e["type"] == "tool_result"][0]
+    assert err["result"] == "Error: boom"
+    k = kinds(cases["no_runner"])
+    assert k[-3:] == ["message_added", "info", "agent_done"] and k.count("round_start") == 1
+    assert kinds(cases["round_cap"]).count("round_start") == 8 and len(cases["round_cap"]["toolCalls"]) == 8
+    se = cases["stream_error"]
+    assert kinds(se)[-3:] == ["info", "error", "agent_done"]
+    assert [e for e in se["events"] if e["type"] == "error"][0]["message"] == "Qwen3 dense: device lost"
+    ab = cases["aborted"]
+    assert ab["rejected"] == "AbortError: aborted" and ab["events"] == []
+
+
+def test_conversation_never_blank(conv):
+    """No answer and no call: the turn's content is a notice, and a turn cut off inside its
+    reasoning names the context limit."""
+    for name, needle in (("blank", "returned nothing"), ("cut_in_think", "4096-token context")):
+        c = conv[0][name]
+        end = [e for e in c["events"] if e["type"] == "round_end"][0]["content"]
+        assert end.startswith("⚠️") and needle in end
+        assert deltas(c, "content").endswith(end)
+    assert deltas(conv[0]["cut_in_think"], "reasoning") == "step one step two"
+
+
+def test_conversation_transcript_and_ids(conv):
+    c = conv[0]["transcript"]
+    assert c["prompts"][0] == [{"role": "system", "content": "S"}, {"role": "user", "content": "q"}]
+    assert c["prompts"][1][2]["content"] == '<tool_call>\n{"name": "f", "arguments": {"a":[1,2]}}\n</tool_call>'
+    parsed = conv[1]
+    assert parsed[0] == {"id": "call_2_3", "type": "function", "function": {"name": "a", "arguments": "{}"}}
+    assert parsed[1] is None and parsed[2] is None
+    assert parsed[3]["function"]["arguments"] == '{"x":"y"}'
