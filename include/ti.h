@@ -65,7 +65,7 @@ int ti_buf_read(ti_ctx* ctx, const void* src, size_t off, void* dst, size_t byte
  * page-locked (ti_host_alloc) for the copy to be asynchronous. Refused during a capture. */
 int ti_buf_read_async(ti_ctx* ctx, const void* src, size_t off, void* dst, size_t bytes);
 int ti_host_alloc(size_t bytes, void** host_ptr);                                           /* pinned */
-int ti_host_free(void* host_ptr);
+int ti_host_free(void* host_ptr);   /* waits for the device first: no queued copy lands in freed memory */
 int ti_buf_copy(ti_ctx* ctx, void* dst, size_t doff, const void* src, size_t soff, size_t bytes);
 int ti_buf_fill_u32(ti_ctx* ctx, void* dst, uint32_t value, size_t count);                 /* kernel fill  */
 int ti_sync(ti_ctx* ctx);

@@ -759,8 +759,28 @@ extern "C" int ti_bonsai_tensor(ti_bonsai* m, const char* name, void** data, siz
     return ti_fail(TI_ERR_INVALID, "ti_bonsai_tensor: unknown tensor '%s'", name);
 }
 
+// [N, K] of a ternary tensor by its name, as check_shapes (model.rs:288-309) derives them
+// from the config: q [nq, H], k/v [nkv, H], o [H, nq], gate/up [I, H], down [H, I],
+// lm_head [vocab, H]
+static void tern_shape(const ti_bonsai_config& C, const std::string& n, long long& N, long long& K) {
+    const long long H = C.hidden, I = C.intermediate, nq = (long long)C.n_heads * C.head_dim,
+                    nkv = (long long)C.n_kv_heads * C.head_dim;
+    auto ends = [&](const char* suf) {
+        const size_t ls = strlen(suf);
+        return n.size() >= ls && n.compare(n.size() - ls, ls, suf) == 0;
+    };
+    N = K = 0;
+    if (ends("q_proj.weight")) { N = nq; K = H; }
+    else if (ends("k_proj.weight") || ends("v_proj.weight")) { N = nkv; K = H; }
+    else if (ends("o_proj.weight")) { N = H; K = nq; }
+    else if (ends("gate_proj.weight") || ends("up_proj.weight")) { N = I; K = H; }
+    else if (ends("down_proj.weight")) { N = H; K = I; }
+    else if (n == "lm_head.weight") { N = C.vocab; K = H; }
+}
+
 // Model::load + check_shapes (model.rs:256-322): every tensor the forward needs, of the
-// kind and shape the config implies, uploaded from the container.
+// kind and shape the config implies (each ternary tensor's N and K compared with the
+// config's, in every layer), uploaded from the container.
 extern "C" int ti_bonsai_load(ti_ctx* c, ti_bonsai* m, const ti_cpubin* bin) {
     TI_CHECK_CTX(c);
     TI_REQUIRE(m && bin, "ti_bonsai_load: null argument");
@@ -783,9 +803,18 @@ extern "C" int ti_bonsai_load(ti_ctx* c, ti_bonsai* m, const ti_cpubin* bin) {
         const int want = s ? TI_CPUBIN_TERN : (n == "model.embed_tokens.weight" ? TI_CPUBIN_EMBED_F16 : TI_CPUBIN_F32);
         const char* wk = want == TI_CPUBIN_TERN ? "tern" : want == TI_CPUBIN_F32 ? "f32" : "embed_f16";
         if (t.kind != want) return ti_fail(TI_ERR_INVALID, "%s: expected `%s`", n.c_str(), wk);
-        if (want == TI_CPUBIN_TERN && ((size_t)t.N * t.K / 4 != db || t.scale_bytes != sb))
-            return ti_fail(TI_ERR_INVALID, "%s: container says [%lld, %lld], config implies %zu codes bytes", n.c_str(), t.N,
-                           t.K, db);
+        if (want == TI_CPUBIN_TERN) {
+            // the [N, K] the config implies, compared dimension by dimension: a transposed
+            // projection has the byte counts of the right one
+            long long en = 0, ek = 0;
+            tern_shape(C, n, en, ek);
+            if (t.N != en || t.K != ek)
+                return ti_fail(TI_ERR_INVALID, "%s: container says [%lld, %lld], config implies [%lld, %lld]", n.c_str(), t.N,
+                               t.K, en, ek);
+            if ((size_t)t.N * t.K / 4 != db || t.scale_bytes != sb)
+                return ti_fail(TI_ERR_INVALID, "%s: container holds %zu code and %zu scale bytes, the config implies %zu and %zu",
+                               n.c_str(), t.data_bytes, t.scale_bytes, db, sb);
+        }
         if (t.data_bytes != db)
             return ti_fail(TI_ERR_INVALID, "%s: container holds %zu bytes, the config implies %zu", n.c_str(), t.data_bytes, db);
         TI_HIP(hipMemcpyAsync(d, t.data, db, hipMemcpyHostToDevice, c->stream));

@@ -446,7 +446,9 @@ extern "C" int ti_cpubin_embed_row(const ti_cpubin* c, const char* name, long lo
     if (t->shape.empty()) return ti_fail(TI_ERR_INVALID, "embedding has no shape");
     const long long d = t->shape.back();
     if (dim != d) return ti_fail(TI_ERR_INVALID, "dst is %d long, embedding dim is %lld", dim, d);
-    if (row < 0 || (row + 1) * d * 2 > t->len) return ti_fail(TI_ERR_INVALID, "row %lld is out of range for %s", row, name);
+    // row < len / (2 d) without forming a product that could overflow (row is the caller's)
+    if (d <= 0 || row < 0 || (unsigned long long)row >= (unsigned long long)t->len / (2ull * (unsigned long long)d))
+        return ti_fail(TI_ERR_INVALID, "row %lld is out of range for %s", row, name);
     const uint8_t* s = c->blob.get() + t->off + row * d * 2;
     for (long long i = 0; i < d; i++) dst[i] = f16_value((uint16_t)(s[2 * i] | (s[2 * i + 1] << 8)));
     return TI_OK;

@@ -168,8 +168,12 @@ extern "C" int ti_host_alloc(size_t bytes, void** out) {
     return TI_OK;
 }
 
+// frees ti_host_alloc memory after the device has finished every queued operation, so a
+// copy still in flight into the memory never lands in freed pages
 extern "C" int ti_host_free(void* p) {
-    if (p) TI_HIP(hipHostFree(p));
+    if (!p) return TI_OK;
+    TI_HIP(hipDeviceSynchronize());
+    TI_HIP(hipHostFree(p));
     return TI_OK;
 }
 

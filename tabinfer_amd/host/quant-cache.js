@@ -11,6 +11,12 @@
 //                                  kind, shape, numel, N, K}]}
 //   <dir>/v1/<variant>/c0, c1, ...  the stream: every segment starts 16-byte aligned
 //
+// The manifest also records `source`, the checkpoint the bytes were quantized from (each
+// safetensors file's resolved path, size, modification time and a SHA-256 of its header;
+// the reference needs no such field because its variant fixes the download URL). A load
+// that names a checkpoint reads the cache only when the checkpoint's identity matches; a
+// load from the cache alone accepts any source.
+//
 // The manifest is the commit point, as in the reference: removed before a write starts,
 // written after the last chunk, so a cache whose write was cut short is never read. A
 // manifest that does not match (version, variant, group size, chunk size, the model's
@@ -18,6 +24,7 @@
 // go to `put(seg, offset, bytes)`, so the format is testable without a GPU.
 const fs = require('fs');
 const path = require('path');
+const crypto = require('crypto');
 
 const QCACHE_VER = 1;
 const QCHUNK = 64 * 1024 * 1024;
@@ -30,12 +37,43 @@ function configKey(c) {
     intermediate: c.intermediate, vocab: c.vocab };
 }
 
+// the identity of a checkpoint (one or more safetensors files, in load order)
+function checkpointIdentity(files) {
+  return {
+    files: [].concat(files).map((f) => {
+      const abs = path.resolve(f);
+      const st = fs.statSync(abs);
+      const fd = fs.openSync(abs, 'r');
+      try {
+        const lenBuf = Buffer.alloc(8);
+        if (fs.readSync(fd, lenBuf, 0, 8, 0) !== 8) throw new Error('safetensors: ' + abs + ' is shorter than its header length');
+        const n = Number(lenBuf.readBigUInt64LE(0));
+        if (!(n > 0 && n <= st.size - 8)) throw new Error('safetensors: bad header length ' + n + ' in ' + abs);
+        const hb = Buffer.alloc(n);
+        if (fs.readSync(fd, hb, 0, n, 8) !== n) throw new Error('safetensors: short header read in ' + abs);
+        return { path: abs, size: st.size, mtimeMs: st.mtimeMs, header: crypto.createHash('sha256').update(lenBuf).update(hb).digest('hex') };
+      } finally {
+        fs.closeSync(fd);
+      }
+    }),
+  };
+}
+
+function sameSource(a, b) {
+  if (!a || !b || !Array.isArray(a.files) || !Array.isArray(b.files) || a.files.length !== b.files.length) return false;
+  return a.files.every((f, i) => {
+    const g = b.files[i];
+    return !!g && f.path === g.path && f.size === g.size && f.mtimeMs === g.mtimeMs && f.header === g.header;
+  });
+}
+
 function cacheDir(dir, variant) { return path.join(dir, 'v' + QCACHE_VER, variant); }
 
-// writeQuantCache(dir, variant, config, segs, get): segs = [{name, role, len, kind, shape,
-// numel, N, K}] in stream order, get(seg) -> Uint8Array of seg.len bytes. chunkSize is for
+// writeQuantCache(dir, variant, config, segs, get, {source}): segs = [{name, role, len, kind,
+// shape, numel, N, K}] in stream order, get(seg) -> Uint8Array of seg.len bytes, source =
+// checkpointIdentity(...) of the checkpoint they came from (null: unknown). chunkSize is for
 // tests (a manifest records it; a reader accepts only QCHUNK).
-function writeQuantCache(dir, variant, config, segs, get, chunkSize = QCHUNK) {
+function writeQuantCache(dir, variant, config, segs, get, { chunkSize = QCHUNK, source = null } = {}) {
   const d = cacheDir(dir, variant);
   fs.mkdirSync(d, { recursive: true });
   const mf = path.join(d, 'manifest');
@@ -69,29 +107,32 @@ function writeQuantCache(dir, variant, config, segs, get, chunkSize = QCHUNK) {
   }
   flush();
   const manifest = { ver: QCACHE_VER, variant, qgroup: QGROUP, chunkSize, nChunks: idx, totalBytes: off,
-    config: configKey(config), segs: out };
+    config: configKey(config), source: source || null, segs: out };
   fs.writeFileSync(mf + '.tmp', JSON.stringify(manifest));
   fs.renameSync(mf + '.tmp', mf);                                 // the commit point
   return manifest;
 }
 
-// the manifest of a usable cache for (variant, config), or null (chunkSize: tests only)
-function readManifest(dir, variant, config, chunkSize = QCHUNK) {
+// the manifest of a usable cache for (variant, config), or null; with a source (the
+// checkpoint the caller would otherwise load) the manifest must record the same one
+// (chunkSize: tests only)
+function readManifest(dir, variant, config, { chunkSize = QCHUNK, source = null } = {}) {
   let m;
   try { m = JSON.parse(fs.readFileSync(path.join(cacheDir(dir, variant), 'manifest'), 'utf8')); } catch (_) { return null; }
   if (!m || m.ver !== QCACHE_VER || m.variant !== variant || m.qgroup !== QGROUP || m.chunkSize !== chunkSize) return null;
   const want = configKey(config);
   for (const k in want) if (!m.config || m.config[k] !== want[k]) return null;
   if (!Array.isArray(m.segs)) return null;
+  if (source && !sameSource(source, m.source)) return null;
   return m;
 }
 
-// readQuantCache(dir, variant, config, put, {onProgress, check}) -> false when there is no
-// usable cache, else true after every segment's bytes went to put(seg, offset, bytes).
+// readQuantCache(dir, variant, config, put, {onProgress, check, source}) -> false when there
+// is no usable cache, else true after every segment's bytes went to put(seg, offset, bytes).
 // check(seg) may reject a manifest whose segments do not fit the caller's buffers (it
 // throws); chunks are read one at a time (peak host memory: one chunk). chunkSize: tests.
-function readQuantCache(dir, variant, config, put, { onProgress, check, chunkSize = QCHUNK } = {}) {
-  const m = readManifest(dir, variant, config, chunkSize);
+function readQuantCache(dir, variant, config, put, { onProgress, check, chunkSize = QCHUNK, source = null } = {}) {
+  const m = readManifest(dir, variant, config, { chunkSize, source });
   if (!m) return false;
   if (check) for (const s of m.segs) check(s);
   const d = cacheDir(dir, variant);
@@ -117,5 +158,5 @@ function dropQuantCache(dir, variant) {
   if (fs.existsSync(mf)) fs.unlinkSync(mf);
 }
 
-module.exports = { writeQuantCache, readQuantCache, readManifest, dropQuantCache, configKey, cacheDir, QCHUNK, QGROUP,
-  QCACHE_VER };
+module.exports = { writeQuantCache, readQuantCache, readManifest, dropQuantCache, configKey, cacheDir, checkpointIdentity,
+  sameSource, QCHUNK, QGROUP, QCACHE_VER };

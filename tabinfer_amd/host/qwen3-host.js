@@ -213,10 +213,11 @@ function createQwen3Host({ device = 0 } = {}) {
 
   // the fast load (models/qwen3.js:3675-3717): every segment of a valid cache written
   // straight into the decoder's buffers; false when the directory holds no usable cache
-  function loadQuantCache(dir, variant, onProgress) {
+  function loadQuantCache(dir, variant, onProgress, source) {
     const bufs = new Map(cacheSegments().map((s) => [s.name + '.' + s.role, s]));
     return QC.readQuantCache(dir, variant, C, (seg, off, bytes) => E.writeBuffer(bufs.get(seg.name + '.' + seg.role).buf, off, bytes), {
       onProgress,
+      source,
       check: (seg) => {
         const mine = bufs.get(seg.name + '.' + seg.role);
         if (!mine || mine.len !== seg.len) throw new Error('quant cache: segment ' + seg.name + '.' + seg.role + ' does not fit this model');
@@ -225,16 +226,20 @@ function createQwen3Host({ device = 0 } = {}) {
   }
 
   // the writer (:3629-3664): the quantized bytes read back from the GPU, one tensor at a time
-  function writeQuantCache(dir, variant) {
+  function writeQuantCache(dir, variant, source) {
     E.sync();
-    return QC.writeQuantCache(dir, variant, C, cacheSegments(), (seg) => new Uint8Array(E.readBytes(seg.buf, 0, seg.len)));
+    return QC.writeQuantCache(dir, variant, C, cacheSegments(), (seg) => new Uint8Array(E.readBytes(seg.buf, 0, seg.len)), { source });
   }
 
   // loadModel({variant, nCtx, config, safetensors, random, tokenizer, quantCache, onProgress})
   // (models/qwen3.js:3719): allocates the decoder for `nCtx` positions and fills it. With
   // quantCache (a directory), a valid cache of this variant and geometry is loaded instead
-  // of the checkpoint; after a checkpoint load the cache is (re)written. A cache that
-  // cannot be read falls back to the checkpoint (:3752-3759); a failed write only warns.
+  // of the checkpoint; after a checkpoint load the cache is (re)written. When safetensors
+  // are named, only a cache quantized from those same files is read (path, size,
+  // modification time and header hash), so another checkpoint of the same geometry is a
+  // miss. A cache that cannot be read falls back to the checkpoint (:3752-3759); a failed
+  // write only warns. With no usable source of weights (a cache miss and neither
+  // safetensors nor random) loadModel throws and leaves no model loaded.
   async function loadModel(opts = {}) {
     if (M && !opts.reload) return;
     if (M) unload();
@@ -252,21 +257,31 @@ function createQwen3Host({ device = 0 } = {}) {
       const beside = path.join(path.dirname([].concat(opts.safetensors)[0]), 'tokenizer.json');
       if (fs.existsSync(beside)) TOK = loadTokenizer(beside);
     }
+    const files = opts.safetensors ? [].concat(opts.safetensors) : null;
+    let source = null;
+    if (files && opts.quantCache) {
+      try { source = QC.checkpointIdentity(files); } catch (e) { unload(); throw e; }
+    }
     let cached = false;
     if (opts.quantCache) {
-      try { cached = loadQuantCache(opts.quantCache, variant, opts.onProgress); } catch (e) {
+      try { cached = loadQuantCache(opts.quantCache, variant, opts.onProgress, source); } catch (e) {
         console.warn('[qwen3] quant cache load failed, loading the checkpoint:', (e && e.message) || e);
       }
     }
     if (!cached) {
-      if (opts.safetensors) {
-        loadWeights([].concat(opts.safetensors), opts.onProgress);
+      if (files) {
+        loadWeights(files, opts.onProgress);
         if (opts.quantCache) {
-          try { writeQuantCache(opts.quantCache, variant); } catch (e) {
+          try { writeQuantCache(opts.quantCache, variant, source); } catch (e) {
             console.warn('[qwen3] quant cache write failed (the next load quantizes again):', (e && e.message) || e);
           }
         }
       } else if (opts.random != null) randomWeights(opts.random);
+      else {
+        unload();
+        throw new Error('loadModel: no weights: ' + (opts.quantCache ? 'no usable quant cache in ' + opts.quantCache + ', and ' : '') +
+          'neither safetensors nor random was given');
+      }
     }
     E.sync();
     _lastLoadCached = cached;

@@ -19,6 +19,7 @@
 #include <cstdio>
 #include <cstring>
 #include <limits>
+#include <map>
 #include <mutex>
 #include <string>
 #include <unordered_set>
@@ -573,13 +574,27 @@ napi_value js_event_wait_async(napi_env env, napi_callback_info info) {
 }
 
 // host_alloc(bytes) -> ArrayBuffer over page-locked memory, freed by host_free(ab) (which
-// detaches it) or with the ArrayBuffer; the live set keeps the two from freeing twice
+// detaches it) or with the ArrayBuffer; the live set (start -> bytes) keeps the two from
+// freeing twice and lets the asynchronous reads check that their destination lies inside
+// one live allocation (memory the JS heap owns could move or be collected mid-copy).
+// ti_host_free waits for the device first, so no queued copy writes freed memory.
 std::mutex g_pin_mu;
-std::unordered_set<void*> g_pinned;
+std::map<const char*, size_t> g_pinned;
 
 bool pin_release(void* p) {
     std::lock_guard<std::mutex> lk(g_pin_mu);
-    return g_pinned.erase(p) > 0;
+    return g_pinned.erase(static_cast<const char*>(p)) > 0;
+}
+
+// [p, p + len) inside one live host_alloc allocation
+bool pinned_range(const void* p, size_t len) {
+    const char* q = static_cast<const char*>(p);
+    std::lock_guard<std::mutex> lk(g_pin_mu);
+    auto it = g_pinned.upper_bound(q);
+    if (it == g_pinned.begin()) return false;
+    --it;
+    const size_t off = (size_t)(q - it->first);
+    return off <= it->second && len <= it->second - off;
 }
 
 void fin_host(napi_env, void* data, void*) {
@@ -597,7 +612,7 @@ napi_value js_host_alloc(napi_env env, napi_callback_info info) {
     if (rc) return throw_ti(env, "host_alloc", rc);
     {
         std::lock_guard<std::mutex> lk(g_pin_mu);
-        g_pinned.insert(p);
+        g_pinned[static_cast<const char*>(p)] = (size_t)bytes;
     }
     napi_value ab;
     if (napi_create_external_arraybuffer(env, p, (size_t)bytes, fin_host, nullptr, &ab) != napi_ok) {
@@ -668,6 +683,8 @@ napi_value js_buf_read_async(napi_env env, napi_callback_info info) {
     size_t cap;
     if (!host_bytes(env, a.v[3], &dst, &cap)) return arg_error(env, fn, 3, "a TypedArray or ArrayBuffer"), nullptr;
     if ((size_t)len > cap) return throw_msg(env, "buf_read_async: the destination is too small");
+    if (len && !pinned_range(dst, (size_t)len))
+        return throw_msg(env, "buf_read_async: the destination is not live host_alloc memory");
     const int rc = ti_buf_read_async(c->c, src, (size_t)off, dst, (size_t)len);
     return rc ? throw_ti(env, fn, rc) : undefined(env);
 }
@@ -1429,6 +1446,8 @@ napi_value js_qwen3_read_tokens_async(napi_env env, napi_callback_info info) {
     napi_get_typedarray_info(env, a.v[4], &tt, &len, &data, &ab, &boff);
     if (tt != napi_int32_array) return arg_error(env, fn, 4, "an Int32Array"), nullptr;
     if (count < 0 || (size_t)count > len) return throw_msg(env, "qwen3_read_tokens_async: count exceeds the array");
+    if (count && !pinned_range(data, (size_t)count * 4))
+        return throw_msg(env, "qwen3_read_tokens_async: the array is not live host_alloc memory");
     const int rc = ti_qwen3_read_tokens_async(c->c, m->m, (int)from, (int)count, static_cast<int32_t*>(data));
     return rc ? throw_ti(env, fn, rc) : undefined(env);
 }

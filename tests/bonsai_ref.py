@@ -61,9 +61,10 @@ def emb_row(W, tok, H):
     return W["model.embed_tokens.weight"][int(tok) * H:(int(tok) + 1) * H]
 
 
-def write_cpubin(path, cfg, W):
+def write_cpubin(path, cfg, W, shapes=None):
     """A `.cpu.bin` container (native/docs/FORMAT.md) as native/tools/pack_bin.py lays it
-    out: u32 header length, JSON header with blob-relative offsets, every entry 16-aligned."""
+    out: u32 header length, JSON header with blob-relative offsets, every entry 16-aligned.
+    shapes: {name: (N, K)} recorded in place of a ternary tensor's own (a mislabelled file)."""
     d = dims(cfg)
     blob, tensors = bytearray(), {}
 
@@ -78,6 +79,8 @@ def write_cpubin(path, cfg, W):
             codes, sc = val
             K = d["I"] if name.endswith("down_proj.weight") else (d["nq"] if name.endswith("o_proj.weight") else d["H"])
             N = codes.size * 4 // K
+            if shapes and name in shapes:
+                N, K = shapes[name]
             co = put(codes.tobytes())
             so = put(sc.tobytes())
             tensors[name] = {"kind": "tern", "N": N, "K": K, "codesOff": co, "codesLen": codes.size, "scalesOff": so,

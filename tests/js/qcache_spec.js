@@ -14,7 +14,7 @@ const segs = lens.map((len, i) => ({ name: 't' + i, role: i % 3 === 0 ? 'pack' :
   len, kind: i % 3 === 2 ? 'f16' : 'int4', shape: [len], numel: len, N: 1, K: len }));
 const data = segs.map((g) => Uint8Array.from({ length: g.len }, () => rnd() & 0xff));
 const res = {};
-const man = QC.writeQuantCache(dir, 'T', cfg, segs, (g) => data[segs.indexOf(g)], 1000);
+const man = QC.writeQuantCache(dir, 'T', cfg, segs, (g) => data[segs.indexOf(g)], { chunkSize: 1000 });
 res.manifest = man;
 res.files = fs.readdirSync(QC.cacheDir(dir, 'T')).sort();
 // read back into fresh buffers
@@ -36,8 +36,34 @@ fs.writeFileSync(c1, keep.subarray(0, 10));
 try { QC.readQuantCache(dir, 'T', cfg, () => {}, { chunkSize: 1000 }); res.truncThrew = false; } catch (e) { res.truncThrew = e.message; }
 fs.writeFileSync(c1, keep);
 // a write cut short leaves no manifest: the next write removes the old one first
-try { QC.writeQuantCache(dir, 'T', cfg, segs, (g) => { if (g.name === 't4') throw new Error('cut'); return data[segs.indexOf(g)]; }, 1000); } catch (_) { /* expected */ }
+try { QC.writeQuantCache(dir, 'T', cfg, segs, (g) => { if (g.name === 't4') throw new Error('cut'); return data[segs.indexOf(g)]; }, { chunkSize: 1000 }); } catch (_) { /* expected */ }
 res.afterCut = QC.readQuantCache(dir, 'T', cfg, () => {}, { chunkSize: 1000 });
+// the checkpoint identity: two safetensors files with the same header (a fine-tune of the
+// same geometry) are different sources; a cache written from A is read for A or for a load
+// from the cache alone, never for B; touching A's modification time makes it a miss too
+const st = (name, fill) => {
+  const hdr = Buffer.from(JSON.stringify({ w: { dtype: 'F16', shape: [4, 4], data_offsets: [0, 32] } }));
+  const len = Buffer.alloc(8); len.writeBigUInt64LE(BigInt(hdr.length));
+  const f = path.join(dir, name);
+  fs.writeFileSync(f, Buffer.concat([len, hdr, Buffer.alloc(32, fill)]));
+  return f;
+};
+const fa = st('a.safetensors', 1), fb = st('b.safetensors', 2);
+const ida = QC.checkpointIdentity([fa]), idb = QC.checkpointIdentity([fb]);
+res.ident = { sameHeader: ida.files[0].header === idb.files[0].header, absolute: path.isAbsolute(ida.files[0].path),
+  size: ida.files[0].size };
+QC.writeQuantCache(dir, 'S', cfg, segs, (g) => data[segs.indexOf(g)], { chunkSize: 1000, source: ida });
+const rd = (source) => QC.readQuantCache(dir, 'S', cfg, () => {}, { chunkSize: 1000, source });
+res.sourceA = rd(ida);
+res.sourceB = rd(idb);
+res.sourceNone = rd(null);
+res.sourceTwo = rd(QC.checkpointIdentity([fa, fb]));
+const later = new Date(Date.now() + 5000);
+fs.utimesSync(fa, later, later);
+res.sourceTouched = rd(QC.checkpointIdentity([fa]));
+res.manifestSource = JSON.parse(fs.readFileSync(path.join(QC.cacheDir(dir, 'S'), 'manifest'), 'utf8')).source;
+fs.writeFileSync(path.join(dir, 'bad.safetensors'), Buffer.from([200, 0, 0, 0, 0, 0, 0, 0, 1, 2]));
+try { QC.checkpointIdentity([path.join(dir, 'bad.safetensors')]); res.badHeader = false; } catch (e) { res.badHeader = e.message; }
 // claimSystemBlock: the reference's conditions
 const S = Array.from({ length: 20 }, (_, i) => 100 + i), P = S.concat([7, 8, 9]);
 res.claim = [

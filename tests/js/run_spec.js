@@ -173,6 +173,23 @@ async function runQcache(host, m, dir) {
   out.fromCache.push(host.loadedFromCache());
   out.gens.push(Array.from(await host.generate(q.prompt, { maxTokens: q.maxTokens })));
   out.manifest = JSON.parse(fs.readFileSync(mf, 'utf8'));
+  // another checkpoint of the same geometry through the same cache: a miss, its own weights
+  // (dumped as c.*), and the cache then holds it (a cache-only load gives c.* again as d.*)
+  if (q.safetensorsB) {
+    await host.loadModel(Object.assign({ safetensors: q.safetensorsB }, base));
+    out.fromCache.push(host.loadedFromCache());
+    dump('c');
+    await host.loadModel(base);
+    out.fromCache.push(host.loadedFromCache());
+    dump('d');
+    out.manifestB = JSON.parse(fs.readFileSync(mf, 'utf8'));
+  }
+  // no usable weights: an empty cache directory and no checkpoint is an error, no model stays loaded
+  try {
+    await host.loadModel({ config: m.config, nCtx: m.nCtx, quantCache: path.join(dir, 'empty-cache'), reload: true });
+    out.noWeights = null;
+  } catch (e) { out.noWeights = e.message; }
+  out.modelAfterNoWeights = host.model() === null;
   return out;
 }
 

@@ -123,6 +123,11 @@ def test_embedding_rows_decode_f16_exactly():
         with pytest.raises(abi.TIError) as e:
             c.embed_row("model.embed_tokens.weight", 0, 5)
         assert "embedding dim is 6" in str(e.value)
+        # rows whose byte offset overflows a signed 64-bit product are out of range too
+        for row in ((2 ** 63 - 1) // 6, (2 ** 63 - 1) // 12 + 1, 2 ** 62, -1):
+            with pytest.raises(abi.TIError) as e:
+                c.embed_row("model.embed_tokens.weight", row, 6)
+            assert "out of range" in str(e.value)
 
 
 def test_open_reads_a_file_and_sorts_names(tmp_path):

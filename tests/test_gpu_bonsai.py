@@ -191,5 +191,19 @@ def test_load_refuses_mismatched_containers(ctx, tmp_path):
             with pytest.raises(abi.TIError) as e:
                 m.load(c)
         assert "gate_proj" in str(e.value)
+        # a transposed projection has the right byte counts: gate_proj recorded as [H, I]
+        # instead of [I, H] (model.rs:288-309 compares N and K one by one)
+        H, I = cfg["hidden"], cfg["intermediate"]
+        p = str(tmp_path / "transposed.cpu.bin")
+        B.write_cpubin(p, cfg, W, shapes={"model.layers.1.mlp.gate_proj.weight": (H, I)})
+        with abi.CpuBin(path=p) as c:
+            with pytest.raises(abi.TIError) as e:
+                m.load(c)
+        assert ("model.layers.1.mlp.gate_proj.weight: container says [%d, %d], config implies [%d, %d]"
+                % (H, I, I, H)) in str(e.value)
+        p = str(tmp_path / "good.cpu.bin")
+        B.write_cpubin(p, cfg, W)
+        with abi.CpuBin(path=p) as c:
+            m.load(c)
     finally:
         m.close()

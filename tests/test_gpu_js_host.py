@@ -412,6 +412,8 @@ def test_quant_cache_and_text_prompts(tmp_path, orc):
     rng = np.random.default_rng(41)
     c = dict(SMALL)
     T, ckpt = _checkpoint(d, rng, c)
+    os.makedirs(os.path.join(d, "b"))
+    _, ckpt_b = _checkpoint(os.path.join(d, "b"), np.random.default_rng(43), c)   # same geometry, other weights
     names = ["model.embed_tokens.weight", "lm_head.weight", "model.norm.weight", "model.layers.1.mlp.down_proj.weight",
              "model.layers.0.self_attn.q_norm.weight", "model.layers.1.self_attn.v_proj.weight"]
     prompt = [11, 502, 7, 999, 123]
@@ -429,16 +431,21 @@ def test_quant_cache_and_text_prompts(tmp_path, orc):
     tok.save(os.path.join(tdir, "tokenizer.json"))
     text, system = "Summarise the decode attention in one line, please 🙂", "You are a careful assistant. " * 6
     spec = {"model": {"config": c, "nCtx": 256, "safetensors": ckpt, "prompt": prompt, "maxTokens": 2,
-                      "qcache": {"dir": os.path.join(d, "qc"), "dump": names, "prompt": prompt, "maxTokens": 24},
+                      "qcache": {"dir": os.path.join(d, "qc"), "dump": names, "prompt": prompt, "maxTokens": 24,
+                                 "safetensorsB": ckpt_b},
                       "tokchat": {"tokenizer": tdir, "text": text, "system": system, "maxTokens": 20}}}
     res = run_spec(d, spec, {})
     q = res["qcache"]
-    assert q["fromCache"] == [False, True, False, True]
+    assert q["fromCache"] == [False, True, False, True, False, True]
+    rd = lambda tag, nm, part: open(os.path.join(d, "%s.%s.%s" % (tag, nm, part)), "rb").read()
     for nm in names:
         for part in ("data", "scales"):
-            fa = os.path.join(d, "a.%s.%s" % (nm, part))
-            if os.path.exists(fa):
-                assert open(fa, "rb").read() == open(os.path.join(d, "b.%s.%s" % (nm, part)), "rb").read(), (nm, part)
+            if os.path.exists(os.path.join(d, "a.%s.%s" % (nm, part))):
+                assert rd("a", nm, part) == rd("b", nm, part), (nm, part)
+                # checkpoint B of the same geometry: its own bytes, not A's from the cache
+                assert rd("c", nm, part) != rd("a", nm, part) and rd("c", nm, part) == rd("d", nm, part), (nm, part)
+    assert q["manifestB"]["source"]["files"][0]["path"] == os.path.abspath(ckpt_b)
+    assert "no weights" in q["noWeights"] and q["modelAfterNoWeights"]
     assert q["gens"][0] == q["gens"][1] == q["gens"][2] and len(q["gens"][0]) == 24
     assert q["manifest"]["config"]["vocab"] == c["vocab"] and q["manifest"]["chunkSize"] == 64 << 20
     tc = res["tokchat"]

@@ -63,5 +63,20 @@ def test_mismatches_and_failures(res):
     assert res["afterCut"] is False
 
 
+def test_checkpoint_identity(res):
+    """A cache records the checkpoint it was quantized from: a load naming another checkpoint
+    of the same geometry (same safetensors header) or a changed file is a miss; a load from
+    the cache alone reads it; a safetensors header that overruns its file is an error."""
+    ident = res["ident"]
+    hdr = json.dumps({"w": {"dtype": "F16", "shape": [4, 4], "data_offsets": [0, 32]}}, separators=(",", ":"))
+    assert ident["sameHeader"] and ident["absolute"] and ident["size"] == 8 + len(hdr) + 32
+    assert res["sourceA"] is True and res["sourceNone"] is True
+    assert res["sourceB"] is False and res["sourceTwo"] is False and res["sourceTouched"] is False
+    src = res["manifestSource"]
+    assert len(src["files"]) == 1 and src["files"][0]["path"].endswith("a.safetensors")
+    assert set(src["files"][0]) == {"path", "size", "mtimeMs", "header"}
+    assert "bad header length" in res["badHeader"]
+
+
 def test_system_block_claim(res):
     assert res["claim"] == [True, False, True, False, False, False, False, False, False]
