@@ -422,8 +422,19 @@ def test_moe_prefill_fused_matches_chain(ctx, orc, T, H, I, nE, topk):
             v.free()
     for k in runs[0]:
         assert np.array_equal(runs[0][k].view(np.uint32), runs[1][k].view(np.uint32)), k
-    oi, _ = orc.router(logits, bias, T, nE, topk)
+    oi, ow = orc.router(logits, bias, T, nE, topk)
     assert np.array_equal(runs[0]["idx"], oi)
+    # the fused block against the oracle itself (models/lfm25.js:2145-2166), as
+    # test_moe_block holds the chain: the expert activations first, then the block output
+    # with the down projection teacher-forced on the GPU's activations (its int8
+    # re-quantization is the only place an f32/f64 difference can flip a code)
+    g = oracle_gemm(orc, normed, T, *w1, oi, P, I, H, topk)
+    u = oracle_gemm(orc, normed, T, *w3, oi, P, I, H, topk)
+    a = g / (1.0 + np.exp(-g)) * u
+    assert norm_err(runs[0]["act"], a) <= 1e-4
+    o = oracle_gemm(orc, runs[0]["act"], P, *w2, oi, P, H, I, 1)
+    want = (ow.astype(np.float64).reshape(T, topk, 1) * o.reshape(T, topk, H)).sum(1).ravel()
+    assert norm_err(runs[0]["x"].astype(np.float64) - x, want) <= 1e-4
     for v in d.values():
         v.free()
 

@@ -87,6 +87,33 @@ def test_rope_preserves_pair_norms_at_32k(orc):
         assert abs(np.angle(np.exp(1j * (ang - pos)))) < 1e-5
 
 
+@pytest.mark.parametrize("hd", [64, 128])
+def test_qk_rmsnorm_against_f64(orc, hd):
+    """The per-head RMSNorm of attnPrepQ8 (models/qwen3.js:2258-2262): x / sqrt(mean(x^2) + eps)
+    * w in f64, with non-unit f16 weights and an eps that matters (mean x^2 ~ 2.5e-3 against
+    eps 1e-3: eps outside the root, a sum in place of the mean or a dropped weight each miss
+    by far more than the f32 tolerance). At pos 0 the rotation is the identity; at pos > 0
+    the output is the f64 split-half rotation of the f64-normed row."""
+    rng = np.random.default_rng(hd)
+    theta, eps = 1e6, 1e-3
+    for trial in range(4):
+        x = (rng.standard_normal(hd) * 0.05).astype(np.float32)
+        w = (0.5 + rng.uniform(0, 1, hd)).astype(np.float16)
+        x64, w64 = x.astype(np.float64), w.astype(np.float64)
+        n = x64 / np.sqrt(np.mean(x64 * x64) + eps) * w64
+        got = orc.rope_norm_row(x, w.view(np.uint16), hd, 0, theta, eps, True).astype(np.float64)
+        assert np.max(np.abs(got - n)) <= 1e-6 * np.max(np.abs(n))
+        pos = int(rng.integers(1, 32768))
+        half = hd // 2
+        ang = pos * theta ** (-(2.0 * np.arange(half)) / hd)
+        c, sn = np.cos(ang), np.sin(ang)
+        want = np.concatenate([n[:half] * c - n[half:] * sn, n[half:] * c + n[:half] * sn])
+        got = orc.rope_norm_row(x, w.view(np.uint16), hd, pos, theta, eps, True).astype(np.float64)
+        # the angle pos * theta^(-2i/hd) is formed in f32 by the reference's rotary table:
+        # ~pos * 2^-24 radians of phase error at most
+        assert np.max(np.abs(got - want)) <= (4e-6 + pos * 2.0 ** -22) * np.max(np.abs(n))
+
+
 def test_attn_prep_qk_norm_and_kv_write(orc):
     nHq, nKv, hd, pos = 4, 2, 128, 7
     i = np.arange(nHq * hd)

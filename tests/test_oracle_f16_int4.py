@@ -117,6 +117,28 @@ def test_int4_known_answers(orc):
     assert (pack[0] & 0xF) == 15 and ((pack[0] >> 4) & 0xF) == 1 and ((pack[0] >> 8) & 0xF) == 8
 
 
+def test_int4_ties_round_toward_plus_infinity(orc):
+    """Math.round (qwen3.js:3419): a half rounds toward +Inf, so 2.5 -> 3 but -2.5 -> -2, and
+    -0.5 -> -0, whose nibble is 8. Scales are exact here (maxabs 7 -> 1.0, maxabs 3.5 -> 0.5),
+    so every w * inv is an exact half or whole number; ties to even, or away from zero,
+    would give other nibbles."""
+    K = 64
+    g0 = [7, 2.5, -2.5, -0.5, 0.5, 3.5, -3.5, 1.5, -1.5, 0, -7, 6.5, -6.5]
+    g1 = [3.5, 1.25, -1.25, -0.25, 0.25, -0.75, 0.75, -3.25, 3.25, 0]       # inv = 2
+    vals = np.zeros(K, np.float32)
+    vals[:len(g0)] = g0
+    vals[32:32 + len(g1)] = g1
+    pack, sc = orc.quant_int4_bf16(_bf16(vals), 1, K)
+    assert sc[0] == 0x3C00 and sc[1] == 0x3800
+    codes = _unpack(pack, 1, K)[0]
+    want0 = [7, 3, -2, 0, 1, 4, -3, 2, -1, 0, -7, 7, -6]
+    want1 = [7, 3, -2, 0, 1, -1, 2, -6, 7, 0]
+    assert list(codes[:len(g0)] - 8) == want0
+    assert list(codes[32:32 + len(g1)] - 8) == want1
+    # the nibbles of -0.5 and 0.5 (k = 3, 4: word 0, bits 12 and 16)
+    assert ((pack[0] >> 12) & 0xF) == 8 and ((pack[0] >> 16) & 0xF) == 9
+
+
 def test_int4_zero_and_tiny_groups(orc):
     K = 64
     vals = np.zeros(K, np.float32)
