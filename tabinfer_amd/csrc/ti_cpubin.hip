@@ -15,7 +15,7 @@
 // N*(K/G)*4, and any byte range that overruns the blob; f32 ranges must be whole f32s at
 // 4-byte-aligned offsets. The blob is held in its own 16-byte-aligned allocation, so an
 // odd header length does not misalign it (binfmt.rs:55-78).
-#include "ti_internal.h"
+#include "ti_host.h"
 #include <errno.h>
 #include <math.h>
 #include <stdio.h>

@@ -1,16 +1,11 @@
 // ti_internal.h — shared host/device helpers for libtabinfer (gfx950 only).
 #pragma once
 #include <hip/hip_runtime.h>
-#include <stdint.h>
-#include <stddef.h>
-#include "../../include/ti.h"
+#include "ti_host.h"
 
-// ---- host-side error plumbing ------------------------------------------------
-int ti_fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+// ---- host-side error plumbing (ti_fail, TI_REQUIRE: ti_host.h) -----------------
 int ti_hip_fail(hipError_t e, const char* what);
 
-#define TI_CHECK_CTX(ctx) do { if (!(ctx)) return ti_fail(TI_ERR_INVALID, "%s: null context", __func__); } while (0)
-#define TI_REQUIRE(cond, ...) do { if (!(cond)) return ti_fail(TI_ERR_INVALID, __VA_ARGS__); } while (0)
 #define TI_HIP(call) do { hipError_t _e = (call); if (_e != hipSuccess) return ti_hip_fail(_e, #call); } while (0)
 #define TI_LAUNCHED(name) do { hipError_t _e = hipGetLastError(); if (_e != hipSuccess) return ti_hip_fail(_e, name); } while (0)
 

@@ -8,18 +8,6 @@
 #include <string.h>
 #include <stdlib.h>
 
-static thread_local char g_err[512] = "";
-
-extern "C" const char* ti_last_error(void) { return g_err; }
-
-int ti_fail(int code, const char* fmt, ...) {
-    va_list ap;
-    va_start(ap, fmt);
-    vsnprintf(g_err, sizeof g_err, fmt, ap);
-    va_end(ap);
-    return code;
-}
-
 int ti_hip_fail(hipError_t e, const char* what) {
     int code = (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) ? TI_ERR_OOM
              : (e == hipErrorNoDevice || e == hipErrorInvalidDevice) ? TI_ERR_NO_DEVICE : TI_ERR_HIP;
