@@ -200,7 +200,9 @@ int ti_attn_decode_q8(ti_ctx* ctx, const float* qr, const uint32_t* kq, const fl
  * file-scope device array of the library (2.03 MiB, held by every device the call runs on
  * until the process ends), so nHq * splits <= 4096 (splits as ti_attn_decode_q8 picks
  * them for nsplit = 0; at most 512); larger calls fail with TI_ERR_INVALID. `stream` is a
- * hipStream_t (NULL: the null stream); the call is ordered on it and does not block. All
+ * hipStream_t (NULL: the null stream); the call is ordered on it and does not block. The
+ * array used is the copy on the stream's device (the current device for NULL), whatever
+ * device is current; the first call on a device looks its address up once. All
  * calls on one device share the array, so calls whose execution overlaps on one device
  * (two streams, two threads) race; calls ordered on one stream do not. */
 int ti_attn_decode_q8_noalloc(void* stream, const float* qr, const uint32_t* kq, const float* ks,

@@ -707,11 +707,17 @@ static __device__ __align__(256) float scratch[NOALLOC_ROWSPLITS * (TI_ATTN_HD_M
 static std::mutex g_scratch_mu;
 static float* g_scratch_addr[NOALLOC_DEVICES];
 
+// the array's address on device dev (looked up with dev current, the caller's device restored)
 static int scratch_address(int dev, float** out) {
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     if (!g_scratch_addr[dev]) {
+        int cur = -1;
+        TI_HIP(hipGetDevice(&cur));
+        if (cur != dev) TI_HIP(hipSetDevice(dev));
         void* p = nullptr;
-        TI_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (cur != dev) TI_HIP(hipSetDevice(cur));
+        if (e != hipSuccess) return ti_hip_fail(e, "hipGetSymbolAddress(scratch)");
         if (!p) return ti_fail(TI_ERR_HIP, "ti_attn_decode_q8_noalloc: no device address for the scratch array");
         g_scratch_addr[dev] = static_cast<float*>(p);
     }
@@ -732,8 +738,11 @@ extern "C" int ti_attn_decode_q8_noalloc(void* stream, const float* qr, const ui
     TI_REQUIRE(nsplit <= TI_ATTN_SPLITS_MAX && (long)nHq * nsplit <= NOALLOC_ROWSPLITS,
                "ti_attn_decode_q8_noalloc: %d heads x %d splits exceed the scratch array (%d head-splits, %d splits at most)",
                nHq, nsplit, NOALLOC_ROWSPLITS, TI_ATTN_SPLITS_MAX);
+    // the kernels run on the stream's device, so the scratch address is that device's
+    // (the null stream: the current device's)
     int dev = -1;
-    TI_HIP(hipGetDevice(&dev));
+    if (stream) TI_HIP(hipStreamGetDevice(static_cast<hipStream_t>(stream), &dev));
+    else TI_HIP(hipGetDevice(&dev));
     TI_REQUIRE(dev >= 0 && dev < NOALLOC_DEVICES, "ti_attn_decode_q8_noalloc: device %d out of range", dev);
     float* base = nullptr;
     const int rc = scratch_address(dev, &base);
