@@ -844,7 +844,7 @@ struct AttnFArgs {
     float* out;
     float* po;
     float* pml;
-    uint32_t* counter;     // [nKv]
+    uint32_t* counter;     // KV head hk's at counter[hk * TI_SYNC_ATTN_STRIDE]
     // the position and its rotary row come from device memory (dev = 1: the decode
     // step's device position) or from these arguments; both pointers are always
     // valid so the kernel loads them unconditionally (no branch, no flat access)
@@ -901,15 +901,17 @@ __device__ __forceinline__ float ub(uint32_t wflip, int k) { return (float)((wfl
 // waves' slots (s_red: unnormalised outputs with the +128 code offset already removed,
 // s_wml: per-wave (m, l)) into this split's partial and publish it; the last split of
 // KV head hk to arrive merges the NS partials by log-sum-exp, writes the head outputs
-// (and their quantQ8 codes) and resets the counter.
+// (and their quantQ8 codes) and resets the counter. s_part: 1024 floats of LDS that the
+// last arriver may use once the publish has read s_red.
 template <int HD, int G, int TPW>
 __device__ __forceinline__ void attn_merge_tail(const AttnFArgs& a, int hk, int w, int NS, int ntiles, bool valid,
                                                 float (&s_red)[4][TPW][G * HD], float (&s_wml)[4][G][2],
                                                 float (&s_ml)[G][ATTF_MAXS][2], float (&s_e)[G][ATTF_MAXS], float* s_L,
-                                                int* s_last_p) {
+                                                int* s_last_p, float* s_part) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int NW = NS * 4;
     int& s_last = *s_last_p;
+    uint32_t* counter = a.counter + (size_t)hk * TI_SYNC_ATTN_STRIDE;
     __syncthreads();
     // merge the 4 waves x TPW slots into this split's partial and publish it
     const size_t ms = (size_t)NS;
@@ -940,22 +942,40 @@ __device__ __forceinline__ void attn_merge_tail(const AttnFArgs& a, int hk, int 
     }
     ti_stores_done();
     __syncthreads();
-    if (tid == 0) s_last = ti_arrive(a.counter + hk) == (unsigned)(NS - 1);
+    if (tid == 0) s_last = ti_arrive(counter) == (unsigned)(NS - 1);
     __syncthreads();
     if (!s_last) return;
-    // the last split of hk: log-sum-exp over the splits that saw a tile; the o loads
-    // are issued before the (m, l) pairs are reduced, one round trip for both
+    // the last split of hk: log-sum-exp over the splits that saw a tile
     const int nused = ntiles < NW ? (ntiles > 0 ? (ntiles + 3) / 4 : 1) : NS;   // >= 1: no index -1
-    // every split's o in one round trip (indices past nused repeat the last one and get
-    // weight 0), then the splits' weights once per head: one wave per head, lane = split
-    float ov[ATTF_MAXS];
-    const int oh = tid / HD, od = tid % HD;
-    const float* pp = a.po + (size_t)(hk * G + (oh < G ? oh : 0)) * ms * HD + od;
+    // Loads in the order they are needed (vmcnt counts in order): every used split's
+    // (m, l) first, one word a thread, then the outputs as 16-byte agent-scope loads —
+    // thread (sg, dg) takes 4 consecutive dims 4 dg of splits sg, sg + SG, ... (an index
+    // past nused repeats the last split and gets weight 0). The splits' weights are formed
+    // while the outputs are still arriving.
+    constexpr int GHD = G * HD, D4 = GHD / 4, SG = 256 / D4, MAXL = ATTF_MAXS / SG;
+    static_assert(SG * GHD == 1024 && SG * MAXL == ATTF_MAXS, "merge layout");
+    const int nml = G * nused * 2;
+    float mlv = 0.0f;
+    if (tid < nml) {
+        const int hh = tid / (nused * 2), r = tid % (nused * 2);
+        mlv = ti_pub_load(a.pml + ((size_t)(hk * G + hh) * ms + (r >> 1)) * 2 + (r & 1));
+    }
+    TI_ISSUE_FENCE();
+    const int dg = tid % D4, sg = tid / D4;
+    const int oh = (4 * dg) / HD, od = (4 * dg) % HD;
+    const __amdgpu_buffer_rsrc_t rpo = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(a.po + (size_t)hk * G * ms * HD), (short)0, (int)(G * ms * HD * 4), 0x00020000);
+    float4 ov[MAXL];
 #pragma unroll
-    for (int i = 0; i < ATTF_MAXS; i++) ov[i] = ti_pub_load(pp + (size_t)(i < nused ? i : nused - 1) * HD);
-    for (int e = tid; e < G * nused * 2; e += 256) {
-        const int hh = e / (nused * 2), r = e % (nused * 2);
-        s_ml[hh][r >> 1][r & 1] = ti_pub_load(a.pml + ((size_t)(hk * G + hh) * ms + (r >> 1)) * 2 + (r & 1));
+    for (int j = 0; j < MAXL; j++) {
+        const int i = sg + SG * j < nused ? sg + SG * j : nused - 1;
+        ov[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                               rpo, (uint32_t)(((size_t)oh * ms + i) * HD + od) * 4u, 0, TI_CPOL_SC1));
+    }
+    TI_ISSUE_FENCE();
+    if (tid < nml) {
+        const int hh = tid / (nused * 2), r = tid % (nused * 2);
+        s_ml[hh][r >> 1][r & 1] = mlv;
     }
     __syncthreads();
     if (wave < G) {
@@ -972,14 +992,27 @@ __device__ __forceinline__ void attn_merge_tail(const AttnFArgs& a, int hk, int 
         if (lane == 0) s_L[wave] = L;
     }
     __syncthreads();
-    if (valid && tid < G * HD) {
-        float o4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    {
+        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
-        for (int i = 0; i < ATTF_MAXS; i++) o4[i & 3] = fmaf(ov[i], s_e[oh][i], o4[i & 3]);
-        const float o = (o4[0] + o4[1]) + (o4[2] + o4[3]);
-        const float L = s_L[oh];
+        for (int j = 0; j < MAXL; j++) {
+            const float e = s_e[oh][sg + SG * j];   // 0 past nused
+            acc.x = fmaf(ov[j].x, e, acc.x);
+            acc.y = fmaf(ov[j].y, e, acc.y);
+            acc.z = fmaf(ov[j].z, e, acc.z);
+            acc.w = fmaf(ov[j].w, e, acc.w);
+        }
+        *reinterpret_cast<float4*>(s_part + sg * GHD + 4 * dg) = acc;
+    }
+    __syncthreads();
+    if (valid && tid < GHD) {
+        const int hh = tid / HD, d = tid % HD;
+        float o = 0.0f;
+#pragma unroll
+        for (int q = 0; q < SG; q++) o += s_part[q * GHD + tid];
+        const float L = s_L[hh];
         const float res = o / L;
-        const size_t e = (size_t)(hk * G + oh) * HD + od;
+        const size_t e = (size_t)(hk * G + hh) * HD + d;
         a.out[e] = res;
         if (a.oq) {   // quantQ8 of 32 consecutive outputs = 32 consecutive lanes (q8_group's arithmetic)
             float mx = fabsf(res);
@@ -996,7 +1029,7 @@ __device__ __forceinline__ void attn_merge_tail(const AttnFArgs& a, int hk, int 
             if ((lane & 31) == 0) a.os[e / 32] = scale;
         }
     }
-    if (tid == 0) __hip_atomic_store(a.counter + hk, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int HD, int G>
@@ -1233,7 +1266,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_fused_q8(AttnFArgs a) {
             s_wml[wave][hh][1] = l_run[hh];
         }
     }
-    attn_merge_tail<HD, G, TPW>(a, hk, w, NS, ntiles, valid, s_red, s_wml, s_ml, s_e, s_L, &s_last);
+    attn_merge_tail<HD, G, TPW>(a, hk, w, NS, ntiles, valid, s_red, s_wml, s_ml, s_e, s_L, &s_last, &s_red[0][0][0]);
 }
 
 // head_dim 128 decode attention with both products on the matrix cores.
@@ -1649,7 +1682,8 @@ __global__ __launch_bounds__(256, 2) void k_attn_fused_pv(AttnFArgs a) {
             s_wml[wave][sh][1] = l32;
         }
     }
-    attn_merge_tail<HD, G, 1>(a, hk, w, NS, ntiles, valid, s_red, s_wml, s_ml, s_e, s_L, &s_last);
+    attn_merge_tail<HD, G, 1>(a, hk, w, NS, ntiles, valid, s_red, s_wml, s_ml, s_e, s_L, &s_last,
+                              reinterpret_cast<float*>(&s_k[2][0][0]));
 }
 }  // namespace
 
@@ -1680,7 +1714,7 @@ int ti_attn_fused_launch(ti_ctx* c, const float* q, const float* k, const float*
                          int nKv, int hd, const int* dpos, int pos, int cap, float theta, float eps, int max_splits,
                          const float* rope_cur, uint32_t* oq, float* os) {
     const int G = nHq / nKv;
-    if (nKv > TI_SYNC_DUMMY - TI_SYNC_ATTN) return ti_fail(TI_ERR_INVALID, "fused attention: too many KV heads");
+    if (nKv > TI_ATTN_COUNTERS) return ti_fail(TI_ERR_INVALID, "fused attention: more than %d KV heads", TI_ATTN_COUNTERS);
     if (hd > TI_ATTN_HD_MAX) return ti_fail(TI_ERR_INVALID, "fused attention: hd=%d > %d", hd, TI_ATTN_HD_MAX);
     if (dpos && !rope_cur) return ti_fail(TI_ERR_INVALID, "fused attention: a device position needs its rope row");
     if (max_splits <= 0 || max_splits > ATTF_MAXS)   // a host position gives the context; a device one only the cache

@@ -52,10 +52,12 @@ struct ti_graph {
 #define TI_AMAX_PARTS 1024
 #define TI_MOE_P_MAX 8192
 #define TI_MOE_E_MAX 256
-#define TI_SYNC_WORDS 1024
+#define TI_SYNC_WORDS (TI_SYNC_ATTN + TI_ATTN_COUNTERS * TI_SYNC_ATTN_STRIDE)
 #define TI_SYNC_LMHEAD 0          // lm_head argmax
 #define TI_SYNC_BONSAI 1          // Bonsai attention merge: the head workgroups' arrivals
-#define TI_SYNC_ATTN 64           // fused attention: one counter per KV head (up to 64)
+#define TI_SYNC_ATTN 1024         // fused attention: one counter per KV head (up to 64), each on its
+#define TI_SYNC_ATTN_STRIDE 64    //   own 256-byte line (atomics on one line serialise at the memory side)
+#define TI_ATTN_COUNTERS 64
 #define TI_SYNC_TGEMM 512         // split-K T-token projections: one counter per 16-row block
 #define TI_TG_SPLIT_BLOCKS 128    // (blocks of one split-K launch, at most)
 #define TI_SYNC_DUMMY 256         // 256 words never written: a valid read target for unused inputs
@@ -163,6 +165,9 @@ __device__ __forceinline__ ti_h8 ti_i8x8_h8(uint32_t lo, uint32_t hi) {
 // otherwise sink a kernel's weight loads below the wait for its activation loads,
 // which serialises two memory round trips that were meant to overlap.
 #define TI_ISSUE_FENCE() __builtin_amdgcn_sched_barrier(0)
+// cache policy of a buffer load/store (gfx950): sc1 = agent scope, as the agent-scope
+// atomic loads and stores of the hand-offs (the access misses the non-coherent caches)
+#define TI_CPOL_SC1 16
 
 // ---- lane exchange as VALU operations ------------------------------------------------
 // ti_xor(v, o): the value held by lane (lane ^ o), o in {1, 2, 4, 8, 16, 32}, without
