@@ -410,9 +410,8 @@ def decode_1p7b(ctx, pool, contexts=(8192, 32768), steps=64, batch8=True, batch1
     kx = ctx.upload(rng.standard_normal(chunk * nkv).astype(np.float16).astype(np.float32))
     vx = ctx.upload(rng.standard_normal(chunk * nkv).astype(np.float16).astype(np.float32))
     for l in range(cfg["layers"]):
-        kq, ks, vq, vs = m.kv(l)
         for p0 in range(0, max(contexts), chunk):
-            ctx.call("ti_kv_write_q8", kx, vx, kq, ks, vq, vs, chunk, cfg["n_kv"], hd, p0)
+            m.kv_write(l, kx, vx, chunk, p0)
     m.write_tokens(0, rng.integers(0, cfg["vocab"], cap + 1).astype(np.int32))
     ctx.sync()
     res = {}

@@ -410,6 +410,16 @@ int ti_qwen3_destroy(ti_ctx* ctx, ti_qwen3* m);
 int ti_qwen3_tensor(ti_qwen3* m, const char* name, void** data, size_t* data_bytes,
                     void** scales, size_t* scale_bytes);
 int ti_qwen3_kv(ti_qwen3* m, int layer, uint32_t** kq, float** ks, uint32_t** vq, float** vs);
+/* The layout of those buffers. Scales: [max_ctx][n_kv_heads][head_dim/32] f32, as the
+ * reference's. Codes: [max_ctx][slots][head_dim] int8, where *slots >= n_kv_heads; the
+ * decoder keeps one spare head slot per position (with 4 or more KV heads), so that a
+ * head's slice does not sit at the same offset of every row (no reference counterpart:
+ * the reference's cache is its own buffer). Head h of position p is slot h. */
+int ti_qwen3_kv_layout(const ti_qwen3* m, int* slots);
+/* kvQuantWrite (models/qwen3.js:2180-2216) into the decoder's own cache of `layer`: rows
+ * [pos, pos+T) from the roped K rows kr and the V rows v ([T][n_kv_heads*head_dim] f32,
+ * 16-byte aligned). */
+int ti_qwen3_kv_write(ti_ctx* ctx, ti_qwen3* m, int layer, const float* kr, const float* v, int T, int pos);
 int ti_qwen3_logits(ti_qwen3* m, float** logits);
 /* forward(ids, pos) at T >= 1 (models/qwen3.js:3938): history[pos..pos+T) = ids, KV
  * written, argmax of the last logits to history[pos+T], device position = pos+T.

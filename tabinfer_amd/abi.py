@@ -91,6 +91,8 @@ SIGS = {
     "ti_qwen3_destroy": [_p, _p],
     "ti_qwen3_tensor": [_p, C.c_char_p, C.POINTER(_p), C.POINTER(_sz), C.POINTER(_p), C.POINTER(_sz)],
     "ti_qwen3_kv": [_p, _i, C.POINTER(_p), C.POINTER(_p), C.POINTER(_p), C.POINTER(_p)],
+    "ti_qwen3_kv_layout": [_p, C.POINTER(_i)],
+    "ti_qwen3_kv_write": [_p, _p, _i, _p, _p, _i, _i],
     "ti_qwen3_logits": [_p, C.POINTER(_p)],
     "ti_qwen3_forward": [_p, _p, _p, _i, _i],
     "ti_qwen3_decode": [_p, _p],
@@ -328,6 +330,16 @@ class Qwen3:
         ptrs = [C.c_void_p() for _ in range(4)]
         check(lib().ti_qwen3_kv(self.h, layer, *[C.byref(p) for p in ptrs]))
         return [p.value for p in ptrs]
+
+    def kv_slots(self):
+        """Code slots per cached position (>= n_kv_heads; the scale rows are n_kv_heads wide)."""
+        n = C.c_int()
+        check(lib().ti_qwen3_kv_layout(self.h, C.byref(n)))
+        return n.value
+
+    def kv_write(self, layer, kr, v, T, pos):
+        """kvQuantWrite of T rows (device f32 [T][n_kv*head_dim] K (roped) and V) at pos."""
+        check(lib().ti_qwen3_kv_write(self.ctx.h, self.h, layer, int(kr), int(v), T, pos))
 
     def logits_ptr(self):
         p = C.c_void_p()

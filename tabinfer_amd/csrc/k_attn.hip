@@ -143,9 +143,12 @@ __global__ __launch_bounds__(128) void k_rope_qk(const float* __restrict__ x, co
 }
 
 // kvQuantWrite: thread = one 32-group; threads [0,nG) quantize K rows, [nG,2nG) V rows.
+// Group gg (flat over positions x heads x groups, rowg groups per position) has its scale
+// at gg and its codes at group slot (gg / rowg) * crowg + gg % rowg (crowg >= rowg: the
+// code rows may carry spare slots).
 __global__ void k_kv_write_q8(const float* __restrict__ kr, const float* __restrict__ vv, uint32_t* __restrict__ kq,
                               float* __restrict__ ks, uint32_t* __restrict__ vq, float* __restrict__ vs, long nG,
-                              long dst_g0) {
+                              long dst_g0, int rowg, int crowg) {
     long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= 2 * nG) return;
     const bool isV = idx >= nG;
@@ -157,7 +160,9 @@ __global__ void k_kv_write_q8(const float* __restrict__ kr, const float* __restr
         float4 t = src[i];
         vals[4 * i] = t.x; vals[4 * i + 1] = t.y; vals[4 * i + 2] = t.z; vals[4 * i + 3] = t.w;
     }
-    snorm_group(vals, (isV ? vq : kq) + (dst_g0 + g) * 8, (isV ? vs : ks) + dst_g0 + g);
+    const long gg = dst_g0 + g;
+    const long cg = (gg / rowg) * crowg + gg % rowg;
+    snorm_group(vals, (isV ? vq : kq) + cg * 8, (isV ? vs : ks) + gg);
 }
 
 // ---------------------------------------------------------------------------
@@ -179,7 +184,8 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split_q8(const float* __re
                                                                const float* __restrict__ ks, const uint4* __restrict__ vq,
                                                                const float* __restrict__ vs, float* __restrict__ po,
                                                                float* __restrict__ pml, int S, int nKv, int nsplit,
-                                                               int per, int ns_stride, const int* __restrict__ dpos) {
+                                                               int per, int ns_stride, const int* __restrict__ dpos,
+                                                               int kvs) {
     constexpr int LPT = HD / 16;              // lanes per token row
     constexpr int TPP = ATT_THREADS / LPT;    // tokens per pass
     constexpr int PASSES = ATT_TILE / TPP;
@@ -207,7 +213,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_split_q8(const float* __re
     const int tp = tid / LPT, sl = tid % LPT;       // token slot in a pass, 16-dim slice
     const int c0 = split * per;
     const int c1 = min(S, c0 + per);
-    const int row_words4 = nKv * HD / 16;           // uint4 per cached position
+    const int row_words4 = kvs * HD / 16;           // uint4 per cached position (codes: kvs slots)
     const int row_groups = nKv * HD / 32;
     const float qk_scale = 1.0f / (127.0f * sqrtf((float)HD));
 
@@ -369,6 +375,7 @@ struct AttnMArgs {
     float* po;
     float* pml;
     int S0, T, nHq, nKv, G, nsplit, per, ns_stride;
+    int kvs;   // K/V code slots per cached position
 };
 
 __global__ __launch_bounds__(256) void k_attn_multi_q8(AttnMArgs a) {
@@ -385,7 +392,7 @@ __global__ __launch_bounds__(256) void k_attn_multi_q8(AttnMArgs a) {
     const int Smax = a.S0 + a.T - 1;
     const int c0 = split * a.per;
     const int c1 = min(Smax, c0 + a.per);
-    const int row_bytes = a.nKv * HD, row_words4 = a.nKv * HD / 16, row_groups = a.nKv * NG;
+    const int row_bytes = a.kvs * HD, row_words4 = a.kvs * HD / 16, row_groups = a.nKv * NG;
     const float qk_scale = 1.0f / (127.0f * sqrtf((float)HD));
     if (tid < AM_ROWS) {
         s_m[tid] = -3.0e38f;
@@ -618,13 +625,13 @@ static int auto_nsplit(int S, int nKv) {
 // before it is read, so nothing in them needs clearing).
 static int split_combine(hipStream_t st, float* po, float* ml, const float* qr, const uint32_t* kq, const float* ks,
                          const uint32_t* vq, const float* vs, float* out, int S, int T, int nHq, int nKv, int hd,
-                         int nsplit, int per, int ns_stride, const int* dpos) {
+                         int nsplit, int per, int ns_stride, const int* dpos, int kvs) {
     const int G = nHq / nKv;
     dim3 grid(nKv * nsplit, T);
     const uint4* k4 = reinterpret_cast<const uint4*>(kq);
     const uint4* v4 = reinterpret_cast<const uint4*>(vq);
 #define ATT(HD_, G_) \
-    if (hd == HD_ && G == G_) { k_attn_split_q8<HD_, G_><<<grid, ATT_THREADS, 0, st>>>(qr, k4, ks, v4, vs, po, ml, S, nKv, nsplit, per, ns_stride, dpos); }
+    if (hd == HD_ && G == G_) { k_attn_split_q8<HD_, G_><<<grid, ATT_THREADS, 0, st>>>(qr, k4, ks, v4, vs, po, ml, S, nKv, nsplit, per, ns_stride, dpos, kvs); }
     ATT(128, 1) else ATT(128, 2) else ATT(128, 4) else ATT(64, 1) else ATT(64, 2) else ATT(32, 2)
     else return ti_fail(TI_ERR_INVALID, "ti_attn_decode_q8: unsupported hd=%d / group=%d", hd, G);
 #undef ATT
@@ -639,7 +646,8 @@ static int split_combine(hipStream_t st, float* po, float* ml, const float* qr, 
 // `cap` positions in splits of `per` keys.
 int ti_attn_decode_launch(ti_ctx* c, const float* qr, const uint32_t* kq, const float* ks, const uint32_t* vq,
                           const float* vs, float* out, int S, int T, int nHq, int nKv, int hd, int nsplit,
-                          const int* dpos, int cap) {
+                          const int* dpos, int cap, int kvs) {
+    if (kvs < nKv) return ti_fail(TI_ERR_INVALID, "attention: %d code slots per position < %d KV heads", kvs, nKv);
     int per, ns_stride;
     if (dpos) {
         per = 128;
@@ -672,7 +680,7 @@ int ti_attn_decode_launch(ti_ctx* c, const float* qr, const uint32_t* kq, const 
             ns2 = (Smax + per2 - 1) / per2;
         }
         AttnMArgs m = {qr, reinterpret_cast<const uint8_t*>(kq), ks, reinterpret_cast<const uint4*>(vq), vs,
-                       c->attn_po, c->attn_ml, S, T, nHq, nKv, G, ns2, per2, ns2};
+                       c->attn_po, c->attn_ml, S, T, nHq, nKv, G, ns2, per2, ns2, kvs};
         dim3 g2(nKv * ns2, (G * T + AM_ROWS - 1) / AM_ROWS);
         k_attn_multi_q8<<<g2, 256, 0, c->stream>>>(m);
         TI_LAUNCHED("k_attn_multi_q8");
@@ -681,7 +689,7 @@ int ti_attn_decode_launch(ti_ctx* c, const float* qr, const uint32_t* kq, const 
         return TI_OK;
     }
     return split_combine(c->stream, c->attn_po, c->attn_ml, qr, kq, ks, vq, vs, out, S, T, nHq, nKv, hd, nsplit, per,
-                         ns_stride, dpos);
+                         ns_stride, dpos, kvs);
 }
 
 extern "C" int ti_attn_decode_q8(ti_ctx* c, const float* qr, const uint32_t* kq, const float* ks, const uint32_t* vq,
@@ -691,7 +699,7 @@ extern "C" int ti_attn_decode_q8(ti_ctx* c, const float* qr, const uint32_t* kq,
     TI_REQUIRE(S > 0 && nKv > 0 && nHq % nKv == 0 && nHq <= TI_ATTN_HEADS_MAX, "ti_attn_decode_q8: bad heads/context (S=%d nHq=%d nKv=%d)", S, nHq, nKv);
     TI_REQUIRE(hd % 32 == 0 && hd <= TI_ATTN_HD_MAX, "ti_attn_decode_q8: hd must be a multiple of 32 and <= %d", TI_ATTN_HD_MAX);
     TI_REQUIRE(al16(kq) && al16(vq), "ti_attn_decode_q8: kq/vq must be 16-byte aligned");
-    return ti_attn_decode_launch(c, qr, kq, ks, vq, vs, out, S, 1, nHq, nKv, hd, nsplit, nullptr, 0);
+    return ti_attn_decode_launch(c, qr, kq, ks, vq, vs, out, S, 1, nHq, nKv, hd, nsplit, nullptr, 0, nKv);
 }
 
 // ---- the same call without a context (nothing allocated) ---------------------------------
@@ -749,7 +757,7 @@ extern "C" int ti_attn_decode_q8_noalloc(void* stream, const float* qr, const ui
     if (rc) return rc;
     const int per = (S + nsplit - 1) / nsplit;
     return split_combine(static_cast<hipStream_t>(stream), base, base + (size_t)NOALLOC_ROWSPLITS * TI_ATTN_HD_MAX, qr, kq,
-                         ks, vq, vs, out, S, 1, nHq, nKv, hd, nsplit, per, nsplit, nullptr);
+                         ks, vq, vs, out, S, 1, nHq, nKv, hd, nsplit, per, nsplit, nullptr, nKv);
 }
 
 extern "C" int ti_attn_causal_q8(ti_ctx* c, const float* qr, const uint32_t* kq, const float* ks, const uint32_t* vq,
@@ -759,7 +767,7 @@ extern "C" int ti_attn_causal_q8(ti_ctx* c, const float* qr, const uint32_t* kq,
     TI_REQUIRE(T > 0 && pos0 >= 0 && nKv > 0 && nHq % nKv == 0, "ti_attn_causal_q8: bad shape (T=%d pos0=%d)", T, pos0);
     TI_REQUIRE(hd % 32 == 0 && hd <= TI_ATTN_HD_MAX, "ti_attn_causal_q8: bad hd=%d", hd);
     TI_REQUIRE(al16(kq) && al16(vq), "ti_attn_causal_q8: kq/vq must be 16-byte aligned");
-    return ti_attn_decode_launch(c, qr, kq, ks, vq, vs, out, pos0 + 1, T, nHq, nKv, hd, 0, nullptr, 0);
+    return ti_attn_decode_launch(c, qr, kq, ks, vq, vs, out, pos0 + 1, T, nHq, nKv, hd, 0, nullptr, 0, nKv);
 }
 
 int ti_attn_prep_launch(ti_ctx* c, const float* q, const float* k, const float* v, const uint16_t* qw,
@@ -792,17 +800,25 @@ extern "C" int ti_rope_qk(ti_ctx* c, const float* x, const uint16_t* w, float* o
     return TI_OK;
 }
 
+// the write into a cache whose code rows hold kvs >= nKv slots per position
+int ti_kv_write_launch(ti_ctx* c, const float* kr, const float* v, uint32_t* kq, float* ks, uint32_t* vq, float* vs,
+                       int T, int nKv, int hd, int pos, int kvs) {
+    TI_REQUIRE(kvs >= nKv, "kv write: %d code slots per position < %d KV heads", kvs, nKv);
+    const long nG = (long)T * nKv * hd / 32;
+    const long g0 = (long)pos * nKv * hd / 32;
+    k_kv_write_q8<<<(unsigned)((2 * nG + 63) / 64), 64, 0, c->stream>>>(kr, v, kq, ks, vq, vs, nG, g0, nKv * hd / 32,
+                                                                        kvs * hd / 32);
+    TI_LAUNCHED("k_kv_write_q8");
+    return TI_OK;
+}
+
 extern "C" int ti_kv_write_q8(ti_ctx* c, const float* kr, const float* v, uint32_t* kq, float* ks, uint32_t* vq,
                               float* vs, int T, int nKv, int hd, int pos) {
     TI_CHECK_CTX(c);
     TI_REQUIRE(kr && v && kq && ks && vq && vs, "ti_kv_write_q8: null buffer");
     TI_REQUIRE(T > 0 && nKv > 0 && hd % 32 == 0 && pos >= 0, "ti_kv_write_q8: bad shape");
     TI_REQUIRE(al16(kr) && al16(v), "ti_kv_write_q8: kr/v must be 16-byte aligned");
-    long nG = (long)T * nKv * hd / 32;
-    long g0 = (long)pos * nKv * hd / 32;
-    k_kv_write_q8<<<(unsigned)((2 * nG + 63) / 64), 64, 0, c->stream>>>(kr, v, kq, ks, vq, vs, nG, g0);
-    TI_LAUNCHED("k_kv_write_q8");
-    return TI_OK;
+    return ti_kv_write_launch(c, kr, v, kq, ks, vq, vs, T, nKv, hd, pos, nKv);
 }
 
 // ---------------------------------------------------------------------------
@@ -853,6 +869,7 @@ struct AttnFArgs {
     int dev;
     int pos;
     int nKv, ns, cap;
+    int kvs;               // K/V code slots per cached position (>= nKv; the scale rows stay nKv wide)
     float eps;
     uint32_t* oq;          // optional: the output quantized per 32 (quantQ8, for o_proj's linearQ)
     float* os;
@@ -1067,7 +1084,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_fused_q8(AttnFArgs a) {
     const int gw = w * 4 + wave;               // this wave's index among them
     const int h = tid >> 7, j = tid & 127;
     const int tp = lane / LPT, sl = lane % LPT;
-    const int row_words4 = a.nKv * HD / 16;
+    const int row_words4 = a.kvs * HD / 16;
     const int row_groups = a.nKv * NG;
     const float qk_scale = 1.0f / (127.0f * sqrtf((float)HD));
     const uint4* kq4 = reinterpret_cast<const uint4*>(a.kq);
@@ -1128,7 +1145,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_fused_q8(AttnFArgs a) {
         const uint32_t code = snorm_code(val, mx);
         const uint32_t word = ti_quad_or(code << (8 * (lane & 3)));
         if (j < HD) {
-            const size_t rowq = ((size_t)pos * a.nKv + hk) * (HD / 4), rows = ((size_t)pos * a.nKv + hk) * NG;
+            const size_t rowq = ((size_t)pos * a.kvs + hk) * (HD / 4), rows = ((size_t)pos * a.nKv + hk) * NG;
             if ((j & 3) == 0) {
                 (h ? a.vq : a.kq)[rowq + j / 4] = word;
                 (h ? s_vw : s_kw)[j / 4] = word;
@@ -1359,7 +1376,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_fused_pv(AttnFArgs a) {
     const int r16 = lane & 15, kq = lane >> 4;    // MFMA lanes: row / column, K quarter
     const int sh = kq & 1;                        // head of this lane's scores and P V rows
     const int key_t = 16 * (lane >> 5) + r16;     // key (in the tile) of this lane's score
-    const uint32_t rowb = (uint32_t)a.nKv * HD;   // cache bytes per position (codes)
+    const uint32_t rowb = (uint32_t)a.kvs * HD;   // cache bytes per position (codes)
     const uint32_t rows16 = (uint32_t)a.nKv * 16; // bytes per position (the 4 group scales)
     const float l2s = 1.4426950408889634f / (127.0f * sqrtf((float)HD));
 
@@ -1384,13 +1401,13 @@ __global__ __launch_bounds__(256, 2) void k_attn_fused_pv(AttnFArgs a) {
     auto tile_rs = [&](int t0, int lim, __amdgpu_buffer_rsrc_t& rk, __amdgpu_buffer_rsrc_t& rv,
                        __amdgpu_buffer_rsrc_t& rks, __amdgpu_buffer_rsrc_t& rvs) {
         const int n = lim - t0;
-        const size_t row0 = (size_t)t0 * a.nKv + hk;
+        const size_t crow0 = (size_t)t0 * a.kvs + hk, srow0 = (size_t)t0 * a.nKv + hk;
         const int cb = n > 0 ? (int)((uint32_t)(n - 1) * rowb + HD) : 0;
         const int sb = n > 0 ? (int)((uint32_t)(n - 1) * rows16 + 16) : 0;
-        rk = pv_rsrc(kq_b + row0 * HD, cb);
-        rv = pv_rsrc(vq_b + row0 * HD, cb);
-        rks = pv_rsrc(ks_b + row0 * 16, sb);
-        rvs = pv_rsrc(vs_b + row0 * 16, sb);
+        rk = pv_rsrc(kq_b + crow0 * HD, cb);
+        rv = pv_rsrc(vq_b + crow0 * HD, cb);
+        rks = pv_rsrc(ks_b + srow0 * 16, sb);
+        rvs = pv_rsrc(vs_b + srow0 * 16, sb);
     };
 
     // ---- every load that does not depend on the position, in one batch. Wave 0 (and 1
@@ -1656,7 +1673,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_fused_pv(AttnFArgs a) {
     }
     if (has_pos && wave >= 2) {   // the new K / V row into the cache, from LDS
         const bool isv = wave == 3;
-        const size_t rowq = ((size_t)pos * a.nKv + hk) * (HD / 4), rows = ((size_t)pos * a.nKv + hk) * NG;
+        const size_t rowq = ((size_t)pos * a.kvs + hk) * (HD / 4), rows = ((size_t)pos * a.nKv + hk) * NG;
         if (lane < HD / 4) (isv ? a.vq : a.kq)[rowq + lane] = (isv ? s_vw : s_kw)[lane];
         if (lane < NG) (isv ? a.vs : a.ks)[rows + lane] = (isv ? s_vsc : s_ksc)[lane];
     }
@@ -1712,8 +1729,9 @@ int ti_attn_decode_splits(int S) {
 int ti_attn_fused_launch(ti_ctx* c, const float* q, const float* k, const float* v, const uint16_t* qw,
                          const uint16_t* kw, uint32_t* kq, float* ks, uint32_t* vq, float* vs, float* out, int nHq,
                          int nKv, int hd, const int* dpos, int pos, int cap, float theta, float eps, int max_splits,
-                         const float* rope_cur, uint32_t* oq, float* os) {
+                         const float* rope_cur, uint32_t* oq, float* os, int kvs) {
     const int G = nHq / nKv;
+    if (kvs < nKv) return ti_fail(TI_ERR_INVALID, "fused attention: %d code slots per position < %d KV heads", kvs, nKv);
     if (nKv > TI_ATTN_COUNTERS) return ti_fail(TI_ERR_INVALID, "fused attention: more than %d KV heads", TI_ATTN_COUNTERS);
     if (hd > TI_ATTN_HD_MAX) return ti_fail(TI_ERR_INVALID, "fused attention: hd=%d > %d", hd, TI_ATTN_HD_MAX);
     if (dpos && !rope_cur) return ti_fail(TI_ERR_INVALID, "fused attention: a device position needs its rope row");
@@ -1727,7 +1745,7 @@ int ti_attn_fused_launch(ti_ctx* c, const float* q, const float* k, const float*
     const int* dp = dpos ? dpos : reinterpret_cast<const int*>(c->sync + TI_SYNC_DUMMY);
     const float* rc = rope_cur ? rope_cur : reinterpret_cast<const float*>(c->sync + TI_SYNC_DUMMY);
     AttnFArgs a = {q, k, v, qw, kw, kq, ks, vq, vs, out, c->attn_po, c->attn_ml, c->sync + TI_SYNC_ATTN, dp, rc,
-                   dpos ? 1 : 0, pos, nKv, max_splits, cap, eps, oq, os, {}};
+                   dpos ? 1 : 0, pos, nKv, max_splits, cap, kvs, eps, oq, os, {}};
     if (!dpos) ti_rope_row(a.rope_row, pos, hd, theta);
     dim3 grid(nKv * max_splits);
 #define AF(HD_, G_) \
@@ -1752,5 +1770,5 @@ extern "C" int ti_attn_step_q8(ti_ctx* c, const float* q, const float* k, const 
     TI_REQUIRE(max_splits >= 0 && max_splits <= ATTF_MAXS, "ti_attn_step_q8: max_splits in [0, %d]", ATTF_MAXS);
     TI_REQUIRE((out_q == nullptr) == (out_s == nullptr), "ti_attn_step_q8: out_q and out_s go together");
     return ti_attn_fused_launch(c, q, k, v, qn_w, kn_w, kq, ks, vq, vs, out, nHq, nKv, hd, nullptr, pos, cap, theta, eps,
-                                max_splits, nullptr, out_q, out_s);
+                                max_splits, nullptr, out_q, out_s, nKv);
 }

@@ -55,7 +55,7 @@ struct TAttnArgs {
     const uint16_t* qw;    // q_norm / k_norm weights (f16)
     const uint16_t* kw;
     const float* rope;     // [cap][HD]: cos(pos*theta^(-2i/HD)) at i, sin at HD/2 + i
-    uint8_t* kq;           // cache: [pos][nKv][HD] codes, [pos][nKv][NG] scales
+    uint8_t* kq;           // cache: [pos][kvs][HD] codes (kvs >= nKv slots), [pos][nKv][NG] scales
     float* ks;
     uint8_t* vq;
     float* vs;
@@ -64,6 +64,7 @@ struct TAttnArgs {
     int S0, T, nKv, G, NS;
     float eps;
     int RT;                // row tiles: workgroups (hk, rt, split) serve rows 16 rt .. 16 rt + 15
+    int kvs;               // code slots per cached position
 };
 
 // RMSNorm in the reference's order for a head row held as (element L, element L+64) by
@@ -123,7 +124,7 @@ __global__ __launch_bounds__(64 * TA_W) void k_attn_tq8(TAttnArgs a) {
         for (int p = 0; p < 4; p++) {
             int key = k0 + (lane >> 3) + 8 * p;
             key = key < S0 ? key : (S0 > 0 ? S0 - 1 : 0);
-            const size_t off = ((size_t)key * a.nKv + hk) * HD + 16 * (lane & 7);
+            const size_t off = ((size_t)key * a.kvs + hk) * HD + 16 * (lane & 7);
             kr[p] = ti_ld_nt(reinterpret_cast<const uint4*>(a.kq + off));
             vr[p] = ti_ld_nt(reinterpret_cast<const uint4*>(a.vq + off));
         }
@@ -204,8 +205,8 @@ __global__ __launch_bounds__(64 * TA_W) void k_attn_tq8(TAttnArgs a) {
                 const float mx1 = fmaxf(ti_max32_nonneg(fabsf(o1)), 1e-12f);
                 const uint32_t wd0 = ti_quad_or(snorm_code(o0, mx0) << (8 * (lane & 3)));
                 const uint32_t wd1 = ti_quad_or(snorm_code(o1, mx1) << (8 * (lane & 3)));
-                const size_t row = (size_t)(S0 + t) * a.nKv + hk;
-                uint32_t* gq = reinterpret_cast<uint32_t*>((isv ? a.vq : a.kq) + row * HD);
+                const size_t row = (size_t)(S0 + t) * a.nKv + hk, crow = (size_t)(S0 + t) * a.kvs + hk;
+                uint32_t* gq = reinterpret_cast<uint32_t*>((isv ? a.vq : a.kq) + crow * HD);
                 float* gs = (isv ? a.vs : a.ks) + row * NG;
                 uint8_t* lt = (isv ? vt + t * TA_VS : kt + t * TA_KS);
                 float* lsc = isv ? &s_vs[TA_W][t][0] : &s_ks[TA_W][t][0];
@@ -484,7 +485,8 @@ bool ti_tattn_ok(int T, int nHq, int nKv, int hd) {
 // into the cache and the output's quantQ8T codes/scales (oq [T][nHq*HD/4], os [T][nHq*HD/32]).
 int ti_tattn_launch(ti_ctx* c, const float* q, const float* k, const float* v, const uint16_t* qw, const uint16_t* kw,
                     const float* rope, uint32_t* kq, float* ks, uint32_t* vq, float* vs, int S0, int T, int nHq, int nKv,
-                    int hd, float eps, uint32_t* oq, float* os) {
+                    int hd, float eps, uint32_t* oq, float* os, int kvs) {
+    if (kvs < nKv) return ti_fail(TI_ERR_INVALID, "T-token attention: %d code slots per position < %d KV heads", kvs, nKv);
     if (!ti_tattn_ok(T, nHq, nKv, hd)) return ti_fail(TI_ERR_INVALID, "T-token attention: unsupported T=%d heads %d/%d hd=%d", T, nHq, nKv, hd);
     const int nb = (S0 + TA_BLK - 1) / TA_BLK;
     // about 2048 waves (8 per CU) over the KV heads and row tiles, at most TA_MAXS
@@ -497,7 +499,7 @@ int ti_tattn_launch(ti_ctx* c, const float* q, const float* k, const float* v, c
     if (NS > TA_MAXS) NS = TA_MAXS;
     if (NS < 1) NS = 1;
     TAttnArgs a = {q, k, v, qw, kw, rope, reinterpret_cast<uint8_t*>(kq), ks, reinterpret_cast<uint8_t*>(vq), vs,
-                   c->attn_po, c->attn_ml, S0, T, nKv, nHq / nKv, NS, eps, RT};
+                   c->attn_po, c->attn_ml, S0, T, nKv, nHq / nKv, NS, eps, RT, kvs};
     k_attn_tq8<<<nKv * RT * NS, 64 * TA_W, 0, c->stream>>>(a);
     TI_LAUNCHED("k_attn_tq8");
     TCombArgs cb = {c->attn_po, c->attn_ml, oq, os, NS, nKv, nHq / nKv, R, RT};

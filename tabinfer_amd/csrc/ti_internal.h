@@ -123,7 +123,7 @@ int ti_tgemm_gateup_launch(ti_ctx* c, const TgIn& in, const uint32_t* gpack, con
 bool ti_tattn_ok(int T, int nHq, int nKv, int hd);
 int ti_tattn_launch(ti_ctx* c, const float* q, const float* k, const float* v, const uint16_t* qw, const uint16_t* kw,
                     const float* rope, uint32_t* kq, float* ks, uint32_t* vq, float* vs, int S0, int T, int nHq, int nKv,
-                    int hd, float eps, uint32_t* oq, float* os);
+                    int hd, float eps, uint32_t* oq, float* os, int kvs);
 
 // ---- device helpers -----------------------------------------------------------
 // f16 bits -> f32 (exact).

@@ -21,11 +21,12 @@ int ti_quant_act_q8_async(ti_ctx*, const float*, uint32_t*, float*, int32_t*, in
 int ti_attn_prep_launch(ti_ctx*, const float*, const float*, const float*, const uint16_t*, const uint16_t*, float*,
                         uint32_t*, float*, uint32_t*, float*, int, int, int, int, float, float, const int*);
 int ti_attn_decode_launch(ti_ctx*, const float*, const uint32_t*, const float*, const uint32_t*, const float*, float*,
-                          int, int, int, int, int, int, const int*, int);
+                          int, int, int, int, int, int, const int*, int, int);
+int ti_kv_write_launch(ti_ctx*, const float*, const float*, uint32_t*, float*, uint32_t*, float*, int, int, int, int, int);
 int ti_attn_decode_splits(int S);
 int ti_attn_fused_launch(ti_ctx*, const float*, const float*, const float*, const uint16_t*, const uint16_t*, uint32_t*,
                          float*, uint32_t*, float*, float*, int, int, int, const int*, int, int, float, float, int,
-                         const float*, uint32_t*, float*);
+                         const float*, uint32_t*, float*, int);
 void ti_rope_row(float* cs, int pos, int hd, float theta);
 int ti_fused_qkv_launch(ti_ctx*, const float*, const uint16_t*, float, int, int, const uint32_t* const*,
                         const uint16_t* const*, float* const*, const int*, uint32_t*, float*);
@@ -156,8 +157,19 @@ struct ti_qwen3 {
     uint32_t* amx_i;
     uint32_t* trace = nullptr;   // caller's trace buffer (ti_qwen3_trace), or null
     int pos_hint = 0;            // the position last set from the host (set_pos, or a forward's end)
+    int kvs = 0;                 // K/V code slots per cached position (ti_qwen3_kv_layout)
     std::vector<void*> allocs;
 };
+
+// The decoder's K/V code rows carry one spare head slot per position when there are 4 or
+// more KV heads: a head's 128-byte slice then moves to the next slot of the row from one
+// position to the next, instead of sitting at the same offset of every (power-of-two)
+// row. Measured on the decode attention: at a 1 KB row the workgroups of the heads whose
+// slices lie at offsets 384 and 896 stream their keys ~10% slower than the others (the
+// slowness moves with the offset when the cache base is shifted), and a layer waits for
+// its slowest head; with the spare slot every head sees every offset. The scale rows
+// (128 B per position for 8 heads) are left dense.
+static int kv_slots(const ti_qwen3_config& C) { return C.n_kv_heads >= 4 ? C.n_kv_heads + 1 : C.n_kv_heads; }
 
 // ---- the parity trace (ti_qwen3_trace) -------------------------------------------------
 // Per layer, fields of max_tokens rows each, in this order (32-bit words per row):
@@ -253,7 +265,9 @@ extern "C" int ti_qwen3_create(ti_ctx* c, const ti_qwen3_config* cfg, ti_qwen3**
     };
     int rc = 0;
     m->L.resize(C.layers);
-    const size_t kvw = (size_t)C.max_ctx * nkv;   // int8 elements per layer per K or V
+    m->kvs = kv_slots(C);
+    const size_t kvw = (size_t)C.max_ctx * nkv;   // int8 elements per layer per K or V (scales: kvw / 32)
+    const size_t kvc = (size_t)C.max_ctx * m->kvs * hd;   // code bytes per layer per K or V (padded rows)
     for (int l = 0; l < C.layers && !rc; l++) {
         Layer& y = m->L[l];
         rc = lin(y.q, nq, H); if (!rc) rc = lin(y.k, nkv, H); if (!rc) rc = lin(y.v, nkv, H);
@@ -263,8 +277,8 @@ extern "C" int ti_qwen3_create(ti_ctx* c, const ti_qwen3_config* cfg, ti_qwen3**
         if (!rc) rc = mk(m, (void**)&y.post_norm, H * 2);
         if (!rc) rc = mk(m, (void**)&y.q_norm, hd * 2);
         if (!rc) rc = mk(m, (void**)&y.k_norm, hd * 2);
-        if (!rc) rc = mk(m, (void**)&y.kq, kvw);
-        if (!rc) rc = mk(m, (void**)&y.vq, kvw);
+        if (!rc) rc = mk(m, (void**)&y.kq, kvc);
+        if (!rc) rc = mk(m, (void**)&y.vq, kvc);
         if (!rc) rc = mk(m, (void**)&y.ks, kvw / 32 * 4);
         if (!rc) rc = mk(m, (void**)&y.vs, kvw / 32 * 4);
     }
@@ -368,6 +382,22 @@ extern "C" int ti_qwen3_kv(ti_qwen3* m, int layer, uint32_t** kq, float** ks, ui
     *vq = m->L[layer].vq;
     *vs = m->L[layer].vs;
     return TI_OK;
+}
+
+extern "C" int ti_qwen3_kv_layout(const ti_qwen3* m, int* slots) {
+    TI_REQUIRE(m && slots, "ti_qwen3_kv_layout: null argument");
+    *slots = m->kvs;
+    return TI_OK;
+}
+
+extern "C" int ti_qwen3_kv_write(ti_ctx* c, ti_qwen3* m, int layer, const float* kr, const float* v, int T, int pos) {
+    TI_CHECK_CTX(c);
+    TI_REQUIRE(m && layer >= 0 && layer < m->cfg.layers && kr && v, "ti_qwen3_kv_write: bad argument");
+    TI_REQUIRE(T > 0 && pos >= 0 && pos + T <= m->cfg.max_ctx, "ti_qwen3_kv_write: rows [%d, %d) outside the cache (%d)", pos,
+               pos + T, m->cfg.max_ctx);
+    TI_REQUIRE(((uintptr_t)kr & 15u) == 0 && ((uintptr_t)v & 15u) == 0, "ti_qwen3_kv_write: kr/v must be 16-byte aligned");
+    const Layer& y = m->L[layer];
+    return ti_kv_write_launch(c, kr, v, y.kq, y.ks, y.vq, y.vs, T, m->cfg.n_kv_heads, m->cfg.head_dim, pos, m->kvs);
 }
 
 extern "C" int ti_qwen3_logits(ti_qwen3* m, float** logits) {
@@ -546,7 +576,7 @@ extern "C" int ti_qwen3_decode(ti_ctx* c, ti_qwen3* m) {
         RC(trace_put(c, m, l, TR_V, m->v, 1));
         RC(ti_attn_fused_launch(c, m->q, m->k, m->v, y.q_norm, y.k_norm, y.kq, y.ks, y.vq, y.vs, m->attn, nHq, nKv, hd,
                                 m->dpos, 0, C.max_ctx, C.rope_theta, C.rms_eps, decode_splits(m, m->pos_hint), m->rope_cur,
-                                m->xq, m->xs));
+                                m->xq, m->xs, m->kvs));
         RC(trace_put(c, m, l, TR_ATTN, m->attn, 1));
         RC(trace_put(c, m, l, TR_A_Q, m->xq, 1));
         RC(trace_put(c, m, l, TR_A_S, m->xs, 1));
@@ -622,12 +652,13 @@ extern "C" int ti_qwen3_forward(ti_ctx* c, ti_qwen3* m, const int32_t* ids, int 
         }
         if (fused && fused_attn) {
             RC(ti_tattn_launch(c, m->q, m->k, m->v, y.q_norm, y.k_norm, m->rope, y.kq, y.ks, y.vq, y.vs, pos, T, nHq, nKv,
-                               hd, C.rms_eps, m->xq, m->xs));
+                               hd, C.rms_eps, m->xq, m->xs, m->kvs));
         } else {
             RC(ti_rope_qk(c, m->q, y.q_norm, m->qr, T, nHq, hd, pos, C.rope_theta, C.rms_eps));
             RC(ti_rope_qk(c, m->k, y.k_norm, m->kr, T, nKv, hd, pos, C.rope_theta, C.rms_eps));
-            RC(ti_kv_write_q8(c, m->kr, m->v, y.kq, y.ks, y.vq, y.vs, T, nKv, hd, pos));
-            RC(ti_attn_decode_launch(c, m->qr, y.kq, y.ks, y.vq, y.vs, m->attn, pos + 1, T, nHq, nKv, hd, 0, nullptr, 0));
+            RC(ti_kv_write_launch(c, m->kr, m->v, y.kq, y.ks, y.vq, y.vs, T, nKv, hd, pos, m->kvs));
+            RC(ti_attn_decode_launch(c, m->qr, y.kq, y.ks, y.vq, y.vs, m->attn, pos + 1, T, nHq, nKv, hd, 0, nullptr, 0,
+                                     m->kvs));
         }
         RC(trace_put(c, m, l, TR_Q, m->q, T));
         RC(trace_put(c, m, l, TR_K, m->k, T));

@@ -935,16 +935,49 @@ napi_value js_qwen3_kv(napi_env env, napi_callback_info info) {
     if (!m || !get_i64(env, a.v[1], &layer, "qwen3_kv", 1)) return nullptr;
     uint32_t *kq, *vq;
     float *ks, *vs;
-    const int rc = ti_qwen3_kv(m->m, (int)layer, &kq, &ks, &vq, &vs);
+    int rc = ti_qwen3_kv(m->m, (int)layer, &kq, &ks, &vq, &vs);
+    int slots = 0;
+    if (!rc) rc = ti_qwen3_kv_layout(m->m, &slots);
     if (rc) return throw_ti(env, "qwen3_kv", rc);
     napi_value o;
     napi_create_object(env, &o);
-    const size_t codes = (size_t)m->cfg.max_ctx * m->cfg.n_kv_heads * m->cfg.head_dim;   // int8 per K or V
+    const size_t scales = (size_t)m->cfg.max_ctx * m->cfg.n_kv_heads * (m->cfg.head_dim / 32) * 4;
+    const size_t codes = (size_t)m->cfg.max_ctx * slots * m->cfg.head_dim;   // int8 per K or V (padded rows)
     napi_set_named_property(env, o, "kq", make_buf(env, m->ctx, kq, codes, false, a.v[0]));
-    napi_set_named_property(env, o, "ks", make_buf(env, m->ctx, ks, codes / 32 * 4, false, a.v[0]));
+    napi_set_named_property(env, o, "ks", make_buf(env, m->ctx, ks, scales, false, a.v[0]));
     napi_set_named_property(env, o, "vq", make_buf(env, m->ctx, vq, codes, false, a.v[0]));
-    napi_set_named_property(env, o, "vs", make_buf(env, m->ctx, vs, codes / 32 * 4, false, a.v[0]));
+    napi_set_named_property(env, o, "vs", make_buf(env, m->ctx, vs, scales, false, a.v[0]));
+    napi_set_named_property(env, o, "slots", num(env, slots));
     return o;
+}
+
+// qwen3_kv_layout(model) -> code slots per cached position
+napi_value js_qwen3_kv_layout(napi_env env, napi_callback_info info) {
+    const char* fn = "qwen3_kv_layout";
+    Args a(env, info);
+    if (!want_args(env, a, 1, fn)) return nullptr;
+    ModelH* m = get_model(env, a.v[0], fn, 0);
+    if (!m) return nullptr;
+    int slots = 0;
+    const int rc = ti_qwen3_kv_layout(m->m, &slots);
+    return rc ? throw_ti(env, fn, rc) : num(env, slots);
+}
+
+// qwen3_kv_write(ctx, model, layer, kr, v, T, pos): kvQuantWrite into the model's cache
+napi_value js_qwen3_kv_write(napi_env env, napi_callback_info info) {
+    const char* fn = "qwen3_kv_write";
+    Args a(env, info);
+    if (!want_args(env, a, 7, fn)) return nullptr;
+    CtxH* c = get_ctx(env, a.v[0], fn);
+    ModelH* m = c ? get_model(env, a.v[1], fn, 1) : nullptr;
+    int64_t layer, T, pos;
+    void *kr, *v;
+    if (!m || !get_i64(env, a.v[2], &layer, fn, 2) || !get_dptr(env, a.v[3], &kr, fn, 3) ||
+        !get_dptr(env, a.v[4], &v, fn, 4) || !get_i64(env, a.v[5], &T, fn, 5) || !get_i64(env, a.v[6], &pos, fn, 6))
+        return nullptr;
+    const int rc = ti_qwen3_kv_write(c->c, m->m, (int)layer, static_cast<const float*>(kr), static_cast<const float*>(v),
+                                     (int)T, (int)pos);
+    return rc ? throw_ti(env, fn, rc) : undefined(env);
 }
 
 napi_value js_qwen3_logits(napi_env env, napi_callback_info info) {
@@ -1551,6 +1584,8 @@ napi_value module_init(napi_env env, napi_value exports) {
         FN("qwen3_destroy", js_qwen3_destroy),
         FN("qwen3_tensor", js_qwen3_tensor),
         FN("qwen3_kv", js_qwen3_kv),
+        FN("qwen3_kv_layout", js_qwen3_kv_layout),
+        FN("qwen3_kv_write", js_qwen3_kv_write),
         FN("qwen3_logits", js_qwen3_logits),
         FN("qwen3_forward", js_qwen3_forward),
         FN("qwen3_decode", js_qwen3_decode),

@@ -80,6 +80,23 @@ def load_into(ctx, model, W, H):
             ctx.write(dp, val)
 
 
+def write_kv_codes(ctx, model, dst, codes, P, cfg):
+    """Dense int8 code rows [P][nkv] (as uint32 words) into the decoder's code buffer, whose
+    rows carry model.kv_slots() head slots (the spare slots stay zero)."""
+    nkv, hd = dims(cfg)["nkv"], cfg["head_dim"]
+    slots = model.kv_slots()
+    rows = np.zeros((P, slots * hd // 4), np.uint32)
+    rows[:, :nkv // 4] = np.asarray(codes, np.uint32).reshape(P, nkv // 4)
+    ctx.write(dst, rows)
+
+
+def read_kv_codes(ctx, model, src, P, T, cfg):
+    """Code rows [P, P+T) of the decoder's code buffer as dense uint32 words [T][nkv/4]."""
+    nkv, hd = dims(cfg)["nkv"], cfg["head_dim"]
+    row_w = model.kv_slots() * hd // 4
+    return ctx.download(src, np.uint32, T * row_w, off=P * row_w * 4).reshape(T, row_w)[:, :nkv // 4].copy()
+
+
 def seed_prefix(ctx, model, cfg, P, cap, seed):
     """Seeded prefix KV of P positions in every layer, written to the model; returns the
     host copies with room for cap positions: [(kq, ks, vq, vs)] per layer."""
@@ -96,8 +113,11 @@ def seed_prefix(ctx, model, cfg, P, cap, seed):
             s[:P * nkv // 32] = rng.uniform(1.0, 3.0, P * nkv // 32).astype(np.float32)
             arrs += [q.view(np.uint32), s]
         dk = model.kv(l)
-        for dst, src, n in zip(dk, arrs, (P * nkv // 4, P * nkv // 32) * 2):
-            ctx.write(dst, src[:n])
+        for i, (dst, src, n) in enumerate(zip(dk, arrs, (P * nkv // 4, P * nkv // 32) * 2)):
+            if i % 2 == 0:
+                write_kv_codes(ctx, model, dst, src[:n], P, cfg)
+            else:
+                ctx.write(dst, src[:n])
         host.append(arrs)
     return host
 
@@ -246,9 +266,9 @@ def new_kv_rows(ctx, model, cfg, P, T):
     rows = []
     for l in range(cfg["layers"]):
         kq, ks, vq, vs = model.kv(l)
-        rows.append((ctx.download(kq, np.uint32, T * nkv // 4, off=P * nkv).reshape(T, -1),
+        rows.append((read_kv_codes(ctx, model, kq, P, T, cfg),
                      ctx.download(ks, np.float32, T * nkv // 32, off=P * nkv // 8).reshape(T, -1),
-                     ctx.download(vq, np.uint32, T * nkv // 4, off=P * nkv).reshape(T, -1),
+                     read_kv_codes(ctx, model, vq, P, T, cfg),
                      ctx.download(vs, np.float32, T * nkv // 32, off=P * nkv // 8).reshape(T, -1)))
     return rows
 

@@ -70,8 +70,7 @@ def test_prefill_then_chained_decode(ctx):
                 assert tok == rt
         # KV rows written by the GPU match the reference's within one int8 step
         kq, ks, vq, vs = m.kv(1)
-        nkv = SMALL["n_kv_heads"] * SMALL["head_dim"]
-        gk = ctx.download(kq, np.uint32, 9 * nkv // 4).view(np.int8).astype(int).reshape(9, -1)
+        gk = TF.read_kv_codes(ctx, m, kq, 0, 9, SMALL).view(np.int8).astype(int).reshape(9, -1)
         rk = ref.kv[1][0][:9].view(np.int8).astype(int).reshape(9, -1)
         assert np.max(np.abs(gk - rk)) <= 1
         assert np.mean(gk != rk) < 0.01
@@ -113,7 +112,7 @@ def test_prefill_in_256_token_chunks(ctx):
         nkv = cfg["n_kv_heads"] * cfg["head_dim"]
         for layer, frac in ((0, 0.005), (1, 0.02)):
             kq, ks, vq, vs = m.kv(layer)
-            gk = ctx.download(kq, np.uint32, 300 * nkv // 4).view(np.int8).astype(int).reshape(300, -1)
+            gk = TF.read_kv_codes(ctx, m, kq, 0, 300, cfg).view(np.int8).astype(int).reshape(300, -1)
             rk = ref.kv[layer][0][:300].view(np.int8).astype(int).reshape(300, -1)
             print("[qwen3] 256-token chunks: layer %d K codes differing %.4f" % (layer, np.mean(gk != rk)), flush=True)
             assert np.max(np.abs(gk - rk)) <= 1
@@ -187,9 +186,8 @@ def test_decode_splits_follow_the_context(ctx):
         kx = ctx.upload(rng.standard_normal(chunk * nkv).astype(np.float32))
         vx = ctx.upload(rng.standard_normal(chunk * nkv).astype(np.float32))
         for l in range(cfg["layers"]):
-            kq, ks, vq, vs = m.kv(l)
             for p0 in range(0, P, chunk):
-                ctx.call("ti_kv_write_q8", kx, vx, kq, ks, vq, vs, chunk, cfg["n_kv_heads"], cfg["head_dim"], p0)
+                m.kv_write(l, kx, vx, chunk, p0)
         m.write_tokens(0, rng.integers(0, cfg["vocab"], P + 2).astype(np.int32))
         m.set_pos(P)
         m.decode()                                  # eager at the long context: 24 splits
@@ -225,8 +223,10 @@ def _seed_prefix(ctx, orc, m, ref, cfg, P, seed):
         kq, ks = orc.kv_quant(K)
         vq, vs = orc.kv_quant(V)
         dk = m.kv(l)
-        for dst, src in zip(dk, (kq, ks, vq, vs)):
-            ctx.write(dst, src)
+        TF.write_kv_codes(ctx, m, dk[0], kq, P, cfg)
+        ctx.write(dk[1], ks)
+        TF.write_kv_codes(ctx, m, dk[2], vq, P, cfg)
+        ctx.write(dk[3], vs)
         ref.kv[l][0][:P], ref.kv[l][1][:P] = kq.reshape(P, -1), ks.reshape(P, -1)
         ref.kv[l][2][:P], ref.kv[l][3][:P] = vq.reshape(P, -1), vs.reshape(P, -1)
 
@@ -380,7 +380,7 @@ def test_batched_forward_graph_replays(ctx, T):
         l0 = _logits(ctx, m, cfg["vocab"]).copy()
         nkv = cfg["n_kv_heads"] * cfg["head_dim"]
         kq = m.kv(0)[0]
-        k0 = ctx.download(kq, np.uint32, (P + T) * nkv // 4).copy()
+        k0 = TF.read_kv_codes(ctx, m, kq, 0, P + T, cfg)
         ctx.graph_begin()
         m.forward(None, P, T=T)
         g = ctx.graph_end()
@@ -389,7 +389,7 @@ def test_batched_forward_graph_replays(ctx, T):
                 ctx.graph_launch(g)
                 ctx.sync()
                 assert np.array_equal(_logits(ctx, m, cfg["vocab"]), l0), rep
-                assert np.array_equal(ctx.download(kq, np.uint32, (P + T) * nkv // 4), k0), rep
+                assert np.array_equal(TF.read_kv_codes(ctx, m, kq, 0, P + T, cfg), k0), rep
                 ctx.download(m.logits_ptr(), np.float32, 16)      # eager work between replays
         finally:
             ctx.graph_destroy(g)
