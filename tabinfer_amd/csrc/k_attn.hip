@@ -1326,6 +1326,40 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t pv_rsrc(const void* base, int 
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes > 0 ? bytes : 0, 0x00020000);
 }
 
+// The LDS reads of a tile's P V step, issued as one block that ends with its own wait:
+// the P' words other lanes of the wave wrote just before (a wave's LDS instructions
+// execute in order; the block is a compiler memory barrier, so the writes stay above it)
+// and the 8 transposing reads of the V tile (ds_read_b64_tr_b8). Written by hand because
+// the compiler puts a wait for every direct-to-LDS load in flight before such reads (it
+// cannot tell that those loads fill the other tile buffer), which would hold each tile's
+// P V products until the next tile had arrived. This tile's loads were waited for at the
+// top of its iteration.
+__device__ __forceinline__ void pv_read_pv(const uint8_t* pa, const uint8_t* vt, const uint32_t (&voff8)[8], uint4& wa,
+                                           uint4& wb, pv_v2i (&vb)[8]) {
+    typedef __attribute__((address_space(3))) const uint8_t* lds_p;
+    const uint32_t pw = (uint32_t)reinterpret_cast<uintptr_t>((lds_p)pa);
+    uint32_t ad[8];
+#pragma unroll
+    for (int D = 0; D < 8; D++) ad[D] = (uint32_t)reinterpret_cast<uintptr_t>((lds_p)(vt + voff8[D]));
+    __builtin_amdgcn_wave_barrier();
+    asm volatile(
+        "ds_read_b128 %0, %10\n\t"
+        "ds_read_b128 %1, %10 offset:16\n\t"
+        "ds_read_b64_tr_b8 %2, %11\n\t"
+        "ds_read_b64_tr_b8 %3, %12\n\t"
+        "ds_read_b64_tr_b8 %4, %13\n\t"
+        "ds_read_b64_tr_b8 %5, %14\n\t"
+        "ds_read_b64_tr_b8 %6, %15\n\t"
+        "ds_read_b64_tr_b8 %7, %16\n\t"
+        "ds_read_b64_tr_b8 %8, %17\n\t"
+        "ds_read_b64_tr_b8 %9, %18\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(wa), "=&v"(wb), "=&v"(vb[0]), "=&v"(vb[1]), "=&v"(vb[2]), "=&v"(vb[3]), "=&v"(vb[4]), "=&v"(vb[5]),
+          "=&v"(vb[6]), "=&v"(vb[7])
+        : "v"(pw), "v"(ad[0]), "v"(ad[1]), "v"(ad[2]), "v"(ad[3]), "v"(ad[4]), "v"(ad[5]), "v"(ad[6]), "v"(ad[7])
+        : "memory");
+}
+
 // max / sum over the 16 lanes of a row (DPP), every lane receiving the result
 __device__ __forceinline__ float pv_row_max(float v) {
     v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false)));
@@ -1599,20 +1633,16 @@ __global__ __launch_bounds__(256, 2) void k_attn_fused_pv(AttnFArgs a) {
             *reinterpret_cast<uint32_t*>(pa + pa_w + 128 * g) =
                 (uint32_t)__builtin_bit_cast(uint16_t, hi) | ((uint32_t)__builtin_bit_cast(uint16_t, lo) << 16);
         }
-        // the other lanes' P' words: one wave's LDS accesses complete in order
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        const uint4 wa = *reinterpret_cast<const uint4*>(pa + pa_r);
-        const uint4 wb = *reinterpret_cast<const uint4*>(pa + pa_r + 16);
+        // the other lanes' P' words, then the V tile (8 keys of one dimension per lane)
+        uint4 wa, wb;
+        pv_v2i vb[8];
+        pv_read_pv(pa + pa_r, vt, voff8, wa, wb, vb);
         const uint4 ap = make_uint4(__builtin_amdgcn_perm(wa.y, wa.x, psel), __builtin_amdgcn_perm(wa.w, wa.z, psel),
                                     __builtin_amdgcn_perm(wb.y, wb.x, psel), __builtin_amdgcn_perm(wb.w, wb.z, psel));
         const ti_h8 A = __builtin_bit_cast(ti_h8, ap);
 #pragma unroll
-        for (int D = 0; D < 8; D++) {
-            const pv_v2i vb = __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) pv_v2i*)(vt + voff8[D]));
-            O[D] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, ti_i8x8_h8((uint32_t)vb.x, (uint32_t)vb.y), O[D], 0, 0, 0);
-        }
+        for (int D = 0; D < 8; D++)
+            O[D] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, ti_i8x8_h8((uint32_t)vb[D].x, (uint32_t)vb[D].y), O[D], 0, 0, 0);
     };
     // the tile holding pos: that key's rows from the prologue's LDS copy (this launch writes
     // them to the cache)
