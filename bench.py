@@ -39,6 +39,7 @@ Beside it, each bounded to a few seconds (not `value`):
                 min of 31)
 """
 import argparse
+import hashlib
 import json
 import os
 import sys
@@ -279,6 +280,65 @@ def family_profile(ctx, step, sets, flush, reps=12):
     return out
 
 
+def launch_durations(ctx, step, sets, fam, reps=4):
+    """The average duration of one launch of family `fam` inside the whole step: event-record
+    nodes placed just before and just after each of its launches in the step's graph (16
+    launches per graph, event slots 32-63), the graphs replayed over both weight sets with a
+    synchronisation after each replay. Like the profiler's per-dispatch record, each interval
+    covers one dispatch from its start to its completion, with nothing overlapping it."""
+    n = step.fam_launches[fam]
+    durs = []
+    for first in range(0, n, 16):
+        sel = range(first, min(n, first + 16))
+
+        def issue(ws, sel=sel, first=first):
+            seen = [0]
+
+            def mark(f, when):
+                if f != fam:
+                    return
+                if seen[0] in sel:
+                    ctx.record(32 + 2 * (seen[0] - first) + when)
+                seen[0] += when
+            step.issue(ws, mark=mark)
+        gs = [graph_of(ctx, lambda ws=ws: issue(ws)) for ws in sets]
+        for r in range(reps + 1):
+            for g in gs:
+                ctx.graph_launch(g)
+                ctx.sync()
+                if r:                  # the first pass over both graphs is a warm-up
+                    durs += [ctx.elapsed_ms(32 + 2 * j, 33 + 2 * j) * 1e3 for j in range(len(sel))]
+        for g in gs:
+            ctx.graph_destroy(g)
+    return sum(durs) / len(durs), len(durs)
+
+
+def sha256_file(path):
+    with open(path, "rb") as f:
+        return hashlib.sha256(f.read()).hexdigest()
+
+
+def traffic_record(fam):
+    """The HBM bytes per dispatch of family `fam`'s kernel from profiles/traffic.json (two
+    rocprofv3 --pmc runs of this command, summarised by `python -m tabinfer_amd.rocprof_summary
+    traffic`), its source line, the commit it was measured at, and whether it is stale: the
+    file stamps the sha256 of each kernel source it was measured on, and any of them that
+    differs from the file here now makes the figure stale (None when there is no stamp)."""
+    tp = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(tp):
+        return None, None, None, None
+    with open(tp) as f:
+        tj = json.load(f)
+    stamp = tj.get("_stamp") or {}
+    srcs = stamp.get("sources")
+    stale = None
+    if srcs:
+        stale = any(not os.path.exists(os.path.join(ROOT, p)) or sha256_file(os.path.join(ROOT, p)) != h
+                    for p, h in srcs.items())
+    fams = tj.get("families", tj)
+    return fams.get(fam), tj.get("_source"), stamp.get("commit"), stale
+
+
 # ---- the launch boundary ----------------------------------------------------------------------
 def launch_floor(ctx, n, reps=20):
     """The cost of a kernel boundary when nothing else is done: chains of n stream-ordered
@@ -312,29 +372,31 @@ def launch_floor(ctx, n, reps=20):
 def gemv_sustained(ctx, pool, reps=12):
     """The batch-1 projection GEMV (int8 activation codes x int4 weights, ti_gemv_q4_q8) over
     many rows at the Qwen3-1.7B reduction sizes: the 28 layers' gate matrices stacked
-    (172032 x 2048, 198 MB) and their down matrices stacked (57344 x 6144, 198 MB), four
-    launches back to back in one graph over two weight sets (past the 256 MB Infinity
-    Cache). The kernel's streaming rate once its launch and first round trip are amortised,
-    which the decode step's 1-14 MB GEMVs never reach (see launch_floor)."""
+    (172032 x 2048, 198 MB) and their down matrices stacked (57344 x 6144, 198 MB), six
+    launches back to back in one graph cycling over three weight sets (a 594 MB live set,
+    more than twice the 256 MB Infinity Cache, so each launch streams from HBM). The
+    kernel's streaming rate once its launch and first round trip are amortised, which the
+    decode step's 1-14 MB GEMVs never reach (see launch_floor)."""
     rng = np.random.default_rng(77)
     out = {}
     for name, N, K in (("gate_x28_2048", 172032, 2048), ("down_x28_6144", 57344, 6144)):
-        sets = [pool.quantized(N, K, rng) for _ in range(2)]
+        sets = [pool.quantized(N, K, rng) for _ in range(3)]
         x = ctx.upload(rng.standard_normal(K).astype(np.float32))
         xq, xs, xsum = ctx.zeros(K), ctx.zeros(K // 8), ctx.zeros(K)
         ctx.call("ti_quant_act_q8", x, xq, xs, xsum, K)
         y = ctx.zeros(N * 4)
 
         def issue():
-            for i in range(4):
-                p, sc = sets[i % 2]
+            for i in range(6):
+                p, sc = sets[i % 3]
                 ctx.call("ti_gemv_q4_q8", xq, xs, p, sc, y, N, K, 0)
         g = graph_of(ctx, issue)
         time_graphs(ctx, [g], 2)
-        us = time_graphs(ctx, [g], reps) * 1e3 / 4
+        us = time_graphs(ctx, [g], reps) * 1e3 / 6
         ctx.graph_destroy(g)
         nb = int4_bytes(N, K) + K + (K // 32) * 4 + N * 4
         out[name] = {"N": N, "K": K, "us_per_launch": round(us, 2), "bytes_per_launch": nb,
+                     "live_set_bytes": 3 * int4_bytes(N, K),
                      "GB_s": round(nb / (us * 1e-6) / 1e9, 1), "pct_of_hbm_peak": round(100 * nb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 1)}
         for b in (x, xq, xs, xsum, y):
             b.free()
@@ -512,12 +574,13 @@ def int3_bytes(N, K):
     return N * K // 32 * 14          # three u32 bitplanes + one f16 scale per 32 weights
 
 
-def moe(ctx, flush, reps=4, layers=16):
+def moe(ctx, flush, reps=4, layers=28):
     """One MoE block (router -> w1/w3 -> swiglu -> w2 -> combine, models/lfm25.js:2145-2166)
     at batch 1 (the fused decode launches) and batch 16 (ti_moe_prefill_q3: expert-grouped GEMMs, 5 launches), over
     `layers` independent expert sets (copies of one seeded set at distinct addresses) in
-    one graph, so the weights stream from HBM (16 x 19 MB at batch 1, past the 256 MB
-    Infinity Cache) the way consecutive decode layers do; us per block = graph time / layers."""
+    one graph, so the weights stream from HBM the way consecutive decode layers do: at batch
+    1 the 4 routed experts of 28 sets are 28 x 19.3 MB = 540 MB, more than twice the 256 MB
+    Infinity Cache; us per block = graph time / layers."""
     H, I, nE, K = 2048, 1792, 32, 4
     rng = np.random.default_rng(5)
     base = []
@@ -566,6 +629,7 @@ def moe(ctx, flush, reps=4, layers=16):
         ctx.graph_destroy(g)
         wbytes = ne * (2 * int3_bytes(I, H) + int3_bytes(H, I))
         out["batch%d" % T] = {"block_us": round(us, 2), "distinct_experts": ne, "weight_bytes": wbytes,
+                              "live_set_bytes": layers * wbytes,
                               "GB_s": round(wbytes / (us * 1e-6) / 1e9, 1),
                               "pct_of_hbm_peak": round(100 * wbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 2),
                               "launches": 2 if T == 1 else 5}
@@ -974,18 +1038,17 @@ def main():
     log("kernel families")
     flush = Flush(ctx)
     kern = family_profile(ctx, step, sets, flush)
-    timing = ("cold: a family's launches of one step (every layer's weights) back to back in one graph, timed with "
-              "HIP events around the graph on the context stream after a 512 MiB flush; the per-dispatch averages of "
-              "the rocprofv3 kernel trace of this workload agree within ~1 us (profiles/gemv06_set_kernel_trace.md)")
     dom_name = max(kern, key=lambda k: kern[k]["avg_us"] * kern[k]["launches_per_step"])
     dom = kern[dom_name]
-    achieved = dom["bytes_per_launch"] / (dom["avg_us"] * 1e-6) / 1e9
-    traffic, traffic_src = None, None
-    tp = os.path.join(ROOT, "profiles", "traffic.json")
-    if os.path.exists(tp):
-        tj = json.load(open(tp))
-        traffic = tj.get(dom_name)
-        traffic_src = tj.get("_source")
+    log("launch durations of %s" % dom_name)
+    per_us, n_meas = launch_durations(ctx, step, sets, dom_name)
+    achieved = dom["bytes_per_launch"] / (per_us * 1e-6) / 1e9
+    timing = ("per launch: HIP event-record nodes just before and just after each %s launch inside the step's graph "
+              "(both weight sets, %d intervals), each interval one dispatch from start to completion as in the "
+              "rocprofv3 kernel trace of this command (profiles/gemv06_set_kernel_trace.md); kernels[].avg_us is "
+              "the family's launches back to back in one graph after a 512 MiB flush, the cost inside the step "
+              "(in_graph_us here)" % (dom_name, n_meas))
+    traffic, traffic_src, traffic_stamp, traffic_stale = traffic_record(dom_name)
     out = {
         "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
@@ -998,7 +1061,9 @@ def main():
                    "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2)},
         "roofline": {"bound": "hbm", "kernel": dom_name, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "timing": timing, "traffic_source": traffic_src},
+                     "avg_us": round(per_us, 3), "bytes_per_launch": dom["bytes_per_launch"],
+                     "in_graph_us": dom["avg_us"], "timing": timing, "traffic_source": traffic_src,
+                     "traffic_measured_at": traffic_stamp, "traffic_stale": traffic_stale},
         "kernels": kern,
         "launch_floor": {
             "us_per_launch": round(floor_us, 3), "us_per_launch_1wg_copy": round(floor_copy_us, 3),
