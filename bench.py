@@ -280,39 +280,6 @@ def family_profile(ctx, step, sets, flush, reps=12):
     return out
 
 
-def launch_durations(ctx, step, sets, fam, reps=4):
-    """The average duration of one launch of family `fam` inside the whole step: event-record
-    nodes placed just before and just after each of its launches in the step's graph (16
-    launches per graph, event slots 32-63), the graphs replayed over both weight sets with a
-    synchronisation after each replay. Like the profiler's per-dispatch record, each interval
-    covers one dispatch from its start to its completion, with nothing overlapping it."""
-    n = step.fam_launches[fam]
-    durs = []
-    for first in range(0, n, 16):
-        sel = range(first, min(n, first + 16))
-
-        def issue(ws, sel=sel, first=first):
-            seen = [0]
-
-            def mark(f, when):
-                if f != fam:
-                    return
-                if seen[0] in sel:
-                    ctx.record(32 + 2 * (seen[0] - first) + when)
-                seen[0] += when
-            step.issue(ws, mark=mark)
-        gs = [graph_of(ctx, lambda ws=ws: issue(ws)) for ws in sets]
-        for r in range(reps + 1):
-            for g in gs:
-                ctx.graph_launch(g)
-                ctx.sync()
-                if r:                  # the first pass over both graphs is a warm-up
-                    durs += [ctx.elapsed_ms(32 + 2 * j, 33 + 2 * j) * 1e3 for j in range(len(sel))]
-        for g in gs:
-            ctx.graph_destroy(g)
-    return sum(durs) / len(durs), len(durs)
-
-
 def sha256_file(path):
     with open(path, "rb") as f:
         return hashlib.sha256(f.read()).hexdigest()
@@ -1040,14 +1007,12 @@ def main():
     kern = family_profile(ctx, step, sets, flush)
     dom_name = max(kern, key=lambda k: kern[k]["avg_us"] * kern[k]["launches_per_step"])
     dom = kern[dom_name]
-    log("launch durations of %s" % dom_name)
-    per_us, n_meas = launch_durations(ctx, step, sets, dom_name)
-    achieved = dom["bytes_per_launch"] / (per_us * 1e-6) / 1e9
-    timing = ("per launch: HIP event-record nodes just before and just after each %s launch inside the step's graph "
-              "(both weight sets, %d intervals), each interval one dispatch from start to completion as in the "
-              "rocprofv3 kernel trace of this command (profiles/gemv06_set_kernel_trace.md); kernels[].avg_us is "
-              "the family's launches back to back in one graph after a 512 MiB flush, the cost inside the step "
-              "(in_graph_us here)" % (dom_name, n_meas))
+    achieved = dom["bytes_per_launch"] / (dom["avg_us"] * 1e-6) / 1e9
+    timing = ("cold, in the graph: the family's launches of one step (every layer's weights) back to back in one "
+              "graph, timed with HIP events around the graph on the context stream after a 512 MiB flush, divided "
+              "by the launches (gaps included); the rocprofv3 kernel trace of this command "
+              "(profiles/gemv06_set_kernel_trace.md) records each dispatch about 0.5 us longer, its own "
+              "per-dispatch timestamps included")
     traffic, traffic_src, traffic_stamp, traffic_stale = traffic_record(dom_name)
     out = {
         "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
@@ -1061,8 +1026,8 @@ def main():
                    "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2)},
         "roofline": {"bound": "hbm", "kernel": dom_name, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "avg_us": round(per_us, 3), "bytes_per_launch": dom["bytes_per_launch"],
-                     "in_graph_us": dom["avg_us"], "timing": timing, "traffic_source": traffic_src,
+                     "avg_us": dom["avg_us"], "bytes_per_launch": dom["bytes_per_launch"],
+                     "timing": timing, "traffic_source": traffic_src,
                      "traffic_measured_at": traffic_stamp, "traffic_stale": traffic_stale},
         "kernels": kern,
         "launch_floor": {
