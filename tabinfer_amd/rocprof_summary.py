@@ -5,6 +5,7 @@
     python -m tabinfer_amd.rocprof_summary counters <dir> COUNTER [COUNTER ...]
     python -m tabinfer_amd.rocprof_summary traffic <fetch-dir> <write-dir> --calib KERNEL BYTES
         --commit HASH --sources FILE [FILE ...] --map NAME=KERNEL [NAME=KERNEL ...] -o OUT.json
+        [--note WORD ...]
 
 `stats` prints the per-kernel table of a `rocprofv3 --kernel-trace --stats`
 run (calls, average and total duration).
@@ -103,7 +104,7 @@ def pmc(fetch_dir, write_dir, calib=None):
     return "\n".join(lines)
 
 
-def traffic(fetch_dir, write_dir, calib, commit, sources, mapping):
+def traffic(fetch_dir, write_dir, calib, commit, sources, mapping, note=""):
     fa, fn = pmc_avg(fetch_dir, "FETCH_SIZE")
     wa, _ = pmc_avg(write_dir, "WRITE_SIZE")
     kf, kw, _ = calib_factors(fetch_dir, write_dir, calib)
@@ -119,7 +120,8 @@ def traffic(fetch_dir, write_dir, calib, commit, sources, mapping):
         with open(path, "rb") as f:
             stamp["sources"][os.path.relpath(path)] = hashlib.sha256(f.read()).hexdigest()
     return {"families": fams, "kernels": {n: short(s, 200) for n, s in mapping},
-            "_source": "rocprofv3 --pmc FETCH_SIZE x %.4f + WRITE_SIZE x %.4f (%s %d-byte calibration), HBM bytes per "
+            "_source": ("%s: " % note if note else "") +
+                       "rocprofv3 --pmc FETCH_SIZE x %.4f + WRITE_SIZE x %.4f (%s %d-byte calibration), HBM bytes per "
                        "dispatch" % (kf, kw, calib[0], calib[1]),
             "_stamp": stamp}
 
@@ -155,7 +157,8 @@ def main(argv):
                 opts[cur].append(a)
         calib = (opts["--calib"][0], int(opts["--calib"][1]))
         mapping = [tuple(m.split("=", 1)) for m in opts["--map"]]
-        res = traffic(argv[1], argv[2], calib, opts["--commit"][0], opts.get("--sources", []), mapping)
+        res = traffic(argv[1], argv[2], calib, opts["--commit"][0], opts.get("--sources", []), mapping,
+                      " ".join(opts.get("--note", [])))
         with open(opts["-o"][0], "w") as f:
             json.dump(res, f, indent=1)
             f.write("\n")
