@@ -15,6 +15,9 @@
 //            qcache: {dir, dump, prompt, maxTokens}   load from safetensors writing the quant
 //                    cache, then from the cache alone, then after a manifest of another geometry
 //            tokchat: {tokenizer, text, system, maxTokens}   generate() and runConversation on text
+//   kvw:     {config, nCtx, layer, T, pos, kr, v}   a randomly initialised model: qwen3_kv_layout,
+//            then qwen3_kv_write of buffers kr, v at pos; the layer's K/V code rows and scales
+//            [pos, pos + T) before and after are written to kvw_{before,after}.{kq,ks,vq,vs}
 // Writes <dir>/result.json (and the files named by `read`).
 const fs = require('fs');
 const path = require('path');
@@ -101,9 +104,30 @@ async function main() {
     if (m.qcache) result.qcache = await runQcache(host, m, dir);
     if (m.tokchat) result.tokchat = await runTokChat(host, m);
   }
+  if (spec.kvw) result.kvw = await runKvWrite(host, spec.kvw, B, dir);
   E.sync();
   fs.writeFileSync(path.join(dir, 'result.json'), JSON.stringify(result));
   host.shutdown();
+}
+
+async function runKvWrite(host, k, B, dir) {
+  const { E } = host.engine;
+  await host.loadModel({ config: k.config, nCtx: k.nCtx, random: 7, reload: true });
+  const model = host.model();
+  const slots = E.TI.qwen3_kv_layout(model);
+  const kv = E.TI.qwen3_kv(model, k.layer);
+  const hd = k.config.head_dim, nKv = k.config.n_kv_heads;
+  const dump = (tag) => {
+    const rowc = slots * hd, rows = nKv * (hd / 32) * 4;
+    for (const [n, bytes] of [['kq', rowc], ['vq', rowc], ['ks', rows], ['vs', rows]])
+      fs.writeFileSync(path.join(dir, 'kvw_' + tag + '.' + n), Buffer.from(E.readBytes(kv[n], k.pos * bytes, k.T * bytes)));
+  };
+  E.sync();
+  dump('before');
+  E.TI.qwen3_kv_write(E.ctx, model, k.layer, B(k.kr), B(k.v), k.T, k.pos);
+  E.sync();
+  dump('after');
+  return { slots, kvSlots: kv.slots };
 }
 
 // a toy tokenizer over raw ids: encodeChat joins the messages' id lists

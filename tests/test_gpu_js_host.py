@@ -469,3 +469,29 @@ def test_self_test_kernels(tmp_path):
     names = [c["name"] for c in st]
     assert len(names) >= 18 and len(set(names)) == len(names)
     assert all(c["ok"] for c in st), [c for c in st if not c["ok"]]
+
+
+def test_kv_layout_and_write(tmp_path, orc):
+    """qwen3_kv_layout / qwen3_kv_write from JS on a model with 8 KV heads: the code rows hold
+    a spare slot, the written rows equal the oracle's kvQuantWrite of the same K/V (bit for
+    bit), and the spare slot is left as it was."""
+    d = str(tmp_path)
+    c = dict(layers=2, hidden=256, intermediate=512, n_heads=16, n_kv_heads=8, head_dim=128, vocab=1000,
+             rope_theta=1e6, rms_eps=1e-6)
+    T, pos, layer, nKv, hd = 3, 37, 1, 8, 128
+    n = T * nKv * hd
+    i = np.arange(n)
+    kr = (np.sin(i * 0.11) * (1 + (i % 5))).astype(np.float32)
+    vv = (np.cos(i * 0.07) * (1 + (i % 3))).astype(np.float32)
+    spec = {"buffers": {"kr": {"file": "kr.bin"}, "v": {"file": "v.bin"}},
+            "kvw": {"config": c, "nCtx": 64, "layer": layer, "T": T, "pos": pos, "kr": "kr", "v": "v"}}
+    res = run_spec(d, spec, {"kr.bin": kr, "v.bin": vv})
+    slots = res["kvw"]["slots"]
+    assert slots == nKv + 1 and res["kvw"]["kvSlots"] == slots
+    for src, q, s in ((kr, "kq", "ks"), (vv, "vq", "vs")):
+        want_q, want_s = orc.kv_quant(src)
+        before = load(d, "kvw_before." + q, np.uint8).reshape(T, slots, hd)
+        after = load(d, "kvw_after." + q, np.uint8).reshape(T, slots, hd)
+        assert np.array_equal(after[:, :nKv].reshape(-1), want_q.view(np.uint8))
+        assert np.array_equal(after[:, nKv:], before[:, nKv:])
+        assert np.array_equal(load(d, "kvw_after." + s, np.float32), want_s)
