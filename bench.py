@@ -18,7 +18,8 @@ bytes of the step / wall time of the timed steps (launch gaps included).
 Beside it, each bounded to a few seconds (not `value`):
   kernels       per kernel family, its average launch duration (the family's launches of
                 one step back to back in one graph, after a cache flush); the dominant
-                family by total time sets `roofline`
+                family by total time sets `roofline`; in_chain_us: one more launch of the
+                family in a chain (graph over both weight sets minus graph over one)
   gemv_set_1p7b the same GEMV set at the Qwen3-1.7B shapes (967.75 MB of int4 weights)
   gemv_sustained_1p7b  the projection GEMV kernel at the 1.7B reduction sizes over 198 MB
                 of stacked rows per launch: its streaming rate with the launch amortised
@@ -265,7 +266,11 @@ def cold_ms(ctx, graphs, reps, flush):
 def family_profile(ctx, step, sets, flush, reps=12):
     """Per kernel family: its launches of one step (real shapes, all layers' weights)
     captured into one graph and timed with HIP events after a cache flush; the
-    average per launch includes the back-to-back dispatch gaps inside the graph."""
+    average per launch includes the back-to-back dispatch gaps inside the graph, and the
+    graph's own launch. With two weight sets, also `in_chain_us`: the cost of one more
+    launch in a chain, from a graph of the family's launches over both sets minus the
+    graph over one (both cold), which leaves the graph launch and the first launch's
+    start-up out, as inside the step."""
     out = {}
     for fam in Step.FAMILIES:
         gs = [graph_of(ctx, lambda ws=ws: step.issue(ws, (fam,))) for ws in sets]
@@ -275,6 +280,14 @@ def family_profile(ctx, step, sets, flush, reps=12):
         us = ms * 1e3 / n
         out[fam] = {"launches_per_step": n, "avg_us": round(us, 3), "bytes_per_launch": step.fam_bytes[fam],
                     "GB_s": round(step.fam_bytes[fam] / (us * 1e-6) / 1e9, 1)}
+        if len(sets) >= 2:
+            g2 = [graph_of(ctx, lambda a=a, b=b: (step.issue(a, (fam,)), step.issue(b, (fam,))))
+                  for a, b in ((sets[0], sets[1]), (sets[1], sets[0]))]
+            time_graphs(ctx, g2, 2)
+            ms2 = cold_ms(ctx, g2, reps, flush)
+            out[fam]["in_chain_us"] = round((ms2 - ms) * 1e3 / n, 3)
+            for g in g2:
+                ctx.graph_destroy(g)
         for g in gs:
             ctx.graph_destroy(g)
     return out
@@ -1030,6 +1043,8 @@ def main():
                      "timing": timing, "traffic_source": traffic_src,
                      "traffic_measured_at": traffic_stamp, "traffic_stale": traffic_stale},
         "kernels": kern,
+        "kernels_in_chain_ms_per_step": (round(sum(k["in_chain_us"] * k["launches_per_step"] for k in kern.values()) * 1e-3, 4)
+                                         if all("in_chain_us" in k for k in kern.values()) else None),
         "launch_floor": {
             "us_per_launch": round(floor_us, 3), "us_per_launch_1wg_copy": round(floor_copy_us, 3),
             "launches": step.launches, "floor_ms_per_step": round(floor_us * step.launches * 1e-3, 4),
