@@ -439,6 +439,72 @@ __device__ __forceinline__ void wave_route(const float* __restrict__ logits, con
         if (k < topk) wk[k] = chosen_s[k] / (sum + 1e-6f);
 }
 
+// a group's Limbs as 28 words (l[3][8], then sum[3] and the scale's bits), for LDS
+struct LimbsPacked {
+    int4 w[7];          // l[3][8] as 6 int4, then sum[3] and the scale's bits
+};
+__device__ __forceinline__ void unpack_limbs(const LimbsPacked& d, Limbs& L) {
+#pragma unroll
+    for (int q = 0; q < 3; q++) {
+        const int4 a = d.w[2 * q], b = d.w[2 * q + 1];
+        L.l[q][0] = a.x; L.l[q][1] = a.y; L.l[q][2] = a.z; L.l[q][3] = a.w;
+        L.l[q][4] = b.x; L.l[q][5] = b.y; L.l[q][6] = b.z; L.l[q][7] = b.w;
+    }
+    const int4 t = d.w[6];
+    L.sum[0] = t.x; L.sum[1] = t.y; L.sum[2] = t.z; L.S = __int_as_float(t.w);
+}
+
+// make_limbs of one 32-element group shared by TPG adjacent lanes, each converting 32/TPG
+// consecutive elements (part = the lane's index among them): the group's max through a
+// butterfly over the TPG lanes, then the same per-element conversion, words and sums as
+// make_limbs (so the same bits). Every lane of the TPG must take part.
+template <int TPG>
+__device__ __forceinline__ void coop_limbs(const float* grp, int part, LimbsPacked& d) {
+    constexpr int EPT = 32 / TPG;
+    float v[EPT];
+#pragma unroll
+    for (int i = 0; i < EPT; i++) v[i] = grp[part * EPT + i];
+    float mx = 0.0f;
+#pragma unroll
+    for (int i = 0; i < EPT; i++) mx = fmaxf(mx, fabsf(v[i]));
+#pragma unroll
+    for (int o = 1; o < TPG; o <<= 1) mx = fmaxf(mx, ti_xor(mx, o));
+    int ex = 0;
+    if (mx > 0.0f) (void)frexpf(mx, &ex);
+    int* out = reinterpret_cast<int*>(&d);
+    int sum[3] = {0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < EPT / 4; j++) {
+        uint32_t word[3] = {0u, 0u, 0u};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int X = mx > 0.0f ? (int)rintf(ldexpf(v[4 * j + e], 22 - ex)) : 0;
+            const int l0 = ((X & 0xff) ^ 0x80) - 0x80;
+            const int X1 = (X - l0) >> 8;
+            const int l1 = ((X1 & 0xff) ^ 0x80) - 0x80;
+            const int l2 = (X1 - l1) >> 8;
+            word[0] |= (uint32_t)(l0 & 0xff) << (8 * e);
+            word[1] |= (uint32_t)(l1 & 0xff) << (8 * e);
+            word[2] |= (uint32_t)(l2 & 0xff) << (8 * e);
+            sum[0] += l0;
+            sum[1] += l1;
+            sum[2] += l2;
+        }
+#pragma unroll
+        for (int q = 0; q < 3; q++) out[8 * q + part * (EPT / 4) + j] = (int)word[q];
+    }
+#pragma unroll
+    for (int o = 1; o < TPG; o <<= 1)
+#pragma unroll
+        for (int q = 0; q < 3; q++) sum[q] += ti_xor(sum[q], o);
+    if (part == 0) {
+        out[24] = sum[0];
+        out[25] = sum[1];
+        out[26] = sum[2];
+        out[27] = __float_as_int(ldexpf(1.0f, ex - 22));
+    }
+}
+
 // grid (row blocks of 4R, topk): workgroup (., k) runs the router, takes expert e of
 // slot k, and computes act[k*I + n] = silu(w1_e x)_n * (w3_e x)_n for its 4R rows
 // (R per wave) with the exact fixed-point dot of k_moe_gemv_q3. Workgroup (0, k) stores
@@ -475,6 +541,7 @@ __global__ __launch_bounds__(256) void k_moe_gateup_dec(const float* __restrict_
         wt[k] = w;
     }
     const int row0 = (blockIdx.x * 4 + wave) * R;
+    __shared__ LimbsPacked s_lb[GL * 64];
     uint32_t pg[GL][R][3], pu[GL][R][3];
     uint16_t sg[GL][R], su[GL][R];
 #pragma unroll
@@ -495,19 +562,20 @@ __global__ __launch_bounds__(256) void k_moe_gateup_dec(const float* __restrict_
         }
     }
     __syncthreads();
+    {   // every group's limbs once per workgroup: 4 / GL threads a group (the waves would
+        // otherwise each convert the same 64 GL groups)
+        constexpr int TPG = 4 / GL;
+        const int grp = threadIdx.x / TPG;
+        if (grp < gpr) coop_limbs<TPG>(&s_x[grp * 36], threadIdx.x % TPG, s_lb[grp]);   // uniform per TPG lanes
+    }
+    __syncthreads();
     float accv[2 * R] = {};
 #pragma unroll
     for (int h = 0; h < GL; h++) {
         const int g = lane + 64 * h;
         const int gc = g < gpr ? g : gpr - 1;
-        float v[32];
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const float4 t = *reinterpret_cast<const float4*>(&s_x[gc * 36 + 4 * i]);
-            v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
-        }
         Limbs L;
-        make_limbs(v, L);
+        unpack_limbs(s_lb[gc], L);
         const bool live = lane + 64 * h < gpr;
 #pragma unroll
         for (int r = 0; r < R; r++) {
@@ -599,9 +667,6 @@ __global__ __launch_bounds__(256) void k_moe_down_dec(const float* __restrict__ 
 
 // the same with the slots' activation limbs computed once per workgroup (wave k: slot k,
 // P <= 4) and shared through LDS; R rows per wave (I <= 2048)
-struct LimbsPacked {
-    int4 w[7];          // l[3][8] as 6 int4, then sum[3] and the scale's bits
-};
 template <int P, int R>
 __global__ __launch_bounds__(256) void k_moe_down_dec_pl(const float* __restrict__ act, const uint32_t* __restrict__ p2,
                                                          const uint16_t* __restrict__ s2, const int32_t* __restrict__ idx,
@@ -654,16 +719,8 @@ __global__ __launch_bounds__(256) void k_moe_down_dec_pl(const float* __restrict
     float accv[R * P];
 #pragma unroll
     for (int k = 0; k < P; k++) {
-        const LimbsPacked& d = s_l[k][lane];
         Limbs L;
-#pragma unroll
-        for (int q = 0; q < 3; q++) {
-            const int4 a = d.w[2 * q], b = d.w[2 * q + 1];
-            L.l[q][0] = a.x; L.l[q][1] = a.y; L.l[q][2] = a.z; L.l[q][3] = a.w;
-            L.l[q][4] = b.x; L.l[q][5] = b.y; L.l[q][6] = b.z; L.l[q][7] = b.w;
-        }
-        const int4 t = d.w[6];
-        L.sum[0] = t.x; L.sum[1] = t.y; L.sum[2] = t.z; L.S = __int_as_float(t.w);
+        unpack_limbs(s_l[k][lane], L);
 #pragma unroll
         for (int r = 0; r < R; r++) {
             const float dd = group_dot_q3_limbs(pl[k][r][0], pl[k][r][1], pl[k][r][2], L);
