@@ -756,7 +756,7 @@ def tern2_step(ctx, reps=10):
 
 def bonsai_decode(ctx, contexts=(1024, 8192), steps=64, eager=False):
     """The Bonsai-1.7B ternary decoder (ti_bonsai_*, model.rs's forward) at batch 1: one
-    captured decode step (~11 launches per layer) replayed token after token over an f32 KV
+    captured decode step (6 launches per layer) replayed token after token over an f32 KV
     prefix of S positions; every layer's distinct ternary weights (541 MB with the lm_head)
     and the f32 KV cache (S x 8 KV heads x 128 x 2 x 4 B per layer) stream from HBM."""
     from tabinfer_amd import abi
