@@ -66,3 +66,10 @@ def test_bench_marks_traffic_measured_on_other_sources(tmp_path, monkeypatch):
     assert bench.traffic_record("qkv") == (123, "s", "c0ffee", True)
     src.unlink()
     assert bench.traffic_record("qkv")[3] is True
+
+
+def test_bench_refuses_more_than_one_gpu():
+    import subprocess
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], stdout=subprocess.PIPE,
+                       stderr=subprocess.PIPE, text=True, timeout=120)
+    assert r.returncode == 2 and "single GPU" in r.stderr and not r.stdout
