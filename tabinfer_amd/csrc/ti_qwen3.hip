@@ -619,7 +619,9 @@ extern "C" int ti_qwen3_forward(ti_ctx* c, ti_qwen3* m, const int32_t* ids, int 
     // workgroup quantises all T x H elements) costs more than the launch it saves, and a
     // per-token norm kernel writes the codes into the context's activation scratch
     // first (1.7B geometry at 8k: T = 2 1.22 against 1.29 ms, T = 4 1.26 against 1.32,
-    // T = 8 1.39 against 1.36, T = 16 3.13 against 2.94; both paths give the same bits).
+    // T = 8 1.39 against 1.36, T = 16 3.13 against 2.94; with the pairwise-group MFMA,
+    // T = 8 1.37 against 1.32 at 8k and 1.60 against 1.55 at 32k; both paths give the same
+    // bits).
     // The attention and SwiGLU codes live in the model's scratch.
     const bool fused = ti_tnorm_ok(H) && ti_tgemm_gateup_ok(T, H) && ti_tgemm_ok(T, nq) && ti_tgemm_ok(T, I) &&
                        nq % 16 == 0 && nkv % 16 == 0 && I % 32 == 0;
