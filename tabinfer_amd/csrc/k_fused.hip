@@ -885,7 +885,11 @@ int ti_fused_lmhead_launch(ti_ctx* c, const float* x, const uint16_t* nw, float 
     Shape s = fshape(K / 32);
     int R = fpick_R(N, s.lpr);
     long nblocks = ((long)N + (64 / s.lpr) * R - 1) / ((64 / s.lpr) * R);
-    unsigned grid = fgrid(nblocks);
+    // half the GEMVs' persistent grid: every workgroup runs the norm and the limbs of the
+    // whole activation and leaves one argmax partial, and at 2048 waves those cost less
+    // than the streaming they leave to each wave (151936 x 1024: 26.9 -> 24.1 us per
+    // launch in a chain; x 2048 unchanged)
+    unsigned grid = fgrid(nblocks < 2048 ? nblocks : 2048);
     if (grid > TI_AMAX_PARTS) return ti_fail(TI_ERR_INVALID, "lm_head: %u workgroups > %d partials", grid, TI_AMAX_PARTS);
 #define X(L, G)                                                                                     \
     if (s.lpr == L && s.gpl == G && G <= 3) {                                                       \
