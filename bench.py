@@ -263,7 +263,7 @@ def cold_ms(ctx, graphs, reps, flush):
     return total / reps
 
 
-def family_profile(ctx, step, sets, flush, reps=12):
+def family_profile(ctx, step, sets, flush, reps=12, keep=None):
     """Per kernel family: its launches of one step (real shapes, all layers' weights)
     captured into one graph and timed with HIP events after a cache flush; the
     average per launch includes the back-to-back dispatch gaps inside the graph, and the
@@ -272,8 +272,12 @@ def family_profile(ctx, step, sets, flush, reps=12):
     graph over one (both cold), which leaves the graph launch and the first launch's
     start-up out, as inside the step."""
     out = {}
+    out_keep = keep
+    keep = []      # destroyed together at the end: under rocprofv3's kernel trace, launching a
+    #                graph instantiated after another was destroyed has crashed the profiler
     for fam in Step.FAMILIES:
         gs = [graph_of(ctx, lambda ws=ws: step.issue(ws, (fam,))) for ws in sets]
+        keep += gs
         time_graphs(ctx, gs, 2)
         ms = cold_ms(ctx, gs, reps, flush)
         n = step.fam_launches[fam]
@@ -283,12 +287,15 @@ def family_profile(ctx, step, sets, flush, reps=12):
         if len(sets) >= 2:
             g2 = [graph_of(ctx, lambda a=a, b=b: (step.issue(a, (fam,)), step.issue(b, (fam,))))
                   for a, b in ((sets[0], sets[1]), (sets[1], sets[0]))]
+            keep += g2
             time_graphs(ctx, g2, 2)
             ms2 = cold_ms(ctx, g2, reps, flush)
             out[fam]["in_chain_us"] = round((ms2 - ms) * 1e3 / n, 3)
-            for g in g2:
-                ctx.graph_destroy(g)
-        for g in gs:
+    ctx.sync()
+    if out_keep is not None:
+        out_keep += keep
+    else:
+        for g in keep:
             ctx.graph_destroy(g)
     return out
 
@@ -320,7 +327,7 @@ def traffic_record(fam):
 
 
 # ---- the launch boundary ----------------------------------------------------------------------
-def launch_floor(ctx, n, reps=20):
+def launch_floor(ctx, n, reps=20, keep=None):
     """The cost of a kernel boundary when nothing else is done: chains of n stream-ordered
     launches captured in one HIP graph and launched like a decode step, (a) 4 KB copies
     of one workgroup, each reading what the previous one wrote, (b) 256 KB fills of 256
@@ -338,11 +345,18 @@ def launch_floor(ctx, n, reps=20):
         for i in range(n):
             ctx.call("ti_buf_fill_u32", big.at((i % 8) << 18), i, 1 << 16)
     out = []
+    gs = []
     for issue in (copies, fills):
         g = graph_of(ctx, issue)
+        gs.append(g)
         time_graphs(ctx, [g], 3)
         out.append(time_graphs(ctx, [g], reps) * 1e3 / n)
-        ctx.graph_destroy(g)
+    ctx.sync()
+    if keep is not None:       # the caller destroys them (see family_profile)
+        keep += gs
+    else:
+        for g in gs:
+            ctx.graph_destroy(g)
     buf.free()
     big.free()
     return out
@@ -1010,17 +1024,19 @@ def main():
     ctx.sync()
     ms_per_step = ctx.elapsed_ms(10, 11) / args.steps
     value = step.bytes / (ms_per_step * 1e-3) / 1e9
-    for g in graphs:
-        ctx.graph_destroy(g)
 
     log("launch floor")
-    floor_copy_us, floor_us = launch_floor(ctx, step.launches)
+    held = list(graphs)        # every graph of this leg is destroyed after the last launch
+    floor_copy_us, floor_us = launch_floor(ctx, step.launches, keep=held)
     log("kernel families")
     flush = Flush(ctx)
-    kern = family_profile(ctx, step, sets, flush)
+    kern = family_profile(ctx, step, sets, flush, keep=held)
     # the family that carries the most of the step's HBM bytes (gate/up: 99 of 337 MB); by
     # time per step gate/up and q/k/v are within 1% of each other and trade places between
     # runs, while the byte count is fixed by the shapes
+    ctx.sync()
+    for g in held:
+        ctx.graph_destroy(g)
     dom_name = max(kern, key=lambda k: kern[k]["bytes_per_launch"] * kern[k]["launches_per_step"])
     dom = kern[dom_name]
     achieved = dom["bytes_per_launch"] / (dom["avg_us"] * 1e-6) / 1e9
