@@ -263,7 +263,7 @@ def cold_ms(ctx, graphs, reps, flush):
     return total / reps
 
 
-def family_profile(ctx, step, sets, flush, reps=12, keep=None):
+def family_profile(ctx, step, sets, flush, reps=12, keep=None, chain=True):
     """Per kernel family: its launches of one step (real shapes, all layers' weights)
     captured into one graph and timed with HIP events after a cache flush; the
     average per launch includes the back-to-back dispatch gaps inside the graph, and the
@@ -284,7 +284,7 @@ def family_profile(ctx, step, sets, flush, reps=12, keep=None):
         us = ms * 1e3 / n
         out[fam] = {"launches_per_step": n, "avg_us": round(us, 3), "bytes_per_launch": step.fam_bytes[fam],
                     "GB_s": round(step.fam_bytes[fam] / (us * 1e-6) / 1e9, 1)}
-        if len(sets) >= 2:
+        if chain and len(sets) >= 2:
             g2 = [graph_of(ctx, lambda a=a, b=b: (step.issue(a, (fam,)), step.issue(b, (fam,))))
                   for a, b in ((sets[0], sets[1]), (sets[1], sets[0]))]
             keep += g2
@@ -973,6 +973,9 @@ def main():
                          "the same step in the on-GPU ternary format; "
                          "bonsai: the Bonsai decoder alone at --ctx (default 1024) (no headline line)")
     ap.add_argument("--eager", action="store_true", help="--only bonsai: launch the steps directly, without a graph")
+    ap.add_argument("--no-chain", action="store_true",
+                    help="skip kernels[].in_chain_us (its two-set graphs crash rocprofv3's kernel trace; profiling "
+                         "runs pass this)")
     ap.add_argument("--ctx", type=int, nargs="*", default=None,
                     help="context lengths of the decode leg (default 8192 32768)")
     args = ap.parse_args()
@@ -1030,7 +1033,7 @@ def main():
     floor_copy_us, floor_us = launch_floor(ctx, step.launches, keep=held)
     log("kernel families")
     flush = Flush(ctx)
-    kern = family_profile(ctx, step, sets, flush, keep=held)
+    kern = family_profile(ctx, step, sets, flush, keep=held, chain=not args.no_chain)
     # the family that carries the most of the step's HBM bytes (gate/up: 99 of 337 MB); by
     # time per step gate/up and q/k/v are within 1% of each other and trade places between
     # runs, while the byte count is fixed by the shapes
