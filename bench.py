@@ -52,6 +52,9 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+# the decode step's q/k/v GEMV runs inside its attention launch unless this is set (the
+# library reads it when a context is created)
+QKV_SEPARATE = os.environ.get("TI_DECODE_QKV_SEPARATE", "0") not in ("", "0")
 METRIC = "int4 GEMV HBM GB/s (% of peak) + Qwen3-1.7B bs1 decode tok/s at 32k ctx"
 
 QWEN3_06B = dict(layers=28, hidden=1024, inter=3072, n_heads=16, n_kv=8, head_dim=128, vocab=151936)
@@ -493,7 +496,8 @@ def decode_1p7b(ctx, pool, contexts=(8192, 32768), steps=64, batch8=True, batch1
             res["ctx_%d" % S].update({"tok_s": round(1e3 / ms, 1), "ms_per_token": round(ms, 4),
                                       "step_GB_s": round(step_bytes / (ms * 1e-3) / 1e9, 1),
                                       "pct_of_hbm_peak": round(100 * step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
-                                      "bytes_per_step": step_bytes, "launches_per_step": 2 + 5 * cfg["layers"]})
+                                      "bytes_per_step": step_bytes,
+                                      "launches_per_step": 2 + (5 if QKV_SEPARATE else 4) * cfg["layers"]})
             log("decode 1.7B at %d: %.1f tok/s" % (S, 1e3 / ms))
         if not batch8:
             continue

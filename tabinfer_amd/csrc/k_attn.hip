@@ -8,7 +8,7 @@
 // KV layout is the reference's: per layer, position-major, then head, then dim;
 // int8 codes packed 4 per u32 (snorm: code/127 * group max), one f32 scale per
 // 32 dims.
-#include "ti_internal.h"
+#include "ti_dev.h"
 #include <math.h>
 #include <mutex>
 
@@ -846,6 +846,19 @@ constexpr int ATTF_MAXS = 64;
 // decode step is captured, the context length is not): measured on MI355X, 32 is best
 // for contexts up to ~16k, 64 beyond (more waves streaming the keys)
 constexpr int ATTF_SPLITS_SHORT = 32, ATTF_SPLITS_LONG = 64, ATTF_LONG_CAP = 16384;
+// rounds of the q/k/v hand-off's poll (each a device-scope round trip of ~1 us plus a
+// short sleep) before a wave gives up and computes its rows itself
+constexpr int ATTF_QKV_POLLS = 1 << 15;
+
+// the activation prologue's inputs (act_regs_load / act_regs_quant read these fields)
+struct AttnNormIn {
+    const float* x;
+    const uint16_t* nw;
+    int K;
+    float eps;
+    uint32_t* xq_out;
+    float* xs_out;
+};
 
 struct AttnFArgs {
     const float* q;
@@ -874,6 +887,15 @@ struct AttnFArgs {
     uint32_t* oq;          // optional: the output quantized per 32 (quantQ8, for o_proj's linearQ)
     float* os;
     float rope_row[TI_ATTN_HD_MAX];
+    // The q/k/v projection of the same launch (k_attn_fused_pv with QL > 0): rmsnormQ of
+    // the residual stream (nin), the int4 q, k and v matrices (packs and f16 scales, rows of
+    // nin.K / 32 groups), the tagged words that carry the rows between the workgroups, and
+    // optional plain copies of q, k and v (nullptr: none)
+    AttnNormIn nin;
+    const uint4* wpk[3];
+    const uint16_t* wsc[3];
+    uint64_t* pub;
+    float* qkv_copy[3];
 };
 
 // RMSNorm over one head row held by 128 threads (j = element, 0 past hd) in the
@@ -924,7 +946,7 @@ template <int HD, int G, int TPW>
 __device__ __forceinline__ void attn_merge_tail(const AttnFArgs& a, int hk, int w, int NS, int ntiles, bool valid,
                                                 float (&s_red)[4][TPW][G * HD], float (&s_wml)[4][G][2],
                                                 float (&s_ml)[G][ATTF_MAXS][2], float (&s_e)[G][ATTF_MAXS], float* s_L,
-                                                int* s_last_p, float* s_part) {
+                                                int* s_last_p, float* s_part, uint32_t epoch = 0) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int NW = NS * 4;
     int& s_last = *s_last_p;
@@ -1046,7 +1068,12 @@ __device__ __forceinline__ void attn_merge_tail(const AttnFArgs& a, int hk, int 
             if ((lane & 31) == 0) a.os[e / 32] = scale;
         }
     }
-    if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) {
+        __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // the q/k/v hand-off of this launch is over (every split of hk has arrived here):
+        // the next launch's words carry the next epoch
+        if (epoch) __hip_atomic_store(counter + TI_SYNC_ATTN_EPOCH, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 
 template <int HD, int G>
@@ -1376,7 +1403,7 @@ __device__ __forceinline__ float pv_row_sum(float v) {
     return v;
 }
 
-template <int G>
+template <int G, int QL = 0, int QR = 2>
 __global__ __launch_bounds__(256, 2) void k_attn_fused_pv(AttnFArgs a) {
     static_assert(G == 1 || G == 2, "MFMA decode attention: G <= 2");
     constexpr int HD = 128, NG = HD / 32;
@@ -1448,30 +1475,162 @@ __global__ __launch_bounds__(256, 2) void k_attn_fused_pv(AttnFArgs a) {
     // when G = 2) holds query head `wave`, wave 2 the new K row, wave 3 the new V row;
     // lane L holds elements L and L + 64, so RMSNorm, RoPE and the limb split of q run in
     // registers
-    const int pos_dev = *a.dpos;
-    const float* xrow = wave < 2 ? a.q + (size_t)(hk * G + (wave < G ? wave : 0)) * HD
-                                 : (wave == 2 ? a.k : a.v) + (size_t)hk * HD;
     const uint16_t* nwrow = wave < 2 ? a.qw : a.kw;
-    const float x0 = xrow[lane], x1 = xrow[lane + 64];
-    const float w0 = ti_h2f(nwrow[lane]), w1 = ti_h2f(nwrow[lane + 64]);
-    const float c_dev = a.rope_cur[lane], s_dev = a.rope_cur[lane + 64];
-    const float c_arg = a.rope_row[lane], s_arg = a.rope_row[lane + 64];
+    // The device position is read with a vector load issued behind the first tile's: as a
+    // scalar load at the top it held every vector load of the prologue for its own round
+    // trip (the compiler waits for all scalar loads before the first vector one).
+    int pos_dev = 0;
     // the first tile through registers, bounded by the capacity until the context is known
     // (a load straight to LDS in flight would make the prologue's waits full ones)
     uint4 kf[4], vf[4], sf;
-    {
+    auto first_tile = [&](int wt_gw, uint4 (&tk)[4], uint4 (&tv)[4], uint4& ts) {
         __amdgpu_buffer_rsrc_t rk, rv, rks, rvs;
-        tile_rs(gw * PV_WT, a.cap, rk, rv, rks, rvs);
+        tile_rs(wt_gw * PV_WT, a.cap, rk, rv, rks, rvs);
 #pragma unroll
         for (int p = 0; p < 4; p++) {
-            kf[p] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, toff[p], 0, 2));
-            vf[p] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, toff[p], 0, 2));
+            tk[p] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, toff[p], 0, 2));
+            tv[p] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, toff[p], 0, 2));
         }
         const uint4 sk = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rks, soff, 0, 2));
         const uint4 sv = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rvs, soff, 0, 2));
-        sf = lane < 32 ? sk : sv;
+        ts = lane < 32 ? sk : sv;
+    };
+    float x0, x1;
+    uint32_t epoch = 0;
+    if constexpr (QL == 0) {
+        const float* xrow = wave < 2 ? a.q + (size_t)(hk * G + (wave < G ? wave : 0)) * HD
+                                     : (wave == 2 ? a.k : a.v) + (size_t)hk * HD;
+        x0 = xrow[lane];
+        x1 = xrow[lane + 64];
     }
-    TI_ISSUE_FENCE();
+    const float w0 = ti_h2f(nwrow[lane]), w1 = ti_h2f(nwrow[lane + 64]);
+    const float c_dev = a.rope_cur[lane], s_dev = a.rope_cur[lane + 64];
+    const float c_arg = a.rope_row[lane], s_arg = a.rope_row[lane + 64];
+    if constexpr (QL == 0) {
+        first_tile(gw, kf, vf, sf);
+        pos_dev = (int)ti_pub_load(reinterpret_cast<const uint32_t*>(a.dpos));
+        TI_ISSUE_FENCE();
+    } else {
+        // ---- q, k and v of this KV head, computed by its NS workgroups together.
+        // rmsnormQ of x in every workgroup (the q/k/v GEMV's prologue: the same codes),
+        // then each wave takes units of RS rows of the head's (G + 2) * HD rows (q heads
+        // hk*G.., the k head, the v head), units gw, gw + 4 NS, ...: QL lanes per row, one
+        // 32-group a lane, the exact int32 group dots scaled and summed as the stand-alone
+        // GEMV does (k_fgemv), so the rows are the same bits. Each row goes out as a 64-bit
+        // word, its value beside the launch's epoch; the wave that needs a row (its q head,
+        // the k or the v row) polls those words until all carry the epoch. No counter: a
+        // word is complete when it lands. The epoch of KV head hk sits beside its merge
+        // counter; the merge's last arriver (every split of hk has passed its poll by then)
+        // advances it for the next launch. A poll that does not complete in
+        // ATTF_QKV_POLLS rounds (workgroups of the head not resident) gives up, and the
+        // wave computes its 128 rows itself, with the same arithmetic.
+        constexpr int RPP = 64 / QL, R = QR, RS = RPP * R, NU = (G + 2) * HD / RS, SPAN = QL / R, EPT = QL / 8;
+        static_assert(HD % RS == 0, "a unit of rows never straddles two heads");
+        const int sub = lane / QL, li = lane % QL;
+        uint32_t* s_xq = reinterpret_cast<uint32_t*>(&s_v[0][1][0]);      // free until the tile loop
+        float* s_xs = reinterpret_cast<float*>(&s_v[0][1][2048]);
+        float* s_nred = reinterpret_cast<float*>(&s_v[1][1][0]);
+        uint32_t* ctr = a.counter + (size_t)hk * TI_SYNC_ATTN_STRIDE;
+        epoch = ti_pub_load(ctr + TI_SYNC_ATTN_EPOCH) + 1u;
+        uint64_t* pub = a.pub + (size_t)hk * (G + 2) * HD;
+        ActRegs<EPT, true> ar;
+        act_regs_load<MODE_NORM>(a.nin, ar);
+        // a unit's rows: local rows u*RS + sub + r*RPP (r < R); its matrix and first row
+        // are wave-uniform (selects of argument pointers stay scalar)
+        auto unit_rows = [&](int u, const uint4*& P, const uint16_t*& SC, int& grow0) {
+            const int lr0 = u * RS, seg = lr0 / HD;
+            P = seg < G ? a.wpk[0] : (seg == G ? a.wpk[1] : a.wpk[2]);
+            SC = seg < G ? a.wsc[0] : (seg == G ? a.wsc[1] : a.wsc[2]);
+            grow0 = (seg < G ? (hk * G + seg) * HD : hk * HD) + lr0 - seg * HD;
+        };
+        uint4 wq[R];
+        uint16_t sq[R];
+        const int gwv = w * 4 + wave, wstep = 4 * NS;
+        auto unit_load = [&](int j) {
+            int u = gwv + j * wstep;
+            u = u < NU ? u : NU - 1;                      // past the head's units: a repeat, unused
+            const uint4* P;
+            const uint16_t* SC;
+            int grow0;
+            unit_rows(u, P, SC, grow0);
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const size_t gi = (size_t)(grow0 + sub + r * RPP) * QL + li;
+                wq[r] = ti_ld_nt(P + gi);
+                sq[r] = __builtin_nontemporal_load(SC + gi);
+            }
+        };
+        unit_load(0);
+        first_tile(gw, kf, vf, sf);
+        pos_dev = (int)ti_pub_load(reinterpret_cast<const uint32_t*>(a.dpos));
+        TI_ISSUE_FENCE();
+        act_regs_quant<MODE_NORM>(a.nin, ar, s_xq, s_xs, s_nred);
+        ActQ8 act;
+        load_act_q8(s_xq, s_xs, li, act);
+        // the unit's R rows, summed over the QL lanes of each: lane li holds row li / SPAN
+        // (the same butterfly tree for every R, so the same bits as the stand-alone GEMV)
+        auto unit_dot = [&](const uint4 (&wu)[R], const uint16_t (&su)[R]) {
+            float ga[R];
+#pragma unroll
+            for (int r = 0; r < R; r++) ga[r] = fmaf((float)group_dot_q8(wu[r], act), ti_h2f(su[r]) * act.s, 0.0f);
+            return transpose_reduce<QL, R>(ga, li);
+        };
+        const int rounds = (NU + wstep - 1) / wstep;
+        for (int j = 0; j < rounds; j++) {
+            if (j > 0) unit_load(j);
+            const int u = gwv + j * wstep;
+            const float tot = unit_dot(wq, sq);
+            if (u < NU && li % SPAN == 0) {
+                const int lr = u * RS + sub + (li / SPAN) * RPP;
+                ti_pub_store(pub + lr, ((uint64_t)epoch << 32) | __builtin_bit_cast(uint32_t, tot));
+                const int seg = lr / HD;                  // plain copy: row of q, k or v
+                float* cp = seg < G ? a.qkv_copy[0] : (seg == G ? a.qkv_copy[1] : a.qkv_copy[2]);
+                if (cp) cp[(seg < G ? (hk * G + seg) * HD : hk * HD) + lr - seg * HD] = tot;
+            }
+        }
+        // this wave's row: q head (wave < G), k (wave 2) or v (wave 3); local rows cb..cb+127
+        // (the k and v rows only in the split that holds the position: no other reads them)
+        const int cb = (wave < 2 ? (wave < G ? wave : 0) : (wave == 2 ? G : G + 1)) * HD;
+        const int pos_e = a.dev ? pos_dev : a.pos;
+        const int ntiles_e = pos_e >= 0 && pos_e < a.cap ? (pos_e + PV_WT) / PV_WT : 0;
+        const bool need = wave < 2 || (ntiles_e > 0 && ((ntiles_e - 1) % NW) >> 2 == w);
+        uint64_t e0 = 0, e1 = 0;
+        bool got = !need;
+        for (int it = 0; need && it < ATTF_QKV_POLLS; it++) {
+            e0 = ti_pub_load(pub + cb + lane);
+            e1 = ti_pub_load(pub + cb + lane + 64);
+            got = __all((uint32_t)(e0 >> 32) == epoch && (uint32_t)(e1 >> 32) == epoch);
+            if (got) break;
+            __builtin_amdgcn_s_sleep(2);
+        }
+        if (got) {
+            x0 = __builtin_bit_cast(float, (uint32_t)e0);
+            x1 = __builtin_bit_cast(float, (uint32_t)e1);
+        } else {   // the wave's 128 rows here (LDS of its second K tile, unused until the loop)
+            float* fb = reinterpret_cast<float*>(&s_k[wave][1][0]);
+            for (int u = cb / RS; u < (cb + HD) / RS; u++) {
+                const uint4* P;
+                const uint16_t* SC;
+                int grow0;
+                unit_rows(u, P, SC, grow0);
+                uint4 wu[R];
+                uint16_t su[R];
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    const size_t gi = (size_t)(grow0 + sub + r * RPP) * QL + li;
+                    wu[r] = ti_ld_nt(P + gi);
+                    su[r] = __builtin_nontemporal_load(SC + gi);
+                }
+                const float tot = unit_dot(wu, su);
+                if (li % SPAN == 0) fb[u * RS + sub + (li / SPAN) * RPP - cb] = tot;
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            x0 = fb[lane];
+            x1 = fb[lane + 64];
+        }
+    }
 
     const int pos = a.dev ? pos_dev : a.pos;
     const bool valid = pos >= 0 && pos < a.cap;
@@ -1730,7 +1889,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_fused_pv(AttnFArgs a) {
         }
     }
     attn_merge_tail<HD, G, 1>(a, hk, w, NS, ntiles, valid, s_red, s_wml, s_ml, s_e, s_L, &s_last,
-                              reinterpret_cast<float*>(&s_k[2][0][0]));
+                              reinterpret_cast<float*>(&s_k[2][0][0]), epoch);
 }
 }  // namespace
 
@@ -1786,6 +1945,76 @@ int ti_attn_fused_launch(ti_ctx* c, const float* q, const float* k, const float*
     AF(64, 2) AF(64, 1)
 #undef AF
     return ti_fail(TI_ERR_INVALID, "fused attention: no kernel for hd=%d group=%d", hd, G);
+}
+
+int ti_fused_qkv_launch(ti_ctx*, const float*, const uint16_t*, float, int, int, const uint32_t* const*,
+                        const uint16_t* const*, float* const*, const int*, uint32_t*, float*);
+
+// The decode step's q/k/v projection and its attention as one launch (k_attn_fused_pv with
+// QL > 0): rmsnormQ(x) -> q, k, v rows (int4 GEMV) -> attnPrep + split-KV attention +
+// combine + quantQ8 of the output. Taken for head_dim 128, two query heads per KV head and
+// H = 1024 or 2048 (QL = H / 32 lanes per row) when the whole grid can be resident at once
+// (its workgroups wait for each other's rows); otherwise the q/k/v GEMV and the attention
+// run as two launches, with the same results. ys: q, k and v row buffers ([nHq*hd],
+// [nKv*hd] x 2), written by the two-launch path always and by the fused kernel when
+// copy_rows is set; xq_out / xs_out: the normed x's int8 codes (or null).
+bool ti_attn_qkv_ok(int nHq, int nKv, int hd, int H) {
+    return hd == 128 && nKv > 0 && nHq == 2 * nKv && (H == 1024 || H == 2048) && nKv <= TI_ATTN_COUNTERS &&
+           nKv * (nHq / nKv + 2) * hd <= TI_QKV_PUB_WORDS;
+}
+
+int ti_attn_qkv_launch(ti_ctx* c, const float* x, const uint16_t* in_norm, float in_eps, int H,
+                       const uint32_t* const* packs, const uint16_t* const* scs, float* const* ys, int copy_rows,
+                       uint32_t* xq_out, float* xs_out, const uint16_t* qw, const uint16_t* kw, uint32_t* kq,
+                       float* ks, uint32_t* vq, float* vs, float* out, int nHq, int nKv, int hd, const int* dpos,
+                       int cap, float theta, float eps, int max_splits, const float* rope_cur, uint32_t* oq,
+                       float* os, int kvs) {
+    auto two_launches = [&]() {
+        const int Ns[3] = {nHq * hd, nKv * hd, nKv * hd};
+        int rc = ti_fused_qkv_launch(c, x, in_norm, in_eps, H, 3, packs, scs, ys, Ns, xq_out, xs_out);
+        if (!rc) rc = ti_attn_fused_launch(c, ys[0], ys[1], ys[2], qw, kw, kq, ks, vq, vs, out, nHq, nKv, hd, dpos, 0,
+                                           cap, theta, eps, max_splits, rope_cur, oq, os, kvs);
+        return rc;
+    };
+    if (c->qkv_separate || !ti_attn_qkv_ok(nHq, nKv, hd, H) || !dpos || !rope_cur || kvs < nKv) return two_launches();
+    int NS = max_splits;
+    if (NS <= 0 || NS > ATTF_MAXS) NS = cap > ATTF_LONG_CAP ? ATTF_SPLITS_LONG : ATTF_SPLITS_SHORT;
+    const int wt = 4 * (64 / (hd / 16));
+    const int cap_splits = (cap + 4 * wt - 1) / (4 * wt);   // as ti_attn_fused_launch clamps it
+    if (NS > cap_splits) NS = cap_splits;
+    // rows per unit: the head's (G + 2) * hd rows as at most 4 NS units (one per wave of the
+    // head's workgroups), so that every unit is done in the first round whenever NS >= 16
+    // (and no row waits for a second); R rows per lane group, 64 / QL lane groups a wave
+    const int QL = H / 32, G = 2;
+    int RS = 2;
+    while (RS < 8 && (G + 2) * hd / RS > 4 * NS) RS *= 2;
+    const int QR = RS * QL / 64;
+    const void* fn = nullptr;
+#define QV(QL_, QR_) if (QL == QL_ && QR == QR_) fn = reinterpret_cast<const void*>(k_attn_fused_pv<2, QL_, QR_>);
+    QV(32, 1) QV(32, 2) QV(32, 4) QV(64, 2) QV(64, 4) QV(64, 8)
+#undef QV
+    int per_cu = 0;
+    if (fn) TI_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256, 0));
+    const long grid = (long)nKv * NS;
+    if (!fn || grid > (long)per_cu * c->cus) return two_launches();
+    AttnFArgs a = {nullptr, nullptr, nullptr, qw, kw, kq, ks, vq, vs, out, c->attn_po, c->attn_ml, c->sync + TI_SYNC_ATTN,
+                   dpos, rope_cur, 1, 0, nKv, NS, cap, kvs, eps, oq, os, {}};
+    a.nin = {x, in_norm, H, in_eps, xq_out, xs_out};
+    for (int i = 0; i < 3; i++) {
+        a.wpk[i] = reinterpret_cast<const uint4*>(packs[i]);
+        a.wsc[i] = scs[i];
+        a.qkv_copy[i] = copy_rows ? ys[i] : nullptr;
+    }
+    a.pub = c->qkv_pub;
+#define QV(QL_, QR_)                                                                      \
+    if (QL == QL_ && QR == QR_) {                                                         \
+        k_attn_fused_pv<2, QL_, QR_><<<dim3((unsigned)grid), 256, 0, c->stream>>>(a);       \
+        TI_LAUNCHED("k_attn_fused_pv (q/k/v)");                                           \
+        return TI_OK;                                                                     \
+    }
+    QV(32, 1) QV(32, 2) QV(32, 4) QV(64, 2) QV(64, 4) QV(64, 8)
+#undef QV
+    return two_launches();
 }
 
 extern "C" int ti_attn_step_q8(ti_ctx* c, const float* q, const float* k, const float* v, const uint16_t* qn_w,

@@ -348,4 +348,170 @@ __device__ __forceinline__ int q8_code(float v, float inv) {
 // SwiGLU of one row: silu(g) * u, silu(g) = g / (1 + e^-g)
 __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
 
+
+// ---- the activation prologue of the norm-fused GEMVs ---------------------------------
+// MODE_NORM: rmsnormQ of x (weight nw, eps); MODE_F32: quantQ8 of x; MODE_Q8: given codes.
+// A is the kernel's argument block: it supplies x, nw, K, eps and the optional copies
+// xq_out / xs_out of the codes (written by workgroup 0).
+enum { MODE_Q8 = 0, MODE_F32 = 1, MODE_NORM = 2 };
+
+// Register-resident variant of the prologue for the specialised kernels: thread t
+// holds elements t, t+256, ... (EPT of them), loaded before the weights so that one
+// memory round trip serves the whole prologue. The sum of squares keeps the
+// reference's order (per-thread strided partials, then the 128..1 tree); a 32-group
+// is 32 consecutive lanes, whose absmax is a 32-lane butterfly (max is exact in any
+// order), so every code and scale equals q8_group's.
+template <int EPT, bool FULL>
+struct ActRegs {
+    // CONTIG: K = 256*EPT (FULL) and EPT divides 32 or is a multiple of it. The quantizer
+    // then works on a second, contiguous copy (thread t: elements EPT*t .. EPT*t+EPT-1),
+    // so a 32-group spans 32/EPT neighbouring lanes and each thread computes its
+    // group's scale once; the strided copy only feeds the sum of squares.
+    static constexpr bool CONTIG = FULL && (EPT <= 32 ? (32 % EPT == 0) : (EPT % 32 == 0));
+    static constexpr int NC = CONTIG ? EPT : 1;
+    float x[EPT];
+    uint16_t w[EPT];
+    float xc[NC];
+    uint16_t wc[NC];
+};
+
+template <int MODE, int EPT, bool FULL, class A>
+__device__ __forceinline__ void act_regs_load(const A& a, ActRegs<EPT, FULL>& r) {
+    const int t = threadIdx.x;
+    // unconditional loads (clamped index, value masked after): straight-line code
+    // lets the compiler wait for exactly these loads, not the weights behind them
+#pragma unroll
+    for (int i = 0; i < EPT; i++) {
+        const int e = t + 256 * i;
+        const int ec = e < a.K ? e : a.K - 1;
+        r.x[i] = a.x[ec];
+        if (MODE == MODE_NORM) r.w[i] = a.nw[ec];
+    }
+    if constexpr (ActRegs<EPT, FULL>::CONTIG) {   // FULL: K = 256*EPT exactly
+        if constexpr (EPT % 4 == 0) {
+            const float4* xs4 = reinterpret_cast<const float4*>(a.x + (size_t)EPT * t);
+#pragma unroll
+            for (int i = 0; i < EPT / 4; i++) {
+                const float4 v = xs4[i];
+                r.xc[4 * i] = v.x; r.xc[4 * i + 1] = v.y; r.xc[4 * i + 2] = v.z; r.xc[4 * i + 3] = v.w;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < EPT; i++) r.xc[i] = a.x[(size_t)EPT * t + i];
+        }
+        if (MODE == MODE_NORM) {
+#pragma unroll
+            for (int i = 0; i < EPT; i++) r.wc[i] = a.nw[(size_t)EPT * t + i];
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < EPT; i++) {
+        if (t + 256 * i >= a.K) {
+            r.x[i] = 0.0f;
+            r.w[i] = 0;
+        }
+    }
+}
+
+template <int MODE, int EPT, bool FULL, class A>
+__device__ __forceinline__ void act_regs_quant(const A& a, ActRegs<EPT, FULL>& r, uint32_t* s_xq, float* s_xs,
+                                               float* red) {
+    const int t = threadIdx.x;
+    float inv_rms = 0.0f;
+    if (MODE == MODE_NORM) {
+        float s = 0.0f;
+#pragma unroll
+        for (int i = 0; i < EPT; i++) {
+            float sq = r.x[i] * r.x[i];
+            s = s + sq;
+        }
+        float m = ti_tree_sum_256(s, red) / (float)a.K;
+        m = m + a.eps;
+        inv_rms = 1.0f / sqrtf(m);
+    }
+    if constexpr (ActRegs<EPT, FULL>::CONTIG) {
+        float v[EPT];
+        float mx = 0.0f;
+#pragma unroll
+        for (int i = 0; i < EPT; i++) {
+            v[i] = r.xc[i];
+            if (MODE == MODE_NORM) {
+                const float p = v[i] * inv_rms;
+                v[i] = p * ti_h2f(r.wc[i]);
+            }
+        }
+        uint8_t* qb = reinterpret_cast<uint8_t*>(s_xq);
+        if constexpr (EPT <= 32) {
+#pragma unroll
+            for (int i = 0; i < EPT; i++) mx = fmaxf(mx, fabsf(v[i]));
+            mx = group_max_contig<EPT>(mx);
+            const float scale = mx / 127.0f;
+            const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
+            uint32_t wd[(EPT + 3) / 4] = {};
+#pragma unroll
+            for (int i = 0; i < EPT; i++) wd[i / 4] |= (uint32_t)(q8_code(v[i], inv) & 0xff) << (8 * (i % 4));
+            if constexpr (EPT >= 4) {
+#pragma unroll
+                for (int k = 0; k < EPT / 4; k++) s_xq[EPT / 4 * t + k] = wd[k];
+            } else {
+#pragma unroll
+                for (int i = 0; i < EPT; i++) qb[EPT * t + i] = (uint8_t)((wd[0] >> (8 * i)) & 0xff);
+            }
+            if (t % (32 / EPT) == 0) s_xs[EPT * t / 32] = scale;
+        } else {   // several whole groups per thread
+#pragma unroll
+            for (int g = 0; g < EPT / 32; g++) {
+                float gm = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 32; i++) gm = fmaxf(gm, fabsf(v[32 * g + i]));
+                const float scale = gm / 127.0f;
+                const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    uint32_t wd = 0;
+#pragma unroll
+                    for (int i = 0; i < 4; i++) wd |= (uint32_t)(q8_code(v[32 * g + 4 * k + i], inv) & 0xff) << (8 * i);
+                    s_xq[EPT / 4 * t + 8 * g + k] = wd;
+                }
+                s_xs[EPT / 32 * t + g] = scale;
+            }
+        }
+    } else {
+        if (MODE == MODE_NORM) {
+#pragma unroll
+            for (int i = 0; i < EPT; i++) {
+                float p = r.x[i] * inv_rms;
+                r.x[i] = p * ti_h2f(r.w[i]);
+            }
+        }
+        uint8_t* qb = reinterpret_cast<uint8_t*>(s_xq);
+        // EPT independent chains (group max, two IEEE divisions, rounding) computed
+        // without branches so they interleave; only the LDS stores are predicated
+        float gsc[EPT];
+        int gq[EPT];
+#pragma unroll
+        for (int i = 0; i < EPT; i++) {
+            const float mx = ti_max32_nonneg(fabsf(r.x[i]));
+            const float scale = mx / 127.0f;
+            const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
+            gsc[i] = scale;
+            gq[i] = q8_code(r.x[i], inv);
+        }
+#pragma unroll
+        for (int i = 0; i < EPT; i++) {
+            const int e = t + 256 * i;
+            if (e < a.K) {
+                qb[e] = (uint8_t)(gq[i] & 0xff);
+                if ((t & 31) == 0) s_xs[e >> 5] = gsc[i];
+            }
+        }
+    }
+    __syncthreads();
+    if (a.xq_out && blockIdx.x == 0) {
+        for (int i = t; i < a.K / 4; i += 256) a.xq_out[i] = s_xq[i];
+        for (int g = t; g < a.K / 32; g += 256) a.xs_out[g] = s_xs[g];
+    }
+}
+
+
 }  // namespace

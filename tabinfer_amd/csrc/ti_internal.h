@@ -11,6 +11,9 @@ int ti_hip_fail(hipError_t e, const char* what);
 
 struct ti_ctx {
     int device;
+    int cus;              // compute units of the device
+    int qkv_separate;     // TI_DECODE_QKV_SEPARATE set at ti_init: the decode step's q/k/v GEMV
+                          // and attention as two launches (same results; for A/B checks)
     hipStream_t stream;
     hipEvent_t ev[64];
     int capturing;
@@ -29,6 +32,8 @@ struct ti_ctx {
     uint32_t* moe_fill;
     uint32_t* moe_sidx;
     float* tg_part;       // split-K halves of the T-token projections ([TI_TG_SPLIT_BLOCKS][2][256])
+    uint64_t* qkv_pub;    // q/k/v rows handed between the workgroups of a decode attention
+                          // launch that computes them (value | epoch << 32; TI_QKV_PUB_WORDS)
     // device-scope counters of "last workgroup finishes the reduction" kernels;
     // zero between launches (each kernel's last workgroup resets its own)
     uint32_t* sync;
@@ -61,6 +66,8 @@ struct ti_graph {
 #define TI_SYNC_TGEMM 512         // split-K T-token projections: one counter per 16-row block
 #define TI_TG_SPLIT_BLOCKS 128    // (blocks of one split-K launch, at most)
 #define TI_SYNC_DUMMY 256         // 256 words never written: a valid read target for unused inputs
+#define TI_SYNC_ATTN_EPOCH 1      // word of a KV head's counter line: the epoch of its q/k/v hand-off
+#define TI_QKV_PUB_WORDS 16384    // KV heads x (query heads per KV head + 2) x head_dim, at most
 
 // ---- the T-token forward (2 <= T <= 16) ---------------------------------------------
 // Input of a T-token projection: int8 codes (xq [T][K/4], xs [T][K/32]) or, with x set,
@@ -350,6 +357,13 @@ __device__ __forceinline__ float ti_pub_load(const float* p) {
 }
 __device__ __forceinline__ uint32_t ti_pub_load(const uint32_t* p) {
     return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// 8-byte words (a value and the epoch it belongs to) as one naturally aligned access each
+__device__ __forceinline__ void ti_pub_store(uint64_t* p, uint64_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t ti_pub_load(const uint64_t* p) {
+    return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 // all of this thread's prior memory operations acknowledged (gfx9 encoding of
 // s_waitcnt vmcnt(0) expcnt(7) lgkmcnt(15))

@@ -36,6 +36,10 @@ int ti_fused_gateup_launch(ti_ctx*, const float*, const uint16_t*, float, const 
 int ti_fused_lmhead_launch(ti_ctx*, const float*, const uint16_t*, float, const uint32_t*, const uint16_t*, float*, int,
                            int, uint32_t*, int*, int, int, const float*, float*, int, uint32_t*);
 int ti_fused_kmax(int lm);
+int ti_attn_qkv_launch(ti_ctx*, const float*, const uint16_t*, float, int, const uint32_t* const*, const uint16_t* const*,
+                       float* const*, int, uint32_t*, float*, const uint16_t*, const uint16_t*, uint32_t*, float*,
+                       uint32_t*, float*, float*, int, int, int, const int*, int, float, float, int, const float*,
+                       uint32_t*, float*, int);
 
 // ---------------------------------------------------------------------------
 // glue kernels
@@ -542,10 +546,11 @@ extern "C" int ti_embed(ti_ctx* c, const int32_t* ids, const uint16_t* emb, floa
 }
 
 // One decode step at the device position (forward(null, pos, {chain: true}),
-// models/qwen3.js:3951-4055) in 2 + 5 x layers launches:
+// models/qwen3.js:3951-4055) in 2 + 4 x layers launches:
 //   embed(tok[pos])
-//   per layer: [rmsnormQ + q/k/v GEMVs]
-//              [attnPrep + split-KV attention + combine + quantQ8 of the output]
+//   per layer: [rmsnormQ + q/k/v GEMV + attnPrep + split-KV attention + combine +
+//               quantQ8 of the output] (the q/k/v rows handed between the attention's own
+//               workgroups, k_attn.hip; as two launches where that kernel does not apply)
 //              [o_proj GEMV + residual]
 //              [rmsnormQ + gate/up + SiLU + quantQ8 of swi]
 //              [down_proj GEMV + residual]
@@ -566,17 +571,15 @@ extern "C" int ti_qwen3_decode(ti_ctx* c, ti_qwen3* m) {
         const uint32_t* packs[3] = {y.q.pack, y.k.pack, y.v.pack};
         const uint16_t* scs[3] = {y.q.sc, y.k.sc, y.v.sc};
         float* ys[3] = {m->q, m->k, m->v};
-        const int Ns[3] = {nq, nkv, nkv};
         RC(trace_put(c, m, l, TR_X_IN, m->x, 1));
-        RC(ti_fused_qkv_launch(c, m->x, y.in_norm, C.rms_eps, H, 3, packs, scs, ys, Ns,
-                               tr ? trace_slot(m, l, TR_XN_Q) : nullptr,
-                               tr ? reinterpret_cast<float*>(trace_slot(m, l, TR_XN_S)) : nullptr));
+        RC(ti_attn_qkv_launch(c, m->x, y.in_norm, C.rms_eps, H, packs, scs, ys, tr ? 1 : 0,
+                              tr ? trace_slot(m, l, TR_XN_Q) : nullptr,
+                              tr ? reinterpret_cast<float*>(trace_slot(m, l, TR_XN_S)) : nullptr, y.q_norm, y.k_norm,
+                              y.kq, y.ks, y.vq, y.vs, m->attn, nHq, nKv, hd, m->dpos, C.max_ctx, C.rope_theta,
+                              C.rms_eps, decode_splits(m, m->pos_hint), m->rope_cur, m->xq, m->xs, m->kvs));
         RC(trace_put(c, m, l, TR_Q, m->q, 1));
         RC(trace_put(c, m, l, TR_K, m->k, 1));
         RC(trace_put(c, m, l, TR_V, m->v, 1));
-        RC(ti_attn_fused_launch(c, m->q, m->k, m->v, y.q_norm, y.k_norm, y.kq, y.ks, y.vq, y.vs, m->attn, nHq, nKv, hd,
-                                m->dpos, 0, C.max_ctx, C.rope_theta, C.rms_eps, decode_splits(m, m->pos_hint), m->rope_cur,
-                                m->xq, m->xs, m->kvs));
         RC(trace_put(c, m, l, TR_ATTN, m->attn, 1));
         RC(trace_put(c, m, l, TR_A_Q, m->xq, 1));
         RC(trace_put(c, m, l, TR_A_S, m->xs, 1));

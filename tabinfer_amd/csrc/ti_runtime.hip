@@ -30,7 +30,7 @@ extern "C" int ti_device_count(int* n) {
 // the stream, the host struct. Used by ti_shutdown and by every ti_init error path.
 static void destroy_ctx(ti_ctx* c) {
     void* ps[] = {c->act_q, c->act_s, c->act_sum, c->attn_po, c->attn_ml, c->amax_v, c->amax_i,
-                  c->moe_cnt, c->moe_off, c->moe_fill, c->moe_sidx, c->tg_part, c->sync};
+                  c->moe_cnt, c->moe_off, c->moe_fill, c->moe_sidx, c->tg_part, c->qkv_pub, c->sync};
     for (void* p : ps) if (p) (void)hipFree(p);
     for (int i = 0; i < 64; i++) if (c->ev[i]) (void)hipEventDestroy(c->ev[i]);
     if (c->stream) (void)hipStreamDestroy(c->stream);
@@ -53,6 +53,11 @@ extern "C" int ti_init(int device, ti_ctx** out) {
     ti_ctx* c = (ti_ctx*)calloc(1, sizeof(ti_ctx));
     if (!c) return ti_fail(TI_ERR_OOM, "ti_init: host allocation failed");
     c->device = device;
+    c->cus = prop.multiProcessorCount;
+    {
+        const char* sep = getenv("TI_DECODE_QKV_SEPARATE");
+        c->qkv_separate = sep && *sep && strcmp(sep, "0") != 0;
+    }
     hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
     if (e != hipSuccess) { c->stream = nullptr; destroy_ctx(c); return ti_hip_fail(e, "hipStreamCreateWithFlags"); }
     for (int i = 0; i < 64; i++) {
@@ -72,6 +77,7 @@ extern "C" int ti_init(int device, ti_ctx** out) {
         {(void**)&c->moe_fill, (size_t)TI_MOE_E_MAX * 4},
         {(void**)&c->moe_sidx, (size_t)TI_MOE_P_MAX * 4},
         {(void**)&c->tg_part, (size_t)TI_TG_SPLIT_BLOCKS * 2 * 256 * 4},
+        {(void**)&c->qkv_pub, (size_t)TI_QKV_PUB_WORDS * 8},
         {(void**)&c->sync, (size_t)TI_SYNC_WORDS * 4},
     };
     for (auto& a : allocs) {
@@ -80,6 +86,7 @@ extern "C" int ti_init(int device, ti_ctx** out) {
     }
     e = hipMemset(c->moe_cnt, 0, TI_MOE_E_MAX * 4);
     if (e == hipSuccess) e = hipMemset(c->sync, 0, TI_SYNC_WORDS * 4);
+    if (e == hipSuccess) e = hipMemset(c->qkv_pub, 0, (size_t)TI_QKV_PUB_WORDS * 8);   // epoch 0: never current
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) { destroy_ctx(c); return ti_hip_fail(e, "ti_init scratch clear"); }
     *out = c;
