@@ -896,6 +896,7 @@ struct AttnFArgs {
     const uint16_t* wsc[3];
     uint64_t* pub;
     float* qkv_copy[3];
+    int qkv_polls;         // poll rounds before a wave computes its rows itself
 };
 
 // RMSNorm over one head row held by 128 threads (j = element, 0 past hd) in the
@@ -1596,7 +1597,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_fused_pv(AttnFArgs a) {
         const bool need = wave < 2 || (ntiles_e > 0 && ((ntiles_e - 1) % NW) >> 2 == w);
         uint64_t e0 = 0, e1 = 0;
         bool got = !need;
-        for (int it = 0; need && it < ATTF_QKV_POLLS; it++) {
+        for (int it = 0; need && it < a.qkv_polls; it++) {
             e0 = ti_pub_load(pub + cb + lane);
             e1 = ti_pub_load(pub + cb + lane + 64);
             got = __all((uint32_t)(e0 >> 32) == epoch && (uint32_t)(e1 >> 32) == epoch);
@@ -2006,6 +2007,7 @@ int ti_attn_qkv_launch(ti_ctx* c, const float* x, const uint16_t* in_norm, float
         a.qkv_copy[i] = copy_rows ? ys[i] : nullptr;
     }
     a.pub = c->qkv_pub;
+    a.qkv_polls = c->qkv_polls >= 0 ? c->qkv_polls : ATTF_QKV_POLLS;
 #define QV(QL_, QR_)                                                                      \
     if (QL == QL_ && QR == QR_) {                                                         \
         k_attn_fused_pv<2, QL_, QR_><<<dim3((unsigned)grid), 256, 0, c->stream>>>(a);       \

@@ -14,6 +14,8 @@ struct ti_ctx {
     int cus;              // compute units of the device
     int qkv_separate;     // TI_DECODE_QKV_SEPARATE set at ti_init: the decode step's q/k/v GEMV
                           // and attention as two launches (same results; for A/B checks)
+    int qkv_polls;        // rounds a wave polls for its q/k/v rows before computing them itself
+                          // (TI_DECODE_QKV_POLLS at ti_init; 0 takes that path at once, for tests)
     hipStream_t stream;
     hipEvent_t ev[64];
     int capturing;

@@ -57,6 +57,8 @@ extern "C" int ti_init(int device, ti_ctx** out) {
     {
         const char* sep = getenv("TI_DECODE_QKV_SEPARATE");
         c->qkv_separate = sep && *sep && strcmp(sep, "0") != 0;
+        const char* polls = getenv("TI_DECODE_QKV_POLLS");
+        c->qkv_polls = polls && *polls ? atoi(polls) : -1;   // -1: the kernel's own bound
     }
     hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
     if (e != hipSuccess) { c->stream = nullptr; destroy_ctx(c); return ti_hip_fail(e, "hipStreamCreateWithFlags"); }

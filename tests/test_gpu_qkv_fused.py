@@ -7,8 +7,11 @@ two-launch path is the one a context takes with TI_DECODE_QKV_SEPARATE set at ti
 Both decoders start from the same weights, tokens and seeded KV prefix and take three
 chained decode steps: logits, next tokens and the new KV rows must be identical. The
 cases cover both projection widths (hidden 1024: 32 lanes a row; 2048: 64) and split
-counts that give every number of row units per wave (1 to 4) and, with a 256-position
-cache (2 splits per KV head), several rounds of units per wave."""
+counts that give every row-unit size (2, 4 and 8 rows) and, with a 256-position cache
+(2 splits per KV head), several rounds of units per wave. A third context is created
+with TI_DECODE_QKV_POLLS=0: its waves never wait for the rows another workgroup
+publishes and compute their own (the path a wave takes when its poll gives up), which
+must give the same bits too."""
 import os
 
 import numpy as np
@@ -32,19 +35,26 @@ def _weights(H):
     return _W[H]
 
 
-@pytest.fixture(scope="module")
-def ctx_pair():
-    fused = abi.Ctx(0)
-    old = os.environ.get("TI_DECODE_QKV_SEPARATE")
-    os.environ["TI_DECODE_QKV_SEPARATE"] = "1"
+def _ctx_with(var, value):
+    old = os.environ.get(var)
+    os.environ[var] = value
     try:
-        sep = abi.Ctx(0)
+        return abi.Ctx(0)
     finally:
         if old is None:
-            del os.environ["TI_DECODE_QKV_SEPARATE"]
+            del os.environ[var]
         else:
-            os.environ["TI_DECODE_QKV_SEPARATE"] = old
-    yield fused, sep
+            os.environ[var] = old
+
+
+@pytest.fixture(scope="module")
+def ctx_pair():
+    """(fused, three launches, fused with every wave computing its own q/k/v rows)"""
+    fused = abi.Ctx(0)
+    sep = _ctx_with("TI_DECODE_QKV_SEPARATE", "1")
+    own = _ctx_with("TI_DECODE_QKV_POLLS", "0")
+    yield fused, sep, own
+    own.close()
     sep.close()
     fused.close()
 
@@ -73,25 +83,29 @@ def test_decode_fused_qkv_same_bits(ctx_pair, H, P, cap):
         for step in range(3):
             for m in ms:
                 m.decode()
-            la = ctx_pair[0].download(ms[0].logits_ptr(), np.float32, cfg["vocab"])
             lb = ctx_pair[1].download(ms[1].logits_ptr(), np.float32, cfg["vocab"])
-            assert np.isfinite(la).all()
-            assert np.array_equal(la.view(np.uint32), lb.view(np.uint32)), "step %d: logits differ" % step
-        ta, tb = ms[0].read_tokens(P + 1, 3), ms[1].read_tokens(P + 1, 3)
-        assert np.array_equal(ta, tb)
+            assert np.isfinite(lb).all()
+            for k in (0, 2):
+                la = ctx_pair[k].download(ms[k].logits_ptr(), np.float32, cfg["vocab"])
+                assert np.array_equal(la.view(np.uint32), lb.view(np.uint32)), "context %d step %d: logits differ" % (k, step)
+        tb = ms[1].read_tokens(P + 1, 3)
+        for k in (0, 2):
+            assert np.array_equal(ms[k].read_tokens(P + 1, 3), tb)
         for l in range(cfg["layers"]):
-            ka, kb = ms[0].kv(l), ms[1].kv(l)
-            for i in range(4):
-                if i % 2 == 0:
-                    a = TF.read_kv_codes(ctx_pair[0], ms[0], ka[i], P, 3, cfg)
-                    b = TF.read_kv_codes(ctx_pair[1], ms[1], kb[i], P, 3, cfg)
-                else:
-                    n = 3 * cfg["n_kv_heads"] * cfg["head_dim"] // 32
-                    off = P * cfg["n_kv_heads"] * cfg["head_dim"] // 32 * 4
-                    a = ctx_pair[0].download(ka[i], np.float32, n, off=off)
-                    b = ctx_pair[1].download(kb[i], np.float32, n, off=off)
-                assert np.array_equal(np.asarray(a).view(np.uint32), np.asarray(b).view(np.uint32)), \
-                    "layer %d KV buffer %d differs" % (l, i)
+            kb = ms[1].kv(l)
+            for k in (0, 2):
+                ka = ms[k].kv(l)
+                for i in range(4):
+                    if i % 2 == 0:
+                        a = TF.read_kv_codes(ctx_pair[k], ms[k], ka[i], P, 3, cfg)
+                        b = TF.read_kv_codes(ctx_pair[1], ms[1], kb[i], P, 3, cfg)
+                    else:
+                        n = 3 * cfg["n_kv_heads"] * cfg["head_dim"] // 32
+                        off = P * cfg["n_kv_heads"] * cfg["head_dim"] // 32 * 4
+                        a = ctx_pair[k].download(ka[i], np.float32, n, off=off)
+                        b = ctx_pair[1].download(kb[i], np.float32, n, off=off)
+                    assert np.array_equal(np.asarray(a).view(np.uint32), np.asarray(b).view(np.uint32)), \
+                        "context %d layer %d KV buffer %d differs" % (k, l, i)
     finally:
         for m in ms:
             m.close()
