@@ -7,9 +7,10 @@
 //
 // int3 group (32 weights): three u32 bitplanes, bit i of plane b = bit b of (q3 + 4) for
 // element i, then one f16 scale; rows of all experts stacked expert-major (row = e*N + n).
-// The kernels turn 4 elements' plane bits into 4 bytes of (q3 + 4) with the bit-spread
-// multiply ((b >> i) & 15) * 0x00204081 & 0x01010101 (bit k lands at bit 8k) and dot them
-// with v_dot4_i32_i8; the +4 offset is removed once per group from the activation sum.
+// The kernels turn a group's three planes into eight words of (q3 + 4) bytes, word c
+// holding elements c, c+8, c+16, c+24 (q3_cols), and dot them with v_dot4_i32_i8 against
+// activation words packed in the same order; the +4 offset is removed once per group from
+// the activation sum. The int32 group dot is the same integer in any element order.
 #include "ti_dev.h"
 
 namespace {
@@ -134,8 +135,8 @@ __global__ __launch_bounds__(64) void k_router(const float* __restrict__ logits,
 }
 
 // the router (workgroups 0 .. T-1, one per token) and, in the same launch, quantAct8 of
-// the normed rows (the remaining workgroups, a 32-group per thread): the two do not depend
-// on each other
+// the normed rows (the remaining workgroups, a 32-group per thread, words in
+// k_moe_gemm_q3's element order): the two do not depend on each other
 __global__ __launch_bounds__(64) void k_router_quant(const float* __restrict__ logits, const float* __restrict__ bias,
                                                      int nE, int topk, int32_t* __restrict__ idx, float* __restrict__ wt,
                                                      int T, const float* __restrict__ x, uint32_t* __restrict__ xq,
@@ -148,22 +149,35 @@ __global__ __launch_bounds__(64) void k_router_quant(const float* __restrict__ l
     if (gi >= ng) return;
     float v[32];
     load32(x + (size_t)gi * 32, v);
-    q8_group(v, xq + (size_t)gi * 8, xs + gi, nullptr);
+    q8_group<true>(v, xq + (size_t)gi * 8, xs + gi, nullptr);
 }
 
 // ---- decode: pair-indexed GEMV with the f32 activation ----------------------------
-// 4 elements' (q3 + 4) as bytes from the three planes' bits i..i+3
-__device__ __forceinline__ uint32_t q3_bytes(uint32_t b0, uint32_t b1, uint32_t b2, int i) {
-    const uint32_t s0 = (((b0 >> i) & 15u) * 0x00204081u) & 0x01010101u;
-    const uint32_t s1 = (((b1 >> i) & 15u) * 0x00204081u) & 0x01010101u;
-    const uint32_t s2 = (((b2 >> i) & 15u) * 0x00204081u) & 0x01010101u;
-    return s0 | (s1 << 1) | (s2 << 2);
+// A group's (q3 + 4) codes as bytes, q[c] byte i = element 8i + c. Elements 4t + r
+// (r = 0..3, t = 0..7) take plane bit positions 4t + r; gathering plane b's bits of one r
+// beside each other gives X_r with element 4t + r's code in nibble t (bits 4t + r + b for
+// r < 2, shifted down by 2 for r >= 2 so nothing leaves the word), then q[4h + r] is
+// nibbles h, h+2, h+4, h+6 of X_r, one per byte. 36 VALU operations per 32 codes.
+__device__ __forceinline__ void q3_cols(uint32_t b0, uint32_t b1, uint32_t b2, uint32_t (&q)[8]) {
+    constexpr uint32_t M = 0x11111111u, B = 0x07070707u;
+    const uint32_t x0 = (b0 & M) | ((b1 & M) << 1) | ((b2 & M) << 2);
+    const uint32_t x1 = (b0 & (M << 1)) | ((b1 & (M << 1)) << 1) | ((b2 & (M << 1)) << 2);
+    const uint32_t x2 = ((b0 & (M << 2)) >> 2) | ((b1 & (M << 2)) >> 1) | (b2 & (M << 2));
+    const uint32_t x3 = ((b0 & (M << 3)) >> 2) | ((b1 & (M << 3)) >> 1) | (b2 & (M << 3));
+    q[0] = x0 & B;
+    q[4] = (x0 >> 4) & B;
+    q[1] = (x1 >> 1) & B;
+    q[5] = (x1 >> 5) & B;
+    q[2] = x2 & B;
+    q[6] = (x2 >> 4) & B;
+    q[3] = (x3 >> 1) & B;
+    q[7] = (x3 >> 5) & B;
 }
 
 // f32 activation group as exact fixed point (as k_gemv_q4_f32): x_j = X_j * 2^(ex-22),
-// X = l2*65536 + l1*256 + l0 with signed int8 limbs, natural element order
+// X = l2*65536 + l1*256 + l0 with signed int8 limbs, words in q3_cols's element order
 struct Limbs {
-    int l[3][8];        // limb, word of 4 elements
+    int l[3][8];        // limb, word c = elements c, c+8, c+16, c+24
     int sum[3];         // sum of each limb over the 32 elements
     float S;            // 2^(ex-22)
 };
@@ -190,9 +204,9 @@ __device__ __forceinline__ void make_limbs(const float* v, Limbs& L) {
         int s = 0;
 #pragma unroll
         for (int w = 0; w < 8; w++) {
-            L.l[q][w] = (int)((uint32_t)(b[q][4 * w] & 0xff) | ((uint32_t)(b[q][4 * w + 1] & 0xff) << 8) |
-                              ((uint32_t)(b[q][4 * w + 2] & 0xff) << 16) | ((uint32_t)(b[q][4 * w + 3] & 0xff) << 24));
-            s += b[q][4 * w] + b[q][4 * w + 1] + b[q][4 * w + 2] + b[q][4 * w + 3];
+            L.l[q][w] = (int)((uint32_t)(b[q][w] & 0xff) | ((uint32_t)(b[q][w + 8] & 0xff) << 8) |
+                              ((uint32_t)(b[q][w + 16] & 0xff) << 16) | ((uint32_t)(b[q][w + 24] & 0xff) << 24));
+            s += b[q][w] + b[q][w + 8] + b[q][w + 16] + b[q][w + 24];
         }
         L.sum[q] = s;
     }
@@ -201,12 +215,12 @@ __device__ __forceinline__ void make_limbs(const float* v, Limbs& L) {
 // sum_i (q3_i) * x_i over one group, q3 = stored - 4
 __device__ __forceinline__ float group_dot_q3_limbs(uint32_t b0, uint32_t b1, uint32_t b2, const Limbs& L) {
     int d[3] = {0, 0, 0};
+    uint32_t q[8];
+    q3_cols(b0, b1, b2, q);
 #pragma unroll
-    for (int w = 0; w < 8; w++) {
-        const int q = (int)q3_bytes(b0, b1, b2, 4 * w);
+    for (int w = 0; w < 8; w++)
 #pragma unroll
-        for (int k = 0; k < 3; k++) d[k] = __builtin_amdgcn_sdot4(q, L.l[k][w], d[k], false);
-    }
+        for (int k = 0; k < 3; k++) d[k] = __builtin_amdgcn_sdot4((int)q[w], L.l[k][w], d[k], false);
     const int t = (d[2] - 4 * L.sum[2]) * 256 + (d[1] - 4 * L.sum[1]);   // |t| < 2^24
     return fmaf((float)t, 256.0f, (float)(d[0] - 4 * L.sum[0])) * L.S;
 }
@@ -270,8 +284,9 @@ __global__ __launch_bounds__(256) void k_moe_gemv_q3(const float* __restrict__ x
 // ---- T > 1: rows of one expert against all pairs routed to it ----------------------
 // grid (row blocks of 16, experts). The workgroup scans the routing ids 256 at a time and
 // lists its expert's pairs in pair order (ballot compaction in LDS). Each wave turns its 4
-// rows' bitplanes into (q + 4) bytes, kept in registers; the listed pairs then read their
-// int8 activation groups (L2-resident) and scales, four pairs' loads in flight at once:
+// rows' bitplanes into (q + 4) bytes (q3_cols), kept in registers; the listed pairs then
+// read their int8 activation groups (L2-resident, words in the same element order) and
+// scales, four pairs' loads in flight at once:
 //   dot = sum (q + 4) a - 4 sum a   (exact int32),   y[pair, n] = sum_g dot * s_x * s_w.
 // spec (most experts are routed to, as at 16 tokens x top-4 over 32 experts): the weight
 // loads are issued before the scan, so their round trip overlaps it; otherwise they wait
@@ -337,8 +352,7 @@ __global__ __launch_bounds__(256) void k_moe_gemm_q3(const uint32_t* __restrict_
                 for (int h = 0; h < GL; h++) {
                     const int g = lane + 64 * h;
                     sw[r][h] = g < gpr ? ti_h2f(sr[r][h]) : 0.0f;
-#pragma unroll
-                    for (int w = 0; w < 8; w++) qb[r][h][w] = q3_bytes(pb[r][h][0], pb[r][h][1], pb[r][h][2], 4 * w);
+                    q3_cols(pb[r][h][0], pb[r][h][1], pb[r][h][2], qb[r][h]);
                 }
         }
         for (int i0 = 0; i0 < tot; i0 += MOE_PB) {
@@ -454,16 +468,19 @@ __device__ __forceinline__ void unpack_limbs(const LimbsPacked& d, Limbs& L) {
     L.sum[0] = t.x; L.sum[1] = t.y; L.sum[2] = t.z; L.S = __int_as_float(t.w);
 }
 
-// make_limbs of one 32-element group shared by TPG adjacent lanes, each converting 32/TPG
-// consecutive elements (part = the lane's index among them): the group's max through a
-// butterfly over the TPG lanes, then the same per-element conversion, words and sums as
-// make_limbs (so the same bits). Every lane of the TPG must take part.
+// make_limbs of one 32-element group shared by TPG adjacent lanes, each converting the
+// 32/TPG elements of words part*CPW .. part*CPW + CPW-1 (part = the lane's index among
+// them): the group's max through a butterfly over the TPG lanes, then the same
+// per-element conversion, words and sums as make_limbs (so the same bits). Every lane of
+// the TPG must take part.
 template <int TPG>
 __device__ __forceinline__ void coop_limbs(const float* grp, int part, LimbsPacked& d) {
-    constexpr int EPT = 32 / TPG;
-    float v[EPT];
+    constexpr int EPT = 32 / TPG, CPW = 8 / TPG;
+    float v[EPT];   // v[4j + i] = element part*CPW + j + 8i
 #pragma unroll
-    for (int i = 0; i < EPT; i++) v[i] = grp[part * EPT + i];
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < CPW; j++) v[4 * j + i] = grp[part * CPW + j + 8 * i];
     float mx = 0.0f;
 #pragma unroll
     for (int i = 0; i < EPT; i++) mx = fmaxf(mx, fabsf(v[i]));
@@ -474,7 +491,7 @@ __device__ __forceinline__ void coop_limbs(const float* grp, int part, LimbsPack
     int* out = reinterpret_cast<int*>(&d);
     int sum[3] = {0, 0, 0};
 #pragma unroll
-    for (int j = 0; j < EPT / 4; j++) {
+    for (int j = 0; j < CPW; j++) {
         uint32_t word[3] = {0u, 0u, 0u};
 #pragma unroll
         for (int e = 0; e < 4; e++) {
@@ -491,7 +508,7 @@ __device__ __forceinline__ void coop_limbs(const float* grp, int part, LimbsPack
             sum[2] += l2;
         }
 #pragma unroll
-        for (int q = 0; q < 3; q++) out[8 * q + part * (EPT / 4) + j] = (int)word[q];
+        for (int q = 0; q < 3; q++) out[8 * q + part * CPW + j] = (int)word[q];
     }
 #pragma unroll
     for (int o = 1; o < TPG; o <<= 1)
@@ -795,8 +812,6 @@ extern "C" int ti_router(ti_ctx* c, const float* logits, const float* bias, int 
     return TI_OK;
 }
 
-int ti_quant_act_q8_async(ti_ctx* c, const float* x, uint32_t* xq, float* xs, int32_t* xsum, int groups);
-
 extern "C" int ti_moe_gemv_q3(ti_ctx* c, const float* x, const uint32_t* p3, const uint16_t* s3, const int32_t* idx,
                               float* y, int pairs, int N, int K, int in_stride, int xdiv, int nE) {
     TI_CHECK_CTX(c);
@@ -823,9 +838,12 @@ extern "C" int ti_moe_gemm_q3(ti_ctx* c, const float* src, int src_rows, const u
                (P - 1) / src_div, src_rows);
     TI_REQUIRE((long)src_rows * K <= (long)TI_ACT_CAP * TI_ACT_TMAX, "ti_moe_gemm_q3: src_rows*K=%ld exceeds %ld",
                (long)src_rows * K, (long)TI_ACT_CAP * TI_ACT_TMAX);
-    // quantAct8 (lfm25.js:1487-1494): per row, per 32-group int8 into the context's scratch
-    int rc = ti_quant_act_q8_async(c, src, c->act_q, c->act_s, nullptr, src_rows * (K / 32));
-    if (rc) return rc;
+    // quantAct8 (lfm25.js:1487-1494): per row, per 32-group int8 into the context's scratch,
+    // words in the GEMM's element order (k_router_quant with no router workgroups)
+    const int nq = src_rows * (K / 32);
+    k_router_quant<<<(unsigned)((nq + 63) / 64), 64, 0, c->stream>>>(nullptr, nullptr, 0, 0, nullptr, nullptr, 0, src,
+                                                                     c->act_q, c->act_s, nq);
+    TI_LAUNCHED("k_router_quant (quantizer only)");
     dim3 grid((unsigned)((N + 15) / 16), (unsigned)nE);
     const int spec = 2 * P >= nE;   // most experts are routed to: weights loaded before the scan
     if (K <= 2048) k_moe_gemm_q3<1><<<grid, 256, 0, c->stream>>>(c->act_q, c->act_s, p3, s3, ridx, y, P, N, K, src_div, spec, p3, s3, y);
@@ -835,7 +853,8 @@ extern "C" int ti_moe_gemm_q3(ti_ctx* c, const float* src, int src_rows, const u
 }
 
 // quantAct8 of swiglu(g, u) (lfm25.js:1831-1847 then :1487-1494): group gi's 32 values
-// a / (1 + e^-a) * u with k_swiglu_f32's operations, written to act as well, then q8_group.
+// a / (1 + e^-a) * u with k_swiglu_f32's operations, written to act as well, then q8_group
+// (words in k_moe_gemm_q3's element order).
 __global__ __launch_bounds__(64) void k_quant_swiglu_q8(const float* __restrict__ g, const float* __restrict__ u,
                                                         float* __restrict__ act, uint32_t* __restrict__ xq,
                                                         float* __restrict__ xs, int ng) {
@@ -852,7 +871,7 @@ __global__ __launch_bounds__(64) void k_quant_swiglu_q8(const float* __restrict_
     float4* ao = reinterpret_cast<float4*>(act + (size_t)gi * 32);
 #pragma unroll
     for (int j = 0; j < 8; j++) ao[j] = make_float4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
-    q8_group(v, xq + (size_t)gi * 8, xs + gi, nullptr);
+    q8_group<true>(v, xq + (size_t)gi * 8, xs + gi, nullptr);
 }
 
 extern "C" int ti_moe_prefill_q3(ti_ctx* c, float* x, const float* normed, const float* logits, const float* bias,

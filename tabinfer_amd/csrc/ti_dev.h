@@ -254,8 +254,10 @@ __device__ __forceinline__ float group_dot_limbs(const uint4 w, const ActLimb& a
 // ---------------------------------------------------------------------------
 // one thread per 32-group. scale = absmax/127, inv = 1/scale (0 if the
 // group is zero), q = clamp(round-half-even(v*inv), -127, 127); the per-16
-// sums feed the ternary identity.
+// sums feed the ternary identity. Word w holds elements 4w..4w+3; with COLS,
+// elements w, w+8, w+16, w+24 (the order the int3 expert kernels dot in).
 // ---------------------------------------------------------------------------
+template <bool COLS = false>
 __device__ __forceinline__ void q8_group(const float* v, uint32_t* xq, float* xs, int32_t* xsum16) {
     float mx = 0.0f;
 #pragma unroll
@@ -273,9 +275,11 @@ __device__ __forceinline__ void q8_group(const float* v, uint32_t* xq, float* xs
     }
     uint32_t wds[8];
 #pragma unroll
-    for (int w = 0; w < 8; w++)
-        wds[w] = (uint32_t)(q[4 * w] & 0xff) | ((uint32_t)(q[4 * w + 1] & 0xff) << 8) |
-                 ((uint32_t)(q[4 * w + 2] & 0xff) << 16) | ((uint32_t)(q[4 * w + 3] & 0xff) << 24);
+    for (int w = 0; w < 8; w++) {
+        const int st = COLS ? 8 : 1, e0 = COLS ? w : 4 * w;
+        wds[w] = (uint32_t)(q[e0] & 0xff) | ((uint32_t)(q[e0 + st] & 0xff) << 8) |
+                 ((uint32_t)(q[e0 + 2 * st] & 0xff) << 16) | ((uint32_t)(q[e0 + 3 * st] & 0xff) << 24);
+    }
     uint4* o = reinterpret_cast<uint4*>(xq);
     o[0] = make_uint4(wds[0], wds[1], wds[2], wds[3]);
     o[1] = make_uint4(wds[4], wds[5], wds[6], wds[7]);
