@@ -325,13 +325,19 @@ __global__ __launch_bounds__(256) void k_moe_gemm_q3(const uint32_t* __restrict_
             }
         }
     };
+    // the first chunk's routing ids are loaded before the weights, so that the scan waits
+    // for them alone; at GL = 1 the first pairs' activation loads are then issued before the
+    // codes are expanded, and their round trip overlaps the weights' (at GL = 2 the codes
+    // and four pairs' activations together would not fit in the registers)
+    constexpr bool ACT_FIRST = GL == 1;
+    const int rid0 = tid < P ? ridx[tid] : -1;
     if (spec) wload();
     uint32_t qb[MOE_R][GL][8];
     float sw[MOE_R][GL];
     bool have = false;
     for (int c0 = 0; c0 < P; c0 += 256) {
         const int p = c0 + tid;
-        const bool hit = p < P && ridx[p] == e;
+        const bool hit = p < P && (c0 == 0 ? rid0 : ridx[p]) == e;
         const uint64_t m = __ballot(hit);
         __syncthreads();                                    // the previous chunk's list is consumed
         if (lane == 0) s_wcnt[wave] = __popcll(m);
@@ -343,9 +349,8 @@ __global__ __launch_bounds__(256) void k_moe_gemm_q3(const uint32_t* __restrict_
         if (hit) s_list[base + __popcll(m & ((1ull << lane) - 1ull))] = p;
         __syncthreads();
         if (tot == 0) continue;
-        if (!have) {
-            have = true;
-            if (!spec) wload();
+        if (!have && !spec) wload();
+        auto expand = [&]() {
 #pragma unroll
             for (int r = 0; r < MOE_R; r++)
 #pragma unroll
@@ -354,6 +359,10 @@ __global__ __launch_bounds__(256) void k_moe_gemm_q3(const uint32_t* __restrict_
                     sw[r][h] = g < gpr ? ti_h2f(sr[r][h]) : 0.0f;
                     q3_cols(pb[r][h][0], pb[r][h][1], pb[r][h][2], qb[r][h]);
                 }
+        };
+        if (!ACT_FIRST && !have) {
+            have = true;
+            expand();
         }
         for (int i0 = 0; i0 < tot; i0 += MOE_PB) {
             uint4 u0[MOE_PB][GL], u1[MOE_PB][GL];
@@ -372,6 +381,10 @@ __global__ __launch_bounds__(256) void k_moe_gemm_q3(const uint32_t* __restrict_
                     u1[q][h] = a4[1];
                     as[q][h] = xs[(size_t)src * gpr + gc];
                 }
+            }
+            if (ACT_FIRST && !have) {                       // workgroup-uniform
+                have = true;
+                expand();
             }
 #pragma unroll
             for (int q = 0; q < MOE_PB; q++) {
