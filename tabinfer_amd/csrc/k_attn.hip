@@ -1477,10 +1477,22 @@ __global__ __launch_bounds__(256, 2) void k_attn_fused_pv(AttnFArgs a) {
     // lane L holds elements L and L + 64, so RMSNorm, RoPE and the limb split of q run in
     // registers
     const uint16_t* nwrow = wave < 2 ? a.qw : a.kw;
-    // The device position is read with a vector load issued behind the first tile's: as a
-    // scalar load at the top it held every vector load of the prologue for its own round
-    // trip (the compiler waits for all scalar loads before the first vector one).
-    int pos_dev = 0;
+    // The device position is read with a vector load issued behind the first tile's, and
+    // the value is held opaque (an empty asm that rewrites the register) until it is
+    // needed: as a scalar load at the top it held every vector load of the prologue for
+    // its own round trip (the compiler waits for all scalar loads before the first vector
+    // one), and a use the compiler is free to hoist (a readfirstlane right after the load)
+    // makes the wave wait for every load issued before it, the first tile's included,
+    // before the prologue's arithmetic. Without a device position the load reads a word
+    // that is always there, unused.
+    uint32_t pos_raw = 0;
+    auto pos_load = [&]() {
+        pos_raw = ti_pub_load(a.dev ? reinterpret_cast<const uint32_t*>(a.dpos) : a.counter);
+    };
+    auto pos_now = [&]() {
+        asm volatile("" : "+v"(pos_raw));
+        return a.dev ? (int)pos_raw : a.pos;
+    };
     // the first tile through registers, bounded by the capacity until the context is known
     // (a load straight to LDS in flight would make the prologue's waits full ones)
     uint4 kf[4], vf[4], sf;
@@ -1509,7 +1521,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_fused_pv(AttnFArgs a) {
     const float c_arg = a.rope_row[lane], s_arg = a.rope_row[lane + 64];
     if constexpr (QL == 0) {
         first_tile(gw, kf, vf, sf);
-        pos_dev = (int)ti_pub_load(reinterpret_cast<const uint32_t*>(a.dpos));
+        pos_load();
         TI_ISSUE_FENCE();
     } else {
         // ---- q, k and v of this KV head, computed by its NS workgroups together.
@@ -1563,7 +1575,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_fused_pv(AttnFArgs a) {
         };
         unit_load(0);
         first_tile(gw, kf, vf, sf);
-        pos_dev = (int)ti_pub_load(reinterpret_cast<const uint32_t*>(a.dpos));
+        pos_load();
         TI_ISSUE_FENCE();
         act_regs_quant<MODE_NORM>(a.nin, ar, s_xq, s_xs, s_nred);
         ActQ8 act;
@@ -1592,7 +1604,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_fused_pv(AttnFArgs a) {
         // this wave's row: q head (wave < G), k (wave 2) or v (wave 3); local rows cb..cb+127
         // (the k and v rows only in the split that holds the position: no other reads them)
         const int cb = (wave < 2 ? (wave < G ? wave : 0) : (wave == 2 ? G : G + 1)) * HD;
-        const int pos_e = a.dev ? pos_dev : a.pos;
+        const int pos_e = pos_now();
         const int ntiles_e = pos_e >= 0 && pos_e < a.cap ? (pos_e + PV_WT) / PV_WT : 0;
         const bool need = wave < 2 || (ntiles_e > 0 && ((ntiles_e - 1) % NW) >> 2 == w);
         uint64_t e0 = 0, e1 = 0;
@@ -1633,7 +1645,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_fused_pv(AttnFArgs a) {
         }
     }
 
-    const int pos = a.dev ? pos_dev : a.pos;
+    const int pos = pos_now();
     const bool valid = pos >= 0 && pos < a.cap;
     const int S = valid ? pos + 1 : 0;
     const int ntiles = (S + PV_WT - 1) / PV_WT;
