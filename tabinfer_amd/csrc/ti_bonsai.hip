@@ -181,10 +181,12 @@ __host__ __device__ inline int bn_chunk(int cap) {
 
 // workgroup (KV head hk, split of CH keys), the G = 2 query heads of hk (hd 128):
 //  prologue (model.rs:399-418): q of both heads scaled by 1/scale, per-head RMSNorm (the sum
-//          of squares as a 64..1 tree), the q_norm weight and split-half RoPE at position P,
-//          into LDS (every workgroup); the workgroup whose split holds P also forms K (scaled,
-//          k_norm, RoPE) and V (scaled) of hk at P, stores them into the cache and waits for
-//          the stores before it loads its keys (no other workgroup reads row P);
+//          of squares as a 64..1 tree), the q_norm weight and split-half RoPE at position P
+//          (the rotary row kept beside the device position), into LDS (every workgroup), with
+//          the first 64 keys' K and V rows already in flight; the workgroup whose split holds
+//          P also forms K (scaled, k_norm, RoPE) and V (scaled) of hk at P, stores them into
+//          the cache for later tokens and uses them from LDS for its own key P (no other
+//          workgroup reads row P);
 //  scores: 4 lanes per key, 32 dims each (8 float4 loads a lane, in flight together), a quad
 //          sum, 64 keys per pass;
 //  max / exp / sum over the split's keys;
@@ -193,9 +195,9 @@ __host__ __device__ inline int bn_chunk(int cap) {
 //  partials (o, m, l) per (query head, split).
 // RMSNorm of one head row held one element per thread (the 128 threads with act, element
 // i, LDS slots from `base`): the sum of squares as a 64..1 tree in red, then split-half RoPE
-// from the table row. Every thread of the workgroup calls it (it holds barriers); only
-// those with act write.
-__device__ __forceinline__ float bn_head_norm_rope(float a, int i, float nw, const float* tab, float eps, float* red,
+// with the rotary row's cos c and sin s of element i's pair. Every thread of the workgroup
+// calls it (it holds barriers); only those with act write.
+__device__ __forceinline__ float bn_head_norm_rope(float a, int i, float nw, float c, float s, float eps, float* red,
                                                    float* y, int base, bool act) {
     constexpr int HD = 128, half = HD / 2;
     if (act) red[base + i] = a * a;
@@ -209,7 +211,6 @@ __device__ __forceinline__ float bn_head_norm_rope(float a, int i, float nw, con
     if (act) y[base + i] = a * rinv * nw;
     __syncthreads();
     const int j = i < half ? i : i - half;
-    const float c = tab[j], s = tab[half + j];
     const float x0 = y[base + j], x1 = y[base + half + j];
     return i < half ? x0 * c - x1 * s : x1 * c + x0 * s;
 }
@@ -218,57 +219,73 @@ template <int CH>
 __global__ __launch_bounds__(256) void k_bn_attn(const float* __restrict__ qraw, const float* __restrict__ kraw,
                                                  const float* __restrict__ vraw, const float* __restrict__ act_scale,
                                                  const float* __restrict__ qn, const float* __restrict__ kn,
-                                                 const float* __restrict__ rope, float eps, float* __restrict__ kc,
+                                                 const float* __restrict__ rope_cur, float eps, float* __restrict__ kc,
                                                  float* __restrict__ vc, const int* __restrict__ dpos, int nKv,
                                                  float* __restrict__ po, float* __restrict__ pml, int ns_stride, int cap) {
-    constexpr int G = 2, HD = 128;
+    constexpr int G = 2, HD = 128, half = HD / 2;
     __shared__ float sc[G][CH];
     __shared__ float4 so[8][G][HD / 4];
     __shared__ float red[G][4];
     __shared__ __align__(16) float s_q[G][HD];
+    __shared__ __align__(16) float s_kp[HD];           // K and V of row P (the own split)
+    __shared__ __align__(16) float s_vp[HD];
     __shared__ float s_red[G * HD], s_y[G * HD];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int hk = blockIdx.x % nKv, split = blockIdx.x / nKv;
-    const int P = *dpos;
-    const int S = min(P + 1, cap);
     const int c0 = split * CH;
-    if (c0 >= S) return;                               // the merge reads splits below ceil(S / CH) only
-    const int n = min(CH, S - c0);
-    const bool own = P < cap && P < c0 + CH;           // this split holds row P: it writes K, V there first
     const size_t kvd = (size_t)nKv * HD;
     const float scale = 1.0f / sqrtf((float)HD);
     const int qd = t & 3;
-    // prologue loads: raw q of both heads (thread t: head t / 128, dim t % 128), the scale,
-    // the norm weight and the rope row of P; the own split's K, V raw rows as well
     const int pg = t >> 7, pi = t & 127;
-    const float inv = 1.0f / *act_scale;
-    const float qa = qraw[(size_t)(hk * G + pg) * HD + pi] * inv;
-    const float qnw = qn[pi];
-    const float* tab = rope + (size_t)(P < cap ? P : 0) * HD;
-    // the V rows of the first 64 keys, for the P V pass below, issued before the K loads so
-    // that both tiles are in flight together (one memory round trip instead of two); the
-    // own split issues them after its stores of row P have landed
     const int kg = t >> 5, d4 = t & 31;
-    const float4* vb = reinterpret_cast<const float4*>(vc + (size_t)c0 * kvd + (size_t)hk * HD) + d4;
-    float4 vpre[8];
-    auto vload = [&]() {
+    // ---- every load in one batch, none of them waiting for the position: raw q (thread t:
+    // head t / 128, dim t % 128), the activation scale, the norm weights, the rotary row of
+    // the device position (kept beside it by the kernels that move it), the new token's raw K
+    // (threads 0..127) or V (128..255) row of hk, the first 64 keys' K rows (4 lanes a key,
+    // 32 dims each) and V rows (as the P V pass reads them), clamped to the cache; the
+    // position last, its value held opaque until it is needed (a use hoisted next to the
+    // load would wait for every load issued before it). Rows past the split's keys are
+    // loaded and never used.
+    const float qr = qraw[(size_t)(hk * G + pg) * HD + pi];
+    const float asc = ti_pub_load(act_scale);           // a vector load: no scalar wait before the others
+    const float qnw = qn[pi], knw = kn[pi];
+    const int jr = pi < half ? pi : pi - half;
+    const float rc = rope_cur[jr], rs = rope_cur[half + jr];
+    const float kvr = (pg == 0 ? kraw : vraw)[(size_t)hk * HD + pi];
+    float4 kpre[8], vpre[8];
+    {
+        const int key = min(c0 + (t >> 2), cap - 1);
+        const float4* kr = reinterpret_cast<const float4*>(kc + (size_t)key * kvd + (size_t)hk * HD + qd * 32);
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int j = kg + 8 * i;
-            vpre[i] = vb[(size_t)(j < n ? j : n - 1) * (kvd / 4)];
-        }
-    };
-    if (!own) vload();
-    s_q[pg][pi] = bn_head_norm_rope(qa, pi, qnw, tab, eps, s_red, s_y, pg * HD, true);
-    if (own) {   // K (threads 0..127) and V (128..255) of hk at P (model.rs:405-418)
+        for (int i = 0; i < 8; i++) kpre[i] = kr[i];
+    }
+    const float4* vb = reinterpret_cast<const float4*>(vc + (size_t)c0 * kvd + (size_t)hk * HD) + d4;
+#pragma unroll
+    for (int i = 0; i < 8; i++) vpre[i] = vb[(size_t)(min(c0 + kg + 8 * i, cap - 1) - c0) * (kvd / 4)];
+    uint32_t praw = ti_pub_load(reinterpret_cast<const uint32_t*>(dpos));
+    TI_ISSUE_FENCE();
+    const float inv = 1.0f / asc;
+    s_q[pg][pi] = bn_head_norm_rope(qr * inv, pi, qnw, rc, rs, eps, s_red, s_y, pg * HD, true);
+    asm volatile("" : "+v"(praw));
+    const int P = (int)praw;
+    const int S = min(P + 1, cap);
+    if (c0 >= S) return;                               // the merge reads splits below ceil(S / CH) only
+    const int n = min(CH, S - c0);
+    const bool own = P < cap && P < c0 + CH;           // this split holds row P: it writes K, V there
+    if (own) {   // K (threads 0..127) and V (128..255) of hk at P (model.rs:405-418): into the cache
+        // for later tokens, and through LDS for this split's own key P (its cache row may not
+        // have landed before the loads above, which were issued before it was formed)
         const size_t row = (size_t)P * kvd + (size_t)hk * HD + pi;
         __syncthreads();   // every thread has read the q tree's slots
-        const float kr = bn_head_norm_rope(kraw[(size_t)hk * HD + pi] * inv, pi, kn[pi], tab, eps, s_red, s_y, 0, pg == 0);
-        if (pg == 0) kc[row] = kr;
-        else vc[row] = vraw[(size_t)hk * HD + pi] * inv;
-        ti_stores_done();
-        __syncthreads();
-        vload();
+        const float kr = bn_head_norm_rope(kvr * inv, pi, knw, rc, rs, eps, s_red, s_y, 0, pg == 0);
+        if (pg == 0) {
+            kc[row] = kr;
+            s_kp[pi] = kr;
+        } else {
+            const float vv = kvr * inv;
+            vc[row] = vv;
+            s_vp[pi] = vv;
+        }
     }
     __syncthreads();
     float4 q[G][8];
@@ -276,13 +293,22 @@ __global__ __launch_bounds__(256) void k_bn_attn(const float* __restrict__ qraw,
     for (int g = 0; g < G; g++)
 #pragma unroll
         for (int i = 0; i < 8; i++) q[g][i] = reinterpret_cast<const float4*>(&s_q[g][qd * 32])[i];
+    const int jp = own ? P - c0 : -1;                  // the split's key P, if it holds it
     for (int k0 = 0; k0 < n; k0 += 64) {
         const int j = k0 + (t >> 2);
         const int key = c0 + (j < n ? j : n - 1);
-        const float4* kr = reinterpret_cast<const float4*>(kc + (size_t)key * kvd + (size_t)hk * HD + qd * 32);
         float4 kv[8];
+        if (k0 == 0) {
 #pragma unroll
-        for (int i = 0; i < 8; i++) kv[i] = kr[i];
+            for (int i = 0; i < 8; i++) kv[i] = kpre[i];
+        } else {
+            const float4* kr = reinterpret_cast<const float4*>(kc + (size_t)key * kvd + (size_t)hk * HD + qd * 32);
+#pragma unroll
+            for (int i = 0; i < 8; i++) kv[i] = kr[i];
+        }
+        if (j == jp)
+#pragma unroll
+            for (int i = 0; i < 8; i++) kv[i] = reinterpret_cast<const float4*>(&s_kp[qd * 32])[i];
         float part[G];
 #pragma unroll
         for (int g = 0; g < G; g++) {
@@ -335,23 +361,25 @@ __global__ __launch_bounds__(256) void k_bn_attn(const float* __restrict__ qraw,
     float4 o[G];
 #pragma unroll
     for (int g = 0; g < G; g++) o[g] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const float4 vp = reinterpret_cast<const float4*>(s_vp)[d4];   // used only by the own split
 #pragma unroll
     for (int i = 0; i < 8; i++) {                      // keys kg + 8i < 64: the prefetched rows
         const int j = kg + 8 * i;
         if (j < n) {
+            const float4 vv = j == jp ? vp : vpre[i];
 #pragma unroll
             for (int g = 0; g < G; g++) {
                 const float p = sc[g][j];
-                o[g].x = fmaf(p, vpre[i].x, o[g].x);
-                o[g].y = fmaf(p, vpre[i].y, o[g].y);
-                o[g].z = fmaf(p, vpre[i].z, o[g].z);
-                o[g].w = fmaf(p, vpre[i].w, o[g].w);
+                o[g].x = fmaf(p, vv.x, o[g].x);
+                o[g].y = fmaf(p, vv.y, o[g].y);
+                o[g].z = fmaf(p, vv.z, o[g].z);
+                o[g].w = fmaf(p, vv.w, o[g].w);
             }
         }
     }
 #pragma unroll 4
     for (int j = kg + 64; j < n; j += 8) {
-        const float4 vv = vb[(size_t)j * (kvd / 4)];
+        const float4 vv = j == jp ? vp : vb[(size_t)j * (kvd / 4)];
 #pragma unroll
         for (int g = 0; g < G; g++) {
             const float p = sc[g][j];
@@ -509,10 +537,13 @@ __global__ __launch_bounds__(256) void k_bn_logits(const float* __restrict__ raw
 }
 
 __global__ __launch_bounds__(BN_AMAX_PARTS) void k_bn_argmax(const float* __restrict__ pv, const int* __restrict__ pi, int parts,
-                                                            uint32_t* __restrict__ hist, int* __restrict__ dpos, int cap) {
+                                                            uint32_t* __restrict__ hist, int* __restrict__ dpos, int cap,
+                                                            const float* __restrict__ rope, float* __restrict__ rope_cur,
+                                                            int hd) {
     __shared__ float sv[BN_AMAX_PARTS];
     __shared__ int si[BN_AMAX_PARTS];
     const int t = threadIdx.x;
+    const int P = *dpos;   // every thread, before thread 0 advances it (barriers below)
     sv[t] = t < parts ? pv[t] : -INFINITY;
     si[t] = t < parts ? pi[t] : 0x7fffffff;
     __syncthreads();
@@ -527,14 +558,27 @@ __global__ __launch_bounds__(BN_AMAX_PARTS) void k_bn_argmax(const float* __rest
         __syncthreads();
     }
     if (t == 0) {
-        const int P = *dpos;
         if (P + 1 <= cap) hist[P + 1] = (uint32_t)(sv[0] > -INFINITY ? si[0] : 0);
         *dpos = P + 1;
     }
+    for (int i = t; i < hd; i += BN_AMAX_PARTS)
+        if (P + 1 < cap) rope_cur[i] = rope[(size_t)(P + 1) * hd + i];
 }
 
-__global__ void k_bn_advance(int* __restrict__ dpos) { *dpos = *dpos + 1; }
-__global__ void k_bn_set_pos(int* __restrict__ dpos, int pos) { *dpos = pos; }
+// device position + 1 and its rotary row (one workgroup, hd threads or more)
+__global__ void k_bn_advance(int* __restrict__ dpos, const float* __restrict__ rope, float* __restrict__ rope_cur, int hd,
+                             int cap) {
+    const int P = *dpos;
+    __syncthreads();   // every thread has read it
+    if (threadIdx.x == 0) *dpos = P + 1;
+    if ((int)threadIdx.x < hd && P + 1 < cap) rope_cur[threadIdx.x] = rope[(size_t)(P + 1) * hd + threadIdx.x];
+}
+// device position := pos, and its rotary row
+__global__ void k_bn_set_pos(int* __restrict__ dpos, int pos, const float* __restrict__ rope, float* __restrict__ rope_cur,
+                             int hd, int cap) {
+    if (threadIdx.x == 0) *dpos = pos;
+    if ((int)threadIdx.x < hd && pos < cap) rope_cur[threadIdx.x] = rope[(size_t)pos * hd + threadIdx.x];
+}
 
 __global__ void k_bn_copy_u32(const uint32_t* __restrict__ s, uint32_t* __restrict__ d, long n) {
     const long stride = (long)gridDim.x * blockDim.x;
@@ -570,6 +614,7 @@ struct ti_bonsai {
     uint32_t* hist;
     int* dpos;
     float* rope;          // [max_ctx][head_dim]: cos then sin of each position (ops.rs rope_table)
+    float* rope_cur;      // the row of the device position, kept in step with dpos
     uint32_t* trace = nullptr;
     std::vector<void*> allocs;
 };
@@ -685,6 +730,7 @@ extern "C" int ti_bonsai_create(ti_ctx* c, const ti_bonsai_config* cfg, ti_bonsa
     if (!rc) rc = bmk(m, (void**)&m->hist, (size_t)(C.max_ctx + 1) * 4);
     if (!rc) rc = bmk(m, (void**)&m->dpos, 4);
     if (!rc) rc = bmk(m, (void**)&m->rope, (size_t)C.max_ctx * hd * 4);
+    if (!rc) rc = bmk(m, (void**)&m->rope_cur, (size_t)hd * 4);
     if (!rc) {
         // ops.rs:79-90 in f32 with the platform's powf / cosf / sinf, the functions Rust's
         // f32::powf and sin_cos call on Linux
@@ -698,6 +744,7 @@ extern "C" int ti_bonsai_create(ti_ctx* c, const ti_bonsai_config* cfg, ti_bonsa
                 tab[(size_t)p * hd + half + i] = sinf(ang);
             }
         hipError_t e = hipMemcpy(m->rope, tab.data(), tab.size() * 4, hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = hipMemcpy(m->rope_cur, tab.data(), (size_t)hd * 4, hipMemcpyHostToDevice);   // position 0
         if (e == hipSuccess) e = hipMemset(m->hist, 0, (size_t)(C.max_ctx + 1) * 4);
         if (e == hipSuccess) e = hipMemset(m->dpos, 0, 4);
         if (e == hipSuccess) e = hipDeviceSynchronize();
@@ -840,7 +887,7 @@ extern "C" int ti_bonsai_logits(ti_bonsai* m, float** logits) {
 extern "C" int ti_bonsai_set_pos(ti_ctx* c, ti_bonsai* m, int pos) {
     TI_CHECK_CTX(c);
     TI_REQUIRE(m && pos >= 0 && pos < m->cfg.max_ctx, "ti_bonsai_set_pos: pos %d out of [0, %d)", pos, m ? m->cfg.max_ctx : 0);
-    k_bn_set_pos<<<1, 1, 0, c->stream>>>(m->dpos, pos);
+    k_bn_set_pos<<<1, 256, 0, c->stream>>>(m->dpos, pos, m->rope, m->rope_cur, m->cfg.head_dim, m->cfg.max_ctx);
     TI_LAUNCHED("k_bn_set_pos");
     return TI_OK;
 }
@@ -928,7 +975,7 @@ static int bonsai_step(ti_ctx* c, ti_bonsai* m, bool want_logits) {
             RC(bput(c, m, l, B_V, m->vraw));
         }
         const int chunk = bn_chunk(C.max_ctx);
-#define BA(CH_) k_bn_attn<CH_><<<nKv * nsplit, 256, 0, c->stream>>>(m->qraw, m->kraw, m->vraw, sa, y.q_norm, y.k_norm, m->rope, \
+#define BA(CH_) k_bn_attn<CH_><<<nKv * nsplit, 256, 0, c->stream>>>(m->qraw, m->kraw, m->vraw, sa, y.q_norm, y.k_norm, m->rope_cur, \
                                                                     C.rms_eps, y.kc, y.vc, m->dpos, nKv, m->po, m->pml, nsplit, C.max_ctx)
         if (chunk == 64) BA(64);
         else if (chunk == 128) BA(128);
@@ -999,7 +1046,7 @@ static int bonsai_step(ti_ctx* c, ti_bonsai* m, bool want_logits) {
     if (!want_logits) {
         // a prompt token: its KV rows are written; the residual restarts at the next
         // token's embedding, so nothing past the last layer is computed (model.rs:486-490)
-        k_bn_advance<<<1, 1, 0, c->stream>>>(m->dpos);
+        k_bn_advance<<<1, 256, 0, c->stream>>>(m->dpos, m->rope, m->rope_cur, hd, C.max_ctx);
         TI_LAUNCHED("k_bn_advance");
         return TI_OK;
     }
@@ -1016,7 +1063,8 @@ static int bonsai_step(ti_ctx* c, ti_bonsai* m, bool want_logits) {
     RC(ti_tern_gemv(c, m->lraw, m->lm.codes, m->lm.scales, m->act, m->xsum, C.vocab, H));
     k_bn_logits<<<BN_AMAX_PARTS, 256, 0, c->stream>>>(m->lraw, sa, C.vocab, m->logits, m->amax_v, m->amax_i);
     TI_LAUNCHED("k_bn_logits");
-    k_bn_argmax<<<1, BN_AMAX_PARTS, 0, c->stream>>>(m->amax_v, m->amax_i, BN_AMAX_PARTS, m->hist, m->dpos, C.max_ctx);
+    k_bn_argmax<<<1, BN_AMAX_PARTS, 0, c->stream>>>(m->amax_v, m->amax_i, BN_AMAX_PARTS, m->hist, m->dpos, C.max_ctx, m->rope,
+                                                    m->rope_cur, hd);
     TI_LAUNCHED("k_bn_argmax");
     return TI_OK;
 #undef RC
