@@ -188,8 +188,12 @@ __global__ __launch_bounds__(64 * TA_W) void k_attn_tq8(TAttnArgs a) {
         s_ql[r][lane] = (_Float16)(o0 - (float)h0);
         s_ql[r][lane + 64] = (_Float16)(o1 - (float)h1);
     }
-    // ---- the new keys: K normed + roped, V as is; snorm int8 into the cache row S0 + t
-    // and into the new-key tile (the last region); its rows T..31 are zero
+    // ---- the new keys: K normed + roped, V as is; snorm int8 into the new-key tile (the
+    // last region; its rows T..31 are zero) and, after the block loop, into the cache row
+    // S0 + t (no other workgroup reads those rows in this launch; a global store here would
+    // wait for a slot behind the block loads in flight)
+    uint32_t nkw[KPW][2];
+    float nks[KPW][2];
     if (tail_wg) {
         uint8_t* kt = kt_base + TA_W * TA_KBYTES;
         uint8_t* vt = vt_base + TA_W * TA_VBYTES;
@@ -205,25 +209,18 @@ __global__ __launch_bounds__(64 * TA_W) void k_attn_tq8(TAttnArgs a) {
                 const float mx1 = fmaxf(ti_max32_nonneg(fabsf(o1)), 1e-12f);
                 const uint32_t wd0 = ti_quad_or(snorm_code(o0, mx0) << (8 * (lane & 3)));
                 const uint32_t wd1 = ti_quad_or(snorm_code(o1, mx1) << (8 * (lane & 3)));
-                const size_t row = (size_t)(S0 + t) * a.nKv + hk, crow = (size_t)(S0 + t) * a.kvs + hk;
-                uint32_t* gq = reinterpret_cast<uint32_t*>((isv ? a.vq : a.kq) + crow * HD);
-                float* gs = (isv ? a.vs : a.ks) + row * NG;
                 uint8_t* lt = (isv ? vt + t * TA_VS : kt + t * TA_KS);
                 float* lsc = isv ? &s_vs[TA_W][t][0] : &s_ks[TA_W][t][0];
                 const float lm = isv ? 1.0f : qk2;
+                nkw[i][0] = wd0;
+                nkw[i][1] = wd1;
+                nks[i][0] = mx0;
+                nks[i][1] = mx1;
                 if ((lane & 3) == 0) {
-                    if (rt == 0) {                        // one row tile writes the cache
-                        gq[lane / 4] = wd0;
-                        gq[16 + lane / 4] = wd1;
-                    }
                     *reinterpret_cast<uint32_t*>(lt + lane) = wd0;
                     *reinterpret_cast<uint32_t*>(lt + 64 + lane) = wd1;
                 }
                 if ((lane & 31) == 0) {
-                    if (rt == 0) {
-                        gs[lane / 32] = mx0;
-                        gs[2 + lane / 32] = mx1;
-                    }
                     lsc[lane / 32] = mx0 * lm;
                     lsc[2 + lane / 32] = mx1 * lm;
                 }
@@ -381,6 +378,27 @@ __global__ __launch_bounds__(64 * TA_W) void k_attn_tq8(TAttnArgs a) {
         process(wave, S0 - k0, false);
     }
     if (gw == tail_gw) process(TA_W, T, true);
+    if (tail_wg && rt == 0) {   // the new keys into the cache (one row tile writes them)
+#pragma unroll
+        for (int i = 0; i < KPW; i++) {
+            const int jb = wave + TA_W * i;
+            if (jb < 2 * T) {                             // wave-uniform
+                const bool isv = jb >= T;
+                const int t = isv ? jb - T : jb;
+                const size_t row = (size_t)(S0 + t) * a.nKv + hk, crow = (size_t)(S0 + t) * a.kvs + hk;
+                uint32_t* gq = reinterpret_cast<uint32_t*>((isv ? a.vq : a.kq) + crow * HD);
+                float* gs = (isv ? a.vs : a.ks) + row * NG;
+                if ((lane & 3) == 0) {
+                    gq[lane / 4] = nkw[i][0];
+                    gq[16 + lane / 4] = nkw[i][1];
+                }
+                if ((lane & 31) == 0) {
+                    gs[lane / 32] = nks[i][0];
+                    gs[2 + lane / 32] = nks[i][1];
+                }
+            }
+        }
+    }
 
     // ---- merge the waves into the split's partial (plain stores: the combine kernel
     // that reads them runs after this launch)
