@@ -238,40 +238,50 @@ __global__ __launch_bounds__(256) void k_bn_attn(const float* __restrict__ qraw,
     const int qd = t & 3;
     const int pg = t >> 7, pi = t & 127;
     const int kg = t >> 5, d4 = t & 31;
-    // ---- every load in one batch, none of them waiting for the position: raw q (thread t:
+    // ---- the prologue's loads: the device position first (a vector load: as a scalar one it
+    // would hold every vector load behind the kernel arguments' wait), then raw q (thread t:
     // head t / 128, dim t % 128), the activation scale, the norm weights, the rotary row of
-    // the device position (kept beside it by the kernels that move it), the new token's raw K
-    // (threads 0..127) or V (128..255) row of hk, the first 64 keys' K rows (4 lanes a key,
-    // 32 dims each) and V rows (as the P V pass reads them), clamped to the cache; the
-    // position last, its value held opaque until it is needed (a use hoisted next to the
-    // load would wait for every load issued before it). Rows past the split's keys are
-    // loaded and never used.
-    const float qr = qraw[(size_t)(hk * G + pg) * HD + pi];
-    const float asc = ti_pub_load(act_scale);           // a vector load: no scalar wait before the others
-    const float qnw = qn[pi], knw = kn[pi];
+    // the device position (kept beside it by the kernels that move it) and the new token's
+    // raw K (threads 0..127) or V (128..255) row of hk, none of which waits for the position;
+    // once the position is known (its own round trip, overlapping theirs), a split past the
+    // context leaves, and the others request the first 64 keys' V rows (as the P V pass reads
+    // them) and, for one-pass splits, K rows (4 lanes a key, 32 dims each) before the norm.
+    const uint32_t praw = ti_pub_load(reinterpret_cast<const uint32_t*>(dpos));
+    float qr = qraw[(size_t)(hk * G + pg) * HD + pi];
+    float asc = ti_pub_load(act_scale);                 // a vector load: no scalar wait before the others
+    float qnw = qn[pi], knw = kn[pi];
     const int jr = pi < half ? pi : pi - half;
-    const float rc = rope_cur[jr], rs = rope_cur[half + jr];
-    const float kvr = (pg == 0 ? kraw : vraw)[(size_t)hk * HD + pi];
+    float rc = rope_cur[jr], rs = rope_cur[half + jr];
+    float kvr = (pg == 0 ? kraw : vraw)[(size_t)hk * HD + pi];
+    uint32_t pv = praw;
+    // every load above is issued, and has landed, before the exit test (the compiler would
+    // otherwise sink them past it, behind the position's round trip)
+    asm volatile("" : "+v"(pv), "+v"(qr), "+v"(asc), "+v"(qnw), "+v"(knw), "+v"(rc), "+v"(rs), "+v"(kvr));
+    const int P = (int)pv;
+    const int S = min(P + 1, cap);
+    if (c0 >= S) return;                               // the merge reads splits below ceil(S / CH) only
+    const int n = min(CH, S - c0);
+    const bool own = P < cap && P < c0 + CH;           // this split holds row P: it writes K, V there
+    // the first pass's K rows are prefetched only when the split is one pass (CH = 64): with
+    // more, the prefetched rows and the second pass's together cost a wave per SIMD
+    constexpr bool KPRE = CH == 64;
     float4 kpre[8], vpre[8];
-    {
-        const int key = min(c0 + (t >> 2), cap - 1);
-        const float4* kr = reinterpret_cast<const float4*>(kc + (size_t)key * kvd + (size_t)hk * HD + qd * 32);
+    if (KPRE) {
+        const int j = t >> 2;
+        const float4* kr = reinterpret_cast<const float4*>(kc + (size_t)(c0 + (j < n ? j : n - 1)) * kvd +
+                                                           (size_t)hk * HD + qd * 32);
 #pragma unroll
         for (int i = 0; i < 8; i++) kpre[i] = kr[i];
     }
     const float4* vb = reinterpret_cast<const float4*>(vc + (size_t)c0 * kvd + (size_t)hk * HD) + d4;
 #pragma unroll
-    for (int i = 0; i < 8; i++) vpre[i] = vb[(size_t)(min(c0 + kg + 8 * i, cap - 1) - c0) * (kvd / 4)];
-    uint32_t praw = ti_pub_load(reinterpret_cast<const uint32_t*>(dpos));
+    for (int i = 0; i < 8; i++) {
+        const int j = kg + 8 * i;
+        vpre[i] = vb[(size_t)(j < n ? j : n - 1) * (kvd / 4)];
+    }
     TI_ISSUE_FENCE();
     const float inv = 1.0f / asc;
     s_q[pg][pi] = bn_head_norm_rope(qr * inv, pi, qnw, rc, rs, eps, s_red, s_y, pg * HD, true);
-    asm volatile("" : "+v"(praw));
-    const int P = (int)praw;
-    const int S = min(P + 1, cap);
-    if (c0 >= S) return;                               // the merge reads splits below ceil(S / CH) only
-    const int n = min(CH, S - c0);
-    const bool own = P < cap && P < c0 + CH;           // this split holds row P: it writes K, V there
     if (own) {   // K (threads 0..127) and V (128..255) of hk at P (model.rs:405-418): into the cache
         // for later tokens, and through LDS for this split's own key P (its cache row may not
         // have landed before the loads above, which were issued before it was formed)
@@ -298,7 +308,7 @@ __global__ __launch_bounds__(256) void k_bn_attn(const float* __restrict__ qraw,
         const int j = k0 + (t >> 2);
         const int key = c0 + (j < n ? j : n - 1);
         float4 kv[8];
-        if (k0 == 0) {
+        if (KPRE && k0 == 0) {
 #pragma unroll
             for (int i = 0; i < 8; i++) kv[i] = kpre[i];
         } else {
@@ -379,7 +389,9 @@ __global__ __launch_bounds__(256) void k_bn_attn(const float* __restrict__ qraw,
     }
 #pragma unroll 4
     for (int j = kg + 64; j < n; j += 8) {
-        const float4 vv = j == jp ? vp : vb[(size_t)j * (kvd / 4)];
+        const float4 vl = vb[(size_t)j * (kvd / 4)];    // always loaded: the select below stays a
+        const bool mine = j == jp;                         // value select, and the loads pipeline
+        const float4 vv = make_float4(mine ? vp.x : vl.x, mine ? vp.y : vl.y, mine ? vp.z : vl.z, mine ? vp.w : vl.w);
 #pragma unroll
         for (int g = 0; g < G; g++) {
             const float p = sc[g][j];
