@@ -1995,16 +1995,18 @@ int ti_attn_qkv_launch(ti_ctx* c, const float* x, const uint16_t* in_norm, float
     const int wt = 4 * (64 / (hd / 16));
     const int cap_splits = (cap + 4 * wt - 1) / (4 * wt);   // as ti_attn_fused_launch clamps it
     if (NS > cap_splits) NS = cap_splits;
-    // rows per unit: the head's (G + 2) * hd rows as at most 4 NS units (one per wave of the
-    // head's workgroups), so that every unit is done in the first round whenever NS >= 16
-    // (and no row waits for a second); R rows per lane group, 64 / QL lane groups a wave
+    // rows per unit: 4, or 8 where 4-row units would not fit in one round (at most 4 NS units,
+    // one per wave of the head's workgroups), so that every unit is done in the first round
+    // whenever NS >= 16 (and no row waits for a second); 2-row units at 64 splits, where they
+    // also fit, measured 1% slower at 32k than 4-row ones (a wave's poll waits on more of
+    // them). R rows per lane group, 64 / QL lane groups a wave
     const int QL = H / 32, G = 2;
-    int RS = 2;
+    int RS = 4;
     while (RS < 8 && (G + 2) * hd / RS > 4 * NS) RS *= 2;
     const int QR = RS * QL / 64;
     const void* fn = nullptr;
 #define QV(QL_, QR_) if (QL == QL_ && QR == QR_) fn = reinterpret_cast<const void*>(k_attn_fused_pv<2, QL_, QR_>);
-    QV(32, 1) QV(32, 2) QV(32, 4) QV(64, 2) QV(64, 4) QV(64, 8)
+    QV(32, 2) QV(32, 4) QV(64, 4) QV(64, 8)
 #undef QV
     int per_cu = 0;
     if (fn) TI_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256, 0));
@@ -2026,7 +2028,7 @@ int ti_attn_qkv_launch(ti_ctx* c, const float* x, const uint16_t* in_norm, float
         TI_LAUNCHED("k_attn_fused_pv (q/k/v)");                                           \
         return TI_OK;                                                                     \
     }
-    QV(32, 1) QV(32, 2) QV(32, 4) QV(64, 2) QV(64, 4) QV(64, 8)
+    QV(32, 2) QV(32, 4) QV(64, 4) QV(64, 8)
 #undef QV
     return two_launches();
 }

@@ -7,7 +7,7 @@ two-launch path is the one a context takes with TI_DECODE_QKV_SEPARATE set at ti
 Both decoders start from the same weights, tokens and seeded KV prefix and take three
 chained decode steps: logits, next tokens and the new KV rows must be identical. The
 cases cover both projection widths (hidden 1024: 32 lanes a row; 2048: 64) and split
-counts that give every row-unit size (2, 4 and 8 rows) and, with a 256-position cache
+counts that give both row-unit sizes (4 and 8 rows) and, with a 256-position cache
 (2 splits per KV head), several rounds of units per wave. A third context is created
 with TI_DECODE_QKV_POLLS=0: its waves never wait for the rows another workgroup
 publishes and compute their own (the path a wave takes when its poll gives up), which
@@ -59,7 +59,7 @@ def ctx_pair():
     fused.close()
 
 
-# (hidden, prefix P, cache capacity): splits per KV head 2, 24, 40, 16, 24, 40, 64
+# (hidden, prefix P, cache capacity): splits per KV head 2, 24, 40, 2, 16, 24, 40, 64
 CASES = [(1024, 100, 256), (1024, 5000, 5100), (1024, 20000, 20100), (2048, 100, 256), (2048, 4090, 4200),
          (2048, 12000, 12100), (2048, 20000, 20100), (2048, 32760, 32800)]
 
