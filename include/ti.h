@@ -213,8 +213,8 @@ int ti_attn_decode_q8_noalloc(void* stream, const float* qr, const uint32_t* kq,
  * projections [nHq*hd], [nKv*hd], [nKv*hd]; k and v are written into cache row pos;
  * out[nHq*hd] is the attention over positions 0..pos; out_q/out_s (both or neither)
  * receive it quantized per 32 (quantQ8, for o_proj's linearQ). max_splits workgroups
- * per KV head (0 = the default for pos + 1 positions: 16 up to 4096, then about one per
- * 512 positions, between 24 and 64; at most 64).
+ * per KV head (0 = the default for pos + 1 positions: 16 up to 2048, 32 up to 14336,
+ * then 64; at most 64).
  * Covers hd 64/128 with nHq/nKv <= 2. */
 int ti_attn_step_q8(ti_ctx* ctx, const float* q, const float* k, const float* v,
                     const uint16_t* qn_w, const uint16_t* kn_w, uint32_t* kq, float* ks,

@@ -1923,9 +1923,12 @@ void ti_rope_row(float* cs, int pos, int hd, float theta) {
 // at most 64. Measured on the Qwen3-1.7B step (8 KV heads, head_dim 128): within ~3% of
 // the best count at every context from 1k to 32k, and up to 10% faster than 64 splits.
 int ti_attn_decode_splits(int S) {
-    if (S <= 4096) return 16;
-    const int ns = (S + 511) / 512;
-    return ns < 24 ? 24 : (ns > ATTF_MAXS ? ATTF_MAXS : ns);
+    // the grid is 8 x NS workgroups: 32 and 64 splits fill the 256 CUs once or twice over;
+    // counts in between leave some CUs two workgroups and the rest one, and the step waits
+    // for the CUs that stream twice (a sweep of the 1.7B step, 4k-32k, over 16-64 splits:
+    // 32 best up to ~12k, 64 from ~16k; 1159 / 1003 tok/s at 16k for 32 / 33 splits)
+    if (S <= 2048) return 16;
+    return S <= 14336 ? 32 : 64;
 }
 
 int ti_attn_fused_launch(ti_ctx* c, const float* q, const float* k, const float* v, const uint16_t* qw,

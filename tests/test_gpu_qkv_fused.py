@@ -59,8 +59,9 @@ def ctx_pair():
     fused.close()
 
 
-# (hidden, prefix P, cache capacity): splits per KV head 2, 24, 40, 2, 16, 24, 40, 64
-CASES = [(1024, 100, 256), (1024, 5000, 5100), (1024, 20000, 20100), (2048, 100, 256), (2048, 4090, 4200),
+# (hidden, prefix P, cache capacity): splits per KV head 2, 24 (the capacity's clamp), 64, 2,
+# 16, 32, 64, 64; row units of 8 rows at 16 and 24 splits, 4 at 32 and 64
+CASES = [(1024, 100, 256), (1024, 2900, 3000), (1024, 20000, 20100), (2048, 100, 256), (2048, 1500, 2100),
          (2048, 12000, 12100), (2048, 20000, 20100), (2048, 32760, 32800)]
 
 

@@ -168,15 +168,14 @@ def test_graph_replay_decodes_like_eager(ctx):
 
 def test_decode_splits_follow_the_context(ctx):
     """The attention split count of a captured step follows the context it is captured at
-    (ti_qwen3_decode_splits: 16 up to 4096 positions, then ceil(S / 512) between 24 and
-    64); a step captured at a short context and replayed over a long one gives the logits
+    (ti_qwen3_decode_splits: 16 up to 2048 positions, 32 up to 14336, then 64); a step
+    captured at a short context and replayed over a long one gives the logits
     and token of a step captured there (only the split count, hence the summation order of
     the split merge, differs)."""
     cfg = dict(SMALL, head_dim=128, max_ctx=33000)
     m = abi.Qwen3(ctx, **cfg)
     try:
-        want = {0: 16, 4095: 16, 4096: 24, 8191: 24, 12287: 24, 12288: 25, 16383: 32, 16384: 33, 32767: 64,
-                32999: 64}
+        want = {0: 16, 2047: 16, 2048: 32, 8191: 32, 14335: 32, 14336: 64, 16384: 64, 32767: 64, 32999: 64}
         assert {p: m.decode_splits(p) for p in want} == want
         with pytest.raises(abi.TIError):
             m.decode_splits(33000)
@@ -190,7 +189,7 @@ def test_decode_splits_follow_the_context(ctx):
                 m.kv_write(l, kx, vx, chunk, p0)
         m.write_tokens(0, rng.integers(0, cfg["vocab"], P + 2).astype(np.int32))
         m.set_pos(P)
-        m.decode()                                  # eager at the long context: 24 splits
+        m.decode()                                  # eager at the long context: 32 splits
         ctx.sync()
         want_logits = _logits(ctx, m, cfg["vocab"]).copy()
         want_tok = int(m.read_tokens(P + 1, 1)[0])
