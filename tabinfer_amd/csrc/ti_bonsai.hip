@@ -242,10 +242,10 @@ __global__ __launch_bounds__(256) void k_bn_attn(const float* __restrict__ qraw,
     // would hold every vector load behind the kernel arguments' wait), then raw q (thread t:
     // head t / 128, dim t % 128), the activation scale, the norm weights, the rotary row of
     // the device position (kept beside it by the kernels that move it) and the new token's
-    // raw K (threads 0..127) or V (128..255) row of hk, none of which waits for the position;
-    // once the position is known (its own round trip, overlapping theirs), a split past the
-    // context leaves, and the others request the first 64 keys' V rows (as the P V pass reads
-    // them) and, for one-pass splits, K rows (4 lanes a key, 32 dims each) before the norm.
+    // raw K (threads 0..127) or V (128..255) row of hk, none of which depends on the
+    // position, so all of them arrive in one round trip; then a split past the context
+    // leaves, and the others request the first 64 keys' V rows (as the P V pass reads them)
+    // and, for one-pass splits, K rows (4 lanes a key, 32 dims each) before the norm.
     const uint32_t praw = ti_pub_load(reinterpret_cast<const uint32_t*>(dpos));
     float qr = qraw[(size_t)(hk * G + pg) * HD + pi];
     float asc = ti_pub_load(act_scale);                 // a vector load: no scalar wait before the others
